@@ -1,0 +1,249 @@
+"""Benchmark of the gfx950 attention hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload decode64k|decode4k|verify|prefill8k|chunked]
+                    [--no-cpu-baseline] [--no-secondary]
+
+A step is one pass of the hot path over one batch of synthetic seeded input already resident in HBM:
+  decode64k  config 2: one token, 32 query / 4 kv heads, head 128, 65536-key f16 cache (the default: the
+             headline metric's decode half, HBM GB/s of K+V bytes)
+  decode4k   config 1: one token, 32 / 8 heads, 4096 keys
+  verify     config 4: 8 draft tokens on a 32768-key prefix, 32 / 4 heads
+  prefill8k  config 3: causal prefill of 8192 tokens, 32 / 8 heads, f16 in and out (MFMA TFLOP/s)
+  chunked    config 5: 131072 tokens in 2048-token chunks against the growing cache, 32 / 4 heads
+Decode steps rotate over several layers' caches whose total exceeds the 256 MB Infinity Cache, as a
+model's layer loop does, so no step finds its K/V in the last-level cache.
+
+Prints ONE JSON line (rank 0). With the default workload the line also carries the prefill figure
+(config 3) under "secondary", and the CPU baseline: the oracle's restatement of the reference's CPU
+attention (src/model.rs:1320-1409) timed on this host on a bounded sample of the same workload.
+"""
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "ghost-infer_amd"))
+
+HBM_PEAK_GBS = 8000.0      # MI355X HBM3E, published
+F16_DENSE_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA, published
+METRIC = "decode-attn HBM GB/s @64K ctx; prefill-attn TFLOPS @8K; % of roofline"
+HD = 128
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def seeded_cache(gen, rows, n_kv, dev, torch):
+    k = torch.randn((rows, n_kv, HD), generator=gen, device=dev, dtype=torch.float32).half()
+    v = torch.randn((rows, n_kv, HD), generator=gen, device=dev, dtype=torch.float32).half()
+    return k, v
+
+
+def time_steps(fn, steps, warmup, torch):
+    """Runs warmup untimed steps, then times exactly `steps` steps between synchronisations with events on
+    the stream the kernels are launched on (torch's current stream). Returns seconds per step."""
+    for i in range(warmup):
+        fn(i)
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for i in range(steps):
+        fn(i)
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / 1e3 / steps
+
+
+# ---------------------------------------------------------------- workloads
+
+def decode_workload(torch, gi_attn, dev, ctx, n_heads, n_kv, n_tok, steps, warmup, seed):
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(seed)
+    cache_bytes = 2 * ctx * n_kv * HD * 2
+    layers = max(1, math.ceil(512e6 / cache_bytes))  # > 256 MB Infinity Cache in total
+    caches = [seeded_cache(gen, ctx, n_kv, dev, torch) for _ in range(layers)]
+    q = torch.randn((n_tok, n_heads * HD), generator=gen, device=dev, dtype=torch.float32)
+    out = torch.empty((n_tok, n_heads * HD), device=dev, dtype=torch.float32)
+    pos0 = ctx - n_tok
+    ws = gi_attn.new_workspace(ctx, n_tok, n_heads, n_kv, device=dev)
+
+    def step(i):
+        k, v = caches[i % layers]
+        gi_attn.decode(q, k, v, pos0, n_heads, n_kv, out=out, workspace=ws)
+
+    t = time_steps(step, steps, warmup, torch)
+    algo_bytes = 2 * ctx * n_kv * HD * 2
+    return {"seconds": t, "bytes": algo_bytes, "layers": layers, "q": q, "cache": caches[0], "pos0": pos0}
+
+
+def prefill_flops(n, pos0, n_heads):
+    # QK^T and PV, 2 flops per multiply-add, causal: query i sees pos0 + i + 1 keys
+    keys = n * pos0 + n * (n + 1) // 2
+    return 4 * n_heads * HD * keys
+
+
+def prefill_workload(torch, gi_attn, dev, n, n_heads, n_kv, steps, warmup, seed):
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(seed)
+    q = torch.randn((n, n_heads * HD), generator=gen, device=dev, dtype=torch.float32).half()
+    k, v = seeded_cache(gen, n, n_kv, dev, torch)
+    out = torch.empty((n, n_heads * HD), device=dev, dtype=torch.float16)
+
+    def step(i):
+        gi_attn.prefill(q, k, v, 0, n_heads, n_kv, out=out)
+
+    t = time_steps(step, steps, warmup, torch)
+    return {"seconds": t, "flops": prefill_flops(n, 0, n_heads)}
+
+
+def chunked_workload(torch, gi_attn, dev, total, chunk, n_heads, n_kv, seed):
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(seed)
+    k, v = seeded_cache(gen, total, n_kv, dev, torch)
+    q = torch.randn((total, n_heads * HD), generator=gen, device=dev, dtype=torch.float32).half()
+    out = torch.empty((total, n_heads * HD), device=dev, dtype=torch.float16)
+    events = []
+    for c0 in range(0, total, chunk):  # warm-up pass
+        gi_attn.prefill(q[c0:c0 + chunk], k, v, c0, n_heads, n_kv, out=out[c0:c0 + chunk])
+    torch.cuda.synchronize()
+    for c0 in range(0, total, chunk):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        gi_attn.prefill(q[c0:c0 + chunk], k, v, c0, n_heads, n_kv, out=out[c0:c0 + chunk])
+        e1.record()
+        events.append((c0, e0, e1))
+    torch.cuda.synchronize()
+    per_chunk = []
+    for c0, e0, e1 in events:
+        s = e0.elapsed_time(e1) / 1e3
+        per_chunk.append((c0, s, prefill_flops(chunk, c0, n_heads) / s / 1e12))
+    return per_chunk
+
+
+def hbm_copy_gbs(torch, dev):
+    """Measured device copy bandwidth (read + write bytes / time) of a 1 GiB buffer: a sanity figure beside
+    the published peak."""
+    a = torch.empty(1 << 28, dtype=torch.float32, device=dev)
+    b = torch.empty_like(a)
+    t = time_steps(lambda i: b.copy_(a), 10, 3, torch)
+    return 2 * a.numel() * 4 / t / 1e9
+
+
+# ---------------------------------------------------------------- CPU baseline (the oracle)
+
+def cpu_baseline_decode(q, cache, pos0, n_heads, n_kv, budget_s=12.0):
+    """Times the oracle's restatement of Model::attention on this host for the same decode (q, cache), on
+    as many repetitions as fit in about budget_s seconds (median)."""
+    import numpy as np
+
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import gi_oracle
+
+    threads = min(16, os.cpu_count() or 1)
+    qn = q.cpu().numpy()
+    kn = cache[0].cpu().numpy().view(np.uint16).reshape(cache[0].shape[0], -1)
+    vn = cache[1].cpu().numpy().view(np.uint16).reshape(cache[1].shape[0], -1)
+    gi_oracle.attention(qn, kn, vn, pos0, n_heads, n_kv, threads=threads)  # warm-up (also builds tables)
+    times = []
+    t_end = time.time() + budget_s
+    while time.time() < t_end or len(times) < 5:
+        t0 = time.perf_counter()
+        gi_oracle.attention(qn, kn, vn, pos0, n_heads, n_kv, threads=threads)
+        times.append(time.perf_counter() - t0)
+        if len(times) >= 200:
+            break
+    times.sort()
+    return times[len(times) // 2], threads, len(times)
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--workload", default="decode64k",
+                    choices=["decode64k", "decode4k", "verify", "prefill8k", "chunked"])
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-secondary", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only: this build has no multi-GPU path (asked for {args.gpus})",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    import gi_attn
+
+    dev = torch.device("cuda:0")
+    gi_attn.init()
+    result = {"metric": METRIC, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+              "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "data": "synthetic"}
+    w = args.workload
+    if w in ("decode64k", "decode4k", "verify"):
+        ctx, n_heads, n_kv, n_tok, cfg = {
+            "decode64k": (65536, 32, 4, 1, "config 2: decode, 1 token, ctx 65536, 32q/4kv, hd 128"),
+            "decode4k": (4096, 32, 8, 1, "config 1: decode, 1 token, ctx 4096, 32q/8kv, hd 128"),
+            "verify": (32776, 32, 4, 8, "config 4: verify, 8 tokens at a 32768-key prefix, 32q/4kv, hd 128"),
+        }[w]
+        log(f"[bench] {cfg}")
+        r = decode_workload(torch, gi_attn, dev, ctx, n_heads, n_kv, n_tok, args.steps, args.warmup, 1234)
+        gbs = r["bytes"] / r["seconds"] / 1e9
+        chunk, nsplit = gi_attn.decode_plan(ctx, n_tok, n_heads, n_kv)
+        result.update({
+            "value": round(gbs, 1), "unit": "GB/s", "ms_per_step": r["seconds"] * 1e3, "dtype": "f16 K/V, f32 math",
+            "config": {"workload": cfg, "ctx": ctx, "n_tok": n_tok, "n_heads": n_heads, "n_kv": n_kv, "hd": HD,
+                       "kv_bytes_per_step": r["bytes"], "layers_rotated": r["layers"],
+                       "slices": nsplit, "keys_per_slice": chunk},
+            "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                         "note": "achieved = K+V bytes / decode step time (split kernel + combine kernel)"},
+        })
+        if not args.no_cpu_baseline:
+            log("[bench] cpu baseline (oracle, Model::attention restatement)")
+            t_cpu, threads, reps = cpu_baseline_decode(r["q"], r["cache"], r["pos0"], n_heads, n_kv)
+            result["cpu_baseline"] = {"value": round(r["bytes"] / t_cpu / 1e9, 3), "unit": "GB/s", "cores": threads,
+                                      "kind": "port",
+                                      "sample": f"{reps} runs of the same decode (median {t_cpu * 1e3:.1f} ms/run)"}
+    elif w == "prefill8k":
+        log("[bench] config 3: causal prefill 8192 tokens, 32q/8kv")
+        r = prefill_workload(torch, gi_attn, dev, 8192, 32, 8, args.steps, args.warmup, 99)
+        tf = r["flops"] / r["seconds"] / 1e12
+        result.update({
+            "value": round(tf, 1), "unit": "TFLOP/s", "ms_per_step": r["seconds"] * 1e3, "dtype": "f16 MFMA, f32 acc",
+            "config": {"workload": "config 3: causal prefill, 8192 tokens, 32q/8kv, hd 128", "flops_per_step": r["flops"]},
+            "roofline": {"bound": "mfma", "achieved": round(tf, 1), "peak": F16_DENSE_PEAK_TFLOPS, "unit": "TFLOP/s",
+                         "frac": round(tf / F16_DENSE_PEAK_TFLOPS, 4), "traffic": None},
+        })
+    else:
+        log("[bench] config 5: chunked prefill 131072 in 2048 chunks, 32q/4kv")
+        per = chunked_workload(torch, gi_attn, dev, 131072, 2048, 32, 4, 5)
+        total = sum(s for _, s, _ in per)
+        flops = sum(prefill_flops(2048, c0, 32) for c0, _, _ in per)
+        tf = flops / total / 1e12
+        result.update({
+            "value": round(tf, 1), "unit": "TFLOP/s", "ms_per_step": total * 1e3, "dtype": "f16 MFMA, f32 acc",
+            "config": {"workload": "config 5: chunked prefill, 131072 tokens in 2048 chunks, 32q/4kv",
+                       "total_seconds": total,
+                       "per_chunk_tflops": [round(t, 1) for _, _, t in per]},
+            "roofline": {"bound": "mfma", "achieved": round(tf, 1), "peak": F16_DENSE_PEAK_TFLOPS, "unit": "TFLOP/s",
+                         "frac": round(tf / F16_DENSE_PEAK_TFLOPS, 4), "traffic": None},
+        })
+        result["steps"] = len(per)
+    if w == "decode64k" and not args.no_secondary:
+        r = prefill_workload(torch, gi_attn, dev, 8192, 32, 8, 20, 3, 99)
+        tf = r["flops"] / r["seconds"] / 1e12
+        result["secondary"] = {"prefill8k": {"value": round(tf, 1), "unit": "TFLOP/s",
+                                             "ms_per_step": r["seconds"] * 1e3,
+                                             "frac_of_f16_dense_peak": round(tf / F16_DENSE_PEAK_TFLOPS, 4)},
+                               "hbm_copy_measured_GBs": round(hbm_copy_gbs(torch, dev), 1)}
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,314 @@
+// C-ABI host side of the gfx950 attention path (declarations and contracts in include/gi_attn.h).
+//
+// Replaces the reference's NVRTC launch layer (src/cuda.rs:4870-5128 driver/NVRTC loading,
+// src/cuda.rs:5377-5763 Kernels/launch3): the kernels are an offline-built code object loaded with
+// hipModuleLoad once per device and launched by name with hipModuleLaunchKernel on the caller's stream.
+// No entry point allocates device memory or synchronises the host.
+#include "gi_attn.h"
+
+#include <hip/hip_runtime.h>
+
+#include <dlfcn.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <string>
+
+namespace {
+
+// Must match the kernels' GiDecodeArgs (gi_attn_kernels.hip).
+struct GiDecodeArgs {
+    const float* q;
+    const uint16_t* kc;
+    const uint16_t* vc;
+    float* part;
+    float* out;
+    const int* posp;
+    long long q_stride;
+    long long kv_stride;
+    long long out_stride;
+    int pos0;
+    int n_tok;
+    int n_heads;
+    int n_kv;
+    int chunk;
+    int nsplit;
+    float qscale;
+    int pad_;
+};
+
+// Must match the kernels' GiPrefillArgs.
+struct GiPrefillArgs {
+    const void* q;
+    const uint16_t* kc;
+    const uint16_t* vc;
+    void* out;
+    long long q_stride;
+    long long kv_stride;
+    long long out_stride;
+    int pos0;
+    int n;
+    int n_heads;
+    int n_kv;
+    float qscale;
+    int q_f16;
+    int out_f16;
+    int pad_;
+};
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr int kMaxDevices = 64;
+constexpr int kDecWaves = 4, kDecTile = 32, kDecPairs = 8;
+constexpr int kSliceUnit = kDecWaves * kDecTile; // 128 keys
+constexpr int kPrefillBQ = 128;                   // query rows per prefill workgroup
+constexpr int kSplitMaxBatch = 15;                // tokens per split launch (src/cuda.rs:119)
+constexpr int kTiledMinBatch = 16;                // prefill from this many tokens (src/cuda.rs:95)
+
+thread_local std::string g_err;
+
+int fail(const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return GI_EINVAL;
+}
+
+int check(hipError_t r, const char* what) {
+    if (r == hipSuccess) return 0;
+    char buf[512];
+    snprintf(buf, sizeof buf, "HIP %s failed: %s (%d)", what, hipGetErrorString(r), (int)r);
+    g_err = buf;
+    return (int)r;
+}
+
+struct Module {
+    bool loaded = false;
+    hipModule_t mod = nullptr;
+    hipFunction_t dec1 = nullptr, dec2 = nullptr, combine = nullptr, prefill = nullptr;
+};
+std::mutex g_mu;
+Module g_mods[kMaxDevices];
+
+std::string default_code_object() {
+    Dl_info info;
+    if (dladdr((void*)&default_code_object, &info) && info.dli_fname) {
+        std::string p = info.dli_fname;
+        size_t slash = p.rfind('/');
+        return (slash == std::string::npos ? std::string(".") : p.substr(0, slash)) + "/gi_attn_gfx950.hsaco";
+    }
+    return "gi_attn_gfx950.hsaco";
+}
+
+int load_module(const char* path, Module** out) {
+    int dev = 0;
+    if (int e = check(hipGetDevice(&dev), "hipGetDevice")) return e;
+    if (dev < 0 || dev >= kMaxDevices) return fail("device %d out of range", dev);
+    std::lock_guard<std::mutex> lock(g_mu);
+    Module& m = g_mods[dev];
+    if (!m.loaded) {
+        std::string p = path ? std::string(path) : default_code_object();
+        if (int e = check(hipModuleLoad(&m.mod, p.c_str()), ("hipModuleLoad(" + p + ")").c_str())) return e;
+        struct { hipFunction_t* f; const char* name; } fns[] = {
+            {&m.dec1, "gi_decode_partial_1"},
+            {&m.dec2, "gi_decode_partial_2"},
+            {&m.combine, "gi_decode_combine"},
+            {&m.prefill, "gi_prefill_fwd"},
+        };
+        for (auto& f : fns)
+            if (int e = check(hipModuleGetFunction(f.f, m.mod, f.name), f.name)) {
+                (void)hipModuleUnload(m.mod);
+                m.mod = nullptr;
+                return e;
+            }
+        m.loaded = true;
+    }
+    *out = &m;
+    return 0;
+}
+
+int launch(hipFunction_t f, dim3 grid, dim3 block, hipStream_t stream, void* args, size_t args_size) {
+    void* config[] = {HIP_LAUNCH_PARAM_BUFFER_POINTER, args, HIP_LAUNCH_PARAM_BUFFER_SIZE, &args_size,
+                      HIP_LAUNCH_PARAM_END};
+    return check(hipModuleLaunchKernel(f, grid.x, grid.y, grid.z, block.x, block.y, block.z, 0, stream, nullptr,
+                                       config),
+                 "kernel launch");
+}
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+// Workgroups to aim for per decode launch: about two per CU of the 256 on MI355X.
+int decode_target_wgs() {
+    static int target = [] {
+        const char* e = getenv("GI_DECODE_TARGET_WGS");
+        int v = e ? atoi(e) : 0;
+        return v > 0 ? v : 512;
+    }();
+    return target;
+}
+
+int ncb_for(int n_tok, int G) { return n_tok * G > kDecPairs ? 2 : 1; }
+
+void plan(int max_span, int n_tok, int n_heads, int n_kv, int* chunk, int* nsplit) {
+    int G = n_heads / n_kv;
+    int ncb = ncb_for(n_tok, G);
+    int groups = (n_tok * G + kDecPairs * ncb - 1) / (kDecPairs * ncb);
+    int units = (max_span + kSliceUnit - 1) / kSliceUnit; // 128-key units
+    int per_slot = std::max(1, decode_target_wgs() / std::max(1, n_kv * groups));
+    int per = std::max(1, (units + per_slot - 1) / per_slot);
+    *chunk = per * kSliceUnit;
+    *nsplit = std::max(1, (max_span + *chunk - 1) / *chunk);
+}
+
+int check_shape(int n_heads, int n_kv, int hd) {
+    if (hd != 128) return fail("head size %d unsupported (the gfx950 kernels take 128)", hd);
+    if (n_kv <= 0 || n_heads <= 0 || n_heads % n_kv != 0)
+        return fail("n_heads %d must be a positive multiple of n_kv %d", n_heads, n_kv);
+    return 0;
+}
+
+} // namespace
+
+extern "C" {
+
+int gi_init(const char* code_object_path) {
+    Module* m;
+    return load_module(code_object_path, &m);
+}
+
+const char* gi_last_error(void) { return g_err.c_str(); }
+
+int gi_attn_decode_plan(int max_span, int n_tok, int n_heads, int n_kv, int hd, int* chunk, int* nsplit) {
+    if (int e = check_shape(n_heads, n_kv, hd)) return e;
+    if (max_span <= 0 || n_tok <= 0) return fail("max_span %d and n_tok %d must be positive", max_span, n_tok);
+    if (!chunk || !nsplit) return fail("null output pointer");
+    plan(max_span, n_tok, n_heads, n_kv, chunk, nsplit);
+    return 0;
+}
+
+size_t gi_attn_decode_workspace_bytes(int ctx_cap, int n_tok, int n_heads, int n_kv, int hd) {
+    if (check_shape(n_heads, n_kv, hd) || ctx_cap <= 0 || n_tok <= 0) return 0;
+    // the most partials any launch of up to n_tok tokens whose spans reach at most ctx_cap keys writes:
+    // plan() caps the slices per (kv head, pair group) at per_slot, and a span never has more slices
+    // than 128-key units
+    size_t best = 16;
+    int G = n_heads / n_kv;
+    for (int t = 1; t <= n_tok; t++) {
+        int ncb = ncb_for(t, G);
+        int groups = (t * G + kDecPairs * ncb - 1) / (kDecPairs * ncb);
+        int per_slot = std::max(1, decode_target_wgs() / std::max(1, n_kv * groups));
+        int most = std::max(1, std::min(per_slot, (ctx_cap + kSliceUnit - 1) / kSliceUnit));
+        best = std::max(best, (size_t)t * n_heads * most * (hd + 2) * sizeof(float));
+    }
+    return best;
+}
+
+int gi_attn_decode(void* stream, const float* q, long long q_stride, const uint16_t* kc, const uint16_t* vc,
+                   long long kv_stride, float* out, long long out_stride, void* workspace, size_t workspace_bytes,
+                   int pos0, const int* posp, int ctx_cap, int n_tok, int n_heads, int n_kv, int hd, float scale) {
+    if (int e = check_shape(n_heads, n_kv, hd)) return e;
+    if (n_tok <= 0) return fail("n_tok %d must be positive", n_tok);
+    if (!q || !kc || !vc || !out) return fail("null tensor pointer");
+    if (!aligned16(q) || !aligned16(kc) || !aligned16(vc) || q_stride % 4 || kv_stride % 8)
+        return fail("q, kc, vc must be 16-byte aligned, q_stride a multiple of 4 and kv_stride of 8");
+    if (kv_stride < (long long)n_kv * hd || q_stride < (long long)n_heads * hd || out_stride < (long long)n_heads * hd)
+        return fail("row strides too small for %d heads / %d kv heads", n_heads, n_kv);
+    if (!posp && pos0 < 0) return fail("pos0 %d must be >= 0", pos0);
+    int max_span = posp ? ctx_cap : pos0 + n_tok;
+    if (posp && ctx_cap < n_tok) return fail("ctx_cap %d must cover the %d tokens", ctx_cap, n_tok);
+    Module* m;
+    if (int e = load_module(nullptr, &m)) return e;
+    int G = n_heads / n_kv;
+    int ncb = ncb_for(n_tok, G);
+    int groups = (n_tok * G + kDecPairs * ncb - 1) / (kDecPairs * ncb);
+    GiDecodeArgs a{};
+    plan(max_span, n_tok, n_heads, n_kv, &a.chunk, &a.nsplit);
+    size_t need = a.nsplit == 1 ? 0 : (size_t)n_tok * n_heads * a.nsplit * (hd + 2) * sizeof(float);
+    if (need && (!workspace || workspace_bytes < need))
+        return fail("workspace of %zu bytes too small: %zu needed", workspace_bytes, need);
+    a.q = q;
+    a.kc = kc;
+    a.vc = vc;
+    a.part = (float*)workspace;
+    a.out = out;
+    a.posp = posp;
+    a.q_stride = q_stride;
+    a.kv_stride = kv_stride;
+    a.out_stride = out_stride;
+    a.pos0 = pos0;
+    a.n_tok = n_tok;
+    a.n_heads = n_heads;
+    a.n_kv = n_kv;
+    a.qscale = scale * kLog2e;
+    hipStream_t st = (hipStream_t)stream;
+    if (int e = launch(ncb == 2 ? m->dec2 : m->dec1, dim3(a.nsplit, n_kv, groups), dim3(256), st, &a, sizeof a))
+        return e;
+    if (a.nsplit > 1)
+        if (int e = launch(m->combine, dim3(n_heads, n_tok, 1), dim3(128), st, &a, sizeof a)) return e;
+    return 0;
+}
+
+int gi_attn_prefill(void* stream, const void* q, int q_dtype, long long q_stride, const uint16_t* kc,
+                    const uint16_t* vc, long long kv_stride, void* out, int out_dtype, long long out_stride, int pos0,
+                    int n, int n_heads, int n_kv, int hd, float scale) {
+    if (int e = check_shape(n_heads, n_kv, hd)) return e;
+    if (n <= 0 || pos0 < 0) return fail("n %d must be positive and pos0 %d >= 0", n, pos0);
+    if (!q || !kc || !vc || !out) return fail("null tensor pointer");
+    if ((q_dtype != GI_F32 && q_dtype != GI_F16) || (out_dtype != GI_F32 && out_dtype != GI_F16))
+        return fail("dtypes must be GI_F32 or GI_F16");
+    if (!aligned16(q) || !aligned16(kc) || !aligned16(vc) || !aligned16(out) || kv_stride % 8 ||
+        q_stride % (q_dtype == GI_F16 ? 8 : 4) || out_stride % (out_dtype == GI_F16 ? 8 : 4))
+        return fail("tensors must be 16-byte aligned with row strides of whole 16-byte units");
+    if (kv_stride < (long long)n_kv * hd || q_stride < (long long)n_heads * hd || out_stride < (long long)n_heads * hd)
+        return fail("row strides too small for %d heads / %d kv heads", n_heads, n_kv);
+    Module* m;
+    if (int e = load_module(nullptr, &m)) return e;
+    GiPrefillArgs a{};
+    a.q = q;
+    a.kc = kc;
+    a.vc = vc;
+    a.out = out;
+    a.q_stride = q_stride;
+    a.kv_stride = kv_stride;
+    a.out_stride = out_stride;
+    a.pos0 = pos0;
+    a.n = n;
+    a.n_heads = n_heads;
+    a.n_kv = n_kv;
+    a.qscale = scale * kLog2e;
+    a.q_f16 = q_dtype == GI_F16;
+    a.out_f16 = out_dtype == GI_F16;
+    int qtiles = (n + kPrefillBQ - 1) / kPrefillBQ;
+    return launch(m->prefill, dim3(qtiles * n_heads, 1, 1), dim3(256), (hipStream_t)stream, &a, sizeof a);
+}
+
+int gi_attention(void* stream, const float* qkv, const uint16_t* kc, const uint16_t* vc, float* out,
+                 void* workspace, size_t workspace_bytes, int pos0, const int* posp, int ctx_cap, int n, int n_heads,
+                 int n_kv, int hd, int exact) {
+    if (int e = check_shape(n_heads, n_kv, hd)) return e;
+    if (n <= 0) return fail("n %d must be positive", n);
+    const long long q_dim = (long long)n_heads * hd, kv_dim = (long long)n_kv * hd, row = q_dim + 2 * kv_dim;
+    const float scale = 1.0f / std::sqrt((float)hd);
+    if (n >= kTiledMinBatch && !exact) {
+        if (posp) return fail("a device position (posp) is only taken by the split path");
+        return gi_attn_prefill(stream, qkv, GI_F32, row, kc, vc, kv_dim, out, GI_F32, q_dim, pos0, n, n_heads, n_kv,
+                               hd, scale);
+    }
+    for (int b0 = 0; b0 < n; b0 += kSplitMaxBatch) {
+        int m = std::min(n - b0, kSplitMaxBatch);
+        // with a device position every launch reads *posp, so only single launches take it
+        if (posp && n > kSplitMaxBatch) return fail("posp takes at most %d tokens", kSplitMaxBatch);
+        if (int e = gi_attn_decode(stream, qkv + b0 * row, row, kc, vc, kv_dim, out + b0 * q_dim, q_dim, workspace,
+                                   workspace_bytes, pos0 + b0, posp, ctx_cap, m, n_heads, n_kv, hd, scale))
+            return e;
+    }
+    return 0;
+}
+
+} // extern "C"

@@ -1,0 +1,217 @@
+"""Python mirror of ghost-infer's attention operator over the gfx950 C ABI (include/gi_attn.h).
+
+The reference's operator is GpuModel::attention (src/cuda.rs:8448-8541): for a layer it takes the
+[q | k | v] f32 rows of the batch, the layer's f16 K/V cache, the session position and a verify
+("exact") flag, and writes the f32 attention output. `attention()` keeps that contract; `decode()` and
+`prefill()` expose the two kernels it dispatches to, with the shapes the benchmark configs name.
+
+Tensors are torch CUDA tensors (torch is the device-memory and stream plumbing here; every computation
+runs in the HIP kernels of libgi_attn.so). Work goes on torch's current stream. Errors raise
+GiAttnError with the library's message, as the reference returns Err(String) from Api::check
+(src/cuda.rs:5058-5068). There is no CPU fallback: without the built library every call raises.
+"""
+import ctypes
+import math
+import os
+
+import torch
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libgi_attn.so")
+HSACO_PATH = os.path.join(HERE, "gi_attn_gfx950.hsaco")
+
+GI_F32 = 0
+GI_F16 = 1
+SPLIT_MAX_BATCH = 15  # src/cuda.rs:119
+TILED_MIN_BATCH = 16  # src/cuda.rs:95
+
+# Exported symbols of include/gi_attn.h
+SYMBOLS = (
+    "gi_init",
+    "gi_last_error",
+    "gi_attn_decode_plan",
+    "gi_attn_decode_workspace_bytes",
+    "gi_attn_decode",
+    "gi_attn_prefill",
+    "gi_attention",
+)
+
+
+class GiAttnError(RuntimeError):
+    pass
+
+
+_lib = None
+
+
+def load_library(path=LIB_PATH):
+    """Loads libgi_attn.so and declares its signatures (no GPU work)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(path):
+        raise GiAttnError(f"{path} is not built: run ghost-infer_amd/gi_build.py (no fallback path exists)")
+    lib = ctypes.CDLL(path)
+    vp, i, ll, sz, f = ctypes.c_void_p, ctypes.c_int, ctypes.c_longlong, ctypes.c_size_t, ctypes.c_float
+    lib.gi_init.argtypes = [ctypes.c_char_p]
+    lib.gi_init.restype = i
+    lib.gi_last_error.argtypes = []
+    lib.gi_last_error.restype = ctypes.c_char_p
+    lib.gi_attn_decode_plan.argtypes = [i, i, i, i, i, ctypes.POINTER(i), ctypes.POINTER(i)]
+    lib.gi_attn_decode_plan.restype = i
+    lib.gi_attn_decode_workspace_bytes.argtypes = [i, i, i, i, i]
+    lib.gi_attn_decode_workspace_bytes.restype = sz
+    lib.gi_attn_decode.argtypes = [vp, vp, ll, vp, vp, ll, vp, ll, vp, sz, i, vp, i, i, i, i, i, f]
+    lib.gi_attn_decode.restype = i
+    lib.gi_attn_prefill.argtypes = [vp, vp, i, ll, vp, vp, ll, vp, i, ll, i, i, i, i, i, f]
+    lib.gi_attn_prefill.restype = i
+    lib.gi_attention.argtypes = [vp, vp, vp, vp, vp, vp, sz, i, vp, i, i, i, i, i, i]
+    lib.gi_attention.restype = i
+    _lib = lib
+    return lib
+
+
+def _check(rc):
+    if rc != 0:
+        raise GiAttnError(load_library().gi_last_error().decode())
+
+
+def _stream():
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _ptr(t):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else None
+
+
+def _need(t, name, dtype):
+    if not isinstance(t, torch.Tensor) or not t.is_cuda:
+        raise GiAttnError(f"{name} must be a CUDA tensor")
+    if t.dtype != dtype:
+        raise GiAttnError(f"{name} must be {dtype}, got {t.dtype}")
+    if t.stride(-1) != 1:
+        raise GiAttnError(f"{name} rows must be contiguous")
+
+
+def _cache_stride(kc, vc, n_kv, hd):
+    for t, name in ((kc, "k_cache"), (vc, "v_cache")):
+        _need(t, name, torch.float16)
+        if not t.is_contiguous():
+            raise GiAttnError(f"{name} must be contiguous [pos][n_kv][hd]")
+    if kc.shape != vc.shape:
+        raise GiAttnError("k_cache and v_cache shapes differ")
+    return n_kv * hd
+
+
+def init(code_object_path=None):
+    """Loads the code object on the current device (optional: the first call does it)."""
+    lib = load_library()
+    _check(lib.gi_init(code_object_path.encode() if code_object_path else None))
+
+
+def decode_plan(max_span, n_tok, n_heads, n_kv, hd=128):
+    """(keys per slice, slices per token) of a decode call; counterpart of att_chunk/max_splits."""
+    lib = load_library()
+    chunk, nsplit = ctypes.c_int(), ctypes.c_int()
+    _check(lib.gi_attn_decode_plan(max_span, n_tok, n_heads, n_kv, hd, ctypes.byref(chunk), ctypes.byref(nsplit)))
+    return chunk.value, nsplit.value
+
+
+def workspace_bytes(ctx_cap, n_tok, n_heads, n_kv, hd=128):
+    """Workspace bytes of decode calls of up to n_tok tokens with spans up to ctx_cap."""
+    return int(load_library().gi_attn_decode_workspace_bytes(ctx_cap, n_tok, n_heads, n_kv, hd))
+
+
+def new_workspace(ctx_cap, n_tok, n_heads, n_kv, hd=128, device="cuda"):
+    nbytes = workspace_bytes(ctx_cap, n_tok, n_heads, n_kv, hd)
+    return torch.empty((nbytes + 3) // 4, dtype=torch.float32, device=device)
+
+
+def decode(q, k_cache, v_cache, pos0, n_heads, n_kv, hd=128, scale=None, out=None, workspace=None, posp=None,
+           ctx_cap=0):
+    """Decode/verify attention of n_tok = q.shape[0] tokens at positions pos0.. (causal within the block).
+
+    q: f32 [n_tok, >= n_heads*hd] (row stride q.stride(0)); caches f16 [cap, n_kv, hd] (or [cap, n_kv*hd]);
+    returns f32 [n_tok, n_heads*hd]. posp: an int32 CUDA tensor holding the position (graph replay), with
+    ctx_cap the largest span the launch shape must cover.
+    """
+    _need(q, "q", torch.float32)
+    kv_stride = _cache_stride(k_cache, v_cache, n_kv, hd)
+    n_tok = q.shape[0]
+    if scale is None:
+        scale = 1.0 / math.sqrt(hd)
+    if out is None:
+        out = torch.empty((n_tok, n_heads * hd), dtype=torch.float32, device=q.device)
+    _need(out, "out", torch.float32)
+    if posp is not None:
+        _need(posp, "posp", torch.int32)
+    need_rows = ctx_cap if posp is not None else pos0 + n_tok
+    if k_cache.shape[0] < need_rows:
+        raise GiAttnError(f"the cache holds {k_cache.shape[0]} positions; {need_rows} needed")
+    if workspace is None:
+        workspace = new_workspace(need_rows, n_tok, n_heads, n_kv, hd, q.device)
+    lib = load_library()
+    _check(lib.gi_attn_decode(_stream(), _ptr(q), q.stride(0), _ptr(k_cache), _ptr(v_cache), kv_stride, _ptr(out),
+                              out.stride(0), _ptr(workspace), workspace.numel() * workspace.element_size(), pos0,
+                              _ptr(posp), ctx_cap, n_tok, n_heads, n_kv, hd, scale))
+    return out
+
+
+def prefill(q, k_cache, v_cache, pos0, n_heads, n_kv, hd=128, scale=None, out=None, out_dtype=None):
+    """Causal prefill of n = q.shape[0] tokens at positions pos0..pos0+n-1 (their K/V already cached).
+
+    q: f32 or f16 [n, >= n_heads*hd]; returns [n, n_heads*hd] of out_dtype (default: q's dtype).
+    """
+    if q.dtype not in (torch.float32, torch.float16):
+        raise GiAttnError("q must be float32 or float16")
+    _need(q, "q", q.dtype)
+    kv_stride = _cache_stride(k_cache, v_cache, n_kv, hd)
+    n = q.shape[0]
+    if k_cache.shape[0] < pos0 + n:
+        raise GiAttnError(f"the cache holds {k_cache.shape[0]} positions; {pos0 + n} needed")
+    if scale is None:
+        scale = 1.0 / math.sqrt(hd)
+    if out is None:
+        out = torch.empty((n, n_heads * hd), dtype=out_dtype or q.dtype, device=q.device)
+    if out.dtype not in (torch.float32, torch.float16):
+        raise GiAttnError("out must be float32 or float16")
+    _need(out, "out", out.dtype)
+    lib = load_library()
+    _check(lib.gi_attn_prefill(_stream(), _ptr(q), GI_F16 if q.dtype == torch.float16 else GI_F32, q.stride(0),
+                               _ptr(k_cache), _ptr(v_cache), kv_stride, _ptr(out),
+                               GI_F16 if out.dtype == torch.float16 else GI_F32, out.stride(0), pos0, n, n_heads,
+                               n_kv, hd, scale))
+    return out
+
+
+def attention(qkv, k_cache, v_cache, pos0, n_heads, n_kv, hd=128, exact=False, out=None, workspace=None,
+              posp=None, ctx_cap=0):
+    """GpuModel::attention (src/cuda.rs:8448-8541) for one layer.
+
+    qkv: f32 [n, n_heads*hd + 2*n_kv*hd] rows [q | k | v] (only q is read: the cache already holds this
+    batch's K/V rows, as qk_norm_rope wrote them); returns f32 [n, n_heads*hd]. n >= 16 and not exact ->
+    causal prefill kernel; otherwise the split decode path, 15 tokens per launch.
+    """
+    _need(qkv, "qkv", torch.float32)
+    n = qkv.shape[0]
+    row = n_heads * hd + 2 * n_kv * hd
+    if qkv.shape[1] != row or not qkv.is_contiguous():
+        raise GiAttnError(f"qkv must be contiguous [n, {row}]")
+    _cache_stride(k_cache, v_cache, n_kv, hd)
+    if k_cache.shape[0] < max(pos0 + n, ctx_cap if posp is not None else 0):
+        raise GiAttnError(f"the cache holds {k_cache.shape[0]} positions; {pos0 + n} needed")
+    if out is None:
+        out = torch.empty((n, n_heads * hd), dtype=torch.float32, device=qkv.device)
+    _need(out, "out", torch.float32)
+    if posp is not None:
+        _need(posp, "posp", torch.int32)
+    ws_ptr, ws_bytes = None, 0
+    if n < TILED_MIN_BATCH or exact:
+        if workspace is None:
+            cap = ctx_cap if posp is not None else pos0 + n
+            workspace = new_workspace(cap, min(n, SPLIT_MAX_BATCH), n_heads, n_kv, hd, qkv.device)
+        ws_ptr, ws_bytes = _ptr(workspace), workspace.numel() * workspace.element_size()
+    lib = load_library()
+    _check(lib.gi_attention(_stream(), _ptr(qkv), _ptr(k_cache), _ptr(v_cache), _ptr(out), ws_ptr, ws_bytes, pos0,
+                            _ptr(posp), ctx_cap, n, n_heads, n_kv, hd, 1 if exact else 0))
+    return out

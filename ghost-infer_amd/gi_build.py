@@ -1,0 +1,45 @@
+"""Builds the gfx950 attention path in-tree: the kernels' code object and the C-ABI host library.
+
+    python ghost-infer_amd/gi_build.py
+
+Outputs (beside this file): gi_attn_gfx950.hsaco (hipcc --genco, loaded at run time with hipModuleLoad)
+and libgi_attn.so (the C ABI of include/gi_attn.h). hipcc cross-compiles for gfx950, so this runs on a
+machine without a GPU.
+"""
+import os
+import subprocess
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(HERE)
+CSRC = os.path.join(HERE, "csrc")
+HSACO = os.path.join(HERE, "gi_attn_gfx950.hsaco")
+LIB = os.path.join(HERE, "libgi_attn.so")
+
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+# packed f32 VALU ops are disabled for all device code (see the project's design notes on gfx950 boxes)
+DEVICE_FLAGS = ["--offload-arch=gfx950", "-O3", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+
+
+def run(cmd):
+    print("+", " ".join(cmd), flush=True)
+    subprocess.run(cmd, check=True)
+
+
+def build_kernels():
+    run([HIPCC, *DEVICE_FLAGS, "--genco", os.path.join(CSRC, "gi_attn_kernels.hip"), "-o", HSACO])
+
+
+def build_host():
+    run([HIPCC, "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall", "-I", os.path.join(ROOT, "include"),
+         os.path.join(CSRC, "gi_attn_host.cpp"), "-o", LIB, "-ldl"])
+
+
+def build():
+    build_kernels()
+    build_host()
+
+
+if __name__ == "__main__":
+    build()
+    sys.exit(0)

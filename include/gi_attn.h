@@ -1,0 +1,91 @@
+/* gi_attn.h — C ABI of the MI355X (gfx950) attention path: split-K flash decoding and causal flash
+ * prefill over a grouped-query f16 KV cache.
+ *
+ * This is the drop-in boundary for ghost-infer's attention operator. In the reference the engine's
+ * layer loop calls GpuModel::attention (src/cuda.rs:8448-8541), which launches NVRTC-compiled kernels
+ * through Kernels::launch3 (src/cuda.rs:5746-5762). Here a Rust (or C, C++, Python ctypes) caller binds
+ * these functions instead; kernels come from an offline-built gfx950 code object loaded with
+ * hipModuleLoad.
+ *
+ * Conventions shared by every entry point (the reference's, src/cuda.rs:5377-5413, 8403-8541):
+ *  - All tensor pointers are device pointers owned by the caller; no entry point allocates device
+ *    memory. Work is enqueued on `stream` (a hipStream_t; NULL = the null stream) without host sync.
+ *  - Return 0 on success. On failure the return is non-zero (GI_EINVAL for a bad argument, otherwise the
+ *    hipError_t value) and gi_last_error() gives "HIP <what> failed: <text> (<code>)" or the argument
+ *    problem, as the reference's Api::check builds "CUDA {what} failed: {text} ({r})"
+ *    (src/cuda.rs:5058-5068). The message is per thread.
+ *  - Layouts: query/output rows hold head h at element h*hd of the row (row strides in elements); the
+ *    KV cache is two buffers of rows [position][n_kv][hd] f16 (IEEE binary16 bits), kv_stride elements
+ *    per position (n_kv*hd for the reference layout, src/cuda.rs:365-369).
+ *  - Causality: token b of a call sits at position pos0 + b and attends to keys 0..pos0+b.
+ *  - hd must be 128; n_heads must be a multiple of n_kv.
+ */
+#ifndef GI_ATTN_H
+#define GI_ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define GI_EINVAL (-1)
+
+/* element types of gi_attn_prefill's query and output */
+#define GI_F32 0
+#define GI_F16 1
+
+/* Load the code object (path to gi_attn_gfx950.hsaco; NULL = the file beside this library) on the
+ * current device. Optional: every entry point loads it on first use per device.
+ * Replaces: Kernels::binary + compile_on (src/cuda.rs:5485-5655), which NVRTC-compile KERNELS and
+ * resolve the functions by name. */
+int gi_init(const char* code_object_path);
+
+/* Last error message of the calling thread ("" if none). Replaces Api::check's String
+ * (src/cuda.rs:5058-5068). */
+const char* gi_last_error(void);
+
+/* Slice plan of a decode call: keys per slice (`chunk`) and slices per token (`nsplit`) for tokens whose
+ * largest span is max_span. Counterpart of att_want / att_chunk / max_splits (src/cuda.rs:8426-8444),
+ * re-chosen for 256 CUs: slices are multiples of 128 keys and about 2 workgroups per CU in total. */
+int gi_attn_decode_plan(int max_span, int n_tok, int n_heads, int n_kv, int hd, int* chunk, int* nsplit);
+
+/* Bytes of workspace gi_attn_decode needs for n_tok tokens whose spans reach at most ctx_cap keys
+ * (the slice partials, [token][head][slice][hd + 2] f32). The counterpart of the session's att_part
+ * buffer (GpuSession, src/cuda.rs:9826-9870). */
+size_t gi_attn_decode_workspace_bytes(int ctx_cap, int n_tok, int n_heads, int n_kv, int hd);
+
+/* Decode / verify attention for n_tok tokens (one generated token, or a speculative verify block that
+ * is causal within itself). q: f32 rows (q_stride elements apart); out: f32 rows. When posp is non-NULL
+ * the position is read from device memory (*posp replaces pos0; graph replay) and the grid is sized for
+ * ctx_cap keys, so one launch shape serves every position up to ctx_cap - n_tok; otherwise ctx_cap is
+ * ignored. Replaces: attention_partial_gqa + attention_combine, launched by GpuModel::attention's split
+ * path (src/cuda.rs:1684-1865, src/cuda.rs:2806-2836, src/cuda.rs:8478-8538). */
+int gi_attn_decode(void* stream, const float* q, long long q_stride, const uint16_t* kc, const uint16_t* vc,
+                   long long kv_stride, float* out, long long out_stride, void* workspace, size_t workspace_bytes,
+                   int pos0, const int* posp, int ctx_cap, int n_tok, int n_heads, int n_kv, int hd, float scale);
+
+/* Causal prefill attention for n tokens at positions pos0..pos0+n-1 whose K/V rows are already in the
+ * cache (keys 0..pos0+n-1 are read; pos0 > 0 is a chunk of a longer prompt). q: rows of q_dtype
+ * (GI_F32 or GI_F16); out: rows of out_dtype. Replaces: attention_prefill_tc128 (src/cuda.rs:2408-2621),
+ * launched by GpuModel::attention for batches of >= 16 tokens (src/cuda.rs:8459-8466). */
+int gi_attn_prefill(void* stream, const void* q, int q_dtype, long long q_stride, const uint16_t* kc,
+                    const uint16_t* vc, long long kv_stride, void* out, int out_dtype, long long out_stride, int pos0,
+                    int n, int n_heads, int n_kv, int hd, float scale);
+
+/* The attention operator of one layer, as GpuModel::attention (src/cuda.rs:8448-8541) dispatches it:
+ * qkv rows are [q (n_heads*hd) | k | v] f32 (stride n_heads*hd + 2*n_kv*hd, src/cuda.rs:1713), out rows
+ * n_heads*hd f32. Batches of >= 16 tokens that are not `exact` (verify) go to prefill; the rest to the
+ * split decode path in launches of at most 15 tokens (SPLIT_MAX_BATCH, src/cuda.rs:119). fixed_split
+ * with posp: the grid is sized for ctx_cap (the session capacity), as max_splits does. scale is
+ * 1/sqrt(hd) as in the reference. */
+int gi_attention(void* stream, const float* qkv, const uint16_t* kc, const uint16_t* vc, float* out,
+                 void* workspace, size_t workspace_bytes, int pos0, const int* posp, int ctx_cap, int n, int n_heads,
+                 int n_kv, int hd, int exact);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GI_ATTN_H */

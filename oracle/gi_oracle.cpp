@@ -1,0 +1,463 @@
+// gi_oracle — CPU restatement of ghost-infer's attention, used ONLY as test infrastructure.
+//
+// This library is the checker for the HIP attention path and the timed CPU baseline in bench.py.
+// Nothing in the product path (ghost-infer_amd/) links, loads or calls it; only tests/, the smoke
+// check in __graft_entry__.py and bench.py's cpu_baseline leg do.
+//
+// Functions and the reference code they restate (paths relative to the reference repository):
+//   gio_f16_to_f32 / gio_f32_to_f16   src/quant.rs:10-60  (IEEE binary16, round to nearest even)
+//   gio_dot_f32                       src/quant.rs:758-768 (8 independent lanes, then the tail)
+//   gio_att_chunk / gio_max_splits    src/cuda.rs:1642-1644, src/cuda.rs:8426-8444 (slice arithmetic)
+//   gio_attention                     src/model.rs:1320-1409 (Model::attention: work units of
+//                                     (token, kv head, slice), per-slice softmax, serial LSE merge)
+//   gio_decode_gpu                    src/cuda.rs:1684-1865 + 2806-2836 (attention_partial_gqa with
+//                                     an f16 cache, head size 128, then attention_combine)
+//   gio_prefill_tc                    src/cuda.rs:2408-2617 (attn_prefill_tc<128>: Q*scale*log2e and
+//                                     P rounded to f16, base-2 online softmax over 32-key tiles)
+//
+// How each is pinned (tests/test_oracle.py): the f16 conversion exhaustively against numpy's float16
+// and against src/quant.rs:1160-1169's known values; the attention functions against an independent
+// float64 brute-force softmax attention, closed forms (one position -> V0, zero keys -> mean of V,
+// one dominant key -> its V row), invariance to the split count, causality and GQA group symmetry,
+// and torch's scaled_dot_product_attention.
+#include <algorithm>
+#include <atomic>
+#include <cmath>
+#include <cstddef>
+#include <cstdint>
+#include <cstring>
+#include <limits>
+#include <thread>
+#include <vector>
+
+namespace {
+
+// ---------------------------------------------------------------- f16 <-> f32 (src/quant.rs:10-60)
+float f16_to_f32(uint16_t h) {
+    uint32_t sign = (uint32_t)(h & 0x8000) << 16;
+    uint32_t exp = (h >> 10) & 0x1f;
+    uint32_t mant = h & 0x3ff;
+    uint32_t bits;
+    if (exp == 0 && mant == 0) {
+        bits = sign;
+    } else if (exp == 0) { // subnormal: shift the mantissa up until its leading one is the implicit bit
+        int e = 127 - 15 + 1;
+        uint32_t m = mant;
+        while ((m & 0x400) == 0) { m <<= 1; e -= 1; }
+        bits = sign | ((uint32_t)e << 23) | ((m & 0x3ff) << 13);
+    } else if (exp == 0x1f) {
+        bits = sign | 0x7f800000u | (mant << 13);
+    } else {
+        bits = sign | ((exp + 127 - 15) << 23) | (mant << 13);
+    }
+    float f;
+    std::memcpy(&f, &bits, 4);
+    return f;
+}
+
+uint16_t f32_to_f16(float f) {
+    uint32_t bits;
+    std::memcpy(&bits, &f, 4);
+    uint16_t sign = (uint16_t)((bits >> 16) & 0x8000);
+    int exp = (int)((bits >> 23) & 0xff);
+    uint32_t mant = bits & 0x7fffff;
+    if (exp == 0xff) return sign | 0x7c00 | (mant ? 0x200 : 0);
+    int e = exp - 127 + 15;
+    if (e >= 0x1f) return sign | 0x7c00;
+    if (e <= 0) {
+        if (e < -10) return sign;
+        uint32_t m = mant | 0x800000;
+        uint32_t shift = (uint32_t)(14 - e);
+        uint32_t half = 1u << (shift - 1);
+        uint32_t r = m >> shift;
+        uint32_t rem = m & ((1u << shift) - 1);
+        if (rem > half || (rem == half && (r & 1))) r += 1;
+        return sign | (uint16_t)r;
+    }
+    uint32_t r = ((uint32_t)e << 10) | (mant >> 13);
+    uint32_t rem = mant & 0x1fff;
+    if (rem > 0x1000 || (rem == 0x1000 && (r & 1))) r += 1; // may carry into the exponent: still RNE
+    return sign | (uint16_t)r;
+}
+
+// 65536-entry widening table: the f16 cache widened exactly to f32, row by row as it is read
+struct WidenTable {
+    float v[65536];
+    WidenTable() { for (uint32_t i = 0; i < 65536; i++) v[i] = f16_to_f32((uint16_t)i); }
+};
+const WidenTable& widen() { static WidenTable t; return t; }
+
+// ---------------------------------------------------------------- dot_f32 (src/quant.rs:758-768)
+float dot_f32(const float* a, const float* b, int n) {
+    float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    int full = n / 8 * 8;
+    float tail = 0.f;
+    for (int i = full; i < n; i++) tail += a[i] * b[i];
+    for (int c = 0; c < full; c += 8)
+        for (int i = 0; i < 8; i++) acc[i] += a[c + i] * b[c + i];
+    float s = 0.f;
+    for (int i = 0; i < 8; i++) s += acc[i];
+    return s + tail;
+}
+
+// A cache row reader: f32 rows, or f16 rows widened into a scratch row.
+struct Cache {
+    const float* f32 = nullptr;
+    const uint16_t* f16 = nullptr;
+    long stride = 0; // elements per position
+    const float* row(long t, int off, int len, float* tmp) const {
+        if (f32) return f32 + t * stride + off;
+        const uint16_t* p = f16 + t * stride + off;
+        const float* w = widen().v;
+        for (int i = 0; i < len; i++) tmp[i] = w[p[i]];
+        return tmp;
+    }
+};
+
+// Runs f(i) for i in [0, count) over `threads` workers (rayon's par_chunks_mut.for_each_init stand-in:
+// every unit's arithmetic is independent of which worker runs it, so the results do not depend on it).
+template <class F>
+void parallel_for(long count, int threads, F f) {
+    if (threads <= 1 || count <= 1) {
+        for (long i = 0; i < count; i++) f(i);
+        return;
+    }
+    std::atomic<long> next{0};
+    std::vector<std::thread> pool;
+    int nt = (int)std::min<long>(threads, count);
+    for (int w = 0; w < nt; w++)
+        pool.emplace_back([&] {
+            for (long i; (i = next.fetch_add(1)) < count;) f(i);
+        });
+    for (auto& t : pool) t.join();
+}
+
+// ---------------------------------------------------------------- Model::attention (src/model.rs:1320-1409)
+void model_attention(const float* q, long q_stride, const Cache& kc, const Cache& vc, float* out, long out_stride,
+                     int pos0, int n, int n_heads, int n_kv, int hd, float scale, int threads) {
+    const int group = n_heads / n_kv;
+    const int kd = hd, vd = hd;
+    auto span_of = [&](int b) { return pos0 + b + 1; }; // causal: token b sees positions 0..=pos0+b
+    const long pairs = (long)n * n_kv;
+    long splits;
+    if (pairs >= threads) {
+        splits = 1;
+    } else {
+        long a = (threads + pairs - 1) / pairs;
+        long c = ((long)span_of(0) + 63) / 64;
+        splits = std::max<long>(1, std::min(a, c));
+    }
+    const long unit = (long)group * vd + 2 * group; // per slice: unnormalised outputs, then (max, sum) per head
+    std::vector<float> partial((size_t)(pairs * splits * unit), 0.f);
+
+    auto slice_task = [&](long idx) {
+        std::vector<float> scores, krow(kd), vrow(vd);
+        float* part = partial.data() + idx * unit;
+        long pair = idx / splits, split = idx % splits;
+        int b = (int)(pair / n_kv), kvh = (int)(pair % n_kv);
+        long span = span_of(b);
+        long per = (span + splits - 1) / splits;
+        long t0 = std::min(split * per, span), t1 = std::min((split + 1) * per, span);
+        long len = t1 - t0;
+        const float* qs = q + (long)b * q_stride + (long)kvh * group * kd;
+        float* o = part;
+        float* stats = part + (long)group * vd;
+        std::fill(o, o + (long)group * vd, 0.f);
+        if (len == 0) {
+            for (int g = 0; g < group; g++) {
+                stats[2 * g] = -std::numeric_limits<float>::infinity();
+                stats[2 * g + 1] = 0.f;
+            }
+            return;
+        }
+        scores.assign((size_t)(group * len), 0.f);
+        for (long t = t0; t < t1; t++) {
+            const float* kt = kc.row(t, kvh * kd, kd, krow.data());
+            for (int g = 0; g < group; g++) scores[g * len + (t - t0)] = dot_f32(qs + (long)g * kd, kt, kd) * scale;
+        }
+        for (int g = 0; g < group; g++) {
+            float* row = scores.data() + g * len;
+            float mx = -std::numeric_limits<float>::infinity();
+            for (long i = 0; i < len; i++) mx = std::max(mx, row[i]);
+            float total = 0.f;
+            for (long i = 0; i < len; i++) {
+                row[i] = std::exp(row[i] - mx);
+                total += row[i];
+            }
+            stats[2 * g] = mx;
+            stats[2 * g + 1] = total;
+        }
+        for (long t = t0; t < t1; t++) {
+            const float* vt = vc.row(t, kvh * vd, vd, vrow.data());
+            for (int g = 0; g < group; g++) {
+                float w = scores[g * len + (t - t0)];
+                float* oh = o + (long)g * vd;
+                for (int d = 0; d < vd; d++) oh[d] += w * vt[d];
+            }
+        }
+    };
+    // a single token over a short context is too little work to be worth waking threads
+    long work = (long)n * n_heads * (pos0 + n) * kd;
+    parallel_for(pairs * splits, work < (1L << 16) ? 1 : threads, slice_task);
+
+    // merge the slices of each (token, kv head) into normalised head outputs (serial, slice order)
+    for (long pair = 0; pair < pairs; pair++) {
+        int b = (int)(pair / n_kv), kvh = (int)(pair % n_kv);
+        const float* parts = partial.data() + pair * splits * unit;
+        for (int g = 0; g < group; g++) {
+            float m = -std::numeric_limits<float>::infinity();
+            for (long s = 0; s < splits; s++) m = std::max(m, parts[s * unit + (long)group * vd + 2 * g]);
+            float* o = out + (long)b * out_stride + (long)(kvh * group + g) * vd;
+            std::fill(o, o + vd, 0.f);
+            float total = 0.f;
+            for (long s = 0; s < splits; s++) {
+                const float* p = parts + s * unit;
+                float w = std::exp(p[(long)group * vd + 2 * g] - m);
+                if (w == 0.f) continue;
+                total += p[(long)group * vd + 2 * g + 1] * w;
+                for (int d = 0; d < vd; d++) o[d] += w * p[(long)g * vd + d];
+            }
+            float inv = 1.f / total;
+            for (int d = 0; d < vd; d++) o[d] *= inv;
+        }
+    }
+}
+
+// ---------------------------------------------------------------- slice arithmetic (src/cuda.rs:1642, 8426-8444)
+constexpr int ATT_MAX_CHUNK = 256;
+constexpr int SPLIT_MIN_SPAN = 32;
+constexpr int ATT_TARGET_BLOCKS = 96;
+int att_chunk(int span, int want, int cap) {
+    if (span <= SPLIT_MIN_SPAN) return ATT_MAX_CHUNK;
+    return std::min(std::max((span + want - 1) / want, 32), cap);
+}
+
+// ---------------------------------------------------------------- attention_partial_gqa + attention_combine
+// (src/cuda.rs:1684-1865, 2806-2836), f16 cache, head size 128, restated for one block at a time.
+float lane_dot(const float* q, const float* k) { // src/cuda.rs:1647-1649: fma chain over 4 products
+    return std::fma(q[3], k[3], std::fma(q[2], k[2], std::fma(q[1], k[1], q[0] * k[0])));
+}
+// score of one key row for one head, in the butterfly order of src/cuda.rs:1716-1754
+float butterfly_score(const float* qs, const float* k) {
+    float s1[16];
+    for (int j = 0; j < 16; j++) s1[j] = lane_dot(qs + 4 * j, k + 4 * j) + lane_dot(qs + 4 * j + 64, k + 4 * j + 64);
+    float s2[8], s3[4], s4[2];
+    for (int j = 0; j < 8; j++) s2[j] = s1[j] + s1[j + 8];
+    for (int j = 0; j < 4; j++) s3[j] = s2[j] + s2[j + 4];
+    for (int j = 0; j < 2; j++) s4[j] = s3[j] + s3[j + 2];
+    return s4[0] + s4[1];
+}
+// block_sum over 128 threads (src/cuda.rs:148-168): per-thread strided sums, warp_sum by shfl_down, then
+// warp 0 sums the 4 warp totals the same way
+float block_sum128(const float* per_thread) {
+    float w[4];
+    for (int wp = 0; wp < 4; wp++) {
+        float v[32];
+        for (int l = 0; l < 32; l++) v[l] = per_thread[32 * wp + l];
+        for (int o = 16; o > 0; o >>= 1)
+            for (int l = 0; l < 32; l++) if (l + o < 32) v[l] = v[l] + v[l + o];
+        w[wp] = v[0];
+    }
+    float v[32] = {0};
+    for (int i = 0; i < 4; i++) v[i] = w[i];
+    for (int o = 16; o > 0; o >>= 1)
+        for (int l = 0; l < 32; l++) if (l + o < 32) v[l] = v[l] + v[l + o];
+    return v[0];
+}
+
+void decode_gpu(const float* qkv, long q_stride, const uint16_t* kc, const uint16_t* vc, long kv_stride, float* out,
+                long out_stride, int pos0, int m, int n_heads, int n_kv, float scale, int nsplit, int want, int cap,
+                int threads) {
+    const int hd = 128, G = n_heads / n_kv;
+    const float* W = widen().v;
+    // partials [token][head][slice][hd + 2]: (unnormalised O, max, exp-sum) in natural-log units
+    std::vector<float> part((size_t)m * n_heads * nsplit * (hd + 2), 0.f);
+    auto block = [&](long idx) { // one block = (kv head, token, slice)
+        int s = (int)(idx % nsplit);
+        int b = (int)((idx / nsplit) % m);
+        int kvh = (int)(idx / nsplit / m);
+        int span = pos0 + b + 1;
+        int chunk = att_chunk(span, want, cap);
+        int t0 = s * chunk, len = std::min(span, t0 + chunk) - t0;
+        auto P = [&](int g) { return part.data() + (((size_t)b * n_heads + kvh * G + g) * nsplit + s) * (hd + 2); };
+        if (len <= 0) {
+            for (int g = 0; g < G; g++) {
+                float* p = P(g);
+                std::fill(p, p + hd, 0.f);
+                p[hd] = -std::numeric_limits<float>::infinity();
+                p[hd + 1] = 0.f;
+            }
+            return;
+        }
+        std::vector<float> qsh((size_t)G * hd), sc((size_t)len * G), krow(hd);
+        const float* qb = qkv + (long)b * q_stride + (long)kvh * G * hd;
+        for (int i = 0; i < G * hd; i++) qsh[i] = qb[i] * scale;
+        for (int t = 0; t < len; t++) {
+            const uint16_t* kt = kc + (long)(t0 + t) * kv_stride + kvh * hd;
+            for (int i = 0; i < hd; i++) krow[i] = W[kt[i]];
+            for (int g = 0; g < G; g++) sc[(size_t)t * G + g] = butterfly_score(qsh.data() + g * hd, krow.data());
+        }
+        for (int g = 0; g < G; g++) {
+            float mx = -std::numeric_limits<float>::infinity();
+            for (int t = 0; t < len; t++) mx = std::max(mx, sc[(size_t)t * G + g]);
+            float thr[128] = {0};
+            for (int t = 0; t < len; t++) {
+                float e = std::exp(sc[(size_t)t * G + g] - mx);
+                sc[(size_t)t * G + g] = e;
+                thr[t % 128] = thr[t % 128] + e;
+            }
+            float seg = block_sum128(thr);
+            for (int d = 0; d < hd; d++) {
+                float a = 0.f;
+                for (int t = 0; t < len; t++) a = std::fma(sc[(size_t)t * G + g], W[vc[(long)(t0 + t) * kv_stride + kvh * hd + d]], a);
+                int h = kvh * G + g;
+                if (nsplit == 1) {
+                    out[(long)b * out_stride + (long)h * hd + d] = a * (1.f / seg);
+                } else {
+                    float* p = P(g);
+                    p[d] = a;
+                    if (d == 0) { p[hd] = mx; p[hd + 1] = seg; }
+                }
+            }
+        }
+    };
+    parallel_for((long)n_kv * m * nsplit, threads, block);
+    if (nsplit == 1) return;
+    for (int b = 0; b < m; b++) // attention_combine
+        for (int h = 0; h < n_heads; h++) {
+            int span = pos0 + b + 1;
+            int chunk = att_chunk(span, want, cap);
+            int used = std::min(nsplit, (span + chunk - 1) / chunk);
+            const float* p = part.data() + ((size_t)b * n_heads + h) * nsplit * (hd + 2);
+            float mm = -std::numeric_limits<float>::infinity();
+            for (int s = 0; s < used; s++) mm = std::max(mm, p[s * (hd + 2) + hd]);
+            std::vector<float> w(used);
+            for (int s = 0; s < used; s++) w[s] = std::exp(p[s * (hd + 2) + hd] - mm);
+            float total = 0.f;
+            for (int s = 0; s < used; s++) total = std::fma(p[s * (hd + 2) + hd + 1], w[s], total);
+            float inv = 1.f / total;
+            for (int d = 0; d < hd; d++) {
+                float acc = 0.f;
+                for (int s = 0; s < used; s++) acc = std::fma(p[s * (hd + 2) + d], w[s], acc);
+                out[(long)b * out_stride + (long)h * hd + d] = acc * inv;
+            }
+        }
+}
+
+// ---------------------------------------------------------------- attn_prefill_tc<128> (src/cuda.rs:2408-2617)
+// Per query row: Q rounded to f16 after scaling by scale*log2(e); per 32-key tile S = f16 Q . f16 K in f32;
+// mask keys past the row's position; running max in base 2; P = f16(exp2(s - m)); l = alpha*l + sum(P);
+// O = alpha*O + P V; out = O / l.
+void prefill_tc(const float* q, long q_stride, const uint16_t* kc, const uint16_t* vc, long kv_stride, float* out,
+                long out_stride, int pos0, int n, int n_heads, int n_kv, float scale, int threads) {
+    const int hd = 128, BK = 32, G = n_heads / n_kv;
+    const float* W = widen().v;
+    const float qs = scale * 1.4426950408889634f;
+    const int kv_len = pos0 + n;
+    auto row_task = [&](long idx) {
+        int r = (int)(idx / n_heads), h = (int)(idx % n_heads);
+        int kvh = h / G;
+        float qh[128], o[128] = {0};
+        for (int d = 0; d < hd; d++) qh[d] = W[f32_to_f16(q[(long)r * q_stride + (long)h * hd + d] * qs)];
+        int p_row = pos0 + r;
+        float m = -std::numeric_limits<float>::infinity(), l = 0.f;
+        // the block's key range: its 64-query tile ends at pos0 + q0 + 64 (tiles are still masked per row)
+        int kmax = std::min(kv_len, pos0 + (r / 64) * 64 + 64);
+        for (int t0 = 0; t0 < kmax; t0 += BK) {
+            if (t0 > p_row) break; // every key of the tile is masked for this row: p stays 0, alpha 1
+            float s[32], mx = -std::numeric_limits<float>::infinity();
+            for (int j = 0; j < BK; j++) {
+                int kp = t0 + j;
+                if (kp > p_row || kp >= kv_len) { s[j] = -std::numeric_limits<float>::infinity(); continue; }
+                const uint16_t* kt = kc + (long)kp * kv_stride + kvh * hd;
+                float a = 0.f;
+                for (int d = 0; d < hd; d++) a += qh[d] * W[kt[d]];
+                s[j] = a;
+                mx = std::max(mx, a);
+            }
+            float mn = std::max(m, mx);
+            float alpha = std::exp2(m - mn);
+            m = mn;
+            float p[32], psum = 0.f;
+            for (int j = 0; j < BK; j++) {
+                p[j] = W[f32_to_f16(std::exp2(s[j] - mn))];
+                psum += p[j];
+            }
+            l = l * alpha + psum;
+            for (int d = 0; d < hd; d++) o[d] *= alpha;
+            for (int j = 0; j < BK; j++) {
+                int kp = t0 + j;
+                if (p[j] == 0.f || kp >= kv_len) continue;
+                const uint16_t* vt = vc + (long)kp * kv_stride + kvh * hd;
+                for (int d = 0; d < hd; d++) o[d] += p[j] * W[vt[d]];
+            }
+        }
+        float inv = 1.f / l;
+        for (int d = 0; d < hd; d++) out[(long)r * out_stride + (long)h * hd + d] = o[d] * inv;
+    };
+    parallel_for((long)n * n_heads, threads, row_task);
+}
+
+} // namespace
+
+extern "C" {
+
+float gio_f16_to_f32(uint16_t h) { return f16_to_f32(h); }
+uint16_t gio_f32_to_f16(float f) { return f32_to_f16(f); }
+
+void gio_f16_to_f32_array(const uint16_t* src, float* dst, size_t count) {
+    const float* w = widen().v;
+    for (size_t i = 0; i < count; i++) dst[i] = w[src[i]];
+}
+void gio_f32_to_f16_array(const float* src, uint16_t* dst, size_t count) {
+    for (size_t i = 0; i < count; i++) dst[i] = f32_to_f16(src[i]);
+}
+
+float gio_dot_f32(const float* a, const float* b, int n) { return dot_f32(a, b, n); }
+
+// att_want (src/cuda.rs:8426-8428) for the grouped-query kernel: ceil(96 / n_kv)
+int gio_att_want(int n_kv) { return (ATT_TARGET_BLOCKS + n_kv - 1) / n_kv; }
+int gio_att_chunk(int span, int want, int cap) { return att_chunk(span, want, cap); }
+// max_splits (src/cuda.rs:8441-8444): most slices any span 1..=ctx needs
+int gio_max_splits(int ctx, int want, int cap) {
+    int best = 1;
+    for (int span = 1; span <= ctx; span++) best = std::max(best, (span + att_chunk(span, want, cap) - 1) / att_chunk(span, want, cap));
+    return best;
+}
+
+// Model::attention over an f32 cache. q: [n][q_stride] (the query heads at the start of each row),
+// caches [pos][kv_stride] with kv head h at h*hd, out [n][out_stride]. threads = the worker count
+// (rayon's current_num_threads), which also fixes the split count.
+void gio_attention_f32(const float* q, long q_stride, const float* kc, const float* vc, long kv_stride, float* out,
+                       long out_stride, int pos0, int n, int n_heads, int n_kv, int hd, float scale, int threads) {
+    Cache k, v;
+    k.f32 = kc; v.f32 = vc; k.stride = v.stride = kv_stride;
+    model_attention(q, q_stride, k, v, out, out_stride, pos0, n, n_heads, n_kv, hd, scale, threads);
+}
+
+// The same over an f16 cache, each row widened exactly to f32 as it is read (the reference caches f32 on
+// the CPU; the widening is exact, so this equals gio_attention_f32 on the widened cache).
+void gio_attention_f16kv(const float* q, long q_stride, const uint16_t* kc, const uint16_t* vc, long kv_stride,
+                         float* out, long out_stride, int pos0, int n, int n_heads, int n_kv, int hd, float scale,
+                         int threads) {
+    Cache k, v;
+    k.f16 = kc; v.f16 = vc; k.stride = v.stride = kv_stride;
+    model_attention(q, q_stride, k, v, out, out_stride, pos0, n, n_heads, n_kv, hd, scale, threads);
+}
+
+// attention_partial_gqa + attention_combine semantics for m tokens (head size 128, f16 cache). nsplit,
+// want and cap as the reference's host computes them (gio_att_want, gio_max_splits, cap 128).
+void gio_decode_gpu(const float* qkv, long q_stride, const uint16_t* kc, const uint16_t* vc, long kv_stride, float* out,
+                    long out_stride, int pos0, int m, int n_heads, int n_kv, float scale, int nsplit, int want, int cap,
+                    int threads) {
+    decode_gpu(qkv, q_stride, kc, vc, kv_stride, out, out_stride, pos0, m, n_heads, n_kv, scale, nsplit, want, cap,
+               threads);
+}
+
+// attn_prefill_tc<128> semantics (f16 rounding of the scaled Q and of P).
+void gio_prefill_tc(const float* q, long q_stride, const uint16_t* kc, const uint16_t* vc, long kv_stride, float* out,
+                    long out_stride, int pos0, int n, int n_heads, int n_kv, float scale, int threads) {
+    prefill_tc(q, q_stride, kc, vc, kv_stride, out, out_stride, pos0, n, n_heads, n_kv, scale, threads);
+}
+
+} // extern "C"

@@ -1,0 +1,140 @@
+"""ctypes wrapper of the CPU oracle (libgi_oracle.so). Test infrastructure only: imported by tests/,
+__graft_entry__.smoke() and bench.py's cpu_baseline leg, never by the product path.
+
+Each function names the reference code it restates; gi_oracle.cpp's header lists how each is pinned.
+"""
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libgi_oracle.so")
+
+_lib = None
+
+
+def build():
+    subprocess.run(["make", "-s", "-B", "-C", HERE, "libgi_oracle.so"], check=True)
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        L = ctypes.CDLL(LIB_PATH)
+        vp, i, l, f = ctypes.c_void_p, ctypes.c_int, ctypes.c_long, ctypes.c_float
+        L.gio_f16_to_f32.argtypes = [ctypes.c_uint16]
+        L.gio_f16_to_f32.restype = f
+        L.gio_f32_to_f16.argtypes = [f]
+        L.gio_f32_to_f16.restype = ctypes.c_uint16
+        L.gio_f16_to_f32_array.argtypes = [vp, vp, ctypes.c_size_t]
+        L.gio_f32_to_f16_array.argtypes = [vp, vp, ctypes.c_size_t]
+        L.gio_dot_f32.argtypes = [vp, vp, i]
+        L.gio_dot_f32.restype = f
+        L.gio_att_want.argtypes = [i]
+        L.gio_att_want.restype = i
+        L.gio_att_chunk.argtypes = [i, i, i]
+        L.gio_att_chunk.restype = i
+        L.gio_max_splits.argtypes = [i, i, i]
+        L.gio_max_splits.restype = i
+        L.gio_attention_f32.argtypes = [vp, l, vp, vp, l, vp, l, i, i, i, i, i, f, i]
+        L.gio_attention_f16kv.argtypes = [vp, l, vp, vp, l, vp, l, i, i, i, i, i, f, i]
+        L.gio_decode_gpu.argtypes = [vp, l, vp, vp, l, vp, l, i, i, i, i, f, i, i, i, i]
+        L.gio_prefill_tc.argtypes = [vp, l, vp, vp, l, vp, l, i, i, i, i, f, i]
+        _lib = L
+    return _lib
+
+
+def _p(a):
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+def f16_bits_to_f32(bits):
+    """src/quant.rs:10-32 over an array of uint16 bit patterns."""
+    bits = np.ascontiguousarray(bits, dtype=np.uint16)
+    out = np.empty(bits.shape, dtype=np.float32)
+    lib().gio_f16_to_f32_array(_p(bits), _p(out), bits.size)
+    return out
+
+
+def f32_to_f16_bits(x):
+    """src/quant.rs:34-60 (round to nearest even) over an array."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(x.shape, dtype=np.uint16)
+    lib().gio_f32_to_f16_array(_p(x), _p(out), x.size)
+    return out
+
+
+def dot_f32(a, b):
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    b = np.ascontiguousarray(b, dtype=np.float32)
+    return lib().gio_dot_f32(_p(a), _p(b), a.size)
+
+
+def att_want(n_kv):
+    return lib().gio_att_want(n_kv)
+
+
+def att_chunk(span, want, cap=128):
+    return lib().gio_att_chunk(span, want, cap)
+
+
+def max_splits(ctx, want, cap=128):
+    return lib().gio_max_splits(ctx, want, cap)
+
+
+def _rows(a, dtype):
+    a = np.ascontiguousarray(a, dtype=dtype)
+    return a.reshape(a.shape[0], -1)
+
+
+def attention(q, kc, vc, pos0, n_heads, n_kv, hd=128, scale=None, threads=8):
+    """Model::attention (src/model.rs:1320-1409). q: f32 [n, n_heads*hd]; kc/vc: [pos, n_kv*hd] as f32
+    values or as f16 bit patterns (uint16, widened exactly). Returns f32 [n, n_heads*hd]."""
+    q = _rows(q, np.float32)
+    n = q.shape[0]
+    if scale is None:
+        scale = 1.0 / np.sqrt(hd)
+    out = np.zeros((n, n_heads * hd), dtype=np.float32)
+    if kc.dtype == np.uint16:
+        kc, vc = _rows(kc, np.uint16), _rows(vc, np.uint16)
+        fn = lib().gio_attention_f16kv
+    else:
+        kc, vc = _rows(kc, np.float32), _rows(vc, np.float32)
+        fn = lib().gio_attention_f32
+    assert kc.shape[0] >= pos0 + n and kc.shape[1] == n_kv * hd
+    fn(_p(q), q.shape[1], _p(kc), _p(vc), kc.shape[1], _p(out), out.shape[1], pos0, n, n_heads, n_kv, hd, scale,
+       threads)
+    return out
+
+
+def decode_gpu_semantics(q, kc, vc, pos0, n_heads, n_kv, scale=None, cap=128, threads=8):
+    """attention_partial_gqa + attention_combine (src/cuda.rs:1684-1865, 2806-2836) with the host's
+    split arithmetic (src/cuda.rs:8426-8444, 8506-8511). kc/vc: uint16 f16 bits [pos, n_kv*128]."""
+    q = _rows(q, np.float32)
+    m = q.shape[0]
+    kc, vc = _rows(kc, np.uint16), _rows(vc, np.uint16)
+    if scale is None:
+        scale = 1.0 / np.sqrt(128)
+    want = att_want(n_kv)
+    nsplit = max(-(-span // att_chunk(span, want, cap)) for span in range(pos0 + 1, pos0 + m + 1))
+    out = np.zeros((m, n_heads * 128), dtype=np.float32)
+    lib().gio_decode_gpu(_p(q), q.shape[1], _p(kc), _p(vc), kc.shape[1], _p(out), out.shape[1], pos0, m, n_heads,
+                         n_kv, scale, nsplit, want, cap, threads)
+    return out
+
+
+def prefill_tc_semantics(q, kc, vc, pos0, n_heads, n_kv, scale=None, threads=8):
+    """attn_prefill_tc<128> (src/cuda.rs:2408-2617): f16-rounded Q*scale*log2(e) and P."""
+    q = _rows(q, np.float32)
+    n = q.shape[0]
+    kc, vc = _rows(kc, np.uint16), _rows(vc, np.uint16)
+    if scale is None:
+        scale = 1.0 / np.sqrt(128)
+    out = np.zeros((n, n_heads * 128), dtype=np.float32)
+    lib().gio_prefill_tc(_p(q), q.shape[1], _p(kc), _p(vc), kc.shape[1], _p(out), out.shape[1], pos0, n, n_heads,
+                         n_kv, scale, threads)
+    return out

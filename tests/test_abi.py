@@ -1,0 +1,80 @@
+"""The C-ABI library: it loads, exports every symbol include/gi_attn.h declares, and rejects bad
+arguments with a message before touching the GPU (no compute calls here)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+import gi_attn
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def declared_symbols():
+    text = open(os.path.join(ROOT, "include", "gi_attn.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(gi_\w+)\s*\(", text)))
+
+
+def test_header_declares_the_python_symbols():
+    assert declared_symbols() == sorted(gi_attn.SYMBOLS)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = gi_attn.load_library()
+    for name in declared_symbols():
+        assert hasattr(lib, name), name
+
+
+def test_code_object_built():
+    assert os.path.getsize(gi_attn.HSACO_PATH) > 0
+
+
+def test_unsupported_head_size_is_rejected_with_message():
+    lib = gi_attn.load_library()
+    c, n = ctypes.c_int(), ctypes.c_int()
+    rc = lib.gi_attn_decode_plan(100, 1, 32, 8, 64, ctypes.byref(c), ctypes.byref(n))
+    assert rc == -1
+    assert "head size 64" in lib.gi_last_error().decode()
+    rc = lib.gi_attn_decode_plan(100, 1, 30, 8, 128, ctypes.byref(c), ctypes.byref(n))
+    assert rc == -1 and "multiple of n_kv" in lib.gi_last_error().decode()
+
+
+def test_decode_rejects_bad_arguments_before_any_launch():
+    lib = gi_attn.load_library()
+    # null tensors, hd 96, misaligned pointers: all refused on the host
+    rc = lib.gi_attn_decode(None, None, 4096, None, None, 512, None, 4096, None, 0, 0, None, 0, 1, 32, 4, 128,
+                            0.088)
+    assert rc == -1 and "null" in lib.gi_last_error().decode()
+    rc = lib.gi_attn_decode(None, 16, 4096, 16, 16, 512, 16, 4096, None, 0, 0, None, 0, 1, 32, 4, 96, 0.1)
+    assert rc == -1 and "head size" in lib.gi_last_error().decode()
+    rc = lib.gi_attn_decode(None, 8, 4096, 16, 16, 512, 16, 4096, None, 0, 0, None, 0, 1, 32, 4, 128, 0.1)
+    assert rc == -1 and "aligned" in lib.gi_last_error().decode()
+    rc = lib.gi_attn_prefill(None, 16, 7, 4096, 16, 16, 1024, 16, 0, 4096, 0, 16, 32, 8, 128, 0.1)
+    assert rc == -1 and "dtypes" in lib.gi_last_error().decode()
+
+
+@pytest.mark.parametrize("ctx,n_tok,n_heads,n_kv", [(4096, 1, 32, 8), (65536, 1, 32, 4), (32776, 8, 32, 4),
+                                                    (100, 15, 8, 1), (1, 1, 32, 4)])
+def test_decode_plan_covers_the_span(ctx, n_tok, n_heads, n_kv):
+    chunk, nsplit = gi_attn.decode_plan(ctx, n_tok, n_heads, n_kv)
+    assert chunk % 128 == 0 and chunk > 0
+    assert (nsplit - 1) * chunk < ctx <= nsplit * chunk
+    if nsplit > 1:
+        # every launch of up to n_tok tokens with spans up to ctx fits the workspace size query
+        need = n_tok * n_heads * nsplit * 130 * 4
+        assert gi_attn.workspace_bytes(ctx, n_tok, n_heads, n_kv) >= need
+    for span in (1, ctx // 3 + 1, ctx):
+        for t in range(1, n_tok + 1):
+            c2, s2 = gi_attn.decode_plan(span, t, n_heads, n_kv)
+            if s2 > 1:
+                assert gi_attn.workspace_bytes(ctx, n_tok, n_heads, n_kv) >= t * n_heads * s2 * 130 * 4
+
+
+def test_python_mirror_raises_without_gpu_tensors():
+    import torch
+
+    with pytest.raises(gi_attn.GiAttnError):
+        gi_attn.decode(torch.zeros(1, 4096), torch.zeros(8, 512, dtype=torch.float16),
+                       torch.zeros(8, 512, dtype=torch.float16), 7, 32, 4)

@@ -1,0 +1,253 @@
+"""Parity of the gfx950 HIP attention path (through the C ABI) with the oracle and the float64 reference.
+
+Bar (from the north star): max-abs error <= 2e-3 and relative L2 <= 1e-3 on the f32 outputs, on seeded
+inputs shared with the CPU oracle. Full-size configs are checked against the float64 reference directly
+(decode) or on sampled rows and against a torch fp32 reference of the whole output (prefill).
+"""
+import math
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+import gi_attn
+import gi_oracle as O
+from attn_common import assert_close, make_inputs, reference_f64
+
+pytestmark = pytest.mark.gpu
+
+
+def say(*a):
+    print("[case]", *a, flush=True)
+    sys.stdout.flush()
+
+
+def to_dev(q, k, v, dev):
+    qt = torch.from_numpy(np.ascontiguousarray(q)).to(dev)
+    kt = torch.from_numpy(np.ascontiguousarray(k).view(np.int16)).to(dev).view(torch.float16)
+    vt = torch.from_numpy(np.ascontiguousarray(v).view(np.int16)).to(dev).view(torch.float16)
+    return qt, kt, vt
+
+
+def run_decode(q, k, v, pos0, n_heads, n_kv, dev, **kw):
+    qt, kt, vt = to_dev(q, k, v, dev)
+    out = gi_attn.decode(qt, kt, vt, pos0, n_heads, n_kv, **kw)
+    torch.cuda.synchronize()
+    return out.cpu().numpy()
+
+
+DECODE_SHAPES = [
+    # (n_tok, pos0, n_heads, n_kv)
+    (1, 0, 32, 8),
+    (1, 1, 32, 8),
+    (1, 31, 32, 4),
+    (1, 32, 32, 4),
+    (1, 127, 8, 8),
+    (1, 128, 32, 4),
+    (1, 129, 16, 2),
+    (1, 1000, 32, 4),
+    (1, 4095, 32, 8),
+    (2, 300, 32, 4),
+    (3, 60, 16, 2),
+    (8, 200, 32, 4),
+    (15, 513, 32, 8),
+    (5, 77, 12, 4),   # G = 3: (token, head) pairs straddle column blocks
+    (4, 40, 6, 1),    # G = 6
+]
+
+
+@pytest.mark.parametrize("n_tok,pos0,n_heads,n_kv", DECODE_SHAPES)
+def test_decode_small(gpu, n_tok, pos0, n_heads, n_kv):
+    say("decode", n_tok, pos0, n_heads, n_kv)
+    q, k, v = make_inputs(1000 + pos0, n_tok, pos0 + n_tok, n_heads, n_kv)
+    got = run_decode(q, k, v, pos0, n_heads, n_kv, gpu)
+    assert_close(got, O.attention(q, k, v, pos0, n_heads, n_kv), what="decode vs oracle")
+    assert_close(got, reference_f64(q, k, v, pos0, n_heads, n_kv), max_abs=2e-5, rel_l2=2e-5,
+                 what="decode vs f64")
+
+
+def test_decode_config1_ctx4096(gpu):
+    say("decode C1 ctx 4096 32q/8kv")
+    q, k, v = make_inputs(1, 1, 4096, 32, 8)
+    got = run_decode(q, k, v, 4095, 32, 8, gpu)
+    assert_close(got, O.attention(q, k, v, 4095, 32, 8), what="C1 vs oracle (Model::attention)")
+    assert_close(got, O.decode_gpu_semantics(q, k, v, 4095, 32, 8), what="C1 vs reference GPU semantics")
+    assert_close(got, reference_f64(q, k, v, 4095, 32, 8), max_abs=2e-5, rel_l2=2e-5, what="C1 vs f64")
+
+
+def test_decode_config2_ctx65536(gpu):
+    say("decode C2 ctx 65536 32q/4kv")
+    q, k, v = make_inputs(2, 1, 65536, 32, 4)
+    got = run_decode(q, k, v, 65535, 32, 4, gpu)
+    assert_close(got, O.attention(q, k, v, 65535, 32, 4), what="C2 vs oracle")
+    assert_close(got, reference_f64(q, k, v, 65535, 32, 4), max_abs=2e-5, rel_l2=2e-5, what="C2 vs f64")
+
+
+def test_verify_config4_8tok_at_32768(gpu):
+    say("verify C4 8 tokens @ 32768 32q/4kv")
+    q, k, v = make_inputs(4, 8, 32776, 32, 4)
+    got = run_decode(q, k, v, 32768, 32, 4, gpu)
+    assert_close(got, O.attention(q, k, v, 32768, 32, 4), what="C4 vs oracle")
+    assert_close(got, reference_f64(q, k, v, 32768, 32, 4), max_abs=2e-5, rel_l2=2e-5, what="C4 vs f64")
+
+
+def test_decode_device_position_one_launch_shape(gpu):
+    # posp: the position comes from device memory and the grid is sized for ctx_cap, so one launch shape
+    # serves every position (graph replay, src/cuda.rs:8686-8712)
+    n_heads, n_kv, cap = 32, 4, 3000
+    q, k, v = make_inputs(77, 1, cap, n_heads, n_kv)
+    qt, kt, vt = to_dev(q, k, v, gpu)
+    ws = gi_attn.new_workspace(cap, 1, n_heads, n_kv, device=gpu)
+    posp = torch.zeros(1, dtype=torch.int32, device=gpu)
+    for pos in (0, 1, 500, 2047, 2999):
+        say("decode posp", pos)
+        posp.fill_(pos)
+        out = gi_attn.decode(qt, kt, vt, 123456, n_heads, n_kv, workspace=ws, posp=posp, ctx_cap=cap)
+        torch.cuda.synchronize()
+        assert_close(out.cpu().numpy(), reference_f64(q, k, v, pos, n_heads, n_kv), max_abs=2e-5, rel_l2=2e-5,
+                     what=f"posp {pos}")
+
+
+def test_decode_is_deterministic(gpu):
+    q, k, v = make_inputs(5, 1, 20000, 32, 4)
+    a = run_decode(q, k, v, 19999, 32, 4, gpu)
+    b = run_decode(q, k, v, 19999, 32, 4, gpu)
+    assert np.array_equal(a, b)
+
+
+def test_decode_causal_within_verify_block(gpu):
+    q, k, v = make_inputs(6, 6, 506, 32, 4)
+    a = run_decode(q, k, v, 500, 32, 4, gpu)
+    k2, v2 = k.copy(), v.copy()
+    k2[503:] = 0x4400
+    v2[503:] = 0xC400
+    b = run_decode(q, k2, v2, 500, 32, 4, gpu)
+    assert np.array_equal(a[:3], b[:3])
+    assert not np.array_equal(a[3:], b[3:])
+
+
+# ---------------------------------------------------------------- prefill
+
+def run_prefill(q, k, v, pos0, n_heads, n_kv, dev, out_dtype=None):
+    qt, kt, vt = to_dev(q, k, v, dev)
+    out = gi_attn.prefill(qt, kt, vt, pos0, n_heads, n_kv, out_dtype=out_dtype)
+    torch.cuda.synchronize()
+    return out.float().cpu().numpy()
+
+
+PREFILL_SHAPES = [
+    # (n, pos0, n_heads, n_kv, q dtype, out dtype)
+    (16, 0, 8, 2, np.float16, torch.float32),
+    (64, 0, 8, 2, np.float16, torch.float32),
+    (100, 0, 4, 1, np.float32, torch.float32),
+    (128, 0, 32, 8, np.float16, torch.float16),
+    (129, 0, 8, 8, np.float16, torch.float32),
+    (300, 0, 32, 4, np.float32, torch.float32),
+    (70, 130, 8, 4, np.float16, torch.float32),
+    (256, 256, 32, 4, np.float16, torch.float16),
+    (1000, 24, 16, 2, np.float16, torch.float32),
+]
+
+
+@pytest.mark.parametrize("n,pos0,n_heads,n_kv,qd,od", PREFILL_SHAPES)
+def test_prefill_small(gpu, n, pos0, n_heads, n_kv, qd, od):
+    say("prefill", n, pos0, n_heads, n_kv, qd.__name__, od)
+    q, k, v = make_inputs(2000 + n + pos0, n, pos0 + n, n_heads, n_kv, q_dtype=qd)
+    got = run_prefill(q, k, v, pos0, n_heads, n_kv, gpu, out_dtype=od)
+    assert_close(got, O.attention(q.astype(np.float32), k, v, pos0, n_heads, n_kv), what="prefill vs oracle")
+    assert_close(got, reference_f64(q, k, v, pos0, n_heads, n_kv), what="prefill vs f64")
+
+
+def torch_reference_prefill(qt, kt, vt, pos0, n_heads, n_kv, hd=128):
+    """fp32 torch reference on the GPU, one head at a time."""
+    n = qt.shape[0]
+    G = n_heads // n_kv
+    out = torch.empty((n, n_heads, hd), dtype=torch.float32, device=qt.device)
+    K = kt.view(-1, n_kv, hd).float()
+    V = vt.view(-1, n_kv, hd).float()
+    Q = qt.view(n, n_heads, hd).float()
+    mask = torch.arange(pos0 + n, device=qt.device)[None, :] > (pos0 + torch.arange(n, device=qt.device))[:, None]
+    for h in range(n_heads):
+        s = (Q[:, h] @ K[: pos0 + n, h // G].T) / math.sqrt(hd)
+        s.masked_fill_(mask, float("-inf"))
+        out[:, h] = torch.softmax(s, dim=-1) @ V[: pos0 + n, h // G]
+    return out.view(n, -1)
+
+
+def test_prefill_config3_8192(gpu):
+    say("prefill C3 8192 32q/8kv f16")
+    n, n_heads, n_kv = 8192, 32, 8
+    q, k, v = make_inputs(3, n, n, n_heads, n_kv, q_dtype=np.float16)
+    qt, kt, vt = to_dev(q, k, v, gpu)
+    out = gi_attn.prefill(qt, kt, vt, 0, n_heads, n_kv, out_dtype=torch.float16)
+    ref = torch_reference_prefill(qt, kt, vt, 0, n_heads, n_kv)
+    torch.cuda.synchronize()
+    got = out.float().cpu().numpy()
+    assert_close(got, ref.cpu().numpy(), what="C3 vs torch fp32")
+    rows = [0, 1, 63, 64, 127, 128, 1000, 4095, 8191]
+    for r in rows:
+        want = reference_f64(q[r:r + 1], k, v, r, n_heads, n_kv)
+        assert_close(got[r:r + 1], want, what=f"C3 row {r} vs f64")
+
+
+def test_chunked_prefill_matches_whole_prompt(gpu):
+    # config 5's pattern at a small size: a prompt in causal chunks against the growing cache equals the
+    # prompt in one call, and both equal the f64 reference
+    n, chunk, n_heads, n_kv = 1536, 512, 32, 4
+    q, k, v = make_inputs(55, n, n, n_heads, n_kv, q_dtype=np.float16)
+    qt, kt, vt = to_dev(q, k, v, gpu)
+    whole = gi_attn.prefill(qt, kt, vt, 0, n_heads, n_kv, out_dtype=torch.float32)
+    parts = []
+    for c0 in range(0, n, chunk):
+        say("chunk at", c0)
+        parts.append(gi_attn.prefill(qt[c0:c0 + chunk], kt, vt, c0, n_heads, n_kv, out_dtype=torch.float32))
+    torch.cuda.synchronize()
+    chunked = torch.cat(parts).cpu().numpy()
+    assert np.array_equal(chunked, whole.cpu().numpy())
+    rows = [0, 511, 512, 1023, 1535]
+    for r in rows:
+        assert_close(chunked[r:r + 1], reference_f64(q[r:r + 1], k, v, r, n_heads, n_kv), what=f"row {r}")
+
+
+def test_chunked_prefill_config5_last_chunk(gpu):
+    # config 5's largest chunk: 2048 queries at pos0 = 129024 against a 131072-key cache (sampled rows)
+    n_heads, n_kv, chunk, ctx = 32, 4, 2048, 131072
+    pos0 = ctx - chunk
+    say("prefill C5 last chunk pos0", pos0)
+    q, k, v = make_inputs(5, chunk, ctx, n_heads, n_kv, q_dtype=np.float16)
+    got = run_prefill(q, k, v, pos0, n_heads, n_kv, gpu, out_dtype=torch.float32)
+    for r in (0, 1, 1023, 2047):
+        assert_close(got[r:r + 1], reference_f64(q[r:r + 1], k, v, pos0 + r, n_heads, n_kv), what=f"row {r}")
+
+
+def test_prefill_and_decode_agree(gpu):
+    # decoding token by token equals one prefill over the same prompt, up to the prefill's f16 P
+    n, n_heads, n_kv = 40, 32, 8
+    q, k, v = make_inputs(66, n, n, n_heads, n_kv)
+    pre = run_prefill(q, k, v, 0, n_heads, n_kv, gpu, out_dtype=torch.float32)
+    dec = np.concatenate([run_decode(q[b:b + 1], k, v, b, n_heads, n_kv, gpu) for b in range(n)])
+    assert_close(pre, dec, what="prefill vs decode")
+
+
+# ---------------------------------------------------------------- the operator (GpuModel::attention)
+
+@pytest.mark.parametrize("n,pos0,exact", [(1, 99, False), (8, 300, True), (20, 0, False), (20, 50, True),
+                                          (40, 17, True)])
+def test_attention_operator_dispatch(gpu, n, pos0, exact):
+    say("operator", n, pos0, exact)
+    n_heads, n_kv, hd = 32, 8, 128
+    row = n_heads * hd + 2 * n_kv * hd
+    rng = np.random.default_rng(90 + n)
+    qkv = rng.standard_normal((n, row), dtype=np.float32)
+    _, k, v = make_inputs(91 + n, 1, pos0 + n, n_heads, n_kv)
+    qkv_t = torch.from_numpy(qkv).to(gpu)
+    _, kt, vt = to_dev(qkv[:, :1], k, v, gpu)
+    out = gi_attn.attention(qkv_t, kt, vt, pos0, n_heads, n_kv, exact=exact)
+    torch.cuda.synchronize()
+    q = np.ascontiguousarray(qkv[:, : n_heads * hd])
+    got = out.cpu().numpy()
+    want = reference_f64(q, k, v, pos0, n_heads, n_kv)
+    split_path = n < 16 or exact
+    assert_close(got, want, max_abs=2e-5 if split_path else 2e-3, rel_l2=2e-5 if split_path else 1e-3,
+                 what="operator vs f64")

@@ -1,0 +1,253 @@
+"""Pins the CPU oracle (oracle/gi_oracle.cpp) before it is trusted as the GPU path's checker.
+
+The reference has no attention test and no golden vector for this path (its tests cover the f16
+conversion only, src/quant.rs:1160-1169). So each oracle function is pinned here by checks a plausible
+mistake (a dropped term, a wrong index, a missing scale, a wrong causal bound) would fail:
+  - the reference's own known values for the f16 conversion, and an exhaustive check against numpy;
+  - an independent float64 softmax attention (tests/attn_common.py) on small shapes;
+  - closed forms: one visible position -> V0; zero keys -> the mean of V; one dominant key -> its V row;
+  - invariants: the split count (thread count) does not change the result; causality; GQA symmetry;
+  - torch's scaled_dot_product_attention as a library cross-check;
+  - the committed golden fixtures (tests/golden/), made by tests/golden/make_golden.py in float64.
+"""
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import gi_oracle as O
+from attn_common import assert_close, errors, make_inputs, reference_f64
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+# ---------------------------------------------------------------- f16 conversion (src/quant.rs:10-60)
+
+def test_f16_known_values_from_reference_test():
+    # src/quant.rs:1160-1169: round trips within 1e-3 relative, exact 0x3c00 -> 1.0 and 0xc000 -> -2.0
+    for v in [0.0, 1.0, -2.5, 0.000061035156, 65504.0, 3.1415927, 1e-7]:
+        back = O.f16_bits_to_f32(O.f32_to_f16_bits(np.array([v], np.float32)))[0]
+        assert abs(back - v) <= abs(v) * 1e-3 + 1e-7, (v, back)
+    assert O.lib().gio_f16_to_f32(0x3C00) == 1.0
+    assert O.lib().gio_f16_to_f32(0xC000) == -2.0
+
+
+def test_f16_to_f32_exhaustive():
+    bits = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    got = O.f16_bits_to_f32(bits)
+    want = bits.view(np.float16).astype(np.float32)
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32))
+
+
+def test_f32_to_f16_round_to_nearest_even():
+    rng = np.random.default_rng(7)
+    x = np.concatenate([
+        rng.standard_normal(200000).astype(np.float32) * np.float32(10.0) ** rng.integers(-9, 6, 200000),
+        # halfway cases between adjacent f16 values (ties to even), subnormals, overflow, specials
+        (np.arange(-2048, 2048, dtype=np.float32) + 0.5) * np.float32(2.0 ** -10),
+        np.float32(2.0 ** -24) * np.arange(0, 64, dtype=np.float32) / 4,
+        np.array([65504, 65519.99, 65520, 1e30, -1e30, np.inf, -np.inf, 0.0, -0.0], np.float32),
+    ]).astype(np.float32)
+    got = O.f32_to_f16_bits(x)
+    want = x.astype(np.float16).view(np.uint16)
+    assert np.array_equal(got, want)
+    nanbits = O.f32_to_f16_bits(np.array([np.nan], np.float32))[0]
+    assert (nanbits & 0x7C00) == 0x7C00 and (nanbits & 0x3FF) != 0
+
+
+def test_dot_f32_lanes():
+    # 8 partial sums then the tail (src/quant.rs:758-768): equal to the exact sum for integer inputs,
+    # and to a float64 dot within f32 rounding for random ones
+    a = np.arange(1, 20, dtype=np.float32)
+    b = np.arange(20, 1, -1, dtype=np.float32)[:19]
+    assert O.dot_f32(a, b) == float(np.dot(a.astype(np.float64), b))
+    rng = np.random.default_rng(3)
+    x, y = rng.standard_normal(131).astype(np.float32), rng.standard_normal(131).astype(np.float32)
+    assert abs(O.dot_f32(x, y) - float(np.dot(x.astype(np.float64), y))) < 1e-4
+    # the lane structure: 8 lanes summed in order, then + tail
+    acc = np.zeros(8, np.float32)
+    for c in range(0, 128, 8):
+        acc += x[c:c + 8] * y[c:c + 8]
+    tail = np.float32(0)
+    for i in range(128, 131):
+        tail = np.float32(tail + x[i] * y[i])
+    s = np.float32(0)
+    for v in acc:
+        s = np.float32(s + v)
+    assert O.dot_f32(x, y) == float(np.float32(s + tail))
+
+
+# ---------------------------------------------------------------- slice arithmetic (src/cuda.rs:1642, 8426-8444)
+
+def test_slice_arithmetic_at_configs():
+    # worked values for the configs: want = ceil(96 / n_kv); chunk = clamp(ceil(span / want), 32, 128)
+    assert O.att_want(8) == 12 and O.att_want(4) == 24
+    assert O.att_chunk(4096, 12) == 128 and -(-4096 // 128) == 32        # C1: nsplit 32
+    assert O.att_chunk(65536, 24) == 128 and -(-65536 // 128) == 512     # C2: nsplit 512
+    assert O.att_chunk(32, 24) == 256 and O.att_chunk(33, 24) == 32     # one block up to 32 positions
+    assert O.att_chunk(1000, 24) == 42
+    # max_splits over spans 1..ctx equals the brute-force maximum
+    for ctx in (1, 31, 32, 33, 100, 777, 4096):
+        want = O.att_want(4)
+        brute = max(-(-s // O.att_chunk(s, want)) for s in range(1, ctx + 1))
+        assert O.max_splits(ctx, want) == brute
+
+
+# ---------------------------------------------------------------- Model::attention (src/model.rs:1320-1409)
+
+SHAPES = [
+    # (n_tok, pos0, n_heads, n_kv)
+    (1, 0, 4, 1),
+    (1, 1, 8, 2),
+    (1, 30, 8, 1),
+    (1, 31, 32, 8),
+    (1, 32, 32, 4),
+    (1, 127, 8, 8),
+    (1, 128, 32, 4),
+    (3, 60, 16, 2),
+    (8, 200, 32, 4),
+    (20, 5, 8, 1),
+]
+
+
+@pytest.mark.parametrize("n_tok,pos0,n_heads,n_kv", SHAPES)
+@pytest.mark.parametrize("threads", [1, 3, 8])
+def test_attention_matches_f64(n_tok, pos0, n_heads, n_kv, threads):
+    q, k, v = make_inputs(11 + pos0, n_tok, pos0 + n_tok, n_heads, n_kv)
+    got = O.attention(q, k, v, pos0, n_heads, n_kv, threads=threads)
+    want = reference_f64(q, k, v, pos0, n_heads, n_kv)
+    assert_close(got, want, max_abs=2e-5, rel_l2=2e-6, what="oracle vs f64")
+
+
+def test_attention_f32_cache_equals_widened_f16_cache():
+    q, k, v = make_inputs(5, 2, 300, 8, 2)
+    a = O.attention(q, k, v, 298, 8, 2)
+    b = O.attention(q, O.f16_bits_to_f32(k), O.f16_bits_to_f32(v), 298, 8, 2)
+    assert np.array_equal(a, b)
+
+
+def test_attention_split_invariance_long():
+    # splits = min(ceil(threads / pairs), ceil(span / 64)): 1, 4 and 16 slices must agree closely
+    q, k, v = make_inputs(21, 1, 4096, 8, 4)
+    outs = [O.attention(q, k, v, 4095, 8, 4, threads=t) for t in (1, 16, 64)]
+    for o in outs[1:]:
+        assert errors(o, outs[0])[0] < 1e-6
+
+
+def test_closed_form_single_position_is_v0():
+    q, k, v = make_inputs(3, 1, 1, 8, 2)
+    out = O.attention(q, k, v, 0, 8, 2).reshape(8, 128)
+    vv = O.f16_bits_to_f32(v).reshape(2, 128)
+    for h in range(8):
+        assert np.array_equal(out[h], vv[h // 4])
+
+
+def test_closed_form_zero_keys_give_mean_of_v():
+    q, k, v = make_inputs(4, 1, 777, 8, 2)
+    k[:] = 0
+    out = O.attention(q, k, v, 776, 8, 2).reshape(8, 128)
+    mean = O.f16_bits_to_f32(v).astype(np.float64).reshape(777, 2, 128).mean(axis=0)
+    for h in range(8):
+        assert np.abs(out[h] - mean[h // 4]).max() < 1e-5
+
+
+def test_closed_form_dominant_key_selects_its_v_row():
+    q, k, v = make_inputs(6, 1, 500, 4, 1)
+    q[:] = 0
+    q[0, :128] = 1.0  # head 0 only
+    kk = k.view(np.float16)
+    kk[:] = 0
+    kk[321, :] = np.float16(8.0)  # score 8*128/sqrt(128) ~ 90.5 above the rest
+    out = O.attention(q, k, v, 499, 4, 1).reshape(4, 128)
+    vv = O.f16_bits_to_f32(v)
+    assert np.abs(out[0] - vv[321]).max() < 1e-6
+
+
+def test_causality():
+    q, k, v = make_inputs(8, 5, 100, 8, 2)
+    a = O.attention(q, k, v, 95, 8, 2)
+    k2, v2 = k.copy(), v.copy()
+    k2[98:] = 0x3C00
+    v2[98:] = 0x4000
+    b = O.attention(q, k2, v2, 95, 8, 2)
+    # tokens at positions 95..97 see keys 0..97 only; tokens 98, 99 see the change
+    assert np.array_equal(a[:3], b[:3])
+    assert not np.array_equal(a[3:], b[3:])
+
+
+def test_gqa_heads_with_equal_queries_agree():
+    q, k, v = make_inputs(9, 1, 333, 8, 2)
+    qq = q.reshape(8, 128)
+    qq[1] = qq[0]
+    qq[5] = qq[4]
+    out = O.attention(q, k, v, 332, 8, 2).reshape(8, 128)
+    assert np.array_equal(out[0], out[1]) and np.array_equal(out[4], out[5])
+    assert not np.array_equal(out[0], out[4])
+
+
+def test_matches_torch_sdpa():
+    n_heads, n_kv, n, pos0 = 8, 2, 40, 24
+    q, k, v = make_inputs(31, n, pos0 + n, n_heads, n_kv)
+    got = O.attention(q, k, v, pos0, n_heads, n_kv)
+    K = torch.from_numpy(O.f16_bits_to_f32(k)).view(-1, n_kv, 128).double()
+    V = torch.from_numpy(O.f16_bits_to_f32(v)).view(-1, n_kv, 128).double()
+    Q = torch.from_numpy(q).view(n, n_heads, 128).double()
+    G = n_heads // n_kv
+    Kx = K.repeat_interleave(G, dim=1).transpose(0, 1)  # [h, t, d]
+    Vx = V.repeat_interleave(G, dim=1).transpose(0, 1)
+    mask = torch.arange(pos0 + n)[None, :] <= (pos0 + torch.arange(n))[:, None]
+    ref = torch.nn.functional.scaled_dot_product_attention(Q.transpose(0, 1), Kx, Vx, attn_mask=mask)
+    ref = ref.transpose(0, 1).reshape(n, -1).numpy()
+    assert_close(got, ref, max_abs=2e-5, rel_l2=2e-6, what="oracle vs sdpa")
+
+
+# ---------------------------------------------------------------- GPU-kernel semantics restatements
+
+@pytest.mark.parametrize("n_tok,pos0,n_heads,n_kv", [(1, 0, 32, 8), (1, 31, 32, 8), (1, 32, 32, 4),
+                                                     (1, 1000, 32, 4), (8, 4000, 32, 4), (3, 129, 16, 8)])
+def test_decode_gpu_semantics_matches_f64(n_tok, pos0, n_heads, n_kv):
+    q, k, v = make_inputs(41 + pos0, n_tok, pos0 + n_tok, n_heads, n_kv)
+    got = O.decode_gpu_semantics(q, k, v, pos0, n_heads, n_kv)
+    want = reference_f64(q, k, v, pos0, n_heads, n_kv)
+    assert_close(got, want, max_abs=2e-5, rel_l2=2e-6, what="decode semantics vs f64")
+
+
+def test_decode_gpu_semantics_butterfly_score_is_a_dot():
+    # one position: out = V0 whatever the score; two positions with equal keys: the mean of both values
+    q, k, v = make_inputs(2, 1, 2, 8, 1)
+    k[1] = k[0]
+    out = O.decode_gpu_semantics(q, k, v, 1, 8, 1).reshape(8, 128)
+    vv = O.f16_bits_to_f32(v).astype(np.float64)
+    assert np.abs(out - (vv[0] + vv[1]) / 2).max() < 1e-6
+
+
+@pytest.mark.parametrize("n,pos0,n_heads,n_kv", [(64, 0, 8, 2), (100, 0, 4, 1), (70, 130, 8, 4)])
+def test_prefill_tc_semantics_within_parity_bar(n, pos0, n_heads, n_kv):
+    # the reference's tensor-core prefill rounds Q*scale*log2e and P to f16: within the north star's bar of
+    # the exact result, but not equal to it
+    q, k, v = make_inputs(51 + n, n, pos0 + n, n_heads, n_kv)
+    got = O.prefill_tc_semantics(q, k, v, pos0, n_heads, n_kv)
+    want = reference_f64(q, k, v, pos0, n_heads, n_kv)
+    ma, rl = assert_close(got, want, what="prefill_tc semantics vs f64")
+    assert ma > 1e-6  # the f16 roundings are visible
+
+
+# ---------------------------------------------------------------- golden fixtures
+
+def _golden_files():
+    return sorted(f for f in os.listdir(GOLDEN) if f.endswith(".npz"))
+
+
+def test_golden_fixtures_exist():
+    assert len(_golden_files()) >= 4
+
+
+@pytest.mark.parametrize("name", _golden_files() if os.path.isdir(GOLDEN) else [])
+def test_oracle_against_golden(name):
+    z = np.load(os.path.join(GOLDEN, name))
+    n_heads, n_kv, pos0 = int(z["n_heads"]), int(z["n_kv"]), int(z["pos0"])
+    got = O.attention(z["q"].astype(np.float32), z["k"], z["v"], pos0, n_heads, n_kv)
+    assert_close(got, z["out"], max_abs=2e-5, rel_l2=2e-6, what=name)
