@@ -37,9 +37,12 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def seeded_cache(gen, rows, n_kv, dev, torch):
-    k = torch.randn((rows, n_kv, HD), generator=gen, device=dev, dtype=torch.float32).half()
-    v = torch.randn((rows, n_kv, HD), generator=gen, device=dev, dtype=torch.float32).half()
+def seeded_cache(gen, rows, n_kv, dev, torch, layout="reference"):
+    """K and V caches of N(0,1) f16 values: [rows, n_kv, HD] (the reference's layout) or [n_kv, rows, HD]
+    (head-major, each kv head's rows contiguous)."""
+    shape = (rows, n_kv, HD) if layout == "reference" else (n_kv, rows, HD)
+    k = torch.randn(shape, generator=gen, device=dev, dtype=torch.float32).half()
+    v = torch.randn(shape, generator=gen, device=dev, dtype=torch.float32).half()
     return k, v
 
 
@@ -61,12 +64,34 @@ def time_steps(fn, steps, warmup, torch):
 
 # ---------------------------------------------------------------- workloads
 
-def decode_workload(torch, gi_attn, dev, ctx, n_heads, n_kv, n_tok, steps, warmup, seed):
+def time_steps_graph(fn, steps, warmup, torch):
+    """As time_steps, but the `steps` timed steps are captured once into a HIP graph and replayed, as the
+    reference replays its one-token decode step (src/cuda.rs:8686-8712): the time is the GPU's, not the
+    Python launch path's. The graph is replayed once untimed (upload) before the timed replay."""
+    for i in range(warmup):
+        fn(i)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for i in range(steps):
+            fn(i)
+    g.replay()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    g.replay()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / 1e3 / steps
+
+
+def decode_workload(torch, gi_attn, dev, ctx, n_heads, n_kv, n_tok, steps, warmup, seed, layout="head_major"):
     gen = torch.Generator(device=dev)
     gen.manual_seed(seed)
     cache_bytes = 2 * ctx * n_kv * HD * 2
     layers = max(1, math.ceil(512e6 / cache_bytes))  # > 256 MB Infinity Cache in total
-    caches = [seeded_cache(gen, ctx, n_kv, dev, torch) for _ in range(layers)]
+    caches = [seeded_cache(gen, ctx, n_kv, dev, torch, layout) for _ in range(layers)]
     q = torch.randn((n_tok, n_heads * HD), generator=gen, device=dev, dtype=torch.float32)
     out = torch.empty((n_tok, n_heads * HD), device=dev, dtype=torch.float32)
     pos0 = ctx - n_tok
@@ -74,11 +99,12 @@ def decode_workload(torch, gi_attn, dev, ctx, n_heads, n_kv, n_tok, steps, warmu
 
     def step(i):
         k, v = caches[i % layers]
-        gi_attn.decode(q, k, v, pos0, n_heads, n_kv, out=out, workspace=ws)
+        gi_attn.decode(q, k, v, pos0, n_heads, n_kv, out=out, workspace=ws, kv_layout=layout)
 
-    t = time_steps(step, steps, warmup, torch)
+    t = time_steps_graph(step, steps, warmup, torch)
     algo_bytes = 2 * ctx * n_kv * HD * 2
-    return {"seconds": t, "bytes": algo_bytes, "layers": layers, "q": q, "cache": caches[0], "pos0": pos0}
+    return {"seconds": t, "bytes": algo_bytes, "layers": layers, "q": q, "cache": caches[0], "pos0": pos0,
+            "layout": layout}
 
 
 def prefill_flops(n, pos0, n_heads):
@@ -146,8 +172,11 @@ def cpu_baseline_decode(q, cache, pos0, n_heads, n_kv, budget_s=12.0):
 
     threads = min(16, os.cpu_count() or 1)
     qn = q.cpu().numpy()
-    kn = cache[0].cpu().numpy().view(np.uint16).reshape(cache[0].shape[0], -1)
-    vn = cache[1].cpu().numpy().view(np.uint16).reshape(cache[1].shape[0], -1)
+    k, v = cache
+    if k.shape[0] == n_kv and k.dim() == 3 and k.shape[1] != n_kv:  # head-major: to the reference's layout
+        k, v = k.transpose(0, 1).contiguous(), v.transpose(0, 1).contiguous()
+    kn = k.cpu().numpy().view(np.uint16).reshape(k.shape[0], -1)
+    vn = v.cpu().numpy().view(np.uint16).reshape(v.shape[0], -1)
     gi_oracle.attention(qn, kn, vn, pos0, n_heads, n_kv, threads=threads)  # warm-up (also builds tables)
     times = []
     t_end = time.time() + budget_s
@@ -194,15 +223,23 @@ def main():
         log(f"[bench] {cfg}")
         r = decode_workload(torch, gi_attn, dev, ctx, n_heads, n_kv, n_tok, args.steps, args.warmup, 1234)
         gbs = r["bytes"] / r["seconds"] / 1e9
+        r_ref = decode_workload(torch, gi_attn, dev, ctx, n_heads, n_kv, n_tok, args.steps, args.warmup, 1234,
+                                layout="reference")
+        gbs_ref = r_ref["bytes"] / r_ref["seconds"] / 1e9
+        r_ref_ms = r_ref["seconds"] * 1e3
+        del r_ref
         chunk, nsplit = gi_attn.decode_plan(ctx, n_tok, n_heads, n_kv)
         result.update({
             "value": round(gbs, 1), "unit": "GB/s", "ms_per_step": r["seconds"] * 1e3, "dtype": "f16 K/V, f32 math",
             "config": {"workload": cfg, "ctx": ctx, "n_tok": n_tok, "n_heads": n_heads, "n_kv": n_kv, "hd": HD,
                        "kv_bytes_per_step": r["bytes"], "layers_rotated": r["layers"],
-                       "slices": nsplit, "keys_per_slice": chunk},
+                       "slices": nsplit, "keys_per_slice": chunk, "kv_layout": "head_major [n_kv][ctx][128]",
+                       "reference_layout_GBs": round(gbs_ref, 1),
+                       "reference_layout_ms_per_step": r_ref_ms},
             "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
-                         "note": "achieved = K+V bytes / decode step time (split kernel + combine kernel)"},
+                         "note": "achieved = K+V bytes / decode step time (split kernel + combine kernel), "
+                                 "steps replayed from a HIP graph"},
         })
         if not args.no_cpu_baseline:
             log("[bench] cpu baseline (oracle, Model::attention restatement)")

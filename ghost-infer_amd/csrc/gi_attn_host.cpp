@@ -31,6 +31,7 @@ struct GiDecodeArgs {
     long long q_stride;
     long long kv_stride;
     long long out_stride;
+    long long kv_head_stride;
     int pos0;
     int n_tok;
     int n_heads;
@@ -50,6 +51,7 @@ struct GiPrefillArgs {
     long long q_stride;
     long long kv_stride;
     long long out_stride;
+    long long kv_head_stride;
     int pos0;
     int n;
     int n_heads;
@@ -62,7 +64,7 @@ struct GiPrefillArgs {
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kMaxDevices = 64;
-constexpr int kDecWaves = 4, kDecTile = 32, kDecPairs = 8;
+constexpr int kDecWaves = 4, kDecTile = 32, kDecPairs = 8, kDecPart = 132; // kDecPart: floats per slice partial
 constexpr int kSliceUnit = kDecWaves * kDecTile; // 128 keys
 constexpr int kPrefillBQ = 128;                   // query rows per prefill workgroup
 constexpr int kSplitMaxBatch = 15;                // tokens per split launch (src/cuda.rs:119)
@@ -166,6 +168,18 @@ void plan(int max_span, int n_tok, int n_heads, int n_kv, int* chunk, int* nspli
     *nsplit = std::max(1, (max_span + *chunk - 1) / *chunk);
 }
 
+// K/V rows of 128 elements must not overlap: either positions outer (kv_stride covers all heads) or heads
+// outer (a head's block holds whole rows); both strides in 16-byte units.
+int check_kv_strides(long long kv_stride, long long kv_head_stride, int n_kv, int hd) {
+    if (kv_stride % 8 || kv_head_stride % 8 || kv_stride <= 0 || kv_head_stride <= 0)
+        return fail("kv_stride %lld and kv_head_stride %lld must be positive multiples of 8", kv_stride, kv_head_stride);
+    bool pos_outer = kv_head_stride >= hd && kv_stride >= (long long)n_kv * kv_head_stride;
+    bool head_outer = kv_stride >= hd && (n_kv == 1 || kv_head_stride >= kv_stride);
+    if (!pos_outer && !head_outer)
+        return fail("kv_stride %lld / kv_head_stride %lld overlap rows of %d kv heads", kv_stride, kv_head_stride, n_kv);
+    return 0;
+}
+
 int check_shape(int n_heads, int n_kv, int hd) {
     if (hd != 128) return fail("head size %d unsupported (the gfx950 kernels take 128)", hd);
     if (n_kv <= 0 || n_heads <= 0 || n_heads % n_kv != 0)
@@ -204,21 +218,24 @@ size_t gi_attn_decode_workspace_bytes(int ctx_cap, int n_tok, int n_heads, int n
         int groups = (t * G + kDecPairs * ncb - 1) / (kDecPairs * ncb);
         int per_slot = std::max(1, decode_target_wgs() / std::max(1, n_kv * groups));
         int most = std::max(1, std::min(per_slot, (ctx_cap + kSliceUnit - 1) / kSliceUnit));
-        best = std::max(best, (size_t)t * n_heads * most * (hd + 2) * sizeof(float));
+        best = std::max(best, (size_t)t * n_heads * most * kDecPart * sizeof(float));
     }
     return best;
 }
 
 int gi_attn_decode(void* stream, const float* q, long long q_stride, const uint16_t* kc, const uint16_t* vc,
-                   long long kv_stride, float* out, long long out_stride, void* workspace, size_t workspace_bytes,
-                   int pos0, const int* posp, int ctx_cap, int n_tok, int n_heads, int n_kv, int hd, float scale) {
+                   long long kv_stride, long long kv_head_stride, float* out, long long out_stride, void* workspace,
+                   size_t workspace_bytes, int pos0, const int* posp, int ctx_cap, int n_tok, int n_heads, int n_kv,
+                   int hd, float scale) {
     if (int e = check_shape(n_heads, n_kv, hd)) return e;
     if (n_tok <= 0) return fail("n_tok %d must be positive", n_tok);
     if (!q || !kc || !vc || !out) return fail("null tensor pointer");
-    if (!aligned16(q) || !aligned16(kc) || !aligned16(vc) || q_stride % 4 || kv_stride % 8)
-        return fail("q, kc, vc must be 16-byte aligned, q_stride a multiple of 4 and kv_stride of 8");
-    if (kv_stride < (long long)n_kv * hd || q_stride < (long long)n_heads * hd || out_stride < (long long)n_heads * hd)
-        return fail("row strides too small for %d heads / %d kv heads", n_heads, n_kv);
+    if (kv_head_stride == 0) kv_head_stride = hd;
+    if (int e = check_kv_strides(kv_stride, kv_head_stride, n_kv, hd)) return e;
+    if (!aligned16(q) || !aligned16(kc) || !aligned16(vc) || q_stride % 4)
+        return fail("q, kc, vc must be 16-byte aligned and q_stride a multiple of 4");
+    if (q_stride < (long long)n_heads * hd || out_stride < (long long)n_heads * hd)
+        return fail("row strides too small for %d heads", n_heads);
     if (!posp && pos0 < 0) return fail("pos0 %d must be >= 0", pos0);
     int max_span = posp ? ctx_cap : pos0 + n_tok;
     if (posp && ctx_cap < n_tok) return fail("ctx_cap %d must cover the %d tokens", ctx_cap, n_tok);
@@ -229,7 +246,7 @@ int gi_attn_decode(void* stream, const float* q, long long q_stride, const uint1
     int groups = (n_tok * G + kDecPairs * ncb - 1) / (kDecPairs * ncb);
     GiDecodeArgs a{};
     plan(max_span, n_tok, n_heads, n_kv, &a.chunk, &a.nsplit);
-    size_t need = a.nsplit == 1 ? 0 : (size_t)n_tok * n_heads * a.nsplit * (hd + 2) * sizeof(float);
+    size_t need = a.nsplit == 1 ? 0 : (size_t)n_tok * n_heads * a.nsplit * kDecPart * sizeof(float);
     if (need && (!workspace || workspace_bytes < need))
         return fail("workspace of %zu bytes too small: %zu needed", workspace_bytes, need);
     a.q = q;
@@ -241,6 +258,7 @@ int gi_attn_decode(void* stream, const float* q, long long q_stride, const uint1
     a.q_stride = q_stride;
     a.kv_stride = kv_stride;
     a.out_stride = out_stride;
+    a.kv_head_stride = kv_head_stride;
     a.pos0 = pos0;
     a.n_tok = n_tok;
     a.n_heads = n_heads;
@@ -250,23 +268,25 @@ int gi_attn_decode(void* stream, const float* q, long long q_stride, const uint1
     if (int e = launch(ncb == 2 ? m->dec2 : m->dec1, dim3(a.nsplit, n_kv, groups), dim3(256), st, &a, sizeof a))
         return e;
     if (a.nsplit > 1)
-        if (int e = launch(m->combine, dim3(n_heads, n_tok, 1), dim3(128), st, &a, sizeof a)) return e;
+        if (int e = launch(m->combine, dim3(n_heads, n_tok, 1), dim3(256), st, &a, sizeof a)) return e;
     return 0;
 }
 
 int gi_attn_prefill(void* stream, const void* q, int q_dtype, long long q_stride, const uint16_t* kc,
-                    const uint16_t* vc, long long kv_stride, void* out, int out_dtype, long long out_stride, int pos0,
-                    int n, int n_heads, int n_kv, int hd, float scale) {
+                    const uint16_t* vc, long long kv_stride, long long kv_head_stride, void* out, int out_dtype,
+                    long long out_stride, int pos0, int n, int n_heads, int n_kv, int hd, float scale) {
     if (int e = check_shape(n_heads, n_kv, hd)) return e;
     if (n <= 0 || pos0 < 0) return fail("n %d must be positive and pos0 %d >= 0", n, pos0);
     if (!q || !kc || !vc || !out) return fail("null tensor pointer");
     if ((q_dtype != GI_F32 && q_dtype != GI_F16) || (out_dtype != GI_F32 && out_dtype != GI_F16))
         return fail("dtypes must be GI_F32 or GI_F16");
-    if (!aligned16(q) || !aligned16(kc) || !aligned16(vc) || !aligned16(out) || kv_stride % 8 ||
+    if (kv_head_stride == 0) kv_head_stride = hd;
+    if (int e = check_kv_strides(kv_stride, kv_head_stride, n_kv, hd)) return e;
+    if (!aligned16(q) || !aligned16(kc) || !aligned16(vc) || !aligned16(out) ||
         q_stride % (q_dtype == GI_F16 ? 8 : 4) || out_stride % (out_dtype == GI_F16 ? 8 : 4))
         return fail("tensors must be 16-byte aligned with row strides of whole 16-byte units");
-    if (kv_stride < (long long)n_kv * hd || q_stride < (long long)n_heads * hd || out_stride < (long long)n_heads * hd)
-        return fail("row strides too small for %d heads / %d kv heads", n_heads, n_kv);
+    if (q_stride < (long long)n_heads * hd || out_stride < (long long)n_heads * hd)
+        return fail("row strides too small for %d heads", n_heads);
     Module* m;
     if (int e = load_module(nullptr, &m)) return e;
     GiPrefillArgs a{};
@@ -277,6 +297,7 @@ int gi_attn_prefill(void* stream, const void* q, int q_dtype, long long q_stride
     a.q_stride = q_stride;
     a.kv_stride = kv_stride;
     a.out_stride = out_stride;
+    a.kv_head_stride = kv_head_stride;
     a.pos0 = pos0;
     a.n = n;
     a.n_heads = n_heads;
@@ -297,14 +318,14 @@ int gi_attention(void* stream, const float* qkv, const uint16_t* kc, const uint1
     const float scale = 1.0f / std::sqrt((float)hd);
     if (n >= kTiledMinBatch && !exact) {
         if (posp) return fail("a device position (posp) is only taken by the split path");
-        return gi_attn_prefill(stream, qkv, GI_F32, row, kc, vc, kv_dim, out, GI_F32, q_dim, pos0, n, n_heads, n_kv,
-                               hd, scale);
+        return gi_attn_prefill(stream, qkv, GI_F32, row, kc, vc, kv_dim, hd, out, GI_F32, q_dim, pos0, n, n_heads,
+                               n_kv, hd, scale);
     }
     for (int b0 = 0; b0 < n; b0 += kSplitMaxBatch) {
         int m = std::min(n - b0, kSplitMaxBatch);
         // with a device position every launch reads *posp, so only single launches take it
         if (posp && n > kSplitMaxBatch) return fail("posp takes at most %d tokens", kSplitMaxBatch);
-        if (int e = gi_attn_decode(stream, qkv + b0 * row, row, kc, vc, kv_dim, out + b0 * q_dim, q_dim, workspace,
+        if (int e = gi_attn_decode(stream, qkv + b0 * row, row, kc, vc, kv_dim, hd, out + b0 * q_dim, q_dim, workspace,
                                    workspace_bytes, pos0 + b0, posp, ctx_cap, m, n_heads, n_kv, hd, scale))
             return e;
     }

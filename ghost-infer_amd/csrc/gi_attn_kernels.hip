@@ -2,8 +2,11 @@
 // grouped-query f16 KV cache. Built offline into a code object (gi_attn_gfx950.hsaco) that the C-ABI
 // library (gi_attn_host.cpp) loads with hipModuleLoad and launches by name.
 //
-// Cache layout (as the reference keeps it, src/cuda.rs:365-369, src/cuda.rs:10229-10242): K and V are
-// separate buffers of rows [position][kv head][128] f16, kv_stride elements per position.
+// Cache layout: K and V are separate f16 buffers; key/value t of kv head h starts at element
+// t*kv_stride + h*kv_head_stride. The reference's layout (src/cuda.rs:365-369, src/cuda.rs:10229-10242) is
+// [position][kv head][128] (kv_stride = n_kv*128, kv_head_stride = 128); the head-major layout
+// [kv head][position][128] (kv_stride = 128, kv_head_stride = capacity*128) keeps each head contiguous,
+// which streams evenly over the HBM channels.
 //
 // Decode (reference semantics: attention_partial_gqa + attention_combine, src/cuda.rs:1684-1865,
 // src/cuda.rs:2806-2836). One workgroup of 4 waves per (context slice, kv head, group of query
@@ -39,12 +42,13 @@ struct GiDecodeArgs {
     const float* q;        // query rows: token b's head h at q + b*q_stride + h*128 (f32)
     const uint16_t* kc;    // K cache [pos][n_kv][128] f16, kv_stride elements per position
     const uint16_t* vc;    // V cache, same layout
-    float* part;           // slice partials [token][head][nsplit][130]: O (128), max (base 2), sum
+    float* part;           // slice partials [token][head][nsplit][DEC_PART]: O (128), max (base 2), sum
     float* out;            // output rows: token b's head h at out + b*out_stride + h*128 (f32)
     const int* posp;       // device position (overrides pos0 when non-null)
     long long q_stride;
     long long kv_stride;
     long long out_stride;
+    long long kv_head_stride;
     int pos0;              // position of token 0: token b attends to keys 0..pos0+b
     int n_tok;
     int n_heads;
@@ -58,49 +62,91 @@ struct GiDecodeArgs {
 #define DEC_WAVES 4
 #define DEC_TILE 32
 #define DEC_PAIRS 8 // (token, head) pairs per column block of 16 columns
+#define DEC_RESCALE_LOG2 8.0f
+#define DEC_PART 132 // floats per slice partial: O (128), max (base 2), sum, 2 pad (16-byte rows)
+#define GI_RSRC_FLAGS 0x00020000
 
 __device__ __forceinline__ float wave_xor(float v, int m) { return __shfl_xor(v, m, 64); }
+// v of lane l ^ 1 (DPP quad permutation, no LDS round trip)
+__device__ __forceinline__ float lane_xor1(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, false));
+}
+// max / sum of v over lanes l, l^16, l^32, l^48 (the four 16-lane rows), left in every lane: the
+// permlane swaps pair row r of one copy with row r^2 (32-swap) or r^1 (16-swap) of the other
+__device__ __forceinline__ float rows_max(float v) {
+    auto p = __builtin_amdgcn_permlane32_swap(__float_as_int(v), __float_as_int(v), false, false);
+    v = fmaxf(__int_as_float(p[0]), __int_as_float(p[1]));
+    auto q = __builtin_amdgcn_permlane16_swap(__float_as_int(v), __float_as_int(v), false, false);
+    return fmaxf(__int_as_float(q[0]), __int_as_float(q[1]));
+}
+__device__ __forceinline__ float rows_sum(float v) {
+    auto p = __builtin_amdgcn_permlane32_swap(__float_as_int(v), __float_as_int(v), false, false);
+    v = __int_as_float(p[0]) + __int_as_float(p[1]);
+    auto q = __builtin_amdgcn_permlane16_swap(__float_as_int(v), __float_as_int(v), false, false);
+    return __int_as_float(q[0]) + __int_as_float(q[1]);
+}
+
+// Buffer resource over `bytes` bytes from p: loads at offsets >= bytes return zeros without touching memory.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t gi_rsrc(const void* p, long long bytes) {
+    int n = (int)(bytes < 0 ? 0 : (bytes > 0x7ffffff0ll ? 0x7ffffff0ll : bytes));
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, n, GI_RSRC_FLAGS);
+}
+__device__ __forceinline__ u4 gi_load16(__amdgpu_buffer_rsrc_t r, int off) {
+    return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+}
 
 // Lane l of a wave: c = l % 16 (MFMA column / A-row), grp = l / 16 (k-group of 8).
 template <int NCB>
 __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int c = lane & 15, grp = lane >> 4;
     const int s = blockIdx.x, kvh = blockIdx.y;
+#ifdef GI_DEC_TIMESTAMPS
+    unsigned long long ts[8];
+    ts[0] = wall_clock64();
+#define GI_TS(i) ts[i] = wall_clock64()
+#else
+#define GI_TS(i)
+#endif
     const int pos0 = a.posp ? *a.posp : a.pos0;
     const int G = a.n_heads / a.n_kv;
     const int npairs = a.n_tok * G;
     const int pair0 = blockIdx.z * (DEC_PAIRS * NCB);
     const int kv_len = pos0 + a.n_tok; // keys any token of the launch may see
     const int k_begin = s * a.chunk;
-    const int k_end = min(k_begin + a.chunk, kv_len);
+    const int nkeys = min(a.chunk, kv_len - k_begin); // keys of this slice (<= 0: an empty slice)
 
-    // this lane's column(s): pair and hi/lo half; span of the pair's token
-    int span[NCB];
+    // this lane's column(s): pair and hi/lo half; span of the pair's token, relative to the slice
+    int span[NCB], qoff[NCB];
     bool valid[NCB];
-    h8 qf[NCB][4]; // B operand of S^T = K Qc^T: k-step kk covers dims 32kk..32kk+31, this lane dims 32kk+8grp..+7
 #pragma unroll
     for (int cb = 0; cb < NCB; cb++) {
         int pi = pair0 + cb * DEC_PAIRS + (c >> 1);
         valid[cb] = pi < npairs;
         int t = valid[cb] ? pi / G : 0, g = valid[cb] ? pi % G : 0;
-        span[cb] = valid[cb] ? pos0 + t + 1 : 0;
-        const float* qrow = a.q + (long long)t * a.q_stride + (long long)(kvh * G + g) * 128;
-#pragma unroll
-        for (int kk = 0; kk < 4; kk++) {
-            const float4* qp = reinterpret_cast<const float4*>(qrow + 32 * kk + 8 * grp);
-            float4 x0 = valid[cb] ? qp[0] : make_float4(0.f, 0.f, 0.f, 0.f);
-            float4 x1 = valid[cb] ? qp[1] : make_float4(0.f, 0.f, 0.f, 0.f);
-            float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-#pragma unroll
-            for (int e = 0; e < 8; e++) {
-                float v = xs[e] * a.qscale;
-                _Float16 hi = (_Float16)v;
-                qf[cb][kk][e] = (c & 1) ? (_Float16)(v - (float)hi) : hi;
-            }
-        }
+        span[cb] = valid[cb] ? min(pos0 + t + 1 - k_begin, nkeys) : 0; // keys of the slice this column sees
+        qoff[cb] = ((int)(t * a.q_stride) + (kvh * G + g) * 128 + 8 * grp) * 4;
     }
-
+    // smallest span among the wave's valid columns (the lowest token's: column 0 of block 0 is always valid):
+    // tiles below it need no masking
+    const int span_lo = min(pos0 + pair0 / G + 1 - k_begin, nkeys);
+    // Q rows (f32, 8 dims per lane per k-step), issued before the first K/V tiles so that waiting for them
+    // leaves the K/V loads in flight
+    u4 qraw[NCB][4][2];
+    h8 qf[NCB][4]; // B operand of S^T = K Qc^T: k-step kk covers dims 32kk..32kk+31, this lane dims 32kk+8grp..+7
+    {
+        __amdgpu_buffer_rsrc_t rq = gi_rsrc(a.q, (long long)a.n_tok * a.q_stride * 4);
+#pragma unroll
+        for (int cb = 0; cb < NCB; cb++)
+#pragma unroll
+            for (int kk = 0; kk < 4; kk++) {
+                qraw[cb][kk][0] = gi_load16(rq, qoff[cb] + 128 * kk);
+                qraw[cb][kk][1] = gi_load16(rq, qoff[cb] + 128 * kk + 16);
+            }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    GI_TS(1);
     float m_run[NCB], l_run[NCB];
     f4 o[NCB][8]; // O^T: MFMA dd holds rows m = dims 8m + dd; this lane rows 4grp..4grp+3 -> dims 32grp + 8j + dd
 #pragma unroll
@@ -111,135 +157,224 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
         for (int dd = 0; dd < 8; dd++) o[cb][dd] = f4{0.f, 0.f, 0.f, 0.f};
     }
 
+    // Loads go through buffer resources that start at the wave's current tile and end at the slice's last
+    // key: offsets are 32-bit per lane, constant across tiles, and keys past the end read as zeros. Two
+    // register buffers (X, Y) keep two tiles in flight per wave: a buffer is refilled with the tile two
+    // ahead as soon as its data is consumed (K after the QK MFMAs, V after its transpose).
     const long long kvs = a.kv_stride;
-    const uint16_t* kbase = a.kc + (long long)kvh * 128;
-    const uint16_t* vbase = a.vc + (long long)kvh * 128;
+    const uint16_t* kslice = a.kc + (long long)k_begin * kvs + kvh * a.kv_head_stride;
+    const uint16_t* vslice = a.vc + (long long)k_begin * kvs + kvh * a.kv_head_stride;
     // A-row r = c of S^T block b holds tile key 8*(c/4) + 4b + c%4; V: this lane loads keys 8grp+i, dims 8c..8c+7
     const int krow0 = 8 * (c >> 2) + (c & 3);
+    const int koff0 = (krow0 * (int)kvs + 8 * grp) * 2;
+    const int koff1 = koff0 + 4 * (int)kvs * 2;
+    const int voff = (8 * grp * (int)kvs + 8 * c) * 2;
+    const int vstep = (int)kvs * 2;
+    constexpr int STRIDE = DEC_WAVES * DEC_TILE; // keys between a wave's consecutive tiles
 
-    for (int t0 = k_begin + wave * DEC_TILE; t0 < k_end; t0 += DEC_WAVES * DEC_TILE) {
-        // ---- loads: K (2 blocks x 4 k-steps), V (8 keys), 16 bytes each; zeros past the keys in use
-        u4 kw[2][4], vw[8];
+    struct Buf { u4 k[2][4]; u4 v[8]; };
+    auto load_k = [&](Buf& B, int t) {
+        __amdgpu_buffer_rsrc_t r = gi_rsrc(kslice + (long long)t * kvs, (long long)(nkeys - t) * kvs * 2);
 #pragma unroll
-        for (int b = 0; b < 2; b++) {
-            int key = t0 + krow0 + 4 * b;
-            const u4* kp = reinterpret_cast<const u4*>(kbase + (long long)key * kvs + 8 * grp);
-#pragma unroll
-            for (int kk = 0; kk < 4; kk++) kw[b][kk] = key < k_end ? kp[4 * kk] : u4{0u, 0u, 0u, 0u};
+        for (int kk = 0; kk < 4; kk++) {
+            B.k[0][kk] = gi_load16(r, koff0 + 64 * kk);
+            B.k[1][kk] = gi_load16(r, koff1 + 64 * kk);
         }
+    };
+    auto load_v = [&](Buf& B, int t) {
+        __amdgpu_buffer_rsrc_t r = gi_rsrc(vslice + (long long)t * kvs, (long long)(nkeys - t) * kvs * 2);
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
-            int key = t0 + 8 * grp + i;
-            vw[i] = key < k_end ? *reinterpret_cast<const u4*>(vbase + (long long)key * kvs + 8 * c) : u4{0u, 0u, 0u, 0u};
-        }
-        // ---- V^T: vt[dd] = the 8 keys' values of dim 8c + dd
-        h8 vt[8];
+        for (int i = 0; i < 8; i++) B.v[i] = gi_load16(r, voff + i * vstep);
+    };
+    // One tile from buffer B at key offset t; with `reload`, B is refilled with the tile at t + 2*STRIDE.
+    auto process = [&](Buf& B, int t, bool reload) {
+        __builtin_amdgcn_sched_barrier(0); // keep tiles in order: each waits only for its own buffer
+        f4 sacc[NCB][2];
 #pragma unroll
-        for (int dd = 0; dd < 8; dd++) {
-            u4 w;
-#pragma unroll
-            for (int p = 0; p < 4; p++) {
-                uint32_t lo = vw[2 * p][dd >> 1], hi = vw[2 * p + 1][dd >> 1];
-                w[p] = (dd & 1) ? ((lo >> 16) | (hi & 0xffff0000u)) : ((lo & 0xffffu) | (hi << 16));
-            }
-            vt[dd] = __builtin_bit_cast(h8, w);
-        }
-#pragma unroll
-        for (int cb = 0; cb < NCB; cb++) {
-            // ---- S^T blocks: this lane gets column c, tile keys 8grp + 4b + j
-            f4 sacc[2];
+        for (int cb = 0; cb < NCB; cb++)
 #pragma unroll
             for (int b = 0; b < 2; b++) {
-                sacc[b] = f4{0.f, 0.f, 0.f, 0.f};
+                sacc[cb][b] = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                 for (int kk = 0; kk < 4; kk++)
-                    sacc[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, kw[b][kk]), qf[cb][kk], sacc[b], 0, 0, 0);
+                    sacc[cb][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, B.k[b][kk]), qf[cb][kk],
+                                                                         sacc[cb][b], 0, 0, 0);
             }
+        if (reload) load_k(B, t + 2 * STRIDE);
+        __builtin_amdgcn_sched_barrier(0);
+        const bool masked = t + DEC_TILE > span_lo; // some valid column sees only part of this tile
+        h8 pf[NCB];
+#pragma unroll
+        for (int cb = 0; cb < NCB; cb++) {
+            // this lane: column c, tile keys 8grp + 4b + j
             float sc[8], mx = GI_NEG_INF;
 #pragma unroll
             for (int b = 0; b < 2; b++)
 #pragma unroll
                 for (int j = 0; j < 4; j++) {
-                    float v = sacc[b][j];
-                    v = v + wave_xor(v, 1); // hi + lo columns of the pair (same sum in both lanes)
-                    int key = t0 + 8 * grp + 4 * b + j;
-                    v = key < span[cb] ? v : GI_NEG_INF;
+                    float v = sacc[cb][b][j];
+                    v = v + lane_xor1(v); // hi + lo columns of the pair (same sum in both lanes)
+                    if (masked) {
+                        int key = t + 8 * grp + 4 * b + j;
+                        v = key < span[cb] ? v : GI_NEG_INF;
+                    }
                     sc[4 * b + j] = v;
                     mx = fmaxf(mx, v);
                 }
-            mx = fmaxf(mx, wave_xor(mx, 16));
-            mx = fmaxf(mx, wave_xor(mx, 32));
-            float m_new = fmaxf(m_run[cb], mx);
-            float m_use = m_new == GI_NEG_INF ? 0.f : m_new; // nothing seen yet: keep everything at zero
-            float alpha = exp2f(m_run[cb] - m_use);
-            m_run[cb] = m_new;
+            mx = rows_max(mx);
+            // the column's reference max moves only when a score exceeds it by more than 2^8 in probability:
+            // P <= 256 is exact enough in the f16 hi/lo split, and most tiles skip rescaling O
+            const bool up = mx > m_run[cb] + DEC_RESCALE_LOG2;
+            if (__builtin_amdgcn_ballot_w64(up)) {
+                const float m_new = up ? mx : m_run[cb];
+                const float alpha = __builtin_amdgcn_exp2f(m_run[cb] - m_new); // 0 when nothing was seen yet
+                m_run[cb] = m_new;
+                l_run[cb] *= alpha;
+#pragma unroll
+                for (int dd = 0; dd < 8; dd++) o[cb][dd] *= alpha;
+            }
+            const float m_use = m_run[cb] == GI_NEG_INF ? 0.f : m_run[cb]; // no key seen yet: p = 0
             float psum = 0.f;
-            h8 pf;
 #pragma unroll
             for (int i = 0; i < 8; i++) {
-                float p = exp2f(sc[i] - m_use);
+                float p = __builtin_amdgcn_exp2f(sc[i] - m_use);
                 psum += p;
                 _Float16 hi = (_Float16)p;
-                pf[i] = (c & 1) ? (_Float16)(p - (float)hi) : hi;
+                pf[cb][i] = (c & 1) ? (_Float16)(p - (float)hi) : hi;
             }
-            l_run[cb] = l_run[cb] * alpha + psum;
-#pragma unroll
-            for (int dd = 0; dd < 8; dd++) {
-                o[cb][dd] *= alpha;
-                o[cb][dd] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vt[dd], pf, o[cb][dd], 0, 0, 0);
-            }
+            l_run[cb] += psum;
         }
-    }
+        // O^T += V^T P^T, V^T built one dim group at a time: vt = the 8 keys' values of dim 8c + dd
+#pragma unroll
+        for (int dd = 0; dd < 8; dd++) {
+            u4 w;
+#pragma unroll
+            for (int p = 0; p < 4; p++) {
+                uint32_t lo = B.v[2 * p][dd >> 1], hi = B.v[2 * p + 1][dd >> 1];
+                w[p] = (dd & 1) ? ((lo >> 16) | (hi & 0xffff0000u)) : ((lo & 0xffffu) | (hi << 16));
+            }
+            const h8 vt = __builtin_bit_cast(h8, w);
+#pragma unroll
+            for (int cb = 0; cb < NCB; cb++)
+                o[cb][dd] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vt, pf[cb], o[cb][dd], 0, 0, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        if (reload) load_v(B, t + 2 * STRIDE);
+    };
 
-    // ---- wave results: l over the 4 k-groups, O hi + lo columns
-    __shared__ float sm_o[DEC_WAVES][DEC_PAIRS * NCB][128];
+    // (the first loads are issued unconditionally, before the loop, so every iteration starts with the same
+    // loads outstanding and the compiler's load counters wait for exactly the buffer in use)
+    Buf X, Y;
+    const int t_first = wave * DEC_TILE;
+    load_k(X, t_first);
+    __builtin_amdgcn_sched_barrier(0);
+    load_v(X, t_first);
+    __builtin_amdgcn_sched_barrier(0);
+    load_k(Y, t_first + STRIDE);
+    __builtin_amdgcn_sched_barrier(0);
+    load_v(Y, t_first + STRIDE);
+    __builtin_amdgcn_sched_barrier(0);
+    // Q * scale * log2(e) in f32, split into an f16 high part (even columns) and its f16 remainder (odd)
+#pragma unroll
+    for (int cb = 0; cb < NCB; cb++)
+#pragma unroll
+        for (int kk = 0; kk < 4; kk++)
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                // (the element is copied to a scalar first: clang's __builtin_bit_cast of a vector-element
+                // lvalue reads element 0)
+                const uint32_t bits = qraw[cb][kk][e >> 2][e & 3];
+                float v = valid[cb] ? __uint_as_float(bits) * a.qscale : 0.f;
+                _Float16 hi = (_Float16)v;
+                qf[cb][kk][e] = (c & 1) ? (_Float16)(v - (float)hi) : hi;
+            }
+    GI_TS(2);
+    // Steady state: both buffers get a further tile (Y's may lie past the slice: zeros, never processed).
+    // The last one or two tiles run without reloads, so no load is left in flight at the end.
+    int t = t_first;
+    for (; t + 2 * STRIDE < nkeys; t += 2 * STRIDE) {
+        process(X, t, true);
+#ifdef GI_DEC_TIMESTAMPS
+        if (t == t_first) ts[3] = wall_clock64();
+#endif
+        process(Y, t + STRIDE, true);
+    }
+    if (t < nkeys) process(X, t, false);
+    if (t + STRIDE < nkeys) process(Y, t + STRIDE, false);
+    GI_TS(4);
+
+    // ---- wave results to LDS: every lane's 32 O^T values (its column, dims 32grp + 8j + dd) as 8 16-byte
+    // stores; per pair the max and the sum over the 4 k-groups
+    __shared__ __attribute__((aligned(16))) float sm_o[DEC_WAVES][16 * NCB][128 + 4];
     __shared__ float sm_m[DEC_WAVES][DEC_PAIRS * NCB], sm_l[DEC_WAVES][DEC_PAIRS * NCB];
 #pragma unroll
     for (int cb = 0; cb < NCB; cb++) {
-        float l = l_run[cb];
-        l += wave_xor(l, 16);
-        l += wave_xor(l, 32);
-        int pl = cb * DEC_PAIRS + (c >> 1);
+        float l = rows_sum(l_run[cb]);
 #pragma unroll
-        for (int dd = 0; dd < 8; dd++)
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                float v = o[cb][dd][j];
-                v += wave_xor(v, 1);
-                if ((c & 1) == 0) sm_o[wave][pl][32 * grp + 8 * j + dd] = v;
-            }
+        for (int j = 0; j < 4; j++) {
+            float* row = &sm_o[wave][16 * cb + c][32 * grp + 8 * j];
+            *reinterpret_cast<float4*>(row) = make_float4(o[cb][0][j], o[cb][1][j], o[cb][2][j], o[cb][3][j]);
+            *reinterpret_cast<float4*>(row + 4) = make_float4(o[cb][4][j], o[cb][5][j], o[cb][6][j], o[cb][7][j]);
+        }
         if (lane < 16 && (c & 1) == 0) {
-            sm_m[wave][pl] = m_run[cb];
-            sm_l[wave][pl] = l;
+            sm_m[wave][cb * DEC_PAIRS + (c >> 1)] = m_run[cb];
+            sm_l[wave][cb * DEC_PAIRS + (c >> 1)] = l;
         }
     }
+    GI_TS(6);
     __syncthreads();
-    // ---- merge the waves: thread -> (pair, dim)
-    for (int idx = threadIdx.x; idx < DEC_PAIRS * NCB * 128; idx += 256) {
-        int pl = idx >> 7, d = idx & 127;
-        int pi = pair0 + pl;
-        if (pi >= npairs) continue;
-        float M = GI_NEG_INF;
+    GI_TS(7);
+    // ---- merge the waves and the hi/lo columns: thread -> (pair, 4 dims)
 #pragma unroll
-        for (int w = 0; w < DEC_WAVES; w++) M = fmaxf(M, sm_m[w][pl]);
-        float L = 0.f, O = 0.f;
-        if (M != GI_NEG_INF) {
+    for (int it = 0; it < NCB; it++) {
+        const int item = threadIdx.x + 256 * it;
+        const int pl = item >> 5, d4 = 4 * (item & 31);
+        const int pi = pair0 + pl;
+        if (pi < npairs) {
+            const int row = 16 * (pl >> 3) + 2 * (pl & 7);
+            float M = GI_NEG_INF;
 #pragma unroll
-            for (int w = 0; w < DEC_WAVES; w++) {
-                float wt = exp2f(sm_m[w][pl] - M);
-                L += wt * sm_l[w][pl];
-                O += wt * sm_o[w][pl][d];
+            for (int w = 0; w < DEC_WAVES; w++) M = fmaxf(M, sm_m[w][pl]);
+            float L = 0.f;
+            float4 O = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (M != GI_NEG_INF) {
+#pragma unroll
+                for (int w = 0; w < DEC_WAVES; w++) {
+                    const float wt = __builtin_amdgcn_exp2f(sm_m[w][pl] - M);
+                    const float4 hi = *reinterpret_cast<const float4*>(&sm_o[w][row][d4]);
+                    const float4 lo = *reinterpret_cast<const float4*>(&sm_o[w][row + 1][d4]);
+                    L += wt * sm_l[w][pl];
+                    O.x += wt * (hi.x + lo.x);
+                    O.y += wt * (hi.y + lo.y);
+                    O.z += wt * (hi.z + lo.z);
+                    O.w += wt * (hi.w + lo.w);
+                }
+            }
+            const int tk = pi / G, h = kvh * G + pi % G;
+            if (a.nsplit == 1) {
+                const float inv = 1.f / L;
+                *reinterpret_cast<float4*>(a.out + (long long)tk * a.out_stride + (long long)h * 128 + d4) =
+                    make_float4(O.x * inv, O.y * inv, O.z * inv, O.w * inv);
+            } else {
+                float* p = a.part + (((long long)tk * a.n_heads + h) * a.nsplit + s) * DEC_PART;
+                *reinterpret_cast<float4*>(p + d4) = O;
+                if (d4 == 0) *reinterpret_cast<float2*>(p + 128) = make_float2(M, L);
             }
         }
-        int t = pi / G, h = kvh * G + pi % G;
-        if (a.nsplit == 1) {
-            a.out[(long long)t * a.out_stride + (long long)h * 128 + d] = O / L;
-        } else {
-            float* p = a.part + (((long long)t * a.n_heads + h) * a.nsplit + s) * 130;
-            p[d] = O;
-            if (d == 0) { p[128] = M; p[129] = L; }
-        }
     }
+#ifdef GI_DEC_TIMESTAMPS
+    ts[5] = wall_clock64();
+    if (lane == 0) {
+        unsigned long long* dbg = (unsigned long long*)(a.part + (long long)a.n_tok * a.n_heads * a.nsplit * DEC_PART);
+        long long w = ((long long)(blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x) * DEC_WAVES + wave;
+        for (int i = 0; i < 6; i++) dbg[w * 16 + i] = ts[i];
+        dbg[w * 16 + 8] = ts[6];
+        dbg[w * 16 + 9] = ts[7];
+        unsigned xcc;
+        asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+        dbg[w * 16 + 6] = __smid() | ((unsigned long long)xcc << 32);
+    }
+#endif
 }
 
 extern "C" __global__ void __launch_bounds__(256) gi_decode_partial_1(GiDecodeArgs a) { gi_decode_partial_t<1>(a); }
@@ -247,30 +382,61 @@ extern "C" __global__ void __launch_bounds__(256) gi_decode_partial_2(GiDecodeAr
 
 // Merge the slices of each (token, head): M = max m_s, w_s = 2^(m_s - M), out = sum w_s O_s / sum w_s l_s
 // (attention_combine's maths in base 2; empty slices carry m = -inf and weigh nothing). One workgroup of
-// 128 threads per (head, token); thread d owns output dim d.
-extern "C" __global__ void __launch_bounds__(128) gi_decode_combine(GiDecodeArgs a) {
-    __shared__ float wsh[1024];
-    __shared__ float red[2];
-    const int h = blockIdx.x, t = blockIdx.y, d = threadIdx.x;
-    const float* p = a.part + ((long long)t * a.n_heads + h) * a.nsplit * 130;
-    float M = GI_NEG_INF;
-    for (int s = d; s < a.nsplit; s += 128) M = fmaxf(M, p[s * 130 + 128]);
-    // block max: 2 waves
-    for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
-    if ((d & 63) == 0) red[d >> 6] = M;
-    __syncthreads();
-    M = fmaxf(red[0], red[1]);
-    const bool held = a.nsplit <= 1024;
-    if (held)
-        for (int s = d; s < a.nsplit; s += 128) wsh[s] = M == GI_NEG_INF ? 0.f : exp2f(p[s * 130 + 128] - M);
-    __syncthreads();
-    float L = 0.f, O = 0.f;
-    for (int s = 0; s < a.nsplit; s++) {
-        float w = held ? wsh[s] : (M == GI_NEG_INF ? 0.f : exp2f(p[s * 130 + 128] - M));
-        L += w * p[s * 130 + 129];
-        O += w * p[s * 130 + d];
+// 256 threads per (head, token). Thread t takes slices t/4, t/4 + 64, ... and dims 32(t%4)..+31, issuing
+// all of a slice's loads at once and folding its slices with a running max, so up to 64 slices cost one
+// memory round trip; the 64 slice lanes then meet in LDS.
+#define CMB_SLOTS 64
+extern "C" __global__ void __launch_bounds__(256) gi_decode_combine(GiDecodeArgs a) {
+    __shared__ float red_m[4];
+    __shared__ float acc_o[CMB_SLOTS][132];
+    __shared__ float acc_l[CMB_SLOTS];
+    const int h = blockIdx.x, t = blockIdx.y, tid = threadIdx.x;
+    const int slot = tid >> 2, dq = tid & 3;
+    const float* p = a.part + ((long long)t * a.n_heads + h) * a.nsplit * DEC_PART;
+    float m = GI_NEG_INF, L = 0.f, o[32];
+#pragma unroll
+    for (int i = 0; i < 32; i++) o[i] = 0.f;
+    for (int s = slot; s < a.nsplit; s += CMB_SLOTS) {
+        const float* ps = p + s * DEC_PART;
+        float4 v[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) v[i] = *reinterpret_cast<const float4*>(ps + 32 * dq + 4 * i);
+        const float2 ml = *reinterpret_cast<const float2*>(ps + 128);
+        if (ml.x == GI_NEG_INF) continue; // an empty slice
+        const float mn = fmaxf(m, ml.x);
+        const float a_old = __builtin_amdgcn_exp2f(m - mn), a_new = __builtin_amdgcn_exp2f(ml.x - mn);
+        m = mn;
+        L = L * a_old + ml.y * a_new;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            o[4 * i] = o[4 * i] * a_old + v[i].x * a_new;
+            o[4 * i + 1] = o[4 * i + 1] * a_old + v[i].y * a_new;
+            o[4 * i + 2] = o[4 * i + 2] * a_old + v[i].z * a_new;
+            o[4 * i + 3] = o[4 * i + 3] * a_old + v[i].w * a_new;
+        }
     }
-    a.out[(long long)t * a.out_stride + (long long)h * 128 + d] = O / L;
+    // block max of the slot maxima (every slot's thread group holds the same m)
+    float M = m;
+    for (int x = 32; x > 0; x >>= 1) M = fmaxf(M, __shfl_xor(M, x, 64));
+    if ((tid & 63) == 0) red_m[tid >> 6] = M;
+    __syncthreads();
+    M = fmaxf(fmaxf(red_m[0], red_m[1]), fmaxf(red_m[2], red_m[3]));
+    const float w = m == GI_NEG_INF ? 0.f : __builtin_amdgcn_exp2f(m - M);
+#pragma unroll
+    for (int i = 0; i < 8; i++)
+        *reinterpret_cast<float4*>(&acc_o[slot][32 * dq + 4 * i]) =
+            make_float4(o[4 * i] * w, o[4 * i + 1] * w, o[4 * i + 2] * w, o[4 * i + 3] * w);
+    if (dq == 0) acc_l[slot] = L * w;
+    __syncthreads();
+    if (tid < 128) {
+        float O = 0.f, LL = 0.f;
+#pragma unroll 8
+        for (int k = 0; k < CMB_SLOTS; k++) {
+            O += acc_o[k][tid];
+            LL += acc_l[k];
+        }
+        a.out[(long long)t * a.out_stride + (long long)h * 128 + tid] = O / LL;
+    }
 }
 
 // ------------------------------------------------------------------------------------------------ prefill
@@ -284,6 +450,7 @@ struct GiPrefillArgs {
     long long q_stride;
     long long kv_stride;
     long long out_stride;
+    long long kv_head_stride;
     int pos0;              // position of query 0 (keys before it are all visible: chunked prefill)
     int n;                 // query tokens
     int n_heads;
@@ -307,15 +474,22 @@ struct GiPrefillArgs {
 // A-row r of S^T block bb holds tile key 32bb + 16(i/2) + 8h + 4(i%2) + j for r = 8i + 4h + j, so the 16
 // values a lane holds per block are exactly the keys its PV B operand needs (k-step 2bb + i/2, element
 // 4(i%2) + j). K/V tiles are double-buffered in LDS with one barrier per tile; threads 0-127 stage K rows,
-// threads 128-255 stage V as 8x8 blocks transposed in registers. Causal: a wave stops at its last row's
-// position; only tiles crossing the diagonal are masked. Work order: the grid is remapped so that each of
-// the 8 XCDs (blockIdx round-robin) walks a contiguous run of (kv head, query tile, head) items, longest
-// query tiles first, so one kv head's K/V stays in one XCD's L2.
+// threads 128-255 stage V as 8x8 blocks transposed in registers; global loads go through buffer
+// resources, so keys past the cache's end read as zeros without branches. Softmax: scores stay raw, the
+// scale*log2(e) is folded into the exp2 argument; a row's reference max only moves when a tile's max
+// exceeds it by more than 2^8 in probability (then O and l are rescaled), so P <= 256 fits f16 and most
+// tiles skip the rescale. Row sums add the f16-rounded P that PV uses (v_dot2 against ones). Causal: a
+// wave stops at its last row's position; only tiles crossing the diagonal are masked. Work order: the
+// grid is remapped so that each of the 8 XCDs (blockIdx round-robin) walks a contiguous run of
+// (kv head, query tile, head) items, longest query tiles first, so one kv head's K/V stays in one
+// XCD's L2.
+#define PF_RESCALE_LOG2 8.0f
 extern "C" __global__ void __launch_bounds__(256, 2) gi_prefill_fwd(GiPrefillArgs a) {
     __shared__ __attribute__((aligned(16))) _Float16 sk[2][PF_KBUF];
     __shared__ __attribute__((aligned(16))) _Float16 sv[2][PF_VBUF];
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int G = a.n_heads / a.n_kv;
     const int qtiles = (a.n + PF_BQ - 1) / PF_BQ;
     const int nwg = gridDim.x;
@@ -336,59 +510,43 @@ extern "C" __global__ void __launch_bounds__(256, 2) gi_prefill_fwd(GiPrefillArg
     const int qpos = a.pos0 + qrow;              // its position
     h8 qf[8];
     {
-        const bool ok = qrow < a.n;
+        const int qr = qrow < a.n ? qrow : a.n - 1; // rows past n compute garbage that is never written
         if (a.q_f16) {
-            const _Float16* qp = (const _Float16*)a.q + (long long)(ok ? qrow : 0) * a.q_stride + h * 128 + 8 * half;
+            const _Float16* qp = (const _Float16*)a.q + (long long)qr * a.q_stride + h * 128 + 8 * half;
 #pragma unroll
-            for (int ks = 0; ks < 8; ks++) {
-                u4 w = ok ? *reinterpret_cast<const u4*>(qp + 16 * ks) : u4{0u, 0u, 0u, 0u};
-                qf[ks] = __builtin_bit_cast(h8, w);
-            }
+            for (int ks = 0; ks < 8; ks++) qf[ks] = __builtin_bit_cast(h8, *reinterpret_cast<const u4*>(qp + 16 * ks));
         } else {
-            const float* qp = (const float*)a.q + (long long)(ok ? qrow : 0) * a.q_stride + h * 128 + 8 * half;
+            const float* qp = (const float*)a.q + (long long)qr * a.q_stride + h * 128 + 8 * half;
 #pragma unroll
             for (int ks = 0; ks < 8; ks++) {
-                float4 x0 = ok ? *reinterpret_cast<const float4*>(qp + 16 * ks) : make_float4(0.f, 0.f, 0.f, 0.f);
-                float4 x1 = ok ? *reinterpret_cast<const float4*>(qp + 16 * ks + 4) : make_float4(0.f, 0.f, 0.f, 0.f);
+                float4 x0 = *reinterpret_cast<const float4*>(qp + 16 * ks);
+                float4 x1 = *reinterpret_cast<const float4*>(qp + 16 * ks + 4);
                 qf[ks] = h8{(_Float16)x0.x, (_Float16)x0.y, (_Float16)x0.z, (_Float16)x0.w,
                             (_Float16)x1.x, (_Float16)x1.y, (_Float16)x1.z, (_Float16)x1.w};
             }
         }
     }
 
-    // ---- staging roles
-    const bool stage_k = tid < 128;
+    // ---- staging roles (wave-uniform): waves 0-1 stage K, waves 2-3 stage V
+    const bool stage_k = wave < 2;
     const int st = tid & 127;
-    // K: chunk ids st + 128i -> key (id / 16), 16-byte column (id % 16)
-    // V: thread -> dim group dg = st / 8 (dims 8dg..8dg+7), key group kg = st % 8 (keys 8kg..8kg+7)
+    const long long kvs = a.kv_stride;
+    // K: rows (st/16) + 8i, 16-byte column st%16; V: keys 8*(st%8) + i, dims 8*(st/8)..+7
     const int vdg = st >> 3, vkg = st & 7;
-    const uint16_t* kbase = a.kc + (long long)kvh * 128;
-    const uint16_t* vbase = a.vc + (long long)kvh * 128;
+    const int soff = stage_k ? (((st >> 4) * (int)kvs + 8 * (st & 15)) * 2) : ((8 * vkg * (int)kvs + 8 * vdg) * 2);
+    const int sstep = stage_k ? 8 * (int)kvs * 2 : (int)kvs * 2;
+    const uint16_t* sbase = (stage_k ? a.kc : a.vc) + kvh * a.kv_head_stride;
     u4 stg[8];
     auto load_tile = [&](int t0) {
-        if (stage_k) {
+        __amdgpu_buffer_rsrc_t r = gi_rsrc(sbase + (long long)t0 * kvs, (long long)(kv_len - t0) * kvs * 2);
 #pragma unroll
-            for (int i = 0; i < 8; i++) {
-                int id = st + 128 * i, key = t0 + (id >> 4);
-                stg[i] = key < kv_len ? *reinterpret_cast<const u4*>(kbase + (long long)key * a.kv_stride + 8 * (id & 15))
-                                      : u4{0u, 0u, 0u, 0u};
-            }
-        } else {
-#pragma unroll
-            for (int i = 0; i < 8; i++) {
-                int key = t0 + 8 * vkg + i;
-                stg[i] = key < kv_len ? *reinterpret_cast<const u4*>(vbase + (long long)key * a.kv_stride + 8 * vdg)
-                                      : u4{0u, 0u, 0u, 0u};
-            }
-        }
+        for (int i = 0; i < 8; i++) stg[i] = gi_load16(r, soff + i * sstep);
     };
     auto store_tile = [&](int buf) {
         if (stage_k) {
 #pragma unroll
-            for (int i = 0; i < 8; i++) {
-                int id = st + 128 * i;
-                *reinterpret_cast<u4*>(&sk[buf][(id >> 4) * PF_KLD + 8 * (id & 15)]) = stg[i];
-            }
+            for (int i = 0; i < 8; i++)
+                *reinterpret_cast<u4*>(&sk[buf][((st >> 4) + 8 * i) * PF_KLD + 8 * (st & 15)]) = stg[i];
         } else {
 #pragma unroll
             for (int dd = 0; dd < 8; dd++) {
@@ -403,19 +561,24 @@ extern "C" __global__ void __launch_bounds__(256, 2) gi_prefill_fwd(GiPrefillArg
         }
     };
 
-    // ---- per-lane state: O^T (4 dim blocks of 32), running max (raw score units), partial row sum
+    // ---- per-lane state: O^T (4 dim blocks of 32), reference max (raw score units), row sum
     f16x o[4];
 #pragma unroll
     for (int db = 0; db < 4; db++)
 #pragma unroll
         for (int e = 0; e < 16; e++) o[db][e] = 0.f;
     float m_run = GI_NEG_INF, l_run = 0.f;
+    const float qs = a.qscale;
+    const float th = PF_RESCALE_LOG2 / qs; // rescale threshold in raw score units
     const int wave_first = a.pos0 + q0 + 32 * wave;  // position of the wave's first row
     const int wave_last = wave_first + 31;
     // A-operand row of this lane in an S^T block: key offset within the block
     const int r = lane & 31;
     const int kperm = 16 * ((r >> 3) >> 1) + 8 * ((r >> 2) & 1) + 4 * ((r >> 3) & 1) + (r & 3);
-    const int khalf = lane >> 5; // A k-group: dims 16ks + 8*khalf
+    const _Float16* krd = &sk[0][0] + kperm * PF_KLD + 8 * half;
+    const _Float16* vrd = &sv[0][0] + r * PF_VLD + 8 * half;
+    const h8 ones = h8{1, 1, 1, 1, 1, 1, 1, 1};
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 
     load_tile(0);
     store_tile(0);
@@ -424,24 +587,21 @@ extern "C" __global__ void __launch_bounds__(256, 2) gi_prefill_fwd(GiPrefillArg
         const int t0 = it * PF_BK, buf = it & 1;
         if (it + 1 < ntiles) load_tile(t0 + PF_BK);
         if (t0 <= wave_last) {
-            const _Float16* K = sk[buf];
-            const _Float16* V = sv[buf];
+            const _Float16* K = krd + buf * PF_KBUF;
+            const _Float16* V = vrd + buf * PF_VBUF;
             f16x s[2];
 #pragma unroll
             for (int bb = 0; bb < 2; bb++) {
 #pragma unroll
                 for (int e = 0; e < 16; e++) s[bb][e] = 0.f;
-                const _Float16* krow = K + (32 * bb + kperm) * PF_KLD + 8 * khalf;
 #pragma unroll
                 for (int ks = 0; ks < 8; ks++) {
-                    h8 kf = *reinterpret_cast<const h8*>(krow + 16 * ks);
+                    h8 kf = *reinterpret_cast<const h8*>(K + 32 * bb * PF_KLD + 16 * ks);
                     s[bb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[ks], s[bb], 0, 0, 0);
                 }
             }
             // lane holds, for query qcol: block bb, element 4i + jj -> tile key 32bb + 16(i/2) + 8*half + 4(i%2) + jj
-            const bool diag = t0 + PF_BK - 1 > wave_first || t0 + PF_BK > kv_len;
-            float mx = GI_NEG_INF;
-            if (diag) {
+            if (t0 + PF_BK - 1 > wave_first) { // the tile crosses the diagonal (or the end) somewhere in the wave
 #pragma unroll
                 for (int bb = 0; bb < 2; bb++)
 #pragma unroll
@@ -449,43 +609,43 @@ extern "C" __global__ void __launch_bounds__(256, 2) gi_prefill_fwd(GiPrefillArg
 #pragma unroll
                         for (int jj = 0; jj < 4; jj++) {
                             int key = t0 + 32 * bb + 16 * (i >> 1) + 8 * half + 4 * (i & 1) + jj;
-                            float v = s[bb][4 * i + jj];
-                            v = (key > qpos || key >= kv_len) ? GI_NEG_INF : v;
-                            s[bb][4 * i + jj] = v;
-                            mx = fmaxf(mx, v);
+                            if (key > qpos) s[bb][4 * i + jj] = GI_NEG_INF;
                         }
-            } else {
-#pragma unroll
-                for (int bb = 0; bb < 2; bb++)
-#pragma unroll
-                    for (int e = 0; e < 16; e++) mx = fmaxf(mx, s[bb][e]);
             }
+            float mx = GI_NEG_INF;
+#pragma unroll
+            for (int bb = 0; bb < 2; bb++)
+#pragma unroll
+                for (int e = 0; e < 16; e++) mx = fmaxf(mx, s[bb][e]);
             mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-            const float m_new = fmaxf(m_run, mx);
-            const float m_use = m_new == GI_NEG_INF ? 0.f : m_new;
-            const float alpha = exp2f((m_run - m_use) * a.qscale);
-            m_run = m_new;
-            const float mo = -m_use * a.qscale;
-            float psum = 0.f;
+            const bool up = mx > m_run + th;
+            if (__builtin_amdgcn_ballot_w64(up)) { // some row's max moved: rescale (alpha = 1 for the others)
+                const float m_new = up ? mx : m_run;
+                const float alpha = __builtin_amdgcn_exp2f((m_run - m_new) * qs);
+                m_run = m_new;
+                l_run *= alpha;
+#pragma unroll
+                for (int db = 0; db < 4; db++) o[db] *= alpha;
+            }
+            const float mo = -m_run * qs;
             h8 pf[4]; // PV B operands, k-step ks = 2bb + i/2, element 4(i%2) + jj
 #pragma unroll
             for (int bb = 0; bb < 2; bb++)
 #pragma unroll
                 for (int i = 0; i < 4; i++)
 #pragma unroll
-                    for (int jj = 0; jj < 4; jj++) {
-                        float p = exp2f(fmaf(s[bb][4 * i + jj], a.qscale, mo));
-                        psum += p;
-                        pf[2 * bb + (i >> 1)][4 * (i & 1) + jj] = (_Float16)p;
-                    }
-            l_run = l_run * alpha + psum;
+                    for (int jj = 0; jj < 4; jj++)
+                        pf[2 * bb + (i >> 1)][4 * (i & 1) + jj] = (_Float16)__builtin_amdgcn_exp2f(fmaf(s[bb][4 * i + jj], qs, mo));
+#pragma unroll
+            for (int ks = 0; ks < 4; ks++)
+#pragma unroll
+                for (int e = 0; e < 4; e++)
+                    l_run = __builtin_amdgcn_fdot2(h2{pf[ks][2 * e], pf[ks][2 * e + 1]}, h2{ones[0], ones[1]}, l_run, false);
 #pragma unroll
             for (int db = 0; db < 4; db++) {
-                o[db] *= alpha;
-                const _Float16* vrow = V + (32 * db + r) * PF_VLD + 8 * khalf;
 #pragma unroll
                 for (int ks = 0; ks < 4; ks++) {
-                    h8 vf = *reinterpret_cast<const h8*>(vrow + 16 * ks);
+                    h8 vf = *reinterpret_cast<const h8*>(V + 32 * db * PF_VLD + 16 * ks);
                     o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf[ks], o[db], 0, 0, 0);
                 }
             }

@@ -61,9 +61,9 @@ def load_library(path=LIB_PATH):
     lib.gi_attn_decode_plan.restype = i
     lib.gi_attn_decode_workspace_bytes.argtypes = [i, i, i, i, i]
     lib.gi_attn_decode_workspace_bytes.restype = sz
-    lib.gi_attn_decode.argtypes = [vp, vp, ll, vp, vp, ll, vp, ll, vp, sz, i, vp, i, i, i, i, i, f]
+    lib.gi_attn_decode.argtypes = [vp, vp, ll, vp, vp, ll, ll, vp, ll, vp, sz, i, vp, i, i, i, i, i, f]
     lib.gi_attn_decode.restype = i
-    lib.gi_attn_prefill.argtypes = [vp, vp, i, ll, vp, vp, ll, vp, i, ll, i, i, i, i, i, f]
+    lib.gi_attn_prefill.argtypes = [vp, vp, i, ll, vp, vp, ll, ll, vp, i, ll, i, i, i, i, i, f]
     lib.gi_attn_prefill.restype = i
     lib.gi_attention.argtypes = [vp, vp, vp, vp, vp, vp, sz, i, vp, i, i, i, i, i, i]
     lib.gi_attention.restype = i
@@ -93,14 +93,26 @@ def _need(t, name, dtype):
         raise GiAttnError(f"{name} rows must be contiguous")
 
 
-def _cache_stride(kc, vc, n_kv, hd):
+def _cache_layout(kc, vc, n_kv, hd, layout):
+    """(kv_stride, kv_head_stride, capacity) of a cache pair.
+
+    layout "reference": [capacity, n_kv, hd] (or [capacity, n_kv*hd]), as the reference keeps it
+    (src/cuda.rs:365-369); "head_major": [n_kv, capacity, hd], each kv head's rows contiguous."""
     for t, name in ((kc, "k_cache"), (vc, "v_cache")):
         _need(t, name, torch.float16)
         if not t.is_contiguous():
-            raise GiAttnError(f"{name} must be contiguous [pos][n_kv][hd]")
+            raise GiAttnError(f"{name} must be contiguous")
     if kc.shape != vc.shape:
         raise GiAttnError("k_cache and v_cache shapes differ")
-    return n_kv * hd
+    if layout == "reference":
+        if kc.numel() % (n_kv * hd):
+            raise GiAttnError(f"cache of shape {tuple(kc.shape)} is not [capacity, {n_kv}, {hd}]")
+        return n_kv * hd, hd, kc.numel() // (n_kv * hd)
+    if layout == "head_major":
+        if kc.dim() != 3 or kc.shape[0] != n_kv or kc.shape[2] != hd:
+            raise GiAttnError(f"head-major cache must be [{n_kv}, capacity, {hd}], got {tuple(kc.shape)}")
+        return hd, kc.shape[1] * hd, kc.shape[1]
+    raise GiAttnError(f"unknown cache layout {layout!r}")
 
 
 def init(code_object_path=None):
@@ -128,15 +140,15 @@ def new_workspace(ctx_cap, n_tok, n_heads, n_kv, hd=128, device="cuda"):
 
 
 def decode(q, k_cache, v_cache, pos0, n_heads, n_kv, hd=128, scale=None, out=None, workspace=None, posp=None,
-           ctx_cap=0):
+           ctx_cap=0, kv_layout="reference"):
     """Decode/verify attention of n_tok = q.shape[0] tokens at positions pos0.. (causal within the block).
 
-    q: f32 [n_tok, >= n_heads*hd] (row stride q.stride(0)); caches f16 [cap, n_kv, hd] (or [cap, n_kv*hd]);
+    q: f32 [n_tok, >= n_heads*hd] (row stride q.stride(0)); caches f16 in kv_layout (see _cache_layout);
     returns f32 [n_tok, n_heads*hd]. posp: an int32 CUDA tensor holding the position (graph replay), with
     ctx_cap the largest span the launch shape must cover.
     """
     _need(q, "q", torch.float32)
-    kv_stride = _cache_stride(k_cache, v_cache, n_kv, hd)
+    kv_stride, kv_head_stride, capacity = _cache_layout(k_cache, v_cache, n_kv, hd, kv_layout)
     n_tok = q.shape[0]
     if scale is None:
         scale = 1.0 / math.sqrt(hd)
@@ -146,18 +158,20 @@ def decode(q, k_cache, v_cache, pos0, n_heads, n_kv, hd=128, scale=None, out=Non
     if posp is not None:
         _need(posp, "posp", torch.int32)
     need_rows = ctx_cap if posp is not None else pos0 + n_tok
-    if k_cache.shape[0] < need_rows:
-        raise GiAttnError(f"the cache holds {k_cache.shape[0]} positions; {need_rows} needed")
+    if capacity < need_rows:
+        raise GiAttnError(f"the cache holds {capacity} positions; {need_rows} needed")
     if workspace is None:
         workspace = new_workspace(need_rows, n_tok, n_heads, n_kv, hd, q.device)
     lib = load_library()
-    _check(lib.gi_attn_decode(_stream(), _ptr(q), q.stride(0), _ptr(k_cache), _ptr(v_cache), kv_stride, _ptr(out),
+    _check(lib.gi_attn_decode(_stream(), _ptr(q), q.stride(0), _ptr(k_cache), _ptr(v_cache), kv_stride,
+                              kv_head_stride, _ptr(out),
                               out.stride(0), _ptr(workspace), workspace.numel() * workspace.element_size(), pos0,
                               _ptr(posp), ctx_cap, n_tok, n_heads, n_kv, hd, scale))
     return out
 
 
-def prefill(q, k_cache, v_cache, pos0, n_heads, n_kv, hd=128, scale=None, out=None, out_dtype=None):
+def prefill(q, k_cache, v_cache, pos0, n_heads, n_kv, hd=128, scale=None, out=None, out_dtype=None,
+            kv_layout="reference"):
     """Causal prefill of n = q.shape[0] tokens at positions pos0..pos0+n-1 (their K/V already cached).
 
     q: f32 or f16 [n, >= n_heads*hd]; returns [n, n_heads*hd] of out_dtype (default: q's dtype).
@@ -165,10 +179,10 @@ def prefill(q, k_cache, v_cache, pos0, n_heads, n_kv, hd=128, scale=None, out=No
     if q.dtype not in (torch.float32, torch.float16):
         raise GiAttnError("q must be float32 or float16")
     _need(q, "q", q.dtype)
-    kv_stride = _cache_stride(k_cache, v_cache, n_kv, hd)
+    kv_stride, kv_head_stride, capacity = _cache_layout(k_cache, v_cache, n_kv, hd, kv_layout)
     n = q.shape[0]
-    if k_cache.shape[0] < pos0 + n:
-        raise GiAttnError(f"the cache holds {k_cache.shape[0]} positions; {pos0 + n} needed")
+    if capacity < pos0 + n:
+        raise GiAttnError(f"the cache holds {capacity} positions; {pos0 + n} needed")
     if scale is None:
         scale = 1.0 / math.sqrt(hd)
     if out is None:
@@ -178,7 +192,7 @@ def prefill(q, k_cache, v_cache, pos0, n_heads, n_kv, hd=128, scale=None, out=No
     _need(out, "out", out.dtype)
     lib = load_library()
     _check(lib.gi_attn_prefill(_stream(), _ptr(q), GI_F16 if q.dtype == torch.float16 else GI_F32, q.stride(0),
-                               _ptr(k_cache), _ptr(v_cache), kv_stride, _ptr(out),
+                               _ptr(k_cache), _ptr(v_cache), kv_stride, kv_head_stride, _ptr(out),
                                GI_F16 if out.dtype == torch.float16 else GI_F32, out.stride(0), pos0, n, n_heads,
                                n_kv, hd, scale))
     return out
@@ -197,9 +211,9 @@ def attention(qkv, k_cache, v_cache, pos0, n_heads, n_kv, hd=128, exact=False, o
     row = n_heads * hd + 2 * n_kv * hd
     if qkv.shape[1] != row or not qkv.is_contiguous():
         raise GiAttnError(f"qkv must be contiguous [n, {row}]")
-    _cache_stride(k_cache, v_cache, n_kv, hd)
-    if k_cache.shape[0] < max(pos0 + n, ctx_cap if posp is not None else 0):
-        raise GiAttnError(f"the cache holds {k_cache.shape[0]} positions; {pos0 + n} needed")
+    _, _, capacity = _cache_layout(k_cache, v_cache, n_kv, hd, "reference")
+    if capacity < max(pos0 + n, ctx_cap if posp is not None else 0):
+        raise GiAttnError(f"the cache holds {capacity} positions; {pos0 + n} needed")
     if out is None:
         out = torch.empty((n, n_heads * hd), dtype=torch.float32, device=qkv.device)
     _need(out, "out", torch.float32)

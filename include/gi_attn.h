@@ -14,9 +14,13 @@
  *    hipError_t value) and gi_last_error() gives "HIP <what> failed: <text> (<code>)" or the argument
  *    problem, as the reference's Api::check builds "CUDA {what} failed: {text} ({r})"
  *    (src/cuda.rs:5058-5068). The message is per thread.
- *  - Layouts: query/output rows hold head h at element h*hd of the row (row strides in elements); the
- *    KV cache is two buffers of rows [position][n_kv][hd] f16 (IEEE binary16 bits), kv_stride elements
- *    per position (n_kv*hd for the reference layout, src/cuda.rs:365-369).
+ *  - Layouts: query/output rows hold head h at element h*hd of the row (row strides in elements). The
+ *    KV cache is two f16 buffers (IEEE binary16 bits); the row of position t, kv head h starts at element
+ *    t*kv_stride + h*kv_head_stride. The reference's layout [position][n_kv][hd] (src/cuda.rs:365-369)
+ *    is kv_stride = n_kv*hd, kv_head_stride = hd (pass 0 for hd). The head-major layout
+ *    [n_kv][capacity][hd] is kv_stride = hd, kv_head_stride = capacity*hd: each head's rows are
+ *    contiguous, which spreads a head's stream evenly over the HBM channels (the decode kernel is
+ *    fastest with it). Strides are multiples of 8 elements and pointers 16-byte aligned.
  *  - Causality: token b of a call sits at position pos0 + b and attends to keys 0..pos0+b.
  *  - hd must be 128; n_heads must be a multiple of n_kv.
  */
@@ -52,7 +56,7 @@ const char* gi_last_error(void);
 int gi_attn_decode_plan(int max_span, int n_tok, int n_heads, int n_kv, int hd, int* chunk, int* nsplit);
 
 /* Bytes of workspace gi_attn_decode needs for n_tok tokens whose spans reach at most ctx_cap keys
- * (the slice partials, [token][head][slice][hd + 2] f32). The counterpart of the session's att_part
+ * (the slice partials, [token][head][slice][hd + 4] f32: O, max, sum, 2 pad). The counterpart of the session's att_part
  * buffer (GpuSession, src/cuda.rs:9826-9870). */
 size_t gi_attn_decode_workspace_bytes(int ctx_cap, int n_tok, int n_heads, int n_kv, int hd);
 
@@ -63,16 +67,17 @@ size_t gi_attn_decode_workspace_bytes(int ctx_cap, int n_tok, int n_heads, int n
  * ignored. Replaces: attention_partial_gqa + attention_combine, launched by GpuModel::attention's split
  * path (src/cuda.rs:1684-1865, src/cuda.rs:2806-2836, src/cuda.rs:8478-8538). */
 int gi_attn_decode(void* stream, const float* q, long long q_stride, const uint16_t* kc, const uint16_t* vc,
-                   long long kv_stride, float* out, long long out_stride, void* workspace, size_t workspace_bytes,
-                   int pos0, const int* posp, int ctx_cap, int n_tok, int n_heads, int n_kv, int hd, float scale);
+                   long long kv_stride, long long kv_head_stride, float* out, long long out_stride, void* workspace,
+                   size_t workspace_bytes, int pos0, const int* posp, int ctx_cap, int n_tok, int n_heads, int n_kv,
+                   int hd, float scale);
 
 /* Causal prefill attention for n tokens at positions pos0..pos0+n-1 whose K/V rows are already in the
  * cache (keys 0..pos0+n-1 are read; pos0 > 0 is a chunk of a longer prompt). q: rows of q_dtype
  * (GI_F32 or GI_F16); out: rows of out_dtype. Replaces: attention_prefill_tc128 (src/cuda.rs:2408-2621),
  * launched by GpuModel::attention for batches of >= 16 tokens (src/cuda.rs:8459-8466). */
 int gi_attn_prefill(void* stream, const void* q, int q_dtype, long long q_stride, const uint16_t* kc,
-                    const uint16_t* vc, long long kv_stride, void* out, int out_dtype, long long out_stride, int pos0,
-                    int n, int n_heads, int n_kv, int hd, float scale);
+                    const uint16_t* vc, long long kv_stride, long long kv_head_stride, void* out, int out_dtype,
+                    long long out_stride, int pos0, int n, int n_heads, int n_kv, int hd, float scale);
 
 /* The attention operator of one layer, as GpuModel::attention (src/cuda.rs:8448-8541) dispatches it:
  * qkv rows are [q (n_heads*hd) | k | v] f32 (stride n_heads*hd + 2*n_kv*hd, src/cuda.rs:1713), out rows

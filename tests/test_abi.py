@@ -44,14 +44,14 @@ def test_unsupported_head_size_is_rejected_with_message():
 def test_decode_rejects_bad_arguments_before_any_launch():
     lib = gi_attn.load_library()
     # null tensors, hd 96, misaligned pointers: all refused on the host
-    rc = lib.gi_attn_decode(None, None, 4096, None, None, 512, None, 4096, None, 0, 0, None, 0, 1, 32, 4, 128,
+    rc = lib.gi_attn_decode(None, None, 4096, None, None, 512, 128, None, 4096, None, 0, 0, None, 0, 1, 32, 4, 128,
                             0.088)
     assert rc == -1 and "null" in lib.gi_last_error().decode()
-    rc = lib.gi_attn_decode(None, 16, 4096, 16, 16, 512, 16, 4096, None, 0, 0, None, 0, 1, 32, 4, 96, 0.1)
+    rc = lib.gi_attn_decode(None, 16, 4096, 16, 16, 512, 128, 16, 4096, None, 0, 0, None, 0, 1, 32, 4, 96, 0.1)
     assert rc == -1 and "head size" in lib.gi_last_error().decode()
-    rc = lib.gi_attn_decode(None, 8, 4096, 16, 16, 512, 16, 4096, None, 0, 0, None, 0, 1, 32, 4, 128, 0.1)
+    rc = lib.gi_attn_decode(None, 8, 4096, 16, 16, 512, 128, 16, 4096, None, 0, 0, None, 0, 1, 32, 4, 128, 0.1)
     assert rc == -1 and "aligned" in lib.gi_last_error().decode()
-    rc = lib.gi_attn_prefill(None, 16, 7, 4096, 16, 16, 1024, 16, 0, 4096, 0, 16, 32, 8, 128, 0.1)
+    rc = lib.gi_attn_prefill(None, 16, 7, 4096, 16, 16, 1024, 128, 16, 0, 4096, 0, 16, 32, 8, 128, 0.1)
     assert rc == -1 and "dtypes" in lib.gi_last_error().decode()
 
 
@@ -63,13 +63,13 @@ def test_decode_plan_covers_the_span(ctx, n_tok, n_heads, n_kv):
     assert (nsplit - 1) * chunk < ctx <= nsplit * chunk
     if nsplit > 1:
         # every launch of up to n_tok tokens with spans up to ctx fits the workspace size query
-        need = n_tok * n_heads * nsplit * 130 * 4
+        need = n_tok * n_heads * nsplit * 132 * 4
         assert gi_attn.workspace_bytes(ctx, n_tok, n_heads, n_kv) >= need
     for span in (1, ctx // 3 + 1, ctx):
         for t in range(1, n_tok + 1):
             c2, s2 = gi_attn.decode_plan(span, t, n_heads, n_kv)
             if s2 > 1:
-                assert gi_attn.workspace_bytes(ctx, n_tok, n_heads, n_kv) >= t * n_heads * s2 * 130 * 4
+                assert gi_attn.workspace_bytes(ctx, n_tok, n_heads, n_kv) >= t * n_heads * s2 * 132 * 4
 
 
 def test_python_mirror_raises_without_gpu_tensors():
