@@ -251,3 +251,35 @@ def test_attention_operator_dispatch(gpu, n, pos0, exact):
     split_path = n < 16 or exact
     assert_close(got, want, max_abs=2e-5 if split_path else 2e-3, rel_l2=2e-5 if split_path else 1e-3,
                  what="operator vs f64")
+
+
+# ---------------------------------------------------------------- head-major cache layout [n_kv][capacity][128]
+
+def to_head_major(kbits, vbits, n_kv, dev):
+    """The reference-layout caches [pos][n_kv*128] as head-major [n_kv][pos][128] f16 tensors."""
+    k = torch.from_numpy(np.ascontiguousarray(kbits).view(np.int16)).view(-1, n_kv, 128).transpose(0, 1).contiguous()
+    v = torch.from_numpy(np.ascontiguousarray(vbits).view(np.int16)).view(-1, n_kv, 128).transpose(0, 1).contiguous()
+    return k.to(dev).view(torch.float16), v.to(dev).view(torch.float16)
+
+
+@pytest.mark.parametrize("n_tok,pos0,n_heads,n_kv", [(1, 0, 32, 8), (1, 300, 32, 4), (1, 4095, 32, 8),
+                                                     (8, 1000, 32, 4), (1, 65535, 32, 4)])
+def test_decode_head_major(gpu, n_tok, pos0, n_heads, n_kv):
+    say("decode head-major", n_tok, pos0, n_heads, n_kv)
+    q, k, v = make_inputs(3000 + pos0, n_tok, pos0 + n_tok, n_heads, n_kv)
+    kt, vt = to_head_major(k, v, n_kv, gpu)
+    out = gi_attn.decode(torch.from_numpy(q).to(gpu), kt, vt, pos0, n_heads, n_kv, kv_layout="head_major")
+    torch.cuda.synchronize()
+    assert_close(out.cpu().numpy(), reference_f64(q, k, v, pos0, n_heads, n_kv), max_abs=2e-5, rel_l2=2e-5,
+                 what="head-major decode vs f64")
+
+
+@pytest.mark.parametrize("n,pos0,n_heads,n_kv", [(200, 0, 32, 8), (512, 512, 32, 4)])
+def test_prefill_head_major(gpu, n, pos0, n_heads, n_kv):
+    say("prefill head-major", n, pos0, n_heads, n_kv)
+    q, k, v = make_inputs(4000 + n, n, pos0 + n, n_heads, n_kv, q_dtype=np.float16)
+    kt, vt = to_head_major(k, v, n_kv, gpu)
+    out = gi_attn.prefill(torch.from_numpy(q).to(gpu), kt, vt, pos0, n_heads, n_kv, out_dtype=torch.float32,
+                          kv_layout="head_major")
+    torch.cuda.synchronize()
+    assert_close(out.cpu().numpy(), reference_f64(q, k, v, pos0, n_heads, n_kv), what="head-major prefill vs f64")
