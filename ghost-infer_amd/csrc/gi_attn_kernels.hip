@@ -31,6 +31,7 @@ typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef float f4 __attribute__((ext_vector_type(4)));
 typedef float f16x __attribute__((ext_vector_type(16)));
 typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+typedef _Float16 h4x __attribute__((ext_vector_type(4)));
 
 #define GI_NEG_INF (-__builtin_inff())
 #define GI_LOG2E 1.4426950408889634f
@@ -461,32 +462,38 @@ struct GiPrefillArgs {
     int pad_;
 };
 
-#define PF_BQ 128          // query rows per workgroup (4 waves x 32)
+#define PF_WAVES 8         // waves per workgroup, 32 query rows each
+#define PF_BQ 256          // query rows per workgroup
+#define PF_NBUF 4          // LDS tile buffers: tiles it+1..it+3 stream in while tile it is used
 #define PF_BK 64           // keys per tile
-#define PF_KLD 136         // K tile row stride in f16 (272 bytes: rows 4 banks apart)
-#define PF_VLD 72          // V^T tile row stride in f16 (144 bytes)
-#define PF_KBUF (PF_BK * PF_KLD)
-#define PF_VBUF (128 * PF_VLD)
-
-// One workgroup = (head, 128 query rows); wave w owns rows 32w..32w+31 of the tile. Per 64-key tile:
-//   S^T[key, q] = K[key, :] . Q[q, :]       v_mfma_f32_32x32x16_f16, K from LDS (A), Q in registers (B)
-//   O^T[d, q]  += V^T[d, key] . P^T[key, q]  V^T from LDS (A), P^T straight from the S^T accumulators (B)
-// A-row r of S^T block bb holds tile key 32bb + 16(i/2) + 8h + 4(i%2) + j for r = 8i + 4h + j, so the 16
-// values a lane holds per block are exactly the keys its PV B operand needs (k-step 2bb + i/2, element
-// 4(i%2) + j). K/V tiles are double-buffered in LDS with one barrier per tile; threads 0-127 stage K rows,
-// threads 128-255 stage V as 8x8 blocks transposed in registers; global loads go through buffer
-// resources, so keys past the cache's end read as zeros without branches. Softmax: scores stay raw, the
-// scale*log2(e) is folded into the exp2 argument; a row's reference max only moves when a tile's max
-// exceeds it by more than 2^8 in probability (then O and l are rescaled), so P <= 256 fits f16 and most
-// tiles skip the rescale. Row sums add the f16-rounded P that PV uses (v_dot2 against ones). Causal: a
-// wave stops at its last row's position; only tiles crossing the diagonal are masked. Work order: the
-// grid is remapped so that each of the 8 XCDs (blockIdx round-robin) walks a contiguous run of
-// (kv head, query tile, head) items, longest query tiles first, so one kv head's K/V stays in one
-// XCD's L2.
+#define PF_TILE 16384      // bytes of one K or V tile: 64 rows of 256 bytes
 #define PF_RESCALE_LOG2 8.0f
-extern "C" __global__ void __launch_bounds__(256, 2) gi_prefill_fwd(GiPrefillArgs a) {
-    __shared__ __attribute__((aligned(16))) _Float16 sk[2][PF_KBUF];
-    __shared__ __attribute__((aligned(16))) _Float16 sv[2][PF_VBUF];
+#define GI_LDS __attribute__((address_space(3)))
+typedef short gi_s4 __attribute__((__vector_size__(8))); // 4 f16 as ds_read_b64_tr_b16 returns them
+
+// One workgroup = (head, 256 query rows); wave w of 8 owns rows 32w..32w+31 of the tile. Per 64-key tile:
+//   S^T[key, q] = K[key, :] . Q[q, :]       v_mfma_f32_32x32x16_f16, K from LDS (A), Q in registers (B)
+//   O^T[d, q]  += V^T[d, key] . P^T[key, q]  V^T from LDS (A, by transposing reads), P^T from S^T (B)
+// Staging: K and V tiles go global -> LDS with direct-to-LDS buffer loads (no registers, no VALU): each of
+// the 8 waves moves 4 KB per tile as 4 loads of 1 KB (64 lanes x 16 bytes, written at base + 16*lane).
+// Rows are stored unpadded with an XOR swizzle of their 16-byte units (K: unit ^ row%16, V: unit ^
+// 4*(row%4)) so the MFMA operand reads hit distinct banks. Four LDS buffers keep three tiles in flight (an
+// L2/MALL round trip is several tiles of compute); one barrier per tile.
+// Keys past the cache's end read as zeros (buffer bounds) and are masked.
+// K operand: A-row r of S^T block bb holds tile key 32bb + 16(i/2) + 8h + 4(i%2) + j for r = 8i + 4h + j,
+// so the 16 values a lane holds per block are exactly the keys its PV B operand needs (k-step 2bb + i/2,
+// element 4(i%2) + j). V^T operand: ds_read_b64_tr_b16 gives output lane i of a 16-lane group element
+// i%4 of the 8 bytes source lane 4e + i/4 addresses, as its element e; with source lane (e, c) pointing at
+// key e, dims 16*(group%2) + 4c of the dim block, lane i receives V[key e][dim i]: the A operand rows.
+// Softmax: scores stay raw, scale*log2(e) is folded into the exp2 argument; a row's reference max only
+// moves when a tile's max exceeds it by more than 2^8 in probability (then O and l are rescaled), so
+// P <= 256 fits f16 and most tiles skip the rescale. Row sums add the f16-rounded P that PV uses
+// (v_dot2 against ones). Causal: a wave skips tiles past its last row; only tiles crossing the diagonal
+// are masked. Work order: the grid is remapped so that each of the 8 XCDs (blockIdx round-robin) walks a
+// contiguous run of (kv head, query tile, head) items, longest query tiles first, so one kv head's K/V
+// stays in one XCD's L2.
+extern "C" __global__ void __launch_bounds__(512, 1) gi_prefill_fwd(GiPrefillArgs a) {
+    __shared__ __attribute__((aligned(1024))) unsigned char smem[PF_NBUF][2][PF_TILE]; // [buffer][K, V]
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -503,6 +510,26 @@ extern "C" __global__ void __launch_bounds__(256, 2) gi_prefill_fwd(GiPrefillArg
     const int kv_len = a.pos0 + a.n;
     const int k_lim = min(kv_len, a.pos0 + q0 + PF_BQ); // keys any row of the tile may see
     const int ntiles = (k_lim + PF_BK - 1) / PF_BK;
+    const long long kvs = a.kv_stride;
+
+    // ---- staging: waves 0-3 move K rows, waves 4-7 V rows; wave w's load i covers tile rows
+    // 4*(4*(w%4) + i) + lane/16, LDS unit lane%16 holding global unit (lane%16) ^ swizzle(row)
+    const bool stage_v = wave >= 4;
+    const uint16_t* sbase = (stage_v ? a.vc : a.kc) + kvh * a.kv_head_stride;
+    int soff[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int r = 4 * (4 * (wave & 3) + i) + (lane >> 4);
+        const int u = (lane & 15) ^ (stage_v ? ((r & 3) << 2) : (r & 15));
+        soff[i] = (r * (int)kvs + 8 * u) * 2;
+    }
+    auto stage = [&](int t0, int buf) {
+        __amdgpu_buffer_rsrc_t rs = gi_rsrc(sbase + (long long)t0 * kvs, (long long)(kv_len - t0) * kvs * 2);
+        unsigned char* dst = &smem[buf][stage_v ? 1 : 0][4096 * (wave & 3)];
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (GI_LDS void*)(dst + 1024 * i), 16, soff[i], 0, 0, 0);
+    };
 
     // ---- Q as B operands: lane (col = l%32, half = l/32), k-step ks: dims 16ks + 8*half .. +7
     const int qcol = lane & 31, half = lane >> 5;
@@ -527,39 +554,17 @@ extern "C" __global__ void __launch_bounds__(256, 2) gi_prefill_fwd(GiPrefillArg
         }
     }
 
-    // ---- staging roles (wave-uniform): waves 0-1 stage K, waves 2-3 stage V
-    const bool stage_k = wave < 2;
-    const int st = tid & 127;
-    const long long kvs = a.kv_stride;
-    // K: rows (st/16) + 8i, 16-byte column st%16; V: keys 8*(st%8) + i, dims 8*(st/8)..+7
-    const int vdg = st >> 3, vkg = st & 7;
-    const int soff = stage_k ? (((st >> 4) * (int)kvs + 8 * (st & 15)) * 2) : ((8 * vkg * (int)kvs + 8 * vdg) * 2);
-    const int sstep = stage_k ? 8 * (int)kvs * 2 : (int)kvs * 2;
-    const uint16_t* sbase = (stage_k ? a.kc : a.vc) + kvh * a.kv_head_stride;
-    u4 stg[8];
-    auto load_tile = [&](int t0) {
-        __amdgpu_buffer_rsrc_t r = gi_rsrc(sbase + (long long)t0 * kvs, (long long)(kv_len - t0) * kvs * 2);
+    // ---- operand read offsets (bytes within a buffer's K or V tile)
+    const int r = lane & 31;
+    const int kperm = 16 * ((r >> 3) >> 1) + 8 * ((r >> 2) & 1) + 4 * ((r >> 3) & 1) + (r & 3);
+    int koff[8]; // K row kperm (block 0; block 1 is 32 rows = 8192 bytes further), unit 2ks + half, swizzled
 #pragma unroll
-        for (int i = 0; i < 8; i++) stg[i] = gi_load16(r, soff + i * sstep);
-    };
-    auto store_tile = [&](int buf) {
-        if (stage_k) {
+    for (int ks = 0; ks < 8; ks++) koff[ks] = kperm * 256 + (((2 * ks + half) ^ (kperm & 15)) << 4);
+    const int tg = lane >> 4, ts = lane & 15, te = ts >> 2, tc = ts & 3;
+    int voff[4]; // V row 8*half + te (+16ks, +4 for the second read), unit 4*(db ^ te) + 2*(tg%2) + tc/2
 #pragma unroll
-            for (int i = 0; i < 8; i++)
-                *reinterpret_cast<u4*>(&sk[buf][((st >> 4) + 8 * i) * PF_KLD + 8 * (st & 15)]) = stg[i];
-        } else {
-#pragma unroll
-            for (int dd = 0; dd < 8; dd++) {
-                u4 w;
-#pragma unroll
-                for (int p = 0; p < 4; p++) {
-                    uint32_t lo = stg[2 * p][dd >> 1], hi = stg[2 * p + 1][dd >> 1];
-                    w[p] = (dd & 1) ? ((lo >> 16) | (hi & 0xffff0000u)) : ((lo & 0xffffu) | (hi << 16));
-                }
-                *reinterpret_cast<u4*>(&sv[buf][(8 * vdg + dd) * PF_VLD + 8 * vkg]) = w;
-            }
-        }
-    };
+    for (int db = 0; db < 4; db++)
+        voff[db] = (8 * half + te) * 256 + ((4 * (db ^ te) + 2 * (tg & 1) + (tc >> 1)) << 4) + 8 * (tc & 1);
 
     // ---- per-lane state: O^T (4 dim blocks of 32), reference max (raw score units), row sum
     f16x o[4];
@@ -572,34 +577,41 @@ extern "C" __global__ void __launch_bounds__(256, 2) gi_prefill_fwd(GiPrefillArg
     const float th = PF_RESCALE_LOG2 / qs; // rescale threshold in raw score units
     const int wave_first = a.pos0 + q0 + 32 * wave;  // position of the wave's first row
     const int wave_last = wave_first + 31;
-    // A-operand row of this lane in an S^T block: key offset within the block
-    const int r = lane & 31;
-    const int kperm = 16 * ((r >> 3) >> 1) + 8 * ((r >> 2) & 1) + 4 * ((r >> 3) & 1) + (r & 3);
-    const _Float16* krd = &sk[0][0] + kperm * PF_KLD + 8 * half;
-    const _Float16* vrd = &sv[0][0] + r * PF_VLD + 8 * half;
     const h8 ones = h8{1, 1, 1, 1, 1, 1, 1, 1};
     typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 
-    load_tile(0);
-    store_tile(0);
-    __syncthreads();
+    // Pipeline: tiles it+1 and it+2 are in flight when tile it is waited for; after the barrier (every
+    // wave is done with tile it-1) tile it+3 streams into tile it-1's buffer. Each wave waits for its own
+    // loads of tile it (vmcnt counts the 4 loads per younger tile still allowed in flight); the barrier
+    // publishes the whole tile. Barriers are bare s_barrier: __syncthreads' release fence would also wait
+    // for the younger tiles' loads. The memory clobbers keep the compiler from moving LDS accesses across.
+#pragma unroll
+    for (int i = 0; i < PF_NBUF - 1; i++)
+        if (i < ntiles) stage(i * PF_BK, i);
     for (int it = 0; it < ntiles; it++) {
-        const int t0 = it * PF_BK, buf = it & 1;
-        if (it + 1 < ntiles) load_tile(t0 + PF_BK);
+        const int t0 = it * PF_BK, buf = it & (PF_NBUF - 1);
+        const int younger = min(ntiles - 1 - it, PF_NBUF - 2); // tiles after `it` already being loaded
+        if (younger >= 2) __builtin_amdgcn_s_waitcnt(0xF78);      // vmcnt(8)
+        else if (younger == 1) __builtin_amdgcn_s_waitcnt(0xF74); // vmcnt(4)
+        else __builtin_amdgcn_s_waitcnt(0xF70);                   // vmcnt(0)
+        asm volatile("s_barrier" ::: "memory"); // every wave's part of the tile is in; tile it-1 is done
+        if (it + PF_NBUF - 1 < ntiles) stage((it + PF_NBUF - 1) * PF_BK, (it + PF_NBUF - 1) & (PF_NBUF - 1));
         if (t0 <= wave_last) {
-            const _Float16* K = krd + buf * PF_KBUF;
-            const _Float16* V = vrd + buf * PF_VBUF;
+            const unsigned char* K = &smem[buf][0][0];
+            const unsigned char* V = &smem[buf][1][0];
             f16x s[2];
 #pragma unroll
-            for (int bb = 0; bb < 2; bb++) {
+            for (int bb = 0; bb < 2; bb++)
 #pragma unroll
                 for (int e = 0; e < 16; e++) s[bb][e] = 0.f;
+            // the two key blocks' accumulation chains alternate, so consecutive MFMAs are independent
 #pragma unroll
-                for (int ks = 0; ks < 8; ks++) {
-                    h8 kf = *reinterpret_cast<const h8*>(K + 32 * bb * PF_KLD + 16 * ks);
+            for (int ks = 0; ks < 8; ks++)
+#pragma unroll
+                for (int bb = 0; bb < 2; bb++) {
+                    h8 kf = *reinterpret_cast<const h8*>(K + 8192 * bb + koff[ks]);
                     s[bb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[ks], s[bb], 0, 0, 0);
                 }
-            }
             // lane holds, for query qcol: block bb, element 4i + jj -> tile key 32bb + 16(i/2) + 8*half + 4(i%2) + jj
             if (t0 + PF_BK - 1 > wave_first) { // the tile crosses the diagonal (or the end) somewhere in the wave
 #pragma unroll
@@ -641,17 +653,20 @@ extern "C" __global__ void __launch_bounds__(256, 2) gi_prefill_fwd(GiPrefillArg
 #pragma unroll
                 for (int e = 0; e < 4; e++)
                     l_run = __builtin_amdgcn_fdot2(h2{pf[ks][2 * e], pf[ks][2 * e + 1]}, h2{ones[0], ones[1]}, l_run, false);
+            // PV: the four dim blocks' chains alternate
 #pragma unroll
-            for (int db = 0; db < 4; db++) {
+            for (int ks = 0; ks < 4; ks++) {
 #pragma unroll
-                for (int ks = 0; ks < 4; ks++) {
-                    h8 vf = *reinterpret_cast<const h8*>(V + 32 * db * PF_VLD + 16 * ks);
+                for (int db = 0; db < 4; db++) {
+                    const unsigned char* vp = V + voff[db] + 4096 * ks;
+                    gi_s4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((GI_LDS gi_s4*)(vp));
+                    gi_s4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((GI_LDS gi_s4*)(vp + 1024));
+                    h8 vf = __builtin_shufflevector(__builtin_bit_cast(h4x, lo), __builtin_bit_cast(h4x, hi),
+                                                    0, 1, 2, 3, 4, 5, 6, 7);
                     o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf[ks], o[db], 0, 0, 0);
                 }
             }
         }
-        if (it + 1 < ntiles) store_tile(buf ^ 1);
-        __syncthreads();
     }
 
     // ---- normalise and write: lane holds query qcol, dims 32db + 8i + 4*half + jj
@@ -664,10 +679,9 @@ extern "C" __global__ void __launch_bounds__(256, 2) gi_prefill_fwd(GiPrefillArg
             for (int db = 0; db < 4; db++)
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
-                    typedef _Float16 h4 __attribute__((ext_vector_type(4)));
-                    h4 v = h4{(_Float16)(o[db][4 * i] * inv), (_Float16)(o[db][4 * i + 1] * inv),
-                              (_Float16)(o[db][4 * i + 2] * inv), (_Float16)(o[db][4 * i + 3] * inv)};
-                    *reinterpret_cast<h4*>(op + 32 * db + 8 * i) = v;
+                    h4x v = h4x{(_Float16)(o[db][4 * i] * inv), (_Float16)(o[db][4 * i + 1] * inv),
+                                (_Float16)(o[db][4 * i + 2] * inv), (_Float16)(o[db][4 * i + 3] * inv)};
+                    *reinterpret_cast<h4x*>(op + 32 * db + 8 * i) = v;
                 }
         } else {
             float* op = (float*)a.out + (long long)qrow * a.out_stride + h * 128 + 4 * half;
