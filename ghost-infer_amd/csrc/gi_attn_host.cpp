@@ -66,7 +66,7 @@ constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kMaxDevices = 64;
 constexpr int kDecWaves = 4, kDecTile = 32, kDecPairs = 8, kDecPart = 132; // kDecPart: floats per slice partial
 constexpr int kSliceUnit = kDecWaves * kDecTile; // 128 keys
-constexpr int kPrefillBQ = 256;                   // query rows per prefill workgroup (8 waves x 32)
+constexpr int kPrefillBQ = 256;                   // query rows per prefill workgroup
 constexpr int kSplitMaxBatch = 15;                // tokens per split launch (src/cuda.rs:119)
 constexpr int kTiledMinBatch = 16;                // prefill from this many tokens (src/cuda.rs:95)
 
@@ -94,6 +94,7 @@ struct Module {
     bool loaded = false;
     hipModule_t mod = nullptr;
     hipFunction_t dec1 = nullptr, dec2 = nullptr, combine = nullptr, prefill = nullptr;
+    int prefill_threads = 0; // the prefill kernel's block size (its launch bound: waves x 64)
 };
 std::mutex g_mu;
 Module g_mods[kMaxDevices];
@@ -129,6 +130,12 @@ int load_module(const char* path, Module** out) {
                 m.mod = nullptr;
                 return e;
             }
+        if (int e = check(hipFuncGetAttribute(&m.prefill_threads, HIP_FUNC_ATTRIBUTE_MAX_THREADS_PER_BLOCK, m.prefill),
+                          "hipFuncGetAttribute(gi_prefill_fwd)")) {
+            (void)hipModuleUnload(m.mod);
+            m.mod = nullptr;
+            return e;
+        }
         m.loaded = true;
     }
     *out = &m;
@@ -306,7 +313,7 @@ int gi_attn_prefill(void* stream, const void* q, int q_dtype, long long q_stride
     a.q_f16 = q_dtype == GI_F16;
     a.out_f16 = out_dtype == GI_F16;
     int qtiles = (n + kPrefillBQ - 1) / kPrefillBQ;
-    return launch(m->prefill, dim3(qtiles * n_heads, 1, 1), dim3(512), (hipStream_t)stream, &a, sizeof a);
+    return launch(m->prefill, dim3(qtiles * n_heads, 1, 1), dim3(m->prefill_threads), (hipStream_t)stream, &a, sizeof a);
 }
 
 int gi_attention(void* stream, const float* qkv, const uint16_t* kc, const uint16_t* vc, float* out,

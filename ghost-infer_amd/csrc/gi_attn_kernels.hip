@@ -464,7 +464,7 @@ struct GiPrefillArgs {
 
 #define PF_WAVES 8         // waves per workgroup, 32 query rows each
 #define PF_BQ 256          // query rows per workgroup
-#define PF_NBUF 4          // LDS tile buffers: tiles it+1..it+3 stream in while tile it is used
+#define PF_NBUF 4          // LDS tile buffers
 #define PF_BK 64           // keys per tile
 #define PF_TILE 16384      // bytes of one K or V tile: 64 rows of 256 bytes
 #define PF_RESCALE_LOG2 8.0f
@@ -474,11 +474,15 @@ typedef short gi_s4 __attribute__((__vector_size__(8))); // 4 f16 as ds_read_b64
 // One workgroup = (head, 256 query rows); wave w of 8 owns rows 32w..32w+31 of the tile. Per 64-key tile:
 //   S^T[key, q] = K[key, :] . Q[q, :]       v_mfma_f32_32x32x16_f16, K from LDS (A), Q in registers (B)
 //   O^T[d, q]  += V^T[d, key] . P^T[key, q]  V^T from LDS (A, by transposing reads), P^T from S^T (B)
+// Software pipeline inside each wave: the softmax of tile t (VALU) runs between the MFMAs of QK for
+// tile t+1 and of PV for tile t, which do not depend on it, so the VALU work hides under the matrix core's
+// 32-cycle MFMAs instead of following them (a SIMD does not overlap one wave's VALU with another wave's
+// back-to-back MFMAs, so the overlap has to come from within the wave).
 // Staging: K and V tiles go global -> LDS with direct-to-LDS buffer loads (no registers, no VALU): each of
 // the 8 waves moves 4 KB per tile as 4 loads of 1 KB (64 lanes x 16 bytes, written at base + 16*lane).
 // Rows are stored unpadded with an XOR swizzle of their 16-byte units (K: unit ^ row%16, V: unit ^
-// 4*(row%4)) so the MFMA operand reads hit distinct banks. Four LDS buffers keep three tiles in flight (an
-// L2/MALL round trip is several tiles of compute); one barrier per tile.
+// 4*(row%4)) so the MFMA operand reads hit distinct banks. Iteration t reads V of tile t and K of tile
+// t+1; once every wave has passed its barrier tile t-1 is free and tile t+3 streams into its buffer.
 // Keys past the cache's end read as zeros (buffer bounds) and are masked.
 // K operand: A-row r of S^T block bb holds tile key 32bb + 16(i/2) + 8h + 4(i%2) + j for r = 8i + 4h + j,
 // so the 16 values a lane holds per block are exactly the keys its PV B operand needs (k-step 2bb + i/2,
@@ -488,10 +492,10 @@ typedef short gi_s4 __attribute__((__vector_size__(8))); // 4 f16 as ds_read_b64
 // Softmax: scores stay raw, scale*log2(e) is folded into the exp2 argument; a row's reference max only
 // moves when a tile's max exceeds it by more than 2^8 in probability (then O and l are rescaled), so
 // P <= 256 fits f16 and most tiles skip the rescale. Row sums add the f16-rounded P that PV uses
-// (v_dot2 against ones). Causal: a wave skips tiles past its last row; only tiles crossing the diagonal
-// are masked. Work order: the grid is remapped so that each of the 8 XCDs (blockIdx round-robin) walks a
-// contiguous run of (kv head, query tile, head) items, longest query tiles first, so one kv head's K/V
-// stays in one XCD's L2.
+// (v_dot2 against ones). Causal: a wave skips tiles past its last row (keeping every barrier); only
+// tiles crossing the diagonal are masked. Work order: the grid is remapped so that each of the 8 XCDs
+// (blockIdx round-robin) walks a contiguous run of (kv head, query tile, head) items, longest query
+// tiles first, so one kv head's K/V stays in one XCD's L2.
 extern "C" __global__ void __launch_bounds__(512, 1) gi_prefill_fwd(GiPrefillArgs a) {
     __shared__ __attribute__((aligned(1024))) unsigned char smem[PF_NBUF][2][PF_TILE]; // [buffer][K, V]
 
@@ -523,9 +527,10 @@ extern "C" __global__ void __launch_bounds__(512, 1) gi_prefill_fwd(GiPrefillArg
         const int u = (lane & 15) ^ (stage_v ? ((r & 3) << 2) : (r & 15));
         soff[i] = (r * (int)kvs + 8 * u) * 2;
     }
-    auto stage = [&](int t0, int buf) {
+    auto stage = [&](int t) {
+        const int t0 = t * PF_BK;
         __amdgpu_buffer_rsrc_t rs = gi_rsrc(sbase + (long long)t0 * kvs, (long long)(kv_len - t0) * kvs * 2);
-        unsigned char* dst = &smem[buf][stage_v ? 1 : 0][4096 * (wave & 3)];
+        unsigned char* dst = &smem[t & (PF_NBUF - 1)][stage_v ? 1 : 0][4096 * (wave & 3)];
 #pragma unroll
         for (int i = 0; i < 4; i++)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (GI_LDS void*)(dst + 1024 * i), 16, soff[i], 0, 0, 0);
@@ -557,14 +562,28 @@ extern "C" __global__ void __launch_bounds__(512, 1) gi_prefill_fwd(GiPrefillArg
     // ---- operand read offsets (bytes within a buffer's K or V tile)
     const int r = lane & 31;
     const int kperm = 16 * ((r >> 3) >> 1) + 8 * ((r >> 2) & 1) + 4 * ((r >> 3) & 1) + (r & 3);
-    int koff[8]; // K row kperm (block 0; block 1 is 32 rows = 8192 bytes further), unit 2ks + half, swizzled
-#pragma unroll
-    for (int ks = 0; ks < 8; ks++) koff[ks] = kperm * 256 + (((2 * ks + half) ^ (kperm & 15)) << 4);
+    // K row kperm (block 1 is 32 rows = 8192 bytes further), unit (2ks + half) ^ (kperm % 16)
+    //   = 2(ks ^ ky) + (half ^ kperm % 2)
+    const int kbase = kperm * 256 + ((half ^ (kperm & 1)) << 4);
+    const int ky = (kperm >> 1) & 7;
     const int tg = lane >> 4, ts = lane & 15, te = ts >> 2, tc = ts & 3;
-    int voff[4]; // V row 8*half + te (+16ks, +4 for the second read), unit 4*(db ^ te) + 2*(tg%2) + tc/2
+    // V row 8*half + te (+16ks, +4 for the second read), unit 4*(db ^ te) + 2*(tg%2) + tc/2
+    const int vbase = (8 * half + te) * 256 + ((2 * (tg & 1) + (tc >> 1)) << 4) + 8 * (tc & 1);
+
+    auto qk = [&](int t, f16x* s) { // S^T of tile t (its K in buffer t%4)
+        const unsigned char* K = &smem[t & (PF_NBUF - 1)][0][0];
 #pragma unroll
-    for (int db = 0; db < 4; db++)
-        voff[db] = (8 * half + te) * 256 + ((4 * (db ^ te) + 2 * (tg & 1) + (tc >> 1)) << 4) + 8 * (tc & 1);
+        for (int bb = 0; bb < 2; bb++)
+#pragma unroll
+            for (int e = 0; e < 16; e++) s[bb][e] = 0.f;
+#pragma unroll
+        for (int ks = 0; ks < 8; ks++)
+#pragma unroll
+            for (int bb = 0; bb < 2; bb++) {
+                h8 kf = *reinterpret_cast<const h8*>(K + 8192 * bb + kbase + 32 * (ks ^ ky));
+                s[bb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[ks], s[bb], 0, 0, 0);
+            }
+    };
 
     // ---- per-lane state: O^T (4 dim blocks of 32), reference max (raw score units), row sum
     f16x o[4];
@@ -577,96 +596,94 @@ extern "C" __global__ void __launch_bounds__(512, 1) gi_prefill_fwd(GiPrefillArg
     const float th = PF_RESCALE_LOG2 / qs; // rescale threshold in raw score units
     const int wave_first = a.pos0 + q0 + 32 * wave;  // position of the wave's first row
     const int wave_last = wave_first + 31;
-    const h8 ones = h8{1, 1, 1, 1, 1, 1, 1, 1};
+    const int my_tiles = min(ntiles, wave_last / PF_BK + 1); // tiles this wave computes
     typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 
-    // Pipeline: tiles it+1 and it+2 are in flight when tile it is waited for; after the barrier (every
-    // wave is done with tile it-1) tile it+3 streams into tile it-1's buffer. Each wave waits for its own
-    // loads of tile it (vmcnt counts the 4 loads per younger tile still allowed in flight); the barrier
-    // publishes the whole tile. Barriers are bare s_barrier: __syncthreads' release fence would also wait
-    // for the younger tiles' loads. The memory clobbers keep the compiler from moving LDS accesses across.
+    // Prologue: tiles 0-2 start loading; tile 0 is waited for and published, and its QK issued.
+    stage(0);
+    if (ntiles > 1) stage(1);
+    if (ntiles > 2) stage(2);
+    if (ntiles > 2) __builtin_amdgcn_s_waitcnt(0xF78);      // vmcnt(8): tile 0 is in
+    else if (ntiles > 1) __builtin_amdgcn_s_waitcnt(0xF74); // vmcnt(4)
+    else __builtin_amdgcn_s_waitcnt(0xF70);                 // vmcnt(0)
+    asm volatile("s_barrier" ::: "memory");
+    // One pipeline step: tile it's softmax and PV, with QK of tile it+1 into sn (past this wave's last
+    // tile that QK reads a stale buffer and is never used). No branch separates the QK MFMAs from the
+    // VALU work they hide.
+    auto step = [&](int it, f16x* s, f16x* sn) {
+        qk(it + 1, sn);
+        float mx = GI_NEG_INF;
 #pragma unroll
-    for (int i = 0; i < PF_NBUF - 1; i++)
-        if (i < ntiles) stage(i * PF_BK, i);
-    for (int it = 0; it < ntiles; it++) {
-        const int t0 = it * PF_BK, buf = it & (PF_NBUF - 1);
-        const int younger = min(ntiles - 1 - it, PF_NBUF - 2); // tiles after `it` already being loaded
-        if (younger >= 2) __builtin_amdgcn_s_waitcnt(0xF78);      // vmcnt(8)
-        else if (younger == 1) __builtin_amdgcn_s_waitcnt(0xF74); // vmcnt(4)
-        else __builtin_amdgcn_s_waitcnt(0xF70);                   // vmcnt(0)
-        asm volatile("s_barrier" ::: "memory"); // every wave's part of the tile is in; tile it-1 is done
-        if (it + PF_NBUF - 1 < ntiles) stage((it + PF_NBUF - 1) * PF_BK, (it + PF_NBUF - 1) & (PF_NBUF - 1));
-        if (t0 <= wave_last) {
-            const unsigned char* K = &smem[buf][0][0];
-            const unsigned char* V = &smem[buf][1][0];
-            f16x s[2];
+        for (int bb = 0; bb < 2; bb++)
 #pragma unroll
-            for (int bb = 0; bb < 2; bb++)
+            for (int e = 0; e < 16; e++) mx = fmaxf(mx, s[bb][e]);
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        const bool up = mx > m_run + th;
+        if (__builtin_amdgcn_ballot_w64(up)) { // some row's max moved: rescale (alpha = 1 for the others)
+            const float m_new = up ? mx : m_run;
+            const float alpha = __builtin_amdgcn_exp2f((m_run - m_new) * qs);
+            m_run = m_new;
+            l_run *= alpha;
 #pragma unroll
-                for (int e = 0; e < 16; e++) s[bb][e] = 0.f;
-            // the two key blocks' accumulation chains alternate, so consecutive MFMAs are independent
+            for (int db = 0; db < 4; db++) o[db] *= alpha;
+        }
+        // probabilities of k-step ks feed the PV MFMAs of k-step ks
+        const float mo = -m_run * qs;
+        const unsigned char* V = &smem[it & (PF_NBUF - 1)][1][0];
 #pragma unroll
-            for (int ks = 0; ks < 8; ks++)
+        for (int ks = 0; ks < 4; ks++) {
+            const int bb = ks >> 1;
+            h8 pf;
 #pragma unroll
-                for (int bb = 0; bb < 2; bb++) {
-                    h8 kf = *reinterpret_cast<const h8*>(K + 8192 * bb + koff[ks]);
-                    s[bb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[ks], s[bb], 0, 0, 0);
-                }
-            // lane holds, for query qcol: block bb, element 4i + jj -> tile key 32bb + 16(i/2) + 8*half + 4(i%2) + jj
+            for (int e = 0; e < 8; e += 2) {
+                const int i = 2 * (ks & 1) + (e >> 2), jj = e & 3;
+                const _Float16 h0 = (_Float16)__builtin_amdgcn_exp2f(fmaf(s[bb][4 * i + jj], qs, mo));
+                const _Float16 h1 = (_Float16)__builtin_amdgcn_exp2f(fmaf(s[bb][4 * i + jj + 1], qs, mo));
+                pf[e] = h0;
+                pf[e + 1] = h1;
+                l_run = __builtin_amdgcn_fdot2(h2{h0, h1}, h2{(_Float16)1.f, (_Float16)1.f}, l_run, false);
+            }
+#pragma unroll
+            for (int db = 0; db < 4; db++) {
+                const unsigned char* vp = V + vbase + ((db ^ te) << 6) + 4096 * ks;
+                gi_s4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((GI_LDS gi_s4*)(vp));
+                gi_s4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((GI_LDS gi_s4*)(vp + 1024));
+                h8 vf = __builtin_shufflevector(__builtin_bit_cast(h4x, lo), __builtin_bit_cast(h4x, hi),
+                                                0, 1, 2, 3, 4, 5, 6, 7);
+                o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf, o[db], 0, 0, 0);
+            }
+        }
+    };
+    // Iteration it: before the barrier each wave waits for its own loads of tile it+1 (tile it+2's may
+    // stay in flight); the barrier publishes the tile and tells that every wave is done with tile it-1,
+    // whose buffer then takes tile it+3. Barriers are bare s_barrier (__syncthreads' release fence would
+    // also wait for tile it+2's loads); the memory clobber keeps LDS accesses on their side.
+    auto iteration = [&](int it, f16x* s, f16x* sn) {
+        if (it + 2 < ntiles) __builtin_amdgcn_s_waitcnt(0xF74); // vmcnt(4)
+        else __builtin_amdgcn_s_waitcnt(0xF70);                // vmcnt(0)
+        asm volatile("s_barrier" ::: "memory");
+        if (it + 3 < ntiles) stage(it + 3);
+        if (it < my_tiles) {
+            const int t0 = it * PF_BK;
             if (t0 + PF_BK - 1 > wave_first) { // the tile crosses the diagonal (or the end) somewhere in the wave
+                // lane holds, for query qcol: block bb, element 4i + jj -> tile key 32bb + 16(i/2) + 8*half + 4(i%2) + jj
+                const int lim = qpos - t0 - 8 * half;
 #pragma unroll
                 for (int bb = 0; bb < 2; bb++)
 #pragma unroll
                     for (int i = 0; i < 4; i++)
 #pragma unroll
-                        for (int jj = 0; jj < 4; jj++) {
-                            int key = t0 + 32 * bb + 16 * (i >> 1) + 8 * half + 4 * (i & 1) + jj;
-                            if (key > qpos) s[bb][4 * i + jj] = GI_NEG_INF;
-                        }
+                        for (int jj = 0; jj < 4; jj++)
+                            if (32 * bb + 16 * (i >> 1) + 4 * (i & 1) + jj > lim) s[bb][4 * i + jj] = GI_NEG_INF;
             }
-            float mx = GI_NEG_INF;
-#pragma unroll
-            for (int bb = 0; bb < 2; bb++)
-#pragma unroll
-                for (int e = 0; e < 16; e++) mx = fmaxf(mx, s[bb][e]);
-            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-            const bool up = mx > m_run + th;
-            if (__builtin_amdgcn_ballot_w64(up)) { // some row's max moved: rescale (alpha = 1 for the others)
-                const float m_new = up ? mx : m_run;
-                const float alpha = __builtin_amdgcn_exp2f((m_run - m_new) * qs);
-                m_run = m_new;
-                l_run *= alpha;
-#pragma unroll
-                for (int db = 0; db < 4; db++) o[db] *= alpha;
-            }
-            const float mo = -m_run * qs;
-            h8 pf[4]; // PV B operands, k-step ks = 2bb + i/2, element 4(i%2) + jj
-#pragma unroll
-            for (int bb = 0; bb < 2; bb++)
-#pragma unroll
-                for (int i = 0; i < 4; i++)
-#pragma unroll
-                    for (int jj = 0; jj < 4; jj++)
-                        pf[2 * bb + (i >> 1)][4 * (i & 1) + jj] = (_Float16)__builtin_amdgcn_exp2f(fmaf(s[bb][4 * i + jj], qs, mo));
-#pragma unroll
-            for (int ks = 0; ks < 4; ks++)
-#pragma unroll
-                for (int e = 0; e < 4; e++)
-                    l_run = __builtin_amdgcn_fdot2(h2{pf[ks][2 * e], pf[ks][2 * e + 1]}, h2{ones[0], ones[1]}, l_run, false);
-            // PV: the four dim blocks' chains alternate
-#pragma unroll
-            for (int ks = 0; ks < 4; ks++) {
-#pragma unroll
-                for (int db = 0; db < 4; db++) {
-                    const unsigned char* vp = V + voff[db] + 4096 * ks;
-                    gi_s4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((GI_LDS gi_s4*)(vp));
-                    gi_s4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((GI_LDS gi_s4*)(vp + 1024));
-                    h8 vf = __builtin_shufflevector(__builtin_bit_cast(h4x, lo), __builtin_bit_cast(h4x, hi),
-                                                    0, 1, 2, 3, 4, 5, 6, 7);
-                    o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf[ks], o[db], 0, 0, 0);
-                }
-            }
+            step(it, s, sn);
         }
+    };
+    f16x sa[2], sb[2]; // scores of alternate tiles
+    if (my_tiles > 0) qk(0, sa);
+    for (int it = 0; it < ntiles; it += 2) {
+        iteration(it, sa, sb);
+        if (it + 1 < ntiles) iteration(it + 1, sb, sa);
     }
 
     // ---- normalise and write: lane holds query qcol, dims 32db + 8i + 4*half + jj
