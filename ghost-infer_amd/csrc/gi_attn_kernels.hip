@@ -540,21 +540,28 @@ extern "C" __global__ void __launch_bounds__(512, 1) gi_prefill_fwd(GiPrefillArg
     const int qcol = lane & 31, half = lane >> 5;
     const int qrow = q0 + 32 * wave + qcol;      // this lane's query row
     const int qpos = a.pos0 + qrow;              // its position
+    // Q is held pre-multiplied by scale*log2(e), so scores come out of the MFMA in log2 units (the f16
+    // rounding of the scaled value is the same size as the rounding of Q itself)
+    const float qs = a.qscale;
     h8 qf[8];
     {
         const int qr = qrow < a.n ? qrow : a.n - 1; // rows past n compute garbage that is never written
         if (a.q_f16) {
             const _Float16* qp = (const _Float16*)a.q + (long long)qr * a.q_stride + h * 128 + 8 * half;
 #pragma unroll
-            for (int ks = 0; ks < 8; ks++) qf[ks] = __builtin_bit_cast(h8, *reinterpret_cast<const u4*>(qp + 16 * ks));
+            for (int ks = 0; ks < 8; ks++) {
+                const h8 x = __builtin_bit_cast(h8, *reinterpret_cast<const u4*>(qp + 16 * ks));
+#pragma unroll
+                for (int e = 0; e < 8; e++) qf[ks][e] = (_Float16)((float)x[e] * qs);
+            }
         } else {
             const float* qp = (const float*)a.q + (long long)qr * a.q_stride + h * 128 + 8 * half;
 #pragma unroll
             for (int ks = 0; ks < 8; ks++) {
                 float4 x0 = *reinterpret_cast<const float4*>(qp + 16 * ks);
                 float4 x1 = *reinterpret_cast<const float4*>(qp + 16 * ks + 4);
-                qf[ks] = h8{(_Float16)x0.x, (_Float16)x0.y, (_Float16)x0.z, (_Float16)x0.w,
-                            (_Float16)x1.x, (_Float16)x1.y, (_Float16)x1.z, (_Float16)x1.w};
+                qf[ks] = h8{(_Float16)(x0.x * qs), (_Float16)(x0.y * qs), (_Float16)(x0.z * qs), (_Float16)(x0.w * qs),
+                            (_Float16)(x1.x * qs), (_Float16)(x1.y * qs), (_Float16)(x1.z * qs), (_Float16)(x1.w * qs)};
             }
         }
     }
@@ -570,12 +577,22 @@ extern "C" __global__ void __launch_bounds__(512, 1) gi_prefill_fwd(GiPrefillArg
     // V row 8*half + te (+16ks, +4 for the second read), unit 4*(db ^ te) + 2*(tg%2) + tc/2
     const int vbase = (8 * half + te) * 256 + ((2 * (tg & 1) + (tc >> 1)) << 4) + 8 * (tc & 1);
 
-    auto qk = [&](int t, f16x* s) { // S^T of tile t (its K in buffer t%4)
+    // ---- per-lane state: O^T (4 dim blocks of 32), reference max (log2 units; tile 0 sets it), row sum
+    f16x o[4];
+#pragma unroll
+    for (int db = 0; db < 4; db++)
+#pragma unroll
+        for (int e = 0; e < 16; e++) o[db][e] = 0.f;
+    float m_run = 0.f, l_run = 0.f;
+
+    // S^T of tile t (its K in buffer t%4) minus the row's reference max: the accumulators start at -m_run,
+    // so the MFMA output is the exp2 argument itself
+    auto qk = [&](int t, f16x* s) {
         const unsigned char* K = &smem[t & (PF_NBUF - 1)][0][0];
 #pragma unroll
         for (int bb = 0; bb < 2; bb++)
 #pragma unroll
-            for (int e = 0; e < 16; e++) s[bb][e] = 0.f;
+            for (int e = 0; e < 16; e++) s[bb][e] = -m_run;
 #pragma unroll
         for (int ks = 0; ks < 8; ks++)
 #pragma unroll
@@ -585,15 +602,6 @@ extern "C" __global__ void __launch_bounds__(512, 1) gi_prefill_fwd(GiPrefillArg
             }
     };
 
-    // ---- per-lane state: O^T (4 dim blocks of 32), reference max (raw score units), row sum
-    f16x o[4];
-#pragma unroll
-    for (int db = 0; db < 4; db++)
-#pragma unroll
-        for (int e = 0; e < 16; e++) o[db][e] = 0.f;
-    float m_run = GI_NEG_INF, l_run = 0.f;
-    const float qs = a.qscale;
-    const float th = PF_RESCALE_LOG2 / qs; // rescale threshold in raw score units
     const int wave_first = a.pos0 + q0 + 32 * wave;  // position of the wave's first row
     const int wave_last = wave_first + 31;
     const int my_tiles = min(ntiles, wave_last / PF_BK + 1); // tiles this wave computes
@@ -617,18 +625,25 @@ extern "C" __global__ void __launch_bounds__(512, 1) gi_prefill_fwd(GiPrefillArg
         for (int bb = 0; bb < 2; bb++)
 #pragma unroll
             for (int e = 0; e < 16; e++) mx = fmaxf(mx, s[bb][e]);
-        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-        const bool up = mx > m_run + th;
-        if (__builtin_amdgcn_ballot_w64(up)) { // some row's max moved: rescale (alpha = 1 for the others)
-            const float m_new = up ? mx : m_run;
-            const float alpha = __builtin_amdgcn_exp2f((m_run - m_new) * qs);
-            m_run = m_new;
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64)); // the tile's row max relative to m_run
+        const bool up = mx > PF_RESCALE_LOG2 || it == 0;
+        if (__builtin_amdgcn_ballot_w64(up)) {
+            // some row's max moved (tile 0: every row takes its first max): shift the reference by delta,
+            // rescale O and l (alpha = 1 for the other rows; O and l are still 0 at tile 0) and the scores
+            // already computed against the old reference, this tile's and the next one's
+            const float delta = up ? mx : 0.f;
+            const float alpha = __builtin_amdgcn_exp2f(-fmaxf(delta, 0.f));
+            m_run += delta;
             l_run *= alpha;
 #pragma unroll
             for (int db = 0; db < 4; db++) o[db] *= alpha;
+#pragma unroll
+            for (int bb = 0; bb < 2; bb++) {
+                s[bb] -= delta;
+                sn[bb] -= delta;
+            }
         }
         // probabilities of k-step ks feed the PV MFMAs of k-step ks
-        const float mo = -m_run * qs;
         const unsigned char* V = &smem[it & (PF_NBUF - 1)][1][0];
 #pragma unroll
         for (int ks = 0; ks < 4; ks++) {
@@ -637,8 +652,8 @@ extern "C" __global__ void __launch_bounds__(512, 1) gi_prefill_fwd(GiPrefillArg
 #pragma unroll
             for (int e = 0; e < 8; e += 2) {
                 const int i = 2 * (ks & 1) + (e >> 2), jj = e & 3;
-                const _Float16 h0 = (_Float16)__builtin_amdgcn_exp2f(fmaf(s[bb][4 * i + jj], qs, mo));
-                const _Float16 h1 = (_Float16)__builtin_amdgcn_exp2f(fmaf(s[bb][4 * i + jj + 1], qs, mo));
+                const _Float16 h0 = (_Float16)__builtin_amdgcn_exp2f(s[bb][4 * i + jj]);
+                const _Float16 h1 = (_Float16)__builtin_amdgcn_exp2f(s[bb][4 * i + jj + 1]);
                 pf[e] = h0;
                 pf[e + 1] = h1;
                 l_run = __builtin_amdgcn_fdot2(h2{h0, h1}, h2{(_Float16)1.f, (_Float16)1.f}, l_run, false);
