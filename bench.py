@@ -1,7 +1,7 @@
 """Benchmark of the gfx950 attention hot path on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload decode64k|decode4k|verify|prefill8k|chunked]
-                    [--no-cpu-baseline] [--no-secondary]
+                    [--no-cpu-baseline] [--no-secondary] [--reference-layout]
 
 A step is one pass of the hot path over one batch of synthetic seeded input already resident in HBM:
   decode64k  config 2: one token, 32 query / 4 kv heads, head 128, 65536-key f16 cache (the default: the
@@ -44,6 +44,43 @@ def seeded_cache(gen, rows, n_kv, dev, torch, layout="reference"):
     k = torch.randn(shape, generator=gen, device=dev, dtype=torch.float32).half()
     v = torch.randn(shape, generator=gen, device=dev, dtype=torch.float32).half()
     return k, v
+
+
+def kernel_times(gi_attn, fn, steps, torch, kinds):
+    """Runs `steps` more steps eagerly with the library's per-kernel event timing on (HIP events recorded
+    around each launch, on the stream it is launched on) and returns {kind: (mean ms per launch,
+    launches)}."""
+    for k in kinds:
+        gi_attn.kernel_timing_read(k)  # drop anything recorded before
+    gi_attn.kernel_timing(True)
+    try:
+        # a spin kernel in front keeps the GPU busy while the host enqueues every step, so each event pair
+        # brackets its kernel back to back and not the host's submission gaps
+        torch.cuda._sleep(int(5e7))
+        for i in range(steps):
+            fn(i)
+        torch.cuda.synchronize()
+    finally:
+        gi_attn.kernel_timing(False)
+    res = {}
+    for k in kinds:
+        ms, n = gi_attn.kernel_timing_read(k)
+        res[k] = (ms / n if n else None, n)
+    return res
+
+
+def profile_traffic(name):
+    """HBM bytes per launch of a kernel from the committed rocprofv3 --pmc summary profiles/<name>.md
+    (its line "traffic_bytes_per_launch: N"), or None when there is none."""
+    path = os.path.join(ROOT, "profiles", name + ".md")
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.strip().startswith("traffic_bytes_per_launch:"):
+                    return int(float(line.split(":", 1)[1]))
+    except OSError:
+        pass
+    return None
 
 
 def time_steps(fn, steps, warmup, torch):
@@ -102,9 +139,9 @@ def decode_workload(torch, gi_attn, dev, ctx, n_heads, n_kv, n_tok, steps, warmu
         gi_attn.decode(q, k, v, pos0, n_heads, n_kv, out=out, workspace=ws, kv_layout=layout)
 
     t = time_steps_graph(step, steps, warmup, torch)
-    algo_bytes = 2 * ctx * n_kv * HD * 2
-    return {"seconds": t, "bytes": algo_bytes, "layers": layers, "q": q, "cache": caches[0], "pos0": pos0,
-            "layout": layout}
+    kv_bytes = 2 * ctx * n_kv * HD * 2
+    return {"seconds": t, "bytes": kv_bytes, "layers": layers, "q": q, "cache": caches[0], "pos0": pos0,
+            "layout": layout, "step": step, "ws": ws}
 
 
 def prefill_flops(n, pos0, n_heads):
@@ -124,7 +161,7 @@ def prefill_workload(torch, gi_attn, dev, n, n_heads, n_kv, steps, warmup, seed)
         gi_attn.prefill(q, k, v, 0, n_heads, n_kv, out=out)
 
     t = time_steps(step, steps, warmup, torch)
-    return {"seconds": t, "flops": prefill_flops(n, 0, n_heads)}
+    return {"seconds": t, "flops": prefill_flops(n, 0, n_heads), "step": step}
 
 
 def chunked_workload(torch, gi_attn, dev, total, chunk, n_heads, n_kv, seed):
@@ -190,6 +227,16 @@ def cpu_baseline_decode(q, cache, pos0, n_heads, n_kv, budget_s=12.0):
     return times[len(times) // 2], threads, len(times)
 
 
+def prefill_roofline(gi_attn, r, steps, torch):
+    """Roofline object of the prefill kernel: algorithmic flops of one launch / its mean duration."""
+    ms, n = kernel_times(gi_attn, r["step"], steps, torch, ("prefill",))["prefill"]
+    tf = r["flops"] / (ms / 1e3) / 1e12
+    return {"bound": "mfma", "achieved": round(tf, 1), "peak": F16_DENSE_PEAK_TFLOPS, "unit": "TFLOP/s",
+            "frac": round(tf / F16_DENSE_PEAK_TFLOPS, 4), "traffic": profile_traffic("pmc_prefill_prefill8k"),
+            "kernel": "gi_prefill_fwd", "algorithmic_flops_per_launch": r["flops"],
+            "kernel_ms_per_launch": round(ms, 5), "launches_timed": n}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -199,6 +246,8 @@ def main():
                     choices=["decode64k", "decode4k", "verify", "prefill8k", "chunked"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-secondary", action="store_true")
+    ap.add_argument("--reference-layout", action="store_true",
+                    help="decode workloads: also time the reference's cache layout")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: this build has no multi-GPU path (asked for {args.gpus})",
@@ -223,24 +272,35 @@ def main():
         log(f"[bench] {cfg}")
         r = decode_workload(torch, gi_attn, dev, ctx, n_heads, n_kv, n_tok, args.steps, args.warmup, 1234)
         gbs = r["bytes"] / r["seconds"] / 1e9
-        r_ref = decode_workload(torch, gi_attn, dev, ctx, n_heads, n_kv, n_tok, args.steps, args.warmup, 1234,
-                                layout="reference")
-        gbs_ref = r_ref["bytes"] / r_ref["seconds"] / 1e9
-        r_ref_ms = r_ref["seconds"] * 1e3
-        del r_ref
         chunk, nsplit = gi_attn.decode_plan(ctx, n_tok, n_heads, n_kv)
+        kt = kernel_times(gi_attn, r["step"], args.steps, torch, ("decode_partial", "decode_combine"))
+        part_ms, part_n = kt["decode_partial"]
+        comb_ms, _ = kt["decode_combine"]
+        # algorithmic bytes of one split-kernel launch: K and V of every span key, the queries, and the
+        # slice partials it writes ([token][head][slice][hd + 4] f32)
+        part_bytes = r["bytes"] + n_tok * n_heads * HD * 4 + n_tok * n_heads * nsplit * (HD + 4) * 4
+        kern_gbs = part_bytes / (part_ms / 1e3) / 1e9
+        traffic = profile_traffic(f"pmc_decode_partial_{w}")
         result.update({
             "value": round(gbs, 1), "unit": "GB/s", "ms_per_step": r["seconds"] * 1e3, "dtype": "f16 K/V, f32 math",
             "config": {"workload": cfg, "ctx": ctx, "n_tok": n_tok, "n_heads": n_heads, "n_kv": n_kv, "hd": HD,
                        "kv_bytes_per_step": r["bytes"], "layers_rotated": r["layers"],
-                       "slices": nsplit, "keys_per_slice": chunk, "kv_layout": "head_major [n_kv][ctx][128]",
-                       "reference_layout_GBs": round(gbs_ref, 1),
-                       "reference_layout_ms_per_step": r_ref_ms},
-            "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                         "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
-                         "note": "achieved = K+V bytes / decode step time (split kernel + combine kernel), "
-                                 "steps replayed from a HIP graph"},
+                       "slices": nsplit, "keys_per_slice": chunk, "kv_layout": "head_major [n_kv][ctx][128]"},
+            "roofline": {"bound": "hbm", "achieved": round(kern_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(kern_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
+                         "kernel": "gi_decode_partial (split-K pass)",
+                         "algorithmic_bytes_per_launch": part_bytes,
+                         "kernel_ms_per_launch": round(part_ms, 5), "launches_timed": part_n,
+                         "combine_ms_per_launch": round(comb_ms, 5) if comb_ms else None,
+                         "step_GBs_KV": round(gbs, 1)},
         })
+        if args.reference_layout:
+            # the same decode over caches in the reference's [position][n_kv][128] layout
+            r_ref = decode_workload(torch, gi_attn, dev, ctx, n_heads, n_kv, n_tok, args.steps, args.warmup, 1234,
+                                    layout="reference")
+            result["config"]["reference_layout_GBs"] = round(r_ref["bytes"] / r_ref["seconds"] / 1e9, 1)
+            result["config"]["reference_layout_ms_per_step"] = r_ref["seconds"] * 1e3
+            del r_ref
         if not args.no_cpu_baseline:
             log("[bench] cpu baseline (oracle, Model::attention restatement)")
             t_cpu, threads, reps = cpu_baseline_decode(r["q"], r["cache"], r["pos0"], n_heads, n_kv)
@@ -254,8 +314,7 @@ def main():
         result.update({
             "value": round(tf, 1), "unit": "TFLOP/s", "ms_per_step": r["seconds"] * 1e3, "dtype": "f16 MFMA, f32 acc",
             "config": {"workload": "config 3: causal prefill, 8192 tokens, 32q/8kv, hd 128", "flops_per_step": r["flops"]},
-            "roofline": {"bound": "mfma", "achieved": round(tf, 1), "peak": F16_DENSE_PEAK_TFLOPS, "unit": "TFLOP/s",
-                         "frac": round(tf / F16_DENSE_PEAK_TFLOPS, 4), "traffic": None},
+            "roofline": prefill_roofline(gi_attn, r, args.steps, torch),
         })
     else:
         log("[bench] config 5: chunked prefill 131072 in 2048 chunks, 32q/4kv")
@@ -273,11 +332,12 @@ def main():
         })
         result["steps"] = len(per)
     if w == "decode64k" and not args.no_secondary:
-        r = prefill_workload(torch, gi_attn, dev, 8192, 32, 8, 20, 3, 99)
+        r = prefill_workload(torch, gi_attn, dev, 8192, 32, 8, 30, 10, 99)
         tf = r["flops"] / r["seconds"] / 1e12
         result["secondary"] = {"prefill8k": {"value": round(tf, 1), "unit": "TFLOP/s",
                                              "ms_per_step": r["seconds"] * 1e3,
-                                             "frac_of_f16_dense_peak": round(tf / F16_DENSE_PEAK_TFLOPS, 4)},
+                                             "frac_of_f16_dense_peak": round(tf / F16_DENSE_PEAK_TFLOPS, 4),
+                                             "roofline": prefill_roofline(gi_attn, r, 30, torch)},
                                "hbm_copy_measured_GBs": round(hbm_copy_gbs(torch, dev), 1)}
     print(json.dumps(result), flush=True)
 

@@ -17,6 +17,8 @@
 #include <cstring>
 #include <mutex>
 #include <string>
+#include <utility>
+#include <vector>
 
 namespace {
 
@@ -142,12 +144,38 @@ int load_module(const char* path, Module** out) {
     return 0;
 }
 
-int launch(hipFunction_t f, dim3 grid, dim3 block, hipStream_t stream, void* args, size_t args_size) {
+// ---- per-kernel timing (gi_kernel_timing): event pairs around each launch, per kernel kind
+enum Kind { kDecodePartial = 0, kDecodeCombine = 1, kPrefill = 2, kKinds = 3 };
+const char* const kKindNames[kKinds] = {"decode_partial", "decode_combine", "prefill"};
+struct Timing {
+    std::mutex mu;
+    bool on = false;
+    std::vector<std::pair<hipEvent_t, hipEvent_t>> ev[kKinds];
+};
+Timing g_timing;
+
+int launch(Kind kind, hipFunction_t f, dim3 grid, dim3 block, hipStream_t stream, void* args, size_t args_size) {
     void* config[] = {HIP_LAUNCH_PARAM_BUFFER_POINTER, args, HIP_LAUNCH_PARAM_BUFFER_SIZE, &args_size,
                       HIP_LAUNCH_PARAM_END};
-    return check(hipModuleLaunchKernel(f, grid.x, grid.y, grid.z, block.x, block.y, block.z, 0, stream, nullptr,
-                                       config),
-                 "kernel launch");
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    if (g_timing.on) {
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        if (hipStreamIsCapturing(stream, &cs) == hipSuccess && cs == hipStreamCaptureStatusNone) {
+            // timing-only events: no system-scope fence (cache writeback/invalidate) around the kernel
+            if (int e = check(hipEventCreateWithFlags(&e0, hipEventDisableSystemFence), "hipEventCreate")) return e;
+            if (int e = check(hipEventCreateWithFlags(&e1, hipEventDisableSystemFence), "hipEventCreate")) return e;
+            if (int e = check(hipEventRecord(e0, stream), "hipEventRecord")) return e;
+        }
+    }
+    int r = check(hipModuleLaunchKernel(f, grid.x, grid.y, grid.z, block.x, block.y, block.z, 0, stream, nullptr,
+                                        config),
+                  "kernel launch");
+    if (e0) {
+        if (int e = check(hipEventRecord(e1, stream), "hipEventRecord")) return e;
+        std::lock_guard<std::mutex> lock(g_timing.mu);
+        g_timing.ev[kind].emplace_back(e0, e1);
+    }
+    return r;
 }
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
@@ -272,10 +300,10 @@ int gi_attn_decode(void* stream, const float* q, long long q_stride, const uint1
     a.n_kv = n_kv;
     a.qscale = scale * kLog2e;
     hipStream_t st = (hipStream_t)stream;
-    if (int e = launch(ncb == 2 ? m->dec2 : m->dec1, dim3(a.nsplit, n_kv, groups), dim3(256), st, &a, sizeof a))
+    if (int e = launch(kDecodePartial, ncb == 2 ? m->dec2 : m->dec1, dim3(a.nsplit, n_kv, groups), dim3(256), st, &a, sizeof a))
         return e;
     if (a.nsplit > 1)
-        if (int e = launch(m->combine, dim3(n_heads, n_tok, 1), dim3(256), st, &a, sizeof a)) return e;
+        if (int e = launch(kDecodeCombine, m->combine, dim3(n_heads, n_tok, 1), dim3(256), st, &a, sizeof a)) return e;
     return 0;
 }
 
@@ -313,7 +341,7 @@ int gi_attn_prefill(void* stream, const void* q, int q_dtype, long long q_stride
     a.q_f16 = q_dtype == GI_F16;
     a.out_f16 = out_dtype == GI_F16;
     int qtiles = (n + kPrefillBQ - 1) / kPrefillBQ;
-    return launch(m->prefill, dim3(qtiles * n_heads, 1, 1), dim3(m->prefill_threads), (hipStream_t)stream, &a, sizeof a);
+    return launch(kPrefill, m->prefill, dim3(qtiles * n_heads, 1, 1), dim3(m->prefill_threads), (hipStream_t)stream, &a, sizeof a);
 }
 
 int gi_attention(void* stream, const float* qkv, const uint16_t* kc, const uint16_t* vc, float* out,
@@ -337,6 +365,39 @@ int gi_attention(void* stream, const float* qkv, const uint16_t* kc, const uint1
             return e;
     }
     return 0;
+}
+
+
+int gi_kernel_timing(int on) {
+    std::lock_guard<std::mutex> lock(g_timing.mu);
+    g_timing.on = on != 0;
+    return 0;
+}
+
+int gi_kernel_timing_read(const char* kernel, double* total_ms, int* launches) {
+    if (!kernel || !total_ms || !launches) return fail("gi_kernel_timing_read: null argument");
+    int kind = -1;
+    for (int k = 0; k < kKinds; k++)
+        if (std::strcmp(kernel, kKindNames[k]) == 0) kind = k;
+    if (kind < 0) return fail("unknown kernel \"%s\" (decode_partial, decode_combine or prefill)", kernel);
+    std::vector<std::pair<hipEvent_t, hipEvent_t>> ev;
+    {
+        std::lock_guard<std::mutex> lock(g_timing.mu);
+        ev.swap(g_timing.ev[kind]);
+    }
+    double sum = 0.0;
+    int err = 0;
+    for (auto& p : ev) {
+        float ms = 0.f;
+        if (!err) err = check(hipEventSynchronize(p.second), "hipEventSynchronize");
+        if (!err) err = check(hipEventElapsedTime(&ms, p.first, p.second), "hipEventElapsedTime");
+        sum += ms;
+        (void)hipEventDestroy(p.first);
+        (void)hipEventDestroy(p.second);
+    }
+    *total_ms = sum;
+    *launches = (int)ev.size();
+    return err;
 }
 
 } // extern "C"

@@ -22,8 +22,9 @@
 // its slice's (unnormalised O, max, sum) or, with one slice, the normalised output. gi_decode_combine
 // merges the slices.
 //
-// Prefill (reference semantics: attn_prefill_tc<128>, src/cuda.rs:2408-2617, without its rounding of
-// Q*scale*log2(e) to f16: the scale is applied to the f32 scores). Defined further below.
+// Prefill (reference semantics: attn_prefill_tc<128>, src/cuda.rs:2408-2617: Q*scale*log2(e) rounded to
+// f16, base-2 online softmax, P rounded to f16, the row sum taken over the rounded P). Defined further
+// below.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 

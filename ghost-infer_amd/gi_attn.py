@@ -34,6 +34,8 @@ SYMBOLS = (
     "gi_attn_decode",
     "gi_attn_prefill",
     "gi_attention",
+    "gi_kernel_timing",
+    "gi_kernel_timing_read",
 )
 
 
@@ -67,6 +69,10 @@ def load_library(path=LIB_PATH):
     lib.gi_attn_prefill.restype = i
     lib.gi_attention.argtypes = [vp, vp, vp, vp, vp, vp, sz, i, vp, i, i, i, i, i, i]
     lib.gi_attention.restype = i
+    lib.gi_kernel_timing.argtypes = [i]
+    lib.gi_kernel_timing.restype = i
+    lib.gi_kernel_timing_read.argtypes = [ctypes.c_char_p, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(i)]
+    lib.gi_kernel_timing_read.restype = i
     _lib = lib
     return lib
 
@@ -229,3 +235,17 @@ def attention(qkv, k_cache, v_cache, pos0, n_heads, n_kv, hd=128, exact=False, o
     _check(lib.gi_attention(_stream(), _ptr(qkv), _ptr(k_cache), _ptr(v_cache), _ptr(out), ws_ptr, ws_bytes, pos0,
                             _ptr(posp), ctx_cap, n, n_heads, n_kv, hd, 1 if exact else 0))
     return out
+
+
+def kernel_timing(on):
+    """Switches per-kernel event timing on or off (benchmarks only; launches under graph capture are
+    not timed)."""
+    _check(load_library().gi_kernel_timing(1 if on else 0))
+
+
+def kernel_timing_read(kernel):
+    """(total milliseconds, launches) of kernel kind "decode_partial", "decode_combine" or "prefill"
+    since the previous read of that kind."""
+    ms, n = ctypes.c_double(), ctypes.c_int()
+    _check(load_library().gi_kernel_timing_read(kernel.encode(), ctypes.byref(ms), ctypes.byref(n)))
+    return ms.value, n.value

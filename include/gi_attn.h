@@ -89,6 +89,16 @@ int gi_attention(void* stream, const float* qkv, const uint16_t* kc, const uint1
                  void* workspace, size_t workspace_bytes, int pos0, const int* posp, int ctx_cap, int n, int n_heads,
                  int n_kv, int hd, int exact);
 
+/* Per-kernel GPU time, for benchmarks. No counterpart in the reference. While on (process-wide), every
+ * kernel the library launches outside graph capture is bracketed by a pair of HIP events on its stream.
+ * Not for production use: each launch creates two events. */
+int gi_kernel_timing(int on);
+
+/* Total milliseconds and launch count of kernel kind `kernel` ("decode_partial", "decode_combine" or
+ * "prefill") recorded since the previous read of that kind; waits for the recorded events and
+ * releases them. */
+int gi_kernel_timing_read(const char* kernel, double* total_ms, int* launches);
+
 #ifdef __cplusplus
 }
 #endif

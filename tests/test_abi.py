@@ -78,3 +78,17 @@ def test_python_mirror_raises_without_gpu_tensors():
     with pytest.raises(gi_attn.GiAttnError):
         gi_attn.decode(torch.zeros(1, 4096), torch.zeros(8, 512, dtype=torch.float16),
                        torch.zeros(8, 512, dtype=torch.float16), 7, 32, 4)
+
+
+def test_kernel_timing_reads_and_rejects_unknown_kinds():
+    lib = gi_attn.load_library()
+    ms, n = ctypes.c_double(-1), ctypes.c_int(-1)
+    rc = lib.gi_kernel_timing_read(b"gemm", ctypes.byref(ms), ctypes.byref(n))
+    assert rc == -1 and "unknown kernel" in lib.gi_last_error().decode()
+    assert lib.gi_kernel_timing_read(None, ctypes.byref(ms), ctypes.byref(n)) == -1
+    # nothing launched: every kind reads as zero launches, without touching a GPU
+    assert lib.gi_kernel_timing(1) == 0
+    for kind in (b"decode_partial", b"decode_combine", b"prefill"):
+        assert lib.gi_kernel_timing_read(kind, ctypes.byref(ms), ctypes.byref(n)) == 0
+        assert (ms.value, n.value) == (0.0, 0)
+    assert lib.gi_kernel_timing(0) == 0
