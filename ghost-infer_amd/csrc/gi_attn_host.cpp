@@ -95,13 +95,17 @@ int check(hipError_t r, const char* what) {
 struct Module {
     bool loaded = false;
     hipModule_t mod = nullptr;
-    hipFunction_t dec1 = nullptr, dec2 = nullptr, combine = nullptr, prefill = nullptr;
+    hipFunction_t dec[2][2] = {}; // [shared][column blocks - 1]
+    hipFunction_t combine = nullptr, prefill = nullptr;
     int prefill_threads = 0; // the prefill kernel's block size (its launch bound: waves x 64)
 };
 std::mutex g_mu;
 Module g_mods[kMaxDevices];
 
+// The code object: $GI_CODE_OBJECT when set, else gi_attn_gfx950.hsaco beside this library.
 std::string default_code_object() {
+    if (const char* env = getenv("GI_CODE_OBJECT"))
+        if (*env) return env;
     Dl_info info;
     if (dladdr((void*)&default_code_object, &info) && info.dli_fname) {
         std::string p = info.dli_fname;
@@ -121,8 +125,10 @@ int load_module(const char* path, Module** out) {
         std::string p = path ? std::string(path) : default_code_object();
         if (int e = check(hipModuleLoad(&m.mod, p.c_str()), ("hipModuleLoad(" + p + ")").c_str())) return e;
         struct { hipFunction_t* f; const char* name; } fns[] = {
-            {&m.dec1, "gi_decode_partial_1"},
-            {&m.dec2, "gi_decode_partial_2"},
+            {&m.dec[0][0], "gi_decode_partial_1"},
+            {&m.dec[0][1], "gi_decode_partial_2"},
+            {&m.dec[1][0], "gi_decode_shared_1"},
+            {&m.dec[1][1], "gi_decode_shared_2"},
             {&m.combine, "gi_decode_combine"},
             {&m.prefill, "gi_prefill_fwd"},
         };
@@ -180,22 +186,38 @@ int launch(Kind kind, hipFunction_t f, dim3 grid, dim3 block, hipStream_t stream
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
-// Workgroups to aim for per decode launch: about two per CU of the 256 on MI355X.
+// Workgroups to aim for per decode launch: one per CU of the 256 on MI355X. A decode workgroup holds a
+// whole CU's registers, so more workgroups run in sequential rounds, each paying the ramp-up and drain of
+// the memory pipeline.
 int decode_target_wgs() {
     static int target = [] {
         const char* e = getenv("GI_DECODE_TARGET_WGS");
         int v = e ? atoi(e) : 0;
-        return v > 0 ? v : 512;
+        return v > 0 ? v : 256;
     }();
     return target;
 }
 
-int ncb_for(int n_tok, int G) { return n_tok * G > kDecPairs ? 2 : 1; }
+// Decode kernel variant for n_tok tokens of G heads per kv head: column blocks of 8 (token, head) pairs per
+// wave (1 or 2) and whether the 4 waves share the slice (each serving its own pairs) or split it.
+struct DecVariant {
+    int ncb;
+    bool shared;
+    int groups; // workgroups per (slice, kv head)
+};
+DecVariant dec_variant(int n_tok, int G) {
+    const int pairs = n_tok * G;
+    DecVariant v;
+    v.ncb = (pairs > kDecPairs && pairs <= 2 * kDecPairs) || pairs > 4 * kDecPairs ? 2 : 1;
+    v.shared = pairs > 2 * kDecPairs;
+    const int per_wg = (v.shared ? 4 : 1) * kDecPairs * v.ncb;
+    v.groups = (pairs + per_wg - 1) / per_wg;
+    return v;
+}
 
 void plan(int max_span, int n_tok, int n_heads, int n_kv, int* chunk, int* nsplit) {
     int G = n_heads / n_kv;
-    int ncb = ncb_for(n_tok, G);
-    int groups = (n_tok * G + kDecPairs * ncb - 1) / (kDecPairs * ncb);
+    int groups = dec_variant(n_tok, G).groups;
     int units = (max_span + kSliceUnit - 1) / kSliceUnit; // 128-key units
     int per_slot = std::max(1, decode_target_wgs() / std::max(1, n_kv * groups));
     int per = std::max(1, (units + per_slot - 1) / per_slot);
@@ -249,8 +271,7 @@ size_t gi_attn_decode_workspace_bytes(int ctx_cap, int n_tok, int n_heads, int n
     size_t best = 16;
     int G = n_heads / n_kv;
     for (int t = 1; t <= n_tok; t++) {
-        int ncb = ncb_for(t, G);
-        int groups = (t * G + kDecPairs * ncb - 1) / (kDecPairs * ncb);
+        int groups = dec_variant(t, G).groups;
         int per_slot = std::max(1, decode_target_wgs() / std::max(1, n_kv * groups));
         int most = std::max(1, std::min(per_slot, (ctx_cap + kSliceUnit - 1) / kSliceUnit));
         best = std::max(best, (size_t)t * n_heads * most * kDecPart * sizeof(float));
@@ -276,14 +297,13 @@ int gi_attn_decode(void* stream, const float* q, long long q_stride, const uint1
     if (posp && ctx_cap < n_tok) return fail("ctx_cap %d must cover the %d tokens", ctx_cap, n_tok);
     Module* m;
     if (int e = load_module(nullptr, &m)) return e;
-    int G = n_heads / n_kv;
-    int ncb = ncb_for(n_tok, G);
-    int groups = (n_tok * G + kDecPairs * ncb - 1) / (kDecPairs * ncb);
+    const DecVariant var = dec_variant(n_tok, n_heads / n_kv);
     GiDecodeArgs a{};
     plan(max_span, n_tok, n_heads, n_kv, &a.chunk, &a.nsplit);
     size_t need = a.nsplit == 1 ? 0 : (size_t)n_tok * n_heads * a.nsplit * kDecPart * sizeof(float);
     if (need && (!workspace || workspace_bytes < need))
         return fail("workspace of %zu bytes too small: %zu needed", workspace_bytes, need);
+    if (need && !aligned16(workspace)) return fail("the workspace must be 16-byte aligned");
     a.q = q;
     a.kc = kc;
     a.vc = vc;
@@ -300,7 +320,8 @@ int gi_attn_decode(void* stream, const float* q, long long q_stride, const uint1
     a.n_kv = n_kv;
     a.qscale = scale * kLog2e;
     hipStream_t st = (hipStream_t)stream;
-    if (int e = launch(kDecodePartial, ncb == 2 ? m->dec2 : m->dec1, dim3(a.nsplit, n_kv, groups), dim3(256), st, &a, sizeof a))
+    if (int e = launch(kDecodePartial, m->dec[var.shared][var.ncb - 1], dim3(a.nsplit, n_kv, var.groups), dim3(256), st,
+                       &a, sizeof a))
         return e;
     if (a.nsplit > 1)
         if (int e = launch(kDecodeCombine, m->combine, dim3(n_heads, n_tok, 1), dim3(256), st, &a, sizeof a)) return e;

@@ -62,6 +62,12 @@ struct GiDecodeArgs {
 };
 
 #define DEC_WAVES 4
+#ifndef DEC_NB
+#define DEC_NB 2 // register buffers of K/V tiles per wave (tiles in flight)
+#endif
+#ifndef DEC_MINWG
+#define DEC_MINWG 1 // workgroups per CU the register budget is sized for
+#endif
 #define DEC_TILE 32
 #define DEC_PAIRS 8 // (token, head) pairs per column block of 16 columns
 #define DEC_RESCALE_LOG2 8.0f
@@ -98,7 +104,12 @@ __device__ __forceinline__ u4 gi_load16(__amdgpu_buffer_rsrc_t r, int off) {
 }
 
 // Lane l of a wave: c = l % 16 (MFMA column / A-row), grp = l / 16 (k-group of 8).
-template <int NCB>
+// SHARE = false: the 4 waves split the slice's tiles and serve the same DEC_PAIRS*NCB (token, head)
+// pairs, merging through LDS at the end. SHARE = true (many pairs per kv head, as in a verify block):
+// every wave walks the whole slice for its own DEC_PAIRS*NCB pairs, so one workgroup serves 4 times as
+// many pairs and the slice's K/V comes from HBM once (the waves' repeated loads of the same lines are
+// served by the caches).
+template <int NCB, bool SHARE>
 __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -114,7 +125,8 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
     const int pos0 = a.posp ? *a.posp : a.pos0;
     const int G = a.n_heads / a.n_kv;
     const int npairs = a.n_tok * G;
-    const int pair0 = blockIdx.z * (DEC_PAIRS * NCB);
+    constexpr int WG_PAIRS = (SHARE ? DEC_WAVES : 1) * DEC_PAIRS * NCB; // pairs per workgroup
+    const int pair0 = blockIdx.z * WG_PAIRS + (SHARE ? wave * DEC_PAIRS * NCB : 0); // this wave's first pair
     const int kv_len = pos0 + a.n_tok; // keys any token of the launch may see
     const int k_begin = s * a.chunk;
     const int nkeys = min(a.chunk, kv_len - k_begin); // keys of this slice (<= 0: an empty slice)
@@ -172,7 +184,7 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
     const int koff1 = koff0 + 4 * (int)kvs * 2;
     const int voff = (8 * grp * (int)kvs + 8 * c) * 2;
     const int vstep = (int)kvs * 2;
-    constexpr int STRIDE = DEC_WAVES * DEC_TILE; // keys between a wave's consecutive tiles
+    constexpr int STRIDE = SHARE ? DEC_TILE : DEC_WAVES * DEC_TILE; // keys between a wave's consecutive tiles
 
     struct Buf { u4 k[2][4]; u4 v[8]; };
     auto load_k = [&](Buf& B, int t) {
@@ -188,7 +200,7 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
 #pragma unroll
         for (int i = 0; i < 8; i++) B.v[i] = gi_load16(r, voff + i * vstep);
     };
-    // One tile from buffer B at key offset t; with `reload`, B is refilled with the tile at t + 2*STRIDE.
+    // One tile from buffer B at key offset t; with `reload`, B is refilled with the tile DEC_NB tiles on.
     auto process = [&](Buf& B, int t, bool reload) {
         __builtin_amdgcn_sched_barrier(0); // keep tiles in order: each waits only for its own buffer
         f4 sacc[NCB][2];
@@ -202,7 +214,7 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
                     sacc[cb][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, B.k[b][kk]), qf[cb][kk],
                                                                          sacc[cb][b], 0, 0, 0);
             }
-        if (reload) load_k(B, t + 2 * STRIDE);
+        if (reload) load_k(B, t + DEC_NB * STRIDE);
         __builtin_amdgcn_sched_barrier(0);
         const bool masked = t + DEC_TILE > span_lo; // some valid column sees only part of this tile
         h8 pf[NCB];
@@ -261,21 +273,25 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
                 o[cb][dd] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vt, pf[cb], o[cb][dd], 0, 0, 0);
         }
         __builtin_amdgcn_sched_barrier(0);
-        if (reload) load_v(B, t + 2 * STRIDE);
+        if (reload) load_v(B, t + DEC_NB * STRIDE);
     };
 
     // (the first loads are issued unconditionally, before the loop, so every iteration starts with the same
     // loads outstanding and the compiler's load counters wait for exactly the buffer in use)
+    // a SHARE wave whose pairs all lie past the last one has nothing to compute (it still joins the merge)
+    if (!SHARE || pair0 < npairs) {
     Buf X, Y;
-    const int t_first = wave * DEC_TILE;
+    const int t_first = SHARE ? 0 : wave * DEC_TILE;
     load_k(X, t_first);
     __builtin_amdgcn_sched_barrier(0);
     load_v(X, t_first);
     __builtin_amdgcn_sched_barrier(0);
+#if DEC_NB == 2
     load_k(Y, t_first + STRIDE);
     __builtin_amdgcn_sched_barrier(0);
     load_v(Y, t_first + STRIDE);
     __builtin_amdgcn_sched_barrier(0);
+#endif
     // Q * scale * log2(e) in f32, split into an f16 high part (even columns) and its f16 remainder (odd)
 #pragma unroll
     for (int cb = 0; cb < NCB; cb++)
@@ -294,6 +310,7 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
     // Steady state: both buffers get a further tile (Y's may lie past the slice: zeros, never processed).
     // The last one or two tiles run without reloads, so no load is left in flight at the end.
     int t = t_first;
+#if DEC_NB == 2
     for (; t + 2 * STRIDE < nkeys; t += 2 * STRIDE) {
         process(X, t, true);
 #ifdef GI_DEC_TIMESTAMPS
@@ -303,6 +320,11 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
     }
     if (t < nkeys) process(X, t, false);
     if (t + STRIDE < nkeys) process(Y, t + STRIDE, false);
+#else
+    for (; t + STRIDE < nkeys; t += STRIDE) process(X, t, true);
+    if (t < nkeys) process(X, t, false);
+#endif
+    }
     GI_TS(4);
 
     // ---- wave results to LDS: every lane's 32 O^T values (its column, dims 32grp + 8j + dd) as 8 16-byte
@@ -326,26 +348,27 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
     GI_TS(6);
     __syncthreads();
     GI_TS(7);
-    // ---- merge the waves and the hi/lo columns: thread -> (pair, 4 dims)
+    // ---- merge the waves (SHARE: each pair has one wave) and the hi/lo columns: thread -> (pair, 4 dims)
 #pragma unroll
-    for (int it = 0; it < NCB; it++) {
+    for (int it = 0; it < WG_PAIRS / DEC_PAIRS; it++) {
         const int item = threadIdx.x + 256 * it;
-        const int pl = item >> 5, d4 = 4 * (item & 31);
-        const int pi = pair0 + pl;
+        const int pl = item >> 5, d4 = 4 * (item & 31);      // pair within the workgroup
+        const int pi = blockIdx.z * WG_PAIRS + pl;
+        const int w0 = SHARE ? pl / (DEC_PAIRS * NCB) : 0;   // the waves holding the pair
+        const int w1 = SHARE ? w0 + 1 : DEC_WAVES;
+        const int lp = SHARE ? pl % (DEC_PAIRS * NCB) : pl;  // the pair within those waves
         if (pi < npairs) {
-            const int row = 16 * (pl >> 3) + 2 * (pl & 7);
+            const int row = 16 * (lp >> 3) + 2 * (lp & 7);
             float M = GI_NEG_INF;
-#pragma unroll
-            for (int w = 0; w < DEC_WAVES; w++) M = fmaxf(M, sm_m[w][pl]);
+            for (int w = w0; w < w1; w++) M = fmaxf(M, sm_m[w][lp]);
             float L = 0.f;
             float4 O = make_float4(0.f, 0.f, 0.f, 0.f);
             if (M != GI_NEG_INF) {
-#pragma unroll
-                for (int w = 0; w < DEC_WAVES; w++) {
-                    const float wt = __builtin_amdgcn_exp2f(sm_m[w][pl] - M);
+                for (int w = w0; w < w1; w++) {
+                    const float wt = __builtin_amdgcn_exp2f(sm_m[w][lp] - M);
                     const float4 hi = *reinterpret_cast<const float4*>(&sm_o[w][row][d4]);
                     const float4 lo = *reinterpret_cast<const float4*>(&sm_o[w][row + 1][d4]);
-                    L += wt * sm_l[w][pl];
+                    L += wt * sm_l[w][lp];
                     O.x += wt * (hi.x + lo.x);
                     O.y += wt * (hi.y + lo.y);
                     O.z += wt * (hi.z + lo.z);
@@ -379,8 +402,10 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
 #endif
 }
 
-extern "C" __global__ void __launch_bounds__(256) gi_decode_partial_1(GiDecodeArgs a) { gi_decode_partial_t<1>(a); }
-extern "C" __global__ void __launch_bounds__(256) gi_decode_partial_2(GiDecodeArgs a) { gi_decode_partial_t<2>(a); }
+extern "C" __global__ void __launch_bounds__(256, DEC_MINWG) gi_decode_partial_1(GiDecodeArgs a) { gi_decode_partial_t<1, false>(a); }
+extern "C" __global__ void __launch_bounds__(256, DEC_MINWG) gi_decode_partial_2(GiDecodeArgs a) { gi_decode_partial_t<2, false>(a); }
+extern "C" __global__ void __launch_bounds__(256, DEC_MINWG) gi_decode_shared_1(GiDecodeArgs a) { gi_decode_partial_t<1, true>(a); }
+extern "C" __global__ void __launch_bounds__(256, DEC_MINWG) gi_decode_shared_2(GiDecodeArgs a) { gi_decode_partial_t<2, true>(a); }
 
 // Merge the slices of each (token, head): M = max m_s, w_s = 2^(m_s - M), out = sum w_s O_s / sum w_s l_s
 // (attention_combine's maths in base 2; empty slices carry m = -inf and weigh nothing). One workgroup of

@@ -141,6 +141,7 @@ def workspace_bytes(ctx_cap, n_tok, n_heads, n_kv, hd=128):
 
 
 def new_workspace(ctx_cap, n_tok, n_heads, n_kv, hd=128, device="cuda"):
+    """A decode workspace (uninitialised: every call writes the partials it reads)."""
     nbytes = workspace_bytes(ctx_cap, n_tok, n_heads, n_kv, hd)
     return torch.empty((nbytes + 3) // 4, dtype=torch.float32, device=device)
 

@@ -40,8 +40,8 @@ extern "C" {
 #define GI_F32 0
 #define GI_F16 1
 
-/* Load the code object (path to gi_attn_gfx950.hsaco; NULL = the file beside this library) on the
- * current device. Optional: every entry point loads it on first use per device.
+/* Load the code object (path to gi_attn_gfx950.hsaco; NULL = $GI_CODE_OBJECT if set, else the file
+ * beside this library) on the current device. Optional: every entry point loads it on first use per device.
  * Replaces: Kernels::binary + compile_on (src/cuda.rs:5485-5655), which NVRTC-compile KERNELS and
  * resolve the functions by name. */
 int gi_init(const char* code_object_path);
@@ -52,12 +52,12 @@ const char* gi_last_error(void);
 
 /* Slice plan of a decode call: keys per slice (`chunk`) and slices per token (`nsplit`) for tokens whose
  * largest span is max_span. Counterpart of att_want / att_chunk / max_splits (src/cuda.rs:8426-8444),
- * re-chosen for 256 CUs: slices are multiples of 128 keys and about 2 workgroups per CU in total. */
+ * re-chosen for 256 CUs: slices are multiples of 128 keys and about one workgroup per CU in total. */
 int gi_attn_decode_plan(int max_span, int n_tok, int n_heads, int n_kv, int hd, int* chunk, int* nsplit);
 
-/* Bytes of workspace gi_attn_decode needs for n_tok tokens whose spans reach at most ctx_cap keys
- * (the slice partials, [token][head][slice][hd + 4] f32: O, max, sum, 2 pad). The counterpart of the session's att_part
- * buffer (GpuSession, src/cuda.rs:9826-9870). */
+/* Bytes of workspace gi_attn_decode needs for n_tok tokens whose spans reach at most ctx_cap keys (the
+ * slice partials, [token][head][slice][hd + 4] f32: O, max, sum, 2 pad; 16-byte aligned). The
+ * counterpart of the session's att_part buffer (GpuSession, src/cuda.rs:9826-9870). */
 size_t gi_attn_decode_workspace_bytes(int ctx_cap, int n_tok, int n_heads, int n_kv, int hd);
 
 /* Decode / verify attention for n_tok tokens (one generated token, or a speculative verify block that

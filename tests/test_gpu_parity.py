@@ -109,6 +109,46 @@ def test_decode_device_position_one_launch_shape(gpu):
                      what=f"posp {pos}")
 
 
+def test_decode_workspace_reuse_across_shapes(gpu):
+    # one workspace through calls of different shapes and kernel variants (few pairs per kv head, a
+    # verify block whose workgroups share each slice): every output is right whatever the earlier calls
+    # left in the workspace
+    n_heads, n_kv, cap = 32, 4, 6000
+    ws = gi_attn.new_workspace(cap, 15, n_heads, n_kv, device=gpu)
+    for i, (n_tok, pos0) in enumerate(((1, 5999), (8, 3000), (2, 4000), (15, 100), (1, 200), (1, 5999))):
+        say("decode workspace reuse", n_tok, pos0)
+        q, k, v = make_inputs(300 + i, n_tok, pos0 + n_tok, n_heads, n_kv)
+        qt, kt, vt = to_dev(q, k, v, gpu)
+        out = gi_attn.decode(qt, kt, vt, pos0, n_heads, n_kv, workspace=ws)
+        torch.cuda.synchronize()
+        assert_close(out.cpu().numpy(), reference_f64(q, k, v, pos0, n_heads, n_kv), max_abs=2e-5, rel_l2=2e-5,
+                     what=f"reuse {n_tok}@{pos0}")
+
+
+def test_decode_graph_replay(gpu):
+    # a decode step with a device position captured once and replayed at several positions, with eager work
+    # between the replays; each replay matches the float64 reference
+    n_heads, n_kv, cap = 32, 8, 5000
+    q, k, v = make_inputs(91, 1, cap, n_heads, n_kv)
+    qt, kt, vt = to_dev(q, k, v, gpu)
+    ws = gi_attn.new_workspace(cap, 1, n_heads, n_kv, device=gpu)
+    posp = torch.zeros(1, dtype=torch.int32, device=gpu)
+    out = torch.zeros((1, n_heads * 128), dtype=torch.float32, device=gpu)
+    gi_attn.decode(qt, kt, vt, 0, n_heads, n_kv, out=out, workspace=ws, posp=posp, ctx_cap=cap)  # warm-up
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        gi_attn.decode(qt, kt, vt, 0, n_heads, n_kv, out=out, workspace=ws, posp=posp, ctx_cap=cap)
+    for pos in (4999, 17, 2500, 4999, 0):
+        say("decode graph replay", pos)
+        posp.fill_(pos)
+        out.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert_close(out.cpu().numpy(), reference_f64(q, k, v, pos, n_heads, n_kv), max_abs=2e-5, rel_l2=2e-5,
+                     what=f"replay at {pos}")
+
+
 def test_decode_is_deterministic(gpu):
     q, k, v = make_inputs(5, 1, 20000, 32, 4)
     a = run_decode(q, k, v, 19999, 32, 4, gpu)
