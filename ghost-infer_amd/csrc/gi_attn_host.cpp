@@ -66,6 +66,10 @@ struct GiPrefillArgs {
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kMaxDevices = 64;
+#ifndef CMB_DSPLIT
+#define CMB_DSPLIT 8
+#endif
+constexpr int kCombineSplit = CMB_DSPLIT; // combine workgroups per (head, token); must match the kernels'
 constexpr int kDecWaves = 4, kDecTile = 32, kDecPairs = 8, kDecPart = 132; // kDecPart: floats per slice partial
 constexpr int kSliceUnit = kDecWaves * kDecTile; // 128 keys
 constexpr int kPrefillBQ = 256;                   // query rows per prefill workgroup
@@ -324,7 +328,7 @@ int gi_attn_decode(void* stream, const float* q, long long q_stride, const uint1
                        &a, sizeof a))
         return e;
     if (a.nsplit > 1)
-        if (int e = launch(kDecodeCombine, m->combine, dim3(n_heads, n_tok, 1), dim3(256), st, &a, sizeof a)) return e;
+        if (int e = launch(kDecodeCombine, m->combine, dim3(n_heads, n_tok, kCombineSplit), dim3(64), st, &a, sizeof a)) return e;
     return 0;
 }
 

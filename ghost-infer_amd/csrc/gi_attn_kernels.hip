@@ -172,9 +172,10 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
     }
 
     // Loads go through buffer resources that start at the wave's current tile and end at the slice's last
-    // key: offsets are 32-bit per lane, constant across tiles, and keys past the end read as zeros. Two
-    // register buffers (X, Y) keep two tiles in flight per wave: a buffer is refilled with the tile two
-    // ahead as soon as its data is consumed (K after the QK MFMAs, V after its transpose).
+    // key: offsets are 32-bit per lane, constant across tiles, and keys past the end read as zeros. DEC_NB
+    // register buffers keep DEC_NB tiles in flight per wave: a buffer is refilled with the tile DEC_NB
+    // ahead as soon as its data is consumed (K after the QK MFMAs, V after its transpose). Two measured
+    // fastest; three or four only add register pressure.
     const long long kvs = a.kv_stride;
     const uint16_t* kslice = a.kc + (long long)k_begin * kvs + kvh * a.kv_head_stride;
     const uint16_t* vslice = a.vc + (long long)k_begin * kvs + kvh * a.kv_head_stride;
@@ -280,18 +281,15 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
     // loads outstanding and the compiler's load counters wait for exactly the buffer in use)
     // a SHARE wave whose pairs all lie past the last one has nothing to compute (it still joins the merge)
     if (!SHARE || pair0 < npairs) {
-    Buf X, Y;
+    Buf B[DEC_NB];
     const int t_first = SHARE ? 0 : wave * DEC_TILE;
-    load_k(X, t_first);
-    __builtin_amdgcn_sched_barrier(0);
-    load_v(X, t_first);
-    __builtin_amdgcn_sched_barrier(0);
-#if DEC_NB == 2
-    load_k(Y, t_first + STRIDE);
-    __builtin_amdgcn_sched_barrier(0);
-    load_v(Y, t_first + STRIDE);
-    __builtin_amdgcn_sched_barrier(0);
-#endif
+#pragma unroll
+    for (int i = 0; i < DEC_NB; i++) {
+        load_k(B[i], t_first + i * STRIDE);
+        __builtin_amdgcn_sched_barrier(0);
+        load_v(B[i], t_first + i * STRIDE);
+        __builtin_amdgcn_sched_barrier(0);
+    }
     // Q * scale * log2(e) in f32, split into an f16 high part (even columns) and its f16 remainder (odd)
 #pragma unroll
     for (int cb = 0; cb < NCB; cb++)
@@ -307,23 +305,16 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
                 qf[cb][kk][e] = (c & 1) ? (_Float16)(v - (float)hi) : hi;
             }
     GI_TS(2);
-    // Steady state: both buffers get a further tile (Y's may lie past the slice: zeros, never processed).
-    // The last one or two tiles run without reloads, so no load is left in flight at the end.
+    // Steady state: every buffer gets a further tile (those past the slice read zeros and are never
+    // processed). The last round of tiles runs without reloads, so no load is left in flight at the end.
     int t = t_first;
-#if DEC_NB == 2
-    for (; t + 2 * STRIDE < nkeys; t += 2 * STRIDE) {
-        process(X, t, true);
-#ifdef GI_DEC_TIMESTAMPS
-        if (t == t_first) ts[3] = wall_clock64();
-#endif
-        process(Y, t + STRIDE, true);
+    for (; t + DEC_NB * STRIDE < nkeys; t += DEC_NB * STRIDE) {
+#pragma unroll
+        for (int i = 0; i < DEC_NB; i++) process(B[i], t + i * STRIDE, true);
     }
-    if (t < nkeys) process(X, t, false);
-    if (t + STRIDE < nkeys) process(Y, t + STRIDE, false);
-#else
-    for (; t + STRIDE < nkeys; t += STRIDE) process(X, t, true);
-    if (t < nkeys) process(X, t, false);
-#endif
+#pragma unroll
+    for (int i = 0; i < DEC_NB; i++)
+        if (t + i * STRIDE < nkeys) process(B[i], t + i * STRIDE, false);
     }
     GI_TS(4);
 
@@ -408,26 +399,27 @@ extern "C" __global__ void __launch_bounds__(256, DEC_MINWG) gi_decode_shared_1(
 extern "C" __global__ void __launch_bounds__(256, DEC_MINWG) gi_decode_shared_2(GiDecodeArgs a) { gi_decode_partial_t<2, true>(a); }
 
 // Merge the slices of each (token, head): M = max m_s, w_s = 2^(m_s - M), out = sum w_s O_s / sum w_s l_s
-// (attention_combine's maths in base 2; empty slices carry m = -inf and weigh nothing). One workgroup of
-// 256 threads per (head, token). Thread t takes slices t/4, t/4 + 64, ... and dims 32(t%4)..+31, issuing
-// all of a slice's loads at once and folding its slices with a running max, so up to 64 slices cost one
-// memory round trip; the 64 slice lanes then meet in LDS.
-#define CMB_SLOTS 64
-extern "C" __global__ void __launch_bounds__(256) gi_decode_combine(GiDecodeArgs a) {
-    __shared__ float red_m[4];
-    __shared__ float acc_o[CMB_SLOTS][132];
-    __shared__ float acc_l[CMB_SLOTS];
-    const int h = blockIdx.x, t = blockIdx.y, tid = threadIdx.x;
-    const int slot = tid >> 2, dq = tid & 3;
+// (attention_combine's maths in base 2; empty slices carry m = -inf and weigh nothing). One wave per
+// (head, token, 128/CMB_DSPLIT dims): lane l takes slices l, l + 64, ..., issuing all of a slice's loads
+// at once and folding its slices with a running max, so up to 64 slices cost one memory round trip;
+// shuffles agree on the max and the sum, and LDS sums the lanes' O. Many small workgroups keep the merge
+// short: it runs between two launches, on the critical path of every decode step.
+#ifndef CMB_DSPLIT
+#define CMB_DSPLIT 8 // workgroups per (head, token), each over 128 / CMB_DSPLIT dims
+#endif
+#define CMB_DIMS (128 / CMB_DSPLIT)
+extern "C" __global__ void __launch_bounds__(64) gi_decode_combine(GiDecodeArgs a) {
+    __shared__ float acc_o[64][CMB_DIMS + 1];
+    const int h = blockIdx.x, t = blockIdx.y, d0 = blockIdx.z * CMB_DIMS, lane = threadIdx.x;
     const float* p = a.part + ((long long)t * a.n_heads + h) * a.nsplit * DEC_PART;
-    float m = GI_NEG_INF, L = 0.f, o[32];
+    float m = GI_NEG_INF, L = 0.f, o[CMB_DIMS];
 #pragma unroll
-    for (int i = 0; i < 32; i++) o[i] = 0.f;
-    for (int s = slot; s < a.nsplit; s += CMB_SLOTS) {
+    for (int i = 0; i < CMB_DIMS; i++) o[i] = 0.f;
+    for (int s = lane; s < a.nsplit; s += 64) {
         const float* ps = p + s * DEC_PART;
-        float4 v[8];
+        float4 v[CMB_DIMS / 4];
 #pragma unroll
-        for (int i = 0; i < 8; i++) v[i] = *reinterpret_cast<const float4*>(ps + 32 * dq + 4 * i);
+        for (int i = 0; i < CMB_DIMS / 4; i++) v[i] = *reinterpret_cast<const float4*>(ps + d0 + 4 * i);
         const float2 ml = *reinterpret_cast<const float2*>(ps + 128);
         if (ml.x == GI_NEG_INF) continue; // an empty slice
         const float mn = fmaxf(m, ml.x);
@@ -435,34 +427,26 @@ extern "C" __global__ void __launch_bounds__(256) gi_decode_combine(GiDecodeArgs
         m = mn;
         L = L * a_old + ml.y * a_new;
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
+        for (int i = 0; i < CMB_DIMS / 4; i++) {
             o[4 * i] = o[4 * i] * a_old + v[i].x * a_new;
             o[4 * i + 1] = o[4 * i + 1] * a_old + v[i].y * a_new;
             o[4 * i + 2] = o[4 * i + 2] * a_old + v[i].z * a_new;
             o[4 * i + 3] = o[4 * i + 3] * a_old + v[i].w * a_new;
         }
     }
-    // block max of the slot maxima (every slot's thread group holds the same m)
     float M = m;
     for (int x = 32; x > 0; x >>= 1) M = fmaxf(M, __shfl_xor(M, x, 64));
-    if ((tid & 63) == 0) red_m[tid >> 6] = M;
-    __syncthreads();
-    M = fmaxf(fmaxf(red_m[0], red_m[1]), fmaxf(red_m[2], red_m[3]));
     const float w = m == GI_NEG_INF ? 0.f : __builtin_amdgcn_exp2f(m - M);
+    float LL = L * w;
+    for (int x = 32; x > 0; x >>= 1) LL += __shfl_xor(LL, x, 64);
 #pragma unroll
-    for (int i = 0; i < 8; i++)
-        *reinterpret_cast<float4*>(&acc_o[slot][32 * dq + 4 * i]) =
-            make_float4(o[4 * i] * w, o[4 * i + 1] * w, o[4 * i + 2] * w, o[4 * i + 3] * w);
-    if (dq == 0) acc_l[slot] = L * w;
+    for (int i = 0; i < CMB_DIMS; i++) acc_o[lane][i] = o[i] * w;
     __syncthreads();
-    if (tid < 128) {
-        float O = 0.f, LL = 0.f;
+    if (lane < CMB_DIMS) {
+        float O = 0.f;
 #pragma unroll 8
-        for (int k = 0; k < CMB_SLOTS; k++) {
-            O += acc_o[k][tid];
-            LL += acc_l[k];
-        }
-        a.out[(long long)t * a.out_stride + (long long)h * 128 + tid] = O / LL;
+        for (int k = 0; k < 64; k++) O += acc_o[k][lane];
+        a.out[(long long)t * a.out_stride + (long long)h * 128 + d0 + lane] = O / LL;
     }
 }
 
