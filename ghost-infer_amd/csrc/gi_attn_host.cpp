@@ -72,7 +72,6 @@ constexpr int kMaxDevices = 64;
 constexpr int kCombineSplit = CMB_DSPLIT; // combine workgroups per (head, token); must match the kernels'
 constexpr int kDecWaves = 4, kDecTile = 32, kDecPairs = 8, kDecPart = 132; // kDecPart: floats per slice partial
 constexpr int kSliceUnit = kDecWaves * kDecTile; // 128 keys
-constexpr int kPrefillBQ = 256;                   // query rows per prefill workgroup
 constexpr int kSplitMaxBatch = 15;                // tokens per split launch (src/cuda.rs:119)
 constexpr int kTiledMinBatch = 16;                // prefill from this many tokens (src/cuda.rs:95)
 
@@ -365,7 +364,8 @@ int gi_attn_prefill(void* stream, const void* q, int q_dtype, long long q_stride
     a.qscale = scale * kLog2e;
     a.q_f16 = q_dtype == GI_F16;
     a.out_f16 = out_dtype == GI_F16;
-    int qtiles = (n + kPrefillBQ - 1) / kPrefillBQ;
+    const int bq = m->prefill_threads / 2; // query rows per workgroup: 32 per wave of 64 threads
+    int qtiles = (n + bq - 1) / bq;
     return launch(kPrefill, m->prefill, dim3(qtiles * n_heads, 1, 1), dim3(m->prefill_threads), (hipStream_t)stream, &a, sizeof a);
 }
 

@@ -472,12 +472,22 @@ struct GiPrefillArgs {
     int pad_;
 };
 
+#ifndef PF_WAVES
 #define PF_WAVES 8         // waves per workgroup, 32 query rows each
-#define PF_BQ 256          // query rows per workgroup
+#endif
+#define PF_BQ (32 * PF_WAVES) // query rows per workgroup
+#define PF_SW (PF_WAVES / 2)  // waves staging each of K and V
+// s_waitcnt immediate waiting until at most n vector memory operations are outstanding (gfx9 encoding:
+// vmcnt in bits 3:0 and 15:14, expcnt and lgkmcnt left at their maxima)
+#define GI_VMCNT(n) (0x0F70 | ((n) & 15) | (((n) >> 4) << 14))
+#define PF_LPW (16 / PF_SW)   // 1 KB loads per staging wave and tile
 #define PF_NBUF 4          // LDS tile buffers
 #define PF_BK 64           // keys per tile
 #define PF_TILE 16384      // bytes of one K or V tile: 64 rows of 256 bytes
 #define PF_RESCALE_LOG2 8.0f
+#ifndef PF_KPF
+#define PF_KPF 8           // K fragments in flight in the QK loop
+#endif
 #define GI_LDS __attribute__((address_space(3)))
 typedef short gi_s4 __attribute__((__vector_size__(8))); // 4 f16 as ds_read_b64_tr_b16 returns them
 
@@ -506,7 +516,7 @@ typedef short gi_s4 __attribute__((__vector_size__(8))); // 4 f16 as ds_read_b64
 // tiles crossing the diagonal are masked. Work order: the grid is remapped so that each of the 8 XCDs
 // (blockIdx round-robin) walks a contiguous run of (kv head, query tile, head) items, longest query
 // tiles first, so one kv head's K/V stays in one XCD's L2.
-extern "C" __global__ void __launch_bounds__(512, 1) gi_prefill_fwd(GiPrefillArgs a) {
+extern "C" __global__ void __launch_bounds__(64 * PF_WAVES, 1) gi_prefill_fwd(GiPrefillArgs a) {
     __shared__ __attribute__((aligned(1024))) unsigned char smem[PF_NBUF][2][PF_TILE]; // [buffer][K, V]
 
     const int tid = threadIdx.x, lane = tid & 63;
@@ -526,23 +536,24 @@ extern "C" __global__ void __launch_bounds__(512, 1) gi_prefill_fwd(GiPrefillArg
     const int ntiles = (k_lim + PF_BK - 1) / PF_BK;
     const long long kvs = a.kv_stride;
 
-    // ---- staging: waves 0-3 move K rows, waves 4-7 V rows; wave w's load i covers tile rows
-    // 4*(4*(w%4) + i) + lane/16, LDS unit lane%16 holding global unit (lane%16) ^ swizzle(row)
-    const bool stage_v = wave >= 4;
+    // ---- staging: the first half of the waves moves K rows, the second half V rows (PF_SW waves each,
+    // PF_LPW loads of 1 KB per wave and tile); wave w's load i covers tile rows 4*(PF_LPW*(w%PF_SW) + i)
+    // + lane/16, LDS unit lane%16 holding global unit (lane%16) ^ swizzle(row)
+    const bool stage_v = wave >= PF_SW;
     const uint16_t* sbase = (stage_v ? a.vc : a.kc) + kvh * a.kv_head_stride;
-    int soff[4];
+    int soff[PF_LPW];
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const int r = 4 * (4 * (wave & 3) + i) + (lane >> 4);
+    for (int i = 0; i < PF_LPW; i++) {
+        const int r = 4 * (PF_LPW * (wave % PF_SW) + i) + (lane >> 4);
         const int u = (lane & 15) ^ (stage_v ? ((r & 3) << 2) : (r & 15));
         soff[i] = (r * (int)kvs + 8 * u) * 2;
     }
     auto stage = [&](int t) {
         const int t0 = t * PF_BK;
         __amdgpu_buffer_rsrc_t rs = gi_rsrc(sbase + (long long)t0 * kvs, (long long)(kv_len - t0) * kvs * 2);
-        unsigned char* dst = &smem[t & (PF_NBUF - 1)][stage_v ? 1 : 0][4096 * (wave & 3)];
+        unsigned char* dst = &smem[t & (PF_NBUF - 1)][stage_v ? 1 : 0][1024 * PF_LPW * (wave % PF_SW)];
 #pragma unroll
-        for (int i = 0; i < 4; i++)
+        for (int i = 0; i < PF_LPW; i++)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (GI_LDS void*)(dst + 1024 * i), 16, soff[i], 0, 0, 0);
     };
 
@@ -594,22 +605,28 @@ extern "C" __global__ void __launch_bounds__(512, 1) gi_prefill_fwd(GiPrefillArg
 #pragma unroll
         for (int e = 0; e < 16; e++) o[db][e] = 0.f;
     float m_run = 0.f, l_run = 0.f;
+    f16x negm; // -m_run in every element: the C operand that starts each QK chain
+#pragma unroll
+    for (int e = 0; e < 16; e++) negm[e] = 0.f;
 
-    // S^T of tile t (its K in buffer t%4) minus the row's reference max: the accumulators start at -m_run,
+    // S^T of tile t (its K in buffer t%4) minus the row's reference max: each chain starts from C = negm,
     // so the MFMA output is the exp2 argument itself
     auto qk = [&](int t, f16x* s) {
         const unsigned char* K = &smem[t & (PF_NBUF - 1)][0][0];
+        // K fragments stream through a ring of PF_KPF registers, each read PF_KPF MFMAs before its use
+        h8 kf[PF_KPF];
 #pragma unroll
-        for (int bb = 0; bb < 2; bb++)
+        for (int st = 0; st < PF_KPF; st++)
+            kf[st] = *reinterpret_cast<const h8*>(K + 8192 * (st & 1) + kbase + 32 * ((st >> 1) ^ ky));
 #pragma unroll
-            for (int e = 0; e < 16; e++) s[bb][e] = -m_run;
-#pragma unroll
-        for (int ks = 0; ks < 8; ks++)
-#pragma unroll
-            for (int bb = 0; bb < 2; bb++) {
-                h8 kf = *reinterpret_cast<const h8*>(K + 8192 * bb + kbase + 32 * (ks ^ ky));
-                s[bb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[ks], s[bb], 0, 0, 0);
-            }
+        for (int st = 0; st < 16; st++) {
+            const int ks = st >> 1, bb = st & 1;
+            const h8 cur = kf[st % PF_KPF];
+            if (st + PF_KPF < 16)
+                kf[st % PF_KPF] =
+                    *reinterpret_cast<const h8*>(K + 8192 * ((st + PF_KPF) & 1) + kbase + 32 * (((st + PF_KPF) >> 1) ^ ky));
+            s[bb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(cur, qf[ks], ks == 0 ? negm : s[bb], 0, 0, 0);
+        }
     };
 
     const int wave_first = a.pos0 + q0 + 32 * wave;  // position of the wave's first row
@@ -621,21 +638,27 @@ extern "C" __global__ void __launch_bounds__(512, 1) gi_prefill_fwd(GiPrefillArg
     stage(0);
     if (ntiles > 1) stage(1);
     if (ntiles > 2) stage(2);
-    if (ntiles > 2) __builtin_amdgcn_s_waitcnt(0xF78);      // vmcnt(8): tile 0 is in
-    else if (ntiles > 1) __builtin_amdgcn_s_waitcnt(0xF74); // vmcnt(4)
-    else __builtin_amdgcn_s_waitcnt(0xF70);                 // vmcnt(0)
+    if (ntiles > 2) __builtin_amdgcn_s_waitcnt(GI_VMCNT(2 * PF_LPW)); // tile 0 is in
+    else if (ntiles > 1) __builtin_amdgcn_s_waitcnt(GI_VMCNT(PF_LPW));
+    else __builtin_amdgcn_s_waitcnt(GI_VMCNT(0));
     asm volatile("s_barrier" ::: "memory");
     // One pipeline step: tile it's softmax and PV, with QK of tile it+1 into sn (past this wave's last
     // tile that QK reads a stale buffer and is never used). No branch separates the QK MFMAs from the
     // VALU work they hide.
     auto step = [&](int it, f16x* s, f16x* sn) {
+        // the QK half runs at raised wave priority: of a SIMD's two waves, the one entering its MFMA-heavy
+        // QK half is served first (measured ~1% faster than equal priority)
+        __builtin_amdgcn_s_setprio(2);
         qk(it + 1, sn);
         float mx = GI_NEG_INF;
 #pragma unroll
         for (int bb = 0; bb < 2; bb++)
 #pragma unroll
             for (int e = 0; e < 16; e++) mx = fmaxf(mx, s[bb][e]);
-        mx = fmaxf(mx, __shfl_xor(mx, 32, 64)); // the tile's row max relative to m_run
+        {   // with lane l + 32 (the row's other half of the keys): a VALU lane swap, no LDS round trip
+            const auto p = __builtin_amdgcn_permlane32_swap(__float_as_int(mx), __float_as_int(mx), false, false);
+            mx = fmaxf(__int_as_float(p[0]), __int_as_float(p[1])); // the tile's row max relative to m_run
+        }
         const bool up = mx > PF_RESCALE_LOG2 || it == 0;
         if (__builtin_amdgcn_ballot_w64(up)) {
             // some row's max moved (tile 0: every row takes its first max): shift the reference by delta,
@@ -644,6 +667,8 @@ extern "C" __global__ void __launch_bounds__(512, 1) gi_prefill_fwd(GiPrefillArg
             const float delta = up ? mx : 0.f;
             const float alpha = __builtin_amdgcn_exp2f(-fmaxf(delta, 0.f));
             m_run += delta;
+#pragma unroll
+            for (int e = 0; e < 16; e++) negm[e] = -m_run;
             l_run *= alpha;
 #pragma unroll
             for (int db = 0; db < 4; db++) o[db] *= alpha;
@@ -653,6 +678,7 @@ extern "C" __global__ void __launch_bounds__(512, 1) gi_prefill_fwd(GiPrefillArg
                 sn[bb] -= delta;
             }
         }
+        __builtin_amdgcn_s_setprio(0);
         // probabilities of k-step ks feed the PV MFMAs of k-step ks
         const unsigned char* V = &smem[it & (PF_NBUF - 1)][1][0];
 #pragma unroll
@@ -684,8 +710,8 @@ extern "C" __global__ void __launch_bounds__(512, 1) gi_prefill_fwd(GiPrefillArg
     // whose buffer then takes tile it+3. Barriers are bare s_barrier (__syncthreads' release fence would
     // also wait for tile it+2's loads); the memory clobber keeps LDS accesses on their side.
     auto iteration = [&](int it, f16x* s, f16x* sn) {
-        if (it + 2 < ntiles) __builtin_amdgcn_s_waitcnt(0xF74); // vmcnt(4)
-        else __builtin_amdgcn_s_waitcnt(0xF70);                // vmcnt(0)
+        if (it + 2 < ntiles) __builtin_amdgcn_s_waitcnt(GI_VMCNT(PF_LPW)); // tile it+2's loads may stay in flight
+        else __builtin_amdgcn_s_waitcnt(GI_VMCNT(0));
         asm volatile("s_barrier" ::: "memory");
         if (it + 3 < ntiles) stage(it + 3);
         if (it < my_tiles) {
