@@ -485,6 +485,15 @@ struct GiPrefillArgs {
 #define PF_BK 64           // keys per tile
 #define PF_TILE 16384      // bytes of one K or V tile: 64 rows of 256 bytes
 #define PF_RESCALE_LOG2 8.0f
+#ifndef PF_SGB
+#define PF_SGB 1           // instruction-order hints for the step block (see the step)
+#endif
+#ifndef PF_V1
+#define PF_V1 2            // VALU instructions scheduled after each QK MFMA
+#endif
+#ifndef PF_V2
+#define PF_V2 3            // after each PV MFMA
+#endif
 #ifndef PF_KPF
 #define PF_KPF 8           // K fragments in flight in the QK loop
 #endif
@@ -618,6 +627,7 @@ extern "C" __global__ void __launch_bounds__(64 * PF_WAVES, 1) gi_prefill_fwd(Gi
 #pragma unroll
         for (int st = 0; st < PF_KPF; st++)
             kf[st] = *reinterpret_cast<const h8*>(K + 8192 * (st & 1) + kbase + 32 * ((st >> 1) ^ ky));
+        __builtin_amdgcn_sched_barrier(0); // the first PF_KPF reads go out before any of the MFMAs
 #pragma unroll
         for (int st = 0; st < 16; st++) {
             const int ks = st >> 1, bb = st & 1;
@@ -645,25 +655,28 @@ extern "C" __global__ void __launch_bounds__(64 * PF_WAVES, 1) gi_prefill_fwd(Gi
     // One pipeline step: tile it's softmax and PV, with QK of tile it+1 into sn (past this wave's last
     // tile that QK reads a stale buffer and is never used). No branch separates the QK MFMAs from the
     // VALU work they hide.
-    auto step = [&](int it, f16x* s, f16x* sn) {
-        // the QK half runs at raised wave priority: of a SIMD's two waves, the one entering its MFMA-heavy
-        // QK half is served first (measured ~1% faster than equal priority)
-        __builtin_amdgcn_s_setprio(2);
-        qk(it + 1, sn);
+    // row max of a tile's scores (relative to m_run) over the row's two lane halves (lanes l and l + 32,
+    // exchanged by a VALU lane swap, no LDS round trip)
+    auto rowmax = [&](const f16x* sc) {
         float mx = GI_NEG_INF;
 #pragma unroll
         for (int bb = 0; bb < 2; bb++)
 #pragma unroll
-            for (int e = 0; e < 16; e++) mx = fmaxf(mx, s[bb][e]);
-        {   // with lane l + 32 (the row's other half of the keys): a VALU lane swap, no LDS round trip
-            const auto p = __builtin_amdgcn_permlane32_swap(__float_as_int(mx), __float_as_int(mx), false, false);
-            mx = fmaxf(__int_as_float(p[0]), __int_as_float(p[1])); // the tile's row max relative to m_run
-        }
+            for (int e = 0; e < 16; e++) mx = fmaxf(mx, sc[bb][e]);
+        const auto p = __builtin_amdgcn_permlane32_swap(__float_as_int(mx), __float_as_int(mx), false, false);
+        return fmaxf(__int_as_float(p[0]), __int_as_float(p[1]));
+    };
+    // One pipeline step for tile it (scores s, their row max mx): the rare rescale first, then one
+    // branch-free block that issues QK of tile it+1 into sn, computes tile it's probabilities k-step by
+    // k-step under those MFMAs and the PV MFMAs of tile it, and ends with tile it+1's row max (mx on exit),
+    // so that the next step can start its exp2 work at once. Past this wave's last tile the QK reads a
+    // stale buffer and is never used.
+    auto step = [&](int it, f16x* s, f16x* sn, float& mx) {
         const bool up = mx > PF_RESCALE_LOG2 || it == 0;
         if (__builtin_amdgcn_ballot_w64(up)) {
             // some row's max moved (tile 0: every row takes its first max): shift the reference by delta,
-            // rescale O and l (alpha = 1 for the other rows; O and l are still 0 at tile 0) and the scores
-            // already computed against the old reference, this tile's and the next one's
+            // rescale O and l (alpha = 1 for the other rows; O and l are still 0 at tile 0) and this tile's
+            // scores; the next tile's QK starts from the new reference
             const float delta = up ? mx : 0.f;
             const float alpha = __builtin_amdgcn_exp2f(-fmaxf(delta, 0.f));
             m_run += delta;
@@ -673,12 +686,9 @@ extern "C" __global__ void __launch_bounds__(64 * PF_WAVES, 1) gi_prefill_fwd(Gi
 #pragma unroll
             for (int db = 0; db < 4; db++) o[db] *= alpha;
 #pragma unroll
-            for (int bb = 0; bb < 2; bb++) {
-                s[bb] -= delta;
-                sn[bb] -= delta;
-            }
+            for (int bb = 0; bb < 2; bb++) s[bb] -= delta;
         }
-        __builtin_amdgcn_s_setprio(0);
+        qk(it + 1, sn);
         // probabilities of k-step ks feed the PV MFMAs of k-step ks
         const unsigned char* V = &smem[it & (PF_NBUF - 1)][1][0];
 #pragma unroll
@@ -704,11 +714,50 @@ extern "C" __global__ void __launch_bounds__(64 * PF_WAVES, 1) gi_prefill_fwd(Gi
                 o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf, o[db], 0, 0, 0);
             }
         }
+        mx = rowmax(sn); // unmasked: a diagonal tile recomputes it after masking
+        // Instruction order of the block (the compiler's scheduler follows these groups in sequence):
+        // QK phase, per QK MFMA: one LDS read (the K fragment PF_KPF steps on, then V fragments of the first
+        // k-step) and PF_V1 VALU (tile it's exp2 / pack / row sum of k-steps 0-1); PV phase, per PV MFMA: up
+        // to two V reads and PF_V2 VALU (k-steps 2-3, then tile it+1's row max).
+#if PF_SGB == 1
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                // MFMA
+            if (i + PF_KPF < 16) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0); // its K refill
+        }
+#elif PF_SGB == 2
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            if (i + PF_KPF < 16) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x002, PF_V1, 0);
+        }
+#elif PF_SGB == 3
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
+#elif PF_SGB == 4
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);     // MFMA
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);     // LDS read
+            __builtin_amdgcn_sched_group_barrier(0x002, PF_V1, 0); // VALU
+        }
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x002, PF_V2, 0);
+        }
+#endif
     };
     // Iteration it: before the barrier each wave waits for its own loads of tile it+1 (tile it+2's may
     // stay in flight); the barrier publishes the tile and tells that every wave is done with tile it-1,
     // whose buffer then takes tile it+3. Barriers are bare s_barrier (__syncthreads' release fence would
     // also wait for tile it+2's loads); the memory clobber keeps LDS accesses on their side.
+    float mx = GI_NEG_INF;
     auto iteration = [&](int it, f16x* s, f16x* sn) {
         if (it + 2 < ntiles) __builtin_amdgcn_s_waitcnt(GI_VMCNT(PF_LPW)); // tile it+2's loads may stay in flight
         else __builtin_amdgcn_s_waitcnt(GI_VMCNT(0));
@@ -726,12 +775,16 @@ extern "C" __global__ void __launch_bounds__(64 * PF_WAVES, 1) gi_prefill_fwd(Gi
 #pragma unroll
                         for (int jj = 0; jj < 4; jj++)
                             if (32 * bb + 16 * (i >> 1) + 4 * (i & 1) + jj > lim) s[bb][4 * i + jj] = GI_NEG_INF;
+                mx = rowmax(s);
             }
-            step(it, s, sn);
+            step(it, s, sn, mx);
         }
     };
     f16x sa[2], sb[2]; // scores of alternate tiles
-    if (my_tiles > 0) qk(0, sa);
+    if (my_tiles > 0) {
+        qk(0, sa);
+        mx = rowmax(sa);
+    }
     for (int it = 0; it < ntiles; it += 2) {
         iteration(it, sa, sb);
         if (it + 1 < ntiles) iteration(it + 1, sb, sa);
