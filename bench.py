@@ -1,6 +1,6 @@
 """Benchmark of the gfx950 attention hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload decode64k|decode4k|verify|prefill8k|chunked]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload decode64k|decode4k|verify|prefill8k|chunked|qkrope]
                     [--no-cpu-baseline] [--no-secondary] [--reference-layout]
 
 A step is one pass of the hot path over one batch of synthetic seeded input already resident in HBM:
@@ -10,6 +10,7 @@ A step is one pass of the hot path over one batch of synthetic seeded input alre
   verify     config 4: 8 draft tokens on a 32768-key prefix, 32 / 4 heads
   prefill8k  config 3: causal prefill of 8192 tokens, 32 / 8 heads, f16 in and out (MFMA TFLOP/s)
   chunked    config 5: 131072 tokens in 2048-token chunks against the growing cache, 32 / 4 heads
+  qkrope     the cache write before attention (qk_norm_rope + f16 KV store) for config 3's 8192 tokens
 Decode steps rotate over several layers' caches whose total exceeds the 256 MB Infinity Cache, as a
 model's layer loop does, so no step finds its K/V in the last-level cache.
 
@@ -164,6 +165,27 @@ def prefill_workload(torch, gi_attn, dev, n, n_heads, n_kv, steps, warmup, seed)
     return {"seconds": t, "flops": prefill_flops(n, 0, n_heads), "step": step}
 
 
+def qkrope_workload(torch, gi_attn, dev, n, n_heads, n_kv, steps, warmup, seed):
+    """layer_attn's qk_norm_rope step (RMSNorm + RoPE of q and k, K/V into the f16 cache) for n tokens."""
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(seed)
+    row = (n_heads + 2 * n_kv) * HD
+    qkv0 = torch.randn((n, row), generator=gen, device=dev, dtype=torch.float32)
+    qkv = qkv0.clone()
+    k = torch.empty((n, n_kv, HD), device=dev, dtype=torch.float16)
+    v = torch.empty_like(k)
+    qn = torch.rand(HD, generator=gen, device=dev) + 0.5
+    kn = torch.rand(HD, generator=gen, device=dev) + 0.5
+
+    def step(i):
+        gi_attn.qk_norm_rope(qkv, k, v, 0, n_heads, n_kv, qn=qn, kn=kn, base=1e6)
+
+    t = time_steps(step, steps, warmup, torch)
+    # bytes the step must move: every qkv row read, the q and k heads written back, K and V rows stored (f16)
+    nbytes = n * row * 4 + n * (n_heads + n_kv) * HD * 4 + 2 * n * n_kv * HD * 2
+    return {"seconds": t, "bytes": nbytes, "step": step}
+
+
 def chunked_workload(torch, gi_attn, dev, total, chunk, n_heads, n_kv, seed):
     gen = torch.Generator(device=dev)
     gen.manual_seed(seed)
@@ -243,7 +265,7 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="decode64k",
-                    choices=["decode64k", "decode4k", "verify", "prefill8k", "chunked"])
+                    choices=["decode64k", "decode4k", "verify", "prefill8k", "chunked", "qkrope"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--reference-layout", action="store_true",
@@ -307,6 +329,20 @@ def main():
             result["cpu_baseline"] = {"value": round(r["bytes"] / t_cpu / 1e9, 3), "unit": "GB/s", "cores": threads,
                                       "kind": "port",
                                       "sample": f"{reps} runs of the same decode (median {t_cpu * 1e3:.1f} ms/run)"}
+    elif w == "qkrope":
+        log("[bench] qk_norm_rope + KV store for 8192 tokens, 32q/8kv (the cache write of config 3)")
+        r = qkrope_workload(torch, gi_attn, dev, 8192, 32, 8, args.steps, args.warmup, 7)
+        gbs = r["bytes"] / r["seconds"] / 1e9
+        ms, n_l = kernel_times(gi_attn, r["step"], args.steps, torch, ("qk_norm_rope",))["qk_norm_rope"]
+        kern = r["bytes"] / (ms / 1e3) / 1e9
+        result.update({
+            "value": round(gbs, 1), "unit": "GB/s", "ms_per_step": r["seconds"] * 1e3, "dtype": "f32 math, f16 cache",
+            "config": {"workload": "qk_norm_rope + f16 KV store, 8192 tokens, 32q/8kv, hd 128", "bytes_per_step": r["bytes"]},
+            "roofline": {"bound": "hbm", "achieved": round(kern, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(kern / HBM_PEAK_GBS, 4), "traffic": None, "kernel": "gi_qk_norm_rope",
+                         "algorithmic_bytes_per_launch": r["bytes"], "kernel_ms_per_launch": round(ms, 5),
+                         "launches_timed": n_l},
+        })
     elif w == "prefill8k":
         log("[bench] config 3: causal prefill 8192 tokens, 32q/8kv")
         r = prefill_workload(torch, gi_attn, dev, 8192, 32, 8, args.steps, args.warmup, 99)

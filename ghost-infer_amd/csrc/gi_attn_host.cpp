@@ -44,6 +44,30 @@ struct GiDecodeArgs {
     int pad_;
 };
 
+// Must match the kernels' GiRopeArgs.
+struct GiRopeArgs {
+    float* qkv;
+    const float* qn;
+    const float* kn;
+    uint16_t* kc;
+    uint16_t* vc;
+    const float* ff;
+    const int* posp;
+    long long row_stride;
+    long long kv_stride;
+    long long kv_head_stride;
+    int pos0;
+    int n;
+    int n_heads;
+    int n_kv;
+    int hd;
+    int rope_dim;
+    float base;
+    float eps;
+    int neox;
+    int pad_;
+};
+
 // Must match the kernels' GiPrefillArgs.
 struct GiPrefillArgs {
     const void* q;
@@ -69,6 +93,7 @@ constexpr int kMaxDevices = 64;
 #ifndef CMB_DSPLIT
 #define CMB_DSPLIT 8
 #endif
+constexpr int kRopeHeads = 16; // heads per gi_qk_norm_rope workgroup; must match the kernels' ROPE_HEADS
 constexpr int kCombineSplit = CMB_DSPLIT; // combine workgroups per (head, token); must match the kernels'
 constexpr int kDecWaves = 4, kDecTile = 32, kDecPairs = 8, kDecPart = 132; // kDecPart: floats per slice partial
 constexpr int kSliceUnit = kDecWaves * kDecTile; // 128 keys
@@ -99,7 +124,7 @@ struct Module {
     bool loaded = false;
     hipModule_t mod = nullptr;
     hipFunction_t dec[2][2] = {}; // [shared][column blocks - 1]
-    hipFunction_t combine = nullptr, prefill = nullptr;
+    hipFunction_t combine = nullptr, prefill = nullptr, rope = nullptr;
     int prefill_threads = 0; // the prefill kernel's block size (its launch bound: waves x 64)
 };
 std::mutex g_mu;
@@ -134,6 +159,7 @@ int load_module(const char* path, Module** out) {
             {&m.dec[1][1], "gi_decode_shared_2"},
             {&m.combine, "gi_decode_combine"},
             {&m.prefill, "gi_prefill_fwd"},
+            {&m.rope, "gi_qk_norm_rope"},
         };
         for (auto& f : fns)
             if (int e = check(hipModuleGetFunction(f.f, m.mod, f.name), f.name)) {
@@ -154,8 +180,8 @@ int load_module(const char* path, Module** out) {
 }
 
 // ---- per-kernel timing (gi_kernel_timing): event pairs around each launch, per kernel kind
-enum Kind { kDecodePartial = 0, kDecodeCombine = 1, kPrefill = 2, kKinds = 3 };
-const char* const kKindNames[kKinds] = {"decode_partial", "decode_combine", "prefill"};
+enum Kind { kDecodePartial = 0, kDecodeCombine = 1, kPrefill = 2, kRope = 3, kKinds = 4 };
+const char* const kKindNames[kKinds] = {"decode_partial", "decode_combine", "prefill", "qk_norm_rope"};
 struct Timing {
     std::mutex mu;
     bool on = false;
@@ -404,7 +430,7 @@ int gi_kernel_timing_read(const char* kernel, double* total_ms, int* launches) {
     int kind = -1;
     for (int k = 0; k < kKinds; k++)
         if (std::strcmp(kernel, kKindNames[k]) == 0) kind = k;
-    if (kind < 0) return fail("unknown kernel \"%s\" (decode_partial, decode_combine or prefill)", kernel);
+    if (kind < 0) return fail("unknown kernel \"%s\" (decode_partial, decode_combine, prefill or qk_norm_rope)", kernel);
     std::vector<std::pair<hipEvent_t, hipEvent_t>> ev;
     {
         std::lock_guard<std::mutex> lock(g_timing.mu);
@@ -423,6 +449,45 @@ int gi_kernel_timing_read(const char* kernel, double* total_ms, int* launches) {
     *total_ms = sum;
     *launches = (int)ev.size();
     return err;
+}
+
+int gi_qk_norm_rope(void* stream, float* qkv, const float* qn, const float* kn, uint16_t* kc, uint16_t* vc,
+                    long long kv_stride, long long kv_head_stride, int pos0, const int* posp, int n, int n_heads,
+                    int n_kv, int hd, int rope_dim, float base, const float* ff, int neox, float eps) {
+    if (hd != 64 && hd != 128 && hd != 256) return fail("head size %d unsupported by the KV store (64, 128, 256)", hd);
+    if (n_kv <= 0 || n_heads <= 0 || n_heads % n_kv != 0)
+        return fail("n_heads %d must be a positive multiple of n_kv %d", n_heads, n_kv);
+    if (n <= 0) return fail("n %d must be positive", n);
+    if (rope_dim < 0 || rope_dim > hd || rope_dim % 2) return fail("rope_dim %d must be even and at most %d", rope_dim, hd);
+    if (!qkv || !kc || !vc) return fail("null tensor pointer");
+    if ((qn == nullptr) != (kn == nullptr)) return fail("qn and kn must both be given or both be null");
+    if (!posp && pos0 < 0) return fail("pos0 %d must be >= 0", pos0);
+    if (kv_head_stride == 0) kv_head_stride = hd;
+    if (int e = check_kv_strides(kv_stride, kv_head_stride, n_kv, hd)) return e;
+    Module* m;
+    if (int e = load_module(nullptr, &m)) return e;
+    GiRopeArgs a{};
+    a.qkv = qkv;
+    a.qn = qn;
+    a.kn = kn;
+    a.kc = kc;
+    a.vc = vc;
+    a.ff = ff;
+    a.posp = posp;
+    a.row_stride = (long long)(n_heads + 2 * n_kv) * hd;
+    a.kv_stride = kv_stride;
+    a.kv_head_stride = kv_head_stride;
+    a.pos0 = pos0;
+    a.n = n;
+    a.n_heads = n_heads;
+    a.n_kv = n_kv;
+    a.hd = hd;
+    a.rope_dim = rope_dim;
+    a.base = base;
+    a.eps = eps;
+    a.neox = neox != 0;
+    const int groups = (n_heads + 2 * n_kv + kRopeHeads - 1) / kRopeHeads; // workgroups per token
+    return launch(kRope, m->rope, dim3(groups, n, 1), dim3(256), (hipStream_t)stream, &a, sizeof a);
 }
 
 } // extern "C"

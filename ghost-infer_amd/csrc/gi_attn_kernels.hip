@@ -815,3 +815,117 @@ extern "C" __global__ void __launch_bounds__(64 * PF_WAVES, 1) gi_prefill_fwd(Gi
         }
     }
 }
+
+// ------------------------------------------------------------------------------------------------ KV store
+
+// Arguments of gi_qk_norm_rope (must match gi_attn_host.cpp).
+struct GiRopeArgs {
+    float* qkv;            // packed rows [q (n_heads*hd) | k (n_kv*hd) | v (n_kv*hd)] f32, row_stride apart
+    const float* qn;       // RMSNorm weights of q heads [hd] (null: no norm)
+    const float* kn;       // of k heads
+    uint16_t* kc;          // f16 caches: position t, kv head h at t*kv_stride + h*kv_head_stride
+    uint16_t* vc;
+    const float* ff;       // RoPE frequency factors [rope_dim/2] (null: none)
+    const int* posp;       // device position (overrides pos0 when non-null)
+    long long row_stride;
+    long long kv_stride;
+    long long kv_head_stride;
+    int pos0;
+    int n;                 // tokens
+    int n_heads;
+    int n_kv;
+    int hd;                // 64, 128 or 256
+    int rope_dim;          // rotated dims (even, <= hd); the rest pass unchanged
+    float base;
+    float eps;
+    int neox;              // pairs (i, i + rope_dim/2); otherwise (2i, 2i+1)
+    int pad_;
+};
+
+// Reference semantics: qk_norm_rope (src/cuda.rs:437-486) with an f16 cache (kv_store, src/cuda.rs:312-362).
+// A q or k head: RMSNorm (ss = sum of squares over the head, scale = rsqrt(ss/hd + eps), times the
+// weights), then RoPE on rope_dim/2 pairs (freq_i = base^(-2i/rope_dim) / ff[i], angle = pos * freq_i, all
+// f32), written back into qkv; a k head also goes to the K cache. A v head goes to the V cache unchanged.
+// Cache values are rounded to nearest even. One workgroup per (token, group of ROPE_HEADS heads of the
+// packed row: q heads, then k, then v): the pairs' sines and cosines depend only on the position, so the
+// workgroup computes them once into LDS for all its heads; each wave loads its ROPE_HEADS/4 heads at once
+// and takes them one at a time through a per-wave LDS row (any two dims can pair).
+#define ROPE_HEADS 16
+// PER = hd / 64 values per lane, dims PER*lane .. PER*lane + PER - 1 (one 4, 8 or 16-byte access per row)
+template <int PER>
+__device__ __forceinline__ void gi_qk_norm_rope_t(const GiRopeArgs& a, float (*cs_sh)[2], float (*row_sh)[256]) {
+    typedef float fv __attribute__((ext_vector_type(PER)));
+    typedef _Float16 hv __attribute__((ext_vector_type(PER)));
+    constexpr int HD = 64 * PER;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int items = a.n_heads + 2 * a.n_kv;
+    const int b = blockIdx.y, h0 = blockIdx.x * ROPE_HEADS;
+    const int pos = (a.posp ? *a.posp : a.pos0) + b;
+    const int half = a.rope_dim >> 1;
+    if (tid < half && h0 < a.n_heads + a.n_kv) { // (a workgroup of v heads only rotates nothing)
+        float freq = powf(a.base, -2.0f * (float)tid / (float)a.rope_dim);
+        if (a.ff) freq /= a.ff[tid];
+        float s, c;
+        sincosf((float)pos * freq, &s, &c);
+        cs_sh[tid][0] = c;
+        cs_sh[tid][1] = s;
+    }
+    __syncthreads();
+    float* row = a.qkv + (long long)b * a.row_stride;
+    float* sh = row_sh[wave];
+    // all of this wave's head rows are loaded up front (more bytes in flight per wave), then processed
+    constexpr int HPW = ROPE_HEADS / 4;
+    fv v[HPW];
+#pragma unroll
+    for (int k = 0; k < HPW; k++) {
+        const int h = h0 + wave + 4 * k;
+        if (h < items) v[k] = *reinterpret_cast<const fv*>(row + (long long)h * HD + PER * lane); // q, k, v heads in turn
+    }
+#pragma unroll
+    for (int k = 0; k < HPW; k++) {
+        const int h = h0 + wave + 4 * k;
+        if (h >= items) break;
+        if (h >= a.n_heads + a.n_kv) { // a v head: into the cache
+            const int vh = h - a.n_heads - a.n_kv;
+            uint16_t* dst = a.vc + (long long)pos * a.kv_stride + (long long)vh * a.kv_head_stride;
+            *reinterpret_cast<hv*>(dst + PER * lane) = __builtin_convertvector(v[k], hv);
+            continue;
+        }
+        fv x = v[k];
+        if (a.qn) {
+            const float* w = h < a.n_heads ? a.qn : a.kn;
+            float ss = 0.f;
+#pragma unroll
+            for (int j = 0; j < PER; j++) ss = fmaf(x[j], x[j], ss);
+            for (int m = 32; m > 0; m >>= 1) ss += __shfl_xor(ss, m, 64);
+            const float scale = __frsqrt_rn(ss / (float)HD + a.eps);
+            const fv wv = *reinterpret_cast<const fv*>(w + PER * lane);
+#pragma unroll
+            for (int j = 0; j < PER; j++) x[j] = x[j] * scale * wv[j];
+        }
+        *reinterpret_cast<fv*>(sh + PER * lane) = x;
+        __builtin_amdgcn_wave_barrier();
+        for (int i = lane; i < half; i += 64) {
+            const int ia = a.neox ? i : 2 * i, ib = a.neox ? i + half : 2 * i + 1;
+            const float p = sh[ia], q = sh[ib], c = cs_sh[i][0], s = cs_sh[i][1];
+            sh[ia] = p * c - q * s;
+            sh[ib] = p * s + q * c;
+        }
+        __builtin_amdgcn_wave_barrier();
+        x = *reinterpret_cast<const fv*>(sh + PER * lane);
+        *reinterpret_cast<fv*>(row + (long long)h * HD + PER * lane) = x;
+        if (h >= a.n_heads) {
+            const int kh = h - a.n_heads;
+            uint16_t* dst = a.kc + (long long)pos * a.kv_stride + (long long)kh * a.kv_head_stride;
+            *reinterpret_cast<hv*>(dst + PER * lane) = __builtin_convertvector(x, hv);
+        }
+        __builtin_amdgcn_wave_barrier(); // the row buffer is reused by the wave's next head
+    }
+}
+extern "C" __global__ void __launch_bounds__(256) gi_qk_norm_rope(GiRopeArgs a) {
+    __shared__ float cs_sh[128][2];  // cos, sin of pair i
+    __shared__ float row_sh[4][256]; // a head row per wave
+    if (a.hd == 64) gi_qk_norm_rope_t<1>(a, cs_sh, row_sh);
+    else if (a.hd == 128) gi_qk_norm_rope_t<2>(a, cs_sh, row_sh);
+    else gi_qk_norm_rope_t<4>(a, cs_sh, row_sh);
+}

@@ -34,6 +34,7 @@ SYMBOLS = (
     "gi_attn_decode",
     "gi_attn_prefill",
     "gi_attention",
+    "gi_qk_norm_rope",
     "gi_kernel_timing",
     "gi_kernel_timing_read",
 )
@@ -69,6 +70,8 @@ def load_library(path=LIB_PATH):
     lib.gi_attn_prefill.restype = i
     lib.gi_attention.argtypes = [vp, vp, vp, vp, vp, vp, sz, i, vp, i, i, i, i, i, i]
     lib.gi_attention.restype = i
+    lib.gi_qk_norm_rope.argtypes = [vp, vp, vp, vp, vp, vp, ll, ll, i, vp, i, i, i, i, i, f, vp, i, f]
+    lib.gi_qk_norm_rope.restype = i
     lib.gi_kernel_timing.argtypes = [i]
     lib.gi_kernel_timing.restype = i
     lib.gi_kernel_timing_read.argtypes = [ctypes.c_char_p, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(i)]
@@ -238,6 +241,28 @@ def attention(qkv, k_cache, v_cache, pos0, n_heads, n_kv, hd=128, exact=False, o
     return out
 
 
+def qk_norm_rope(qkv, k_cache, v_cache, pos0, n_heads, n_kv, hd=128, rope_dim=None, base=10000.0, qn=None, kn=None,
+                 ff=None, neox=True, eps=1e-6, posp=None, kv_layout="reference"):
+    """RMSNorm + RoPE of the q and k heads of f32 rows [q | k | v] (in place) and the k and v heads into the
+    f16 caches at positions pos0.. (layer_attn's qk_norm_rope step, src/cuda.rs:437-486)."""
+    _need(qkv, "qkv", torch.float32)
+    if not qkv.is_contiguous() or qkv.dim() != 2 or qkv.shape[1] != (n_heads + 2 * n_kv) * hd:
+        raise GiAttnError(f"qkv must be contiguous [n, {(n_heads + 2 * n_kv) * hd}]")
+    kv_stride, kv_head_stride, capacity = _cache_layout(k_cache, v_cache, n_kv, hd, kv_layout)
+    n = qkv.shape[0]
+    if posp is None and capacity < pos0 + n:
+        raise GiAttnError(f"the cache holds {capacity} positions; {pos0 + n} needed")
+    for t, name in ((qn, "qn"), (kn, "kn"), (ff, "ff")):
+        if t is not None:
+            _need(t, name, torch.float32)
+    if posp is not None:
+        _need(posp, "posp", torch.int32)
+    _check(load_library().gi_qk_norm_rope(_stream(), _ptr(qkv), _ptr(qn), _ptr(kn), _ptr(k_cache), _ptr(v_cache),
+                                          kv_stride, kv_head_stride, pos0, _ptr(posp), n, n_heads, n_kv, hd,
+                                          hd if rope_dim is None else rope_dim, base, _ptr(ff), 1 if neox else 0, eps))
+    return qkv
+
+
 def kernel_timing(on):
     """Switches per-kernel event timing on or off (benchmarks only; launches under graph capture are
     not timed)."""
@@ -245,7 +270,8 @@ def kernel_timing(on):
 
 
 def kernel_timing_read(kernel):
-    """(total milliseconds, launches) of kernel kind "decode_partial", "decode_combine" or "prefill"
+    """(total milliseconds, launches) of kernel kind "decode_partial", "decode_combine", "prefill" or
+    "qk_norm_rope"
     since the previous read of that kind."""
     ms, n = ctypes.c_double(), ctypes.c_int()
     _check(load_library().gi_kernel_timing_read(kernel.encode(), ctypes.byref(ms), ctypes.byref(n)))

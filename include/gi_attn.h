@@ -89,13 +89,25 @@ int gi_attention(void* stream, const float* qkv, const uint16_t* kc, const uint1
                  void* workspace, size_t workspace_bytes, int pos0, const int* posp, int ctx_cap, int n, int n_heads,
                  int n_kv, int hd, int exact);
 
+/* The layer's step before attention, for a batch of n tokens at positions pos0.. (posp: read from device
+ * memory, graph replay). qkv: f32 rows [q (n_heads*hd) | k (n_kv*hd) | v (n_kv*hd)], updated in place:
+ * each q and k head gets an RMSNorm (skipped when qn and kn are NULL: ss = sum of squares, x * rsqrt(ss/hd
+ * + eps) * weight) and RoPE on its first rope_dim dims (pairs (i, i + rope_dim/2) when neox, else
+ * (2i, 2i+1); angle = pos * base^(-2i/rope_dim) / ff[i], ff NULL = 1). The k and v heads are then stored
+ * into the f16 caches (round to nearest even) in the layout of gi_attn_decode. hd 64, 128 or 256.
+ * Replaces: qk_norm_rope with an f16 cache (src/cuda.rs:437-486, kv_store src/cuda.rs:312-362), launched
+ * by layer_attn (src/cuda.rs:9706-9717). */
+int gi_qk_norm_rope(void* stream, float* qkv, const float* qn, const float* kn, uint16_t* kc, uint16_t* vc,
+                    long long kv_stride, long long kv_head_stride, int pos0, const int* posp, int n, int n_heads,
+                    int n_kv, int hd, int rope_dim, float base, const float* ff, int neox, float eps);
+
 /* Per-kernel GPU time, for benchmarks. No counterpart in the reference. While on (process-wide), every
  * kernel the library launches outside graph capture is bracketed by a pair of HIP events on its stream.
  * Not for production use: each launch creates two events. */
 int gi_kernel_timing(int on);
 
-/* Total milliseconds and launch count of kernel kind `kernel` ("decode_partial", "decode_combine" or
- * "prefill") recorded since the previous read of that kind; waits for the recorded events and
+/* Total milliseconds and launch count of kernel kind `kernel` ("decode_partial", "decode_combine",
+ * "prefill" or "qk_norm_rope") recorded since the previous read of that kind; waits for the recorded events and
  * releases them. */
 int gi_kernel_timing_read(const char* kernel, double* total_ms, int* launches);
 

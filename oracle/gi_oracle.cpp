@@ -14,12 +14,17 @@
 //                                     an f16 cache, head size 128, then attention_combine)
 //   gio_prefill_tc                    src/cuda.rs:2408-2617 (attn_prefill_tc<128>: Q*scale*log2e and
 //                                     P rounded to f16, base-2 online softmax over 32-key tiles)
+//   gio_qk_norm_rope                  src/cuda.rs:437-486 with the f16 kv_store (src/cuda.rs:312-362):
+//                                     RMSNorm of q/k heads, RoPE, K/V rows into the f16 cache
 //
 // How each is pinned (tests/test_oracle.py): the f16 conversion exhaustively against numpy's float16
 // and against src/quant.rs:1160-1169's known values; the attention functions against an independent
 // float64 brute-force softmax attention, closed forms (one position -> V0, zero keys -> mean of V,
 // one dominant key -> its V row), invariance to the split count, causality and GQA group symmetry,
-// and torch's scaled_dot_product_attention.
+// and torch's scaled_dot_product_attention. gio_qk_norm_rope against closed forms: position 0 leaves a
+// head unrotated, every rotation keeps each pair's length, a one-hot pair element lands on its partner
+// with the float64 sine and cosine, unit weights give a unit-RMS head, and the cache holds numpy's f16
+// rounding of the result.
 #include <algorithm>
 #include <atomic>
 #include <cmath>
@@ -458,6 +463,52 @@ void gio_decode_gpu(const float* qkv, long q_stride, const uint16_t* kc, const u
 void gio_prefill_tc(const float* q, long q_stride, const uint16_t* kc, const uint16_t* vc, long kv_stride, float* out,
                     long out_stride, int pos0, int n, int n_heads, int n_kv, float scale, int threads) {
     prefill_tc(q, q_stride, kc, vc, kv_stride, out, out_stride, pos0, n, n_heads, n_kv, scale, threads);
+}
+
+// Reference: qk_norm_rope (src/cuda.rs:437-486), f16 cache. qkv rows [q | k | v] f32 are updated in place
+// (q and k heads normalised and rotated); k and v heads are stored into kc / vc (f16 bits, RNE). Sums in
+// index order; 1/sqrt correctly rounded (the reference's rsqrtf is an approximation of it).
+void gio_qk_norm_rope(float* qkv, const float* qn, const float* kn, uint16_t* kc, uint16_t* vc, long kv_stride,
+                      long kv_head_stride, int pos0, int n, int n_heads, int n_kv, int hd, int rope_dim, float base,
+                      const float* ff, int neox, float eps) {
+    const long q_dim = (long)n_heads * hd, kv_dim = (long)n_kv * hd, row_len = q_dim + 2 * kv_dim;
+    for (int b = 0; b < n; b++) {
+        const int pos = pos0 + b;
+        float* row = qkv + b * row_len;
+        for (int h = 0; h < n_heads + 2 * n_kv; h++) {
+            if (h >= n_heads + n_kv) {
+                const int vh = h - n_heads - n_kv;
+                const float* src = row + q_dim + kv_dim + (long)vh * hd;
+                uint16_t* dst = vc + (long)pos * kv_stride + (long)vh * kv_head_stride;
+                for (int d = 0; d < hd; d++) dst[d] = f32_to_f16(src[d]);
+                continue;
+            }
+            float* vec = row + (long)h * hd;
+            if (qn) {
+                const float* w = h < n_heads ? qn : kn;
+                float ss = 0.f;
+                for (int d = 0; d < hd; d++) ss += vec[d] * vec[d];
+                const float scale = 1.0f / std::sqrt(ss / (float)hd + eps);
+                for (int d = 0; d < hd; d++) vec[d] = vec[d] * scale * w[d];
+            }
+            const int half = rope_dim / 2;
+            for (int i = 0; i < half; i++) {
+                float freq = std::pow(base, -2.0f * (float)i / (float)rope_dim);
+                if (ff) freq /= ff[i];
+                const float ang = (float)pos * freq;
+                const float s = std::sin(ang), c = std::cos(ang);
+                const int ia = neox ? i : 2 * i, ib = neox ? i + half : 2 * i + 1;
+                const float x = vec[ia], y = vec[ib];
+                vec[ia] = x * c - y * s;
+                vec[ib] = x * s + y * c;
+            }
+            if (h >= n_heads) {
+                const int kh = h - n_heads;
+                uint16_t* dst = kc + (long)pos * kv_stride + (long)kh * kv_head_stride;
+                for (int d = 0; d < hd; d++) dst[d] = f32_to_f16(vec[d]);
+            }
+        }
+    }
 }
 
 } // extern "C"

@@ -44,6 +44,7 @@ def lib():
         L.gio_attention_f16kv.argtypes = [vp, l, vp, vp, l, vp, l, i, i, i, i, i, f, i]
         L.gio_decode_gpu.argtypes = [vp, l, vp, vp, l, vp, l, i, i, i, i, f, i, i, i, i]
         L.gio_prefill_tc.argtypes = [vp, l, vp, vp, l, vp, l, i, i, i, i, f, i]
+        L.gio_qk_norm_rope.argtypes = [vp, vp, vp, vp, vp, l, l, i, i, i, i, i, i, f, vp, i, f]
         _lib = L
     return _lib
 
@@ -138,3 +139,22 @@ def prefill_tc_semantics(q, kc, vc, pos0, n_heads, n_kv, scale=None, threads=8):
     lib().gio_prefill_tc(_p(q), q.shape[1], _p(kc), _p(vc), kc.shape[1], _p(out), out.shape[1], pos0, n, n_heads,
                          n_kv, scale, threads)
     return out
+
+
+def qk_norm_rope(qkv, kc, vc, pos0, n_heads, n_kv, hd=128, rope_dim=None, base=10000.0, qn=None, kn=None, ff=None,
+                 neox=True, eps=1e-6, kv_head_stride=None):
+    """qk_norm_rope (src/cuda.rs:437-486) with an f16 cache: returns (qkv after norm and RoPE, kc, vc), the
+    caches (uint16 f16 bits, rows of position t kv_stride elements apart) updated at positions pos0 ..
+    pos0 + n - 1. Inputs are not modified."""
+    qkv = np.array(qkv, dtype=np.float32, order="C", copy=True)
+    kc = np.array(kc, dtype=np.uint16, order="C", copy=True)
+    vc = np.array(vc, dtype=np.uint16, order="C", copy=True)
+    n = qkv.shape[0]
+    rope_dim = hd if rope_dim is None else rope_dim
+    kv_stride = kc.strides[0] // 2
+    kv_head_stride = hd if kv_head_stride is None else kv_head_stride
+    opts = [None if a is None else np.ascontiguousarray(a, dtype=np.float32) for a in (qn, kn, ff)]
+    ptrs = [None if a is None else _p(a) for a in opts]
+    lib().gio_qk_norm_rope(_p(qkv), ptrs[0], ptrs[1], _p(kc), _p(vc), kv_stride, kv_head_stride, pos0, n, n_heads,
+                           n_kv, hd, rope_dim, base, ptrs[2], 1 if neox else 0, eps)
+    return qkv, kc, vc

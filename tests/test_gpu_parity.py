@@ -323,3 +323,76 @@ def test_prefill_head_major(gpu, n, pos0, n_heads, n_kv):
                           kv_layout="head_major")
     torch.cuda.synchronize()
     assert_close(out.cpu().numpy(), reference_f64(q, k, v, pos0, n_heads, n_kv), what="head-major prefill vs f64")
+
+
+# ---------------------------------------------------------------- qk_norm_rope (KV store)
+
+ROPE_SHAPES = [
+    # (n, pos0, n_heads, n_kv, hd, rope_dim, neox, norm, ff, layout)
+    (1, 4095, 32, 8, 128, 128, True, True, False, "reference"),
+    (7, 100, 16, 4, 64, 64, False, False, False, "reference"),
+    (300, 0, 32, 4, 128, 64, True, True, True, "head_major"),
+    (3, 2000, 8, 2, 256, 256, True, True, False, "reference"),
+    (16, 17, 12, 4, 128, 128, False, True, True, "head_major"),
+]
+
+
+@pytest.mark.parametrize("n,pos0,n_heads,n_kv,hd,rope_dim,neox,norm,use_ff,layout", ROPE_SHAPES)
+def test_qk_norm_rope_matches_oracle(gpu, n, pos0, n_heads, n_kv, hd, rope_dim, neox, norm, use_ff, layout):
+    say("qk_norm_rope", n, pos0, n_heads, n_kv, hd, rope_dim, neox, norm, use_ff, layout)
+    rng = np.random.default_rng(700 + n)
+    qkv = rng.standard_normal((n, (n_heads + 2 * n_kv) * hd), dtype=np.float32)
+    cap = pos0 + n + 5
+    sentinel = np.float16(7.0).view(np.uint16)
+    kc = np.full((cap, n_kv * hd), sentinel, dtype=np.uint16)
+    vc = kc.copy()
+    qn = rng.uniform(0.5, 1.5, hd).astype(np.float32) if norm else None
+    kn = rng.uniform(0.5, 1.5, hd).astype(np.float32) if norm else None
+    ff = rng.uniform(1.0, 8.0, rope_dim // 2).astype(np.float32) if use_ff else None
+    want, wk, wv = O.qk_norm_rope(qkv, kc, vc, pos0, n_heads, n_kv, hd=hd, rope_dim=rope_dim, base=1e6, qn=qn, kn=kn,
+                                  ff=ff, neox=neox)
+    dev = lambda a: None if a is None else torch.from_numpy(a).to(gpu)
+    qt = torch.from_numpy(qkv).to(gpu)
+    kt = torch.from_numpy(kc.view(np.int16)).to(gpu).view(torch.float16).view(cap, n_kv, hd)
+    vt = torch.from_numpy(vc.view(np.int16)).to(gpu).view(torch.float16).view(cap, n_kv, hd)
+    if layout == "head_major":
+        kt, vt = kt.transpose(0, 1).contiguous(), vt.transpose(0, 1).contiguous()
+    gi_attn.qk_norm_rope(qt, kt, vt, pos0, n_heads, n_kv, hd=hd, rope_dim=rope_dim, base=1e6, qn=dev(qn), kn=dev(kn),
+                         ff=dev(ff), neox=neox, kv_layout=layout)
+    torch.cuda.synchronize()
+    if layout == "head_major":
+        kt, vt = kt.transpose(0, 1).contiguous(), vt.transpose(0, 1).contiguous()
+    got = qt.cpu().numpy()
+    gk = kt.cpu().view(torch.int16).numpy().view(np.uint16).reshape(cap, n_kv * hd)
+    gv = vt.cpu().view(torch.int16).numpy().view(np.uint16).reshape(cap, n_kv * hd)
+    # q and k rows: f32 within 2e-3 (a one-ulp difference between sin/cos/pow implementations moves a
+    # rotation angle of a few thousand radians by ~1e-4); the caches: their f16 values within 2e-3 plus one
+    # f16 step; V is copied and rounded only, so it matches exactly; positions outside the batch untouched
+    assert np.abs(got - want).max() <= 2e-3
+    gkf, wkf = gk.view(np.float16).astype(np.float32), wk.view(np.float16).astype(np.float32)
+    assert np.all(np.abs(gkf - wkf) <= 2e-3 + np.abs(wkf) * 2.0 ** -10)
+    np.testing.assert_array_equal(gv, wv)
+    rows = np.r_[0:pos0, pos0 + n:cap]
+    assert np.all(gk[rows] == sentinel) and np.all(gv[rows] == sentinel)
+
+
+def test_qk_norm_rope_then_decode_matches_the_oracle_pipeline(gpu):
+    # the layer's attention step end to end: norm + RoPE + cache store of a new token, then decode over the
+    # cache (its earlier rows filled by the oracle), against the oracle doing both
+    n_heads, n_kv, hd, pos = 32, 8, 128, 1500
+    rng = np.random.default_rng(811)
+    kc = rng.standard_normal((pos + 1, n_kv * hd), dtype=np.float32).astype(np.float16).view(np.uint16)
+    vc = rng.standard_normal((pos + 1, n_kv * hd), dtype=np.float32).astype(np.float16).view(np.uint16)
+    qkv = rng.standard_normal((1, (n_heads + 2 * n_kv) * hd), dtype=np.float32)
+    qn = rng.uniform(0.5, 1.5, hd).astype(np.float32)
+    kn = rng.uniform(0.5, 1.5, hd).astype(np.float32)
+    o_qkv, o_kc, o_vc = O.qk_norm_rope(qkv, kc, vc, pos, n_heads, n_kv, qn=qn, kn=kn, base=1e6)
+    want = O.attention(o_qkv[:, :n_heads * hd], o_kc, o_vc, pos, n_heads, n_kv)
+    qt = torch.from_numpy(qkv).to(gpu)
+    kt = torch.from_numpy(kc.view(np.int16)).to(gpu).view(torch.float16)
+    vt = torch.from_numpy(vc.view(np.int16)).to(gpu).view(torch.float16)
+    gi_attn.qk_norm_rope(qt, kt, vt, pos, n_heads, n_kv, qn=torch.from_numpy(qn).to(gpu),
+                         kn=torch.from_numpy(kn).to(gpu), base=1e6)
+    out = gi_attn.decode(qt[:, :n_heads * hd], kt, vt, pos, n_heads, n_kv)
+    torch.cuda.synchronize()
+    assert_close(out.cpu().numpy(), want, what="qk_norm_rope + decode vs oracle")

@@ -10,6 +10,7 @@ mistake (a dropped term, a wrong index, a missing scale, a wrong causal bound) w
   - torch's scaled_dot_product_attention as a library cross-check;
   - the committed golden fixtures (tests/golden/), made by tests/golden/make_golden.py in float64.
 """
+import math
 import os
 
 import numpy as np
@@ -251,3 +252,70 @@ def test_oracle_against_golden(name):
     n_heads, n_kv, pos0 = int(z["n_heads"]), int(z["n_kv"]), int(z["pos0"])
     got = O.attention(z["q"].astype(np.float32), z["k"], z["v"], pos0, n_heads, n_kv)
     assert_close(got, z["out"], max_abs=2e-5, rel_l2=2e-6, what=name)
+
+
+# ---------------------------------------------------------------- qk_norm_rope (KV store)
+
+def _rope_inputs(seed, n, n_heads, n_kv, hd, cap):
+    rng = np.random.default_rng(seed)
+    qkv = rng.standard_normal((n, (n_heads + 2 * n_kv) * hd), dtype=np.float32)
+    kc = np.zeros((cap, n_kv * hd), dtype=np.uint16)
+    return qkv, kc, kc.copy()
+
+
+def test_rope_position_zero_is_identity_and_cache_rounds_like_numpy():
+    qkv, kc, vc = _rope_inputs(1, 2, 4, 2, 128, 4)
+    out, kc2, vc2 = O.qk_norm_rope(qkv, kc, vc, 0, 4, 2)
+    # token 0 sits at position 0: nothing rotates; token 1 at position 1 does
+    np.testing.assert_array_equal(out[0], qkv[0])
+    assert not np.array_equal(out[1, :4 * 128], qkv[1, :4 * 128])
+    kv = out[:, 4 * 128:].reshape(2, 2, 2 * 128)
+    np.testing.assert_array_equal(kc2[:2], kv[:, 0].astype(np.float16).view(np.uint16))
+    np.testing.assert_array_equal(vc2[:2], kv[:, 1].astype(np.float16).view(np.uint16))
+    assert not kc2[2:].any() and not vc2[2:].any()  # other positions untouched
+
+
+@pytest.mark.parametrize("neox", [True, False])
+def test_rope_keeps_pair_lengths(neox):
+    hd, rope_dim = 128, 96
+    qkv, kc, vc = _rope_inputs(2, 3, 2, 1, hd, 1300)
+    out, _, _ = O.qk_norm_rope(qkv, kc, vc, 1234, 2, 1, rope_dim=rope_dim, neox=neox)
+    half = rope_dim // 2
+    for h in range(3):  # q heads and the k head
+        a = qkv[:, h * hd:(h + 1) * hd].astype(np.float64)
+        b = out[:, h * hd:(h + 1) * hd].astype(np.float64)
+        ia = np.arange(half) if neox else 2 * np.arange(half)
+        ib = ia + half if neox else ia + 1
+        np.testing.assert_allclose(np.hypot(b[:, ia], b[:, ib]), np.hypot(a[:, ia], a[:, ib]), rtol=2e-6)
+        np.testing.assert_array_equal(b[:, rope_dim:], a[:, rope_dim:])  # partial rotary: the rest unchanged
+
+
+@pytest.mark.parametrize("neox,use_ff", [(True, False), (False, False), (True, True)])
+def test_rope_one_hot_lands_on_its_partner(neox, use_ff):
+    hd, base, pos = 64, 500000.0, 37
+    half = hd // 2
+    ff = (1.0 + np.arange(half, dtype=np.float32) / 7).astype(np.float32) if use_ff else None
+    for i in (0, 1, 5, half - 1):
+        ia = i if neox else 2 * i
+        ib = ia + half if neox else ia + 1
+        qkv = np.zeros((1, 3 * hd), dtype=np.float32)
+        qkv[0, ia] = 1.0
+        out, _, _ = O.qk_norm_rope(qkv, np.zeros((64, hd), np.uint16), np.zeros((64, hd), np.uint16), pos, 1, 1, hd=hd,
+                                   base=base, ff=ff, neox=neox)
+        theta = pos * base ** (-2.0 * i / hd) / (ff[i] if use_ff else 1.0)  # float64
+        assert abs(out[0, ia] - math.cos(theta)) < 2e-6
+        assert abs(out[0, ib] - math.sin(theta)) < 2e-6
+        assert np.count_nonzero(out[0, :hd]) <= 2
+
+
+def test_rms_norm_gives_unit_rms_times_weights():
+    hd = 128
+    qkv, kc, vc = _rope_inputs(3, 2, 2, 1, hd, 2)
+    w = np.random.default_rng(9).uniform(0.5, 2.0, hd).astype(np.float32)
+    out, _, _ = O.qk_norm_rope(qkv, kc, vc, 0, 2, 1, qn=np.ones(hd, np.float32), kn=w)
+    # token 0 (position 0, unrotated): q heads have RMS 1, the k head is normalised then weighted
+    for h in range(2):
+        assert abs(np.sqrt(np.mean(out[0, h * hd:(h + 1) * hd].astype(np.float64) ** 2)) - 1.0) < 1e-6
+    k = qkv[0, 2 * hd:3 * hd].astype(np.float64)
+    want = k / np.sqrt(np.mean(k ** 2) + 1e-6) * w
+    np.testing.assert_allclose(out[0, 2 * hd:3 * hd], want, rtol=1e-5, atol=1e-6)
