@@ -339,7 +339,8 @@ def main():
             "value": round(gbs, 1), "unit": "GB/s", "ms_per_step": r["seconds"] * 1e3, "dtype": "f32 math, f16 cache",
             "config": {"workload": "qk_norm_rope + f16 KV store, 8192 tokens, 32q/8kv, hd 128", "bytes_per_step": r["bytes"]},
             "roofline": {"bound": "hbm", "achieved": round(kern, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                         "frac": round(kern / HBM_PEAK_GBS, 4), "traffic": None, "kernel": "gi_qk_norm_rope",
+                         "frac": round(kern / HBM_PEAK_GBS, 4), "traffic": profile_traffic("pmc_qk_norm_rope_qkrope"),
+                         "kernel": "gi_qk_norm_rope",
                          "algorithmic_bytes_per_launch": r["bytes"], "kernel_ms_per_launch": round(ms, 5),
                          "launches_timed": n_l},
         })
