@@ -1,6 +1,6 @@
 """Benchmark of the gfx950 attention hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload decode64k|decode4k|verify|prefill8k|chunked|qkrope]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload decode64k|decode4k|verify|prefill8k|chunked|qkrope|decode64k_i8|verify_i8]
                     [--no-cpu-baseline] [--no-secondary] [--reference-layout]
 
 A step is one pass of the hot path over one batch of synthetic seeded input already resident in HBM:
@@ -11,6 +11,9 @@ A step is one pass of the hot path over one batch of synthetic seeded input alre
   prefill8k  config 3: causal prefill of 8192 tokens, 32 / 8 heads, f16 in and out (MFMA TFLOP/s)
   chunked    config 5: 131072 tokens in 2048-token chunks against the growing cache, 32 / 4 heads
   qkrope     the cache write before attention (qk_norm_rope + f16 KV store) for config 3's 8192 tokens
+  decode64k_i8, verify_i8
+             configs 2 and 4 over the int8 cache (the reference's KV8 format: int8 rows, an f32 scale per
+             position and kv head); bytes are the int8 rows plus their scales
 Decode steps rotate over several layers' caches whose total exceeds the 256 MB Infinity Cache, as a
 model's layer loop does, so no step finds its K/V in the last-level cache.
 
@@ -38,13 +41,21 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def seeded_cache(gen, rows, n_kv, dev, torch, layout="reference"):
+def seeded_cache(gen, rows, n_kv, dev, torch, layout="reference", i8=False):
     """K and V caches of N(0,1) f16 values: [rows, n_kv, HD] (the reference's layout) or [n_kv, rows, HD]
-    (head-major, each kv head's rows contiguous)."""
+    (head-major, each kv head's rows contiguous). i8: int8 rows uniform in -127..127 and f32 scales in
+    [0.015, 0.035] ([rows, n_kv] or [n_kv, rows]); returns (k, v, k_scale, v_scale)."""
     shape = (rows, n_kv, HD) if layout == "reference" else (n_kv, rows, HD)
+    if i8:
+        k = torch.randint(-127, 128, shape, generator=gen, device=dev, dtype=torch.int8)
+        v = torch.randint(-127, 128, shape, generator=gen, device=dev, dtype=torch.int8)
+        sc = shape[:2]
+        ks = torch.rand(sc, generator=gen, device=dev, dtype=torch.float32) * 0.02 + 0.015
+        vs = torch.rand(sc, generator=gen, device=dev, dtype=torch.float32) * 0.02 + 0.015
+        return k, v, ks, vs
     k = torch.randn(shape, generator=gen, device=dev, dtype=torch.float32).half()
     v = torch.randn(shape, generator=gen, device=dev, dtype=torch.float32).half()
-    return k, v
+    return k, v, None, None
 
 
 def kernel_times(gi_attn, fn, steps, torch, kinds):
@@ -124,23 +135,24 @@ def time_steps_graph(fn, steps, warmup, torch):
     return start.elapsed_time(end) / 1e3 / steps
 
 
-def decode_workload(torch, gi_attn, dev, ctx, n_heads, n_kv, n_tok, steps, warmup, seed, layout="head_major"):
+def decode_workload(torch, gi_attn, dev, ctx, n_heads, n_kv, n_tok, steps, warmup, seed, layout="head_major",
+                    i8=False):
     gen = torch.Generator(device=dev)
     gen.manual_seed(seed)
-    cache_bytes = 2 * ctx * n_kv * HD * 2
-    layers = max(1, math.ceil(512e6 / cache_bytes))  # > 256 MB Infinity Cache in total
-    caches = [seeded_cache(gen, ctx, n_kv, dev, torch, layout) for _ in range(layers)]
+    # K+V bytes of one step: every key row once (int8 rows plus their two f32 scales)
+    kv_bytes = 2 * ctx * n_kv * (HD + 4) if i8 else 2 * ctx * n_kv * HD * 2
+    layers = max(1, math.ceil(512e6 / kv_bytes))  # > 256 MB Infinity Cache in total
+    caches = [seeded_cache(gen, ctx, n_kv, dev, torch, layout, i8) for _ in range(layers)]
     q = torch.randn((n_tok, n_heads * HD), generator=gen, device=dev, dtype=torch.float32)
     out = torch.empty((n_tok, n_heads * HD), device=dev, dtype=torch.float32)
     pos0 = ctx - n_tok
     ws = gi_attn.new_workspace(ctx, n_tok, n_heads, n_kv, device=dev)
 
     def step(i):
-        k, v = caches[i % layers]
-        gi_attn.decode(q, k, v, pos0, n_heads, n_kv, out=out, workspace=ws, kv_layout=layout)
+        k, v, ks, vs = caches[i % layers]
+        gi_attn.decode(q, k, v, pos0, n_heads, n_kv, out=out, workspace=ws, kv_layout=layout, k_scale=ks, v_scale=vs)
 
     t = time_steps_graph(step, steps, warmup, torch)
-    kv_bytes = 2 * ctx * n_kv * HD * 2
     return {"seconds": t, "bytes": kv_bytes, "layers": layers, "q": q, "cache": caches[0], "pos0": pos0,
             "layout": layout, "step": step, "ws": ws}
 
@@ -231,7 +243,7 @@ def cpu_baseline_decode(q, cache, pos0, n_heads, n_kv, budget_s=12.0):
 
     threads = min(16, os.cpu_count() or 1)
     qn = q.cpu().numpy()
-    k, v = cache
+    k, v = cache[:2]
     if k.shape[0] == n_kv and k.dim() == 3 and k.shape[1] != n_kv:  # head-major: to the reference's layout
         k, v = k.transpose(0, 1).contiguous(), v.transpose(0, 1).contiguous()
     kn = k.cpu().numpy().view(np.uint16).reshape(k.shape[0], -1)
@@ -265,7 +277,8 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="decode64k",
-                    choices=["decode64k", "decode4k", "verify", "prefill8k", "chunked", "qkrope"])
+                    choices=["decode64k", "decode4k", "verify", "prefill8k", "chunked", "qkrope", "decode64k_i8",
+                             "verify_i8"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--reference-layout", action="store_true",
@@ -285,16 +298,22 @@ def main():
     result = {"metric": METRIC, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
               "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "data": "synthetic"}
     w = args.workload
-    if w in ("decode64k", "decode4k", "verify"):
+    if w in ("decode64k", "decode4k", "verify", "decode64k_i8", "verify_i8"):
         ctx, n_heads, n_kv, n_tok, cfg = {
             "decode64k": (65536, 32, 4, 1, "config 2: decode, 1 token, ctx 65536, 32q/4kv, hd 128"),
             "decode4k": (4096, 32, 8, 1, "config 1: decode, 1 token, ctx 4096, 32q/8kv, hd 128"),
             "verify": (32776, 32, 4, 8, "config 4: verify, 8 tokens at a 32768-key prefix, 32q/4kv, hd 128"),
+            "decode64k_i8": (65536, 32, 4, 1, "config 2 over the int8 cache: decode, 1 token, ctx 65536, 32q/4kv"),
+            "verify_i8": (32776, 32, 4, 8, "config 4 over the int8 cache: verify, 8 tokens at 32768, 32q/4kv"),
         }[w]
+        i8 = w.endswith("_i8")
         log(f"[bench] {cfg}")
-        r = decode_workload(torch, gi_attn, dev, ctx, n_heads, n_kv, n_tok, args.steps, args.warmup, 1234)
+        r = decode_workload(torch, gi_attn, dev, ctx, n_heads, n_kv, n_tok, args.steps, args.warmup, 1234, i8=i8)
         gbs = r["bytes"] / r["seconds"] / 1e9
         chunk, nsplit = gi_attn.decode_plan(ctx, n_tok, n_heads, n_kv)
+        if i8:  # int8 slices are whole 256-key units (64-key tiles, 4 waves)
+            chunk = -(-chunk // 256) * 256
+            nsplit = -(-ctx // chunk)
         kt = kernel_times(gi_attn, r["step"], args.steps, torch, ("decode_partial", "decode_combine"))
         part_ms, part_n = kt["decode_partial"]
         comb_ms, _ = kt["decode_combine"]
@@ -304,26 +323,27 @@ def main():
         kern_gbs = part_bytes / (part_ms / 1e3) / 1e9
         traffic = profile_traffic(f"pmc_decode_partial_{w}")
         result.update({
-            "value": round(gbs, 1), "unit": "GB/s", "ms_per_step": r["seconds"] * 1e3, "dtype": "f16 K/V, f32 math",
+            "value": round(gbs, 1), "unit": "GB/s", "ms_per_step": r["seconds"] * 1e3,
+            "dtype": "int8 K/V + f32 scales, f32 math" if i8 else "f16 K/V, f32 math",
             "config": {"workload": cfg, "ctx": ctx, "n_tok": n_tok, "n_heads": n_heads, "n_kv": n_kv, "hd": HD,
                        "kv_bytes_per_step": r["bytes"], "layers_rotated": r["layers"],
                        "slices": nsplit, "keys_per_slice": chunk, "kv_layout": "head_major [n_kv][ctx][128]"},
             "roofline": {"bound": "hbm", "achieved": round(kern_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": round(kern_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
-                         "kernel": "gi_decode_partial (split-K pass)",
+                         "kernel": "gi_decode_partial_*_i8 (split-K pass)" if i8 else "gi_decode_partial (split-K pass)",
                          "algorithmic_bytes_per_launch": part_bytes,
                          "kernel_ms_per_launch": round(part_ms, 5), "launches_timed": part_n,
                          "combine_ms_per_launch": round(comb_ms, 5) if comb_ms else None,
                          "step_GBs_KV": round(gbs, 1)},
         })
-        if args.reference_layout:
+        if args.reference_layout and not i8:
             # the same decode over caches in the reference's [position][n_kv][128] layout
             r_ref = decode_workload(torch, gi_attn, dev, ctx, n_heads, n_kv, n_tok, args.steps, args.warmup, 1234,
                                     layout="reference")
             result["config"]["reference_layout_GBs"] = round(r_ref["bytes"] / r_ref["seconds"] / 1e9, 1)
             result["config"]["reference_layout_ms_per_step"] = r_ref["seconds"] * 1e3
             del r_ref
-        if not args.no_cpu_baseline:
+        if not args.no_cpu_baseline and not i8:
             log("[bench] cpu baseline (oracle, Model::attention restatement)")
             t_cpu, threads, reps = cpu_baseline_decode(r["q"], r["cache"], r["pos0"], n_heads, n_kv)
             result["cpu_baseline"] = {"value": round(r["bytes"] / t_cpu / 1e9, 3), "unit": "GB/s", "cores": threads,

@@ -42,6 +42,10 @@ struct GiDecodeArgs {
     int nsplit;
     float qscale;
     int pad_;
+    const float* ks;
+    const float* vs;
+    long long sc_stride;
+    long long sc_head_stride;
 };
 
 // Must match the kernels' GiRopeArgs.
@@ -65,7 +69,11 @@ struct GiRopeArgs {
     float base;
     float eps;
     int neox;
-    int pad_;
+    int i8;
+    float* ks;
+    float* vs;
+    long long sc_stride;
+    long long sc_head_stride;
 };
 
 // Must match the kernels' GiPrefillArgs.
@@ -123,7 +131,7 @@ int check(hipError_t r, const char* what) {
 struct Module {
     bool loaded = false;
     hipModule_t mod = nullptr;
-    hipFunction_t dec[2][2] = {}; // [shared][column blocks - 1]
+    hipFunction_t dec[2][2][2] = {}; // [int8 cache][shared][column blocks - 1]
     hipFunction_t combine = nullptr, prefill = nullptr, rope = nullptr;
     int prefill_threads = 0; // the prefill kernel's block size (its launch bound: waves x 64)
 };
@@ -153,10 +161,14 @@ int load_module(const char* path, Module** out) {
         std::string p = path ? std::string(path) : default_code_object();
         if (int e = check(hipModuleLoad(&m.mod, p.c_str()), ("hipModuleLoad(" + p + ")").c_str())) return e;
         struct { hipFunction_t* f; const char* name; } fns[] = {
-            {&m.dec[0][0], "gi_decode_partial_1"},
-            {&m.dec[0][1], "gi_decode_partial_2"},
-            {&m.dec[1][0], "gi_decode_shared_1"},
-            {&m.dec[1][1], "gi_decode_shared_2"},
+            {&m.dec[0][0][0], "gi_decode_partial_1"},
+            {&m.dec[0][0][1], "gi_decode_partial_2"},
+            {&m.dec[0][1][0], "gi_decode_shared_1"},
+            {&m.dec[0][1][1], "gi_decode_shared_2"},
+            {&m.dec[1][0][0], "gi_decode_partial_1_i8"},
+            {&m.dec[1][0][1], "gi_decode_partial_2_i8"},
+            {&m.dec[1][1][0], "gi_decode_shared_1_i8"},
+            {&m.dec[1][1][1], "gi_decode_shared_2_i8"},
             {&m.combine, "gi_decode_combine"},
             {&m.prefill, "gi_prefill_fwd"},
             {&m.rope, "gi_qk_norm_rope"},
@@ -244,25 +256,37 @@ DecVariant dec_variant(int n_tok, int G) {
     return v;
 }
 
-void plan(int max_span, int n_tok, int n_heads, int n_kv, int* chunk, int* nsplit) {
+// Slices are whole units of `unit` keys: one tile per wave (128 keys with the f16 cache's 32-key tiles,
+// 256 with int8's 64-key tiles), so the 4 waves of a workgroup get equal shares.
+void plan(int max_span, int n_tok, int n_heads, int n_kv, int* chunk, int* nsplit, int unit = kSliceUnit) {
     int G = n_heads / n_kv;
     int groups = dec_variant(n_tok, G).groups;
-    int units = (max_span + kSliceUnit - 1) / kSliceUnit; // 128-key units
+    int units = (max_span + unit - 1) / unit;
     int per_slot = std::max(1, decode_target_wgs() / std::max(1, n_kv * groups));
     int per = std::max(1, (units + per_slot - 1) / per_slot);
-    *chunk = per * kSliceUnit;
+    *chunk = per * unit;
     *nsplit = std::max(1, (max_span + *chunk - 1) / *chunk);
 }
 
-// K/V rows of 128 elements must not overlap: either positions outer (kv_stride covers all heads) or heads
-// outer (a head's block holds whole rows); both strides in 16-byte units.
-int check_kv_strides(long long kv_stride, long long kv_head_stride, int n_kv, int hd) {
-    if (kv_stride % 8 || kv_head_stride % 8 || kv_stride <= 0 || kv_head_stride <= 0)
-        return fail("kv_stride %lld and kv_head_stride %lld must be positive multiples of 8", kv_stride, kv_head_stride);
+// K/V rows of hd elements must not overlap: either positions outer (kv_stride covers all heads) or heads
+// outer (a head's block holds whole rows); both strides in 16-byte units (`unit` elements: 8 f16, 16 int8).
+int check_kv_strides(long long kv_stride, long long kv_head_stride, int n_kv, int hd, int unit = 8) {
+    if (kv_stride % unit || kv_head_stride % unit || kv_stride <= 0 || kv_head_stride <= 0)
+        return fail("kv_stride %lld and kv_head_stride %lld must be positive multiples of %d", kv_stride, kv_head_stride,
+                    unit);
     bool pos_outer = kv_head_stride >= hd && kv_stride >= (long long)n_kv * kv_head_stride;
     bool head_outer = kv_stride >= hd && (n_kv == 1 || kv_head_stride >= kv_stride);
     if (!pos_outer && !head_outer)
         return fail("kv_stride %lld / kv_head_stride %lld overlap rows of %d kv heads", kv_stride, kv_head_stride, n_kv);
+    return 0;
+}
+
+// An int8 cache's scales: positive strides (in floats), 4-byte aligned arrays.
+int check_scales(const float* ks, const float* vs, long long sc_stride, long long sc_head_stride) {
+    if (!ks || !vs) return fail("null scale pointer");
+    if (((uintptr_t)ks & 3) || ((uintptr_t)vs & 3)) return fail("ks and vs must be 4-byte aligned");
+    if (sc_stride <= 0 || sc_head_stride <= 0)
+        return fail("sc_stride %lld and sc_head_stride %lld must be positive", sc_stride, sc_head_stride);
     return 0;
 }
 
@@ -271,6 +295,111 @@ int check_shape(int n_heads, int n_kv, int hd) {
     if (n_kv <= 0 || n_heads <= 0 || n_heads % n_kv != 0)
         return fail("n_heads %d must be a positive multiple of n_kv %d", n_heads, n_kv);
     return 0;
+}
+
+// gi_attn_decode and gi_attn_decode_i8: the same launch with the f16 or the int8 kernels.
+int decode_impl(void* stream, const float* q, long long q_stride, const void* kc, const void* vc, const float* ks,
+                const float* vs, long long sc_stride, long long sc_head_stride, bool i8, long long kv_stride,
+                long long kv_head_stride, float* out, long long out_stride, void* workspace, size_t workspace_bytes,
+                int pos0, const int* posp, int ctx_cap, int n_tok, int n_heads, int n_kv, int hd, float scale) {
+    if (int e = check_shape(n_heads, n_kv, hd)) return e;
+    if (n_tok <= 0) return fail("n_tok %d must be positive", n_tok);
+    if (!q || !kc || !vc || !out) return fail("null tensor pointer");
+    if (kv_head_stride == 0) kv_head_stride = hd;
+    if (int e = check_kv_strides(kv_stride, kv_head_stride, n_kv, hd, i8 ? 16 : 8)) return e;
+    if (i8)
+        if (int e = check_scales(ks, vs, sc_stride, sc_head_stride)) return e;
+    if (!aligned16(q) || !aligned16(kc) || !aligned16(vc) || q_stride % 4)
+        return fail("q, kc, vc must be 16-byte aligned and q_stride a multiple of 4");
+    if (q_stride < (long long)n_heads * hd || out_stride < (long long)n_heads * hd)
+        return fail("row strides too small for %d heads", n_heads);
+    if (!posp && pos0 < 0) return fail("pos0 %d must be >= 0", pos0);
+    int max_span = posp ? ctx_cap : pos0 + n_tok;
+    if (posp && ctx_cap < n_tok) return fail("ctx_cap %d must cover the %d tokens", ctx_cap, n_tok);
+    Module* m;
+    if (int e = load_module(nullptr, &m)) return e;
+    const DecVariant var = dec_variant(n_tok, n_heads / n_kv);
+    GiDecodeArgs a{};
+    plan(max_span, n_tok, n_heads, n_kv, &a.chunk, &a.nsplit, i8 ? 2 * kSliceUnit : kSliceUnit);
+    size_t need = a.nsplit == 1 ? 0 : (size_t)n_tok * n_heads * a.nsplit * kDecPart * sizeof(float);
+    if (need && (!workspace || workspace_bytes < need))
+        return fail("workspace of %zu bytes too small: %zu needed", workspace_bytes, need);
+    if (need && !aligned16(workspace)) return fail("the workspace must be 16-byte aligned");
+    a.q = q;
+    a.kc = (const uint16_t*)kc;
+    a.vc = (const uint16_t*)vc;
+    a.part = (float*)workspace;
+    a.out = out;
+    a.posp = posp;
+    a.q_stride = q_stride;
+    a.kv_stride = kv_stride;
+    a.out_stride = out_stride;
+    a.kv_head_stride = kv_head_stride;
+    a.pos0 = pos0;
+    a.n_tok = n_tok;
+    a.n_heads = n_heads;
+    a.n_kv = n_kv;
+    a.qscale = scale * kLog2e;
+    if (i8) {
+        a.ks = ks;
+        a.vs = vs;
+        a.sc_stride = sc_stride;
+        a.sc_head_stride = sc_head_stride;
+    }
+    hipStream_t st = (hipStream_t)stream;
+    if (int e = launch(kDecodePartial, m->dec[i8][var.shared][var.ncb - 1], dim3(a.nsplit, n_kv, var.groups), dim3(256),
+                       st, &a, sizeof a))
+        return e;
+    if (a.nsplit > 1)
+        if (int e = launch(kDecodeCombine, m->combine, dim3(n_heads, n_tok, kCombineSplit), dim3(64), st, &a, sizeof a)) return e;
+    return 0;
+}
+
+// gi_qk_norm_rope and gi_qk_norm_rope_i8: one kernel, f16 or int8 cache rows.
+int rope_impl(void* stream, float* qkv, const float* qn, const float* kn, void* kc, void* vc, float* ks, float* vs,
+              long long sc_stride, long long sc_head_stride, bool i8, long long kv_stride, long long kv_head_stride, int pos0, const int* posp, int n, int n_heads,
+                    int n_kv, int hd, int rope_dim, float base, const float* ff, int neox, float eps) {
+    if (hd != 64 && hd != 128 && hd != 256) return fail("head size %d unsupported by the KV store (64, 128, 256)", hd);
+    if (n_kv <= 0 || n_heads <= 0 || n_heads % n_kv != 0)
+        return fail("n_heads %d must be a positive multiple of n_kv %d", n_heads, n_kv);
+    if (n <= 0) return fail("n %d must be positive", n);
+    if (rope_dim < 0 || rope_dim > hd || rope_dim % 2) return fail("rope_dim %d must be even and at most %d", rope_dim, hd);
+    if (!qkv || !kc || !vc) return fail("null tensor pointer");
+    if ((qn == nullptr) != (kn == nullptr)) return fail("qn and kn must both be given or both be null");
+    if (!posp && pos0 < 0) return fail("pos0 %d must be >= 0", pos0);
+    if (kv_head_stride == 0) kv_head_stride = hd;
+    if (int e = check_kv_strides(kv_stride, kv_head_stride, n_kv, hd, i8 ? 16 : 8)) return e;
+    if (i8)
+        if (int e = check_scales(ks, vs, sc_stride, sc_head_stride)) return e;
+    Module* m;
+    if (int e = load_module(nullptr, &m)) return e;
+    GiRopeArgs a{};
+    a.qkv = qkv;
+    a.qn = qn;
+    a.kn = kn;
+    a.kc = (uint16_t*)kc;
+    a.vc = (uint16_t*)vc;
+    a.i8 = i8;
+    a.ks = ks;
+    a.vs = vs;
+    a.sc_stride = sc_stride;
+    a.sc_head_stride = sc_head_stride;
+    a.ff = ff;
+    a.posp = posp;
+    a.row_stride = (long long)(n_heads + 2 * n_kv) * hd;
+    a.kv_stride = kv_stride;
+    a.kv_head_stride = kv_head_stride;
+    a.pos0 = pos0;
+    a.n = n;
+    a.n_heads = n_heads;
+    a.n_kv = n_kv;
+    a.hd = hd;
+    a.rope_dim = rope_dim;
+    a.base = base;
+    a.eps = eps;
+    a.neox = neox != 0;
+    const int groups = (n_heads + 2 * n_kv + kRopeHeads - 1) / kRopeHeads; // workgroups per token
+    return launch(kRope, m->rope, dim3(groups, n, 1), dim3(256), (hipStream_t)stream, &a, sizeof a);
 }
 
 } // namespace
@@ -312,49 +441,18 @@ int gi_attn_decode(void* stream, const float* q, long long q_stride, const uint1
                    long long kv_stride, long long kv_head_stride, float* out, long long out_stride, void* workspace,
                    size_t workspace_bytes, int pos0, const int* posp, int ctx_cap, int n_tok, int n_heads, int n_kv,
                    int hd, float scale) {
-    if (int e = check_shape(n_heads, n_kv, hd)) return e;
-    if (n_tok <= 0) return fail("n_tok %d must be positive", n_tok);
-    if (!q || !kc || !vc || !out) return fail("null tensor pointer");
-    if (kv_head_stride == 0) kv_head_stride = hd;
-    if (int e = check_kv_strides(kv_stride, kv_head_stride, n_kv, hd)) return e;
-    if (!aligned16(q) || !aligned16(kc) || !aligned16(vc) || q_stride % 4)
-        return fail("q, kc, vc must be 16-byte aligned and q_stride a multiple of 4");
-    if (q_stride < (long long)n_heads * hd || out_stride < (long long)n_heads * hd)
-        return fail("row strides too small for %d heads", n_heads);
-    if (!posp && pos0 < 0) return fail("pos0 %d must be >= 0", pos0);
-    int max_span = posp ? ctx_cap : pos0 + n_tok;
-    if (posp && ctx_cap < n_tok) return fail("ctx_cap %d must cover the %d tokens", ctx_cap, n_tok);
-    Module* m;
-    if (int e = load_module(nullptr, &m)) return e;
-    const DecVariant var = dec_variant(n_tok, n_heads / n_kv);
-    GiDecodeArgs a{};
-    plan(max_span, n_tok, n_heads, n_kv, &a.chunk, &a.nsplit);
-    size_t need = a.nsplit == 1 ? 0 : (size_t)n_tok * n_heads * a.nsplit * kDecPart * sizeof(float);
-    if (need && (!workspace || workspace_bytes < need))
-        return fail("workspace of %zu bytes too small: %zu needed", workspace_bytes, need);
-    if (need && !aligned16(workspace)) return fail("the workspace must be 16-byte aligned");
-    a.q = q;
-    a.kc = kc;
-    a.vc = vc;
-    a.part = (float*)workspace;
-    a.out = out;
-    a.posp = posp;
-    a.q_stride = q_stride;
-    a.kv_stride = kv_stride;
-    a.out_stride = out_stride;
-    a.kv_head_stride = kv_head_stride;
-    a.pos0 = pos0;
-    a.n_tok = n_tok;
-    a.n_heads = n_heads;
-    a.n_kv = n_kv;
-    a.qscale = scale * kLog2e;
-    hipStream_t st = (hipStream_t)stream;
-    if (int e = launch(kDecodePartial, m->dec[var.shared][var.ncb - 1], dim3(a.nsplit, n_kv, var.groups), dim3(256), st,
-                       &a, sizeof a))
-        return e;
-    if (a.nsplit > 1)
-        if (int e = launch(kDecodeCombine, m->combine, dim3(n_heads, n_tok, kCombineSplit), dim3(64), st, &a, sizeof a)) return e;
-    return 0;
+    return decode_impl(stream, q, q_stride, kc, vc, nullptr, nullptr, 0, 0, false, kv_stride, kv_head_stride, out,
+                       out_stride, workspace, workspace_bytes, pos0, posp, ctx_cap, n_tok, n_heads, n_kv, hd, scale);
+}
+
+int gi_attn_decode_i8(void* stream, const float* q, long long q_stride, const int8_t* kc, const int8_t* vc,
+                      const float* ks, const float* vs, long long kv_stride, long long kv_head_stride,
+                      long long sc_stride, long long sc_head_stride, float* out, long long out_stride, void* workspace,
+                      size_t workspace_bytes, int pos0, const int* posp, int ctx_cap, int n_tok, int n_heads, int n_kv,
+                      int hd, float scale) {
+    if (sc_stride == 0 && sc_head_stride == 0) sc_stride = n_kv, sc_head_stride = 1;
+    return decode_impl(stream, q, q_stride, kc, vc, ks, vs, sc_stride, sc_head_stride, true, kv_stride, kv_head_stride,
+                       out, out_stride, workspace, workspace_bytes, pos0, posp, ctx_cap, n_tok, n_heads, n_kv, hd, scale);
 }
 
 int gi_attn_prefill(void* stream, const void* q, int q_dtype, long long q_stride, const uint16_t* kc,
@@ -454,40 +552,17 @@ int gi_kernel_timing_read(const char* kernel, double* total_ms, int* launches) {
 int gi_qk_norm_rope(void* stream, float* qkv, const float* qn, const float* kn, uint16_t* kc, uint16_t* vc,
                     long long kv_stride, long long kv_head_stride, int pos0, const int* posp, int n, int n_heads,
                     int n_kv, int hd, int rope_dim, float base, const float* ff, int neox, float eps) {
-    if (hd != 64 && hd != 128 && hd != 256) return fail("head size %d unsupported by the KV store (64, 128, 256)", hd);
-    if (n_kv <= 0 || n_heads <= 0 || n_heads % n_kv != 0)
-        return fail("n_heads %d must be a positive multiple of n_kv %d", n_heads, n_kv);
-    if (n <= 0) return fail("n %d must be positive", n);
-    if (rope_dim < 0 || rope_dim > hd || rope_dim % 2) return fail("rope_dim %d must be even and at most %d", rope_dim, hd);
-    if (!qkv || !kc || !vc) return fail("null tensor pointer");
-    if ((qn == nullptr) != (kn == nullptr)) return fail("qn and kn must both be given or both be null");
-    if (!posp && pos0 < 0) return fail("pos0 %d must be >= 0", pos0);
-    if (kv_head_stride == 0) kv_head_stride = hd;
-    if (int e = check_kv_strides(kv_stride, kv_head_stride, n_kv, hd)) return e;
-    Module* m;
-    if (int e = load_module(nullptr, &m)) return e;
-    GiRopeArgs a{};
-    a.qkv = qkv;
-    a.qn = qn;
-    a.kn = kn;
-    a.kc = kc;
-    a.vc = vc;
-    a.ff = ff;
-    a.posp = posp;
-    a.row_stride = (long long)(n_heads + 2 * n_kv) * hd;
-    a.kv_stride = kv_stride;
-    a.kv_head_stride = kv_head_stride;
-    a.pos0 = pos0;
-    a.n = n;
-    a.n_heads = n_heads;
-    a.n_kv = n_kv;
-    a.hd = hd;
-    a.rope_dim = rope_dim;
-    a.base = base;
-    a.eps = eps;
-    a.neox = neox != 0;
-    const int groups = (n_heads + 2 * n_kv + kRopeHeads - 1) / kRopeHeads; // workgroups per token
-    return launch(kRope, m->rope, dim3(groups, n, 1), dim3(256), (hipStream_t)stream, &a, sizeof a);
+    return rope_impl(stream, qkv, qn, kn, kc, vc, nullptr, nullptr, 0, 0, false, kv_stride, kv_head_stride, pos0, posp, n,
+                     n_heads, n_kv, hd, rope_dim, base, ff, neox, eps);
+}
+
+int gi_qk_norm_rope_i8(void* stream, float* qkv, const float* qn, const float* kn, int8_t* kc, int8_t* vc, float* ks,
+                       float* vs, long long kv_stride, long long kv_head_stride, long long sc_stride,
+                       long long sc_head_stride, int pos0, const int* posp, int n, int n_heads, int n_kv, int hd,
+                       int rope_dim, float base, const float* ff, int neox, float eps) {
+    if (sc_stride == 0 && sc_head_stride == 0) sc_stride = n_kv, sc_head_stride = 1;
+    return rope_impl(stream, qkv, qn, kn, kc, vc, ks, vs, sc_stride, sc_head_stride, true, kv_stride, kv_head_stride,
+                     pos0, posp, n, n_heads, n_kv, hd, rope_dim, base, ff, neox, eps);
 }
 
 } // extern "C"

@@ -59,6 +59,12 @@ struct GiDecodeArgs {
     int nsplit;            // slices per token (the grid's x)
     float qscale;          // scale * log2(e)
     int pad_;
+    // int8 cache only (the kernels named *_i8): kc / vc hold int8 rows in the same element layout, and the
+    // f32 scale of position t, kv head h is at ks / vs [t*sc_stride + h*sc_head_stride]
+    const float* ks;
+    const float* vs;
+    long long sc_stride;
+    long long sc_head_stride;
 };
 
 #define DEC_WAVES 4
@@ -72,6 +78,9 @@ struct GiDecodeArgs {
 #define DEC_PAIRS 8 // (token, head) pairs per column block of 16 columns
 #define DEC_RESCALE_LOG2 8.0f
 #define DEC_PART 132 // floats per slice partial: O (128), max (base 2), sum, 2 pad (16-byte rows)
+// int8 cache: the probability's f16 remainder column is scaled by 2^12 (undone when the columns merge).
+// Times a value scale of ~0.03 the remainder would otherwise fall into f16's subnormal range.
+#define DEC_I8_LO 4096.f
 #define GI_RSRC_FLAGS 0x00020000
 
 __device__ __forceinline__ float wave_xor(float v, int m) { return __shfl_xor(v, m, 64); }
@@ -102,15 +111,54 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t gi_rsrc(const void* p, long lo
 __device__ __forceinline__ u4 gi_load16(__amdgpu_buffer_rsrc_t r, int off) {
     return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
 }
+typedef uint32_t u2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ u2 gi_load8(__amdgpu_buffer_rsrc_t r, int off) {
+    return __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
+}
+__device__ __forceinline__ float gi_load4f(__amdgpu_buffer_rsrc_t r, int off) {
+    return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
+}
+
+// int8 -> f16, exactly. With its sign bit flipped a byte is u = v + 128 in 0..255; the f16 with bits
+// 0x6400 | u is 1024 + u, so subtracting 1152 leaves v. x holds 4 bytes already flipped (x ^ 0x80808080);
+// v_perm picks bytes of {0x64646464 : x} (selector bytes 0-3 take x, 4-7 the constant).
+typedef _Float16 h2x __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t i8_f16x2(uint32_t x, uint32_t sel) {
+    const h2x v = __builtin_bit_cast(h2x, __builtin_amdgcn_perm(0x64646464u, x, sel)) -
+                  h2x{(_Float16)1152.f, (_Float16)1152.f};
+    return __builtin_bit_cast(uint32_t, v);
+}
+#define GI_I8_LO 0x04010400u // bytes 0, 1 of x -> f16 pair
+#define GI_I8_HI 0x04030402u // bytes 2, 3
+// v of lane 16*(l/16) + m: the lane's 16-lane row broadcasts its m-th lane (DPP row_newbcast)
+template <int M>
+__device__ __forceinline__ float row_bcast(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x150 + M, 0xF, 0xF, false));
+}
+
+// Register buffers of one wave's tile. f16: 32 keys; K as the S^T A operand (2 blocks of 16 keys, 4 k-steps
+// of 32 dims), V as 8 keys x 8 dims. int8: 64 keys in the same registers; K 4 blocks x 32 bytes, V 16 keys x
+// 8 dims, plus the scale of key `lane` of the tile.
+template <bool I8> struct DecBuf { u4 k[2][4]; u4 v[8]; };
+template <> struct DecBuf<true> { u4 k[4][2]; u2 v[16]; float ksc, vsc; };
 
 // Lane l of a wave: c = l % 16 (MFMA column / A-row), grp = l / 16 (k-group of 8).
+// I8 = true: an int8 cache (kv_store's KV8 format, src/cuda.rs:333-339: a row of int8 values and one f32
+// scale per (position, kv head)). Scores are attention_partial_gqa's (src/cuda.rs:1750-1760): the dot
+// product with the integer key, times the key's scale; the value scale rides on the probability
+// (src/cuda.rs:1812-1822) and the exp-sum is of the unscaled probabilities. Bytes are widened to exact f16
+// in registers and both products stay on the f16 MFMA. Tiles are 64 keys (the same register bytes as 32
+// f16 keys); lane (c, grp) holds the S^T rows of keys 16grp + 4b + j (block b, row 4grp + j, so A-row c of
+// block b loads key 16(c/4) + c%4 + 4b) and feeds PV with V rows 16grp..16grp+15 (k-step ks: 8ks..8ks+7),
+// dims 8c..8c+7. Each key's scale is loaded by lane key%64 and broadcast across its 16-lane row.
 // SHARE = false: the 4 waves split the slice's tiles and serve the same DEC_PAIRS*NCB (token, head)
 // pairs, merging through LDS at the end. SHARE = true (many pairs per kv head, as in a verify block):
 // every wave walks the whole slice for its own DEC_PAIRS*NCB pairs, so one workgroup serves 4 times as
 // many pairs and the slice's K/V comes from HBM once (the waves' repeated loads of the same lines are
 // served by the caches).
-template <int NCB, bool SHARE>
+template <int NCB, bool SHARE, bool I8>
 __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
+    constexpr int TILE = I8 ? 2 * DEC_TILE : DEC_TILE; // keys per wave tile
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int c = lane & 15, grp = lane >> 4;
@@ -140,7 +188,7 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
         valid[cb] = pi < npairs;
         int t = valid[cb] ? pi / G : 0, g = valid[cb] ? pi % G : 0;
         span[cb] = valid[cb] ? min(pos0 + t + 1 - k_begin, nkeys) : 0; // keys of the slice this column sees
-        qoff[cb] = ((int)(t * a.q_stride) + (kvh * G + g) * 128 + 8 * grp) * 4;
+        qoff[cb] = ((int)(t * a.q_stride) + (kvh * G + g) * 128 + (I8 ? 16 : 8) * grp) * 4;
     }
     // smallest span among the wave's valid columns (the lowest token's: column 0 of block 0 is always valid):
     // tiles below it need no masking
@@ -148,15 +196,18 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
     // Q rows (f32, 8 dims per lane per k-step), issued before the first K/V tiles so that waiting for them
     // leaves the K/V loads in flight
     u4 qraw[NCB][4][2];
-    h8 qf[NCB][4]; // B operand of S^T = K Qc^T: k-step kk covers dims 32kk..32kk+31, this lane dims 32kk+8grp..+7
+    // B operand of S^T = K Qc^T. f16: k-step kk covers dims 32kk..32kk+31, this lane dims 32kk+8grp..+7.
+    // int8: this lane dims 16grp + 8(kk%2) + 64(kk/2) .. +7 (the bytes its two 16-byte key loads bring)
+    h8 qf[NCB][4];
     {
         __amdgpu_buffer_rsrc_t rq = gi_rsrc(a.q, (long long)a.n_tok * a.q_stride * 4);
 #pragma unroll
         for (int cb = 0; cb < NCB; cb++)
 #pragma unroll
             for (int kk = 0; kk < 4; kk++) {
-                qraw[cb][kk][0] = gi_load16(rq, qoff[cb] + 128 * kk);
-                qraw[cb][kk][1] = gi_load16(rq, qoff[cb] + 128 * kk + 16);
+                const int off = qoff[cb] + (I8 ? 32 * (kk & 1) + 256 * (kk >> 1) : 128 * kk);
+                qraw[cb][kk][0] = gi_load16(rq, off);
+                qraw[cb][kk][1] = gi_load16(rq, off + 16);
             }
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -185,24 +236,50 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
     const int koff1 = koff0 + 4 * (int)kvs * 2;
     const int voff = (8 * grp * (int)kvs + 8 * c) * 2;
     const int vstep = (int)kvs * 2;
-    constexpr int STRIDE = SHARE ? DEC_TILE : DEC_WAVES * DEC_TILE; // keys between a wave's consecutive tiles
+    constexpr int STRIDE = SHARE ? TILE : DEC_WAVES * TILE; // keys between a wave's consecutive tiles
+    // int8 element offsets (bytes): key rows of block 0 and the V rows of this lane; scales
+    const int8_t* kslice8 = reinterpret_cast<const int8_t*>(a.kc) + (long long)k_begin * kvs + kvh * a.kv_head_stride;
+    const int8_t* vslice8 = reinterpret_cast<const int8_t*>(a.vc) + (long long)k_begin * kvs + kvh * a.kv_head_stride;
+    const long long scs = a.sc_stride;
+    const float* kscl = I8 ? a.ks + (long long)k_begin * scs + kvh * a.sc_head_stride : nullptr;
+    const float* vscl = I8 ? a.vs + (long long)k_begin * scs + kvh * a.sc_head_stride : nullptr;
+    const int koff8 = (16 * (c >> 2) + (c & 3)) * (int)kvs + 16 * grp;
+    const int voff8 = 16 * grp * (int)kvs + 8 * c;
+    const int scoff = lane * (int)scs * 4;
 
-    struct Buf { u4 k[2][4]; u4 v[8]; };
+    using Buf = DecBuf<I8>;
     auto load_k = [&](Buf& B, int t) {
-        __amdgpu_buffer_rsrc_t r = gi_rsrc(kslice + (long long)t * kvs, (long long)(nkeys - t) * kvs * 2);
+        if constexpr (I8) {
+            __amdgpu_buffer_rsrc_t r = gi_rsrc(kslice8 + (long long)t * kvs, (long long)(nkeys - t) * kvs);
 #pragma unroll
-        for (int kk = 0; kk < 4; kk++) {
-            B.k[0][kk] = gi_load16(r, koff0 + 64 * kk);
-            B.k[1][kk] = gi_load16(r, koff1 + 64 * kk);
+            for (int b = 0; b < 4; b++) {
+                B.k[b][0] = gi_load16(r, koff8 + 4 * b * (int)kvs);
+                B.k[b][1] = gi_load16(r, koff8 + 4 * b * (int)kvs + 64);
+            }
+            B.ksc = gi_load4f(gi_rsrc(kscl + (long long)t * scs, (long long)(nkeys - t) * scs * 4), scoff);
+        } else {
+            __amdgpu_buffer_rsrc_t r = gi_rsrc(kslice + (long long)t * kvs, (long long)(nkeys - t) * kvs * 2);
+#pragma unroll
+            for (int kk = 0; kk < 4; kk++) {
+                B.k[0][kk] = gi_load16(r, koff0 + 64 * kk);
+                B.k[1][kk] = gi_load16(r, koff1 + 64 * kk);
+            }
         }
     };
     auto load_v = [&](Buf& B, int t) {
-        __amdgpu_buffer_rsrc_t r = gi_rsrc(vslice + (long long)t * kvs, (long long)(nkeys - t) * kvs * 2);
+        if constexpr (I8) {
+            __amdgpu_buffer_rsrc_t r = gi_rsrc(vslice8 + (long long)t * kvs, (long long)(nkeys - t) * kvs);
 #pragma unroll
-        for (int i = 0; i < 8; i++) B.v[i] = gi_load16(r, voff + i * vstep);
+            for (int i = 0; i < 16; i++) B.v[i] = gi_load8(r, voff8 + i * (int)kvs);
+            B.vsc = gi_load4f(gi_rsrc(vscl + (long long)t * scs, (long long)(nkeys - t) * scs * 4), scoff);
+        } else {
+            __amdgpu_buffer_rsrc_t r = gi_rsrc(vslice + (long long)t * kvs, (long long)(nkeys - t) * kvs * 2);
+#pragma unroll
+            for (int i = 0; i < 8; i++) B.v[i] = gi_load16(r, voff + i * vstep);
+        }
     };
     // One tile from buffer B at key offset t; with `reload`, B is refilled with the tile DEC_NB tiles on.
-    auto process = [&](Buf& B, int t, bool reload) {
+    auto process_h = [&](auto& B, int t, bool reload) {
         __builtin_amdgcn_sched_barrier(0); // keep tiles in order: each waits only for its own buffer
         f4 sacc[NCB][2];
 #pragma unroll
@@ -276,13 +353,111 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
         __builtin_amdgcn_sched_barrier(0);
         if (reload) load_v(B, t + DEC_NB * STRIDE);
     };
+    auto process_i8 = [&](auto& B, int t, bool reload) {
+        __builtin_amdgcn_sched_barrier(0);
+        f4 sacc[NCB][4];
+#pragma unroll
+        for (int b = 0; b < 4; b++) {
+            u4 kf[4]; // k-step kk: dims 16grp + 8(kk%2) + 64(kk/2) of this block's key, as f16 pairs
+#pragma unroll
+            for (int half = 0; half < 2; half++)
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const uint32_t x = B.k[b][half][e] ^ 0x80808080u;
+                    kf[2 * half + (e >> 1)][2 * (e & 1)] = i8_f16x2(x, GI_I8_LO);
+                    kf[2 * half + (e >> 1)][2 * (e & 1) + 1] = i8_f16x2(x, GI_I8_HI);
+                }
+#pragma unroll
+            for (int cb = 0; cb < NCB; cb++) {
+                sacc[cb][b] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int kk = 0; kk < 4; kk++)
+                    sacc[cb][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, kf[kk]), qf[cb][kk],
+                                                                         sacc[cb][b], 0, 0, 0);
+            }
+        }
+        const float ksc = B.ksc;
+        if (reload) load_k(B, t + DEC_NB * STRIDE);
+        __builtin_amdgcn_sched_barrier(0);
+        // the scales of this lane's 16 keys (16grp + m, m = 4b + j)
+        float ksb[16], vsb[16];
+#define GI_BC(m) ksb[m] = row_bcast<m>(ksc); vsb[m] = row_bcast<m>(B.vsc);
+        GI_BC(0) GI_BC(1) GI_BC(2) GI_BC(3) GI_BC(4) GI_BC(5) GI_BC(6) GI_BC(7)
+        GI_BC(8) GI_BC(9) GI_BC(10) GI_BC(11) GI_BC(12) GI_BC(13) GI_BC(14) GI_BC(15)
+#undef GI_BC
+        const bool masked = t + TILE > span_lo;
+        h8 pf[NCB][2]; // PV k-step ks: keys 16grp + 8ks + i
+#pragma unroll
+        for (int cb = 0; cb < NCB; cb++) {
+            float sc[16], mx = GI_NEG_INF;
+#pragma unroll
+            for (int m = 0; m < 16; m++) {
+                float v = sacc[cb][m >> 2][m & 3];
+                v = (v + lane_xor1(v)) * ksb[m]; // hi + lo columns, then the key's scale
+                if (masked) v = t + 16 * grp + m < span[cb] ? v : GI_NEG_INF;
+                sc[m] = v;
+                mx = fmaxf(mx, v);
+            }
+            mx = rows_max(mx);
+            const bool up = mx > m_run[cb] + DEC_RESCALE_LOG2;
+            if (__builtin_amdgcn_ballot_w64(up)) {
+                const float m_new = up ? mx : m_run[cb];
+                const float alpha = __builtin_amdgcn_exp2f(m_run[cb] - m_new);
+                m_run[cb] = m_new;
+                l_run[cb] *= alpha;
+#pragma unroll
+                for (int dd = 0; dd < 8; dd++) o[cb][dd] *= alpha;
+            }
+            const float m_use = m_run[cb] == GI_NEG_INF ? 0.f : m_run[cb];
+            float psum = 0.f;
+#pragma unroll
+            for (int m = 0; m < 16; m++) {
+                const float p = __builtin_amdgcn_exp2f(sc[m] - m_use);
+                psum += p;
+                const float pv = p * vsb[m];
+                _Float16 hi = (_Float16)pv;
+                pf[cb][m >> 3][m & 7] = (c & 1) ? (_Float16)((pv - (float)hi) * DEC_I8_LO) : hi;
+            }
+            l_run[cb] += psum;
+        }
+        // O^T += V^T P^T: for dims dd, dd+1 (bytes k, k+1 of word dd/4) and keys 2p, 2p+1 of a k-step, one
+        // v_perm gathers the four bytes and two more widen them to the two f16 pairs
+#pragma unroll
+        for (int i = 0; i < 16; i++) B.v[i] ^= u2{0x80808080u, 0x80808080u};
+#pragma unroll
+        for (int dd = 0; dd < 8; dd += 2) {
+            const int wi = dd >> 2, k = dd & 3;
+            const uint32_t sel = (uint32_t)k | (uint32_t)(k + 4) << 8 | (uint32_t)(k + 1) << 16 | (uint32_t)(k + 5) << 24;
+#pragma unroll
+            for (int ks = 0; ks < 2; ks++) {
+                u4 w0, w1;
+#pragma unroll
+                for (int p = 0; p < 4; p++) {
+                    const uint32_t g = __builtin_amdgcn_perm(B.v[8 * ks + 2 * p + 1][wi], B.v[8 * ks + 2 * p][wi], sel);
+                    w0[p] = i8_f16x2(g, GI_I8_LO);
+                    w1[p] = i8_f16x2(g, GI_I8_HI);
+                }
+#pragma unroll
+                for (int cb = 0; cb < NCB; cb++) {
+                    o[cb][dd] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, w0), pf[cb][ks], o[cb][dd], 0, 0, 0);
+                    o[cb][dd + 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, w1), pf[cb][ks], o[cb][dd + 1], 0, 0, 0);
+                }
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        if (reload) load_v(B, t + DEC_NB * STRIDE);
+    };
+    auto process = [&](Buf& B, int t, bool reload) {
+        if constexpr (I8) process_i8(B, t, reload);
+        else process_h(B, t, reload);
+    };
 
     // (the first loads are issued unconditionally, before the loop, so every iteration starts with the same
     // loads outstanding and the compiler's load counters wait for exactly the buffer in use)
     // a SHARE wave whose pairs all lie past the last one has nothing to compute (it still joins the merge)
     if (!SHARE || pair0 < npairs) {
     Buf B[DEC_NB];
-    const int t_first = SHARE ? 0 : wave * DEC_TILE;
+    const int t_first = SHARE ? 0 : wave * TILE;
 #pragma unroll
     for (int i = 0; i < DEC_NB; i++) {
         load_k(B[i], t_first + i * STRIDE);
@@ -340,6 +515,7 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
     __syncthreads();
     GI_TS(7);
     // ---- merge the waves (SHARE: each pair has one wave) and the hi/lo columns: thread -> (pair, 4 dims)
+    constexpr float LO = I8 ? 1.f / DEC_I8_LO : 1.f;
 #pragma unroll
     for (int it = 0; it < WG_PAIRS / DEC_PAIRS; it++) {
         const int item = threadIdx.x + 256 * it;
@@ -360,10 +536,10 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
                     const float4 hi = *reinterpret_cast<const float4*>(&sm_o[w][row][d4]);
                     const float4 lo = *reinterpret_cast<const float4*>(&sm_o[w][row + 1][d4]);
                     L += wt * sm_l[w][lp];
-                    O.x += wt * (hi.x + lo.x);
-                    O.y += wt * (hi.y + lo.y);
-                    O.z += wt * (hi.z + lo.z);
-                    O.w += wt * (hi.w + lo.w);
+                    O.x += wt * (hi.x + lo.x * LO);
+                    O.y += wt * (hi.y + lo.y * LO);
+                    O.z += wt * (hi.z + lo.z * LO);
+                    O.w += wt * (hi.w + lo.w * LO);
                 }
             }
             const int tk = pi / G, h = kvh * G + pi % G;
@@ -393,10 +569,16 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
 #endif
 }
 
-extern "C" __global__ void __launch_bounds__(256, DEC_MINWG) gi_decode_partial_1(GiDecodeArgs a) { gi_decode_partial_t<1, false>(a); }
-extern "C" __global__ void __launch_bounds__(256, DEC_MINWG) gi_decode_partial_2(GiDecodeArgs a) { gi_decode_partial_t<2, false>(a); }
-extern "C" __global__ void __launch_bounds__(256, DEC_MINWG) gi_decode_shared_1(GiDecodeArgs a) { gi_decode_partial_t<1, true>(a); }
-extern "C" __global__ void __launch_bounds__(256, DEC_MINWG) gi_decode_shared_2(GiDecodeArgs a) { gi_decode_partial_t<2, true>(a); }
+#define GI_DEC_KERNEL(name, NCB, SHARE, I8) \
+    extern "C" __global__ void __launch_bounds__(256, DEC_MINWG) name(GiDecodeArgs a) { gi_decode_partial_t<NCB, SHARE, I8>(a); }
+GI_DEC_KERNEL(gi_decode_partial_1, 1, false, false)
+GI_DEC_KERNEL(gi_decode_partial_2, 2, false, false)
+GI_DEC_KERNEL(gi_decode_shared_1, 1, true, false)
+GI_DEC_KERNEL(gi_decode_shared_2, 2, true, false)
+GI_DEC_KERNEL(gi_decode_partial_1_i8, 1, false, true)
+GI_DEC_KERNEL(gi_decode_partial_2_i8, 2, false, true)
+GI_DEC_KERNEL(gi_decode_shared_1_i8, 1, true, true)
+GI_DEC_KERNEL(gi_decode_shared_2_i8, 2, true, true)
 
 // Merge the slices of each (token, head): M = max m_s, w_s = 2^(m_s - M), out = sum w_s O_s / sum w_s l_s
 // (attention_combine's maths in base 2; empty slices carry m = -inf and weigh nothing). One wave per
@@ -839,7 +1021,11 @@ struct GiRopeArgs {
     float base;
     float eps;
     int neox;              // pairs (i, i + rope_dim/2); otherwise (2i, 2i+1)
-    int pad_;
+    int i8;                // the caches are int8 (kc / vc as bytes, same element offsets) with scales:
+    float* ks;             // f32 scale of position t, kv head h at t*sc_stride + h*sc_head_stride
+    float* vs;
+    long long sc_stride;
+    long long sc_head_stride;
 };
 
 // Reference semantics: qk_norm_rope (src/cuda.rs:437-486) with an f16 cache (kv_store, src/cuda.rs:312-362).
@@ -851,11 +1037,34 @@ struct GiRopeArgs {
 // workgroup computes them once into LDS for all its heads; each wave loads its ROPE_HEADS/4 heads at once
 // and takes them one at a time through a per-wave LDS row (any two dims can pair).
 #define ROPE_HEADS 16
+// One head row (PER values per lane) into a cache row. f16: rounded to nearest even. int8 (kv_store's KV8,
+// src/cuda.rs:333-339): dd = max|x| / 127, each value rint(x * (1/dd)) (0 when dd is 0), dd to the scale.
+template <int PER>
+__device__ __forceinline__ void gi_store_row(const GiRopeArgs& a, uint16_t* cache, float* scale, int pos, int kh,
+                                             const float __attribute__((ext_vector_type(PER))) x, int lane) {
+    const long long off = (long long)pos * a.kv_stride + (long long)kh * a.kv_head_stride;
+    if (!a.i8) {
+        typedef _Float16 hv __attribute__((ext_vector_type(PER)));
+        *reinterpret_cast<hv*>(cache + off + PER * lane) = __builtin_convertvector(x, hv);
+        return;
+    }
+    float amax = 0.f;
+#pragma unroll
+    for (int j = 0; j < PER; j++) amax = fmaxf(amax, fabsf(x[j]));
+    for (int m = 32; m > 0; m >>= 1) amax = fmaxf(amax, __shfl_xor(amax, m, 64));
+    const float dd = __fdiv_rn(amax, 127.f), inv = dd != 0.f ? __fdiv_rn(1.f, dd) : 0.f;
+    typedef int8_t bv __attribute__((ext_vector_type(PER)));
+    bv q;
+#pragma unroll
+    for (int j = 0; j < PER; j++) q[j] = (int8_t)__float2int_rn(x[j] * inv);
+    *reinterpret_cast<bv*>(reinterpret_cast<int8_t*>(cache) + off + PER * lane) = q;
+    if (lane == 0) scale[(long long)pos * a.sc_stride + (long long)kh * a.sc_head_stride] = dd;
+}
+
 // PER = hd / 64 values per lane, dims PER*lane .. PER*lane + PER - 1 (one 4, 8 or 16-byte access per row)
 template <int PER>
 __device__ __forceinline__ void gi_qk_norm_rope_t(const GiRopeArgs& a, float (*cs_sh)[2], float (*row_sh)[256]) {
     typedef float fv __attribute__((ext_vector_type(PER)));
-    typedef _Float16 hv __attribute__((ext_vector_type(PER)));
     constexpr int HD = 64 * PER;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int items = a.n_heads + 2 * a.n_kv;
@@ -886,9 +1095,7 @@ __device__ __forceinline__ void gi_qk_norm_rope_t(const GiRopeArgs& a, float (*c
         const int h = h0 + wave + 4 * k;
         if (h >= items) break;
         if (h >= a.n_heads + a.n_kv) { // a v head: into the cache
-            const int vh = h - a.n_heads - a.n_kv;
-            uint16_t* dst = a.vc + (long long)pos * a.kv_stride + (long long)vh * a.kv_head_stride;
-            *reinterpret_cast<hv*>(dst + PER * lane) = __builtin_convertvector(v[k], hv);
+            gi_store_row<PER>(a, a.vc, a.vs, pos, h - a.n_heads - a.n_kv, v[k], lane);
             continue;
         }
         fv x = v[k];
@@ -914,11 +1121,7 @@ __device__ __forceinline__ void gi_qk_norm_rope_t(const GiRopeArgs& a, float (*c
         __builtin_amdgcn_wave_barrier();
         x = *reinterpret_cast<const fv*>(sh + PER * lane);
         *reinterpret_cast<fv*>(row + (long long)h * HD + PER * lane) = x;
-        if (h >= a.n_heads) {
-            const int kh = h - a.n_heads;
-            uint16_t* dst = a.kc + (long long)pos * a.kv_stride + (long long)kh * a.kv_head_stride;
-            *reinterpret_cast<hv*>(dst + PER * lane) = __builtin_convertvector(x, hv);
-        }
+        if (h >= a.n_heads) gi_store_row<PER>(a, a.kc, a.ks, pos, h - a.n_heads, x, lane);
         __builtin_amdgcn_wave_barrier(); // the row buffer is reused by the wave's next head
     }
 }

@@ -32,9 +32,11 @@ SYMBOLS = (
     "gi_attn_decode_plan",
     "gi_attn_decode_workspace_bytes",
     "gi_attn_decode",
+    "gi_attn_decode_i8",
     "gi_attn_prefill",
     "gi_attention",
     "gi_qk_norm_rope",
+    "gi_qk_norm_rope_i8",
     "gi_kernel_timing",
     "gi_kernel_timing_read",
 )
@@ -66,12 +68,18 @@ def load_library(path=LIB_PATH):
     lib.gi_attn_decode_workspace_bytes.restype = sz
     lib.gi_attn_decode.argtypes = [vp, vp, ll, vp, vp, ll, ll, vp, ll, vp, sz, i, vp, i, i, i, i, i, f]
     lib.gi_attn_decode.restype = i
+    lib.gi_attn_decode_i8.argtypes = [vp, vp, ll, vp, vp, vp, vp, ll, ll, ll, ll, vp, ll, vp, sz, i, vp, i, i, i, i, i,
+                                      f]
+    lib.gi_attn_decode_i8.restype = i
     lib.gi_attn_prefill.argtypes = [vp, vp, i, ll, vp, vp, ll, ll, vp, i, ll, i, i, i, i, i, f]
     lib.gi_attn_prefill.restype = i
     lib.gi_attention.argtypes = [vp, vp, vp, vp, vp, vp, sz, i, vp, i, i, i, i, i, i]
     lib.gi_attention.restype = i
     lib.gi_qk_norm_rope.argtypes = [vp, vp, vp, vp, vp, vp, ll, ll, i, vp, i, i, i, i, i, f, vp, i, f]
     lib.gi_qk_norm_rope.restype = i
+    lib.gi_qk_norm_rope_i8.argtypes = [vp, vp, vp, vp, vp, vp, vp, vp, ll, ll, ll, ll, i, vp, i, i, i, i, i, f, vp, i,
+                                       f]
+    lib.gi_qk_norm_rope_i8.restype = i
     lib.gi_kernel_timing.argtypes = [i]
     lib.gi_kernel_timing.restype = i
     lib.gi_kernel_timing_read.argtypes = [ctypes.c_char_p, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(i)]
@@ -102,13 +110,16 @@ def _need(t, name, dtype):
         raise GiAttnError(f"{name} rows must be contiguous")
 
 
-def _cache_layout(kc, vc, n_kv, hd, layout):
+def _cache_layout(kc, vc, n_kv, hd, layout, dtypes=(torch.float16,)):
     """(kv_stride, kv_head_stride, capacity) of a cache pair.
 
     layout "reference": [capacity, n_kv, hd] (or [capacity, n_kv*hd]), as the reference keeps it
-    (src/cuda.rs:365-369); "head_major": [n_kv, capacity, hd], each kv head's rows contiguous."""
+    (src/cuda.rs:365-369); "head_major": [n_kv, capacity, hd], each kv head's rows contiguous. The caches
+    are f16, or int8 where dtypes allows it (with f32 scales, see _scale_layout)."""
+    if kc.dtype not in dtypes:
+        raise GiAttnError(f"k_cache must be one of {dtypes}, got {kc.dtype}")
     for t, name in ((kc, "k_cache"), (vc, "v_cache")):
-        _need(t, name, torch.float16)
+        _need(t, name, kc.dtype)
         if not t.is_contiguous():
             raise GiAttnError(f"{name} must be contiguous")
     if kc.shape != vc.shape:
@@ -122,6 +133,21 @@ def _cache_layout(kc, vc, n_kv, hd, layout):
             raise GiAttnError(f"head-major cache must be [{n_kv}, capacity, {hd}], got {tuple(kc.shape)}")
         return hd, kc.shape[1] * hd, kc.shape[1]
     raise GiAttnError(f"unknown cache layout {layout!r}")
+
+
+def _scale_layout(ks, vs, n_kv, capacity, layout):
+    """(sc_stride, sc_head_stride) of an int8 cache's f32 scales: [capacity, n_kv] with the reference layout
+    (kv_store's KV_SROWP, src/cuda.rs:365-369), [n_kv, capacity] with the head-major one."""
+    for t, name in ((ks, "k_scale"), (vs, "v_scale")):
+        if t is None:
+            raise GiAttnError(f"an int8 cache needs {name}")
+        _need(t, name, torch.float32)
+        if not t.is_contiguous():
+            raise GiAttnError(f"{name} must be contiguous")
+    want = (capacity, n_kv) if layout == "reference" else (n_kv, capacity)
+    if tuple(ks.shape) != want or tuple(vs.shape) != want:
+        raise GiAttnError(f"scales must be {list(want)}, got {tuple(ks.shape)} and {tuple(vs.shape)}")
+    return (n_kv, 1) if layout == "reference" else (1, capacity)
 
 
 def init(code_object_path=None):
@@ -150,15 +176,20 @@ def new_workspace(ctx_cap, n_tok, n_heads, n_kv, hd=128, device="cuda"):
 
 
 def decode(q, k_cache, v_cache, pos0, n_heads, n_kv, hd=128, scale=None, out=None, workspace=None, posp=None,
-           ctx_cap=0, kv_layout="reference"):
+           ctx_cap=0, kv_layout="reference", k_scale=None, v_scale=None):
     """Decode/verify attention of n_tok = q.shape[0] tokens at positions pos0.. (causal within the block).
 
-    q: f32 [n_tok, >= n_heads*hd] (row stride q.stride(0)); caches f16 in kv_layout (see _cache_layout);
-    returns f32 [n_tok, n_heads*hd]. posp: an int32 CUDA tensor holding the position (graph replay), with
-    ctx_cap the largest span the launch shape must cover.
+    q: f32 [n_tok, >= n_heads*hd] (row stride q.stride(0)); caches f16, or int8 with f32 k_scale / v_scale
+    (the reference's KV8 cache), in kv_layout (see _cache_layout, _scale_layout); returns f32
+    [n_tok, n_heads*hd]. posp: an int32 CUDA tensor holding the position (graph replay), with ctx_cap the
+    largest span the launch shape must cover.
     """
     _need(q, "q", torch.float32)
-    kv_stride, kv_head_stride, capacity = _cache_layout(k_cache, v_cache, n_kv, hd, kv_layout)
+    kv_stride, kv_head_stride, capacity = _cache_layout(k_cache, v_cache, n_kv, hd, kv_layout,
+                                                        (torch.float16, torch.int8))
+    i8 = k_cache.dtype == torch.int8
+    if i8:
+        sc_stride, sc_head_stride = _scale_layout(k_scale, v_scale, n_kv, capacity, kv_layout)
     n_tok = q.shape[0]
     if scale is None:
         scale = 1.0 / math.sqrt(hd)
@@ -173,10 +204,15 @@ def decode(q, k_cache, v_cache, pos0, n_heads, n_kv, hd=128, scale=None, out=Non
     if workspace is None:
         workspace = new_workspace(need_rows, n_tok, n_heads, n_kv, hd, q.device)
     lib = load_library()
-    _check(lib.gi_attn_decode(_stream(), _ptr(q), q.stride(0), _ptr(k_cache), _ptr(v_cache), kv_stride,
-                              kv_head_stride, _ptr(out),
-                              out.stride(0), _ptr(workspace), workspace.numel() * workspace.element_size(), pos0,
-                              _ptr(posp), ctx_cap, n_tok, n_heads, n_kv, hd, scale))
+    ws = (_ptr(workspace), workspace.numel() * workspace.element_size())
+    if i8:
+        _check(lib.gi_attn_decode_i8(_stream(), _ptr(q), q.stride(0), _ptr(k_cache), _ptr(v_cache), _ptr(k_scale),
+                                     _ptr(v_scale), kv_stride, kv_head_stride, sc_stride, sc_head_stride, _ptr(out),
+                                     out.stride(0), *ws, pos0, _ptr(posp), ctx_cap, n_tok, n_heads, n_kv, hd, scale))
+    else:
+        _check(lib.gi_attn_decode(_stream(), _ptr(q), q.stride(0), _ptr(k_cache), _ptr(v_cache), kv_stride,
+                                  kv_head_stride, _ptr(out), out.stride(0), *ws, pos0, _ptr(posp), ctx_cap, n_tok,
+                                  n_heads, n_kv, hd, scale))
     return out
 
 
@@ -242,13 +278,15 @@ def attention(qkv, k_cache, v_cache, pos0, n_heads, n_kv, hd=128, exact=False, o
 
 
 def qk_norm_rope(qkv, k_cache, v_cache, pos0, n_heads, n_kv, hd=128, rope_dim=None, base=10000.0, qn=None, kn=None,
-                 ff=None, neox=True, eps=1e-6, posp=None, kv_layout="reference"):
+                 ff=None, neox=True, eps=1e-6, posp=None, kv_layout="reference", k_scale=None, v_scale=None):
     """RMSNorm + RoPE of the q and k heads of f32 rows [q | k | v] (in place) and the k and v heads into the
-    f16 caches at positions pos0.. (layer_attn's qk_norm_rope step, src/cuda.rs:437-486)."""
+    caches at positions pos0.. (layer_attn's qk_norm_rope step, src/cuda.rs:437-486): f16 caches, or int8
+    ones quantised per row into k_scale / v_scale (kv_store with KV8, src/cuda.rs:333-339)."""
     _need(qkv, "qkv", torch.float32)
     if not qkv.is_contiguous() or qkv.dim() != 2 or qkv.shape[1] != (n_heads + 2 * n_kv) * hd:
         raise GiAttnError(f"qkv must be contiguous [n, {(n_heads + 2 * n_kv) * hd}]")
-    kv_stride, kv_head_stride, capacity = _cache_layout(k_cache, v_cache, n_kv, hd, kv_layout)
+    kv_stride, kv_head_stride, capacity = _cache_layout(k_cache, v_cache, n_kv, hd, kv_layout,
+                                                        (torch.float16, torch.int8))
     n = qkv.shape[0]
     if posp is None and capacity < pos0 + n:
         raise GiAttnError(f"the cache holds {capacity} positions; {pos0 + n} needed")
@@ -257,9 +295,17 @@ def qk_norm_rope(qkv, k_cache, v_cache, pos0, n_heads, n_kv, hd=128, rope_dim=No
             _need(t, name, torch.float32)
     if posp is not None:
         _need(posp, "posp", torch.int32)
-    _check(load_library().gi_qk_norm_rope(_stream(), _ptr(qkv), _ptr(qn), _ptr(kn), _ptr(k_cache), _ptr(v_cache),
-                                          kv_stride, kv_head_stride, pos0, _ptr(posp), n, n_heads, n_kv, hd,
-                                          hd if rope_dim is None else rope_dim, base, _ptr(ff), 1 if neox else 0, eps))
+    rope = (hd if rope_dim is None else rope_dim, base, _ptr(ff), 1 if neox else 0, eps)
+    if k_cache.dtype == torch.int8:
+        sc_stride, sc_head_stride = _scale_layout(k_scale, v_scale, n_kv, capacity, kv_layout)
+        _check(load_library().gi_qk_norm_rope_i8(_stream(), _ptr(qkv), _ptr(qn), _ptr(kn), _ptr(k_cache),
+                                                 _ptr(v_cache), _ptr(k_scale), _ptr(v_scale), kv_stride,
+                                                 kv_head_stride, sc_stride, sc_head_stride, pos0, _ptr(posp), n,
+                                                 n_heads, n_kv, hd, *rope))
+    else:
+        _check(load_library().gi_qk_norm_rope(_stream(), _ptr(qkv), _ptr(qn), _ptr(kn), _ptr(k_cache), _ptr(v_cache),
+                                              kv_stride, kv_head_stride, pos0, _ptr(posp), n, n_heads, n_kv, hd,
+                                              *rope))
     return qkv
 
 

@@ -71,6 +71,18 @@ int gi_attn_decode(void* stream, const float* q, long long q_stride, const uint1
                    size_t workspace_bytes, int pos0, const int* posp, int ctx_cap, int n_tok, int n_heads, int n_kv,
                    int hd, float scale);
 
+/* gi_attn_decode over an int8 KV cache: kc / vc hold int8 rows in the element layout above (kv_stride and
+ * kv_head_stride multiples of 16), and position t, kv head h has the f32 scales ks / vs [t*sc_stride +
+ * h*sc_head_stride] (value = int8 * scale); sc_stride = sc_head_stride = 0 means the reference's [position]
+ * [n_kv] (sc_stride = n_kv, sc_head_stride = 1). Scores are (q*scale) . k_int8 * ks, the exp-sum is of the
+ * unscaled probabilities and each value row is weighted by probability * vs. Replaces: attention_partial_gqa
+ * + attention_combine compiled with KV8 (src/cuda.rs:209-226, src/cuda.rs:1684-1865, src/cuda.rs:2806-2836). */
+int gi_attn_decode_i8(void* stream, const float* q, long long q_stride, const int8_t* kc, const int8_t* vc,
+                      const float* ks, const float* vs, long long kv_stride, long long kv_head_stride,
+                      long long sc_stride, long long sc_head_stride, float* out, long long out_stride, void* workspace,
+                      size_t workspace_bytes, int pos0, const int* posp, int ctx_cap, int n_tok, int n_heads, int n_kv,
+                      int hd, float scale);
+
 /* Causal prefill attention for n tokens at positions pos0..pos0+n-1 whose K/V rows are already in the
  * cache (keys 0..pos0+n-1 are read; pos0 > 0 is a chunk of a longer prompt). q: rows of q_dtype
  * (GI_F32 or GI_F16); out: rows of out_dtype. Replaces: attention_prefill_tc128 (src/cuda.rs:2408-2621),
@@ -100,6 +112,14 @@ int gi_attention(void* stream, const float* qkv, const uint16_t* kc, const uint1
 int gi_qk_norm_rope(void* stream, float* qkv, const float* qn, const float* kn, uint16_t* kc, uint16_t* vc,
                     long long kv_stride, long long kv_head_stride, int pos0, const int* posp, int n, int n_heads,
                     int n_kv, int hd, int rope_dim, float base, const float* ff, int neox, float eps);
+
+/* gi_qk_norm_rope with an int8 cache (the layouts of gi_attn_decode_i8): each k and v row is quantised as it
+ * is stored, dd = max|x| / 127, byte = round-to-nearest-even(x * (1/dd)) (0 when dd is 0), and dd goes to
+ * ks / vs. Replaces: qk_norm_rope compiled with KV8 (kv_store, src/cuda.rs:333-339). */
+int gi_qk_norm_rope_i8(void* stream, float* qkv, const float* qn, const float* kn, int8_t* kc, int8_t* vc, float* ks,
+                       float* vs, long long kv_stride, long long kv_head_stride, long long sc_stride,
+                       long long sc_head_stride, int pos0, const int* posp, int n, int n_heads, int n_kv, int hd,
+                       int rope_dim, float base, const float* ff, int neox, float eps);
 
 /* Per-kernel GPU time, for benchmarks. No counterpart in the reference. While on (process-wide), every
  * kernel the library launches outside graph capture is bracketed by a pair of HIP events on its stream.

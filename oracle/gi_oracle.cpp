@@ -16,6 +16,10 @@
 //                                     P rounded to f16, base-2 online softmax over 32-key tiles)
 //   gio_qk_norm_rope                  src/cuda.rs:437-486 with the f16 kv_store (src/cuda.rs:312-362):
 //                                     RMSNorm of q/k heads, RoPE, K/V rows into the f16 cache
+//   gio_kv_quant_i8                   src/cuda.rs:333-339 (kv_store with KV8: row max / 127, rint)
+//   gio_qk_norm_rope_i8               src/cuda.rs:437-486 storing with kv_quant_i8
+//   gio_decode_gpu_i8                 gio_decode_gpu over the KV8 cache (src/cuda.rs:209-226, 1758-1760,
+//                                     1821-1827: key scale on the score, value scale on the weight)
 //
 // How each is pinned (tests/test_oracle.py): the f16 conversion exhaustively against numpy's float16
 // and against src/quant.rs:1160-1169's known values; the attention functions against an independent
@@ -270,11 +274,19 @@ float block_sum128(const float* per_thread) {
     return v[0];
 }
 
-void decode_gpu(const float* qkv, long q_stride, const uint16_t* kc, const uint16_t* vc, long kv_stride, float* out,
-                long out_stride, int pos0, int m, int n_heads, int n_kv, float scale, int nsplit, int want, int cap,
-                int threads) {
+// A cache element as the kernels widen it: f16 bits exactly, int8 as its integer value.
+inline float kv_value(uint16_t h) { return widen().v[h]; }
+inline float kv_value(int8_t v) { return (float)v; }
+
+// KV_T = uint16_t: the f16 cache (scales are 1: KV_SCALE's products are exact). KV_T = int8_t: the KV8 cache
+// (src/cuda.rs:209-226) with f32 scales ks / vs [pos][n_kv]: score = butterfly dot * key scale (src/cuda.rs:1758-
+// 1760), the value scale rides on the weight and the exp-sum is of the unscaled exponentials (src/cuda.rs:1821-
+// 1827).
+template <typename KV_T>
+void decode_gpu(const float* qkv, long q_stride, const KV_T* kc, const KV_T* vc, const float* ks, const float* vs,
+                long kv_stride, float* out, long out_stride, int pos0, int m, int n_heads, int n_kv, float scale,
+                int nsplit, int want, int cap, int threads) {
     const int hd = 128, G = n_heads / n_kv;
-    const float* W = widen().v;
     // partials [token][head][slice][hd + 2]: (unnormalised O, max, exp-sum) in natural-log units
     std::vector<float> part((size_t)m * n_heads * nsplit * (hd + 2), 0.f);
     auto block = [&](long idx) { // one block = (kv head, token, slice)
@@ -298,9 +310,11 @@ void decode_gpu(const float* qkv, long q_stride, const uint16_t* kc, const uint1
         const float* qb = qkv + (long)b * q_stride + (long)kvh * G * hd;
         for (int i = 0; i < G * hd; i++) qsh[i] = qb[i] * scale;
         for (int t = 0; t < len; t++) {
-            const uint16_t* kt = kc + (long)(t0 + t) * kv_stride + kvh * hd;
-            for (int i = 0; i < hd; i++) krow[i] = W[kt[i]];
-            for (int g = 0; g < G; g++) sc[(size_t)t * G + g] = butterfly_score(qsh.data() + g * hd, krow.data());
+            const KV_T* kt = kc + (long)(t0 + t) * kv_stride + kvh * hd;
+            for (int i = 0; i < hd; i++) krow[i] = kv_value(kt[i]);
+            const float kscale = ks ? ks[(long)(t0 + t) * n_kv + kvh] : 1.f;
+            for (int g = 0; g < G; g++)
+                sc[(size_t)t * G + g] = butterfly_score(qsh.data() + g * hd, krow.data()) * kscale;
         }
         for (int g = 0; g < G; g++) {
             float mx = -std::numeric_limits<float>::infinity();
@@ -308,13 +322,14 @@ void decode_gpu(const float* qkv, long q_stride, const uint16_t* kc, const uint1
             float thr[128] = {0};
             for (int t = 0; t < len; t++) {
                 float e = std::exp(sc[(size_t)t * G + g] - mx);
-                sc[(size_t)t * G + g] = e;
+                sc[(size_t)t * G + g] = e * (vs ? vs[(long)(t0 + t) * n_kv + kvh] : 1.f);
                 thr[t % 128] = thr[t % 128] + e;
             }
             float seg = block_sum128(thr);
             for (int d = 0; d < hd; d++) {
                 float a = 0.f;
-                for (int t = 0; t < len; t++) a = std::fma(sc[(size_t)t * G + g], W[vc[(long)(t0 + t) * kv_stride + kvh * hd + d]], a);
+                for (int t = 0; t < len; t++)
+                    a = std::fma(sc[(size_t)t * G + g], kv_value(vc[(long)(t0 + t) * kv_stride + kvh * hd + d]), a);
                 int h = kvh * G + g;
                 if (nsplit == 1) {
                     out[(long)b * out_stride + (long)h * hd + d] = a * (1.f / seg);
@@ -403,6 +418,55 @@ void prefill_tc(const float* q, long q_stride, const uint16_t* kc, const uint16_
     parallel_for((long)n * n_heads, threads, row_task);
 }
 
+// kv_store's int8 branch (src/cuda.rs:333-339) for one row.
+void kv_quant_i8(const float* src, int hd, int8_t* dst, float* scale) {
+    float amax = 0.f;
+    for (int d = 0; d < hd; d++) amax = std::max(amax, std::fabs(src[d]));
+    const float dd = amax / 127.f, inv = dd != 0.f ? 1.f / dd : 0.f;
+    for (int d = 0; d < hd; d++) dst[d] = (int8_t)std::nearbyint(src[d] * inv);
+    *scale = dd;
+}
+
+// qk_norm_rope's arithmetic (src/cuda.rs:437-486); store(is_k, pos, kv_head, row) writes a k or v row
+// into the cache in its format.
+template <typename Store>
+void qk_norm_rope(float* qkv, const float* qn, const float* kn, int pos0, int n, int n_heads, int n_kv, int hd,
+                  int rope_dim, float base, const float* ff, int neox, float eps, Store store) {
+    const long q_dim = (long)n_heads * hd, kv_dim = (long)n_kv * hd, row_len = q_dim + 2 * kv_dim;
+    for (int b = 0; b < n; b++) {
+        const int pos = pos0 + b;
+        float* row = qkv + b * row_len;
+        for (int h = 0; h < n_heads + 2 * n_kv; h++) {
+            if (h >= n_heads + n_kv) {
+                const int vh = h - n_heads - n_kv;
+                store(0, pos, vh, row + q_dim + kv_dim + (long)vh * hd);
+                continue;
+            }
+            float* vec = row + (long)h * hd;
+            if (qn) {
+                const float* w = h < n_heads ? qn : kn;
+                float ss = 0.f;
+                for (int d = 0; d < hd; d++) ss += vec[d] * vec[d];
+                const float scale = 1.0f / std::sqrt(ss / (float)hd + eps);
+                for (int d = 0; d < hd; d++) vec[d] = vec[d] * scale * w[d];
+            }
+            const int half = rope_dim / 2;
+            for (int i = 0; i < half; i++) {
+                float freq = std::pow(base, -2.0f * (float)i / (float)rope_dim);
+                if (ff) freq /= ff[i];
+                const float ang = (float)pos * freq;
+                const float s = std::sin(ang), c = std::cos(ang);
+                const int ia = neox ? i : 2 * i, ib = neox ? i + half : 2 * i + 1;
+                const float x = vec[ia], y = vec[ib];
+                vec[ia] = x * c - y * s;
+                vec[ib] = x * s + y * c;
+            }
+            if (h >= n_heads) store(1, pos, h - n_heads, vec);
+        }
+    }
+}
+
+
 } // namespace
 
 extern "C" {
@@ -455,8 +519,23 @@ void gio_attention_f16kv(const float* q, long q_stride, const uint16_t* kc, cons
 void gio_decode_gpu(const float* qkv, long q_stride, const uint16_t* kc, const uint16_t* vc, long kv_stride, float* out,
                     long out_stride, int pos0, int m, int n_heads, int n_kv, float scale, int nsplit, int want, int cap,
                     int threads) {
-    decode_gpu(qkv, q_stride, kc, vc, kv_stride, out, out_stride, pos0, m, n_heads, n_kv, scale, nsplit, want, cap,
-               threads);
+    decode_gpu<uint16_t>(qkv, q_stride, kc, vc, nullptr, nullptr, kv_stride, out, out_stride, pos0, m, n_heads, n_kv,
+                         scale, nsplit, want, cap, threads);
+}
+
+// The same with the int8 cache (KV8): kc / vc int8 rows, ks / vs f32 scales [pos][n_kv].
+void gio_decode_gpu_i8(const float* qkv, long q_stride, const int8_t* kc, const int8_t* vc, const float* ks,
+                       const float* vs, long kv_stride, float* out, long out_stride, int pos0, int m, int n_heads,
+                       int n_kv, float scale, int nsplit, int want, int cap, int threads) {
+    decode_gpu<int8_t>(qkv, q_stride, kc, vc, ks, vs, kv_stride, out, out_stride, pos0, m, n_heads, n_kv, scale, nsplit,
+                       want, cap, threads);
+}
+
+// kv_store with KV8 (src/cuda.rs:333-339) over `rows` rows of hd values: dd = max|x| / 127, each value
+// rint(x * (1/dd)) as int8 (0 when dd is 0), dd to the row's scale. Division correctly rounded, rint to
+// nearest even (the reference's IEEE `/` and __float2int_rn).
+void gio_kv_quant_i8(const float* src, long rows, int hd, int8_t* dst, float* scales) {
+    for (long r = 0; r < rows; r++) kv_quant_i8(src + r * hd, hd, dst + r * hd, scales + r);
 }
 
 // attn_prefill_tc<128> semantics (f16 rounding of the scaled Q and of P).
@@ -465,50 +544,30 @@ void gio_prefill_tc(const float* q, long q_stride, const uint16_t* kc, const uin
     prefill_tc(q, q_stride, kc, vc, kv_stride, out, out_stride, pos0, n, n_heads, n_kv, scale, threads);
 }
 
+// qk_norm_rope storing into an int8 cache (kv_store with KV8, src/cuda.rs:333-339): kc / vc int8 rows in the
+// element layout of gio_qk_norm_rope, scales at ks / vs [pos*sc_stride + h*sc_head_stride].
+void gio_qk_norm_rope_i8(float* qkv, const float* qn, const float* kn, int8_t* kc, int8_t* vc, float* ks, float* vs,
+                         long kv_stride, long kv_head_stride, long sc_stride, long sc_head_stride, int pos0, int n,
+                         int n_heads, int n_kv, int hd, int rope_dim, float base, const float* ff, int neox, float eps) {
+    qk_norm_rope(qkv, qn, kn, pos0, n, n_heads, n_kv, hd, rope_dim, base, ff, neox, eps,
+                 [&](int is_k, int pos, int h, const float* src) {
+                     const long off = (long)pos * kv_stride + (long)h * kv_head_stride;
+                     float* sc = (is_k ? ks : vs) + (long)pos * sc_stride + (long)h * sc_head_stride;
+                     kv_quant_i8(src, hd, (is_k ? kc : vc) + off, sc);
+                 });
+}
+
 // Reference: qk_norm_rope (src/cuda.rs:437-486), f16 cache. qkv rows [q | k | v] f32 are updated in place
 // (q and k heads normalised and rotated); k and v heads are stored into kc / vc (f16 bits, RNE). Sums in
 // index order; 1/sqrt correctly rounded (the reference's rsqrtf is an approximation of it).
 void gio_qk_norm_rope(float* qkv, const float* qn, const float* kn, uint16_t* kc, uint16_t* vc, long kv_stride,
                       long kv_head_stride, int pos0, int n, int n_heads, int n_kv, int hd, int rope_dim, float base,
                       const float* ff, int neox, float eps) {
-    const long q_dim = (long)n_heads * hd, kv_dim = (long)n_kv * hd, row_len = q_dim + 2 * kv_dim;
-    for (int b = 0; b < n; b++) {
-        const int pos = pos0 + b;
-        float* row = qkv + b * row_len;
-        for (int h = 0; h < n_heads + 2 * n_kv; h++) {
-            if (h >= n_heads + n_kv) {
-                const int vh = h - n_heads - n_kv;
-                const float* src = row + q_dim + kv_dim + (long)vh * hd;
-                uint16_t* dst = vc + (long)pos * kv_stride + (long)vh * kv_head_stride;
-                for (int d = 0; d < hd; d++) dst[d] = f32_to_f16(src[d]);
-                continue;
-            }
-            float* vec = row + (long)h * hd;
-            if (qn) {
-                const float* w = h < n_heads ? qn : kn;
-                float ss = 0.f;
-                for (int d = 0; d < hd; d++) ss += vec[d] * vec[d];
-                const float scale = 1.0f / std::sqrt(ss / (float)hd + eps);
-                for (int d = 0; d < hd; d++) vec[d] = vec[d] * scale * w[d];
-            }
-            const int half = rope_dim / 2;
-            for (int i = 0; i < half; i++) {
-                float freq = std::pow(base, -2.0f * (float)i / (float)rope_dim);
-                if (ff) freq /= ff[i];
-                const float ang = (float)pos * freq;
-                const float s = std::sin(ang), c = std::cos(ang);
-                const int ia = neox ? i : 2 * i, ib = neox ? i + half : 2 * i + 1;
-                const float x = vec[ia], y = vec[ib];
-                vec[ia] = x * c - y * s;
-                vec[ib] = x * s + y * c;
-            }
-            if (h >= n_heads) {
-                const int kh = h - n_heads;
-                uint16_t* dst = kc + (long)pos * kv_stride + (long)kh * kv_head_stride;
-                for (int d = 0; d < hd; d++) dst[d] = f32_to_f16(vec[d]);
-            }
-        }
-    }
+    qk_norm_rope(qkv, qn, kn, pos0, n, n_heads, n_kv, hd, rope_dim, base, ff, neox, eps,
+                 [&](int is_k, int pos, int h, const float* src) {
+                     uint16_t* dst = (is_k ? kc : vc) + (long)pos * kv_stride + (long)h * kv_head_stride;
+                     for (int d = 0; d < hd; d++) dst[d] = f32_to_f16(src[d]);
+                 });
 }
 
 } // extern "C"

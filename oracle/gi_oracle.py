@@ -45,6 +45,9 @@ def lib():
         L.gio_decode_gpu.argtypes = [vp, l, vp, vp, l, vp, l, i, i, i, i, f, i, i, i, i]
         L.gio_prefill_tc.argtypes = [vp, l, vp, vp, l, vp, l, i, i, i, i, f, i]
         L.gio_qk_norm_rope.argtypes = [vp, vp, vp, vp, vp, l, l, i, i, i, i, i, i, f, vp, i, f]
+        L.gio_qk_norm_rope_i8.argtypes = [vp, vp, vp, vp, vp, vp, vp, l, l, l, l, i, i, i, i, i, i, f, vp, i, f]
+        L.gio_decode_gpu_i8.argtypes = [vp, l, vp, vp, vp, vp, l, vp, l, i, i, i, i, f, i, i, i, i]
+        L.gio_kv_quant_i8.argtypes = [vp, l, i, vp, vp]
         _lib = L
     return _lib
 
@@ -128,6 +131,35 @@ def decode_gpu_semantics(q, kc, vc, pos0, n_heads, n_kv, scale=None, cap=128, th
     return out
 
 
+def decode_gpu_semantics_i8(q, kc, vc, ks, vs, pos0, n_heads, n_kv, scale=None, cap=128, threads=8):
+    """attention_partial_gqa + attention_combine over the KV8 cache (src/cuda.rs:209-226, 1684-1865, 2806-2836).
+    kc/vc: int8 [pos, n_kv*128]; ks/vs: f32 scales [pos, n_kv]."""
+    q = _rows(q, np.float32)
+    m = q.shape[0]
+    kc, vc = _rows(kc, np.int8), _rows(vc, np.int8)
+    ks, vs = _rows(ks, np.float32), _rows(vs, np.float32)
+    assert ks.shape == (kc.shape[0], n_kv) and vs.shape == ks.shape
+    if scale is None:
+        scale = 1.0 / np.sqrt(128)
+    want = att_want(n_kv)
+    nsplit = max(-(-span // att_chunk(span, want, cap)) for span in range(pos0 + 1, pos0 + m + 1))
+    out = np.zeros((m, n_heads * 128), dtype=np.float32)
+    lib().gio_decode_gpu_i8(_p(q), q.shape[1], _p(kc), _p(vc), _p(ks), _p(vs), kc.shape[1], _p(out), out.shape[1],
+                            pos0, m, n_heads, n_kv, scale, nsplit, want, cap, threads)
+    return out
+
+
+def kv_quant_i8(x):
+    """kv_store with KV8 (src/cuda.rs:333-339) over rows of x (f32 [..., hd]): returns (int8 rows, f32 scales)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    hd = x.shape[-1]
+    rows = x.size // hd
+    q = np.empty(x.shape, dtype=np.int8)
+    sc = np.empty(x.shape[:-1], dtype=np.float32)
+    lib().gio_kv_quant_i8(_p(x), rows, hd, _p(q), _p(sc))
+    return q, sc
+
+
 def prefill_tc_semantics(q, kc, vc, pos0, n_heads, n_kv, scale=None, threads=8):
     """attn_prefill_tc<128> (src/cuda.rs:2408-2617): f16-rounded Q*scale*log2(e) and P."""
     q = _rows(q, np.float32)
@@ -158,3 +190,26 @@ def qk_norm_rope(qkv, kc, vc, pos0, n_heads, n_kv, hd=128, rope_dim=None, base=1
     lib().gio_qk_norm_rope(_p(qkv), ptrs[0], ptrs[1], _p(kc), _p(vc), kv_stride, kv_head_stride, pos0, n, n_heads,
                            n_kv, hd, rope_dim, base, ptrs[2], 1 if neox else 0, eps)
     return qkv, kc, vc
+
+
+def qk_norm_rope_i8(qkv, kc, vc, ks, vs, pos0, n_heads, n_kv, hd=128, rope_dim=None, base=10000.0, qn=None, kn=None,
+                    ff=None, neox=True, eps=1e-6, kv_head_stride=None, sc_stride=None, sc_head_stride=1):
+    """qk_norm_rope (src/cuda.rs:437-486) storing into an int8 cache (kv_store with KV8, src/cuda.rs:333-339).
+    kc/vc: int8, rows of position t kv_stride elements apart; ks/vs: f32 scales, position t kv head h at
+    t*sc_stride + h*sc_head_stride (default [pos][n_kv]). Returns (qkv, kc, vc, ks, vs) copies."""
+    qkv = np.array(qkv, dtype=np.float32, order="C", copy=True)
+    kc = np.array(kc, dtype=np.int8, order="C", copy=True)
+    vc = np.array(vc, dtype=np.int8, order="C", copy=True)
+    ks = np.array(ks, dtype=np.float32, order="C", copy=True)
+    vs = np.array(vs, dtype=np.float32, order="C", copy=True)
+    n = qkv.shape[0]
+    rope_dim = hd if rope_dim is None else rope_dim
+    kv_stride = kc.strides[0]
+    kv_head_stride = hd if kv_head_stride is None else kv_head_stride
+    sc_stride = n_kv if sc_stride is None else sc_stride
+    opts = [None if a is None else np.ascontiguousarray(a, dtype=np.float32) for a in (qn, kn, ff)]
+    ptrs = [None if a is None else _p(a) for a in opts]
+    lib().gio_qk_norm_rope_i8(_p(qkv), ptrs[0], ptrs[1], _p(kc), _p(vc), _p(ks), _p(vs), kv_stride, kv_head_stride,
+                              sc_stride, sc_head_stride, pos0, n, n_heads, n_kv, hd, rope_dim, base, ptrs[2],
+                              1 if neox else 0, eps)
+    return qkv, kc, vc, ks, vs

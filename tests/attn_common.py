@@ -22,27 +22,8 @@ def f16_values(bits):
 
 
 def reference_f64(q, kbits, vbits, pos0, n_heads, n_kv, hd=128, scale=None):
-    """Textbook causal softmax attention in float64: token b attends to keys 0..pos0+b."""
-    q = np.asarray(q, dtype=np.float64).reshape(q.shape[0], n_heads, hd)
-    n = q.shape[0]
-    k = f16_values(kbits).reshape(-1, n_kv, hd)
-    v = f16_values(vbits).reshape(-1, n_kv, hd)
-    if scale is None:
-        scale = 1.0 / np.sqrt(hd)
-    G = n_heads // n_kv
-    out = np.zeros((n, n_heads, hd))
-    for kvh in range(n_kv):
-        K = k[: pos0 + n, kvh]
-        V = v[: pos0 + n, kvh]
-        qh = q[:, kvh * G:(kvh + 1) * G]  # [n, G, hd]
-        s = np.einsum("ngd,td->ngt", qh, K) * scale
-        mask = np.arange(pos0 + n)[None, :] > (pos0 + np.arange(n))[:, None]
-        s = np.where(mask[:, None, :], -np.inf, s)
-        s -= s.max(axis=-1, keepdims=True)
-        p = np.exp(s)
-        p /= p.sum(axis=-1, keepdims=True)
-        out[:, kvh * G:(kvh + 1) * G] = np.einsum("ngt,td->ngd", p, V)
-    return out.reshape(n, n_heads * hd)
+    """Textbook causal softmax attention in float64 over an f16 cache: token b attends to keys 0..pos0+b."""
+    return _reference_f64_values(q, f16_values(kbits), f16_values(vbits), pos0, n_heads, n_kv, hd, scale)
 
 
 def errors(got, want):
@@ -59,3 +40,50 @@ def assert_close(got, want, max_abs=MAX_ABS_TOL, rel_l2=REL_L2_TOL, what=""):
     ma, rl = errors(got, want)
     assert ma <= max_abs and rl <= rel_l2, f"{what}: max_abs {ma:.3g} (tol {max_abs}), rel_l2 {rl:.3g} (tol {rel_l2})"
     return ma, rl
+
+
+def make_inputs_i8(seed, n_tok, ctx, n_heads, n_kv, hd=128):
+    """Seeded int8-cache inputs: q f32 [n_tok, n_heads*hd] N(0,1); K/V int8 [ctx, n_kv*hd] uniform in
+    -127..127; scales f32 [ctx, n_kv] uniform in [0.015, 0.035] (about what N(0,1) rows quantise to).
+    One generator per tensor: seed .. seed + 4."""
+    q = np.random.default_rng(seed).standard_normal((n_tok, n_heads * hd), dtype=np.float32)
+    k = np.random.default_rng(seed + 1).integers(-127, 128, (ctx, n_kv * hd), dtype=np.int8)
+    v = np.random.default_rng(seed + 2).integers(-127, 128, (ctx, n_kv * hd), dtype=np.int8)
+    ks = np.random.default_rng(seed + 3).uniform(0.015, 0.035, (ctx, n_kv)).astype(np.float32)
+    vs = np.random.default_rng(seed + 4).uniform(0.015, 0.035, (ctx, n_kv)).astype(np.float32)
+    return q, k, v, ks, vs
+
+
+def dequant_f64(c, sc, n_kv, hd=128):
+    """int8 rows [pos, n_kv*hd] times their (position, kv head) scales, in float64."""
+    c = np.asarray(c, dtype=np.float64).reshape(-1, n_kv, hd)
+    return (c * np.asarray(sc, dtype=np.float64)[:, :, None]).reshape(c.shape[0], n_kv * hd)
+
+
+def reference_f64_i8(q, kc, vc, ks, vs, pos0, n_heads, n_kv, hd=128, scale=None):
+    """reference_f64 over the dequantised int8 cache."""
+    return _reference_f64_values(q, dequant_f64(kc, ks, n_kv, hd), dequant_f64(vc, vs, n_kv, hd), pos0, n_heads, n_kv,
+                                 hd, scale)
+
+
+def _reference_f64_values(q, k, v, pos0, n_heads, n_kv, hd=128, scale=None):
+    q = np.asarray(q, dtype=np.float64).reshape(q.shape[0], n_heads, hd)
+    n = q.shape[0]
+    k = np.asarray(k, dtype=np.float64).reshape(-1, n_kv, hd)
+    v = np.asarray(v, dtype=np.float64).reshape(-1, n_kv, hd)
+    if scale is None:
+        scale = 1.0 / np.sqrt(hd)
+    G = n_heads // n_kv
+    out = np.zeros((n, n_heads, hd))
+    for kvh in range(n_kv):
+        K = k[: pos0 + n, kvh]
+        V = v[: pos0 + n, kvh]
+        qh = q[:, kvh * G:(kvh + 1) * G]
+        s = np.einsum("ngd,td->ngt", qh, K) * scale
+        mask = np.arange(pos0 + n)[None, :] > (pos0 + np.arange(n))[:, None]
+        s = np.where(mask[:, None, :], -np.inf, s)
+        s -= s.max(axis=-1, keepdims=True)
+        p = np.exp(s)
+        p /= p.sum(axis=-1, keepdims=True)
+        out[:, kvh * G:(kvh + 1) * G] = np.einsum("ngt,td->ngd", p, V)
+    return out.reshape(n, n_heads * hd)

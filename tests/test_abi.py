@@ -55,6 +55,26 @@ def test_decode_rejects_bad_arguments_before_any_launch():
     assert rc == -1 and "dtypes" in lib.gi_last_error().decode()
 
 
+def test_int8_entry_points_reject_bad_arguments_before_any_launch():
+    lib = gi_attn.load_library()
+    # int8 rows need 16-element strides, non-null 4-byte aligned scales and positive scale strides
+    rc = lib.gi_attn_decode_i8(None, 16, 4096, 16, 16, 16, 16, 520, 8, 0, 0, 16, 4096, None, 0, 0, None, 0, 1, 32, 4,
+                               128, 0.1)
+    assert rc == -1 and "multiples of 16" in lib.gi_last_error().decode()
+    rc = lib.gi_attn_decode_i8(None, 16, 4096, 16, 16, None, 16, 512, 128, 0, 0, 16, 4096, None, 0, 0, None, 0, 1, 32,
+                               4, 128, 0.1)
+    assert rc == -1 and "scale" in lib.gi_last_error().decode()
+    rc = lib.gi_attn_decode_i8(None, 16, 4096, 16, 16, 18, 16, 512, 128, 0, 0, 16, 4096, None, 0, 0, None, 0, 1, 32,
+                               4, 128, 0.1)
+    assert rc == -1 and "4-byte aligned" in lib.gi_last_error().decode()
+    rc = lib.gi_attn_decode_i8(None, 16, 4096, 16, 16, 16, 16, 512, 128, -4, 1, 16, 4096, None, 0, 0, None, 0, 1, 32,
+                               4, 128, 0.1)
+    assert rc == -1 and "sc_stride" in lib.gi_last_error().decode()
+    rc = lib.gi_qk_norm_rope_i8(None, 16, None, None, 16, 16, None, None, 512, 128, 0, 0, 0, None, 1, 32, 4, 128, 128,
+                                1e4, None, 1, 1e-6)
+    assert rc == -1 and "scale" in lib.gi_last_error().decode()
+
+
 @pytest.mark.parametrize("ctx,n_tok,n_heads,n_kv", [(4096, 1, 32, 8), (65536, 1, 32, 4), (32776, 8, 32, 4),
                                                     (100, 15, 8, 1), (1, 1, 32, 4)])
 def test_decode_plan_covers_the_span(ctx, n_tok, n_heads, n_kv):

@@ -1,0 +1,221 @@
+"""Parity of the int8 KV cache path (the reference's KV8 build: kv_store src/cuda.rs:333-339, decode
+src/cuda.rs:1684-1865 + 2806-2836) on the gfx950 kernels, through the C ABI.
+
+Bar: max-abs 2e-3 and relative L2 1e-3 against the oracle's restatement of the reference's int8 decode,
+and 2e-5 against float64 attention over the dequantised cache (the kernels widen int8 exactly and keep
+f32 scores). The cache write is checked against the oracle's quantiser: V rows (copied, not rotated)
+byte for byte with equal scales; K rows (after RoPE, whose angles differ by an ulp between sin/cos
+implementations) within one quantisation step plus the f32 tolerance.
+"""
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+import gi_attn
+import gi_oracle as O
+from attn_common import assert_close, make_inputs_i8, reference_f64_i8
+
+pytestmark = pytest.mark.gpu
+
+
+def say(*a):
+    print("[case]", *a, flush=True)
+    sys.stdout.flush()
+
+
+def to_dev_i8(q, k, v, ks, vs, dev, layout="reference", n_kv=None):
+    qt = torch.from_numpy(np.ascontiguousarray(q)).to(dev)
+    if layout == "head_major":
+        k = np.ascontiguousarray(k.reshape(k.shape[0], n_kv, -1).transpose(1, 0, 2))
+        v = np.ascontiguousarray(v.reshape(v.shape[0], n_kv, -1).transpose(1, 0, 2))
+        ks, vs = np.ascontiguousarray(ks.T), np.ascontiguousarray(vs.T)
+    return (qt, torch.from_numpy(np.ascontiguousarray(k)).to(dev), torch.from_numpy(np.ascontiguousarray(v)).to(dev),
+            torch.from_numpy(np.ascontiguousarray(ks)).to(dev), torch.from_numpy(np.ascontiguousarray(vs)).to(dev))
+
+
+def run_decode_i8(q, k, v, ks, vs, pos0, n_heads, n_kv, dev, layout="reference", **kw):
+    qt, kt, vt, kst, vst = to_dev_i8(q, k, v, ks, vs, dev, layout, n_kv)
+    out = gi_attn.decode(qt, kt, vt, pos0, n_heads, n_kv, k_scale=kst, v_scale=vst, kv_layout=layout, **kw)
+    torch.cuda.synchronize()
+    return out.cpu().numpy()
+
+
+def check(got, q, k, v, ks, vs, pos0, n_heads, n_kv, what):
+    assert_close(got, O.decode_gpu_semantics_i8(q, k, v, ks, vs, pos0, n_heads, n_kv), what=f"{what} vs oracle")
+    assert_close(got, reference_f64_i8(q, k, v, ks, vs, pos0, n_heads, n_kv), max_abs=2e-5, rel_l2=2e-5,
+                 what=f"{what} vs f64")
+
+
+DECODE_SHAPES_I8 = [
+    # (n_tok, pos0, n_heads, n_kv): spans inside one tile, at tile and slice edges, verify blocks of every
+    # kernel variant (1 and 2 column blocks, the shared-slice variant), G = 3 and 6 pair layouts
+    (1, 0, 32, 8),
+    (1, 63, 32, 4),
+    (1, 64, 32, 4),
+    (1, 255, 8, 8),
+    (1, 256, 32, 4),
+    (1, 1000, 32, 4),
+    (1, 4095, 32, 8),
+    (2, 300, 32, 4),
+    (3, 60, 16, 2),
+    (8, 200, 32, 4),
+    (15, 513, 32, 8),
+    (5, 77, 12, 4),
+    (4, 40, 6, 1),
+]
+
+
+@pytest.mark.parametrize("n_tok,pos0,n_heads,n_kv", DECODE_SHAPES_I8)
+def test_decode_i8_small(gpu, n_tok, pos0, n_heads, n_kv):
+    say("decode i8", n_tok, pos0, n_heads, n_kv)
+    q, k, v, ks, vs = make_inputs_i8(5000 + pos0, n_tok, pos0 + n_tok, n_heads, n_kv)
+    got = run_decode_i8(q, k, v, ks, vs, pos0, n_heads, n_kv, gpu)
+    check(got, q, k, v, ks, vs, pos0, n_heads, n_kv, "decode i8")
+
+
+def test_decode_i8_ctx65536(gpu):
+    say("decode i8 ctx 65536 32q/4kv")
+    q, k, v, ks, vs = make_inputs_i8(6, 1, 65536, 32, 4)
+    got = run_decode_i8(q, k, v, ks, vs, 65535, 32, 4, gpu)
+    check(got, q, k, v, ks, vs, 65535, 32, 4, "decode i8 C2 shape")
+
+
+def test_verify_i8_8tok_at_32768(gpu):
+    say("verify i8 8 tokens @ 32768 32q/4kv")
+    q, k, v, ks, vs = make_inputs_i8(7, 8, 32776, 32, 4)
+    got = run_decode_i8(q, k, v, ks, vs, 32768, 32, 4, gpu)
+    check(got, q, k, v, ks, vs, 32768, 32, 4, "verify i8 C4 shape")
+
+
+@pytest.mark.parametrize("n_tok,pos0,n_heads,n_kv", [(1, 300, 32, 4), (1, 65535, 32, 4), (8, 1000, 32, 4)])
+def test_decode_i8_head_major(gpu, n_tok, pos0, n_heads, n_kv):
+    say("decode i8 head-major", n_tok, pos0, n_heads, n_kv)
+    q, k, v, ks, vs = make_inputs_i8(7000 + pos0, n_tok, pos0 + n_tok, n_heads, n_kv)
+    got = run_decode_i8(q, k, v, ks, vs, pos0, n_heads, n_kv, gpu, layout="head_major")
+    check(got, q, k, v, ks, vs, pos0, n_heads, n_kv, "decode i8 head-major")
+
+
+def test_decode_i8_zero_scale_rows(gpu):
+    # rows whose scale is 0 (an all-zero row as kv_store writes it) score 0 and weigh nothing in V
+    q, k, v, ks, vs = make_inputs_i8(71, 1, 700, 32, 4)
+    ks[100:164] = 0
+    vs[300:310] = 0
+    k[100:164] = 0
+    v[300:310] = 0
+    say("decode i8 zero-scale rows")
+    got = run_decode_i8(q, k, v, ks, vs, 699, 32, 4, gpu)
+    check(got, q, k, v, ks, vs, 699, 32, 4, "decode i8 zero rows")
+
+
+def test_decode_i8_device_position(gpu):
+    n_heads, n_kv, cap = 32, 4, 3000
+    q, k, v, ks, vs = make_inputs_i8(78, 1, cap, n_heads, n_kv)
+    qt, kt, vt, kst, vst = to_dev_i8(q, k, v, ks, vs, gpu)
+    ws = gi_attn.new_workspace(cap, 1, n_heads, n_kv, device=gpu)
+    posp = torch.zeros(1, dtype=torch.int32, device=gpu)
+    for pos in (0, 64, 1999, 2999):
+        say("decode i8 posp", pos)
+        posp.fill_(pos)
+        out = gi_attn.decode(qt, kt, vt, 99999, n_heads, n_kv, k_scale=kst, v_scale=vst, workspace=ws, posp=posp,
+                             ctx_cap=cap)
+        torch.cuda.synchronize()
+        assert_close(out.cpu().numpy(), reference_f64_i8(q, k, v, ks, vs, pos, n_heads, n_kv), max_abs=2e-5,
+                     rel_l2=2e-5, what=f"i8 posp {pos}")
+
+
+def test_decode_i8_and_f16_share_a_workspace(gpu):
+    # calls of both cache types through one workspace, in turn: each matches its own reference
+    from attn_common import make_inputs, reference_f64
+    n_heads, n_kv, cap = 32, 4, 5000
+    ws = gi_attn.new_workspace(cap, 15, n_heads, n_kv, device=gpu)
+    for i, (n_tok, pos0) in enumerate(((1, 4999), (15, 100), (8, 3000), (1, 200))):
+        say("decode i8/f16 shared workspace", n_tok, pos0)
+        q, k, v, ks, vs = make_inputs_i8(900 + i, n_tok, pos0 + n_tok, n_heads, n_kv)
+        got = run_decode_i8(q, k, v, ks, vs, pos0, n_heads, n_kv, gpu, workspace=ws)
+        assert_close(got, reference_f64_i8(q, k, v, ks, vs, pos0, n_heads, n_kv), max_abs=2e-5, rel_l2=2e-5,
+                     what=f"i8 {n_tok}@{pos0}")
+        q, kb, vb = make_inputs(950 + i, n_tok, pos0 + n_tok, n_heads, n_kv)
+        qt = torch.from_numpy(q).to(gpu)
+        kt = torch.from_numpy(kb.view(np.int16)).to(gpu).view(torch.float16)
+        vt = torch.from_numpy(vb.view(np.int16)).to(gpu).view(torch.float16)
+        out = gi_attn.decode(qt, kt, vt, pos0, n_heads, n_kv, workspace=ws)
+        torch.cuda.synchronize()
+        assert_close(out.cpu().numpy(), reference_f64(q, kb, vb, pos0, n_heads, n_kv), max_abs=2e-5, rel_l2=2e-5,
+                     what=f"f16 {n_tok}@{pos0}")
+
+
+# ---------------------------------------------------------------- cache write (qk_norm_rope with KV8)
+
+ROPE_I8_SHAPES = [
+    # (n, pos0, n_heads, n_kv, hd, neox, norm, layout)
+    (1, 4095, 32, 8, 128, True, True, "reference"),
+    (7, 100, 16, 4, 64, False, False, "reference"),
+    (300, 0, 32, 4, 128, True, True, "head_major"),
+    (3, 2000, 8, 2, 256, True, True, "reference"),
+]
+
+
+@pytest.mark.parametrize("n,pos0,n_heads,n_kv,hd,neox,norm,layout", ROPE_I8_SHAPES)
+def test_qk_norm_rope_i8_matches_oracle(gpu, n, pos0, n_heads, n_kv, hd, neox, norm, layout):
+    say("qk_norm_rope i8", n, pos0, n_heads, n_kv, hd, neox, norm, layout)
+    rng = np.random.default_rng(900 + n)
+    qkv = rng.standard_normal((n, (n_heads + 2 * n_kv) * hd), dtype=np.float32)
+    qkv[0, (n_heads + n_kv) * hd:(n_heads + n_kv + 1) * hd] = 0  # a zero v row: scale 0, zero bytes
+    cap = pos0 + n + 5
+    kc = np.full((cap, n_kv * hd), 99, dtype=np.int8)
+    sc = np.full((cap, n_kv), -1.0, dtype=np.float32)
+    qn = rng.uniform(0.5, 1.5, hd).astype(np.float32) if norm else None
+    kn = rng.uniform(0.5, 1.5, hd).astype(np.float32) if norm else None
+    want, wk, wv, wks, wvs = O.qk_norm_rope_i8(qkv, kc, kc, sc, sc, pos0, n_heads, n_kv, hd=hd, base=1e6, qn=qn,
+                                               kn=kn, neox=neox)
+    dev = lambda a: None if a is None else torch.from_numpy(np.ascontiguousarray(a)).to(gpu)
+    qt = dev(qkv)
+    kt, vt = dev(kc.reshape(cap, n_kv, hd)), dev(kc.reshape(cap, n_kv, hd))
+    kst, vst = dev(sc), dev(sc)
+    if layout == "head_major":
+        kt, vt = kt.transpose(0, 1).contiguous(), vt.transpose(0, 1).contiguous()
+        kst, vst = kst.t().contiguous(), vst.t().contiguous()
+    gi_attn.qk_norm_rope(qt, kt, vt, pos0, n_heads, n_kv, hd=hd, base=1e6, qn=dev(qn), kn=dev(kn), neox=neox,
+                         kv_layout=layout, k_scale=kst, v_scale=vst)
+    torch.cuda.synchronize()
+    if layout == "head_major":
+        kt, vt = kt.transpose(0, 1).contiguous(), vt.transpose(0, 1).contiguous()
+        kst, vst = kst.t().contiguous(), vst.t().contiguous()
+    got = qt.cpu().numpy()
+    gk, gv = kt.cpu().numpy().reshape(cap, -1), vt.cpu().numpy().reshape(cap, -1)
+    gks, gvs = kst.cpu().numpy(), vst.cpu().numpy()
+    assert np.abs(got - want).max() <= 2e-3
+    # V: the input rows quantised, bit for bit (including the zero row's scale 0)
+    np.testing.assert_array_equal(gv, wv)
+    np.testing.assert_array_equal(gvs, wvs)
+    assert gvs[pos0, 0] == 0
+    # K: dequantised values within one step of the oracle's plus the rotation tolerance
+    rows = slice(pos0, pos0 + n)
+    gkd = gk[rows].reshape(n, n_kv, hd).astype(np.float64) * gks[rows][:, :, None]
+    wkd = wk[rows].reshape(n, n_kv, hd).astype(np.float64) * wks[rows][:, :, None]
+    assert np.all(np.abs(gkd - wkd) <= 2e-3 + wks[rows][:, :, None] * 1.0001)
+    np.testing.assert_allclose(gks[rows], wks[rows], rtol=2e-3, atol=2e-5)
+    other = np.r_[0:pos0, pos0 + n:cap]
+    assert np.all(gk[other] == 99) and np.all(gv[other] == 99)
+    assert np.all(gks[other] == -1) and np.all(gvs[other] == -1)
+
+
+def test_qk_norm_rope_i8_then_decode_matches_the_oracle_pipeline(gpu):
+    # store a new token's K/V into an int8 cache, then decode over it, against the oracle doing both
+    n_heads, n_kv, hd, pos = 32, 4, 128, 2500
+    _, kc, vc, ks, vs = make_inputs_i8(812, 1, pos + 1, n_heads, n_kv)
+    rng = np.random.default_rng(813)
+    qkv = rng.standard_normal((1, (n_heads + 2 * n_kv) * hd), dtype=np.float32)
+    qn = rng.uniform(0.5, 1.5, hd).astype(np.float32)
+    kn = rng.uniform(0.5, 1.5, hd).astype(np.float32)
+    o_qkv, o_kc, o_vc, o_ks, o_vs = O.qk_norm_rope_i8(qkv, kc, vc, ks, vs, pos, n_heads, n_kv, qn=qn, kn=kn, base=1e6)
+    want = O.decode_gpu_semantics_i8(o_qkv[:, :n_heads * hd], o_kc, o_vc, o_ks, o_vs, pos, n_heads, n_kv)
+    say("qk_norm_rope i8 + decode i8")
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(gpu)
+    qt, kt, vt, kst, vst = dev(qkv), dev(kc), dev(vc), dev(ks), dev(vs)
+    gi_attn.qk_norm_rope(qt, kt, vt, pos, n_heads, n_kv, qn=dev(qn), kn=dev(kn), base=1e6, k_scale=kst, v_scale=vst)
+    out = gi_attn.decode(qt[:, :n_heads * hd], kt, vt, pos, n_heads, n_kv, k_scale=kst, v_scale=vst)
+    torch.cuda.synchronize()
+    assert_close(out.cpu().numpy(), want, what="qk_norm_rope i8 + decode i8 vs oracle")

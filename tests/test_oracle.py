@@ -18,7 +18,7 @@ import pytest
 import torch
 
 import gi_oracle as O
-from attn_common import assert_close, errors, make_inputs, reference_f64
+from attn_common import assert_close, errors, make_inputs, make_inputs_i8, reference_f64, reference_f64_i8
 
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
 
@@ -319,3 +319,81 @@ def test_rms_norm_gives_unit_rms_times_weights():
     k = qkv[0, 2 * hd:3 * hd].astype(np.float64)
     want = k / np.sqrt(np.mean(k ** 2) + 1e-6) * w
     np.testing.assert_allclose(out[0, 2 * hd:3 * hd], want, rtol=1e-5, atol=1e-6)
+
+
+# ---------------------------------------------------------------- int8 cache (KV8)
+
+def test_kv_quant_i8_closed_forms():
+    hd = 128
+    x = np.zeros((4, hd), dtype=np.float32)
+    # row 0: all zero -> scale 0 and zero bytes (inv = 0, no division by zero)
+    # row 1: max |x| = 127 -> scale exactly 1, so integers are kept and halves round to even
+    x[1, :8] = [127, -3, 2.5, 3.5, -0.5, -1.5, 0.49, -126.5]
+    # row 2: max |x| = 127 * 2^-5 -> scale 2^-5 exactly; multiples of 2^-5 map to their integers
+    ints = np.arange(-127, 1, dtype=np.float32)
+    x[2, :128] = ints * 2.0 ** -5
+    # row 3: negative extreme -> -127
+    x[3, 7] = -3.0
+    x[3, 9] = 1.0
+    q, sc = O.kv_quant_i8(x)
+    assert sc[0] == 0 and not q[0].any()
+    assert sc[1] == 1.0
+    np.testing.assert_array_equal(q[1, :8], [127, -3, 2, 4, 0, -2, 0, -126])
+    assert sc[2] == 2.0 ** -5
+    np.testing.assert_array_equal(q[2], ints.astype(np.int8))
+    assert q[3, 7] == -127 and q[3, 9] == round(127 / 3)
+
+
+def test_kv_quant_i8_error_bound_and_extremes():
+    x = np.random.default_rng(5).standard_normal((64, 256), dtype=np.float32) * np.float32(3)
+    q, sc = O.kv_quant_i8(x)
+    err = np.abs(q.astype(np.float64) * sc[:, None] - x)
+    assert np.all(err <= sc[:, None] * (0.5 + 1e-5))
+    np.testing.assert_array_equal(np.abs(q.astype(np.int32)).max(axis=1), 127)  # each row's max maps to +-127
+    np.testing.assert_allclose(sc, np.abs(x).max(axis=1) / 127, rtol=1e-6)
+
+
+@pytest.mark.parametrize("n_tok,pos0,n_heads,n_kv", [(1, 0, 32, 8), (1, 33, 32, 4), (1, 1000, 32, 4),
+                                                     (5, 300, 16, 8), (8, 2000, 32, 4)])
+def test_decode_gpu_semantics_i8_matches_f64(n_tok, pos0, n_heads, n_kv):
+    q, k, v, ks, vs = make_inputs_i8(61 + pos0, n_tok, pos0 + n_tok, n_heads, n_kv)
+    got = O.decode_gpu_semantics_i8(q, k, v, ks, vs, pos0, n_heads, n_kv)
+    want = reference_f64_i8(q, k, v, ks, vs, pos0, n_heads, n_kv)
+    assert_close(got, want, max_abs=2e-5, rel_l2=2e-6, what="int8 decode semantics vs f64")
+
+
+def test_decode_i8_unit_scales_equal_the_f16_path():
+    # small integers are exact in f16 and unit scales multiply exactly: both restatements must agree bit for bit
+    q, k, v, _, _ = make_inputs_i8(7, 3, 700, 16, 4)
+    k = (k // 8).astype(np.int8)  # keep scores moderate
+    ones = np.ones((700, 4), dtype=np.float32)
+    got = O.decode_gpu_semantics_i8(q, k, v, ones, ones, 697, 16, 4)
+    kb = k.astype(np.float16).view(np.uint16)
+    vb = v.astype(np.float16).view(np.uint16)
+    np.testing.assert_array_equal(got, O.decode_gpu_semantics(q, kb, vb, 697, 16, 4))
+
+
+@pytest.mark.parametrize("hd,neox", [(128, True), (64, False), (256, True)])
+def test_rope_i8_stores_the_quantised_rows(hd, neox):
+    n_heads, n_kv, n, pos0, cap = 4, 2, 3, 50, 60
+    rng = np.random.default_rng(hd)
+    qkv = rng.standard_normal((n, (n_heads + 2 * n_kv) * hd), dtype=np.float32)
+    qn = rng.uniform(0.5, 1.5, hd).astype(np.float32)
+    kn = rng.uniform(0.5, 1.5, hd).astype(np.float32)
+    kc = np.zeros((cap, n_kv * hd), np.int8)
+    sc = np.full((cap, n_kv), -1.0, np.float32)
+    out, kc8, vc8, ks, vs = O.qk_norm_rope_i8(qkv, kc, kc, sc, sc, pos0, n_heads, n_kv, hd=hd, qn=qn, kn=kn,
+                                             neox=neox)
+    # the rows themselves are the f16 path's
+    out16, _, _ = O.qk_norm_rope(qkv, np.zeros((cap, n_kv * hd), np.uint16), np.zeros((cap, n_kv * hd), np.uint16),
+                                 pos0, n_heads, n_kv, hd=hd, qn=qn, kn=kn, neox=neox)
+    np.testing.assert_array_equal(out, out16)
+    k_rows = out[:, n_heads * hd:(n_heads + n_kv) * hd]
+    v_rows = qkv[:, (n_heads + n_kv) * hd:]
+    for cache, scales, rows in ((kc8, ks, k_rows), (vc8, vs, v_rows)):
+        got = cache[pos0:pos0 + n].reshape(n, n_kv, hd).astype(np.float64) * scales[pos0:pos0 + n, :, None]
+        want = rows.reshape(n, n_kv, hd)
+        assert np.all(np.abs(got - want) <= scales[pos0:pos0 + n, :, None] * (0.5 + 1e-5))
+        np.testing.assert_allclose(scales[pos0:pos0 + n], np.abs(want).max(axis=2) / 127, rtol=1e-6)
+        assert not cache[:pos0].any() and not cache[pos0 + n:].any()
+        assert np.all(scales[:pos0] == -1) and np.all(scales[pos0 + n:] == -1)
