@@ -1,6 +1,7 @@
 """Benchmark of the gfx950 attention hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload decode64k|decode4k|verify|prefill8k|chunked|qkrope|decode64k_i8|verify_i8]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload decode64k|decode4k|verify|prefill8k|chunked|qkrope|
+                    decode64k_i8|verify_i8|prefill8k_i8]
                     [--no-cpu-baseline] [--no-secondary] [--reference-layout]
 
 A step is one pass of the hot path over one batch of synthetic seeded input already resident in HBM:
@@ -11,8 +12,8 @@ A step is one pass of the hot path over one batch of synthetic seeded input alre
   prefill8k  config 3: causal prefill of 8192 tokens, 32 / 8 heads, f16 in and out (MFMA TFLOP/s)
   chunked    config 5: 131072 tokens in 2048-token chunks against the growing cache, 32 / 4 heads
   qkrope     the cache write before attention (qk_norm_rope + f16 KV store) for config 3's 8192 tokens
-  decode64k_i8, verify_i8
-             configs 2 and 4 over the int8 cache (the reference's KV8 format: int8 rows, an f32 scale per
+  decode64k_i8, verify_i8, prefill8k_i8
+             configs 2, 4 and 3 over the int8 cache (the reference's KV8 format: int8 rows, an f32 scale per
              position and kv head); bytes are the int8 rows plus their scales
 Decode steps rotate over several layers' caches whose total exceeds the 256 MB Infinity Cache, as a
 model's layer loop does, so no step finds its K/V in the last-level cache.
@@ -43,15 +44,19 @@ def log(*a):
 
 def seeded_cache(gen, rows, n_kv, dev, torch, layout="reference", i8=False):
     """K and V caches of N(0,1) f16 values: [rows, n_kv, HD] (the reference's layout) or [n_kv, rows, HD]
-    (head-major, each kv head's rows contiguous). i8: int8 rows uniform in -127..127 and f32 scales in
-    [0.015, 0.035] ([rows, n_kv] or [n_kv, rows]); returns (k, v, k_scale, v_scale)."""
+    (head-major, each kv head's rows contiguous). i8: int8 rows round(40 N(0,1)) clipped to -127..127 and
+    f32 scales in [0.02, 0.03] ([rows, n_kv] or [n_kv, rows]), like quantised N(0,1) rows; returns
+    (k, v, k_scale, v_scale)."""
     shape = (rows, n_kv, HD) if layout == "reference" else (n_kv, rows, HD)
     if i8:
-        k = torch.randint(-127, 128, shape, generator=gen, device=dev, dtype=torch.int8)
-        v = torch.randint(-127, 128, shape, generator=gen, device=dev, dtype=torch.int8)
+        def ints():
+            x = torch.randn(shape, generator=gen, device=dev, dtype=torch.float32) * 40
+            return x.round().clamp(-127, 127).to(torch.int8)
+
+        k, v = ints(), ints()
         sc = shape[:2]
-        ks = torch.rand(sc, generator=gen, device=dev, dtype=torch.float32) * 0.02 + 0.015
-        vs = torch.rand(sc, generator=gen, device=dev, dtype=torch.float32) * 0.02 + 0.015
+        ks = torch.rand(sc, generator=gen, device=dev, dtype=torch.float32) * 0.01 + 0.02
+        vs = torch.rand(sc, generator=gen, device=dev, dtype=torch.float32) * 0.01 + 0.02
         return k, v, ks, vs
     k = torch.randn(shape, generator=gen, device=dev, dtype=torch.float32).half()
     v = torch.randn(shape, generator=gen, device=dev, dtype=torch.float32).half()
@@ -163,15 +168,15 @@ def prefill_flops(n, pos0, n_heads):
     return 4 * n_heads * HD * keys
 
 
-def prefill_workload(torch, gi_attn, dev, n, n_heads, n_kv, steps, warmup, seed):
+def prefill_workload(torch, gi_attn, dev, n, n_heads, n_kv, steps, warmup, seed, i8=False):
     gen = torch.Generator(device=dev)
     gen.manual_seed(seed)
     q = torch.randn((n, n_heads * HD), generator=gen, device=dev, dtype=torch.float32).half()
-    k, v = seeded_cache(gen, n, n_kv, dev, torch)
+    k, v, ks, vs = seeded_cache(gen, n, n_kv, dev, torch, i8=i8)
     out = torch.empty((n, n_heads * HD), device=dev, dtype=torch.float16)
 
     def step(i):
-        gi_attn.prefill(q, k, v, 0, n_heads, n_kv, out=out)
+        gi_attn.prefill(q, k, v, 0, n_heads, n_kv, out=out, k_scale=ks, v_scale=vs)
 
     t = time_steps(step, steps, warmup, torch)
     return {"seconds": t, "flops": prefill_flops(n, 0, n_heads), "step": step}
@@ -261,13 +266,13 @@ def cpu_baseline_decode(q, cache, pos0, n_heads, n_kv, budget_s=12.0):
     return times[len(times) // 2], threads, len(times)
 
 
-def prefill_roofline(gi_attn, r, steps, torch):
+def prefill_roofline(gi_attn, r, steps, torch, profile="pmc_prefill_prefill8k", kernel="gi_prefill_fwd"):
     """Roofline object of the prefill kernel: algorithmic flops of one launch / its mean duration."""
     ms, n = kernel_times(gi_attn, r["step"], steps, torch, ("prefill",))["prefill"]
     tf = r["flops"] / (ms / 1e3) / 1e12
     return {"bound": "mfma", "achieved": round(tf, 1), "peak": F16_DENSE_PEAK_TFLOPS, "unit": "TFLOP/s",
-            "frac": round(tf / F16_DENSE_PEAK_TFLOPS, 4), "traffic": profile_traffic("pmc_prefill_prefill8k"),
-            "kernel": "gi_prefill_fwd", "algorithmic_flops_per_launch": r["flops"],
+            "frac": round(tf / F16_DENSE_PEAK_TFLOPS, 4), "traffic": profile_traffic(profile),
+            "kernel": kernel, "algorithmic_flops_per_launch": r["flops"],
             "kernel_ms_per_launch": round(ms, 5), "launches_timed": n}
 
 
@@ -278,7 +283,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="decode64k",
                     choices=["decode64k", "decode4k", "verify", "prefill8k", "chunked", "qkrope", "decode64k_i8",
-                             "verify_i8"])
+                             "verify_i8", "prefill8k_i8"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--reference-layout", action="store_true",
@@ -364,14 +369,18 @@ def main():
                          "algorithmic_bytes_per_launch": r["bytes"], "kernel_ms_per_launch": round(ms, 5),
                          "launches_timed": n_l},
         })
-    elif w == "prefill8k":
-        log("[bench] config 3: causal prefill 8192 tokens, 32q/8kv")
-        r = prefill_workload(torch, gi_attn, dev, 8192, 32, 8, args.steps, args.warmup, 99)
+    elif w in ("prefill8k", "prefill8k_i8"):
+        i8 = w == "prefill8k_i8"
+        log(f"[bench] config 3: causal prefill 8192 tokens, 32q/8kv{' over the int8 cache' if i8 else ''}")
+        r = prefill_workload(torch, gi_attn, dev, 8192, 32, 8, args.steps, args.warmup, 99, i8=i8)
         tf = r["flops"] / r["seconds"] / 1e12
         result.update({
-            "value": round(tf, 1), "unit": "TFLOP/s", "ms_per_step": r["seconds"] * 1e3, "dtype": "f16 MFMA, f32 acc",
-            "config": {"workload": "config 3: causal prefill, 8192 tokens, 32q/8kv, hd 128", "flops_per_step": r["flops"]},
-            "roofline": prefill_roofline(gi_attn, r, args.steps, torch),
+            "value": round(tf, 1), "unit": "TFLOP/s", "ms_per_step": r["seconds"] * 1e3,
+            "dtype": "int8 K/V widened to f16 MFMA, f32 acc" if i8 else "f16 MFMA, f32 acc",
+            "config": {"workload": "config 3: causal prefill, 8192 tokens, 32q/8kv, hd 128" +
+                                   (", int8 cache" if i8 else ""), "flops_per_step": r["flops"]},
+            "roofline": prefill_roofline(gi_attn, r, args.steps, torch, f"pmc_prefill_{w}",
+                                         "gi_prefill_fwd_i8" if i8 else "gi_prefill_fwd"),
         })
     else:
         log("[bench] config 5: chunked prefill 131072 in 2048 chunks, 32q/4kv")

@@ -94,6 +94,10 @@ struct GiPrefillArgs {
     int q_f16;
     int out_f16;
     int pad_;
+    const float* ks;
+    const float* vs;
+    long long sc_stride;
+    long long sc_head_stride;
 };
 
 constexpr float kLog2e = 1.4426950408889634f;
@@ -132,7 +136,8 @@ struct Module {
     bool loaded = false;
     hipModule_t mod = nullptr;
     hipFunction_t dec[2][2][2] = {}; // [int8 cache][shared][column blocks - 1]
-    hipFunction_t combine = nullptr, prefill = nullptr, rope = nullptr;
+    hipFunction_t prefill[2] = {};   // [int8 cache]
+    hipFunction_t combine = nullptr, rope = nullptr;
     int prefill_threads = 0; // the prefill kernel's block size (its launch bound: waves x 64)
 };
 std::mutex g_mu;
@@ -170,7 +175,8 @@ int load_module(const char* path, Module** out) {
             {&m.dec[1][1][0], "gi_decode_shared_1_i8"},
             {&m.dec[1][1][1], "gi_decode_shared_2_i8"},
             {&m.combine, "gi_decode_combine"},
-            {&m.prefill, "gi_prefill_fwd"},
+            {&m.prefill[0], "gi_prefill_fwd"},
+            {&m.prefill[1], "gi_prefill_fwd_i8"},
             {&m.rope, "gi_qk_norm_rope"},
         };
         for (auto& f : fns)
@@ -179,7 +185,7 @@ int load_module(const char* path, Module** out) {
                 m.mod = nullptr;
                 return e;
             }
-        if (int e = check(hipFuncGetAttribute(&m.prefill_threads, HIP_FUNC_ATTRIBUTE_MAX_THREADS_PER_BLOCK, m.prefill),
+        if (int e = check(hipFuncGetAttribute(&m.prefill_threads, HIP_FUNC_ATTRIBUTE_MAX_THREADS_PER_BLOCK, m.prefill[0]),
                           "hipFuncGetAttribute(gi_prefill_fwd)")) {
             (void)hipModuleUnload(m.mod);
             m.mod = nullptr;
@@ -402,6 +408,58 @@ int rope_impl(void* stream, float* qkv, const float* qn, const float* kn, void* 
     return launch(kRope, m->rope, dim3(groups, n, 1), dim3(256), (hipStream_t)stream, &a, sizeof a);
 }
 
+// gi_attn_prefill and gi_attn_prefill_i8: the same launch with the f16 or the int8 kernel.
+int prefill_impl(void* stream, const void* q, int q_dtype, long long q_stride, const void* kc, const void* vc,
+                 const float* ks, const float* vs, long long sc_stride, long long sc_head_stride, bool i8,
+                 long long kv_stride, long long kv_head_stride, void* out, int out_dtype, long long out_stride, int pos0,
+                 int n, int n_heads, int n_kv, int hd, float scale) {
+    if (int e = check_shape(n_heads, n_kv, hd)) return e;
+    if (n <= 0 || pos0 < 0) return fail("n %d must be positive and pos0 %d >= 0", n, pos0);
+    if (!q || !kc || !vc || !out) return fail("null tensor pointer");
+    if ((q_dtype != GI_F32 && q_dtype != GI_F16) || (out_dtype != GI_F32 && out_dtype != GI_F16))
+        return fail("dtypes must be GI_F32 or GI_F16");
+    if (kv_head_stride == 0) kv_head_stride = hd;
+    if (int e = check_kv_strides(kv_stride, kv_head_stride, n_kv, hd, i8 ? 16 : 8)) return e;
+    if (i8)
+        if (int e = check_scales(ks, vs, sc_stride, sc_head_stride)) return e;
+    if (!aligned16(q) || !aligned16(kc) || !aligned16(vc) || !aligned16(out) ||
+        q_stride % (q_dtype == GI_F16 ? 8 : 4) || out_stride % (out_dtype == GI_F16 ? 8 : 4))
+        return fail("tensors must be 16-byte aligned with row strides of whole 16-byte units");
+    if (q_stride < (long long)n_heads * hd || out_stride < (long long)n_heads * hd)
+        return fail("row strides too small for %d heads", n_heads);
+    Module* m;
+    if (int e = load_module(nullptr, &m)) return e;
+    GiPrefillArgs a{};
+    a.q = q;
+    a.kc = (const uint16_t*)kc;
+    a.vc = (const uint16_t*)vc;
+    if (i8) {
+        a.ks = ks;
+        a.vs = vs;
+        a.sc_stride = sc_stride;
+        a.sc_head_stride = sc_head_stride;
+    }
+    a.out = out;
+    a.q_stride = q_stride;
+    a.kv_stride = kv_stride;
+    a.out_stride = out_stride;
+    a.kv_head_stride = kv_head_stride;
+    a.pos0 = pos0;
+    a.n = n;
+    a.n_heads = n_heads;
+    a.n_kv = n_kv;
+    a.qscale = scale * kLog2e;
+    a.q_f16 = q_dtype == GI_F16;
+    a.out_f16 = out_dtype == GI_F16;
+    const int bq = m->prefill_threads / 2; // query rows per workgroup: 32 per wave of 64 threads
+    int qtiles = (n + bq - 1) / bq;
+    return launch(kPrefill, m->prefill[i8], dim3(qtiles * n_heads, 1, 1), dim3(m->prefill_threads), (hipStream_t)stream, &a, sizeof a);
+}
+
+int attention_impl(void* stream, const float* qkv, const void* kc, const void* vc, const float* ks, const float* vs,
+                   bool i8, float* out, void* workspace, size_t workspace_bytes, int pos0, const int* posp, int ctx_cap,
+                   int n, int n_heads, int n_kv, int hd, int exact);
+
 } // namespace
 
 extern "C" {
@@ -458,63 +516,62 @@ int gi_attn_decode_i8(void* stream, const float* q, long long q_stride, const in
 int gi_attn_prefill(void* stream, const void* q, int q_dtype, long long q_stride, const uint16_t* kc,
                     const uint16_t* vc, long long kv_stride, long long kv_head_stride, void* out, int out_dtype,
                     long long out_stride, int pos0, int n, int n_heads, int n_kv, int hd, float scale) {
-    if (int e = check_shape(n_heads, n_kv, hd)) return e;
-    if (n <= 0 || pos0 < 0) return fail("n %d must be positive and pos0 %d >= 0", n, pos0);
-    if (!q || !kc || !vc || !out) return fail("null tensor pointer");
-    if ((q_dtype != GI_F32 && q_dtype != GI_F16) || (out_dtype != GI_F32 && out_dtype != GI_F16))
-        return fail("dtypes must be GI_F32 or GI_F16");
-    if (kv_head_stride == 0) kv_head_stride = hd;
-    if (int e = check_kv_strides(kv_stride, kv_head_stride, n_kv, hd)) return e;
-    if (!aligned16(q) || !aligned16(kc) || !aligned16(vc) || !aligned16(out) ||
-        q_stride % (q_dtype == GI_F16 ? 8 : 4) || out_stride % (out_dtype == GI_F16 ? 8 : 4))
-        return fail("tensors must be 16-byte aligned with row strides of whole 16-byte units");
-    if (q_stride < (long long)n_heads * hd || out_stride < (long long)n_heads * hd)
-        return fail("row strides too small for %d heads", n_heads);
-    Module* m;
-    if (int e = load_module(nullptr, &m)) return e;
-    GiPrefillArgs a{};
-    a.q = q;
-    a.kc = kc;
-    a.vc = vc;
-    a.out = out;
-    a.q_stride = q_stride;
-    a.kv_stride = kv_stride;
-    a.out_stride = out_stride;
-    a.kv_head_stride = kv_head_stride;
-    a.pos0 = pos0;
-    a.n = n;
-    a.n_heads = n_heads;
-    a.n_kv = n_kv;
-    a.qscale = scale * kLog2e;
-    a.q_f16 = q_dtype == GI_F16;
-    a.out_f16 = out_dtype == GI_F16;
-    const int bq = m->prefill_threads / 2; // query rows per workgroup: 32 per wave of 64 threads
-    int qtiles = (n + bq - 1) / bq;
-    return launch(kPrefill, m->prefill, dim3(qtiles * n_heads, 1, 1), dim3(m->prefill_threads), (hipStream_t)stream, &a, sizeof a);
+    return prefill_impl(stream, q, q_dtype, q_stride, kc, vc, nullptr, nullptr, 0, 0, false, kv_stride, kv_head_stride,
+                        out, out_dtype, out_stride, pos0, n, n_heads, n_kv, hd, scale);
+}
+
+int gi_attn_prefill_i8(void* stream, const void* q, int q_dtype, long long q_stride, const int8_t* kc, const int8_t* vc,
+                       const float* ks, const float* vs, long long kv_stride, long long kv_head_stride,
+                       long long sc_stride, long long sc_head_stride, void* out, int out_dtype, long long out_stride,
+                       int pos0, int n, int n_heads, int n_kv, int hd, float scale) {
+    if (sc_stride == 0 && sc_head_stride == 0) sc_stride = n_kv, sc_head_stride = 1;
+    return prefill_impl(stream, q, q_dtype, q_stride, kc, vc, ks, vs, sc_stride, sc_head_stride, true, kv_stride,
+                        kv_head_stride, out, out_dtype, out_stride, pos0, n, n_heads, n_kv, hd, scale);
 }
 
 int gi_attention(void* stream, const float* qkv, const uint16_t* kc, const uint16_t* vc, float* out,
                  void* workspace, size_t workspace_bytes, int pos0, const int* posp, int ctx_cap, int n, int n_heads,
                  int n_kv, int hd, int exact) {
+    return attention_impl(stream, qkv, kc, vc, nullptr, nullptr, false, out, workspace, workspace_bytes, pos0, posp,
+                          ctx_cap, n, n_heads, n_kv, hd, exact);
+}
+
+int gi_attention_i8(void* stream, const float* qkv, const int8_t* kc, const int8_t* vc, const float* ks,
+                    const float* vs, float* out, void* workspace, size_t workspace_bytes, int pos0, const int* posp,
+                    int ctx_cap, int n, int n_heads, int n_kv, int hd, int exact) {
+    return attention_impl(stream, qkv, kc, vc, ks, vs, true, out, workspace, workspace_bytes, pos0, posp, ctx_cap, n,
+                          n_heads, n_kv, hd, exact);
+}
+
+} // extern "C"
+
+namespace {
+// GpuModel::attention's dispatch over either cache type (the reference's layout, scales [pos][n_kv]).
+int attention_impl(void* stream, const float* qkv, const void* kc, const void* vc, const float* ks, const float* vs,
+                   bool i8, float* out, void* workspace, size_t workspace_bytes, int pos0, const int* posp, int ctx_cap,
+                   int n, int n_heads, int n_kv, int hd, int exact) {
     if (int e = check_shape(n_heads, n_kv, hd)) return e;
     if (n <= 0) return fail("n %d must be positive", n);
     const long long q_dim = (long long)n_heads * hd, kv_dim = (long long)n_kv * hd, row = q_dim + 2 * kv_dim;
     const float scale = 1.0f / std::sqrt((float)hd);
     if (n >= kTiledMinBatch && !exact) {
         if (posp) return fail("a device position (posp) is only taken by the split path");
-        return gi_attn_prefill(stream, qkv, GI_F32, row, kc, vc, kv_dim, hd, out, GI_F32, q_dim, pos0, n, n_heads,
-                               n_kv, hd, scale);
+        return prefill_impl(stream, qkv, GI_F32, row, kc, vc, ks, vs, n_kv, 1, i8, kv_dim, hd, out, GI_F32, q_dim, pos0,
+                            n, n_heads, n_kv, hd, scale);
     }
     for (int b0 = 0; b0 < n; b0 += kSplitMaxBatch) {
         int m = std::min(n - b0, kSplitMaxBatch);
         // with a device position every launch reads *posp, so only single launches take it
         if (posp && n > kSplitMaxBatch) return fail("posp takes at most %d tokens", kSplitMaxBatch);
-        if (int e = gi_attn_decode(stream, qkv + b0 * row, row, kc, vc, kv_dim, hd, out + b0 * q_dim, q_dim, workspace,
-                                   workspace_bytes, pos0 + b0, posp, ctx_cap, m, n_heads, n_kv, hd, scale))
+        if (int e = decode_impl(stream, qkv + b0 * row, row, kc, vc, ks, vs, n_kv, 1, i8, kv_dim, hd, out + b0 * q_dim,
+                                q_dim, workspace, workspace_bytes, pos0 + b0, posp, ctx_cap, m, n_heads, n_kv, hd, scale))
             return e;
     }
     return 0;
 }
+} // namespace
+
+extern "C" {
 
 
 int gi_kernel_timing(int on) {

@@ -652,6 +652,12 @@ struct GiPrefillArgs {
     int q_f16;
     int out_f16;
     int pad_;
+    // int8 cache only (gi_prefill_fwd_i8): kc / vc hold int8 rows in the same element layout; the f32 scale
+    // of position t, kv head h is at ks / vs [t*sc_stride + h*sc_head_stride]
+    const float* ks;
+    const float* vs;
+    long long sc_stride;
+    long long sc_head_stride;
 };
 
 #ifndef PF_WAVES
@@ -680,6 +686,10 @@ struct GiPrefillArgs {
 #define PF_KPF 8           // K fragments in flight in the QK loop
 #endif
 #define GI_LDS __attribute__((address_space(3)))
+// int8 cache: the value scale goes into the f16 probabilities times this power of two (undone at the
+// end) so that small products stay normal f16; with P <= 2^8 a dequantised |V| up to 127 * 65504 / (2^8 *
+// PF_I8_VBIAS) ~ 4000 fits (the reference biases by 2^10 with P <= 1, src/cuda.rs:2416-2420)
+#define PF_I8_VBIAS 8.f
 typedef short gi_s4 __attribute__((__vector_size__(8))); // 4 f16 as ds_read_b64_tr_b16 returns them
 
 // One workgroup = (head, 256 query rows); wave w of 8 owns rows 32w..32w+31 of the tile. Per 64-key tile:
@@ -707,8 +717,16 @@ typedef short gi_s4 __attribute__((__vector_size__(8))); // 4 f16 as ds_read_b64
 // tiles crossing the diagonal are masked. Work order: the grid is remapped so that each of the 8 XCDs
 // (blockIdx round-robin) walks a contiguous run of (kv head, query tile, head) items, longest query
 // tiles first, so one kv head's K/V stays in one XCD's L2.
-extern "C" __global__ void __launch_bounds__(64 * PF_WAVES, 1) gi_prefill_fwd(GiPrefillArgs a) {
+// I8 = true: an int8 cache (the reference's KV8 prefill, src/cuda.rs:2466-2498, 2548-2605): each thread
+// loads 16 bytes of a K row and of a V row of the tile into registers one iteration ahead, widens them to
+// exact f16 and writes them into the same swizzled LDS layout (so the MFMA operand reads are unchanged),
+// and the tile's 64 key and value scales go to LDS beside it. Scores are the integer-key dot products
+// times the key scale (QK chains start from zero; s = acc * kscale - m); P V takes f16(p * vscale *
+// PF_I8_VBIAS) and the row sum the f16-rounded p, as the reference's pv / pf.
+template <bool I8>
+__device__ __forceinline__ void gi_prefill_t(const GiPrefillArgs& a) {
     __shared__ __attribute__((aligned(1024))) unsigned char smem[PF_NBUF][2][PF_TILE]; // [buffer][K, V]
+    __shared__ __attribute__((aligned(16))) float scl[I8 ? PF_NBUF : 1][2][PF_BK];      // int8: [buffer][K, V] scales
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -746,6 +764,43 @@ extern "C" __global__ void __launch_bounds__(64 * PF_WAVES, 1) gi_prefill_fwd(Gi
 #pragma unroll
         for (int i = 0; i < PF_LPW; i++)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (GI_LDS void*)(dst + 1024 * i), 16, soff[i], 0, 0, 0);
+    };
+    // int8 staging: thread -> tile row sr, 16-byte chunk sch (dims 16sch..16sch+15) of K and of V; threads
+    // 0-63 also take the K scale of key tid, 64-127 the V scale of key tid-64 (times PF_I8_VBIAS)
+    const int sr = tid >> 3, sch = tid & 7;
+    const int8_t* kb8 = reinterpret_cast<const int8_t*>(a.kc) + kvh * a.kv_head_stride;
+    const int8_t* vb8 = reinterpret_cast<const int8_t*>(a.vc) + kvh * a.kv_head_stride;
+    const float* scb = I8 ? (tid < 64 ? a.ks : a.vs) + kvh * a.sc_head_stride : nullptr;
+    u4 rk = u4{0u, 0u, 0u, 0u}, rv = rk;
+    float rsc = 0.f;
+    auto load8 = [&](int t) {
+        const int t0 = t * PF_BK;
+        const int off = sr * (int)kvs + 16 * sch;
+        rk = gi_load16(gi_rsrc(kb8 + (long long)t0 * kvs, (long long)(kv_len - t0) * kvs), off);
+        rv = gi_load16(gi_rsrc(vb8 + (long long)t0 * kvs, (long long)(kv_len - t0) * kvs), off);
+        if (tid < 2 * PF_BK)
+            rsc = gi_load4f(gi_rsrc(scb + (long long)t0 * a.sc_stride, (long long)(kv_len - t0) * a.sc_stride * 4),
+                            (tid & (PF_BK - 1)) * (int)a.sc_stride * 4);
+    };
+    auto write8 = [&](int t) {
+        unsigned char* K = &smem[t & (PF_NBUF - 1)][0][sr * 256];
+        unsigned char* V = &smem[t & (PF_NBUF - 1)][1][sr * 256];
+#pragma unroll
+        for (int hw = 0; hw < 2; hw++) { // f16 units 2sch + hw: dims 16sch + 8hw .. +7
+            const int u = 2 * sch + hw;
+            u4 kw, vw;
+#pragma unroll
+            for (int e = 0; e < 2; e++) {
+                const uint32_t xk = rk[2 * hw + e] ^ 0x80808080u, xv = rv[2 * hw + e] ^ 0x80808080u;
+                kw[2 * e] = i8_f16x2(xk, GI_I8_LO);
+                kw[2 * e + 1] = i8_f16x2(xk, GI_I8_HI);
+                vw[2 * e] = i8_f16x2(xv, GI_I8_LO);
+                vw[2 * e + 1] = i8_f16x2(xv, GI_I8_HI);
+            }
+            *reinterpret_cast<u4*>(K + ((u ^ (sr & 15)) << 4)) = kw;
+            *reinterpret_cast<u4*>(V + ((u ^ ((sr & 3) << 2)) << 4)) = vw;
+        }
+        if (tid < 2 * PF_BK) scl[t & (PF_NBUF - 1)][tid >> 6][tid & (PF_BK - 1)] = tid < PF_BK ? rsc : rsc * PF_I8_VBIAS;
     };
 
     // ---- Q as B operands: lane (col = l%32, half = l/32), k-step ks: dims 16ks + 8*half .. +7
@@ -817,7 +872,24 @@ extern "C" __global__ void __launch_bounds__(64 * PF_WAVES, 1) gi_prefill_fwd(Gi
             if (st + PF_KPF < 16)
                 kf[st % PF_KPF] =
                     *reinterpret_cast<const h8*>(K + 8192 * ((st + PF_KPF) & 1) + kbase + 32 * (((st + PF_KPF) >> 1) ^ ky));
-            s[bb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(cur, qf[ks], ks == 0 ? negm : s[bb], 0, 0, 0);
+            s[bb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(cur, qf[ks], ks == 0 ? (I8 ? f16x{} : negm) : s[bb], 0, 0, 0);
+        }
+    };
+    // int8: scores of tile t (its QK sums in s) times their key scales, minus the reference max. Lane holds
+    // block bb, element 4i + jj: tile key 32bb + 16(i/2) + 8*half + 4(i%2) + jj
+    auto kscale = [&](int t, f16x* s) {
+        if constexpr (I8) {
+            const float* ksl = &scl[t & (PF_NBUF - 1)][0][8 * half];
+#pragma unroll
+            for (int bb = 0; bb < 2; bb++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const float4 k4 = *reinterpret_cast<const float4*>(ksl + 32 * bb + 16 * (i >> 1) + 4 * (i & 1));
+                    s[bb][4 * i] = fmaf(s[bb][4 * i], k4.x, -m_run);
+                    s[bb][4 * i + 1] = fmaf(s[bb][4 * i + 1], k4.y, -m_run);
+                    s[bb][4 * i + 2] = fmaf(s[bb][4 * i + 2], k4.z, -m_run);
+                    s[bb][4 * i + 3] = fmaf(s[bb][4 * i + 3], k4.w, -m_run);
+                }
         }
     };
 
@@ -826,13 +898,25 @@ extern "C" __global__ void __launch_bounds__(64 * PF_WAVES, 1) gi_prefill_fwd(Gi
     const int my_tiles = min(ntiles, wave_last / PF_BK + 1); // tiles this wave computes
     typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 
-    // Prologue: tiles 0-2 start loading; tile 0 is waited for and published, and its QK issued.
-    stage(0);
-    if (ntiles > 1) stage(1);
-    if (ntiles > 2) stage(2);
-    if (ntiles > 2) __builtin_amdgcn_s_waitcnt(GI_VMCNT(2 * PF_LPW)); // tile 0 is in
-    else if (ntiles > 1) __builtin_amdgcn_s_waitcnt(GI_VMCNT(PF_LPW));
-    else __builtin_amdgcn_s_waitcnt(GI_VMCNT(0));
+    // Prologue: tiles 0-2 start loading; tile 0 is waited for and published, and its QK issued. (int8:
+    // tiles 0 and 1 are loaded and written, tile 2's loads stay in flight into registers.)
+    if constexpr (I8) {
+        load8(0);
+        write8(0);
+        if (ntiles > 1) {
+            load8(1);
+            write8(1);
+        }
+        if (ntiles > 2) load8(2);
+        __builtin_amdgcn_s_waitcnt(0xC07F); // lgkmcnt(0): this thread's LDS writes are done
+    } else {
+        stage(0);
+        if (ntiles > 1) stage(1);
+        if (ntiles > 2) stage(2);
+        if (ntiles > 2) __builtin_amdgcn_s_waitcnt(GI_VMCNT(2 * PF_LPW)); // tile 0 is in
+        else if (ntiles > 1) __builtin_amdgcn_s_waitcnt(GI_VMCNT(PF_LPW));
+        else __builtin_amdgcn_s_waitcnt(GI_VMCNT(0));
+    }
     asm volatile("s_barrier" ::: "memory");
     // One pipeline step: tile it's softmax and PV, with QK of tile it+1 into sn (past this wave's last
     // tile that QK reads a stale buffer and is never used). No branch separates the QK MFMAs from the
@@ -880,10 +964,17 @@ extern "C" __global__ void __launch_bounds__(64 * PF_WAVES, 1) gi_prefill_fwd(Gi
 #pragma unroll
             for (int e = 0; e < 8; e += 2) {
                 const int i = 2 * (ks & 1) + (e >> 2), jj = e & 3;
-                const _Float16 h0 = (_Float16)__builtin_amdgcn_exp2f(s[bb][4 * i + jj]);
-                const _Float16 h1 = (_Float16)__builtin_amdgcn_exp2f(s[bb][4 * i + jj + 1]);
-                pf[e] = h0;
-                pf[e + 1] = h1;
+                const float p0 = __builtin_amdgcn_exp2f(s[bb][4 * i + jj]);
+                const float p1 = __builtin_amdgcn_exp2f(s[bb][4 * i + jj + 1]);
+                const _Float16 h0 = (_Float16)p0, h1 = (_Float16)p1;
+                if constexpr (I8) { // P V takes p times the value scale; the row sum the rounded p
+                    const float* vsl = &scl[it & (PF_NBUF - 1)][1][32 * bb + 16 * (i >> 1) + 8 * half + 4 * (i & 1) + jj];
+                    pf[e] = (_Float16)(p0 * vsl[0]);
+                    pf[e + 1] = (_Float16)(p1 * vsl[1]);
+                } else {
+                    pf[e] = h0;
+                    pf[e + 1] = h1;
+                }
                 l_run = __builtin_amdgcn_fdot2(h2{h0, h1}, h2{(_Float16)1.f, (_Float16)1.f}, l_run, false);
             }
 #pragma unroll
@@ -896,6 +987,7 @@ extern "C" __global__ void __launch_bounds__(64 * PF_WAVES, 1) gi_prefill_fwd(Gi
                 o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf, o[db], 0, 0, 0);
             }
         }
+        kscale(it + 1, sn);
         mx = rowmax(sn); // unmasked: a diagonal tile recomputes it after masking
         // Instruction order of the block (the compiler's scheduler follows these groups in sequence):
         // QK phase, per QK MFMA: one LDS read (the K fragment PF_KPF steps on, then V fragments of the first
@@ -940,11 +1032,25 @@ extern "C" __global__ void __launch_bounds__(64 * PF_WAVES, 1) gi_prefill_fwd(Gi
     // whose buffer then takes tile it+3. Barriers are bare s_barrier (__syncthreads' release fence would
     // also wait for tile it+2's loads); the memory clobber keeps LDS accesses on their side.
     float mx = GI_NEG_INF;
+    // int8: the registers loaded in iteration it-1 (tile it+2) are written into its buffer (free: every wave
+    // has passed tile it-2) right after the barrier, and tile it+3's loads go out; a wave's LDS writes are
+    // complete before the next barrier publishes them.
     auto iteration = [&](int it, f16x* s, f16x* sn) {
-        if (it + 2 < ntiles) __builtin_amdgcn_s_waitcnt(GI_VMCNT(PF_LPW)); // tile it+2's loads may stay in flight
-        else __builtin_amdgcn_s_waitcnt(GI_VMCNT(0));
+        if constexpr (I8) {
+            __builtin_amdgcn_s_waitcnt(0xC07F); // lgkmcnt(0)
+        } else {
+            if (it + 2 < ntiles) __builtin_amdgcn_s_waitcnt(GI_VMCNT(PF_LPW)); // tile it+2's loads may stay in flight
+            else __builtin_amdgcn_s_waitcnt(GI_VMCNT(0));
+        }
         asm volatile("s_barrier" ::: "memory");
-        if (it + 3 < ntiles) stage(it + 3);
+        if constexpr (I8) {
+            if (it + 2 < ntiles) {
+                write8(it + 2);
+                if (it + 3 < ntiles) load8(it + 3);
+            }
+        } else {
+            if (it + 3 < ntiles) stage(it + 3);
+        }
         if (it < my_tiles) {
             const int t0 = it * PF_BK;
             if (t0 + PF_BK - 1 > wave_first) { // the tile crosses the diagonal (or the end) somewhere in the wave
@@ -965,6 +1071,7 @@ extern "C" __global__ void __launch_bounds__(64 * PF_WAVES, 1) gi_prefill_fwd(Gi
     f16x sa[2], sb[2]; // scores of alternate tiles
     if (my_tiles > 0) {
         qk(0, sa);
+        kscale(0, sa);
         mx = rowmax(sa);
     }
     for (int it = 0; it < ntiles; it += 2) {
@@ -975,7 +1082,7 @@ extern "C" __global__ void __launch_bounds__(64 * PF_WAVES, 1) gi_prefill_fwd(Gi
     // ---- normalise and write: lane holds query qcol, dims 32db + 8i + 4*half + jj
     float l = l_run + __shfl_xor(l_run, 32, 64);
     if (qrow < a.n) {
-        const float inv = 1.f / l;
+        const float inv = (I8 ? 1.f / PF_I8_VBIAS : 1.f) / l;
         if (a.out_f16) {
             _Float16* op = (_Float16*)a.out + (long long)qrow * a.out_stride + h * 128 + 4 * half;
 #pragma unroll
@@ -997,6 +1104,9 @@ extern "C" __global__ void __launch_bounds__(64 * PF_WAVES, 1) gi_prefill_fwd(Gi
         }
     }
 }
+
+extern "C" __global__ void __launch_bounds__(64 * PF_WAVES, 1) gi_prefill_fwd(GiPrefillArgs a) { gi_prefill_t<false>(a); }
+extern "C" __global__ void __launch_bounds__(64 * PF_WAVES, 1) gi_prefill_fwd_i8(GiPrefillArgs a) { gi_prefill_t<true>(a); }
 
 // ------------------------------------------------------------------------------------------------ KV store
 

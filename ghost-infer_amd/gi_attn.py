@@ -34,7 +34,9 @@ SYMBOLS = (
     "gi_attn_decode",
     "gi_attn_decode_i8",
     "gi_attn_prefill",
+    "gi_attn_prefill_i8",
     "gi_attention",
+    "gi_attention_i8",
     "gi_qk_norm_rope",
     "gi_qk_norm_rope_i8",
     "gi_kernel_timing",
@@ -75,6 +77,10 @@ def load_library(path=LIB_PATH):
     lib.gi_attn_prefill.restype = i
     lib.gi_attention.argtypes = [vp, vp, vp, vp, vp, vp, sz, i, vp, i, i, i, i, i, i]
     lib.gi_attention.restype = i
+    lib.gi_attn_prefill_i8.argtypes = [vp, vp, i, ll, vp, vp, vp, vp, ll, ll, ll, ll, vp, i, ll, i, i, i, i, i, f]
+    lib.gi_attn_prefill_i8.restype = i
+    lib.gi_attention_i8.argtypes = [vp, vp, vp, vp, vp, vp, vp, vp, sz, i, vp, i, i, i, i, i, i]
+    lib.gi_attention_i8.restype = i
     lib.gi_qk_norm_rope.argtypes = [vp, vp, vp, vp, vp, vp, ll, ll, i, vp, i, i, i, i, i, f, vp, i, f]
     lib.gi_qk_norm_rope.restype = i
     lib.gi_qk_norm_rope_i8.argtypes = [vp, vp, vp, vp, vp, vp, vp, vp, ll, ll, ll, ll, i, vp, i, i, i, i, i, f, vp, i,
@@ -217,15 +223,20 @@ def decode(q, k_cache, v_cache, pos0, n_heads, n_kv, hd=128, scale=None, out=Non
 
 
 def prefill(q, k_cache, v_cache, pos0, n_heads, n_kv, hd=128, scale=None, out=None, out_dtype=None,
-            kv_layout="reference"):
+            kv_layout="reference", k_scale=None, v_scale=None):
     """Causal prefill of n = q.shape[0] tokens at positions pos0..pos0+n-1 (their K/V already cached).
 
-    q: f32 or f16 [n, >= n_heads*hd]; returns [n, n_heads*hd] of out_dtype (default: q's dtype).
+    q: f32 or f16 [n, >= n_heads*hd]; caches f16, or int8 with f32 k_scale / v_scale; returns
+    [n, n_heads*hd] of out_dtype (default: q's dtype).
     """
     if q.dtype not in (torch.float32, torch.float16):
         raise GiAttnError("q must be float32 or float16")
     _need(q, "q", q.dtype)
-    kv_stride, kv_head_stride, capacity = _cache_layout(k_cache, v_cache, n_kv, hd, kv_layout)
+    kv_stride, kv_head_stride, capacity = _cache_layout(k_cache, v_cache, n_kv, hd, kv_layout,
+                                                        (torch.float16, torch.int8))
+    i8 = k_cache.dtype == torch.int8
+    if i8:
+        sc = _scale_layout(k_scale, v_scale, n_kv, capacity, kv_layout)
     n = q.shape[0]
     if capacity < pos0 + n:
         raise GiAttnError(f"the cache holds {capacity} positions; {pos0 + n} needed")
@@ -237,27 +248,36 @@ def prefill(q, k_cache, v_cache, pos0, n_heads, n_kv, hd=128, scale=None, out=No
         raise GiAttnError("out must be float32 or float16")
     _need(out, "out", out.dtype)
     lib = load_library()
-    _check(lib.gi_attn_prefill(_stream(), _ptr(q), GI_F16 if q.dtype == torch.float16 else GI_F32, q.stride(0),
-                               _ptr(k_cache), _ptr(v_cache), kv_stride, kv_head_stride, _ptr(out),
-                               GI_F16 if out.dtype == torch.float16 else GI_F32, out.stride(0), pos0, n, n_heads,
-                               n_kv, hd, scale))
+    qd = GI_F16 if q.dtype == torch.float16 else GI_F32
+    od = GI_F16 if out.dtype == torch.float16 else GI_F32
+    if i8:
+        _check(lib.gi_attn_prefill_i8(_stream(), _ptr(q), qd, q.stride(0), _ptr(k_cache), _ptr(v_cache), _ptr(k_scale),
+                                      _ptr(v_scale), kv_stride, kv_head_stride, sc[0], sc[1], _ptr(out), od,
+                                      out.stride(0), pos0, n, n_heads, n_kv, hd, scale))
+    else:
+        _check(lib.gi_attn_prefill(_stream(), _ptr(q), qd, q.stride(0), _ptr(k_cache), _ptr(v_cache), kv_stride,
+                                   kv_head_stride, _ptr(out), od, out.stride(0), pos0, n, n_heads, n_kv, hd, scale))
     return out
 
 
 def attention(qkv, k_cache, v_cache, pos0, n_heads, n_kv, hd=128, exact=False, out=None, workspace=None,
-              posp=None, ctx_cap=0):
+              posp=None, ctx_cap=0, k_scale=None, v_scale=None):
     """GpuModel::attention (src/cuda.rs:8448-8541) for one layer.
 
     qkv: f32 [n, n_heads*hd + 2*n_kv*hd] rows [q | k | v] (only q is read: the cache already holds this
     batch's K/V rows, as qk_norm_rope wrote them); returns f32 [n, n_heads*hd]. n >= 16 and not exact ->
-    causal prefill kernel; otherwise the split decode path, 15 tokens per launch.
+    causal prefill kernel; otherwise the split decode path, 15 tokens per launch. The caches are the
+    reference's [capacity, n_kv, hd]: f16, or int8 with f32 scales [capacity, n_kv] (its (kc, vc, ks, vs)).
     """
     _need(qkv, "qkv", torch.float32)
     n = qkv.shape[0]
     row = n_heads * hd + 2 * n_kv * hd
     if qkv.shape[1] != row or not qkv.is_contiguous():
         raise GiAttnError(f"qkv must be contiguous [n, {row}]")
-    _, _, capacity = _cache_layout(k_cache, v_cache, n_kv, hd, "reference")
+    _, _, capacity = _cache_layout(k_cache, v_cache, n_kv, hd, "reference", (torch.float16, torch.int8))
+    i8 = k_cache.dtype == torch.int8
+    if i8:
+        _scale_layout(k_scale, v_scale, n_kv, capacity, "reference")
     if capacity < max(pos0 + n, ctx_cap if posp is not None else 0):
         raise GiAttnError(f"the cache holds {capacity} positions; {pos0 + n} needed")
     if out is None:
@@ -272,8 +292,13 @@ def attention(qkv, k_cache, v_cache, pos0, n_heads, n_kv, hd=128, exact=False, o
             workspace = new_workspace(cap, min(n, SPLIT_MAX_BATCH), n_heads, n_kv, hd, qkv.device)
         ws_ptr, ws_bytes = _ptr(workspace), workspace.numel() * workspace.element_size()
     lib = load_library()
-    _check(lib.gi_attention(_stream(), _ptr(qkv), _ptr(k_cache), _ptr(v_cache), _ptr(out), ws_ptr, ws_bytes, pos0,
-                            _ptr(posp), ctx_cap, n, n_heads, n_kv, hd, 1 if exact else 0))
+    if i8:
+        _check(lib.gi_attention_i8(_stream(), _ptr(qkv), _ptr(k_cache), _ptr(v_cache), _ptr(k_scale), _ptr(v_scale),
+                                   _ptr(out), ws_ptr, ws_bytes, pos0, _ptr(posp), ctx_cap, n, n_heads, n_kv, hd,
+                                   1 if exact else 0))
+    else:
+        _check(lib.gi_attention(_stream(), _ptr(qkv), _ptr(k_cache), _ptr(v_cache), _ptr(out), ws_ptr, ws_bytes, pos0,
+                                _ptr(posp), ctx_cap, n, n_heads, n_kv, hd, 1 if exact else 0))
     return out
 
 

@@ -91,6 +91,15 @@ int gi_attn_prefill(void* stream, const void* q, int q_dtype, long long q_stride
                     const uint16_t* vc, long long kv_stride, long long kv_head_stride, void* out, int out_dtype,
                     long long out_stride, int pos0, int n, int n_heads, int n_kv, int hd, float scale);
 
+/* gi_attn_prefill over an int8 KV cache (layouts and scales as gi_attn_decode_i8). The keys enter the
+ * scores as exact integers times their scale; P V takes f16(p * vs) and the row sum the f16-rounded p.
+ * Dequantised values must stay within |v| < 4000 (the f16 range of p * vs with p <= 256). Replaces:
+ * attention_prefill_tc128 compiled with KV8 (src/cuda.rs:2408-2621, int8 staging src/cuda.rs:2466-2498). */
+int gi_attn_prefill_i8(void* stream, const void* q, int q_dtype, long long q_stride, const int8_t* kc, const int8_t* vc,
+                       const float* ks, const float* vs, long long kv_stride, long long kv_head_stride,
+                       long long sc_stride, long long sc_head_stride, void* out, int out_dtype, long long out_stride,
+                       int pos0, int n, int n_heads, int n_kv, int hd, float scale);
+
 /* The attention operator of one layer, as GpuModel::attention (src/cuda.rs:8448-8541) dispatches it:
  * qkv rows are [q (n_heads*hd) | k | v] f32 (stride n_heads*hd + 2*n_kv*hd, src/cuda.rs:1713), out rows
  * n_heads*hd f32. Batches of >= 16 tokens that are not `exact` (verify) go to prefill; the rest to the
@@ -100,6 +109,12 @@ int gi_attn_prefill(void* stream, const void* q, int q_dtype, long long q_stride
 int gi_attention(void* stream, const float* qkv, const uint16_t* kc, const uint16_t* vc, float* out,
                  void* workspace, size_t workspace_bytes, int pos0, const int* posp, int ctx_cap, int n, int n_heads,
                  int n_kv, int hd, int exact);
+
+/* gi_attention over the reference's int8 cache: kc / vc int8 [position][n_kv][hd] with f32 scales ks / vs
+ * [position][n_kv], the operator's (kc, vc, ks, vs) tuple (src/cuda.rs:8448-8541 with KV8). */
+int gi_attention_i8(void* stream, const float* qkv, const int8_t* kc, const int8_t* vc, const float* ks,
+                    const float* vs, float* out, void* workspace, size_t workspace_bytes, int pos0, const int* posp,
+                    int ctx_cap, int n, int n_heads, int n_kv, int hd, int exact);
 
 /* The layer's step before attention, for a batch of n tokens at positions pos0.. (posp: read from device
  * memory, graph replay). qkv: f32 rows [q (n_heads*hd) | k (n_kv*hd) | v (n_kv*hd)], updated in place:

@@ -18,6 +18,8 @@
 //                                     RMSNorm of q/k heads, RoPE, K/V rows into the f16 cache
 //   gio_kv_quant_i8                   src/cuda.rs:333-339 (kv_store with KV8: row max / 127, rint)
 //   gio_qk_norm_rope_i8               src/cuda.rs:437-486 storing with kv_quant_i8
+//   gio_prefill_tc_i8                 gio_prefill_tc over the KV8 cache (src/cuda.rs:2466-2498, 2548-2605:
+//                                     integer keys, score times key scale, P V with f16(p * vs * 2^10))
 //   gio_decode_gpu_i8                 gio_decode_gpu over the KV8 cache (src/cuda.rs:209-226, 1758-1760,
 //                                     1821-1827: key scale on the score, value scale on the weight)
 //
@@ -368,10 +370,15 @@ void decode_gpu(const float* qkv, long q_stride, const KV_T* kc, const KV_T* vc,
 // Per query row: Q rounded to f16 after scaling by scale*log2(e); per 32-key tile S = f16 Q . f16 K in f32;
 // mask keys past the row's position; running max in base 2; P = f16(exp2(s - m)); l = alpha*l + sum(P);
 // O = alpha*O + P V; out = O / l.
-void prefill_tc(const float* q, long q_stride, const uint16_t* kc, const uint16_t* vc, long kv_stride, float* out,
-                long out_stride, int pos0, int n, int n_heads, int n_kv, float scale, int threads) {
+// KV_T = int8_t: the KV8 build (src/cuda.rs:2466-2498, 2548-2605): keys staged as exact integers, the score
+// times the key's scale; P V takes f16(p * vscale * 2^10) and the row sum the f16-rounded p; out = O / 2^10 / l.
+template <typename KV_T>
+void prefill_tc(const float* q, long q_stride, const KV_T* kc, const KV_T* vc, const float* ks, const float* vs,
+                long kv_stride, float* out, long out_stride, int pos0, int n, int n_heads, int n_kv, float scale,
+                int threads) {
     const int hd = 128, BK = 32, G = n_heads / n_kv;
     const float* W = widen().v;
+    const float vbias = ks ? 1024.f : 1.f;
     const float qs = scale * 1.4426950408889634f;
     const int kv_len = pos0 + n;
     auto row_task = [&](long idx) {
@@ -389,30 +396,32 @@ void prefill_tc(const float* q, long q_stride, const uint16_t* kc, const uint16_
             for (int j = 0; j < BK; j++) {
                 int kp = t0 + j;
                 if (kp > p_row || kp >= kv_len) { s[j] = -std::numeric_limits<float>::infinity(); continue; }
-                const uint16_t* kt = kc + (long)kp * kv_stride + kvh * hd;
+                const KV_T* kt = kc + (long)kp * kv_stride + kvh * hd;
                 float a = 0.f;
-                for (int d = 0; d < hd; d++) a += qh[d] * W[kt[d]];
-                s[j] = a;
-                mx = std::max(mx, a);
+                for (int d = 0; d < hd; d++) a += qh[d] * kv_value(kt[d]);
+                s[j] = ks ? a * ks[(long)kp * n_kv + kvh] : a;
+                mx = std::max(mx, s[j]);
             }
             float mn = std::max(m, mx);
             float alpha = std::exp2(m - mn);
             m = mn;
-            float p[32], psum = 0.f;
+            float p[32], pv[32], psum = 0.f;
             for (int j = 0; j < BK; j++) {
-                p[j] = W[f32_to_f16(std::exp2(s[j] - mn))];
+                const float e = std::exp2(s[j] - mn);
+                p[j] = W[f32_to_f16(e)];
+                pv[j] = vs && t0 + j < kv_len ? W[f32_to_f16(e * (vs[(long)(t0 + j) * n_kv + kvh] * vbias))] : p[j];
                 psum += p[j];
             }
             l = l * alpha + psum;
             for (int d = 0; d < hd; d++) o[d] *= alpha;
             for (int j = 0; j < BK; j++) {
                 int kp = t0 + j;
-                if (p[j] == 0.f || kp >= kv_len) continue;
-                const uint16_t* vt = vc + (long)kp * kv_stride + kvh * hd;
-                for (int d = 0; d < hd; d++) o[d] += p[j] * W[vt[d]];
+                if (pv[j] == 0.f || kp >= kv_len) continue;
+                const KV_T* vt = vc + (long)kp * kv_stride + kvh * hd;
+                for (int d = 0; d < hd; d++) o[d] += pv[j] * kv_value(vt[d]);
             }
         }
-        float inv = 1.f / l;
+        float inv = (1.f / vbias) / l;
         for (int d = 0; d < hd; d++) out[(long)r * out_stride + (long)h * hd + d] = o[d] * inv;
     };
     parallel_for((long)n * n_heads, threads, row_task);
@@ -541,7 +550,15 @@ void gio_kv_quant_i8(const float* src, long rows, int hd, int8_t* dst, float* sc
 // attn_prefill_tc<128> semantics (f16 rounding of the scaled Q and of P).
 void gio_prefill_tc(const float* q, long q_stride, const uint16_t* kc, const uint16_t* vc, long kv_stride, float* out,
                     long out_stride, int pos0, int n, int n_heads, int n_kv, float scale, int threads) {
-    prefill_tc(q, q_stride, kc, vc, kv_stride, out, out_stride, pos0, n, n_heads, n_kv, scale, threads);
+    prefill_tc<uint16_t>(q, q_stride, kc, vc, nullptr, nullptr, kv_stride, out, out_stride, pos0, n, n_heads, n_kv, scale,
+                         threads);
+}
+
+// attn_prefill_tc<128> with the KV8 cache: kc / vc int8 rows, ks / vs f32 scales [pos][n_kv].
+void gio_prefill_tc_i8(const float* q, long q_stride, const int8_t* kc, const int8_t* vc, const float* ks,
+                       const float* vs, long kv_stride, float* out, long out_stride, int pos0, int n, int n_heads,
+                       int n_kv, float scale, int threads) {
+    prefill_tc<int8_t>(q, q_stride, kc, vc, ks, vs, kv_stride, out, out_stride, pos0, n, n_heads, n_kv, scale, threads);
 }
 
 // qk_norm_rope storing into an int8 cache (kv_store with KV8, src/cuda.rs:333-339): kc / vc int8 rows in the

@@ -43,15 +43,19 @@ def assert_close(got, want, max_abs=MAX_ABS_TOL, rel_l2=REL_L2_TOL, what=""):
 
 
 def make_inputs_i8(seed, n_tok, ctx, n_heads, n_kv, hd=128):
-    """Seeded int8-cache inputs: q f32 [n_tok, n_heads*hd] N(0,1); K/V int8 [ctx, n_kv*hd] uniform in
-    -127..127; scales f32 [ctx, n_kv] uniform in [0.015, 0.035] (about what N(0,1) rows quantise to).
-    One generator per tensor: seed .. seed + 4."""
+    """Seeded int8-cache inputs shaped like N(0,1) rows quantised by kv_store: q f32 [n_tok, n_heads*hd]
+    N(0,1); K/V int8 [ctx, n_kv*hd] = round(40 * N(0,1)) clipped to -127..127; scales f32 [ctx, n_kv]
+    uniform in [0.02, 0.03] (dequantised values have a standard deviation near 1). One generator per
+    tensor: seed .. seed + 4."""
     q = np.random.default_rng(seed).standard_normal((n_tok, n_heads * hd), dtype=np.float32)
-    k = np.random.default_rng(seed + 1).integers(-127, 128, (ctx, n_kv * hd), dtype=np.int8)
-    v = np.random.default_rng(seed + 2).integers(-127, 128, (ctx, n_kv * hd), dtype=np.int8)
-    ks = np.random.default_rng(seed + 3).uniform(0.015, 0.035, (ctx, n_kv)).astype(np.float32)
-    vs = np.random.default_rng(seed + 4).uniform(0.015, 0.035, (ctx, n_kv)).astype(np.float32)
-    return q, k, v, ks, vs
+
+    def ints(g):
+        x = np.random.default_rng(g).standard_normal((ctx, n_kv * hd), dtype=np.float32) * 40
+        return np.clip(np.rint(x), -127, 127).astype(np.int8)
+
+    ks = np.random.default_rng(seed + 3).uniform(0.02, 0.03, (ctx, n_kv)).astype(np.float32)
+    vs = np.random.default_rng(seed + 4).uniform(0.02, 0.03, (ctx, n_kv)).astype(np.float32)
+    return q, ints(seed + 1), ints(seed + 2), ks, vs
 
 
 def dequant_f64(c, sc, n_kv, hd=128):

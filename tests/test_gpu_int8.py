@@ -219,3 +219,84 @@ def test_qk_norm_rope_i8_then_decode_matches_the_oracle_pipeline(gpu):
     out = gi_attn.decode(qt[:, :n_heads * hd], kt, vt, pos, n_heads, n_kv, k_scale=kst, v_scale=vst)
     torch.cuda.synchronize()
     assert_close(out.cpu().numpy(), want, what="qk_norm_rope i8 + decode i8 vs oracle")
+
+
+# ---------------------------------------------------------------- prefill (attention_prefill_tc with KV8)
+
+PREFILL_I8_SHAPES = [
+    # (n, pos0, n_heads, n_kv, q dtype, out dtype, layout): tile and diagonal edges, chunks at a prefix,
+    # partial last tiles, both layouts
+    (16, 0, 8, 2, np.float16, torch.float32, "reference"),
+    (64, 0, 8, 2, np.float32, torch.float32, "reference"),
+    (129, 0, 8, 8, np.float16, torch.float32, "reference"),
+    (300, 0, 32, 4, np.float32, torch.float32, "head_major"),
+    (70, 130, 8, 4, np.float16, torch.float32, "reference"),
+    (256, 256, 32, 4, np.float16, torch.float16, "head_major"),
+    (1000, 24, 16, 2, np.float16, torch.float32, "reference"),
+]
+
+
+def run_prefill_i8(q, k, v, ks, vs, pos0, n_heads, n_kv, dev, layout="reference", out_dtype=torch.float32):
+    qt, kt, vt, kst, vst = to_dev_i8(q, k, v, ks, vs, dev, layout, n_kv)
+    out = gi_attn.prefill(qt, kt, vt, pos0, n_heads, n_kv, out_dtype=out_dtype, kv_layout=layout, k_scale=kst,
+                          v_scale=vst)
+    torch.cuda.synchronize()
+    return out.float().cpu().numpy()
+
+
+@pytest.mark.parametrize("n,pos0,n_heads,n_kv,qd,od,layout", PREFILL_I8_SHAPES)
+def test_prefill_i8_small(gpu, n, pos0, n_heads, n_kv, qd, od, layout):
+    say("prefill i8", n, pos0, n_heads, n_kv, qd.__name__, od, layout)
+    q, k, v, ks, vs = make_inputs_i8(8000 + n + pos0, n, pos0 + n, n_heads, n_kv)
+    q = q.astype(qd)
+    got = run_prefill_i8(q, k, v, ks, vs, pos0, n_heads, n_kv, gpu, layout, od)
+    q32 = q.astype(np.float32)
+    assert_close(got, O.prefill_tc_semantics_i8(q32, k, v, ks, vs, pos0, n_heads, n_kv),
+                 what="prefill i8 vs oracle (reference int8 prefill semantics)")
+    assert_close(got, reference_f64_i8(q32, k, v, ks, vs, pos0, n_heads, n_kv), what="prefill i8 vs f64")
+
+
+def test_prefill_i8_8192(gpu):
+    # config 3's shape over an int8 cache: the whole output against a torch fp32 reference over the
+    # dequantised cache (on the GPU), sampled rows against the float64 reference
+    n, n_heads, n_kv = 8192, 32, 8
+    say("prefill i8 8192 32q/8kv")
+    q, k, v, ks, vs = make_inputs_i8(9, n, n, n_heads, n_kv)
+    q = q.astype(np.float16)
+    qt, kt, vt, kst, vst = to_dev_i8(q, k, v, ks, vs, gpu)
+    out = gi_attn.prefill(qt, kt, vt, 0, n_heads, n_kv, out_dtype=torch.float16, k_scale=kst, v_scale=vst)
+    kd = (kt.view(n, n_kv, 128).float() * kst[:, :, None]).view(n, -1)
+    vd = (vt.view(n, n_kv, 128).float() * vst[:, :, None]).view(n, -1)
+    G = n_heads // n_kv
+    Q = qt.view(n, n_heads, 128).float()
+    K, V = kd.view(n, n_kv, 128), vd.view(n, n_kv, 128)
+    mask = torch.arange(n, device=gpu)[None, :] > torch.arange(n, device=gpu)[:, None]
+    ref = torch.empty((n, n_heads, 128), dtype=torch.float32, device=gpu)
+    for h in range(n_heads):
+        s = (Q[:, h] @ K[:, h // G].T) / 128 ** 0.5
+        s.masked_fill_(mask, float("-inf"))
+        ref[:, h] = torch.softmax(s, dim=-1) @ V[:, h // G]
+    torch.cuda.synchronize()
+    got = out.float().cpu().numpy()
+    assert_close(got, ref.view(n, -1).cpu().numpy(), what="prefill i8 8192 vs torch fp32")
+    for r in (0, 63, 64, 1000, 8191):
+        assert_close(got[r:r + 1], reference_f64_i8(q[r:r + 1].astype(np.float32), k, v, ks, vs, r, n_heads, n_kv),
+                     what=f"prefill i8 row {r} vs f64")
+
+
+@pytest.mark.parametrize("n,pos0,exact", [(1, 99, False), (8, 300, True), (20, 0, False), (40, 17, True)])
+def test_attention_operator_i8(gpu, n, pos0, exact):
+    # GpuModel::attention over the int8 cache: prefill for >= 16 tokens unless exact, the split path otherwise
+    say("operator i8", n, pos0, exact)
+    n_heads, n_kv, hd = 32, 8, 128
+    row = n_heads * hd + 2 * n_kv * hd
+    qkv = np.random.default_rng(95 + n).standard_normal((n, row), dtype=np.float32)
+    _, k, v, ks, vs = make_inputs_i8(96 + n, 1, pos0 + n, n_heads, n_kv)
+    qkv_t = torch.from_numpy(qkv).to(gpu)
+    _, kt, vt, kst, vst = to_dev_i8(qkv[:, :1], k, v, ks, vs, gpu)
+    out = gi_attn.attention(qkv_t, kt, vt, pos0, n_heads, n_kv, exact=exact, k_scale=kst, v_scale=vst)
+    torch.cuda.synchronize()
+    q = np.ascontiguousarray(qkv[:, :n_heads * hd])
+    split_path = n < 16 or exact
+    assert_close(out.cpu().numpy(), reference_f64_i8(q, k, v, ks, vs, pos0, n_heads, n_kv),
+                 max_abs=2e-5 if split_path else 2e-3, rel_l2=2e-5 if split_path else 1e-3, what="operator i8 vs f64")

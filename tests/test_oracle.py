@@ -397,3 +397,26 @@ def test_rope_i8_stores_the_quantised_rows(hd, neox):
         np.testing.assert_allclose(scales[pos0:pos0 + n], np.abs(want).max(axis=2) / 127, rtol=1e-6)
         assert not cache[:pos0].any() and not cache[pos0 + n:].any()
         assert np.all(scales[:pos0] == -1) and np.all(scales[pos0 + n:] == -1)
+
+
+@pytest.mark.parametrize("n,pos0,n_heads,n_kv", [(64, 0, 8, 2), (100, 0, 4, 1), (70, 130, 8, 4)])
+def test_prefill_tc_semantics_i8_within_parity_bar(n, pos0, n_heads, n_kv):
+    # the reference's int8 prefill rounds Q*scale*log2e, P and P*vscale to f16: within the bar of the exact
+    # attention over the dequantised cache
+    q, k, v, ks, vs = make_inputs_i8(71 + n, n, pos0 + n, n_heads, n_kv)
+    got = O.prefill_tc_semantics_i8(q, k, v, ks, vs, pos0, n_heads, n_kv)
+    want = reference_f64_i8(q, k, v, ks, vs, pos0, n_heads, n_kv)
+    ma, _ = assert_close(got, want, what="int8 prefill semantics vs f64")
+    assert ma > 1e-6  # the f16 roundings are visible
+
+
+def test_prefill_i8_unit_scales_follow_the_f16_path():
+    # unit scales and small integers: the int8 restatement differs from the f16 one only by where P*1024
+    # rounds (the 2^10 bias keeps tiny probabilities normal), far below the f16 step of P itself
+    q, k, v, _, _ = make_inputs_i8(8, 80, 200, 8, 2)
+    k = (k // 16).astype(np.int8)
+    ones = np.ones((200, 2), dtype=np.float32)
+    got = O.prefill_tc_semantics_i8(q, k, v, ones, ones, 120, 8, 2)
+    want = O.prefill_tc_semantics(q, k.astype(np.float16).view(np.uint16), v.astype(np.float16).view(np.uint16), 120,
+                                  8, 2)
+    np.testing.assert_allclose(got, want, rtol=0, atol=1e-4)
