@@ -75,6 +75,9 @@ struct GiDecodeArgs {
 #define DEC_MINWG 1 // workgroups per CU the register budget is sized for
 #endif
 #define DEC_TILE 32
+#ifndef DEC_QFIRST
+#define DEC_QFIRST 0
+#endif
 #define DEC_PAIRS 8 // (token, head) pairs per column block of 16 columns
 #define DEC_RESCALE_LOG2 8.0f
 #define DEC_PART 132 // floats per slice partial: O (128), max (base 2), sum, 2 pad (16-byte rows)
@@ -458,6 +461,9 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
     if (!SHARE || pair0 < npairs) {
     Buf B[DEC_NB];
     const int t_first = SHARE ? 0 : wave * TILE;
+#if DEC_QFIRST
+    __builtin_amdgcn_s_waitcnt(0x0F70); // vmcnt(0): the queries are in before any K/V load goes out
+#endif
 #pragma unroll
     for (int i = 0; i < DEC_NB; i++) {
         load_k(B[i], t_first + i * STRIDE);
