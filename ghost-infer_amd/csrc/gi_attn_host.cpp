@@ -41,7 +41,7 @@ struct GiDecodeArgs {
     int chunk;
     int nsplit;
     float qscale;
-    int pad_;
+    int hd;
     const float* ks;
     const float* vs;
     long long sc_stride;
@@ -107,7 +107,7 @@ constexpr int kMaxDevices = 64;
 #endif
 constexpr int kRopeHeads = 16; // heads per gi_qk_norm_rope workgroup; must match the kernels' ROPE_HEADS
 constexpr int kCombineSplit = CMB_DSPLIT; // combine workgroups per (head, token); must match the kernels'
-constexpr int kDecWaves = 4, kDecTile = 32, kDecPairs = 8, kDecPart = 132; // kDecPart: floats per slice partial
+constexpr int kDecWaves = 4, kDecTile = 32, kDecPairs = 8; // slice partials are hd + 4 floats
 constexpr int kSliceUnit = kDecWaves * kDecTile; // 128 keys
 constexpr int kSplitMaxBatch = 15;                // tokens per split launch (src/cuda.rs:119)
 constexpr int kTiledMinBatch = 16;                // prefill from this many tokens (src/cuda.rs:95)
@@ -135,7 +135,8 @@ int check(hipError_t r, const char* what) {
 struct Module {
     bool loaded = false;
     hipModule_t mod = nullptr;
-    hipFunction_t dec[2][2][2] = {}; // [int8 cache][shared][column blocks - 1]
+    hipFunction_t dec[2][2][2] = {}; // [int8 cache][shared][column blocks - 1], head size 128
+    hipFunction_t dec256[2][2] = {};  // [shared][column blocks - 1], head size 256 (f16 cache)
     hipFunction_t prefill[2] = {};   // [int8 cache]
     hipFunction_t combine = nullptr, rope = nullptr;
     int prefill_threads = 0; // the prefill kernel's block size (its launch bound: waves x 64)
@@ -174,6 +175,10 @@ int load_module(const char* path, Module** out) {
             {&m.dec[1][0][1], "gi_decode_partial_2_i8"},
             {&m.dec[1][1][0], "gi_decode_shared_1_i8"},
             {&m.dec[1][1][1], "gi_decode_shared_2_i8"},
+            {&m.dec256[0][0], "gi_decode_partial_1_h256"},
+            {&m.dec256[0][1], "gi_decode_partial_2_h256"},
+            {&m.dec256[1][0], "gi_decode_shared_1_h256"},
+            {&m.dec256[1][1], "gi_decode_shared_2_h256"},
             {&m.combine, "gi_decode_combine"},
             {&m.prefill[0], "gi_prefill_fwd"},
             {&m.prefill[1], "gi_prefill_fwd_i8"},
@@ -296,8 +301,13 @@ int check_scales(const float* ks, const float* vs, long long sc_stride, long lon
     return 0;
 }
 
-int check_shape(int n_heads, int n_kv, int hd) {
-    if (hd != 128) return fail("head size %d unsupported (the gfx950 kernels take 128)", hd);
+// Keys per slice unit: one tile per wave (32 f16 keys at head size 128, 64 int8 keys, 16 f16 keys at 256).
+int slice_unit(bool i8, int hd) { return hd == 256 ? kDecWaves * kDecTile / 2 : i8 ? 2 * kSliceUnit : kSliceUnit; }
+
+// hd256: whether the entry point takes head size 256 as well as 128.
+int check_shape(int n_heads, int n_kv, int hd, bool hd256 = false) {
+    if (hd != 128 && !(hd256 && hd == 256))
+        return fail("head size %d unsupported (the gfx950 kernels take 128%s)", hd, hd256 ? " or 256" : "");
     if (n_kv <= 0 || n_heads <= 0 || n_heads % n_kv != 0)
         return fail("n_heads %d must be a positive multiple of n_kv %d", n_heads, n_kv);
     return 0;
@@ -308,7 +318,7 @@ int decode_impl(void* stream, const float* q, long long q_stride, const void* kc
                 const float* vs, long long sc_stride, long long sc_head_stride, bool i8, long long kv_stride,
                 long long kv_head_stride, float* out, long long out_stride, void* workspace, size_t workspace_bytes,
                 int pos0, const int* posp, int ctx_cap, int n_tok, int n_heads, int n_kv, int hd, float scale) {
-    if (int e = check_shape(n_heads, n_kv, hd)) return e;
+    if (int e = check_shape(n_heads, n_kv, hd, !i8)) return e;
     if (n_tok <= 0) return fail("n_tok %d must be positive", n_tok);
     if (!q || !kc || !vc || !out) return fail("null tensor pointer");
     if (kv_head_stride == 0) kv_head_stride = hd;
@@ -326,8 +336,8 @@ int decode_impl(void* stream, const float* q, long long q_stride, const void* kc
     if (int e = load_module(nullptr, &m)) return e;
     const DecVariant var = dec_variant(n_tok, n_heads / n_kv);
     GiDecodeArgs a{};
-    plan(max_span, n_tok, n_heads, n_kv, &a.chunk, &a.nsplit, i8 ? 2 * kSliceUnit : kSliceUnit);
-    size_t need = a.nsplit == 1 ? 0 : (size_t)n_tok * n_heads * a.nsplit * kDecPart * sizeof(float);
+    plan(max_span, n_tok, n_heads, n_kv, &a.chunk, &a.nsplit, slice_unit(i8, hd));
+    size_t need = a.nsplit == 1 ? 0 : (size_t)n_tok * n_heads * a.nsplit * (hd + 4) * sizeof(float);
     if (need && (!workspace || workspace_bytes < need))
         return fail("workspace of %zu bytes too small: %zu needed", workspace_bytes, need);
     if (need && !aligned16(workspace)) return fail("the workspace must be 16-byte aligned");
@@ -346,6 +356,7 @@ int decode_impl(void* stream, const float* q, long long q_stride, const void* kc
     a.n_heads = n_heads;
     a.n_kv = n_kv;
     a.qscale = scale * kLog2e;
+    a.hd = hd;
     if (i8) {
         a.ks = ks;
         a.vs = vs;
@@ -353,11 +364,12 @@ int decode_impl(void* stream, const float* q, long long q_stride, const void* kc
         a.sc_head_stride = sc_head_stride;
     }
     hipStream_t st = (hipStream_t)stream;
-    if (int e = launch(kDecodePartial, m->dec[i8][var.shared][var.ncb - 1], dim3(a.nsplit, n_kv, var.groups), dim3(256),
-                       st, &a, sizeof a))
-        return e;
+    hipFunction_t f = hd == 256 ? m->dec256[var.shared][var.ncb - 1] : m->dec[i8][var.shared][var.ncb - 1];
+    if (int e = launch(kDecodePartial, f, dim3(a.nsplit, n_kv, var.groups), dim3(256), st, &a, sizeof a)) return e;
     if (a.nsplit > 1)
-        if (int e = launch(kDecodeCombine, m->combine, dim3(n_heads, n_tok, kCombineSplit), dim3(64), st, &a, sizeof a)) return e;
+        if (int e = launch(kDecodeCombine, m->combine, dim3(n_heads, n_tok, kCombineSplit * hd / 128), dim3(64), st, &a,
+                           sizeof a))
+            return e;
     return 0;
 }
 
@@ -472,25 +484,26 @@ int gi_init(const char* code_object_path) {
 const char* gi_last_error(void) { return g_err.c_str(); }
 
 int gi_attn_decode_plan(int max_span, int n_tok, int n_heads, int n_kv, int hd, int* chunk, int* nsplit) {
-    if (int e = check_shape(n_heads, n_kv, hd)) return e;
+    if (int e = check_shape(n_heads, n_kv, hd, true)) return e;
     if (max_span <= 0 || n_tok <= 0) return fail("max_span %d and n_tok %d must be positive", max_span, n_tok);
     if (!chunk || !nsplit) return fail("null output pointer");
-    plan(max_span, n_tok, n_heads, n_kv, chunk, nsplit);
+    plan(max_span, n_tok, n_heads, n_kv, chunk, nsplit, slice_unit(false, hd));
     return 0;
 }
 
 size_t gi_attn_decode_workspace_bytes(int ctx_cap, int n_tok, int n_heads, int n_kv, int hd) {
-    if (check_shape(n_heads, n_kv, hd) || ctx_cap <= 0 || n_tok <= 0) return 0;
+    if (check_shape(n_heads, n_kv, hd, true) || ctx_cap <= 0 || n_tok <= 0) return 0;
     // the most partials any launch of up to n_tok tokens whose spans reach at most ctx_cap keys writes:
     // plan() caps the slices per (kv head, pair group) at per_slot, and a span never has more slices
-    // than 128-key units
+    // than slice units (the smallest unit of the head size, f16's)
+    const int unit = slice_unit(false, hd);
     size_t best = 16;
     int G = n_heads / n_kv;
     for (int t = 1; t <= n_tok; t++) {
         int groups = dec_variant(t, G).groups;
         int per_slot = std::max(1, decode_target_wgs() / std::max(1, n_kv * groups));
-        int most = std::max(1, std::min(per_slot, (ctx_cap + kSliceUnit - 1) / kSliceUnit));
-        best = std::max(best, (size_t)t * n_heads * most * kDecPart * sizeof(float));
+        int most = std::max(1, std::min(per_slot, (ctx_cap + unit - 1) / unit));
+        best = std::max(best, (size_t)t * n_heads * most * (hd + 4) * sizeof(float));
     }
     return best;
 }

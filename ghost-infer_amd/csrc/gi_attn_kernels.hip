@@ -44,7 +44,7 @@ struct GiDecodeArgs {
     const float* q;        // query rows: token b's head h at q + b*q_stride + h*128 (f32)
     const uint16_t* kc;    // K cache [pos][n_kv][128] f16, kv_stride elements per position
     const uint16_t* vc;    // V cache, same layout
-    float* part;           // slice partials [token][head][nsplit][DEC_PART]: O (128), max (base 2), sum
+    float* part;           // slice partials [token][head][nsplit][hd + 4]: O (hd), max (base 2), sum, 2 pad
     float* out;            // output rows: token b's head h at out + b*out_stride + h*128 (f32)
     const int* posp;       // device position (overrides pos0 when non-null)
     long long q_stride;
@@ -58,7 +58,7 @@ struct GiDecodeArgs {
     int chunk;             // keys per slice, a multiple of 128
     int nsplit;            // slices per token (the grid's x)
     float qscale;          // scale * log2(e)
-    int pad_;
+    int hd;                // head size: 128 or 256 (f16 cache); partial rows are hd + 4 floats
     // int8 cache only (the kernels named *_i8): kc / vc hold int8 rows in the same element layout, and the
     // f32 scale of position t, kv head h is at ks / vs [t*sc_stride + h*sc_head_stride]
     const float* ks;
@@ -80,7 +80,6 @@ struct GiDecodeArgs {
 #endif
 #define DEC_PAIRS 8 // (token, head) pairs per column block of 16 columns
 #define DEC_RESCALE_LOG2 8.0f
-#define DEC_PART 132 // floats per slice partial: O (128), max (base 2), sum, 2 pad (16-byte rows)
 // int8 cache: the probability's f16 remainder column is scaled by 2^12 (undone when the columns merge).
 // Times a value scale of ~0.03 the remainder would otherwise fall into f16's subnormal range.
 #define DEC_I8_LO 4096.f
@@ -142,8 +141,10 @@ __device__ __forceinline__ float row_bcast(float v) {
 // Register buffers of one wave's tile. f16: 32 keys; K as the S^T A operand (2 blocks of 16 keys, 4 k-steps
 // of 32 dims), V as 8 keys x 8 dims. int8: 64 keys in the same registers; K 4 blocks x 32 bytes, V 16 keys x
 // 8 dims, plus the scale of key `lane` of the tile.
-template <bool I8> struct DecBuf { u4 k[2][4]; u4 v[8]; };
-template <> struct DecBuf<true> { u4 k[4][2]; u2 v[16]; float ksc, vsc; };
+template <bool I8, int HD> struct DecBuf { u4 k[2][4]; u4 v[8]; };
+template <> struct DecBuf<true, 128> { u4 k[4][2]; u2 v[16]; float ksc, vsc; };
+// head size 256 (f16): 16 keys; K row c of the tile, 8 k-steps of 32 dims; V keys 4grp..4grp+3, dims 16c..16c+15
+template <> struct DecBuf<false, 256> { u4 k[8]; u4 v[4][2]; };
 
 // Lane l of a wave: c = l % 16 (MFMA column / A-row), grp = l / 16 (k-group of 8).
 // I8 = true: an int8 cache (kv_store's KV8 format, src/cuda.rs:333-339: a row of int8 values and one f32
@@ -154,14 +155,23 @@ template <> struct DecBuf<true> { u4 k[4][2]; u2 v[16]; float ksc, vsc; };
 // f16 keys); lane (c, grp) holds the S^T rows of keys 16grp + 4b + j (block b, row 4grp + j, so A-row c of
 // block b loads key 16(c/4) + c%4 + 4b) and feeds PV with V rows 16grp..16grp+15 (k-step ks: 8ks..8ks+7),
 // dims 8c..8c+7. Each key's scale is loaded by lane key%64 and broadcast across its 16-lane row.
+// HD = 256 (f16 cache): tiles of 16 keys (16 KB of K and V, as before). S^T comes from 8 k-steps of
+// v_mfma_f32_16x16x32_f16 with A-row c = tile key c; lane (c, grp) then holds the scores of keys 4grp..4grp+3,
+// exactly the B operand of v_mfma_f32_16x16x16_f16 for O^T += V^T P^T over the tile, so no key permutation
+// is needed. V^T block dd has A-row c = dim 16c + dd (the lane loads dims 16c..16c+15 of its 4 keys), so a
+// lane ends with dims 64grp..64grp+63 of its column.
 // SHARE = false: the 4 waves split the slice's tiles and serve the same DEC_PAIRS*NCB (token, head)
 // pairs, merging through LDS at the end. SHARE = true (many pairs per kv head, as in a verify block):
 // every wave walks the whole slice for its own DEC_PAIRS*NCB pairs, so one workgroup serves 4 times as
 // many pairs and the slice's K/V comes from HBM once (the waves' repeated loads of the same lines are
 // served by the caches).
-template <int NCB, bool SHARE, bool I8>
+template <int NCB, bool SHARE, bool I8, int HD = 128>
 __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
-    constexpr int TILE = I8 ? 2 * DEC_TILE : DEC_TILE; // keys per wave tile
+    static_assert(HD == 128 || (HD == 256 && !I8), "head sizes: 128 (f16, int8), 256 (f16)");
+    constexpr int TILE = HD == 256 ? DEC_TILE / 2 : I8 ? 2 * DEC_TILE : DEC_TILE; // keys per wave tile
+    constexpr int KK = HD / 32;                 // QK k-steps
+    constexpr int ND = HD == 256 ? 16 : 8;      // O^T MFMA blocks
+    constexpr int PART = HD + 4;                // floats per slice partial
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int c = lane & 15, grp = lane >> 4;
@@ -191,23 +201,23 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
         valid[cb] = pi < npairs;
         int t = valid[cb] ? pi / G : 0, g = valid[cb] ? pi % G : 0;
         span[cb] = valid[cb] ? min(pos0 + t + 1 - k_begin, nkeys) : 0; // keys of the slice this column sees
-        qoff[cb] = ((int)(t * a.q_stride) + (kvh * G + g) * 128 + (I8 ? 16 : 8) * grp) * 4;
+        qoff[cb] = ((int)(t * a.q_stride) + (kvh * G + g) * HD + (I8 ? 16 : 8) * grp) * 4;
     }
     // smallest span among the wave's valid columns (the lowest token's: column 0 of block 0 is always valid):
     // tiles below it need no masking
     const int span_lo = min(pos0 + pair0 / G + 1 - k_begin, nkeys);
     // Q rows (f32, 8 dims per lane per k-step), issued before the first K/V tiles so that waiting for them
     // leaves the K/V loads in flight
-    u4 qraw[NCB][4][2];
+    u4 qraw[NCB][KK][2];
     // B operand of S^T = K Qc^T. f16: k-step kk covers dims 32kk..32kk+31, this lane dims 32kk+8grp..+7.
     // int8: this lane dims 16grp + 8(kk%2) + 64(kk/2) .. +7 (the bytes its two 16-byte key loads bring)
-    h8 qf[NCB][4];
+    h8 qf[NCB][KK];
     {
         __amdgpu_buffer_rsrc_t rq = gi_rsrc(a.q, (long long)a.n_tok * a.q_stride * 4);
 #pragma unroll
         for (int cb = 0; cb < NCB; cb++)
 #pragma unroll
-            for (int kk = 0; kk < 4; kk++) {
+            for (int kk = 0; kk < KK; kk++) {
                 const int off = qoff[cb] + (I8 ? 32 * (kk & 1) + 256 * (kk >> 1) : 128 * kk);
                 qraw[cb][kk][0] = gi_load16(rq, off);
                 qraw[cb][kk][1] = gi_load16(rq, off + 16);
@@ -216,13 +226,15 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
     __builtin_amdgcn_sched_barrier(0);
     GI_TS(1);
     float m_run[NCB], l_run[NCB];
-    f4 o[NCB][8]; // O^T: MFMA dd holds rows m = dims 8m + dd; this lane rows 4grp..4grp+3 -> dims 32grp + 8j + dd
+    // O^T: MFMA dd holds rows m = dims 8m + dd; this lane rows 4grp..4grp+3 -> dims 32grp + 8j + dd
+    // (HD 256: rows m = dims 16m + dd -> dims 64grp + 16j + dd)
+    f4 o[NCB][ND];
 #pragma unroll
     for (int cb = 0; cb < NCB; cb++) {
         m_run[cb] = GI_NEG_INF;
         l_run[cb] = 0.f;
 #pragma unroll
-        for (int dd = 0; dd < 8; dd++) o[cb][dd] = f4{0.f, 0.f, 0.f, 0.f};
+        for (int dd = 0; dd < ND; dd++) o[cb][dd] = f4{0.f, 0.f, 0.f, 0.f};
     }
 
     // Loads go through buffer resources that start at the wave's current tile and end at the slice's last
@@ -249,10 +261,17 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
     const int koff8 = (16 * (c >> 2) + (c & 3)) * (int)kvs + 16 * grp;
     const int voff8 = 16 * grp * (int)kvs + 8 * c;
     const int scoff = lane * (int)scs * 4;
+    // head size 256: K row c, dims 8grp + 32kk; V keys 4grp + i, dims 16c..16c+15
+    const int koff256 = (c * (int)kvs + 8 * grp) * 2;
+    const int voff256 = (4 * grp * (int)kvs + 16 * c) * 2;
 
-    using Buf = DecBuf<I8>;
+    using Buf = DecBuf<I8, HD>;
     auto load_k = [&](Buf& B, int t) {
-        if constexpr (I8) {
+        if constexpr (HD == 256) {
+            __amdgpu_buffer_rsrc_t r = gi_rsrc(kslice + (long long)t * kvs, (long long)(nkeys - t) * kvs * 2);
+#pragma unroll
+            for (int kk = 0; kk < 8; kk++) B.k[kk] = gi_load16(r, koff256 + 64 * kk);
+        } else if constexpr (I8) {
             __amdgpu_buffer_rsrc_t r = gi_rsrc(kslice8 + (long long)t * kvs, (long long)(nkeys - t) * kvs);
 #pragma unroll
             for (int b = 0; b < 4; b++) {
@@ -270,7 +289,14 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
         }
     };
     auto load_v = [&](Buf& B, int t) {
-        if constexpr (I8) {
+        if constexpr (HD == 256) {
+            __amdgpu_buffer_rsrc_t r = gi_rsrc(vslice + (long long)t * kvs, (long long)(nkeys - t) * kvs * 2);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                B.v[i][0] = gi_load16(r, voff256 + i * vstep);
+                B.v[i][1] = gi_load16(r, voff256 + i * vstep + 16);
+            }
+        } else if constexpr (I8) {
             __amdgpu_buffer_rsrc_t r = gi_rsrc(vslice8 + (long long)t * kvs, (long long)(nkeys - t) * kvs);
 #pragma unroll
             for (int i = 0; i < 16; i++) B.v[i] = gi_load8(r, voff8 + i * (int)kvs);
@@ -321,8 +347,10 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
             // P <= 256 is exact enough in the f16 hi/lo split, and most tiles skip rescaling O
             const bool up = mx > m_run[cb] + DEC_RESCALE_LOG2;
             if (__builtin_amdgcn_ballot_w64(up)) {
+                // alpha = 0 when nothing was seen yet; lanes that do not move keep 1 (their m_run may still be
+                // -inf: a column whose keys all lie past this tile's start, beside one that sees some)
                 const float m_new = up ? mx : m_run[cb];
-                const float alpha = __builtin_amdgcn_exp2f(m_run[cb] - m_new); // 0 when nothing was seen yet
+                const float alpha = up ? __builtin_amdgcn_exp2f(m_run[cb] - m_new) : 1.f;
                 m_run[cb] = m_new;
                 l_run[cb] *= alpha;
 #pragma unroll
@@ -405,7 +433,7 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
             const bool up = mx > m_run[cb] + DEC_RESCALE_LOG2;
             if (__builtin_amdgcn_ballot_w64(up)) {
                 const float m_new = up ? mx : m_run[cb];
-                const float alpha = __builtin_amdgcn_exp2f(m_run[cb] - m_new);
+                const float alpha = up ? __builtin_amdgcn_exp2f(m_run[cb] - m_new) : 1.f;
                 m_run[cb] = m_new;
                 l_run[cb] *= alpha;
 #pragma unroll
@@ -450,8 +478,73 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
         __builtin_amdgcn_sched_barrier(0);
         if (reload) load_v(B, t + DEC_NB * STRIDE);
     };
+    auto process_256 = [&](auto& B, int t, bool reload) {
+        __builtin_amdgcn_sched_barrier(0);
+        f4 sacc[NCB];
+#pragma unroll
+        for (int cb = 0; cb < NCB; cb++) {
+            sacc[cb] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int kk = 0; kk < 8; kk++)
+                sacc[cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, B.k[kk]), qf[cb][kk], sacc[cb], 0, 0, 0);
+        }
+        if (reload) load_k(B, t + DEC_NB * STRIDE);
+        __builtin_amdgcn_sched_barrier(0);
+        const bool masked = t + TILE > span_lo;
+        h4x pf[NCB]; // PV B operand: keys 4grp + j of column c
+#pragma unroll
+        for (int cb = 0; cb < NCB; cb++) {
+            float sc[4], mx = GI_NEG_INF;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                float v = sacc[cb][j];
+                v = v + lane_xor1(v);
+                if (masked) v = t + 4 * grp + j < span[cb] ? v : GI_NEG_INF;
+                sc[j] = v;
+                mx = fmaxf(mx, v);
+            }
+            mx = rows_max(mx);
+            const bool up = mx > m_run[cb] + DEC_RESCALE_LOG2;
+            if (__builtin_amdgcn_ballot_w64(up)) {
+                const float m_new = up ? mx : m_run[cb];
+                const float alpha = up ? __builtin_amdgcn_exp2f(m_run[cb] - m_new) : 1.f;
+                m_run[cb] = m_new;
+                l_run[cb] *= alpha;
+#pragma unroll
+                for (int dd = 0; dd < ND; dd++) o[cb][dd] *= alpha;
+            }
+            const float m_use = m_run[cb] == GI_NEG_INF ? 0.f : m_run[cb];
+            float psum = 0.f;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const float p = __builtin_amdgcn_exp2f(sc[j] - m_use);
+                psum += p;
+                _Float16 hi = (_Float16)p;
+                pf[cb][j] = (c & 1) ? (_Float16)(p - (float)hi) : hi;
+            }
+            l_run[cb] += psum;
+        }
+        // V^T block dd: element i of the A operand = V[key 4grp + i][dim 16c + dd]
+#pragma unroll
+        for (int dd = 0; dd < 16; dd++) {
+            const int h = dd >> 3, w = (dd & 7) >> 1;
+            u2 vw;
+#pragma unroll
+            for (int p = 0; p < 2; p++) {
+                const uint32_t lo = B.v[2 * p][h][w], hi = B.v[2 * p + 1][h][w];
+                vw[p] = (dd & 1) ? ((lo >> 16) | (hi & 0xffff0000u)) : ((lo & 0xffffu) | (hi << 16));
+            }
+            const h4x vt = __builtin_bit_cast(h4x, vw);
+#pragma unroll
+            for (int cb = 0; cb < NCB; cb++)
+                o[cb][dd] = __builtin_amdgcn_mfma_f32_16x16x16f16(vt, pf[cb], o[cb][dd], 0, 0, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        if (reload) load_v(B, t + DEC_NB * STRIDE);
+    };
     auto process = [&](Buf& B, int t, bool reload) {
-        if constexpr (I8) process_i8(B, t, reload);
+        if constexpr (HD == 256) process_256(B, t, reload);
+        else if constexpr (I8) process_i8(B, t, reload);
         else process_h(B, t, reload);
     };
 
@@ -475,7 +568,7 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
 #pragma unroll
     for (int cb = 0; cb < NCB; cb++)
 #pragma unroll
-        for (int kk = 0; kk < 4; kk++)
+        for (int kk = 0; kk < KK; kk++)
 #pragma unroll
             for (int e = 0; e < 8; e++) {
                 // (the element is copied to a scalar first: clang's __builtin_bit_cast of a vector-element
@@ -501,16 +594,19 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
 
     // ---- wave results to LDS: every lane's 32 O^T values (its column, dims 32grp + 8j + dd) as 8 16-byte
     // stores; per pair the max and the sum over the 4 k-groups
-    __shared__ __attribute__((aligned(16))) float sm_o[DEC_WAVES][16 * NCB][128 + 4];
+    // (HD 256: 64 values, dims 64grp + 16j + dd, as 16 stores)
+    __shared__ __attribute__((aligned(16))) float sm_o[DEC_WAVES][16 * NCB][HD + 4];
     __shared__ float sm_m[DEC_WAVES][DEC_PAIRS * NCB], sm_l[DEC_WAVES][DEC_PAIRS * NCB];
 #pragma unroll
     for (int cb = 0; cb < NCB; cb++) {
         float l = rows_sum(l_run[cb]);
 #pragma unroll
         for (int j = 0; j < 4; j++) {
-            float* row = &sm_o[wave][16 * cb + c][32 * grp + 8 * j];
-            *reinterpret_cast<float4*>(row) = make_float4(o[cb][0][j], o[cb][1][j], o[cb][2][j], o[cb][3][j]);
-            *reinterpret_cast<float4*>(row + 4) = make_float4(o[cb][4][j], o[cb][5][j], o[cb][6][j], o[cb][7][j]);
+            float* row = &sm_o[wave][16 * cb + c][(HD / 4) * grp + (ND)*j];
+#pragma unroll
+            for (int q4 = 0; q4 < ND / 4; q4++)
+                *reinterpret_cast<float4*>(row + 4 * q4) =
+                    make_float4(o[cb][4 * q4][j], o[cb][4 * q4 + 1][j], o[cb][4 * q4 + 2][j], o[cb][4 * q4 + 3][j]);
         }
         if (lane < 16 && (c & 1) == 0) {
             sm_m[wave][cb * DEC_PAIRS + (c >> 1)] = m_run[cb];
@@ -523,9 +619,9 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
     // ---- merge the waves (SHARE: each pair has one wave) and the hi/lo columns: thread -> (pair, 4 dims)
     constexpr float LO = I8 ? 1.f / DEC_I8_LO : 1.f;
 #pragma unroll
-    for (int it = 0; it < WG_PAIRS / DEC_PAIRS; it++) {
+    for (int it = 0; it < WG_PAIRS * HD / 1024; it++) {
         const int item = threadIdx.x + 256 * it;
-        const int pl = item >> 5, d4 = 4 * (item & 31);      // pair within the workgroup
+        const int pl = item / (HD / 4), d4 = 4 * (item % (HD / 4)); // pair within the workgroup
         const int pi = blockIdx.z * WG_PAIRS + pl;
         const int w0 = SHARE ? pl / (DEC_PAIRS * NCB) : 0;   // the waves holding the pair
         const int w1 = SHARE ? w0 + 1 : DEC_WAVES;
@@ -551,19 +647,19 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
             const int tk = pi / G, h = kvh * G + pi % G;
             if (a.nsplit == 1) {
                 const float inv = 1.f / L;
-                *reinterpret_cast<float4*>(a.out + (long long)tk * a.out_stride + (long long)h * 128 + d4) =
+                *reinterpret_cast<float4*>(a.out + (long long)tk * a.out_stride + (long long)h * HD + d4) =
                     make_float4(O.x * inv, O.y * inv, O.z * inv, O.w * inv);
             } else {
-                float* p = a.part + (((long long)tk * a.n_heads + h) * a.nsplit + s) * DEC_PART;
+                float* p = a.part + (((long long)tk * a.n_heads + h) * a.nsplit + s) * PART;
                 *reinterpret_cast<float4*>(p + d4) = O;
-                if (d4 == 0) *reinterpret_cast<float2*>(p + 128) = make_float2(M, L);
+                if (d4 == 0) *reinterpret_cast<float2*>(p + HD) = make_float2(M, L);
             }
         }
     }
 #ifdef GI_DEC_TIMESTAMPS
     ts[5] = wall_clock64();
     if (lane == 0) {
-        unsigned long long* dbg = (unsigned long long*)(a.part + (long long)a.n_tok * a.n_heads * a.nsplit * DEC_PART);
+        unsigned long long* dbg = (unsigned long long*)(a.part + (long long)a.n_tok * a.n_heads * a.nsplit * PART);
         long long w = ((long long)(blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x) * DEC_WAVES + wave;
         for (int i = 0; i < 6; i++) dbg[w * 16 + i] = ts[i];
         dbg[w * 16 + 8] = ts[6];
@@ -575,16 +671,20 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
 #endif
 }
 
-#define GI_DEC_KERNEL(name, NCB, SHARE, I8) \
-    extern "C" __global__ void __launch_bounds__(256, DEC_MINWG) name(GiDecodeArgs a) { gi_decode_partial_t<NCB, SHARE, I8>(a); }
-GI_DEC_KERNEL(gi_decode_partial_1, 1, false, false)
-GI_DEC_KERNEL(gi_decode_partial_2, 2, false, false)
-GI_DEC_KERNEL(gi_decode_shared_1, 1, true, false)
-GI_DEC_KERNEL(gi_decode_shared_2, 2, true, false)
-GI_DEC_KERNEL(gi_decode_partial_1_i8, 1, false, true)
-GI_DEC_KERNEL(gi_decode_partial_2_i8, 2, false, true)
-GI_DEC_KERNEL(gi_decode_shared_1_i8, 1, true, true)
-GI_DEC_KERNEL(gi_decode_shared_2_i8, 2, true, true)
+#define GI_DEC_KERNEL(name, NCB, SHARE, I8, HD) \
+    extern "C" __global__ void __launch_bounds__(256, DEC_MINWG) name(GiDecodeArgs a) { gi_decode_partial_t<NCB, SHARE, I8, HD>(a); }
+GI_DEC_KERNEL(gi_decode_partial_1, 1, false, false, 128)
+GI_DEC_KERNEL(gi_decode_partial_2, 2, false, false, 128)
+GI_DEC_KERNEL(gi_decode_shared_1, 1, true, false, 128)
+GI_DEC_KERNEL(gi_decode_shared_2, 2, true, false, 128)
+GI_DEC_KERNEL(gi_decode_partial_1_i8, 1, false, true, 128)
+GI_DEC_KERNEL(gi_decode_partial_2_i8, 2, false, true, 128)
+GI_DEC_KERNEL(gi_decode_shared_1_i8, 1, true, true, 128)
+GI_DEC_KERNEL(gi_decode_shared_2_i8, 2, true, true, 128)
+GI_DEC_KERNEL(gi_decode_partial_1_h256, 1, false, false, 256)
+GI_DEC_KERNEL(gi_decode_partial_2_h256, 2, false, false, 256)
+GI_DEC_KERNEL(gi_decode_shared_1_h256, 1, true, false, 256)
+GI_DEC_KERNEL(gi_decode_shared_2_h256, 2, true, false, 256)
 
 // Merge the slices of each (token, head): M = max m_s, w_s = 2^(m_s - M), out = sum w_s O_s / sum w_s l_s
 // (attention_combine's maths in base 2; empty slices carry m = -inf and weigh nothing). One wave per
@@ -595,20 +695,21 @@ GI_DEC_KERNEL(gi_decode_shared_2_i8, 2, true, true)
 #ifndef CMB_DSPLIT
 #define CMB_DSPLIT 8 // workgroups per (head, token), each over 128 / CMB_DSPLIT dims
 #endif
-#define CMB_DIMS (128 / CMB_DSPLIT)
+#define CMB_DIMS (128 / CMB_DSPLIT) // dims per workgroup (grid z = hd / CMB_DIMS)
 extern "C" __global__ void __launch_bounds__(64) gi_decode_combine(GiDecodeArgs a) {
     __shared__ float acc_o[64][CMB_DIMS + 1];
     const int h = blockIdx.x, t = blockIdx.y, d0 = blockIdx.z * CMB_DIMS, lane = threadIdx.x;
-    const float* p = a.part + ((long long)t * a.n_heads + h) * a.nsplit * DEC_PART;
+    const int hd = a.hd, part = hd + 4;
+    const float* p = a.part + ((long long)t * a.n_heads + h) * a.nsplit * part;
     float m = GI_NEG_INF, L = 0.f, o[CMB_DIMS];
 #pragma unroll
     for (int i = 0; i < CMB_DIMS; i++) o[i] = 0.f;
     for (int s = lane; s < a.nsplit; s += 64) {
-        const float* ps = p + s * DEC_PART;
+        const float* ps = p + s * part;
         float4 v[CMB_DIMS / 4];
 #pragma unroll
         for (int i = 0; i < CMB_DIMS / 4; i++) v[i] = *reinterpret_cast<const float4*>(ps + d0 + 4 * i);
-        const float2 ml = *reinterpret_cast<const float2*>(ps + 128);
+        const float2 ml = *reinterpret_cast<const float2*>(ps + hd);
         if (ml.x == GI_NEG_INF) continue; // an empty slice
         const float mn = fmaxf(m, ml.x);
         const float a_old = __builtin_amdgcn_exp2f(m - mn), a_new = __builtin_amdgcn_exp2f(ml.x - mn);
@@ -634,7 +735,7 @@ extern "C" __global__ void __launch_bounds__(64) gi_decode_combine(GiDecodeArgs 
         float O = 0.f;
 #pragma unroll 8
         for (int k = 0; k < 64; k++) O += acc_o[k][lane];
-        a.out[(long long)t * a.out_stride + (long long)h * 128 + d0 + lane] = O / LL;
+        a.out[(long long)t * a.out_stride + (long long)h * hd + d0 + lane] = O / LL;
     }
 }
 

@@ -54,6 +54,7 @@ DECODE_SHAPES = [
     (15, 513, 32, 8),
     (5, 77, 12, 4),   # G = 3: (token, head) pairs straddle column blocks
     (4, 40, 6, 1),    # G = 6
+    (2, 95, 32, 4),   # wave 3's first tile (keys 96..) lies past token 0's span but not token 1's
 ]
 
 
