@@ -1,7 +1,7 @@
 """Benchmark of the gfx950 attention hot path on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload decode64k|decode4k|verify|prefill8k|chunked|qkrope|
-                    decode64k_i8|verify_i8|prefill8k_i8]
+                    decode64k_i8|verify_i8|prefill8k_i8|decode64k_h256|prefill8k_h256]
                     [--no-cpu-baseline] [--no-secondary] [--reference-layout]
 
 A step is one pass of the hot path over one batch of synthetic seeded input already resident in HBM:
@@ -12,6 +12,8 @@ A step is one pass of the hot path over one batch of synthetic seeded input alre
   prefill8k  config 3: causal prefill of 8192 tokens, 32 / 8 heads, f16 in and out (MFMA TFLOP/s)
   chunked    config 5: 131072 tokens in 2048-token chunks against the growing cache, 32 / 4 heads
   qkrope     the cache write before attention (qk_norm_rope + f16 KV store) for config 3's 8192 tokens
+  decode64k_h256, prefill8k_h256
+             head size 256 (Qwen3.5-style 16 query / 2 kv heads): decode at 65536 keys, prefill of 8192
   decode64k_i8, verify_i8, prefill8k_i8
              configs 2, 4 and 3 over the int8 cache (the reference's KV8 format: int8 rows, an f32 scale per
              position and kv head); bytes are the int8 rows plus their scales
@@ -42,12 +44,12 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def seeded_cache(gen, rows, n_kv, dev, torch, layout="reference", i8=False):
+def seeded_cache(gen, rows, n_kv, dev, torch, layout="reference", i8=False, hd=HD):
     """K and V caches of N(0,1) f16 values: [rows, n_kv, HD] (the reference's layout) or [n_kv, rows, HD]
     (head-major, each kv head's rows contiguous). i8: int8 rows round(40 N(0,1)) clipped to -127..127 and
     f32 scales in [0.02, 0.03] ([rows, n_kv] or [n_kv, rows]), like quantised N(0,1) rows; returns
     (k, v, k_scale, v_scale)."""
-    shape = (rows, n_kv, HD) if layout == "reference" else (n_kv, rows, HD)
+    shape = (rows, n_kv, hd) if layout == "reference" else (n_kv, rows, hd)
     if i8:
         def ints():
             x = torch.randn(shape, generator=gen, device=dev, dtype=torch.float32) * 40
@@ -141,45 +143,46 @@ def time_steps_graph(fn, steps, warmup, torch):
 
 
 def decode_workload(torch, gi_attn, dev, ctx, n_heads, n_kv, n_tok, steps, warmup, seed, layout="head_major",
-                    i8=False):
+                    i8=False, hd=HD):
     gen = torch.Generator(device=dev)
     gen.manual_seed(seed)
     # K+V bytes of one step: every key row once (int8 rows plus their two f32 scales)
-    kv_bytes = 2 * ctx * n_kv * (HD + 4) if i8 else 2 * ctx * n_kv * HD * 2
+    kv_bytes = 2 * ctx * n_kv * (hd + 4) if i8 else 2 * ctx * n_kv * hd * 2
     layers = max(1, math.ceil(512e6 / kv_bytes))  # > 256 MB Infinity Cache in total
-    caches = [seeded_cache(gen, ctx, n_kv, dev, torch, layout, i8) for _ in range(layers)]
-    q = torch.randn((n_tok, n_heads * HD), generator=gen, device=dev, dtype=torch.float32)
-    out = torch.empty((n_tok, n_heads * HD), device=dev, dtype=torch.float32)
+    caches = [seeded_cache(gen, ctx, n_kv, dev, torch, layout, i8, hd) for _ in range(layers)]
+    q = torch.randn((n_tok, n_heads * hd), generator=gen, device=dev, dtype=torch.float32)
+    out = torch.empty((n_tok, n_heads * hd), device=dev, dtype=torch.float32)
     pos0 = ctx - n_tok
-    ws = gi_attn.new_workspace(ctx, n_tok, n_heads, n_kv, device=dev)
+    ws = gi_attn.new_workspace(ctx, n_tok, n_heads, n_kv, hd=hd, device=dev)
 
     def step(i):
         k, v, ks, vs = caches[i % layers]
-        gi_attn.decode(q, k, v, pos0, n_heads, n_kv, out=out, workspace=ws, kv_layout=layout, k_scale=ks, v_scale=vs)
+        gi_attn.decode(q, k, v, pos0, n_heads, n_kv, hd=hd, out=out, workspace=ws, kv_layout=layout, k_scale=ks,
+                       v_scale=vs)
 
     t = time_steps_graph(step, steps, warmup, torch)
     return {"seconds": t, "bytes": kv_bytes, "layers": layers, "q": q, "cache": caches[0], "pos0": pos0,
             "layout": layout, "step": step, "ws": ws}
 
 
-def prefill_flops(n, pos0, n_heads):
+def prefill_flops(n, pos0, n_heads, hd=HD):
     # QK^T and PV, 2 flops per multiply-add, causal: query i sees pos0 + i + 1 keys
     keys = n * pos0 + n * (n + 1) // 2
-    return 4 * n_heads * HD * keys
+    return 4 * n_heads * hd * keys
 
 
-def prefill_workload(torch, gi_attn, dev, n, n_heads, n_kv, steps, warmup, seed, i8=False):
+def prefill_workload(torch, gi_attn, dev, n, n_heads, n_kv, steps, warmup, seed, i8=False, hd=HD):
     gen = torch.Generator(device=dev)
     gen.manual_seed(seed)
-    q = torch.randn((n, n_heads * HD), generator=gen, device=dev, dtype=torch.float32).half()
-    k, v, ks, vs = seeded_cache(gen, n, n_kv, dev, torch, i8=i8)
-    out = torch.empty((n, n_heads * HD), device=dev, dtype=torch.float16)
+    q = torch.randn((n, n_heads * hd), generator=gen, device=dev, dtype=torch.float32).half()
+    k, v, ks, vs = seeded_cache(gen, n, n_kv, dev, torch, i8=i8, hd=hd)
+    out = torch.empty((n, n_heads * hd), device=dev, dtype=torch.float16)
 
     def step(i):
-        gi_attn.prefill(q, k, v, 0, n_heads, n_kv, out=out, k_scale=ks, v_scale=vs)
+        gi_attn.prefill(q, k, v, 0, n_heads, n_kv, hd=hd, out=out, k_scale=ks, v_scale=vs)
 
     t = time_steps(step, steps, warmup, torch)
-    return {"seconds": t, "flops": prefill_flops(n, 0, n_heads), "step": step}
+    return {"seconds": t, "flops": prefill_flops(n, 0, n_heads, hd), "step": step}
 
 
 def qkrope_workload(torch, gi_attn, dev, n, n_heads, n_kv, steps, warmup, seed):
@@ -206,7 +209,7 @@ def qkrope_workload(torch, gi_attn, dev, n, n_heads, n_kv, steps, warmup, seed):
 def chunked_workload(torch, gi_attn, dev, total, chunk, n_heads, n_kv, seed):
     gen = torch.Generator(device=dev)
     gen.manual_seed(seed)
-    k, v = seeded_cache(gen, total, n_kv, dev, torch)
+    k, v, _, _ = seeded_cache(gen, total, n_kv, dev, torch)
     q = torch.randn((total, n_heads * HD), generator=gen, device=dev, dtype=torch.float32).half()
     out = torch.empty((total, n_heads * HD), device=dev, dtype=torch.float16)
     events = []
@@ -283,7 +286,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="decode64k",
                     choices=["decode64k", "decode4k", "verify", "prefill8k", "chunked", "qkrope", "decode64k_i8",
-                             "verify_i8", "prefill8k_i8"])
+                             "verify_i8", "prefill8k_i8", "decode64k_h256", "prefill8k_h256"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--reference-layout", action="store_true",
@@ -303,19 +306,23 @@ def main():
     result = {"metric": METRIC, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
               "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "data": "synthetic"}
     w = args.workload
-    if w in ("decode64k", "decode4k", "verify", "decode64k_i8", "verify_i8"):
+    if w in ("decode64k", "decode4k", "verify", "decode64k_i8", "verify_i8", "decode64k_h256"):
+        hd = 256 if w.endswith("_h256") else HD
         ctx, n_heads, n_kv, n_tok, cfg = {
             "decode64k": (65536, 32, 4, 1, "config 2: decode, 1 token, ctx 65536, 32q/4kv, hd 128"),
             "decode4k": (4096, 32, 8, 1, "config 1: decode, 1 token, ctx 4096, 32q/8kv, hd 128"),
             "verify": (32776, 32, 4, 8, "config 4: verify, 8 tokens at a 32768-key prefix, 32q/4kv, hd 128"),
             "decode64k_i8": (65536, 32, 4, 1, "config 2 over the int8 cache: decode, 1 token, ctx 65536, 32q/4kv"),
             "verify_i8": (32776, 32, 4, 8, "config 4 over the int8 cache: verify, 8 tokens at 32768, 32q/4kv"),
+            "decode64k_h256": (65536, 16, 2, 1, "decode with 256-wide heads (Qwen3.5-style 16q/2kv), 1 token, "
+                                                "ctx 65536, f16 cache"),
         }[w]
         i8 = w.endswith("_i8")
         log(f"[bench] {cfg}")
-        r = decode_workload(torch, gi_attn, dev, ctx, n_heads, n_kv, n_tok, args.steps, args.warmup, 1234, i8=i8)
+        r = decode_workload(torch, gi_attn, dev, ctx, n_heads, n_kv, n_tok, args.steps, args.warmup, 1234, i8=i8,
+                            hd=hd)
         gbs = r["bytes"] / r["seconds"] / 1e9
-        chunk, nsplit = gi_attn.decode_plan(ctx, n_tok, n_heads, n_kv)
+        chunk, nsplit = gi_attn.decode_plan(ctx, n_tok, n_heads, n_kv, hd)
         if i8:  # int8 slices are whole 256-key units (64-key tiles, 4 waves)
             chunk = -(-chunk // 256) * 256
             nsplit = -(-ctx // chunk)
@@ -324,15 +331,15 @@ def main():
         comb_ms, _ = kt["decode_combine"]
         # algorithmic bytes of one split-kernel launch: K and V of every span key, the queries, and the
         # slice partials it writes ([token][head][slice][hd + 4] f32)
-        part_bytes = r["bytes"] + n_tok * n_heads * HD * 4 + n_tok * n_heads * nsplit * (HD + 4) * 4
+        part_bytes = r["bytes"] + n_tok * n_heads * hd * 4 + n_tok * n_heads * nsplit * (hd + 4) * 4
         kern_gbs = part_bytes / (part_ms / 1e3) / 1e9
         traffic = profile_traffic(f"pmc_decode_partial_{w}")
         result.update({
             "value": round(gbs, 1), "unit": "GB/s", "ms_per_step": r["seconds"] * 1e3,
             "dtype": "int8 K/V + f32 scales, f32 math" if i8 else "f16 K/V, f32 math",
-            "config": {"workload": cfg, "ctx": ctx, "n_tok": n_tok, "n_heads": n_heads, "n_kv": n_kv, "hd": HD,
+            "config": {"workload": cfg, "ctx": ctx, "n_tok": n_tok, "n_heads": n_heads, "n_kv": n_kv, "hd": hd,
                        "kv_bytes_per_step": r["bytes"], "layers_rotated": r["layers"],
-                       "slices": nsplit, "keys_per_slice": chunk, "kv_layout": "head_major [n_kv][ctx][128]"},
+                       "slices": nsplit, "keys_per_slice": chunk, "kv_layout": f"head_major [n_kv][ctx][{hd}]"},
             "roofline": {"bound": "hbm", "achieved": round(kern_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": round(kern_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
                          "kernel": "gi_decode_partial_*_i8 (split-K pass)" if i8 else "gi_decode_partial (split-K pass)",
@@ -341,14 +348,14 @@ def main():
                          "combine_ms_per_launch": round(comb_ms, 5) if comb_ms else None,
                          "step_GBs_KV": round(gbs, 1)},
         })
-        if args.reference_layout and not i8:
+        if args.reference_layout and not i8 and hd == HD:
             # the same decode over caches in the reference's [position][n_kv][128] layout
             r_ref = decode_workload(torch, gi_attn, dev, ctx, n_heads, n_kv, n_tok, args.steps, args.warmup, 1234,
                                     layout="reference")
             result["config"]["reference_layout_GBs"] = round(r_ref["bytes"] / r_ref["seconds"] / 1e9, 1)
             result["config"]["reference_layout_ms_per_step"] = r_ref["seconds"] * 1e3
             del r_ref
-        if not args.no_cpu_baseline and not i8:
+        if not args.no_cpu_baseline and not i8 and hd == HD:
             log("[bench] cpu baseline (oracle, Model::attention restatement)")
             t_cpu, threads, reps = cpu_baseline_decode(r["q"], r["cache"], r["pos0"], n_heads, n_kv)
             result["cpu_baseline"] = {"value": round(r["bytes"] / t_cpu / 1e9, 3), "unit": "GB/s", "cores": threads,
@@ -369,18 +376,22 @@ def main():
                          "algorithmic_bytes_per_launch": r["bytes"], "kernel_ms_per_launch": round(ms, 5),
                          "launches_timed": n_l},
         })
-    elif w in ("prefill8k", "prefill8k_i8"):
+    elif w in ("prefill8k", "prefill8k_i8", "prefill8k_h256"):
         i8 = w == "prefill8k_i8"
-        log(f"[bench] config 3: causal prefill 8192 tokens, 32q/8kv{' over the int8 cache' if i8 else ''}")
-        r = prefill_workload(torch, gi_attn, dev, 8192, 32, 8, args.steps, args.warmup, 99, i8=i8)
+        hd = 256 if w.endswith("_h256") else HD
+        nh, nkv = (16, 2) if hd == 256 else (32, 8)
+        log(f"[bench] causal prefill 8192 tokens, {nh}q/{nkv}kv, hd {hd}{' over the int8 cache' if i8 else ''}")
+        r = prefill_workload(torch, gi_attn, dev, 8192, nh, nkv, args.steps, args.warmup, 99, i8=i8, hd=hd)
         tf = r["flops"] / r["seconds"] / 1e12
         result.update({
             "value": round(tf, 1), "unit": "TFLOP/s", "ms_per_step": r["seconds"] * 1e3,
             "dtype": "int8 K/V widened to f16 MFMA, f32 acc" if i8 else "f16 MFMA, f32 acc",
-            "config": {"workload": "config 3: causal prefill, 8192 tokens, 32q/8kv, hd 128" +
-                                   (", int8 cache" if i8 else ""), "flops_per_step": r["flops"]},
+            "config": {"workload": (f"causal prefill, 8192 tokens, {nh}q/{nkv}kv, hd 256 (Qwen3.5-style heads)"
+                                    if hd == 256 else "config 3: causal prefill, 8192 tokens, 32q/8kv, hd 128" +
+                                    (", int8 cache" if i8 else "")), "flops_per_step": r["flops"]},
             "roofline": prefill_roofline(gi_attn, r, args.steps, torch, f"pmc_prefill_{w}",
-                                         "gi_prefill_fwd_i8" if i8 else "gi_prefill_fwd"),
+                                         "gi_prefill_fwd_i8" if i8 else "gi_prefill_fwd_h256" if hd == 256
+                                         else "gi_prefill_fwd"),
         })
     else:
         log("[bench] config 5: chunked prefill 131072 in 2048 chunks, 32q/4kv")

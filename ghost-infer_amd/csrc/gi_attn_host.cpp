@@ -137,9 +137,11 @@ struct Module {
     hipModule_t mod = nullptr;
     hipFunction_t dec[2][2][2] = {}; // [int8 cache][shared][column blocks - 1], head size 128
     hipFunction_t dec256[2][2] = {};  // [shared][column blocks - 1], head size 256 (f16 cache)
-    hipFunction_t prefill[2] = {};   // [int8 cache]
+    hipFunction_t prefill[2] = {};   // [int8 cache], head size 128
+    hipFunction_t prefill256 = nullptr; // head size 256 (f16 cache)
     hipFunction_t combine = nullptr, rope = nullptr;
     int prefill_threads = 0; // the prefill kernel's block size (its launch bound: waves x 64)
+    int prefill256_threads = 0;
 };
 std::mutex g_mu;
 Module g_mods[kMaxDevices];
@@ -182,6 +184,7 @@ int load_module(const char* path, Module** out) {
             {&m.combine, "gi_decode_combine"},
             {&m.prefill[0], "gi_prefill_fwd"},
             {&m.prefill[1], "gi_prefill_fwd_i8"},
+            {&m.prefill256, "gi_prefill_fwd_h256"},
             {&m.rope, "gi_qk_norm_rope"},
         };
         for (auto& f : fns)
@@ -191,7 +194,9 @@ int load_module(const char* path, Module** out) {
                 return e;
             }
         if (int e = check(hipFuncGetAttribute(&m.prefill_threads, HIP_FUNC_ATTRIBUTE_MAX_THREADS_PER_BLOCK, m.prefill[0]),
-                          "hipFuncGetAttribute(gi_prefill_fwd)")) {
+                          "hipFuncGetAttribute(gi_prefill_fwd)") ||
+                    check(hipFuncGetAttribute(&m.prefill256_threads, HIP_FUNC_ATTRIBUTE_MAX_THREADS_PER_BLOCK, m.prefill256),
+                          "hipFuncGetAttribute(gi_prefill_fwd_h256)")) {
             (void)hipModuleUnload(m.mod);
             m.mod = nullptr;
             return e;
@@ -425,7 +430,7 @@ int prefill_impl(void* stream, const void* q, int q_dtype, long long q_stride, c
                  const float* ks, const float* vs, long long sc_stride, long long sc_head_stride, bool i8,
                  long long kv_stride, long long kv_head_stride, void* out, int out_dtype, long long out_stride, int pos0,
                  int n, int n_heads, int n_kv, int hd, float scale) {
-    if (int e = check_shape(n_heads, n_kv, hd)) return e;
+    if (int e = check_shape(n_heads, n_kv, hd, !i8)) return e;
     if (n <= 0 || pos0 < 0) return fail("n %d must be positive and pos0 %d >= 0", n, pos0);
     if (!q || !kc || !vc || !out) return fail("null tensor pointer");
     if ((q_dtype != GI_F32 && q_dtype != GI_F16) || (out_dtype != GI_F32 && out_dtype != GI_F16))
@@ -463,9 +468,12 @@ int prefill_impl(void* stream, const void* q, int q_dtype, long long q_stride, c
     a.qscale = scale * kLog2e;
     a.q_f16 = q_dtype == GI_F16;
     a.out_f16 = out_dtype == GI_F16;
-    const int bq = m->prefill_threads / 2; // query rows per workgroup: 32 per wave of 64 threads
+    const int threads = hd == 256 ? m->prefill256_threads : m->prefill_threads;
+    const int bq = threads / 2; // query rows per workgroup: 32 per wave of 64 threads
     int qtiles = (n + bq - 1) / bq;
-    return launch(kPrefill, m->prefill[i8], dim3(qtiles * n_heads, 1, 1), dim3(m->prefill_threads), (hipStream_t)stream, &a, sizeof a);
+    // head size 256: two workgroups per (head, query tile), one per half of the output dims
+    return launch(kPrefill, hd == 256 ? m->prefill256 : m->prefill[i8], dim3(qtiles * n_heads * (hd / 128), 1, 1),
+                  dim3(threads), (hipStream_t)stream, &a, sizeof a);
 }
 
 int attention_impl(void* stream, const float* qkv, const void* kc, const void* vc, const float* ks, const float* vs,
@@ -563,7 +571,7 @@ namespace {
 int attention_impl(void* stream, const float* qkv, const void* kc, const void* vc, const float* ks, const float* vs,
                    bool i8, float* out, void* workspace, size_t workspace_bytes, int pos0, const int* posp, int ctx_cap,
                    int n, int n_heads, int n_kv, int hd, int exact) {
-    if (int e = check_shape(n_heads, n_kv, hd)) return e;
+    if (int e = check_shape(n_heads, n_kv, hd, !i8)) return e;
     if (n <= 0) return fail("n %d must be positive", n);
     const long long q_dim = (long long)n_heads * hd, kv_dim = (long long)n_kv * hd, row = q_dim + 2 * kv_dim;
     const float scale = 1.0f / std::sqrt((float)hd);

@@ -830,46 +830,64 @@ typedef short gi_s4 __attribute__((__vector_size__(8))); // 4 f16 as ds_read_b64
 // and the tile's 64 key and value scales go to LDS beside it. Scores are the integer-key dot products
 // times the key scale (QK chains start from zero; s = acc * kscale - m); P V takes f16(p * vscale *
 // PF_I8_VBIAS) and the row sum the f16-rounded p, as the reference's pv / pf.
-template <bool I8>
+template <bool I8, int HD>
 __device__ __forceinline__ void gi_prefill_t(const GiPrefillArgs& a) {
+    static_assert(HD == 128 || (HD == 256 && !I8), "head sizes: 128 (f16, int8), 256 (f16)");
+    // head size 256: 32-key tiles, so a K or V tile is still 16 KB: staged as 64 half-rows of 256 bytes, keys
+    // 0..31 with dims 0..127 then keys 0..31 with dims 128..255, which is the 64-key tile's LDS image at head
+    // size 128 (every swizzle and operand read below is unchanged; the dim half stands where the key block
+    // was). As the reference's attention_prefill_tc256 (src/cuda.rs:2622-2623), a workgroup computes the
+    // output dims of one half (DS = 2 workgroups per head and query tile, each with all of QK): O^T of 128
+    // dims keeps a wave within half the register file, so two waves share each SIMD as at head size 128.
+    constexpr int WAVES = PF_WAVES;
+    constexpr int BQ = 32 * WAVES;  // query rows per workgroup
+    constexpr int SW = WAVES / 2;   // waves staging each of K and V
+    constexpr int LPW = 16 / SW;    // 1 KB loads per staging wave and tile
+    constexpr int BK = HD == 256 ? 32 : PF_BK; // keys per tile
+    constexpr int NBLK = BK / 32;   // S^T blocks of 32 keys
+    constexpr int KS = HD / 16;     // QK k-steps
+    constexpr int NDB = 4;          // O^T blocks of 32 dims: 128 output dims per workgroup
+    constexpr int DS = HD / 128;    // workgroups per (head, query tile), each with 128 output dims
     __shared__ __attribute__((aligned(1024))) unsigned char smem[PF_NBUF][2][PF_TILE]; // [buffer][K, V]
-    __shared__ __attribute__((aligned(16))) float scl[I8 ? PF_NBUF : 1][2][PF_BK];      // int8: [buffer][K, V] scales
+    __shared__ __attribute__((aligned(16))) float scl[I8 ? PF_NBUF : 1][2][BK];         // int8: [buffer][K, V] scales
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int G = a.n_heads / a.n_kv;
-    const int qtiles = (a.n + PF_BQ - 1) / PF_BQ;
+    const int qtiles = (a.n + BQ - 1) / BQ;
     const int nwg = gridDim.x;
     int j = blockIdx.x;
     if ((nwg & 7) == 0) j = (j & 7) * (nwg >> 3) + (j >> 3);
-    const int kvh = j / (qtiles * G);
-    const int rest = j % (qtiles * G);
-    const int qt = qtiles - 1 - rest / G;
-    const int h = kvh * G + rest % G;
-    const int q0 = qt * PF_BQ;
+    const int kvh = j / (qtiles * G * DS);
+    const int rest = j % (qtiles * G * DS);
+    const int qt = qtiles - 1 - rest / (G * DS);
+    const int h = kvh * G + (rest % (G * DS)) / DS;
+    const int dh = rest % DS; // the workgroup's half of the output dims (head size 256)
+    const int q0 = qt * BQ;
     const int kv_len = a.pos0 + a.n;
-    const int k_lim = min(kv_len, a.pos0 + q0 + PF_BQ); // keys any row of the tile may see
-    const int ntiles = (k_lim + PF_BK - 1) / PF_BK;
+    const int k_lim = min(kv_len, a.pos0 + q0 + BQ); // keys any row of the tile may see
+    const int ntiles = (k_lim + BK - 1) / BK;
     const long long kvs = a.kv_stride;
 
-    // ---- staging: the first half of the waves moves K rows, the second half V rows (PF_SW waves each,
-    // PF_LPW loads of 1 KB per wave and tile); wave w's load i covers tile rows 4*(PF_LPW*(w%PF_SW) + i)
+    // ---- staging: the first half of the waves moves K rows, the second half V rows (SW waves each,
+    // LPW loads of 1 KB per wave and tile); wave w's load i covers tile rows 4*(LPW*(w%SW) + i)
     // + lane/16, LDS unit lane%16 holding global unit (lane%16) ^ swizzle(row)
-    const bool stage_v = wave >= PF_SW;
+    const bool stage_v = wave >= SW;
     const uint16_t* sbase = (stage_v ? a.vc : a.kc) + kvh * a.kv_head_stride;
-    int soff[PF_LPW];
+    int soff[LPW];
 #pragma unroll
-    for (int i = 0; i < PF_LPW; i++) {
-        const int r = 4 * (PF_LPW * (wave % PF_SW) + i) + (lane >> 4);
+    for (int i = 0; i < LPW; i++) {
+        const int r = 4 * (LPW * (wave % SW) + i) + (lane >> 4);
         const int u = (lane & 15) ^ (stage_v ? ((r & 3) << 2) : (r & 15));
-        soff[i] = (r * (int)kvs + 8 * u) * 2;
+        // image row r: key r (head size 128); key r%32, dims 128*(r/32).. (head size 256)
+        soff[i] = HD == 256 ? ((r & 31) * (int)kvs + 128 * (r >> 5) + 8 * u) * 2 : (r * (int)kvs + 8 * u) * 2;
     }
     auto stage = [&](int t) {
-        const int t0 = t * PF_BK;
+        const int t0 = t * BK;
         __amdgpu_buffer_rsrc_t rs = gi_rsrc(sbase + (long long)t0 * kvs, (long long)(kv_len - t0) * kvs * 2);
-        unsigned char* dst = &smem[t & (PF_NBUF - 1)][stage_v ? 1 : 0][1024 * PF_LPW * (wave % PF_SW)];
+        unsigned char* dst = &smem[t & (PF_NBUF - 1)][stage_v ? 1 : 0][1024 * LPW * (wave % SW)];
 #pragma unroll
-        for (int i = 0; i < PF_LPW; i++)
+        for (int i = 0; i < LPW; i++)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (GI_LDS void*)(dst + 1024 * i), 16, soff[i], 0, 0, 0);
     };
     // int8 staging: thread -> tile row sr, 16-byte chunk sch (dims 16sch..16sch+15) of K and of V; threads
@@ -917,21 +935,21 @@ __device__ __forceinline__ void gi_prefill_t(const GiPrefillArgs& a) {
     // Q is held pre-multiplied by scale*log2(e), so scores come out of the MFMA in log2 units (the f16
     // rounding of the scaled value is the same size as the rounding of Q itself)
     const float qs = a.qscale;
-    h8 qf[8];
+    h8 qf[KS];
     {
         const int qr = qrow < a.n ? qrow : a.n - 1; // rows past n compute garbage that is never written
         if (a.q_f16) {
-            const _Float16* qp = (const _Float16*)a.q + (long long)qr * a.q_stride + h * 128 + 8 * half;
+            const _Float16* qp = (const _Float16*)a.q + (long long)qr * a.q_stride + h * HD + 8 * half;
 #pragma unroll
-            for (int ks = 0; ks < 8; ks++) {
+            for (int ks = 0; ks < KS; ks++) {
                 const h8 x = __builtin_bit_cast(h8, *reinterpret_cast<const u4*>(qp + 16 * ks));
 #pragma unroll
                 for (int e = 0; e < 8; e++) qf[ks][e] = (_Float16)((float)x[e] * qs);
             }
         } else {
-            const float* qp = (const float*)a.q + (long long)qr * a.q_stride + h * 128 + 8 * half;
+            const float* qp = (const float*)a.q + (long long)qr * a.q_stride + h * HD + 8 * half;
 #pragma unroll
-            for (int ks = 0; ks < 8; ks++) {
+            for (int ks = 0; ks < KS; ks++) {
                 float4 x0 = *reinterpret_cast<const float4*>(qp + 16 * ks);
                 float4 x1 = *reinterpret_cast<const float4*>(qp + 16 * ks + 4);
                 qf[ks] = h8{(_Float16)(x0.x * qs), (_Float16)(x0.y * qs), (_Float16)(x0.z * qs), (_Float16)(x0.w * qs),
@@ -952,9 +970,9 @@ __device__ __forceinline__ void gi_prefill_t(const GiPrefillArgs& a) {
     const int vbase = (8 * half + te) * 256 + ((2 * (tg & 1) + (tc >> 1)) << 4) + 8 * (tc & 1);
 
     // ---- per-lane state: O^T (4 dim blocks of 32), reference max (log2 units; tile 0 sets it), row sum
-    f16x o[4];
+    f16x o[NDB];
 #pragma unroll
-    for (int db = 0; db < 4; db++)
+    for (int db = 0; db < NDB; db++)
 #pragma unroll
         for (int e = 0; e < 16; e++) o[db][e] = 0.f;
     float m_run = 0.f, l_run = 0.f;
@@ -964,21 +982,24 @@ __device__ __forceinline__ void gi_prefill_t(const GiPrefillArgs& a) {
 
     // S^T of tile t (its K in buffer t%4) minus the row's reference max: each chain starts from C = negm,
     // so the MFMA output is the exp2 argument itself
+    // MFMA st of a tile's 16: head size 128 alternates the two key blocks (k-step st/2, image half st%2);
+    // head size 256 has one key block, k-step st, its dims in image half st/8
+    auto kfrag = [&](const unsigned char* K, int st) {
+        const int reg = HD == 256 ? st >> 3 : st & 1, ksr = HD == 256 ? st & 7 : st >> 1;
+        return *reinterpret_cast<const h8*>(K + 8192 * reg + kbase + 32 * (ksr ^ ky));
+    };
     auto qk = [&](int t, f16x* s) {
         const unsigned char* K = &smem[t & (PF_NBUF - 1)][0][0];
         // K fragments stream through a ring of PF_KPF registers, each read PF_KPF MFMAs before its use
         h8 kf[PF_KPF];
 #pragma unroll
-        for (int st = 0; st < PF_KPF; st++)
-            kf[st] = *reinterpret_cast<const h8*>(K + 8192 * (st & 1) + kbase + 32 * ((st >> 1) ^ ky));
+        for (int st = 0; st < PF_KPF; st++) kf[st] = kfrag(K, st);
         __builtin_amdgcn_sched_barrier(0); // the first PF_KPF reads go out before any of the MFMAs
 #pragma unroll
         for (int st = 0; st < 16; st++) {
-            const int ks = st >> 1, bb = st & 1;
+            const int ks = HD == 256 ? st : st >> 1, bb = HD == 256 ? 0 : st & 1;
             const h8 cur = kf[st % PF_KPF];
-            if (st + PF_KPF < 16)
-                kf[st % PF_KPF] =
-                    *reinterpret_cast<const h8*>(K + 8192 * ((st + PF_KPF) & 1) + kbase + 32 * (((st + PF_KPF) >> 1) ^ ky));
+            if (st + PF_KPF < 16) kf[st % PF_KPF] = kfrag(K, st + PF_KPF);
             s[bb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(cur, qf[ks], ks == 0 ? (I8 ? f16x{} : negm) : s[bb], 0, 0, 0);
         }
     };
@@ -1002,7 +1023,7 @@ __device__ __forceinline__ void gi_prefill_t(const GiPrefillArgs& a) {
 
     const int wave_first = a.pos0 + q0 + 32 * wave;  // position of the wave's first row
     const int wave_last = wave_first + 31;
-    const int my_tiles = min(ntiles, wave_last / PF_BK + 1); // tiles this wave computes
+    const int my_tiles = min(ntiles, wave_last / BK + 1); // tiles this wave computes
     typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 
     // Prologue: tiles 0-2 start loading; tile 0 is waited for and published, and its QK issued. (int8:
@@ -1020,8 +1041,8 @@ __device__ __forceinline__ void gi_prefill_t(const GiPrefillArgs& a) {
         stage(0);
         if (ntiles > 1) stage(1);
         if (ntiles > 2) stage(2);
-        if (ntiles > 2) __builtin_amdgcn_s_waitcnt(GI_VMCNT(2 * PF_LPW)); // tile 0 is in
-        else if (ntiles > 1) __builtin_amdgcn_s_waitcnt(GI_VMCNT(PF_LPW));
+        if (ntiles > 2) __builtin_amdgcn_s_waitcnt(GI_VMCNT(2 * LPW)); // tile 0 is in
+        else if (ntiles > 1) __builtin_amdgcn_s_waitcnt(GI_VMCNT(LPW));
         else __builtin_amdgcn_s_waitcnt(GI_VMCNT(0));
     }
     asm volatile("s_barrier" ::: "memory");
@@ -1033,7 +1054,7 @@ __device__ __forceinline__ void gi_prefill_t(const GiPrefillArgs& a) {
     auto rowmax = [&](const f16x* sc) {
         float mx = GI_NEG_INF;
 #pragma unroll
-        for (int bb = 0; bb < 2; bb++)
+        for (int bb = 0; bb < NBLK; bb++)
 #pragma unroll
             for (int e = 0; e < 16; e++) mx = fmaxf(mx, sc[bb][e]);
         const auto p = __builtin_amdgcn_permlane32_swap(__float_as_int(mx), __float_as_int(mx), false, false);
@@ -1057,15 +1078,15 @@ __device__ __forceinline__ void gi_prefill_t(const GiPrefillArgs& a) {
             for (int e = 0; e < 16; e++) negm[e] = -m_run;
             l_run *= alpha;
 #pragma unroll
-            for (int db = 0; db < 4; db++) o[db] *= alpha;
+            for (int db = 0; db < NDB; db++) o[db] *= alpha;
 #pragma unroll
-            for (int bb = 0; bb < 2; bb++) s[bb] -= delta;
+            for (int bb = 0; bb < NBLK; bb++) s[bb] -= delta;
         }
         qk(it + 1, sn);
         // probabilities of k-step ks feed the PV MFMAs of k-step ks
         const unsigned char* V = &smem[it & (PF_NBUF - 1)][1][0];
 #pragma unroll
-        for (int ks = 0; ks < 4; ks++) {
+        for (int ks = 0; ks < BK / 16; ks++) {
             const int bb = ks >> 1;
             h8 pf;
 #pragma unroll
@@ -1085,8 +1106,8 @@ __device__ __forceinline__ void gi_prefill_t(const GiPrefillArgs& a) {
                 l_run = __builtin_amdgcn_fdot2(h2{h0, h1}, h2{(_Float16)1.f, (_Float16)1.f}, l_run, false);
             }
 #pragma unroll
-            for (int db = 0; db < 4; db++) {
-                const unsigned char* vp = V + vbase + ((db ^ te) << 6) + 4096 * ks;
+            for (int db = 0; db < NDB; db++) { // (head size 256: dims 128dh.. in the image's half dh)
+                const unsigned char* vp = V + 8192 * dh + vbase + ((db ^ te) << 6) + 4096 * ks;
                 gi_s4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((GI_LDS gi_s4*)(vp));
                 gi_s4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((GI_LDS gi_s4*)(vp + 1024));
                 h8 vf = __builtin_shufflevector(__builtin_bit_cast(h4x, lo), __builtin_bit_cast(h4x, hi),
@@ -1146,7 +1167,7 @@ __device__ __forceinline__ void gi_prefill_t(const GiPrefillArgs& a) {
         if constexpr (I8) {
             __builtin_amdgcn_s_waitcnt(0xC07F); // lgkmcnt(0)
         } else {
-            if (it + 2 < ntiles) __builtin_amdgcn_s_waitcnt(GI_VMCNT(PF_LPW)); // tile it+2's loads may stay in flight
+            if (it + 2 < ntiles) __builtin_amdgcn_s_waitcnt(GI_VMCNT(LPW)); // tile it+2's loads may stay in flight
             else __builtin_amdgcn_s_waitcnt(GI_VMCNT(0));
         }
         asm volatile("s_barrier" ::: "memory");
@@ -1159,12 +1180,12 @@ __device__ __forceinline__ void gi_prefill_t(const GiPrefillArgs& a) {
             if (it + 3 < ntiles) stage(it + 3);
         }
         if (it < my_tiles) {
-            const int t0 = it * PF_BK;
-            if (t0 + PF_BK - 1 > wave_first) { // the tile crosses the diagonal (or the end) somewhere in the wave
+            const int t0 = it * BK;
+            if (t0 + BK - 1 > wave_first) { // the tile crosses the diagonal (or the end) somewhere in the wave
                 // lane holds, for query qcol: block bb, element 4i + jj -> tile key 32bb + 16(i/2) + 8*half + 4(i%2) + jj
                 const int lim = qpos - t0 - 8 * half;
 #pragma unroll
-                for (int bb = 0; bb < 2; bb++)
+                for (int bb = 0; bb < NBLK; bb++)
 #pragma unroll
                     for (int i = 0; i < 4; i++)
 #pragma unroll
@@ -1175,7 +1196,7 @@ __device__ __forceinline__ void gi_prefill_t(const GiPrefillArgs& a) {
             step(it, s, sn, mx);
         }
     };
-    f16x sa[2], sb[2]; // scores of alternate tiles
+    f16x sa[NBLK], sb[NBLK]; // scores of alternate tiles
     if (my_tiles > 0) {
         qk(0, sa);
         kscale(0, sa);
@@ -1191,9 +1212,9 @@ __device__ __forceinline__ void gi_prefill_t(const GiPrefillArgs& a) {
     if (qrow < a.n) {
         const float inv = (I8 ? 1.f / PF_I8_VBIAS : 1.f) / l;
         if (a.out_f16) {
-            _Float16* op = (_Float16*)a.out + (long long)qrow * a.out_stride + h * 128 + 4 * half;
+            _Float16* op = (_Float16*)a.out + (long long)qrow * a.out_stride + h * HD + 128 * dh + 4 * half;
 #pragma unroll
-            for (int db = 0; db < 4; db++)
+            for (int db = 0; db < NDB; db++)
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
                     h4x v = h4x{(_Float16)(o[db][4 * i] * inv), (_Float16)(o[db][4 * i + 1] * inv),
@@ -1201,9 +1222,9 @@ __device__ __forceinline__ void gi_prefill_t(const GiPrefillArgs& a) {
                     *reinterpret_cast<h4x*>(op + 32 * db + 8 * i) = v;
                 }
         } else {
-            float* op = (float*)a.out + (long long)qrow * a.out_stride + h * 128 + 4 * half;
+            float* op = (float*)a.out + (long long)qrow * a.out_stride + h * HD + 128 * dh + 4 * half;
 #pragma unroll
-            for (int db = 0; db < 4; db++)
+            for (int db = 0; db < NDB; db++)
 #pragma unroll
                 for (int i = 0; i < 4; i++)
                     *reinterpret_cast<float4*>(op + 32 * db + 8 * i) =
@@ -1212,8 +1233,9 @@ __device__ __forceinline__ void gi_prefill_t(const GiPrefillArgs& a) {
     }
 }
 
-extern "C" __global__ void __launch_bounds__(64 * PF_WAVES, 1) gi_prefill_fwd(GiPrefillArgs a) { gi_prefill_t<false>(a); }
-extern "C" __global__ void __launch_bounds__(64 * PF_WAVES, 1) gi_prefill_fwd_i8(GiPrefillArgs a) { gi_prefill_t<true>(a); }
+extern "C" __global__ void __launch_bounds__(64 * PF_WAVES, 1) gi_prefill_fwd(GiPrefillArgs a) { gi_prefill_t<false, 128>(a); }
+extern "C" __global__ void __launch_bounds__(64 * PF_WAVES, 1) gi_prefill_fwd_i8(GiPrefillArgs a) { gi_prefill_t<true, 128>(a); }
+extern "C" __global__ void __launch_bounds__(64 * PF_WAVES, 1) gi_prefill_fwd_h256(GiPrefillArgs a) { gi_prefill_t<false, 256>(a); }
 
 // ------------------------------------------------------------------------------------------------ KV store
 

@@ -18,6 +18,7 @@
 //                                     RMSNorm of q/k heads, RoPE, K/V rows into the f16 cache
 //   gio_kv_quant_i8                   src/cuda.rs:333-339 (kv_store with KV8: row max / 127, rint)
 //   gio_qk_norm_rope_i8               src/cuda.rs:437-486 storing with kv_quant_i8
+//   gio_prefill_tc256                 gio_prefill_tc at head size 256 (attention_prefill_tc256, src/cuda.rs:2623)
 //   gio_prefill_tc_i8                 gio_prefill_tc over the KV8 cache (src/cuda.rs:2466-2498, 2548-2605:
 //                                     integer keys, score times key scale, P V with f16(p * vs * 2^10))
 //   gio_decode_gpu_i8                 gio_decode_gpu over the KV8 cache (src/cuda.rs:209-226, 1758-1760,
@@ -372,11 +373,13 @@ void decode_gpu(const float* qkv, long q_stride, const KV_T* kc, const KV_T* vc,
 // O = alpha*O + P V; out = O / l.
 // KV_T = int8_t: the KV8 build (src/cuda.rs:2466-2498, 2548-2605): keys staged as exact integers, the score
 // times the key's scale; P V takes f16(p * vscale * 2^10) and the row sum the f16-rounded p; out = O / 2^10 / l.
+// hd: 128, or 256 (attention_prefill_tc256 = attn_prefill_tc<256, 2>, src/cuda.rs:2623: the same roundings; its
+// two blocks per head split the output dims only).
 template <typename KV_T>
 void prefill_tc(const float* q, long q_stride, const KV_T* kc, const KV_T* vc, const float* ks, const float* vs,
                 long kv_stride, float* out, long out_stride, int pos0, int n, int n_heads, int n_kv, float scale,
-                int threads) {
-    const int hd = 128, BK = 32, G = n_heads / n_kv;
+                int threads, int hd = 128) {
+    const int BK = 32, G = n_heads / n_kv;
     const float* W = widen().v;
     const float vbias = ks ? 1024.f : 1.f;
     const float qs = scale * 1.4426950408889634f;
@@ -384,7 +387,7 @@ void prefill_tc(const float* q, long q_stride, const KV_T* kc, const KV_T* vc, c
     auto row_task = [&](long idx) {
         int r = (int)(idx / n_heads), h = (int)(idx % n_heads);
         int kvh = h / G;
-        float qh[128], o[128] = {0};
+        float qh[256], o[256] = {0};
         for (int d = 0; d < hd; d++) qh[d] = W[f32_to_f16(q[(long)r * q_stride + (long)h * hd + d] * qs)];
         int p_row = pos0 + r;
         float m = -std::numeric_limits<float>::infinity(), l = 0.f;
@@ -552,6 +555,13 @@ void gio_prefill_tc(const float* q, long q_stride, const uint16_t* kc, const uin
                     long out_stride, int pos0, int n, int n_heads, int n_kv, float scale, int threads) {
     prefill_tc<uint16_t>(q, q_stride, kc, vc, nullptr, nullptr, kv_stride, out, out_stride, pos0, n, n_heads, n_kv, scale,
                          threads);
+}
+
+// attn_prefill_tc<256, 2> (f16 cache, head size 256): kv_stride in elements, rows of hd = 256.
+void gio_prefill_tc256(const float* q, long q_stride, const uint16_t* kc, const uint16_t* vc, long kv_stride, float* out,
+                       long out_stride, int pos0, int n, int n_heads, int n_kv, float scale, int threads) {
+    prefill_tc<uint16_t>(q, q_stride, kc, vc, nullptr, nullptr, kv_stride, out, out_stride, pos0, n, n_heads, n_kv, scale,
+                         threads, 256);
 }
 
 // attn_prefill_tc<128> with the KV8 cache: kc / vc int8 rows, ks / vs f32 scales [pos][n_kv].

@@ -49,6 +49,7 @@ def lib():
         L.gio_decode_gpu_i8.argtypes = [vp, l, vp, vp, vp, vp, l, vp, l, i, i, i, i, f, i, i, i, i]
         L.gio_kv_quant_i8.argtypes = [vp, l, i, vp, vp]
         L.gio_prefill_tc_i8.argtypes = [vp, l, vp, vp, vp, vp, l, vp, l, i, i, i, i, f, i]
+        L.gio_prefill_tc256.argtypes = [vp, l, vp, vp, l, vp, l, i, i, i, i, f, i]
         _lib = L
     return _lib
 
@@ -161,16 +162,18 @@ def kv_quant_i8(x):
     return q, sc
 
 
-def prefill_tc_semantics(q, kc, vc, pos0, n_heads, n_kv, scale=None, threads=8):
-    """attn_prefill_tc<128> (src/cuda.rs:2408-2617): f16-rounded Q*scale*log2(e) and P."""
+def prefill_tc_semantics(q, kc, vc, pos0, n_heads, n_kv, scale=None, threads=8, hd=128):
+    """attn_prefill_tc<128> (src/cuda.rs:2408-2617): f16-rounded Q*scale*log2(e) and P; hd=256 follows
+    attention_prefill_tc256 (src/cuda.rs:2623), the same arithmetic."""
     q = _rows(q, np.float32)
     n = q.shape[0]
     kc, vc = _rows(kc, np.uint16), _rows(vc, np.uint16)
     if scale is None:
-        scale = 1.0 / np.sqrt(128)
-    out = np.zeros((n, n_heads * 128), dtype=np.float32)
-    lib().gio_prefill_tc(_p(q), q.shape[1], _p(kc), _p(vc), kc.shape[1], _p(out), out.shape[1], pos0, n, n_heads,
-                         n_kv, scale, threads)
+        scale = 1.0 / np.sqrt(hd)
+    out = np.zeros((n, n_heads * hd), dtype=np.float32)
+    fn = lib().gio_prefill_tc256 if hd == 256 else lib().gio_prefill_tc
+    assert hd in (128, 256)
+    fn(_p(q), q.shape[1], _p(kc), _p(vc), kc.shape[1], _p(out), out.shape[1], pos0, n, n_heads, n_kv, scale, threads)
     return out
 
 

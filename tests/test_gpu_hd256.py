@@ -90,3 +90,88 @@ def test_decode_hd256_device_position(gpu):
         torch.cuda.synchronize()
         assert_close(out.cpu().numpy(), reference_f64(q, k, v, pos, n_heads, n_kv, hd=HD), max_abs=2e-5,
                      rel_l2=2e-5, what=f"hd256 posp {pos}")
+
+
+# ---------------------------------------------------------------- prefill (attention_prefill_tc256)
+
+PREFILL_SHAPES_256 = [
+    # (n, pos0, n_heads, n_kv, q dtype, out dtype, layout): one tile, diagonal and tile edges (32 keys,
+    # 128 query rows per workgroup), chunks at a prefix, both layouts
+    (16, 0, 8, 2, np.float16, torch.float32, "reference"),
+    (33, 0, 4, 1, np.float32, torch.float32, "reference"),
+    (128, 0, 16, 2, np.float16, torch.float16, "reference"),
+    (129, 0, 8, 8, np.float16, torch.float32, "head_major"),
+    (300, 40, 16, 2, np.float32, torch.float32, "reference"),
+    (70, 130, 8, 4, np.float16, torch.float32, "head_major"),
+    (1000, 24, 16, 2, np.float16, torch.float32, "reference"),
+]
+
+
+@pytest.mark.parametrize("n,pos0,n_heads,n_kv,qd,od,layout", PREFILL_SHAPES_256)
+def test_prefill_hd256(gpu, n, pos0, n_heads, n_kv, qd, od, layout):
+    say("prefill hd256", n, pos0, n_heads, n_kv, qd.__name__, od, layout)
+    q, k, v = make_inputs(7000 + n + pos0, n, pos0 + n, n_heads, n_kv, hd=HD, q_dtype=qd)
+    qt, kt, vt = to_dev(q, k, v, gpu, n_kv, layout)
+    out = gi_attn.prefill(qt, kt, vt, pos0, n_heads, n_kv, hd=HD, out_dtype=od, kv_layout=layout)
+    torch.cuda.synchronize()
+    got = out.float().cpu().numpy()
+    q32 = q.astype(np.float32)
+    assert_close(got, O.prefill_tc_semantics(q32, k, v, pos0, n_heads, n_kv, hd=HD),
+                 what="prefill hd256 vs oracle (attention_prefill_tc256 semantics)")
+    assert_close(got, reference_f64(q32, k, v, pos0, n_heads, n_kv, hd=HD), what="prefill hd256 vs f64")
+
+
+def test_prefill_hd256_4096(gpu):
+    # a 4096-token prompt with 256-wide heads (16 query / 2 kv heads): the whole output against a torch fp32
+    # reference on the GPU, sampled rows against float64
+    n, n_heads, n_kv = 4096, 16, 2
+    say("prefill hd256 4096 16q/2kv")
+    q, k, v = make_inputs(71, n, n, n_heads, n_kv, hd=HD, q_dtype=np.float16)
+    qt, kt, vt = to_dev(q, k, v, gpu, n_kv)
+    out = gi_attn.prefill(qt, kt, vt, 0, n_heads, n_kv, hd=HD, out_dtype=torch.float16)
+    G = n_heads // n_kv
+    Q = qt.view(n, n_heads, HD).float()
+    K, V = kt.view(n, n_kv, HD).float(), vt.view(n, n_kv, HD).float()
+    mask = torch.arange(n, device=gpu)[None, :] > torch.arange(n, device=gpu)[:, None]
+    ref = torch.empty((n, n_heads, HD), dtype=torch.float32, device=gpu)
+    for h in range(n_heads):
+        s = (Q[:, h] @ K[:, h // G].T) / HD ** 0.5
+        s.masked_fill_(mask, float("-inf"))
+        ref[:, h] = torch.softmax(s, dim=-1) @ V[:, h // G]
+    torch.cuda.synchronize()
+    got = out.float().cpu().numpy()
+    assert_close(got, ref.view(n, -1).cpu().numpy(), what="prefill hd256 4096 vs torch fp32")
+    for r in (0, 31, 32, 127, 128, 4095):
+        assert_close(got[r:r + 1], reference_f64(q[r:r + 1], k, v, r, n_heads, n_kv, hd=HD),
+                     what=f"prefill hd256 row {r} vs f64")
+
+
+def test_chunked_prefill_hd256_matches_whole_prompt(gpu):
+    n, chunk, n_heads, n_kv = 768, 256, 16, 2
+    q, k, v = make_inputs(72, n, n, n_heads, n_kv, hd=HD, q_dtype=np.float16)
+    qt, kt, vt = to_dev(q, k, v, gpu, n_kv)
+    whole = gi_attn.prefill(qt, kt, vt, 0, n_heads, n_kv, hd=HD, out_dtype=torch.float32)
+    parts = []
+    for c0 in range(0, n, chunk):
+        say("hd256 chunk at", c0)
+        parts.append(gi_attn.prefill(qt[c0:c0 + chunk], kt, vt, c0, n_heads, n_kv, hd=HD, out_dtype=torch.float32))
+    torch.cuda.synchronize()
+    assert np.array_equal(torch.cat(parts).cpu().numpy(), whole.cpu().numpy())
+
+
+@pytest.mark.parametrize("n,pos0,exact", [(1, 99, False), (8, 300, True), (20, 0, False), (40, 17, True)])
+def test_attention_operator_hd256(gpu, n, pos0, exact):
+    say("operator hd256", n, pos0, exact)
+    n_heads, n_kv = 16, 2
+    row = n_heads * HD + 2 * n_kv * HD
+    qkv = np.random.default_rng(97 + n).standard_normal((n, row), dtype=np.float32)
+    _, k, v = make_inputs(98 + n, 1, pos0 + n, n_heads, n_kv, hd=HD)
+    qkv_t = torch.from_numpy(qkv).to(gpu)
+    _, kt, vt = to_dev(qkv[:, :1], k, v, gpu, n_kv)
+    out = gi_attn.attention(qkv_t, kt, vt, pos0, n_heads, n_kv, hd=HD, exact=exact)
+    torch.cuda.synchronize()
+    q = np.ascontiguousarray(qkv[:, :n_heads * HD])
+    split_path = n < 16 or exact
+    assert_close(out.cpu().numpy(), reference_f64(q, k, v, pos0, n_heads, n_kv, hd=HD),
+                 max_abs=2e-5 if split_path else 2e-3, rel_l2=2e-5 if split_path else 1e-3,
+                 what="operator hd256 vs f64")

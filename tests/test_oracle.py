@@ -420,3 +420,19 @@ def test_prefill_i8_unit_scales_follow_the_f16_path():
     want = O.prefill_tc_semantics(q, k.astype(np.float16).view(np.uint16), v.astype(np.float16).view(np.uint16), 120,
                                   8, 2)
     np.testing.assert_allclose(got, want, rtol=0, atol=1e-4)
+
+
+@pytest.mark.parametrize("n,pos0,n_heads,n_kv", [(48, 0, 4, 2), (70, 33, 4, 1)])
+def test_prefill_tc_semantics_hd256_within_parity_bar(n, pos0, n_heads, n_kv):
+    # attention_prefill_tc256's arithmetic (head size 256): within the bar of the exact attention, and its
+    # first 128 dims of V feed the first 128 output dims only (a head of 256 = two halves of P V)
+    q, k, v = make_inputs(81 + n, n, pos0 + n, n_heads, n_kv, hd=256)
+    got = O.prefill_tc_semantics(q, k, v, pos0, n_heads, n_kv, hd=256)
+    want = reference_f64(q, k, v, pos0, n_heads, n_kv, hd=256)
+    ma, _ = assert_close(got, want, what="prefill_tc hd256 semantics vs f64")
+    assert ma > 1e-6
+    v2 = v.reshape(v.shape[0], n_kv, 256).copy()
+    v2[:, :, 128:] = 0
+    got2 = O.prefill_tc_semantics(q, k, v2.reshape(v.shape), pos0, n_heads, n_kv, hd=256).reshape(n, n_heads, 256)
+    np.testing.assert_array_equal(got2[:, :, :128], got.reshape(n, n_heads, 256)[:, :, :128])
+    assert not got2[:, :, 128:].any()
