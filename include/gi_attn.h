@@ -22,7 +22,9 @@
  *    contiguous, which spreads a head's stream evenly over the HBM channels (the decode kernel is
  *    fastest with it). Strides are multiples of 8 elements and pointers 16-byte aligned.
  *  - Causality: token b of a call sits at position pos0 + b and attends to keys 0..pos0+b.
- *  - hd must be 128; n_heads must be a multiple of n_kv.
+ *  - hd is 128, or 256 with the f16 cache (the reference's wide heads: attention_partial_gqa's hd 256 branch
+ *    src/cuda.rs:1762-1781, attention_prefill_tc256 src/cuda.rs:2622-2623); n_heads must be a multiple of
+ *    n_kv. The int8 entry points take hd 128.
  */
 #ifndef GI_ATTN_H
 #define GI_ATTN_H
@@ -52,11 +54,13 @@ const char* gi_last_error(void);
 
 /* Slice plan of a decode call: keys per slice (`chunk`) and slices per token (`nsplit`) for tokens whose
  * largest span is max_span. Counterpart of att_want / att_chunk / max_splits (src/cuda.rs:8426-8444),
- * re-chosen for 256 CUs: slices are multiples of 128 keys and about one workgroup per CU in total. */
+ * re-chosen for 256 CUs: slices are multiples of 128 keys (64 at hd 256; the int8 kernels round up to 256)
+ * and about one workgroup per CU in total. */
 int gi_attn_decode_plan(int max_span, int n_tok, int n_heads, int n_kv, int hd, int* chunk, int* nsplit);
 
 /* Bytes of workspace gi_attn_decode needs for n_tok tokens whose spans reach at most ctx_cap keys (the
- * slice partials, [token][head][slice][hd + 4] f32: O, max, sum, 2 pad; 16-byte aligned). The
+ * slice partials, [token][head][slice][hd + 4] f32: O, max, sum, 2 pad; 16-byte aligned). Covers the int8
+ * entry points too. The
  * counterpart of the session's att_part buffer (GpuSession, src/cuda.rs:9826-9870). */
 size_t gi_attn_decode_workspace_bytes(int ctx_cap, int n_tok, int n_heads, int n_kv, int hd);
 
