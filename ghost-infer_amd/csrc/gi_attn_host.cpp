@@ -111,6 +111,7 @@ constexpr int kDecWaves = 4, kDecTile = 32, kDecPairs = 8; // slice partials are
 constexpr int kSliceUnit = kDecWaves * kDecTile; // 128 keys
 constexpr int kSplitMaxBatch = 15;                // tokens per split launch (src/cuda.rs:119)
 constexpr int kTiledMinBatch = 16;                // prefill from this many tokens (src/cuda.rs:95)
+constexpr int kPrefillRows = 256; // query rows per prefill workgroup; must match the kernels' PF_BQ
 
 thread_local std::string g_err;
 
@@ -140,7 +141,7 @@ struct Module {
     hipFunction_t prefill[2] = {};   // [int8 cache], head size 128
     hipFunction_t prefill256 = nullptr; // head size 256 (f16 cache)
     hipFunction_t combine = nullptr, rope = nullptr;
-    int prefill_threads = 0; // the prefill kernel's block size (its launch bound: waves x 64)
+    int prefill_threads[2] = {}; // each prefill kernel's block size (its launch bound: waves x 64)
     int prefill256_threads = 0;
 };
 std::mutex g_mu;
@@ -193,8 +194,10 @@ int load_module(const char* path, Module** out) {
                 m.mod = nullptr;
                 return e;
             }
-        if (int e = check(hipFuncGetAttribute(&m.prefill_threads, HIP_FUNC_ATTRIBUTE_MAX_THREADS_PER_BLOCK, m.prefill[0]),
+        if (int e = check(hipFuncGetAttribute(&m.prefill_threads[0], HIP_FUNC_ATTRIBUTE_MAX_THREADS_PER_BLOCK, m.prefill[0]),
                           "hipFuncGetAttribute(gi_prefill_fwd)") ||
+                    check(hipFuncGetAttribute(&m.prefill_threads[1], HIP_FUNC_ATTRIBUTE_MAX_THREADS_PER_BLOCK, m.prefill[1]),
+                          "hipFuncGetAttribute(gi_prefill_fwd_i8)") ||
                     check(hipFuncGetAttribute(&m.prefill256_threads, HIP_FUNC_ATTRIBUTE_MAX_THREADS_PER_BLOCK, m.prefill256),
                           "hipFuncGetAttribute(gi_prefill_fwd_h256)")) {
             (void)hipModuleUnload(m.mod);
@@ -468,9 +471,8 @@ int prefill_impl(void* stream, const void* q, int q_dtype, long long q_stride, c
     a.qscale = scale * kLog2e;
     a.q_f16 = q_dtype == GI_F16;
     a.out_f16 = out_dtype == GI_F16;
-    const int threads = hd == 256 ? m->prefill256_threads : m->prefill_threads;
-    const int bq = threads / 2; // query rows per workgroup: 32 per wave of 64 threads
-    int qtiles = (n + bq - 1) / bq;
+    const int threads = hd == 256 ? m->prefill256_threads : m->prefill_threads[i8];
+    int qtiles = (n + kPrefillRows - 1) / kPrefillRows;
     // head size 256: two workgroups per (head, query tile), one per half of the output dims
     return launch(kPrefill, hd == 256 ? m->prefill256 : m->prefill[i8], dim3(qtiles * n_heads * (hd / 128), 1, 1),
                   dim3(threads), (hipStream_t)stream, &a, sizeof a);
