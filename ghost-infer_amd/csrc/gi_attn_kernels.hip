@@ -882,7 +882,11 @@ __device__ __forceinline__ void gi_prefill_t(const GiPrefillArgs& a) {
         // image row r: key r (head size 128); key r%32, dims 128*(r/32).. (head size 256)
         soff[i] = HD == 256 ? ((r & 31) * (int)kvs + 128 * (r >> 5) + 8 * u) * 2 : (r * (int)kvs + 8 * u) * 2;
     }
+    // head size 256: the V image's rows 32*dh.. (this workgroup's dim half) are the only ones read, so the
+    // V waves staging the other half have nothing to load (their waits below hold with none outstanding)
+    const bool stage_idle = HD == 256 && stage_v && (4 * LPW * (wave % SW)) / 32 != dh;
     auto stage = [&](int t) {
+        if (stage_idle) return;
         const int t0 = t * BK;
         __amdgpu_buffer_rsrc_t rs = gi_rsrc(sbase + (long long)t0 * kvs, (long long)(kv_len - t0) * kvs * 2);
         unsigned char* dst = &smem[t & (PF_NBUF - 1)][stage_v ? 1 : 0][1024 * LPW * (wave % SW)];
