@@ -138,6 +138,7 @@ struct Module {
     hipModule_t mod = nullptr;
     hipFunction_t dec[2][2][2] = {}; // [int8 cache][shared][column blocks - 1], head size 128
     hipFunction_t dec256[2][2] = {};  // [shared][column blocks - 1], head size 256 (f16 cache)
+    hipFunction_t dec_pm[2][3] = {};  // [int8 cache][split 1, shared 1, shared 2]: one pair per column
     hipFunction_t prefill[2] = {};   // [int8 cache], head size 128
     hipFunction_t prefill256 = nullptr; // head size 256 (f16 cache)
     hipFunction_t combine = nullptr, rope = nullptr;
@@ -182,6 +183,12 @@ int load_module(const char* path, Module** out) {
             {&m.dec256[0][1], "gi_decode_partial_2_h256"},
             {&m.dec256[1][0], "gi_decode_shared_1_h256"},
             {&m.dec256[1][1], "gi_decode_shared_2_h256"},
+            {&m.dec_pm[0][0], "gi_decode_pm_1"},
+            {&m.dec_pm[0][1], "gi_decode_pm_shared_1"},
+            {&m.dec_pm[0][2], "gi_decode_pm_shared_2"},
+            {&m.dec_pm[1][0], "gi_decode_pm_1_i8"},
+            {&m.dec_pm[1][1], "gi_decode_pm_shared_1_i8"},
+            {&m.dec_pm[1][2], "gi_decode_pm_shared_2_i8"},
             {&m.combine, "gi_decode_combine"},
             {&m.prefill[0], "gi_prefill_fwd"},
             {&m.prefill[1], "gi_prefill_fwd_i8"},
@@ -258,28 +265,44 @@ int decode_target_wgs() {
     return target;
 }
 
-// Decode kernel variant for n_tok tokens of G heads per kv head: column blocks of 8 (token, head) pairs per
-// wave (1 or 2) and whether the 4 waves share the slice (each serving its own pairs) or split it.
+// Decode kernel variant for n_tok tokens of G heads per kv head (head size hd). Up to 8 (token, head) pairs:
+// one column block of 8 pairs, each pair's f16 high and remainder parts in two columns. More pairs (head
+// size 128): one pair per column (pm), 16 per column block, so no lane repeats its neighbour's softmax; up
+// to 16 pairs in one wave's block, up to 64 with the 4 waves sharing the slice, then two blocks per wave.
+// (Head size 256 keeps the two-column layout: 1 or 2 blocks per wave, shared beyond 16 pairs.)
 struct DecVariant {
     int ncb;
     bool shared;
+    bool pm;
     int groups; // workgroups per (slice, kv head)
 };
-DecVariant dec_variant(int n_tok, int G) {
+bool decode_pm() {
+    static bool on = [] {
+        const char* e = getenv("GI_DECODE_PM");
+        return !e || atoi(e) != 0;
+    }();
+    return on;
+}
+DecVariant dec_variant(int n_tok, int G, int hd = 128) {
     const int pairs = n_tok * G;
     DecVariant v;
-    v.ncb = (pairs > kDecPairs && pairs <= 2 * kDecPairs) || pairs > 4 * kDecPairs ? 2 : 1;
-    v.shared = pairs > 2 * kDecPairs;
-    const int per_wg = (v.shared ? 4 : 1) * kDecPairs * v.ncb;
+    v.pm = hd == 128 && pairs > kDecPairs && decode_pm();
+    if (v.pm) {
+        v.shared = pairs > 2 * kDecPairs;
+        v.ncb = pairs > 8 * kDecPairs ? 2 : 1;
+    } else {
+        v.ncb = (pairs > kDecPairs && pairs <= 2 * kDecPairs) || pairs > 4 * kDecPairs ? 2 : 1;
+        v.shared = pairs > 2 * kDecPairs;
+    }
+    const int per_wg = (v.shared ? 4 : 1) * kDecPairs * (v.pm ? 2 : 1) * v.ncb;
     v.groups = (pairs + per_wg - 1) / per_wg;
     return v;
 }
 
-// Slices are whole units of `unit` keys: one tile per wave (128 keys with the f16 cache's 32-key tiles,
-// 256 with int8's 64-key tiles), so the 4 waves of a workgroup get equal shares.
-void plan(int max_span, int n_tok, int n_heads, int n_kv, int* chunk, int* nsplit, int unit = kSliceUnit) {
+void plan(int max_span, int n_tok, int n_heads, int n_kv, int* chunk, int* nsplit, int unit = kSliceUnit,
+          int hd = 128) {
     int G = n_heads / n_kv;
-    int groups = dec_variant(n_tok, G).groups;
+    int groups = dec_variant(n_tok, G, hd).groups;
     int units = (max_span + unit - 1) / unit;
     int per_slot = std::max(1, decode_target_wgs() / std::max(1, n_kv * groups));
     int per = std::max(1, (units + per_slot - 1) / per_slot);
@@ -342,9 +365,9 @@ int decode_impl(void* stream, const float* q, long long q_stride, const void* kc
     if (posp && ctx_cap < n_tok) return fail("ctx_cap %d must cover the %d tokens", ctx_cap, n_tok);
     Module* m;
     if (int e = load_module(nullptr, &m)) return e;
-    const DecVariant var = dec_variant(n_tok, n_heads / n_kv);
+    const DecVariant var = dec_variant(n_tok, n_heads / n_kv, hd);
     GiDecodeArgs a{};
-    plan(max_span, n_tok, n_heads, n_kv, &a.chunk, &a.nsplit, slice_unit(i8, hd));
+    plan(max_span, n_tok, n_heads, n_kv, &a.chunk, &a.nsplit, slice_unit(i8, hd), hd);
     size_t need = a.nsplit == 1 ? 0 : (size_t)n_tok * n_heads * a.nsplit * (hd + 4) * sizeof(float);
     if (need && (!workspace || workspace_bytes < need))
         return fail("workspace of %zu bytes too small: %zu needed", workspace_bytes, need);
@@ -372,7 +395,9 @@ int decode_impl(void* stream, const float* q, long long q_stride, const void* kc
         a.sc_head_stride = sc_head_stride;
     }
     hipStream_t st = (hipStream_t)stream;
-    hipFunction_t f = hd == 256 ? m->dec256[var.shared][var.ncb - 1] : m->dec[i8][var.shared][var.ncb - 1];
+    hipFunction_t f = hd == 256 ? m->dec256[var.shared][var.ncb - 1]
+                      : var.pm  ? m->dec_pm[i8][var.shared ? var.ncb : 0]
+                                : m->dec[i8][var.shared][var.ncb - 1];
     if (int e = launch(kDecodePartial, f, dim3(a.nsplit, n_kv, var.groups), dim3(256), st, &a, sizeof a)) return e;
     if (a.nsplit > 1)
         if (int e = launch(kDecodeCombine, m->combine, dim3(n_heads, n_tok, kCombineSplit * hd / 128), dim3(64), st, &a,
@@ -497,7 +522,7 @@ int gi_attn_decode_plan(int max_span, int n_tok, int n_heads, int n_kv, int hd, 
     if (int e = check_shape(n_heads, n_kv, hd, true)) return e;
     if (max_span <= 0 || n_tok <= 0) return fail("max_span %d and n_tok %d must be positive", max_span, n_tok);
     if (!chunk || !nsplit) return fail("null output pointer");
-    plan(max_span, n_tok, n_heads, n_kv, chunk, nsplit, slice_unit(false, hd));
+    plan(max_span, n_tok, n_heads, n_kv, chunk, nsplit, slice_unit(false, hd), hd);
     return 0;
 }
 
@@ -510,7 +535,7 @@ size_t gi_attn_decode_workspace_bytes(int ctx_cap, int n_tok, int n_heads, int n
     size_t best = 16;
     int G = n_heads / n_kv;
     for (int t = 1; t <= n_tok; t++) {
-        int groups = dec_variant(t, G).groups;
+        int groups = dec_variant(t, G, hd).groups;
         int per_slot = std::max(1, decode_target_wgs() / std::max(1, n_kv * groups));
         int most = std::max(1, std::min(per_slot, (ctx_cap + unit - 1) / unit));
         best = std::max(best, (size_t)t * n_heads * most * (hd + 4) * sizeof(float));

@@ -83,6 +83,9 @@ struct GiDecodeArgs {
 // int8 cache: the probability's f16 remainder column is scaled by 2^12 (undone when the columns merge).
 // Times a value scale of ~0.03 the remainder would otherwise fall into f16's subnormal range.
 #define DEC_I8_LO 4096.f
+// (with one pair per column the high and remainder parts share an accumulator, so P times the value scale is
+// biased as a whole instead; the merge divides it out)
+#define DEC_I8_VB 64.f
 #define GI_RSRC_FLAGS 0x00020000
 
 __device__ __forceinline__ float wave_xor(float v, int m) { return __shfl_xor(v, m, 64); }
@@ -160,14 +163,20 @@ template <> struct DecBuf<false, 256> { u4 k[8]; u4 v[4][2]; };
 // exactly the B operand of v_mfma_f32_16x16x16_f16 for O^T += V^T P^T over the tile, so no key permutation
 // is needed. V^T block dd has A-row c = dim 16c + dd (the lane loads dims 16c..16c+15 of its 4 keys), so a
 // lane ends with dims 64grp..64grp+63 of its column.
+// PM = true (head size 128, blocks of more than 8 pairs): one (token, head) pair per column, 16 per column
+// block; the f16 high part and remainder of Q and of P are separate MFMAs into the same accumulator instead
+// of neighbouring columns, so a lane's softmax serves one pair and no lane repeats its neighbour's (half the
+// VALU per pair; twice the MFMAs per column, so blocks of at most 8 pairs keep PM = false).
 // SHARE = false: the 4 waves split the slice's tiles and serve the same DEC_PAIRS*NCB (token, head)
 // pairs, merging through LDS at the end. SHARE = true (many pairs per kv head, as in a verify block):
 // every wave walks the whole slice for its own DEC_PAIRS*NCB pairs, so one workgroup serves 4 times as
 // many pairs and the slice's K/V comes from HBM once (the waves' repeated loads of the same lines are
 // served by the caches).
-template <int NCB, bool SHARE, bool I8, int HD = 128>
+template <int NCB, bool SHARE, bool I8, int HD = 128, bool PM = false>
 __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
     static_assert(HD == 128 || (HD == 256 && !I8), "head sizes: 128 (f16, int8), 256 (f16)");
+    static_assert(!PM || HD == 128, "one pair per column: head size 128");
+    constexpr int CPAIRS = PM ? 2 * DEC_PAIRS : DEC_PAIRS; // pairs per column block
     constexpr int TILE = HD == 256 ? DEC_TILE / 2 : I8 ? 2 * DEC_TILE : DEC_TILE; // keys per wave tile
     constexpr int KK = HD / 32;                 // QK k-steps
     constexpr int ND = HD == 256 ? 16 : 8;      // O^T MFMA blocks
@@ -186,8 +195,8 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
     const int pos0 = a.posp ? *a.posp : a.pos0;
     const int G = a.n_heads / a.n_kv;
     const int npairs = a.n_tok * G;
-    constexpr int WG_PAIRS = (SHARE ? DEC_WAVES : 1) * DEC_PAIRS * NCB; // pairs per workgroup
-    const int pair0 = blockIdx.z * WG_PAIRS + (SHARE ? wave * DEC_PAIRS * NCB : 0); // this wave's first pair
+    constexpr int WG_PAIRS = (SHARE ? DEC_WAVES : 1) * CPAIRS * NCB; // pairs per workgroup
+    const int pair0 = blockIdx.z * WG_PAIRS + (SHARE ? wave * CPAIRS * NCB : 0); // this wave's first pair
     const int kv_len = pos0 + a.n_tok; // keys any token of the launch may see
     const int k_begin = s * a.chunk;
     const int nkeys = min(a.chunk, kv_len - k_begin); // keys of this slice (<= 0: an empty slice)
@@ -197,7 +206,7 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
     bool valid[NCB];
 #pragma unroll
     for (int cb = 0; cb < NCB; cb++) {
-        int pi = pair0 + cb * DEC_PAIRS + (c >> 1);
+        int pi = pair0 + cb * CPAIRS + (PM ? c : c >> 1);
         valid[cb] = pi < npairs;
         int t = valid[cb] ? pi / G : 0, g = valid[cb] ? pi % G : 0;
         span[cb] = valid[cb] ? min(pos0 + t + 1 - k_begin, nkeys) : 0; // keys of the slice this column sees
@@ -212,6 +221,7 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
     // B operand of S^T = K Qc^T. f16: k-step kk covers dims 32kk..32kk+31, this lane dims 32kk+8grp..+7.
     // int8: this lane dims 16grp + 8(kk%2) + 64(kk/2) .. +7 (the bytes its two 16-byte key loads bring)
     h8 qf[NCB][KK];
+    h8 qfl[NCB][KK]; // PM: the remainders (else unused)
     {
         __amdgpu_buffer_rsrc_t rq = gi_rsrc(a.q, (long long)a.n_tok * a.q_stride * 4);
 #pragma unroll
@@ -317,14 +327,18 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
             for (int b = 0; b < 2; b++) {
                 sacc[cb][b] = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-                for (int kk = 0; kk < 4; kk++)
+                for (int kk = 0; kk < 4; kk++) {
                     sacc[cb][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, B.k[b][kk]), qf[cb][kk],
                                                                          sacc[cb][b], 0, 0, 0);
+                    if constexpr (PM)
+                        sacc[cb][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, B.k[b][kk]),
+                                                                             qfl[cb][kk], sacc[cb][b], 0, 0, 0);
+                }
             }
         if (reload) load_k(B, t + DEC_NB * STRIDE);
         __builtin_amdgcn_sched_barrier(0);
         const bool masked = t + DEC_TILE > span_lo; // some valid column sees only part of this tile
-        h8 pf[NCB];
+        h8 pf[NCB], pfl[NCB];
 #pragma unroll
         for (int cb = 0; cb < NCB; cb++) {
             // this lane: column c, tile keys 8grp + 4b + j
@@ -334,7 +348,7 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
 #pragma unroll
                 for (int j = 0; j < 4; j++) {
                     float v = sacc[cb][b][j];
-                    v = v + lane_xor1(v); // hi + lo columns of the pair (same sum in both lanes)
+                    if constexpr (!PM) v = v + lane_xor1(v); // hi + lo columns of the pair (same sum in both lanes)
                     if (masked) {
                         int key = t + 8 * grp + 4 * b + j;
                         v = key < span[cb] ? v : GI_NEG_INF;
@@ -363,7 +377,12 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
                 float p = __builtin_amdgcn_exp2f(sc[i] - m_use);
                 psum += p;
                 _Float16 hi = (_Float16)p;
-                pf[cb][i] = (c & 1) ? (_Float16)(p - (float)hi) : hi;
+                if constexpr (PM) {
+                    pf[cb][i] = hi;
+                    pfl[cb][i] = (_Float16)(p - (float)hi);
+                } else {
+                    pf[cb][i] = (c & 1) ? (_Float16)(p - (float)hi) : hi;
+                }
             }
             l_run[cb] += psum;
         }
@@ -378,8 +397,10 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
             }
             const h8 vt = __builtin_bit_cast(h8, w);
 #pragma unroll
-            for (int cb = 0; cb < NCB; cb++)
+            for (int cb = 0; cb < NCB; cb++) {
                 o[cb][dd] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vt, pf[cb], o[cb][dd], 0, 0, 0);
+                if constexpr (PM) o[cb][dd] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vt, pfl[cb], o[cb][dd], 0, 0, 0);
+            }
         }
         __builtin_amdgcn_sched_barrier(0);
         if (reload) load_v(B, t + DEC_NB * STRIDE);
@@ -402,9 +423,13 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
             for (int cb = 0; cb < NCB; cb++) {
                 sacc[cb][b] = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-                for (int kk = 0; kk < 4; kk++)
+                for (int kk = 0; kk < 4; kk++) {
                     sacc[cb][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, kf[kk]), qf[cb][kk],
                                                                          sacc[cb][b], 0, 0, 0);
+                    if constexpr (PM)
+                        sacc[cb][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, kf[kk]), qfl[cb][kk],
+                                                                             sacc[cb][b], 0, 0, 0);
+                }
             }
         }
         const float ksc = B.ksc;
@@ -417,14 +442,15 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
         GI_BC(8) GI_BC(9) GI_BC(10) GI_BC(11) GI_BC(12) GI_BC(13) GI_BC(14) GI_BC(15)
 #undef GI_BC
         const bool masked = t + TILE > span_lo;
-        h8 pf[NCB][2]; // PV k-step ks: keys 16grp + 8ks + i
+        h8 pf[NCB][2], pfl[NCB][2]; // PV k-step ks: keys 16grp + 8ks + i
 #pragma unroll
         for (int cb = 0; cb < NCB; cb++) {
             float sc[16], mx = GI_NEG_INF;
 #pragma unroll
             for (int m = 0; m < 16; m++) {
                 float v = sacc[cb][m >> 2][m & 3];
-                v = (v + lane_xor1(v)) * ksb[m]; // hi + lo columns, then the key's scale
+                if constexpr (!PM) v = v + lane_xor1(v); // hi + lo columns of the pair
+                v *= ksb[m];                             // the key's scale
                 if (masked) v = t + 16 * grp + m < span[cb] ? v : GI_NEG_INF;
                 sc[m] = v;
                 mx = fmaxf(mx, v);
@@ -445,9 +471,14 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
             for (int m = 0; m < 16; m++) {
                 const float p = __builtin_amdgcn_exp2f(sc[m] - m_use);
                 psum += p;
-                const float pv = p * vsb[m];
+                const float pv = p * vsb[m] * (PM ? DEC_I8_VB : 1.f);
                 _Float16 hi = (_Float16)pv;
-                pf[cb][m >> 3][m & 7] = (c & 1) ? (_Float16)((pv - (float)hi) * DEC_I8_LO) : hi;
+                if constexpr (PM) {
+                    pf[cb][m >> 3][m & 7] = hi;
+                    pfl[cb][m >> 3][m & 7] = (_Float16)(pv - (float)hi);
+                } else {
+                    pf[cb][m >> 3][m & 7] = (c & 1) ? (_Float16)((pv - (float)hi) * DEC_I8_LO) : hi;
+                }
             }
             l_run[cb] += psum;
         }
@@ -472,6 +503,11 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
                 for (int cb = 0; cb < NCB; cb++) {
                     o[cb][dd] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, w0), pf[cb][ks], o[cb][dd], 0, 0, 0);
                     o[cb][dd + 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, w1), pf[cb][ks], o[cb][dd + 1], 0, 0, 0);
+                    if constexpr (PM) {
+                        o[cb][dd] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, w0), pfl[cb][ks], o[cb][dd], 0, 0, 0);
+                        o[cb][dd + 1] =
+                            __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, w1), pfl[cb][ks], o[cb][dd + 1], 0, 0, 0);
+                    }
                 }
             }
         }
@@ -576,7 +612,12 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
                 const uint32_t bits = qraw[cb][kk][e >> 2][e & 3];
                 float v = valid[cb] ? __uint_as_float(bits) * a.qscale : 0.f;
                 _Float16 hi = (_Float16)v;
-                qf[cb][kk][e] = (c & 1) ? (_Float16)(v - (float)hi) : hi;
+                if constexpr (PM) {
+                    qf[cb][kk][e] = hi;
+                    qfl[cb][kk][e] = (_Float16)(v - (float)hi);
+                } else {
+                    qf[cb][kk][e] = (c & 1) ? (_Float16)(v - (float)hi) : hi;
+                }
             }
     GI_TS(2);
     // Steady state: every buffer gets a further tile (those past the slice read zeros and are never
@@ -596,7 +637,7 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
     // stores; per pair the max and the sum over the 4 k-groups
     // (HD 256: 64 values, dims 64grp + 16j + dd, as 16 stores)
     __shared__ __attribute__((aligned(16))) float sm_o[DEC_WAVES][16 * NCB][HD + 4];
-    __shared__ float sm_m[DEC_WAVES][DEC_PAIRS * NCB], sm_l[DEC_WAVES][DEC_PAIRS * NCB];
+    __shared__ float sm_m[DEC_WAVES][CPAIRS * NCB], sm_l[DEC_WAVES][CPAIRS * NCB];
 #pragma unroll
     for (int cb = 0; cb < NCB; cb++) {
         float l = rows_sum(l_run[cb]);
@@ -608,26 +649,27 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
                 *reinterpret_cast<float4*>(row + 4 * q4) =
                     make_float4(o[cb][4 * q4][j], o[cb][4 * q4 + 1][j], o[cb][4 * q4 + 2][j], o[cb][4 * q4 + 3][j]);
         }
-        if (lane < 16 && (c & 1) == 0) {
-            sm_m[wave][cb * DEC_PAIRS + (c >> 1)] = m_run[cb];
-            sm_l[wave][cb * DEC_PAIRS + (c >> 1)] = l;
+        if (lane < 16 && (PM || (c & 1) == 0)) {
+            sm_m[wave][cb * CPAIRS + (PM ? c : c >> 1)] = m_run[cb];
+            sm_l[wave][cb * CPAIRS + (PM ? c : c >> 1)] = l;
         }
     }
     GI_TS(6);
     __syncthreads();
     GI_TS(7);
     // ---- merge the waves (SHARE: each pair has one wave) and the hi/lo columns: thread -> (pair, 4 dims)
-    constexpr float LO = I8 ? 1.f / DEC_I8_LO : 1.f;
+    constexpr float LO = I8 ? 1.f / DEC_I8_LO : 1.f;      // the remainder column's scale (PM: no column)
+    constexpr float OSC = I8 && PM ? 1.f / DEC_I8_VB : 1.f; // PM int8: the bias on P
 #pragma unroll
     for (int it = 0; it < WG_PAIRS * HD / 1024; it++) {
         const int item = threadIdx.x + 256 * it;
         const int pl = item / (HD / 4), d4 = 4 * (item % (HD / 4)); // pair within the workgroup
         const int pi = blockIdx.z * WG_PAIRS + pl;
-        const int w0 = SHARE ? pl / (DEC_PAIRS * NCB) : 0;   // the waves holding the pair
+        const int w0 = SHARE ? pl / (CPAIRS * NCB) : 0;   // the waves holding the pair
         const int w1 = SHARE ? w0 + 1 : DEC_WAVES;
-        const int lp = SHARE ? pl % (DEC_PAIRS * NCB) : pl;  // the pair within those waves
+        const int lp = SHARE ? pl % (CPAIRS * NCB) : pl;  // the pair within those waves
         if (pi < npairs) {
-            const int row = 16 * (lp >> 3) + 2 * (lp & 7);
+            const int row = PM ? lp : 16 * (lp >> 3) + 2 * (lp & 7); // its (first) column
             float M = GI_NEG_INF;
             for (int w = w0; w < w1; w++) M = fmaxf(M, sm_m[w][lp]);
             float L = 0.f;
@@ -635,13 +677,21 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
             if (M != GI_NEG_INF) {
                 for (int w = w0; w < w1; w++) {
                     const float wt = __builtin_amdgcn_exp2f(sm_m[w][lp] - M);
-                    const float4 hi = *reinterpret_cast<const float4*>(&sm_o[w][row][d4]);
-                    const float4 lo = *reinterpret_cast<const float4*>(&sm_o[w][row + 1][d4]);
                     L += wt * sm_l[w][lp];
-                    O.x += wt * (hi.x + lo.x * LO);
-                    O.y += wt * (hi.y + lo.y * LO);
-                    O.z += wt * (hi.z + lo.z * LO);
-                    O.w += wt * (hi.w + lo.w * LO);
+                    const float4 hi = *reinterpret_cast<const float4*>(&sm_o[w][row][d4]);
+                    if constexpr (PM) {
+                        const float ws = wt * OSC;
+                        O.x += ws * hi.x;
+                        O.y += ws * hi.y;
+                        O.z += ws * hi.z;
+                        O.w += ws * hi.w;
+                    } else {
+                        const float4 lo = *reinterpret_cast<const float4*>(&sm_o[w][row + 1][d4]);
+                        O.x += wt * (hi.x + lo.x * LO);
+                        O.y += wt * (hi.y + lo.y * LO);
+                        O.z += wt * (hi.z + lo.z * LO);
+                        O.w += wt * (hi.w + lo.w * LO);
+                    }
                 }
             }
             const int tk = pi / G, h = kvh * G + pi % G;
@@ -673,6 +723,8 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
 
 #define GI_DEC_KERNEL(name, NCB, SHARE, I8, HD) \
     extern "C" __global__ void __launch_bounds__(256, DEC_MINWG) name(GiDecodeArgs a) { gi_decode_partial_t<NCB, SHARE, I8, HD>(a); }
+#define GI_DEC_PM_KERNEL(name, NCB, SHARE, I8) \
+    extern "C" __global__ void __launch_bounds__(256, DEC_MINWG) name(GiDecodeArgs a) { gi_decode_partial_t<NCB, SHARE, I8, 128, true>(a); }
 GI_DEC_KERNEL(gi_decode_partial_1, 1, false, false, 128)
 GI_DEC_KERNEL(gi_decode_partial_2, 2, false, false, 128)
 GI_DEC_KERNEL(gi_decode_shared_1, 1, true, false, 128)
@@ -685,6 +737,12 @@ GI_DEC_KERNEL(gi_decode_partial_1_h256, 1, false, false, 256)
 GI_DEC_KERNEL(gi_decode_partial_2_h256, 2, false, false, 256)
 GI_DEC_KERNEL(gi_decode_shared_1_h256, 1, true, false, 256)
 GI_DEC_KERNEL(gi_decode_shared_2_h256, 2, true, false, 256)
+GI_DEC_PM_KERNEL(gi_decode_pm_1, 1, false, false)
+GI_DEC_PM_KERNEL(gi_decode_pm_shared_1, 1, true, false)
+GI_DEC_PM_KERNEL(gi_decode_pm_shared_2, 2, true, false)
+GI_DEC_PM_KERNEL(gi_decode_pm_1_i8, 1, false, true)
+GI_DEC_PM_KERNEL(gi_decode_pm_shared_1_i8, 1, true, true)
+GI_DEC_PM_KERNEL(gi_decode_pm_shared_2_i8, 2, true, true)
 
 // Merge the slices of each (token, head): M = max m_s, w_s = 2^(m_s - M), out = sum w_s O_s / sum w_s l_s
 // (attention_combine's maths in base 2; empty slices carry m = -inf and weigh nothing). One wave per

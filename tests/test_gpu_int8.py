@@ -65,6 +65,7 @@ DECODE_SHAPES_I8 = [
     (5, 77, 12, 4),
     (4, 40, 6, 1),
     (2, 63, 32, 4),  # wave 1's first tile (keys 64..) lies past token 0's span but not token 1's
+    (15, 700, 32, 4),  # 120 pairs per kv head: one pair per column, two column blocks, shared slice
 ]
 
 

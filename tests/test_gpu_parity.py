@@ -55,6 +55,7 @@ DECODE_SHAPES = [
     (5, 77, 12, 4),   # G = 3: (token, head) pairs straddle column blocks
     (4, 40, 6, 1),    # G = 6
     (2, 95, 32, 4),   # wave 3's first tile (keys 96..) lies past token 0's span but not token 1's
+    (15, 700, 32, 4), # 120 pairs per kv head: one pair per column, two column blocks, shared slice
 ]
 
 
