@@ -88,6 +88,19 @@ def kernel_times(gi_attn, fn, steps, torch, kinds):
     return res
 
 
+def decode_kernel_name(n_tok, n_heads, n_kv, hd, i8):
+    """Name of the split-K kernel a decode call of this shape launches: the host library's variant rule
+    (8 (token, head) pairs per column group; one pair per MFMA column above 8 pairs at head size 128,
+    4-wave shared groups above 16 pairs, two column groups per wave where that pays)."""
+    pairs, p = n_tok * (n_heads // n_kv), 8
+    if hd == 128 and pairs > p and os.environ.get("GI_DECODE_PM", "1") != "0":
+        name = f"gi_decode_pm_shared_{2 if pairs > 8 * p else 1}" if pairs > 2 * p else "gi_decode_pm_1"
+    else:
+        ncb = 2 if (p < pairs <= 2 * p) or pairs > 4 * p else 1
+        name = f"gi_decode_{'shared' if pairs > 2 * p else 'partial'}_{ncb}"
+    return name + ("_i8" if i8 else "") + ("_h256" if hd == 256 else "")
+
+
 def profile_traffic(name):
     """HBM bytes per launch of a kernel from the committed rocprofv3 --pmc summary profiles/<name>.md
     (its line "traffic_bytes_per_launch: N"), or None when there is none."""
@@ -342,7 +355,7 @@ def main():
                        "slices": nsplit, "keys_per_slice": chunk, "kv_layout": f"head_major [n_kv][ctx][{hd}]"},
             "roofline": {"bound": "hbm", "achieved": round(kern_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": round(kern_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
-                         "kernel": "gi_decode_partial_*_i8 (split-K pass)" if i8 else "gi_decode_partial (split-K pass)",
+                         "kernel": decode_kernel_name(n_tok, n_heads, n_kv, hd, i8) + " (split-K pass)",
                          "algorithmic_bytes_per_launch": part_bytes,
                          "kernel_ms_per_launch": round(part_ms, 5), "launches_timed": part_n,
                          "combine_ms_per_launch": round(comb_ms, 5) if comb_ms else None,
