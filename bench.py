@@ -90,11 +90,14 @@ def kernel_times(gi_attn, fn, steps, torch, kinds):
 
 def decode_kernel_name(n_tok, n_heads, n_kv, hd, i8):
     """Name of the split-K kernel a decode call of this shape launches: the host library's variant rule
-    (8 (token, head) pairs per column group; one pair per MFMA column above 8 pairs at head size 128,
-    4-wave shared groups above 16 pairs, two column groups per wave where that pays)."""
+    (8 (token, head) pairs per column group; one pair per MFMA column above 8 pairs at head size 128, two
+    column groups per wave at 17..32 and 64 such pairs, else 4-wave shared groups above 16 pairs)."""
     pairs, p = n_tok * (n_heads // n_kv), 8
     if hd == 128 and pairs > p and os.environ.get("GI_DECODE_PM", "1") != "0":
-        name = f"gi_decode_pm_shared_{2 if pairs > 8 * p else 1}" if pairs > 2 * p else "gi_decode_pm_1"
+        if 2 * p < pairs <= 4 * p or pairs == 8 * p:
+            name = "gi_decode_pm_2"
+        else:
+            name = f"gi_decode_pm_shared_{2 if pairs > 8 * p else 1}" if pairs > 2 * p else "gi_decode_pm_1"
     else:
         ncb = 2 if (p < pairs <= 2 * p) or pairs > 4 * p else 1
         name = f"gi_decode_{'shared' if pairs > 2 * p else 'partial'}_{ncb}"
@@ -302,6 +305,8 @@ def main():
                              "verify_i8", "prefill8k_i8", "decode64k_h256", "prefill8k_h256"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-secondary", action="store_true")
+    ap.add_argument("--n-tok", type=int, default=None,
+                    help="verify workloads: draft tokens per block (default 8, config 4's)")
     ap.add_argument("--reference-layout", action="store_true",
                     help="decode workloads: also time the reference's cache layout")
     args = ap.parse_args()
@@ -330,6 +335,9 @@ def main():
             "decode64k_h256": (65536, 16, 2, 1, "decode with 256-wide heads (Qwen3.5-style 16q/2kv), 1 token, "
                                                 "ctx 65536, f16 cache"),
         }[w]
+        if args.n_tok and w.startswith("verify") and args.n_tok != n_tok:
+            ctx, n_tok = 32768 + args.n_tok, args.n_tok
+            cfg = f"config 4's shape with {n_tok} tokens per block" + (" over the int8 cache" if w.endswith("_i8") else "")
         i8 = w.endswith("_i8")
         log(f"[bench] {cfg}")
         r = decode_workload(torch, gi_attn, dev, ctx, n_heads, n_kv, n_tok, args.steps, args.warmup, 1234, i8=i8,

@@ -71,6 +71,9 @@ struct GiDecodeArgs {
 #ifndef DEC_NB
 #define DEC_NB 2 // register buffers of K/V tiles per wave (tiles in flight)
 #endif
+#ifndef DEC_XCD_GROUPS // pair groups of one slice on one XCD
+#define DEC_XCD_GROUPS 1
+#endif
 #ifndef DEC_MINWG
 #define DEC_MINWG 1 // workgroups per CU the register budget is sized for
 #endif
@@ -195,7 +198,26 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int c = lane & 15, grp = lane >> 4;
-    const int s = blockIdx.x, kvh = blockIdx.y;
+    // workgroup -> (slice s, kv head, pair group gz). With several pair groups, the groups of one (slice, kv head)
+    // take linear ids 8 apart: workgroups go to the 8 XCDs round-robin, so they run on one XCD at about the same
+    // time and the later ones find the slice's K/V in that XCD's L2. The (slice, kv head) items past the last
+    // whole 8 take the ids left at the end, in plain order.
+    int s = blockIdx.x, kvh = blockIdx.y, gz = blockIdx.z;
+    if (DEC_XCD_GROUPS && gridDim.z > 1) {
+        const int lin = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
+        const int items = gridDim.x * gridDim.y, full = items & ~7;
+        int sk; // (slice, kv head) index
+        if (lin < full * (int)gridDim.z) {
+            gz = (lin >> 3) % gridDim.z;
+            sk = (lin / (8 * gridDim.z)) * 8 + (lin & 7);
+        } else {
+            const int r = lin - full * gridDim.z, tail = items - full;
+            gz = r / tail;
+            sk = full + r % tail;
+        }
+        s = sk % gridDim.x;
+        kvh = sk / gridDim.x;
+    }
 #ifdef GI_DEC_TIMESTAMPS
     unsigned long long ts[8];
     ts[0] = wall_clock64();
@@ -207,7 +229,7 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
     const int G = a.n_heads / a.n_kv;
     const int npairs = a.n_tok * G;
     constexpr int WG_PAIRS = (SHARE ? DEC_WAVES : 1) * CPAIRS * NCB; // pairs per workgroup
-    const int pair0 = blockIdx.z * WG_PAIRS + (SHARE ? wave * CPAIRS * NCB : 0); // this wave's first pair
+    const int pair0 = gz * WG_PAIRS + (SHARE ? wave * CPAIRS * NCB : 0); // this wave's first pair
     const int kv_len = pos0 + a.n_tok; // keys any token of the launch may see
     const int k_begin = s * a.chunk;
     const int nkeys = min(a.chunk, kv_len - k_begin); // keys of this slice (<= 0: an empty slice)
@@ -679,7 +701,7 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
     for (int it = 0; it < WG_PAIRS * HD / 1024; it++) {
         const int item = threadIdx.x + 256 * it;
         const int pl = item / (HD / 4), d4 = 4 * (item % (HD / 4)); // pair within the workgroup
-        const int pi = blockIdx.z * WG_PAIRS + pl;
+        const int pi = gz * WG_PAIRS + pl;
         const int w0 = SHARE ? pl / (CPAIRS * NCB) : 0;   // the waves holding the pair
         const int w1 = SHARE ? w0 + 1 : DEC_WAVES;
         const int lp = SHARE ? pl % (CPAIRS * NCB) : pl;  // the pair within those waves
@@ -725,7 +747,7 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
     ts[5] = wall_clock64();
     if (lane == 0) {
         unsigned long long* dbg = (unsigned long long*)(a.part + (long long)a.n_tok * a.n_heads * a.nsplit * PART);
-        long long w = ((long long)(blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x) * DEC_WAVES + wave;
+        long long w = ((long long)(gz * gridDim.y + kvh) * gridDim.x + s) * DEC_WAVES + wave;
         for (int i = 0; i < 6; i++) dbg[w * 16 + i] = ts[i];
         dbg[w * 16 + 8] = ts[6];
         dbg[w * 16 + 9] = ts[7];
@@ -758,6 +780,8 @@ GI_DEC_PM_KERNEL(gi_decode_pm_shared_2, 2, true, false)
 GI_DEC_PM_KERNEL(gi_decode_pm_1_i8, 1, false, true)
 GI_DEC_PM_KERNEL(gi_decode_pm_shared_1_i8, 1, true, true)
 GI_DEC_PM_KERNEL(gi_decode_pm_shared_2_i8, 2, true, true)
+GI_DEC_PM_KERNEL(gi_decode_pm_2, 2, false, false)
+GI_DEC_PM_KERNEL(gi_decode_pm_2_i8, 2, false, true)
 
 // Merge the slices of each (token, head): M = max m_s, w_s = 2^(m_s - M), out = sum w_s O_s / sum w_s l_s
 // (attention_combine's maths in base 2; empty slices carry m = -inf and weigh nothing). One wave per

@@ -66,6 +66,8 @@ DECODE_SHAPES_I8 = [
     (4, 40, 6, 1),
     (2, 63, 32, 4),  # wave 1's first tile (keys 64..) lies past token 0's span but not token 1's
     (15, 700, 32, 4),  # 120 pairs per kv head: one pair per column, two column blocks, shared slice
+    (4, 1000, 32, 4),  # 32 pairs: two full column blocks per wave, waves on tiles of their own
+    (6, 130, 32, 4),   # 48 pairs: one column block per wave, shared slice
 ]
 
 
