@@ -90,14 +90,11 @@ def kernel_times(gi_attn, fn, steps, torch, kinds):
 
 def decode_kernel_name(n_tok, n_heads, n_kv, hd, i8):
     """Name of the split-K kernel a decode call of this shape launches: the host library's variant rule
-    (8 (token, head) pairs per column group; one pair per MFMA column above 8 pairs at head size 128, two
-    column groups per wave at 17..32 and 64 such pairs, else 4-wave shared groups above 16 pairs)."""
+    (8 (token, head) pairs per column group; at head size 128 above 8 pairs one pair per MFMA column, and
+    two column groups per wave above 16; else 4-wave shared groups above 16 pairs)."""
     pairs, p = n_tok * (n_heads // n_kv), 8
     if hd == 128 and pairs > p and os.environ.get("GI_DECODE_PM", "1") != "0":
-        if 2 * p < pairs <= 4 * p or pairs == 8 * p:
-            name = "gi_decode_pm_2"
-        else:
-            name = f"gi_decode_pm_shared_{2 if pairs > 8 * p else 1}" if pairs > 2 * p else "gi_decode_pm_1"
+        name = "gi_decode_pm_2" if pairs > 2 * p else "gi_decode_pm_1"
     else:
         ncb = 2 if (p < pairs <= 2 * p) or pairs > 4 * p else 1
         name = f"gi_decode_{'shared' if pairs > 2 * p else 'partial'}_{ncb}"

@@ -138,7 +138,7 @@ struct Module {
     hipModule_t mod = nullptr;
     hipFunction_t dec[2][2][2] = {}; // [int8 cache][shared][column blocks - 1], head size 128
     hipFunction_t dec256[2][2] = {};  // [shared][column blocks - 1], head size 256 (f16 cache)
-    hipFunction_t dec_pm[2][4] = {};  // [int8 cache][split 1, shared 1, shared 2, split 2]: one pair per column
+    hipFunction_t dec_pm[2][2] = {};  // [int8 cache][column blocks - 1]: one pair per column
     hipFunction_t prefill[2] = {};   // [int8 cache], head size 128
     hipFunction_t prefill256 = nullptr; // head size 256 (f16 cache)
     hipFunction_t combine = nullptr, rope = nullptr;
@@ -184,13 +184,9 @@ int load_module(const char* path, Module** out) {
             {&m.dec256[1][0], "gi_decode_shared_1_h256"},
             {&m.dec256[1][1], "gi_decode_shared_2_h256"},
             {&m.dec_pm[0][0], "gi_decode_pm_1"},
-            {&m.dec_pm[0][1], "gi_decode_pm_shared_1"},
-            {&m.dec_pm[0][2], "gi_decode_pm_shared_2"},
+            {&m.dec_pm[0][1], "gi_decode_pm_2"},
             {&m.dec_pm[1][0], "gi_decode_pm_1_i8"},
-            {&m.dec_pm[1][1], "gi_decode_pm_shared_1_i8"},
-            {&m.dec_pm[1][2], "gi_decode_pm_shared_2_i8"},
-            {&m.dec_pm[0][3], "gi_decode_pm_2"},
-            {&m.dec_pm[1][3], "gi_decode_pm_2_i8"},
+            {&m.dec_pm[1][1], "gi_decode_pm_2_i8"},
             {&m.combine, "gi_decode_combine"},
             {&m.prefill[0], "gi_prefill_fwd"},
             {&m.prefill[1], "gi_prefill_fwd_i8"},
@@ -290,16 +286,13 @@ DecVariant dec_variant(int n_tok, int G, int hd = 128) {
     DecVariant v;
     v.pm = hd == 128 && pairs > kDecPairs && decode_pm();
     if (v.pm) {
-        v.shared = pairs > 2 * kDecPairs;
-        v.ncb = pairs > 8 * kDecPairs ? 2 : 1;
-        // 17..32 pairs, and 64: two column blocks per wave, each wave on slice tiles of its own (every tile
-        // is loaded and its V transposed once per workgroup, and each wave has two independent chains). Config
-        // 4's 64 pairs: 32.5 -> 30.4 us (f16), 32.5 -> 28.0 us (int8). At 33..63 pairs the second group is
-        // partly idle and the shared layout measured faster.
-        if ((pairs > 2 * kDecPairs && pairs <= 4 * kDecPairs) || pairs == 8 * kDecPairs) {
-            v.shared = false;
-            v.ncb = 2;
-        }
+        // above 16 pairs, two column blocks per wave, each wave on slice tiles of its own, and as many pair
+        // groups (workgroups per (slice, kv head), placed on one XCD) as needed: every tile is loaded,
+        // transposed and masked once per workgroup, and each wave has two independent MFMA chains. Measured
+        // against 4 waves sharing every tile: config 4's 64 pairs 32.5 -> 27.8 us (f16), 32.5 -> 28.4 us
+        // (int8); 96 pairs 36.5 -> 34.3 and 50.1 -> 35.5 us; equal at 48 and 128 pairs (f16).
+        v.shared = false;
+        v.ncb = pairs > 2 * kDecPairs ? 2 : 1;
     } else {
         v.ncb = (pairs > kDecPairs && pairs <= 2 * kDecPairs) || pairs > 4 * kDecPairs ? 2 : 1;
         v.shared = pairs > 2 * kDecPairs;
@@ -406,7 +399,7 @@ int decode_impl(void* stream, const float* q, long long q_stride, const void* kc
     }
     hipStream_t st = (hipStream_t)stream;
     hipFunction_t f = hd == 256 ? m->dec256[var.shared][var.ncb - 1]
-                      : var.pm  ? m->dec_pm[i8][var.shared ? var.ncb : var.ncb == 1 ? 0 : 3]
+                      : var.pm  ? m->dec_pm[i8][var.ncb - 1]
                                 : m->dec[i8][var.shared][var.ncb - 1];
     if (int e = launch(kDecodePartial, f, dim3(a.nsplit, n_kv, var.groups), dim3(256), st, &a, sizeof a)) return e;
     if (a.nsplit > 1)

@@ -775,12 +775,8 @@ GI_DEC_KERNEL(gi_decode_partial_2_h256, 2, false, false, 256)
 GI_DEC_KERNEL(gi_decode_shared_1_h256, 1, true, false, 256)
 GI_DEC_KERNEL(gi_decode_shared_2_h256, 2, true, false, 256)
 GI_DEC_PM_KERNEL(gi_decode_pm_1, 1, false, false)
-GI_DEC_PM_KERNEL(gi_decode_pm_shared_1, 1, true, false)
-GI_DEC_PM_KERNEL(gi_decode_pm_shared_2, 2, true, false)
-GI_DEC_PM_KERNEL(gi_decode_pm_1_i8, 1, false, true)
-GI_DEC_PM_KERNEL(gi_decode_pm_shared_1_i8, 1, true, true)
-GI_DEC_PM_KERNEL(gi_decode_pm_shared_2_i8, 2, true, true)
 GI_DEC_PM_KERNEL(gi_decode_pm_2, 2, false, false)
+GI_DEC_PM_KERNEL(gi_decode_pm_1_i8, 1, false, true)
 GI_DEC_PM_KERNEL(gi_decode_pm_2_i8, 2, false, true)
 
 // Merge the slices of each (token, head): M = max m_s, w_s = 2^(m_s - M), out = sum w_s O_s / sum w_s l_s

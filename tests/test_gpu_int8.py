@@ -50,7 +50,7 @@ def check(got, q, k, v, ks, vs, pos0, n_heads, n_kv, what):
 
 DECODE_SHAPES_I8 = [
     # (n_tok, pos0, n_heads, n_kv): spans inside one tile, at tile and slice edges, verify blocks of every
-    # kernel variant (1 and 2 column blocks, the shared-slice variant), G = 3 and 6 pair layouts
+    # kernel variant (1 and 2 column blocks, one to four pair groups), G = 3 and 6 pair layouts
     (1, 0, 32, 8),
     (1, 63, 32, 4),
     (1, 64, 32, 4),
@@ -65,9 +65,9 @@ DECODE_SHAPES_I8 = [
     (5, 77, 12, 4),
     (4, 40, 6, 1),
     (2, 63, 32, 4),  # wave 1's first tile (keys 64..) lies past token 0's span but not token 1's
-    (15, 700, 32, 4),  # 120 pairs per kv head: one pair per column, two column blocks, shared slice
-    (4, 1000, 32, 4),  # 32 pairs: two full column blocks per wave, waves on tiles of their own
-    (6, 130, 32, 4),   # 48 pairs: one column block per wave, shared slice
+    (15, 700, 32, 4),  # 120 pairs per kv head: one pair per column, four workgroups per (slice, kv head)
+    (4, 1000, 32, 4),  # 32 pairs: two full column blocks per wave
+    (6, 130, 32, 4),   # 48 pairs: two workgroups per (slice, kv head), the second half idle
 ]
 
 

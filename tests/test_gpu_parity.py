@@ -55,9 +55,9 @@ DECODE_SHAPES = [
     (5, 77, 12, 4),   # G = 3: (token, head) pairs straddle column blocks
     (4, 40, 6, 1),    # G = 6
     (2, 95, 32, 4),   # wave 3's first tile (keys 96..) lies past token 0's span but not token 1's
-    (15, 700, 32, 4), # 120 pairs per kv head: one pair per column, two column blocks, shared slice
-    (4, 1000, 32, 4),  # 32 pairs: two full column blocks per wave, waves on tiles of their own
-    (6, 130, 32, 4),   # 48 pairs: one column block per wave, shared slice
+    (15, 700, 32, 4), # 120 pairs per kv head: one pair per column, four workgroups per (slice, kv head)
+    (4, 1000, 32, 4),  # 32 pairs: two full column blocks per wave
+    (6, 130, 32, 4),   # 48 pairs: two workgroups per (slice, kv head), the second half idle
 ]
 
 
