@@ -299,7 +299,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="decode64k",
                     choices=["decode64k", "decode4k", "verify", "prefill8k", "chunked", "qkrope", "decode64k_i8",
-                             "verify_i8", "prefill8k_i8", "decode64k_h256", "prefill8k_h256"])
+                             "verify_i8", "prefill8k_i8", "decode64k_h256", "verify_h256", "prefill8k_h256"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--n-tok", type=int, default=None,
@@ -321,7 +321,7 @@ def main():
     result = {"metric": METRIC, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
               "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "data": "synthetic"}
     w = args.workload
-    if w in ("decode64k", "decode4k", "verify", "decode64k_i8", "verify_i8", "decode64k_h256"):
+    if w in ("decode64k", "decode4k", "verify", "decode64k_i8", "verify_i8", "decode64k_h256", "verify_h256"):
         hd = 256 if w.endswith("_h256") else HD
         ctx, n_heads, n_kv, n_tok, cfg = {
             "decode64k": (65536, 32, 4, 1, "config 2: decode, 1 token, ctx 65536, 32q/4kv, hd 128"),
@@ -331,6 +331,8 @@ def main():
             "verify_i8": (32776, 32, 4, 8, "config 4 over the int8 cache: verify, 8 tokens at 32768, 32q/4kv"),
             "decode64k_h256": (65536, 16, 2, 1, "decode with 256-wide heads (Qwen3.5-style 16q/2kv), 1 token, "
                                                 "ctx 65536, f16 cache"),
+            "verify_h256": (32776, 16, 2, 8, "verify with 256-wide heads (Qwen3.5-style 16q/2kv), 8 tokens at a "
+                                             "32768-key prefix, f16 cache"),
         }[w]
         if args.n_tok and w.startswith("verify") and args.n_tok != n_tok:
             ctx, n_tok = 32768 + args.n_tok, args.n_tok
