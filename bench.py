@@ -90,10 +90,12 @@ def kernel_times(gi_attn, fn, steps, torch, kinds):
 
 def decode_kernel_name(n_tok, n_heads, n_kv, hd, i8):
     """Name of the split-K kernel a decode call of this shape launches: the host library's variant rule
-    (8 (token, head) pairs per column group; at head size 128 above 8 pairs one pair per MFMA column, and
-    two column groups per wave above 16; else 4-wave shared groups above 16 pairs)."""
+    (8 (token, head) pairs per column group; above 8 pairs one pair per MFMA column, with two column
+    groups per wave above 16 at head size 128, and 4 waves sharing each tile at head size 256)."""
     pairs, p = n_tok * (n_heads // n_kv), 8
-    if hd == 128 and pairs > p and os.environ.get("GI_DECODE_PM", "1") != "0":
+    if pairs > p and os.environ.get("GI_DECODE_PM", "1") != "0":
+        if hd == 256:
+            return "gi_decode_pm_shared_1_h256"
         name = "gi_decode_pm_2" if pairs > 2 * p else "gi_decode_pm_1"
     else:
         ncb = 2 if (p < pairs <= 2 * p) or pairs > 4 * p else 1

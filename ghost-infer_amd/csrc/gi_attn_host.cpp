@@ -139,6 +139,7 @@ struct Module {
     hipFunction_t dec[2][2][2] = {}; // [int8 cache][shared][column blocks - 1], head size 128
     hipFunction_t dec256[2][2] = {};  // [shared][column blocks - 1], head size 256 (f16 cache)
     hipFunction_t dec_pm[2][2] = {};  // [int8 cache][column blocks - 1]: one pair per column
+    hipFunction_t dec_pm256 = {};     // head size 256, one pair per column, 4 waves sharing each tile
     hipFunction_t prefill[2] = {};   // [int8 cache], head size 128
     hipFunction_t prefill256 = nullptr; // head size 256 (f16 cache)
     hipFunction_t combine = nullptr, rope = nullptr;
@@ -187,6 +188,7 @@ int load_module(const char* path, Module** out) {
             {&m.dec_pm[0][1], "gi_decode_pm_2"},
             {&m.dec_pm[1][0], "gi_decode_pm_1_i8"},
             {&m.dec_pm[1][1], "gi_decode_pm_2_i8"},
+            {&m.dec_pm256, "gi_decode_pm_shared_1_h256"},
             {&m.combine, "gi_decode_combine"},
             {&m.prefill[0], "gi_prefill_fwd"},
             {&m.prefill[1], "gi_prefill_fwd_i8"},
@@ -284,7 +286,16 @@ bool decode_pm() {
 DecVariant dec_variant(int n_tok, int G, int hd = 128) {
     const int pairs = n_tok * G;
     DecVariant v;
-    v.pm = hd == 128 && pairs > kDecPairs && decode_pm();
+    v.pm = pairs > kDecPairs && decode_pm();
+    if (v.pm && hd == 256) {
+        // one pair per column, 4 waves of 16 pairs sharing every tile of the slice (two column blocks per wave
+        // exceed the register file at this head size). Against the hi/lo column layout: 16 pairs 23.2 ->
+        // 20.0 us, 24 pairs 26.6 -> 23.3, 64 pairs 42.1 -> 38.2, 128 pairs 61.7 -> 57.7 (32768 keys, 16/2).
+        v.shared = true;
+        v.ncb = 1;
+        v.groups = (pairs + 4 * 2 * kDecPairs - 1) / (4 * 2 * kDecPairs);
+        return v;
+    }
     if (v.pm) {
         // above 16 pairs, two column blocks per wave, each wave on slice tiles of its own, and as many pair
         // groups (workgroups per (slice, kv head), placed on one XCD) as needed: every tile is loaded,
@@ -398,7 +409,7 @@ int decode_impl(void* stream, const float* q, long long q_stride, const void* kc
         a.sc_head_stride = sc_head_stride;
     }
     hipStream_t st = (hipStream_t)stream;
-    hipFunction_t f = hd == 256 ? m->dec256[var.shared][var.ncb - 1]
+    hipFunction_t f = hd == 256 ? (var.pm ? m->dec_pm256 : m->dec256[var.shared][var.ncb - 1])
                       : var.pm  ? m->dec_pm[i8][var.ncb - 1]
                                 : m->dec[i8][var.shared][var.ncb - 1];
     if (int e = launch(kDecodePartial, f, dim3(a.nsplit, n_kv, var.groups), dim3(256), st, &a, sizeof a)) return e;

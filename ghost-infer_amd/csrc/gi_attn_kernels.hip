@@ -189,7 +189,7 @@ template <> struct DecBuf<false, 256> { u4 k[8]; u4 v[4][2]; };
 template <int NCB, bool SHARE, bool I8, int HD = 128, bool PM = false>
 __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
     static_assert(HD == 128 || (HD == 256 && !I8), "head sizes: 128 (f16, int8), 256 (f16)");
-    static_assert(!PM || HD == 128, "one pair per column: head size 128");
+    static_assert(!PM || !I8 || HD == 128, "one pair per column: head size 128, or 256 with the f16 cache");
     constexpr int CPAIRS = PM ? 2 * DEC_PAIRS : DEC_PAIRS; // pairs per column block
     constexpr int TILE = HD == 256 ? DEC_TILE / 2 : I8 ? 2 * DEC_TILE : DEC_TILE; // keys per wave tile
     constexpr int KK = HD / 32;                 // QK k-steps
@@ -558,20 +558,23 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
         for (int cb = 0; cb < NCB; cb++) {
             sacc[cb] = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int kk = 0; kk < 8; kk++)
+            for (int kk = 0; kk < 8; kk++) {
                 sacc[cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, B.k[kk]), qf[cb][kk], sacc[cb], 0, 0, 0);
+                if constexpr (PM)
+                    sacc[cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, B.k[kk]), qfl[cb][kk], sacc[cb], 0, 0, 0);
+            }
         }
         if (reload) load_k(B, t + DEC_NB * STRIDE);
         __builtin_amdgcn_sched_barrier(0);
         const bool masked = t + TILE > span_lo;
-        h4x pf[NCB]; // PV B operand: keys 4grp + j of column c
+        h4x pf[NCB], pfl[NCB]; // PV B operand: keys 4grp + j of column c (PM: high parts and remainders)
 #pragma unroll
         for (int cb = 0; cb < NCB; cb++) {
             float sc[4], mx = GI_NEG_INF;
 #pragma unroll
             for (int j = 0; j < 4; j++) {
                 float v = sacc[cb][j];
-                v = v + lane_xor1(v);
+                if constexpr (!PM) v = v + lane_xor1(v); // hi + lo columns of the pair
                 if (masked) v = t + 4 * grp + j < span[cb] ? v : GI_NEG_INF;
                 sc[j] = v;
                 mx = fmaxf(mx, v);
@@ -593,7 +596,12 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
                 const float p = __builtin_amdgcn_exp2f(sc[j] - m_use);
                 psum += p;
                 _Float16 hi = (_Float16)p;
-                pf[cb][j] = (c & 1) ? (_Float16)(p - (float)hi) : hi;
+                if constexpr (PM) {
+                    pf[cb][j] = hi;
+                    pfl[cb][j] = (_Float16)(p - (float)hi);
+                } else {
+                    pf[cb][j] = (c & 1) ? (_Float16)(p - (float)hi) : hi;
+                }
             }
             l_run[cb] += psum;
         }
@@ -609,8 +617,10 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
             }
             const h4x vt = __builtin_bit_cast(h4x, vw);
 #pragma unroll
-            for (int cb = 0; cb < NCB; cb++)
+            for (int cb = 0; cb < NCB; cb++) {
                 o[cb][dd] = __builtin_amdgcn_mfma_f32_16x16x16f16(vt, pf[cb], o[cb][dd], 0, 0, 0);
+                if constexpr (PM) o[cb][dd] = __builtin_amdgcn_mfma_f32_16x16x16f16(vt, pfl[cb], o[cb][dd], 0, 0, 0);
+            }
         }
         __builtin_amdgcn_sched_barrier(0);
         if (reload) load_v(B, t + DEC_NB * STRIDE);
@@ -778,6 +788,9 @@ GI_DEC_PM_KERNEL(gi_decode_pm_1, 1, false, false)
 GI_DEC_PM_KERNEL(gi_decode_pm_2, 2, false, false)
 GI_DEC_PM_KERNEL(gi_decode_pm_1_i8, 1, false, true)
 GI_DEC_PM_KERNEL(gi_decode_pm_2_i8, 2, false, true)
+#define GI_DEC_PM256_KERNEL(name, NCB, SHARE) \
+    extern "C" __global__ void __launch_bounds__(256, DEC_MINWG) name(GiDecodeArgs a) { gi_decode_partial_t<NCB, SHARE, false, 256, true>(a); }
+GI_DEC_PM256_KERNEL(gi_decode_pm_shared_1_h256, 1, true)
 
 // Merge the slices of each (token, head): M = max m_s, w_s = 2^(m_s - M), out = sum w_s O_s / sum w_s l_s
 // (attention_combine's maths in base 2; empty slices carry m = -inf and weigh nothing). One wave per

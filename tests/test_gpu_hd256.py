@@ -36,7 +36,7 @@ def to_dev(q, k, v, dev, n_kv, layout="reference"):
 
 DECODE_SHAPES_256 = [
     # (n_tok, pos0, n_heads, n_kv): spans inside one 16-key tile, at tile and slice edges, every kernel
-    # variant (1 and 2 column blocks, the shared-slice variant), G = 3
+    # variant (up to 8 pairs: 1 and 2 column blocks; above: one pair per column, shared slice), G = 3
     (1, 0, 16, 2),
     (1, 15, 16, 2),
     (1, 16, 32, 4),
@@ -49,6 +49,8 @@ DECODE_SHAPES_256 = [
     (15, 513, 16, 2),
     (5, 77, 12, 4),   # slice 1's second wave tile lies past token 0's span but not token 4's
     (2, 15, 16, 2),   # wave 1's first tile (keys 16..) lies past token 0's span but not token 1's
+    (3, 60, 16, 2),   # 24 pairs: one pair per column, waves 2 and 3 idle
+    (6, 130, 16, 2),  # 48 pairs
 ]
 
 
