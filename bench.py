@@ -90,16 +90,16 @@ def kernel_times(gi_attn, fn, steps, torch, kinds):
 
 def decode_kernel_name(n_tok, n_heads, n_kv, hd, i8):
     """Name of the split-K kernel a decode call of this shape launches: the host library's variant rule
-    (8 (token, head) pairs per column group; above 8 pairs one pair per MFMA column, with two column
-    groups per wave above 16 at head size 128, and 4 waves sharing each tile at head size 256)."""
+    (up to 8 (token, head) pairs per kv head: one column block with two columns per pair; above, one pair
+    per MFMA column, with two column blocks per wave above 16 pairs at head size 128, and 4 waves sharing
+    each tile at head size 256)."""
     pairs, p = n_tok * (n_heads // n_kv), 8
-    if pairs > p and os.environ.get("GI_DECODE_PM", "1") != "0":
-        if hd == 256:
-            return "gi_decode_pm_shared_1_h256"
-        name = "gi_decode_pm_2" if pairs > 2 * p else "gi_decode_pm_1"
+    if pairs <= p:
+        name = "gi_decode_partial_1"
+    elif hd == 256:
+        return "gi_decode_pm_shared_1_h256"
     else:
-        ncb = 2 if (p < pairs <= 2 * p) or pairs > 4 * p else 1
-        name = f"gi_decode_{'shared' if pairs > 2 * p else 'partial'}_{ncb}"
+        name = "gi_decode_pm_2" if pairs > 2 * p else "gi_decode_pm_1"
     return name + ("_i8" if i8 else "") + ("_h256" if hd == 256 else "")
 
 

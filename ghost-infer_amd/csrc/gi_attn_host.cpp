@@ -136,8 +136,8 @@ int check(hipError_t r, const char* what) {
 struct Module {
     bool loaded = false;
     hipModule_t mod = nullptr;
-    hipFunction_t dec[2][2][2] = {}; // [int8 cache][shared][column blocks - 1], head size 128
-    hipFunction_t dec256[2][2] = {};  // [shared][column blocks - 1], head size 256 (f16 cache)
+    hipFunction_t dec[2] = {};        // up to 8 pairs, head size 128: [int8 cache]
+    hipFunction_t dec256 = {};        // up to 8 pairs, head size 256 (f16 cache)
     hipFunction_t dec_pm[2][2] = {};  // [int8 cache][column blocks - 1]: one pair per column
     hipFunction_t dec_pm256 = {};     // head size 256, one pair per column, 4 waves sharing each tile
     hipFunction_t prefill[2] = {};   // [int8 cache], head size 128
@@ -172,18 +172,9 @@ int load_module(const char* path, Module** out) {
         std::string p = path ? std::string(path) : default_code_object();
         if (int e = check(hipModuleLoad(&m.mod, p.c_str()), ("hipModuleLoad(" + p + ")").c_str())) return e;
         struct { hipFunction_t* f; const char* name; } fns[] = {
-            {&m.dec[0][0][0], "gi_decode_partial_1"},
-            {&m.dec[0][0][1], "gi_decode_partial_2"},
-            {&m.dec[0][1][0], "gi_decode_shared_1"},
-            {&m.dec[0][1][1], "gi_decode_shared_2"},
-            {&m.dec[1][0][0], "gi_decode_partial_1_i8"},
-            {&m.dec[1][0][1], "gi_decode_partial_2_i8"},
-            {&m.dec[1][1][0], "gi_decode_shared_1_i8"},
-            {&m.dec[1][1][1], "gi_decode_shared_2_i8"},
-            {&m.dec256[0][0], "gi_decode_partial_1_h256"},
-            {&m.dec256[0][1], "gi_decode_partial_2_h256"},
-            {&m.dec256[1][0], "gi_decode_shared_1_h256"},
-            {&m.dec256[1][1], "gi_decode_shared_2_h256"},
+            {&m.dec[0], "gi_decode_partial_1"},
+            {&m.dec[1], "gi_decode_partial_1_i8"},
+            {&m.dec256, "gi_decode_partial_1_h256"},
             {&m.dec_pm[0][0], "gi_decode_pm_1"},
             {&m.dec_pm[0][1], "gi_decode_pm_2"},
             {&m.dec_pm[1][0], "gi_decode_pm_1_i8"},
@@ -266,50 +257,34 @@ int decode_target_wgs() {
 }
 
 // Decode kernel variant for n_tok tokens of G heads per kv head (head size hd). Up to 8 (token, head) pairs:
-// one column block of 8 pairs, each pair's f16 high and remainder parts in two columns. More pairs (head
-// size 128): one pair per column (pm), 16 per column block, so no lane repeats its neighbour's softmax; up
-// to 16 pairs in one wave's block, up to 64 with the 4 waves sharing the slice, then two blocks per wave.
-// (Head size 256 keeps the two-column layout: 1 or 2 blocks per wave, shared beyond 16 pairs.)
+// one column block of 8 pairs, each pair's f16 high and remainder parts in two columns (gi_decode_partial_1).
+// More pairs: one pair per column (pm), 16 per column block, the high and remainder parts as two MFMAs into
+// one accumulator, so no lane repeats its neighbour's softmax.
 struct DecVariant {
-    int ncb;
-    bool shared;
-    bool pm;
-    int groups; // workgroups per (slice, kv head)
+    int ncb;     // column blocks per wave
+    bool shared; // the 4 waves share every tile of the slice (else each wave takes tiles of its own)
+    bool pm;     // one pair per column
+    int groups;  // workgroups per (slice, kv head)
 };
-bool decode_pm() {
-    static bool on = [] {
-        const char* e = getenv("GI_DECODE_PM");
-        return !e || atoi(e) != 0;
-    }();
-    return on;
-}
 DecVariant dec_variant(int n_tok, int G, int hd = 128) {
     const int pairs = n_tok * G;
-    DecVariant v;
-    v.pm = pairs > kDecPairs && decode_pm();
-    if (v.pm && hd == 256) {
-        // one pair per column, 4 waves of 16 pairs sharing every tile of the slice (two column blocks per wave
-        // exceed the register file at this head size). Against the hi/lo column layout: 16 pairs 23.2 ->
-        // 20.0 us, 24 pairs 26.6 -> 23.3, 64 pairs 42.1 -> 38.2, 128 pairs 61.7 -> 57.7 (32768 keys, 16/2).
+    DecVariant v{1, false, pairs > kDecPairs, 1};
+    if (!v.pm) return v;
+    if (hd == 256) {
+        // 4 waves of 16 pairs sharing every tile of the slice (two column blocks per wave exceed the register
+        // file at this head size). Against the two-column layout: 16 pairs 23.2 -> 20.0 us, 24 pairs 26.6 ->
+        // 23.3, 64 pairs 42.1 -> 38.2, 128 pairs 61.7 -> 57.7 (32768 keys, 16/2).
         v.shared = true;
-        v.ncb = 1;
         v.groups = (pairs + 4 * 2 * kDecPairs - 1) / (4 * 2 * kDecPairs);
         return v;
     }
-    if (v.pm) {
-        // above 16 pairs, two column blocks per wave, each wave on slice tiles of its own, and as many pair
-        // groups (workgroups per (slice, kv head), placed on one XCD) as needed: every tile is loaded,
-        // transposed and masked once per workgroup, and each wave has two independent MFMA chains. Measured
-        // against 4 waves sharing every tile: config 4's 64 pairs 32.5 -> 27.8 us (f16), 32.5 -> 28.4 us
-        // (int8); 96 pairs 36.5 -> 34.3 and 50.1 -> 35.5 us; equal at 48 and 128 pairs (f16).
-        v.shared = false;
-        v.ncb = pairs > 2 * kDecPairs ? 2 : 1;
-    } else {
-        v.ncb = (pairs > kDecPairs && pairs <= 2 * kDecPairs) || pairs > 4 * kDecPairs ? 2 : 1;
-        v.shared = pairs > 2 * kDecPairs;
-    }
-    const int per_wg = (v.shared ? 4 : 1) * kDecPairs * (v.pm ? 2 : 1) * v.ncb;
-    v.groups = (pairs + per_wg - 1) / per_wg;
+    // head size 128, above 16 pairs: two column blocks per wave, each wave on slice tiles of its own, and as
+    // many pair groups (workgroups per (slice, kv head), placed on one XCD) as needed: every tile is loaded,
+    // transposed and masked once per workgroup, and each wave has two independent MFMA chains. Measured
+    // against 4 waves sharing every tile: config 4's 64 pairs 32.5 -> 27.8 us (f16), 32.5 -> 28.4 us
+    // (int8); 96 pairs 36.5 -> 34.3 and 50.1 -> 35.5 us; equal at 48 and 128 pairs (f16).
+    v.ncb = pairs > 2 * kDecPairs ? 2 : 1;
+    v.groups = (pairs + 2 * kDecPairs * v.ncb - 1) / (2 * kDecPairs * v.ncb);
     return v;
 }
 
@@ -409,9 +384,7 @@ int decode_impl(void* stream, const float* q, long long q_stride, const void* kc
         a.sc_head_stride = sc_head_stride;
     }
     hipStream_t st = (hipStream_t)stream;
-    hipFunction_t f = hd == 256 ? (var.pm ? m->dec_pm256 : m->dec256[var.shared][var.ncb - 1])
-                      : var.pm  ? m->dec_pm[i8][var.ncb - 1]
-                                : m->dec[i8][var.shared][var.ncb - 1];
+    hipFunction_t f = hd == 256 ? (var.pm ? m->dec_pm256 : m->dec256) : var.pm ? m->dec_pm[i8][var.ncb - 1] : m->dec[i8];
     if (int e = launch(kDecodePartial, f, dim3(a.nsplit, n_kv, var.groups), dim3(256), st, &a, sizeof a)) return e;
     if (a.nsplit > 1)
         if (int e = launch(kDecodeCombine, m->combine, dim3(n_heads, n_tok, kCombineSplit * hd / 128), dim3(64), st, &a,

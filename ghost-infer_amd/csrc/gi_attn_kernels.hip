@@ -773,17 +773,8 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
 #define GI_DEC_PM_KERNEL(name, NCB, SHARE, I8) \
     extern "C" __global__ void __launch_bounds__(256, DEC_MINWG) name(GiDecodeArgs a) { gi_decode_partial_t<NCB, SHARE, I8, 128, true>(a); }
 GI_DEC_KERNEL(gi_decode_partial_1, 1, false, false, 128)
-GI_DEC_KERNEL(gi_decode_partial_2, 2, false, false, 128)
-GI_DEC_KERNEL(gi_decode_shared_1, 1, true, false, 128)
-GI_DEC_KERNEL(gi_decode_shared_2, 2, true, false, 128)
 GI_DEC_KERNEL(gi_decode_partial_1_i8, 1, false, true, 128)
-GI_DEC_KERNEL(gi_decode_partial_2_i8, 2, false, true, 128)
-GI_DEC_KERNEL(gi_decode_shared_1_i8, 1, true, true, 128)
-GI_DEC_KERNEL(gi_decode_shared_2_i8, 2, true, true, 128)
 GI_DEC_KERNEL(gi_decode_partial_1_h256, 1, false, false, 256)
-GI_DEC_KERNEL(gi_decode_partial_2_h256, 2, false, false, 256)
-GI_DEC_KERNEL(gi_decode_shared_1_h256, 1, true, false, 256)
-GI_DEC_KERNEL(gi_decode_shared_2_h256, 2, true, false, 256)
 GI_DEC_PM_KERNEL(gi_decode_pm_1, 1, false, false)
 GI_DEC_PM_KERNEL(gi_decode_pm_2, 2, false, false)
 GI_DEC_PM_KERNEL(gi_decode_pm_1_i8, 1, false, true)
