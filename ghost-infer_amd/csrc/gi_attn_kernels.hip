@@ -138,17 +138,36 @@ __device__ __forceinline__ float gi_load4f(__amdgpu_buffer_rsrc_t r, int off) {
     return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
 }
 
-// int8 -> f16, exactly. With its sign bit flipped a byte is u = v + 128 in 0..255; the f16 with bits
-// 0x6400 | u is 1024 + u, so subtracting 1152 leaves v. x holds 4 bytes already flipped (x ^ 0x80808080);
-// v_perm picks bytes of {0x64646464 : x} (selector bytes 0-3 take x, 4-7 the constant).
+#ifndef GI_I8_SDWA // int8 -> f16 by sub-dword converts (1) or by byte permutes (0)
+#define GI_I8_SDWA 1
+#endif
+// int8 -> f16, exactly, two bytes of x (bytes 0-1 for GI_I8_LO, 2-3 for GI_I8_HI) into one f16 pair.
+// GI_I8_SDWA: v_cvt_f16_i16 reads one byte, sign-extended, through its sub-dword operand select and writes
+// one half of the result (the second keeps the first's half): one instruction per value, on the raw bytes.
+// Else: with its sign bit flipped a byte is u = v + 128 in 0..255; the f16 with bits 0x6400 | u is
+// 1024 + u, so subtracting 1152 leaves v. x then holds 4 bytes already flipped (gi_i8_in), and v_perm picks
+// bytes of {0x64646464 : x} (selector bytes 0-3 take x, 4-7 the constant).
 typedef _Float16 h2x __attribute__((ext_vector_type(2)));
+#define GI_I8_LO 0x04010400u // bytes 0, 1 of x -> f16 pair
+#define GI_I8_HI 0x04030402u // bytes 2, 3
+__device__ __forceinline__ uint32_t gi_i8_in(uint32_t x) { return GI_I8_SDWA ? x : x ^ 0x80808080u; }
 __device__ __forceinline__ uint32_t i8_f16x2(uint32_t x, uint32_t sel) {
+#if GI_I8_SDWA
+    uint32_t r;
+    if (sel == GI_I8_LO) {
+        asm("v_cvt_f16_i16_sdwa %0, sext(%1) dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:BYTE_0" : "=v"(r) : "v"(x));
+        asm("v_cvt_f16_i16_sdwa %0, sext(%1) dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:BYTE_1" : "+v"(r) : "v"(x));
+    } else {
+        asm("v_cvt_f16_i16_sdwa %0, sext(%1) dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:BYTE_2" : "=v"(r) : "v"(x));
+        asm("v_cvt_f16_i16_sdwa %0, sext(%1) dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:BYTE_3" : "+v"(r) : "v"(x));
+    }
+    return r;
+#else
     const h2x v = __builtin_bit_cast(h2x, __builtin_amdgcn_perm(0x64646464u, x, sel)) -
                   h2x{(_Float16)1152.f, (_Float16)1152.f};
     return __builtin_bit_cast(uint32_t, v);
+#endif
 }
-#define GI_I8_LO 0x04010400u // bytes 0, 1 of x -> f16 pair
-#define GI_I8_HI 0x04030402u // bytes 2, 3
 // v of lane 16*(l/16) + m: the lane's 16-lane row broadcasts its m-th lane (DPP row_newbcast)
 template <int M>
 __device__ __forceinline__ float row_bcast(float v) {
@@ -452,7 +471,7 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
             for (int half = 0; half < 2; half++)
 #pragma unroll
                 for (int e = 0; e < 4; e++) {
-                    const uint32_t x = B.k[b][half][e] ^ 0x80808080u;
+                    const uint32_t x = gi_i8_in(B.k[b][half][e]);
                     kf[2 * half + (e >> 1)][2 * (e & 1)] = i8_f16x2(x, GI_I8_LO);
                     kf[2 * half + (e >> 1)][2 * (e & 1) + 1] = i8_f16x2(x, GI_I8_HI);
                 }
@@ -522,7 +541,7 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
         // O^T += V^T P^T: for dims dd, dd+1 (bytes k, k+1 of word dd/4) and keys 2p, 2p+1 of a k-step, one
         // v_perm gathers the four bytes and two more widen them to the two f16 pairs
 #pragma unroll
-        for (int i = 0; i < 16; i++) B.v[i] ^= u2{0x80808080u, 0x80808080u};
+        for (int i = 0; i < 16; i++) B.v[i] = u2{gi_i8_in(B.v[i][0]), gi_i8_in(B.v[i][1])};
 #pragma unroll
         for (int dd = 0; dd < 8; dd += 2) {
             const int wi = dd >> 2, k = dd & 3;
@@ -1017,7 +1036,7 @@ __device__ __forceinline__ void gi_prefill_t(const GiPrefillArgs& a) {
             u4 kw, vw;
 #pragma unroll
             for (int e = 0; e < 2; e++) {
-                const uint32_t xk = rk[2 * hw + e] ^ 0x80808080u, xv = rv[2 * hw + e] ^ 0x80808080u;
+                const uint32_t xk = gi_i8_in(rk[2 * hw + e]), xv = gi_i8_in(rv[2 * hw + e]);
                 kw[2 * e] = i8_f16x2(xk, GI_I8_LO);
                 kw[2 * e + 1] = i8_f16x2(xk, GI_I8_HI);
                 vw[2 * e] = i8_f16x2(xv, GI_I8_LO);
