@@ -68,6 +68,7 @@ DECODE_SHAPES_I8 = [
     (15, 700, 32, 4),  # 120 pairs per kv head: one pair per column, four workgroups per (slice, kv head)
     (4, 1000, 32, 4),  # 32 pairs: two full column blocks per wave
     (6, 130, 32, 4),   # 48 pairs: two workgroups per (slice, kv head), the second half idle
+    (4, 40, 16, 1),    # 64 pairs on one kv head, one slice: fewer (slice, kv head) items than XCDs
 ]
 
 
