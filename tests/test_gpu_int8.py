@@ -48,6 +48,31 @@ def check(got, q, k, v, ks, vs, pos0, n_heads, n_kv, what):
                  what=f"{what} vs f64")
 
 
+def test_decode_i8_graph_replay(gpu):
+    # an 8-token verify block over the int8 cache with a device position, captured once and replayed at
+    # several positions with eager work between the replays
+    n_tok, n_heads, n_kv, cap = 8, 32, 4, 3000
+    q, k, v, ks, vs = make_inputs_i8(93, n_tok, cap, n_heads, n_kv)
+    qt, kt, vt, kst, vst = to_dev_i8(q, k, v, ks, vs, gpu)
+    ws = gi_attn.new_workspace(cap, n_tok, n_heads, n_kv, device=gpu)
+    posp = torch.zeros(1, dtype=torch.int32, device=gpu)
+    out = torch.zeros((n_tok, n_heads * 128), dtype=torch.float32, device=gpu)
+    kw = dict(out=out, workspace=ws, posp=posp, ctx_cap=cap, k_scale=kst, v_scale=vst)
+    gi_attn.decode(qt, kt, vt, 0, n_heads, n_kv, **kw)  # warm-up
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        gi_attn.decode(qt, kt, vt, 0, n_heads, n_kv, **kw)
+    for pos in (cap - n_tok, 40, 1500, 0):
+        say("decode i8 graph replay", pos)
+        posp.fill_(pos)
+        out.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert_close(out.cpu().numpy(), reference_f64_i8(q, k, v, ks, vs, pos, n_heads, n_kv), max_abs=2e-5,
+                     rel_l2=2e-5, what=f"i8 replay at {pos}")
+
+
 DECODE_SHAPES_I8 = [
     # (n_tok, pos0, n_heads, n_kv): spans inside one tile, at tile and slice edges, verify blocks of every
     # kernel variant (1 and 2 column blocks, one to four pair groups), G = 3 and 6 pair layouts

@@ -130,22 +130,24 @@ def test_decode_workspace_reuse_across_shapes(gpu):
                      what=f"reuse {n_tok}@{pos0}")
 
 
-def test_decode_graph_replay(gpu):
-    # a decode step with a device position captured once and replayed at several positions, with eager work
-    # between the replays; each replay matches the float64 reference
-    n_heads, n_kv, cap = 32, 8, 5000
-    q, k, v = make_inputs(91, 1, cap, n_heads, n_kv)
+@pytest.mark.parametrize("n_tok,n_heads,n_kv", [(1, 32, 8), (8, 32, 4)])
+def test_decode_graph_replay(gpu, n_tok, n_heads, n_kv):
+    # a decode step (or an 8-token verify block: two pair groups per slice) with a device position, captured
+    # once and replayed at several positions, with eager work between the replays; each replay matches the
+    # float64 reference
+    cap = 5000
+    q, k, v = make_inputs(91, n_tok, cap, n_heads, n_kv)
     qt, kt, vt = to_dev(q, k, v, gpu)
-    ws = gi_attn.new_workspace(cap, 1, n_heads, n_kv, device=gpu)
+    ws = gi_attn.new_workspace(cap, n_tok, n_heads, n_kv, device=gpu)
     posp = torch.zeros(1, dtype=torch.int32, device=gpu)
-    out = torch.zeros((1, n_heads * 128), dtype=torch.float32, device=gpu)
+    out = torch.zeros((n_tok, n_heads * 128), dtype=torch.float32, device=gpu)
     gi_attn.decode(qt, kt, vt, 0, n_heads, n_kv, out=out, workspace=ws, posp=posp, ctx_cap=cap)  # warm-up
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g):
         gi_attn.decode(qt, kt, vt, 0, n_heads, n_kv, out=out, workspace=ws, posp=posp, ctx_cap=cap)
-    for pos in (4999, 17, 2500, 4999, 0):
-        say("decode graph replay", pos)
+    for pos in (cap - n_tok, 17, 2500, cap - n_tok, 0):
+        say("decode graph replay", n_tok, pos)
         posp.fill_(pos)
         out.zero_()
         g.replay()
