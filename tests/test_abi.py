@@ -75,21 +75,24 @@ def test_int8_entry_points_reject_bad_arguments_before_any_launch():
     assert rc == -1 and "scale" in lib.gi_last_error().decode()
 
 
-@pytest.mark.parametrize("ctx,n_tok,n_heads,n_kv", [(4096, 1, 32, 8), (65536, 1, 32, 4), (32776, 8, 32, 4),
-                                                    (100, 15, 8, 1), (1, 1, 32, 4)])
-def test_decode_plan_covers_the_span(ctx, n_tok, n_heads, n_kv):
-    chunk, nsplit = gi_attn.decode_plan(ctx, n_tok, n_heads, n_kv)
-    assert chunk % 128 == 0 and chunk > 0
+@pytest.mark.parametrize("ctx,n_tok,n_heads,n_kv,hd", [(4096, 1, 32, 8, 128), (65536, 1, 32, 4, 128),
+                                                       (32776, 8, 32, 4, 128), (100, 15, 8, 1, 128),
+                                                       (1, 1, 32, 4, 128), (65536, 1, 16, 2, 256),
+                                                       (32776, 8, 16, 2, 256), (5000, 15, 16, 2, 256)])
+def test_decode_plan_covers_the_span(ctx, n_tok, n_heads, n_kv, hd):
+    part = (hd + 4) * 4  # bytes of one slice partial
+    chunk, nsplit = gi_attn.decode_plan(ctx, n_tok, n_heads, n_kv, hd)
+    assert chunk % (64 if hd == 256 else 128) == 0 and chunk > 0
     assert (nsplit - 1) * chunk < ctx <= nsplit * chunk
     if nsplit > 1:
         # every launch of up to n_tok tokens with spans up to ctx fits the workspace size query
-        need = n_tok * n_heads * nsplit * 132 * 4
-        assert gi_attn.workspace_bytes(ctx, n_tok, n_heads, n_kv) >= need
+        need = n_tok * n_heads * nsplit * part
+        assert gi_attn.workspace_bytes(ctx, n_tok, n_heads, n_kv, hd) >= need
     for span in (1, ctx // 3 + 1, ctx):
         for t in range(1, n_tok + 1):
-            c2, s2 = gi_attn.decode_plan(span, t, n_heads, n_kv)
+            c2, s2 = gi_attn.decode_plan(span, t, n_heads, n_kv, hd)
             if s2 > 1:
-                assert gi_attn.workspace_bytes(ctx, n_tok, n_heads, n_kv) >= t * n_heads * s2 * 132 * 4
+                assert gi_attn.workspace_bytes(ctx, n_tok, n_heads, n_kv, hd) >= t * n_heads * s2 * part
 
 
 def test_python_mirror_raises_without_gpu_tensors():
