@@ -78,6 +78,9 @@ struct GiDecodeArgs {
 #define DEC_MINWG 1 // workgroups per CU the register budget is sized for
 #endif
 #define DEC_TILE 32
+// An empty volatile asm: a block holding it cannot be executed speculatively, so the compiler keeps the
+// (wave-uniform) branch around it instead of turning the block into selects that run every time.
+#define GI_KEEP_BRANCH() asm volatile("")
 #ifndef DEC_CPOL // cache policy of the K/V loads of decode variants whose waves stream tiles of their own (2: nt)
 #define DEC_CPOL 2
 #endif
@@ -507,10 +510,18 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
                 float v = sacc[cb][m >> 2][m & 3];
                 if constexpr (!PM) v = v + lane_xor1(v); // hi + lo columns of the pair
                 v *= ksb[m];                             // the key's scale
-                if (masked) v = t + 16 * grp + m < span[cb] ? v : GI_NEG_INF;
                 sc[m] = v;
-                mx = fmaxf(mx, v);
             }
+            // the mask as a real branch, which only a slice's last tiles take (int8 decode measured 2% faster
+            // than with the selects on every tile; the f16 kernels gain nothing)
+            if (masked) {
+                GI_KEEP_BRANCH();
+#pragma unroll
+                for (int m = 0; m < 16; m++)
+                    if (t + 16 * grp + m >= span[cb]) sc[m] = GI_NEG_INF;
+            }
+#pragma unroll
+            for (int m = 0; m < 16; m++) mx = fmaxf(mx, sc[m]);
             mx = rows_max(mx);
             const bool up = mx > m_run[cb] + DEC_RESCALE_LOG2;
             if (__builtin_amdgcn_ballot_w64(up)) {
