@@ -2,8 +2,9 @@
 
     python ghost-infer_amd/gi_build.py
 
-Outputs (beside this file): gi_attn_gfx950.hsaco (hipcc --genco, loaded at run time with hipModuleLoad)
-and libgi_attn.so (the C ABI of include/gi_attn.h). hipcc cross-compiles for gfx950, so this runs on a
+Outputs (beside this file): gi_attn_gfx950.hsaco (hipcc --genco, loaded at run time with hipModuleLoad),
+libgi_attn.so (the C ABI of include/gi_attn.h) and gi_layer_harness (a C++ caller of that ABI playing one
+layer's attention, harness/gi_layer_harness.cpp). hipcc cross-compiles for gfx950, so this runs on a
 machine without a GPU.
 """
 import os
@@ -15,6 +16,7 @@ ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 HSACO = os.path.join(HERE, "gi_attn_gfx950.hsaco")
 LIB = os.path.join(HERE, "libgi_attn.so")
+HARNESS = os.path.join(HERE, "gi_layer_harness")
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 # packed f32 VALU ops are disabled for all device code (see the project's design notes on gfx950 boxes)
@@ -35,9 +37,16 @@ def build_host():
          os.path.join(CSRC, "gi_attn_host.cpp"), "-o", LIB, "-ldl"])
 
 
+def build_harness():
+    run([HIPCC, "-O2", "-std=c++17", "-Wall", "-I", os.path.join(ROOT, "include"),
+         os.path.join(HERE, "harness", "gi_layer_harness.cpp"), "-o", HARNESS, "-L", HERE, "-lgi_attn",
+         "-Wl,-rpath,$ORIGIN"])
+
+
 def build():
     build_kernels()
     build_host()
+    build_harness()
 
 
 if __name__ == "__main__":

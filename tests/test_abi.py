@@ -3,6 +3,7 @@ arguments with a message before touching the GPU (no compute calls here)."""
 import ctypes
 import os
 import re
+import subprocess
 
 import pytest
 
@@ -115,3 +116,12 @@ def test_kernel_timing_reads_and_rejects_unknown_kinds():
         assert lib.gi_kernel_timing_read(kind, ctypes.byref(ms), ctypes.byref(n)) == 0
         assert (ms.value, n.value) == (0.0, 0)
     assert lib.gi_kernel_timing(0) == 0
+
+
+def test_layer_harness_built_and_prints_usage():
+    # the C++ caller of the ABI; --help exits before touching a GPU
+    harness = os.path.join(os.path.dirname(os.path.abspath(__file__)), "..", "ghost-infer_amd", "gi_layer_harness")
+    assert os.path.exists(harness), "gi_layer_harness is not built (run __graft_entry__.build())"
+    r = subprocess.run([harness, "--help"], capture_output=True, text=True, timeout=60)
+    assert r.returncode == 0 and "usage: gi_layer_harness" in r.stdout
+
