@@ -254,6 +254,77 @@ def hbm_copy_gbs(torch, dev):
     return 2 * a.numel() * 4 / t / 1e9
 
 
+def peak_probes(torch, dev, reps=5):
+    """The box's own peaks, from the probe kernels of ghost-infer_amd/gi_probes_gfx950.hsaco (built beside
+    the library): the dense f16 MFMA rate (v_mfma_f32_32x32x16_f16 alone, two waves per SIMD) and an HBM
+    read stream (contiguous chunks per workgroup, 16 16-byte streaming loads in flight per lane) over 1 GiB
+    and over config 2's 134 MB (three buffers in turn, past the 256 MB Infinity Cache). Medians over `reps`
+    timings with events on torch's current stream."""
+    import ctypes
+    path = os.path.join(ROOT, "ghost-infer_amd", "gi_probes_gfx950.hsaco")
+    if not os.path.exists(path):
+        raise RuntimeError(f"{path} is not built (run __graft_entry__.build())")
+    hip = ctypes.CDLL("libamdhip64.so")
+    mod = ctypes.c_void_p()
+    if hip.hipModuleLoad(ctypes.byref(mod), path.encode()):
+        raise RuntimeError("hipModuleLoad of the probe code object failed")
+    fns = {}
+    for name in ("gi_probe_mfma", "gi_probe_read"):
+        f = ctypes.c_void_p()
+        if hip.hipModuleGetFunction(ctypes.byref(f), mod, name.encode()):
+            raise RuntimeError(f"probe kernel {name} not found")
+        fns[name] = f
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+    def launch(f, grid, args):
+        buf = ctypes.create_string_buffer(bytes(args), len(bytes(args)))
+        sz = ctypes.c_size_t(len(bytes(args)))
+        cfg = (ctypes.c_void_p * 5)(ctypes.c_void_p(1), ctypes.cast(buf, ctypes.c_void_p), ctypes.c_void_p(2),
+                                    ctypes.cast(ctypes.pointer(sz), ctypes.c_void_p), ctypes.c_void_p(3))
+        if hip.hipModuleLaunchKernel(f, grid, 1, 1, 256, 1, 1, 0, stream, None, cfg):
+            raise RuntimeError("probe launch failed")
+
+    def timed(fn, inner=1):
+        # seconds per launch: `inner` launches back to back between two events, so that the host's launch
+        # latency stays off short kernels
+        ts = []
+        for _ in range(reps + 1):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(inner):
+                fn()
+            e1.record()
+            torch.cuda.synchronize()
+            ts.append(e0.elapsed_time(e1) / 1e3 / inner)
+        ts = sorted(ts[1:])
+        return ts[len(ts) // 2]
+
+    class MfmaArgs(ctypes.Structure):
+        _fields_ = [("iters", ctypes.c_int), ("pad", ctypes.c_int), ("out", ctypes.c_void_p)]
+
+    class ReadArgs(ctypes.Structure):
+        _fields_ = [("p", ctypes.c_void_p), ("n16", ctypes.c_longlong), ("out", ctypes.c_void_p)]
+
+    wgs, iters = 512, 4000  # 2048 waves: two per SIMD
+    sink = torch.zeros(wgs * 256, dtype=torch.float32, device=dev)
+    t = timed(lambda: launch(fns["gi_probe_mfma"], wgs, MfmaArgs(iters, 0, sink.data_ptr())))
+    mfma_tflops = wgs * 4 * iters * 32 * 32768 / t / 1e12
+    res = {"mfma_f16_dense_TFLOPs": round(mfma_tflops, 1)}
+    flag = torch.zeros(1, dtype=torch.int32, device=dev)
+    for label, nbytes, rd_wgs in (("hbm_read_GBs_1GiB", 1 << 30, 1024), ("hbm_read_GBs_134MB", 134217728, 256)):
+        bufs = [torch.empty(nbytes, dtype=torch.uint8, device=dev) for _ in range(3)]  # rotate past the 256 MB cache
+        k = [0]
+
+        def one():
+            b = bufs[k[0] % len(bufs)]
+            k[0] += 1
+            launch(fns["gi_probe_read"], rd_wgs, ReadArgs(b.data_ptr(), nbytes // 16 // rd_wgs, flag.data_ptr()))
+        res[label] = round(nbytes / timed(one, inner=24) / 1e9, 1)
+        del bufs
+    res["hbm_copy_GBs_1GiB"] = round(hbm_copy_gbs(torch, dev), 1)
+    return res
+
+
 # ---------------------------------------------------------------- CPU baseline (the oracle)
 
 def cpu_baseline_decode(q, cache, pos0, n_heads, n_kv, budget_s=12.0):
@@ -301,7 +372,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="decode64k",
                     choices=["decode64k", "decode4k", "verify", "prefill8k", "chunked", "qkrope", "decode64k_i8",
-                             "verify_i8", "prefill8k_i8", "decode64k_h256", "verify_h256", "prefill8k_h256"])
+                             "verify_i8", "prefill8k_i8", "decode64k_h256", "verify_h256", "prefill8k_h256",
+                             "peaks"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--n-tok", type=int, default=None,
@@ -323,7 +395,16 @@ def main():
     result = {"metric": METRIC, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
               "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "data": "synthetic"}
     w = args.workload
-    if w in ("decode64k", "decode4k", "verify", "decode64k_i8", "verify_i8", "decode64k_h256", "verify_h256"):
+    if w == "peaks":
+        log("[bench] peak probes: dense f16 MFMA rate, HBM read stream, device copy")
+        pk = peak_probes(torch, dev)
+        result.update({"value": pk["mfma_f16_dense_TFLOPs"], "unit": "TFLOP/s", "ms_per_step": None,
+                       "dtype": "f16 MFMA, f32 acc", "config": {"workload": "peak probes of this box", **pk},
+                       "roofline": {"bound": "mfma", "achieved": pk["mfma_f16_dense_TFLOPs"],
+                                    "peak": F16_DENSE_PEAK_TFLOPS, "unit": "TFLOP/s",
+                                    "frac": round(pk["mfma_f16_dense_TFLOPs"] / F16_DENSE_PEAK_TFLOPS, 4),
+                                    "traffic": None, "kernel": "gi_probe_mfma"}})
+    elif w in ("decode64k", "decode4k", "verify", "decode64k_i8", "verify_i8", "decode64k_h256", "verify_h256"):
         hd = 256 if w.endswith("_h256") else HD
         ctx, n_heads, n_kv, n_tok, cfg = {
             "decode64k": (65536, 32, 4, 1, "config 2: decode, 1 token, ctx 65536, 32q/4kv, hd 128"),
@@ -437,7 +518,8 @@ def main():
                                              "ms_per_step": r["seconds"] * 1e3,
                                              "frac_of_f16_dense_peak": round(tf / F16_DENSE_PEAK_TFLOPS, 4),
                                              "roofline": prefill_roofline(gi_attn, r, 30, torch)},
-                               "hbm_copy_measured_GBs": round(hbm_copy_gbs(torch, dev), 1)}
+                               "hbm_copy_measured_GBs": round(hbm_copy_gbs(torch, dev), 1),
+                               "peaks_measured": peak_probes(torch, dev)}
     print(json.dumps(result), flush=True)
 
 

@@ -30,6 +30,8 @@ def test_library_exports_every_declared_symbol():
 
 def test_code_object_built():
     assert os.path.getsize(gi_attn.HSACO_PATH) > 0
+    # the bench's peak probes: their own code object beside it
+    assert os.path.getsize(os.path.join(os.path.dirname(gi_attn.HSACO_PATH), "gi_probes_gfx950.hsaco")) > 0
 
 
 def test_unsupported_head_size_is_rejected_with_message():
