@@ -197,7 +197,7 @@ def prefill_workload(torch, gi_attn, dev, n, n_heads, n_kv, steps, warmup, seed,
         gi_attn.prefill(q, k, v, 0, n_heads, n_kv, hd=hd, out=out, k_scale=ks, v_scale=vs)
 
     t = time_steps(step, steps, warmup, torch)
-    return {"seconds": t, "flops": prefill_flops(n, 0, n_heads, hd), "step": step}
+    return {"seconds": t, "flops": prefill_flops(n, 0, n_heads, hd), "step": step, "q": q, "k": k, "v": v}
 
 
 def qkrope_workload(torch, gi_attn, dev, n, n_heads, n_kv, steps, warmup, seed):
@@ -355,6 +355,36 @@ def cpu_baseline_decode(q, cache, pos0, n_heads, n_kv, budget_s=12.0):
     return times[len(times) // 2], threads, len(times)
 
 
+def cpu_baseline_prefill(q, k, v, n_heads, n_kv, rows=64, budget_s=12.0):
+    """Times the oracle's restatement of Model::attention on this host for a bounded sample of a causal
+    prefill: the last `rows` query rows of the prompt (each sees nearly the whole prompt), all heads, over
+    the same cache. Returns (TFLOP/s, threads, repetitions, sample flops, median seconds)."""
+    import numpy as np
+
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import gi_oracle
+
+    threads = min(16, os.cpu_count() or 1)
+    n = q.shape[0]
+    pos0 = n - rows
+    qn = q[pos0:].float().cpu().numpy()
+    kn = k.cpu().numpy().view(np.uint16).reshape(k.shape[0], -1)
+    vn = v.cpu().numpy().view(np.uint16).reshape(v.shape[0], -1)
+    gi_oracle.attention(qn, kn, vn, pos0, n_heads, n_kv, threads=threads)  # warm-up
+    times = []
+    t_end = time.time() + budget_s
+    while time.time() < t_end or len(times) < 3:
+        t0 = time.perf_counter()
+        gi_oracle.attention(qn, kn, vn, pos0, n_heads, n_kv, threads=threads)
+        times.append(time.perf_counter() - t0)
+        if len(times) >= 50:
+            break
+    times.sort()
+    t = times[len(times) // 2]
+    flops = prefill_flops(rows, pos0, n_heads)
+    return flops / t / 1e12, threads, len(times), flops, t
+
+
 def prefill_roofline(gi_attn, r, steps, torch, profile="pmc_prefill_prefill8k", kernel="gi_prefill_fwd"):
     """Roofline object of the prefill kernel: algorithmic flops of one launch / its mean duration."""
     ms, n = kernel_times(gi_attn, r["step"], steps, torch, ("prefill",))["prefill"]
@@ -496,6 +526,12 @@ def main():
                                          "gi_prefill_fwd_i8" if i8 else "gi_prefill_fwd_h256" if hd == 256
                                          else "gi_prefill_fwd"),
         })
+        if not args.no_cpu_baseline and not i8 and hd == HD:
+            log("[bench] cpu baseline (oracle, Model::attention restatement) on the last 64 query rows")
+            tf_cpu, threads, reps, fl, t_cpu = cpu_baseline_prefill(r["q"], r["k"], r["v"], nh, nkv)
+            result["cpu_baseline"] = {"value": round(tf_cpu, 4), "unit": "TFLOP/s", "cores": threads, "kind": "port",
+                                      "sample": f"the last 64 of the 8192 query rows, all heads ({fl / 1e9:.1f} "
+                                                f"GFLOP), {reps} runs (median {t_cpu * 1e3:.1f} ms/run)"}
     else:
         log("[bench] config 5: chunked prefill 131072 in 2048 chunks, 32q/4kv")
         per = chunked_workload(torch, gi_attn, dev, 131072, 2048, 32, 4, 5)
