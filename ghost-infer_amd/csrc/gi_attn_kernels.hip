@@ -84,9 +84,6 @@ struct GiDecodeArgs {
 #ifndef DEC_CPOL // cache policy of the K/V loads of decode variants whose waves stream tiles of their own (2: nt)
 #define DEC_CPOL 2
 #endif
-#ifndef DEC_QFIRST
-#define DEC_QFIRST 0
-#endif
 #define DEC_PAIRS 8 // (token, head) pairs per column block of 16 columns
 #define DEC_RESCALE_LOG2 8.0f
 // int8 cache: the probability's f16 remainder column is scaled by 2^12 (undone when the columns merge).
@@ -667,9 +664,6 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
     if (!SHARE || pair0 < npairs) {
     Buf B[DEC_NB];
     const int t_first = SHARE ? 0 : wave * TILE;
-#if DEC_QFIRST
-    __builtin_amdgcn_s_waitcnt(0x0F70); // vmcnt(0): the queries are in before any K/V load goes out
-#endif
 #pragma unroll
     for (int i = 0; i < DEC_NB; i++) {
         load_k(B[i], t_first + i * STRIDE);
@@ -907,15 +901,6 @@ struct GiPrefillArgs {
 #define PF_BK 64           // keys per tile
 #define PF_TILE 16384      // bytes of one K or V tile: 64 rows of 256 bytes
 #define PF_RESCALE_LOG2 8.0f
-#ifndef PF_SGB
-#define PF_SGB 1           // instruction-order hints for the step block (see the step)
-#endif
-#ifndef PF_V1
-#define PF_V1 2            // VALU instructions scheduled after each QK MFMA
-#endif
-#ifndef PF_V2
-#define PF_V2 3            // after each PV MFMA
-#endif
 #ifndef PF_KPF
 #define PF_KPF 8           // K fragments in flight in the QK loop
 #endif
@@ -1248,43 +1233,14 @@ __device__ __forceinline__ void gi_prefill_t(const GiPrefillArgs& a) {
         }
         kscale(it + 1, sn);
         mx = rowmax(sn); // unmasked: a diagonal tile recomputes it after masking
-        // Instruction order of the block (the compiler's scheduler follows these groups in sequence):
-        // QK phase, per QK MFMA: one LDS read (the K fragment PF_KPF steps on, then V fragments of the first
-        // k-step) and PF_V1 VALU (tile it's exp2 / pack / row sum of k-steps 0-1); PV phase, per PV MFMA: up
-        // to two V reads and PF_V2 VALU (k-steps 2-3, then tile it+1's row max).
-#if PF_SGB == 1
+        // Instruction order of the QK phase: every QK MFMA is followed by the read of the K fragment PF_KPF
+        // MFMAs on (the compiler otherwise reads each fragment just before its MFMA). Interleaving the
+        // softmax VALU or the V reads by further groups measured no better.
 #pragma unroll
         for (int i = 0; i < 16; i++) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                // MFMA
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                      // MFMA
             if (i + PF_KPF < 16) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0); // its K refill
         }
-#elif PF_SGB == 2
-#pragma unroll
-        for (int i = 0; i < 16; i++) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-            if (i + PF_KPF < 16) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-            __builtin_amdgcn_sched_group_barrier(0x002, PF_V1, 0);
-        }
-#elif PF_SGB == 3
-#pragma unroll
-        for (int i = 0; i < 16; i++) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-        }
-#elif PF_SGB == 4
-#pragma unroll
-        for (int i = 0; i < 16; i++) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);     // MFMA
-            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);     // LDS read
-            __builtin_amdgcn_sched_group_barrier(0x002, PF_V1, 0); // VALU
-        }
-#pragma unroll
-        for (int i = 0; i < 16; i++) {
-            __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-            __builtin_amdgcn_sched_group_barrier(0x002, PF_V2, 0);
-        }
-#endif
     };
     // Iteration it: before the barrier each wave waits for its own loads of tile it+1 (tile it+2's may
     // stay in flight); the barrier publishes the tile and tells that every wave is done with tile it-1,
