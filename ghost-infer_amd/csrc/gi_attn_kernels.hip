@@ -1320,9 +1320,252 @@ __device__ __forceinline__ void gi_prefill_t(const GiPrefillArgs& a) {
     }
 }
 
+// ---------------------------------------------------------------- prefill, head size 256, 16 rows per wave
+// One workgroup per (head, 128 query rows): 8 waves of 16 rows, each with all 256 output dims, so QK and the
+// softmax are computed once (the two-workgroup split above computes both twice). On v_mfma_f32_16x16x32_f16:
+//  - S^T (16 keys x 16 queries per block) = K Q^T over 8 k-steps of 32 dims, from C = -max as above. Lane l
+//    holds query column c = l%16 and rows 4g + r (g = l/16) of each block. A-row rho of key block kb reads
+//    tile key 8(rho/4) + 4kb + rho%4, so those rows are keys 8g + 4kb + r: exactly the keys 8g + e
+//    (e = 4kb + r) the lane holds in the P^T operand of P V, with no data movement.
+//  - O^T (16 dims x 16 queries per block) += V^T P^T over the tile's 32 keys: one MFMA per 16-dim block,
+//    V^T from two transposing reads (keys 8g..8g+3 and 8g+4..8g+7, 16 dims) per block.
+// K and V tiles are the 32-key, two-half-row LDS image of the head-size-256 kernel above (same staging,
+// swizzles and buffers). Per tile a wave issues 32 MFMAs against 32 KB of LDS operand reads, twice the
+// bytes per flop of the 32-row waves: the kernel is bound by LDS operand bandwidth, not MFMA.
+__device__ __forceinline__ int pf256r_swz_k(int r) { return (r & 15) ^ (((r >> 4) & 1) << 2); }
+__device__ __forceinline__ int pf256r_swz_v(int r) { return ((r & 3) << 2) | (((r >> 3) & 1) << 1); }
+#define PF256R_WAVES 8
+#define PF256R_ROWS 16
+#define PF256R_BQ (PF256R_ROWS * PF256R_WAVES) // query rows per workgroup
+__device__ __forceinline__ void gi_prefill256r(const GiPrefillArgs& a) {
+    constexpr int HD = 256, WAVES = PF256R_WAVES, BQ = PF256R_BQ;
+    constexpr int SW = WAVES / 2;    // waves staging each of K and V
+    constexpr int LPW = 16 / SW;     // 1 KB loads per staging wave and tile
+    constexpr int BK = 32;           // keys per tile
+    constexpr int KS = HD / 32;      // QK k-steps
+    constexpr int NDB = HD / 16;     // O^T blocks of 16 dims
+    __shared__ __attribute__((aligned(1024))) unsigned char smem[PF_NBUF][2][PF_TILE]; // [buffer][K, V]
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int G = a.n_heads / a.n_kv;
+    const int qtiles = (a.n + BQ - 1) / BQ;
+    const int nwg = gridDim.x;
+    int j = blockIdx.x;
+    if ((nwg & 7) == 0) j = (j & 7) * (nwg >> 3) + (j >> 3); // each XCD a contiguous run of items
+    const int kvh = j / (qtiles * G);
+    const int rest = j % (qtiles * G);
+    const int qt = qtiles - 1 - rest / G; // longest query tiles first
+    const int h = kvh * G + rest % G;
+    const int q0 = qt * BQ;
+    const int kv_len = a.pos0 + a.n;
+    const int k_lim = min(kv_len, a.pos0 + q0 + BQ);
+    const int ntiles = (k_lim + BK - 1) / BK;
+    const long long kvs = a.kv_stride;
+
+    // ---- staging, as the head-size-256 path of gi_prefill_t (image row r = key r%32, dims 128*(r/32)..), with
+    // this kernel's swizzles of the 16-byte units. K: the key's low 4 bits with bit 4 folded into bit 2, so
+    // that the 16 rows one K fragment read touches (keys 8(c/4) + c%4 (+4), c = 0..15: low 4 bits repeat at
+    // c and c + 8) fall on 16 different unit positions. V: (key % 4) << 2 with bit 3 into bit 1, so that lane
+    // groups g and g + 1 of a transposing read (keys 8g + te and 8g + 8 + te) use disjoint banks.
+    const bool stage_v = wave >= SW;
+    const uint16_t* sbase = (stage_v ? a.vc : a.kc) + kvh * a.kv_head_stride;
+    int soff[LPW];
+#pragma unroll
+    for (int i = 0; i < LPW; i++) {
+        const int r = 4 * (LPW * (wave % SW) + i) + (lane >> 4);
+        const int u = (lane & 15) ^ (stage_v ? pf256r_swz_v(r) : pf256r_swz_k(r));
+        soff[i] = ((r & 31) * (int)kvs + 128 * (r >> 5) + 8 * u) * 2;
+    }
+    auto stage = [&](int t) {
+        const int t0 = t * BK;
+        __amdgpu_buffer_rsrc_t rs = gi_rsrc(sbase + (long long)t0 * kvs, (long long)(kv_len - t0) * kvs * 2);
+        unsigned char* dst = &smem[t & (PF_NBUF - 1)][stage_v ? 1 : 0][1024 * LPW * (wave % SW)];
+#pragma unroll
+        for (int i = 0; i < LPW; i++)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (GI_LDS void*)(dst + 1024 * i), 16, soff[i], 0, 0, 0);
+    };
+
+    // ---- Q as B operands: lane (column c, k-group g), k-step ks: dims 32ks + 8g .. +7, times scale*log2(e)
+    const int c = lane & 15, g = lane >> 4;
+    const int qrow = q0 + PF256R_ROWS * wave + c;
+    const int qpos = a.pos0 + qrow;
+    const float qs = a.qscale;
+    h8 qf[KS];
+    {
+        const int qr = qrow < a.n ? qrow : a.n - 1; // rows past n compute garbage that is never written
+        if (a.q_f16) {
+            const _Float16* qp = (const _Float16*)a.q + (long long)qr * a.q_stride + h * HD + 8 * g;
+#pragma unroll
+            for (int ks = 0; ks < KS; ks++) {
+                const h8 x = __builtin_bit_cast(h8, *reinterpret_cast<const u4*>(qp + 32 * ks));
+#pragma unroll
+                for (int e = 0; e < 8; e++) qf[ks][e] = (_Float16)((float)x[e] * qs);
+            }
+        } else {
+            const float* qp = (const float*)a.q + (long long)qr * a.q_stride + h * HD + 8 * g;
+#pragma unroll
+            for (int ks = 0; ks < KS; ks++) {
+                const float4 x0 = *reinterpret_cast<const float4*>(qp + 32 * ks);
+                const float4 x1 = *reinterpret_cast<const float4*>(qp + 32 * ks + 4);
+                qf[ks] = h8{(_Float16)(x0.x * qs), (_Float16)(x0.y * qs), (_Float16)(x0.z * qs), (_Float16)(x0.w * qs),
+                            (_Float16)(x1.x * qs), (_Float16)(x1.y * qs), (_Float16)(x1.z * qs), (_Float16)(x1.w * qs)};
+            }
+        }
+    }
+
+    // ---- operand read offsets (bytes within a buffer's K or V image)
+    // K: block kb, k-step ks: key krow + 4kb (krow = 8(c/4) + c%4), image half ks/4, unit 4(ks%4) + g swizzled
+    const int krow = 8 * (c >> 2) + (c & 3);
+    auto kfrag = [&](const unsigned char* K, int st) { // MFMA st of a tile's 16: block st%2, k-step st/2
+        const int kb = st & 1, ks = st >> 1;
+        const int row = krow + 4 * kb + 32 * (ks >> 2);
+        const int unit = (4 * (ks & 3) + g) ^ pf256r_swz_k(krow + 4 * kb);
+        return *reinterpret_cast<const h8*>(K + row * 256 + (unit << 4));
+    };
+    // V: block db (dims 16db..), keys 8g + te (+4): image row 32*(db/8) + 8g + te, unit 2*(db%8) + tc/2 swizzled,
+    // plus 8 bytes for odd tc (te = (lane%16)/4, tc = lane%4); the +4 rows of the second read keep the swizzle
+    const int te = c >> 2, tc = c & 3;
+    const int vbase = (8 * g + te) * 256 + 8 * (tc & 1);
+    auto vfrag = [&](const unsigned char* V, int db) {
+        const int off = vbase + 8192 * (db >> 3) + (((2 * (db & 7) + (tc >> 1)) ^ pf256r_swz_v(8 * g + te)) << 4);
+        gi_s4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((GI_LDS gi_s4*)(V + off));
+        gi_s4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((GI_LDS gi_s4*)(V + off + 1024));
+        return __builtin_shufflevector(__builtin_bit_cast(h4x, lo), __builtin_bit_cast(h4x, hi), 0, 1, 2, 3, 4, 5,
+                                       6, 7);
+    };
+
+    // ---- per-lane state: O^T (16 blocks of 16 dims; this lane dims 16db + 4g + r), reference max, row sum
+    f4 o[NDB];
+#pragma unroll
+    for (int db = 0; db < NDB; db++) o[db] = f4{0.f, 0.f, 0.f, 0.f};
+    float m_run = 0.f, l_run = 0.f;
+    f4 negm = f4{0.f, 0.f, 0.f, 0.f}; // -m_run: the C operand that starts each QK chain
+
+    auto qk = [&](int t, f4* s) {
+        const unsigned char* K = &smem[t & (PF_NBUF - 1)][0][0];
+        h8 kf[PF_KPF];
+#pragma unroll
+        for (int st = 0; st < PF_KPF; st++) kf[st] = kfrag(K, st);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int st = 0; st < 2 * KS; st++) {
+            const int kb = st & 1, ks = st >> 1;
+            const h8 cur = kf[st % PF_KPF];
+            if (st + PF_KPF < 2 * KS) kf[st % PF_KPF] = kfrag(K, st + PF_KPF);
+            s[kb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(cur, qf[ks], ks == 0 ? negm : s[kb], 0, 0, 0);
+        }
+    };
+    auto rowmax = [&](const f4* sc) {
+        float mx = fmaxf(fmaxf(fmaxf(sc[0][0], sc[0][1]), fmaxf(sc[0][2], sc[0][3])),
+                         fmaxf(fmaxf(sc[1][0], sc[1][1]), fmaxf(sc[1][2], sc[1][3])));
+        return rows_max(mx);
+    };
+    const int wave_first = a.pos0 + q0 + PF256R_ROWS * wave; // position of the wave's first row
+    const int wave_last = wave_first + PF256R_ROWS - 1;
+    const int my_tiles = min(ntiles, wave_last / BK + 1);
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+
+    // one step: the rare rescale, then QK of tile it+1 into sn under tile it's probabilities and P V, and tile
+    // it+1's row max (mx on exit)
+    auto step = [&](int it, f4* s, f4* sn, float& mx) {
+        const bool up = mx > PF_RESCALE_LOG2 || it == 0;
+        if (__builtin_amdgcn_ballot_w64(up)) {
+            const float delta = up ? mx : 0.f;
+            const float alpha = __builtin_amdgcn_exp2f(-fmaxf(delta, 0.f));
+            m_run += delta;
+            negm = f4{-m_run, -m_run, -m_run, -m_run};
+            l_run *= alpha;
+#pragma unroll
+            for (int db = 0; db < NDB; db++) o[db] *= alpha;
+            s[0] -= delta;
+            s[1] -= delta;
+        }
+        qk(it + 1, sn);
+        h8 pf; // keys 8g + e, e = 4kb + r
+#pragma unroll
+        for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+            for (int r = 0; r < 4; r += 2) {
+                const _Float16 h0 = (_Float16)__builtin_amdgcn_exp2f(s[kb][r]);
+                const _Float16 h1 = (_Float16)__builtin_amdgcn_exp2f(s[kb][r + 1]);
+                pf[4 * kb + r] = h0;
+                pf[4 * kb + r + 1] = h1;
+                l_run = __builtin_amdgcn_fdot2(h2{h0, h1}, h2{(_Float16)1.f, (_Float16)1.f}, l_run, false);
+            }
+        const unsigned char* V = &smem[it & (PF_NBUF - 1)][1][0];
+#pragma unroll
+        for (int db = 0; db < NDB; db++) o[db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vfrag(V, db), pf, o[db], 0, 0, 0);
+        mx = rowmax(sn);
+#pragma unroll
+        for (int i = 0; i < 2 * KS; i++) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            if (i + PF_KPF < 2 * KS) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
+    };
+
+    // prologue: tiles 0-2 start loading; tile 0 is waited for and published
+    stage(0);
+    if (ntiles > 1) stage(1);
+    if (ntiles > 2) stage(2);
+    if (ntiles > 2) __builtin_amdgcn_s_waitcnt(GI_VMCNT(2 * LPW));
+    else if (ntiles > 1) __builtin_amdgcn_s_waitcnt(GI_VMCNT(LPW));
+    else __builtin_amdgcn_s_waitcnt(GI_VMCNT(0));
+    asm volatile("s_barrier" ::: "memory");
+    float mx = GI_NEG_INF;
+    auto iteration = [&](int it, f4* s, f4* sn) {
+        if (it + 2 < ntiles) __builtin_amdgcn_s_waitcnt(GI_VMCNT(LPW));
+        else __builtin_amdgcn_s_waitcnt(GI_VMCNT(0));
+        asm volatile("s_barrier" ::: "memory");
+        if (it + 3 < ntiles) stage(it + 3);
+        if (it < my_tiles) {
+            const int t0 = it * BK;
+            if (t0 + BK - 1 > wave_first) { // the tile crosses the diagonal somewhere in the wave
+                const int lim = qpos - t0;
+#pragma unroll
+                for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+                    for (int r = 0; r < 4; r++)
+                        if (8 * g + 4 * kb + r > lim) s[kb][r] = GI_NEG_INF;
+                mx = rowmax(s);
+            }
+            step(it, s, sn, mx);
+        }
+    };
+    f4 sa[2], sb[2];
+    if (my_tiles > 0) {
+        qk(0, sa);
+        mx = rowmax(sa);
+    }
+    for (int it = 0; it < ntiles; it += 2) {
+        iteration(it, sa, sb);
+        if (it + 1 < ntiles) iteration(it + 1, sb, sa);
+    }
+
+    // ---- normalise and write: lane holds query c, dims 16db + 4g + r
+    const float l = rows_sum(l_run);
+    if (qrow < a.n) {
+        const float inv = 1.f / l;
+        if (a.out_f16) {
+            _Float16* op = (_Float16*)a.out + (long long)qrow * a.out_stride + h * HD + 4 * g;
+#pragma unroll
+            for (int db = 0; db < NDB; db++)
+                *reinterpret_cast<h4x*>(op + 16 * db) = h4x{(_Float16)(o[db][0] * inv), (_Float16)(o[db][1] * inv),
+                                                            (_Float16)(o[db][2] * inv), (_Float16)(o[db][3] * inv)};
+        } else {
+            float* op = (float*)a.out + (long long)qrow * a.out_stride + h * HD + 4 * g;
+#pragma unroll
+            for (int db = 0; db < NDB; db++)
+                *reinterpret_cast<float4*>(op + 16 * db) =
+                    make_float4(o[db][0] * inv, o[db][1] * inv, o[db][2] * inv, o[db][3] * inv);
+        }
+    }
+}
+
 extern "C" __global__ void __launch_bounds__(64 * PF_WAVES, 1) gi_prefill_fwd(GiPrefillArgs a) { gi_prefill_t<false, 128>(a); }
 extern "C" __global__ void __launch_bounds__(64 * PF_WAVES, 1) gi_prefill_fwd_i8(GiPrefillArgs a) { gi_prefill_t<true, 128>(a); }
 extern "C" __global__ void __launch_bounds__(64 * PF_WAVES, 1) gi_prefill_fwd_h256(GiPrefillArgs a) { gi_prefill_t<false, 256>(a); }
+extern "C" __global__ void __launch_bounds__(64 * PF256R_WAVES, 1) gi_prefill_fwd_h256r(GiPrefillArgs a) { gi_prefill256r(a); }
 
 // ------------------------------------------------------------------------------------------------ KV store
 
