@@ -905,6 +905,30 @@ struct GiPrefillArgs {
 #define PF_KPF 8           // K fragments in flight in the QK loop
 #endif
 #define GI_LDS __attribute__((address_space(3)))
+// Tile staging from HBM straight into LDS (buffer_load_dwordx4 ... lds: lane i's 16 bytes land at
+// M0 + 16i). Issued from inline asm, so the compiler does not track these loads: were it to see them, it
+// places s_waitcnt vmcnt(0) before every transposing LDS read (ds_read_b64_tr_b16) that it cannot prove
+// disjoint from them, which makes each wave wait for the tile it has just requested. The kernels order the
+// loads themselves (s_waitcnt vmcnt on the issuing wave, then s_barrier). Vector memory loads retire in
+// order, so the compiler's own vmcnt(N) waits for the loads it knows stay correct with these in flight
+// (more younger loads only make such a wait stricter).
+#ifndef GI_DMA_ASM
+#define GI_DMA_ASM 1
+#endif
+__device__ __forceinline__ u4 gi_rsrc_words(const void* p, long long bytes) {
+    const uint32_t n = (uint32_t)(bytes < 0 ? 0 : (bytes > 0x7ffffff0ll ? 0x7ffffff0ll : bytes));
+    const unsigned long long b = (unsigned long long)p;
+    return u4{(uint32_t)b, (uint32_t)(b >> 32) & 0xffffu, n, (uint32_t)GI_RSRC_FLAGS};
+}
+__device__ __forceinline__ void gi_stage16(const void* base, long long bytes, GI_LDS void* dst, int voff) {
+#if GI_DMA_ASM
+    const u4 rs = gi_rsrc_words(base, bytes);
+    const uint32_t m0 = (uint32_t)(uintptr_t)dst;
+    asm volatile("buffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voff), "s"(rs), "{m0}"(m0) : "memory");
+#else
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(gi_rsrc(base, bytes), dst, 16, voff, 0, 0, 0);
+#endif
+}
 // int8 cache: the value scale goes into the f16 probabilities times this power of two (undone at the
 // end) so that small products stay normal f16; with P <= 2^8 a dequantised |V| up to 127 * 65504 / (2^8 *
 // PF_I8_VBIAS) ~ 4000 fits (the reference biases by 2^10 with P <= 1, src/cuda.rs:2416-2420)
@@ -1000,11 +1024,11 @@ __device__ __forceinline__ void gi_prefill_t(const GiPrefillArgs& a) {
     auto stage = [&](int t) {
         if (stage_idle) return;
         const int t0 = t * BK;
-        __amdgpu_buffer_rsrc_t rs = gi_rsrc(sbase + (long long)t0 * kvs, (long long)(kv_len - t0) * kvs * 2);
+        const uint16_t* src = sbase + (long long)t0 * kvs;
+        const long long bytes = (long long)(kv_len - t0) * kvs * 2;
         unsigned char* dst = &smem[t & (PF_NBUF - 1)][stage_v ? 1 : 0][1024 * LPW * (wave % SW)];
 #pragma unroll
-        for (int i = 0; i < LPW; i++)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (GI_LDS void*)(dst + 1024 * i), 16, soff[i], 0, 0, 0);
+        for (int i = 0; i < LPW; i++) gi_stage16(src, bytes, (GI_LDS void*)(dst + 1024 * i), soff[i]);
     };
     // int8 staging: thread -> tile row sr, 16-byte chunk sch (dims 16sch..16sch+15) of K and of V; threads
     // 0-63 also take the K scale of key tid, 64-127 the V scale of key tid-64 (times PF_I8_VBIAS)
@@ -1329,22 +1353,39 @@ __device__ __forceinline__ void gi_prefill_t(const GiPrefillArgs& a) {
 //    (e = 4kb + r) the lane holds in the P^T operand of P V, with no data movement.
 //  - O^T (16 dims x 16 queries per block) += V^T P^T over the tile's 32 keys: one MFMA per 16-dim block,
 //    V^T from two transposing reads (keys 8g..8g+3 and 8g+4..8g+7, 16 dims) per block.
-// K and V tiles are the 32-key, two-half-row LDS image of the head-size-256 kernel above (same staging,
-// swizzles and buffers). Per tile a wave issues 32 MFMAs against 32 KB of LDS operand reads, twice the
-// bytes per flop of the 32-row waves: the kernel is bound by LDS operand bandwidth, not MFMA.
+// K and V tiles hold 64 keys in the two-half-row LDS image of the head-size-256 kernel above (dims 0-127 of
+// the 64 keys, then dims 128-255), 32 KB each, with this kernel's swizzles. Per tile a wave issues 64 MFMAs
+// against 64 KB of LDS operand reads, twice the bytes per flop of the 32-row waves.
 __device__ __forceinline__ int pf256r_swz_k(int r) { return (r & 15) ^ (((r >> 4) & 1) << 2); }
 __device__ __forceinline__ int pf256r_swz_v(int r) { return ((r & 3) << 2) | (((r >> 3) & 1) << 1); }
 #define PF256R_WAVES 8
 #define PF256R_ROWS 16
 #define PF256R_BQ (PF256R_ROWS * PF256R_WAVES) // query rows per workgroup
+// K and V rings: NKBUF and NVBUF buffers of one tile each (NKBUF + NVBUF <= 5 in 160 KB of LDS). Iteration
+// it reads K of tile it+1 (its QK) and V of tile it (its P V); after its barrier the buffers of K(it) and
+// V(it-1) have no reader left, so it refills them with K(it + NKBUF) and V(it + NVBUF - 1): each tile is
+// issued NKBUF - 1 (K) or NVBUF - 1 (V) iterations before its use. Half the waves stage K, half V, and
+// each waits for its own loads only, then the barrier publishes them.
+template <int NKBUF, int NVBUF>
 __device__ __forceinline__ void gi_prefill256r(const GiPrefillArgs& a) {
-    constexpr int HD = 256, WAVES = PF256R_WAVES, BQ = PF256R_BQ;
-    constexpr int SW = WAVES / 2;    // waves staging each of K and V
-    constexpr int LPW = 16 / SW;     // 1 KB loads per staging wave and tile
-    constexpr int BK = 32;           // keys per tile
-    constexpr int KS = HD / 32;      // QK k-steps
-    constexpr int NDB = HD / 16;     // O^T blocks of 16 dims
-    __shared__ __attribute__((aligned(1024))) unsigned char smem[PF_NBUF][2][PF_TILE]; // [buffer][K, V]
+    static_assert(NKBUF >= 2 && NVBUF >= 2 && NKBUF + NVBUF <= 5, "K and V rings within 160 KB");
+    constexpr int HD = 256, WAVES = PF256R_WAVES, BQ = PF256R_BQ, BK = 64;
+    constexpr int SW = WAVES / 2;            // waves staging each of K and V
+    constexpr int LPW = (BK / 2) / SW;       // 1 KB loads per staging wave and tile (K or V: BK * 512 bytes)
+    constexpr int KS = HD / 32;              // QK k-steps
+    constexpr int NKB = BK / 16;             // S^T blocks of 16 keys
+    constexpr int NDB = HD / 16;             // O^T blocks of 16 dims
+    constexpr int TILE = BK * 512;           // bytes of one K or V tile image
+    __shared__ __attribute__((aligned(1024))) unsigned char smem[(NKBUF + NVBUF) * TILE];
+    auto kbuf = [&](int t) { return smem + (t % NKBUF) * TILE; };
+    auto vbuf = [&](int t) { return smem + (NKBUF + t % NVBUF) * TILE; };
+    // wait until at most n (0..2) of this wave's tile loads are outstanding
+    auto wait_tiles = [&](int n) {
+        if (n >= 2) __builtin_amdgcn_s_waitcnt(GI_VMCNT(2 * LPW));
+        else if (n == 1) __builtin_amdgcn_s_waitcnt(GI_VMCNT(LPW));
+        else __builtin_amdgcn_s_waitcnt(GI_VMCNT(0));
+    };
+    static_assert(NKBUF <= 4 && NVBUF <= 4, "wait_tiles covers two tiles in flight past the one waited for");
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1363,7 +1404,7 @@ __device__ __forceinline__ void gi_prefill256r(const GiPrefillArgs& a) {
     const int ntiles = (k_lim + BK - 1) / BK;
     const long long kvs = a.kv_stride;
 
-    // ---- staging, as the head-size-256 path of gi_prefill_t (image row r = key r%32, dims 128*(r/32)..), with
+    // ---- staging, as the head-size-256 path of gi_prefill_t (image row r = key r%BK, dims 128*(r/BK)..), with
     // this kernel's swizzles of the 16-byte units. K: the key's low 4 bits with bit 4 folded into bit 2, so
     // that the 16 rows one K fragment read touches (keys 8(c/4) + c%4 (+4), c = 0..15: low 4 bits repeat at
     // c and c + 8) fall on 16 different unit positions. V: (key % 4) << 2 with bit 3 into bit 1, so that lane
@@ -1375,15 +1416,16 @@ __device__ __forceinline__ void gi_prefill256r(const GiPrefillArgs& a) {
     for (int i = 0; i < LPW; i++) {
         const int r = 4 * (LPW * (wave % SW) + i) + (lane >> 4);
         const int u = (lane & 15) ^ (stage_v ? pf256r_swz_v(r) : pf256r_swz_k(r));
-        soff[i] = ((r & 31) * (int)kvs + 128 * (r >> 5) + 8 * u) * 2;
+        soff[i] = ((r & (BK - 1)) * (int)kvs + 128 * (r / BK) + 8 * u) * 2;
     }
+    // this wave's share of tile t (its K if it stages K, else its V)
     auto stage = [&](int t) {
         const int t0 = t * BK;
-        __amdgpu_buffer_rsrc_t rs = gi_rsrc(sbase + (long long)t0 * kvs, (long long)(kv_len - t0) * kvs * 2);
-        unsigned char* dst = &smem[t & (PF_NBUF - 1)][stage_v ? 1 : 0][1024 * LPW * (wave % SW)];
+        const uint16_t* src = sbase + (long long)t0 * kvs;
+        const long long bytes = (long long)(kv_len - t0) * kvs * 2;
+        unsigned char* dst = (stage_v ? vbuf(t) : kbuf(t)) + 1024 * LPW * (wave % SW);
 #pragma unroll
-        for (int i = 0; i < LPW; i++)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (GI_LDS void*)(dst + 1024 * i), 16, soff[i], 0, 0, 0);
+        for (int i = 0; i < LPW; i++) gi_stage16(src, bytes, (GI_LDS void*)(dst + 1024 * i), soff[i]);
     };
 
     // ---- Q as B operands: lane (column c, k-group g), k-step ks: dims 32ks + 8g .. +7, times scale*log2(e)
@@ -1415,20 +1457,23 @@ __device__ __forceinline__ void gi_prefill256r(const GiPrefillArgs& a) {
     }
 
     // ---- operand read offsets (bytes within a buffer's K or V image)
-    // K: block kb, k-step ks: key krow + 4kb (krow = 8(c/4) + c%4), image half ks/4, unit 4(ks%4) + g swizzled
+    // K: block kb, k-step ks: key krow + 4(kb%2) + 32(kb/2) (krow = 8(c/4) + c%4), image half ks/4, unit
+    // 4(ks%4) + g swizzled
     const int krow = 8 * (c >> 2) + (c & 3);
-    auto kfrag = [&](const unsigned char* K, int st) { // MFMA st of a tile's 16: block st%2, k-step st/2
-        const int kb = st & 1, ks = st >> 1;
-        const int row = krow + 4 * kb + 32 * (ks >> 2);
-        const int unit = (4 * (ks & 3) + g) ^ pf256r_swz_k(krow + 4 * kb);
-        return *reinterpret_cast<const h8*>(K + row * 256 + (unit << 4));
+    auto kfrag = [&](const unsigned char* K, int st) { // MFMA st of a tile's NKB*KS: block st%NKB, k-step st/NKB
+        const int kb = st % NKB, ks = st / NKB;
+        const int key = krow + 4 * (kb & 1) + 32 * (kb >> 1);
+        const int unit = (4 * (ks & 3) + g) ^ pf256r_swz_k(key);
+        return *reinterpret_cast<const h8*>(K + (key + BK * (ks >> 2)) * 256 + (unit << 4));
     };
     // V: block db (dims 16db..), keys 8g + te (+4): image row 32*(db/8) + 8g + te, unit 2*(db%8) + tc/2 swizzled,
     // plus 8 bytes for odd tc (te = (lane%16)/4, tc = lane%4); the +4 rows of the second read keep the swizzle
+    // (BK = 64: k-step kp of P V takes keys 32kp + ..)
     const int te = c >> 2, tc = c & 3;
     const int vbase = (8 * g + te) * 256 + 8 * (tc & 1);
-    auto vfrag = [&](const unsigned char* V, int db) {
-        const int off = vbase + 8192 * (db >> 3) + (((2 * (db & 7) + (tc >> 1)) ^ pf256r_swz_v(8 * g + te)) << 4);
+    auto vfrag = [&](const unsigned char* V, int db, int kp) {
+        const int off = vbase + 8192 * kp + BK * 256 * (db >> 3) +
+                        (((2 * (db & 7) + (tc >> 1)) ^ pf256r_swz_v(8 * g + te)) << 4);
         gi_s4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((GI_LDS gi_s4*)(V + off));
         gi_s4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((GI_LDS gi_s4*)(V + off + 1024));
         return __builtin_shufflevector(__builtin_bit_cast(h4x, lo), __builtin_bit_cast(h4x, hi), 0, 1, 2, 3, 4, 5,
@@ -1443,22 +1488,23 @@ __device__ __forceinline__ void gi_prefill256r(const GiPrefillArgs& a) {
     f4 negm = f4{0.f, 0.f, 0.f, 0.f}; // -m_run: the C operand that starts each QK chain
 
     auto qk = [&](int t, f4* s) {
-        const unsigned char* K = &smem[t & (PF_NBUF - 1)][0][0];
+        const unsigned char* K = kbuf(t);
         h8 kf[PF_KPF];
 #pragma unroll
         for (int st = 0; st < PF_KPF; st++) kf[st] = kfrag(K, st);
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int st = 0; st < 2 * KS; st++) {
-            const int kb = st & 1, ks = st >> 1;
+        for (int st = 0; st < NKB * KS; st++) {
+            const int kb = st % NKB, ks = st / NKB;
             const h8 cur = kf[st % PF_KPF];
-            if (st + PF_KPF < 2 * KS) kf[st % PF_KPF] = kfrag(K, st + PF_KPF);
+            if (st + PF_KPF < NKB * KS) kf[st % PF_KPF] = kfrag(K, st + PF_KPF);
             s[kb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(cur, qf[ks], ks == 0 ? negm : s[kb], 0, 0, 0);
         }
     };
     auto rowmax = [&](const f4* sc) {
-        float mx = fmaxf(fmaxf(fmaxf(sc[0][0], sc[0][1]), fmaxf(sc[0][2], sc[0][3])),
-                         fmaxf(fmaxf(sc[1][0], sc[1][1]), fmaxf(sc[1][2], sc[1][3])));
+        float mx = GI_NEG_INF;
+#pragma unroll
+        for (int kb = 0; kb < NKB; kb++) mx = fmaxf(mx, fmaxf(fmaxf(sc[kb][0], sc[kb][1]), fmaxf(sc[kb][2], sc[kb][3])));
         return rows_max(mx);
     };
     const int wave_first = a.pos0 + q0 + PF256R_ROWS * wave; // position of the wave's first row
@@ -1478,61 +1524,65 @@ __device__ __forceinline__ void gi_prefill256r(const GiPrefillArgs& a) {
             l_run *= alpha;
 #pragma unroll
             for (int db = 0; db < NDB; db++) o[db] *= alpha;
-            s[0] -= delta;
-            s[1] -= delta;
+#pragma unroll
+            for (int kb = 0; kb < NKB; kb++) s[kb] -= delta;
         }
         qk(it + 1, sn);
-        h8 pf; // keys 8g + e, e = 4kb + r
+        h8 pf[NKB / 2]; // k-step kp: keys 32kp + 8g + e, e = 4(kb%2) + r for block kb = 2kp + kb%2
 #pragma unroll
-        for (int kb = 0; kb < 2; kb++)
+        for (int kb = 0; kb < NKB; kb++)
 #pragma unroll
             for (int r = 0; r < 4; r += 2) {
                 const _Float16 h0 = (_Float16)__builtin_amdgcn_exp2f(s[kb][r]);
                 const _Float16 h1 = (_Float16)__builtin_amdgcn_exp2f(s[kb][r + 1]);
-                pf[4 * kb + r] = h0;
-                pf[4 * kb + r + 1] = h1;
+                pf[kb >> 1][4 * (kb & 1) + r] = h0;
+                pf[kb >> 1][4 * (kb & 1) + r + 1] = h1;
                 l_run = __builtin_amdgcn_fdot2(h2{h0, h1}, h2{(_Float16)1.f, (_Float16)1.f}, l_run, false);
             }
-        const unsigned char* V = &smem[it & (PF_NBUF - 1)][1][0];
+        const unsigned char* V = vbuf(it);
 #pragma unroll
-        for (int db = 0; db < NDB; db++) o[db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vfrag(V, db), pf, o[db], 0, 0, 0);
+        for (int kp = 0; kp < NKB / 2; kp++)
+#pragma unroll
+            for (int db = 0; db < NDB; db++)
+                o[db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vfrag(V, db, kp), pf[kp], o[db], 0, 0, 0);
         mx = rowmax(sn);
 #pragma unroll
-        for (int i = 0; i < 2 * KS; i++) {
+        for (int i = 0; i < NKB * KS; i++) {
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-            if (i + PF_KPF < 2 * KS) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            if (i + PF_KPF < NKB * KS) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
         }
     };
 
-    // prologue: tiles 0-2 start loading; tile 0 is waited for and published
-    stage(0);
-    if (ntiles > 1) stage(1);
-    if (ntiles > 2) stage(2);
-    if (ntiles > 2) __builtin_amdgcn_s_waitcnt(GI_VMCNT(2 * LPW));
-    else if (ntiles > 1) __builtin_amdgcn_s_waitcnt(GI_VMCNT(LPW));
-    else __builtin_amdgcn_s_waitcnt(GI_VMCNT(0));
+    // prologue: K of tiles 0..NKBUF-1 and V of tiles 0..NVBUF-2 start loading; K(0) is waited for and
+    // published (the rest are waited for by the iterations that first read them)
+    const int last_k0 = min(NKBUF - 1, ntiles - 1), last_v0 = min(NVBUF - 2, ntiles - 1);
+    for (int t = 0; t <= (stage_v ? last_v0 : last_k0); t++) stage(t);
+    if (!stage_v) wait_tiles(last_k0);
     asm volatile("s_barrier" ::: "memory");
     float mx = GI_NEG_INF;
     auto iteration = [&](int it, f4* s, f4* sn) {
-        if (it + 2 < ntiles) __builtin_amdgcn_s_waitcnt(GI_VMCNT(LPW));
-        else __builtin_amdgcn_s_waitcnt(GI_VMCNT(0));
+        // K waves need K(it+1), having issued up to K(it + NKBUF - 1); V waves need V(it), issued up to
+        // V(it + NVBUF - 2)
+        if (stage_v) wait_tiles(max(min(it + NVBUF - 2, ntiles - 1) - it, 0));
+        else wait_tiles(max(min(it + NKBUF - 1, ntiles - 1) - (it + 1), 0));
         asm volatile("s_barrier" ::: "memory");
-        if (it + 3 < ntiles) stage(it + 3);
+        if (!stage_v && it + NKBUF < ntiles) stage(it + NKBUF);    // into K(it)'s buffer
+        if (stage_v && it + NVBUF - 1 < ntiles) stage(it + NVBUF - 1); // into V(it-1)'s buffer
         if (it < my_tiles) {
             const int t0 = it * BK;
             if (t0 + BK - 1 > wave_first) { // the tile crosses the diagonal somewhere in the wave
                 const int lim = qpos - t0;
 #pragma unroll
-                for (int kb = 0; kb < 2; kb++)
+                for (int kb = 0; kb < NKB; kb++)
 #pragma unroll
                     for (int r = 0; r < 4; r++)
-                        if (8 * g + 4 * kb + r > lim) s[kb][r] = GI_NEG_INF;
+                        if (32 * (kb >> 1) + 8 * g + 4 * (kb & 1) + r > lim) s[kb][r] = GI_NEG_INF;
                 mx = rowmax(s);
             }
             step(it, s, sn, mx);
         }
     };
-    f4 sa[2], sb[2];
+    f4 sa[NKB], sb[NKB];
     if (my_tiles > 0) {
         qk(0, sa);
         mx = rowmax(sa);
@@ -1565,7 +1615,15 @@ __device__ __forceinline__ void gi_prefill256r(const GiPrefillArgs& a) {
 extern "C" __global__ void __launch_bounds__(64 * PF_WAVES, 1) gi_prefill_fwd(GiPrefillArgs a) { gi_prefill_t<false, 128>(a); }
 extern "C" __global__ void __launch_bounds__(64 * PF_WAVES, 1) gi_prefill_fwd_i8(GiPrefillArgs a) { gi_prefill_t<true, 128>(a); }
 extern "C" __global__ void __launch_bounds__(64 * PF_WAVES, 1) gi_prefill_fwd_h256(GiPrefillArgs a) { gi_prefill_t<false, 256>(a); }
-extern "C" __global__ void __launch_bounds__(64 * PF256R_WAVES, 1) gi_prefill_fwd_h256r(GiPrefillArgs a) { gi_prefill256r(a); }
+#ifndef PF256R_KBUF
+#define PF256R_KBUF 2 // K tile buffers of gi_prefill_fwd_h256r
+#endif
+#ifndef PF256R_VBUF
+#define PF256R_VBUF 2 // V tile buffers of gi_prefill_fwd_h256r
+#endif
+extern "C" __global__ void __launch_bounds__(64 * PF256R_WAVES, 1) gi_prefill_fwd_h256r(GiPrefillArgs a) {
+    gi_prefill256r<PF256R_KBUF, PF256R_VBUF>(a);
+}
 
 // ------------------------------------------------------------------------------------------------ KV store
 

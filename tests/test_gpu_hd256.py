@@ -97,10 +97,12 @@ def test_decode_hd256_device_position(gpu):
 # ---------------------------------------------------------------- prefill (attention_prefill_tc256)
 
 PREFILL_SHAPES_256 = [
-    # (n, pos0, n_heads, n_kv, q dtype, out dtype, layout): one tile, diagonal and tile edges (32 keys,
+    # (n, pos0, n_heads, n_kv, q dtype, out dtype, layout): one tile, diagonal and tile edges (64 keys,
     # 128 query rows per workgroup), chunks at a prefix, both layouts
     (16, 0, 8, 2, np.float16, torch.float32, "reference"),
     (33, 0, 4, 1, np.float32, torch.float32, "reference"),
+    (65, 0, 4, 1, np.float16, torch.float32, "reference"),
+    (127, 63, 8, 2, np.float16, torch.float32, "head_major"),
     (128, 0, 16, 2, np.float16, torch.float16, "reference"),
     (129, 0, 8, 8, np.float16, torch.float32, "head_major"),
     (300, 40, 16, 2, np.float32, torch.float32, "reference"),
