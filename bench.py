@@ -523,8 +523,7 @@ def main():
                                     if hd == 256 else "config 3: causal prefill, 8192 tokens, 32q/8kv, hd 128" +
                                     (", int8 cache" if i8 else "")), "flops_per_step": r["flops"]},
             "roofline": prefill_roofline(gi_attn, r, args.steps, torch, f"pmc_prefill_{w}",
-                                         "gi_prefill_fwd_i8" if i8 else ("gi_prefill_fwd_h256r" if os.environ.get(
-                                             "GI_PF256R", "1") != "0" else "gi_prefill_fwd_h256") if hd == 256
+                                         "gi_prefill_fwd_i8" if i8 else "gi_prefill_fwd_h256r" if hd == 256
                                          else "gi_prefill_fwd"),
         })
         if not args.no_cpu_baseline and not i8 and hd == HD:

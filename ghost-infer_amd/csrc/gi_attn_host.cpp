@@ -142,11 +142,10 @@ struct Module {
     hipFunction_t dec_pm[2][2] = {};  // [int8 cache][column blocks - 1]: one pair per column
     hipFunction_t dec_pm256 = {};     // head size 256, one pair per column, 4 waves sharing each tile
     hipFunction_t prefill[2] = {};   // [int8 cache], head size 128
-    hipFunction_t prefill256 = nullptr; // head size 256 (f16 cache): two workgroups per query tile
-    hipFunction_t prefill256r = nullptr; // head size 256, 16 rows per wave: one workgroup per query tile
+    hipFunction_t prefill256r = nullptr; // head size 256 (f16 cache), 16 rows per wave: one workgroup per query tile
     hipFunction_t combine = nullptr, rope = nullptr;
     int prefill_threads[2] = {}; // each prefill kernel's block size (its launch bound: waves x 64)
-    int prefill256_threads = 0, prefill256r_threads = 0;
+    int prefill256r_threads = 0;
 };
 std::mutex g_mu;
 Module g_mods[kMaxDevices];
@@ -185,7 +184,6 @@ int load_module(const char* path, Module** out) {
             {&m.combine, "gi_decode_combine"},
             {&m.prefill[0], "gi_prefill_fwd"},
             {&m.prefill[1], "gi_prefill_fwd_i8"},
-            {&m.prefill256, "gi_prefill_fwd_h256"},
             {&m.prefill256r, "gi_prefill_fwd_h256r"},
             {&m.rope, "gi_qk_norm_rope"},
         };
@@ -199,8 +197,6 @@ int load_module(const char* path, Module** out) {
                           "hipFuncGetAttribute(gi_prefill_fwd)") ||
                     check(hipFuncGetAttribute(&m.prefill_threads[1], HIP_FUNC_ATTRIBUTE_MAX_THREADS_PER_BLOCK, m.prefill[1]),
                           "hipFuncGetAttribute(gi_prefill_fwd_i8)") ||
-                    check(hipFuncGetAttribute(&m.prefill256_threads, HIP_FUNC_ATTRIBUTE_MAX_THREADS_PER_BLOCK, m.prefill256),
-                          "hipFuncGetAttribute(gi_prefill_fwd_h256)") ||
                     check(hipFuncGetAttribute(&m.prefill256r_threads, HIP_FUNC_ATTRIBUTE_MAX_THREADS_PER_BLOCK,
                                               m.prefill256r),
                           "hipFuncGetAttribute(gi_prefill_fwd_h256r)")) {
@@ -489,15 +485,12 @@ int prefill_impl(void* stream, const void* q, int q_dtype, long long q_stride, c
     a.qscale = scale * kLog2e;
     a.q_f16 = q_dtype == GI_F16;
     a.out_f16 = out_dtype == GI_F16;
-    static const bool rows16 = [] { const char* e = getenv("GI_PF256R"); return !e || atoi(e) != 0; }();
-    if (hd == 256 && rows16) // one workgroup per (head, 128 query rows), 16 rows per wave
+    if (hd == 256) // one workgroup per (head, 128 query rows), 16 rows per wave
         return launch(kPrefill, m->prefill256r, dim3((n + kPrefill256rRows - 1) / kPrefill256rRows * n_heads, 1, 1),
                       dim3(m->prefill256r_threads), (hipStream_t)stream, &a, sizeof a);
-    const int threads = hd == 256 ? m->prefill256_threads : m->prefill_threads[i8];
-    int qtiles = (n + kPrefillRows - 1) / kPrefillRows;
-    // head size 256: two workgroups per (head, query tile), one per half of the output dims
-    return launch(kPrefill, hd == 256 ? m->prefill256 : m->prefill[i8], dim3(qtiles * n_heads * (hd / 128), 1, 1),
-                  dim3(threads), (hipStream_t)stream, &a, sizeof a);
+    const int qtiles = (n + kPrefillRows - 1) / kPrefillRows; // one workgroup per (head, 256 query rows)
+    return launch(kPrefill, m->prefill[i8], dim3(qtiles * n_heads, 1, 1), dim3(m->prefill_threads[i8]),
+                  (hipStream_t)stream, &a, sizeof a);
 }
 
 int attention_impl(void* stream, const float* qkv, const void* kc, const void* vc, const float* ks, const float* vs,

@@ -966,24 +966,17 @@ typedef short gi_s4 __attribute__((__vector_size__(8))); // 4 f16 as ds_read_b64
 // and the tile's 64 key and value scales go to LDS beside it. Scores are the integer-key dot products
 // times the key scale (QK chains start from zero; s = acc * kscale - m); P V takes f16(p * vscale *
 // PF_I8_VBIAS) and the row sum the f16-rounded p, as the reference's pv / pf.
-template <bool I8, int HD>
+template <bool I8>
 __device__ __forceinline__ void gi_prefill_t(const GiPrefillArgs& a) {
-    static_assert(HD == 128 || (HD == 256 && !I8), "head sizes: 128 (f16, int8), 256 (f16)");
-    // head size 256: 32-key tiles, so a K or V tile is still 16 KB: staged as 64 half-rows of 256 bytes, keys
-    // 0..31 with dims 0..127 then keys 0..31 with dims 128..255, which is the 64-key tile's LDS image at head
-    // size 128 (every swizzle and operand read below is unchanged; the dim half stands where the key block
-    // was). As the reference's attention_prefill_tc256 (src/cuda.rs:2622-2623), a workgroup computes the
-    // output dims of one half (DS = 2 workgroups per head and query tile, each with all of QK): O^T of 128
-    // dims keeps a wave within half the register file, so two waves share each SIMD as at head size 128.
+    constexpr int HD = 128;
     constexpr int WAVES = PF_WAVES;
     constexpr int BQ = 32 * WAVES;  // query rows per workgroup
     constexpr int SW = WAVES / 2;   // waves staging each of K and V
     constexpr int LPW = 16 / SW;    // 1 KB loads per staging wave and tile
-    constexpr int BK = HD == 256 ? 32 : PF_BK; // keys per tile
+    constexpr int BK = PF_BK;       // keys per tile
     constexpr int NBLK = BK / 32;   // S^T blocks of 32 keys
     constexpr int KS = HD / 16;     // QK k-steps
-    constexpr int NDB = 4;          // O^T blocks of 32 dims: 128 output dims per workgroup
-    constexpr int DS = HD / 128;    // workgroups per (head, query tile), each with 128 output dims
+    constexpr int NDB = HD / 32;    // O^T blocks of 32 dims
     __shared__ __attribute__((aligned(1024))) unsigned char smem[PF_NBUF][2][PF_TILE]; // [buffer][K, V]
     __shared__ __attribute__((aligned(16))) float scl[I8 ? PF_NBUF : 1][2][BK];         // int8: [buffer][K, V] scales
 
@@ -994,11 +987,10 @@ __device__ __forceinline__ void gi_prefill_t(const GiPrefillArgs& a) {
     const int nwg = gridDim.x;
     int j = blockIdx.x;
     if ((nwg & 7) == 0) j = (j & 7) * (nwg >> 3) + (j >> 3);
-    const int kvh = j / (qtiles * G * DS);
-    const int rest = j % (qtiles * G * DS);
-    const int qt = qtiles - 1 - rest / (G * DS);
-    const int h = kvh * G + (rest % (G * DS)) / DS;
-    const int dh = rest % DS; // the workgroup's half of the output dims (head size 256)
+    const int kvh = j / (qtiles * G);
+    const int rest = j % (qtiles * G);
+    const int qt = qtiles - 1 - rest / G; // longest query tiles first
+    const int h = kvh * G + rest % G;
     const int q0 = qt * BQ;
     const int kv_len = a.pos0 + a.n;
     const int k_lim = min(kv_len, a.pos0 + q0 + BQ); // keys any row of the tile may see
@@ -1015,14 +1007,9 @@ __device__ __forceinline__ void gi_prefill_t(const GiPrefillArgs& a) {
     for (int i = 0; i < LPW; i++) {
         const int r = 4 * (LPW * (wave % SW) + i) + (lane >> 4);
         const int u = (lane & 15) ^ (stage_v ? ((r & 3) << 2) : (r & 15));
-        // image row r: key r (head size 128); key r%32, dims 128*(r/32).. (head size 256)
-        soff[i] = HD == 256 ? ((r & 31) * (int)kvs + 128 * (r >> 5) + 8 * u) * 2 : (r * (int)kvs + 8 * u) * 2;
+        soff[i] = (r * (int)kvs + 8 * u) * 2;
     }
-    // head size 256: the V image's rows 32*dh.. (this workgroup's dim half) are the only ones read, so the
-    // V waves staging the other half have nothing to load (their waits below hold with none outstanding)
-    const bool stage_idle = HD == 256 && stage_v && (4 * LPW * (wave % SW)) / 32 != dh;
     auto stage = [&](int t) {
-        if (stage_idle) return;
         const int t0 = t * BK;
         const uint16_t* src = sbase + (long long)t0 * kvs;
         const long long bytes = (long long)(kv_len - t0) * kvs * 2;
@@ -1122,10 +1109,9 @@ __device__ __forceinline__ void gi_prefill_t(const GiPrefillArgs& a) {
 
     // S^T of tile t (its K in buffer t%4) minus the row's reference max: each chain starts from C = negm,
     // so the MFMA output is the exp2 argument itself
-    // MFMA st of a tile's 16: head size 128 alternates the two key blocks (k-step st/2, image half st%2);
-    // head size 256 has one key block, k-step st, its dims in image half st/8
+    // MFMA st of a tile's 16 alternates the two key blocks (k-step st/2, key block st%2)
     auto kfrag = [&](const unsigned char* K, int st) {
-        const int reg = HD == 256 ? st >> 3 : st & 1, ksr = HD == 256 ? st & 7 : st >> 1;
+        const int reg = st & 1, ksr = st >> 1;
         return *reinterpret_cast<const h8*>(K + 8192 * reg + kbase + 32 * (ksr ^ ky));
     };
     auto qk = [&](int t, f16x* s) {
@@ -1137,7 +1123,7 @@ __device__ __forceinline__ void gi_prefill_t(const GiPrefillArgs& a) {
         __builtin_amdgcn_sched_barrier(0); // the first PF_KPF reads go out before any of the MFMAs
 #pragma unroll
         for (int st = 0; st < 16; st++) {
-            const int ks = HD == 256 ? st : st >> 1, bb = HD == 256 ? 0 : st & 1;
+            const int ks = st >> 1, bb = st & 1;
             const h8 cur = kf[st % PF_KPF];
             if (st + PF_KPF < 16) kf[st % PF_KPF] = kfrag(K, st + PF_KPF);
             s[bb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(cur, qf[ks], ks == 0 ? (I8 ? f16x{} : negm) : s[bb], 0, 0, 0);
@@ -1246,8 +1232,8 @@ __device__ __forceinline__ void gi_prefill_t(const GiPrefillArgs& a) {
                 l_run = __builtin_amdgcn_fdot2(h2{h0, h1}, h2{(_Float16)1.f, (_Float16)1.f}, l_run, false);
             }
 #pragma unroll
-            for (int db = 0; db < NDB; db++) { // (head size 256: dims 128dh.. in the image's half dh)
-                const unsigned char* vp = V + 8192 * dh + vbase + ((db ^ te) << 6) + 4096 * ks;
+            for (int db = 0; db < NDB; db++) {
+                const unsigned char* vp = V + vbase + ((db ^ te) << 6) + 4096 * ks;
                 gi_s4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((GI_LDS gi_s4*)(vp));
                 gi_s4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((GI_LDS gi_s4*)(vp + 1024));
                 h8 vf = __builtin_shufflevector(__builtin_bit_cast(h4x, lo), __builtin_bit_cast(h4x, hi),
@@ -1323,7 +1309,7 @@ __device__ __forceinline__ void gi_prefill_t(const GiPrefillArgs& a) {
     if (qrow < a.n) {
         const float inv = (I8 ? 1.f / PF_I8_VBIAS : 1.f) / l;
         if (a.out_f16) {
-            _Float16* op = (_Float16*)a.out + (long long)qrow * a.out_stride + h * HD + 128 * dh + 4 * half;
+            _Float16* op = (_Float16*)a.out + (long long)qrow * a.out_stride + h * HD + 4 * half;
 #pragma unroll
             for (int db = 0; db < NDB; db++)
 #pragma unroll
@@ -1333,7 +1319,7 @@ __device__ __forceinline__ void gi_prefill_t(const GiPrefillArgs& a) {
                     *reinterpret_cast<h4x*>(op + 32 * db + 8 * i) = v;
                 }
         } else {
-            float* op = (float*)a.out + (long long)qrow * a.out_stride + h * HD + 128 * dh + 4 * half;
+            float* op = (float*)a.out + (long long)qrow * a.out_stride + h * HD + 4 * half;
 #pragma unroll
             for (int db = 0; db < NDB; db++)
 #pragma unroll
@@ -1346,16 +1332,18 @@ __device__ __forceinline__ void gi_prefill_t(const GiPrefillArgs& a) {
 
 // ---------------------------------------------------------------- prefill, head size 256, 16 rows per wave
 // One workgroup per (head, 128 query rows): 8 waves of 16 rows, each with all 256 output dims, so QK and the
-// softmax are computed once (the two-workgroup split above computes both twice). On v_mfma_f32_16x16x32_f16:
-//  - S^T (16 keys x 16 queries per block) = K Q^T over 8 k-steps of 32 dims, from C = -max as above. Lane l
-//    holds query column c = l%16 and rows 4g + r (g = l/16) of each block. A-row rho of key block kb reads
-//    tile key 8(rho/4) + 4kb + rho%4, so those rows are keys 8g + 4kb + r: exactly the keys 8g + e
-//    (e = 4kb + r) the lane holds in the P^T operand of P V, with no data movement.
-//  - O^T (16 dims x 16 queries per block) += V^T P^T over the tile's 32 keys: one MFMA per 16-dim block,
-//    V^T from two transposing reads (keys 8g..8g+3 and 8g+4..8g+7, 16 dims) per block.
-// K and V tiles hold 64 keys in the two-half-row LDS image of the head-size-256 kernel above (dims 0-127 of
-// the 64 keys, then dims 128-255), 32 KB each, with this kernel's swizzles. Per tile a wave issues 64 MFMAs
-// against 64 KB of LDS operand reads, twice the bytes per flop of the 32-row waves.
+// softmax are computed once per row (the reference's attention_prefill_tc256 splits the output dims over
+// two blocks that both compute QK, src/cuda.rs:2622-2623). On v_mfma_f32_16x16x32_f16, per 64-key tile:
+//  - S^T (4 blocks of 16 keys x 16 queries) = K Q^T over 8 k-steps of 32 dims, each chain starting from
+//    C = -(reference max). Lane l holds query column c = l%16 and rows 4g + r (g = l/16) of each block.
+//    A-row rho of key block kb reads tile key 8(rho/4) + 4(kb%2) + 32(kb/2) + rho%4, so the lane's rows
+//    are keys 32(kb/2) + 8g + 4(kb%2) + r: exactly the keys 32kp + 8g + e (kp = kb/2, e = 4(kb%2) + r) it
+//    holds in the P^T operand of k-step kp of P V, with no data movement.
+//  - O^T (16 blocks of 16 dims x 16 queries) += V^T P^T: per 16-dim block one MFMA for each 32 keys, V^T
+//    from two transposing reads (keys 8g..8g+3 and 8g+4..8g+7 of the 32, 16 dims).
+// LDS image of a K or V tile (32 KB): row r holds key r%64, dims 128(r/64) .. +127 (256 bytes), its 16-byte
+// units XOR-swizzled (pf256r_swz_k / pf256r_swz_v). Per tile a wave issues 64 MFMAs against 64 KB of LDS
+// operand reads, twice the bytes per flop of the head-size-128 kernel's 32-row waves.
 __device__ __forceinline__ int pf256r_swz_k(int r) { return (r & 15) ^ (((r >> 4) & 1) << 2); }
 __device__ __forceinline__ int pf256r_swz_v(int r) { return ((r & 3) << 2) | (((r >> 3) & 1) << 1); }
 #define PF256R_WAVES 8
@@ -1404,8 +1392,8 @@ __device__ __forceinline__ void gi_prefill256r(const GiPrefillArgs& a) {
     const int ntiles = (k_lim + BK - 1) / BK;
     const long long kvs = a.kv_stride;
 
-    // ---- staging, as the head-size-256 path of gi_prefill_t (image row r = key r%BK, dims 128*(r/BK)..), with
-    // this kernel's swizzles of the 16-byte units. K: the key's low 4 bits with bit 4 folded into bit 2, so
+    // ---- staging: wave w's load i covers image rows 4*(LPW*(w%SW) + i) + lane/16 (row r = key r%BK, dims
+    // 128*(r/BK)..), LDS unit lane%16 holding global unit (lane%16) ^ swizzle(r). K: the key's low 4 bits with bit 4 folded into bit 2, so
     // that the 16 rows one K fragment read touches (keys 8(c/4) + c%4 (+4), c = 0..15: low 4 bits repeat at
     // c and c + 8) fall on 16 different unit positions. V: (key % 4) << 2 with bit 3 into bit 1, so that lane
     // groups g and g + 1 of a transposing read (keys 8g + te and 8g + 8 + te) use disjoint banks.
@@ -1612,9 +1600,8 @@ __device__ __forceinline__ void gi_prefill256r(const GiPrefillArgs& a) {
     }
 }
 
-extern "C" __global__ void __launch_bounds__(64 * PF_WAVES, 1) gi_prefill_fwd(GiPrefillArgs a) { gi_prefill_t<false, 128>(a); }
-extern "C" __global__ void __launch_bounds__(64 * PF_WAVES, 1) gi_prefill_fwd_i8(GiPrefillArgs a) { gi_prefill_t<true, 128>(a); }
-extern "C" __global__ void __launch_bounds__(64 * PF_WAVES, 1) gi_prefill_fwd_h256(GiPrefillArgs a) { gi_prefill_t<false, 256>(a); }
+extern "C" __global__ void __launch_bounds__(64 * PF_WAVES, 1) gi_prefill_fwd(GiPrefillArgs a) { gi_prefill_t<false>(a); }
+extern "C" __global__ void __launch_bounds__(64 * PF_WAVES, 1) gi_prefill_fwd_i8(GiPrefillArgs a) { gi_prefill_t<true>(a); }
 #ifndef PF256R_KBUF
 #define PF256R_KBUF 2 // K tile buffers of gi_prefill_fwd_h256r
 #endif
