@@ -1025,11 +1025,19 @@ __device__ __forceinline__ void gi_prefill_t(const GiPrefillArgs& a) {
     const float* scb = I8 ? (tid < 64 ? a.ks : a.vs) + kvh * a.sc_head_stride : nullptr;
     u4 rk = u4{0u, 0u, 0u, 0u}, rv = rk;
     float rsc = 0.f;
+    // Lanes with sch >= 4 hold their chunk's two 8-byte halves swapped (and write them in that order below):
+    // then the 8 lanes of a row that one 16-byte LDS store serves write 8 different units mod 8, all 32
+    // banks, where 2sch alone would cover half of them twice.
+    const int flip = (sch >> 2) & 1;
     auto load8 = [&](int t) {
         const int t0 = t * PF_BK;
         const int off = sr * (int)kvs + 16 * sch;
-        rk = gi_load16(gi_rsrc(kb8 + (long long)t0 * kvs, (long long)(kv_len - t0) * kvs), off);
-        rv = gi_load16(gi_rsrc(vb8 + (long long)t0 * kvs, (long long)(kv_len - t0) * kvs), off);
+        const __amdgpu_buffer_rsrc_t rsk = gi_rsrc(kb8 + (long long)t0 * kvs, (long long)(kv_len - t0) * kvs);
+        const __amdgpu_buffer_rsrc_t rsv = gi_rsrc(vb8 + (long long)t0 * kvs, (long long)(kv_len - t0) * kvs);
+        const u2 k0 = gi_load8(rsk, off + 8 * flip), k1 = gi_load8(rsk, off + 8 - 8 * flip);
+        const u2 v0 = gi_load8(rsv, off + 8 * flip), v1 = gi_load8(rsv, off + 8 - 8 * flip);
+        rk = u4{k0.x, k0.y, k1.x, k1.y};
+        rv = u4{v0.x, v0.y, v1.x, v1.y};
         if (tid < 2 * PF_BK)
             rsc = gi_load4f(gi_rsrc(scb + (long long)t0 * a.sc_stride, (long long)(kv_len - t0) * a.sc_stride * 4),
                             (tid & (PF_BK - 1)) * (int)a.sc_stride * 4);
@@ -1038,8 +1046,8 @@ __device__ __forceinline__ void gi_prefill_t(const GiPrefillArgs& a) {
         unsigned char* K = &smem[t & (PF_NBUF - 1)][0][sr * 256];
         unsigned char* V = &smem[t & (PF_NBUF - 1)][1][sr * 256];
 #pragma unroll
-        for (int hw = 0; hw < 2; hw++) { // f16 units 2sch + hw: dims 16sch + 8hw .. +7
-            const int u = 2 * sch + hw;
+        for (int hw = 0; hw < 2; hw++) { // f16 unit 2sch + (hw ^ flip): dims 16sch + 8(hw ^ flip) .. +7
+            const int u = 2 * sch + (hw ^ flip);
             u4 kw, vw;
 #pragma unroll
             for (int e = 0; e < 2; e++) {
