@@ -237,13 +237,6 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
         s = sk % gridDim.x;
         kvh = sk / gridDim.x;
     }
-#ifdef GI_DEC_TIMESTAMPS
-    unsigned long long ts[8];
-    ts[0] = wall_clock64();
-#define GI_TS(i) ts[i] = wall_clock64()
-#else
-#define GI_TS(i)
-#endif
     const int pos0 = a.posp ? *a.posp : a.pos0;
     const int G = a.n_heads / a.n_kv;
     const int npairs = a.n_tok * G;
@@ -286,7 +279,6 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
             }
     }
     __builtin_amdgcn_sched_barrier(0);
-    GI_TS(1);
     float m_run[NCB], l_run[NCB];
     // O^T: MFMA dd holds rows m = dims 8m + dd; this lane rows 4grp..4grp+3 -> dims 32grp + 8j + dd
     // (HD 256: rows m = dims 16m + dd -> dims 64grp + 16j + dd)
@@ -690,7 +682,6 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
                     qf[cb][kk][e] = (c & 1) ? (_Float16)(v - (float)hi) : hi;
                 }
             }
-    GI_TS(2);
     // Steady state: every buffer gets a further tile (those past the slice read zeros and are never
     // processed). The last round of tiles runs without reloads, so no load is left in flight at the end.
     int t = t_first;
@@ -702,7 +693,6 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
     for (int i = 0; i < DEC_NB; i++)
         if (t + i * STRIDE < nkeys) process(B[i], t + i * STRIDE, false);
     }
-    GI_TS(4);
 
     // ---- wave results to LDS: every lane's 32 O^T values (its column, dims 32grp + 8j + dd) as 8 16-byte
     // stores; per pair the max and the sum over the 4 k-groups
@@ -725,9 +715,7 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
             sm_l[wave][cb * CPAIRS + (PM ? c : c >> 1)] = l;
         }
     }
-    GI_TS(6);
     __syncthreads();
-    GI_TS(7);
     // ---- merge the waves (SHARE: each pair has one wave) and the hi/lo columns: thread -> (pair, 4 dims)
     constexpr float LO = I8 ? 1.f / DEC_I8_LO : 1.f;      // the remainder column's scale (PM: no column)
     constexpr float OSC = I8 && PM ? 1.f / DEC_I8_VB : 1.f; // PM int8: the bias on P
@@ -777,19 +765,6 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
             }
         }
     }
-#ifdef GI_DEC_TIMESTAMPS
-    ts[5] = wall_clock64();
-    if (lane == 0) {
-        unsigned long long* dbg = (unsigned long long*)(a.part + (long long)a.n_tok * a.n_heads * a.nsplit * PART);
-        long long w = ((long long)(gz * gridDim.y + kvh) * gridDim.x + s) * DEC_WAVES + wave;
-        for (int i = 0; i < 6; i++) dbg[w * 16 + i] = ts[i];
-        dbg[w * 16 + 8] = ts[6];
-        dbg[w * 16 + 9] = ts[7];
-        unsigned xcc;
-        asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
-        dbg[w * 16 + 6] = __smid() | ((unsigned long long)xcc << 32);
-    }
-#endif
 }
 
 #define GI_DEC_KERNEL(name, NCB, SHARE, I8, HD) \
