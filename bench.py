@@ -462,9 +462,9 @@ def main():
         kt = kernel_times(gi_attn, r["step"], args.steps, torch, ("decode_partial", "decode_combine"))
         part_ms, part_n = kt["decode_partial"]
         comb_ms, _ = kt["decode_combine"]
-        # algorithmic bytes of one split-kernel launch: K and V of every span key, the queries, and the
-        # slice partials it writes ([token][head][slice][hd + 4] f32)
-        part_bytes = r["bytes"] + n_tok * n_heads * hd * 4 + n_tok * n_heads * nsplit * (hd + 4) * 4
+        # algorithmic bytes of one split-kernel launch: K and V of every span key and the queries (the slice
+        # partials it writes are overhead of the split, not counted)
+        part_bytes = r["bytes"] + n_tok * n_heads * hd * 4
         kern_gbs = part_bytes / (part_ms / 1e3) / 1e9
         traffic = profile_traffic(f"pmc_decode_partial_{w}")
         result.update({

@@ -46,6 +46,8 @@ struct GiDecodeArgs {
     const float* vs;
     long long sc_stride;
     long long sc_head_stride;
+    int kv_cap;
+    int pad_;
 };
 
 // Must match the kernels' GiRopeArgs.
@@ -74,6 +76,23 @@ struct GiRopeArgs {
     float* vs;
     long long sc_stride;
     long long sc_head_stride;
+    int ctx_cap;
+    int pad_;
+};
+
+// Must match the kernels' GiRelayoutArgs.
+struct GiRelayoutArgs {
+    const void* src;
+    void* dst;
+    long long src_stride;
+    long long src_head_stride;
+    long long dst_stride;
+    long long dst_head_stride;
+    long long n_units;
+    int n_rows;
+    int units_per_row;
+    int unit;
+    int pad_;
 };
 
 // Must match the kernels' GiPrefillArgs.
@@ -102,11 +121,8 @@ struct GiPrefillArgs {
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kMaxDevices = 64;
-#ifndef CMB_DSPLIT
-#define CMB_DSPLIT 8
-#endif
 constexpr int kRopeHeads = 16; // heads per gi_qk_norm_rope workgroup; must match the kernels' ROPE_HEADS
-constexpr int kCombineSplit = CMB_DSPLIT; // combine workgroups per (head, token); must match the kernels'
+constexpr int kCombineSplit = 8; // combine workgroups per (head, token); must match the kernels' CMB_DSPLIT
 constexpr int kDecWaves = 4, kDecTile = 32, kDecPairs = 8; // slice partials are hd + 4 floats
 constexpr int kSliceUnit = kDecWaves * kDecTile; // 128 keys
 constexpr int kSplitMaxBatch = 15;                // tokens per split launch (src/cuda.rs:119)
@@ -143,7 +159,7 @@ struct Module {
     hipFunction_t dec_pm256 = {};     // head size 256, one pair per column, 4 waves sharing each tile
     hipFunction_t prefill[2] = {};   // [int8 cache], head size 128
     hipFunction_t prefill256r = nullptr; // head size 256 (f16 cache), 16 rows per wave: one workgroup per query tile
-    hipFunction_t combine = nullptr, rope = nullptr;
+    hipFunction_t combine = nullptr, rope = nullptr, relayout = nullptr;
     int prefill_threads[2] = {}; // each prefill kernel's block size (its launch bound: waves x 64)
     int prefill256r_threads = 0;
 };
@@ -182,6 +198,7 @@ int load_module(const char* path, Module** out) {
             {&m.dec_pm[1][1], "gi_decode_pm_2_i8"},
             {&m.dec_pm256, "gi_decode_pm_shared_1_h256"},
             {&m.combine, "gi_decode_combine"},
+            {&m.relayout, "gi_kv_relayout"},
             {&m.prefill[0], "gi_prefill_fwd"},
             {&m.prefill[1], "gi_prefill_fwd_i8"},
             {&m.prefill256r, "gi_prefill_fwd_h256r"},
@@ -211,8 +228,8 @@ int load_module(const char* path, Module** out) {
 }
 
 // ---- per-kernel timing (gi_kernel_timing): event pairs around each launch, per kernel kind
-enum Kind { kDecodePartial = 0, kDecodeCombine = 1, kPrefill = 2, kRope = 3, kKinds = 4 };
-const char* const kKindNames[kKinds] = {"decode_partial", "decode_combine", "prefill", "qk_norm_rope"};
+enum Kind { kDecodePartial = 0, kDecodeCombine = 1, kPrefill = 2, kRope = 3, kRelayout = 4, kKinds = 5 };
+const char* const kKindNames[kKinds] = {"decode_partial", "decode_combine", "prefill", "qk_norm_rope", "kv_relayout"};
 struct Timing {
     std::mutex mu;
     bool on = false;
@@ -367,6 +384,7 @@ int decode_impl(void* stream, const float* q, long long q_stride, const void* kc
     a.kc = (const uint16_t*)kc;
     a.vc = (const uint16_t*)vc;
     a.part = (float*)workspace;
+    a.kv_cap = posp ? ctx_cap : pos0 + n_tok;
     a.out = out;
     a.posp = posp;
     a.q_stride = q_stride;
@@ -388,17 +406,14 @@ int decode_impl(void* stream, const float* q, long long q_stride, const void* kc
     hipStream_t st = (hipStream_t)stream;
     hipFunction_t f = hd == 256 ? (var.pm ? m->dec_pm256 : m->dec256) : var.pm ? m->dec_pm[i8][var.ncb - 1] : m->dec[i8];
     if (int e = launch(kDecodePartial, f, dim3(a.nsplit, n_kv, var.groups), dim3(256), st, &a, sizeof a)) return e;
-    if (a.nsplit > 1)
-        if (int e = launch(kDecodeCombine, m->combine, dim3(n_heads, n_tok, kCombineSplit * hd / 128), dim3(64), st, &a,
-                           sizeof a))
-            return e;
-    return 0;
+    if (a.nsplit == 1) return 0;
+    return launch(kDecodeCombine, m->combine, dim3(n_heads, n_tok, kCombineSplit * hd / 128), dim3(64), st, &a, sizeof a);
 }
 
 // gi_qk_norm_rope and gi_qk_norm_rope_i8: one kernel, f16 or int8 cache rows.
 int rope_impl(void* stream, float* qkv, const float* qn, const float* kn, void* kc, void* vc, float* ks, float* vs,
-              long long sc_stride, long long sc_head_stride, bool i8, long long kv_stride, long long kv_head_stride, int pos0, const int* posp, int n, int n_heads,
-                    int n_kv, int hd, int rope_dim, float base, const float* ff, int neox, float eps) {
+              long long sc_stride, long long sc_head_stride, bool i8, long long kv_stride, long long kv_head_stride, int pos0, const int* posp, int ctx_cap, int n,
+              int n_heads, int n_kv, int hd, int rope_dim, float base, const float* ff, int neox, float eps) {
     if (hd != 64 && hd != 128 && hd != 256) return fail("head size %d unsupported by the KV store (64, 128, 256)", hd);
     if (n_kv <= 0 || n_heads <= 0 || n_heads % n_kv != 0)
         return fail("n_heads %d must be a positive multiple of n_kv %d", n_heads, n_kv);
@@ -407,6 +422,9 @@ int rope_impl(void* stream, float* qkv, const float* qn, const float* kn, void* 
     if (!qkv || !kc || !vc) return fail("null tensor pointer");
     if ((qn == nullptr) != (kn == nullptr)) return fail("qn and kn must both be given or both be null");
     if (!posp && pos0 < 0) return fail("pos0 %d must be >= 0", pos0);
+    if (posp && ctx_cap < n) return fail("with posp, ctx_cap %d must cover the %d tokens", ctx_cap, n);
+    if (!posp && ctx_cap > 0 && ctx_cap < pos0 + n)
+        return fail("positions %d..%d exceed ctx_cap %d", pos0, pos0 + n - 1, ctx_cap);
     if (kv_head_stride == 0) kv_head_stride = hd;
     if (int e = check_kv_strides(kv_stride, kv_head_stride, n_kv, hd, i8 ? 16 : 8)) return e;
     if (i8)
@@ -414,6 +432,7 @@ int rope_impl(void* stream, float* qkv, const float* qn, const float* kn, void* 
     Module* m;
     if (int e = load_module(nullptr, &m)) return e;
     GiRopeArgs a{};
+    a.ctx_cap = ctx_cap > 0 ? ctx_cap : pos0 + n;
     a.qkv = qkv;
     a.qn = qn;
     a.kn = kn;
@@ -623,7 +642,8 @@ int gi_kernel_timing_read(const char* kernel, double* total_ms, int* launches) {
     int kind = -1;
     for (int k = 0; k < kKinds; k++)
         if (std::strcmp(kernel, kKindNames[k]) == 0) kind = k;
-    if (kind < 0) return fail("unknown kernel \"%s\" (decode_partial, decode_combine, prefill or qk_norm_rope)", kernel);
+    if (kind < 0) return fail("unknown kernel \"%s\" (decode_partial, decode_combine, prefill, qk_norm_rope or kv_relayout)",
+                             kernel);
     std::vector<std::pair<hipEvent_t, hipEvent_t>> ev;
     {
         std::lock_guard<std::mutex> lock(g_timing.mu);
@@ -645,19 +665,56 @@ int gi_kernel_timing_read(const char* kernel, double* total_ms, int* launches) {
 }
 
 int gi_qk_norm_rope(void* stream, float* qkv, const float* qn, const float* kn, uint16_t* kc, uint16_t* vc,
-                    long long kv_stride, long long kv_head_stride, int pos0, const int* posp, int n, int n_heads,
-                    int n_kv, int hd, int rope_dim, float base, const float* ff, int neox, float eps) {
-    return rope_impl(stream, qkv, qn, kn, kc, vc, nullptr, nullptr, 0, 0, false, kv_stride, kv_head_stride, pos0, posp, n,
-                     n_heads, n_kv, hd, rope_dim, base, ff, neox, eps);
+                    long long kv_stride, long long kv_head_stride, int pos0, const int* posp, int ctx_cap, int n,
+                    int n_heads, int n_kv, int hd, int rope_dim, float base, const float* ff, int neox, float eps) {
+    return rope_impl(stream, qkv, qn, kn, kc, vc, nullptr, nullptr, 0, 0, false, kv_stride, kv_head_stride, pos0, posp,
+                     ctx_cap, n, n_heads, n_kv, hd, rope_dim, base, ff, neox, eps);
 }
 
 int gi_qk_norm_rope_i8(void* stream, float* qkv, const float* qn, const float* kn, int8_t* kc, int8_t* vc, float* ks,
                        float* vs, long long kv_stride, long long kv_head_stride, long long sc_stride,
-                       long long sc_head_stride, int pos0, const int* posp, int n, int n_heads, int n_kv, int hd,
-                       int rope_dim, float base, const float* ff, int neox, float eps) {
+                       long long sc_head_stride, int pos0, const int* posp, int ctx_cap, int n, int n_heads, int n_kv,
+                       int hd, int rope_dim, float base, const float* ff, int neox, float eps) {
     if (sc_stride == 0 && sc_head_stride == 0) sc_stride = n_kv, sc_head_stride = 1;
     return rope_impl(stream, qkv, qn, kn, kc, vc, ks, vs, sc_stride, sc_head_stride, true, kv_stride, kv_head_stride,
-                     pos0, posp, n, n_heads, n_kv, hd, rope_dim, base, ff, neox, eps);
+                     pos0, posp, ctx_cap, n, n_heads, n_kv, hd, rope_dim, base, ff, neox, eps);
+}
+
+int gi_kv_relayout(void* stream, const void* src, long long src_stride, long long src_head_stride, void* dst,
+                   long long dst_stride, long long dst_head_stride, int n_rows, int n_kv, int row_bytes) {
+    if (n_rows < 0 || n_kv <= 0 || row_bytes <= 0 || row_bytes % 4)
+        return fail("n_rows %d >= 0, n_kv %d > 0 and row_bytes %d (a positive multiple of 4) required", n_rows, n_kv,
+                    row_bytes);
+    if (n_rows == 0) return 0;
+    if (!src || !dst) return fail("null tensor pointer");
+    if (((uintptr_t)src | (uintptr_t)dst) & 3 || (src_stride | src_head_stride | dst_stride | dst_head_stride) & 3)
+        return fail("pointers and strides must be multiples of 4 bytes");
+    if (src_stride <= 0 || src_head_stride <= 0 || dst_stride <= 0 || dst_head_stride <= 0)
+        return fail("strides must be positive");
+    // the two sides' spans must not overlap (rows would be read after they are overwritten)
+    auto span = [&](const void* p, long long st, long long hs) {
+        const uintptr_t b = (uintptr_t)p;
+        return std::make_pair(b, b + (uintptr_t)((long long)(n_rows - 1) * st + (long long)(n_kv - 1) * hs + row_bytes));
+    };
+    const auto s = span(src, src_stride, src_head_stride), d = span(dst, dst_stride, dst_head_stride);
+    if (s.first < d.second && d.first < s.second) return fail("source and destination overlap");
+    Module* m;
+    if (int e = load_module(nullptr, &m)) return e;
+    GiRelayoutArgs a{};
+    const bool wide = !(((uintptr_t)src | (uintptr_t)dst) & 15) && !((src_stride | src_head_stride | dst_stride |
+                                                                      dst_head_stride | row_bytes) & 15);
+    a.src = src;
+    a.dst = dst;
+    a.src_stride = src_stride;
+    a.src_head_stride = src_head_stride;
+    a.dst_stride = dst_stride;
+    a.dst_head_stride = dst_head_stride;
+    a.n_rows = n_rows;
+    a.unit = wide ? 16 : 4;
+    a.units_per_row = row_bytes / a.unit;
+    a.n_units = (long long)n_kv * n_rows * a.units_per_row;
+    const long long wgs = std::min<long long>((a.n_units + 255) / 256, 256 * 16);
+    return launch(kRelayout, m->relayout, dim3((unsigned)wgs), dim3(256), (hipStream_t)stream, &a, sizeof a);
 }
 
 } // extern "C"

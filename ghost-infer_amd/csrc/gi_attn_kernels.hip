@@ -65,6 +65,8 @@ struct GiDecodeArgs {
     const float* vs;
     long long sc_stride;
     long long sc_head_stride;
+    int kv_cap;            // with posp: keys the cache holds; *posp is clamped to [0, kv_cap - n_tok]
+    int pad_;
 };
 
 #define DEC_WAVES 4
@@ -237,7 +239,8 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
         s = sk % gridDim.x;
         kvh = sk / gridDim.x;
     }
-    const int pos0 = a.posp ? *a.posp : a.pos0;
+    // a device position is clamped so that no key past the cache's capacity is read
+    const int pos0 = a.posp ? min(max(*a.posp, 0), a.kv_cap - a.n_tok) : a.pos0;
     const int G = a.n_heads / a.n_kv;
     const int npairs = a.n_tok * G;
     constexpr int WG_PAIRS = (SHARE ? DEC_WAVES : 1) * CPAIRS * NCB; // pairs per workgroup
@@ -1623,6 +1626,8 @@ struct GiRopeArgs {
     float* vs;
     long long sc_stride;
     long long sc_head_stride;
+    int ctx_cap;           // positions the cache holds: rows at positions outside [0, ctx_cap) are not stored
+    int pad_;
 };
 
 // Reference semantics: qk_norm_rope (src/cuda.rs:437-486) with an f16 cache (kv_store, src/cuda.rs:312-362).
@@ -1639,6 +1644,7 @@ struct GiRopeArgs {
 template <int PER>
 __device__ __forceinline__ void gi_store_row(const GiRopeArgs& a, uint16_t* cache, float* scale, int pos, int kh,
                                              const float __attribute__((ext_vector_type(PER))) x, int lane) {
+    if (pos < 0 || pos >= a.ctx_cap) return; // (a device position past the capacity writes nothing)
     const long long off = (long long)pos * a.kv_stride + (long long)kh * a.kv_head_stride;
     if (!a.i8) {
         typedef _Float16 hv __attribute__((ext_vector_type(PER)));
@@ -1728,4 +1734,36 @@ extern "C" __global__ void __launch_bounds__(256) gi_qk_norm_rope(GiRopeArgs a) 
     if (a.hd == 64) gi_qk_norm_rope_t<1>(a, cs_sh, row_sh);
     else if (a.hd == 128) gi_qk_norm_rope_t<2>(a, cs_sh, row_sh);
     else gi_qk_norm_rope_t<4>(a, cs_sh, row_sh);
+}
+
+// ------------------------------------------------------------------------------------------- cache growth
+
+// Arguments of gi_kv_relayout (must match gi_attn_host.cpp). Strides in bytes.
+struct GiRelayoutArgs {
+    const unsigned char* src;
+    unsigned char* dst;
+    long long src_stride;      // between positions
+    long long src_head_stride; // between kv heads
+    long long dst_stride;
+    long long dst_head_stride;
+    long long n_units;         // n_kv * n_rows * units_per_row
+    int n_rows;
+    int units_per_row;
+    int unit;                  // bytes per unit: 16 or 4
+    int pad_;
+};
+// Cache growth (LayerCache::resize, src/cuda.rs:9962-9976, which the reference does as one contiguous copy of
+// `keep` rows): rows (position t < n_rows, kv head h) of one layout copied into another, e.g. a head-major
+// cache [n_kv][cap][hd] into one of a larger capacity, whose rows all move. Thread -> one 16-byte (or 4-byte)
+// unit; consecutive threads walk a head's rows in order, so both sides stream whole rows.
+extern "C" __global__ void __launch_bounds__(256) gi_kv_relayout(GiRelayoutArgs a) {
+    for (long long i = blockIdx.x * 256ll + threadIdx.x; i < a.n_units; i += (long long)gridDim.x * 256) {
+        const int u = (int)(i % a.units_per_row);
+        const long long r = i / a.units_per_row;
+        const long long t = r % a.n_rows, h = r / a.n_rows;
+        const unsigned char* sp = a.src + t * a.src_stride + h * a.src_head_stride + (long long)u * a.unit;
+        unsigned char* dp = a.dst + t * a.dst_stride + h * a.dst_head_stride + (long long)u * a.unit;
+        if (a.unit == 16) *reinterpret_cast<u4*>(dp) = *reinterpret_cast<const u4*>(sp);
+        else *reinterpret_cast<uint32_t*>(dp) = *reinterpret_cast<const uint32_t*>(sp);
+    }
 }

@@ -39,6 +39,7 @@ SYMBOLS = (
     "gi_attention_i8",
     "gi_qk_norm_rope",
     "gi_qk_norm_rope_i8",
+    "gi_kv_relayout",
     "gi_kernel_timing",
     "gi_kernel_timing_read",
 )
@@ -68,6 +69,8 @@ def load_library(path=LIB_PATH):
     lib.gi_attn_decode_plan.restype = i
     lib.gi_attn_decode_workspace_bytes.argtypes = [i, i, i, i, i]
     lib.gi_attn_decode_workspace_bytes.restype = sz
+    lib.gi_kv_relayout.argtypes = [vp, vp, ll, ll, vp, ll, ll, i, i, i]
+    lib.gi_kv_relayout.restype = i
     lib.gi_attn_decode.argtypes = [vp, vp, ll, vp, vp, ll, ll, vp, ll, vp, sz, i, vp, i, i, i, i, i, f]
     lib.gi_attn_decode.restype = i
     lib.gi_attn_decode_i8.argtypes = [vp, vp, ll, vp, vp, vp, vp, ll, ll, ll, ll, vp, ll, vp, sz, i, vp, i, i, i, i, i,
@@ -81,10 +84,10 @@ def load_library(path=LIB_PATH):
     lib.gi_attn_prefill_i8.restype = i
     lib.gi_attention_i8.argtypes = [vp, vp, vp, vp, vp, vp, vp, vp, sz, i, vp, i, i, i, i, i, i]
     lib.gi_attention_i8.restype = i
-    lib.gi_qk_norm_rope.argtypes = [vp, vp, vp, vp, vp, vp, ll, ll, i, vp, i, i, i, i, i, f, vp, i, f]
+    lib.gi_qk_norm_rope.argtypes = [vp, vp, vp, vp, vp, vp, ll, ll, i, vp, i, i, i, i, i, i, f, vp, i, f]
     lib.gi_qk_norm_rope.restype = i
-    lib.gi_qk_norm_rope_i8.argtypes = [vp, vp, vp, vp, vp, vp, vp, vp, ll, ll, ll, ll, i, vp, i, i, i, i, i, f, vp, i,
-                                       f]
+    lib.gi_qk_norm_rope_i8.argtypes = [vp, vp, vp, vp, vp, vp, vp, vp, ll, ll, ll, ll, i, vp, i, i, i, i, i, i, f, vp,
+                                       i, f]
     lib.gi_qk_norm_rope_i8.restype = i
     lib.gi_kernel_timing.argtypes = [i]
     lib.gi_kernel_timing.restype = i
@@ -303,10 +306,12 @@ def attention(qkv, k_cache, v_cache, pos0, n_heads, n_kv, hd=128, exact=False, o
 
 
 def qk_norm_rope(qkv, k_cache, v_cache, pos0, n_heads, n_kv, hd=128, rope_dim=None, base=10000.0, qn=None, kn=None,
-                 ff=None, neox=True, eps=1e-6, posp=None, kv_layout="reference", k_scale=None, v_scale=None):
+                 ff=None, neox=True, eps=1e-6, posp=None, kv_layout="reference", k_scale=None, v_scale=None,
+                 ctx_cap=None):
     """RMSNorm + RoPE of the q and k heads of f32 rows [q | k | v] (in place) and the k and v heads into the
     caches at positions pos0.. (layer_attn's qk_norm_rope step, src/cuda.rs:437-486): f16 caches, or int8
-    ones quantised per row into k_scale / v_scale (kv_store with KV8, src/cuda.rs:333-339)."""
+    ones quantised per row into k_scale / v_scale (kv_store with KV8, src/cuda.rs:333-339). Rows at positions
+    past ctx_cap (default: the cache's capacity) are not stored, so a device position cannot write past it."""
     _need(qkv, "qkv", torch.float32)
     if not qkv.is_contiguous() or qkv.dim() != 2 or qkv.shape[1] != (n_heads + 2 * n_kv) * hd:
         raise GiAttnError(f"qkv must be contiguous [n, {(n_heads + 2 * n_kv) * hd}]")
@@ -320,18 +325,54 @@ def qk_norm_rope(qkv, k_cache, v_cache, pos0, n_heads, n_kv, hd=128, rope_dim=No
             _need(t, name, torch.float32)
     if posp is not None:
         _need(posp, "posp", torch.int32)
+    cap = capacity if ctx_cap is None else ctx_cap
+    if cap > capacity:
+        raise GiAttnError(f"ctx_cap {cap} exceeds the cache's {capacity} positions")
     rope = (hd if rope_dim is None else rope_dim, base, _ptr(ff), 1 if neox else 0, eps)
     if k_cache.dtype == torch.int8:
         sc_stride, sc_head_stride = _scale_layout(k_scale, v_scale, n_kv, capacity, kv_layout)
         _check(load_library().gi_qk_norm_rope_i8(_stream(), _ptr(qkv), _ptr(qn), _ptr(kn), _ptr(k_cache),
                                                  _ptr(v_cache), _ptr(k_scale), _ptr(v_scale), kv_stride,
-                                                 kv_head_stride, sc_stride, sc_head_stride, pos0, _ptr(posp), n,
-                                                 n_heads, n_kv, hd, *rope))
+                                                 kv_head_stride, sc_stride, sc_head_stride, pos0, _ptr(posp), cap,
+                                                 n, n_heads, n_kv, hd, *rope))
     else:
         _check(load_library().gi_qk_norm_rope(_stream(), _ptr(qkv), _ptr(qn), _ptr(kn), _ptr(k_cache), _ptr(v_cache),
-                                              kv_stride, kv_head_stride, pos0, _ptr(posp), n, n_heads, n_kv, hd,
-                                              *rope))
+                                              kv_stride, kv_head_stride, pos0, _ptr(posp), cap, n, n_heads, n_kv,
+                                              hd, *rope))
     return qkv
+
+
+def kv_relayout(src, dst, n_rows, layout="head_major", n_kv=None):
+    """Cache growth (LayerCache::resize's copy of the first n_rows positions, src/cuda.rs:9962-9976): copies
+    positions 0..n_rows-1 of every kv head from cache `src` into `dst` of a larger capacity, in the same
+    layout. head_major: [n_kv, cap, row...] (every row moves); reference: [cap, n_kv, row...] (or [cap, n_kv]
+    scales). Works for f16 and int8 rows and f32 scales; returns dst."""
+    if src.dtype != dst.dtype or not src.is_contiguous() or not dst.is_contiguous():
+        raise GiAttnError("src and dst must be contiguous tensors of one dtype")
+    _need(src, "src", src.dtype)
+    _need(dst, "dst", dst.dtype)
+    es = src.element_size()
+    if layout == "head_major":
+        if src.dim() < 2 or src.shape[0] != dst.shape[0] or src.shape[2:] != dst.shape[2:]:
+            raise GiAttnError("head-major caches must be [n_kv, cap, ...] with equal rows")
+        n_kv = src.shape[0]
+        row = es * (src[0, 0].numel())
+        cap_s, cap_d = src.shape[1], dst.shape[1]
+        strides = (row, cap_s * row, row, cap_d * row)
+    elif layout == "reference":
+        if src.dim() < 2 or src.shape[1:] != dst.shape[1:]:
+            raise GiAttnError("reference caches must be [cap, n_kv, ...] with equal rows")
+        n_kv = src.shape[1]
+        row = es * (src[0, 0].numel())
+        cap_s, cap_d = src.shape[0], dst.shape[0]
+        strides = (n_kv * row, row, n_kv * row, row)
+    else:
+        raise GiAttnError(f"unknown cache layout {layout!r}")
+    if n_rows > min(cap_s, cap_d):
+        raise GiAttnError(f"{n_rows} rows do not fit capacities {cap_s} and {cap_d}")
+    _check(load_library().gi_kv_relayout(_stream(), _ptr(src), strides[0], strides[1], _ptr(dst), strides[2],
+                                         strides[3], n_rows, n_kv, row))
+    return dst
 
 
 def kernel_timing(on):
@@ -341,9 +382,8 @@ def kernel_timing(on):
 
 
 def kernel_timing_read(kernel):
-    """(total milliseconds, launches) of kernel kind "decode_partial", "decode_combine", "prefill" or
-    "qk_norm_rope"
-    since the previous read of that kind."""
+    """(total milliseconds, launches) of kernel kind "decode_partial", "decode_combine", "prefill",
+    "qk_norm_rope" or "kv_relayout" since the previous read of that kind."""
     ms, n = ctypes.c_double(), ctypes.c_int()
     _check(load_library().gi_kernel_timing_read(kernel.encode(), ctypes.byref(ms), ctypes.byref(n)))
     return ms.value, n.value

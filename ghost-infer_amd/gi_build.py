@@ -37,12 +37,12 @@ def build_kernels():
 
 
 def build_host():
-    run([HIPCC, "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall", "-I", os.path.join(ROOT, "include"),
+    run([HIPCC, "--offload-arch=gfx950", "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall", "-I", os.path.join(ROOT, "include"),
          os.path.join(CSRC, "gi_attn_host.cpp"), "-o", LIB, "-ldl"])
 
 
 def build_harness():
-    run([HIPCC, "-O2", "-std=c++17", "-Wall", "-I", os.path.join(ROOT, "include"),
+    run([HIPCC, "--offload-arch=gfx950", "-O2", "-std=c++17", "-Wall", "-I", os.path.join(ROOT, "include"),
          os.path.join(HERE, "harness", "gi_layer_harness.cpp"), "-o", HARNESS, "-L", HERE, "-lgi_attn",
          "-Wl,-rpath,$ORIGIN"])
 

@@ -29,6 +29,7 @@ namespace {
 struct Opts {
     int prompt = 300, steps = 24, heads = 32, kv = 8, hd = 128, seed = 1;
     bool i8 = false, graph = true;
+    std::string dump; // file for the final qkv rows and the output rows (f32, raw), for checks outside
 };
 
 [[noreturn]] void die(const std::string& what) {
@@ -44,10 +45,11 @@ void gi_ok(int rc, const char* what) {
 
 void usage() {
     printf("usage: gi_layer_harness [--prompt N] [--steps S] [--heads H] [--kv K] [--hd 128|256] [--int8]\n"
-           "                        [--no-graph] [--seed X]\n"
+           "                        [--no-graph] [--seed X] [--dump FILE]\n"
            "Plays one layer's attention through the C ABI (cache write + prefill for the prompt, then one\n"
            "decode step per token, replayed from a HIP graph), checks every output row against the exact\n"
-           "split path over the whole sequence, and prints one JSON line.\n");
+           "split path over the whole sequence, and prints one JSON line. --dump writes the rotated qkv rows\n"
+           "and the output rows (f32) to FILE.\n");
 }
 
 Opts parse(int argc, char** argv) {
@@ -69,6 +71,10 @@ Opts parse(int argc, char** argv) {
         else if (a == "--seed") num(o.seed);
         else if (a == "--int8") o.i8 = true;
         else if (a == "--no-graph") o.graph = false;
+        else if (a == "--dump") {
+            if (i + 1 >= argc) die("missing value after --dump");
+            o.dump = argv[++i];
+        }
         else die("unknown argument " + a);
     }
     if (o.prompt < 1 || o.steps < 0 || o.heads < 1 || o.kv < 1 || o.heads % o.kv || (o.hd != 128 && o.hd != 256) ||
@@ -127,10 +133,10 @@ int main(int argc, char** argv) {
     auto write_cache = [&](float* rows, int pos0, const int* pp, int n) {
         if (o.i8)
             return gi_qk_norm_rope_i8(st, rows, nullptr, nullptr, (int8_t*)kc, (int8_t*)vc, ks, vs, kv_stride,
-                                      kv_head_stride, sc_stride, sc_head_stride, pos0, pp, n, H, K, hd, rope_dim,
+                                      kv_head_stride, sc_stride, sc_head_stride, pos0, pp, cap, n, H, K, hd, rope_dim,
                                       rope_base, nullptr, 1, eps);
         return gi_qk_norm_rope(st, rows, nullptr, nullptr, (uint16_t*)kc, (uint16_t*)vc, kv_stride, kv_head_stride,
-                               pos0, pp, n, H, K, hd, rope_dim, rope_base, nullptr, 1, eps);
+                               pos0, pp, cap, n, H, K, hd, rope_dim, rope_base, nullptr, 1, eps);
     };
     // gi_attention takes the reference's [position][n_kv][hd] cache; the head-major session cache goes
     // through the decode / prefill entry points with its strides, as the operator would dispatch them
@@ -222,6 +228,14 @@ int main(int argc, char** argv) {
             if (t < o.prompt) err_prompt = d > err_prompt ? d : err_prompt;
             else err_decode = d > err_decode ? d : err_decode;
         }
+    if (!o.dump.empty()) {
+        std::vector<float> rows((size_t)total * row);
+        hip_ok(hipMemcpy(rows.data(), qkv, rows.size() * sizeof(float), hipMemcpyDeviceToHost), "hipMemcpy qkv");
+        FILE* f = fopen(o.dump.c_str(), "wb");
+        if (!f || fwrite(rows.data(), sizeof(float), rows.size(), f) != rows.size() ||
+            fwrite(got.data(), sizeof(float), got.size(), f) != got.size() || fclose(f) != 0)
+            die("cannot write " + o.dump);
+    }
     const double tol_prompt = o.prompt >= 16 ? 2e-3 : 2e-5, tol_decode = 2e-5;
     const bool ok = finite && err_prompt <= tol_prompt && err_decode <= tol_decode;
     printf("{\"prompt\": %d, \"steps\": %d, \"heads\": %d, \"kv\": %d, \"hd\": %d, \"cache\": \"%s\", \"graph\": %s, "

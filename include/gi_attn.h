@@ -60,16 +60,18 @@ int gi_attn_decode_plan(int max_span, int n_tok, int n_heads, int n_kv, int hd, 
 
 /* Bytes of workspace gi_attn_decode needs for n_tok tokens whose spans reach at most ctx_cap keys (the
  * slice partials, [token][head][slice][hd + 4] f32: O, max, sum, 2 pad; 16-byte aligned). Covers the int8
- * entry points too. The
- * counterpart of the session's att_part buffer (GpuSession, src/cuda.rs:9826-9870). */
+ * entry points too. The counterpart of the session's att_part buffer (GpuSession, src/cuda.rs:9826-9870).
+ * The workspace needs no initialisation; calls that share one must be ordered (one stream). */
 size_t gi_attn_decode_workspace_bytes(int ctx_cap, int n_tok, int n_heads, int n_kv, int hd);
 
 /* Decode / verify attention for n_tok tokens (one generated token, or a speculative verify block that
  * is causal within itself). q: f32 rows (q_stride elements apart); out: f32 rows. When posp is non-NULL
  * the position is read from device memory (*posp replaces pos0; graph replay) and the grid is sized for
  * ctx_cap keys, so one launch shape serves every position up to ctx_cap - n_tok; otherwise ctx_cap is
- * ignored. Replaces: attention_partial_gqa + attention_combine, launched by GpuModel::attention's split
- * path (src/cuda.rs:1684-1865, src/cuda.rs:2806-2836, src/cuda.rs:8478-8538). */
+ * ignored. The kernel clamps *posp into [0, ctx_cap - n_tok], so a stale or wrong device position reads no
+ * key past ctx_cap (it gives the attention at the clamped position instead of an error). Replaces:
+ * attention_partial_gqa + attention_combine, launched by GpuModel::attention's split path (src/cuda.rs:1684-1865,
+ * src/cuda.rs:2806-2836, src/cuda.rs:8478-8538). */
 int gi_attn_decode(void* stream, const float* q, long long q_stride, const uint16_t* kc, const uint16_t* vc,
                    long long kv_stride, long long kv_head_stride, float* out, long long out_stride, void* workspace,
                    size_t workspace_bytes, int pos0, const int* posp, int ctx_cap, int n_tok, int n_heads, int n_kv,
@@ -121,7 +123,9 @@ int gi_attention_i8(void* stream, const float* qkv, const int8_t* kc, const int8
                     int ctx_cap, int n, int n_heads, int n_kv, int hd, int exact);
 
 /* The layer's step before attention, for a batch of n tokens at positions pos0.. (posp: read from device
- * memory, graph replay). qkv: f32 rows [q (n_heads*hd) | k (n_kv*hd) | v (n_kv*hd)], updated in place:
+ * memory, graph replay). ctx_cap: positions the cache holds; rows at positions outside [0, ctx_cap) are not
+ * stored (a device position cannot write past the cache). Required (>= n) with posp; 0 without posp means
+ * pos0 + n, which the caller has checked. qkv: f32 rows [q (n_heads*hd) | k (n_kv*hd) | v (n_kv*hd)], updated in place:
  * each q and k head gets an RMSNorm (skipped when qn and kn are NULL: ss = sum of squares, x * rsqrt(ss/hd
  * + eps) * weight) and RoPE on its first rope_dim dims (pairs (i, i + rope_dim/2) when neox, else
  * (2i, 2i+1); angle = pos * base^(-2i/rope_dim) / ff[i], ff NULL = 1). The k and v heads are then stored
@@ -129,16 +133,27 @@ int gi_attention_i8(void* stream, const float* qkv, const int8_t* kc, const int8
  * Replaces: qk_norm_rope with an f16 cache (src/cuda.rs:437-486, kv_store src/cuda.rs:312-362), launched
  * by layer_attn (src/cuda.rs:9706-9717). */
 int gi_qk_norm_rope(void* stream, float* qkv, const float* qn, const float* kn, uint16_t* kc, uint16_t* vc,
-                    long long kv_stride, long long kv_head_stride, int pos0, const int* posp, int n, int n_heads,
-                    int n_kv, int hd, int rope_dim, float base, const float* ff, int neox, float eps);
+                    long long kv_stride, long long kv_head_stride, int pos0, const int* posp, int ctx_cap, int n,
+                    int n_heads, int n_kv, int hd, int rope_dim, float base, const float* ff, int neox, float eps);
 
 /* gi_qk_norm_rope with an int8 cache (the layouts of gi_attn_decode_i8): each k and v row is quantised as it
  * is stored, dd = max|x| / 127, byte = round-to-nearest-even(x * (1/dd)) (0 when dd is 0), and dd goes to
  * ks / vs. Replaces: qk_norm_rope compiled with KV8 (kv_store, src/cuda.rs:333-339). */
 int gi_qk_norm_rope_i8(void* stream, float* qkv, const float* qn, const float* kn, int8_t* kc, int8_t* vc, float* ks,
                        float* vs, long long kv_stride, long long kv_head_stride, long long sc_stride,
-                       long long sc_head_stride, int pos0, const int* posp, int n, int n_heads, int n_kv, int hd,
-                       int rope_dim, float base, const float* ff, int neox, float eps);
+                       long long sc_head_stride, int pos0, const int* posp, int ctx_cap, int n, int n_heads, int n_kv,
+                       int hd, int rope_dim, float base, const float* ff, int neox, float eps);
+
+/* Cache growth: copies rows (position t < n_rows, kv head h < n_kv) of row_bytes bytes from one cache layout
+ * to another, stream-ordered, allocating nothing. Strides are in bytes (src: t*src_stride +
+ * h*src_head_stride). For a head-major cache [n_kv][cap][hd] growing to capacity cap2: src_stride =
+ * dst_stride = row_bytes, src_head_stride = cap*row_bytes, dst_head_stride = cap2*row_bytes; the f32 scales
+ * of an int8 cache move the same way with row_bytes = 4. Source and destination must not overlap. Replaces:
+ * LayerCache::resize's copy of the first `keep` rows (src/cuda.rs:9962-9976), which the engine calls as a
+ * session grows in CTX_STEP = 4096-position steps (src/cuda.rs:10410); with the reference's [position][n_kv]
+ * layout that copy is contiguous, with the head-major one every row moves. */
+int gi_kv_relayout(void* stream, const void* src, long long src_stride, long long src_head_stride, void* dst,
+                   long long dst_stride, long long dst_head_stride, int n_rows, int n_kv, int row_bytes);
 
 /* Per-kernel GPU time, for benchmarks. No counterpart in the reference. While on (process-wide), every
  * kernel the library launches outside graph capture is bracketed by a pair of HIP events on its stream.
@@ -146,7 +161,7 @@ int gi_qk_norm_rope_i8(void* stream, float* qkv, const float* qn, const float* k
 int gi_kernel_timing(int on);
 
 /* Total milliseconds and launch count of kernel kind `kernel` ("decode_partial", "decode_combine",
- * "prefill" or "qk_norm_rope") recorded since the previous read of that kind; waits for the recorded events and
+ * "prefill", "qk_norm_rope" or "kv_relayout") recorded since the previous read of that kind; waits for the recorded events and
  * releases them. */
 int gi_kernel_timing_read(const char* kernel, double* total_ms, int* launches);
 

@@ -73,9 +73,31 @@ def test_int8_entry_points_reject_bad_arguments_before_any_launch():
     rc = lib.gi_attn_decode_i8(None, 16, 4096, 16, 16, 16, 16, 512, 128, -4, 1, 16, 4096, None, 0, 0, None, 0, 1, 32,
                                4, 128, 0.1)
     assert rc == -1 and "sc_stride" in lib.gi_last_error().decode()
-    rc = lib.gi_qk_norm_rope_i8(None, 16, None, None, 16, 16, None, None, 512, 128, 0, 0, 0, None, 1, 32, 4, 128, 128,
-                                1e4, None, 1, 1e-6)
+    rc = lib.gi_qk_norm_rope_i8(None, 16, None, None, 16, 16, None, None, 512, 128, 0, 0, 0, None, 0, 1, 32, 4, 128,
+                                128, 1e4, None, 1, 1e-6)
     assert rc == -1 and "scale" in lib.gi_last_error().decode()
+
+
+def test_device_position_needs_a_capacity():
+    lib = gi_attn.load_library()
+    # the cache write with a device position must be told the capacity (its kernel skips rows past it)
+    rc = lib.gi_qk_norm_rope(None, 16, None, None, 16, 16, 512, 128, 0, 16, 0, 1, 32, 4, 128, 128, 1e4, None, 1, 1e-6)
+    assert rc == -1 and "ctx_cap" in lib.gi_last_error().decode()
+    rc = lib.gi_qk_norm_rope(None, 16, None, None, 16, 16, 512, 128, 100, None, 50, 1, 32, 4, 128, 128, 1e4, None, 1,
+                             1e-6)
+    assert rc == -1 and "exceed ctx_cap" in lib.gi_last_error().decode()
+
+
+def test_relayout_rejects_bad_arguments_before_any_launch():
+    lib = gi_attn.load_library()
+    assert lib.gi_kv_relayout(None, 16, 256, 4096, 1 << 20, 256, 8192, 0, 4, 256) == 0  # nothing to copy
+    rc = lib.gi_kv_relayout(None, 16, 256, 4096, 1 << 20, 256, 8192, 16, 4, 254)
+    assert rc == -1 and "multiple of 4" in lib.gi_last_error().decode()
+    rc = lib.gi_kv_relayout(None, 16, 256, 4096, 1 << 20, 256, -8192, 16, 4, 256)
+    assert rc == -1 and "positive" in lib.gi_last_error().decode()
+    # [4 heads][16 rows][256 B] at 16 into [4][32][256 B] at 4096: the spans overlap
+    rc = lib.gi_kv_relayout(None, 16, 256, 4096, 4096, 256, 8192, 16, 4, 256)
+    assert rc == -1 and "overlap" in lib.gi_last_error().decode()
 
 
 @pytest.mark.parametrize("ctx,n_tok,n_heads,n_kv,hd", [(4096, 1, 32, 8, 128), (65536, 1, 32, 4, 128),
@@ -84,6 +106,7 @@ def test_int8_entry_points_reject_bad_arguments_before_any_launch():
                                                        (32776, 8, 16, 2, 256), (5000, 15, 16, 2, 256)])
 def test_decode_plan_covers_the_span(ctx, n_tok, n_heads, n_kv, hd):
     part = (hd + 4) * 4  # bytes of one slice partial
+
     chunk, nsplit = gi_attn.decode_plan(ctx, n_tok, n_heads, n_kv, hd)
     assert chunk % (64 if hd == 256 else 128) == 0 and chunk > 0
     assert (nsplit - 1) * chunk < ctx <= nsplit * chunk
@@ -114,7 +137,7 @@ def test_kernel_timing_reads_and_rejects_unknown_kinds():
     assert lib.gi_kernel_timing_read(None, ctypes.byref(ms), ctypes.byref(n)) == -1
     # nothing launched: every kind reads as zero launches, without touching a GPU
     assert lib.gi_kernel_timing(1) == 0
-    for kind in (b"decode_partial", b"decode_combine", b"prefill"):
+    for kind in (b"decode_partial", b"decode_combine", b"prefill", b"qk_norm_rope", b"kv_relayout"):
         assert lib.gi_kernel_timing_read(kind, ctypes.byref(ms), ctypes.byref(n)) == 0
         assert (ms.value, n.value) == (0.0, 0)
     assert lib.gi_kernel_timing(0) == 0

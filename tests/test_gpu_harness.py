@@ -1,28 +1,72 @@
 """The C++ caller of the C ABI (ghost-infer_amd/gi_layer_harness): one layer's attention played as the
 reference's layer loop plays it (layer_attn src/cuda.rs:9706-9717, GpuModel::attention
 src/cuda.rs:8448-8541): a prompt through the cache write and the prefill path, then decode steps replayed
-from one captured HIP graph with a device-side position, every output row checked inside the harness
-against the exact split path over the whole sequence."""
+from one captured HIP graph with a device-side position. The harness checks every output row against the
+exact split path over the whole sequence itself; this test also checks the rows it dumps against the CPU
+oracle and the float64 reference, over the cache the harness's rotated k / v rows imply (f16: rounded to
+nearest even; int8: the oracle's restatement of kv_store's quantiser)."""
 import json
 import os
 import subprocess
 import sys
 
+import numpy as np
 import pytest
+
+import gi_oracle as O
+from attn_common import assert_close, reference_f64, reference_f64_i8
 
 HARNESS = os.path.join(os.path.dirname(os.path.abspath(__file__)), "..", "ghost-infer_amd", "gi_layer_harness")
 
+CASES = [
+    # (args, prompt, steps, heads, kv, hd, int8)
+    ([], 300, 24, 32, 8, 128, False),
+    (["--int8"], 300, 24, 32, 8, 128, True),
+    (["--heads", "16", "--kv", "2", "--hd", "256", "--prompt", "100", "--steps", "10"], 100, 10, 16, 2, 256, False),
+    (["--no-graph", "--prompt", "40", "--steps", "6", "--heads", "32", "--kv", "4"], 40, 6, 32, 4, 128, False),
+]
+
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("args", [[], ["--int8"], ["--heads", "16", "--kv", "2", "--hd", "256", "--prompt", "100",
-                                                   "--steps", "10"], ["--no-graph", "--prompt", "40", "--steps", "6",
-                                                                      "--heads", "32", "--kv", "4"]])
-def test_layer_harness(args):
+@pytest.mark.parametrize("case", CASES, ids=lambda c: " ".join(c[0]) or "default")
+def test_layer_harness(case, tmp_path):
+    args, prompt, steps, H, K, hd, i8 = case
     assert os.path.exists(HARNESS), "gi_layer_harness is not built (run __graft_entry__.build())"
+    dump = str(tmp_path / "rows.bin")
     print("harness", " ".join(args), flush=True)
-    r = subprocess.run([HARNESS, *args], capture_output=True, text=True, timeout=120)
+    r = subprocess.run([HARNESS, *args, "--dump", dump], capture_output=True, text=True, timeout=120)
     sys.stdout.write(r.stdout)
     sys.stderr.write(r.stderr)
     assert r.returncode == 0, f"harness exit {r.returncode}: {r.stderr.strip() or r.stdout.strip()}"
     line = json.loads(r.stdout.strip().splitlines()[-1])
     assert line["ok"] and line["max_abs_decode"] <= line["tol_decode"] and line["max_abs_prompt"] <= line["tol_prompt"]
+
+    total, row, orow = prompt + steps, (H + 2 * K) * hd, H * hd
+    raw = np.fromfile(dump, dtype=np.float32)
+    assert raw.size == total * (row + orow)
+    qkv = raw[:total * row].reshape(total, row)
+    got = raw[total * row:].reshape(total, orow)
+    q = np.ascontiguousarray(qkv[:, :orow])
+    kr = qkv[:, orow:orow + K * hd]
+    vr = qkv[:, orow + K * hd:]
+    pre, dec = slice(0, prompt), slice(prompt, total)
+    if i8:
+        kc, ks = O.kv_quant_i8(kr.reshape(total, K, hd))
+        vc, vs = O.kv_quant_i8(vr.reshape(total, K, hd))
+        kc, vc = kc.reshape(total, K * hd), vc.reshape(total, K * hd)
+        want_pre = O.prefill_tc_semantics_i8(q[pre], kc, vc, ks, vs, 0, H, K)
+        want_dec = O.decode_gpu_semantics_i8(q[dec], kc, vc, ks, vs, prompt, H, K)
+        f64 = reference_f64_i8(q, kc, vc, ks, vs, 0, H, K)
+    else:
+        kc = kr.astype(np.float16).view(np.uint16)
+        vc = vr.astype(np.float16).view(np.uint16)
+        want_pre = (O.prefill_tc_semantics(q[pre], kc, vc, 0, H, K, hd=hd) if prompt >= 16
+                    else O.attention(q[pre], kc, vc, 0, H, K, hd=hd))
+        want_dec = O.attention(q[dec], kc, vc, prompt, H, K, hd=hd)
+        f64 = reference_f64(q, kc, vc, 0, H, K, hd=hd)
+    # prompt rows: the prefill path (f16 P) against the reference's prefill semantics and float64, the bar
+    assert_close(got[pre], want_pre, what="harness prompt rows vs oracle")
+    assert_close(got[pre], f64[pre], what="harness prompt rows vs f64")
+    # decoded rows: the split path in f32 precision, against the oracle at the bar and float64 at 2e-5
+    assert_close(got[dec], want_dec, what="harness decode rows vs oracle")
+    assert_close(got[dec], f64[dec], max_abs=2e-5, rel_l2=2e-5, what="harness decode rows vs f64")
