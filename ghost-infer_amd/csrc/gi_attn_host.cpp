@@ -162,6 +162,10 @@ struct Module {
     hipFunction_t combine = nullptr, rope = nullptr, relayout = nullptr;
     int prefill_threads[2] = {}; // each prefill kernel's block size (its launch bound: waves x 64)
     int prefill256r_threads = 0;
+    // gi_attn_decode_noalloc's partials: the device address of the code object's gi_scratch array on this
+    // device (the array's host-side name is no device address; the module gives the real one at load)
+    void* scratch = nullptr;
+    size_t scratch_bytes = 0;
 };
 std::mutex g_mu;
 Module g_mods[kMaxDevices];
@@ -221,6 +225,13 @@ int load_module(const char* path, Module** out) {
             m.mod = nullptr;
             return e;
         }
+        hipDeviceptr_t sp = nullptr;
+        if (int e = check(hipModuleGetGlobal(&sp, &m.scratch_bytes, m.mod, "gi_scratch"), "hipModuleGetGlobal(gi_scratch)")) {
+            (void)hipModuleUnload(m.mod);
+            m.mod = nullptr;
+            return e;
+        }
+        m.scratch = (void*)sp;
         m.loaded = true;
     }
     *out = &m;
@@ -558,6 +569,25 @@ int gi_attn_decode(void* stream, const float* q, long long q_stride, const uint1
                    int hd, float scale) {
     return decode_impl(stream, q, q_stride, kc, vc, nullptr, nullptr, 0, 0, false, kv_stride, kv_head_stride, out,
                        out_stride, workspace, workspace_bytes, pos0, posp, ctx_cap, n_tok, n_heads, n_kv, hd, scale);
+}
+
+int gi_attn_decode_noalloc(void* stream, const float* q, long long q_stride, const uint16_t* kc, const uint16_t* vc,
+                           long long kv_stride, long long kv_head_stride, float* out, long long out_stride, int pos0,
+                           const int* posp, int ctx_cap, int n_tok, int n_heads, int n_kv, int hd, float scale) {
+    if (int e = check_shape(n_heads, n_kv, hd, true)) return e;
+    if (n_tok <= 0) return fail("n_tok %d must be positive", n_tok);
+    Module* m;
+    if (int e = load_module(nullptr, &m)) return e;
+    // the partials this call needs (decode_impl repeats the plan and every other check)
+    int chunk = 0, nsplit = 0;
+    plan(posp ? std::max(ctx_cap, 1) : std::max(pos0 + n_tok, 1), n_tok, n_heads, n_kv, &chunk, &nsplit,
+         slice_unit(false, hd), hd);
+    const size_t need = nsplit == 1 ? 0 : (size_t)n_tok * n_heads * nsplit * (hd + 4) * sizeof(float);
+    if (need > m->scratch_bytes)
+        return fail("gi_attn_decode_noalloc: %zu bytes of slice partials exceed the %zu-byte scratch (use "
+                    "gi_attn_decode with a workspace)", need, m->scratch_bytes);
+    return decode_impl(stream, q, q_stride, kc, vc, nullptr, nullptr, 0, 0, false, kv_stride, kv_head_stride, out,
+                       out_stride, m->scratch, m->scratch_bytes, pos0, posp, ctx_cap, n_tok, n_heads, n_kv, hd, scale);
 }
 
 int gi_attn_decode_i8(void* stream, const float* q, long long q_stride, const int8_t* kc, const int8_t* vc,

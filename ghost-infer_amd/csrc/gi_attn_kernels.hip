@@ -69,6 +69,11 @@ struct GiDecodeArgs {
     int pad_;
 };
 
+// Slice partials of gi_attn_decode_noalloc: a module-global array (one per device, since every device loads
+// the code object itself), for callers that cannot allocate a workspace. Calls on one device share it.
+#define GI_SCRATCH_BYTES (8u << 20)
+__device__ __attribute__((used, aligned(256))) unsigned char gi_scratch[GI_SCRATCH_BYTES];
+
 #define DEC_WAVES 4
 #ifndef DEC_NB
 #define DEC_NB 2 // register buffers of K/V tiles per wave (tiles in flight)

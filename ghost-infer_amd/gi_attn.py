@@ -32,6 +32,7 @@ SYMBOLS = (
     "gi_attn_decode_plan",
     "gi_attn_decode_workspace_bytes",
     "gi_attn_decode",
+    "gi_attn_decode_noalloc",
     "gi_attn_decode_i8",
     "gi_attn_prefill",
     "gi_attn_prefill_i8",
@@ -73,6 +74,8 @@ def load_library(path=LIB_PATH):
     lib.gi_kv_relayout.restype = i
     lib.gi_attn_decode.argtypes = [vp, vp, ll, vp, vp, ll, ll, vp, ll, vp, sz, i, vp, i, i, i, i, i, f]
     lib.gi_attn_decode.restype = i
+    lib.gi_attn_decode_noalloc.argtypes = [vp, vp, ll, vp, vp, ll, ll, vp, ll, i, vp, i, i, i, i, i, f]
+    lib.gi_attn_decode_noalloc.restype = i
     lib.gi_attn_decode_i8.argtypes = [vp, vp, ll, vp, vp, vp, vp, ll, ll, ll, ll, vp, ll, vp, sz, i, vp, i, i, i, i, i,
                                       f]
     lib.gi_attn_decode_i8.restype = i
