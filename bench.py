@@ -20,9 +20,12 @@ A step is one pass of the hot path over one batch of synthetic seeded input alre
 Decode steps rotate over several layers' caches whose total exceeds the 256 MB Infinity Cache, as a
 model's layer loop does, so no step finds its K/V in the last-level cache.
 
-Prints ONE JSON line (rank 0). With the default workload the line also carries the prefill figure
-(config 3) under "secondary", and the CPU baseline: the oracle's restatement of the reference's CPU
-attention (src/model.rs:1320-1409) timed on this host on a bounded sample of the same workload.
+Prints ONE JSON line (rank 0). With the default workload the line also carries every other config of the
+benchmark under "secondary" (decode4k, verify, prefill8k and chunked, each with its own roofline) and the
+box's measured peaks, and the CPU baseline: the oracle's restatement of the reference's CPU attention
+(src/model.rs:1320-1409) over the same inputs with the cache widened to f32 (as the reference's CPU session
+holds it), timed on this host at its CPU share (up to 16 threads) and at half of it (the reference's default
+logical/2), for configs 2 and 1 and a bounded sample of config 3.
 """
 import argparse
 import json
@@ -327,62 +330,77 @@ def peak_probes(torch, dev, reps=5):
 
 # ---------------------------------------------------------------- CPU baseline (the oracle)
 
-def cpu_baseline_decode(q, cache, pos0, n_heads, n_kv, budget_s=12.0):
-    """Times the oracle's restatement of Model::attention on this host for the same decode (q, cache), on
-    as many repetitions as fit in about budget_s seconds (median)."""
-    import numpy as np
+def cpu_threads():
+    """(all, half, logical, model): the worker counts of the CPU baseline. "all" is the CPUs this process may
+    run on (its affinity mask), capped at 16, the host share of one GPU on the benchmark boxes; "half" is
+    logical/2 of that, the reference's default thread count (src/main.rs:122-125)."""
+    try:
+        avail = len(os.sched_getaffinity(0))
+    except AttributeError:
+        avail = os.cpu_count() or 1
+    n = max(1, min(16, avail))
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return n, max(1, n // 2), os.cpu_count() or avail, model
 
-    sys.path.insert(0, os.path.join(ROOT, "oracle"))
-    import gi_oracle
 
-    threads = min(16, os.cpu_count() or 1)
-    qn = q.cpu().numpy()
-    k, v = cache[:2]
-    if k.shape[0] == n_kv and k.dim() == 3 and k.shape[1] != n_kv:  # head-major: to the reference's layout
-        k, v = k.transpose(0, 1).contiguous(), v.transpose(0, 1).contiguous()
-    kn = k.cpu().numpy().view(np.uint16).reshape(k.shape[0], -1)
-    vn = v.cpu().numpy().view(np.uint16).reshape(v.shape[0], -1)
-    gi_oracle.attention(qn, kn, vn, pos0, n_heads, n_kv, threads=threads)  # warm-up (also builds tables)
+def _median_time(fn, budget_s, min_runs=5, max_runs=200):
+    fn()  # warm-up
     times = []
     t_end = time.time() + budget_s
-    while time.time() < t_end or len(times) < 5:
+    while time.time() < t_end or len(times) < min_runs:
         t0 = time.perf_counter()
-        gi_oracle.attention(qn, kn, vn, pos0, n_heads, n_kv, threads=threads)
+        fn()
         times.append(time.perf_counter() - t0)
-        if len(times) >= 200:
+        if len(times) >= max_runs:
             break
     times.sort()
-    return times[len(times) // 2], threads, len(times)
+    return times[len(times) // 2], len(times)
 
 
-def cpu_baseline_prefill(q, k, v, n_heads, n_kv, rows=64, budget_s=12.0):
-    """Times the oracle's restatement of Model::attention on this host for a bounded sample of a causal
-    prefill: the last `rows` query rows of the prompt (each sees nearly the whole prompt), all heads, over
-    the same cache. Returns (TFLOP/s, threads, repetitions, sample flops, median seconds)."""
-    import numpy as np
+def _ref_layout_f32(k, v, n_kv):
+    """K/V caches (torch, f16, reference or head-major layout) as f32 numpy rows [pos, n_kv*hd]: the
+    reference's CPU session holds an f32 cache (src/model.rs:1326-1327); the widening is exact."""
+    if k.dim() == 3 and k.shape[0] == n_kv and k.shape[1] != n_kv:  # head-major: to [pos][n_kv][hd]
+        k, v = k.transpose(0, 1), v.transpose(0, 1)
+    kn = k.float().contiguous().cpu().numpy()
+    vn = v.float().contiguous().cpu().numpy()
+    return kn.reshape(kn.shape[0], -1), vn.reshape(vn.shape[0], -1)
 
+
+def cpu_baseline_decode(q, cache, pos0, n_heads, n_kv, threads, budget_s=8.0):
+    """The oracle's restatement of Model::attention (src/model.rs:1320-1409) for the same decode (q, cache) on
+    an f32 cache, with `threads` workers: (median seconds, runs)."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import gi_oracle
 
-    threads = min(16, os.cpu_count() or 1)
+    qn = q.cpu().numpy()
+    kn, vn = _ref_layout_f32(cache[0], cache[1], n_kv)
+    return _median_time(lambda: gi_oracle.attention(qn, kn, vn, pos0, n_heads, n_kv, threads=threads), budget_s)
+
+
+def cpu_baseline_prefill(q, k, v, n_heads, n_kv, threads, rows=64, budget_s=8.0):
+    """The oracle's Model::attention on a bounded sample of the causal prefill: the last `rows` query rows of
+    the prompt (each sees nearly the whole prompt), all heads, over the same cache widened to f32. Returns
+    (TFLOP/s, runs, sample flops, median seconds)."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import gi_oracle
+
     n = q.shape[0]
     pos0 = n - rows
     qn = q[pos0:].float().cpu().numpy()
-    kn = k.cpu().numpy().view(np.uint16).reshape(k.shape[0], -1)
-    vn = v.cpu().numpy().view(np.uint16).reshape(v.shape[0], -1)
-    gi_oracle.attention(qn, kn, vn, pos0, n_heads, n_kv, threads=threads)  # warm-up
-    times = []
-    t_end = time.time() + budget_s
-    while time.time() < t_end or len(times) < 3:
-        t0 = time.perf_counter()
-        gi_oracle.attention(qn, kn, vn, pos0, n_heads, n_kv, threads=threads)
-        times.append(time.perf_counter() - t0)
-        if len(times) >= 50:
-            break
-    times.sort()
-    t = times[len(times) // 2]
+    kn, vn = _ref_layout_f32(k, v, n_kv)
+    t, runs = _median_time(lambda: gi_oracle.attention(qn, kn, vn, pos0, n_heads, n_kv, threads=threads), budget_s,
+                           min_runs=3, max_runs=50)
     flops = prefill_flops(rows, pos0, n_heads)
-    return flops / t / 1e12, threads, len(times), flops, t
+    return flops / t / 1e12, runs, flops, t
 
 
 def prefill_roofline(gi_attn, r, steps, torch, profile="pmc_prefill_prefill8k", kernel="gi_prefill_fwd"):
@@ -393,6 +411,130 @@ def prefill_roofline(gi_attn, r, steps, torch, profile="pmc_prefill_prefill8k", 
             "frac": round(tf / F16_DENSE_PEAK_TFLOPS, 4), "traffic": profile_traffic(profile),
             "kernel": kernel, "algorithmic_flops_per_launch": r["flops"],
             "kernel_ms_per_launch": round(ms, 5), "launches_timed": n}
+
+
+# ---------------------------------------------------------------- one line per workload
+
+DECODE_WORKLOADS = {
+    # name: (ctx, n_heads, n_kv, n_tok, hd, int8, description)
+    "decode64k": (65536, 32, 4, 1, 128, False, "config 2: decode, 1 token, ctx 65536, 32q/4kv, hd 128"),
+    "decode4k": (4096, 32, 8, 1, 128, False, "config 1: decode, 1 token, ctx 4096, 32q/8kv, hd 128"),
+    "verify": (32776, 32, 4, 8, 128, False, "config 4: verify, 8 tokens at a 32768-key prefix, 32q/4kv, hd 128"),
+    "decode64k_i8": (65536, 32, 4, 1, 128, True, "config 2 over the int8 cache: decode, 1 token, ctx 65536, 32q/4kv"),
+    "verify_i8": (32776, 32, 4, 8, 128, True, "config 4 over the int8 cache: verify, 8 tokens at 32768, 32q/4kv"),
+    "decode64k_h256": (65536, 16, 2, 1, 256, False, "decode with 256-wide heads (Qwen3.5-style 16q/2kv), 1 token, "
+                                                    "ctx 65536, f16 cache"),
+    "verify_h256": (32776, 16, 2, 8, 256, False, "verify with 256-wide heads (Qwen3.5-style 16q/2kv), 8 tokens at a "
+                                                 "32768-key prefix, f16 cache"),
+}
+
+
+def run_decode(torch, gi_attn, dev, w, steps, warmup, n_tok_override=None, reference_layout=False):
+    """One decode workload: the line's fields, plus the workload's tensors for a CPU baseline."""
+    ctx, n_heads, n_kv, n_tok, hd, i8, cfg = DECODE_WORKLOADS[w]
+    if n_tok_override and w.startswith("verify") and n_tok_override != n_tok:
+        ctx, n_tok = 32768 + n_tok_override, n_tok_override
+        cfg = f"config 4's shape with {n_tok} tokens per block" + (" over the int8 cache" if i8 else "")
+    log(f"[bench] {cfg}")
+    r = decode_workload(torch, gi_attn, dev, ctx, n_heads, n_kv, n_tok, steps, warmup, 1234, i8=i8, hd=hd)
+    gbs = r["bytes"] / r["seconds"] / 1e9
+    chunk, nsplit = gi_attn.decode_plan(ctx, n_tok, n_heads, n_kv, hd)
+    if i8:  # int8 slices are whole 256-key units (64-key tiles, 4 waves)
+        chunk = -(-chunk // 256) * 256
+        nsplit = -(-ctx // chunk)
+    kt = kernel_times(gi_attn, r["step"], steps, torch, ("decode_partial", "decode_combine"))
+    part_ms, part_n = kt["decode_partial"]
+    comb_ms, _ = kt["decode_combine"]
+    # algorithmic bytes of one split-kernel launch: K and V of every span key and the queries (the slice
+    # partials it writes are overhead of the split, not counted)
+    part_bytes = r["bytes"] + n_tok * n_heads * hd * 4
+    kern_gbs = part_bytes / (part_ms / 1e3) / 1e9
+    line = {
+        "value": round(gbs, 1), "unit": "GB/s", "ms_per_step": r["seconds"] * 1e3,
+        "dtype": "int8 K/V + f32 scales, f32 math" if i8 else "f16 K/V, f32 math",
+        "config": {"workload": cfg, "ctx": ctx, "n_tok": n_tok, "n_heads": n_heads, "n_kv": n_kv, "hd": hd,
+                   "kv_bytes_per_step": r["bytes"], "layers_rotated": r["layers"],
+                   "slices": nsplit, "keys_per_slice": chunk, "kv_layout": f"head_major [n_kv][ctx][{hd}]"},
+        "roofline": {"bound": "hbm", "achieved": round(kern_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(kern_gbs / HBM_PEAK_GBS, 4), "traffic": profile_traffic(f"pmc_decode_partial_{w}"),
+                     "kernel": decode_kernel_name(n_tok, n_heads, n_kv, hd, i8) + " (split-K pass)",
+                     "algorithmic_bytes_per_launch": part_bytes,
+                     "kernel_ms_per_launch": round(part_ms, 5), "launches_timed": part_n,
+                     "combine_ms_per_launch": round(comb_ms, 5) if comb_ms else None,
+                     "step_frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)},
+    }
+    if reference_layout and not i8 and hd == HD:
+        # the same decode over caches in the reference's [position][n_kv][128] layout
+        r_ref = decode_workload(torch, gi_attn, dev, ctx, n_heads, n_kv, n_tok, steps, warmup, 1234,
+                                layout="reference")
+        line["config"]["reference_layout_GBs"] = round(r_ref["bytes"] / r_ref["seconds"] / 1e9, 1)
+        line["config"]["reference_layout_ms_per_step"] = r_ref["seconds"] * 1e3
+        del r_ref
+    return line, r
+
+
+def run_prefill(torch, gi_attn, dev, w, steps, warmup):
+    i8 = w == "prefill8k_i8"
+    hd = 256 if w.endswith("_h256") else HD
+    nh, nkv = (16, 2) if hd == 256 else (32, 8)
+    log(f"[bench] causal prefill 8192 tokens, {nh}q/{nkv}kv, hd {hd}{' over the int8 cache' if i8 else ''}")
+    r = prefill_workload(torch, gi_attn, dev, 8192, nh, nkv, steps, warmup, 99, i8=i8, hd=hd)
+    tf = r["flops"] / r["seconds"] / 1e12
+    line = {
+        "value": round(tf, 1), "unit": "TFLOP/s", "ms_per_step": r["seconds"] * 1e3,
+        "dtype": "int8 K/V widened to f16 MFMA, f32 acc" if i8 else "f16 MFMA, f32 acc",
+        "config": {"workload": (f"causal prefill, 8192 tokens, {nh}q/{nkv}kv, hd 256 (Qwen3.5-style heads)"
+                                if hd == 256 else "config 3: causal prefill, 8192 tokens, 32q/8kv, hd 128" +
+                                (", int8 cache" if i8 else "")), "flops_per_step": r["flops"]},
+        "roofline": prefill_roofline(gi_attn, r, steps, torch, f"pmc_prefill_{w}",
+                                     "gi_prefill_fwd_i8" if i8 else "gi_prefill_fwd_h256r" if hd == 256
+                                     else "gi_prefill_fwd"),
+    }
+    return line, r
+
+
+def run_chunked(torch, gi_attn, dev):
+    log("[bench] config 5: chunked prefill 131072 in 2048 chunks, 32q/4kv")
+    per = chunked_workload(torch, gi_attn, dev, 131072, 2048, 32, 4, 5)
+    total = sum(s for _, s, _ in per)
+    flops = sum(prefill_flops(2048, c0, 32) for c0, _, _ in per)
+    tf = flops / total / 1e12
+    return {
+        "value": round(tf, 1), "unit": "TFLOP/s", "ms_per_step": total * 1e3, "steps": len(per),
+        "dtype": "f16 MFMA, f32 acc",
+        "config": {"workload": "config 5: chunked prefill, 131072 tokens in 2048 chunks, 32q/4kv",
+                   "total_seconds": total, "total_flops": flops,
+                   "per_chunk_tflops": [round(t, 1) for _, _, t in per]},
+        # one launch per chunk, timed by events around it: the roofline is the whole prefill's flops over the
+        # sum of its launches (the chunks' own figures are in per_chunk_tflops)
+        "roofline": {"bound": "mfma", "achieved": round(tf, 1), "peak": F16_DENSE_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(tf / F16_DENSE_PEAK_TFLOPS, 4), "traffic": profile_traffic("pmc_prefill_chunked"),
+                     "kernel": "gi_prefill_fwd", "algorithmic_flops_per_launch": flops // len(per),
+                     "kernel_ms_per_launch": round(total * 1e3 / len(per), 5), "launches_timed": len(per)},
+    }
+
+
+def run_qkrope(torch, gi_attn, dev, steps, warmup):
+    log("[bench] qk_norm_rope + KV store for 8192 tokens, 32q/8kv (the cache write of config 3)")
+    r = qkrope_workload(torch, gi_attn, dev, 8192, 32, 8, steps, warmup, 7)
+    gbs = r["bytes"] / r["seconds"] / 1e9
+    ms, n_l = kernel_times(gi_attn, r["step"], steps, torch, ("qk_norm_rope",))["qk_norm_rope"]
+    kern = r["bytes"] / (ms / 1e3) / 1e9
+    return {
+        "value": round(gbs, 1), "unit": "GB/s", "ms_per_step": r["seconds"] * 1e3, "dtype": "f32 math, f16 cache",
+        "config": {"workload": "qk_norm_rope + f16 KV store, 8192 tokens, 32q/8kv, hd 128", "bytes_per_step": r["bytes"]},
+        "roofline": {"bound": "hbm", "achieved": round(kern, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(kern / HBM_PEAK_GBS, 4), "traffic": profile_traffic("pmc_qk_norm_rope_qkrope"),
+                     "kernel": "gi_qk_norm_rope",
+                     "algorithmic_bytes_per_launch": r["bytes"], "kernel_ms_per_launch": round(ms, 5),
+                     "launches_timed": n_l},
+    }
+
+
+def secondary_entry(line):
+    """The fields of a workload's line that a secondary entry keeps."""
+    keep = ("value", "unit", "ms_per_step", "dtype", "config", "roofline", "steps")
+    return {k: line[k] for k in keep if k in line}
 
 
 def main():
@@ -425,6 +567,7 @@ def main():
     result = {"metric": METRIC, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
               "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "data": "synthetic"}
     w = args.workload
+    cpu = None  # (kind of workload, workload tensors) for the CPU baseline
     if w == "peaks":
         log("[bench] peak probes: dense f16 MFMA rate, HBM read stream, device copy")
         pk = peak_probes(torch, dev)
@@ -434,128 +577,81 @@ def main():
                                     "peak": F16_DENSE_PEAK_TFLOPS, "unit": "TFLOP/s",
                                     "frac": round(pk["mfma_f16_dense_TFLOPs"] / F16_DENSE_PEAK_TFLOPS, 4),
                                     "traffic": None, "kernel": "gi_probe_mfma"}})
-    elif w in ("decode64k", "decode4k", "verify", "decode64k_i8", "verify_i8", "decode64k_h256", "verify_h256"):
-        hd = 256 if w.endswith("_h256") else HD
-        ctx, n_heads, n_kv, n_tok, cfg = {
-            "decode64k": (65536, 32, 4, 1, "config 2: decode, 1 token, ctx 65536, 32q/4kv, hd 128"),
-            "decode4k": (4096, 32, 8, 1, "config 1: decode, 1 token, ctx 4096, 32q/8kv, hd 128"),
-            "verify": (32776, 32, 4, 8, "config 4: verify, 8 tokens at a 32768-key prefix, 32q/4kv, hd 128"),
-            "decode64k_i8": (65536, 32, 4, 1, "config 2 over the int8 cache: decode, 1 token, ctx 65536, 32q/4kv"),
-            "verify_i8": (32776, 32, 4, 8, "config 4 over the int8 cache: verify, 8 tokens at 32768, 32q/4kv"),
-            "decode64k_h256": (65536, 16, 2, 1, "decode with 256-wide heads (Qwen3.5-style 16q/2kv), 1 token, "
-                                                "ctx 65536, f16 cache"),
-            "verify_h256": (32776, 16, 2, 8, "verify with 256-wide heads (Qwen3.5-style 16q/2kv), 8 tokens at a "
-                                             "32768-key prefix, f16 cache"),
-        }[w]
-        if args.n_tok and w.startswith("verify") and args.n_tok != n_tok:
-            ctx, n_tok = 32768 + args.n_tok, args.n_tok
-            cfg = f"config 4's shape with {n_tok} tokens per block" + (" over the int8 cache" if w.endswith("_i8") else "")
-        i8 = w.endswith("_i8")
-        log(f"[bench] {cfg}")
-        r = decode_workload(torch, gi_attn, dev, ctx, n_heads, n_kv, n_tok, args.steps, args.warmup, 1234, i8=i8,
-                            hd=hd)
-        gbs = r["bytes"] / r["seconds"] / 1e9
-        chunk, nsplit = gi_attn.decode_plan(ctx, n_tok, n_heads, n_kv, hd)
-        if i8:  # int8 slices are whole 256-key units (64-key tiles, 4 waves)
-            chunk = -(-chunk // 256) * 256
-            nsplit = -(-ctx // chunk)
-        kt = kernel_times(gi_attn, r["step"], args.steps, torch, ("decode_partial", "decode_combine"))
-        part_ms, part_n = kt["decode_partial"]
-        comb_ms, _ = kt["decode_combine"]
-        # algorithmic bytes of one split-kernel launch: K and V of every span key and the queries (the slice
-        # partials it writes are overhead of the split, not counted)
-        part_bytes = r["bytes"] + n_tok * n_heads * hd * 4
-        kern_gbs = part_bytes / (part_ms / 1e3) / 1e9
-        traffic = profile_traffic(f"pmc_decode_partial_{w}")
-        result.update({
-            "value": round(gbs, 1), "unit": "GB/s", "ms_per_step": r["seconds"] * 1e3,
-            "dtype": "int8 K/V + f32 scales, f32 math" if i8 else "f16 K/V, f32 math",
-            "config": {"workload": cfg, "ctx": ctx, "n_tok": n_tok, "n_heads": n_heads, "n_kv": n_kv, "hd": hd,
-                       "kv_bytes_per_step": r["bytes"], "layers_rotated": r["layers"],
-                       "slices": nsplit, "keys_per_slice": chunk, "kv_layout": f"head_major [n_kv][ctx][{hd}]"},
-            "roofline": {"bound": "hbm", "achieved": round(kern_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                         "frac": round(kern_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
-                         "kernel": decode_kernel_name(n_tok, n_heads, n_kv, hd, i8) + " (split-K pass)",
-                         "algorithmic_bytes_per_launch": part_bytes,
-                         "kernel_ms_per_launch": round(part_ms, 5), "launches_timed": part_n,
-                         "combine_ms_per_launch": round(comb_ms, 5) if comb_ms else None,
-                         "step_GBs_KV": round(gbs, 1)},
-        })
-        if args.reference_layout and not i8 and hd == HD:
-            # the same decode over caches in the reference's [position][n_kv][128] layout
-            r_ref = decode_workload(torch, gi_attn, dev, ctx, n_heads, n_kv, n_tok, args.steps, args.warmup, 1234,
-                                    layout="reference")
-            result["config"]["reference_layout_GBs"] = round(r_ref["bytes"] / r_ref["seconds"] / 1e9, 1)
-            result["config"]["reference_layout_ms_per_step"] = r_ref["seconds"] * 1e3
-            del r_ref
-        if not args.no_cpu_baseline and not i8 and hd == HD:
-            log("[bench] cpu baseline (oracle, Model::attention restatement)")
-            t_cpu, threads, reps = cpu_baseline_decode(r["q"], r["cache"], r["pos0"], n_heads, n_kv)
-            result["cpu_baseline"] = {"value": round(r["bytes"] / t_cpu / 1e9, 3), "unit": "GB/s", "cores": threads,
-                                      "kind": "port",
-                                      "sample": f"{reps} runs of the same decode (median {t_cpu * 1e3:.1f} ms/run)"}
+    elif w in DECODE_WORKLOADS:
+        line, r = run_decode(torch, gi_attn, dev, w, args.steps, args.warmup, args.n_tok, args.reference_layout)
+        result.update(line)
+        if not DECODE_WORKLOADS[w][5] and DECODE_WORKLOADS[w][4] == HD:
+            cpu = ("decode", w, r)
     elif w == "qkrope":
-        log("[bench] qk_norm_rope + KV store for 8192 tokens, 32q/8kv (the cache write of config 3)")
-        r = qkrope_workload(torch, gi_attn, dev, 8192, 32, 8, args.steps, args.warmup, 7)
-        gbs = r["bytes"] / r["seconds"] / 1e9
-        ms, n_l = kernel_times(gi_attn, r["step"], args.steps, torch, ("qk_norm_rope",))["qk_norm_rope"]
-        kern = r["bytes"] / (ms / 1e3) / 1e9
-        result.update({
-            "value": round(gbs, 1), "unit": "GB/s", "ms_per_step": r["seconds"] * 1e3, "dtype": "f32 math, f16 cache",
-            "config": {"workload": "qk_norm_rope + f16 KV store, 8192 tokens, 32q/8kv, hd 128", "bytes_per_step": r["bytes"]},
-            "roofline": {"bound": "hbm", "achieved": round(kern, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                         "frac": round(kern / HBM_PEAK_GBS, 4), "traffic": profile_traffic("pmc_qk_norm_rope_qkrope"),
-                         "kernel": "gi_qk_norm_rope",
-                         "algorithmic_bytes_per_launch": r["bytes"], "kernel_ms_per_launch": round(ms, 5),
-                         "launches_timed": n_l},
-        })
+        result.update(run_qkrope(torch, gi_attn, dev, args.steps, args.warmup))
     elif w in ("prefill8k", "prefill8k_i8", "prefill8k_h256"):
-        i8 = w == "prefill8k_i8"
-        hd = 256 if w.endswith("_h256") else HD
-        nh, nkv = (16, 2) if hd == 256 else (32, 8)
-        log(f"[bench] causal prefill 8192 tokens, {nh}q/{nkv}kv, hd {hd}{' over the int8 cache' if i8 else ''}")
-        r = prefill_workload(torch, gi_attn, dev, 8192, nh, nkv, args.steps, args.warmup, 99, i8=i8, hd=hd)
-        tf = r["flops"] / r["seconds"] / 1e12
-        result.update({
-            "value": round(tf, 1), "unit": "TFLOP/s", "ms_per_step": r["seconds"] * 1e3,
-            "dtype": "int8 K/V widened to f16 MFMA, f32 acc" if i8 else "f16 MFMA, f32 acc",
-            "config": {"workload": (f"causal prefill, 8192 tokens, {nh}q/{nkv}kv, hd 256 (Qwen3.5-style heads)"
-                                    if hd == 256 else "config 3: causal prefill, 8192 tokens, 32q/8kv, hd 128" +
-                                    (", int8 cache" if i8 else "")), "flops_per_step": r["flops"]},
-            "roofline": prefill_roofline(gi_attn, r, args.steps, torch, f"pmc_prefill_{w}",
-                                         "gi_prefill_fwd_i8" if i8 else "gi_prefill_fwd_h256r" if hd == 256
-                                         else "gi_prefill_fwd"),
-        })
-        if not args.no_cpu_baseline and not i8 and hd == HD:
-            log("[bench] cpu baseline (oracle, Model::attention restatement) on the last 64 query rows")
-            tf_cpu, threads, reps, fl, t_cpu = cpu_baseline_prefill(r["q"], r["k"], r["v"], nh, nkv)
-            result["cpu_baseline"] = {"value": round(tf_cpu, 4), "unit": "TFLOP/s", "cores": threads, "kind": "port",
-                                      "sample": f"the last 64 of the 8192 query rows, all heads ({fl / 1e9:.1f} "
-                                                f"GFLOP), {reps} runs (median {t_cpu * 1e3:.1f} ms/run)"}
+        line, r = run_prefill(torch, gi_attn, dev, w, args.steps, args.warmup)
+        result.update(line)
+        if w == "prefill8k":
+            cpu = ("prefill", w, r)
     else:
-        log("[bench] config 5: chunked prefill 131072 in 2048 chunks, 32q/4kv")
-        per = chunked_workload(torch, gi_attn, dev, 131072, 2048, 32, 4, 5)
-        total = sum(s for _, s, _ in per)
-        flops = sum(prefill_flops(2048, c0, 32) for c0, _, _ in per)
-        tf = flops / total / 1e12
-        result.update({
-            "value": round(tf, 1), "unit": "TFLOP/s", "ms_per_step": total * 1e3, "dtype": "f16 MFMA, f32 acc",
-            "config": {"workload": "config 5: chunked prefill, 131072 tokens in 2048 chunks, 32q/4kv",
-                       "total_seconds": total,
-                       "per_chunk_tflops": [round(t, 1) for _, _, t in per]},
-            "roofline": {"bound": "mfma", "achieved": round(tf, 1), "peak": F16_DENSE_PEAK_TFLOPS, "unit": "TFLOP/s",
-                         "frac": round(tf / F16_DENSE_PEAK_TFLOPS, 4), "traffic": None},
-        })
-        result["steps"] = len(per)
+        result.update(run_chunked(torch, gi_attn, dev))
+
+    sec_r = {}
     if w == "decode64k" and not args.no_secondary:
-        r = prefill_workload(torch, gi_attn, dev, 8192, 32, 8, 30, 10, 99)
-        tf = r["flops"] / r["seconds"] / 1e12
-        result["secondary"] = {"prefill8k": {"value": round(tf, 1), "unit": "TFLOP/s",
-                                             "ms_per_step": r["seconds"] * 1e3,
-                                             "frac_of_f16_dense_peak": round(tf / F16_DENSE_PEAK_TFLOPS, 4),
-                                             "roofline": prefill_roofline(gi_attn, r, 30, torch)},
-                               "hbm_copy_measured_GBs": round(hbm_copy_gbs(torch, dev), 1),
-                               "peaks_measured": peak_probes(torch, dev)}
+        # every other config of the benchmark on the same line, each with its own roofline
+        sec = {}
+        steps2, warm2 = max(20, args.steps // 4), max(5, args.warmup // 2)
+        for w2 in ("decode4k", "verify"):
+            line, r2 = run_decode(torch, gi_attn, dev, w2, steps2, warm2)
+            sec[w2] = secondary_entry(line)
+            if w2 == "decode4k":
+                sec_r["decode4k"] = r2
+            del r2
+        line, r2 = run_prefill(torch, gi_attn, dev, "prefill8k", 30, 10)
+        sec["prefill8k"] = secondary_entry(line)
+        sec_r["prefill8k"] = r2
+        sec["chunked"] = secondary_entry(run_chunked(torch, gi_attn, dev))
+        sec["hbm_copy_measured_GBs"] = round(hbm_copy_gbs(torch, dev), 1)
+        sec["peaks_measured"] = peak_probes(torch, dev)
+        result["secondary"] = sec
+
+    if cpu and not args.no_cpu_baseline:
+        # the reference's CPU attention (the oracle's restatement of Model::attention, f32 cache) on this
+        # host, at all of its CPU share and at logical/2 (the reference's default thread count)
+        n_all, n_half, logical, model = cpu_threads()
+        kind, cw, r = cpu
+        ctx, nh, nkv = (DECODE_WORKLOADS[cw][:3] if kind == "decode" else (8192, 32, 8))
+        log(f"[bench] cpu baseline (oracle, Model::attention restatement, f32 cache) on {n_all} and {n_half} threads")
+        runs = []
+
+        def decode_runs(label, rr, nh_, nkv_):
+            for th in (n_all, n_half):
+                t_cpu, reps = cpu_baseline_decode(rr["q"], rr["cache"], rr["pos0"], nh_, nkv_, th)
+                runs.append({"config": label, "threads": th, "value": round(rr["bytes"] / t_cpu / 1e9, 3),
+                             "unit": "GB/s (K+V bytes of the f16 cache)",
+                             "sample": f"{reps} runs of the whole decode (median {t_cpu * 1e3:.2f} ms/run)"})
+
+        def prefill_runs(rr):
+            for th in (n_all, n_half):
+                tf_cpu, reps, fl, t_cpu = cpu_baseline_prefill(rr["q"], rr["k"], rr["v"], 32, 8, th)
+                runs.append({"config": "prefill8k", "threads": th, "value": round(tf_cpu, 4), "unit": "TFLOP/s",
+                             "sample": f"the last 64 of the 8192 query rows, all heads ({fl / 1e9:.1f} GFLOP), "
+                                       f"{reps} runs (median {t_cpu * 1e3:.1f} ms/run)"})
+
+        if kind == "decode":
+            decode_runs(cw, r, nh, nkv)
+        else:
+            prefill_runs(r)
+        if "decode4k" in sec_r:  # config 1 is the reference's own CPU config
+            decode_runs("decode4k", sec_r["decode4k"], 32, 8)
+        if "prefill8k" in sec_r:
+            prefill_runs(sec_r["prefill8k"])
+        head_run = runs[0]
+        result["cpu_baseline"] = {
+            "value": head_run["value"], "unit": head_run["unit"].split(" ")[0], "cores": head_run["threads"],
+            "kind": "port",
+            "sample": f"{head_run['config']}: {head_run['sample']}; the oracle's C++ restatement of Model::attention "
+                      f"(src/model.rs:1320-1409) over the same inputs with the cache widened to f32",
+            "cpu_model": model, "logical_cpus": logical,
+            "threads_note": f"all = this process's CPUs capped at 16 (the host share of one GPU), half = the "
+                            f"reference's default logical/2",
+            "runs": runs}
     print(json.dumps(result), flush=True)
 
 
