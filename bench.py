@@ -1,7 +1,8 @@
 """Benchmark of the gfx950 attention hot path on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload decode64k|decode4k|verify|prefill8k|chunked|qkrope|
-                    decode64k_i8|verify_i8|prefill8k_i8|decode64k_h256|prefill8k_h256]
+                    decode64k_i8|verify_i8|prefill8k_i8|decode64k_h256|verify_h256|prefill8k_h256|
+                    decode64k_h256_i8|verify_h256_i8]
                     [--no-cpu-baseline] [--no-secondary] [--reference-layout]
 
 A step is one pass of the hot path over one batch of synthetic seeded input already resident in HBM:
@@ -12,8 +13,11 @@ A step is one pass of the hot path over one batch of synthetic seeded input alre
   prefill8k  config 3: causal prefill of 8192 tokens, 32 / 8 heads, f16 in and out (MFMA TFLOP/s)
   chunked    config 5: 131072 tokens in 2048-token chunks against the growing cache, 32 / 4 heads
   qkrope     the cache write before attention (qk_norm_rope + f16 KV store) for config 3's 8192 tokens
-  decode64k_h256, prefill8k_h256
-             head size 256 (Qwen3.5-style 16 query / 2 kv heads): decode at 65536 keys, prefill of 8192
+  decode64k_h256, verify_h256, prefill8k_h256
+             head size 256 (Qwen3.5-style 16 query / 2 kv heads): decode at 65536 keys, an 8-token verify at
+             32768, prefill of 8192
+  decode64k_h256_i8, verify_h256_i8
+             head size 256 over the int8 cache (the reference's attention_decode_tc256 shapes)
   decode64k_i8, verify_i8, prefill8k_i8
              configs 2, 4 and 3 over the int8 cache (the reference's KV8 format: int8 rows, an f32 scale per
              position and kv head); bytes are the int8 rows plus their scales
@@ -100,7 +104,7 @@ def decode_kernel_name(n_tok, n_heads, n_kv, hd, i8):
     if pairs <= p:
         name = "gi_decode_partial_1"
     elif hd == 256:
-        return "gi_decode_pm_shared_1_h256"
+        name = "gi_decode_pm_shared_1"
     else:
         name = "gi_decode_pm_2" if pairs > 2 * p else "gi_decode_pm_1"
     return name + ("_i8" if i8 else "") + ("_h256" if hd == 256 else "")
@@ -426,6 +430,10 @@ DECODE_WORKLOADS = {
                                                     "ctx 65536, f16 cache"),
     "verify_h256": (32776, 16, 2, 8, 256, False, "verify with 256-wide heads (Qwen3.5-style 16q/2kv), 8 tokens at a "
                                                  "32768-key prefix, f16 cache"),
+    "decode64k_h256_i8": (65536, 16, 2, 1, 256, True, "decode with 256-wide heads over the int8 cache (Qwen3.5/3.6-style "
+                                                      "16q/2kv, the reference's attention_decode_tc256), 1 token, ctx 65536"),
+    "verify_h256_i8": (32776, 16, 2, 8, 256, True, "verify with 256-wide heads over the int8 cache, 8 tokens at a "
+                                                   "32768-key prefix, 16q/2kv"),
 }
 
 
@@ -439,7 +447,7 @@ def run_decode(torch, gi_attn, dev, w, steps, warmup, n_tok_override=None, refer
     r = decode_workload(torch, gi_attn, dev, ctx, n_heads, n_kv, n_tok, steps, warmup, 1234, i8=i8, hd=hd)
     gbs = r["bytes"] / r["seconds"] / 1e9
     chunk, nsplit = gi_attn.decode_plan(ctx, n_tok, n_heads, n_kv, hd)
-    if i8:  # int8 slices are whole 256-key units (64-key tiles, 4 waves)
+    if i8 and hd == HD:  # int8 slices at head size 128 are whole 256-key units (64-key tiles, 4 waves)
         chunk = -(-chunk // 256) * 256
         nsplit = -(-ctx // chunk)
     kt = kernel_times(gi_attn, r["step"], steps, torch, ("decode_partial", "decode_combine"))
@@ -543,8 +551,7 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="decode64k",
-                    choices=["decode64k", "decode4k", "verify", "prefill8k", "chunked", "qkrope", "decode64k_i8",
-                             "verify_i8", "prefill8k_i8", "decode64k_h256", "verify_h256", "prefill8k_h256",
+                    choices=[*DECODE_WORKLOADS, "prefill8k", "chunked", "qkrope", "prefill8k_i8", "prefill8k_h256",
                              "peaks"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-secondary", action="store_true")

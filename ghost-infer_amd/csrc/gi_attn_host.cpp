@@ -154,9 +154,9 @@ struct Module {
     bool loaded = false;
     hipModule_t mod = nullptr;
     hipFunction_t dec[2] = {};        // up to 8 pairs, head size 128: [int8 cache]
-    hipFunction_t dec256 = {};        // up to 8 pairs, head size 256 (f16 cache)
+    hipFunction_t dec256[2] = {};     // up to 8 pairs, head size 256: [int8 cache]
     hipFunction_t dec_pm[2][2] = {};  // [int8 cache][column blocks - 1]: one pair per column
-    hipFunction_t dec_pm256 = {};     // head size 256, one pair per column, 4 waves sharing each tile
+    hipFunction_t dec_pm256[2] = {};  // head size 256, one pair per column, 4 waves sharing each tile: [int8 cache]
     hipFunction_t prefill[2] = {};   // [int8 cache], head size 128
     hipFunction_t prefill256r = nullptr; // head size 256 (f16 cache), 16 rows per wave: one workgroup per query tile
     hipFunction_t combine = nullptr, rope = nullptr, relayout = nullptr;
@@ -195,12 +195,14 @@ int load_module(const char* path, Module** out) {
         struct { hipFunction_t* f; const char* name; } fns[] = {
             {&m.dec[0], "gi_decode_partial_1"},
             {&m.dec[1], "gi_decode_partial_1_i8"},
-            {&m.dec256, "gi_decode_partial_1_h256"},
+            {&m.dec256[0], "gi_decode_partial_1_h256"},
+            {&m.dec256[1], "gi_decode_partial_1_i8_h256"},
             {&m.dec_pm[0][0], "gi_decode_pm_1"},
             {&m.dec_pm[0][1], "gi_decode_pm_2"},
             {&m.dec_pm[1][0], "gi_decode_pm_1_i8"},
             {&m.dec_pm[1][1], "gi_decode_pm_2_i8"},
-            {&m.dec_pm256, "gi_decode_pm_shared_1_h256"},
+            {&m.dec_pm256[0], "gi_decode_pm_shared_1_h256"},
+            {&m.dec_pm256[1], "gi_decode_pm_shared_1_i8_h256"},
             {&m.combine, "gi_decode_combine"},
             {&m.relayout, "gi_kv_relayout"},
             {&m.prefill[0], "gi_prefill_fwd"},
@@ -368,7 +370,7 @@ int decode_impl(void* stream, const float* q, long long q_stride, const void* kc
                 const float* vs, long long sc_stride, long long sc_head_stride, bool i8, long long kv_stride,
                 long long kv_head_stride, float* out, long long out_stride, void* workspace, size_t workspace_bytes,
                 int pos0, const int* posp, int ctx_cap, int n_tok, int n_heads, int n_kv, int hd, float scale) {
-    if (int e = check_shape(n_heads, n_kv, hd, !i8)) return e;
+    if (int e = check_shape(n_heads, n_kv, hd, true)) return e;
     if (n_tok <= 0) return fail("n_tok %d must be positive", n_tok);
     if (!q || !kc || !vc || !out) return fail("null tensor pointer");
     if (kv_head_stride == 0) kv_head_stride = hd;
@@ -415,7 +417,7 @@ int decode_impl(void* stream, const float* q, long long q_stride, const void* kc
         a.sc_head_stride = sc_head_stride;
     }
     hipStream_t st = (hipStream_t)stream;
-    hipFunction_t f = hd == 256 ? (var.pm ? m->dec_pm256 : m->dec256) : var.pm ? m->dec_pm[i8][var.ncb - 1] : m->dec[i8];
+    hipFunction_t f = hd == 256 ? (var.pm ? m->dec_pm256[i8] : m->dec256[i8]) : var.pm ? m->dec_pm[i8][var.ncb - 1] : m->dec[i8];
     if (int e = launch(kDecodePartial, f, dim3(a.nsplit, n_kv, var.groups), dim3(256), st, &a, sizeof a)) return e;
     if (a.nsplit == 1) return 0;
     return launch(kDecodeCombine, m->combine, dim3(n_heads, n_tok, kCombineSplit * hd / 128), dim3(64), st, &a, sizeof a);
@@ -637,7 +639,7 @@ namespace {
 int attention_impl(void* stream, const float* qkv, const void* kc, const void* vc, const float* ks, const float* vs,
                    bool i8, float* out, void* workspace, size_t workspace_bytes, int pos0, const int* posp, int ctx_cap,
                    int n, int n_heads, int n_kv, int hd, int exact) {
-    if (int e = check_shape(n_heads, n_kv, hd, !i8)) return e;
+    if (int e = check_shape(n_heads, n_kv, hd, true)) return e;
     if (n <= 0) return fail("n %d must be positive", n);
     const long long q_dim = (long long)n_heads * hd, kv_dim = (long long)n_kv * hd, row = q_dim + 2 * kv_dim;
     const float scale = 1.0f / std::sqrt((float)hd);

@@ -145,35 +145,21 @@ __device__ __forceinline__ float gi_load4f(__amdgpu_buffer_rsrc_t r, int off) {
     return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
 }
 
-#ifndef GI_I8_SDWA // int8 -> f16 by sub-dword converts (1) or by byte permutes (0)
-#define GI_I8_SDWA 1
-#endif
-// int8 -> f16, exactly, two bytes of x (bytes 0-1 for GI_I8_LO, 2-3 for GI_I8_HI) into one f16 pair.
-// GI_I8_SDWA: v_cvt_f16_i16 reads one byte, sign-extended, through its sub-dword operand select and writes
-// one half of the result (the second keeps the first's half): one instruction per value, on the raw bytes.
-// Else: with its sign bit flipped a byte is u = v + 128 in 0..255; the f16 with bits 0x6400 | u is
-// 1024 + u, so subtracting 1152 leaves v. x then holds 4 bytes already flipped (gi_i8_in), and v_perm picks
-// bytes of {0x64646464 : x} (selector bytes 0-3 take x, 4-7 the constant).
+// int8 -> f16, exactly, two bytes of x (bytes 0-1 for GI_I8_LO, 2-3 for GI_I8_HI) into one f16 pair. With its
+// sign bit flipped a byte is u = v + 128 in 0..255; the f16 with bits 0x6400 | u is 1024 + u, so subtracting
+// 1152 leaves v. x holds 4 bytes already flipped (gi_i8_in), and v_perm picks bytes of {0x64646464 : x}
+// (selector bytes 0-3 take x, 4-7 the constant): one v_perm and one packed f16 subtract per two values. Every
+// instruction is visible to the compiler, which must see the writes that feed an MFMA operand to keep the
+// required wait states (a conversion by inline asm right before an MFMA reading its result was measured to
+// lose values).
 typedef _Float16 h2x __attribute__((ext_vector_type(2)));
 #define GI_I8_LO 0x04010400u // bytes 0, 1 of x -> f16 pair
 #define GI_I8_HI 0x04030402u // bytes 2, 3
-__device__ __forceinline__ uint32_t gi_i8_in(uint32_t x) { return GI_I8_SDWA ? x : x ^ 0x80808080u; }
+__device__ __forceinline__ uint32_t gi_i8_in(uint32_t x) { return x ^ 0x80808080u; }
 __device__ __forceinline__ uint32_t i8_f16x2(uint32_t x, uint32_t sel) {
-#if GI_I8_SDWA
-    uint32_t r;
-    if (sel == GI_I8_LO) {
-        asm("v_cvt_f16_i16_sdwa %0, sext(%1) dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:BYTE_0" : "=v"(r) : "v"(x));
-        asm("v_cvt_f16_i16_sdwa %0, sext(%1) dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:BYTE_1" : "+v"(r) : "v"(x));
-    } else {
-        asm("v_cvt_f16_i16_sdwa %0, sext(%1) dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:BYTE_2" : "=v"(r) : "v"(x));
-        asm("v_cvt_f16_i16_sdwa %0, sext(%1) dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:BYTE_3" : "+v"(r) : "v"(x));
-    }
-    return r;
-#else
     const h2x v = __builtin_bit_cast(h2x, __builtin_amdgcn_perm(0x64646464u, x, sel)) -
                   h2x{(_Float16)1152.f, (_Float16)1152.f};
     return __builtin_bit_cast(uint32_t, v);
-#endif
 }
 // v of lane 16*(l/16) + m: the lane's 16-lane row broadcasts its m-th lane (DPP row_newbcast)
 template <int M>
@@ -188,6 +174,9 @@ template <bool I8, int HD> struct DecBuf { u4 k[2][4]; u4 v[8]; };
 template <> struct DecBuf<true, 128> { u4 k[4][2]; u2 v[16]; float ksc, vsc; };
 // head size 256 (f16): 16 keys; K row c of the tile, 8 k-steps of 32 dims; V keys 4grp..4grp+3, dims 16c..16c+15
 template <> struct DecBuf<false, 256> { u4 k[8]; u4 v[4][2]; };
+// head size 256 over the int8 cache: 16 keys; K row c, bytes 64i + 16grp .. +15 (k-steps 2i, 2i + 1); V keys
+// 4grp..4grp+3, bytes 16c..16c+15; the scales of tile key 4(lane/16) + lane%4
+template <> struct DecBuf<true, 256> { u4 k[4]; u4 v[4]; float ksc, vsc; };
 
 // Lane l of a wave: c = l % 16 (MFMA column / A-row), grp = l / 16 (k-group of 8).
 // I8 = true: an int8 cache (kv_store's KV8 format, src/cuda.rs:333-339: a row of int8 values and one f32
@@ -214,8 +203,9 @@ template <> struct DecBuf<false, 256> { u4 k[8]; u4 v[4][2]; };
 // served by the caches).
 template <int NCB, bool SHARE, bool I8, int HD = 128, bool PM = false>
 __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
-    static_assert(HD == 128 || (HD == 256 && !I8), "head sizes: 128 (f16, int8), 256 (f16)");
-    static_assert(!PM || !I8 || HD == 128, "one pair per column: head size 128, or 256 with the f16 cache");
+    static_assert(HD == 128 || HD == 256, "head sizes: 128, 256");
+    // tiles in flight per wave: an int8 tile at head size 256 holds half the bytes of the others
+    constexpr int NB = I8 && HD == 256 ? 2 * DEC_NB : DEC_NB;
     constexpr int CPAIRS = PM ? 2 * DEC_PAIRS : DEC_PAIRS; // pairs per column block
     constexpr int TILE = HD == 256 ? DEC_TILE / 2 : I8 ? 2 * DEC_TILE : DEC_TILE; // keys per wave tile
     constexpr int KK = HD / 32;                 // QK k-steps
@@ -326,6 +316,11 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
     // head size 256: K row c, dims 8grp + 32kk; V keys 4grp + i, dims 16c..16c+15
     const int koff256 = (c * (int)kvs + 8 * grp) * 2;
     const int voff256 = (4 * grp * (int)kvs + 16 * c) * 2;
+    // head size 256, int8 (byte offsets): K row c, bytes 16grp (+64i); V rows 4grp + i, bytes 16c; the scales of
+    // tile key 4(lane/16) + lane%4
+    const int koff256_8 = c * (int)kvs + 16 * grp;
+    const int voff256_8 = 4 * grp * (int)kvs + 16 * c;
+    const int scoff256 = (4 * (lane >> 4) + (lane & 3)) * (int)scs * 4;
 
     using Buf = DecBuf<I8, HD>;
     // K/V stream loads: each tile is read by one wave only, unless SHARE (every wave of the workgroup reads
@@ -333,7 +328,12 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
     // it takes the split kernel from 25.5 to 22.7 us; with SHARE it costs 30%.
     constexpr int CPOL = SHARE ? 0 : DEC_CPOL;
     auto load_k = [&](Buf& B, int t) {
-        if constexpr (HD == 256) {
+        if constexpr (HD == 256 && I8) {
+            __amdgpu_buffer_rsrc_t r = gi_rsrc(kslice8 + (long long)t * kvs, (long long)(nkeys - t) * kvs);
+#pragma unroll
+            for (int i = 0; i < 4; i++) B.k[i] = gi_load16p<CPOL>(r, koff256_8 + 64 * i);
+            B.ksc = gi_load4f(gi_rsrc(kscl + (long long)t * scs, (long long)(nkeys - t) * scs * 4), scoff256);
+        } else if constexpr (HD == 256) {
             __amdgpu_buffer_rsrc_t r = gi_rsrc(kslice + (long long)t * kvs, (long long)(nkeys - t) * kvs * 2);
 #pragma unroll
             for (int kk = 0; kk < 8; kk++) B.k[kk] = gi_load16p<CPOL>(r, koff256 + 64 * kk);
@@ -355,7 +355,12 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
         }
     };
     auto load_v = [&](Buf& B, int t) {
-        if constexpr (HD == 256) {
+        if constexpr (HD == 256 && I8) {
+            __amdgpu_buffer_rsrc_t r = gi_rsrc(vslice8 + (long long)t * kvs, (long long)(nkeys - t) * kvs);
+#pragma unroll
+            for (int i = 0; i < 4; i++) B.v[i] = gi_load16p<CPOL>(r, voff256_8 + i * (int)kvs);
+            B.vsc = gi_load4f(gi_rsrc(vscl + (long long)t * scs, (long long)(nkeys - t) * scs * 4), scoff256);
+        } else if constexpr (HD == 256) {
             __amdgpu_buffer_rsrc_t r = gi_rsrc(vslice + (long long)t * kvs, (long long)(nkeys - t) * kvs * 2);
 #pragma unroll
             for (int i = 0; i < 4; i++) {
@@ -391,7 +396,7 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
                                                                              qfl[cb][kk], sacc[cb][b], 0, 0, 0);
                 }
             }
-        if (reload) load_k(B, t + DEC_NB * STRIDE);
+        if (reload) load_k(B, t + NB * STRIDE);
         __builtin_amdgcn_sched_barrier(0);
         const bool masked = t + DEC_TILE > span_lo; // some valid column sees only part of this tile
         h8 pf[NCB], pfl[NCB];
@@ -459,7 +464,7 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
             }
         }
         __builtin_amdgcn_sched_barrier(0);
-        if (reload) load_v(B, t + DEC_NB * STRIDE);
+        if (reload) load_v(B, t + NB * STRIDE);
     };
     auto process_i8 = [&](auto& B, int t, bool reload) {
         __builtin_amdgcn_sched_barrier(0);
@@ -489,7 +494,7 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
             }
         }
         const float ksc = B.ksc;
-        if (reload) load_k(B, t + DEC_NB * STRIDE);
+        if (reload) load_k(B, t + NB * STRIDE);
         __builtin_amdgcn_sched_barrier(0);
         // the scales of this lane's 16 keys (16grp + m, m = 4b + j)
         float ksb[16], vsb[16];
@@ -576,22 +581,38 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
             }
         }
         __builtin_amdgcn_sched_barrier(0);
-        if (reload) load_v(B, t + DEC_NB * STRIDE);
+        if (reload) load_v(B, t + NB * STRIDE);
     };
     auto process_256 = [&](auto& B, int t, bool reload) {
         __builtin_amdgcn_sched_barrier(0);
+        // K fragment of k-step kk (int8: the lane's 8 bytes of dims 64(kk/2) + 16grp + 8(kk%2), widened)
+        auto kfrag = [&](int kk) -> h8 {
+            if constexpr (I8) {
+                const uint32_t x0 = gi_i8_in(B.k[kk >> 1][2 * (kk & 1)]), x1 = gi_i8_in(B.k[kk >> 1][2 * (kk & 1) + 1]);
+                return __builtin_bit_cast(h8, u4{i8_f16x2(x0, GI_I8_LO), i8_f16x2(x0, GI_I8_HI), i8_f16x2(x1, GI_I8_LO),
+                                                 i8_f16x2(x1, GI_I8_HI)});
+            } else {
+                return __builtin_bit_cast(h8, B.k[kk]);
+            }
+        };
         f4 sacc[NCB];
 #pragma unroll
-        for (int cb = 0; cb < NCB; cb++) {
-            sacc[cb] = f4{0.f, 0.f, 0.f, 0.f};
+        for (int cb = 0; cb < NCB; cb++) sacc[cb] = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int kk = 0; kk < 8; kk++) {
-                sacc[cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, B.k[kk]), qf[cb][kk], sacc[cb], 0, 0, 0);
-                if constexpr (PM)
-                    sacc[cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, B.k[kk]), qfl[cb][kk], sacc[cb], 0, 0, 0);
+        for (int kk = 0; kk < 8; kk++) {
+            const h8 kf = kfrag(kk);
+#pragma unroll
+            for (int cb = 0; cb < NCB; cb++) {
+                sacc[cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[cb][kk], sacc[cb], 0, 0, 0);
+                if constexpr (PM) sacc[cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qfl[cb][kk], sacc[cb], 0, 0, 0);
             }
         }
-        if (reload) load_k(B, t + DEC_NB * STRIDE);
+        float ksb[4], vsb[4]; // int8: the scales of keys 4grp + j
+        if constexpr (I8) {
+            ksb[0] = row_bcast<0>(B.ksc), ksb[1] = row_bcast<1>(B.ksc), ksb[2] = row_bcast<2>(B.ksc), ksb[3] = row_bcast<3>(B.ksc);
+            vsb[0] = row_bcast<0>(B.vsc), vsb[1] = row_bcast<1>(B.vsc), vsb[2] = row_bcast<2>(B.vsc), vsb[3] = row_bcast<3>(B.vsc);
+        }
+        if (reload) load_k(B, t + NB * STRIDE);
         __builtin_amdgcn_sched_barrier(0);
         const bool masked = t + TILE > span_lo;
         h4x pf[NCB], pfl[NCB]; // PV B operand: keys 4grp + j of column c (PM: high parts and remainders)
@@ -602,6 +623,7 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
             for (int j = 0; j < 4; j++) {
                 float v = sacc[cb][j];
                 if constexpr (!PM) v = v + lane_xor1(v); // hi + lo columns of the pair
+                if constexpr (I8) v *= ksb[j];           // the key's scale
                 if (masked) v = t + 4 * grp + j < span[cb] ? v : GI_NEG_INF;
                 sc[j] = v;
                 mx = fmaxf(mx, v);
@@ -622,25 +644,46 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
             for (int j = 0; j < 4; j++) {
                 const float p = __builtin_amdgcn_exp2f(sc[j] - m_use);
                 psum += p;
-                _Float16 hi = (_Float16)p;
+                // int8: P V takes p times the value's scale (biased like the head-128 int8 kernel)
+                const float pv = I8 ? p * vsb[j] * (PM ? DEC_I8_VB : 1.f) : p;
+                _Float16 hi = (_Float16)pv;
                 if constexpr (PM) {
                     pf[cb][j] = hi;
-                    pfl[cb][j] = (_Float16)(p - (float)hi);
+                    pfl[cb][j] = (_Float16)(pv - (float)hi);
                 } else {
-                    pf[cb][j] = (c & 1) ? (_Float16)(p - (float)hi) : hi;
+                    pf[cb][j] = (c & 1) ? (_Float16)((pv - (float)hi) * (I8 ? DEC_I8_LO : 1.f)) : hi;
                 }
             }
             l_run[cb] += psum;
         }
-        // V^T block dd: element i of the A operand = V[key 4grp + i][dim 16c + dd]
+        // V^T block dd: element i of the A operand = V[key 4grp + i][dim 16c + dd]. int8: for dims dd, dd + 1
+        // and keys 2p, 2p + 1 one v_perm gathers the four bytes and two converts widen them to f16 pairs
+        u2 v8[16];
+        if constexpr (I8) {
+#pragma unroll
+            for (int dd = 0; dd < 16; dd += 2) {
+                const int wi = dd >> 2, k = dd & 3;
+                const uint32_t sel = (uint32_t)k | (uint32_t)(k + 4) << 8 | (uint32_t)(k + 1) << 16 | (uint32_t)(k + 5) << 24;
+#pragma unroll
+                for (int p = 0; p < 2; p++) {
+                    const uint32_t g = __builtin_amdgcn_perm(gi_i8_in(B.v[2 * p + 1][wi]), gi_i8_in(B.v[2 * p][wi]), sel);
+                    v8[dd][p] = i8_f16x2(g, GI_I8_LO);
+                    v8[dd + 1][p] = i8_f16x2(g, GI_I8_HI);
+                }
+            }
+        }
 #pragma unroll
         for (int dd = 0; dd < 16; dd++) {
-            const int h = dd >> 3, w = (dd & 7) >> 1;
             u2 vw;
+            if constexpr (I8) {
+                vw = v8[dd];
+            } else {
+                const int h = dd >> 3, w = (dd & 7) >> 1;
 #pragma unroll
-            for (int p = 0; p < 2; p++) {
-                const uint32_t lo = B.v[2 * p][h][w], hi = B.v[2 * p + 1][h][w];
-                vw[p] = (dd & 1) ? ((lo >> 16) | (hi & 0xffff0000u)) : ((lo & 0xffffu) | (hi << 16));
+                for (int p = 0; p < 2; p++) {
+                    const uint32_t lo = B.v[2 * p][h][w], hi = B.v[2 * p + 1][h][w];
+                    vw[p] = (dd & 1) ? ((lo >> 16) | (hi & 0xffff0000u)) : ((lo & 0xffffu) | (hi << 16));
+                }
             }
             const h4x vt = __builtin_bit_cast(h4x, vw);
 #pragma unroll
@@ -650,7 +693,7 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
             }
         }
         __builtin_amdgcn_sched_barrier(0);
-        if (reload) load_v(B, t + DEC_NB * STRIDE);
+        if (reload) load_v(B, t + NB * STRIDE);
     };
     auto process = [&](Buf& B, int t, bool reload) {
         if constexpr (HD == 256) process_256(B, t, reload);
@@ -662,10 +705,10 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
     // loads outstanding and the compiler's load counters wait for exactly the buffer in use)
     // a SHARE wave whose pairs all lie past the last one has nothing to compute (it still joins the merge)
     if (!SHARE || pair0 < npairs) {
-    Buf B[DEC_NB];
+    Buf B[NB];
     const int t_first = SHARE ? 0 : wave * TILE;
 #pragma unroll
-    for (int i = 0; i < DEC_NB; i++) {
+    for (int i = 0; i < NB; i++) {
         load_k(B[i], t_first + i * STRIDE);
         __builtin_amdgcn_sched_barrier(0);
         load_v(B[i], t_first + i * STRIDE);
@@ -693,12 +736,12 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
     // Steady state: every buffer gets a further tile (those past the slice read zeros and are never
     // processed). The last round of tiles runs without reloads, so no load is left in flight at the end.
     int t = t_first;
-    for (; t + DEC_NB * STRIDE < nkeys; t += DEC_NB * STRIDE) {
+    for (; t + NB * STRIDE < nkeys; t += NB * STRIDE) {
 #pragma unroll
-        for (int i = 0; i < DEC_NB; i++) process(B[i], t + i * STRIDE, true);
+        for (int i = 0; i < NB; i++) process(B[i], t + i * STRIDE, true);
     }
 #pragma unroll
-    for (int i = 0; i < DEC_NB; i++)
+    for (int i = 0; i < NB; i++)
         if (t + i * STRIDE < nkeys) process(B[i], t + i * STRIDE, false);
     }
 
@@ -786,9 +829,11 @@ GI_DEC_PM_KERNEL(gi_decode_pm_1, 1, false, false)
 GI_DEC_PM_KERNEL(gi_decode_pm_2, 2, false, false)
 GI_DEC_PM_KERNEL(gi_decode_pm_1_i8, 1, false, true)
 GI_DEC_PM_KERNEL(gi_decode_pm_2_i8, 2, false, true)
-#define GI_DEC_PM256_KERNEL(name, NCB, SHARE) \
-    extern "C" __global__ void __launch_bounds__(256, DEC_MINWG) name(GiDecodeArgs a) { gi_decode_partial_t<NCB, SHARE, false, 256, true>(a); }
-GI_DEC_PM256_KERNEL(gi_decode_pm_shared_1_h256, 1, true)
+GI_DEC_KERNEL(gi_decode_partial_1_i8_h256, 1, false, true, 256)
+#define GI_DEC_PM256_KERNEL(name, NCB, SHARE, I8) \
+    extern "C" __global__ void __launch_bounds__(256, DEC_MINWG) name(GiDecodeArgs a) { gi_decode_partial_t<NCB, SHARE, I8, 256, true>(a); }
+GI_DEC_PM256_KERNEL(gi_decode_pm_shared_1_h256, 1, true, false)
+GI_DEC_PM256_KERNEL(gi_decode_pm_shared_1_i8_h256, 1, true, true)
 
 // Merge the slices of each (token, head): M = max m_s, w_s = 2^(m_s - M), out = sum w_s O_s / sum w_s l_s
 // (attention_combine's maths in base 2; empty slices carry m = -inf and weigh nothing). One wave per
@@ -907,7 +952,9 @@ __device__ __forceinline__ void gi_stage16(const void* base, long long bytes, GI
 #if GI_DMA_ASM
     const u4 rs = gi_rsrc_words(base, bytes);
     const uint32_t m0 = (uint32_t)(uintptr_t)dst;
-    asm volatile("buffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voff), "s"(rs), "{m0}"(m0) : "memory");
+    // (s_nop 0: the one wait state an M0 write needs before an LDS-DMA load reads it; the compiler cannot see
+    // the load inside the asm, so it would not insert it)
+    asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voff), "s"(rs), "{m0}"(m0) : "memory");
 #else
     __builtin_amdgcn_raw_ptr_buffer_load_lds(gi_rsrc(base, bytes), dst, 16, voff, 0, 0, 0);
 #endif

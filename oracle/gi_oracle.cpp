@@ -23,6 +23,9 @@
 //                                     integer keys, score times key scale, P V with f16(p * vs * 2^10))
 //   gio_decode_gpu_i8                 gio_decode_gpu over the KV8 cache (src/cuda.rs:209-226, 1758-1760,
 //                                     1821-1827: key scale on the score, value scale on the weight)
+//   gio_decode_tc256_i8               src/cuda.rs:2625-2802 (attention_decode_tc256 over the KV8 cache: head
+//                                     size 256, f16 Q, P = f16(p * vscale * 2^10), l of the unrounded p) + the
+//                                     attention_combine merge
 //
 // How each is pinned (tests/test_oracle.py): the f16 conversion exhaustively against numpy's float16
 // and against src/quant.rs:1160-1169's known values; the attention functions against an independent
@@ -277,6 +280,9 @@ float block_sum128(const float* per_thread) {
     return v[0];
 }
 
+void combine(const float* part_base, float* out, long out_stride, int pos0, int m, int n_heads, int hd, int nsplit,
+             int want, int cap);
+
 // A cache element as the kernels widen it: f16 bits exactly, int8 as its integer value.
 inline float kv_value(uint16_t h) { return widen().v[h]; }
 inline float kv_value(int8_t v) { return (float)v; }
@@ -345,13 +351,19 @@ void decode_gpu(const float* qkv, long q_stride, const KV_T* kc, const KV_T* vc,
         }
     };
     parallel_for((long)n_kv * m * nsplit, threads, block);
-    if (nsplit == 1) return;
-    for (int b = 0; b < m; b++) // attention_combine
+    if (nsplit > 1) combine(part.data(), out, out_stride, pos0, m, n_heads, hd, nsplit, want, cap);
+}
+
+// attention_combine (src/cuda.rs:2806-2836): per (token, head) the slices' max, each slice's weight exp(m_s -
+// max), the weighted exp-sums and outputs in slice order. part: [token][head][slice][hd + 2], natural log.
+void combine(const float* part_base, float* out, long out_stride, int pos0, int m, int n_heads, int hd, int nsplit,
+             int want, int cap) {
+    for (int b = 0; b < m; b++)
         for (int h = 0; h < n_heads; h++) {
             int span = pos0 + b + 1;
             int chunk = att_chunk(span, want, cap);
             int used = std::min(nsplit, (span + chunk - 1) / chunk);
-            const float* p = part.data() + ((size_t)b * n_heads + h) * nsplit * (hd + 2);
+            const float* p = part_base + ((size_t)b * n_heads + h) * nsplit * (hd + 2);
             float mm = -std::numeric_limits<float>::infinity();
             for (int s = 0; s < used; s++) mm = std::max(mm, p[s * (hd + 2) + hd]);
             std::vector<float> w(used);
@@ -365,6 +377,104 @@ void decode_gpu(const float* qkv, long q_stride, const KV_T* kc, const KV_T* vc,
                 out[(long)b * out_stride + (long)h * hd + d] = acc * inv;
             }
         }
+}
+
+// ---------------------------------------------------------------- attention_decode_tc256, KV8 (src/cuda.rs:2625-2802)
+// The tensor-core decode of 256-wide grouped heads over the int8 cache, on attention_partial_gqa's grid and
+// slices (its partials merged by attention_combine). Per block (kv head, token, slice), warp w of 4 takes the
+// slice's 8-position tiles w, w + 4, ...: Q rounded to f16 after scaling by scale*log2(e); per tile the scores
+// (the f16 Q times the integer keys, f32 sums) times the key scales; the running max moves every tile
+// (alpha = exp2(m - m_new)); l = alpha*l + the unrounded p; P = f16(p * vscale * 2^10) and O = alpha*O + P V.
+// Warps 1..3 merge into warp 0 in order; out = O / 2^10 / l, or the partial (O / 2^10, m*ln2, l).
+void decode_tc256_i8(const float* qkv, long q_stride, const int8_t* kc, const int8_t* vc, const float* ks,
+                     const float* vs, long kv_stride, float* out, long out_stride, int pos0, int m, int n_heads, int n_kv,
+                     float scale, int nsplit, int want, int cap, int threads) {
+    const int hd = 256, G = n_heads / n_kv;
+    const float NEG = -std::numeric_limits<float>::infinity(), LN2 = 0.6931471805599453f, BIAS = 1024.f;
+    const float qs = scale * 1.4426950408889634f;
+    std::vector<float> part((size_t)m * n_heads * nsplit * (hd + 2), 0.f);
+    auto block = [&](long idx) {
+        int s = (int)(idx % nsplit);
+        int b = (int)((idx / nsplit) % m);
+        int kvh = (int)(idx / nsplit / m);
+        int span = pos0 + b + 1;
+        int chunk = att_chunk(span, want, cap);
+        int t0 = s * chunk, len = std::min(span, t0 + chunk) - t0;
+        auto P = [&](int g) { return part.data() + (((size_t)b * n_heads + kvh * G + g) * nsplit + s) * (hd + 2); };
+        if (len <= 0) {
+            for (int g = 0; g < G; g++) {
+                float* p = P(g);
+                std::fill(p, p + hd, 0.f);
+                p[hd] = NEG;
+                p[hd + 1] = 0.f;
+            }
+            return;
+        }
+        // Q as the f16 fragments hold it
+        std::vector<float> qh((size_t)G * hd);
+        const float* qb = qkv + (long)b * q_stride + (long)kvh * G * hd;
+        for (int i = 0; i < G * hd; i++) qh[i] = f16_to_f32(f32_to_f16(qb[i] * qs));
+        // per warp and head: running max, sum, O
+        std::vector<float> wm(4 * G, NEG), wl(4 * G, 0.f), wo((size_t)4 * G * hd, 0.f);
+        for (int w = 0; w < 4; w++)
+            for (int tt = 8 * w; tt < len; tt += 32)
+                for (int g = 0; g < G; g++) {
+                    float sc[8], mx = NEG;
+                    for (int j = 0; j < 8; j++) {
+                        int pa = tt + j;
+                        if (pa >= len) { sc[j] = NEG; continue; }
+                        const int8_t* kr = kc + (long)(t0 + pa) * kv_stride + kvh * hd;
+                        float acc = 0.f;
+                        for (int d = 0; d < hd; d++) acc += qh[(size_t)g * hd + d] * (float)kr[d];
+                        sc[j] = acc * ks[(long)(t0 + pa) * n_kv + kvh];
+                        mx = std::max(mx, sc[j]);
+                    }
+                    float& mr = wm[w * G + g];
+                    float& lr = wl[w * G + g];
+                    float* o = wo.data() + ((size_t)w * G + g) * hd;
+                    const float mn = std::max(mr, mx), alpha = std::exp2(mr - mn);
+                    mr = mn;
+                    float psum = 0.f, pv[8];
+                    for (int j = 0; j < 8; j++) {
+                        const float p = std::exp2(sc[j] - mn);
+                        psum += p;
+                        const float v = tt + j < len ? vs[(long)(t0 + tt + j) * n_kv + kvh] * BIAS : 0.f;
+                        pv[j] = f16_to_f32(f32_to_f16(p * v));
+                    }
+                    lr = lr * alpha + psum;
+                    for (int d = 0; d < hd; d++) {
+                        float a = o[d] * alpha;
+                        for (int j = 0; j < 8; j++)
+                            if (tt + j < len) a += pv[j] * (float)vc[(long)(t0 + tt + j) * kv_stride + kvh * hd + d];
+                        o[d] = a;
+                    }
+                }
+        for (int g = 0; g < G; g++) {
+            float mr = wm[g], lr = wl[g];
+            float* o = wo.data() + (size_t)g * hd;
+            for (int w = 1; w < 4; w++) {
+                const float mw = wm[w * G + g];
+                if (mw == NEG) continue;
+                const float mn = std::max(mr, mw), a = std::exp2(mr - mn), aw = std::exp2(mw - mn);
+                lr = lr * a + wl[w * G + g] * aw;
+                const float* ow = wo.data() + ((size_t)w * G + g) * hd;
+                for (int d = 0; d < hd; d++) o[d] = o[d] * a + ow[d] * aw;
+                mr = mn;
+            }
+            const int h = kvh * G + g;
+            if (nsplit == 1) {
+                const float f = (1.f / BIAS) / lr;
+                for (int d = 0; d < hd; d++) out[(long)b * out_stride + (long)h * hd + d] = o[d] * f;
+            } else {
+                float* p = P(g);
+                for (int d = 0; d < hd; d++) p[d] = o[d] * (1.f / BIAS);
+                p[hd] = mr * LN2;
+                p[hd + 1] = lr;
+            }
+        }
+    };
+    parallel_for((long)n_kv * m * nsplit, threads, block);
+    if (nsplit > 1) combine(part.data(), out, out_stride, pos0, m, n_heads, hd, nsplit, want, cap);
 }
 
 // ---------------------------------------------------------------- attn_prefill_tc<128> (src/cuda.rs:2408-2617)
@@ -546,6 +656,13 @@ void gio_decode_gpu_i8(const float* qkv, long q_stride, const int8_t* kc, const 
 // kv_store with KV8 (src/cuda.rs:333-339) over `rows` rows of hd values: dd = max|x| / 127, each value
 // rint(x * (1/dd)) as int8 (0 when dd is 0), dd to the row's scale. Division correctly rounded, rint to
 // nearest even (the reference's IEEE `/` and __float2int_rn).
+void gio_decode_tc256_i8(const float* qkv, long q_stride, const int8_t* kc, const int8_t* vc, const float* ks,
+                         const float* vs, long kv_stride, float* out, long out_stride, int pos0, int m, int n_heads,
+                         int n_kv, float scale, int nsplit, int want, int cap, int threads) {
+    decode_tc256_i8(qkv, q_stride, kc, vc, ks, vs, kv_stride, out, out_stride, pos0, m, n_heads, n_kv, scale, nsplit,
+                    want, cap, threads);
+}
+
 void gio_kv_quant_i8(const float* src, long rows, int hd, int8_t* dst, float* scales) {
     for (long r = 0; r < rows; r++) kv_quant_i8(src + r * hd, hd, dst + r * hd, scales + r);
 }

@@ -47,6 +47,7 @@ def lib():
         L.gio_qk_norm_rope.argtypes = [vp, vp, vp, vp, vp, l, l, i, i, i, i, i, i, f, vp, i, f]
         L.gio_qk_norm_rope_i8.argtypes = [vp, vp, vp, vp, vp, vp, vp, l, l, l, l, i, i, i, i, i, i, f, vp, i, f]
         L.gio_decode_gpu_i8.argtypes = [vp, l, vp, vp, vp, vp, l, vp, l, i, i, i, i, f, i, i, i, i]
+        L.gio_decode_tc256_i8.argtypes = [vp, l, vp, vp, vp, vp, l, vp, l, i, i, i, i, f, i, i, i, i]
         L.gio_kv_quant_i8.argtypes = [vp, l, i, vp, vp]
         L.gio_prefill_tc_i8.argtypes = [vp, l, vp, vp, vp, vp, l, vp, l, i, i, i, i, f, i]
         L.gio_prefill_tc256.argtypes = [vp, l, vp, vp, l, vp, l, i, i, i, i, f, i]
@@ -148,6 +149,24 @@ def decode_gpu_semantics_i8(q, kc, vc, ks, vs, pos0, n_heads, n_kv, scale=None, 
     out = np.zeros((m, n_heads * 128), dtype=np.float32)
     lib().gio_decode_gpu_i8(_p(q), q.shape[1], _p(kc), _p(vc), _p(ks), _p(vs), kc.shape[1], _p(out), out.shape[1],
                             pos0, m, n_heads, n_kv, scale, nsplit, want, cap, threads)
+    return out
+
+
+def decode_tc256_i8(q, kc, vc, ks, vs, pos0, n_heads, n_kv, scale=None, cap=128, threads=8, want=None):
+    """attention_decode_tc256 over the KV8 cache (src/cuda.rs:2625-2802) + attention_combine (src/cuda.rs:2806-2836),
+    with the host's split arithmetic (src/cuda.rs:8426-8444). kc/vc int8 [pos, n_kv*256]; ks/vs f32 [pos, n_kv]."""
+    q = _rows(q, np.float32)
+    m = q.shape[0]
+    kc, vc = _rows(kc, np.int8), _rows(vc, np.int8)
+    ks, vs = _rows(ks, np.float32), _rows(vs, np.float32)
+    assert ks.shape == (kc.shape[0], n_kv) and vs.shape == ks.shape and kc.shape[1] == n_kv * 256
+    if scale is None:
+        scale = 1.0 / 16.0
+    want = att_want(n_kv) if want is None else want
+    nsplit = max(-(-span // att_chunk(span, want, cap)) for span in range(pos0 + 1, pos0 + m + 1))
+    out = np.zeros((m, n_heads * 256), dtype=np.float32)
+    lib().gio_decode_tc256_i8(_p(q), q.shape[1], _p(kc), _p(vc), _p(ks), _p(vs), kc.shape[1], _p(out), out.shape[1],
+                              pos0, m, n_heads, n_kv, scale, nsplit, want, cap, threads)
     return out
 
 

@@ -13,7 +13,7 @@ import torch
 
 import gi_attn
 import gi_oracle as O
-from attn_common import assert_close, make_inputs, reference_f64
+from attn_common import assert_close, make_inputs, make_inputs_i8, reference_f64, reference_f64_i8
 
 pytestmark = pytest.mark.gpu
 HD = 256
@@ -92,6 +92,70 @@ def test_decode_hd256_device_position(gpu):
         torch.cuda.synchronize()
         assert_close(out.cpu().numpy(), reference_f64(q, k, v, pos, n_heads, n_kv, hd=HD), max_abs=2e-5,
                      rel_l2=2e-5, what=f"hd256 posp {pos}")
+
+
+# ---------------------------------------------------------------- decode over the int8 cache (attention_decode_tc256)
+
+def to_dev_i8(q, k, v, ks, vs, dev, n_kv, layout="reference"):
+    if layout == "head_major":
+        k = np.ascontiguousarray(k.reshape(k.shape[0], n_kv, HD).transpose(1, 0, 2))
+        v = np.ascontiguousarray(v.reshape(v.shape[0], n_kv, HD).transpose(1, 0, 2))
+        ks, vs = np.ascontiguousarray(ks.T), np.ascontiguousarray(vs.T)
+    return [torch.from_numpy(np.ascontiguousarray(x)).to(dev) for x in (q, k, v, ks, vs)]
+
+
+def check_i8(got, q, k, v, ks, vs, pos0, n_heads, n_kv, what, oracle=True):
+    # the reference's tc256 rounds Q and P*vscale to f16 (the parity bar); these kernels keep f32 precision
+    if oracle:
+        assert_close(got, O.decode_tc256_i8(q, k, v, ks, vs, pos0, n_heads, n_kv), what=f"{what} vs oracle (tc256)")
+    assert_close(got, reference_f64_i8(q, k, v, ks, vs, pos0, n_heads, n_kv, hd=HD), max_abs=2e-5, rel_l2=2e-5,
+                 what=f"{what} vs f64")
+
+
+@pytest.mark.parametrize("n_tok,pos0,n_heads,n_kv", DECODE_SHAPES_256)
+def test_decode_hd256_i8(gpu, n_tok, pos0, n_heads, n_kv):
+    say("decode hd256 i8", n_tok, pos0, n_heads, n_kv)
+    q, k, v, ks, vs = make_inputs_i8(7000 + pos0, n_tok, pos0 + n_tok, n_heads, n_kv, hd=HD)
+    qt, kt, vt, kst, vst = to_dev_i8(q, k, v, ks, vs, gpu, n_kv)
+    out = gi_attn.decode(qt, kt, vt, pos0, n_heads, n_kv, hd=HD, k_scale=kst, v_scale=vst)
+    torch.cuda.synchronize()
+    check_i8(out.cpu().numpy(), q, k, v, ks, vs, pos0, n_heads, n_kv, "decode hd256 i8")
+
+
+@pytest.mark.parametrize("n_tok,layout", [(1, "reference"), (1, "head_major"), (8, "head_major")])
+def test_decode_hd256_i8_long_context(gpu, n_tok, layout):
+    # 65536 keys (one token) and an 8-token verify block at a 32768-key prefix, 16 query / 2 kv heads
+    ctx = 65536 if n_tok == 1 else 32768 + n_tok
+    say("decode hd256 i8", ctx, n_tok, layout)
+    q, k, v, ks, vs = make_inputs_i8(71 + n_tok, n_tok, ctx, 16, 2, hd=HD)
+    qt, kt, vt, kst, vst = to_dev_i8(q, k, v, ks, vs, gpu, 2, layout)
+    out = gi_attn.decode(qt, kt, vt, ctx - n_tok, 16, 2, hd=HD, k_scale=kst, v_scale=vst, kv_layout=layout)
+    torch.cuda.synchronize()
+    check_i8(out.cpu().numpy(), q, k, v, ks, vs, ctx - n_tok, 16, 2, f"hd256 i8 {ctx} keys", oracle=n_tok > 1)
+
+
+def test_decode_hd256_i8_graph_replay(gpu):
+    # an 8-token verify block (one pair per column, shared slices) with a device position, captured once and
+    # replayed at several positions with eager work between the replays
+    n_tok, n_heads, n_kv, cap = 8, 16, 2, 2500
+    q, k, v, ks, vs = make_inputs_i8(95, n_tok, cap, n_heads, n_kv, hd=HD)
+    qt, kt, vt, kst, vst = to_dev_i8(q, k, v, ks, vs, gpu, n_kv)
+    ws = gi_attn.new_workspace(cap, n_tok, n_heads, n_kv, hd=HD, device=gpu)
+    posp = torch.zeros(1, dtype=torch.int32, device=gpu)
+    out = torch.zeros((n_tok, n_heads * HD), dtype=torch.float32, device=gpu)
+    kw = dict(hd=HD, out=out, workspace=ws, posp=posp, ctx_cap=cap, k_scale=kst, v_scale=vst)
+    gi_attn.decode(qt, kt, vt, 0, n_heads, n_kv, **kw)  # warm-up
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        gi_attn.decode(qt, kt, vt, 0, n_heads, n_kv, **kw)
+    for pos in (cap - n_tok, 31, 1000, 0):
+        say("decode hd256 i8 graph replay", pos)
+        posp.fill_(pos)
+        out.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        check_i8(out.cpu().numpy(), q, k, v, ks, vs, pos, n_heads, n_kv, f"hd256 i8 replay at {pos}", oracle=False)
 
 
 # ---------------------------------------------------------------- prefill (attention_prefill_tc256)

@@ -236,6 +236,102 @@ def test_prefill_tc_semantics_within_parity_bar(n, pos0, n_heads, n_kv):
     assert ma > 1e-6  # the f16 roundings are visible
 
 
+def _f16(x):
+    return np.float32(np.float16(np.float32(x)))
+
+
+def _q_between_f16(hd, n_heads, x):
+    """A query row whose every element, times scale*log2(e) in f32, is x (not an f16 value)."""
+    qs = np.float32(1.0 / math.sqrt(hd)) * np.float32(1.4426950408889634)
+    q = np.full((1, n_heads * hd), np.float32(np.float64(x) / np.float64(qs)), dtype=np.float32)
+    assert q[0, 0] * qs != _f16(q[0, 0] * qs)  # the product is not an f16 value: its rounding matters
+    return q, qs
+
+
+def test_prefill_tc_semantics_roundings_by_hand():
+    # One query at position 1 over two keys: key 0 all ones, key 1 zero; value 0 all ones, value 1 zero. Each
+    # element of Q*scale*log2e is 2^-7 (1 + 1.25 * 2^-10), which f16 rounds down to 2^-7 (1 + 2^-10), so the
+    # score of key 0 is 128 * that = 1 + 2^-10 exactly (unrounded: 1 + 1.25 * 2^-10). Then P0 = 1, P1 =
+    # f16(exp2(-(1 + 2^-10))), l = P0 + P1 (the rounded P), out = P0 / l in every dim.
+    x = 2.0 ** -7 * (1 + 1.25 * 2.0 ** -10)
+    q, qs = _q_between_f16(128, 1, x)
+    k = np.zeros((2, 128), np.float16)
+    k[0] = 1
+    v = np.zeros((2, 128), np.float16)
+    v[0] = 1
+    got = O.prefill_tc_semantics(q, k.view(np.uint16), v.view(np.uint16), 1, 1, 1)
+    s0 = np.float32(128) * _f16(q[0, 0] * qs)
+    assert s0 == np.float32(1 + 2.0 ** -10)
+    p1 = _f16(np.exp2(-s0))
+    want = np.float32(1) / (np.float32(1) + p1)
+    np.testing.assert_allclose(got, want, rtol=2e-7, atol=0)
+    # each plausible slip moves the result far beyond that tolerance
+    s0_unrounded = np.float32(128) * (q[0, 0] * qs)
+    slips = {"Q not rounded": 1 / (1 + _f16(np.exp2(-s0_unrounded))),
+             "P not rounded": 1 / (1 + np.exp2(-s0)),
+             "natural-log softmax": 1 / (1 + _f16(np.exp(-s0)))}
+    for what, alt in slips.items():
+        assert abs(float(alt) - float(want)) > 1e-5, what
+
+
+def test_decode_tc256_i8_roundings_by_hand():
+    # attention_decode_tc256 over the int8 cache, one token at position 1 over two keys (one 8-position tile):
+    # key 0 all ones (scale 1), key 1 zero; each element of Q*scale*log2e is 2^-8 (1 + 1.25 * 2^-10), which
+    # f16 rounds down, so score 0 = 256 * 2^-8 (1 + 2^-10) = 1 + 2^-10 exactly and score 1 = 0. Values: row 0
+    # all 1 with scale 1/3, row 1 all 2 with scale 1/5. P = f16(p * vscale * 2^10): P0 = f16(1024/3) = 341.25,
+    # P1 = f16(2^-(1 + 2^-10) * 1024/5); l = 1 + 2^-(1 + 2^-10) (the unrounded p); out = (P0 + 2 P1) / 1024 / l.
+    x = 2.0 ** -8 * (1 + 1.25 * 2.0 ** -10)
+    q, qs = _q_between_f16(256, 1, x)
+    k = np.zeros((2, 256), np.int8)
+    k[0] = 1
+    v = np.zeros((2, 256), np.int8)
+    v[0], v[1] = 1, 2
+    ks = np.ones((2, 1), np.float32)
+    vs = np.array([[1 / 3], [1 / 5]], np.float32)
+    got = O.decode_tc256_i8(q, k, v, ks, vs, 1, 1, 1)
+    s0 = np.float32(256) * _f16(q[0, 0] * qs)
+    assert s0 == np.float32(1 + 2.0 ** -10)
+    p1 = np.exp2(-s0)
+    P0 = _f16(np.float32(1) * (vs[0, 0] * np.float32(1024)))
+    P1 = _f16(p1 * (vs[1, 0] * np.float32(1024)))
+    assert P0 == np.float32(341.25)
+    want = (P0 + np.float32(2) * P1) * (np.float32(1) / np.float32(1024) / (np.float32(1) + p1))
+    np.testing.assert_allclose(got, want, rtol=2e-7, atol=0)
+    s0_unrounded = np.float32(256) * (q[0, 0] * qs)
+    p1u = np.exp2(-s0_unrounded)
+    slips = {"Q not rounded": (P0 + 2 * _f16(p1u * vs[1, 0] * 1024)) / 1024 / (1 + p1u),
+             "l of the rounded P": (P0 + 2 * P1) / (P0 + P1),
+             "P not rounded": (vs[0, 0] * 1024 + 2 * p1 * vs[1, 0] * 1024) / 1024 / (1 + p1),
+             "value scale in l": (P0 + 2 * P1) / 1024 / (vs[0, 0] + p1 * vs[1, 0]) / 1024}
+    for what, alt in slips.items():
+        assert abs(float(alt) - float(want)) > 1e-5 * float(want), what
+
+
+@pytest.mark.parametrize("n_tok,pos0,n_heads,n_kv", [(1, 0, 16, 2), (1, 7, 16, 2), (1, 8, 8, 1), (1, 300, 16, 2),
+                                                     (3, 100, 8, 1), (8, 2000, 16, 2), (1, 4095, 16, 16)])
+def test_decode_tc256_i8_within_parity_bar(n_tok, pos0, n_heads, n_kv):
+    # f16 Q and f16 P*vscale*2^10: within the bar of float64 attention over the dequantised cache, not equal
+    q, k, v, ks, vs = make_inputs_i8(91 + pos0, n_tok, pos0 + n_tok, n_heads, n_kv, hd=256)
+    got = O.decode_tc256_i8(q, k, v, ks, vs, pos0, n_heads, n_kv)
+    want = reference_f64_i8(q, k, v, ks, vs, pos0, n_heads, n_kv, hd=256)
+    ma, _ = assert_close(got, want, what="decode_tc256 int8 semantics vs f64")
+    assert ma > 1e-6
+
+
+def test_decode_tc256_i8_slice_count_and_gqa():
+    # the result does not depend on the slice count beyond the f16 rounding of P (taken against each warp's
+    # running max, which the slicing moves), and heads of one group with equal queries give equal outputs
+    q, k, v, ks, vs = make_inputs_i8(17, 2, 3000, 8, 2, hd=256)
+    a = O.decode_tc256_i8(q, k, v, ks, vs, 2998, 8, 2)
+    b = O.decode_tc256_i8(q, k, v, ks, vs, 2998, 8, 2, cap=4096, want=1)  # one slice per token (48 above)
+    ma, _ = errors(a, b)
+    assert 0 < ma < 1e-4
+    q2 = q.reshape(2, 8, 256).copy()
+    q2[:, 1] = q2[:, 0]
+    o = O.decode_tc256_i8(q2.reshape(2, -1), k, v, ks, vs, 2998, 8, 2).reshape(2, 8, 256)
+    np.testing.assert_array_equal(o[:, 0], o[:, 1])
+
+
 # ---------------------------------------------------------------- golden fixtures
 
 def _golden_files():
