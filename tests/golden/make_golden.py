@@ -3,8 +3,9 @@
     python tests/golden/make_golden.py
 
 The expected outputs come from the textbook causal softmax attention in float64
-(tests/attn_common.reference_f64), not from the oracle under test. Inputs follow the configs' recipe
-(Q N(0,1), K/V N(0,1) rounded to f16, scale 1/sqrt(128)) at sizes small enough to commit.
+(tests/attn_common.reference_f64, over the dequantised cache for int8), not from the oracle under test.
+Inputs follow the configs' recipe (Q N(0,1), K/V N(0,1) rounded to f16, scale 1/sqrt(head size)) at sizes
+small enough to commit; the int8 cases hold int8 rows and their f32 scales (keys ks, vs).
 """
 import os
 import sys
@@ -13,24 +14,36 @@ import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.dirname(HERE))
-from attn_common import make_inputs, reference_f64  # noqa: E402
+from attn_common import make_inputs, make_inputs_i8, reference_f64, reference_f64_i8  # noqa: E402
 
 CASES = {
-    # name: (seed, n_tok, pos0, n_heads, n_kv, q dtype)
-    "decode_g4_ctx64": (101, 1, 63, 32, 8, np.float32),
-    "decode_g8_ctx300": (102, 1, 299, 32, 4, np.float32),
-    "verify_8tok_ctx136": (103, 8, 128, 32, 4, np.float32),
-    "prefill_48tok": (104, 48, 0, 8, 2, np.float16),
-    "prefill_chunk_32at64": (105, 32, 64, 8, 2, np.float16),
+    # name: (seed, n_tok, pos0, n_heads, n_kv, q dtype, head size, int8 cache)
+    "decode_g4_ctx64": (101, 1, 63, 32, 8, np.float32, 128, False),
+    "decode_g8_ctx300": (102, 1, 299, 32, 4, np.float32, 128, False),
+    "verify_8tok_ctx136": (103, 8, 128, 32, 4, np.float32, 128, False),
+    "prefill_48tok": (104, 48, 0, 8, 2, np.float16, 128, False),
+    "prefill_chunk_32at64": (105, 32, 64, 8, 2, np.float16, 128, False),
+    "decode_h256_ctx200": (106, 1, 199, 16, 2, np.float32, 256, False),
+    "prefill_h256_40tok": (107, 40, 0, 4, 1, np.float16, 256, False),
+    "decode_i8_g8_ctx300": (108, 1, 299, 32, 4, np.float32, 128, True),
+    "verify_i8_4tok_ctx100": (109, 4, 96, 16, 2, np.float32, 128, True),
+    "decode_h256_i8_ctx200": (110, 1, 199, 16, 2, np.float32, 256, True),
+    "verify_h256_i8_3tok_ctx90": (111, 3, 87, 16, 2, np.float32, 256, True),
 }
 
 
 def main():
-    for name, (seed, n_tok, pos0, n_heads, n_kv, qd) in CASES.items():
-        q, k, v = make_inputs(seed, n_tok, pos0 + n_tok, n_heads, n_kv, q_dtype=qd)
-        out = reference_f64(q, k, v, pos0, n_heads, n_kv).astype(np.float32)
+    for name, (seed, n_tok, pos0, n_heads, n_kv, qd, hd, i8) in CASES.items():
+        extra = {}
+        if i8:  # int8 rows round(40 N(0,1)) with f32 scales near 1/40, as quantised N(0,1) rows
+            q, k, v, ks, vs = make_inputs_i8(seed, n_tok, pos0 + n_tok, n_heads, n_kv, hd=hd)
+            out = reference_f64_i8(q, k, v, ks, vs, pos0, n_heads, n_kv, hd=hd).astype(np.float32)
+            extra = {"ks": ks, "vs": vs}
+        else:
+            q, k, v = make_inputs(seed, n_tok, pos0 + n_tok, n_heads, n_kv, hd=hd, q_dtype=qd)
+            out = reference_f64(q, k, v, pos0, n_heads, n_kv, hd=hd).astype(np.float32)
         np.savez_compressed(os.path.join(HERE, name + ".npz"), q=q, k=k, v=v, out=out, pos0=pos0,
-                            n_heads=n_heads, n_kv=n_kv)
+                            n_heads=n_heads, n_kv=n_kv, hd=hd, **extra)
         print(name, q.shape, k.shape)
 
 

@@ -1,0 +1,64 @@
+"""The committed golden fixtures (tests/golden/*.npz: seeded inputs and float64 expected outputs, written by
+tests/golden/make_golden.py) through the HIP path: the decode / verify cases through gi_attn_decode(_i8) and,
+packed as the reference's qkv rows, through the operator gi_attention(_i8) (src/cuda.rs:8448-8541); the
+prefill cases through gi_attn_prefill.
+
+Bar: decode and verify within 2e-5 of float64 (the split path keeps f32 precision), prefill within the
+north star's 2e-3 / 1e-3 (it rounds P to f16 as the reference does)."""
+import os
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+import gi_attn
+from attn_common import assert_close
+
+pytestmark = pytest.mark.gpu
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+NAMES = sorted(f[:-4] for f in os.listdir(GOLDEN) if f.endswith(".npz"))
+
+
+def say(*a):
+    print("[case]", *a, flush=True)
+    sys.stdout.flush()
+
+
+def load(name, dev):
+    z = np.load(os.path.join(GOLDEN, name + ".npz"))
+    meta = {k: int(z[k]) for k in ("pos0", "n_heads", "n_kv")}
+    meta["hd"] = int(z["hd"]) if "hd" in z.files else 128
+    i8 = "ks" in z.files
+    q = torch.from_numpy(z["q"]).to(dev)
+    if i8:
+        k, v = torch.from_numpy(z["k"]).to(dev), torch.from_numpy(z["v"]).to(dev)
+        sc = dict(k_scale=torch.from_numpy(z["ks"]).to(dev), v_scale=torch.from_numpy(z["vs"]).to(dev))
+    else:
+        k = torch.from_numpy(z["k"].view(np.int16)).to(dev).view(torch.float16)
+        v = torch.from_numpy(z["v"].view(np.int16)).to(dev).view(torch.float16)
+        sc = {}
+    return z, meta, q, k, v, sc
+
+
+@pytest.mark.parametrize("name", NAMES)
+def test_golden_through_the_hip_path(gpu, name):
+    say("golden", name)
+    z, m, q, k, v, sc = load(name, gpu)
+    n = q.shape[0]
+    want = z["out"]
+    if name.startswith("prefill"):
+        out = gi_attn.prefill(q, k, v, m["pos0"], m["n_heads"], m["n_kv"], hd=m["hd"], out_dtype=torch.float32, **sc)
+        torch.cuda.synchronize()
+        assert_close(out.cpu().numpy(), want, what=f"{name} prefill")
+        return
+    out = gi_attn.decode(q, k, v, m["pos0"], m["n_heads"], m["n_kv"], hd=m["hd"], **sc)
+    torch.cuda.synchronize()
+    assert_close(out.cpu().numpy(), want, max_abs=2e-5, rel_l2=2e-5, what=f"{name} decode")
+    # the operator over the reference's qkv rows [q | k | v] (only q is read: the cache already holds the rows)
+    qd, kvd = m["n_heads"] * m["hd"], m["n_kv"] * m["hd"]
+    qkv = torch.zeros((n, qd + 2 * kvd), dtype=torch.float32, device=gpu)
+    qkv[:, :qd] = q
+    out2 = gi_attn.attention(qkv, k, v, m["pos0"], m["n_heads"], m["n_kv"], hd=m["hd"], exact=True, **sc)
+    torch.cuda.synchronize()
+    assert_close(out2.cpu().numpy(), want, max_abs=2e-5, rel_l2=2e-5, what=f"{name} operator")

@@ -346,8 +346,17 @@ def test_golden_fixtures_exist():
 def test_oracle_against_golden(name):
     z = np.load(os.path.join(GOLDEN, name))
     n_heads, n_kv, pos0 = int(z["n_heads"]), int(z["n_kv"]), int(z["pos0"])
-    got = O.attention(z["q"].astype(np.float32), z["k"], z["v"], pos0, n_heads, n_kv)
-    assert_close(got, z["out"], max_abs=2e-5, rel_l2=2e-6, what=name)
+    hd = int(z["hd"]) if "hd" in z.files else 128
+    q = z["q"].astype(np.float32)
+    if "ks" in z.files and hd == 256:  # attention_decode_tc256 rounds Q and P*vscale to f16: the parity bar
+        got = O.decode_tc256_i8(q, z["k"], z["v"], z["ks"], z["vs"], pos0, n_heads, n_kv)
+        assert_close(got, z["out"], what=name)
+    elif "ks" in z.files:  # the int8 split path keeps f32 precision
+        got = O.decode_gpu_semantics_i8(q, z["k"], z["v"], z["ks"], z["vs"], pos0, n_heads, n_kv)
+        assert_close(got, z["out"], max_abs=2e-5, rel_l2=2e-6, what=name)
+    else:
+        got = O.attention(q, z["k"], z["v"], pos0, n_heads, n_kv, hd=hd)
+        assert_close(got, z["out"], max_abs=2e-5, rel_l2=2e-6, what=name)
 
 
 # ---------------------------------------------------------------- qk_norm_rope (KV store)
