@@ -98,15 +98,16 @@ def kernel_times(gi_attn, fn, steps, torch, kinds):
 def decode_kernel_name(n_tok, n_heads, n_kv, hd, i8):
     """Name of the split-K kernel a decode call of this shape launches: the host library's variant rule
     (up to 8 (token, head) pairs per kv head: one column block with two columns per pair; above, one pair
-    per MFMA column, with two column blocks per wave above 16 pairs at head size 128, and 4 waves sharing
-    each tile at head size 256)."""
+    per MFMA column, with two column blocks per wave above 16 pairs at head size 128 (f16 above 32 pairs:
+    two pair sets per workgroup, each over two waves), and 4 waves sharing each tile at head size 256)."""
     pairs, p = n_tok * (n_heads // n_kv), 8
     if pairs <= p:
         name = "gi_decode_partial_1"
     elif hd == 256:
         name = "gi_decode_pm_shared_1"
     else:
-        name = "gi_decode_pm_2" if pairs > 2 * p else "gi_decode_pm_1"
+        name = ("gi_decode_pm_ws2_2" if pairs > 4 * p and not i8 else
+                "gi_decode_pm_2" if pairs > 2 * p else "gi_decode_pm_1")
     return name + ("_i8" if i8 else "") + ("_h256" if hd == 256 else "")
 
 

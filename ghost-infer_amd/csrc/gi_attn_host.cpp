@@ -156,6 +156,7 @@ struct Module {
     hipFunction_t dec[2] = {};        // up to 8 pairs, head size 128: [int8 cache]
     hipFunction_t dec256[2] = {};     // up to 8 pairs, head size 256: [int8 cache]
     hipFunction_t dec_pm[2][2] = {};  // [int8 cache][column blocks - 1]: one pair per column
+    hipFunction_t dec_ws2[2] = {};    // head size 128, two column blocks, two pair sets of two waves: [int8 cache]
     hipFunction_t dec_pm256[2] = {};  // head size 256, one pair per column, 4 waves sharing each tile: [int8 cache]
     hipFunction_t prefill[2] = {};   // [int8 cache], head size 128
     hipFunction_t prefill256r = nullptr; // head size 256 (f16 cache), 16 rows per wave: one workgroup per query tile
@@ -201,6 +202,8 @@ int load_module(const char* path, Module** out) {
             {&m.dec_pm[0][1], "gi_decode_pm_2"},
             {&m.dec_pm[1][0], "gi_decode_pm_1_i8"},
             {&m.dec_pm[1][1], "gi_decode_pm_2_i8"},
+            {&m.dec_ws2[0], "gi_decode_pm_ws2_2"},
+            {&m.dec_ws2[1], "gi_decode_pm_ws2_2_i8"},
             {&m.dec_pm256[0], "gi_decode_pm_shared_1_h256"},
             {&m.dec_pm256[1], "gi_decode_pm_shared_1_i8_h256"},
             {&m.combine, "gi_decode_combine"},
@@ -295,12 +298,13 @@ int decode_target_wgs() {
 struct DecVariant {
     int ncb;     // column blocks per wave
     bool shared; // the 4 waves share every tile of the slice (else each wave takes tiles of its own)
+    bool ws2;    // two pair sets per workgroup, each split over two waves
     bool pm;     // one pair per column
     int groups;  // workgroups per (slice, kv head)
 };
-DecVariant dec_variant(int n_tok, int G, int hd = 128) {
+DecVariant dec_variant(int n_tok, int G, int hd = 128, bool i8 = false) {
     const int pairs = n_tok * G;
-    DecVariant v{1, false, pairs > kDecPairs, 1};
+    DecVariant v{1, false, false, pairs > kDecPairs, 1};
     if (!v.pm) return v;
     if (hd == 256) {
         // 4 waves of 16 pairs sharing every tile of the slice (two column blocks per wave exceed the register
@@ -316,14 +320,24 @@ DecVariant dec_variant(int n_tok, int G, int hd = 128) {
     // against 4 waves sharing every tile: config 4's 64 pairs 32.5 -> 27.8 us (f16), 32.5 -> 28.4 us
     // (int8); 96 pairs 36.5 -> 34.3 and 50.1 -> 35.5 us; equal at 48 and 128 pairs (f16).
     v.ncb = pairs > 2 * kDecPairs ? 2 : 1;
+    if (!i8 && pairs > 4 * kDecPairs) {
+        // f16 above 32 pairs: two pair sets of 32 per workgroup, each split over two waves, so a tile's second
+        // read comes from the same CU rather than another workgroup. Split kernel at 32768 keys, 32/4:
+        // 48 pairs 27.1 -> 25.9 us, 64 pairs 27.9 -> 26.9, 96 pairs 34.6 -> 34.2, 128 pairs 40.7 -> 37.2.
+        // The int8 cache loses (64 pairs 28.0 -> 31.2 us): its tiles are half the bytes, so the read that
+        // moves is cheap while the halved waves per pair set lengthen the dequantising chain.
+        v.ws2 = true;
+        v.groups = (pairs + 8 * kDecPairs - 1) / (8 * kDecPairs);
+        return v;
+    }
     v.groups = (pairs + 2 * kDecPairs * v.ncb - 1) / (2 * kDecPairs * v.ncb);
     return v;
 }
 
 void plan(int max_span, int n_tok, int n_heads, int n_kv, int* chunk, int* nsplit, int unit = kSliceUnit,
-          int hd = 128) {
+          int hd = 128, bool i8 = false) {
     int G = n_heads / n_kv;
-    int groups = dec_variant(n_tok, G, hd).groups;
+    int groups = dec_variant(n_tok, G, hd, i8).groups;
     int units = (max_span + unit - 1) / unit;
     int per_slot = std::max(1, decode_target_wgs() / std::max(1, n_kv * groups));
     int per = std::max(1, (units + per_slot - 1) / per_slot);
@@ -386,9 +400,9 @@ int decode_impl(void* stream, const float* q, long long q_stride, const void* kc
     if (posp && ctx_cap < n_tok) return fail("ctx_cap %d must cover the %d tokens", ctx_cap, n_tok);
     Module* m;
     if (int e = load_module(nullptr, &m)) return e;
-    const DecVariant var = dec_variant(n_tok, n_heads / n_kv, hd);
+    const DecVariant var = dec_variant(n_tok, n_heads / n_kv, hd, i8);
     GiDecodeArgs a{};
-    plan(max_span, n_tok, n_heads, n_kv, &a.chunk, &a.nsplit, slice_unit(i8, hd), hd);
+    plan(max_span, n_tok, n_heads, n_kv, &a.chunk, &a.nsplit, slice_unit(i8, hd), hd, i8);
     size_t need = a.nsplit == 1 ? 0 : (size_t)n_tok * n_heads * a.nsplit * (hd + 4) * sizeof(float);
     if (need && (!workspace || workspace_bytes < need))
         return fail("workspace of %zu bytes too small: %zu needed", workspace_bytes, need);
@@ -417,7 +431,7 @@ int decode_impl(void* stream, const float* q, long long q_stride, const void* kc
         a.sc_head_stride = sc_head_stride;
     }
     hipStream_t st = (hipStream_t)stream;
-    hipFunction_t f = hd == 256 ? (var.pm ? m->dec_pm256[i8] : m->dec256[i8]) : var.pm ? m->dec_pm[i8][var.ncb - 1] : m->dec[i8];
+    hipFunction_t f = hd == 256 ? (var.pm ? m->dec_pm256[i8] : m->dec256[i8]) : var.ws2 ? m->dec_ws2[i8] : var.pm ? m->dec_pm[i8][var.ncb - 1] : m->dec[i8];
     if (int e = launch(kDecodePartial, f, dim3(a.nsplit, n_kv, var.groups), dim3(256), st, &a, sizeof a)) return e;
     if (a.nsplit == 1) return 0;
     return launch(kDecodeCombine, m->combine, dim3(n_heads, n_tok, kCombineSplit * hd / 128), dim3(64), st, &a, sizeof a);
@@ -556,12 +570,13 @@ size_t gi_attn_decode_workspace_bytes(int ctx_cap, int n_tok, int n_heads, int n
     const int unit = slice_unit(false, hd);
     size_t best = 16;
     int G = n_heads / n_kv;
-    for (int t = 1; t <= n_tok; t++) {
-        int groups = dec_variant(t, G, hd).groups;
-        int per_slot = std::max(1, decode_target_wgs() / std::max(1, n_kv * groups));
-        int most = std::max(1, std::min(per_slot, (ctx_cap + unit - 1) / unit));
-        best = std::max(best, (size_t)t * n_heads * most * (hd + 4) * sizeof(float));
-    }
+    for (int t = 1; t <= n_tok; t++)
+        for (bool i8 : {false, true}) {
+            int groups = dec_variant(t, G, hd, i8).groups;
+            int per_slot = std::max(1, decode_target_wgs() / std::max(1, n_kv * groups));
+            int most = std::max(1, std::min(per_slot, (ctx_cap + unit - 1) / unit));
+            best = std::max(best, (size_t)t * n_heads * most * (hd + 4) * sizeof(float));
+        }
     return best;
 }
 

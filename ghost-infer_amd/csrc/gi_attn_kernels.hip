@@ -196,12 +196,14 @@ template <> struct DecBuf<true, 256> { u4 k[4]; u4 v[4]; float ksc, vsc; };
 // block; the f16 high part and remainder of Q and of P are separate MFMAs into the same accumulator instead
 // of neighbouring columns, so a lane's softmax serves one pair and no lane repeats its neighbour's (half the
 // VALU per pair; twice the MFMAs per column, so blocks of at most 8 pairs keep PM = false).
-// SHARE = false: the 4 waves split the slice's tiles and serve the same DEC_PAIRS*NCB (token, head)
-// pairs, merging through LDS at the end. SHARE = true (many pairs per kv head, as in a verify block):
+// WS (waves per pair set) = 4: the 4 waves split the slice's tiles and serve the same DEC_PAIRS*NCB (token, head)
+// pairs, merging through LDS at the end. WS = 2: waves 2p and 2p + 1 split the tiles for pair set p, so one
+// workgroup serves two sets and each tile is read by two waves of one CU. WS = 1 (many pairs per kv head, as in
+// a verify block):
 // every wave walks the whole slice for its own DEC_PAIRS*NCB pairs, so one workgroup serves 4 times as
 // many pairs and the slice's K/V comes from HBM once (the waves' repeated loads of the same lines are
 // served by the caches).
-template <int NCB, bool SHARE, bool I8, int HD = 128, bool PM = false>
+template <int NCB, int WS, bool I8, int HD = 128, bool PM = false>
 __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
     static_assert(HD == 128 || HD == 256, "head sizes: 128, 256");
     // tiles in flight per wave: an int8 tile at head size 256 holds half the bytes of the others
@@ -238,8 +240,10 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
     const int pos0 = a.posp ? min(max(*a.posp, 0), a.kv_cap - a.n_tok) : a.pos0;
     const int G = a.n_heads / a.n_kv;
     const int npairs = a.n_tok * G;
-    constexpr int WG_PAIRS = (SHARE ? DEC_WAVES : 1) * CPAIRS * NCB; // pairs per workgroup
-    const int pair0 = gz * WG_PAIRS + (SHARE ? wave * CPAIRS * NCB : 0); // this wave's first pair
+    static_assert(WS == 1 || WS == 2 || WS == DEC_WAVES, "waves per pair set: 1, 2 or all");
+    constexpr bool SHARE = WS == 1;                  // every wave walks every tile of the slice
+    constexpr int WG_PAIRS = (DEC_WAVES / WS) * CPAIRS * NCB; // pairs per workgroup
+    const int pair0 = gz * WG_PAIRS + (wave / WS) * CPAIRS * NCB; // this wave's first pair
     const int kv_len = pos0 + a.n_tok; // keys any token of the launch may see
     const int k_begin = s * a.chunk;
     const int nkeys = min(a.chunk, kv_len - k_begin); // keys of this slice (<= 0: an empty slice)
@@ -303,7 +307,7 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
     const int koff1 = koff0 + 4 * (int)kvs * 2;
     const int voff = (8 * grp * (int)kvs + 8 * c) * 2;
     const int vstep = (int)kvs * 2;
-    constexpr int STRIDE = SHARE ? TILE : DEC_WAVES * TILE; // keys between a wave's consecutive tiles
+    constexpr int STRIDE = WS * TILE; // keys between a wave's consecutive tiles
     // int8 element offsets (bytes): key rows of block 0 and the V rows of this lane; scales
     const int8_t* kslice8 = reinterpret_cast<const int8_t*>(a.kc) + (long long)k_begin * kvs + kvh * a.kv_head_stride;
     const int8_t* vslice8 = reinterpret_cast<const int8_t*>(a.vc) + (long long)k_begin * kvs + kvh * a.kv_head_stride;
@@ -326,7 +330,7 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
     // K/V stream loads: each tile is read by one wave only, unless SHARE (every wave of the workgroup reads
     // every tile of the slice, from L2 after the first): streaming policy only for the former. At config 2
     // it takes the split kernel from 25.5 to 22.7 us; with SHARE it costs 30%.
-    constexpr int CPOL = SHARE ? 0 : DEC_CPOL;
+    constexpr int CPOL = WS == DEC_WAVES ? DEC_CPOL : 0;
     auto load_k = [&](Buf& B, int t) {
         if constexpr (HD == 256 && I8) {
             __amdgpu_buffer_rsrc_t r = gi_rsrc(kslice8 + (long long)t * kvs, (long long)(nkeys - t) * kvs);
@@ -704,9 +708,9 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
     // (the first loads are issued unconditionally, before the loop, so every iteration starts with the same
     // loads outstanding and the compiler's load counters wait for exactly the buffer in use)
     // a SHARE wave whose pairs all lie past the last one has nothing to compute (it still joins the merge)
-    if (!SHARE || pair0 < npairs) {
+    if (pair0 < npairs) {
     Buf B[NB];
-    const int t_first = SHARE ? 0 : wave * TILE;
+    const int t_first = (wave % WS) * TILE;
 #pragma unroll
     for (int i = 0; i < NB; i++) {
         load_k(B[i], t_first + i * STRIDE);
@@ -775,9 +779,9 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
         const int item = threadIdx.x + 256 * it;
         const int pl = item / (HD / 4), d4 = 4 * (item % (HD / 4)); // pair within the workgroup
         const int pi = gz * WG_PAIRS + pl;
-        const int w0 = SHARE ? pl / (CPAIRS * NCB) : 0;   // the waves holding the pair
-        const int w1 = SHARE ? w0 + 1 : DEC_WAVES;
-        const int lp = SHARE ? pl % (CPAIRS * NCB) : pl;  // the pair within those waves
+        const int w0 = (pl / (CPAIRS * NCB)) * WS;       // the waves holding the pair
+        const int w1 = w0 + WS;
+        const int lp = pl % (CPAIRS * NCB);               // the pair within those waves
         if (pi < npairs) {
             const int row = PM ? lp : 16 * (lp >> 3) + 2 * (lp & 7); // its (first) column
             float M = GI_NEG_INF;
@@ -818,22 +822,24 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
     }
 }
 
-#define GI_DEC_KERNEL(name, NCB, SHARE, I8, HD) \
-    extern "C" __global__ void __launch_bounds__(256, DEC_MINWG) name(GiDecodeArgs a) { gi_decode_partial_t<NCB, SHARE, I8, HD>(a); }
-#define GI_DEC_PM_KERNEL(name, NCB, SHARE, I8) \
-    extern "C" __global__ void __launch_bounds__(256, DEC_MINWG) name(GiDecodeArgs a) { gi_decode_partial_t<NCB, SHARE, I8, 128, true>(a); }
-GI_DEC_KERNEL(gi_decode_partial_1, 1, false, false, 128)
-GI_DEC_KERNEL(gi_decode_partial_1_i8, 1, false, true, 128)
-GI_DEC_KERNEL(gi_decode_partial_1_h256, 1, false, false, 256)
-GI_DEC_PM_KERNEL(gi_decode_pm_1, 1, false, false)
-GI_DEC_PM_KERNEL(gi_decode_pm_2, 2, false, false)
-GI_DEC_PM_KERNEL(gi_decode_pm_1_i8, 1, false, true)
-GI_DEC_PM_KERNEL(gi_decode_pm_2_i8, 2, false, true)
-GI_DEC_KERNEL(gi_decode_partial_1_i8_h256, 1, false, true, 256)
-#define GI_DEC_PM256_KERNEL(name, NCB, SHARE, I8) \
-    extern "C" __global__ void __launch_bounds__(256, DEC_MINWG) name(GiDecodeArgs a) { gi_decode_partial_t<NCB, SHARE, I8, 256, true>(a); }
-GI_DEC_PM256_KERNEL(gi_decode_pm_shared_1_h256, 1, true, false)
-GI_DEC_PM256_KERNEL(gi_decode_pm_shared_1_i8_h256, 1, true, true)
+#define GI_DEC_KERNEL(name, NCB, WS, I8, HD) \
+    extern "C" __global__ void __launch_bounds__(256, DEC_MINWG) name(GiDecodeArgs a) { gi_decode_partial_t<NCB, WS, I8, HD>(a); }
+#define GI_DEC_PM_KERNEL(name, NCB, WS, I8) \
+    extern "C" __global__ void __launch_bounds__(256, DEC_MINWG) name(GiDecodeArgs a) { gi_decode_partial_t<NCB, WS, I8, 128, true>(a); }
+GI_DEC_KERNEL(gi_decode_partial_1, 1, DEC_WAVES, false, 128)
+GI_DEC_KERNEL(gi_decode_partial_1_i8, 1, DEC_WAVES, true, 128)
+GI_DEC_KERNEL(gi_decode_partial_1_h256, 1, DEC_WAVES, false, 256)
+GI_DEC_PM_KERNEL(gi_decode_pm_1, 1, DEC_WAVES, false)
+GI_DEC_PM_KERNEL(gi_decode_pm_2, 2, DEC_WAVES, false)
+GI_DEC_PM_KERNEL(gi_decode_pm_1_i8, 1, DEC_WAVES, true)
+GI_DEC_PM_KERNEL(gi_decode_pm_2_i8, 2, DEC_WAVES, true)
+GI_DEC_PM_KERNEL(gi_decode_pm_ws2_2, 2, 2, false)
+GI_DEC_PM_KERNEL(gi_decode_pm_ws2_2_i8, 2, 2, true)
+GI_DEC_KERNEL(gi_decode_partial_1_i8_h256, 1, DEC_WAVES, true, 256)
+#define GI_DEC_PM256_KERNEL(name, NCB, WS, I8) \
+    extern "C" __global__ void __launch_bounds__(256, DEC_MINWG) name(GiDecodeArgs a) { gi_decode_partial_t<NCB, WS, I8, 256, true>(a); }
+GI_DEC_PM256_KERNEL(gi_decode_pm_shared_1_h256, 1, 1, false)
+GI_DEC_PM256_KERNEL(gi_decode_pm_shared_1_i8_h256, 1, 1, true)
 
 // Merge the slices of each (token, head): M = max m_s, w_s = 2^(m_s - M), out = sum w_s O_s / sum w_s l_s
 // (attention_combine's maths in base 2; empty slices carry m = -inf and weigh nothing). One wave per

@@ -55,9 +55,10 @@ DECODE_SHAPES = [
     (5, 77, 12, 4),   # G = 3: (token, head) pairs straddle column blocks
     (4, 40, 6, 1),    # G = 6
     (2, 95, 32, 4),   # wave 3's first tile (keys 96..) lies past token 0's span but not token 1's
-    (15, 700, 32, 4), # 120 pairs per kv head: one pair per column, four workgroups per (slice, kv head)
+    (15, 700, 32, 4), # 120 pairs per kv head: one pair per column, two workgroups of two pair sets
     (4, 1000, 32, 4),  # 32 pairs: two full column blocks per wave
-    (6, 130, 32, 4),   # 48 pairs: two workgroups per (slice, kv head), the second half idle
+    (6, 130, 32, 4),   # 48 pairs: one workgroup, its second pair set half idle
+    (17, 300, 32, 4),  # 136 pairs: the third workgroup's second pair set has no pair at all
     (4, 40, 16, 1),    # 64 pairs on one kv head, one slice: fewer (slice, kv head) items than XCDs
 ]
 
@@ -116,7 +117,7 @@ def test_decode_device_position_one_launch_shape(gpu):
 
 def test_decode_workspace_reuse_across_shapes(gpu):
     # one workspace through calls of different shapes and kernel variants (few pairs per kv head, a
-    # verify block whose workgroups share each slice): every output is right whatever the earlier calls
+    # verify block whose two pair sets share each slice): every output is right whatever the earlier calls
     # left in the workspace
     n_heads, n_kv, cap = 32, 4, 6000
     ws = gi_attn.new_workspace(cap, 15, n_heads, n_kv, device=gpu)
@@ -132,7 +133,7 @@ def test_decode_workspace_reuse_across_shapes(gpu):
 
 @pytest.mark.parametrize("n_tok,n_heads,n_kv", [(1, 32, 8), (8, 32, 4)])
 def test_decode_graph_replay(gpu, n_tok, n_heads, n_kv):
-    # a decode step (or an 8-token verify block: two pair groups per slice) with a device position, captured
+    # a decode step (or an 8-token verify block: two pair sets per slice) with a device position, captured
     # once and replayed at several positions, with eager work between the replays; each replay matches the
     # float64 reference
     cap = 5000
