@@ -26,6 +26,12 @@
 //   gio_decode_tc256_i8               src/cuda.rs:2625-2802 (attention_decode_tc256 over the KV8 cache: head
 //                                     size 256, f16 Q, P = f16(p * vscale * 2^10), l of the unrounded p) + the
 //                                     attention_combine merge
+//   gio_kv4_fwht                      src/cuda.rs:242-256 (kv4_fwht; hadamard_rows, src/cuda.rs:4675-4693, with
+//                                     block 256 is the same transform)
+//   gio_kv4_quant / gio_kv4_dequant   src/cuda.rs:340-357 (kv_store with KV4) / 238-240 (kv4_pair)
+//   gio_qk_norm_rope_q4               src/cuda.rs:437-486 with KV4 (q, k rotated after RoPE; v rotated in the store)
+//   gio_decode_tc256_q4               attention_decode_tc256 with KV4 (src/cuda.rs:2681-2760) + attention_combine
+//   gio_prefill_tc256_q4              attention_prefill_tc256 with KV4 (src/cuda.rs:2495-2514)
 //
 // How each is pinned (tests/test_oracle.py): the f16 conversion exhaustively against numpy's float16
 // and against src/quant.rs:1160-1169's known values; the attention functions against an independent
@@ -386,9 +392,13 @@ void combine(const float* part_base, float* out, long out_stride, int pos0, int 
 // (the f16 Q times the integer keys, f32 sums) times the key scales; the running max moves every tile
 // (alpha = exp2(m - m_new)); l = alpha*l + the unrounded p; P = f16(p * vscale * 2^10) and O = alpha*O + P V.
 // Warps 1..3 merge into warp 0 in order; out = O / 2^10 / l, or the partial (O / 2^10, m*ln2, l).
-void decode_tc256_i8(const float* qkv, long q_stride, const int8_t* kc, const int8_t* vc, const float* ks,
-                     const float* vs, long kv_stride, float* out, long out_stride, int pos0, int m, int n_heads, int n_kv,
-                     float scale, int nsplit, int want, int cap, int threads) {
+// KV_T = uint16_t (the KV4 build, src/cuda.rs:2681-2700, 2725-2760): the fragments are the f16 values
+// f16((n - 8) * scale) of the 4-bit cache (dequantised beforehand) and the key / value scale factors are 1
+// (KV_SCALE, src/cuda.rs:233), so ks / vs are null: scores are the plain dot products, P = f16(p * 2^10).
+template <typename KV_T>
+void decode_tc256(const float* qkv, long q_stride, const KV_T* kc, const KV_T* vc, const float* ks,
+                  const float* vs, long kv_stride, float* out, long out_stride, int pos0, int m, int n_heads, int n_kv,
+                  float scale, int nsplit, int want, int cap, int threads) {
     const int hd = 256, G = n_heads / n_kv;
     const float NEG = -std::numeric_limits<float>::infinity(), LN2 = 0.6931471805599453f, BIAS = 1024.f;
     const float qs = scale * 1.4426950408889634f;
@@ -423,10 +433,10 @@ void decode_tc256_i8(const float* qkv, long q_stride, const int8_t* kc, const in
                     for (int j = 0; j < 8; j++) {
                         int pa = tt + j;
                         if (pa >= len) { sc[j] = NEG; continue; }
-                        const int8_t* kr = kc + (long)(t0 + pa) * kv_stride + kvh * hd;
+                        const KV_T* kr = kc + (long)(t0 + pa) * kv_stride + kvh * hd;
                         float acc = 0.f;
-                        for (int d = 0; d < hd; d++) acc += qh[(size_t)g * hd + d] * (float)kr[d];
-                        sc[j] = acc * ks[(long)(t0 + pa) * n_kv + kvh];
+                        for (int d = 0; d < hd; d++) acc += qh[(size_t)g * hd + d] * kv_value(kr[d]);
+                        sc[j] = ks ? acc * ks[(long)(t0 + pa) * n_kv + kvh] : acc;
                         mx = std::max(mx, sc[j]);
                     }
                     float& mr = wm[w * G + g];
@@ -438,14 +448,14 @@ void decode_tc256_i8(const float* qkv, long q_stride, const int8_t* kc, const in
                     for (int j = 0; j < 8; j++) {
                         const float p = std::exp2(sc[j] - mn);
                         psum += p;
-                        const float v = tt + j < len ? vs[(long)(t0 + tt + j) * n_kv + kvh] * BIAS : 0.f;
+                        const float v = tt + j < len ? (vs ? vs[(long)(t0 + tt + j) * n_kv + kvh] : 1.f) * BIAS : 0.f;
                         pv[j] = f16_to_f32(f32_to_f16(p * v));
                     }
                     lr = lr * alpha + psum;
                     for (int d = 0; d < hd; d++) {
                         float a = o[d] * alpha;
                         for (int j = 0; j < 8; j++)
-                            if (tt + j < len) a += pv[j] * (float)vc[(long)(t0 + tt + j) * kv_stride + kvh * hd + d];
+                            if (tt + j < len) a += pv[j] * kv_value(vc[(long)(t0 + tt + j) * kv_stride + kvh * hd + d]);
                         o[d] = a;
                     }
                 }
@@ -549,11 +559,67 @@ void kv_quant_i8(const float* src, int hd, int8_t* dst, float* scale) {
     *scale = dd;
 }
 
+// ---------------------------------------------------------------- the 4-bit cache (KV4, src/cuda.rs:226-256)
+// kv4_fwht (src/cuda.rs:242-256): the normalized 256-point Walsh-Hadamard transform in Sylvester order, in place.
+// Butterfly stages h = 1, 2, ..., 128; within a stage element j (bit h of j clear) and j + h become a + c and
+// a - c; then every element times 1/16. Each stage's sums are single f32 additions, so any implementation with
+// the same stage order and pairing gives the same bits. hadamard_rows (src/cuda.rs:4675-4693), which rotates
+// the attention output back, is the same transform (block 256, no signs; its rsqrtf(256) taken as 1/16).
+void kv4_fwht(float* b) {
+    for (int h = 1; h < 256; h <<= 1)
+        for (int i = 0; i < 128; i++) {
+            const int j = (i / h) * 2 * h + (i % h);
+            const float a = b[j], c = b[j + h];
+            b[j] = a + c;
+            b[j + h] = a - c;
+        }
+    for (int i = 0; i < 256; i++) b[i] *= 0.0625f;
+}
+
+// kv_store's KV4 branch (src/cuda.rs:340-357) for one rotated row of 256 values: per group of 32 values
+// dh = f16(max|v| / 7) (IEEE division, then round to nearest even), dd = dh as f32, inv = 1/dd (0 when dd is 0),
+// q = clamp(rint(v * inv), -7, 7) stored as q + 8; byte i holds values 2i (low nibble) and 2i + 1 (high).
+void kv4_quant(const float* v, uint8_t* dst, uint16_t* sc) {
+    for (int g = 0; g < 8; g++) {
+        float amax = 0.f;
+        for (int d = 0; d < 32; d++) amax = std::max(amax, std::fabs(v[32 * g + d]));
+        const uint16_t dh = f32_to_f16(amax / 7.f);
+        const float dd = f16_to_f32(dh), inv = dd != 0.f ? 1.f / dd : 0.f;
+        for (int d = 0; d < 32; d += 2) {
+            auto q = [&](float x) { return (unsigned)(std::min(std::max(std::nearbyint(x * inv), -7.f), 7.f) + 8.f); };
+            dst[(32 * g + d) / 2] = (uint8_t)(q(v[32 * g + d]) | (q(v[32 * g + d + 1]) << 4));
+        }
+        sc[g] = dh;
+    }
+}
+
+// kv4_pair (src/cuda.rs:238-240): the stored nibble n of a group with scale bits s as the f16 f16((n - 8) * s).
+uint16_t kv4_value(unsigned n, uint16_t s) { return f32_to_f16((float)((int)n - 8) * f16_to_f32(s)); }
+
+// A 4-bit cache ([rows][n_kv][128] bytes, scales [rows][n_kv][8] f16) as the f16 rows [rows][n_kv * 256] the
+// tensor-core kernels stage (src/cuda.rs:2495-2514 for the prefill, 2681-2760 for the decode).
+std::vector<uint16_t> kv4_dequant(const uint8_t* c, const uint16_t* sc, long rows, int n_kv) {
+    std::vector<uint16_t> out((size_t)rows * n_kv * 256);
+    for (long r = 0; r < rows; r++)
+        for (int h = 0; h < n_kv; h++) {
+            const uint8_t* row = c + ((size_t)r * n_kv + h) * 128;
+            const uint16_t* s = sc + ((size_t)r * n_kv + h) * 8;
+            uint16_t* o = out.data() + ((size_t)r * n_kv + h) * 256;
+            for (int i = 0; i < 128; i++) {
+                o[2 * i] = kv4_value(row[i] & 15, s[i / 16]);
+                o[2 * i + 1] = kv4_value(row[i] >> 4, s[i / 16]);
+            }
+        }
+    return out;
+}
+
 // qk_norm_rope's arithmetic (src/cuda.rs:437-486); store(is_k, pos, kv_head, row) writes a k or v row
 // into the cache in its format.
+// rotate (the KV4 build, src/cuda.rs:472-479): q and k heads are rotated by kv4_fwht after RoPE (written back
+// rotated); the store rotates v rows itself.
 template <typename Store>
 void qk_norm_rope(float* qkv, const float* qn, const float* kn, int pos0, int n, int n_heads, int n_kv, int hd,
-                  int rope_dim, float base, const float* ff, int neox, float eps, Store store) {
+                  int rope_dim, float base, const float* ff, int neox, float eps, Store store, bool rotate = false) {
     const long q_dim = (long)n_heads * hd, kv_dim = (long)n_kv * hd, row_len = q_dim + 2 * kv_dim;
     for (int b = 0; b < n; b++) {
         const int pos = pos0 + b;
@@ -583,6 +649,7 @@ void qk_norm_rope(float* qkv, const float* qn, const float* kn, int pos0, int n,
                 vec[ia] = x * c - y * s;
                 vec[ib] = x * s + y * c;
             }
+            if (rotate) kv4_fwht(vec);
             if (h >= n_heads) store(1, pos, h - n_heads, vec);
         }
     }
@@ -659,8 +726,8 @@ void gio_decode_gpu_i8(const float* qkv, long q_stride, const int8_t* kc, const 
 void gio_decode_tc256_i8(const float* qkv, long q_stride, const int8_t* kc, const int8_t* vc, const float* ks,
                          const float* vs, long kv_stride, float* out, long out_stride, int pos0, int m, int n_heads,
                          int n_kv, float scale, int nsplit, int want, int cap, int threads) {
-    decode_tc256_i8(qkv, q_stride, kc, vc, ks, vs, kv_stride, out, out_stride, pos0, m, n_heads, n_kv, scale, nsplit,
-                    want, cap, threads);
+    decode_tc256<int8_t>(qkv, q_stride, kc, vc, ks, vs, kv_stride, out, out_stride, pos0, m, n_heads, n_kv, scale,
+                         nsplit, want, cap, threads);
 }
 
 void gio_kv_quant_i8(const float* src, long rows, int hd, int8_t* dst, float* scales) {
@@ -712,6 +779,60 @@ void gio_qk_norm_rope(float* qkv, const float* qn, const float* kn, uint16_t* kc
                      uint16_t* dst = (is_k ? kc : vc) + (long)pos * kv_stride + (long)h * kv_head_stride;
                      for (int d = 0; d < hd; d++) dst[d] = f32_to_f16(src[d]);
                  });
+}
+
+// kv4_fwht over `rows` rows of 256 values, in place (also hadamard_rows with block 256).
+void gio_kv4_fwht(float* x, long rows) {
+    for (long r = 0; r < rows; r++) kv4_fwht(x + r * 256);
+}
+
+// kv_store's KV4 branch over `rows` already-rotated rows of 256 values: dst 128 bytes a row, sc 8 f16 a row.
+void gio_kv4_quant(const float* src, long rows, uint8_t* dst, uint16_t* sc) {
+    for (long r = 0; r < rows; r++) kv4_quant(src + r * 256, dst + r * 128, sc + r * 8);
+}
+
+// The f16 values the kernels use for a 4-bit cache of `rows` rows (reference layout, n_kv heads a row).
+void gio_kv4_dequant(const uint8_t* c, const uint16_t* sc, long rows, int n_kv, uint16_t* out) {
+    std::vector<uint16_t> v = kv4_dequant(c, sc, rows, n_kv);
+    std::memcpy(out, v.data(), v.size() * sizeof(uint16_t));
+}
+
+// qk_norm_rope with the KV4 build (src/cuda.rs:437-486, 340-357): q and k heads rotated after RoPE, the k row
+// quantised as it is, a v row rotated and then quantised. Head size 256; the cache in the reference layout
+// (kc / vc [pos][n_kv][128] bytes, ks / vs [pos][n_kv][8] f16).
+void gio_qk_norm_rope_q4(float* qkv, const float* qn, const float* kn, uint8_t* kc, uint8_t* vc, uint16_t* ks,
+                         uint16_t* vs, int pos0, int n, int n_heads, int n_kv, int rope_dim, float base,
+                         const float* ff, int neox, float eps) {
+    qk_norm_rope(qkv, qn, kn, pos0, n, n_heads, n_kv, 256, rope_dim, base, ff, neox, eps,
+                 [&](int is_k, int pos, int h, const float* src) {
+                     float row[256];
+                     std::memcpy(row, src, sizeof row);
+                     if (!is_k) kv4_fwht(row);
+                     const long r = (long)pos * n_kv + h;
+                     kv4_quant(row, (is_k ? kc : vc) + r * 128, (is_k ? ks : vs) + r * 8);
+                 },
+                 true);
+}
+
+// attention_decode_tc256 with the KV4 build + attention_combine: the 4-bit cache dequantised to the f16
+// fragments, unit scales, P = f16(p * 2^10). q rows are the rotated queries; out is rotated (hadamard_rows
+// turns it back). rows: positions the cache holds (at least pos0 + m).
+void gio_decode_tc256_q4(const float* qkv, long q_stride, const uint8_t* kc, const uint8_t* vc, const uint16_t* ks,
+                         const uint16_t* vs, long rows, float* out, long out_stride, int pos0, int m, int n_heads,
+                         int n_kv, float scale, int nsplit, int want, int cap, int threads) {
+    std::vector<uint16_t> kh = kv4_dequant(kc, ks, rows, n_kv), vh = kv4_dequant(vc, vs, rows, n_kv);
+    decode_tc256<uint16_t>(qkv, q_stride, kh.data(), vh.data(), nullptr, nullptr, (long)n_kv * 256, out, out_stride,
+                           pos0, m, n_heads, n_kv, scale, nsplit, want, cap, threads);
+}
+
+// attention_prefill_tc256 with the KV4 build (src/cuda.rs:2495-2514): the tiles staged as the f16 values of the
+// 4-bit cache, then the f16 cache's arithmetic (P = f16(p), out = O / l).
+void gio_prefill_tc256_q4(const float* q, long q_stride, const uint8_t* kc, const uint8_t* vc, const uint16_t* ks,
+                          const uint16_t* vs, long rows, float* out, long out_stride, int pos0, int n, int n_heads,
+                          int n_kv, float scale, int threads) {
+    std::vector<uint16_t> kh = kv4_dequant(kc, ks, rows, n_kv), vh = kv4_dequant(vc, vs, rows, n_kv);
+    prefill_tc<uint16_t>(q, q_stride, kh.data(), vh.data(), nullptr, nullptr, (long)n_kv * 256, out, out_stride, pos0,
+                         n, n_heads, n_kv, scale, threads, 256);
 }
 
 } // extern "C"

@@ -51,6 +51,12 @@ def lib():
         L.gio_kv_quant_i8.argtypes = [vp, l, i, vp, vp]
         L.gio_prefill_tc_i8.argtypes = [vp, l, vp, vp, vp, vp, l, vp, l, i, i, i, i, f, i]
         L.gio_prefill_tc256.argtypes = [vp, l, vp, vp, l, vp, l, i, i, i, i, f, i]
+        L.gio_kv4_fwht.argtypes = [vp, l]
+        L.gio_kv4_quant.argtypes = [vp, l, vp, vp]
+        L.gio_kv4_dequant.argtypes = [vp, vp, l, i, vp]
+        L.gio_qk_norm_rope_q4.argtypes = [vp, vp, vp, vp, vp, vp, vp, i, i, i, i, i, f, vp, i, f]
+        L.gio_decode_tc256_q4.argtypes = [vp, l, vp, vp, vp, vp, l, vp, l, i, i, i, i, f, i, i, i, i]
+        L.gio_prefill_tc256_q4.argtypes = [vp, l, vp, vp, vp, vp, l, vp, l, i, i, i, i, f, i]
         _lib = L
     return _lib
 
@@ -179,6 +185,92 @@ def kv_quant_i8(x):
     sc = np.empty(x.shape[:-1], dtype=np.float32)
     lib().gio_kv_quant_i8(_p(x), rows, hd, _p(q), _p(sc))
     return q, sc
+
+
+def kv4_fwht(x):
+    """kv4_fwht (src/cuda.rs:242-256) over rows of 256 values: the normalized Walsh-Hadamard transform, Sylvester
+    order, in the reference's butterfly order (also hadamard_rows with block 256, src/cuda.rs:4675-4693)."""
+    x = np.array(x, dtype=np.float32, order="C", copy=True)
+    assert x.shape[-1] == 256
+    lib().gio_kv4_fwht(_p(x), x.size // 256)
+    return x
+
+
+def kv4_quant(x):
+    """kv_store with KV4 (src/cuda.rs:340-357) over already-rotated rows of 256 values: returns (uint8 [..., 128]
+    nibble pairs, uint16 [..., 8] f16 scale bits)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    assert x.shape[-1] == 256
+    rows = x.size // 256
+    q = np.empty(x.shape[:-1] + (128,), dtype=np.uint8)
+    sc = np.empty(x.shape[:-1] + (8,), dtype=np.uint16)
+    lib().gio_kv4_quant(_p(x), rows, _p(q), _p(sc))
+    return q, sc
+
+
+def kv4_dequant(c, sc, n_kv):
+    """The f16 values (uint16 bits, [rows, n_kv*256]) the tensor-core kernels use for a 4-bit cache
+    (kv4_pair, src/cuda.rs:238-240): f16((n - 8) * scale). c: uint8 [rows, n_kv*128]; sc: uint16 [rows, n_kv*8]."""
+    c = np.ascontiguousarray(c, dtype=np.uint8).reshape(-1, n_kv * 128)
+    sc = np.ascontiguousarray(sc, dtype=np.uint16).reshape(-1, n_kv * 8)
+    out = np.empty((c.shape[0], n_kv * 256), dtype=np.uint16)
+    lib().gio_kv4_dequant(_p(c), _p(sc), c.shape[0], n_kv, _p(out))
+    return out
+
+
+def qk_norm_rope_q4(qkv, kc, vc, ks, vs, pos0, n_heads, n_kv, rope_dim=None, base=10000.0, qn=None, kn=None, ff=None,
+                    neox=True, eps=1e-6):
+    """qk_norm_rope with the KV4 build (src/cuda.rs:437-486, 340-357): q and k heads rotated after RoPE (written
+    back rotated), k rows quantised, v rows rotated then quantised. Head size 256; caches in the reference layout:
+    kc/vc uint8 [pos, n_kv*128], ks/vs uint16 f16 bits [pos, n_kv*8]. Returns (qkv, kc, vc, ks, vs) copies."""
+    qkv = np.array(qkv, dtype=np.float32, order="C", copy=True)
+    kc = np.array(kc, dtype=np.uint8, order="C", copy=True)
+    vc = np.array(vc, dtype=np.uint8, order="C", copy=True)
+    ks = np.array(ks, dtype=np.uint16, order="C", copy=True)
+    vs = np.array(vs, dtype=np.uint16, order="C", copy=True)
+    n = qkv.shape[0]
+    rope_dim = 256 if rope_dim is None else rope_dim
+    opts = [None if a is None else np.ascontiguousarray(a, dtype=np.float32) for a in (qn, kn, ff)]
+    ptrs = [None if a is None else _p(a) for a in opts]
+    lib().gio_qk_norm_rope_q4(_p(qkv), ptrs[0], ptrs[1], _p(kc), _p(vc), _p(ks), _p(vs), pos0, n, n_heads, n_kv,
+                              rope_dim, base, ptrs[2], 1 if neox else 0, eps)
+    return qkv, kc, vc, ks, vs
+
+
+def decode_tc256_q4(q, kc, vc, ks, vs, pos0, n_heads, n_kv, scale=None, cap=128, threads=8, want=None):
+    """attention_decode_tc256 with the KV4 build (src/cuda.rs:2681-2760) + attention_combine, over rotated queries:
+    the output is rotated (kv4_fwht turns it back, as hadamard_rows does). kc/vc uint8 [pos, n_kv*128], ks/vs
+    uint16 [pos, n_kv*8]."""
+    q = _rows(q, np.float32)
+    m = q.shape[0]
+    kc, vc = _rows(kc, np.uint8), _rows(vc, np.uint8)
+    ks, vs = _rows(ks, np.uint16), _rows(vs, np.uint16)
+    assert kc.shape[1] == n_kv * 128 and ks.shape == (kc.shape[0], n_kv * 8) and vs.shape == ks.shape
+    assert kc.shape[0] >= pos0 + m
+    if scale is None:
+        scale = 1.0 / 16.0
+    want = att_want(n_kv) if want is None else want
+    nsplit = max(-(-span // att_chunk(span, want, cap)) for span in range(pos0 + 1, pos0 + m + 1))
+    out = np.zeros((m, n_heads * 256), dtype=np.float32)
+    lib().gio_decode_tc256_q4(_p(q), q.shape[1], _p(kc), _p(vc), _p(ks), _p(vs), kc.shape[0], _p(out), out.shape[1],
+                              pos0, m, n_heads, n_kv, scale, nsplit, want, cap, threads)
+    return out
+
+
+def prefill_tc256_q4(q, kc, vc, ks, vs, pos0, n_heads, n_kv, scale=None, threads=8):
+    """attention_prefill_tc256 with the KV4 build (src/cuda.rs:2495-2514): the f16 cache's arithmetic over the
+    4-bit cache's f16 values. Rotated queries in, rotated output out."""
+    q = _rows(q, np.float32)
+    n = q.shape[0]
+    kc, vc = _rows(kc, np.uint8), _rows(vc, np.uint8)
+    ks, vs = _rows(ks, np.uint16), _rows(vs, np.uint16)
+    assert kc.shape[1] == n_kv * 128 and ks.shape == (kc.shape[0], n_kv * 8) and kc.shape[0] >= pos0 + n
+    if scale is None:
+        scale = 1.0 / 16.0
+    out = np.zeros((n, n_heads * 256), dtype=np.float32)
+    lib().gio_prefill_tc256_q4(_p(q), q.shape[1], _p(kc), _p(vc), _p(ks), _p(vs), kc.shape[0], _p(out), out.shape[1],
+                               pos0, n, n_heads, n_kv, scale, threads)
+    return out
 
 
 def prefill_tc_semantics(q, kc, vc, pos0, n_heads, n_kv, scale=None, threads=8, hd=128):

@@ -70,6 +70,41 @@ def reference_f64_i8(q, kc, vc, ks, vs, pos0, n_heads, n_kv, hd=128, scale=None)
                                  hd, scale)
 
 
+def make_inputs_q4(seed, n_tok, ctx, n_heads, n_kv):
+    """Seeded 4-bit-cache inputs (head size 256, the reference layout): q f32 [n_tok, n_heads*256] N(0,1); K/V
+    uint8 [ctx, n_kv*128] of random nibbles 1..15 (stored q + 8 for q in -7..7); scales f16 bits [ctx, n_kv*8]
+    uniform in [0.2, 0.35] (dequantised values have a standard deviation near 1). One generator per tensor:
+    seed .. seed + 4."""
+    q = np.random.default_rng(seed).standard_normal((n_tok, n_heads * 256), dtype=np.float32)
+
+    def nibbles(g):
+        n = np.random.default_rng(g).integers(1, 16, (ctx, n_kv * 256), dtype=np.uint8)
+        return (n[:, 0::2] | (n[:, 1::2] << 4)).astype(np.uint8)
+
+    def scales(g):
+        return np.random.default_rng(g).uniform(0.2, 0.35, (ctx, n_kv * 8)).astype(np.float16).view(np.uint16)
+
+    return q, nibbles(seed + 1), nibbles(seed + 2), scales(seed + 3), scales(seed + 4)
+
+
+def dequant_q4(c, sc, n_kv):
+    """The f16 values of a 4-bit cache as float64 [rows, n_kv*256]: value 2i of a row is byte i's low nibble, 2i + 1
+    its high nibble, each n - 8 times the f16 scale of its group of 32, rounded to f16 (kv4_pair)."""
+    c = np.asarray(c, dtype=np.uint8).reshape(-1, n_kv * 128)
+    n = np.empty((c.shape[0], n_kv * 256), dtype=np.int32)
+    n[:, 0::2] = c & 15
+    n[:, 1::2] = c >> 4
+    s = np.asarray(sc, dtype=np.uint16).reshape(c.shape[0], n_kv * 8).view(np.float16).astype(np.float32)
+    prod = (n - 8).astype(np.float32) * np.repeat(s, 32, axis=1)
+    return prod.astype(np.float16).astype(np.float64)
+
+
+def reference_f64_q4(q, kc, vc, ks, vs, pos0, n_heads, n_kv, scale=None):
+    """reference_f64 over the f16 values of a 4-bit cache (rotated queries give rotated outputs)."""
+    return _reference_f64_values(q, dequant_q4(kc, ks, n_kv), dequant_q4(vc, vs, n_kv), pos0, n_heads, n_kv, 256,
+                                 scale)
+
+
 def _reference_f64_values(q, k, v, pos0, n_heads, n_kv, hd=128, scale=None):
     q = np.asarray(q, dtype=np.float64).reshape(q.shape[0], n_heads, hd)
     n = q.shape[0]

@@ -18,7 +18,8 @@ import pytest
 import torch
 
 import gi_oracle as O
-from attn_common import assert_close, errors, make_inputs, make_inputs_i8, reference_f64, reference_f64_i8
+from attn_common import (assert_close, errors, make_inputs, make_inputs_i8, make_inputs_q4, reference_f64, reference_f64_i8,
+                         reference_f64_q4)
 
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
 
@@ -541,3 +542,184 @@ def test_prefill_tc_semantics_hd256_within_parity_bar(n, pos0, n_heads, n_kv):
     got2 = O.prefill_tc_semantics(q, k, v2.reshape(v.shape), pos0, n_heads, n_kv, hd=256).reshape(n, n_heads, 256)
     np.testing.assert_array_equal(got2[:, :, :128], got.reshape(n, n_heads, 256)[:, :, :128])
     assert not got2[:, :, 128:].any()
+
+
+# ---------------------------------------------------------------- the 4-bit cache (KV4)
+
+def _sylvester(n):
+    """H[i][j] = (-1)^popcount(i & j): the unnormalized Sylvester-order Walsh-Hadamard matrix."""
+    i = np.arange(n)
+    bits = np.vectorize(lambda x: bin(x).count("1"))(i[:, None] & i[None, :])
+    return np.where(bits % 2 == 0, 1, -1).astype(np.int64)
+
+
+def test_kv4_fwht_matches_the_matrix_and_is_its_own_inverse():
+    # src/hadamard.rs:201-219's test (x_i = sin(0.37 i), the matrix (-1)^popcount(i&j) / sqrt(n), applied twice
+    # gives x back) at the cache's 256 points
+    x = np.sin(np.arange(256) * 0.37).astype(np.float32)[None, :]
+    y = O.kv4_fwht(x)
+    want = (_sylvester(256) @ x[0].astype(np.float64)) / 16.0
+    np.testing.assert_allclose(y[0], want, rtol=0, atol=1e-5)
+    np.testing.assert_allclose(O.kv4_fwht(y), x, rtol=0, atol=1e-5)
+
+
+def test_kv4_fwht_exact_on_integers_and_unit_vectors():
+    # small integers: every butterfly sum is exact in f32 and so is the 1/16, so the result equals the integer
+    # matrix product / 16 bit for bit (any order of the stages would); unit vector e_j gives column j / 16
+    rng = np.random.default_rng(5)
+    x = rng.integers(-1000, 1000, (6, 256)).astype(np.float32)
+    want = (x.astype(np.int64) @ _sylvester(256).T).astype(np.float64) / 16.0
+    np.testing.assert_array_equal(O.kv4_fwht(x), want.astype(np.float32))
+    e = np.eye(256, dtype=np.float32)[[0, 1, 37, 255]]
+    np.testing.assert_array_equal(O.kv4_fwht(e), (_sylvester(256)[[0, 1, 37, 255]] / 16.0).astype(np.float32))
+
+
+def _f16_bits(x):
+    return int(np.array(x, dtype=np.float32).astype(np.float16).view(np.uint16))
+
+
+def test_kv4_quant_by_hand():
+    # group 0: max 7 -> scale f16(1) = 1, inv 1: 7 -> 15, -7 -> 1, 3.5 -> rint 4 (ties to even) -> 12, 2.5 -> 2
+    # -> 10, -0.5 -> -0 -> 8, 0.49 -> 8. Byte i = value 2i (low nibble) | value 2i + 1 << 4.
+    row = np.zeros(256, np.float32)
+    row[:6] = [7, -7, 3.5, 2.5, -0.5, 0.49]
+    # group 1 (values 32..63): max 1 -> dh = f16(1/7) = 0.142822265625 (rounded down), inv = 7.0017...:
+    # 0.3571 * inv = 2.5003 -> 3, where an unrounded scale (inv = 7) gives 2.4997 -> 2
+    row[32], row[33] = 1.0, 0.3571
+    # group 2: all zero -> scale 0, inv 0, every value stored as 8
+    # group 3: a max whose /7 falls below f16's smallest subnormal -> scale 0 -> every value 8
+    row[96], row[97] = 1e-9, -1e-9
+    # group 4: -3 max -> dh = f16(3/7) = 0.428466796875 (rounded down), inv = 2.33390: -3 -> -7.0017 -> -7 (nibble
+    # 1), 1.5 -> 3.5009 -> 4 (nibble 12)
+    row[128], row[129] = -3.0, 1.5
+    q, sc = O.kv4_quant(row[None, :])
+    q, sc = q[0], sc[0]
+    assert list(q[:3]) == [15 | (1 << 4), 12 | (10 << 4), 8 | (8 << 4)]
+    assert sc[0] == _f16_bits(1.0)
+    assert sc[1] == _f16_bits(1.0 / 7.0) == 0x3092
+    assert q[16] == 15 | (11 << 4)
+    assert sc[2] == 0 and np.all(q[32:48] == 0x88)
+    assert sc[3] == 0 and np.all(q[48:64] == 0x88)
+    assert sc[4] == _f16_bits(np.float32(3.0) / np.float32(7.0))
+    assert sc[4] == 0x36DB and q[64] == 1 | (12 << 4)
+    assert np.all(q[65:] == 0x88) and np.all(q[3:16] == 0x88)
+
+
+def test_kv4_quant_error_bound_and_dequant_order():
+    # every dequantised value is within half a step (plus the f16 rounding) of the input, the nibble order is
+    # value 2i low / 2i + 1 high, and each group of 32 has its own scale
+    x = np.random.default_rng(2).standard_normal((40, 256)).astype(np.float32) * np.repeat(
+        np.random.default_rng(3).uniform(0.1, 3, (40, 8)), 32, axis=1).astype(np.float32)
+    q, sc = O.kv4_quant(x)
+    deq = O.kv4_dequant(q, sc, 1).view(np.float16).astype(np.float64)
+    step = np.repeat(sc.view(np.float16).astype(np.float64), 32, axis=1)
+    assert np.all(np.abs(deq - x) <= 0.5 * step + np.abs(x) * 2.0 ** -10 + 1e-7)
+    from attn_common import dequant_q4
+    np.testing.assert_array_equal(deq, dequant_q4(q, sc, 1))
+
+
+def test_rope_q4_rotates_q_and_k_and_quantises_the_rotated_rows():
+    # the KV4 build's qk_norm_rope = the f16 build's qk_norm_rope, then kv4_fwht of every q and k head; the cache
+    # holds kv4_quant of the rotated k rows and of the rotated v rows
+    n, H, K, pos0, ctx = 5, 4, 2, 9, 16
+    rng = np.random.default_rng(4)
+    qkv = rng.standard_normal((n, (H + 2 * K) * 256)).astype(np.float32)
+    qn = rng.uniform(0.5, 1.5, 256).astype(np.float32)
+    kn = rng.uniform(0.5, 1.5, 256).astype(np.float32)
+    z8 = np.zeros((ctx, K * 128), np.uint8)
+    z16 = np.zeros((ctx, K * 8), np.uint16)
+    got, kc, vc, ks, vs = O.qk_norm_rope_q4(qkv, z8, z8, z16, z16, pos0, H, K, qn=qn, kn=kn)
+    f16c = np.zeros((ctx, K * 256), np.uint16)
+    plain, _, _ = O.qk_norm_rope(qkv, f16c, f16c, pos0, H, K, hd=256, qn=qn, kn=kn)
+    qk = plain[:, :(H + K) * 256].reshape(n * (H + K), 256)
+    np.testing.assert_array_equal(got[:, :(H + K) * 256], O.kv4_fwht(qk).reshape(n, -1))
+    np.testing.assert_array_equal(got[:, (H + K) * 256:], qkv[:, (H + K) * 256:])  # v heads pass unchanged
+    kq, ksq = O.kv4_quant(got[:, H * 256:(H + K) * 256].reshape(n * K, 256))
+    vq, vsq = O.kv4_quant(O.kv4_fwht(qkv[:, (H + K) * 256:].reshape(n * K, 256)))
+    np.testing.assert_array_equal(kc[pos0:pos0 + n], kq.reshape(n, -1))
+    np.testing.assert_array_equal(ks[pos0:pos0 + n], ksq.reshape(n, -1))
+    np.testing.assert_array_equal(vc[pos0:pos0 + n], vq.reshape(n, -1))
+    np.testing.assert_array_equal(vs[pos0:pos0 + n], vsq.reshape(n, -1))
+    assert not kc[:pos0].any() and not vs[pos0 + n:].any()
+
+
+def _q4_of_ints(ints, n_kv):
+    """A 4-bit cache holding the integers `ints` (-7..7, [rows, n_kv*256]) with unit scales."""
+    n = (ints.astype(np.int32) + 8).astype(np.uint8)
+    return (n[:, 0::2] | (n[:, 1::2] << 4)).astype(np.uint8), np.full((ints.shape[0], n_kv * 8), 0x3C00, np.uint16)
+
+
+def test_decode_tc256_q4_unit_scales_equal_the_int8_path():
+    # integer values with unit scales: the 4-bit cache's f16 values are the integers themselves, so the KV4
+    # decode equals the KV8 decode (pinned by hand above) with int8 rows of those integers and scales 1, bit for bit
+    H, K, pos0, m = 16, 2, 700, 3
+    rng = np.random.default_rng(8)
+    q = rng.standard_normal((m, H * 256)).astype(np.float32)
+    ki = rng.integers(-7, 8, (pos0 + m, K * 256)).astype(np.int8)
+    vi = rng.integers(-7, 8, (pos0 + m, K * 256)).astype(np.int8)
+    kc, ks = _q4_of_ints(ki, K)
+    vc, vs = _q4_of_ints(vi, K)
+    ones = np.ones((pos0 + m, K), np.float32)
+    got = O.decode_tc256_q4(q, kc, vc, ks, vs, pos0, H, K)
+    want = O.decode_tc256_i8(q, ki, vi, ones, ones, pos0, H, K)
+    np.testing.assert_array_equal(got, want)
+
+
+@pytest.mark.parametrize("n_tok,pos0,n_heads,n_kv", [(1, 5, 16, 2), (1, 300, 16, 2), (8, 2000, 16, 2), (3, 77, 8, 1)])
+def test_decode_tc256_q4_within_parity_bar(n_tok, pos0, n_heads, n_kv):
+    q, kc, vc, ks, vs = make_inputs_q4(131 + pos0, n_tok, pos0 + n_tok, n_heads, n_kv)
+    got = O.decode_tc256_q4(q, kc, vc, ks, vs, pos0, n_heads, n_kv)
+    want = reference_f64_q4(q, kc, vc, ks, vs, pos0, n_heads, n_kv)
+    ma, _ = assert_close(got, want, what="decode_tc256 KV4 semantics vs f64")
+    assert ma > 1e-6
+
+
+def test_decode_q4_rotation_gives_the_unrotated_attention():
+    # rows rotated, quantised, attended with rotated queries and the output rotated back: the attention of the
+    # original rows, to within the 4-bit rounding (closed form: one position gives its V row back)
+    H, K, n = 8, 1, 200
+    rng = np.random.default_rng(12)
+    q = rng.standard_normal((1, H * 256)).astype(np.float32)
+    k = rng.standard_normal((n, K * 256)).astype(np.float32)
+    v = rng.standard_normal((n, K * 256)).astype(np.float32)
+    kc, ks = O.kv4_quant(O.kv4_fwht(k.reshape(-1, 256)))
+    vc, vs = O.kv4_quant(O.kv4_fwht(v.reshape(-1, 256)))
+    qr = O.kv4_fwht(q.reshape(-1, 256)).reshape(1, -1)
+    out = O.decode_tc256_q4(qr, kc.reshape(n, -1), vc.reshape(n, -1), ks.reshape(n, -1), vs.reshape(n, -1), n - 1, H, K)
+    back = O.kv4_fwht(out.reshape(-1, 256)).reshape(1, -1)
+    exact = _reference_f64_plain(q, k, v, n - 1, H, K)
+    ma, _ = errors(back, exact)
+    assert ma < 0.1  # 4-bit rows: about 2^-4 of the value range
+    one = O.decode_tc256_q4(qr, kc.reshape(n, -1)[:1], vc.reshape(n, -1)[:1], ks.reshape(n, -1)[:1],
+                            vs.reshape(n, -1)[:1], 0, H, K)
+    v0 = O.kv4_dequant(vc.reshape(n, -1)[:1], vs.reshape(n, -1)[:1], K).view(np.float16).astype(np.float32)
+    np.testing.assert_array_equal(one.reshape(H, 256), np.broadcast_to(v0, (H, 256)))
+
+
+def _reference_f64_plain(q, k, v, pos0, n_heads, n_kv):
+    from attn_common import _reference_f64_values
+    return _reference_f64_values(q, k, v, pos0, n_heads, n_kv, 256)
+
+
+def test_prefill_tc256_q4_unit_scales_equal_the_f16_path():
+    # integer values with unit scales: the KV4 prefill stages exactly the f16 cache holding those integers
+    H, K, pos0, n = 4, 2, 40, 70
+    rng = np.random.default_rng(9)
+    q = rng.standard_normal((n, H * 256)).astype(np.float32)
+    ki = rng.integers(-7, 8, (pos0 + n, K * 256))
+    vi = rng.integers(-7, 8, (pos0 + n, K * 256))
+    kc, ks = _q4_of_ints(ki, K)
+    vc, vs = _q4_of_ints(vi, K)
+    got = O.prefill_tc256_q4(q, kc, vc, ks, vs, pos0, H, K)
+    want = O.prefill_tc_semantics(q, ki.astype(np.float16).view(np.uint16), vi.astype(np.float16).view(np.uint16),
+                                  pos0, H, K, hd=256)
+    np.testing.assert_array_equal(got, want)
+
+
+@pytest.mark.parametrize("n,pos0,n_heads,n_kv", [(48, 0, 4, 2), (70, 33, 8, 1)])
+def test_prefill_tc256_q4_within_parity_bar(n, pos0, n_heads, n_kv):
+    q, kc, vc, ks, vs = make_inputs_q4(77 + n, n, pos0 + n, n_heads, n_kv)
+    got = O.prefill_tc256_q4(q, kc, vc, ks, vs, pos0, n_heads, n_kv)
+    want = reference_f64_q4(q, kc, vc, ks, vs, pos0, n_heads, n_kv)
+    ma, _ = assert_close(got, want, what="prefill_tc256 KV4 semantics vs f64")
+    assert ma > 1e-6
