@@ -71,7 +71,7 @@ struct GiRopeArgs {
     float base;
     float eps;
     int neox;
-    int i8;
+    int fmt; // 0 f16, 1 int8, 2 the 4-bit cache
     float* ks;
     float* vs;
     long long sc_stride;
@@ -157,7 +157,8 @@ struct Module {
     hipFunction_t dec256[2] = {};     // up to 8 pairs, head size 256: [int8 cache]
     hipFunction_t dec_pm[2][2] = {};  // [int8 cache][column blocks - 1]: one pair per column
     hipFunction_t dec_ws2[2] = {};    // head size 128, two column blocks, two pair sets of two waves: [int8 cache]
-    hipFunction_t dec_pm256[2] = {};  // head size 256, one pair per column, 4 waves sharing each tile: [int8 cache]
+    hipFunction_t dec_pm256[2] = {};
+    hipFunction_t dec_q4[2] = {};     // head size 256 over the 4-bit cache: [one pair per column]  // head size 256, one pair per column, 4 waves sharing each tile: [int8 cache]
     hipFunction_t prefill[2] = {};   // [int8 cache], head size 128
     hipFunction_t prefill256r = nullptr; // head size 256 (f16 cache), 16 rows per wave: one workgroup per query tile
     hipFunction_t combine = nullptr, rope = nullptr, relayout = nullptr;
@@ -206,6 +207,8 @@ int load_module(const char* path, Module** out) {
             {&m.dec_ws2[1], "gi_decode_pm_ws2_2_i8"},
             {&m.dec_pm256[0], "gi_decode_pm_shared_1_h256"},
             {&m.dec_pm256[1], "gi_decode_pm_shared_1_i8_h256"},
+            {&m.dec_q4[0], "gi_decode_partial_1_q4"},
+            {&m.dec_q4[1], "gi_decode_pm_shared_1_q4"},
             {&m.combine, "gi_decode_combine"},
             {&m.relayout, "gi_kv_relayout"},
             {&m.prefill[0], "gi_prefill_fwd"},
@@ -379,18 +382,30 @@ int check_shape(int n_heads, int n_kv, int hd, bool hd256 = false) {
     return 0;
 }
 
-// gi_attn_decode and gi_attn_decode_i8: the same launch with the f16 or the int8 kernels.
+// gi_attn_decode, gi_attn_decode_i8 and gi_attn_decode_q4: the same launch with the f16, int8 or 4-bit kernels
+// (fmt 0, 1, 2).
 int decode_impl(void* stream, const float* q, long long q_stride, const void* kc, const void* vc, const float* ks,
-                const float* vs, long long sc_stride, long long sc_head_stride, bool i8, long long kv_stride,
+                const float* vs, long long sc_stride, long long sc_head_stride, int fmt, long long kv_stride,
                 long long kv_head_stride, float* out, long long out_stride, void* workspace, size_t workspace_bytes,
                 int pos0, const int* posp, int ctx_cap, int n_tok, int n_heads, int n_kv, int hd, float scale) {
     if (int e = check_shape(n_heads, n_kv, hd, true)) return e;
+    if (fmt == 2 && hd != 256) return fail("the 4-bit cache takes head size 256 only (got %d)", hd);
+    const bool i8 = fmt == 1;
     if (n_tok <= 0) return fail("n_tok %d must be positive", n_tok);
     if (!q || !kc || !vc || !out) return fail("null tensor pointer");
-    if (kv_head_stride == 0) kv_head_stride = hd;
-    if (int e = check_kv_strides(kv_stride, kv_head_stride, n_kv, hd, i8 ? 16 : 8)) return e;
-    if (i8)
-        if (int e = check_scales(ks, vs, sc_stride, sc_head_stride)) return e;
+    if (fmt == 2) {
+        // rows of 128 bytes (kv strides in bytes), 8 f16 scales a row (scale strides in f16 elements)
+        if (kv_head_stride == 0) kv_head_stride = hd / 2;
+        if (int e = check_kv_strides(kv_stride, kv_head_stride, n_kv, hd / 2, 16)) return e;
+        if (!ks || !vs) return fail("null scale pointer");
+        if (((uintptr_t)ks & 1) || ((uintptr_t)vs & 1)) return fail("ks and vs must be 2-byte aligned");
+        if (int e = check_kv_strides(sc_stride, sc_head_stride, n_kv, 8, 1)) return e;
+    } else {
+        if (kv_head_stride == 0) kv_head_stride = hd;
+        if (int e = check_kv_strides(kv_stride, kv_head_stride, n_kv, hd, fmt ? 16 : 8)) return e;
+        if (fmt)
+            if (int e = check_scales(ks, vs, sc_stride, sc_head_stride)) return e;
+    }
     if (!aligned16(q) || !aligned16(kc) || !aligned16(vc) || q_stride % 4)
         return fail("q, kc, vc must be 16-byte aligned and q_stride a multiple of 4");
     if (q_stride < (long long)n_heads * hd || out_stride < (long long)n_heads * hd)
@@ -424,23 +439,29 @@ int decode_impl(void* stream, const float* q, long long q_stride, const void* kc
     a.n_kv = n_kv;
     a.qscale = scale * kLog2e;
     a.hd = hd;
-    if (i8) {
+    if (fmt) {
         a.ks = ks;
         a.vs = vs;
         a.sc_stride = sc_stride;
         a.sc_head_stride = sc_head_stride;
     }
     hipStream_t st = (hipStream_t)stream;
-    hipFunction_t f = hd == 256 ? (var.pm ? m->dec_pm256[i8] : m->dec256[i8]) : var.ws2 ? m->dec_ws2[i8] : var.pm ? m->dec_pm[i8][var.ncb - 1] : m->dec[i8];
+    hipFunction_t f = fmt == 2    ? m->dec_q4[var.pm]
+                      : hd == 256 ? (var.pm ? m->dec_pm256[i8] : m->dec256[i8])
+                      : var.ws2   ? m->dec_ws2[i8]
+                      : var.pm    ? m->dec_pm[i8][var.ncb - 1]
+                                  : m->dec[i8];
     if (int e = launch(kDecodePartial, f, dim3(a.nsplit, n_kv, var.groups), dim3(256), st, &a, sizeof a)) return e;
     if (a.nsplit == 1) return 0;
     return launch(kDecodeCombine, m->combine, dim3(n_heads, n_tok, kCombineSplit * hd / 128), dim3(64), st, &a, sizeof a);
 }
 
-// gi_qk_norm_rope and gi_qk_norm_rope_i8: one kernel, f16 or int8 cache rows.
+// gi_qk_norm_rope, gi_qk_norm_rope_i8 and gi_qk_norm_rope_q4: one kernel; fmt 0 f16, 1 int8, 2 the 4-bit cache.
 int rope_impl(void* stream, float* qkv, const float* qn, const float* kn, void* kc, void* vc, float* ks, float* vs,
-              long long sc_stride, long long sc_head_stride, bool i8, long long kv_stride, long long kv_head_stride, int pos0, const int* posp, int ctx_cap, int n,
-              int n_heads, int n_kv, int hd, int rope_dim, float base, const float* ff, int neox, float eps) {
+              long long sc_stride, long long sc_head_stride, int fmt, long long kv_stride, long long kv_head_stride,
+              int pos0, const int* posp, int ctx_cap, int n, int n_heads, int n_kv, int hd, int rope_dim, float base,
+              const float* ff, int neox, float eps) {
+    if (fmt == 2 && hd != 256) return fail("the 4-bit cache takes head size 256 only (got %d)", hd);
     if (hd != 64 && hd != 128 && hd != 256) return fail("head size %d unsupported by the KV store (64, 128, 256)", hd);
     if (n_kv <= 0 || n_heads <= 0 || n_heads % n_kv != 0)
         return fail("n_heads %d must be a positive multiple of n_kv %d", n_heads, n_kv);
@@ -452,10 +473,19 @@ int rope_impl(void* stream, float* qkv, const float* qn, const float* kn, void* 
     if (posp && ctx_cap < n) return fail("with posp, ctx_cap %d must cover the %d tokens", ctx_cap, n);
     if (!posp && ctx_cap > 0 && ctx_cap < pos0 + n)
         return fail("positions %d..%d exceed ctx_cap %d", pos0, pos0 + n - 1, ctx_cap);
-    if (kv_head_stride == 0) kv_head_stride = hd;
-    if (int e = check_kv_strides(kv_stride, kv_head_stride, n_kv, hd, i8 ? 16 : 8)) return e;
-    if (i8)
-        if (int e = check_scales(ks, vs, sc_stride, sc_head_stride)) return e;
+    if (fmt == 2) {
+        // rows of 128 bytes (kv strides in bytes), 8 f16 scales a row (scale strides in f16 elements)
+        if (kv_head_stride == 0) kv_head_stride = hd / 2;
+        if (int e = check_kv_strides(kv_stride, kv_head_stride, n_kv, hd / 2, 16)) return e;
+        if (!ks || !vs) return fail("null scale pointer");
+        if (((uintptr_t)ks & 1) || ((uintptr_t)vs & 1)) return fail("ks and vs must be 2-byte aligned");
+        if (int e = check_kv_strides(sc_stride, sc_head_stride, n_kv, 8, 1)) return e;
+    } else {
+        if (kv_head_stride == 0) kv_head_stride = hd;
+        if (int e = check_kv_strides(kv_stride, kv_head_stride, n_kv, hd, fmt ? 16 : 8)) return e;
+        if (fmt)
+            if (int e = check_scales(ks, vs, sc_stride, sc_head_stride)) return e;
+    }
     Module* m;
     if (int e = load_module(nullptr, &m)) return e;
     GiRopeArgs a{};
@@ -465,7 +495,7 @@ int rope_impl(void* stream, float* qkv, const float* qn, const float* kn, void* 
     a.kn = kn;
     a.kc = (uint16_t*)kc;
     a.vc = (uint16_t*)vc;
-    a.i8 = i8;
+    a.fmt = fmt;
     a.ks = ks;
     a.vs = vs;
     a.sc_stride = sc_stride;
@@ -488,20 +518,33 @@ int rope_impl(void* stream, float* qkv, const float* qn, const float* kn, void* 
     return launch(kRope, m->rope, dim3(groups, n, 1), dim3(256), (hipStream_t)stream, &a, sizeof a);
 }
 
-// gi_attn_prefill and gi_attn_prefill_i8: the same launch with the f16 or the int8 kernel.
+// gi_attn_prefill, gi_attn_prefill_i8 and gi_attn_prefill_q4: the same launch with the f16, int8 or 4-bit kernel
+// (fmt 0, 1, 2).
 int prefill_impl(void* stream, const void* q, int q_dtype, long long q_stride, const void* kc, const void* vc,
-                 const float* ks, const float* vs, long long sc_stride, long long sc_head_stride, bool i8,
+                 const float* ks, const float* vs, long long sc_stride, long long sc_head_stride, int fmt,
                  long long kv_stride, long long kv_head_stride, void* out, int out_dtype, long long out_stride, int pos0,
                  int n, int n_heads, int n_kv, int hd, float scale) {
+    const bool i8 = fmt == 1;
     if (int e = check_shape(n_heads, n_kv, hd, !i8)) return e;
+    if (fmt == 2 && hd != 256) return fail("the 4-bit cache takes head size 256 only (got %d)", hd);
+    if (fmt == 2) return fail("the 4-bit prefill kernel is not built");
     if (n <= 0 || pos0 < 0) return fail("n %d must be positive and pos0 %d >= 0", n, pos0);
     if (!q || !kc || !vc || !out) return fail("null tensor pointer");
     if ((q_dtype != GI_F32 && q_dtype != GI_F16) || (out_dtype != GI_F32 && out_dtype != GI_F16))
         return fail("dtypes must be GI_F32 or GI_F16");
-    if (kv_head_stride == 0) kv_head_stride = hd;
-    if (int e = check_kv_strides(kv_stride, kv_head_stride, n_kv, hd, i8 ? 16 : 8)) return e;
-    if (i8)
-        if (int e = check_scales(ks, vs, sc_stride, sc_head_stride)) return e;
+    if (fmt == 2) {
+        // rows of 128 bytes (kv strides in bytes), 8 f16 scales a row (scale strides in f16 elements)
+        if (kv_head_stride == 0) kv_head_stride = hd / 2;
+        if (int e = check_kv_strides(kv_stride, kv_head_stride, n_kv, hd / 2, 16)) return e;
+        if (!ks || !vs) return fail("null scale pointer");
+        if (((uintptr_t)ks & 1) || ((uintptr_t)vs & 1)) return fail("ks and vs must be 2-byte aligned");
+        if (int e = check_kv_strides(sc_stride, sc_head_stride, n_kv, 8, 1)) return e;
+    } else {
+        if (kv_head_stride == 0) kv_head_stride = hd;
+        if (int e = check_kv_strides(kv_stride, kv_head_stride, n_kv, hd, fmt ? 16 : 8)) return e;
+        if (fmt)
+            if (int e = check_scales(ks, vs, sc_stride, sc_head_stride)) return e;
+    }
     if (!aligned16(q) || !aligned16(kc) || !aligned16(vc) || !aligned16(out) ||
         q_stride % (q_dtype == GI_F16 ? 8 : 4) || out_stride % (out_dtype == GI_F16 ? 8 : 4))
         return fail("tensors must be 16-byte aligned with row strides of whole 16-byte units");
@@ -513,7 +556,7 @@ int prefill_impl(void* stream, const void* q, int q_dtype, long long q_stride, c
     a.q = q;
     a.kc = (const uint16_t*)kc;
     a.vc = (const uint16_t*)vc;
-    if (i8) {
+    if (fmt) {
         a.ks = ks;
         a.vs = vs;
         a.sc_stride = sc_stride;
@@ -617,6 +660,17 @@ int gi_attn_decode_i8(void* stream, const float* q, long long q_stride, const in
                        out, out_stride, workspace, workspace_bytes, pos0, posp, ctx_cap, n_tok, n_heads, n_kv, hd, scale);
 }
 
+int gi_attn_decode_q4(void* stream, const float* q, long long q_stride, const uint8_t* kc, const uint8_t* vc,
+                      const uint16_t* ks, const uint16_t* vs, long long kv_stride, long long kv_head_stride,
+                      long long sc_stride, long long sc_head_stride, float* out, long long out_stride, void* workspace,
+                      size_t workspace_bytes, int pos0, const int* posp, int ctx_cap, int n_tok, int n_heads, int n_kv,
+                      float scale) {
+    if (sc_stride == 0 && sc_head_stride == 0) sc_stride = 8LL * n_kv, sc_head_stride = 8;
+    return decode_impl(stream, q, q_stride, kc, vc, (const float*)ks, (const float*)vs, sc_stride, sc_head_stride, 2,
+                       kv_stride, kv_head_stride, out, out_stride, workspace, workspace_bytes, pos0, posp, ctx_cap, n_tok,
+                       n_heads, n_kv, 256, scale);
+}
+
 int gi_attn_prefill(void* stream, const void* q, int q_dtype, long long q_stride, const uint16_t* kc,
                     const uint16_t* vc, long long kv_stride, long long kv_head_stride, void* out, int out_dtype,
                     long long out_stride, int pos0, int n, int n_heads, int n_kv, int hd, float scale) {
@@ -714,7 +768,7 @@ int gi_kernel_timing_read(const char* kernel, double* total_ms, int* launches) {
 int gi_qk_norm_rope(void* stream, float* qkv, const float* qn, const float* kn, uint16_t* kc, uint16_t* vc,
                     long long kv_stride, long long kv_head_stride, int pos0, const int* posp, int ctx_cap, int n,
                     int n_heads, int n_kv, int hd, int rope_dim, float base, const float* ff, int neox, float eps) {
-    return rope_impl(stream, qkv, qn, kn, kc, vc, nullptr, nullptr, 0, 0, false, kv_stride, kv_head_stride, pos0, posp,
+    return rope_impl(stream, qkv, qn, kn, kc, vc, nullptr, nullptr, 0, 0, 0, kv_stride, kv_head_stride, pos0, posp,
                      ctx_cap, n, n_heads, n_kv, hd, rope_dim, base, ff, neox, eps);
 }
 
@@ -723,8 +777,17 @@ int gi_qk_norm_rope_i8(void* stream, float* qkv, const float* qn, const float* k
                        long long sc_head_stride, int pos0, const int* posp, int ctx_cap, int n, int n_heads, int n_kv,
                        int hd, int rope_dim, float base, const float* ff, int neox, float eps) {
     if (sc_stride == 0 && sc_head_stride == 0) sc_stride = n_kv, sc_head_stride = 1;
-    return rope_impl(stream, qkv, qn, kn, kc, vc, ks, vs, sc_stride, sc_head_stride, true, kv_stride, kv_head_stride,
+    return rope_impl(stream, qkv, qn, kn, kc, vc, ks, vs, sc_stride, sc_head_stride, 1, kv_stride, kv_head_stride,
                      pos0, posp, ctx_cap, n, n_heads, n_kv, hd, rope_dim, base, ff, neox, eps);
+}
+
+int gi_qk_norm_rope_q4(void* stream, float* qkv, const float* qn, const float* kn, uint8_t* kc, uint8_t* vc,
+                       uint16_t* ks, uint16_t* vs, long long kv_stride, long long kv_head_stride, long long sc_stride,
+                       long long sc_head_stride, int pos0, const int* posp, int ctx_cap, int n, int n_heads, int n_kv,
+                       int rope_dim, float base, const float* ff, int neox, float eps) {
+    if (sc_stride == 0 && sc_head_stride == 0) sc_stride = 8LL * n_kv, sc_head_stride = 8;
+    return rope_impl(stream, qkv, qn, kn, kc, vc, (float*)ks, (float*)vs, sc_stride, sc_head_stride, 2, kv_stride,
+                     kv_head_stride, pos0, posp, ctx_cap, n, n_heads, n_kv, 256, rope_dim, base, ff, neox, eps);
 }
 
 int gi_kv_relayout(void* stream, const void* src, long long src_stride, long long src_head_stride, void* dst,

@@ -60,7 +60,9 @@ struct GiDecodeArgs {
     float qscale;          // scale * log2(e)
     int hd;                // head size: 128 or 256 (f16 cache); partial rows are hd + 4 floats
     // int8 cache only (the kernels named *_i8): kc / vc hold int8 rows in the same element layout, and the
-    // f32 scale of position t, kv head h is at ks / vs [t*sc_stride + h*sc_head_stride]
+    // f32 scale of position t, kv head h is at ks / vs [t*sc_stride + h*sc_head_stride]. The 4-bit cache (*_q4):
+    // kc / vc rows of 128 bytes with kv_stride / kv_head_stride in bytes, ks / vs the rows' 8 f16 scales with
+    // sc_stride / sc_head_stride in f16 elements
     const float* ks;
     const float* vs;
     long long sc_stride;
@@ -177,6 +179,24 @@ template <> struct DecBuf<false, 256> { u4 k[8]; u4 v[4][2]; };
 // head size 256 over the int8 cache: 16 keys; K row c, bytes 64i + 16grp .. +15 (k-steps 2i, 2i + 1); V keys
 // 4grp..4grp+3, bytes 16c..16c+15; the scales of tile key 4(lane/16) + lane%4
 template <> struct DecBuf<true, 256> { u4 k[4]; u4 v[4]; float ksc, vsc; };
+// head size 256 over the 4-bit cache: 16 keys; K row c, bytes 32grp .. 32grp + 31 (values 64grp .. 64grp + 63,
+// scale groups 2grp and 2grp + 1, both scales in ksc); V keys 4grp + i, bytes 8c .. 8c + 7 (dims 16c .. 16c + 15,
+// scale group c/2, that scale in vsc[i])
+struct DecBufQ4 { u4 k[2]; u2 v[4]; uint32_t ksc; uint32_t vsc[4]; };
+template <bool C, typename A, typename B> struct gi_pick { typedef A type; };
+template <typename A, typename B> struct gi_pick<false, A, B> { typedef B type; };
+
+// 4-bit cache values -> f16 (kv4_pair, src/cuda.rs:238-240: f16((n - 8) * s)). lo and hi hold, in byte j, the
+// nibbles that become the low and high f16 of the pair; v_perm puts byte j of each into the low byte of a half,
+// the and-or keeps the nibbles under the f16 bits 0x6400 (1024 + n), the packed subtract leaves n - 8 exactly
+// and the packed multiply by the scales rounds (n - 8) * s to nearest even once, as the reference's conversion
+// of the exact f32 product does.
+__device__ __forceinline__ uint32_t q4_f16x2(uint32_t hi, uint32_t lo, int j, h2x sc) {
+    const uint32_t sel = (uint32_t)j | 0x0c00u | (uint32_t)(4 + j) << 16 | 0x0c000000u;
+    const uint32_t w = (__builtin_amdgcn_perm(hi, lo, sel) & 0x000f000fu) | 0x64006400u;
+    const h2x v = (__builtin_bit_cast(h2x, w) - h2x{(_Float16)1032.f, (_Float16)1032.f}) * sc;
+    return __builtin_bit_cast(uint32_t, v);
+}
 
 // Lane l of a wave: c = l % 16 (MFMA column / A-row), grp = l / 16 (k-group of 8).
 // I8 = true: an int8 cache (kv_store's KV8 format, src/cuda.rs:333-339: a row of int8 values and one f32
@@ -203,11 +223,17 @@ template <> struct DecBuf<true, 256> { u4 k[4]; u4 v[4]; float ksc, vsc; };
 // every wave walks the whole slice for its own DEC_PAIRS*NCB pairs, so one workgroup serves 4 times as
 // many pairs and the slice's K/V comes from HBM once (the waves' repeated loads of the same lines are
 // served by the caches).
-template <int NCB, int WS, bool I8, int HD = 128, bool PM = false>
+// Q4 = true (head size 256, the 4-bit cache, kv_store's KV4 format, src/cuda.rs:340-357): K and V values are
+// widened to the f16 values f16((n - 8) * scale) that attention_decode_tc256 (src/cuda.rs:2681-2760) feeds its
+// tensor cores, and the rest is the f16 cache's path (unit key and value scales). Lane (c, grp) takes values
+// 64grp .. 64grp + 63 of key row c (k-step kk: 64grp + 8kk .. + 7, the query loaded to match), so each lane's two
+// 16-byte loads are whole scale groups.
+template <int NCB, int WS, bool I8, int HD = 128, bool PM = false, bool Q4 = false>
 __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
     static_assert(HD == 128 || HD == 256, "head sizes: 128, 256");
-    // tiles in flight per wave: an int8 tile at head size 256 holds half the bytes of the others
-    constexpr int NB = I8 && HD == 256 ? 2 * DEC_NB : DEC_NB;
+    static_assert(!Q4 || (HD == 256 && !I8), "the 4-bit cache: head size 256");
+    // tiles in flight per wave: an int8 tile at head size 256 holds half the bytes of the others (4-bit: a quarter)
+    constexpr int NB = (I8 || Q4) && HD == 256 ? 2 * DEC_NB : DEC_NB;
     constexpr int CPAIRS = PM ? 2 * DEC_PAIRS : DEC_PAIRS; // pairs per column block
     constexpr int TILE = HD == 256 ? DEC_TILE / 2 : I8 ? 2 * DEC_TILE : DEC_TILE; // keys per wave tile
     constexpr int KK = HD / 32;                 // QK k-steps
@@ -257,7 +283,7 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
         valid[cb] = pi < npairs;
         int t = valid[cb] ? pi / G : 0, g = valid[cb] ? pi % G : 0;
         span[cb] = valid[cb] ? min(pos0 + t + 1 - k_begin, nkeys) : 0; // keys of the slice this column sees
-        qoff[cb] = ((int)(t * a.q_stride) + (kvh * G + g) * HD + (I8 ? 16 : 8) * grp) * 4;
+        qoff[cb] = ((int)(t * a.q_stride) + (kvh * G + g) * HD + (Q4 ? 64 : I8 ? 16 : 8) * grp) * 4;
     }
     // smallest span among the wave's valid columns (the lowest token's: column 0 of block 0 is always valid):
     // tiles below it need no masking
@@ -275,7 +301,7 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
         for (int cb = 0; cb < NCB; cb++)
 #pragma unroll
             for (int kk = 0; kk < KK; kk++) {
-                const int off = qoff[cb] + (I8 ? 32 * (kk & 1) + 256 * (kk >> 1) : 128 * kk);
+                const int off = qoff[cb] + (Q4 ? 32 * kk : I8 ? 32 * (kk & 1) + 256 * (kk >> 1) : 128 * kk);
                 qraw[cb][kk][0] = gi_load16(rq, off);
                 qraw[cb][kk][1] = gi_load16(rq, off + 16);
             }
@@ -325,14 +351,30 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
     const int koff256_8 = c * (int)kvs + 16 * grp;
     const int voff256_8 = 4 * grp * (int)kvs + 16 * c;
     const int scoff256 = (4 * (lane >> 4) + (lane & 3)) * (int)scs * 4;
+    // 4-bit (bytes): K row c, bytes 32grp (+16); its two scales (4 bytes at f16 element 2grp of the row); V rows
+    // 4grp + i, bytes 8c; their scales (f16 element c/2 of each row)
+    const uint8_t* kslice4 = reinterpret_cast<const uint8_t*>(a.kc) + (long long)k_begin * kvs + kvh * a.kv_head_stride;
+    const uint8_t* vslice4 = reinterpret_cast<const uint8_t*>(a.vc) + (long long)k_begin * kvs + kvh * a.kv_head_stride;
+    const uint16_t* kscl4 = Q4 ? reinterpret_cast<const uint16_t*>(a.ks) + (long long)k_begin * scs + kvh * a.sc_head_stride : nullptr;
+    const uint16_t* vscl4 = Q4 ? reinterpret_cast<const uint16_t*>(a.vs) + (long long)k_begin * scs + kvh * a.sc_head_stride : nullptr;
+    const int koff4 = c * (int)kvs + 32 * grp;
+    const int kscoff4 = (c * (int)scs + 2 * grp) * 2;
+    const int voff4 = 4 * grp * (int)kvs + 8 * c;
+    const int vscoff4 = (4 * grp * (int)scs + (c >> 1)) * 2;
 
-    using Buf = DecBuf<I8, HD>;
+    using Buf = typename gi_pick<Q4, DecBufQ4, DecBuf<I8, HD>>::type;
     // K/V stream loads: each tile is read by one wave only, unless SHARE (every wave of the workgroup reads
     // every tile of the slice, from L2 after the first): streaming policy only for the former. At config 2
     // it takes the split kernel from 25.5 to 22.7 us; with SHARE it costs 30%.
     constexpr int CPOL = WS == DEC_WAVES ? DEC_CPOL : 0;
     auto load_k = [&](Buf& B, int t) {
-        if constexpr (HD == 256 && I8) {
+        if constexpr (Q4) {
+            __amdgpu_buffer_rsrc_t r = gi_rsrc(kslice4 + (long long)t * kvs, (long long)(nkeys - t) * kvs);
+            B.k[0] = gi_load16p<CPOL>(r, koff4);
+            B.k[1] = gi_load16p<CPOL>(r, koff4 + 16);
+            B.ksc = __builtin_amdgcn_raw_buffer_load_b32(
+                gi_rsrc(kscl4 + (long long)t * scs, (long long)(nkeys - t) * scs * 2), kscoff4, 0, 0);
+        } else if constexpr (HD == 256 && I8) {
             __amdgpu_buffer_rsrc_t r = gi_rsrc(kslice8 + (long long)t * kvs, (long long)(nkeys - t) * kvs);
 #pragma unroll
             for (int i = 0; i < 4; i++) B.k[i] = gi_load16p<CPOL>(r, koff256_8 + 64 * i);
@@ -359,7 +401,15 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
         }
     };
     auto load_v = [&](Buf& B, int t) {
-        if constexpr (HD == 256 && I8) {
+        if constexpr (Q4) {
+            __amdgpu_buffer_rsrc_t r = gi_rsrc(vslice4 + (long long)t * kvs, (long long)(nkeys - t) * kvs);
+            __amdgpu_buffer_rsrc_t rs = gi_rsrc(vscl4 + (long long)t * scs, (long long)(nkeys - t) * scs * 2);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                B.v[i] = gi_load8p<CPOL>(r, voff4 + i * (int)kvs);
+                B.vsc[i] = __builtin_amdgcn_raw_buffer_load_b16(rs, vscoff4 + i * (int)scs * 2, 0, 0);
+            }
+        } else if constexpr (HD == 256 && I8) {
             __amdgpu_buffer_rsrc_t r = gi_rsrc(vslice8 + (long long)t * kvs, (long long)(nkeys - t) * kvs);
 #pragma unroll
             for (int i = 0; i < 4; i++) B.v[i] = gi_load16p<CPOL>(r, voff256_8 + i * (int)kvs);
@@ -591,7 +641,14 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
         __builtin_amdgcn_sched_barrier(0);
         // K fragment of k-step kk (int8: the lane's 8 bytes of dims 64(kk/2) + 16grp + 8(kk%2), widened)
         auto kfrag = [&](int kk) -> h8 {
-            if constexpr (I8) {
+            if constexpr (Q4) {
+                // values 64grp + 8kk .. + 7: bytes 4kk .. 4kk + 3 of the lane's 32, scale group 2grp + kk/4
+                const uint32_t x = B.k[kk >> 2][kk & 3];
+                const h2x sc = __builtin_bit_cast(h2x, (kk >> 2) ? (B.ksc >> 16) * 0x10001u : (B.ksc & 0xffffu) * 0x10001u);
+                const uint32_t hi = x >> 4;
+                return __builtin_bit_cast(h8, u4{q4_f16x2(hi, x, 0, sc), q4_f16x2(hi, x, 1, sc), q4_f16x2(hi, x, 2, sc),
+                                                 q4_f16x2(hi, x, 3, sc)});
+            } else if constexpr (I8) {
                 const uint32_t x0 = gi_i8_in(B.k[kk >> 1][2 * (kk & 1)]), x1 = gi_i8_in(B.k[kk >> 1][2 * (kk & 1) + 1]);
                 return __builtin_bit_cast(h8, u4{i8_f16x2(x0, GI_I8_LO), i8_f16x2(x0, GI_I8_HI), i8_f16x2(x1, GI_I8_LO),
                                                  i8_f16x2(x1, GI_I8_HI)});
@@ -676,10 +733,25 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
                 }
             }
         }
+        // 4-bit: for keys 2p, 2p + 1 the pair (key 2p, key 2p + 1) of dim 16c + dd is nibble dd%2 of byte dd/2 of
+        // each row, each times its own key's scale
+        h2x vsp[2];
+        if constexpr (Q4) {
+#pragma unroll
+            for (int p = 0; p < 2; p++)
+                vsp[p] = __builtin_bit_cast(h2x, (B.vsc[2 * p] & 0xffffu) | (B.vsc[2 * p + 1] << 16));
+        }
 #pragma unroll
         for (int dd = 0; dd < 16; dd++) {
             u2 vw;
-            if constexpr (I8) {
+            if constexpr (Q4) {
+                const int w = dd >> 3, j = (dd >> 1) & 3;
+#pragma unroll
+                for (int p = 0; p < 2; p++) {
+                    const uint32_t xa = B.v[2 * p][w], xb = B.v[2 * p + 1][w];
+                    vw[p] = (dd & 1) ? q4_f16x2(xb >> 4, xa >> 4, j, vsp[p]) : q4_f16x2(xb, xa, j, vsp[p]);
+                }
+            } else if constexpr (I8) {
                 vw = v8[dd];
             } else {
                 const int h = dd >> 3, w = (dd & 7) >> 1;
@@ -838,8 +910,12 @@ GI_DEC_PM_KERNEL(gi_decode_pm_ws2_2_i8, 2, 2, true)
 GI_DEC_KERNEL(gi_decode_partial_1_i8_h256, 1, DEC_WAVES, true, 256)
 #define GI_DEC_PM256_KERNEL(name, NCB, WS, I8) \
     extern "C" __global__ void __launch_bounds__(256, DEC_MINWG) name(GiDecodeArgs a) { gi_decode_partial_t<NCB, WS, I8, 256, true>(a); }
+#define GI_DEC_Q4_KERNEL(name, WS, PM) \
+    extern "C" __global__ void __launch_bounds__(256, DEC_MINWG) name(GiDecodeArgs a) { gi_decode_partial_t<1, WS, false, 256, PM, true>(a); }
 GI_DEC_PM256_KERNEL(gi_decode_pm_shared_1_h256, 1, 1, false)
 GI_DEC_PM256_KERNEL(gi_decode_pm_shared_1_i8_h256, 1, 1, true)
+GI_DEC_Q4_KERNEL(gi_decode_partial_1_q4, DEC_WAVES, false)
+GI_DEC_Q4_KERNEL(gi_decode_pm_shared_1_q4, 1, true)
 
 // Merge the slices of each (token, head): M = max m_s, w_s = 2^(m_s - M), out = sum w_s O_s / sum w_s l_s
 // (attention_combine's maths in base 2; empty slices carry m = -inf and weigh nothing). One wave per
@@ -1679,8 +1755,11 @@ struct GiRopeArgs {
     float base;
     float eps;
     int neox;              // pairs (i, i + rope_dim/2); otherwise (2i, 2i+1)
-    int i8;                // the caches are int8 (kc / vc as bytes, same element offsets) with scales:
-    float* ks;             // f32 scale of position t, kv head h at t*sc_stride + h*sc_head_stride
+    int fmt;               // cache format: 0 f16; 1 int8 (kc / vc as bytes, same element offsets) with f32 scales
+                           // (position t, kv head h at t*sc_stride + h*sc_head_stride); 2 the 4-bit cache (head
+                           // size 256: kv strides in bytes, a row of 128 bytes; ks / vs hold 8 f16 scales a row,
+                           // sc strides in f16 elements)
+    float* ks;
     float* vs;
     long long sc_stride;
     long long sc_head_stride;
@@ -1697,14 +1776,40 @@ struct GiRopeArgs {
 // workgroup computes them once into LDS for all its heads; each wave loads its ROPE_HEADS/4 heads at once
 // and takes them one at a time through a per-wave LDS row (any two dims can pair).
 #define ROPE_HEADS 16
+// The normalized 256-point Walsh-Hadamard transform of a row held 4 values per lane (lane l: values 4l..4l+3):
+// kv4_fwht's stages (src/cuda.rs:242-256) in its order, h = 1, 2 inside the lane, h = 4..128 across lanes
+// l and l ^ (h/4). Each stage gives the lower element a + c and the upper one a - c, single f32 operations as
+// the reference's, so the result is bit-identical to it; then every value times 1/16.
+__device__ __forceinline__ void gi_fwht256(float __attribute__((ext_vector_type(4))) & x, int lane) {
+    float t;
+    t = x[0]; x[0] = t + x[1]; x[1] = t - x[1];
+    t = x[2]; x[2] = t + x[3]; x[3] = t - x[3];
+    t = x[0]; x[0] = t + x[2]; x[2] = t - x[2];
+    t = x[1]; x[1] = t + x[3]; x[3] = t - x[3];
+#pragma unroll
+    for (int m = 1; m < 64; m <<= 1) {
+        const bool upper = lane & m;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const float p = __shfl_xor(x[j], m, 64);
+            x[j] = upper ? p - x[j] : x[j] + p;
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < 4; j++) x[j] *= 0.0625f;
+}
+
 // One head row (PER values per lane) into a cache row. f16: rounded to nearest even. int8 (kv_store's KV8,
 // src/cuda.rs:333-339): dd = max|x| / 127, each value rint(x * (1/dd)) (0 when dd is 0), dd to the scale.
+// 4-bit (kv_store's KV4, src/cuda.rs:340-357; PER = 4, the row already rotated): per group of 32 values (8
+// lanes) dh = f16(max|x| / 7), inv = 1/dh (0 when dh is 0), q = clamp(rint(x * inv), -7, 7) + 8; lane l writes
+// the 2 bytes of values 4l..4l+3 (value 2i in byte i's low nibble), the group's first lane its f16 scale.
 template <int PER>
 __device__ __forceinline__ void gi_store_row(const GiRopeArgs& a, uint16_t* cache, float* scale, int pos, int kh,
                                              const float __attribute__((ext_vector_type(PER))) x, int lane) {
     if (pos < 0 || pos >= a.ctx_cap) return; // (a device position past the capacity writes nothing)
     const long long off = (long long)pos * a.kv_stride + (long long)kh * a.kv_head_stride;
-    if (!a.i8) {
+    if (a.fmt == 0) {
         typedef _Float16 hv __attribute__((ext_vector_type(PER)));
         *reinterpret_cast<hv*>(cache + off + PER * lane) = __builtin_convertvector(x, hv);
         return;
@@ -1712,6 +1817,22 @@ __device__ __forceinline__ void gi_store_row(const GiRopeArgs& a, uint16_t* cach
     float amax = 0.f;
 #pragma unroll
     for (int j = 0; j < PER; j++) amax = fmaxf(amax, fabsf(x[j]));
+    if constexpr (PER == 4) {
+        if (a.fmt == 2) {
+            for (int m = 4; m > 0; m >>= 1) amax = fmaxf(amax, __shfl_xor(amax, m, 64));
+            const _Float16 dh = (_Float16)__fdiv_rn(amax, 7.f);
+            const float dd = (float)dh, inv = dd != 0.f ? __fdiv_rn(1.f, dd) : 0.f;
+            uint32_t w = 0;
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                w |= (uint32_t)(fminf(fmaxf(rintf(x[j] * inv), -7.f), 7.f) + 8.f) << (4 * j);
+            *reinterpret_cast<uint16_t*>(reinterpret_cast<uint8_t*>(cache) + off + 2 * lane) = (uint16_t)w;
+            if ((lane & 7) == 0)
+                reinterpret_cast<_Float16*>(scale)[(long long)pos * a.sc_stride + (long long)kh * a.sc_head_stride +
+                                                   (lane >> 3)] = dh;
+            return;
+        }
+    }
     for (int m = 32; m > 0; m >>= 1) amax = fmaxf(amax, __shfl_xor(amax, m, 64));
     const float dd = __fdiv_rn(amax, 127.f), inv = dd != 0.f ? __fdiv_rn(1.f, dd) : 0.f;
     typedef int8_t bv __attribute__((ext_vector_type(PER)));
@@ -1755,8 +1876,11 @@ __device__ __forceinline__ void gi_qk_norm_rope_t(const GiRopeArgs& a, float (*c
     for (int k = 0; k < HPW; k++) {
         const int h = h0 + wave + 4 * k;
         if (h >= items) break;
-        if (h >= a.n_heads + a.n_kv) { // a v head: into the cache
-            gi_store_row<PER>(a, a.vc, a.vs, pos, h - a.n_heads - a.n_kv, v[k], lane);
+        if (h >= a.n_heads + a.n_kv) { // a v head: into the cache (the 4-bit cache: rotated first)
+            fv x = v[k];
+            if constexpr (PER == 4)
+                if (a.fmt == 2) gi_fwht256(x, lane);
+            gi_store_row<PER>(a, a.vc, a.vs, pos, h - a.n_heads - a.n_kv, x, lane);
             continue;
         }
         fv x = v[k];
@@ -1781,6 +1905,9 @@ __device__ __forceinline__ void gi_qk_norm_rope_t(const GiRopeArgs& a, float (*c
         }
         __builtin_amdgcn_wave_barrier();
         x = *reinterpret_cast<const fv*>(sh + PER * lane);
+        // the 4-bit cache (src/cuda.rs:472-479): q and k heads rotated alike, so their dot products are kept
+        if constexpr (PER == 4)
+            if (a.fmt == 2) gi_fwht256(x, lane);
         *reinterpret_cast<fv*>(row + (long long)h * HD + PER * lane) = x;
         if (h >= a.n_heads) gi_store_row<PER>(a, a.kc, a.ks, pos, h - a.n_heads, x, lane);
         __builtin_amdgcn_wave_barrier(); // the row buffer is reused by the wave's next head

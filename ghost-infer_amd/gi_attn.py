@@ -34,12 +34,14 @@ SYMBOLS = (
     "gi_attn_decode",
     "gi_attn_decode_noalloc",
     "gi_attn_decode_i8",
+    "gi_attn_decode_q4",
     "gi_attn_prefill",
     "gi_attn_prefill_i8",
     "gi_attention",
     "gi_attention_i8",
     "gi_qk_norm_rope",
     "gi_qk_norm_rope_i8",
+    "gi_qk_norm_rope_q4",
     "gi_kv_relayout",
     "gi_kernel_timing",
     "gi_kernel_timing_read",
@@ -79,6 +81,8 @@ def load_library(path=LIB_PATH):
     lib.gi_attn_decode_i8.argtypes = [vp, vp, ll, vp, vp, vp, vp, ll, ll, ll, ll, vp, ll, vp, sz, i, vp, i, i, i, i, i,
                                       f]
     lib.gi_attn_decode_i8.restype = i
+    lib.gi_attn_decode_q4.argtypes = [vp, vp, ll, vp, vp, vp, vp, ll, ll, ll, ll, vp, ll, vp, sz, i, vp, i, i, i, i, f]
+    lib.gi_attn_decode_q4.restype = i
     lib.gi_attn_prefill.argtypes = [vp, vp, i, ll, vp, vp, ll, ll, vp, i, ll, i, i, i, i, i, f]
     lib.gi_attn_prefill.restype = i
     lib.gi_attention.argtypes = [vp, vp, vp, vp, vp, vp, sz, i, vp, i, i, i, i, i, i]
@@ -92,6 +96,9 @@ def load_library(path=LIB_PATH):
     lib.gi_qk_norm_rope_i8.argtypes = [vp, vp, vp, vp, vp, vp, vp, vp, ll, ll, ll, ll, i, vp, i, i, i, i, i, i, f, vp,
                                        i, f]
     lib.gi_qk_norm_rope_i8.restype = i
+    lib.gi_qk_norm_rope_q4.argtypes = [vp, vp, vp, vp, vp, vp, vp, vp, ll, ll, ll, ll, i, vp, i, i, i, i, i, f, vp, i,
+                                       f]
+    lib.gi_qk_norm_rope_q4.restype = i
     lib.gi_kernel_timing.argtypes = [i]
     lib.gi_kernel_timing.restype = i
     lib.gi_kernel_timing_read.argtypes = [ctypes.c_char_p, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(i)]
@@ -162,6 +169,37 @@ def _scale_layout(ks, vs, n_kv, capacity, layout):
     return (n_kv, 1) if layout == "reference" else (1, capacity)
 
 
+def _q4_layout(kc, vc, ks, vs, n_kv, layout):
+    """(kv_stride, kv_head_stride, sc_stride, sc_head_stride, capacity) of a 4-bit cache (head size 256): uint8
+    rows of 128 bytes and float16 scales, 8 a row. layout "reference": [capacity, n_kv, 128] and [capacity, n_kv,
+    8] (src/cuda.rs:365-369's KV_ROWP / KV_SROWP with KV4); "head_major": [n_kv, capacity, 128] and [n_kv,
+    capacity, 8]. Strides of the rows in bytes, of the scales in f16 elements."""
+    for t, name, dt in ((kc, "k_cache", torch.uint8), (vc, "v_cache", torch.uint8), (ks, "k_scale", torch.float16),
+                        (vs, "v_scale", torch.float16)):
+        if t is None:
+            raise GiAttnError(f"a 4-bit cache needs {name}")
+        _need(t, name, dt)
+        if not t.is_contiguous():
+            raise GiAttnError(f"{name} must be contiguous")
+    if kc.shape != vc.shape or ks.shape != vs.shape:
+        raise GiAttnError("k and v shapes differ")
+    if layout == "reference":
+        if kc.numel() % (n_kv * 128):
+            raise GiAttnError(f"cache of shape {tuple(kc.shape)} is not [capacity, {n_kv}, 128]")
+        cap = kc.numel() // (n_kv * 128)
+        if ks.numel() != cap * n_kv * 8:
+            raise GiAttnError(f"scales must be [{cap}, {n_kv}, 8], got {tuple(ks.shape)}")
+        return n_kv * 128, 128, n_kv * 8, 8, cap
+    if layout == "head_major":
+        if kc.dim() != 3 or kc.shape[0] != n_kv or kc.shape[2] != 128:
+            raise GiAttnError(f"head-major cache must be [{n_kv}, capacity, 128], got {tuple(kc.shape)}")
+        cap = kc.shape[1]
+        if tuple(ks.shape) != (n_kv, cap, 8):
+            raise GiAttnError(f"head-major scales must be [{n_kv}, {cap}, 8], got {tuple(ks.shape)}")
+        return 128, cap * 128, 8, cap * 8, cap
+    raise GiAttnError(f"unknown cache layout {layout!r}")
+
+
 def init(code_object_path=None):
     """Loads the code object on the current device (optional: the first call does it)."""
     lib = load_library()
@@ -225,6 +263,35 @@ def decode(q, k_cache, v_cache, pos0, n_heads, n_kv, hd=128, scale=None, out=Non
         _check(lib.gi_attn_decode(_stream(), _ptr(q), q.stride(0), _ptr(k_cache), _ptr(v_cache), kv_stride,
                                   kv_head_stride, _ptr(out), out.stride(0), *ws, pos0, _ptr(posp), ctx_cap, n_tok,
                                   n_heads, n_kv, hd, scale))
+    return out
+
+
+def decode_q4(q, k_cache, v_cache, k_scale, v_scale, pos0, n_heads, n_kv, scale=None, out=None, workspace=None,
+              posp=None, ctx_cap=0, kv_layout="reference"):
+    """decode over the 4-bit cache (head size 256; attention_decode_tc256 with KV4, src/cuda.rs:2625-2802): q the
+    rotated queries f32 [n_tok, >= n_heads*256]; k_cache / v_cache uint8 rows, k_scale / v_scale float16 (see
+    _q4_layout). Returns the rotated output f32 [n_tok, n_heads*256] (hadamard_rows turns it back)."""
+    _need(q, "q", torch.float32)
+    kv_stride, kv_head_stride, sc_stride, sc_head_stride, capacity = _q4_layout(k_cache, v_cache, k_scale, v_scale,
+                                                                                n_kv, kv_layout)
+    n_tok = q.shape[0]
+    if scale is None:
+        scale = 1.0 / 16.0
+    if out is None:
+        out = torch.empty((n_tok, n_heads * 256), dtype=torch.float32, device=q.device)
+    _need(out, "out", torch.float32)
+    if posp is not None:
+        _need(posp, "posp", torch.int32)
+    need_rows = ctx_cap if posp is not None else pos0 + n_tok
+    if capacity < need_rows:
+        raise GiAttnError(f"the cache holds {capacity} positions; {need_rows} needed")
+    if workspace is None:
+        workspace = new_workspace(need_rows, n_tok, n_heads, n_kv, 256, q.device)
+    _check(load_library().gi_attn_decode_q4(_stream(), _ptr(q), q.stride(0), _ptr(k_cache), _ptr(v_cache),
+                                            _ptr(k_scale), _ptr(v_scale), kv_stride, kv_head_stride, sc_stride,
+                                            sc_head_stride, _ptr(out), out.stride(0), _ptr(workspace),
+                                            workspace.numel() * workspace.element_size(), pos0, _ptr(posp), ctx_cap,
+                                            n_tok, n_heads, n_kv, scale))
     return out
 
 
@@ -342,6 +409,34 @@ def qk_norm_rope(qkv, k_cache, v_cache, pos0, n_heads, n_kv, hd=128, rope_dim=No
         _check(load_library().gi_qk_norm_rope(_stream(), _ptr(qkv), _ptr(qn), _ptr(kn), _ptr(k_cache), _ptr(v_cache),
                                               kv_stride, kv_head_stride, pos0, _ptr(posp), cap, n, n_heads, n_kv,
                                               hd, *rope))
+    return qkv
+
+
+def qk_norm_rope_q4(qkv, k_cache, v_cache, k_scale, v_scale, pos0, n_heads, n_kv, rope_dim=None, base=10000.0,
+                    qn=None, kn=None, ff=None, neox=True, eps=1e-6, posp=None, kv_layout="reference", ctx_cap=None):
+    """qk_norm_rope into the 4-bit cache (head size 256; qk_norm_rope with KV4, src/cuda.rs:437-486, 340-357): q
+    and k heads rotated after RoPE (in place), k rows quantised, v rows rotated and quantised."""
+    _need(qkv, "qkv", torch.float32)
+    if not qkv.is_contiguous() or qkv.dim() != 2 or qkv.shape[1] != (n_heads + 2 * n_kv) * 256:
+        raise GiAttnError(f"qkv must be contiguous [n, {(n_heads + 2 * n_kv) * 256}]")
+    kv_stride, kv_head_stride, sc_stride, sc_head_stride, capacity = _q4_layout(k_cache, v_cache, k_scale, v_scale,
+                                                                                n_kv, kv_layout)
+    n = qkv.shape[0]
+    if posp is None and capacity < pos0 + n:
+        raise GiAttnError(f"the cache holds {capacity} positions; {pos0 + n} needed")
+    for t, name in ((qn, "qn"), (kn, "kn"), (ff, "ff")):
+        if t is not None:
+            _need(t, name, torch.float32)
+    if posp is not None:
+        _need(posp, "posp", torch.int32)
+    cap = capacity if ctx_cap is None else ctx_cap
+    if cap > capacity:
+        raise GiAttnError(f"ctx_cap {cap} exceeds the cache's {capacity} positions")
+    _check(load_library().gi_qk_norm_rope_q4(_stream(), _ptr(qkv), _ptr(qn), _ptr(kn), _ptr(k_cache), _ptr(v_cache),
+                                             _ptr(k_scale), _ptr(v_scale), kv_stride, kv_head_stride, sc_stride,
+                                             sc_head_stride, pos0, _ptr(posp), cap, n, n_heads, n_kv,
+                                             256 if rope_dim is None else rope_dim, base, _ptr(ff), 1 if neox else 0,
+                                             eps))
     return qkv
 
 

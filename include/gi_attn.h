@@ -101,6 +101,21 @@ int gi_attn_decode_i8(void* stream, const float* q, long long q_stride, const in
                       size_t workspace_bytes, int pos0, const int* posp, int ctx_cap, int n_tok, int n_heads, int n_kv,
                       int hd, float scale);
 
+/* gi_attn_decode over the 4-bit KV cache (head size 256; the reference's --kv q4 format, src/cuda.rs:226-256,
+ * 340-357): position t, kv head h has a row of 128 bytes at kc / vc + t*kv_stride + h*kv_head_stride (strides in
+ * bytes, multiples of 16; kv_head_stride 0 means 128), value 2i in byte i's low nibble and 2i + 1 in its high one,
+ * each stored as q + 8, and 8 f16 scales (one per 32 values) at ks / vs + t*sc_stride + h*sc_head_stride (f16
+ * elements; both 0 mean the reference's [position][n_kv][8]). A value is f16((n - 8) * scale). The rows hold
+ * rotated vectors (gi_qk_norm_rope_q4 rotates q and k alike and v in the store), so q must be the rotated
+ * queries and out holds rotated rows: gi_hadamard_rows turns them back. Replaces: attention_decode_tc256 compiled
+ * with KV4 (src/cuda.rs:2625-2802) + attention_combine, as GpuModel::attention dispatches it for 256-wide heads
+ * (src/cuda.rs:8478-8538). The workspace is gi_attn_decode_workspace_bytes(..., hd = 256). */
+int gi_attn_decode_q4(void* stream, const float* q, long long q_stride, const uint8_t* kc, const uint8_t* vc,
+                      const uint16_t* ks, const uint16_t* vs, long long kv_stride, long long kv_head_stride,
+                      long long sc_stride, long long sc_head_stride, float* out, long long out_stride, void* workspace,
+                      size_t workspace_bytes, int pos0, const int* posp, int ctx_cap, int n_tok, int n_heads, int n_kv,
+                      float scale);
+
 /* Causal prefill attention for n tokens at positions pos0..pos0+n-1 whose K/V rows are already in the
  * cache (keys 0..pos0+n-1 are read; pos0 > 0 is a chunk of a longer prompt). q: rows of q_dtype
  * (GI_F32 or GI_F16); out: rows of out_dtype. Replaces: attention_prefill_tc128 (src/cuda.rs:2408-2621),
@@ -155,6 +170,17 @@ int gi_qk_norm_rope_i8(void* stream, float* qkv, const float* qn, const float* k
                        float* vs, long long kv_stride, long long kv_head_stride, long long sc_stride,
                        long long sc_head_stride, int pos0, const int* posp, int ctx_cap, int n, int n_heads, int n_kv,
                        int hd, int rope_dim, float base, const float* ff, int neox, float eps);
+
+/* gi_qk_norm_rope storing into the 4-bit cache (head size 256; layouts as gi_attn_decode_q4). After RMSNorm and
+ * RoPE every q and k head is rotated by the normalized 256-point Walsh-Hadamard transform (Sylvester order,
+ * bit-identical to kv4_fwht) and written back rotated; a v head is rotated on its way into the cache. Each row
+ * is then quantised per group of 32 values: dh = f16(max|x| / 7), q = clamp(rint(x / dh), -7, 7) (0 when dh is
+ * 0), stored as q + 8 with dh as the group's scale. Replaces: qk_norm_rope compiled with KV4 (src/cuda.rs:437-486,
+ * kv_store src/cuda.rs:340-357, kv4_fwht src/cuda.rs:242-256). */
+int gi_qk_norm_rope_q4(void* stream, float* qkv, const float* qn, const float* kn, uint8_t* kc, uint8_t* vc,
+                       uint16_t* ks, uint16_t* vs, long long kv_stride, long long kv_head_stride, long long sc_stride,
+                       long long sc_head_stride, int pos0, const int* posp, int ctx_cap, int n, int n_heads, int n_kv,
+                       int rope_dim, float base, const float* ff, int neox, float eps);
 
 /* Cache growth: copies rows (position t < n_rows, kv head h < n_kv) of row_bytes bytes from one cache layout
  * to another, stream-ordered, allocating nothing. Strides are in bytes (src: t*src_stride +

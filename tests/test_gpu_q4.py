@@ -1,0 +1,159 @@
+"""Parity of the 4-bit KV cache (the reference's --kv q4, src/cuda.rs:226-256) on the gfx950 kernels, through the
+C ABI: the rotated store (qk_norm_rope with KV4), the tensor-core decode over it (attention_decode_tc256 with KV4)
+and, end to end, the attention of the unrotated rows.
+
+Bar: the cache bytes and scales bit-exact against the oracle's quantiser (on the same rotated rows, and on the
+same input for v rows, whose rotation is bit-identical to kv4_fwht); decode outputs max-abs 2e-3 / relative L2
+1e-3 against the oracle's restatement and 2e-5 against float64 attention over the cache's f16 values.
+"""
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+import gi_attn
+import gi_oracle as O
+from attn_common import assert_close, make_inputs_q4, reference_f64_q4
+
+pytestmark = pytest.mark.gpu
+
+
+def say(*a):
+    print("[case]", *a, flush=True)
+    sys.stdout.flush()
+
+
+def q4_dev(q, kc, vc, ks, vs, dev, n_kv, layout="reference"):
+    qt = torch.from_numpy(np.ascontiguousarray(q)).to(dev)
+    kt = torch.from_numpy(np.ascontiguousarray(kc)).to(dev).view(-1, n_kv, 128)
+    vt = torch.from_numpy(np.ascontiguousarray(vc)).to(dev).view(-1, n_kv, 128)
+    kst = torch.from_numpy(np.ascontiguousarray(ks).view(np.float16)).to(dev).view(-1, n_kv, 8)
+    vst = torch.from_numpy(np.ascontiguousarray(vs).view(np.float16)).to(dev).view(-1, n_kv, 8)
+    if layout == "head_major":
+        kt, vt, kst, vst = (t.transpose(0, 1).contiguous() for t in (kt, vt, kst, vst))
+    return qt, kt, vt, kst, vst
+
+
+DECODE_SHAPES_Q4 = [
+    # (n_tok, pos0, n_heads, n_kv): spans inside one 16-key tile and at tile / slice edges, both kernel variants
+    # (up to 8 pairs per kv head: hi/lo columns; above: one pair per column, waves sharing the slice), G = 3
+    (1, 0, 16, 2),
+    (1, 15, 16, 2),
+    (1, 64, 16, 2),
+    (1, 4095, 16, 2),
+    (2, 300, 8, 2),
+    (3, 77, 12, 4),
+    (8, 2000, 16, 2),
+    (15, 513, 16, 2),
+    (1, 40000, 16, 2),
+]
+
+
+@pytest.mark.parametrize("n_tok,pos0,n_heads,n_kv", DECODE_SHAPES_Q4)
+def test_decode_q4(gpu, n_tok, pos0, n_heads, n_kv):
+    say("decode q4", n_tok, pos0, n_heads, n_kv)
+    q, kc, vc, ks, vs = make_inputs_q4(500 + pos0 + n_tok, n_tok, pos0 + n_tok, n_heads, n_kv)
+    t = q4_dev(q, kc, vc, ks, vs, gpu, n_kv)
+    out = gi_attn.decode_q4(*t, pos0, n_heads, n_kv)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    assert_close(got, O.decode_tc256_q4(q, kc, vc, ks, vs, pos0, n_heads, n_kv), what="q4 decode vs oracle")
+    assert_close(got, reference_f64_q4(q, kc, vc, ks, vs, pos0, n_heads, n_kv), max_abs=2e-5, rel_l2=2e-5,
+                 what="q4 decode vs f64")
+
+
+@pytest.mark.parametrize("n_tok", [1, 8])
+def test_decode_q4_head_major_and_device_position(gpu, n_tok):
+    # the head-major layout, and a device position (graph replay's posp) with the launch sized for ctx_cap
+    n_heads, n_kv, cap, pos0 = 16, 2, 3000, 2500
+    say("decode q4 head-major posp", n_tok)
+    q, kc, vc, ks, vs = make_inputs_q4(77 + n_tok, n_tok, cap, n_heads, n_kv)
+    t = q4_dev(q, kc, vc, ks, vs, gpu, n_kv, layout="head_major")
+    posp = torch.full((1,), pos0, dtype=torch.int32, device=gpu)
+    out = gi_attn.decode_q4(*t, 0, n_heads, n_kv, posp=posp, ctx_cap=cap, kv_layout="head_major")
+    torch.cuda.synchronize()
+    assert_close(out.cpu().numpy(), reference_f64_q4(q, kc, vc, ks, vs, pos0, n_heads, n_kv), max_abs=2e-5,
+                 rel_l2=2e-5, what="q4 decode head-major posp vs f64")
+
+
+def test_rope_q4_store_is_bit_exact(gpu):
+    # q/k heads: RMSNorm + RoPE + rotation, against the oracle within f32 rounding (sincos and pow differ by
+    # ulps); the k cache: the oracle's quantiser of the kernel's own rotated k rows, bit for bit; the v cache:
+    # rotation and quantiser of the same input, bit for bit
+    n, H, K, ctx, pos0 = 7, 8, 2, 40, 11
+    rng = np.random.default_rng(21)
+    qkv = rng.standard_normal((n, (H + 2 * K) * 256)).astype(np.float32)
+    qn = rng.uniform(0.5, 1.5, 256).astype(np.float32)
+    kn = rng.uniform(0.5, 1.5, 256).astype(np.float32)
+    z8 = np.zeros((ctx, K * 128), np.uint8)
+    z16 = np.zeros((ctx, K * 8), np.uint16)
+    want, wkc, wvc, wks, wvs = O.qk_norm_rope_q4(qkv, z8, z8, z16, z16, pos0, H, K, qn=qn, kn=kn)
+    say("rope q4 store")
+    x = torch.from_numpy(qkv).to(gpu)
+    kc = torch.zeros((ctx, K, 128), dtype=torch.uint8, device=gpu)
+    vc = torch.zeros_like(kc)
+    ks = torch.zeros((ctx, K, 8), dtype=torch.float16, device=gpu)
+    vs = torch.zeros_like(ks)
+    gi_attn.qk_norm_rope_q4(x, kc, vc, ks, vs, pos0, H, K, qn=torch.from_numpy(qn).to(gpu),
+                            kn=torch.from_numpy(kn).to(gpu))
+    torch.cuda.synchronize()
+    got = x.cpu().numpy()
+    np.testing.assert_allclose(got, want, rtol=0, atol=2e-5)
+    krot = got[:, H * 256:(H + K) * 256].reshape(n * K, 256)
+    kq, ksq = O.kv4_quant(krot)
+    np.testing.assert_array_equal(kc.cpu().numpy()[pos0:pos0 + n].reshape(n * K, 128), kq)
+    np.testing.assert_array_equal(ks.cpu().numpy()[pos0:pos0 + n].reshape(n * K, 8).view(np.uint16), ksq)
+    np.testing.assert_array_equal(vc.cpu().numpy().reshape(ctx, -1), wvc)
+    np.testing.assert_array_equal(vs.cpu().numpy().reshape(ctx, -1).view(np.uint16), wvs)
+    assert not kc[:pos0].any() and not kc[pos0 + n:].any()
+
+
+def test_rope_q4_rotation_is_bit_identical(gpu):
+    # without norm and RoPE (rope_dim 0) the q and k heads are only rotated: the kernel's transform equals
+    # kv4_fwht bit for bit, on rows with values of every magnitude
+    n, H, K, ctx = 5, 4, 2, 8
+    rng = np.random.default_rng(22)
+    qkv = (rng.standard_normal((n, (H + 2 * K) * 256)) * np.exp(rng.uniform(-8, 8, (n, (H + 2 * K) * 256))))
+    qkv = qkv.astype(np.float32)
+    say("rope q4 rotation")
+    x = torch.from_numpy(qkv).to(gpu)
+    kc = torch.zeros((ctx, K, 128), dtype=torch.uint8, device=gpu)
+    vc = torch.zeros_like(kc)
+    ks = torch.zeros((ctx, K, 8), dtype=torch.float16, device=gpu)
+    vs = torch.zeros_like(ks)
+    gi_attn.qk_norm_rope_q4(x, kc, vc, ks, vs, 0, H, K, rope_dim=0)
+    torch.cuda.synchronize()
+    qk = qkv[:, :(H + K) * 256].reshape(-1, 256)
+    np.testing.assert_array_equal(x.cpu().numpy()[:, :(H + K) * 256], O.kv4_fwht(qk).reshape(n, -1))
+    vq, vsq = O.kv4_quant(O.kv4_fwht(qkv[:, (H + K) * 256:].reshape(-1, 256)))
+    np.testing.assert_array_equal(vc.cpu().numpy()[:n].reshape(n * K, 128), vq)
+    np.testing.assert_array_equal(vs.cpu().numpy()[:n].reshape(n * K, 8).view(np.uint16), vsq)
+
+
+def test_q4_layer_end_to_end(gpu):
+    # a prompt's rows through the rotated store, then a decode step: the output, rotated back on the host with
+    # kv4_fwht, is the attention of the unrotated rows to within the 4-bit rounding, and equals the oracle's
+    # KV4 decode over the kernel's own cache at the parity bar
+    H, K, n, ctx = 16, 2, 600, 1024
+    rng = np.random.default_rng(23)
+    qkv = rng.standard_normal((n, (H + 2 * K) * 256)).astype(np.float32)
+    x = torch.from_numpy(qkv).to(gpu)
+    kc = torch.zeros((ctx, K, 128), dtype=torch.uint8, device=gpu)
+    vc = torch.zeros_like(kc)
+    ks = torch.zeros((ctx, K, 8), dtype=torch.float16, device=gpu)
+    vs = torch.zeros_like(ks)
+    say("q4 end to end")
+    gi_attn.qk_norm_rope_q4(x, kc, vc, ks, vs, 0, H, K, rope_dim=0)
+    qrot = x[n - 1:, :H * 256].contiguous()
+    out = gi_attn.decode_q4(qrot, kc, vc, ks, vs, n - 1, H, K)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    c = [t.cpu().numpy().reshape(ctx, -1) for t in (kc, vc, ks, vs)]
+    c[2], c[3] = c[2].view(np.uint16), c[3].view(np.uint16)
+    assert_close(got, O.decode_tc256_q4(qrot.cpu().numpy(), *c, n - 1, H, K), what="q4 e2e vs oracle")
+    back = O.kv4_fwht(got.reshape(-1, 256)).reshape(1, -1)
+    from attn_common import _reference_f64_values
+    exact = _reference_f64_values(qkv[n - 1:, :H * 256], qkv[:, H * 256:(H + K) * 256], qkv[:, (H + K) * 256:],
+                                  n - 1, H, K, 256)
+    assert np.abs(back - exact).max() < 0.05
