@@ -80,6 +80,14 @@ struct GiRopeArgs {
     int pad_;
 };
 
+// Must match the kernels' GiHadamardArgs.
+struct GiHadamardArgs {
+    float* x;
+    long long row_stride;
+    int rows;
+    int segs;
+};
+
 // Must match the kernels' GiRelayoutArgs.
 struct GiRelayoutArgs {
     const void* src;
@@ -161,7 +169,8 @@ struct Module {
     hipFunction_t dec_q4[2] = {};     // head size 256 over the 4-bit cache: [one pair per column]  // head size 256, one pair per column, 4 waves sharing each tile: [int8 cache]
     hipFunction_t prefill[2] = {};   // [int8 cache], head size 128
     hipFunction_t prefill256r = nullptr; // head size 256 (f16 cache), 16 rows per wave: one workgroup per query tile
-    hipFunction_t combine = nullptr, rope = nullptr, relayout = nullptr;
+    hipFunction_t prefill256r_fmt[2] = {}; // the same over the int8 and the 4-bit cache
+    hipFunction_t combine = nullptr, rope = nullptr, relayout = nullptr, hadamard = nullptr;
     int prefill_threads[2] = {}; // each prefill kernel's block size (its launch bound: waves x 64)
     int prefill256r_threads = 0;
     // gi_attn_decode_noalloc's partials: the device address of the code object's gi_scratch array on this
@@ -211,9 +220,12 @@ int load_module(const char* path, Module** out) {
             {&m.dec_q4[1], "gi_decode_pm_shared_1_q4"},
             {&m.combine, "gi_decode_combine"},
             {&m.relayout, "gi_kv_relayout"},
+            {&m.hadamard, "gi_hadamard_rows"},
             {&m.prefill[0], "gi_prefill_fwd"},
             {&m.prefill[1], "gi_prefill_fwd_i8"},
             {&m.prefill256r, "gi_prefill_fwd_h256r"},
+            {&m.prefill256r_fmt[0], "gi_prefill_fwd_h256r_i8"},
+            {&m.prefill256r_fmt[1], "gi_prefill_fwd_h256r_q4"},
             {&m.rope, "gi_qk_norm_rope"},
         };
         for (auto& f : fns)
@@ -247,8 +259,9 @@ int load_module(const char* path, Module** out) {
 }
 
 // ---- per-kernel timing (gi_kernel_timing): event pairs around each launch, per kernel kind
-enum Kind { kDecodePartial = 0, kDecodeCombine = 1, kPrefill = 2, kRope = 3, kRelayout = 4, kKinds = 5 };
-const char* const kKindNames[kKinds] = {"decode_partial", "decode_combine", "prefill", "qk_norm_rope", "kv_relayout"};
+enum Kind { kDecodePartial = 0, kDecodeCombine = 1, kPrefill = 2, kRope = 3, kRelayout = 4, kHadamard = 5, kKinds = 6 };
+const char* const kKindNames[kKinds] = {"decode_partial", "decode_combine", "prefill", "qk_norm_rope", "kv_relayout",
+                                        "hadamard_rows"};
 struct Timing {
     std::mutex mu;
     bool on = false;
@@ -525,9 +538,8 @@ int prefill_impl(void* stream, const void* q, int q_dtype, long long q_stride, c
                  long long kv_stride, long long kv_head_stride, void* out, int out_dtype, long long out_stride, int pos0,
                  int n, int n_heads, int n_kv, int hd, float scale) {
     const bool i8 = fmt == 1;
-    if (int e = check_shape(n_heads, n_kv, hd, !i8)) return e;
+    if (int e = check_shape(n_heads, n_kv, hd, true)) return e;
     if (fmt == 2 && hd != 256) return fail("the 4-bit cache takes head size 256 only (got %d)", hd);
-    if (fmt == 2) return fail("the 4-bit prefill kernel is not built");
     if (n <= 0 || pos0 < 0) return fail("n %d must be positive and pos0 %d >= 0", n, pos0);
     if (!q || !kc || !vc || !out) return fail("null tensor pointer");
     if ((q_dtype != GI_F32 && q_dtype != GI_F16) || (out_dtype != GI_F32 && out_dtype != GI_F16))
@@ -575,7 +587,7 @@ int prefill_impl(void* stream, const void* q, int q_dtype, long long q_stride, c
     a.q_f16 = q_dtype == GI_F16;
     a.out_f16 = out_dtype == GI_F16;
     if (hd == 256) // one workgroup per (head, 128 query rows), 16 rows per wave
-        return launch(kPrefill, m->prefill256r, dim3((n + kPrefill256rRows - 1) / kPrefill256rRows * n_heads, 1, 1),
+        return launch(kPrefill, fmt ? m->prefill256r_fmt[fmt - 1] : m->prefill256r, dim3((n + kPrefill256rRows - 1) / kPrefill256rRows * n_heads, 1, 1),
                       dim3(m->prefill256r_threads), (hipStream_t)stream, &a, sizeof a);
     const int qtiles = (n + kPrefillRows - 1) / kPrefillRows; // one workgroup per (head, 256 query rows)
     return launch(kPrefill, m->prefill[i8], dim3(qtiles * n_heads, 1, 1), dim3(m->prefill_threads[i8]),
@@ -583,7 +595,7 @@ int prefill_impl(void* stream, const void* q, int q_dtype, long long q_stride, c
 }
 
 int attention_impl(void* stream, const float* qkv, const void* kc, const void* vc, const float* ks, const float* vs,
-                   bool i8, float* out, void* workspace, size_t workspace_bytes, int pos0, const int* posp, int ctx_cap,
+                   int fmt, float* out, void* workspace, size_t workspace_bytes, int pos0, const int* posp, int ctx_cap,
                    int n, int n_heads, int n_kv, int hd, int exact);
 
 } // namespace
@@ -687,18 +699,49 @@ int gi_attn_prefill_i8(void* stream, const void* q, int q_dtype, long long q_str
                         kv_head_stride, out, out_dtype, out_stride, pos0, n, n_heads, n_kv, hd, scale);
 }
 
+int gi_attn_prefill_q4(void* stream, const void* q, int q_dtype, long long q_stride, const uint8_t* kc,
+                       const uint8_t* vc, const uint16_t* ks, const uint16_t* vs, long long kv_stride,
+                       long long kv_head_stride, long long sc_stride, long long sc_head_stride, void* out, int out_dtype,
+                       long long out_stride, int pos0, int n, int n_heads, int n_kv, float scale) {
+    if (sc_stride == 0 && sc_head_stride == 0) sc_stride = 8LL * n_kv, sc_head_stride = 8;
+    return prefill_impl(stream, q, q_dtype, q_stride, kc, vc, (const float*)ks, (const float*)vs, sc_stride,
+                        sc_head_stride, 2, kv_stride, kv_head_stride, out, out_dtype, out_stride, pos0, n, n_heads, n_kv,
+                        256, scale);
+}
+
 int gi_attention(void* stream, const float* qkv, const uint16_t* kc, const uint16_t* vc, float* out,
                  void* workspace, size_t workspace_bytes, int pos0, const int* posp, int ctx_cap, int n, int n_heads,
                  int n_kv, int hd, int exact) {
-    return attention_impl(stream, qkv, kc, vc, nullptr, nullptr, false, out, workspace, workspace_bytes, pos0, posp,
+    return attention_impl(stream, qkv, kc, vc, nullptr, nullptr, 0, out, workspace, workspace_bytes, pos0, posp,
                           ctx_cap, n, n_heads, n_kv, hd, exact);
 }
 
 int gi_attention_i8(void* stream, const float* qkv, const int8_t* kc, const int8_t* vc, const float* ks,
                     const float* vs, float* out, void* workspace, size_t workspace_bytes, int pos0, const int* posp,
                     int ctx_cap, int n, int n_heads, int n_kv, int hd, int exact) {
-    return attention_impl(stream, qkv, kc, vc, ks, vs, true, out, workspace, workspace_bytes, pos0, posp, ctx_cap, n,
+    return attention_impl(stream, qkv, kc, vc, ks, vs, 1, out, workspace, workspace_bytes, pos0, posp, ctx_cap, n,
                           n_heads, n_kv, hd, exact);
+}
+
+int gi_attention_q4(void* stream, const float* qkv, const uint8_t* kc, const uint8_t* vc, const uint16_t* ks,
+                    const uint16_t* vs, float* out, void* workspace, size_t workspace_bytes, int pos0, const int* posp,
+                    int ctx_cap, int n, int n_heads, int n_kv, int exact) {
+    return attention_impl(stream, qkv, kc, vc, (const float*)ks, (const float*)vs, 2, out, workspace, workspace_bytes,
+                          pos0, posp, ctx_cap, n, n_heads, n_kv, 256, exact);
+}
+
+int gi_hadamard_rows(void* stream, float* x, long long row_stride, int rows, int width) {
+    if (rows < 0 || width <= 0 || width % 256) return fail("rows %d >= 0 and width %d (a multiple of 256) required", rows, width);
+    if (rows == 0) return 0;
+    if (!x) return fail("null tensor pointer");
+    if (!aligned16(x) || row_stride % 4 || row_stride < width)
+        return fail("x must be 16-byte aligned with a row stride (a multiple of 4, >= width)");
+    Module* m;
+    if (int e = load_module(nullptr, &m)) return e;
+    GiHadamardArgs a{x, row_stride, rows, width / 256};
+    const long long segs = (long long)rows * a.segs;
+    return launch(kHadamard, m->hadamard, dim3((unsigned)((segs + 3) / 4)), dim3(256), (hipStream_t)stream, &a,
+                  sizeof a);
 }
 
 } // extern "C"
@@ -706,22 +749,26 @@ int gi_attention_i8(void* stream, const float* qkv, const int8_t* kc, const int8
 namespace {
 // GpuModel::attention's dispatch over either cache type (the reference's layout, scales [pos][n_kv]).
 int attention_impl(void* stream, const float* qkv, const void* kc, const void* vc, const float* ks, const float* vs,
-                   bool i8, float* out, void* workspace, size_t workspace_bytes, int pos0, const int* posp, int ctx_cap,
+                   int fmt, float* out, void* workspace, size_t workspace_bytes, int pos0, const int* posp, int ctx_cap,
                    int n, int n_heads, int n_kv, int hd, int exact) {
     if (int e = check_shape(n_heads, n_kv, hd, true)) return e;
     if (n <= 0) return fail("n %d must be positive", n);
     const long long q_dim = (long long)n_heads * hd, kv_dim = (long long)n_kv * hd, row = q_dim + 2 * kv_dim;
     const float scale = 1.0f / std::sqrt((float)hd);
+    // the reference's cache layouts: [position][n_kv][hd] rows (the 4-bit cache: hd / 2 bytes a row) and scales
+    // [position][n_kv] (the 4-bit cache: [position][n_kv][hd / 32] f16)
+    const long long kvs = fmt == 2 ? kv_dim / 2 : kv_dim, kvh = fmt == 2 ? hd / 2 : hd;
+    const long long scs = fmt == 2 ? (long long)n_kv * (hd / 32) : n_kv, sch = fmt == 2 ? hd / 32 : 1;
     if (n >= kTiledMinBatch && !exact) {
         if (posp) return fail("a device position (posp) is only taken by the split path");
-        return prefill_impl(stream, qkv, GI_F32, row, kc, vc, ks, vs, n_kv, 1, i8, kv_dim, hd, out, GI_F32, q_dim, pos0,
+        return prefill_impl(stream, qkv, GI_F32, row, kc, vc, ks, vs, scs, sch, fmt, kvs, kvh, out, GI_F32, q_dim, pos0,
                             n, n_heads, n_kv, hd, scale);
     }
     for (int b0 = 0; b0 < n; b0 += kSplitMaxBatch) {
         int m = std::min(n - b0, kSplitMaxBatch);
         // with a device position every launch reads *posp, so only single launches take it
         if (posp && n > kSplitMaxBatch) return fail("posp takes at most %d tokens", kSplitMaxBatch);
-        if (int e = decode_impl(stream, qkv + b0 * row, row, kc, vc, ks, vs, n_kv, 1, i8, kv_dim, hd, out + b0 * q_dim,
+        if (int e = decode_impl(stream, qkv + b0 * row, row, kc, vc, ks, vs, scs, sch, fmt, kvs, kvh, out + b0 * q_dim,
                                 q_dim, workspace, workspace_bytes, pos0 + b0, posp, ctx_cap, m, n_heads, n_kv, hd, scale))
             return e;
     }
@@ -743,7 +790,7 @@ int gi_kernel_timing_read(const char* kernel, double* total_ms, int* launches) {
     int kind = -1;
     for (int k = 0; k < kKinds; k++)
         if (std::strcmp(kernel, kKindNames[k]) == 0) kind = k;
-    if (kind < 0) return fail("unknown kernel \"%s\" (decode_partial, decode_combine, prefill, qk_norm_rope or kv_relayout)",
+    if (kind < 0) return fail("unknown kernel \"%s\" (decode_partial, decode_combine, prefill, qk_norm_rope, kv_relayout or hadamard_rows)",
                              kernel);
     std::vector<std::pair<hipEvent_t, hipEvent_t>> ev;
     {

@@ -1006,6 +1006,8 @@ struct GiPrefillArgs {
 // s_waitcnt immediate waiting until at most n vector memory operations are outstanding (gfx9 encoding:
 // vmcnt in bits 3:0 and 15:14, expcnt and lgkmcnt left at their maxima)
 #define GI_VMCNT(n) (0x0F70 | ((n) & 15) | (((n) >> 4) << 14))
+// s_waitcnt immediate waiting for this wave's LDS operations (lgkmcnt 0, vmcnt and expcnt at their maxima)
+#define GI_LGKMCNT0 0xC07F
 #define PF_LPW (16 / PF_SW)   // 1 KB loads per staging wave and tile
 #define PF_NBUF 4          // LDS tile buffers
 #define PF_BK 64           // keys per tile
@@ -1474,9 +1476,16 @@ __device__ __forceinline__ int pf256r_swz_v(int r) { return ((r & 3) << 2) | (((
 // V(it-1) have no reader left, so it refills them with K(it + NKBUF) and V(it + NVBUF - 1): each tile is
 // issued NKBUF - 1 (K) or NVBUF - 1 (V) iterations before its use. Half the waves stage K, half V, and
 // each waits for its own loads only, then the barrier publishes them.
-template <int NKBUF, int NVBUF>
+// FMT 1 (the int8 cache, attention_prefill_tc256 with KV8, src/cuda.rs:2466-2498, 2548-2605) and 2 (the 4-bit
+// cache, with KV4, src/cuda.rs:2495-2514): the staging waves load the compressed rows into registers, widen them
+// to f16 (int8: the exact integers; 4-bit: f16((n - 8) * scale)) and write the same swizzled f16 image, one tile
+// ahead of the barrier that publishes it. int8 also stages each tile's key and value scales: a score is the dot
+// product with the integer key times the key's scale, P V takes f16(p * vscale * 2^10), the row sum the f16 p,
+// and the output is divided by 2^10.
+template <int NKBUF, int NVBUF, int FMT = 0>
 __device__ __forceinline__ void gi_prefill256r(const GiPrefillArgs& a) {
     static_assert(NKBUF >= 2 && NVBUF >= 2 && NKBUF + NVBUF <= 5, "K and V rings within 160 KB");
+    constexpr bool REG = FMT != 0; // staging through registers
     constexpr int HD = 256, WAVES = PF256R_WAVES, BQ = PF256R_BQ, BK = 64;
     constexpr int SW = WAVES / 2;            // waves staging each of K and V
     constexpr int LPW = (BK / 2) / SW;       // 1 KB loads per staging wave and tile (K or V: BK * 512 bytes)
@@ -1485,10 +1494,14 @@ __device__ __forceinline__ void gi_prefill256r(const GiPrefillArgs& a) {
     constexpr int NDB = HD / 16;             // O^T blocks of 16 dims
     constexpr int TILE = BK * 512;           // bytes of one K or V tile image
     __shared__ __attribute__((aligned(1024))) unsigned char smem[(NKBUF + NVBUF) * TILE];
+    __shared__ __attribute__((aligned(16))) float sc_sh[FMT == 1 ? NKBUF + NVBUF : 1][BK]; // int8: tile scales
     auto kbuf = [&](int t) { return smem + (t % NKBUF) * TILE; };
     auto vbuf = [&](int t) { return smem + (NKBUF + t % NVBUF) * TILE; };
+    auto kscl = [&](int t) { return &sc_sh[t % NKBUF][0]; };
+    auto vscl = [&](int t) { return &sc_sh[FMT == 1 ? NKBUF + t % NVBUF : 0][0]; };
     // wait until at most n (0..2) of this wave's tile loads are outstanding
     auto wait_tiles = [&](int n) {
+        if constexpr (REG) return; // (register staging: the compiler waits for the loads it issued)
         if (n >= 2) __builtin_amdgcn_s_waitcnt(GI_VMCNT(2 * LPW));
         else if (n == 1) __builtin_amdgcn_s_waitcnt(GI_VMCNT(LPW));
         else __builtin_amdgcn_s_waitcnt(GI_VMCNT(0));
@@ -1534,6 +1547,63 @@ __device__ __forceinline__ void gi_prefill256r(const GiPrefillArgs& a) {
         unsigned char* dst = (stage_v ? vbuf(t) : kbuf(t)) + 1024 * LPW * (wave % SW);
 #pragma unroll
         for (int i = 0; i < LPW; i++) gi_stage16(src, bytes, (GI_LDS void*)(dst + 1024 * i), soff[i]);
+    };
+    // ---- register staging (FMT 1, 2): staging lane lg = 64(wave % SW) + lane takes a quarter of key lg/4's row,
+    // values 64(lg%4) .. +63, i.e. image row key + 64(quarter/2), units 8(quarter%2) .. +7 (swizzled as above).
+    // int8 rows: 4 16-byte loads and the key's f32 scale (quarter 0's lane); 4-bit rows: 2 16-byte loads and the
+    // two f16 scales of its groups. `pend` holds one tile's loads from its issue to its widening.
+    const int lg = 64 * (wave % SW) + lane, skey = lg >> 2, squart = lg & 3;
+    const int srow = skey + BK * (squart >> 1);
+    struct Pend { u4 w[FMT == 1 ? 4 : 2]; uint32_t sc; int t; } pend;
+    pend.t = -1;
+    const unsigned char* sbase8 = reinterpret_cast<const unsigned char*>(stage_v ? a.vc : a.kc) + kvh * a.kv_head_stride;
+    const void* scbase = nullptr;
+    if constexpr (FMT == 1) scbase = (stage_v ? a.vs : a.ks) + kvh * a.sc_head_stride;
+    if constexpr (FMT == 2) scbase = reinterpret_cast<const uint16_t*>(stage_v ? a.vs : a.ks) + kvh * a.sc_head_stride;
+    auto issue = [&](int t) {
+        const int t0 = t * BK;
+        const __amdgpu_buffer_rsrc_t r = gi_rsrc(sbase8 + (long long)t0 * kvs, (long long)(kv_len - t0) * kvs);
+        if constexpr (FMT == 1) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) pend.w[i] = gi_load16(r, skey * (int)kvs + 64 * squart + 16 * i);
+            const float* sp = reinterpret_cast<const float*>(scbase) + (long long)t0 * a.sc_stride;
+            pend.sc = __builtin_amdgcn_raw_buffer_load_b32(gi_rsrc(sp, (long long)(kv_len - t0) * a.sc_stride * 4),
+                                                           skey * (int)a.sc_stride * 4, 0, 0);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 2; i++) pend.w[i] = gi_load16(r, skey * (int)kvs + 32 * squart + 16 * i);
+            const uint16_t* sp = reinterpret_cast<const uint16_t*>(scbase) + (long long)t0 * a.sc_stride;
+            pend.sc = __builtin_amdgcn_raw_buffer_load_b32(gi_rsrc(sp, (long long)(kv_len - t0) * a.sc_stride * 2),
+                                                           (skey * (int)a.sc_stride + 2 * squart) * 2, 0, 0);
+        }
+        pend.t = t;
+    };
+    // widen the pending tile into its buffer (then this wave's LDS writes are waited for: the barrier that
+    // follows publishes them)
+    auto commit = [&]() {
+        if (pend.t < 0) return;
+        const int t = pend.t;
+        unsigned char* img = stage_v ? vbuf(t) : kbuf(t);
+        const int swz = stage_v ? pf256r_swz_v(srow) : pf256r_swz_k(srow);
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            u4 h;
+            if constexpr (FMT == 1) {
+                const uint32_t x0 = gi_i8_in(pend.w[i >> 1][2 * (i & 1)]), x1 = gi_i8_in(pend.w[i >> 1][2 * (i & 1) + 1]);
+                h = u4{i8_f16x2(x0, GI_I8_LO), i8_f16x2(x0, GI_I8_HI), i8_f16x2(x1, GI_I8_LO), i8_f16x2(x1, GI_I8_HI)};
+            } else {
+                const uint32_t x = pend.w[i >> 2][i & 3];
+                const h2x sc = __builtin_bit_cast(h2x, (i >> 2) ? (pend.sc >> 16) * 0x10001u : (pend.sc & 0xffffu) * 0x10001u);
+                h = u4{q4_f16x2(x >> 4, x, 0, sc), q4_f16x2(x >> 4, x, 1, sc), q4_f16x2(x >> 4, x, 2, sc),
+                       q4_f16x2(x >> 4, x, 3, sc)};
+            }
+            const int unit = (8 * (squart & 1) + i) ^ swz;
+            *reinterpret_cast<GI_LDS u4*>((GI_LDS unsigned char*)img + srow * 256 + (unit << 4)) = h;
+        }
+        if constexpr (FMT == 1)
+            if (squart == 0) (stage_v ? vscl(t) : kscl(t))[skey] = __uint_as_float(pend.sc);
+        pend.t = -1;
+        __builtin_amdgcn_s_waitcnt(GI_LGKMCNT0);
     };
 
     // ---- Q as B operands: lane (column c, k-group g), k-step ks: dims 32ks + 8g .. +7, times scale*log2(e)
@@ -1595,18 +1665,34 @@ __device__ __forceinline__ void gi_prefill256r(const GiPrefillArgs& a) {
     float m_run = 0.f, l_run = 0.f;
     f4 negm = f4{0.f, 0.f, 0.f, 0.f}; // -m_run: the C operand that starts each QK chain
 
+    // this lane's keys of a tile: 32(kb/2) + 8g + 4(kb%2) + r, 4 consecutive per block
+    auto key_scales = [&](const float* sc, f4* out) {
+#pragma unroll
+        for (int kb = 0; kb < NKB; kb++)
+            out[kb] = *reinterpret_cast<const f4*>(sc + 32 * (kb >> 1) + 8 * g + 4 * (kb & 1));
+    };
     auto qk = [&](int t, f4* s) {
         const unsigned char* K = kbuf(t);
         h8 kf[PF_KPF];
 #pragma unroll
         for (int st = 0; st < PF_KPF; st++) kf[st] = kfrag(K, st);
         __builtin_amdgcn_sched_barrier(0);
+        const f4 zero = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int st = 0; st < NKB * KS; st++) {
             const int kb = st % NKB, ks = st / NKB;
             const h8 cur = kf[st % PF_KPF];
             if (st + PF_KPF < NKB * KS) kf[st % PF_KPF] = kfrag(K, st + PF_KPF);
-            s[kb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(cur, qf[ks], ks == 0 ? negm : s[kb], 0, 0, 0);
+            s[kb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(cur, qf[ks], ks == 0 ? (FMT == 1 ? zero : negm) : s[kb], 0, 0,
+                                                           0);
+        }
+        if constexpr (FMT == 1) { // the score: the integer key's dot product times its scale, less the max
+            f4 ksv[NKB];
+            key_scales(kscl(t), ksv);
+#pragma unroll
+            for (int kb = 0; kb < NKB; kb++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) s[kb][r] = fmaf(s[kb][r], ksv[kb][r], -m_run);
         }
     };
     auto rowmax = [&](const f4* sc) {
@@ -1637,14 +1723,21 @@ __device__ __forceinline__ void gi_prefill256r(const GiPrefillArgs& a) {
         }
         qk(it + 1, sn);
         h8 pf[NKB / 2]; // k-step kp: keys 32kp + 8g + e, e = 4(kb%2) + r for block kb = 2kp + kb%2
+        f4 vsv[FMT == 1 ? NKB : 1];
+        if constexpr (FMT == 1) key_scales(vscl(it), vsv);
 #pragma unroll
         for (int kb = 0; kb < NKB; kb++)
 #pragma unroll
             for (int r = 0; r < 4; r += 2) {
-                const _Float16 h0 = (_Float16)__builtin_amdgcn_exp2f(s[kb][r]);
-                const _Float16 h1 = (_Float16)__builtin_amdgcn_exp2f(s[kb][r + 1]);
-                pf[kb >> 1][4 * (kb & 1) + r] = h0;
-                pf[kb >> 1][4 * (kb & 1) + r + 1] = h1;
+                const float p0 = __builtin_amdgcn_exp2f(s[kb][r]), p1 = __builtin_amdgcn_exp2f(s[kb][r + 1]);
+                const _Float16 h0 = (_Float16)p0, h1 = (_Float16)p1;
+                if constexpr (FMT == 1) { // P V weights: f16(p * vscale * 2^10)
+                    pf[kb >> 1][4 * (kb & 1) + r] = (_Float16)(p0 * (vsv[kb][r] * 1024.f));
+                    pf[kb >> 1][4 * (kb & 1) + r + 1] = (_Float16)(p1 * (vsv[kb][r + 1] * 1024.f));
+                } else {
+                    pf[kb >> 1][4 * (kb & 1) + r] = h0;
+                    pf[kb >> 1][4 * (kb & 1) + r + 1] = h1;
+                }
                 l_run = __builtin_amdgcn_fdot2(h2{h0, h1}, h2{(_Float16)1.f, (_Float16)1.f}, l_run, false);
             }
         const unsigned char* V = vbuf(it);
@@ -1664,7 +1757,14 @@ __device__ __forceinline__ void gi_prefill256r(const GiPrefillArgs& a) {
     // prologue: K of tiles 0..NKBUF-1 and V of tiles 0..NVBUF-2 start loading; K(0) is waited for and
     // published (the rest are waited for by the iterations that first read them)
     const int last_k0 = min(NKBUF - 1, ntiles - 1), last_v0 = min(NVBUF - 2, ntiles - 1);
-    for (int t = 0; t <= (stage_v ? last_v0 : last_k0); t++) stage(t);
+    for (int t = 0; t <= (stage_v ? last_v0 : last_k0); t++) {
+        if constexpr (REG) {
+            issue(t);
+            commit();
+        } else {
+            stage(t);
+        }
+    }
     if (!stage_v) wait_tiles(last_k0);
     asm volatile("s_barrier" ::: "memory");
     float mx = GI_NEG_INF;
@@ -1673,9 +1773,15 @@ __device__ __forceinline__ void gi_prefill256r(const GiPrefillArgs& a) {
         // V(it + NVBUF - 2)
         if (stage_v) wait_tiles(max(min(it + NVBUF - 2, ntiles - 1) - it, 0));
         else wait_tiles(max(min(it + NKBUF - 1, ntiles - 1) - (it + 1), 0));
+        if constexpr (REG) commit(); // the tile issued last iteration, before the barrier that publishes it
         asm volatile("s_barrier" ::: "memory");
-        if (!stage_v && it + NKBUF < ntiles) stage(it + NKBUF);    // into K(it)'s buffer
-        if (stage_v && it + NVBUF - 1 < ntiles) stage(it + NVBUF - 1); // into V(it-1)'s buffer
+        if constexpr (REG) {
+            if (!stage_v && it + NKBUF < ntiles) issue(it + NKBUF);
+            if (stage_v && it + NVBUF - 1 < ntiles) issue(it + NVBUF - 1);
+        } else {
+            if (!stage_v && it + NKBUF < ntiles) stage(it + NKBUF);    // into K(it)'s buffer
+            if (stage_v && it + NVBUF - 1 < ntiles) stage(it + NVBUF - 1); // into V(it-1)'s buffer
+        }
         if (it < my_tiles) {
             const int t0 = it * BK;
             if (t0 + BK - 1 > wave_first) { // the tile crosses the diagonal somewhere in the wave
@@ -1703,7 +1809,7 @@ __device__ __forceinline__ void gi_prefill256r(const GiPrefillArgs& a) {
     // ---- normalise and write: lane holds query c, dims 16db + 4g + r
     const float l = rows_sum(l_run);
     if (qrow < a.n) {
-        const float inv = 1.f / l;
+        const float inv = FMT == 1 ? (1.f / 1024.f) / l : 1.f / l;
         if (a.out_f16) {
             _Float16* op = (_Float16*)a.out + (long long)qrow * a.out_stride + h * HD + 4 * g;
 #pragma unroll
@@ -1730,6 +1836,12 @@ extern "C" __global__ void __launch_bounds__(64 * PF_WAVES, 1) gi_prefill_fwd_i8
 #endif
 extern "C" __global__ void __launch_bounds__(64 * PF256R_WAVES, 1) gi_prefill_fwd_h256r(GiPrefillArgs a) {
     gi_prefill256r<PF256R_KBUF, PF256R_VBUF>(a);
+}
+extern "C" __global__ void __launch_bounds__(64 * PF256R_WAVES, 1) gi_prefill_fwd_h256r_i8(GiPrefillArgs a) {
+    gi_prefill256r<PF256R_KBUF, PF256R_VBUF, 1>(a);
+}
+extern "C" __global__ void __launch_bounds__(64 * PF256R_WAVES, 1) gi_prefill_fwd_h256r_q4(GiPrefillArgs a) {
+    gi_prefill256r<PF256R_KBUF, PF256R_VBUF, 2>(a);
 }
 
 // ------------------------------------------------------------------------------------------------ KV store
@@ -1919,6 +2031,30 @@ extern "C" __global__ void __launch_bounds__(256) gi_qk_norm_rope(GiRopeArgs a) 
     if (a.hd == 64) gi_qk_norm_rope_t<1>(a, cs_sh, row_sh);
     else if (a.hd == 128) gi_qk_norm_rope_t<2>(a, cs_sh, row_sh);
     else gi_qk_norm_rope_t<4>(a, cs_sh, row_sh);
+}
+
+// ------------------------------------------------------------------------------- output rotation (4-bit cache)
+
+// Arguments of gi_hadamard_rows (must match gi_attn_host.cpp).
+struct GiHadamardArgs {
+    float* x;              // rows of segs * 256 floats, row_stride apart
+    long long row_stride;
+    int rows;
+    int segs;              // 256-value segments a row
+};
+
+// hadamard_rows with block 256 and no signs (src/cuda.rs:4675-4693), as the layer applies it to the attention
+// output of a 4-bit cache (src/cuda.rs:9765-9768): every 256-value segment of a row, in place, through the
+// normalized Walsh-Hadamard transform (the same stages as kv4_fwht; its rsqrtf(256) is 1/16). One wave per
+// segment, 4 values a lane.
+extern "C" __global__ void __launch_bounds__(256) gi_hadamard_rows(GiHadamardArgs a) {
+    const int lane = threadIdx.x & 63;
+    const long long seg = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (seg >= (long long)a.rows * a.segs) return;
+    float* p = a.x + (seg / a.segs) * a.row_stride + (seg % a.segs) * 256 + 4 * lane;
+    float __attribute__((ext_vector_type(4))) v = *reinterpret_cast<float __attribute__((ext_vector_type(4)))*>(p);
+    gi_fwht256(v, lane);
+    *reinterpret_cast<float __attribute__((ext_vector_type(4)))*>(p) = v;
 }
 
 // ------------------------------------------------------------------------------------------- cache growth

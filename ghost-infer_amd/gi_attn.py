@@ -39,6 +39,9 @@ SYMBOLS = (
     "gi_attn_prefill_i8",
     "gi_attention",
     "gi_attention_i8",
+    "gi_attn_prefill_q4",
+    "gi_attention_q4",
+    "gi_hadamard_rows",
     "gi_qk_norm_rope",
     "gi_qk_norm_rope_i8",
     "gi_qk_norm_rope_q4",
@@ -91,6 +94,12 @@ def load_library(path=LIB_PATH):
     lib.gi_attn_prefill_i8.restype = i
     lib.gi_attention_i8.argtypes = [vp, vp, vp, vp, vp, vp, vp, vp, sz, i, vp, i, i, i, i, i, i]
     lib.gi_attention_i8.restype = i
+    lib.gi_attn_prefill_q4.argtypes = [vp, vp, i, ll, vp, vp, vp, vp, ll, ll, ll, ll, vp, i, ll, i, i, i, i, f]
+    lib.gi_attn_prefill_q4.restype = i
+    lib.gi_attention_q4.argtypes = [vp, vp, vp, vp, vp, vp, vp, vp, sz, i, vp, i, i, i, i, i]
+    lib.gi_attention_q4.restype = i
+    lib.gi_hadamard_rows.argtypes = [vp, vp, ll, i, i]
+    lib.gi_hadamard_rows.restype = i
     lib.gi_qk_norm_rope.argtypes = [vp, vp, vp, vp, vp, vp, ll, ll, i, vp, i, i, i, i, i, i, f, vp, i, f]
     lib.gi_qk_norm_rope.restype = i
     lib.gi_qk_norm_rope_i8.argtypes = [vp, vp, vp, vp, vp, vp, vp, vp, ll, ll, ll, ll, i, vp, i, i, i, i, i, i, f, vp,
@@ -293,6 +302,74 @@ def decode_q4(q, k_cache, v_cache, k_scale, v_scale, pos0, n_heads, n_kv, scale=
                                             workspace.numel() * workspace.element_size(), pos0, _ptr(posp), ctx_cap,
                                             n_tok, n_heads, n_kv, scale))
     return out
+
+
+def prefill_q4(q, k_cache, v_cache, k_scale, v_scale, pos0, n_heads, n_kv, scale=None, out=None, out_dtype=None,
+               kv_layout="reference"):
+    """Causal prefill over the 4-bit cache (head size 256; attention_prefill_tc256 with KV4, src/cuda.rs:2495-2514):
+    q the rotated queries, f32 or f16 [n, >= n_heads*256]; returns rotated rows of out_dtype (default q's)."""
+    if q.dtype not in (torch.float32, torch.float16):
+        raise GiAttnError("q must be float32 or float16")
+    _need(q, "q", q.dtype)
+    kv_stride, kv_head_stride, sc_stride, sc_head_stride, capacity = _q4_layout(k_cache, v_cache, k_scale, v_scale,
+                                                                                n_kv, kv_layout)
+    n = q.shape[0]
+    if capacity < pos0 + n:
+        raise GiAttnError(f"the cache holds {capacity} positions; {pos0 + n} needed")
+    if scale is None:
+        scale = 1.0 / 16.0
+    if out is None:
+        out = torch.empty((n, n_heads * 256), dtype=out_dtype or q.dtype, device=q.device)
+    if out.dtype not in (torch.float32, torch.float16):
+        raise GiAttnError("out must be float32 or float16")
+    _need(out, "out", out.dtype)
+    qd = GI_F16 if q.dtype == torch.float16 else GI_F32
+    od = GI_F16 if out.dtype == torch.float16 else GI_F32
+    _check(load_library().gi_attn_prefill_q4(_stream(), _ptr(q), qd, q.stride(0), _ptr(k_cache), _ptr(v_cache),
+                                             _ptr(k_scale), _ptr(v_scale), kv_stride, kv_head_stride, sc_stride,
+                                             sc_head_stride, _ptr(out), od, out.stride(0), pos0, n, n_heads, n_kv,
+                                             scale))
+    return out
+
+
+def attention_q4(qkv, k_cache, v_cache, k_scale, v_scale, pos0, n_heads, n_kv, exact=False, out=None, workspace=None,
+                 posp=None, ctx_cap=0):
+    """GpuModel::attention over the 4-bit cache (head size 256, the reference layout): qkv rows [q | k | v] f32 with
+    the rotated queries qk_norm_rope_q4 leaves; returns the rotated output f32 [n, n_heads*256] (hadamard_rows
+    turns it back, as the layer does)."""
+    _need(qkv, "qkv", torch.float32)
+    n = qkv.shape[0]
+    row = (n_heads + 2 * n_kv) * 256
+    if qkv.shape[1] != row or not qkv.is_contiguous():
+        raise GiAttnError(f"qkv must be contiguous [n, {row}]")
+    *_, capacity = _q4_layout(k_cache, v_cache, k_scale, v_scale, n_kv, "reference")
+    if capacity < max(pos0 + n, ctx_cap if posp is not None else 0):
+        raise GiAttnError(f"the cache holds {capacity} positions; {pos0 + n} needed")
+    if out is None:
+        out = torch.empty((n, n_heads * 256), dtype=torch.float32, device=qkv.device)
+    _need(out, "out", torch.float32)
+    if posp is not None:
+        _need(posp, "posp", torch.int32)
+    ws_ptr, ws_bytes = None, 0
+    if n < TILED_MIN_BATCH or exact:
+        if workspace is None:
+            cap = ctx_cap if posp is not None else pos0 + n
+            workspace = new_workspace(cap, min(n, SPLIT_MAX_BATCH), n_heads, n_kv, 256, qkv.device)
+        ws_ptr, ws_bytes = _ptr(workspace), workspace.numel() * workspace.element_size()
+    _check(load_library().gi_attention_q4(_stream(), _ptr(qkv), _ptr(k_cache), _ptr(v_cache), _ptr(k_scale),
+                                          _ptr(v_scale), _ptr(out), ws_ptr, ws_bytes, pos0, _ptr(posp), ctx_cap, n,
+                                          n_heads, n_kv, 1 if exact else 0))
+    return out
+
+
+def hadamard_rows(x):
+    """hadamard_rows with block 256 (src/cuda.rs:4675-4693), in place on f32 rows [rows, width] (width a multiple of
+    256): turns the rotated attention output of a 4-bit cache back."""
+    _need(x, "x", torch.float32)
+    if x.dim() != 2:
+        raise GiAttnError("x must be [rows, width]")
+    _check(load_library().gi_hadamard_rows(_stream(), _ptr(x), x.stride(0), x.shape[0], x.shape[1]))
+    return x
 
 
 def prefill(q, k_cache, v_cache, pos0, n_heads, n_kv, hd=128, scale=None, out=None, out_dtype=None,

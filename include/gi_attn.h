@@ -126,12 +126,22 @@ int gi_attn_prefill(void* stream, const void* q, int q_dtype, long long q_stride
 
 /* gi_attn_prefill over an int8 KV cache (layouts and scales as gi_attn_decode_i8). The keys enter the
  * scores as exact integers times their scale; P V takes f16(p * vs) and the row sum the f16-rounded p.
- * Dequantised values must stay within |v| < 4000 (the f16 range of p * vs with p <= 256). Replaces:
- * attention_prefill_tc128 compiled with KV8 (src/cuda.rs:2408-2621, int8 staging src/cuda.rs:2466-2498). */
+ * Dequantised values must stay within |v| < 4000 (the f16 range of p * vs with p <= 256); the output is
+ * O / 2^10 / l. hd 128 or 256. Replaces: attention_prefill_tc128 and attention_prefill_tc256 compiled with KV8
+ * (src/cuda.rs:2408-2623, int8 staging src/cuda.rs:2466-2498). */
 int gi_attn_prefill_i8(void* stream, const void* q, int q_dtype, long long q_stride, const int8_t* kc, const int8_t* vc,
                        const float* ks, const float* vs, long long kv_stride, long long kv_head_stride,
                        long long sc_stride, long long sc_head_stride, void* out, int out_dtype, long long out_stride,
                        int pos0, int n, int n_heads, int n_kv, int hd, float scale);
+
+/* gi_attn_prefill over the 4-bit cache (head size 256; layouts as gi_attn_decode_q4): the tiles are widened to
+ * the f16 values f16((n - 8) * scale) and the rest is the f16 cache's prefill. q: the rotated queries; out: rotated
+ * rows (gi_hadamard_rows turns them back). Replaces: attention_prefill_tc256 compiled with KV4 (src/cuda.rs:
+ * 2495-2514, 2622-2623). */
+int gi_attn_prefill_q4(void* stream, const void* q, int q_dtype, long long q_stride, const uint8_t* kc,
+                       const uint8_t* vc, const uint16_t* ks, const uint16_t* vs, long long kv_stride,
+                       long long kv_head_stride, long long sc_stride, long long sc_head_stride, void* out, int out_dtype,
+                       long long out_stride, int pos0, int n, int n_heads, int n_kv, float scale);
 
 /* The attention operator of one layer, as GpuModel::attention (src/cuda.rs:8448-8541) dispatches it:
  * qkv rows are [q (n_heads*hd) | k | v] f32 (stride n_heads*hd + 2*n_kv*hd, src/cuda.rs:1713), out rows
@@ -148,6 +158,20 @@ int gi_attention(void* stream, const float* qkv, const uint16_t* kc, const uint1
 int gi_attention_i8(void* stream, const float* qkv, const int8_t* kc, const int8_t* vc, const float* ks,
                     const float* vs, float* out, void* workspace, size_t workspace_bytes, int pos0, const int* posp,
                     int ctx_cap, int n, int n_heads, int n_kv, int hd, int exact);
+
+/* gi_attention over the reference's 4-bit cache (head size 256): kc / vc [position][n_kv][128] bytes, ks / vs
+ * [position][n_kv][8] f16 (src/cuda.rs:8448-8541 with KV4). q rows of qkv are the rotated queries that
+ * gi_qk_norm_rope_q4 leaves; out holds rotated rows, which the layer turns back with gi_hadamard_rows
+ * (src/cuda.rs:9765-9768). */
+int gi_attention_q4(void* stream, const float* qkv, const uint8_t* kc, const uint8_t* vc, const uint16_t* ks,
+                    const uint16_t* vs, float* out, void* workspace, size_t workspace_bytes, int pos0, const int* posp,
+                    int ctx_cap, int n, int n_heads, int n_kv, int exact);
+
+/* The attention output of a 4-bit cache rotated back: every 256-value segment of rows rows (width floats each,
+ * a multiple of 256, row_stride apart) through the normalized Walsh-Hadamard transform, in place, stream-ordered.
+ * Replaces: hadamard_rows with block 256 and no signs (src/cuda.rs:4675-4693) as the layer launches it after
+ * attention over a 4-bit cache (src/cuda.rs:9765-9768). */
+int gi_hadamard_rows(void* stream, float* x, long long row_stride, int rows, int width);
 
 /* The layer's step before attention, for a batch of n tokens at positions pos0.. (posp: read from device
  * memory, graph replay). ctx_cap: positions the cache holds; rows at positions outside [0, ctx_cap) are not
@@ -199,7 +223,7 @@ int gi_kv_relayout(void* stream, const void* src, long long src_stride, long lon
 int gi_kernel_timing(int on);
 
 /* Total milliseconds and launch count of kernel kind `kernel` ("decode_partial", "decode_combine",
- * "prefill", "qk_norm_rope" or "kv_relayout") recorded since the previous read of that kind; waits for the recorded events and
+ * "prefill", "qk_norm_rope", "kv_relayout" or "hadamard_rows") recorded since the previous read of that kind; waits for the recorded events and
  * releases them. */
 int gi_kernel_timing_read(const char* kernel, double* total_ms, int* launches);
 

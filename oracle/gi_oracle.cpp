@@ -19,7 +19,7 @@
 //   gio_kv_quant_i8                   src/cuda.rs:333-339 (kv_store with KV8: row max / 127, rint)
 //   gio_qk_norm_rope_i8               src/cuda.rs:437-486 storing with kv_quant_i8
 //   gio_prefill_tc256                 gio_prefill_tc at head size 256 (attention_prefill_tc256, src/cuda.rs:2623)
-//   gio_prefill_tc_i8                 gio_prefill_tc over the KV8 cache (src/cuda.rs:2466-2498, 2548-2605:
+//   gio_prefill_tc_i8 / _tc256_i8     gio_prefill_tc (head size 128 / 256) over the KV8 cache (src/cuda.rs:2466-2498, 2548-2605:
 //                                     integer keys, score times key scale, P V with f16(p * vs * 2^10))
 //   gio_decode_gpu_i8                 gio_decode_gpu over the KV8 cache (src/cuda.rs:209-226, 1758-1760,
 //                                     1821-1827: key scale on the score, value scale on the weight)
@@ -753,6 +753,15 @@ void gio_prefill_tc_i8(const float* q, long q_stride, const int8_t* kc, const in
                        const float* vs, long kv_stride, float* out, long out_stride, int pos0, int n, int n_heads,
                        int n_kv, float scale, int threads) {
     prefill_tc<int8_t>(q, q_stride, kc, vc, ks, vs, kv_stride, out, out_stride, pos0, n, n_heads, n_kv, scale, threads);
+}
+
+// attention_prefill_tc256 with KV8 (attn_prefill_tc<256, 2>, src/cuda.rs:2623): gio_prefill_tc_i8's arithmetic at
+// head size 256.
+void gio_prefill_tc256_i8(const float* q, long q_stride, const int8_t* kc, const int8_t* vc, const float* ks,
+                          const float* vs, long kv_stride, float* out, long out_stride, int pos0, int n, int n_heads,
+                          int n_kv, float scale, int threads) {
+    prefill_tc<int8_t>(q, q_stride, kc, vc, ks, vs, kv_stride, out, out_stride, pos0, n, n_heads, n_kv, scale, threads,
+                       256);
 }
 
 // qk_norm_rope storing into an int8 cache (kv_store with KV8, src/cuda.rs:333-339): kc / vc int8 rows in the

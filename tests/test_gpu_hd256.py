@@ -243,3 +243,66 @@ def test_attention_operator_hd256(gpu, n, pos0, exact):
     assert_close(out.cpu().numpy(), reference_f64(q, k, v, pos0, n_heads, n_kv, hd=HD),
                  max_abs=2e-5 if split_path else 2e-3, rel_l2=2e-5 if split_path else 1e-3,
                  what="operator hd256 vs f64")
+
+
+# ---------------------------------------------------------------- prefill over the int8 cache (attn_prefill_tc<256, 2>
+# with KV8): integer keys times their scale on the score, f16(p * vscale * 2^10) for P V, output / 2^10 / l
+
+PREFILL_SHAPES_256_I8 = [
+    (16, 0, 8, 2, "reference"),
+    (65, 0, 4, 1, "reference"),
+    (127, 63, 8, 2, "head_major"),
+    (129, 0, 8, 8, "reference"),
+    (300, 40, 16, 2, "head_major"),
+    (1000, 24, 16, 2, "reference"),
+]
+
+
+@pytest.mark.parametrize("n,pos0,n_heads,n_kv,layout", PREFILL_SHAPES_256_I8)
+def test_prefill_hd256_i8(gpu, n, pos0, n_heads, n_kv, layout):
+    say("prefill hd256 i8", n, pos0, n_heads, n_kv, layout)
+    q, k, v, ks, vs = make_inputs_i8(8100 + n + pos0, n, pos0 + n, n_heads, n_kv, hd=HD)
+    qt, kt, vt, kst, vst = to_dev_i8(q, k, v, ks, vs, gpu, n_kv, layout)
+    out = gi_attn.prefill(qt, kt, vt, pos0, n_heads, n_kv, hd=HD, out_dtype=torch.float32, kv_layout=layout,
+                          k_scale=kst, v_scale=vst)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    assert_close(got, O.prefill_tc_semantics_i8(q, k, v, ks, vs, pos0, n_heads, n_kv, hd=HD),
+                 what="prefill hd256 i8 vs oracle (attention_prefill_tc256 with KV8)")
+    assert_close(got, reference_f64_i8(q, k, v, ks, vs, pos0, n_heads, n_kv, hd=HD), what="prefill hd256 i8 vs f64")
+
+
+def test_prefill_hd256_i8_4096_and_chunks(gpu):
+    # a 4096-token prompt over the int8 cache: sampled rows against float64, and chunks of 1024 at their prefix
+    # give the whole prompt's rows bit for bit
+    n, n_heads, n_kv = 4096, 16, 2
+    say("prefill hd256 i8 4096")
+    q, k, v, ks, vs = make_inputs_i8(83, n, n, n_heads, n_kv, hd=HD)
+    qt, kt, vt, kst, vst = to_dev_i8(q, k, v, ks, vs, gpu, n_kv)
+    whole = gi_attn.prefill(qt, kt, vt, 0, n_heads, n_kv, hd=HD, k_scale=kst, v_scale=vst)
+    parts = [gi_attn.prefill(qt[c0:c0 + 1024], kt, vt, c0, n_heads, n_kv, hd=HD, k_scale=kst, v_scale=vst)
+             for c0 in range(0, n, 1024)]
+    torch.cuda.synchronize()
+    got = whole.cpu().numpy()
+    for r in (0, 31, 127, 128, 2047, 4095):
+        assert_close(got[r:r + 1], reference_f64_i8(q[r:r + 1], k, v, ks, vs, r, n_heads, n_kv, hd=HD),
+                     what=f"prefill hd256 i8 row {r} vs f64")
+    assert np.array_equal(torch.cat(parts).cpu().numpy(), got)
+
+
+@pytest.mark.parametrize("n,pos0,exact", [(1, 99, False), (8, 300, True), (20, 0, False), (40, 17, True)])
+def test_attention_operator_hd256_i8(gpu, n, pos0, exact):
+    say("operator hd256 i8", n, pos0, exact)
+    n_heads, n_kv = 16, 2
+    row = n_heads * HD + 2 * n_kv * HD
+    qkv = np.random.default_rng(197 + n).standard_normal((n, row), dtype=np.float32)
+    _, k, v, ks, vs = make_inputs_i8(198 + n, 1, pos0 + n, n_heads, n_kv, hd=HD)
+    qkv_t = torch.from_numpy(qkv).to(gpu)
+    _, kt, vt, kst, vst = to_dev_i8(qkv[:, :1], k, v, ks, vs, gpu, n_kv)
+    out = gi_attn.attention(qkv_t, kt, vt, pos0, n_heads, n_kv, hd=HD, exact=exact, k_scale=kst, v_scale=vst)
+    torch.cuda.synchronize()
+    q = np.ascontiguousarray(qkv[:, :n_heads * HD])
+    split_path = n < 16 or exact
+    assert_close(out.cpu().numpy(), reference_f64_i8(q, k, v, ks, vs, pos0, n_heads, n_kv, hd=HD),
+                 max_abs=2e-5 if split_path else 2e-3, rel_l2=2e-5 if split_path else 1e-3,
+                 what="operator hd256 i8 vs f64")

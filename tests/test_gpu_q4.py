@@ -157,3 +157,89 @@ def test_q4_layer_end_to_end(gpu):
     exact = _reference_f64_values(qkv[n - 1:, :H * 256], qkv[:, H * 256:(H + K) * 256], qkv[:, (H + K) * 256:],
                                   n - 1, H, K, 256)
     assert np.abs(back - exact).max() < 0.05
+
+
+PREFILL_SHAPES_Q4 = [
+    # (n, pos0, n_heads, n_kv, q dtype, layout): one tile, diagonal and tile edges (64 keys, 128 query rows per
+    # workgroup), chunks at a prefix, both layouts
+    (16, 0, 8, 2, np.float32, "reference"),
+    (65, 0, 4, 1, np.float16, "reference"),
+    (127, 63, 8, 2, np.float32, "head_major"),
+    (129, 0, 8, 8, np.float32, "reference"),
+    (300, 40, 16, 2, np.float16, "head_major"),
+    (1000, 24, 16, 2, np.float32, "reference"),
+]
+
+
+@pytest.mark.parametrize("n,pos0,n_heads,n_kv,qd,layout", PREFILL_SHAPES_Q4)
+def test_prefill_q4(gpu, n, pos0, n_heads, n_kv, qd, layout):
+    say("prefill q4", n, pos0, n_heads, n_kv, qd.__name__, layout)
+    q, kc, vc, ks, vs = make_inputs_q4(900 + n + pos0, n, pos0 + n, n_heads, n_kv)
+    q = q.astype(qd)
+    t = q4_dev(q, kc, vc, ks, vs, gpu, n_kv, layout)
+    out = gi_attn.prefill_q4(*t, pos0, n_heads, n_kv, out_dtype=torch.float32, kv_layout=layout)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    q32 = q.astype(np.float32)
+    assert_close(got, O.prefill_tc256_q4(q32, kc, vc, ks, vs, pos0, n_heads, n_kv),
+                 what="prefill q4 vs oracle (attention_prefill_tc256 with KV4)")
+    assert_close(got, reference_f64_q4(q32, kc, vc, ks, vs, pos0, n_heads, n_kv), what="prefill q4 vs f64")
+
+
+def test_prefill_q4_4096_and_chunks(gpu):
+    n, n_heads, n_kv = 4096, 16, 2
+    say("prefill q4 4096")
+    q, kc, vc, ks, vs = make_inputs_q4(91, n, n, n_heads, n_kv)
+    t = q4_dev(q, kc, vc, ks, vs, gpu, n_kv)
+    whole = gi_attn.prefill_q4(*t, 0, n_heads, n_kv)
+    parts = [gi_attn.prefill_q4(t[0][c0:c0 + 1024], *t[1:], c0, n_heads, n_kv) for c0 in range(0, n, 1024)]
+    torch.cuda.synchronize()
+    got = whole.cpu().numpy()
+    for r in (0, 31, 127, 128, 2047, 4095):
+        assert_close(got[r:r + 1], reference_f64_q4(q[r:r + 1], kc, vc, ks, vs, r, n_heads, n_kv),
+                     what=f"prefill q4 row {r} vs f64")
+    assert np.array_equal(torch.cat(parts).cpu().numpy(), got)
+
+
+def test_hadamard_rows_bit_exact(gpu):
+    # hadamard_rows with block 256: every segment of every row equals kv4_fwht's bits (also with a row stride
+    # wider than the rows)
+    rng = np.random.default_rng(31)
+    x = (rng.standard_normal((37, 16 * 256)) * np.exp(rng.uniform(-10, 10, (37, 16 * 256)))).astype(np.float32)
+    say("hadamard rows")
+    big = torch.zeros((37, 16 * 256 + 64), dtype=torch.float32, device=gpu)
+    big[:, :16 * 256] = torch.from_numpy(x).to(gpu)
+    view = big[:, :16 * 256]
+    gi_attn.hadamard_rows(view)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(view.cpu().numpy(), O.kv4_fwht(x.reshape(-1, 256)).reshape(37, -1))
+    assert not big[:, 16 * 256:].any()
+
+
+@pytest.mark.parametrize("n,pos0,exact", [(1, 99, False), (8, 300, True), (20, 0, False), (40, 17, True)])
+def test_attention_operator_q4(gpu, n, pos0, exact):
+    # GpuModel::attention over the 4-bit cache: prefill from 16 tokens unless exact, else the split decode path;
+    # then hadamard_rows turns the output back, and it is the attention of the unrotated queries over the
+    # unrotated cache rows (the cache's f16 values rotated back in float64)
+    say("operator q4", n, pos0, exact)
+    n_heads, n_kv = 16, 2
+    row = (n_heads + 2 * n_kv) * 256
+    qkv = np.random.default_rng(297 + n).standard_normal((n, row), dtype=np.float32)
+    _, kc, vc, ks, vs = make_inputs_q4(298 + n, 1, pos0 + n, n_heads, n_kv)
+    qkv_t = torch.from_numpy(qkv).to(gpu)
+    _, kt, vt, kst, vst = q4_dev(qkv[:, :1], kc, vc, ks, vs, gpu, n_kv)
+    out = gi_attn.attention_q4(qkv_t, kt, vt, kst, vst, pos0, n_heads, n_kv, exact=exact)
+    gi_attn.hadamard_rows(out)
+    torch.cuda.synchronize()
+    q = np.ascontiguousarray(qkv[:, :n_heads * 256])
+    split_path = n < 16 or exact
+    rot = reference_f64_q4(q, kc, vc, ks, vs, pos0, n_heads, n_kv)
+    want = (rot.reshape(-1, 256) @ _h256()).reshape(rot.shape)
+    assert_close(out.cpu().numpy(), want, max_abs=2e-5 if split_path else 2e-3, rel_l2=2e-5 if split_path else 1e-3,
+                 what="operator q4 (rotated back) vs f64")
+
+
+def _h256():
+    i = np.arange(256)
+    bits = np.vectorize(lambda x: bin(x).count("1"))(i[:, None] & i[None, :])
+    return np.where(bits % 2 == 0, 1.0, -1.0) / 16.0

@@ -723,3 +723,23 @@ def test_prefill_tc256_q4_within_parity_bar(n, pos0, n_heads, n_kv):
     want = reference_f64_q4(q, kc, vc, ks, vs, pos0, n_heads, n_kv)
     ma, _ = assert_close(got, want, what="prefill_tc256 KV4 semantics vs f64")
     assert ma > 1e-6
+
+
+@pytest.mark.parametrize("n,pos0,n_heads,n_kv", [(48, 0, 4, 2), (70, 33, 4, 1)])
+def test_prefill_tc_semantics_i8_hd256_within_parity_bar(n, pos0, n_heads, n_kv):
+    # attention_prefill_tc256 with KV8: the int8 roundings at head size 256, within the bar of the exact attention
+    q, k, v, ks, vs = make_inputs_i8(61 + n, n, pos0 + n, n_heads, n_kv, hd=256)
+    got = O.prefill_tc_semantics_i8(q, k, v, ks, vs, pos0, n_heads, n_kv, hd=256)
+    ma, _ = assert_close(got, reference_f64_i8(q, k, v, ks, vs, pos0, n_heads, n_kv, hd=256),
+                         what="int8 prefill hd256 semantics vs f64")
+    assert ma > 1e-6
+
+
+def test_prefill_i8_hd256_unit_scales_follow_the_f16_path():
+    q, k, v, _, _ = make_inputs_i8(9, 50, 120, 4, 2, hd=256)
+    k = (k // 16).astype(np.int8)
+    ones = np.ones((120, 2), dtype=np.float32)
+    got = O.prefill_tc_semantics_i8(q, k, v, ones, ones, 70, 4, 2, hd=256)
+    want = O.prefill_tc_semantics(q, k.astype(np.float16).view(np.uint16), v.astype(np.float16).view(np.uint16), 70,
+                                  4, 2, hd=256)
+    np.testing.assert_allclose(got, want, rtol=0, atol=1e-4)
