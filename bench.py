@@ -2,7 +2,8 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload decode64k|decode4k|verify|prefill8k|chunked|qkrope|
                     decode64k_i8|verify_i8|prefill8k_i8|decode64k_h256|verify_h256|prefill8k_h256|
-                    decode64k_h256_i8|verify_h256_i8]
+                    decode64k_h256_i8|verify_h256_i8|prefill8k_h256_i8|decode64k_h256_q4|verify_h256_q4|
+                    prefill8k_h256_q4]
                     [--no-cpu-baseline] [--no-secondary] [--reference-layout]
 
 A step is one pass of the hot path over one batch of synthetic seeded input already resident in HBM:
@@ -16,8 +17,10 @@ A step is one pass of the hot path over one batch of synthetic seeded input alre
   decode64k_h256, verify_h256, prefill8k_h256
              head size 256 (Qwen3.5-style 16 query / 2 kv heads): decode at 65536 keys, an 8-token verify at
              32768, prefill of 8192
-  decode64k_h256_i8, verify_h256_i8
-             head size 256 over the int8 cache (the reference's attention_decode_tc256 shapes)
+  decode64k_h256_i8, verify_h256_i8, prefill8k_h256_i8
+             head size 256 over the int8 cache (the reference's attention_decode_tc256 / prefill_tc256 shapes)
+  decode64k_h256_q4, verify_h256_q4, prefill8k_h256_q4
+             head size 256 over the 4-bit cache (the reference's --kv q4: 128 bytes a row plus 8 f16 scales)
   decode64k_i8, verify_i8, prefill8k_i8
              configs 2, 4 and 3 over the int8 cache (the reference's KV8 format: int8 rows, an f32 scale per
              position and kv head); bytes are the int8 rows plus their scales
@@ -54,9 +57,19 @@ def log(*a):
 def seeded_cache(gen, rows, n_kv, dev, torch, layout="reference", i8=False, hd=HD):
     """K and V caches of N(0,1) f16 values: [rows, n_kv, HD] (the reference's layout) or [n_kv, rows, HD]
     (head-major, each kv head's rows contiguous). i8: int8 rows round(40 N(0,1)) clipped to -127..127 and
-    f32 scales in [0.02, 0.03] ([rows, n_kv] or [n_kv, rows]), like quantised N(0,1) rows; returns
-    (k, v, k_scale, v_scale)."""
+    f32 scales in [0.02, 0.03] ([rows, n_kv] or [n_kv, rows]), like quantised N(0,1) rows. i8 == "q4": the
+    4-bit cache (head size 256), random nibbles 1..15 in rows of 128 bytes and f16 scales in [0.2, 0.35], 8 a
+    row. Returns (k, v, k_scale, v_scale)."""
     shape = (rows, n_kv, hd) if layout == "reference" else (n_kv, rows, hd)
+    if i8 == "q4":
+        def nib():
+            return torch.randint(0, 256, shape[:2] + (128,), generator=gen, device=dev, dtype=torch.int32).to(
+                torch.uint8) | 0x11
+
+        def scl():
+            return (torch.rand(shape[:2] + (8,), generator=gen, device=dev) * 0.15 + 0.2).half()
+
+        return nib(), nib(), scl(), scl()
     if i8:
         def ints():
             x = torch.randn(shape, generator=gen, device=dev, dtype=torch.float32) * 40
@@ -101,6 +114,8 @@ def decode_kernel_name(n_tok, n_heads, n_kv, hd, i8):
     per MFMA column, with two column blocks per wave above 16 pairs at head size 128 (f16 above 32 pairs:
     two pair sets per workgroup, each over two waves), and 4 waves sharing each tile at head size 256)."""
     pairs, p = n_tok * (n_heads // n_kv), 8
+    if i8 == "q4":
+        return "gi_decode_pm_shared_1_q4" if pairs > p else "gi_decode_partial_1_q4"
     if pairs <= p:
         name = "gi_decode_partial_1"
     elif hd == 256:
@@ -170,7 +185,8 @@ def decode_workload(torch, gi_attn, dev, ctx, n_heads, n_kv, n_tok, steps, warmu
     gen = torch.Generator(device=dev)
     gen.manual_seed(seed)
     # K+V bytes of one step: every key row once (int8 rows plus their two f32 scales)
-    kv_bytes = 2 * ctx * n_kv * (hd + 4) if i8 else 2 * ctx * n_kv * hd * 2
+    kv_bytes = (2 * ctx * n_kv * (hd // 2 + hd // 16) if i8 == "q4" else 2 * ctx * n_kv * (hd + 4) if i8
+                else 2 * ctx * n_kv * hd * 2)
     layers = max(1, math.ceil(512e6 / kv_bytes))  # > 256 MB Infinity Cache in total
     caches = [seeded_cache(gen, ctx, n_kv, dev, torch, layout, i8, hd) for _ in range(layers)]
     q = torch.randn((n_tok, n_heads * hd), generator=gen, device=dev, dtype=torch.float32)
@@ -180,8 +196,11 @@ def decode_workload(torch, gi_attn, dev, ctx, n_heads, n_kv, n_tok, steps, warmu
 
     def step(i):
         k, v, ks, vs = caches[i % layers]
-        gi_attn.decode(q, k, v, pos0, n_heads, n_kv, hd=hd, out=out, workspace=ws, kv_layout=layout, k_scale=ks,
-                       v_scale=vs)
+        if i8 == "q4":
+            gi_attn.decode_q4(q, k, v, ks, vs, pos0, n_heads, n_kv, out=out, workspace=ws, kv_layout=layout)
+        else:
+            gi_attn.decode(q, k, v, pos0, n_heads, n_kv, hd=hd, out=out, workspace=ws, kv_layout=layout, k_scale=ks,
+                           v_scale=vs)
 
     t = time_steps_graph(step, steps, warmup, torch)
     return {"seconds": t, "bytes": kv_bytes, "layers": layers, "q": q, "cache": caches[0], "pos0": pos0,
@@ -202,7 +221,10 @@ def prefill_workload(torch, gi_attn, dev, n, n_heads, n_kv, steps, warmup, seed,
     out = torch.empty((n, n_heads * hd), device=dev, dtype=torch.float16)
 
     def step(i):
-        gi_attn.prefill(q, k, v, 0, n_heads, n_kv, hd=hd, out=out, k_scale=ks, v_scale=vs)
+        if i8 == "q4":
+            gi_attn.prefill_q4(q, k, v, ks, vs, 0, n_heads, n_kv, out=out)
+        else:
+            gi_attn.prefill(q, k, v, 0, n_heads, n_kv, hd=hd, out=out, k_scale=ks, v_scale=vs)
 
     t = time_steps(step, steps, warmup, torch)
     return {"seconds": t, "flops": prefill_flops(n, 0, n_heads, hd), "step": step, "q": q, "k": k, "v": v}
@@ -435,6 +457,10 @@ DECODE_WORKLOADS = {
                                                       "16q/2kv, the reference's attention_decode_tc256), 1 token, ctx 65536"),
     "verify_h256_i8": (32776, 16, 2, 8, 256, True, "verify with 256-wide heads over the int8 cache, 8 tokens at a "
                                                    "32768-key prefix, 16q/2kv"),
+    "decode64k_h256_q4": (65536, 16, 2, 1, 256, "q4", "decode with 256-wide heads over the 4-bit cache (the "
+                                                      "reference's --kv q4), 1 token, ctx 65536, 16q/2kv"),
+    "verify_h256_q4": (32776, 16, 2, 8, 256, "q4", "verify with 256-wide heads over the 4-bit cache, 8 tokens at a "
+                                                   "32768-key prefix, 16q/2kv"),
 }
 
 
@@ -448,7 +474,7 @@ def run_decode(torch, gi_attn, dev, w, steps, warmup, n_tok_override=None, refer
     r = decode_workload(torch, gi_attn, dev, ctx, n_heads, n_kv, n_tok, steps, warmup, 1234, i8=i8, hd=hd)
     gbs = r["bytes"] / r["seconds"] / 1e9
     chunk, nsplit = gi_attn.decode_plan(ctx, n_tok, n_heads, n_kv, hd)
-    if i8 and hd == HD:  # int8 slices at head size 128 are whole 256-key units (64-key tiles, 4 waves)
+    if i8 is True and hd == HD:  # int8 slices at head size 128 are whole 256-key units (64-key tiles, 4 waves)
         chunk = -(-chunk // 256) * 256
         nsplit = -(-ctx // chunk)
     kt = kernel_times(gi_attn, r["step"], steps, torch, ("decode_partial", "decode_combine"))
@@ -460,7 +486,8 @@ def run_decode(torch, gi_attn, dev, w, steps, warmup, n_tok_override=None, refer
     kern_gbs = part_bytes / (part_ms / 1e3) / 1e9
     line = {
         "value": round(gbs, 1), "unit": "GB/s", "ms_per_step": r["seconds"] * 1e3,
-        "dtype": "int8 K/V + f32 scales, f32 math" if i8 else "f16 K/V, f32 math",
+        "dtype": ("4-bit K/V + f16 scales, f32 math" if i8 == "q4" else "int8 K/V + f32 scales, f32 math" if i8
+                  else "f16 K/V, f32 math"),
         "config": {"workload": cfg, "ctx": ctx, "n_tok": n_tok, "n_heads": n_heads, "n_kv": n_kv, "hd": hd,
                    "kv_bytes_per_step": r["bytes"], "layers_rotated": r["layers"],
                    "slices": nsplit, "keys_per_slice": chunk, "kv_layout": f"head_major [n_kv][ctx][{hd}]"},
@@ -482,22 +509,27 @@ def run_decode(torch, gi_attn, dev, w, steps, warmup, n_tok_override=None, refer
     return line, r
 
 
+PREFILL_WORKLOADS = ("prefill8k", "prefill8k_i8", "prefill8k_h256", "prefill8k_h256_i8", "prefill8k_h256_q4")
+
+
 def run_prefill(torch, gi_attn, dev, w, steps, warmup):
-    i8 = w == "prefill8k_i8"
-    hd = 256 if w.endswith("_h256") else HD
+    i8 = "q4" if w.endswith("_q4") else w.endswith("_i8")
+    hd = 256 if "_h256" in w else HD
     nh, nkv = (16, 2) if hd == 256 else (32, 8)
-    log(f"[bench] causal prefill 8192 tokens, {nh}q/{nkv}kv, hd {hd}{' over the int8 cache' if i8 else ''}")
+    cache = " over the 4-bit cache" if i8 == "q4" else " over the int8 cache" if i8 else ""
+    log(f"[bench] causal prefill 8192 tokens, {nh}q/{nkv}kv, hd {hd}{cache}")
     r = prefill_workload(torch, gi_attn, dev, 8192, nh, nkv, steps, warmup, 99, i8=i8, hd=hd)
     tf = r["flops"] / r["seconds"] / 1e12
+    kernel = ("gi_prefill_fwd_h256r" + ("_q4" if i8 == "q4" else "_i8" if i8 else "") if hd == 256
+              else "gi_prefill_fwd_i8" if i8 else "gi_prefill_fwd")
     line = {
         "value": round(tf, 1), "unit": "TFLOP/s", "ms_per_step": r["seconds"] * 1e3,
-        "dtype": "int8 K/V widened to f16 MFMA, f32 acc" if i8 else "f16 MFMA, f32 acc",
-        "config": {"workload": (f"causal prefill, 8192 tokens, {nh}q/{nkv}kv, hd 256 (Qwen3.5-style heads)"
+        "dtype": ("4-bit K/V widened to f16 MFMA, f32 acc" if i8 == "q4" else
+                  "int8 K/V widened to f16 MFMA, f32 acc" if i8 else "f16 MFMA, f32 acc"),
+        "config": {"workload": (f"causal prefill, 8192 tokens, {nh}q/{nkv}kv, hd 256 (Qwen3.5-style heads){cache}"
                                 if hd == 256 else "config 3: causal prefill, 8192 tokens, 32q/8kv, hd 128" +
                                 (", int8 cache" if i8 else "")), "flops_per_step": r["flops"]},
-        "roofline": prefill_roofline(gi_attn, r, steps, torch, f"pmc_prefill_{w}",
-                                     "gi_prefill_fwd_i8" if i8 else "gi_prefill_fwd_h256r" if hd == 256
-                                     else "gi_prefill_fwd"),
+        "roofline": prefill_roofline(gi_attn, r, steps, torch, f"pmc_prefill_{w}", kernel),
     }
     return line, r
 
@@ -552,8 +584,7 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="decode64k",
-                    choices=[*DECODE_WORKLOADS, "prefill8k", "chunked", "qkrope", "prefill8k_i8", "prefill8k_h256",
-                             "peaks"])
+                    choices=[*DECODE_WORKLOADS, *PREFILL_WORKLOADS, "chunked", "qkrope", "peaks"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--n-tok", type=int, default=None,
@@ -592,7 +623,7 @@ def main():
             cpu = ("decode", w, r)
     elif w == "qkrope":
         result.update(run_qkrope(torch, gi_attn, dev, args.steps, args.warmup))
-    elif w in ("prefill8k", "prefill8k_i8", "prefill8k_h256"):
+    elif w in PREFILL_WORKLOADS:
         line, r = run_prefill(torch, gi_attn, dev, w, args.steps, args.warmup)
         result.update(line)
         if w == "prefill8k":

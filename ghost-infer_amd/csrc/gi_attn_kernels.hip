@@ -1548,11 +1548,15 @@ __device__ __forceinline__ void gi_prefill256r(const GiPrefillArgs& a) {
 #pragma unroll
         for (int i = 0; i < LPW; i++) gi_stage16(src, bytes, (GI_LDS void*)(dst + 1024 * i), soff[i]);
     };
-    // ---- register staging (FMT 1, 2): staging lane lg = 64(wave % SW) + lane takes a quarter of key lg/4's row,
-    // values 64(lg%4) .. +63, i.e. image row key + 64(quarter/2), units 8(quarter%2) .. +7 (swizzled as above).
+    // ---- register staging (FMT 1, 2): staging lane l takes a quarter (l/16) of key 16(wave % SW) + l%16's row,
+    // values 64 quarter .. +63, i.e. image row key + 64(quarter/2), units 8(quarter%2) .. +7 (swizzled as above):
+    // the 16 lanes of a quarter write 16 keys' rows, whose swizzles put their 16-byte units on distinct banks
+    // (one quarter per lane and key instead measured 12% slower). These LDS writes, not the widening, are what
+    // the register path costs against the f16 cache's LDS-DMA staging (widening without the writes: 0.77 ms at
+    // 8192 tokens, 16/2; the writes without the widening: 1.31 ms).
     // int8 rows: 4 16-byte loads and the key's f32 scale (quarter 0's lane); 4-bit rows: 2 16-byte loads and the
     // two f16 scales of its groups. `pend` holds one tile's loads from its issue to its widening.
-    const int lg = 64 * (wave % SW) + lane, skey = lg >> 2, squart = lg & 3;
+    const int skey = 16 * (wave % SW) + (lane & 15), squart = lane >> 4;
     const int srow = skey + BK * (squart >> 1);
     struct Pend { u4 w[FMT == 1 ? 4 : 2]; uint32_t sc; int t; } pend;
     pend.t = -1;
@@ -1578,8 +1582,8 @@ __device__ __forceinline__ void gi_prefill256r(const GiPrefillArgs& a) {
         }
         pend.t = t;
     };
-    // widen the pending tile into its buffer (then this wave's LDS writes are waited for: the barrier that
-    // follows publishes them)
+    // widen the pending tile into its buffer (the next barrier publishes it, after this wave's LDS writes are
+    // waited for)
     auto commit = [&]() {
         if (pend.t < 0) return;
         const int t = pend.t;
@@ -1603,7 +1607,14 @@ __device__ __forceinline__ void gi_prefill256r(const GiPrefillArgs& a) {
         if constexpr (FMT == 1)
             if (squart == 0) (stage_v ? vscl(t) : kscl(t))[skey] = __uint_as_float(pend.sc);
         pend.t = -1;
-        __builtin_amdgcn_s_waitcnt(GI_LGKMCNT0);
+    };
+    // iteration it's staging: the pending tile (K: it + NKBUF into K(it)'s buffer; V: it + NVBUF - 1 into
+    // V(it-1)'s; both free since the barrier of it) is widened, and the loads of the next one are issued, so
+    // each tile's loads have a whole iteration to land and its widening runs among the wave's MFMAs
+    auto restage = [&](int it) {
+        commit();
+        if (!stage_v && it + NKBUF + 1 < ntiles) issue(it + NKBUF + 1);
+        if (stage_v && it + NVBUF < ntiles) issue(it + NVBUF);
     };
 
     // ---- Q as B operands: lane (column c, k-group g), k-step ks: dims 32ks + 8g .. +7, times scale*log2(e)
@@ -1765,6 +1776,11 @@ __device__ __forceinline__ void gi_prefill256r(const GiPrefillArgs& a) {
             stage(t);
         }
     }
+    if constexpr (REG) { // the tile iteration 0 widens
+        if (!stage_v && NKBUF < ntiles) issue(NKBUF);
+        if (stage_v && NVBUF - 1 < ntiles) issue(NVBUF - 1);
+        __builtin_amdgcn_s_waitcnt(GI_LGKMCNT0);
+    }
     if (!stage_v) wait_tiles(last_k0);
     asm volatile("s_barrier" ::: "memory");
     float mx = GI_NEG_INF;
@@ -1773,12 +1789,9 @@ __device__ __forceinline__ void gi_prefill256r(const GiPrefillArgs& a) {
         // V(it + NVBUF - 2)
         if (stage_v) wait_tiles(max(min(it + NVBUF - 2, ntiles - 1) - it, 0));
         else wait_tiles(max(min(it + NKBUF - 1, ntiles - 1) - (it + 1), 0));
-        if constexpr (REG) commit(); // the tile issued last iteration, before the barrier that publishes it
+        if constexpr (REG) __builtin_amdgcn_s_waitcnt(GI_LGKMCNT0); // the widened tile's writes, before they publish
         asm volatile("s_barrier" ::: "memory");
-        if constexpr (REG) {
-            if (!stage_v && it + NKBUF < ntiles) issue(it + NKBUF);
-            if (stage_v && it + NVBUF - 1 < ntiles) issue(it + NVBUF - 1);
-        } else {
+        if constexpr (!REG) {
             if (!stage_v && it + NKBUF < ntiles) stage(it + NKBUF);    // into K(it)'s buffer
             if (stage_v && it + NVBUF - 1 < ntiles) stage(it + NVBUF - 1); // into V(it-1)'s buffer
         }
@@ -1795,6 +1808,7 @@ __device__ __forceinline__ void gi_prefill256r(const GiPrefillArgs& a) {
             }
             step(it, s, sn, mx);
         }
+        if constexpr (REG) restage(it);
     };
     f4 sa[NKB], sb[NKB];
     if (my_tiles > 0) {
