@@ -10,6 +10,8 @@
 //      15 tokens), with every output row checked against it: prompt rows within the path's parity bar
 //      (max-abs 2e-3: the prefill rounds P to f16), decoded rows within 2e-5 (both sides compute in f32
 //      precision).
+// --q4 (head size 256) plays the reference's 4-bit cache: the cache write rotates q, k and v rows, and every
+// attention call is followed by gi_hadamard_rows on its output rows, as the layer does (src/cuda.rs:9765-9768).
 // One JSON line goes to stdout. Exit status 0 when every row agrees, 1 when one does not, 2 on a usage or
 // runtime error. The harness owns all memory (hipMalloc); the library it calls allocates nothing.
 #include <hip/hip_runtime.h>
@@ -28,7 +30,7 @@ namespace {
 
 struct Opts {
     int prompt = 300, steps = 24, heads = 32, kv = 8, hd = 128, seed = 1;
-    bool i8 = false, graph = true;
+    bool i8 = false, q4 = false, graph = true;
     std::string dump; // file for the final qkv rows and the output rows (f32, raw), for checks outside
 };
 
@@ -44,7 +46,7 @@ void gi_ok(int rc, const char* what) {
 }
 
 void usage() {
-    printf("usage: gi_layer_harness [--prompt N] [--steps S] [--heads H] [--kv K] [--hd 128|256] [--int8]\n"
+    printf("usage: gi_layer_harness [--prompt N] [--steps S] [--heads H] [--kv K] [--hd 128|256] [--int8 | --q4]\n"
            "                        [--no-graph] [--seed X] [--dump FILE]\n"
            "Plays one layer's attention through the C ABI (cache write + prefill for the prompt, then one\n"
            "decode step per token, replayed from a HIP graph), checks every output row against the exact\n"
@@ -70,6 +72,7 @@ Opts parse(int argc, char** argv) {
         else if (a == "--hd") num(o.hd);
         else if (a == "--seed") num(o.seed);
         else if (a == "--int8") o.i8 = true;
+        else if (a == "--q4") o.q4 = true;
         else if (a == "--no-graph") o.graph = false;
         else if (a == "--dump") {
             if (i + 1 >= argc) die("missing value after --dump");
@@ -78,8 +81,8 @@ Opts parse(int argc, char** argv) {
         else die("unknown argument " + a);
     }
     if (o.prompt < 1 || o.steps < 0 || o.heads < 1 || o.kv < 1 || o.heads % o.kv || (o.hd != 128 && o.hd != 256) ||
-        (o.i8 && o.hd != 128))
-        die("bad shape (heads a multiple of kv; hd 128, or 256 with the f16 cache)");
+        (o.q4 && (o.hd != 256 || o.i8)))
+        die("bad shape (heads a multiple of kv; hd 128 or 256; --q4 takes hd 256 and not --int8)");
     return o;
 }
 
@@ -114,12 +117,15 @@ int main(int argc, char** argv) {
     float* out = dev_alloc<float>((size_t)total * orow);
     float* ref = dev_alloc<float>((size_t)total * orow);
     hip_ok(hipMemcpy(qkv, qkv_h.data(), qkv_h.size() * sizeof(float), hipMemcpyHostToDevice), "hipMemcpy qkv");
-    const size_t cache_elems = (size_t)K * cap * hd;
-    void* kc = o.i8 ? (void*)dev_alloc<int8_t>(cache_elems) : (void*)dev_alloc<uint16_t>(cache_elems);
-    void* vc = o.i8 ? (void*)dev_alloc<int8_t>(cache_elems) : (void*)dev_alloc<uint16_t>(cache_elems);
-    float* ks = o.i8 ? dev_alloc<float>((size_t)K * cap) : nullptr;
-    float* vs = o.i8 ? dev_alloc<float>((size_t)K * cap) : nullptr;
-    const long long kv_stride = hd, kv_head_stride = (long long)cap * hd, sc_stride = 1, sc_head_stride = cap;
+    // head-major caches; the 4-bit one: rows of hd/2 bytes, hd/32 f16 scales a row
+    const size_t cache_bytes = (size_t)K * cap * (o.q4 ? hd / 2 : o.i8 ? hd : 2 * hd);
+    void* kc = dev_alloc<char>(cache_bytes);
+    void* vc = dev_alloc<char>(cache_bytes);
+    const size_t sc_bytes = (size_t)K * cap * (o.q4 ? hd / 16 : 4);
+    float* ks = o.i8 || o.q4 ? (float*)dev_alloc<char>(sc_bytes) : nullptr;
+    float* vs = o.i8 || o.q4 ? (float*)dev_alloc<char>(sc_bytes) : nullptr;
+    const long long kv_stride = o.q4 ? hd / 2 : hd, kv_head_stride = (long long)cap * kv_stride;
+    const long long sc_stride = o.q4 ? hd / 32 : 1, sc_head_stride = (long long)cap * sc_stride;
     const size_t ws_bytes = gi_attn_decode_workspace_bytes(cap, 15, H, K, hd);
     if (ws_bytes == 0) die("gi_attn_decode_workspace_bytes rejected the shape");
     void* ws = dev_alloc<char>(ws_bytes);
@@ -131,6 +137,10 @@ int main(int argc, char** argv) {
     hip_ok(hipHostMalloc((void**)&pos_host, sizeof(int), hipHostMallocDefault), "hipHostMalloc");
 
     auto write_cache = [&](float* rows, int pos0, const int* pp, int n) {
+        if (o.q4)
+            return gi_qk_norm_rope_q4(st, rows, nullptr, nullptr, (uint8_t*)kc, (uint8_t*)vc, (uint16_t*)ks,
+                                      (uint16_t*)vs, kv_stride, kv_head_stride, sc_stride, sc_head_stride, pos0, pp,
+                                      cap, n, H, K, rope_dim, rope_base, nullptr, 1, eps);
         if (o.i8)
             return gi_qk_norm_rope_i8(st, rows, nullptr, nullptr, (int8_t*)kc, (int8_t*)vc, ks, vs, kv_stride,
                                       kv_head_stride, sc_stride, sc_head_stride, pos0, pp, cap, n, H, K, hd, rope_dim,
@@ -140,9 +150,13 @@ int main(int argc, char** argv) {
     };
     // gi_attention takes the reference's [position][n_kv][hd] cache; the head-major session cache goes
     // through the decode / prefill entry points with its strides, as the operator would dispatch them
-    auto attention = [&](const float* rows, float* o_rows, int pos0, const int* pp, int n, int exact) {
+    auto attention_rotated = [&](const float* rows, float* o_rows, int pos0, const int* pp, int n, int exact) {
         const float scale = 1.f / sqrtf((float)hd);
         if (n >= 16 && !exact) {
+            if (o.q4)
+                return gi_attn_prefill_q4(st, rows, GI_F32, row, (const uint8_t*)kc, (const uint8_t*)vc,
+                                          (const uint16_t*)ks, (const uint16_t*)vs, kv_stride, kv_head_stride,
+                                          sc_stride, sc_head_stride, o_rows, GI_F32, orow, pos0, n, H, K, scale);
             if (o.i8)
                 return gi_attn_prefill_i8(st, rows, GI_F32, row, (const int8_t*)kc, (const int8_t*)vc, ks, vs,
                                           kv_stride, kv_head_stride, sc_stride, sc_head_stride, o_rows, GI_F32, orow,
@@ -152,7 +166,11 @@ int main(int argc, char** argv) {
         }
         for (int b0 = 0; b0 < n; b0 += 15) { // SPLIT_MAX_BATCH (src/cuda.rs:119)
             const int m = n - b0 < 15 ? n - b0 : 15;
-            int rc = o.i8 ? gi_attn_decode_i8(st, rows + b0 * row, row, (const int8_t*)kc, (const int8_t*)vc, ks, vs,
+            int rc = o.q4 ? gi_attn_decode_q4(st, rows + b0 * row, row, (const uint8_t*)kc, (const uint8_t*)vc,
+                                              (const uint16_t*)ks, (const uint16_t*)vs, kv_stride, kv_head_stride,
+                                              sc_stride, sc_head_stride, o_rows + b0 * orow, orow, ws, ws_bytes,
+                                              pos0 + b0, pp, pp ? cap : 0, m, H, K, scale)
+                   : o.i8 ? gi_attn_decode_i8(st, rows + b0 * row, row, (const int8_t*)kc, (const int8_t*)vc, ks, vs,
                                               kv_stride, kv_head_stride, sc_stride, sc_head_stride, o_rows + b0 * orow,
                                               orow, ws, ws_bytes, pos0 + b0, pp, pp ? cap : 0, m, H, K, hd, scale)
                           : gi_attn_decode(st, rows + b0 * row, row, (const uint16_t*)kc, (const uint16_t*)vc,
@@ -161,6 +179,12 @@ int main(int argc, char** argv) {
             if (rc) return rc;
         }
         return 0;
+    };
+    // the layer's attention step: a 4-bit cache's output rows are rotated back
+    auto attention = [&](const float* rows, float* o_rows, int pos0, const int* pp, int n, int exact) {
+        int rc = attention_rotated(rows, o_rows, pos0, pp, n, exact);
+        if (!rc && o.q4) rc = gi_hadamard_rows(st, o_rows, orow, n, (int)orow);
+        return rc;
     };
 
     hipEvent_t e0, e1;
@@ -241,7 +265,7 @@ int main(int argc, char** argv) {
     printf("{\"prompt\": %d, \"steps\": %d, \"heads\": %d, \"kv\": %d, \"hd\": %d, \"cache\": \"%s\", \"graph\": %s, "
            "\"prompt_ms\": %.4f, \"decode_step_us\": %.2f, \"max_abs_prompt\": %.3g, \"max_abs_decode\": %.3g, "
            "\"tol_prompt\": %g, \"tol_decode\": %g, \"ok\": %s}\n",
-           o.prompt, o.steps, H, K, hd, o.i8 ? "int8" : "f16", exec ? "true" : "false", prompt_ms,
+           o.prompt, o.steps, H, K, hd, o.q4 ? "q4" : o.i8 ? "int8" : "f16", exec ? "true" : "false", prompt_ms,
            o.steps ? 1e3 * step_ms / o.steps : 0.0, err_prompt, err_decode, tol_prompt, tol_decode,
            ok ? "true" : "false");
     if (exec) (void)hipGraphExecDestroy(exec);

@@ -3,9 +3,10 @@
     python tests/golden/make_golden.py
 
 The expected outputs come from the textbook causal softmax attention in float64
-(tests/attn_common.reference_f64, over the dequantised cache for int8), not from the oracle under test.
-Inputs follow the configs' recipe (Q N(0,1), K/V N(0,1) rounded to f16, scale 1/sqrt(head size)) at sizes
-small enough to commit; the int8 cases hold int8 rows and their f32 scales (keys ks, vs).
+(tests/attn_common.reference_f64, over the dequantised cache for int8 and the 4-bit cache), not from the oracle
+under test. Inputs follow the configs' recipe (Q N(0,1), K/V N(0,1) rounded to f16, scale 1/sqrt(head size)) at
+sizes small enough to commit; the int8 cases hold int8 rows and their f32 scales (keys ks, vs); the 4-bit cases
+(key q4 = 1) hold rows of 128 nibble-pair bytes and their f16 scale bits, 8 a row (ks, vs as uint16).
 """
 import os
 import sys
@@ -14,10 +15,11 @@ import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.dirname(HERE))
-from attn_common import make_inputs, make_inputs_i8, reference_f64, reference_f64_i8  # noqa: E402
+from attn_common import (make_inputs, make_inputs_i8, make_inputs_q4, reference_f64, reference_f64_i8,  # noqa: E402
+                         reference_f64_q4)
 
 CASES = {
-    # name: (seed, n_tok, pos0, n_heads, n_kv, q dtype, head size, int8 cache)
+    # name: (seed, n_tok, pos0, n_heads, n_kv, q dtype, head size, cache: False f16, True int8, "q4" 4-bit)
     "decode_g4_ctx64": (101, 1, 63, 32, 8, np.float32, 128, False),
     "decode_g8_ctx300": (102, 1, 299, 32, 4, np.float32, 128, False),
     "verify_8tok_ctx136": (103, 8, 128, 32, 4, np.float32, 128, False),
@@ -29,13 +31,21 @@ CASES = {
     "verify_i8_4tok_ctx100": (109, 4, 96, 16, 2, np.float32, 128, True),
     "decode_h256_i8_ctx200": (110, 1, 199, 16, 2, np.float32, 256, True),
     "verify_h256_i8_3tok_ctx90": (111, 3, 87, 16, 2, np.float32, 256, True),
+    "prefill_h256_i8_40tok": (112, 40, 0, 4, 1, np.float32, 256, True),
+    "decode_h256_q4_ctx200": (113, 1, 199, 16, 2, np.float32, 256, "q4"),
+    "verify_h256_q4_3tok_ctx90": (114, 3, 87, 16, 2, np.float32, 256, "q4"),
+    "prefill_h256_q4_40tok": (115, 40, 0, 4, 1, np.float32, 256, "q4"),
 }
 
 
 def main():
     for name, (seed, n_tok, pos0, n_heads, n_kv, qd, hd, i8) in CASES.items():
         extra = {}
-        if i8:  # int8 rows round(40 N(0,1)) with f32 scales near 1/40, as quantised N(0,1) rows
+        if i8 == "q4":  # random nibbles with f16 scales near 1/4, dequantised values of standard deviation ~1
+            q, k, v, ks, vs = make_inputs_q4(seed, n_tok, pos0 + n_tok, n_heads, n_kv)
+            out = reference_f64_q4(q, k, v, ks, vs, pos0, n_heads, n_kv).astype(np.float32)
+            extra = {"ks": ks, "vs": vs, "q4": 1}
+        elif i8:  # int8 rows round(40 N(0,1)) with f32 scales near 1/40, as quantised N(0,1) rows
             q, k, v, ks, vs = make_inputs_i8(seed, n_tok, pos0 + n_tok, n_heads, n_kv, hd=hd)
             out = reference_f64_i8(q, k, v, ks, vs, pos0, n_heads, n_kv, hd=hd).astype(np.float32)
             extra = {"ks": ks, "vs": vs}

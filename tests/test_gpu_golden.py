@@ -1,7 +1,7 @@
 """The committed golden fixtures (tests/golden/*.npz: seeded inputs and float64 expected outputs, written by
-tests/golden/make_golden.py) through the HIP path: the decode / verify cases through gi_attn_decode(_i8) and,
-packed as the reference's qkv rows, through the operator gi_attention(_i8) (src/cuda.rs:8448-8541); the
-prefill cases through gi_attn_prefill.
+tests/golden/make_golden.py) through the HIP path: the decode / verify cases through gi_attn_decode(_i8, _q4)
+and, packed as the reference's qkv rows, through the operator gi_attention(_i8, _q4) (src/cuda.rs:8448-8541);
+the prefill cases through gi_attn_prefill(_i8, _q4).
 
 Bar: decode and verify within 2e-5 of float64 (the split path keeps f32 precision), prefill within the
 north star's 2e-3 / 1e-3 (it rounds P to f16 as the reference does)."""
@@ -31,7 +31,13 @@ def load(name, dev):
     meta["hd"] = int(z["hd"]) if "hd" in z.files else 128
     i8 = "ks" in z.files
     q = torch.from_numpy(z["q"]).to(dev)
-    if i8:
+    if "q4" in z.files:
+        nkv = meta["n_kv"]
+        k = torch.from_numpy(z["k"]).to(dev).view(-1, nkv, 128)
+        v = torch.from_numpy(z["v"]).to(dev).view(-1, nkv, 128)
+        sc = dict(k_scale=torch.from_numpy(z["ks"].view(np.float16)).to(dev).view(-1, nkv, 8),
+                  v_scale=torch.from_numpy(z["vs"].view(np.float16)).to(dev).view(-1, nkv, 8), q4=True)
+    elif i8:
         k, v = torch.from_numpy(z["k"]).to(dev), torch.from_numpy(z["v"]).to(dev)
         sc = dict(k_scale=torch.from_numpy(z["ks"]).to(dev), v_scale=torch.from_numpy(z["vs"]).to(dev))
     else:
@@ -47,6 +53,22 @@ def test_golden_through_the_hip_path(gpu, name):
     z, m, q, k, v, sc = load(name, gpu)
     n = q.shape[0]
     want = z["out"]
+    if sc.pop("q4", False):
+        ks, vs = sc["k_scale"], sc["v_scale"]
+        if name.startswith("prefill"):
+            out = gi_attn.prefill_q4(q, k, v, ks, vs, m["pos0"], m["n_heads"], m["n_kv"], out_dtype=torch.float32)
+            torch.cuda.synchronize()
+            assert_close(out.cpu().numpy(), want, what=f"{name} prefill")
+            return
+        out = gi_attn.decode_q4(q, k, v, ks, vs, m["pos0"], m["n_heads"], m["n_kv"])
+        torch.cuda.synchronize()
+        assert_close(out.cpu().numpy(), want, max_abs=2e-5, rel_l2=2e-5, what=f"{name} decode")
+        qkv = torch.zeros((n, (m["n_heads"] + 2 * m["n_kv"]) * 256), dtype=torch.float32, device=gpu)
+        qkv[:, :m["n_heads"] * 256] = q
+        out2 = gi_attn.attention_q4(qkv, k, v, ks, vs, m["pos0"], m["n_heads"], m["n_kv"], exact=True)
+        torch.cuda.synchronize()
+        assert_close(out2.cpu().numpy(), want, max_abs=2e-5, rel_l2=2e-5, what=f"{name} operator")
+        return
     if name.startswith("prefill"):
         out = gi_attn.prefill(q, k, v, m["pos0"], m["n_heads"], m["n_kv"], hd=m["hd"], out_dtype=torch.float32, **sc)
         torch.cuda.synchronize()

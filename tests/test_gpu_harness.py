@@ -4,7 +4,8 @@ src/cuda.rs:8448-8541): a prompt through the cache write and the prefill path, t
 from one captured HIP graph with a device-side position. The harness checks every output row against the
 exact split path over the whole sequence itself; this test also checks the rows it dumps against the CPU
 oracle and the float64 reference, over the cache the harness's rotated k / v rows imply (f16: rounded to
-nearest even; int8: the oracle's restatement of kv_store's quantiser)."""
+nearest even; int8: the oracle's restatement of kv_store's quantiser; the 4-bit cache: its KV4 quantiser of the
+rotated rows, the outputs rotated back as the layer does)."""
 import json
 import os
 import subprocess
@@ -14,14 +15,18 @@ import numpy as np
 import pytest
 
 import gi_oracle as O
-from attn_common import assert_close, reference_f64, reference_f64_i8
+from attn_common import assert_close, reference_f64, reference_f64_i8, reference_f64_q4
 
 HARNESS = os.path.join(os.path.dirname(os.path.abspath(__file__)), "..", "ghost-infer_amd", "gi_layer_harness")
 
 CASES = [
-    # (args, prompt, steps, heads, kv, hd, int8)
+    # (args, prompt, steps, heads, kv, hd, cache: False f16, True int8, "q4" 4-bit)
     ([], 300, 24, 32, 8, 128, False),
     (["--int8"], 300, 24, 32, 8, 128, True),
+    (["--int8", "--heads", "16", "--kv", "2", "--hd", "256", "--prompt", "100", "--steps", "10"], 100, 10, 16, 2, 256,
+     True),
+    (["--q4", "--heads", "16", "--kv", "2", "--hd", "256", "--prompt", "150", "--steps", "12"], 150, 12, 16, 2, 256,
+     "q4"),
     (["--heads", "16", "--kv", "2", "--hd", "256", "--prompt", "100", "--steps", "10"], 100, 10, 16, 2, 256, False),
     (["--no-graph", "--prompt", "40", "--steps", "6", "--heads", "32", "--kv", "4"], 40, 6, 32, 4, 128, False),
 ]
@@ -50,13 +55,29 @@ def test_layer_harness(case, tmp_path):
     kr = qkv[:, orow:orow + K * hd]
     vr = qkv[:, orow + K * hd:]
     pre, dec = slice(0, prompt), slice(prompt, total)
-    if i8:
+    if i8 == "q4":
+        # the cache the kernels hold: the rotated k rows and the v rows rotated here, each quantised by kv_store's
+        # KV4; the oracle attends with the rotated queries and its output is rotated back
+        kc, ks = O.kv4_quant(kr.reshape(total * K, 256))
+        vc, vs = O.kv4_quant(O.kv4_fwht(vr.reshape(total * K, 256)))
+        kc, vc = kc.reshape(total, -1), vc.reshape(total, -1)
+        ks, vs = ks.reshape(total, -1), vs.reshape(total, -1)
+
+        def back(x):
+            return O.kv4_fwht(np.ascontiguousarray(x, dtype=np.float32).reshape(-1, 256)).reshape(x.shape)
+
+        want_pre = back(O.prefill_tc256_q4(q[pre], kc, vc, ks, vs, 0, H, K))
+        want_dec = back(O.decode_tc256_q4(q[dec], kc, vc, ks, vs, prompt, H, K))
+        h = _h256()
+        f64 = (reference_f64_q4(q, kc, vc, ks, vs, 0, H, K).reshape(-1, 256) @ h).reshape(total, -1)
+    elif i8:
         kc, ks = O.kv_quant_i8(kr.reshape(total, K, hd))
         vc, vs = O.kv_quant_i8(vr.reshape(total, K, hd))
         kc, vc = kc.reshape(total, K * hd), vc.reshape(total, K * hd)
-        want_pre = O.prefill_tc_semantics_i8(q[pre], kc, vc, ks, vs, 0, H, K)
-        want_dec = O.decode_gpu_semantics_i8(q[dec], kc, vc, ks, vs, prompt, H, K)
-        f64 = reference_f64_i8(q, kc, vc, ks, vs, 0, H, K)
+        want_pre = O.prefill_tc_semantics_i8(q[pre], kc, vc, ks, vs, 0, H, K, hd=hd)
+        want_dec = (O.decode_tc256_i8(q[dec], kc, vc, ks, vs, prompt, H, K) if hd == 256
+                    else O.decode_gpu_semantics_i8(q[dec], kc, vc, ks, vs, prompt, H, K))
+        f64 = reference_f64_i8(q, kc, vc, ks, vs, 0, H, K, hd=hd)
     else:
         kc = kr.astype(np.float16).view(np.uint16)
         vc = vr.astype(np.float16).view(np.uint16)
@@ -70,3 +91,9 @@ def test_layer_harness(case, tmp_path):
     # decoded rows: the split path in f32 precision, against the oracle at the bar and float64 at 2e-5
     assert_close(got[dec], want_dec, what="harness decode rows vs oracle")
     assert_close(got[dec], f64[dec], max_abs=2e-5, rel_l2=2e-5, what="harness decode rows vs f64")
+
+
+def _h256():
+    i = np.arange(256)
+    bits = np.vectorize(lambda x: bin(x).count("1"))(i[:, None] & i[None, :])
+    return np.where(bits % 2 == 0, 1.0, -1.0) / 16.0

@@ -349,7 +349,13 @@ def test_oracle_against_golden(name):
     n_heads, n_kv, pos0 = int(z["n_heads"]), int(z["n_kv"]), int(z["pos0"])
     hd = int(z["hd"]) if "hd" in z.files else 128
     q = z["q"].astype(np.float32)
-    if "ks" in z.files and hd == 256:  # attention_decode_tc256 rounds Q and P*vscale to f16: the parity bar
+    if "q4" in z.files:  # the 4-bit cache's tensor-core kernels round Q and P to f16: the parity bar
+        fn = O.prefill_tc256_q4 if name.startswith("prefill") else O.decode_tc256_q4
+        assert_close(fn(q, z["k"], z["v"], z["ks"], z["vs"], pos0, n_heads, n_kv), z["out"], what=name)
+    elif "ks" in z.files and name.startswith("prefill"):  # f16 P * vscale * 2^10: the parity bar
+        got = O.prefill_tc_semantics_i8(q, z["k"], z["v"], z["ks"], z["vs"], pos0, n_heads, n_kv, hd=hd)
+        assert_close(got, z["out"], what=name)
+    elif "ks" in z.files and hd == 256:  # attention_decode_tc256 rounds Q and P*vscale to f16: the parity bar
         got = O.decode_tc256_i8(q, z["k"], z["v"], z["ks"], z["vs"], pos0, n_heads, n_kv)
         assert_close(got, z["out"], what=name)
     elif "ks" in z.files:  # the int8 split path keeps f32 precision
