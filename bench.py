@@ -112,14 +112,15 @@ def decode_kernel_name(n_tok, n_heads, n_kv, hd, i8):
     """Name of the split-K kernel a decode call of this shape launches: the host library's variant rule
     (up to 8 (token, head) pairs per kv head: one column block with two columns per pair; above, one pair
     per MFMA column, with two column blocks per wave above 16 pairs at head size 128 (f16 above 32 pairs:
-    two pair sets per workgroup, each over two waves), and 4 waves sharing each tile at head size 256)."""
+    two pair sets per workgroup, each over two waves), and two pair sets of one column block at head size
+    256)."""
     pairs, p = n_tok * (n_heads // n_kv), 8
     if i8 == "q4":
-        return "gi_decode_pm_shared_1_q4" if pairs > p else "gi_decode_partial_1_q4"
+        return "gi_decode_pm_ws2_1_q4" if pairs > p else "gi_decode_partial_1_q4"
     if pairs <= p:
         name = "gi_decode_partial_1"
     elif hd == 256:
-        name = "gi_decode_pm_shared_1"
+        name = "gi_decode_pm_ws2_1"
     else:
         name = ("gi_decode_pm_ws2_2" if pairs > 4 * p and not i8 else
                 "gi_decode_pm_2" if pairs > 2 * p else "gi_decode_pm_1")

@@ -165,8 +165,8 @@ struct Module {
     hipFunction_t dec256[2] = {};     // up to 8 pairs, head size 256: [int8 cache]
     hipFunction_t dec_pm[2][2] = {};  // [int8 cache][column blocks - 1]: one pair per column
     hipFunction_t dec_ws2[2] = {};    // head size 128, two column blocks, two pair sets of two waves: [int8 cache]
-    hipFunction_t dec_pm256[2] = {};
-    hipFunction_t dec_q4[2] = {};     // head size 256 over the 4-bit cache: [one pair per column]  // head size 256, one pair per column, 4 waves sharing each tile: [int8 cache]
+    hipFunction_t dec_q4 = nullptr;   // up to 8 pairs, head size 256, the 4-bit cache
+    hipFunction_t dec_pm256[3] = {};  // head size 256, one pair per column, two pair sets of two waves: [f16, int8, 4-bit]
     hipFunction_t prefill[2] = {};   // [int8 cache], head size 128
     hipFunction_t prefill256r = nullptr; // head size 256 (f16 cache), 16 rows per wave: one workgroup per query tile
     hipFunction_t prefill256r_fmt[2] = {}; // the same over the int8 and the 4-bit cache
@@ -214,10 +214,10 @@ int load_module(const char* path, Module** out) {
             {&m.dec_pm[1][1], "gi_decode_pm_2_i8"},
             {&m.dec_ws2[0], "gi_decode_pm_ws2_2"},
             {&m.dec_ws2[1], "gi_decode_pm_ws2_2_i8"},
-            {&m.dec_pm256[0], "gi_decode_pm_shared_1_h256"},
-            {&m.dec_pm256[1], "gi_decode_pm_shared_1_i8_h256"},
-            {&m.dec_q4[0], "gi_decode_partial_1_q4"},
-            {&m.dec_q4[1], "gi_decode_pm_shared_1_q4"},
+            {&m.dec_q4, "gi_decode_partial_1_q4"},
+            {&m.dec_pm256[0], "gi_decode_pm_ws2_1_h256"},
+            {&m.dec_pm256[1], "gi_decode_pm_ws2_1_i8_h256"},
+            {&m.dec_pm256[2], "gi_decode_pm_ws2_1_q4"},
             {&m.combine, "gi_decode_combine"},
             {&m.relayout, "gi_kv_relayout"},
             {&m.hadamard, "gi_hadamard_rows"},
@@ -313,21 +313,23 @@ int decode_target_wgs() {
 // one accumulator, so no lane repeats its neighbour's softmax.
 struct DecVariant {
     int ncb;     // column blocks per wave
-    bool shared; // the 4 waves share every tile of the slice (else each wave takes tiles of its own)
-    bool ws2;    // two pair sets per workgroup, each split over two waves
+    bool ws2;    // two pair sets per workgroup, each split over two waves (else the 4 waves serve one set)
     bool pm;     // one pair per column
     int groups;  // workgroups per (slice, kv head)
 };
 DecVariant dec_variant(int n_tok, int G, int hd = 128, bool i8 = false) {
     const int pairs = n_tok * G;
-    DecVariant v{1, false, false, pairs > kDecPairs, 1};
+    DecVariant v{1, false, pairs > kDecPairs, 1};
     if (!v.pm) return v;
     if (hd == 256) {
-        // 4 waves of 16 pairs sharing every tile of the slice (two column blocks per wave exceed the register
-        // file at this head size). Against the two-column layout: 16 pairs 23.2 -> 20.0 us, 24 pairs 26.6 ->
-        // 23.3, 64 pairs 42.1 -> 38.2, 128 pairs 61.7 -> 57.7 (32768 keys, 16/2).
-        v.shared = true;
-        v.groups = (pairs + 4 * 2 * kDecPairs - 1) / (4 * 2 * kDecPairs);
+        // two pair sets of 16 per workgroup, each over two waves that split the slice's tiles (two column
+        // blocks per wave exceed the register file at this head size). Split kernel at 32768 keys, 16/2, against
+        // 4 waves of 16 pairs each walking every tile (which beat the hi/lo column layout at 16-128 pairs):
+        // f16 16 pairs 20.2 -> 17.1 us, 24 pairs 22.7 -> 23.4, 64 pairs 37.9 -> 34.6, 128 pairs 58.4 -> 55.5;
+        // int8 26.0 -> 18.3, 28.1 -> 20.9, 34.4 -> 30.4, 51.9 -> 47.7; 4-bit 30.9 -> 20.2, 32.9 -> 23.2,
+        // 40.3 -> 35.0, 60.2 -> 53.9.
+        v.ws2 = true;
+        v.groups = (pairs + 4 * kDecPairs - 1) / (4 * kDecPairs);
         return v;
     }
     // head size 128, above 16 pairs: two column blocks per wave, each wave on slice tiles of its own, and as
@@ -459,8 +461,7 @@ int decode_impl(void* stream, const float* q, long long q_stride, const void* kc
         a.sc_head_stride = sc_head_stride;
     }
     hipStream_t st = (hipStream_t)stream;
-    hipFunction_t f = fmt == 2    ? m->dec_q4[var.pm]
-                      : hd == 256 ? (var.pm ? m->dec_pm256[i8] : m->dec256[i8])
+    hipFunction_t f = hd == 256 ? (var.pm ? m->dec_pm256[fmt] : fmt == 2 ? m->dec_q4 : m->dec256[i8])
                       : var.ws2   ? m->dec_ws2[i8]
                       : var.pm    ? m->dec_pm[i8][var.ncb - 1]
                                   : m->dec[i8];

@@ -217,12 +217,9 @@ __device__ __forceinline__ uint32_t q4_f16x2(uint32_t hi, uint32_t lo, int j, h2
 // of neighbouring columns, so a lane's softmax serves one pair and no lane repeats its neighbour's (half the
 // VALU per pair; twice the MFMAs per column, so blocks of at most 8 pairs keep PM = false).
 // WS (waves per pair set) = 4: the 4 waves split the slice's tiles and serve the same DEC_PAIRS*NCB (token, head)
-// pairs, merging through LDS at the end. WS = 2: waves 2p and 2p + 1 split the tiles for pair set p, so one
-// workgroup serves two sets and each tile is read by two waves of one CU. WS = 1 (many pairs per kv head, as in
-// a verify block):
-// every wave walks the whole slice for its own DEC_PAIRS*NCB pairs, so one workgroup serves 4 times as
-// many pairs and the slice's K/V comes from HBM once (the waves' repeated loads of the same lines are
-// served by the caches).
+// pairs, merging through LDS at the end. WS = 2 (many pairs per kv head, as in a verify block): waves 2p and
+// 2p + 1 split the tiles for pair set p, so one workgroup serves two sets and each tile's second read comes
+// from the caches of the same CU.
 // Q4 = true (head size 256, the 4-bit cache, kv_store's KV4 format, src/cuda.rs:340-357): K and V values are
 // widened to the f16 values f16((n - 8) * scale) that attention_decode_tc256 (src/cuda.rs:2681-2760) feeds its
 // tensor cores, and the rest is the f16 cache's path (unit key and value scales). Lane (c, grp) takes values
@@ -266,8 +263,7 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
     const int pos0 = a.posp ? min(max(*a.posp, 0), a.kv_cap - a.n_tok) : a.pos0;
     const int G = a.n_heads / a.n_kv;
     const int npairs = a.n_tok * G;
-    static_assert(WS == 1 || WS == 2 || WS == DEC_WAVES, "waves per pair set: 1, 2 or all");
-    constexpr bool SHARE = WS == 1;                  // every wave walks every tile of the slice
+    static_assert(WS == 2 || WS == DEC_WAVES, "waves per pair set: 2 or all");
     constexpr int WG_PAIRS = (DEC_WAVES / WS) * CPAIRS * NCB; // pairs per workgroup
     const int pair0 = gz * WG_PAIRS + (wave / WS) * CPAIRS * NCB; // this wave's first pair
     const int kv_len = pos0 + a.n_tok; // keys any token of the launch may see
@@ -363,9 +359,9 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
     const int vscoff4 = (4 * grp * (int)scs + (c >> 1)) * 2;
 
     using Buf = typename gi_pick<Q4, DecBufQ4, DecBuf<I8, HD>>::type;
-    // K/V stream loads: each tile is read by one wave only, unless SHARE (every wave of the workgroup reads
-    // every tile of the slice, from L2 after the first): streaming policy only for the former. At config 2
-    // it takes the split kernel from 25.5 to 22.7 us; with SHARE it costs 30%.
+    // K/V stream loads: with WS = 4 each tile is read by one wave only, and the loads take the streaming
+    // policy (at config 2 the split kernel went from 25.5 to 22.7 us with it); with WS = 2 a second wave of the
+    // workgroup reads each tile again, from the caches, so the lines stay.
     constexpr int CPOL = WS == DEC_WAVES ? DEC_CPOL : 0;
     auto load_k = [&](Buf& B, int t) {
         if constexpr (Q4) {
@@ -779,7 +775,7 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
 
     // (the first loads are issued unconditionally, before the loop, so every iteration starts with the same
     // loads outstanding and the compiler's load counters wait for exactly the buffer in use)
-    // a SHARE wave whose pairs all lie past the last one has nothing to compute (it still joins the merge)
+    // a pair set whose pairs all lie past the last one has nothing to compute (its waves still join the merge)
     if (pair0 < npairs) {
     Buf B[NB];
     const int t_first = (wave % WS) * TILE;
@@ -843,7 +839,7 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
         }
     }
     __syncthreads();
-    // ---- merge the waves (SHARE: each pair has one wave) and the hi/lo columns: thread -> (pair, 4 dims)
+    // ---- merge each pair set's waves and the hi/lo columns: thread -> (pair, 4 dims)
     constexpr float LO = I8 ? 1.f / DEC_I8_LO : 1.f;      // the remainder column's scale (PM: no column)
     constexpr float OSC = I8 && PM ? 1.f / DEC_I8_VB : 1.f; // PM int8: the bias on P
 #pragma unroll
@@ -912,10 +908,10 @@ GI_DEC_KERNEL(gi_decode_partial_1_i8_h256, 1, DEC_WAVES, true, 256)
     extern "C" __global__ void __launch_bounds__(256, DEC_MINWG) name(GiDecodeArgs a) { gi_decode_partial_t<NCB, WS, I8, 256, true>(a); }
 #define GI_DEC_Q4_KERNEL(name, WS, PM) \
     extern "C" __global__ void __launch_bounds__(256, DEC_MINWG) name(GiDecodeArgs a) { gi_decode_partial_t<1, WS, false, 256, PM, true>(a); }
-GI_DEC_PM256_KERNEL(gi_decode_pm_shared_1_h256, 1, 1, false)
-GI_DEC_PM256_KERNEL(gi_decode_pm_shared_1_i8_h256, 1, 1, true)
+GI_DEC_PM256_KERNEL(gi_decode_pm_ws2_1_h256, 1, 2, false)
+GI_DEC_PM256_KERNEL(gi_decode_pm_ws2_1_i8_h256, 1, 2, true)
 GI_DEC_Q4_KERNEL(gi_decode_partial_1_q4, DEC_WAVES, false)
-GI_DEC_Q4_KERNEL(gi_decode_pm_shared_1_q4, 1, true)
+GI_DEC_Q4_KERNEL(gi_decode_pm_ws2_1_q4, 2, true)
 
 // Merge the slices of each (token, head): M = max m_s, w_s = 2^(m_s - M), out = sum w_s O_s / sum w_s l_s
 // (attention_combine's maths in base 2; empty slices carry m = -inf and weigh nothing). One wave per

@@ -36,7 +36,7 @@ def to_dev(q, k, v, dev, n_kv, layout="reference"):
 
 DECODE_SHAPES_256 = [
     # (n_tok, pos0, n_heads, n_kv): spans inside one 16-key tile, at tile and slice edges, every kernel
-    # variant (up to 8 pairs: 1 and 2 column blocks; above: one pair per column, shared slice), G = 3
+    # variant (up to 8 pairs: 1 and 2 column blocks; above: one pair per column, two pair sets per workgroup), G = 3
     (1, 0, 16, 2),
     (1, 15, 16, 2),
     (1, 16, 32, 4),
@@ -135,7 +135,7 @@ def test_decode_hd256_i8_long_context(gpu, n_tok, layout):
 
 
 def test_decode_hd256_i8_graph_replay(gpu):
-    # an 8-token verify block (one pair per column, shared slices) with a device position, captured once and
+    # an 8-token verify block (one pair per column, two pair sets per workgroup) with a device position, captured once and
     # replayed at several positions with eager work between the replays
     n_tok, n_heads, n_kv, cap = 8, 16, 2, 2500
     q, k, v, ks, vs = make_inputs_i8(95, n_tok, cap, n_heads, n_kv, hd=HD)

@@ -37,7 +37,7 @@ def q4_dev(q, kc, vc, ks, vs, dev, n_kv, layout="reference"):
 
 DECODE_SHAPES_Q4 = [
     # (n_tok, pos0, n_heads, n_kv): spans inside one 16-key tile and at tile / slice edges, both kernel variants
-    # (up to 8 pairs per kv head: hi/lo columns; above: one pair per column, waves sharing the slice), G = 3
+    # (up to 8 pairs per kv head: hi/lo columns; above: one pair per column, two pair sets per workgroup), G = 3
     (1, 0, 16, 2),
     (1, 15, 16, 2),
     (1, 64, 16, 2),

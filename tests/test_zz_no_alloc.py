@@ -60,8 +60,20 @@ def test_noalloc_decode_matches_the_workspace_entry_point(gpu):
 
 
 def test_noalloc_rejects_partials_beyond_the_scratch(gpu):
-    # 15 tokens x 128 heads of size 256 on one kv head over a million keys: ~34 MB of partials
+    # an 8-token verify block of 64 heads on 8 kv heads at 32768 keys: its plan's partials exceed the 8 MiB
+    # array (checked first, from the library's own plan). The call gets real buffers of the shape it names, so
+    # that a wrong acceptance would launch over valid memory and fail here, not fault the device.
+    n_tok, n_heads, n_kv, hd, ctx = 8, 64, 8, 128, 32768
+    chunk, nsplit = gi_attn.decode_plan(ctx, n_tok, n_heads, n_kv, hd)
+    need = n_tok * n_heads * nsplit * (hd + 4) * 4
+    assert need > 8 << 20, f"the shape no longer exceeds the scratch ({need} bytes); pick a larger one"
+    q = torch.zeros((n_tok, n_heads * hd), dtype=torch.float32, device=gpu)
+    k = torch.zeros((ctx, n_kv, hd), dtype=torch.float16, device=gpu)
+    v = torch.zeros_like(k)
+    out = torch.zeros_like(q)
     lib = gi_attn.load_library()
-    rc = lib.gi_attn_decode_noalloc(None, 16, 128 * 256, 16, 16, 256, 256 * (1 << 20), 16, 128 * 256, (1 << 20) - 15,
-                                    None, 0, 15, 128, 1, 256, 0.0625)
+    rc = lib.gi_attn_decode_noalloc(None, q.data_ptr(), n_heads * hd, k.data_ptr(), v.data_ptr(), n_kv * hd, hd,
+                                    out.data_ptr(), n_heads * hd, ctx - n_tok, None, 0, n_tok, n_heads, n_kv, hd,
+                                    0.0625)
+    torch.cuda.synchronize()
     assert rc == -1 and "exceed" in lib.gi_last_error().decode()
