@@ -28,7 +28,8 @@ Decode steps rotate over several layers' caches whose total exceeds the 256 MB I
 model's layer loop does, so no step finds its K/V in the last-level cache.
 
 Prints ONE JSON line (rank 0). With the default workload the line also carries every other config of the
-benchmark under "secondary" (decode4k, verify, prefill8k and chunked, each with its own roofline) and the
+benchmark under "secondary" (decode4k, verify, prefill8k and chunked, each with its own roofline; then the
+int8, head-256 and 4-bit workloads) and the
 box's measured peaks, and the CPU baseline: the oracle's restatement of the reference's CPU attention
 (src/model.rs:1320-1409) over the same inputs with the cache widened to f32 (as the reference's CPU session
 holds it), timed on this host at its CPU share (up to 16 threads) and at half of it (the reference's default
@@ -647,6 +648,16 @@ def main():
         sec["prefill8k"] = secondary_entry(line)
         sec_r["prefill8k"] = r2
         sec["chunked"] = secondary_entry(run_chunked(torch, gi_attn, dev))
+        # the cache formats and head sizes beyond the configs: int8, head size 256 over f16, int8 and 4 bits
+        for w2 in ("decode64k_i8", "verify_i8", "decode64k_h256", "verify_h256", "decode64k_h256_i8",
+                   "verify_h256_i8", "decode64k_h256_q4", "verify_h256_q4"):
+            line, r2 = run_decode(torch, gi_attn, dev, w2, steps2, warm2)
+            sec[w2] = secondary_entry(line)
+            del r2
+        for w2 in ("prefill8k_i8", "prefill8k_h256", "prefill8k_h256_i8", "prefill8k_h256_q4"):
+            line, r2 = run_prefill(torch, gi_attn, dev, w2, 20, 5)
+            sec[w2] = secondary_entry(line)
+            del r2
         sec["hbm_copy_measured_GBs"] = round(hbm_copy_gbs(torch, dev), 1)
         sec["peaks_measured"] = peak_probes(torch, dev)
         result["secondary"] = sec

@@ -413,7 +413,9 @@ int decode_impl(void* stream, const float* q, long long q_stride, const void* kc
         if (kv_head_stride == 0) kv_head_stride = hd / 2;
         if (int e = check_kv_strides(kv_stride, kv_head_stride, n_kv, hd / 2, 16)) return e;
         if (!ks || !vs) return fail("null scale pointer");
-        if (((uintptr_t)ks & 1) || ((uintptr_t)vs & 1)) return fail("ks and vs must be 2-byte aligned");
+        // (the kernels read a row's scales in 4-byte words)
+        if (((uintptr_t)ks & 3) || ((uintptr_t)vs & 3) || ((sc_stride | sc_head_stride) & 1))
+            return fail("ks and vs must be 4-byte aligned and their strides even");
         if (int e = check_kv_strides(sc_stride, sc_head_stride, n_kv, 8, 1)) return e;
     } else {
         if (kv_head_stride == 0) kv_head_stride = hd;
@@ -550,7 +552,9 @@ int prefill_impl(void* stream, const void* q, int q_dtype, long long q_stride, c
         if (kv_head_stride == 0) kv_head_stride = hd / 2;
         if (int e = check_kv_strides(kv_stride, kv_head_stride, n_kv, hd / 2, 16)) return e;
         if (!ks || !vs) return fail("null scale pointer");
-        if (((uintptr_t)ks & 1) || ((uintptr_t)vs & 1)) return fail("ks and vs must be 2-byte aligned");
+        // (the kernels read a row's scales in 4-byte words)
+        if (((uintptr_t)ks & 3) || ((uintptr_t)vs & 3) || ((sc_stride | sc_head_stride) & 1))
+            return fail("ks and vs must be 4-byte aligned and their strides even");
         if (int e = check_kv_strides(sc_stride, sc_head_stride, n_kv, 8, 1)) return e;
     } else {
         if (kv_head_stride == 0) kv_head_stride = hd;

@@ -105,7 +105,7 @@ int gi_attn_decode_i8(void* stream, const float* q, long long q_stride, const in
  * 340-357): position t, kv head h has a row of 128 bytes at kc / vc + t*kv_stride + h*kv_head_stride (strides in
  * bytes, multiples of 16; kv_head_stride 0 means 128), value 2i in byte i's low nibble and 2i + 1 in its high one,
  * each stored as q + 8, and 8 f16 scales (one per 32 values) at ks / vs + t*sc_stride + h*sc_head_stride (f16
- * elements; both 0 mean the reference's [position][n_kv][8]). A value is f16((n - 8) * scale). The rows hold
+ * elements, even; ks / vs 4-byte aligned; both 0 mean the reference's [position][n_kv][8]). A value is f16((n - 8) * scale). The rows hold
  * rotated vectors (gi_qk_norm_rope_q4 rotates q and k alike and v in the store), so q must be the rotated
  * queries and out holds rotated rows: gi_hadamard_rows turns them back. Replaces: attention_decode_tc256 compiled
  * with KV4 (src/cuda.rs:2625-2802) + attention_combine, as GpuModel::attention dispatches it for 256-wide heads

@@ -150,3 +150,27 @@ def test_layer_harness_built_and_prints_usage():
     r = subprocess.run([harness, "--help"], capture_output=True, text=True, timeout=60)
     assert r.returncode == 0 and "usage: gi_layer_harness" in r.stdout
 
+
+
+def test_q4_entry_points_reject_bad_arguments_before_any_launch():
+    lib = gi_attn.load_library()
+    # the 4-bit cache: head size 256 only (the prefill and the operator fix it), 16-byte row strides, scales
+    # 4-byte aligned with even strides (the kernels read two scales per 4-byte word)
+    ok = dict(q=16, kc=16, vc=16, ks=16, vs=16)
+
+    def decode(ks=16, kv_stride=256, sc_stride=16, sc_head_stride=8):
+        return lib.gi_attn_decode_q4(None, ok["q"], 4096, ok["kc"], ok["vc"], ks, 16, kv_stride, 128, sc_stride,
+                                     sc_head_stride, 16, 4096, None, 0, 0, None, 0, 1, 16, 2, 0.0625)
+
+    assert decode(kv_stride=200) == -1 and "multiples of 16" in lib.gi_last_error().decode()
+    assert decode(ks=18) == -1 and "4-byte aligned" in lib.gi_last_error().decode()
+    assert decode(sc_stride=9) == -1 and "strides even" in lib.gi_last_error().decode()
+    assert decode(ks=None) == -1 and "scale" in lib.gi_last_error().decode()
+    rc = lib.gi_qk_norm_rope_q4(None, 16, None, None, 16, 16, 16, 16, 200, 128, 0, 0, 0, None, 0, 1, 16, 2, 256, 1e4,
+                                None, 1, 1e-6)
+    assert rc == -1 and "multiples of 16" in lib.gi_last_error().decode()
+    rc = lib.gi_qk_norm_rope_q4(None, 16, None, None, 16, 16, None, 16, 256, 128, 0, 0, 0, None, 0, 1, 16, 2, 256, 1e4,
+                                None, 1, 1e-6)
+    assert rc == -1 and "scale" in lib.gi_last_error().decode()
+    rc = lib.gi_hadamard_rows(None, 16, 256, 4, 300)
+    assert rc == -1 and "multiple of 256" in lib.gi_last_error().decode()
