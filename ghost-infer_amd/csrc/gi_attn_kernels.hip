@@ -73,7 +73,7 @@ struct GiDecodeArgs {
 
 // Slice partials of gi_attn_decode_noalloc: a module-global array (one per device, since every device loads
 // the code object itself), for callers that cannot allocate a workspace. Calls on one device share it.
-#define GI_SCRATCH_BYTES (8u << 20)
+#define GI_SCRATCH_BYTES (16u << 20)
 __device__ __attribute__((used, aligned(256))) unsigned char gi_scratch[GI_SCRATCH_BYTES];
 
 #define DEC_WAVES 4

@@ -77,12 +77,13 @@ int gi_attn_decode(void* stream, const float* q, long long q_stride, const uint1
                    size_t workspace_bytes, int pos0, const int* posp, int ctx_cap, int n_tok, int n_heads, int n_kv,
                    int hd, float scale);
 
-/* gi_attn_decode without a workspace: the slice partials go to a fixed 8 MiB array in device memory that the
+/* gi_attn_decode without a workspace: the slice partials go to a fixed 16 MiB array in device memory that the
  * library's code object holds on each device (from its load until the process ends), so the call allocates
  * nothing and takes no scratch argument. No counterpart in the reference; it is for callers that cannot
  * allocate (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). Shapes whose
- * partials exceed 8 MiB (n_tok * n_heads * slices * (hd + 4) * 4 bytes; config 2 needs 1.1 MB, an 8-token
- * verify at 32768 keys 3.9 MB) are rejected with GI_EINVAL. Every call on one device shares that array:
+ * partials exceed 16 MiB (n_tok * n_heads * slices * (hd + 4) * 4 bytes; config 2 needs 1.1 MB, an 8-token
+ * verify at 32768 keys 8.7 MB; with the default plan of about 256 workgroups no shape needs more than ~9 MB)
+ * are rejected with GI_EINVAL. Every call on one device shares that array:
  * calls that may overlap on one device (several streams, or several host threads) race and must not be
  * issued. */
 int gi_attn_decode_noalloc(void* stream, const float* q, long long q_stride, const uint16_t* kc, const uint16_t* vc,

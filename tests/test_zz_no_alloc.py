@@ -59,21 +59,54 @@ def test_noalloc_decode_matches_the_workspace_entry_point(gpu):
         assert torch.equal(out.view(torch.int32), want.view(torch.int32)), f"noalloc posp {pos} differs"
 
 
-def test_noalloc_rejects_partials_beyond_the_scratch(gpu):
-    # an 8-token verify block of 64 heads on 8 kv heads at 32768 keys: its plan's partials exceed the 8 MiB
-    # array (checked first, from the library's own plan). The call gets real buffers of the shape it names, so
-    # that a wrong acceptance would launch over valid memory and fail here, not fault the device.
-    n_tok, n_heads, n_kv, hd, ctx = 8, 64, 8, 128, 32768
-    chunk, nsplit = gi_attn.decode_plan(ctx, n_tok, n_heads, n_kv, hd)
-    need = n_tok * n_heads * nsplit * (hd + 4) * 4
-    assert need > 8 << 20, f"the shape no longer exceeds the scratch ({need} bytes); pick a larger one"
-    q = torch.zeros((n_tok, n_heads * hd), dtype=torch.float32, device=gpu)
-    k = torch.zeros((ctx, n_kv, hd), dtype=torch.float16, device=gpu)
-    v = torch.zeros_like(k)
-    out = torch.zeros_like(q)
-    lib = gi_attn.load_library()
-    rc = lib.gi_attn_decode_noalloc(None, q.data_ptr(), n_heads * hd, k.data_ptr(), v.data_ptr(), n_kv * hd, hd,
-                                    out.data_ptr(), n_heads * hd, ctx - n_tok, None, 0, n_tok, n_heads, n_kv, hd,
-                                    0.0625)
+def test_noalloc_config4_verify_fits(gpu):
+    # config 4's verify block (8 tokens at a 32768-key prefix, 32 / 4 heads) fits the array
+    gen = torch.Generator(device=gpu)
+    gen.manual_seed(7)
+    ctx, n_heads, n_kv, n_tok = 32776, 32, 4, 8
+    say("noalloc config 4")
+    k = torch.randn((n_kv, ctx, 128), generator=gen, device=gpu).half()
+    v = torch.randn((n_kv, ctx, 128), generator=gen, device=gpu).half()
+    q = torch.randn((n_tok, n_heads * 128), generator=gen, device=gpu)
+    want = gi_attn.decode(q, k, v, ctx - n_tok, n_heads, n_kv, kv_layout="head_major")
+    out = torch.full_like(want, float("nan"))
+    assert noalloc(q, k, v, ctx - n_tok, n_heads, n_kv, out) == 0, gi_attn.load_library().gi_last_error().decode()
     torch.cuda.synchronize()
-    assert rc == -1 and "exceed" in lib.gi_last_error().decode()
+    assert torch.equal(out.view(torch.int32), want.view(torch.int32))
+
+
+REJECT = r"""
+import ctypes, os, sys
+sys.path.insert(0, os.path.join(sys.argv[1], "ghost-infer_amd"))
+import torch, gi_attn
+n_tok, n_heads, n_kv, hd, ctx = 8, 32, 4, 128, 32776
+chunk, nsplit = gi_attn.decode_plan(ctx, n_tok, n_heads, n_kv, hd)
+need = n_tok * n_heads * nsplit * (hd + 4) * 4
+assert need > 16 << 20, need
+dev = torch.device("cuda:0")
+q = torch.zeros((n_tok, n_heads * hd), dtype=torch.float32, device=dev)
+k = torch.zeros((n_kv, ctx, hd), dtype=torch.float16, device=dev)
+v = torch.zeros_like(k)
+out = torch.zeros_like(q)
+lib = gi_attn.load_library()
+rc = lib.gi_attn_decode_noalloc(None, q.data_ptr(), n_heads * hd, k.data_ptr(), v.data_ptr(), hd, ctx * hd,
+                                out.data_ptr(), n_heads * hd, ctx - n_tok, None, 0, n_tok, n_heads, n_kv, hd, 0.088)
+torch.cuda.synchronize()
+print(rc, lib.gi_last_error().decode(), flush=True)
+"""
+
+
+def test_noalloc_rejects_partials_beyond_the_scratch(gpu, tmp_path):
+    # with the default plan no shape's partials exceed the array, so a child process plans for 2048 workgroups
+    # (GI_DECODE_TARGET_WGS, read once per process): config 4's verify then needs ~35 MB of partials and must be
+    # rejected before any launch. Its buffers are real and sized for the shape, so that a wrong acceptance would
+    # launch over valid memory and fail here rather than fault the device.
+    import os
+    import subprocess
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    say("noalloc rejection (child process)")
+    r = subprocess.run([sys.executable, "-c", REJECT, root], capture_output=True, text=True, timeout=120,
+                       env=dict(os.environ, GI_DECODE_TARGET_WGS="2048"))
+    assert r.returncode == 0, r.stderr[-2000:]
+    rc, msg = r.stdout.strip().split(" ", 1)
+    assert rc == "-1" and "exceed" in msg, r.stdout
