@@ -1,5 +1,5 @@
 /* gi_attn.h — C ABI of the MI355X (gfx950) attention path: split-K flash decoding and causal flash
- * prefill over a grouped-query f16 KV cache.
+ * prefill over a grouped-query KV cache (f16, int8 or 4-bit).
  *
  * This is the drop-in boundary for ghost-infer's attention operator. In the reference the engine's
  * layer loop calls GpuModel::attention (src/cuda.rs:8448-8541), which launches NVRTC-compiled kernels
@@ -22,9 +22,10 @@
  *    contiguous, which spreads a head's stream evenly over the HBM channels (the decode kernel is
  *    fastest with it). Strides are multiples of 8 elements and pointers 16-byte aligned.
  *  - Causality: token b of a call sits at position pos0 + b and attends to keys 0..pos0+b.
- *  - hd is 128, or 256 with the f16 cache (the reference's wide heads: attention_partial_gqa's hd 256 branch
- *    src/cuda.rs:1762-1781, attention_prefill_tc256 src/cuda.rs:2622-2623); n_heads must be a multiple of
- *    n_kv. The int8 entry points take hd 128.
+ *  - hd is 128 or 256 (the reference's wide heads: attention_partial_gqa's hd 256 branch src/cuda.rs:1762-1781,
+ *    attention_prefill_tc256 src/cuda.rs:2622-2623, attention_decode_tc256 src/cuda.rs:2625-2802) with the f16
+ *    and the int8 caches, and 256 with the 4-bit cache (the *_q4 entry points); n_heads must be a multiple of
+ *    n_kv.
  */
 #ifndef GI_ATTN_H
 #define GI_ATTN_H
