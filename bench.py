@@ -476,9 +476,8 @@ def run_decode(torch, gi_attn, dev, w, steps, warmup, n_tok_override=None, refer
     r = decode_workload(torch, gi_attn, dev, ctx, n_heads, n_kv, n_tok, steps, warmup, 1234, i8=i8, hd=hd)
     gbs = r["bytes"] / r["seconds"] / 1e9
     chunk, nsplit = gi_attn.decode_plan(ctx, n_tok, n_heads, n_kv, hd)
-    if i8 is True and hd == HD:  # int8 slices at head size 128 are whole 256-key units (64-key tiles, 4 waves)
-        chunk = -(-chunk // 256) * 256
-        nsplit = -(-ctx // chunk)
+    if i8:  # the plan query is the f16 cache's; the int8 and 4-bit kernels' pair groups (and tiles) differ
+        chunk = nsplit = None
     kt = kernel_times(gi_attn, r["step"], steps, torch, ("decode_partial", "decode_combine"))
     part_ms, part_n = kt["decode_partial"]
     comb_ms, _ = kt["decode_combine"]

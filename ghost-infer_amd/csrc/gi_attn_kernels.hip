@@ -842,40 +842,57 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
     // ---- merge each pair set's waves and the hi/lo columns: thread -> (pair, 4 dims)
     constexpr float LO = I8 ? 1.f / DEC_I8_LO : 1.f;      // the remainder column's scale (PM: no column)
     constexpr float OSC = I8 && PM ? 1.f / DEC_I8_VB : 1.f; // PM int8: the bias on P
+    // all LDS reads of the thread's items are issued before any arithmetic, so the merge waits for LDS once
+    constexpr int ITEMS = WG_PAIRS * HD / 1024;
+    float mw[ITEMS][WS], lw[ITEMS][WS];
+    float4 ohi[ITEMS][WS], olo[ITEMS][WS];
 #pragma unroll
-    for (int it = 0; it < WG_PAIRS * HD / 1024; it++) {
+    for (int it = 0; it < ITEMS; it++) {
         const int item = threadIdx.x + 256 * it;
         const int pl = item / (HD / 4), d4 = 4 * (item % (HD / 4)); // pair within the workgroup
+        const int w0 = (pl / (CPAIRS * NCB)) * WS;                    // the waves holding the pair
+        const int lp = pl % (CPAIRS * NCB);                            // the pair within those waves
+        const int row = PM ? lp : 16 * (lp >> 3) + 2 * (lp & 7);       // its (first) column
+#pragma unroll
+        for (int w = 0; w < WS; w++) {
+            mw[it][w] = sm_m[w0 + w][lp];
+            lw[it][w] = sm_l[w0 + w][lp];
+            ohi[it][w] = *reinterpret_cast<const float4*>(&sm_o[w0 + w][row][d4]);
+            if constexpr (!PM) olo[it][w] = *reinterpret_cast<const float4*>(&sm_o[w0 + w][row + 1][d4]);
+        }
+    }
+#pragma unroll
+    for (int it = 0; it < ITEMS; it++) {
+        const int item = threadIdx.x + 256 * it;
+        const int pl = item / (HD / 4), d4 = 4 * (item % (HD / 4));
         const int pi = gz * WG_PAIRS + pl;
-        const int w0 = (pl / (CPAIRS * NCB)) * WS;       // the waves holding the pair
-        const int w1 = w0 + WS;
-        const int lp = pl % (CPAIRS * NCB);               // the pair within those waves
-        if (pi < npairs) {
-            const int row = PM ? lp : 16 * (lp >> 3) + 2 * (lp & 7); // its (first) column
-            float M = GI_NEG_INF;
-            for (int w = w0; w < w1; w++) M = fmaxf(M, sm_m[w][lp]);
-            float L = 0.f;
-            float4 O = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (M != GI_NEG_INF) {
-                for (int w = w0; w < w1; w++) {
-                    const float wt = __builtin_amdgcn_exp2f(sm_m[w][lp] - M);
-                    L += wt * sm_l[w][lp];
-                    const float4 hi = *reinterpret_cast<const float4*>(&sm_o[w][row][d4]);
-                    if constexpr (PM) {
-                        const float ws = wt * OSC;
-                        O.x += ws * hi.x;
-                        O.y += ws * hi.y;
-                        O.z += ws * hi.z;
-                        O.w += ws * hi.w;
-                    } else {
-                        const float4 lo = *reinterpret_cast<const float4*>(&sm_o[w][row + 1][d4]);
-                        O.x += wt * (hi.x + lo.x * LO);
-                        O.y += wt * (hi.y + lo.y * LO);
-                        O.z += wt * (hi.z + lo.z * LO);
-                        O.w += wt * (hi.w + lo.w * LO);
-                    }
+        float M = GI_NEG_INF;
+#pragma unroll
+        for (int w = 0; w < WS; w++) M = fmaxf(M, mw[it][w]);
+        float L = 0.f;
+        float4 O = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (M != GI_NEG_INF) {
+#pragma unroll
+            for (int w = 0; w < WS; w++) {
+                const float wt = __builtin_amdgcn_exp2f(mw[it][w] - M);
+                L += wt * lw[it][w];
+                const float4 hi = ohi[it][w];
+                if constexpr (PM) {
+                    const float ws = wt * OSC;
+                    O.x += ws * hi.x;
+                    O.y += ws * hi.y;
+                    O.z += ws * hi.z;
+                    O.w += ws * hi.w;
+                } else {
+                    const float4 lo = olo[it][w];
+                    O.x += wt * (hi.x + lo.x * LO);
+                    O.y += wt * (hi.y + lo.y * LO);
+                    O.z += wt * (hi.z + lo.z * LO);
+                    O.w += wt * (hi.w + lo.w * LO);
                 }
             }
+        }
+        if (pi < npairs) {
             const int tk = pi / G, h = kvh * G + pi % G;
             if (a.nsplit == 1) {
                 const float inv = 1.f / L;

@@ -55,8 +55,9 @@ const char* gi_last_error(void);
 
 /* Slice plan of a decode call: keys per slice (`chunk`) and slices per token (`nsplit`) for tokens whose
  * largest span is max_span. Counterpart of att_want / att_chunk / max_splits (src/cuda.rs:8426-8444),
- * re-chosen for 256 CUs: slices are multiples of 128 keys (64 at hd 256; the int8 kernels round up to 256)
- * and about one workgroup per CU in total. The plan of the f16 cache (the int8 kernels may take fewer slices). */
+ * re-chosen for 256 CUs: about one workgroup per CU in total, slices as short as that allows in whole wave tiles
+ * (32 keys; 16 at hd 256; the int8 kernels' 64) and at least one tile per wave (128 keys; 64 at hd 256; int8 256).
+ * The plan of the f16 cache (the int8 and 4-bit kernels may take other slices). */
 int gi_attn_decode_plan(int max_span, int n_tok, int n_heads, int n_kv, int hd, int* chunk, int* nsplit);
 
 /* Bytes of workspace gi_attn_decode needs for n_tok tokens whose spans reach at most ctx_cap keys (the

@@ -122,7 +122,8 @@ def test_decode_plan_covers_the_span(ctx, n_tok, n_heads, n_kv, hd):
     part = (hd + 4) * 4  # bytes of one slice partial
 
     chunk, nsplit = gi_attn.decode_plan(ctx, n_tok, n_heads, n_kv, hd)
-    assert chunk % (64 if hd == 256 else 128) == 0 and chunk > 0
+    # whole wave tiles (16 keys at head size 256, 32 at 128), at least one per wave of the workgroup
+    assert chunk % (16 if hd == 256 else 32) == 0 and chunk >= (64 if hd == 256 else 128)
     assert (nsplit - 1) * chunk < ctx <= nsplit * chunk
     if nsplit > 1:
         # every launch of up to n_tok tokens with spans up to ctx fits the workspace size query
