@@ -90,6 +90,9 @@ __device__ __attribute__((used, aligned(256))) unsigned char gi_scratch[GI_SCRAT
 // An empty volatile asm: a block holding it cannot be executed speculatively, so the compiler keeps the
 // (wave-uniform) branch around it instead of turning the block into selects that run every time.
 #define GI_KEEP_BRANCH() asm volatile("")
+#ifndef DEC_PIPE // software-pipelined tiles in the one-pair-per-column f16 kernels
+#define DEC_PIPE 1
+#endif
 #ifndef DEC_CPOL // cache policy of the K/V loads of decode variants whose waves stream tiles of their own (2: nt)
 #define DEC_CPOL 2
 #endif
@@ -283,7 +286,7 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
     }
     // smallest span among the wave's valid columns (the lowest token's: column 0 of block 0 is always valid):
     // tiles below it need no masking
-    const int span_lo = min(pos0 + pair0 / G + 1 - k_begin, nkeys);
+    const int span_lo = __builtin_amdgcn_readfirstlane(min(pos0 + pair0 / G + 1 - k_begin, nkeys)); // (uniform: an SGPR)
     // Q rows (f32, 8 dims per lane per k-step), issued before the first K/V tiles so that waiting for them
     // leaves the K/V loads in flight
     u4 qraw[NCB][KK][2];
@@ -460,13 +463,17 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
                 for (int j = 0; j < 4; j++) {
                     float v = sacc[cb][b][j];
                     if constexpr (!PM) v = v + lane_xor1(v); // hi + lo columns of the pair (same sum in both lanes)
-                    if (masked) {
-                        int key = t + 8 * grp + 4 * b + j;
-                        v = key < span[cb] ? v : GI_NEG_INF;
-                    }
                     sc[4 * b + j] = v;
-                    mx = fmaxf(mx, v);
                 }
+            // the mask as a real branch: only a slice's last tiles take it
+            if (masked) {
+                GI_KEEP_BRANCH();
+#pragma unroll
+                for (int i = 0; i < 8; i++)
+                    if (t + 8 * grp + i >= span[cb]) sc[i] = GI_NEG_INF;
+            }
+#pragma unroll
+            for (int i = 0; i < 8; i++) mx = fmaxf(mx, sc[i]);
             mx = rows_max(mx);
             // the column's reference max moves only when a score exceeds it by more than 2^8 in probability:
             // P <= 256 is exact enough in the f16 hi/lo split, and most tiles skip rescaling O
@@ -502,10 +509,8 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
         for (int dd = 0; dd < 8; dd++) {
             u4 w;
 #pragma unroll
-            for (int p = 0; p < 4; p++) {
-                uint32_t lo = B.v[2 * p][dd >> 1], hi = B.v[2 * p + 1][dd >> 1];
-                w[p] = (dd & 1) ? ((lo >> 16) | (hi & 0xffff0000u)) : ((lo & 0xffffu) | (hi << 16));
-            }
+            for (int p = 0; p < 4; p++) // halves dd % 2 of keys 2p (low) and 2p + 1 (high): one v_perm
+                w[p] = __builtin_amdgcn_perm(B.v[2 * p + 1][dd >> 1], B.v[2 * p][dd >> 1], (dd & 1) ? 0x07060302u : 0x05040100u);
             const h8 vt = __builtin_bit_cast(h8, w);
 #pragma unroll
             for (int cb = 0; cb < NCB; cb++) {
@@ -681,10 +686,16 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
                 float v = sacc[cb][j];
                 if constexpr (!PM) v = v + lane_xor1(v); // hi + lo columns of the pair
                 if constexpr (I8) v *= ksb[j];           // the key's scale
-                if (masked) v = t + 4 * grp + j < span[cb] ? v : GI_NEG_INF;
                 sc[j] = v;
-                mx = fmaxf(mx, v);
             }
+            if (masked) {
+                GI_KEEP_BRANCH();
+#pragma unroll
+                for (int j = 0; j < 4; j++)
+                    if (t + 4 * grp + j >= span[cb]) sc[j] = GI_NEG_INF;
+            }
+#pragma unroll
+            for (int j = 0; j < 4; j++) mx = fmaxf(mx, sc[j]);
             mx = rows_max(mx);
             const bool up = mx > m_run[cb] + DEC_RESCALE_LOG2;
             if (__builtin_amdgcn_ballot_w64(up)) {
@@ -752,10 +763,8 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
             } else {
                 const int h = dd >> 3, w = (dd & 7) >> 1;
 #pragma unroll
-                for (int p = 0; p < 2; p++) {
-                    const uint32_t lo = B.v[2 * p][h][w], hi = B.v[2 * p + 1][h][w];
-                    vw[p] = (dd & 1) ? ((lo >> 16) | (hi & 0xffff0000u)) : ((lo & 0xffffu) | (hi << 16));
-                }
+                for (int p = 0; p < 2; p++)
+                    vw[p] = __builtin_amdgcn_perm(B.v[2 * p + 1][h][w], B.v[2 * p][h][w], (dd & 1) ? 0x07060302u : 0x05040100u);
             }
             const h4x vt = __builtin_bit_cast(h4x, vw);
 #pragma unroll
@@ -766,6 +775,80 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
         }
         __builtin_amdgcn_sched_barrier(0);
         if (reload) load_v(B, t + NB * STRIDE);
+    };
+    // ---- software pipeline of the one-pair-per-column f16 kernels (head size 128): a tile's QK runs one step
+    // ahead, so the MFMAs of tile t+1's QK interleave with tile t's exp and packing, and tile t's PV MFMAs with
+    // tile t+1's row max. Unmasked tiles only; the rest take process_h.
+    auto pm_qk = [&](auto& B, f4 (&S)[NCB][2]) {
+#pragma unroll
+        for (int cb = 0; cb < NCB; cb++)
+#pragma unroll
+            for (int b = 0; b < 2; b++) {
+                S[cb][b] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int kk = 0; kk < 4; kk++) {
+                    S[cb][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, B.k[b][kk]), qf[cb][kk],
+                                                                      S[cb][b], 0, 0, 0);
+                    S[cb][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, B.k[b][kk]), qfl[cb][kk],
+                                                                      S[cb][b], 0, 0, 0);
+                }
+            }
+    };
+    // the tile's row max per column, and the lazy rescale of O when it moves by more than 2^8
+    auto pm_max = [&](const f4 (&S)[NCB][2]) {
+        float mx[NCB];
+        bool up[NCB];
+        bool any = false;
+#pragma unroll
+        for (int cb = 0; cb < NCB; cb++) {
+            mx[cb] = fmaxf(fmaxf(fmaxf(S[cb][0][0], S[cb][0][1]), fmaxf(S[cb][0][2], S[cb][0][3])),
+                           fmaxf(fmaxf(S[cb][1][0], S[cb][1][1]), fmaxf(S[cb][1][2], S[cb][1][3])));
+            mx[cb] = rows_max(mx[cb]);
+            up[cb] = mx[cb] > m_run[cb] + DEC_RESCALE_LOG2;
+            any = any || up[cb];
+        }
+        if (__builtin_amdgcn_ballot_w64(any)) {
+#pragma unroll
+            for (int cb = 0; cb < NCB; cb++) {
+                const float m_new = up[cb] ? mx[cb] : m_run[cb];
+                const float alpha = up[cb] ? __builtin_amdgcn_exp2f(m_run[cb] - m_new) : 1.f;
+                m_run[cb] = m_new;
+                l_run[cb] *= alpha;
+#pragma unroll
+                for (int dd = 0; dd < 8; dd++) o[cb][dd] *= alpha;
+            }
+        }
+    };
+    auto pm_exp = [&](const f4 (&S)[NCB][2], h8 (&pf)[NCB], h8 (&pfl)[NCB]) {
+#pragma unroll
+        for (int cb = 0; cb < NCB; cb++) {
+            const float m_use = m_run[cb] == GI_NEG_INF ? 0.f : m_run[cb];
+            float psum = 0.f;
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const float p = __builtin_amdgcn_exp2f(S[cb][i >> 2][i & 3] - m_use);
+                psum += p;
+                const _Float16 hi = (_Float16)p;
+                pf[cb][i] = hi;
+                pfl[cb][i] = (_Float16)(p - (float)hi);
+            }
+            l_run[cb] += psum;
+        }
+    };
+    auto pm_pv = [&](auto& B, const h8 (&pf)[NCB], const h8 (&pfl)[NCB]) {
+#pragma unroll
+        for (int dd = 0; dd < 8; dd++) {
+            u4 w;
+#pragma unroll
+            for (int p = 0; p < 4; p++)
+                w[p] = __builtin_amdgcn_perm(B.v[2 * p + 1][dd >> 1], B.v[2 * p][dd >> 1], (dd & 1) ? 0x07060302u : 0x05040100u);
+            const h8 vt = __builtin_bit_cast(h8, w);
+#pragma unroll
+            for (int cb = 0; cb < NCB; cb++) {
+                o[cb][dd] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vt, pf[cb], o[cb][dd], 0, 0, 0);
+                o[cb][dd] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vt, pfl[cb], o[cb][dd], 0, 0, 0);
+            }
+        }
     };
     auto process = [&](Buf& B, int t, bool reload) {
         if constexpr (HD == 256) process_256(B, t, reload);
@@ -808,6 +891,44 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
     // Steady state: every buffer gets a further tile (those past the slice read zeros and are never
     // processed). The last round of tiles runs without reloads, so no load is left in flight at the end.
     int t = t_first;
+    if constexpr (DEC_PIPE && PM && !I8 && !Q4 && HD == 128) {
+        static_assert(NB == 2, "the pipeline alternates two register buffers");
+        // State at the top of each step: tile t in B[0] with its scores S0 (row max taken, O rescaled), its K
+        // buffer already refilled with tile t + 2 STRIDE; tile t + STRIDE in B[1]. A step finishes tiles t and
+        // t + STRIDE and scores tile t + 2 STRIDE, so it runs while that tile needs no mask.
+        if (t + 2 * STRIDE + DEC_TILE <= span_lo) {
+            f4 S0[NCB][2], S1[NCB][2];
+            h8 pf[NCB], pfl[NCB];
+            pm_qk(B[0], S0);
+            load_k(B[0], t + 2 * STRIDE);
+            pm_max(S0);
+            do {
+                __builtin_amdgcn_sched_barrier(0);
+                pm_qk(B[1], S1);
+                pm_exp(S0, pf, pfl);
+                load_k(B[1], t + 3 * STRIDE);
+                pm_pv(B[0], pf, pfl);
+                pm_max(S1);
+                load_v(B[0], t + 2 * STRIDE);
+                __builtin_amdgcn_sched_barrier(0);
+                pm_qk(B[0], S0);
+                pm_exp(S1, pf, pfl);
+                load_k(B[0], t + 4 * STRIDE);
+                pm_pv(B[1], pf, pfl);
+                pm_max(S0);
+                load_v(B[1], t + 3 * STRIDE);
+                t += 2 * STRIDE;
+            } while (t + 2 * STRIDE + DEC_TILE <= span_lo);
+            __builtin_amdgcn_sched_barrier(0);
+            // finish tile t; B[0] then holds tile t + 2 STRIDE and B[1] tile t + STRIDE, which process_h takes,
+            // so the steps below start from t + 2 STRIDE with the buffers in order
+            pm_exp(S0, pf, pfl);
+            pm_pv(B[0], pf, pfl);
+            load_v(B[0], t + 2 * STRIDE);
+            if (t + STRIDE < nkeys) process(B[1], t + STRIDE, true);
+            t += 2 * STRIDE;
+        }
+    }
     for (; t + NB * STRIDE < nkeys; t += NB * STRIDE) {
 #pragma unroll
         for (int i = 0; i < NB; i++) process(B[i], t + i * STRIDE, true);
