@@ -86,17 +86,20 @@ def seeded_cache(gen, rows, n_kv, dev, torch, layout="reference", i8=False, hd=H
     return k, v, None, None
 
 
-def kernel_times(gi_attn, fn, steps, torch, kinds):
+def kernel_times(gi_attn, fn, steps, torch, kinds, warm_steps=0):
     """Runs `steps` more steps eagerly with the library's per-kernel event timing on (HIP events recorded
     around each launch, on the stream it is launched on) and returns {kind: (mean ms per launch,
-    launches)}."""
+    launches)}. warm_steps untimed steps run first, right before them (the clocks drop during the spin
+    below, and an MFMA-bound kernel of a few launches would otherwise be timed while they climb back)."""
     for k in kinds:
         gi_attn.kernel_timing_read(k)  # drop anything recorded before
-    gi_attn.kernel_timing(True)
     try:
         # a spin kernel in front keeps the GPU busy while the host enqueues every step, so each event pair
         # brackets its kernel back to back and not the host's submission gaps
         torch.cuda._sleep(int(5e7))
+        for i in range(warm_steps):
+            fn(i)
+        gi_attn.kernel_timing(True)
         for i in range(steps):
             fn(i)
         torch.cuda.synchronize()
@@ -142,12 +145,28 @@ def profile_traffic(name):
     return None
 
 
-def time_steps(fn, steps, warmup, torch):
-    """Runs warmup untimed steps, then times exactly `steps` steps between synchronisations with events on
-    the stream the kernels are launched on (torch's current stream). Returns seconds per step."""
-    for i in range(warmup):
+# Seconds of untimed work before each timed region (besides the `warmup` steps): the GPU's clocks climb for
+# tens of milliseconds after an idle spell, so a region that starts cold times the ramp (config 3's prefill
+# measured 0.58 ms per launch over 20 launches and 0.52 ms over 200, on one box).
+WARM_SECONDS = float(os.environ.get("GI_BENCH_WARM_SECONDS", "0.3"))
+
+
+def warm_up(fn, warmup, torch):
+    """Runs `warmup` untimed steps, and more until WARM_SECONDS of GPU time have passed."""
+    t0 = time.perf_counter()
+    i = 0
+    while i < warmup or time.perf_counter() - t0 < WARM_SECONDS:
         fn(i)
+        i += 1
+        if i >= warmup and i % 16 == 0:
+            torch.cuda.synchronize()
     torch.cuda.synchronize()
+
+
+def time_steps(fn, steps, warmup, torch):
+    """Runs warmup untimed steps (warm_up), then times exactly `steps` steps between synchronisations with
+    events on the stream the kernels are launched on (torch's current stream). Returns seconds per step."""
+    warm_up(fn, warmup, torch)
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
     start.record()
@@ -163,7 +182,8 @@ def time_steps(fn, steps, warmup, torch):
 def time_steps_graph(fn, steps, warmup, torch):
     """As time_steps, but the `steps` timed steps are captured once into a HIP graph and replayed, as the
     reference replays its one-token decode step (src/cuda.rs:8686-8712): the time is the GPU's, not the
-    Python launch path's. The graph is replayed once untimed (upload) before the timed replay."""
+    Python launch path's. The graph is replayed untimed (upload, then warm_up's time) before the timed
+    replay."""
     for i in range(warmup):
         fn(i)
     torch.cuda.synchronize()
@@ -171,8 +191,7 @@ def time_steps_graph(fn, steps, warmup, torch):
     with torch.cuda.graph(g):
         for i in range(steps):
             fn(i)
-    g.replay()
-    torch.cuda.synchronize()
+    warm_up(lambda i: g.replay(), 1, torch)
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
     start.record()
@@ -434,7 +453,9 @@ def cpu_baseline_prefill(q, k, v, n_heads, n_kv, threads, rows=64, budget_s=8.0)
 
 def prefill_roofline(gi_attn, r, steps, torch, profile="pmc_prefill_prefill8k", kernel="gi_prefill_fwd"):
     """Roofline object of the prefill kernel: algorithmic flops of one launch / its mean duration."""
-    ms, n = kernel_times(gi_attn, r["step"], steps, torch, ("prefill",))["prefill"]
+    # ~0.1 s of launches before the timed ones (at most 100)
+    warm = min(100, max(0, math.ceil(0.1 / r["seconds"])))
+    ms, n = kernel_times(gi_attn, r["step"], steps, torch, ("prefill",), warm)["prefill"]
     tf = r["flops"] / (ms / 1e3) / 1e12
     return {"bound": "mfma", "achieved": round(tf, 1), "peak": F16_DENSE_PEAK_TFLOPS, "unit": "TFLOP/s",
             "frac": round(tf / F16_DENSE_PEAK_TFLOPS, 4), "traffic": profile_traffic(profile),

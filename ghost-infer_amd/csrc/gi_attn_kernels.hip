@@ -55,7 +55,7 @@ struct GiDecodeArgs {
     int n_tok;
     int n_heads;
     int n_kv;
-    int chunk;             // keys per slice, a multiple of 128
+    int chunk;             // keys per slice: whole wave tiles, at least one per wave
     int nsplit;            // slices per token (the grid's x)
     float qscale;          // scale * log2(e)
     int hd;                // head size: 128 or 256 (f16 cache); partial rows are hd + 4 floats
