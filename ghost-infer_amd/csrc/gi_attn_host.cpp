@@ -354,9 +354,9 @@ DecVariant dec_variant(int n_tok, int G, int hd = 128, bool i8 = false) {
 
 // Slices of a span: at most per_slot per (kv head, pair group), so the grid stays near decode_target_wgs(). A
 // slice holds whole wave tiles (unit / 4 keys: the waves of a workgroup take a slice's tiles in turn) and at least
-// `unit` keys (one tile per wave), and is as short as the cap allows, so the slowest workgroup's share is within
-// one tile of the average. At config 4's 32776 keys: 61 slices of 544 keys, where whole units of 4 tiles gave
-// 52 slices of 640 (208 of 256 workgroups busy).
+// `unit` keys (one tile per wave), and is as short as the cap allows: within one tile of the span's even share
+// over per_slot slices. At config 4's 32776 keys: 61 slices of 544 keys, where whole units of 4 tiles gave 52
+// slices of 640 (208 of 256 workgroups busy).
 void plan(int max_span, int n_tok, int n_heads, int n_kv, int* chunk, int* nsplit, int unit = kSliceUnit,
           int hd = 128, bool i8 = false) {
     int G = n_heads / n_kv;
