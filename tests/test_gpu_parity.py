@@ -131,11 +131,11 @@ def test_decode_workspace_reuse_across_shapes(gpu):
                      what=f"reuse {n_tok}@{pos0}")
 
 
-@pytest.mark.parametrize("n_tok,n_heads,n_kv", [(1, 32, 8), (8, 32, 4)])
+@pytest.mark.parametrize("n_tok,n_heads,n_kv", [(1, 32, 8), (2, 32, 4), (3, 32, 4), (8, 32, 4)])
 def test_decode_graph_replay(gpu, n_tok, n_heads, n_kv):
-    # a decode step (or an 8-token verify block: two pair sets per slice) with a device position, captured
-    # once and replayed at several positions, with eager work between the replays; each replay matches the
-    # float64 reference
+    # a decode step (or a verify block: 16 pairs per kv head in one column block, 24 in two, 64 in two pair
+    # sets per slice) with a device position, captured once and replayed at several positions, with eager work
+    # between the replays; each replay matches the float64 reference
     cap = 5000
     q, k, v = make_inputs(91, n_tok, cap, n_heads, n_kv)
     qt, kt, vt = to_dev(q, k, v, gpu)
