@@ -60,6 +60,9 @@ DECODE_SHAPES = [
     (6, 130, 32, 4),   # 48 pairs: one workgroup, its second pair set half idle
     (17, 300, 32, 4),  # 136 pairs: the third workgroup's second pair set has no pair at all
     (4, 40, 16, 1),    # 64 pairs on one kv head, one slice: fewer (slice, kv head) items than XCDs
+    (1, 5000, 64, 4),  # G = 16: one token's 16 pairs in one column block
+    (1, 3000, 32, 1),  # G = 32: two column blocks
+    (2, 2000, 64, 2),  # G = 32, two tokens: 64 pairs, two pair sets
 ]
 
 
@@ -195,6 +198,8 @@ PREFILL_SHAPES = [
     (70, 130, 8, 4, np.float16, torch.float32),
     (256, 256, 32, 4, np.float16, torch.float16),
     (1000, 24, 16, 2, np.float16, torch.float32),
+    (300, 100, 64, 4, np.float32, torch.float32),  # G = 16
+    (200, 0, 32, 1, np.float16, torch.float16),    # G = 32
 ]
 
 
