@@ -51,6 +51,8 @@ DECODE_SHAPES_256 = [
     (2, 15, 16, 2),   # wave 1's first tile (keys 16..) lies past token 0's span but not token 1's
     (3, 60, 16, 2),   # 24 pairs: one pair per column, waves 2 and 3 idle
     (6, 130, 16, 2),  # 48 pairs
+    (1, 3000, 32, 2), # G = 16: one token's 16 pairs, one pair per column
+    (2, 2000, 32, 1), # G = 32, two tokens: 64 pairs on one kv head
 ]
 
 
