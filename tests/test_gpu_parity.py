@@ -350,6 +350,23 @@ ROPE_SHAPES = [
 ]
 
 
+def _rope_cases(count, seed):
+    # seeded random shapes: head sizes 64/128/256, full or half rotary, 1-300 rows at positions up to 5000,
+    # 1-8 kv heads and group sizes 1-8, each option on or off
+    rng = np.random.default_rng(seed)
+    out = []
+    for _ in range(count):
+        hd = int(rng.choice([64, 128, 256]))
+        n_kv = int(rng.choice([1, 2, 4, 8]))
+        out.append((int(rng.integers(1, 301)), int(rng.integers(0, 5001)), n_kv * int(rng.integers(1, 9)), n_kv, hd,
+                    hd // int(rng.choice([1, 2])), bool(rng.integers(0, 2)), bool(rng.integers(0, 2)),
+                    bool(rng.integers(0, 2)), str(rng.choice(["reference", "head_major"]))))
+    return out
+
+
+ROPE_SHAPES += _rope_cases(12, 41)
+
+
 @pytest.mark.parametrize("n,pos0,n_heads,n_kv,hd,rope_dim,neox,norm,use_ff,layout", ROPE_SHAPES)
 def test_qk_norm_rope_matches_oracle(gpu, n, pos0, n_heads, n_kv, hd, rope_dim, neox, norm, use_ff, layout):
     say("qk_norm_rope", n, pos0, n_heads, n_kv, hd, rope_dim, neox, norm, use_ff, layout)
