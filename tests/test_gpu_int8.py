@@ -185,6 +185,13 @@ ROPE_I8_SHAPES = [
     (300, 0, 32, 4, 128, True, True, "head_major"),
     (3, 2000, 8, 2, 256, True, True, "reference"),
 ]
+# seeded random shapes: head sizes 64/128/256, 1-300 rows at positions up to 5000, 1-8 kv heads, group sizes 1-8
+_rng = np.random.default_rng(51)
+for _ in range(8):
+    _kv = int(_rng.choice([1, 2, 4, 8]))
+    ROPE_I8_SHAPES.append((int(_rng.integers(1, 301)), int(_rng.integers(0, 5001)), _kv * int(_rng.integers(1, 9)), _kv,
+                           int(_rng.choice([64, 128, 256])), bool(_rng.integers(0, 2)), bool(_rng.integers(0, 2)),
+                           str(_rng.choice(["reference", "head_major"]))))
 
 
 @pytest.mark.parametrize("n,pos0,n_heads,n_kv,hd,neox,norm,layout", ROPE_I8_SHAPES)
