@@ -77,19 +77,21 @@ def test_decode_q4_head_major_and_device_position(gpu, n_tok):
                  rel_l2=2e-5, what="q4 decode head-major posp vs f64")
 
 
-def test_rope_q4_store_is_bit_exact(gpu):
+@pytest.mark.parametrize("n,H,K,ctx,pos0", [(7, 8, 2, 40, 11), (1, 16, 2, 5000, 4999), (200, 4, 1, 260, 50),
+                                            (33, 32, 4, 100, 60)])
+def test_rope_q4_store_is_bit_exact(gpu, n, H, K, ctx, pos0):
     # q/k heads: RMSNorm + RoPE + rotation, against the oracle within f32 rounding (sincos and pow differ by
-    # ulps); the k cache: the oracle's quantiser of the kernel's own rotated k rows, bit for bit; the v cache:
-    # rotation and quantiser of the same input, bit for bit
-    n, H, K, ctx, pos0 = 7, 8, 2, 40, 11
-    rng = np.random.default_rng(21)
+    # ulps, and a rotation angle of a few thousand radians moves by ~1e-4 at large positions); the k cache: the
+    # oracle's quantiser of the kernel's own rotated k rows, bit for bit; the v cache: rotation and quantiser of
+    # the same input, bit for bit
+    rng = np.random.default_rng(21 + n)
     qkv = rng.standard_normal((n, (H + 2 * K) * 256)).astype(np.float32)
     qn = rng.uniform(0.5, 1.5, 256).astype(np.float32)
     kn = rng.uniform(0.5, 1.5, 256).astype(np.float32)
     z8 = np.zeros((ctx, K * 128), np.uint8)
     z16 = np.zeros((ctx, K * 8), np.uint16)
     want, wkc, wvc, wks, wvs = O.qk_norm_rope_q4(qkv, z8, z8, z16, z16, pos0, H, K, qn=qn, kn=kn)
-    say("rope q4 store")
+    say("rope q4 store", n, H, K, ctx, pos0)
     x = torch.from_numpy(qkv).to(gpu)
     kc = torch.zeros((ctx, K, 128), dtype=torch.uint8, device=gpu)
     vc = torch.zeros_like(kc)
@@ -99,7 +101,7 @@ def test_rope_q4_store_is_bit_exact(gpu):
                             kn=torch.from_numpy(kn).to(gpu))
     torch.cuda.synchronize()
     got = x.cpu().numpy()
-    np.testing.assert_allclose(got, want, rtol=0, atol=2e-5)
+    np.testing.assert_allclose(got, want, rtol=0, atol=2e-5 if pos0 + n < 100 else 2e-3)
     krot = got[:, H * 256:(H + K) * 256].reshape(n * K, 256)
     kq, ksq = O.kv4_quant(krot)
     np.testing.assert_array_equal(kc.cpu().numpy()[pos0:pos0 + n].reshape(n * K, 128), kq)
