@@ -781,13 +781,16 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
     };
     // ---- software pipeline of the one-pair-per-column f16 kernels (head size 128): a tile's QK runs one step
     // ahead, so the MFMAs of tile t+1's QK interleave with tile t's exp and packing, and tile t's PV MFMAs with
-    // tile t+1's row max. Unmasked tiles only; the rest take process_h.
+    // tile t+1's row max. Unmasked tiles only; the rest take process_h. Scores come out of the MFMA relative to
+    // the column's reference max (each chain starts from C = -max), so the exp takes them as they are; a tile
+    // that moves the reference shifts its own scores by the change.
     auto pm_qk = [&](auto& B, f4 (&S)[NCB][2]) {
 #pragma unroll
-        for (int cb = 0; cb < NCB; cb++)
+        for (int cb = 0; cb < NCB; cb++) {
+            const float mu = m_run[cb] == GI_NEG_INF ? 0.f : m_run[cb];
 #pragma unroll
             for (int b = 0; b < 2; b++) {
-                S[cb][b] = f4{0.f, 0.f, 0.f, 0.f};
+                S[cb][b] = f4{-mu, -mu, -mu, -mu};
 #pragma unroll
                 for (int kk = 0; kk < 4; kk++) {
                     S[cb][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, B.k[b][kk]), qf[cb][kk],
@@ -795,41 +798,49 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
                     S[cb][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, B.k[b][kk]), qfl[cb][kk],
                                                                       S[cb][b], 0, 0, 0);
                 }
+                // (in VGPRs once, for the max and then the exp, instead of two reads of an accumulator register)
+                asm volatile("" : "+v"(S[cb][b]));
             }
+        }
     };
-    // the tile's row max per column, and the lazy rescale of O when it moves by more than 2^8
-    auto pm_max = [&](const f4 (&S)[NCB][2]) {
+    // the tile's row max per column, and the lazy rescale of O when the reference moves (by more than 2^8; the
+    // first tile sets it), which also shifts the tile's scores onto the new reference
+    auto pm_max = [&](f4 (&S)[NCB][2]) {
         float mx[NCB];
         bool up[NCB];
         bool any = false;
 #pragma unroll
         for (int cb = 0; cb < NCB; cb++) {
-            mx[cb] = fmaxf(fmaxf(fmaxf(S[cb][0][0], S[cb][0][1]), fmaxf(S[cb][0][2], S[cb][0][3])),
-                           fmaxf(fmaxf(S[cb][1][0], S[cb][1][1]), fmaxf(S[cb][1][2], S[cb][1][3])));
-            mx[cb] = rows_max(mx[cb]);
-            up[cb] = mx[cb] > m_run[cb] + DEC_RESCALE_LOG2;
+            float m = fmaxf(fmaxf(S[cb][0][0], S[cb][0][1]), S[cb][0][2]);
+            m = fmaxf(fmaxf(m, S[cb][0][3]), S[cb][1][0]);
+            m = fmaxf(fmaxf(m, S[cb][1][1]), S[cb][1][2]);
+            mx[cb] = rows_max(fmaxf(m, S[cb][1][3]));
+            up[cb] = m_run[cb] == GI_NEG_INF || mx[cb] > DEC_RESCALE_LOG2;
             any = any || up[cb];
         }
         if (__builtin_amdgcn_ballot_w64(any)) {
 #pragma unroll
             for (int cb = 0; cb < NCB; cb++) {
-                const float m_new = up[cb] ? mx[cb] : m_run[cb];
+                const float mu = m_run[cb] == GI_NEG_INF ? 0.f : m_run[cb];
+                const float m_new = up[cb] ? mx[cb] + mu : m_run[cb];
                 const float alpha = up[cb] ? __builtin_amdgcn_exp2f(m_run[cb] - m_new) : 1.f;
+                const float delta = up[cb] ? m_new - mu : 0.f;
                 m_run[cb] = m_new;
                 l_run[cb] *= alpha;
 #pragma unroll
                 for (int dd = 0; dd < 8; dd++) o[cb][dd] *= alpha;
+#pragma unroll
+                for (int b = 0; b < 2; b++) S[cb][b] -= delta;
             }
         }
     };
     auto pm_exp = [&](const f4 (&S)[NCB][2], h8 (&pf)[NCB], h8 (&pfl)[NCB]) {
 #pragma unroll
         for (int cb = 0; cb < NCB; cb++) {
-            const float m_use = m_run[cb] == GI_NEG_INF ? 0.f : m_run[cb];
             float psum = 0.f;
 #pragma unroll
             for (int i = 0; i < 8; i++) {
-                const float p = __builtin_amdgcn_exp2f(S[cb][i >> 2][i & 3] - m_use);
+                const float p = __builtin_amdgcn_exp2f(S[cb][i >> 2][i & 3]);
                 psum += p;
                 const _Float16 hi = (_Float16)p;
                 pf[cb][i] = hi;
