@@ -842,9 +842,11 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
             for (int i = 0; i < 8; i++) {
                 const float p = __builtin_amdgcn_exp2f(S[cb][i >> 2][i & 3]);
                 psum += p;
-                const _Float16 hi = (_Float16)p;
-                pf[cb][i] = hi;
-                pfl[cb][i] = (_Float16)(p - (float)hi);
+                // the high part: p cut to f16's 11 significant bits, so that it converts exactly and the
+                // remainder is an exact f32 subtraction (no conversion back)
+                const float hi = __uint_as_float(__float_as_uint(p) & 0xffffe000u);
+                pf[cb][i] = (_Float16)hi;
+                pfl[cb][i] = (_Float16)(p - hi);
             }
             l_run[cb] += psum;
         }
