@@ -641,31 +641,85 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
         __builtin_amdgcn_sched_barrier(0);
         if (reload) load_v(B, t + NB * STRIDE);
     };
+    // K fragment of k-step kk of a head-size-256 tile (int8: the lane's 8 bytes of dims 64(kk/2) + 16grp +
+    // 8(kk%2), widened; 4-bit: its values 64grp + 8kk .. + 7, widened with their scale)
+    auto kfrag256 = [&](auto& B, int kk) -> h8 {
+        if constexpr (Q4) {
+            // values 64grp + 8kk .. + 7: bytes 4kk .. 4kk + 3 of the lane's 32, scale group 2grp + kk/4
+            const uint32_t x = B.k[kk >> 2][kk & 3];
+            const h2x sc = __builtin_bit_cast(h2x, (kk >> 2) ? (B.ksc >> 16) * 0x10001u : (B.ksc & 0xffffu) * 0x10001u);
+            const uint32_t hi = x >> 4;
+            return __builtin_bit_cast(h8, u4{q4_f16x2(hi, x, 0, sc), q4_f16x2(hi, x, 1, sc), q4_f16x2(hi, x, 2, sc),
+                                             q4_f16x2(hi, x, 3, sc)});
+        } else if constexpr (I8) {
+            const uint32_t x0 = gi_i8_in(B.k[kk >> 1][2 * (kk & 1)]), x1 = gi_i8_in(B.k[kk >> 1][2 * (kk & 1) + 1]);
+            return __builtin_bit_cast(h8, u4{i8_f16x2(x0, GI_I8_LO), i8_f16x2(x0, GI_I8_HI), i8_f16x2(x1, GI_I8_LO),
+                                             i8_f16x2(x1, GI_I8_HI)});
+        } else {
+            return __builtin_bit_cast(h8, B.k[kk]);
+        }
+    };
+    // O^T += V^T P^T over a head-size-256 tile (P^T: the high parts pf and, with one pair per column, the
+    // remainders pfl)
+    auto pv256 = [&](auto& B, const h4x (&pf)[NCB], const h4x (&pfl)[NCB]) {
+        // V^T block dd: element i of the A operand = V[key 4grp + i][dim 16c + dd]. int8: for dims dd, dd + 1
+        // and keys 2p, 2p + 1 one v_perm gathers the four bytes and two converts widen them to f16 pairs
+        u2 v8[16];
+        if constexpr (I8) {
+#pragma unroll
+            for (int dd = 0; dd < 16; dd += 2) {
+                const int wi = dd >> 2, k = dd & 3;
+                const uint32_t sel = (uint32_t)k | (uint32_t)(k + 4) << 8 | (uint32_t)(k + 1) << 16 | (uint32_t)(k + 5) << 24;
+#pragma unroll
+                for (int p = 0; p < 2; p++) {
+                    const uint32_t g = __builtin_amdgcn_perm(gi_i8_in(B.v[2 * p + 1][wi]), gi_i8_in(B.v[2 * p][wi]), sel);
+                    v8[dd][p] = i8_f16x2(g, GI_I8_LO);
+                    v8[dd + 1][p] = i8_f16x2(g, GI_I8_HI);
+                }
+            }
+        }
+        // 4-bit: for keys 2p, 2p + 1 the pair (key 2p, key 2p + 1) of dim 16c + dd is nibble dd%2 of byte dd/2 of
+        // each row, each times its own key's scale
+        h2x vsp[2];
+        if constexpr (Q4) {
+#pragma unroll
+            for (int p = 0; p < 2; p++)
+                vsp[p] = __builtin_bit_cast(h2x, (B.vsc[2 * p] & 0xffffu) | (B.vsc[2 * p + 1] << 16));
+        }
+#pragma unroll
+        for (int dd = 0; dd < 16; dd++) {
+            u2 vw;
+            if constexpr (Q4) {
+                const int w = dd >> 3, j = (dd >> 1) & 3;
+#pragma unroll
+                for (int p = 0; p < 2; p++) {
+                    const uint32_t xa = B.v[2 * p][w], xb = B.v[2 * p + 1][w];
+                    vw[p] = (dd & 1) ? q4_f16x2(xb >> 4, xa >> 4, j, vsp[p]) : q4_f16x2(xb, xa, j, vsp[p]);
+                }
+            } else if constexpr (I8) {
+                vw = v8[dd];
+            } else {
+                const int h = dd >> 3, w = (dd & 7) >> 1;
+#pragma unroll
+                for (int p = 0; p < 2; p++)
+                    vw[p] = __builtin_amdgcn_perm(B.v[2 * p + 1][h][w], B.v[2 * p][h][w], (dd & 1) ? 0x07060302u : 0x05040100u);
+            }
+            const h4x vt = __builtin_bit_cast(h4x, vw);
+#pragma unroll
+            for (int cb = 0; cb < NCB; cb++) {
+                o[cb][dd] = __builtin_amdgcn_mfma_f32_16x16x16f16(vt, pf[cb], o[cb][dd], 0, 0, 0);
+                if constexpr (PM) o[cb][dd] = __builtin_amdgcn_mfma_f32_16x16x16f16(vt, pfl[cb], o[cb][dd], 0, 0, 0);
+            }
+        }
+    };
     auto process_256 = [&](auto& B, int t, bool reload) {
         __builtin_amdgcn_sched_barrier(0);
-        // K fragment of k-step kk (int8: the lane's 8 bytes of dims 64(kk/2) + 16grp + 8(kk%2), widened)
-        auto kfrag = [&](int kk) -> h8 {
-            if constexpr (Q4) {
-                // values 64grp + 8kk .. + 7: bytes 4kk .. 4kk + 3 of the lane's 32, scale group 2grp + kk/4
-                const uint32_t x = B.k[kk >> 2][kk & 3];
-                const h2x sc = __builtin_bit_cast(h2x, (kk >> 2) ? (B.ksc >> 16) * 0x10001u : (B.ksc & 0xffffu) * 0x10001u);
-                const uint32_t hi = x >> 4;
-                return __builtin_bit_cast(h8, u4{q4_f16x2(hi, x, 0, sc), q4_f16x2(hi, x, 1, sc), q4_f16x2(hi, x, 2, sc),
-                                                 q4_f16x2(hi, x, 3, sc)});
-            } else if constexpr (I8) {
-                const uint32_t x0 = gi_i8_in(B.k[kk >> 1][2 * (kk & 1)]), x1 = gi_i8_in(B.k[kk >> 1][2 * (kk & 1) + 1]);
-                return __builtin_bit_cast(h8, u4{i8_f16x2(x0, GI_I8_LO), i8_f16x2(x0, GI_I8_HI), i8_f16x2(x1, GI_I8_LO),
-                                                 i8_f16x2(x1, GI_I8_HI)});
-            } else {
-                return __builtin_bit_cast(h8, B.k[kk]);
-            }
-        };
         f4 sacc[NCB];
 #pragma unroll
         for (int cb = 0; cb < NCB; cb++) sacc[cb] = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int kk = 0; kk < 8; kk++) {
-            const h8 kf = kfrag(kk);
+            const h8 kf = kfrag256(B, kk);
 #pragma unroll
             for (int cb = 0; cb < NCB; cb++) {
                 sacc[cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[cb][kk], sacc[cb], 0, 0, 0);
@@ -727,94 +781,57 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
             }
             l_run[cb] += psum;
         }
-        // V^T block dd: element i of the A operand = V[key 4grp + i][dim 16c + dd]. int8: for dims dd, dd + 1
-        // and keys 2p, 2p + 1 one v_perm gathers the four bytes and two converts widen them to f16 pairs
-        u2 v8[16];
-        if constexpr (I8) {
-#pragma unroll
-            for (int dd = 0; dd < 16; dd += 2) {
-                const int wi = dd >> 2, k = dd & 3;
-                const uint32_t sel = (uint32_t)k | (uint32_t)(k + 4) << 8 | (uint32_t)(k + 1) << 16 | (uint32_t)(k + 5) << 24;
-#pragma unroll
-                for (int p = 0; p < 2; p++) {
-                    const uint32_t g = __builtin_amdgcn_perm(gi_i8_in(B.v[2 * p + 1][wi]), gi_i8_in(B.v[2 * p][wi]), sel);
-                    v8[dd][p] = i8_f16x2(g, GI_I8_LO);
-                    v8[dd + 1][p] = i8_f16x2(g, GI_I8_HI);
-                }
-            }
-        }
-        // 4-bit: for keys 2p, 2p + 1 the pair (key 2p, key 2p + 1) of dim 16c + dd is nibble dd%2 of byte dd/2 of
-        // each row, each times its own key's scale
-        h2x vsp[2];
-        if constexpr (Q4) {
-#pragma unroll
-            for (int p = 0; p < 2; p++)
-                vsp[p] = __builtin_bit_cast(h2x, (B.vsc[2 * p] & 0xffffu) | (B.vsc[2 * p + 1] << 16));
-        }
-#pragma unroll
-        for (int dd = 0; dd < 16; dd++) {
-            u2 vw;
-            if constexpr (Q4) {
-                const int w = dd >> 3, j = (dd >> 1) & 3;
-#pragma unroll
-                for (int p = 0; p < 2; p++) {
-                    const uint32_t xa = B.v[2 * p][w], xb = B.v[2 * p + 1][w];
-                    vw[p] = (dd & 1) ? q4_f16x2(xb >> 4, xa >> 4, j, vsp[p]) : q4_f16x2(xb, xa, j, vsp[p]);
-                }
-            } else if constexpr (I8) {
-                vw = v8[dd];
-            } else {
-                const int h = dd >> 3, w = (dd & 7) >> 1;
-#pragma unroll
-                for (int p = 0; p < 2; p++)
-                    vw[p] = __builtin_amdgcn_perm(B.v[2 * p + 1][h][w], B.v[2 * p][h][w], (dd & 1) ? 0x07060302u : 0x05040100u);
-            }
-            const h4x vt = __builtin_bit_cast(h4x, vw);
-#pragma unroll
-            for (int cb = 0; cb < NCB; cb++) {
-                o[cb][dd] = __builtin_amdgcn_mfma_f32_16x16x16f16(vt, pf[cb], o[cb][dd], 0, 0, 0);
-                if constexpr (PM) o[cb][dd] = __builtin_amdgcn_mfma_f32_16x16x16f16(vt, pfl[cb], o[cb][dd], 0, 0, 0);
-            }
-        }
+        pv256(B, pf, pfl);
         __builtin_amdgcn_sched_barrier(0);
         if (reload) load_v(B, t + NB * STRIDE);
     };
-    // ---- software pipeline of the one-pair-per-column f16 kernels (head size 128): a tile's QK runs one step
-    // ahead, so the MFMAs of tile t+1's QK interleave with tile t's exp and packing, and tile t's PV MFMAs with
-    // tile t+1's row max. Unmasked tiles only; the rest take process_h. Scores come out of the MFMA relative to
-    // the column's reference max (each chain starts from C = -max), so the exp takes them as they are; a tile
-    // that moves the reference shifts its own scores by the change.
-    auto pm_qk = [&](auto& B, f4 (&S)[NCB][2]) {
+    // ---- software pipeline of the one-pair-per-column kernels over the f16 and 4-bit caches: a tile's QK runs one
+    // step ahead, so the MFMAs of tile t+1's QK interleave with tile t's exp and packing, and tile t's PV MFMAs
+    // with tile t+1's row max. Unmasked tiles only; the rest take process_h / process_256. Scores come out of the
+    // MFMA relative to the column's reference max (each chain starts from C = -max), so the exp takes them as
+    // they are; a tile that moves the reference shifts its own scores by the change.
+    constexpr int PB = HD == 256 ? 1 : 2;                        // S^T blocks of 16 keys per column block
+    typedef typename gi_pick<HD == 256, h4x, h8>::type PT;     // PV B operand: the tile's keys of one column
+    struct PipeS { f4 v[NCB][PB]; };
+    struct PipeP { PT hi[NCB], lo[NCB]; };
+    auto pm_qk = [&](auto& B, PipeS& S) {
 #pragma unroll
         for (int cb = 0; cb < NCB; cb++) {
             const float mu = m_run[cb] == GI_NEG_INF ? 0.f : m_run[cb];
 #pragma unroll
-            for (int b = 0; b < 2; b++) {
-                S[cb][b] = f4{-mu, -mu, -mu, -mu};
+            for (int b = 0; b < PB; b++) {
+                f4 acc = f4{-mu, -mu, -mu, -mu};
 #pragma unroll
-                for (int kk = 0; kk < 4; kk++) {
-                    S[cb][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, B.k[b][kk]), qf[cb][kk],
-                                                                      S[cb][b], 0, 0, 0);
-                    S[cb][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, B.k[b][kk]), qfl[cb][kk],
-                                                                      S[cb][b], 0, 0, 0);
+                for (int kk = 0; kk < KK; kk++) {
+                    h8 kf;
+                    if constexpr (HD == 256) kf = kfrag256(B, kk);
+                    else kf = __builtin_bit_cast(h8, B.k[b][kk]);
+                    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[cb][kk], acc, 0, 0, 0);
+                    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qfl[cb][kk], acc, 0, 0, 0);
                 }
                 // (in VGPRs once, for the max and then the exp, instead of two reads of an accumulator register)
-                asm volatile("" : "+v"(S[cb][b]));
+                asm volatile("" : "+v"(acc));
+                S.v[cb][b] = acc;
             }
         }
     };
     // the tile's row max per column, and the lazy rescale of O when the reference moves (by more than 2^8; the
     // first tile sets it), which also shifts the tile's scores onto the new reference
-    auto pm_max = [&](f4 (&S)[NCB][2]) {
+    auto pm_max = [&](PipeS& S) {
         float mx[NCB];
         bool up[NCB];
         bool any = false;
 #pragma unroll
         for (int cb = 0; cb < NCB; cb++) {
-            float m = fmaxf(fmaxf(S[cb][0][0], S[cb][0][1]), S[cb][0][2]);
-            m = fmaxf(fmaxf(m, S[cb][0][3]), S[cb][1][0]);
-            m = fmaxf(fmaxf(m, S[cb][1][1]), S[cb][1][2]);
-            mx[cb] = rows_max(fmaxf(m, S[cb][1][3]));
+            float m = fmaxf(fmaxf(S.v[cb][0][0], S.v[cb][0][1]), S.v[cb][0][2]);
+            if constexpr (PB == 2) {
+                m = fmaxf(fmaxf(m, S.v[cb][0][3]), S.v[cb][1][0]);
+                m = fmaxf(fmaxf(m, S.v[cb][1][1]), S.v[cb][1][2]);
+                m = fmaxf(m, S.v[cb][1][3]);
+            } else {
+                m = fmaxf(m, S.v[cb][0][3]);
+            }
+            mx[cb] = rows_max(m);
             up[cb] = m_run[cb] == GI_NEG_INF || mx[cb] > DEC_RESCALE_LOG2;
             any = any || up[cb];
         }
@@ -828,41 +845,46 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
                 m_run[cb] = m_new;
                 l_run[cb] *= alpha;
 #pragma unroll
-                for (int dd = 0; dd < 8; dd++) o[cb][dd] *= alpha;
+                for (int dd = 0; dd < ND; dd++) o[cb][dd] *= alpha;
 #pragma unroll
-                for (int b = 0; b < 2; b++) S[cb][b] -= delta;
+                for (int b = 0; b < PB; b++) S.v[cb][b] -= delta;
             }
         }
     };
-    auto pm_exp = [&](const f4 (&S)[NCB][2], h8 (&pf)[NCB], h8 (&pfl)[NCB]) {
+    auto pm_exp = [&](const PipeS& S, PipeP& P) {
 #pragma unroll
         for (int cb = 0; cb < NCB; cb++) {
             float psum = 0.f;
 #pragma unroll
-            for (int i = 0; i < 8; i++) {
-                const float p = __builtin_amdgcn_exp2f(S[cb][i >> 2][i & 3]);
+            for (int i = 0; i < 4 * PB; i++) {
+                const float p = __builtin_amdgcn_exp2f(S.v[cb][i >> 2][i & 3]);
                 psum += p;
                 // the high part: p cut to f16's 11 significant bits, so that it converts exactly and the
                 // remainder is an exact f32 subtraction (no conversion back)
                 const float hi = __uint_as_float(__float_as_uint(p) & 0xffffe000u);
-                pf[cb][i] = (_Float16)hi;
-                pfl[cb][i] = (_Float16)(p - hi);
+                P.hi[cb][i] = (_Float16)hi;
+                P.lo[cb][i] = (_Float16)(p - hi);
             }
             l_run[cb] += psum;
         }
     };
-    auto pm_pv = [&](auto& B, const h8 (&pf)[NCB], const h8 (&pfl)[NCB]) {
+    auto pm_pv = [&](auto& B, const PipeP& P) {
+        if constexpr (HD == 256) {
+            pv256(B, P.hi, P.lo);
+        } else {
 #pragma unroll
-        for (int dd = 0; dd < 8; dd++) {
-            u4 w;
+            for (int dd = 0; dd < 8; dd++) {
+                u4 w;
 #pragma unroll
-            for (int p = 0; p < 4; p++)
-                w[p] = __builtin_amdgcn_perm(B.v[2 * p + 1][dd >> 1], B.v[2 * p][dd >> 1], (dd & 1) ? 0x07060302u : 0x05040100u);
-            const h8 vt = __builtin_bit_cast(h8, w);
+                for (int p = 0; p < 4; p++)
+                    w[p] = __builtin_amdgcn_perm(B.v[2 * p + 1][dd >> 1], B.v[2 * p][dd >> 1],
+                                                 (dd & 1) ? 0x07060302u : 0x05040100u);
+                const h8 vt = __builtin_bit_cast(h8, w);
 #pragma unroll
-            for (int cb = 0; cb < NCB; cb++) {
-                o[cb][dd] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vt, pf[cb], o[cb][dd], 0, 0, 0);
-                o[cb][dd] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vt, pfl[cb], o[cb][dd], 0, 0, 0);
+                for (int cb = 0; cb < NCB; cb++) {
+                    o[cb][dd] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vt, P.hi[cb], o[cb][dd], 0, 0, 0);
+                    o[cb][dd] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vt, P.lo[cb], o[cb][dd], 0, 0, 0);
+                }
             }
         }
     };
@@ -907,42 +929,39 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
     // Steady state: every buffer gets a further tile (those past the slice read zeros and are never
     // processed). The last round of tiles runs without reloads, so no load is left in flight at the end.
     int t = t_first;
-    if constexpr (DEC_PIPE && PM && !I8 && !Q4 && HD == 128) {
-        static_assert(NB == 2, "the pipeline alternates two register buffers");
-        // State at the top of each step: tile t in B[0] with its scores S0 (row max taken, O rescaled), its K
-        // buffer already refilled with tile t + 2 STRIDE; tile t + STRIDE in B[1]. A step finishes tiles t and
-        // t + STRIDE and scores tile t + 2 STRIDE, so it runs while that tile needs no mask.
-        if (t + 2 * STRIDE + DEC_TILE <= span_lo) {
-            f4 S0[NCB][2], S1[NCB][2];
-            h8 pf[NCB], pfl[NCB];
-            pm_qk(B[0], S0);
-            load_k(B[0], t + 2 * STRIDE);
-            pm_max(S0);
+    if constexpr (DEC_PIPE && PM && !I8) {
+        // State at the top of each step: tile t in B[0] with its scores (row max taken, O rescaled), its K buffer
+        // already refilled with tile t + NB STRIDE; tiles t + i STRIDE in B[i]. A step finishes tiles t ..
+        // t + (NB-1) STRIDE and scores tile t + NB STRIDE, so it runs while that tile needs no mask.
+        if (t + NB * STRIDE + TILE <= span_lo) {
+            PipeS S[2];
+            PipeP P;
+            pm_qk(B[0], S[0]);
+            load_k(B[0], t + NB * STRIDE);
+            pm_max(S[0]);
             do {
-                __builtin_amdgcn_sched_barrier(0);
-                pm_qk(B[1], S1);
-                pm_exp(S0, pf, pfl);
-                load_k(B[1], t + 3 * STRIDE);
-                pm_pv(B[0], pf, pfl);
-                pm_max(S1);
-                load_v(B[0], t + 2 * STRIDE);
-                __builtin_amdgcn_sched_barrier(0);
-                pm_qk(B[0], S0);
-                pm_exp(S1, pf, pfl);
-                load_k(B[0], t + 4 * STRIDE);
-                pm_pv(B[1], pf, pfl);
-                pm_max(S0);
-                load_v(B[1], t + 3 * STRIDE);
-                t += 2 * STRIDE;
-            } while (t + 2 * STRIDE + DEC_TILE <= span_lo);
+#pragma unroll
+                for (int i = 0; i < NB; i++) {
+                    __builtin_amdgcn_sched_barrier(0);
+                    pm_qk(B[(i + 1) % NB], S[(i + 1) & 1]);
+                    pm_exp(S[i & 1], P);
+                    load_k(B[(i + 1) % NB], t + (i + 1 + NB) * STRIDE);
+                    pm_pv(B[i], P);
+                    pm_max(S[(i + 1) & 1]);
+                    load_v(B[i], t + (i + NB) * STRIDE);
+                }
+                t += NB * STRIDE;
+            } while (t + NB * STRIDE + TILE <= span_lo);
             __builtin_amdgcn_sched_barrier(0);
-            // finish tile t; B[0] then holds tile t + 2 STRIDE and B[1] tile t + STRIDE, which process_h takes,
-            // so the steps below start from t + 2 STRIDE with the buffers in order
-            pm_exp(S0, pf, pfl);
-            pm_pv(B[0], pf, pfl);
-            load_v(B[0], t + 2 * STRIDE);
-            if (t + STRIDE < nkeys) process(B[1], t + STRIDE, true);
-            t += 2 * STRIDE;
+            // finish tile t; B[0] then holds tile t + NB STRIDE and B[i] tile t + i STRIDE, which the per-tile path
+            // takes, so the steps below start from t + NB STRIDE with the buffers in order
+            pm_exp(S[0], P);
+            pm_pv(B[0], P);
+            load_v(B[0], t + NB * STRIDE);
+#pragma unroll
+            for (int i = 1; i < NB; i++)
+                if (t + i * STRIDE < nkeys) process(B[i], t + i * STRIDE, true);
+            t += NB * STRIDE;
         }
     }
     for (; t + NB * STRIDE < nkeys; t += NB * STRIDE) {
