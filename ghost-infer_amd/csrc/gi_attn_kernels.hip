@@ -524,9 +524,8 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
         __builtin_amdgcn_sched_barrier(0);
         if (reload) load_v(B, t + NB * STRIDE);
     };
-    auto process_i8 = [&](auto& B, int t, bool reload) {
-        __builtin_amdgcn_sched_barrier(0);
-        f4 sacc[NCB][4];
+    // the int8 cache's QK over one 64-key tile: the keys widened to exact f16, sacc from zero
+    auto qk_i8 = [&](auto& B, f4 (&sacc)[NCB][4]) {
 #pragma unroll
         for (int b = 0; b < 4; b++) {
             u4 kf[4]; // k-step kk: dims 16grp + 8(kk%2) + 64(kk/2) of this block's key, as f16 pairs
@@ -551,6 +550,43 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
                 }
             }
         }
+    };
+    // the int8 cache's P V over one 64-key tile (pf, and with one pair per column pfl: P^T by k-step)
+    auto pv_i8 = [&](auto& B, const h8 (&pf)[NCB][2], const h8 (&pfl)[NCB][2]) {
+        // O^T += V^T P^T: for dims dd, dd+1 (bytes k, k+1 of word dd/4) and keys 2p, 2p+1 of a k-step, one
+        // v_perm gathers the four bytes and two more widen them to the two f16 pairs
+#pragma unroll
+        for (int i = 0; i < 16; i++) B.v[i] = u2{gi_i8_in(B.v[i][0]), gi_i8_in(B.v[i][1])};
+#pragma unroll
+        for (int dd = 0; dd < 8; dd += 2) {
+            const int wi = dd >> 2, k = dd & 3;
+            const uint32_t sel = (uint32_t)k | (uint32_t)(k + 4) << 8 | (uint32_t)(k + 1) << 16 | (uint32_t)(k + 5) << 24;
+#pragma unroll
+            for (int ks = 0; ks < 2; ks++) {
+                u4 w0, w1;
+#pragma unroll
+                for (int p = 0; p < 4; p++) {
+                    const uint32_t g = __builtin_amdgcn_perm(B.v[8 * ks + 2 * p + 1][wi], B.v[8 * ks + 2 * p][wi], sel);
+                    w0[p] = i8_f16x2(g, GI_I8_LO);
+                    w1[p] = i8_f16x2(g, GI_I8_HI);
+                }
+#pragma unroll
+                for (int cb = 0; cb < NCB; cb++) {
+                    o[cb][dd] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, w0), pf[cb][ks], o[cb][dd], 0, 0, 0);
+                    o[cb][dd + 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, w1), pf[cb][ks], o[cb][dd + 1], 0, 0, 0);
+                    if constexpr (PM) {
+                        o[cb][dd] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, w0), pfl[cb][ks], o[cb][dd], 0, 0, 0);
+                        o[cb][dd + 1] =
+                            __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, w1), pfl[cb][ks], o[cb][dd + 1], 0, 0, 0);
+                    }
+                }
+            }
+        }
+    };
+    auto process_i8 = [&](auto& B, int t, bool reload) {
+        __builtin_amdgcn_sched_barrier(0);
+        f4 sacc[NCB][4];
+        qk_i8(B, sacc);
         const float ksc = B.ksc;
         if (reload) load_k(B, t + NB * STRIDE);
         __builtin_amdgcn_sched_barrier(0);
@@ -609,35 +645,7 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
             }
             l_run[cb] += psum;
         }
-        // O^T += V^T P^T: for dims dd, dd+1 (bytes k, k+1 of word dd/4) and keys 2p, 2p+1 of a k-step, one
-        // v_perm gathers the four bytes and two more widen them to the two f16 pairs
-#pragma unroll
-        for (int i = 0; i < 16; i++) B.v[i] = u2{gi_i8_in(B.v[i][0]), gi_i8_in(B.v[i][1])};
-#pragma unroll
-        for (int dd = 0; dd < 8; dd += 2) {
-            const int wi = dd >> 2, k = dd & 3;
-            const uint32_t sel = (uint32_t)k | (uint32_t)(k + 4) << 8 | (uint32_t)(k + 1) << 16 | (uint32_t)(k + 5) << 24;
-#pragma unroll
-            for (int ks = 0; ks < 2; ks++) {
-                u4 w0, w1;
-#pragma unroll
-                for (int p = 0; p < 4; p++) {
-                    const uint32_t g = __builtin_amdgcn_perm(B.v[8 * ks + 2 * p + 1][wi], B.v[8 * ks + 2 * p][wi], sel);
-                    w0[p] = i8_f16x2(g, GI_I8_LO);
-                    w1[p] = i8_f16x2(g, GI_I8_HI);
-                }
-#pragma unroll
-                for (int cb = 0; cb < NCB; cb++) {
-                    o[cb][dd] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, w0), pf[cb][ks], o[cb][dd], 0, 0, 0);
-                    o[cb][dd + 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, w1), pf[cb][ks], o[cb][dd + 1], 0, 0, 0);
-                    if constexpr (PM) {
-                        o[cb][dd] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, w0), pfl[cb][ks], o[cb][dd], 0, 0, 0);
-                        o[cb][dd + 1] =
-                            __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, w1), pfl[cb][ks], o[cb][dd + 1], 0, 0, 0);
-                    }
-                }
-            }
-        }
+        pv_i8(B, pf, pfl);
         __builtin_amdgcn_sched_barrier(0);
         if (reload) load_v(B, t + NB * STRIDE);
     };
@@ -790,11 +798,27 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
     // with tile t+1's row max. Unmasked tiles only; the rest take process_h / process_256. Scores come out of the
     // MFMA relative to the column's reference max (each chain starts from C = -max), so the exp takes them as
     // they are; a tile that moves the reference shifts its own scores by the change.
-    constexpr int PB = HD == 256 ? 1 : 2;                        // S^T blocks of 16 keys per column block
-    typedef typename gi_pick<HD == 256, h4x, h8>::type PT;     // PV B operand: the tile's keys of one column
-    struct PipeS { f4 v[NCB][PB]; };
-    struct PipeP { PT hi[NCB], lo[NCB]; };
+    // int8 (head size 128): the key scales multiply the MFMA's dot products, so the scores are made relative
+    // (s * kscale - max) in one FMA each before the row max, and P V takes p times the value scale.
+    constexpr int PB = HD == 256 ? 1 : I8 ? 4 : 2;              // S^T blocks of 16 keys per column block
+    typedef typename gi_pick<HD == 256, h4x, h8>::type PT;     // PV B operand: 16 or 32 keys of one column
+    typedef typename gi_pick<I8 && HD == 128, PT[2], PT>::type PE; // a column's P^T for the tile (int8: 2 k-steps)
+    struct PipeS { f4 v[NCB][PB]; float ksc; };
+    struct PipeP { PE hi[NCB], lo[NCB]; };
     auto pm_qk = [&](auto& B, PipeS& S) {
+        if constexpr (I8) {
+            f4 sacc[NCB][4];
+            qk_i8(B, sacc);
+#pragma unroll
+            for (int cb = 0; cb < NCB; cb++)
+#pragma unroll
+                for (int b = 0; b < PB; b++) {
+                    asm volatile("" : "+v"(sacc[cb][b]));
+                    S.v[cb][b] = sacc[cb][b];
+                }
+            S.ksc = B.ksc; // (the K buffer is refilled before this tile's max)
+            return;
+        }
 #pragma unroll
         for (int cb = 0; cb < NCB; cb++) {
             const float mu = m_run[cb] == GI_NEG_INF ? 0.f : m_run[cb];
@@ -821,16 +845,28 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
         float mx[NCB];
         bool up[NCB];
         bool any = false;
+        if constexpr (I8) {
+            // the scales of this lane's 16 keys (16grp + m, m = 4b + j), and the scores relative to the reference
+            float ksb[16];
+#define GI_BC(m) ksb[m] = row_bcast<m>(S.ksc);
+            GI_BC(0) GI_BC(1) GI_BC(2) GI_BC(3) GI_BC(4) GI_BC(5) GI_BC(6) GI_BC(7)
+            GI_BC(8) GI_BC(9) GI_BC(10) GI_BC(11) GI_BC(12) GI_BC(13) GI_BC(14) GI_BC(15)
+#undef GI_BC
+#pragma unroll
+            for (int cb = 0; cb < NCB; cb++) {
+                const float mu = m_run[cb] == GI_NEG_INF ? 0.f : m_run[cb];
+#pragma unroll
+                for (int m = 0; m < 16; m++) S.v[cb][m >> 2][m & 3] = fmaf(S.v[cb][m >> 2][m & 3], ksb[m], -mu);
+            }
+        }
 #pragma unroll
         for (int cb = 0; cb < NCB; cb++) {
+            // a chain of three-input maxima over the column's 4 PB scores
             float m = fmaxf(fmaxf(S.v[cb][0][0], S.v[cb][0][1]), S.v[cb][0][2]);
-            if constexpr (PB == 2) {
-                m = fmaxf(fmaxf(m, S.v[cb][0][3]), S.v[cb][1][0]);
-                m = fmaxf(fmaxf(m, S.v[cb][1][1]), S.v[cb][1][2]);
-                m = fmaxf(m, S.v[cb][1][3]);
-            } else {
-                m = fmaxf(m, S.v[cb][0][3]);
-            }
+#pragma unroll
+            for (int k = 3; k + 1 < 4 * PB; k += 2)
+                m = fmaxf(fmaxf(m, S.v[cb][k >> 2][k & 3]), S.v[cb][(k + 1) >> 2][(k + 1) & 3]);
+            if constexpr ((4 * PB - 3) % 2 == 1) m = fmaxf(m, S.v[cb][PB - 1][3]);
             mx[cb] = rows_max(m);
             up[cb] = m_run[cb] == GI_NEG_INF || mx[cb] > DEC_RESCALE_LOG2;
             any = any || up[cb];
@@ -851,7 +887,14 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
             }
         }
     };
-    auto pm_exp = [&](const PipeS& S, PipeP& P) {
+    auto pm_exp = [&](auto& B, const PipeS& S, PipeP& P) {
+        float vsb[16]; // int8: the value scales of this lane's 16 keys
+        if constexpr (I8) {
+#define GI_BC(m) vsb[m] = row_bcast<m>(B.vsc);
+            GI_BC(0) GI_BC(1) GI_BC(2) GI_BC(3) GI_BC(4) GI_BC(5) GI_BC(6) GI_BC(7)
+            GI_BC(8) GI_BC(9) GI_BC(10) GI_BC(11) GI_BC(12) GI_BC(13) GI_BC(14) GI_BC(15)
+#undef GI_BC
+        }
 #pragma unroll
         for (int cb = 0; cb < NCB; cb++) {
             float psum = 0.f;
@@ -859,11 +902,18 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
             for (int i = 0; i < 4 * PB; i++) {
                 const float p = __builtin_amdgcn_exp2f(S.v[cb][i >> 2][i & 3]);
                 psum += p;
-                // the high part: p cut to f16's 11 significant bits, so that it converts exactly and the
+                // int8: P V takes p times the value's scale (biased like process_i8)
+                const float pv = I8 ? p * vsb[i] * DEC_I8_VB : p;
+                // the high part: pv cut to f16's 11 significant bits, so that it converts exactly and the
                 // remainder is an exact f32 subtraction (no conversion back)
-                const float hi = __uint_as_float(__float_as_uint(p) & 0xffffe000u);
-                P.hi[cb][i] = (_Float16)hi;
-                P.lo[cb][i] = (_Float16)(p - hi);
+                const float hi = __uint_as_float(__float_as_uint(pv) & 0xffffe000u);
+                if constexpr (I8 && HD == 128) {
+                    P.hi[cb][i >> 3][i & 7] = (_Float16)hi;
+                    P.lo[cb][i >> 3][i & 7] = (_Float16)(pv - hi);
+                } else {
+                    P.hi[cb][i] = (_Float16)hi;
+                    P.lo[cb][i] = (_Float16)(pv - hi);
+                }
             }
             l_run[cb] += psum;
         }
@@ -871,6 +921,8 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
     auto pm_pv = [&](auto& B, const PipeP& P) {
         if constexpr (HD == 256) {
             pv256(B, P.hi, P.lo);
+        } else if constexpr (I8) {
+            pv_i8(B, P.hi, P.lo);
         } else {
 #pragma unroll
             for (int dd = 0; dd < 8; dd++) {
@@ -929,7 +981,7 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
     // Steady state: every buffer gets a further tile (those past the slice read zeros and are never
     // processed). The last round of tiles runs without reloads, so no load is left in flight at the end.
     int t = t_first;
-    if constexpr (DEC_PIPE && PM && !I8) {
+    if constexpr (DEC_PIPE && PM && (!I8 || HD == 128)) {
         // State at the top of each step: tile t in B[0] with its scores (row max taken, O rescaled), its K buffer
         // already refilled with tile t + NB STRIDE; tiles t + i STRIDE in B[i]. A step finishes tiles t ..
         // t + (NB-1) STRIDE and scores tile t + NB STRIDE, so it runs while that tile needs no mask.
@@ -944,7 +996,7 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
                 for (int i = 0; i < NB; i++) {
                     __builtin_amdgcn_sched_barrier(0);
                     pm_qk(B[(i + 1) % NB], S[(i + 1) & 1]);
-                    pm_exp(S[i & 1], P);
+                    pm_exp(B[i], S[i & 1], P);
                     load_k(B[(i + 1) % NB], t + (i + 1 + NB) * STRIDE);
                     pm_pv(B[i], P);
                     pm_max(S[(i + 1) & 1]);
@@ -955,7 +1007,7 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
             __builtin_amdgcn_sched_barrier(0);
             // finish tile t; B[0] then holds tile t + NB STRIDE and B[i] tile t + i STRIDE, which the per-tile path
             // takes, so the steps below start from t + NB STRIDE with the buffers in order
-            pm_exp(S[0], P);
+            pm_exp(B[0], S[0], P);
             pm_pv(B[0], P);
             load_v(B[0], t + NB * STRIDE);
 #pragma unroll
