@@ -806,7 +806,7 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
     struct PipeS { f4 v[NCB][PB]; float ksc; };
     struct PipeP { PE hi[NCB], lo[NCB]; };
     auto pm_qk = [&](auto& B, PipeS& S) {
-        if constexpr (I8) {
+        if constexpr (I8 && HD == 128) {
             f4 sacc[NCB][4];
             qk_i8(B, sacc);
 #pragma unroll
@@ -819,9 +819,11 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
             S.ksc = B.ksc; // (the K buffer is refilled before this tile's max)
             return;
         }
+        if constexpr (I8) S.ksc = B.ksc;
 #pragma unroll
         for (int cb = 0; cb < NCB; cb++) {
-            const float mu = m_run[cb] == GI_NEG_INF ? 0.f : m_run[cb];
+            // int8: the chains start from zero (the key scales come after the dot products)
+            const float mu = I8 || m_run[cb] == GI_NEG_INF ? 0.f : m_run[cb];
 #pragma unroll
             for (int b = 0; b < PB; b++) {
                 f4 acc = f4{-mu, -mu, -mu, -mu};
@@ -846,17 +848,19 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
         bool up[NCB];
         bool any = false;
         if constexpr (I8) {
-            // the scales of this lane's 16 keys (16grp + m, m = 4b + j), and the scores relative to the reference
-            float ksb[16];
+            // the scales of this lane's keys (head size 128: 16grp + m, m = 4b + j; 256: 4grp + m), and the scores
+            // relative to the reference
+            float ksb[4 * PB];
 #define GI_BC(m) ksb[m] = row_bcast<m>(S.ksc);
-            GI_BC(0) GI_BC(1) GI_BC(2) GI_BC(3) GI_BC(4) GI_BC(5) GI_BC(6) GI_BC(7)
-            GI_BC(8) GI_BC(9) GI_BC(10) GI_BC(11) GI_BC(12) GI_BC(13) GI_BC(14) GI_BC(15)
+            GI_BC(0) GI_BC(1) GI_BC(2) GI_BC(3)
+            if constexpr (PB == 4) { GI_BC(4) GI_BC(5) GI_BC(6) GI_BC(7) GI_BC(8) GI_BC(9) GI_BC(10) GI_BC(11)
+                                     GI_BC(12) GI_BC(13) GI_BC(14) GI_BC(15) }
 #undef GI_BC
 #pragma unroll
             for (int cb = 0; cb < NCB; cb++) {
                 const float mu = m_run[cb] == GI_NEG_INF ? 0.f : m_run[cb];
 #pragma unroll
-                for (int m = 0; m < 16; m++) S.v[cb][m >> 2][m & 3] = fmaf(S.v[cb][m >> 2][m & 3], ksb[m], -mu);
+                for (int m = 0; m < 4 * PB; m++) S.v[cb][m >> 2][m & 3] = fmaf(S.v[cb][m >> 2][m & 3], ksb[m], -mu);
             }
         }
 #pragma unroll
@@ -888,11 +892,12 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
         }
     };
     auto pm_exp = [&](auto& B, const PipeS& S, PipeP& P) {
-        float vsb[16]; // int8: the value scales of this lane's 16 keys
+        float vsb[4 * PB]; // int8: the value scales of this lane's keys
         if constexpr (I8) {
 #define GI_BC(m) vsb[m] = row_bcast<m>(B.vsc);
-            GI_BC(0) GI_BC(1) GI_BC(2) GI_BC(3) GI_BC(4) GI_BC(5) GI_BC(6) GI_BC(7)
-            GI_BC(8) GI_BC(9) GI_BC(10) GI_BC(11) GI_BC(12) GI_BC(13) GI_BC(14) GI_BC(15)
+            GI_BC(0) GI_BC(1) GI_BC(2) GI_BC(3)
+            if constexpr (PB == 4) { GI_BC(4) GI_BC(5) GI_BC(6) GI_BC(7) GI_BC(8) GI_BC(9) GI_BC(10) GI_BC(11)
+                                     GI_BC(12) GI_BC(13) GI_BC(14) GI_BC(15) }
 #undef GI_BC
         }
 #pragma unroll
@@ -981,7 +986,7 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
     // Steady state: every buffer gets a further tile (those past the slice read zeros and are never
     // processed). The last round of tiles runs without reloads, so no load is left in flight at the end.
     int t = t_first;
-    if constexpr (DEC_PIPE && PM && (!I8 || HD == 128)) {
+    if constexpr (DEC_PIPE && PM) {
         // State at the top of each step: tile t in B[0] with its scores (row max taken, O rescaled), its K buffer
         // already refilled with tile t + NB STRIDE; tiles t + i STRIDE in B[i]. A step finishes tiles t ..
         // t + (NB-1) STRIDE and scores tile t + NB STRIDE, so it runs while that tile needs no mask.
