@@ -186,6 +186,14 @@ template <> struct DecBuf<true, 256> { u4 k[4]; u4 v[4]; float ksc, vsc; };
 // scale groups 2grp and 2grp + 1, both scales in ksc); V keys 4grp + i, bytes 8c .. 8c + 7 (dims 16c .. 16c + 15,
 // scale group c/2, that scale in vsc[i])
 struct DecBufQ4 { u4 k[2]; u2 v[4]; uint32_t ksc; uint32_t vsc[4]; };
+template <typename T, int N> __device__ __forceinline__ void gi_touch(T (&k)[N]) {
+#pragma unroll
+    for (int i = 0; i < N; i++) asm volatile("" ::"v"(k[i]));
+}
+template <typename T, int N, int M> __device__ __forceinline__ void gi_touch(T (&k)[N][M]) {
+#pragma unroll
+    for (int i = 0; i < N; i++) gi_touch(k[i]);
+}
 template <bool C, typename A, typename B> struct gi_pick { typedef A type; };
 template <typename A, typename B> struct gi_pick<false, A, B> { typedef B type; };
 
@@ -957,8 +965,13 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
     if (pair0 < npairs) {
     Buf B[NB];
     const int t_first = (wave % WS) * TILE;
+    // Only the first tile is requested before the queries are converted; the other buffers are requested once
+    // its keys have arrived. The launch's first requests are then a smaller burst, which the memory system
+    // serves sooner, and the first tile's arithmetic starts earlier (measured faster for every kernel but the
+    // f16 one-pair-per-column ones, whose pipelined loop wants every buffer from the start).
+    constexpr bool DEFER = !PM || I8 || Q4;
 #pragma unroll
-    for (int i = 0; i < NB; i++) {
+    for (int i = 0; i < (DEFER ? 1 : NB); i++) {
         load_k(B[i], t_first + i * STRIDE);
         __builtin_amdgcn_sched_barrier(0);
         load_v(B[i], t_first + i * STRIDE);
@@ -983,6 +996,17 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
                     qf[cb][kk][e] = (c & 1) ? (_Float16)(v - (float)hi) : hi;
                 }
             }
+    if constexpr (DEFER) {
+        gi_touch(B[0].k);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 1; i < NB; i++) {
+            load_k(B[i], t_first + i * STRIDE);
+            __builtin_amdgcn_sched_barrier(0);
+            load_v(B[i], t_first + i * STRIDE);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
     // Steady state: every buffer gets a further tile (those past the slice read zeros and are never
     // processed). The last round of tiles runs without reloads, so no load is left in flight at the end.
     int t = t_first;
