@@ -1743,6 +1743,7 @@ __device__ __forceinline__ void gi_prefill256r(const GiPrefillArgs& a) {
     constexpr int NKB = BK / 16;             // S^T blocks of 16 keys
     constexpr int NDB = HD / 16;             // O^T blocks of 16 dims
     constexpr int TILE = BK * 512;           // bytes of one K or V tile image
+    constexpr int VPF = REG ? 4 : 0;         // V^T fragments read ahead in P V (0: the compiler's order)
     __shared__ __attribute__((aligned(1024))) unsigned char smem[(NKBUF + NVBUF) * TILE];
     __shared__ __attribute__((aligned(16))) float sc_sh[FMT == 1 ? NKBUF + NVBUF : 1][BK]; // int8: tile scales
     auto kbuf = [&](int t) { return smem + (t % NKBUF) * TILE; };
@@ -2002,16 +2003,40 @@ __device__ __forceinline__ void gi_prefill256r(const GiPrefillArgs& a) {
                 l_run = __builtin_amdgcn_fdot2(h2{h0, h1}, h2{(_Float16)1.f, (_Float16)1.f}, l_run, false);
             }
         const unsigned char* V = vbuf(it);
+        if constexpr (VPF > 0) {
+            // register staging: V^T fragments stream through a ring of VPF registers, each read VPF MFMAs
+            // before its use (the f16 kernel measured faster with the compiler's own order)
+            constexpr int NPV = (NKB / 2) * NDB;
+            h8 vq[VPF > 0 ? VPF : 1];
 #pragma unroll
-        for (int kp = 0; kp < NKB / 2; kp++)
+            for (int i = 0; i < VPF; i++) vq[i] = vfrag(V, i % NDB, i / NDB);
 #pragma unroll
-            for (int db = 0; db < NDB; db++)
-                o[db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vfrag(V, db, kp), pf[kp], o[db], 0, 0, 0);
+            for (int i = 0; i < NPV; i++) {
+                const int kp = i / NDB, db = i % NDB;
+                const h8 cur = vq[i % VPF];
+                if (i + VPF < NPV) vq[i % VPF] = vfrag(V, (i + VPF) % NDB, (i + VPF) / NDB);
+                o[db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(cur, pf[kp], o[db], 0, 0, 0);
+            }
+        } else {
+#pragma unroll
+            for (int kp = 0; kp < NKB / 2; kp++)
+#pragma unroll
+                for (int db = 0; db < NDB; db++)
+                    o[db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vfrag(V, db, kp), pf[kp], o[db], 0, 0, 0);
+        }
         mx = rowmax(sn);
 #pragma unroll
         for (int i = 0; i < NKB * KS; i++) {
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
             if (i + PF_KPF < NKB * KS) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
+        if constexpr (VPF > 0) { // then the first V reads, and each P V MFMA followed by its ring refill
+            __builtin_amdgcn_sched_group_barrier(0x100, 2 * VPF, 0);
+#pragma unroll
+            for (int i = 0; i < (NKB / 2) * NDB; i++) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                if (i + VPF < (NKB / 2) * NDB) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+            }
         }
     };
 
