@@ -309,8 +309,9 @@ def peak_probes(torch, dev, reps=5):
     """The box's own peaks, from the probe kernels of ghost-infer_amd/gi_probes_gfx950.hsaco (built beside
     the library): the dense f16 MFMA rate (v_mfma_f32_32x32x16_f16 alone, two waves per SIMD) and an HBM
     read stream (contiguous chunks per workgroup, 16 16-byte streaming loads in flight per lane) over 1 GiB
-    and over config 2's 134 MB (three buffers in turn, past the 256 MB Infinity Cache). Medians over `reps`
-    timings with events on torch's current stream."""
+    and over config 2's 134 MB (three buffers in turn, past the 256 MB Infinity Cache), and the LDS read rate of
+    ds_read_b128 and of the transposing ds_read_b64_tr_b16 at 8 waves per CU (TB/s over all CUs). Medians over
+    `reps` timings with events on torch's current stream."""
     import ctypes
     path = os.path.join(ROOT, "ghost-infer_amd", "gi_probes_gfx950.hsaco")
     if not os.path.exists(path):
@@ -320,7 +321,7 @@ def peak_probes(torch, dev, reps=5):
     if hip.hipModuleLoad(ctypes.byref(mod), path.encode()):
         raise RuntimeError("hipModuleLoad of the probe code object failed")
     fns = {}
-    for name in ("gi_probe_mfma", "gi_probe_read"):
+    for name in ("gi_probe_mfma", "gi_probe_read", "gi_probe_lds"):
         f = ctypes.c_void_p()
         if hip.hipModuleGetFunction(ctypes.byref(f), mod, name.encode()):
             raise RuntimeError(f"probe kernel {name} not found")
@@ -373,6 +374,15 @@ def peak_probes(torch, dev, reps=5):
         res[label] = round(nbytes / timed(one, inner=24) / 1e9, 1)
         del bufs
     res["hbm_copy_GBs_1GiB"] = round(hbm_copy_gbs(torch, dev), 1)
+
+    class LdsArgs(ctypes.Structure):
+        _fields_ = [("iters", ctypes.c_int), ("tr", ctypes.c_int), ("out", ctypes.c_void_p)]
+
+    # LDS operand reads at 8 waves per CU (the prefill kernels' occupancy): 512 workgroups of 4 waves
+    lds_wgs, lds_iters = 512, 2000
+    for label, tr, per_lane in (("lds_read_b128_TBs", 0, 16), ("lds_read_tr16_b64_TBs", 1, 8)):
+        t = timed(lambda: launch(fns["gi_probe_lds"], lds_wgs, LdsArgs(lds_iters, tr, flag.data_ptr())))
+        res[label] = round(lds_wgs * 256 * lds_iters * 16 * per_lane / t / 1e12, 1)
     return res
 
 

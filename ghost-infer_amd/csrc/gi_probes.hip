@@ -4,6 +4,8 @@
 //    chains per wave, two waves per SIMD: the dense f16 MFMA rate at the clock the chip holds under it.
 //  - gi_probe_read: a pure HBM read stream: each workgroup reads one contiguous chunk with 16 16-byte
 //    loads in flight per lane, streaming (nt) cache policy (the decode's access pattern and policy).
+//  - gi_probe_lds: LDS operand reads only, 16 in flight per lane, either ds_read_b128 (the prefill's K
+//    fragments) or the transposing ds_read_b64_tr_b16 (its V^T fragments).
 // Not part of the attention path; built into their own code object, gi_probes_gfx950.hsaco.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -50,4 +52,42 @@ extern "C" __global__ void __launch_bounds__(256) gi_probe_read(const u4* __rest
         for (int u = 0; u < UNR; u++) acc ^= v[u];
     }
     if ((acc.x ^ acc.y ^ acc.z ^ acc.w) == 0x9e3779b9u) out[0] = 1u;
+}
+
+// LDS read rate: every lane issues `iters` rounds of 16 reads from a 32 KB LDS image, ds_read_b128 (tr = 0,
+// 16 bytes per lane) or ds_read_b64_tr_b16 (tr = 1, 8 bytes per lane), conflict-free addresses; out gets a fold
+// of the data (never equal to the sentinel in practice) so that the reads stay. Bytes per launch =
+// gridDim.x * blockDim.x * iters * 16 * (tr ? 8 : 16).
+typedef short gi_s4v __attribute__((__vector_size__(8)));
+extern "C" __global__ void __launch_bounds__(256) gi_probe_lds(int iters, int tr, uint32_t* out) {
+    __shared__ __attribute__((aligned(16))) uint32_t img[8192];
+    for (int i = threadIdx.x; i < 8192; i += 256) img[i] = (uint32_t)i * 2654435761u;
+    __syncthreads();
+    const int lane = threadIdx.x & 63;
+    uint32_t acc = 0u;
+    if (tr) {
+        const __attribute__((address_space(3))) unsigned short* base =
+            (const __attribute__((address_space(3))) unsigned short*)(img);
+        for (int it = 0; it < iters; it++) {
+            gi_s4v v[16];
+#pragma unroll
+            for (int u = 0; u < 16; u++)
+                v[u] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                    (__attribute__((address_space(3))) gi_s4v*)(base + ((lane * 4 + u * 256 + (it & 1) * 128) & 16383)));
+#pragma unroll
+            for (int u = 0; u < 16; u++) acc ^= (uint32_t)(unsigned short)v[u][0] ^ ((uint32_t)(unsigned short)v[u][3] << 16);
+            asm volatile("" ::: "memory");
+        }
+    } else {
+        const __attribute__((address_space(3))) u4* base = (const __attribute__((address_space(3))) u4*)(img) + lane;
+        for (int it = 0; it < iters; it++) {
+            u4 v[16];
+#pragma unroll
+            for (int u = 0; u < 16; u++) v[u] = base[(u * 64 + (it & 1) * 32) & 2047];
+#pragma unroll
+            for (int u = 0; u < 16; u++) acc ^= v[u].x ^ v[u].w;
+            asm volatile("" ::: "memory");
+        }
+    }
+    if (acc == 0x9e3779b9u) out[0] = 1u;
 }
