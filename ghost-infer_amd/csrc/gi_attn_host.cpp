@@ -338,12 +338,15 @@ DecVariant dec_variant(int n_tok, int G, int hd = 128, bool i8 = false) {
     // against 4 waves sharing every tile: config 4's 64 pairs 32.5 -> 27.8 us (f16), 32.5 -> 28.4 us
     // (int8); 96 pairs 36.5 -> 34.3 and 50.1 -> 35.5 us; equal at 48 and 128 pairs (f16).
     v.ncb = pairs > 2 * kDecPairs ? 2 : 1;
-    if (!i8 && pairs > 4 * kDecPairs) {
+    // int8 (on the pipelined tile loop) takes the same layout where its pair groups of 64 are full, measured
+    // at 32768 keys, 32/4 (step µs): 128 pairs 39.9 -> 39.1, 256 pairs 63.1 -> 60.5; at 64 pairs 27.7 ->
+    // 28.0, and at 80 and 96 pairs (a second group part empty) 33.5 -> 36.8 and 34.0 -> 37.0.
+    if (!i8 ? pairs > 4 * kDecPairs : pairs > 8 * kDecPairs && pairs % (8 * kDecPairs) == 0) {
         // f16 above 32 pairs: two pair sets of 32 per workgroup, each split over two waves, so a tile's second
         // read comes from the same CU rather than another workgroup. Split kernel at 32768 keys, 32/4:
         // 48 pairs 27.1 -> 25.9 us, 64 pairs 27.9 -> 26.9, 96 pairs 34.6 -> 34.2, 128 pairs 40.7 -> 37.2.
-        // The int8 cache loses (64 pairs 28.0 -> 31.2 us): its tiles are half the bytes, so the read that
-        // moves is cheap while the halved waves per pair set lengthen the dequantising chain.
+        // The int8 cache lost at 64 pairs (28.0 -> 31.2 us, before its pipelined loop): its tiles are half the
+        // bytes, so the read that moves is cheap while the halved waves per pair set lengthen the chain.
         v.ws2 = true;
         v.groups = (pairs + 8 * kDecPairs - 1) / (8 * kDecPairs);
         return v;

@@ -94,6 +94,9 @@ DECODE_SHAPES_I8 = [
     (4, 1000, 32, 4),  # 32 pairs: two full column blocks per wave
     (6, 130, 32, 4),   # 48 pairs: two workgroups per (slice, kv head), the second half idle
     (4, 40, 16, 1),    # 64 pairs on one kv head, one slice: fewer (slice, kv head) items than XCDs
+    (16, 1000, 32, 4),  # 128 pairs: two pair sets of 32 per workgroup, two workgroups per (slice, kv head)
+    (32, 513, 32, 4),   # 256 pairs: the same layout, four workgroups
+    (8, 2500, 64, 4),   # 128 pairs at G = 16, a span of several slices
 ]
 
 
@@ -119,7 +122,8 @@ def test_verify_i8_8tok_at_32768(gpu):
     check(got, q, k, v, ks, vs, 32768, 32, 4, "verify i8 C4 shape")
 
 
-@pytest.mark.parametrize("n_tok,pos0,n_heads,n_kv", [(1, 300, 32, 4), (1, 65535, 32, 4), (8, 1000, 32, 4)])
+@pytest.mark.parametrize("n_tok,pos0,n_heads,n_kv", [(1, 300, 32, 4), (1, 65535, 32, 4), (8, 1000, 32, 4),
+                                                    (16, 4000, 32, 4)])
 def test_decode_i8_head_major(gpu, n_tok, pos0, n_heads, n_kv):
     say("decode i8 head-major", n_tok, pos0, n_heads, n_kv)
     q, k, v, ks, vs = make_inputs_i8(7000 + pos0, n_tok, pos0 + n_tok, n_heads, n_kv)
