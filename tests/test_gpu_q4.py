@@ -77,6 +77,32 @@ def test_decode_q4_head_major_and_device_position(gpu, n_tok):
                  rel_l2=2e-5, what="q4 decode head-major posp vs f64")
 
 
+@pytest.mark.parametrize("n_tok", [1, 8])
+def test_decode_q4_graph_replay(gpu, n_tok):
+    # a device position, the launch captured once and replayed at several positions with eager work between the
+    # replays (hi/lo columns at 1 token, one pair per column at 8)
+    n_heads, n_kv, cap = 16, 2, 2500
+    q, kc, vc, ks, vs = make_inputs_q4(96 + n_tok, n_tok, cap, n_heads, n_kv)
+    t = q4_dev(q, kc, vc, ks, vs, gpu, n_kv)
+    ws = gi_attn.new_workspace(cap, n_tok, n_heads, n_kv, hd=256, device=gpu)
+    posp = torch.zeros(1, dtype=torch.int32, device=gpu)
+    out = torch.zeros((n_tok, n_heads * 256), dtype=torch.float32, device=gpu)
+    kw = dict(out=out, workspace=ws, posp=posp, ctx_cap=cap)
+    gi_attn.decode_q4(*t, 0, n_heads, n_kv, **kw)  # warm-up
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        gi_attn.decode_q4(*t, 0, n_heads, n_kv, **kw)
+    for pos in (cap - n_tok, 17, 1000, 0):
+        say("decode q4 graph replay", n_tok, pos)
+        posp.fill_(pos)
+        out.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert_close(out.cpu().numpy(), reference_f64_q4(q, kc, vc, ks, vs, pos, n_heads, n_kv), max_abs=2e-5,
+                     rel_l2=2e-5, what=f"q4 replay at {pos}")
+
+
 @pytest.mark.parametrize("n,H,K,ctx,pos0", [(7, 8, 2, 40, 11), (1, 16, 2, 5000, 4999), (200, 4, 1, 260, 50),
                                             (33, 32, 4, 100, 60)])
 def test_rope_q4_store_is_bit_exact(gpu, n, H, K, ctx, pos0):
