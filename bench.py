@@ -4,7 +4,8 @@
                     decode64k_i8|verify_i8|prefill8k_i8|decode64k_h256|verify_h256|prefill8k_h256|
                     decode64k_h256_i8|verify_h256_i8|prefill8k_h256_i8|decode64k_h256_q4|verify_h256_q4|
                     prefill8k_h256_q4]
-                    [--no-cpu-baseline] [--no-secondary] [--reference-layout]
+                    [--no-cpu-baseline] [--no-secondary] [--reference-layout] [--verbose]
+                    [--detail-out FILE] [--full-line]
 
 A step is one pass of the hot path over one batch of synthetic seeded input already resident in HBM:
   decode64k  config 2: one token, 32 query / 4 kv heads, head 128, 65536-key f16 cache (the default: the
@@ -27,13 +28,16 @@ A step is one pass of the hot path over one batch of synthetic seeded input alre
 Decode steps rotate over several layers' caches whose total exceeds the 256 MB Infinity Cache, as a
 model's layer loop does, so no step finds its K/V in the last-level cache.
 
-Prints ONE JSON line (rank 0). With the default workload the line also carries every other config of the
-benchmark under "secondary" (decode4k, verify, prefill8k and chunked, each with its own roofline; then the
-int8, head-256 and 4-bit workloads) and the
-box's measured peaks, and the CPU baseline: the oracle's restatement of the reference's CPU attention
-(src/model.rs:1320-1409) over the same inputs with the cache widened to f32 (as the reference's CPU session
-holds it), timed on this host at its CPU share (up to 16 threads) and at half of it (the reference's default
-logical/2), for configs 2 and 1 and a bounded sample of config 3.
+Prints ONE JSON line (rank 0), kept under ~2 KB so that a record holding only the end of the output holds
+all of it. With the default workload the line also carries configs 1, 3, 4 and 5 under "secondary" (decode4k,
+verify, prefill8k and chunked: value, time, roofline; chunked also the total time and every 16th chunk's
+TFLOP/s) and the roofline fraction of every int8, head-256 and 4-bit workload; and the CPU baseline: the
+oracle's restatement of the reference's CPU attention (src/model.rs:1320-1409) over the same inputs with the
+cache widened to f32 (as the reference's CPU session holds it), timed on this host at its CPU share (up to 16
+threads) and at half of it (the reference's default logical/2), for configs 2 and 1 and a bounded sample of
+config 3. The full record (every field of every workload, every chunk, the box's measured peaks) goes to
+--detail-out (default gpurun_out/bench_detail.json); --full-line prints it instead. Progress messages go to
+stderr with --verbose.
 """
 import argparse
 import json
@@ -51,8 +55,14 @@ METRIC = "decode-attn HBM GB/s @64K ctx; prefill-attn TFLOPS @8K; % of roofline"
 HD = 128
 
 
+VERBOSE = bool(os.environ.get("GI_BENCH_VERBOSE"))
+
+
 def log(*a):
-    print(*a, file=sys.stderr, flush=True)
+    """Progress messages, on stderr only when asked for (--verbose or GI_BENCH_VERBOSE=1): a record that keeps
+    the end of the output must find the result line there, not the progress."""
+    if VERBOSE:
+        print(*a, file=sys.stderr, flush=True)
 
 
 def seeded_cache(gen, rows, n_kv, dev, torch, layout="reference", i8=False, hd=HD):
@@ -604,6 +614,52 @@ def run_qkrope(torch, gi_attn, dev, steps, warmup):
     }
 
 
+ROOF_KEEP = ("bound", "achieved", "peak", "unit", "frac", "traffic")
+
+
+def compact_roofline(rf, extra=()):
+    return {k: rf[k] for k in ROOF_KEEP + tuple(extra) if k in rf}
+
+
+def compact_line(result):
+    """The printed line: the headline fields, its roofline and CPU baseline, and for each other benchmark config
+    (1, 3, 4 and 5) its value, time and roofline; every other workload's roofline fraction. The full record
+    (every field, every workload) goes to the detail file. Kept under ~2 KB so that a record holding only the
+    end of the output still holds all of it."""
+    out = {k: result[k] for k in ("metric", "value", "unit", "n_gpus", "steps", "warmup", "ms_per_step",
+                                  "higher_is_better", "scaling", "vs_baseline", "dtype", "data") if k in result}
+    if isinstance(out.get("ms_per_step"), float):
+        out["ms_per_step"] = round(out["ms_per_step"], 6)
+    cfg = result.get("config", {})
+    out["config"] = {k: cfg[k] for k in ("workload", "ctx", "n_tok", "n_heads", "n_kv", "hd", "slices") if k in cfg}
+    if "roofline" in result:
+        out["roofline"] = compact_roofline(result["roofline"], ("kernel_ms_per_launch",
+                                                                "combine_ms_per_launch", "step_frac_of_hbm_peak"))
+    cb = result.get("cpu_baseline")
+    if cb:
+        out["cpu_baseline"] = {k: cb[k] for k in ("value", "unit", "cores", "kind") if k in cb}
+        out["cpu_baseline"]["sample"] = cb.get("sample_short", cb.get("sample", ""))[:120]
+    sec = result.get("secondary")
+    if sec:
+        cs = {}
+        for w in ("decode4k", "verify", "prefill8k", "chunked"):
+            if w in sec:
+                e = sec[w]
+                cs[w] = {"value": e["value"], "unit": e["unit"], "ms_per_step": round(e["ms_per_step"], 5),
+                         "roofline": compact_roofline(e["roofline"])}
+                if w == "chunked":
+                    c = e["config"]
+                    cs[w]["total_s"] = round(c["total_seconds"], 5)
+                    pc = c["per_chunk_tflops"]
+                    # every 16th chunk (chunk index 16i) and the last; all of them are in the detail file
+                    cs[w]["per_chunk_tflops_every16"] = [round(t) for t in pc[::16]] + [round(pc[-1])]
+        # "workload=frac ..." in one string: the shortest form that keeps every name
+        cs["frac_other"] = " ".join(f"{w}={sec[w]['roofline']['frac']:.3f}" for w in sec
+                                    if w not in cs and isinstance(sec[w], dict) and "roofline" in sec[w])
+        out["secondary"] = cs
+    return out
+
+
 def secondary_entry(line):
     """The fields of a workload's line that a secondary entry keeps."""
     keep = ("value", "unit", "ms_per_step", "dtype", "config", "roofline", "steps")
@@ -623,7 +679,13 @@ def main():
                     help="verify workloads: draft tokens per block (default 8, config 4's)")
     ap.add_argument("--reference-layout", action="store_true",
                     help="decode workloads: also time the reference's cache layout")
+    ap.add_argument("--verbose", action="store_true", help="progress messages on stderr")
+    ap.add_argument("--detail-out", default=os.path.join(ROOT, "gpurun_out", "bench_detail.json"),
+                    help="file for the full record (every field of every workload); '' for none")
+    ap.add_argument("--full-line", action="store_true", help="print the full record instead of the compact line")
     args = ap.parse_args()
+    global VERBOSE
+    VERBOSE = VERBOSE or args.verbose
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: this build has no multi-GPU path (asked for {args.gpus})",
               file=sys.stderr)
@@ -634,7 +696,21 @@ def main():
     import gi_attn
 
     dev = torch.device("cuda:0")
-    gi_attn.init()
+    quiet_fd2 = None
+    if not VERBOSE:
+        # the device's first initialisation prints a libdrm notice on stderr; keep it out of the output's tail
+        sys.stderr.flush()
+        quiet_fd2 = os.dup(2)
+        devnull = os.open(os.devnull, os.O_WRONLY)
+        os.dup2(devnull, 2)
+        os.close(devnull)
+    try:
+        torch.zeros(1, device=dev)
+        gi_attn.init()
+    finally:
+        if quiet_fd2 is not None:
+            os.dup2(quiet_fd2, 2)
+            os.close(quiet_fd2)
     result = {"metric": METRIC, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
               "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "data": "synthetic"}
     w = args.workload
@@ -729,11 +805,21 @@ def main():
             "kind": "port",
             "sample": f"{head_run['config']}: {head_run['sample']}; the oracle's C++ restatement of Model::attention "
                       f"(src/model.rs:1320-1409) over the same inputs with the cache widened to f32",
+            "sample_short": (f"{head_run['config']}: {head_run['sample'].split(' of the')[0].split(' (')[0]}, "
+                             f"oracle Model::attention, f32 cache"),
             "cpu_model": model, "logical_cpus": logical,
             "threads_note": f"all = this process's CPUs capped at 16 (the host share of one GPU), half = the "
                             f"reference's default logical/2",
             "runs": runs}
-    print(json.dumps(result), flush=True)
+    if args.detail_out:
+        try:
+            os.makedirs(os.path.dirname(os.path.abspath(args.detail_out)), exist_ok=True)
+            with open(args.detail_out, "w") as f:
+                json.dump(result, f, indent=1)
+        except OSError as e:
+            log(f"[bench] detail file not written: {e}")
+    print(json.dumps(result) if args.full_line else json.dumps(compact_line(result), separators=(",", ":")),
+          flush=True)
 
 
 if __name__ == "__main__":
