@@ -308,6 +308,99 @@ def test_decode_tc256_i8_roundings_by_hand():
         assert abs(float(alt) - float(want)) > 1e-5 * float(want), what
 
 
+@pytest.mark.parametrize("hd", [128, 256])
+def test_prefill_tc_i8_roundings_by_hand(hd):
+    # attn_prefill_tc over the int8 cache (src/cuda.rs:2466-2498, 2548-2605), one query at position 1 over two
+    # keys: key 0 all ones (scale 1), key 1 zero; Q*scale*log2e rounds to f16 so that score 0 = 1 + 2^-10
+    # exactly. Values: row 0 all 1 with scale 1/3, row 1 all 2 with scale 1/5 (non-unit, so every rounding step
+    # shows). The reference biases each value scale by 2^10 as it loads it, rounds p * (vscale * 2^10) to f16
+    # for P V, sums the f16-rounded p into l, and scales the output by (2^-10 / l).
+    x = (2.0 ** -7 if hd == 128 else 2.0 ** -8) * (1 + 1.25 * 2.0 ** -10)
+    q, qs = _q_between_f16(hd, 1, x)
+    k = np.zeros((2, hd), np.int8)
+    k[0] = 1
+    v = np.zeros((2, hd), np.int8)
+    v[0], v[1] = 1, 2
+    ks = np.ones((2, 1), np.float32)
+    vs = np.array([[1 / 3], [1 / 5]], np.float32)
+    got = O.prefill_tc_semantics_i8(q, k, v, ks, vs, 1, 1, 1, hd=hd)
+    s0 = np.float32(hd) * _f16(q[0, 0] * qs)
+    assert s0 == np.float32(1 + 2.0 ** -10)
+    p1 = np.exp2(np.float32(0) - s0)
+    b0, b1 = vs[0, 0] * np.float32(1024), vs[1, 0] * np.float32(1024)
+    P0, P1 = _f16(np.float32(1) * b0), _f16(p1 * b1)
+    assert P0 == np.float32(341.25)
+    lsum = np.float32(1) + _f16(p1)
+    want = (P0 + np.float32(2) * P1) * ((np.float32(1) / np.float32(1024)) / lsum)
+    np.testing.assert_allclose(got, want, rtol=2e-7, atol=0)
+    slips = {"round p, then times the value scale": (P0 + 2 * _f16(_f16(p1) * b1)) / 1024 / lsum,
+             "l of p times the value scale": (P0 + 2 * P1) / (P0 + P1),
+             "P V of the unrounded product": (b0 + 2 * p1 * b1) / 1024 / lsum,
+             "l of the unrounded p": (P0 + 2 * P1) / 1024 / (1 + p1)}
+    for what, alt in slips.items():
+        assert abs(float(alt) - float(want)) > 1e-5 * float(want), what
+
+
+def _q4_two_keys():
+    """One rotated query at position 1 over two 4-bit keys (head size 256): key 0 all +1 (nibble 9, scale 1), key
+    1 all 0 (nibble 8), so score 0 = 256 * f16(Q*scale*log2e) = 1 + 2^-10 exactly. Values: row 0 all nibble 11
+    (+3) with scale f16(1/3), row 1 all nibble 15 (+7) with scale f16(0.3); each value is f16((n - 8) * scale)
+    (kv4_pair, src/cuda.rs:238-240), and 7 * f16(0.3) is not an f16 value, so its rounding shows."""
+    x = 2.0 ** -8 * (1 + 1.25 * 2.0 ** -10)
+    q, qs = _q_between_f16(256, 1, x)
+    kc = np.array([[0x99] * 128, [0x88] * 128], np.uint8)
+    vc = np.array([[0xBB] * 128, [0xFF] * 128], np.uint8)
+
+    def h(a):
+        return np.float16(a).view(np.uint16)
+
+    ks = np.array([[h(1.0)] * 8] * 2, np.uint16)
+    vs = np.array([[h(1 / 3)] * 8, [h(0.3)] * 8], np.uint16)
+    s0 = np.float32(256) * _f16(q[0, 0] * qs)
+    assert s0 == np.float32(1 + 2.0 ** -10)
+    vau = np.float32(3) * np.float32(np.float16(1 / 3))
+    vbu = np.float32(7) * np.float32(np.float16(0.3))
+    va, vb = _f16(vau), _f16(vbu)
+    assert vb != vbu
+    p1 = np.exp2(np.float32(0) - s0)
+    p1u = np.exp2(np.float32(0) - np.float32(256) * (q[0, 0] * qs))  # had Q not been rounded
+    return (q, kc, vc, ks, vs), p1, p1u, va, vb, vau, vbu
+
+
+def test_decode_tc256_q4_roundings_by_hand():
+    # attention_decode_tc256 over the 4-bit cache (src/cuda.rs:2681-2760): KV_SCALE is 1, so P = f16(p * 2^10),
+    # l sums the unrounded p, and the output is (P V) * (2^-10 / l)
+    args, p1, p1u, va, vb, vau, vbu = _q4_two_keys()
+    got = O.decode_tc256_q4(*args, 1, 1, 1)
+    P0, P1 = _f16(1024), _f16(p1 * np.float32(1024))
+    lsum = np.float32(1) + p1
+    want = (P0 * va + P1 * vb) * ((np.float32(1) / np.float32(1024)) / lsum)
+    np.testing.assert_allclose(got, want, rtol=2e-7, atol=0)
+    slips = {"P not rounded": (P0 * va + p1 * 1024 * vb) / 1024 / lsum,
+             "l of the rounded P": (P0 * va + P1 * vb) / (P0 + P1),
+             "values not rounded": (P0 * vau + P1 * vbu) / 1024 / lsum,
+             "Q not rounded": (P0 * va + _f16(p1u * 1024) * vb) / 1024 / (1 + p1u)}
+    for what, alt in slips.items():
+        assert abs(float(alt) - float(want)) > 1e-5 * float(want), what
+
+
+def test_prefill_tc256_q4_roundings_by_hand():
+    # attn_prefill_tc<256, 2> over the 4-bit cache (src/cuda.rs:2495-2514): the f16 cache's arithmetic over the
+    # staged f16 values, so P = f16(p) for both P V and l, and the output is P V / l
+    args, p1, p1u, va, vb, vau, vbu = _q4_two_keys()
+    got = O.prefill_tc256_q4(*args, 1, 1, 1)
+    P1 = _f16(p1)
+    lsum = np.float32(1) + P1
+    want = (va + P1 * vb) / lsum
+    np.testing.assert_allclose(got, want, rtol=2e-7, atol=0)
+    slips = {"P not rounded": (va + p1 * vb) / (1 + p1),
+             "l of the unrounded p": (va + P1 * vb) / (1 + p1),
+             "values not rounded": (vau + P1 * vbu) / lsum,
+             "Q not rounded": (va + _f16(p1u) * vb) / (1 + _f16(p1u))}
+    for what, alt in slips.items():
+        assert abs(float(alt) - float(want)) > 1e-5 * float(want), what
+
+
 @pytest.mark.parametrize("n_tok,pos0,n_heads,n_kv", [(1, 0, 16, 2), (1, 7, 16, 2), (1, 8, 8, 1), (1, 300, 16, 2),
                                                      (3, 100, 8, 1), (8, 2000, 16, 2), (1, 4095, 16, 16)])
 def test_decode_tc256_i8_within_parity_bar(n_tok, pos0, n_heads, n_kv):
