@@ -22,6 +22,11 @@
  *    contiguous, which spreads a head's stream evenly over the HBM channels (the decode kernel is
  *    fastest with it). Strides are multiples of 8 elements and pointers 16-byte aligned.
  *  - Causality: token b of a call sits at position pos0 + b and attends to keys 0..pos0+b.
+ *  - Device positions (posp, graph replay): no entry point reports a device position that overruns the
+ *    cache, since the host never sees it. The decode kernels (which gi_attention* use whenever posp is
+ *    set) clamp *posp into [0, ctx_cap - n_tok] and return the attention at the clamped position; the
+ *    cache writes store no row at a position outside [0, ctx_cap). A caller that can overrun checks its position on the host before
+ *    replaying (the reference trusts *posp the same way, src/cuda.rs:8686-8712).
  *  - hd is 128 or 256 (the reference's wide heads: attention_partial_gqa's hd 256 branch src/cuda.rs:1762-1781,
  *    attention_prefill_tc256 src/cuda.rs:2622-2623, attention_decode_tc256 src/cuda.rs:2625-2802) with the f16
  *    and the int8 caches, and 256 with the 4-bit cache (the *_q4 entry points); n_heads must be a multiple of
