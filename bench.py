@@ -127,10 +127,13 @@ def decode_kernel_name(n_tok, n_heads, n_kv, hd, i8):
     (up to 8 (token, head) pairs per kv head: one column block with two columns per pair; above, one pair
     per MFMA column, with two column blocks per wave above 16 pairs at head size 128 (f16 above 32 pairs:
     two pair sets per workgroup, each over two waves), and two pair sets of one column block at head size
-    256)."""
+    256 over the f16 cache; over its int8 and 4-bit caches one pair per column throughout, 16 pairs per workgroup
+    or, above 16 pairs, two pair sets (int8) or two column blocks per wave (4-bit))."""
     pairs, p = n_tok * (n_heads // n_kv), 8
-    if i8 == "q4":
-        return "gi_decode_pm_ws2_1_q4" if pairs > p else "gi_decode_partial_1_q4"
+    if hd == 256 and i8:  # the reference's tc256 roundings, one pair per column: 16 or 32 pairs per workgroup
+        if pairs <= 2 * p:
+            return "gi_decode_pm_1" + ("_q4" if i8 == "q4" else "_i8_h256")
+        return "gi_decode_pm_2_q4" if i8 == "q4" else "gi_decode_pm_ws2_1_i8_h256"
     if pairs <= p:
         name = "gi_decode_partial_1"
     elif hd == 256:

@@ -162,11 +162,12 @@ struct Module {
     bool loaded = false;
     hipModule_t mod = nullptr;
     hipFunction_t dec[2] = {};        // up to 8 pairs, head size 128: [int8 cache]
-    hipFunction_t dec256[2] = {};     // up to 8 pairs, head size 256: [int8 cache]
+    hipFunction_t dec256 = nullptr;   // up to 8 pairs, head size 256, the f16 cache
     hipFunction_t dec_pm[2][2] = {};  // [int8 cache][column blocks - 1]: one pair per column
     hipFunction_t dec_ws2[2] = {};    // head size 128, two column blocks, two pair sets of two waves: [int8 cache]
-    hipFunction_t dec_q4 = nullptr;   // up to 8 pairs, head size 256, the 4-bit cache
-    hipFunction_t dec_pm256[3] = {};  // head size 256, one pair per column, two pair sets of two waves: [f16, int8, 4-bit]
+    hipFunction_t dec_ref[3] = {};    // head size 256, one pair per column, the reference's tc256 roundings: int8
+                                      // one column block, 4-bit one and two column blocks
+    hipFunction_t dec_pm256[2] = {};  // head size 256, one pair per column, two pair sets of two waves: [f16, int8]
     hipFunction_t prefill[2] = {};   // [int8 cache], head size 128
     hipFunction_t prefill256r = nullptr; // head size 256 (f16 cache), 16 rows per wave: one workgroup per query tile
     hipFunction_t prefill256r_fmt[2] = {}; // the same over the int8 and the 4-bit cache
@@ -206,18 +207,18 @@ int load_module(const char* path, Module** out) {
         struct { hipFunction_t* f; const char* name; } fns[] = {
             {&m.dec[0], "gi_decode_partial_1"},
             {&m.dec[1], "gi_decode_partial_1_i8"},
-            {&m.dec256[0], "gi_decode_partial_1_h256"},
-            {&m.dec256[1], "gi_decode_partial_1_i8_h256"},
+            {&m.dec256, "gi_decode_partial_1_h256"},
+            {&m.dec_ref[0], "gi_decode_pm_1_i8_h256"},
+            {&m.dec_ref[1], "gi_decode_pm_1_q4"},
+            {&m.dec_ref[2], "gi_decode_pm_2_q4"},
             {&m.dec_pm[0][0], "gi_decode_pm_1"},
             {&m.dec_pm[0][1], "gi_decode_pm_2"},
             {&m.dec_pm[1][0], "gi_decode_pm_1_i8"},
             {&m.dec_pm[1][1], "gi_decode_pm_2_i8"},
             {&m.dec_ws2[0], "gi_decode_pm_ws2_2"},
             {&m.dec_ws2[1], "gi_decode_pm_ws2_2_i8"},
-            {&m.dec_q4, "gi_decode_partial_1_q4"},
             {&m.dec_pm256[0], "gi_decode_pm_ws2_1_h256"},
             {&m.dec_pm256[1], "gi_decode_pm_ws2_1_i8_h256"},
-            {&m.dec_pm256[2], "gi_decode_pm_ws2_1_q4"},
             {&m.combine, "gi_decode_combine"},
             {&m.relayout, "gi_kv_relayout"},
             {&m.hadamard, "gi_hadamard_rows"},
@@ -307,18 +308,29 @@ int decode_target_wgs() {
     return target;
 }
 
-// Decode kernel variant for n_tok tokens of G heads per kv head (head size hd). Up to 8 (token, head) pairs:
-// one column block of 8 pairs, each pair's f16 high and remainder parts in two columns (gi_decode_partial_1).
-// More pairs: one pair per column (pm), 16 per column block, the high and remainder parts as two MFMAs into
-// one accumulator, so no lane repeats its neighbour's softmax.
+// Decode kernel variant for n_tok tokens of G heads per kv head (head size hd, cache format fmt: 0 f16, 1 int8,
+// 2 4-bit). Up to 8 (token, head) pairs: one column block of 8 pairs, each pair's f16 high and remainder parts in
+// two columns (gi_decode_partial_1). More pairs: one pair per column (pm), 16 per column block, the high and
+// remainder parts as two MFMAs into one accumulator, so no lane repeats its neighbour's softmax. Head size 256 over
+// the int8 and 4-bit caches: one pair per column with the reference's single f16 Q and P, 16 pairs per workgroup
+// up to 16 pairs, else two column blocks per wave (32 pairs per workgroup), each tile widened once per workgroup.
 struct DecVariant {
     int ncb;     // column blocks per wave
     bool ws2;    // two pair sets per workgroup, each split over two waves (else the 4 waves serve one set)
     bool pm;     // one pair per column
     int groups;  // workgroups per (slice, kv head)
 };
-DecVariant dec_variant(int n_tok, int G, int hd = 128, bool i8 = false) {
+DecVariant dec_variant(int n_tok, int G, int hd = 128, int fmt = 0) {
     const int pairs = n_tok * G;
+    const bool i8 = fmt == 1;
+    if (hd == 256 && fmt) {
+        // Above 16 pairs, split kernel at 32768 keys, 64 pairs, 16/2 (same box): 4-bit two column blocks per wave
+        // 29.0 us, two pair sets of one block over two waves each 29.5 (the hi/lo-split kernel before: 31.3); int8
+        // 52.3 and 25.4 (before: 28.4; two column blocks leave room for two tiles in flight, not four)
+        if (pairs <= 2 * kDecPairs) return DecVariant{1, false, true, 1};
+        if (fmt == 1) return DecVariant{1, true, true, (pairs + 4 * kDecPairs - 1) / (4 * kDecPairs)};
+        return DecVariant{2, false, true, (pairs + 4 * kDecPairs - 1) / (4 * kDecPairs)};
+    }
     DecVariant v{1, false, pairs > kDecPairs, 1};
     if (!v.pm) return v;
     if (hd == 256) {
@@ -361,9 +373,9 @@ DecVariant dec_variant(int n_tok, int G, int hd = 128, bool i8 = false) {
 // over per_slot slices. At config 4's 32776 keys: 61 slices of 544 keys, where whole units of 4 tiles gave 52
 // slices of 640 (208 of 256 workgroups busy).
 void plan(int max_span, int n_tok, int n_heads, int n_kv, int* chunk, int* nsplit, int unit = kSliceUnit,
-          int hd = 128, bool i8 = false) {
+          int hd = 128, int fmt = 0) {
     int G = n_heads / n_kv;
-    int groups = dec_variant(n_tok, G, hd, i8).groups;
+    int groups = dec_variant(n_tok, G, hd, fmt).groups;
     int per_slot = std::max(1, decode_target_wgs() / std::max(1, n_kv * groups));
     const int tile = unit / kDecWaves;
     const int least = (max_span + per_slot - 1) / per_slot; // the shortest slice the cap allows
@@ -440,9 +452,9 @@ int decode_impl(void* stream, const float* q, long long q_stride, const void* kc
     if (posp && ctx_cap < n_tok) return fail("ctx_cap %d must cover the %d tokens", ctx_cap, n_tok);
     Module* m;
     if (int e = load_module(nullptr, &m)) return e;
-    const DecVariant var = dec_variant(n_tok, n_heads / n_kv, hd, i8);
+    const DecVariant var = dec_variant(n_tok, n_heads / n_kv, hd, fmt);
     GiDecodeArgs a{};
-    plan(max_span, n_tok, n_heads, n_kv, &a.chunk, &a.nsplit, slice_unit(i8, hd), hd, i8);
+    plan(max_span, n_tok, n_heads, n_kv, &a.chunk, &a.nsplit, slice_unit(i8, hd), hd, fmt);
     size_t need = a.nsplit == 1 ? 0 : (size_t)n_tok * n_heads * a.nsplit * (hd + 4) * sizeof(float);
     if (need && (!workspace || workspace_bytes < need))
         return fail("workspace of %zu bytes too small: %zu needed", workspace_bytes, need);
@@ -471,7 +483,8 @@ int decode_impl(void* stream, const float* q, long long q_stride, const void* kc
         a.sc_head_stride = sc_head_stride;
     }
     hipStream_t st = (hipStream_t)stream;
-    hipFunction_t f = hd == 256 ? (var.pm ? m->dec_pm256[fmt] : fmt == 2 ? m->dec_q4 : m->dec256[i8])
+    hipFunction_t f = hd == 256 ? (var.ws2 ? m->dec_pm256[fmt] : fmt ? m->dec_ref[fmt - 1 + var.ncb - 1]
+                                   : var.pm ? m->dec_pm256[0] : m->dec256)
                       : var.ws2   ? m->dec_ws2[i8]
                       : var.pm    ? m->dec_pm[i8][var.ncb - 1]
                                   : m->dec[i8];
@@ -639,8 +652,8 @@ size_t gi_attn_decode_workspace_bytes(int ctx_cap, int n_tok, int n_heads, int n
     size_t best = 16;
     int G = n_heads / n_kv;
     for (int t = 1; t <= n_tok; t++)
-        for (bool i8 : {false, true}) {
-            int groups = dec_variant(t, G, hd, i8).groups;
+        for (int fmt = 0; fmt < (hd == 256 ? 3 : 2); fmt++) {
+            int groups = dec_variant(t, G, hd, fmt).groups;
             int per_slot = std::max(1, decode_target_wgs() / std::max(1, n_kv * groups));
             int most = std::max(1, std::min(per_slot, (ctx_cap + unit - 1) / unit));
             best = std::max(best, (size_t)t * n_heads * most * (hd + 4) * sizeof(float));

@@ -104,6 +104,11 @@ __device__ __attribute__((used, aligned(256))) unsigned char gi_scratch[GI_SCRAT
 // (with one pair per column the high and remainder parts share an accumulator, so P times the value scale is
 // biased as a whole instead; the merge divides it out)
 #define DEC_I8_VB 64.f
+// Head size 256 over the int8 and 4-bit caches (the reference's attention_decode_tc256, src/cuda.rs:2625-2802):
+// one f16 Q (Q*scale*log2e rounded once) and one f16 P (p times the value scale and a bias, rounded once), the
+// reference's own roundings, with the exp-sum of the unrounded p. The reference biases by 2^10 with p <= 1; here p
+// <= 2^8 (the lazy rescale), so the bias is 4: the same largest P for a given value scale.
+#define DEC_REF_VB 4.f
 #define GI_RSRC_FLAGS 0x00020000
 
 __device__ __forceinline__ float wave_xor(float v, int m) { return __shfl_xor(v, m, 64); }
@@ -240,6 +245,12 @@ template <int NCB, int WS, bool I8, int HD = 128, bool PM = false, bool Q4 = fal
 __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
     static_assert(HD == 128 || HD == 256, "head sizes: 128, 256");
     static_assert(!Q4 || (HD == 256 && !I8), "the 4-bit cache: head size 256");
+    // the reference's tc256 arithmetic (one f16 Q, one f16 P; see DEC_REF_VB): head size 256 over the int8 and
+    // 4-bit caches, which these kernels serve with one pair per column
+    constexpr bool REF = (I8 || Q4) && HD == 256;
+    static_assert(!REF || PM, "head size 256 over the int8 and 4-bit caches: one pair per column");
+    // the bias on P that the merge divides out
+    constexpr float PBIAS = REF && I8 ? DEC_REF_VB : I8 && PM ? DEC_I8_VB : 1.f;
     // tiles in flight per wave: an int8 tile at head size 256 holds half the bytes of the others (4-bit: a quarter)
     constexpr int NB = (I8 || Q4) && HD == 256 ? 2 * DEC_NB : DEC_NB;
     constexpr int CPAIRS = PM ? 2 * DEC_PAIRS : DEC_PAIRS; // pairs per column block
@@ -304,7 +315,7 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
     // B operand of S^T = K Qc^T. f16: k-step kk covers dims 32kk..32kk+31, this lane dims 32kk+8grp..+7.
     // int8: this lane dims 16grp + 8(kk%2) + 64(kk/2) .. +7 (the bytes its two 16-byte key loads bring)
     h8 qf[NCB][KK];
-    h8 qfl[NCB][KK]; // PM: the remainders (else unused)
+    h8 qfl[NCB][REF ? 1 : KK]; // PM: the remainders (REF: none; else unused)
     {
         __amdgpu_buffer_rsrc_t rq = gi_rsrc(a.q, (long long)a.n_tok * a.q_stride * 4);
 #pragma unroll
@@ -724,7 +735,7 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
 #pragma unroll
             for (int cb = 0; cb < NCB; cb++) {
                 o[cb][dd] = __builtin_amdgcn_mfma_f32_16x16x16f16(vt, pf[cb], o[cb][dd], 0, 0, 0);
-                if constexpr (PM) o[cb][dd] = __builtin_amdgcn_mfma_f32_16x16x16f16(vt, pfl[cb], o[cb][dd], 0, 0, 0);
+                if constexpr (PM && !REF) o[cb][dd] = __builtin_amdgcn_mfma_f32_16x16x16f16(vt, pfl[cb], o[cb][dd], 0, 0, 0);
             }
         }
     };
@@ -739,7 +750,7 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
 #pragma unroll
             for (int cb = 0; cb < NCB; cb++) {
                 sacc[cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[cb][kk], sacc[cb], 0, 0, 0);
-                if constexpr (PM) sacc[cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qfl[cb][kk], sacc[cb], 0, 0, 0);
+                if constexpr (PM && !REF) sacc[cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qfl[cb][kk], sacc[cb], 0, 0, 0);
             }
         }
         float ksb[4], vsb[4]; // int8: the scales of keys 4grp + j
@@ -786,9 +797,11 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
                 const float p = __builtin_amdgcn_exp2f(sc[j] - m_use);
                 psum += p;
                 // int8: P V takes p times the value's scale (biased like the head-128 int8 kernel)
-                const float pv = I8 ? p * vsb[j] * (PM ? DEC_I8_VB : 1.f) : p;
+                const float pv = I8 ? p * vsb[j] * PBIAS : p;
                 _Float16 hi = (_Float16)pv;
-                if constexpr (PM) {
+                if constexpr (REF) {
+                    pf[cb][j] = hi; // rounded once, as the reference's pack_h2 (src/cuda.rs:2723)
+                } else if constexpr (PM) {
                     pf[cb][j] = hi;
                     pfl[cb][j] = (_Float16)(pv - (float)hi);
                 } else {
@@ -841,7 +854,7 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
                     if constexpr (HD == 256) kf = kfrag256(B, kk);
                     else kf = __builtin_bit_cast(h8, B.k[b][kk]);
                     acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[cb][kk], acc, 0, 0, 0);
-                    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qfl[cb][kk], acc, 0, 0, 0);
+                    if constexpr (!REF) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qfl[cb][kk], acc, 0, 0, 0);
                 }
                 // (in VGPRs once, for the max and then the exp, instead of two reads of an accumulator register)
                 asm volatile("" : "+v"(acc));
@@ -916,11 +929,13 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
                 const float p = __builtin_amdgcn_exp2f(S.v[cb][i >> 2][i & 3]);
                 psum += p;
                 // int8: P V takes p times the value's scale (biased like process_i8)
-                const float pv = I8 ? p * vsb[i] * DEC_I8_VB : p;
+                const float pv = I8 ? p * vsb[i] * PBIAS : p;
                 // the high part: pv cut to f16's 11 significant bits, so that it converts exactly and the
                 // remainder is an exact f32 subtraction (no conversion back)
                 const float hi = __uint_as_float(__float_as_uint(pv) & 0xffffe000u);
-                if constexpr (I8 && HD == 128) {
+                if constexpr (REF) {
+                    P.hi[cb][i] = (_Float16)pv; // rounded once, as the reference's pack_h2 (src/cuda.rs:2723)
+                } else if constexpr (I8 && HD == 128) {
                     P.hi[cb][i >> 3][i & 7] = (_Float16)hi;
                     P.lo[cb][i >> 3][i & 7] = (_Float16)(pv - hi);
                 } else {
@@ -989,7 +1004,9 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
                 const uint32_t bits = qraw[cb][kk][e >> 2][e & 3];
                 float v = valid[cb] ? __uint_as_float(bits) * a.qscale : 0.f;
                 _Float16 hi = (_Float16)v;
-                if constexpr (PM) {
+                if constexpr (REF) {
+                    qf[cb][kk][e] = hi; // rounded once, as the reference's qf (src/cuda.rs:2669)
+                } else if constexpr (PM) {
                     qf[cb][kk][e] = hi;
                     qfl[cb][kk][e] = (_Float16)(v - (float)hi);
                 } else {
@@ -1078,7 +1095,7 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
     __syncthreads();
     // ---- merge each pair set's waves and the hi/lo columns: thread -> (pair, 4 dims)
     constexpr float LO = I8 ? 1.f / DEC_I8_LO : 1.f;      // the remainder column's scale (PM: no column)
-    constexpr float OSC = I8 && PM ? 1.f / DEC_I8_VB : 1.f; // PM int8: the bias on P
+    constexpr float OSC = 1.f / PBIAS; // the bias on P (int8 with one pair per column)
     // all LDS reads of the thread's items are issued before any arithmetic, so the merge waits for LDS once
     constexpr int ITEMS = WG_PAIRS * HD / 1024;
     float mw[ITEMS][WS], lw[ITEMS][WS];
@@ -1157,15 +1174,18 @@ GI_DEC_PM_KERNEL(gi_decode_pm_1_i8, 1, DEC_WAVES, true)
 GI_DEC_PM_KERNEL(gi_decode_pm_2_i8, 2, DEC_WAVES, true)
 GI_DEC_PM_KERNEL(gi_decode_pm_ws2_2, 2, 2, false)
 GI_DEC_PM_KERNEL(gi_decode_pm_ws2_2_i8, 2, 2, true)
-GI_DEC_KERNEL(gi_decode_partial_1_i8_h256, 1, DEC_WAVES, true, 256)
 #define GI_DEC_PM256_KERNEL(name, NCB, WS, I8) \
     extern "C" __global__ void __launch_bounds__(256, DEC_MINWG) name(GiDecodeArgs a) { gi_decode_partial_t<NCB, WS, I8, 256, true>(a); }
-#define GI_DEC_Q4_KERNEL(name, WS, PM) \
-    extern "C" __global__ void __launch_bounds__(256, DEC_MINWG) name(GiDecodeArgs a) { gi_decode_partial_t<1, WS, false, 256, PM, true>(a); }
+#define GI_DEC_Q4_KERNEL(name, NCB, WS) \
+    extern "C" __global__ void __launch_bounds__(256, DEC_MINWG) name(GiDecodeArgs a) { gi_decode_partial_t<NCB, WS, false, 256, true, true>(a); }
 GI_DEC_PM256_KERNEL(gi_decode_pm_ws2_1_h256, 1, 2, false)
+// head size 256 over the int8 and 4-bit caches: the reference's tc256 roundings, 16 pairs per workgroup, or 32 as
+// two pair sets (int8) or two column blocks per wave (4-bit)
+GI_DEC_PM256_KERNEL(gi_decode_pm_1_i8_h256, 1, DEC_WAVES, true)
 GI_DEC_PM256_KERNEL(gi_decode_pm_ws2_1_i8_h256, 1, 2, true)
-GI_DEC_Q4_KERNEL(gi_decode_partial_1_q4, DEC_WAVES, false)
-GI_DEC_Q4_KERNEL(gi_decode_pm_ws2_1_q4, 2, true)
+GI_DEC_Q4_KERNEL(gi_decode_pm_1_q4, 1, DEC_WAVES)
+GI_DEC_Q4_KERNEL(gi_decode_pm_2_q4, 2, DEC_WAVES)
+
 
 // Merge the slices of each (token, head): M = max m_s, w_s = 2^(m_s - M), out = sum w_s O_s / sum w_s l_s
 // (attention_combine's maths in base 2; empty slices carry m = -inf and weigh nothing). One wave per

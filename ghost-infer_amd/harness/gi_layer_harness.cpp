@@ -9,7 +9,8 @@
 //   3. a reference pass: attention over the whole sequence on the exact split path (verify blocks of up to
 //      15 tokens), with every output row checked against it: prompt rows within the path's parity bar
 //      (max-abs 2e-3: the prefill rounds P to f16), decoded rows within 2e-5 (both sides compute in f32
-//      precision).
+//      precision; 1e-3 at head size 256 over the int8 and 4-bit caches, whose split path rounds Q and P to f16
+//      as the reference's attention_decode_tc256 does).
 // --q4 (head size 256) plays the reference's 4-bit cache: the cache write rotates q, k and v rows, and every
 // attention call is followed by gi_hadamard_rows on its output rows, as the layer does (src/cuda.rs:9765-9768).
 // One JSON line goes to stdout. Exit status 0 when every row agrees, 1 when one does not, 2 on a usage or
@@ -260,7 +261,11 @@ int main(int argc, char** argv) {
             fwrite(got.data(), sizeof(float), got.size(), f) != got.size() || fclose(f) != 0)
             die("cannot write " + o.dump);
     }
-    const double tol_prompt = o.prompt >= 16 ? 2e-3 : 2e-5, tol_decode = 2e-5;
+    // (head size 256 over the int8 and 4-bit caches: the split path rounds Q and P to f16 as the reference's
+    // attention_decode_tc256 does, against each launch's own running maxima, so a decode step and a verify block
+    // of the reference pass agree to about f16's step)
+    const double tol_split = hd == 256 && (o.i8 || o.q4) ? 1e-3 : 2e-5;
+    const double tol_prompt = o.prompt >= 16 ? 2e-3 : tol_split, tol_decode = tol_split;
     const bool ok = finite && err_prompt <= tol_prompt && err_decode <= tol_decode;
     printf("{\"prompt\": %d, \"steps\": %d, \"heads\": %d, \"kv\": %d, \"hd\": %d, \"cache\": \"%s\", \"graph\": %s, "
            "\"prompt_ms\": %.4f, \"decode_step_us\": %.2f, \"max_abs_prompt\": %.3g, \"max_abs_decode\": %.3g, "

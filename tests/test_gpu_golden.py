@@ -4,7 +4,8 @@ and, packed as the reference's qkv rows, through the operator gi_attention(_i8, 
 the prefill cases through gi_attn_prefill(_i8, _q4).
 
 Bar: decode and verify within 2e-5 of float64 (the split path keeps f32 precision), prefill within the
-north star's 2e-3 / 1e-3 (it rounds P to f16 as the reference does)."""
+north star's 2e-3 / 1e-3 (it rounds P to f16 as the reference does), and so is decode at head size 256 over the
+int8 and 4-bit caches (it rounds Q and P to f16 as the reference's attention_decode_tc256 does)."""
 import os
 import sys
 
@@ -13,7 +14,7 @@ import pytest
 import torch
 
 import gi_attn
-from attn_common import assert_close
+from attn_common import assert_close, split_f64_tol
 
 pytestmark = pytest.mark.gpu
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
@@ -62,12 +63,13 @@ def test_golden_through_the_hip_path(gpu, name):
             return
         out = gi_attn.decode_q4(q, k, v, ks, vs, m["pos0"], m["n_heads"], m["n_kv"])
         torch.cuda.synchronize()
-        assert_close(out.cpu().numpy(), want, max_abs=2e-5, rel_l2=2e-5, what=f"{name} decode")
+        tol = split_f64_tol("q4", 256)
+        assert_close(out.cpu().numpy(), want, *tol, what=f"{name} decode")
         qkv = torch.zeros((n, (m["n_heads"] + 2 * m["n_kv"]) * 256), dtype=torch.float32, device=gpu)
         qkv[:, :m["n_heads"] * 256] = q
         out2 = gi_attn.attention_q4(qkv, k, v, ks, vs, m["pos0"], m["n_heads"], m["n_kv"], exact=True)
         torch.cuda.synchronize()
-        assert_close(out2.cpu().numpy(), want, max_abs=2e-5, rel_l2=2e-5, what=f"{name} operator")
+        assert_close(out2.cpu().numpy(), want, *tol, what=f"{name} operator")
         return
     if name.startswith("prefill"):
         out = gi_attn.prefill(q, k, v, m["pos0"], m["n_heads"], m["n_kv"], hd=m["hd"], out_dtype=torch.float32, **sc)
@@ -76,11 +78,12 @@ def test_golden_through_the_hip_path(gpu, name):
         return
     out = gi_attn.decode(q, k, v, m["pos0"], m["n_heads"], m["n_kv"], hd=m["hd"], **sc)
     torch.cuda.synchronize()
-    assert_close(out.cpu().numpy(), want, max_abs=2e-5, rel_l2=2e-5, what=f"{name} decode")
+    tol = split_f64_tol("i8" if sc else "f16", m["hd"])
+    assert_close(out.cpu().numpy(), want, *tol, what=f"{name} decode")
     # the operator over the reference's qkv rows [q | k | v] (only q is read: the cache already holds the rows)
     qd, kvd = m["n_heads"] * m["hd"], m["n_kv"] * m["hd"]
     qkv = torch.zeros((n, qd + 2 * kvd), dtype=torch.float32, device=gpu)
     qkv[:, :qd] = q
     out2 = gi_attn.attention(qkv, k, v, m["pos0"], m["n_heads"], m["n_kv"], hd=m["hd"], exact=True, **sc)
     torch.cuda.synchronize()
-    assert_close(out2.cpu().numpy(), want, max_abs=2e-5, rel_l2=2e-5, what=f"{name} operator")
+    assert_close(out2.cpu().numpy(), want, *tol, what=f"{name} operator")

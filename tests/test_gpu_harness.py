@@ -15,7 +15,7 @@ import numpy as np
 import pytest
 
 import gi_oracle as O
-from attn_common import assert_close, reference_f64, reference_f64_i8, reference_f64_q4
+from attn_common import REF_ORACLE_TOL, assert_close, reference_f64, reference_f64_i8, reference_f64_q4, split_f64_tol
 
 HARNESS = os.path.join(os.path.dirname(os.path.abspath(__file__)), "..", "ghost-infer_amd", "gi_layer_harness")
 
@@ -88,9 +88,12 @@ def test_layer_harness(case, tmp_path):
     # prompt rows: the prefill path (f16 P) against the reference's prefill semantics and float64, the bar
     assert_close(got[pre], want_pre, what="harness prompt rows vs oracle")
     assert_close(got[pre], f64[pre], what="harness prompt rows vs f64")
-    # decoded rows: the split path in f32 precision, against the oracle at the bar and float64 at 2e-5
-    assert_close(got[dec], want_dec, what="harness decode rows vs oracle")
-    assert_close(got[dec], f64[dec], max_abs=2e-5, rel_l2=2e-5, what="harness decode rows vs f64")
+    # decoded rows: the split path (f32 precision; head size 256 over the int8 and 4-bit caches the reference's
+    # tc256 roundings), against the oracle and float64
+    fmt = "q4" if i8 == "q4" else "i8" if i8 else "f16"
+    ref256 = hd == 256 and fmt != "f16"
+    assert_close(got[dec], want_dec, *(REF_ORACLE_TOL if ref256 else (2e-3, 1e-3)), what="harness decode rows vs oracle")
+    assert_close(got[dec], f64[dec], *split_f64_tol(fmt, hd), what="harness decode rows vs f64")
 
 
 def _h256():

@@ -3,8 +3,9 @@ C ABI: the rotated store (qk_norm_rope with KV4), the tensor-core decode over it
 and, end to end, the attention of the unrotated rows.
 
 Bar: the cache bytes and scales bit-exact against the oracle's quantiser (on the same rotated rows, and on the
-same input for v rows, whose rotation is bit-identical to kv4_fwht); decode outputs max-abs 2e-3 / relative L2
-1e-3 against the oracle's restatement and 2e-5 against float64 attention over the cache's f16 values.
+same input for v rows, whose rotation is bit-identical to kv4_fwht); decode outputs within REF_ORACLE_TOL of the
+oracle's restatement of attention_decode_tc256 (the same f16 roundings of Q and P) and within max-abs 2e-3 /
+relative L2 1e-3 of float64 attention over the cache's f16 values.
 """
 import sys
 
@@ -14,7 +15,9 @@ import torch
 
 import gi_attn
 import gi_oracle as O
-from attn_common import assert_close, make_inputs_q4, reference_f64_q4
+from attn_common import REF_ORACLE_TOL, assert_close, make_inputs_q4, reference_f64_q4, split_f64_tol
+
+F64_TOL = split_f64_tol("q4", 256)
 
 pytestmark = pytest.mark.gpu
 
@@ -37,7 +40,7 @@ def q4_dev(q, kc, vc, ks, vs, dev, n_kv, layout="reference"):
 
 DECODE_SHAPES_Q4 = [
     # (n_tok, pos0, n_heads, n_kv): spans inside one 16-key tile and at tile / slice edges, both kernel variants
-    # (up to 8 pairs per kv head: hi/lo columns; above: one pair per column, two pair sets per workgroup), G = 3
+    # (up to 16 pairs per kv head: one column block per workgroup; above: two column blocks per wave), G = 3
     (1, 0, 16, 2),
     (1, 15, 16, 2),
     (1, 64, 16, 2),
@@ -58,9 +61,9 @@ def test_decode_q4(gpu, n_tok, pos0, n_heads, n_kv):
     out = gi_attn.decode_q4(*t, pos0, n_heads, n_kv)
     torch.cuda.synchronize()
     got = out.cpu().numpy()
-    assert_close(got, O.decode_tc256_q4(q, kc, vc, ks, vs, pos0, n_heads, n_kv), what="q4 decode vs oracle")
-    assert_close(got, reference_f64_q4(q, kc, vc, ks, vs, pos0, n_heads, n_kv), max_abs=2e-5, rel_l2=2e-5,
-                 what="q4 decode vs f64")
+    assert_close(got, O.decode_tc256_q4(q, kc, vc, ks, vs, pos0, n_heads, n_kv), *REF_ORACLE_TOL,
+                 what="q4 decode vs oracle")
+    assert_close(got, reference_f64_q4(q, kc, vc, ks, vs, pos0, n_heads, n_kv), *F64_TOL, what="q4 decode vs f64")
 
 
 @pytest.mark.parametrize("n_tok", [1, 8])
@@ -73,14 +76,17 @@ def test_decode_q4_head_major_and_device_position(gpu, n_tok):
     posp = torch.full((1,), pos0, dtype=torch.int32, device=gpu)
     out = gi_attn.decode_q4(*t, 0, n_heads, n_kv, posp=posp, ctx_cap=cap, kv_layout="head_major")
     torch.cuda.synchronize()
-    assert_close(out.cpu().numpy(), reference_f64_q4(q, kc, vc, ks, vs, pos0, n_heads, n_kv), max_abs=2e-5,
-                 rel_l2=2e-5, what="q4 decode head-major posp vs f64")
+    got = out.cpu().numpy()
+    assert_close(got, O.decode_tc256_q4(q, kc, vc, ks, vs, pos0, n_heads, n_kv), *REF_ORACLE_TOL,
+                 what="q4 decode head-major posp vs oracle")
+    assert_close(got, reference_f64_q4(q, kc, vc, ks, vs, pos0, n_heads, n_kv), *F64_TOL,
+                 what="q4 decode head-major posp vs f64")
 
 
 @pytest.mark.parametrize("n_tok", [1, 8])
 def test_decode_q4_graph_replay(gpu, n_tok):
     # a device position, the launch captured once and replayed at several positions with eager work between the
-    # replays (hi/lo columns at 1 token, one pair per column at 8)
+    # replays (one column block per workgroup at 1 token, two column blocks per wave at 8)
     n_heads, n_kv, cap = 16, 2, 2500
     q, kc, vc, ks, vs = make_inputs_q4(96 + n_tok, n_tok, cap, n_heads, n_kv)
     t = q4_dev(q, kc, vc, ks, vs, gpu, n_kv)
@@ -99,8 +105,11 @@ def test_decode_q4_graph_replay(gpu, n_tok):
         out.zero_()
         g.replay()
         torch.cuda.synchronize()
-        assert_close(out.cpu().numpy(), reference_f64_q4(q, kc, vc, ks, vs, pos, n_heads, n_kv), max_abs=2e-5,
-                     rel_l2=2e-5, what=f"q4 replay at {pos}")
+        got = out.cpu().numpy()
+        assert_close(got, O.decode_tc256_q4(q, kc, vc, ks, vs, pos, n_heads, n_kv), *REF_ORACLE_TOL,
+                     what=f"q4 replay at {pos} vs oracle")
+        assert_close(got, reference_f64_q4(q, kc, vc, ks, vs, pos, n_heads, n_kv), *F64_TOL,
+                     what=f"q4 replay at {pos} vs f64")
 
 
 @pytest.mark.parametrize("n,H,K,ctx,pos0", [(7, 8, 2, 40, 11), (1, 16, 2, 5000, 4999), (200, 4, 1, 260, 50),
@@ -179,7 +188,7 @@ def test_q4_layer_end_to_end(gpu):
     got = out.cpu().numpy()
     c = [t.cpu().numpy().reshape(ctx, -1) for t in (kc, vc, ks, vs)]
     c[2], c[3] = c[2].view(np.uint16), c[3].view(np.uint16)
-    assert_close(got, O.decode_tc256_q4(qrot.cpu().numpy(), *c, n - 1, H, K), what="q4 e2e vs oracle")
+    assert_close(got, O.decode_tc256_q4(qrot.cpu().numpy(), *c, n - 1, H, K), *REF_ORACLE_TOL, what="q4 e2e vs oracle")
     back = O.kv4_fwht(got.reshape(-1, 256)).reshape(1, -1)
     from attn_common import _reference_f64_values
     exact = _reference_f64_values(qkv[n - 1:, :H * 256], qkv[:, H * 256:(H + K) * 256], qkv[:, (H + K) * 256:],
@@ -260,11 +269,9 @@ def test_attention_operator_q4(gpu, n, pos0, exact):
     gi_attn.hadamard_rows(out)
     torch.cuda.synchronize()
     q = np.ascontiguousarray(qkv[:, :n_heads * 256])
-    split_path = n < 16 or exact
     rot = reference_f64_q4(q, kc, vc, ks, vs, pos0, n_heads, n_kv)
     want = (rot.reshape(-1, 256) @ _h256()).reshape(rot.shape)
-    assert_close(out.cpu().numpy(), want, max_abs=2e-5 if split_path else 2e-3, rel_l2=2e-5 if split_path else 1e-3,
-                 what="operator q4 (rotated back) vs f64")
+    assert_close(out.cpu().numpy(), want, *F64_TOL, what="operator q4 (rotated back) vs f64")
 
 
 def _h256():

@@ -1,6 +1,8 @@
 """Randomised decode shapes through every cache format and head size, against float64 attention over the
-cache's values (the split path's bar: 2e-5 max-abs and relative L2): token counts 1-15, spans up to 6000
-keys, group sizes 1-8 and 1-8 kv heads, seeded so that a failure names its case and reproduces."""
+cache's values (the split path's bar: 2e-5 max-abs and relative L2; head size 256 over the int8 and 4-bit caches,
+which round Q and P to f16 as the reference's attention_decode_tc256 does, the north star's bar) and, for those, the
+oracle's restatement of attention_decode_tc256 (REF_ORACLE_TOL): token counts 1-15, spans up to 6000 keys, group
+sizes 1-8 and 1-8 kv heads, seeded so that a failure names its case and reproduces."""
 import sys
 
 import numpy as np
@@ -8,8 +10,9 @@ import pytest
 import torch
 
 import gi_attn
-from attn_common import (assert_close, make_inputs, make_inputs_i8, make_inputs_q4, reference_f64, reference_f64_i8,
-                         reference_f64_q4)
+import gi_oracle as O
+from attn_common import (REF_ORACLE_TOL, assert_close, make_inputs, make_inputs_i8, make_inputs_q4, reference_f64,
+                         reference_f64_i8, reference_f64_q4, split_f64_tol)
 
 pytestmark = pytest.mark.gpu
 
@@ -50,11 +53,16 @@ def test_random_decode(gpu, fmt, i, n_tok, pos0, n_heads, n_kv, hd):
         t = [torch.from_numpy(x).to(gpu) for x in (q, k, v, ks, vs)]
         out = gi_attn.decode(t[0], t[1], t[2], pos0, n_heads, n_kv, hd=hd, k_scale=t[3], v_scale=t[4])
         want = reference_f64_i8(q, k, v, ks, vs, pos0, n_heads, n_kv, hd=hd)
+        ref = O.decode_tc256_i8(q, k, v, ks, vs, pos0, n_heads, n_kv) if hd == 256 else None
     else:
         q, kc, vc, ks, vs = make_inputs_q4(seed, n_tok, pos0 + n_tok, n_heads, n_kv)
         c = [torch.from_numpy(np.ascontiguousarray(x)).to(gpu).view(-1, n_kv, 128) for x in (kc, vc)]
         s = [torch.from_numpy(np.ascontiguousarray(x).view(np.float16)).to(gpu).view(-1, n_kv, 8) for x in (ks, vs)]
         out = gi_attn.decode_q4(torch.from_numpy(q).to(gpu), c[0], c[1], s[0], s[1], pos0, n_heads, n_kv)
         want = reference_f64_q4(q, kc, vc, ks, vs, pos0, n_heads, n_kv)
+        ref = O.decode_tc256_q4(q, kc, vc, ks, vs, pos0, n_heads, n_kv)
     torch.cuda.synchronize()
-    assert_close(out.cpu().numpy(), want, max_abs=2e-5, rel_l2=2e-5, what=f"{fmt} case {i}")
+    got = out.cpu().numpy()
+    if fmt != "f16" and hd == 256:
+        assert_close(got, ref, *REF_ORACLE_TOL, what=f"{fmt} case {i} vs oracle")
+    assert_close(got, want, *split_f64_tol(fmt, hd), what=f"{fmt} case {i}")
