@@ -163,12 +163,14 @@ struct Module {
     hipModule_t mod = nullptr;
     hipFunction_t dec[2] = {};        // up to 8 pairs, head size 128: [int8 cache]
     hipFunction_t dec256 = nullptr;   // up to 8 pairs, head size 256, the f16 cache
+    hipFunction_t dec64[2][3] = {};   // head size 64: [int8 cache][up to 8 pairs, one column block, two]
     hipFunction_t dec_pm[2][2] = {};  // [int8 cache][column blocks - 1]: one pair per column
     hipFunction_t dec_ws2[2] = {};    // head size 128, two column blocks, two pair sets of two waves: [int8 cache]
     hipFunction_t dec_ref[3] = {};    // head size 256, one pair per column, the reference's tc256 roundings: int8
                                       // one column block, 4-bit one and two column blocks
     hipFunction_t dec_pm256[2] = {};  // head size 256, one pair per column, two pair sets of two waves: [f16, int8]
     hipFunction_t prefill[2] = {};   // [int8 cache], head size 128
+    hipFunction_t prefill64[2] = {}; // [int8 cache], head size 64 (the same launch shape and block size)
     hipFunction_t prefill256r = nullptr; // head size 256 (f16 cache), 16 rows per wave: one workgroup per query tile
     hipFunction_t prefill256r_fmt[2] = {}; // the same over the int8 and the 4-bit cache
     hipFunction_t combine = nullptr, rope = nullptr, relayout = nullptr, hadamard = nullptr;
@@ -208,6 +210,12 @@ int load_module(const char* path, Module** out) {
             {&m.dec[0], "gi_decode_partial_1"},
             {&m.dec[1], "gi_decode_partial_1_i8"},
             {&m.dec256, "gi_decode_partial_1_h256"},
+            {&m.dec64[0][0], "gi_decode_partial_1_h64"},
+            {&m.dec64[0][1], "gi_decode_pm_1_h64"},
+            {&m.dec64[0][2], "gi_decode_pm_2_h64"},
+            {&m.dec64[1][0], "gi_decode_partial_1_i8_h64"},
+            {&m.dec64[1][1], "gi_decode_pm_1_i8_h64"},
+            {&m.dec64[1][2], "gi_decode_pm_2_i8_h64"},
             {&m.dec_ref[0], "gi_decode_pm_1_i8_h256"},
             {&m.dec_ref[1], "gi_decode_pm_1_q4"},
             {&m.dec_ref[2], "gi_decode_pm_2_q4"},
@@ -224,6 +232,8 @@ int load_module(const char* path, Module** out) {
             {&m.hadamard, "gi_hadamard_rows"},
             {&m.prefill[0], "gi_prefill_fwd"},
             {&m.prefill[1], "gi_prefill_fwd_i8"},
+            {&m.prefill64[0], "gi_prefill_fwd_h64"},
+            {&m.prefill64[1], "gi_prefill_fwd_h64_i8"},
             {&m.prefill256r, "gi_prefill_fwd_h256r"},
             {&m.prefill256r_fmt[0], "gi_prefill_fwd_h256r_i8"},
             {&m.prefill256r_fmt[1], "gi_prefill_fwd_h256r_q4"},
@@ -333,6 +343,12 @@ DecVariant dec_variant(int n_tok, int G, int hd = 128, int fmt = 0) {
     }
     DecVariant v{1, false, pairs > kDecPairs, 1};
     if (!v.pm) return v;
+    if (hd == 64) {
+        // one pair per column: one column block up to 16 pairs, else two per wave (32 pairs per workgroup)
+        v.ncb = pairs > 2 * kDecPairs ? 2 : 1;
+        v.groups = (pairs + 2 * kDecPairs * v.ncb - 1) / (2 * kDecPairs * v.ncb);
+        return v;
+    }
     if (hd == 256) {
         // two pair sets of 16 per workgroup, each over two waves that split the slice's tiles (two column
         // blocks per wave exceed the register file at this head size). Split kernel at 32768 keys, 16/2, against
@@ -408,10 +424,11 @@ int check_scales(const float* ks, const float* vs, long long sc_stride, long lon
 // Keys per slice unit: one tile per wave (32 f16 keys at head size 128, 64 int8 keys, 16 f16 keys at 256).
 int slice_unit(bool i8, int hd) { return hd == 256 ? kDecWaves * kDecTile / 2 : i8 ? 2 * kSliceUnit : kSliceUnit; }
 
-// hd256: whether the entry point takes head size 256 as well as 128.
-int check_shape(int n_heads, int n_kv, int hd, bool hd256 = false) {
-    if (hd != 128 && !(hd256 && hd == 256))
-        return fail("head size %d unsupported (the gfx950 kernels take 128%s)", hd, hd256 ? " or 256" : "");
+// Head sizes 64 (attn_prefill_tc<64>, src/cuda.rs:2620; attention_partial_gqa at any multiple of 32), 128 and 256
+// (the 4-bit cache: 256 only, checked by its entry points).
+int check_shape(int n_heads, int n_kv, int hd, bool = true) {
+    if (hd != 64 && hd != 128 && hd != 256)
+        return fail("head size %d unsupported (the gfx950 kernels take 64, 128 or 256)", hd);
     if (n_kv <= 0 || n_heads <= 0 || n_heads % n_kv != 0)
         return fail("n_heads %d must be a positive multiple of n_kv %d", n_heads, n_kv);
     return 0;
@@ -483,7 +500,8 @@ int decode_impl(void* stream, const float* q, long long q_stride, const void* kc
         a.sc_head_stride = sc_head_stride;
     }
     hipStream_t st = (hipStream_t)stream;
-    hipFunction_t f = hd == 256 ? (var.ws2 ? m->dec_pm256[fmt] : fmt ? m->dec_ref[fmt - 1 + var.ncb - 1]
+    hipFunction_t f = hd == 64    ? m->dec64[i8][var.pm ? var.ncb : 0]
+                      : hd == 256 ? (var.ws2 ? m->dec_pm256[fmt] : fmt ? m->dec_ref[fmt - 1 + var.ncb - 1]
                                    : var.pm ? m->dec_pm256[0] : m->dec256)
                       : var.ws2   ? m->dec_ws2[i8]
                       : var.pm    ? m->dec_pm[i8][var.ncb - 1]
@@ -616,7 +634,8 @@ int prefill_impl(void* stream, const void* q, int q_dtype, long long q_stride, c
         return launch(kPrefill, fmt ? m->prefill256r_fmt[fmt - 1] : m->prefill256r, dim3((n + kPrefill256rRows - 1) / kPrefill256rRows * n_heads, 1, 1),
                       dim3(m->prefill256r_threads), (hipStream_t)stream, &a, sizeof a);
     const int qtiles = (n + kPrefillRows - 1) / kPrefillRows; // one workgroup per (head, 256 query rows)
-    return launch(kPrefill, m->prefill[i8], dim3(qtiles * n_heads, 1, 1), dim3(m->prefill_threads[i8]),
+    return launch(kPrefill, hd == 64 ? m->prefill64[i8] : m->prefill[i8], dim3(qtiles * n_heads, 1, 1),
+                  dim3(m->prefill_threads[i8]),
                   (hipStream_t)stream, &a, sizeof a);
 }
 

@@ -182,6 +182,10 @@ __device__ __forceinline__ float row_bcast(float v) {
 // 8 dims, plus the scale of key `lane` of the tile.
 template <bool I8, int HD> struct DecBuf { u4 k[2][4]; u4 v[8]; };
 template <> struct DecBuf<true, 128> { u4 k[4][2]; u2 v[16]; float ksc, vsc; };
+// head size 64: the head-128 tiles with half the K k-steps; V 8 keys x 4 dims (4c..4c+3) as f16, 16 keys x 4 dims
+// as int8 (the second word unused)
+template <> struct DecBuf<false, 64> { u4 k[2][2]; u2 v[8]; };
+template <> struct DecBuf<true, 64> { u4 k[4][1]; u2 v[16]; float ksc, vsc; };
 // head size 256 (f16): 16 keys; K row c of the tile, 8 k-steps of 32 dims; V keys 4grp..4grp+3, dims 16c..16c+15
 template <> struct DecBuf<false, 256> { u4 k[8]; u4 v[4][2]; };
 // head size 256 over the int8 cache: 16 keys; K row c, bytes 64i + 16grp .. +15 (k-steps 2i, 2i + 1); V keys
@@ -243,7 +247,7 @@ __device__ __forceinline__ uint32_t q4_f16x2(uint32_t hi, uint32_t lo, int j, h2
 // 16-byte loads are whole scale groups.
 template <int NCB, int WS, bool I8, int HD = 128, bool PM = false, bool Q4 = false>
 __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
-    static_assert(HD == 128 || HD == 256, "head sizes: 128, 256");
+    static_assert(HD == 64 || HD == 128 || HD == 256, "head sizes: 64, 128, 256");
     static_assert(!Q4 || (HD == 256 && !I8), "the 4-bit cache: head size 256");
     // the reference's tc256 arithmetic (one f16 Q, one f16 P; see DEC_REF_VB): head size 256 over the int8 and
     // 4-bit caches, which these kernels serve with one pair per column
@@ -256,7 +260,7 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
     constexpr int CPAIRS = PM ? 2 * DEC_PAIRS : DEC_PAIRS; // pairs per column block
     constexpr int TILE = HD == 256 ? DEC_TILE / 2 : I8 ? 2 * DEC_TILE : DEC_TILE; // keys per wave tile
     constexpr int KK = HD / 32;                 // QK k-steps
-    constexpr int ND = HD == 256 ? 16 : 8;      // O^T MFMA blocks
+    constexpr int ND = HD / 16;                 // O^T MFMA blocks
     constexpr int PART = HD + 4;                // floats per slice partial
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -352,7 +356,8 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
     const int krow0 = 8 * (c >> 2) + (c & 3);
     const int koff0 = (krow0 * (int)kvs + 8 * grp) * 2;
     const int koff1 = koff0 + 4 * (int)kvs * 2;
-    const int voff = (8 * grp * (int)kvs + 8 * c) * 2;
+    // (head size 64: V dims 4c..4c+3, so O^T block dd has rows m = dims 4m + dd)
+    const int voff = (8 * grp * (int)kvs + (HD == 64 ? 4 : 8) * c) * 2;
     const int vstep = (int)kvs * 2;
     constexpr int STRIDE = WS * TILE; // keys between a wave's consecutive tiles
     // int8 element offsets (bytes): key rows of block 0 and the V rows of this lane; scales
@@ -362,7 +367,7 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
     const float* kscl = I8 ? a.ks + (long long)k_begin * scs + kvh * a.sc_head_stride : nullptr;
     const float* vscl = I8 ? a.vs + (long long)k_begin * scs + kvh * a.sc_head_stride : nullptr;
     const int koff8 = (16 * (c >> 2) + (c & 3)) * (int)kvs + 16 * grp;
-    const int voff8 = 16 * grp * (int)kvs + 8 * c;
+    const int voff8 = 16 * grp * (int)kvs + (HD == 64 ? 4 : 8) * c;
     const int scoff = lane * (int)scs * 4;
     // head size 256: K row c, dims 8grp + 32kk; V keys 4grp + i, dims 16c..16c+15
     const int koff256 = (c * (int)kvs + 8 * grp) * 2;
@@ -409,13 +414,13 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
 #pragma unroll
             for (int b = 0; b < 4; b++) {
                 B.k[b][0] = gi_load16p<CPOL>(r, koff8 + 4 * b * (int)kvs);
-                B.k[b][1] = gi_load16p<CPOL>(r, koff8 + 4 * b * (int)kvs + 64);
+                if constexpr (HD == 128) B.k[b][1] = gi_load16p<CPOL>(r, koff8 + 4 * b * (int)kvs + 64);
             }
             B.ksc = gi_load4f(gi_rsrc(kscl + (long long)t * scs, (long long)(nkeys - t) * scs * 4), scoff);
         } else {
             __amdgpu_buffer_rsrc_t r = gi_rsrc(kslice + (long long)t * kvs, (long long)(nkeys - t) * kvs * 2);
 #pragma unroll
-            for (int kk = 0; kk < 4; kk++) {
+            for (int kk = 0; kk < KK; kk++) {
                 B.k[0][kk] = gi_load16p<CPOL>(r, koff0 + 64 * kk);
                 B.k[1][kk] = gi_load16p<CPOL>(r, koff1 + 64 * kk);
             }
@@ -445,12 +450,18 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
         } else if constexpr (I8) {
             __amdgpu_buffer_rsrc_t r = gi_rsrc(vslice8 + (long long)t * kvs, (long long)(nkeys - t) * kvs);
 #pragma unroll
-            for (int i = 0; i < 16; i++) B.v[i] = gi_load8p<CPOL>(r, voff8 + i * (int)kvs);
+            for (int i = 0; i < 16; i++) {
+                if constexpr (HD == 64) B.v[i] = u2{__builtin_amdgcn_raw_buffer_load_b32(r, voff8 + i * (int)kvs, 0, CPOL), 0u};
+                else B.v[i] = gi_load8p<CPOL>(r, voff8 + i * (int)kvs);
+            }
             B.vsc = gi_load4f(gi_rsrc(vscl + (long long)t * scs, (long long)(nkeys - t) * scs * 4), scoff);
         } else {
             __amdgpu_buffer_rsrc_t r = gi_rsrc(vslice + (long long)t * kvs, (long long)(nkeys - t) * kvs * 2);
 #pragma unroll
-            for (int i = 0; i < 8; i++) B.v[i] = gi_load16p<CPOL>(r, voff + i * vstep);
+            for (int i = 0; i < 8; i++) {
+                if constexpr (HD == 64) B.v[i] = gi_load8p<CPOL>(r, voff + i * vstep);
+                else B.v[i] = gi_load16p<CPOL>(r, voff + i * vstep);
+            }
         }
     };
     // One tile from buffer B at key offset t; with `reload`, B is refilled with the tile DEC_NB tiles on.
@@ -463,7 +474,7 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
             for (int b = 0; b < 2; b++) {
                 sacc[cb][b] = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-                for (int kk = 0; kk < 4; kk++) {
+                for (int kk = 0; kk < KK; kk++) {
                     sacc[cb][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, B.k[b][kk]), qf[cb][kk],
                                                                          sacc[cb][b], 0, 0, 0);
                     if constexpr (PM)
@@ -508,7 +519,7 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
                 m_run[cb] = m_new;
                 l_run[cb] *= alpha;
 #pragma unroll
-                for (int dd = 0; dd < 8; dd++) o[cb][dd] *= alpha;
+                for (int dd = 0; dd < ND; dd++) o[cb][dd] *= alpha;
             }
             const float m_use = m_run[cb] == GI_NEG_INF ? 0.f : m_run[cb]; // no key seen yet: p = 0
             float psum = 0.f;
@@ -526,9 +537,10 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
             }
             l_run[cb] += psum;
         }
-        // O^T += V^T P^T, V^T built one dim group at a time: vt = the 8 keys' values of dim 8c + dd
+        // O^T += V^T P^T, V^T built one dim group at a time: vt = the 8 keys' values of dim 8c + dd (head size
+        // 64: 4c + dd)
 #pragma unroll
-        for (int dd = 0; dd < 8; dd++) {
+        for (int dd = 0; dd < ND; dd++) {
             u4 w;
 #pragma unroll
             for (int p = 0; p < 4; p++) // halves dd % 2 of keys 2p (low) and 2p + 1 (high): one v_perm
@@ -547,9 +559,9 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
     auto qk_i8 = [&](auto& B, f4 (&sacc)[NCB][4]) {
 #pragma unroll
         for (int b = 0; b < 4; b++) {
-            u4 kf[4]; // k-step kk: dims 16grp + 8(kk%2) + 64(kk/2) of this block's key, as f16 pairs
+            u4 kf[KK]; // k-step kk: dims 16grp + 8(kk%2) + 64(kk/2) of this block's key, as f16 pairs
 #pragma unroll
-            for (int half = 0; half < 2; half++)
+            for (int half = 0; half < HD / 64; half++)
 #pragma unroll
                 for (int e = 0; e < 4; e++) {
                     const uint32_t x = gi_i8_in(B.k[b][half][e]);
@@ -560,7 +572,7 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
             for (int cb = 0; cb < NCB; cb++) {
                 sacc[cb][b] = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-                for (int kk = 0; kk < 4; kk++) {
+                for (int kk = 0; kk < KK; kk++) {
                     sacc[cb][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, kf[kk]), qf[cb][kk],
                                                                          sacc[cb][b], 0, 0, 0);
                     if constexpr (PM)
@@ -577,7 +589,7 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
 #pragma unroll
         for (int i = 0; i < 16; i++) B.v[i] = u2{gi_i8_in(B.v[i][0]), gi_i8_in(B.v[i][1])};
 #pragma unroll
-        for (int dd = 0; dd < 8; dd += 2) {
+        for (int dd = 0; dd < ND; dd += 2) {
             const int wi = dd >> 2, k = dd & 3;
             const uint32_t sel = (uint32_t)k | (uint32_t)(k + 4) << 8 | (uint32_t)(k + 1) << 16 | (uint32_t)(k + 5) << 24;
 #pragma unroll
@@ -645,7 +657,7 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
                 m_run[cb] = m_new;
                 l_run[cb] *= alpha;
 #pragma unroll
-                for (int dd = 0; dd < 8; dd++) o[cb][dd] *= alpha;
+                for (int dd = 0; dd < ND; dd++) o[cb][dd] *= alpha;
             }
             const float m_use = m_run[cb] == GI_NEG_INF ? 0.f : m_run[cb];
             float psum = 0.f;
@@ -823,11 +835,11 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
     // (s * kscale - max) in one FMA each before the row max, and P V takes p times the value scale.
     constexpr int PB = HD == 256 ? 1 : I8 ? 4 : 2;              // S^T blocks of 16 keys per column block
     typedef typename gi_pick<HD == 256, h4x, h8>::type PT;     // PV B operand: 16 or 32 keys of one column
-    typedef typename gi_pick<I8 && HD == 128, PT[2], PT>::type PE; // a column's P^T for the tile (int8: 2 k-steps)
+    typedef typename gi_pick<I8 && HD != 256, PT[2], PT>::type PE; // a column's P^T for the tile (int8: 2 k-steps)
     struct PipeS { f4 v[NCB][PB]; float ksc; };
     struct PipeP { PE hi[NCB], lo[NCB]; };
     auto pm_qk = [&](auto& B, PipeS& S) {
-        if constexpr (I8 && HD == 128) {
+        if constexpr (I8 && HD != 256) {
             f4 sacc[NCB][4];
             qk_i8(B, sacc);
 #pragma unroll
@@ -935,7 +947,7 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
                 const float hi = __uint_as_float(__float_as_uint(pv) & 0xffffe000u);
                 if constexpr (REF) {
                     P.hi[cb][i] = (_Float16)pv; // rounded once, as the reference's pack_h2 (src/cuda.rs:2723)
-                } else if constexpr (I8 && HD == 128) {
+                } else if constexpr (I8 && HD != 256) {
                     P.hi[cb][i >> 3][i & 7] = (_Float16)hi;
                     P.lo[cb][i >> 3][i & 7] = (_Float16)(pv - hi);
                 } else {
@@ -953,7 +965,7 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
             pv_i8(B, P.hi, P.lo);
         } else {
 #pragma unroll
-            for (int dd = 0; dd < 8; dd++) {
+            for (int dd = 0; dd < ND; dd++) {
                 u4 w;
 #pragma unroll
                 for (int p = 0; p < 4; p++)
@@ -1097,12 +1109,14 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
     constexpr float LO = I8 ? 1.f / DEC_I8_LO : 1.f;      // the remainder column's scale (PM: no column)
     constexpr float OSC = 1.f / PBIAS; // the bias on P (int8 with one pair per column)
     // all LDS reads of the thread's items are issued before any arithmetic, so the merge waits for LDS once
-    constexpr int ITEMS = WG_PAIRS * HD / 1024;
+    // (head size 64 with 8 pairs: 128 items, so threads 128-255 have none)
+    constexpr int NITEM = WG_PAIRS * HD / 4, ITEMS = (NITEM + 255) / 256;
     float mw[ITEMS][WS], lw[ITEMS][WS];
     float4 ohi[ITEMS][WS], olo[ITEMS][WS];
 #pragma unroll
     for (int it = 0; it < ITEMS; it++) {
         const int item = threadIdx.x + 256 * it;
+        if (NITEM % 256 && item >= NITEM) break;
         const int pl = item / (HD / 4), d4 = 4 * (item % (HD / 4)); // pair within the workgroup
         const int w0 = (pl / (CPAIRS * NCB)) * WS;                    // the waves holding the pair
         const int lp = pl % (CPAIRS * NCB);                            // the pair within those waves
@@ -1118,6 +1132,7 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
 #pragma unroll
     for (int it = 0; it < ITEMS; it++) {
         const int item = threadIdx.x + 256 * it;
+        if (NITEM % 256 && item >= NITEM) break;
         const int pl = item / (HD / 4), d4 = 4 * (item % (HD / 4));
         const int pi = gz * WG_PAIRS + pl;
         float M = GI_NEG_INF;
@@ -1166,6 +1181,15 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
 #define GI_DEC_PM_KERNEL(name, NCB, WS, I8) \
     extern "C" __global__ void __launch_bounds__(256, DEC_MINWG) name(GiDecodeArgs a) { gi_decode_partial_t<NCB, WS, I8, 128, true>(a); }
 GI_DEC_KERNEL(gi_decode_partial_1, 1, DEC_WAVES, false, 128)
+// head size 64 (the reference's attention_partial_gqa at any head size a multiple of 32, src/cuda.rs:1684-1865)
+#define GI_DEC_PM64_KERNEL(name, NCB, I8) \
+    extern "C" __global__ void __launch_bounds__(256, DEC_MINWG) name(GiDecodeArgs a) { gi_decode_partial_t<NCB, DEC_WAVES, I8, 64, true>(a); }
+GI_DEC_KERNEL(gi_decode_partial_1_h64, 1, DEC_WAVES, false, 64)
+GI_DEC_KERNEL(gi_decode_partial_1_i8_h64, 1, DEC_WAVES, true, 64)
+GI_DEC_PM64_KERNEL(gi_decode_pm_1_h64, 1, false)
+GI_DEC_PM64_KERNEL(gi_decode_pm_2_h64, 2, false)
+GI_DEC_PM64_KERNEL(gi_decode_pm_1_i8_h64, 1, true)
+GI_DEC_PM64_KERNEL(gi_decode_pm_2_i8_h64, 2, true)
 GI_DEC_KERNEL(gi_decode_partial_1_i8, 1, DEC_WAVES, true, 128)
 GI_DEC_KERNEL(gi_decode_partial_1_h256, 1, DEC_WAVES, false, 256)
 GI_DEC_PM_KERNEL(gi_decode_pm_1, 1, DEC_WAVES, false)
@@ -1350,9 +1374,12 @@ typedef short gi_s4 __attribute__((__vector_size__(8))); // 4 f16 as ds_read_b64
 // and the tile's 64 key and value scales go to LDS beside it. Scores are the integer-key dot products
 // times the key scale (QK chains start from zero; s = acc * kscale - m); P V takes f16(p * vscale *
 // PF_I8_VBIAS) and the row sum the f16-rounded p, as the reference's pv / pf.
-template <bool I8>
+// HD = 64 (attn_prefill_tc<64>, src/cuda.rs:2620): the same kernel with half the QK k-steps and O^T blocks. The
+// LDS image keeps the head-128 layout: each 128-byte row sits in a 256-byte slot, its 8 units at the swizzled
+// positions the operand reads compute (the staging loads of the other 8 positions are switched off by lane).
+template <bool I8, int HD = 128>
 __device__ __forceinline__ void gi_prefill_t(const GiPrefillArgs& a) {
-    constexpr int HD = 128;
+    static_assert(HD == 64 || HD == 128, "head sizes 64, 128 (256: gi_prefill256r)");
     constexpr int WAVES = PF_WAVES;
     constexpr int BQ = 32 * WAVES;  // query rows per workgroup
     constexpr int SW = WAVES / 2;   // waves staging each of K and V
@@ -1387,11 +1414,13 @@ __device__ __forceinline__ void gi_prefill_t(const GiPrefillArgs& a) {
     const bool stage_v = wave >= SW;
     const uint16_t* sbase = (stage_v ? a.vc : a.kc) + kvh * a.kv_head_stride;
     int soff[LPW];
+    bool sval[LPW]; // head size 64: the lane's LDS unit holds one of the row's 8 units
 #pragma unroll
     for (int i = 0; i < LPW; i++) {
         const int r = 4 * (LPW * (wave % SW) + i) + (lane >> 4);
         const int u = (lane & 15) ^ (stage_v ? ((r & 3) << 2) : (r & 15));
         soff[i] = (r * (int)kvs + 8 * u) * 2;
+        sval[i] = u < HD / 8;
     }
     auto stage = [&](int t) {
         const int t0 = t * BK;
@@ -1399,11 +1428,15 @@ __device__ __forceinline__ void gi_prefill_t(const GiPrefillArgs& a) {
         const long long bytes = (long long)(kv_len - t0) * kvs * 2;
         unsigned char* dst = &smem[t & (PF_NBUF - 1)][stage_v ? 1 : 0][1024 * LPW * (wave % SW)];
 #pragma unroll
-        for (int i = 0; i < LPW; i++) gi_stage16(src, bytes, (GI_LDS void*)(dst + 1024 * i), soff[i]);
+        for (int i = 0; i < LPW; i++)
+            if (HD == 128 || sval[i]) gi_stage16(src, bytes, (GI_LDS void*)(dst + 1024 * i), soff[i]);
     };
     // int8 staging: thread -> tile row sr, 16-byte chunk sch (dims 16sch..16sch+15) of K and of V; threads
     // 0-63 also take the K scale of key tid, 64-127 the V scale of key tid-64 (times PF_I8_VBIAS)
-    const int sr = tid >> 3, sch = tid & 7;
+    // (head size 64: rows of 4 chunks, threads 0-255)
+    constexpr int NCH = HD / 16;
+    const int sr = tid / NCH, sch = tid % NCH;
+    const bool stager = tid < PF_BK * NCH;
     const int8_t* kb8 = reinterpret_cast<const int8_t*>(a.kc) + kvh * a.kv_head_stride;
     const int8_t* vb8 = reinterpret_cast<const int8_t*>(a.vc) + kvh * a.kv_head_stride;
     const float* scb = I8 ? (tid < 64 ? a.ks : a.vs) + kvh * a.sc_head_stride : nullptr;
@@ -1418,10 +1451,12 @@ __device__ __forceinline__ void gi_prefill_t(const GiPrefillArgs& a) {
         const int off = sr * (int)kvs + 16 * sch;
         const __amdgpu_buffer_rsrc_t rsk = gi_rsrc(kb8 + (long long)t0 * kvs, (long long)(kv_len - t0) * kvs);
         const __amdgpu_buffer_rsrc_t rsv = gi_rsrc(vb8 + (long long)t0 * kvs, (long long)(kv_len - t0) * kvs);
-        const u2 k0 = gi_load8(rsk, off + 8 * flip), k1 = gi_load8(rsk, off + 8 - 8 * flip);
-        const u2 v0 = gi_load8(rsv, off + 8 * flip), v1 = gi_load8(rsv, off + 8 - 8 * flip);
-        rk = u4{k0.x, k0.y, k1.x, k1.y};
-        rv = u4{v0.x, v0.y, v1.x, v1.y};
+        if (stager) {
+            const u2 k0 = gi_load8(rsk, off + 8 * flip), k1 = gi_load8(rsk, off + 8 - 8 * flip);
+            const u2 v0 = gi_load8(rsv, off + 8 * flip), v1 = gi_load8(rsv, off + 8 - 8 * flip);
+            rk = u4{k0.x, k0.y, k1.x, k1.y};
+            rv = u4{v0.x, v0.y, v1.x, v1.y};
+        }
         if (tid < 2 * PF_BK)
             rsc = gi_load4f(gi_rsrc(scb + (long long)t0 * a.sc_stride, (long long)(kv_len - t0) * a.sc_stride * 4),
                             (tid & (PF_BK - 1)) * (int)a.sc_stride * 4);
@@ -1431,6 +1466,7 @@ __device__ __forceinline__ void gi_prefill_t(const GiPrefillArgs& a) {
         unsigned char* V = &smem[t & (PF_NBUF - 1)][1][sr * 256];
 #pragma unroll
         for (int hw = 0; hw < 2; hw++) { // f16 unit 2sch + (hw ^ flip): dims 16sch + 8(hw ^ flip) .. +7
+            if (!stager) break;
             const int u = 2 * sch + (hw ^ flip);
             u4 kw, vw;
 #pragma unroll
@@ -1514,10 +1550,10 @@ __device__ __forceinline__ void gi_prefill_t(const GiPrefillArgs& a) {
         for (int st = 0; st < PF_KPF; st++) kf[st] = kfrag(K, st);
         __builtin_amdgcn_sched_barrier(0); // the first PF_KPF reads go out before any of the MFMAs
 #pragma unroll
-        for (int st = 0; st < 16; st++) {
+        for (int st = 0; st < 2 * KS; st++) {
             const int ks = st >> 1, bb = st & 1;
             const h8 cur = kf[st % PF_KPF];
-            if (st + PF_KPF < 16) kf[st % PF_KPF] = kfrag(K, st + PF_KPF);
+            if (st + PF_KPF < 2 * KS) kf[st % PF_KPF] = kfrag(K, st + PF_KPF);
             s[bb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(cur, qf[ks], ks == 0 ? (I8 ? f16x{} : negm) : s[bb], 0, 0, 0);
         }
     };
@@ -1639,9 +1675,9 @@ __device__ __forceinline__ void gi_prefill_t(const GiPrefillArgs& a) {
         // MFMAs on (the compiler otherwise reads each fragment just before its MFMA). Interleaving the
         // softmax VALU or the V reads by further groups measured no better.
 #pragma unroll
-        for (int i = 0; i < 16; i++) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                      // MFMA
-            if (i + PF_KPF < 16) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0); // its K refill
+        for (int i = 0; i < 2 * KS; i++) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                          // MFMA
+            if (i + PF_KPF < 2 * KS) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0); // its K refill
         }
     };
     // Iteration it: before the barrier each wave waits for its own loads of tile it+1 (tile it+2's may
@@ -2137,6 +2173,8 @@ __device__ __forceinline__ void gi_prefill256r(const GiPrefillArgs& a) {
 
 extern "C" __global__ void __launch_bounds__(64 * PF_WAVES, 1) gi_prefill_fwd(GiPrefillArgs a) { gi_prefill_t<false>(a); }
 extern "C" __global__ void __launch_bounds__(64 * PF_WAVES, 1) gi_prefill_fwd_i8(GiPrefillArgs a) { gi_prefill_t<true>(a); }
+extern "C" __global__ void __launch_bounds__(64 * PF_WAVES, 1) gi_prefill_fwd_h64(GiPrefillArgs a) { gi_prefill_t<false, 64>(a); }
+extern "C" __global__ void __launch_bounds__(64 * PF_WAVES, 1) gi_prefill_fwd_h64_i8(GiPrefillArgs a) { gi_prefill_t<true, 64>(a); }
 #ifndef PF256R_KBUF
 #define PF256R_KBUF 2 // K tile buffers of gi_prefill_fwd_h256r
 #endif

@@ -19,6 +19,7 @@
 //   gio_kv_quant_i8                   src/cuda.rs:333-339 (kv_store with KV8: row max / 127, rint)
 //   gio_qk_norm_rope_i8               src/cuda.rs:437-486 storing with kv_quant_i8
 //   gio_prefill_tc256                 gio_prefill_tc at head size 256 (attention_prefill_tc256, src/cuda.rs:2623)
+//   gio_prefill_tc64 / _tc64_i8       gio_prefill_tc at head size 64 (attention_prefill_tc64, src/cuda.rs:2620), f16 / KV8
 //   gio_prefill_tc_i8 / _tc256_i8     gio_prefill_tc (head size 128 / 256) over the KV8 cache (src/cuda.rs:2466-2498, 2548-2605:
 //                                     integer keys, score times key scale, P V with f16(p * vs * 2^10))
 //   gio_decode_gpu_i8                 gio_decode_gpu over the KV8 cache (src/cuda.rs:209-226, 1758-1760,
@@ -753,6 +754,20 @@ void gio_prefill_tc_i8(const float* q, long q_stride, const int8_t* kc, const in
                        const float* vs, long kv_stride, float* out, long out_stride, int pos0, int n, int n_heads,
                        int n_kv, float scale, int threads) {
     prefill_tc<int8_t>(q, q_stride, kc, vc, ks, vs, kv_stride, out, out_stride, pos0, n, n_heads, n_kv, scale, threads);
+}
+
+// attn_prefill_tc<64> (attention_prefill_tc64, src/cuda.rs:2620): gio_prefill_tc's arithmetic at head size 64, over
+// the f16 and the KV8 cache.
+void gio_prefill_tc64(const float* q, long q_stride, const uint16_t* kc, const uint16_t* vc, long kv_stride, float* out,
+                      long out_stride, int pos0, int n, int n_heads, int n_kv, float scale, int threads) {
+    prefill_tc<uint16_t>(q, q_stride, kc, vc, nullptr, nullptr, kv_stride, out, out_stride, pos0, n, n_heads, n_kv, scale,
+                         threads, 64);
+}
+void gio_prefill_tc64_i8(const float* q, long q_stride, const int8_t* kc, const int8_t* vc, const float* ks,
+                         const float* vs, long kv_stride, float* out, long out_stride, int pos0, int n, int n_heads,
+                         int n_kv, float scale, int threads) {
+    prefill_tc<int8_t>(q, q_stride, kc, vc, ks, vs, kv_stride, out, out_stride, pos0, n, n_heads, n_kv, scale, threads,
+                       64);
 }
 
 // attention_prefill_tc256 with KV8 (attn_prefill_tc<256, 2>, src/cuda.rs:2623): gio_prefill_tc_i8's arithmetic at

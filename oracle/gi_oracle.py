@@ -51,6 +51,8 @@ def lib():
         L.gio_kv_quant_i8.argtypes = [vp, l, i, vp, vp]
         L.gio_prefill_tc_i8.argtypes = [vp, l, vp, vp, vp, vp, l, vp, l, i, i, i, i, f, i]
         L.gio_prefill_tc256.argtypes = [vp, l, vp, vp, l, vp, l, i, i, i, i, f, i]
+        L.gio_prefill_tc64.argtypes = [vp, l, vp, vp, l, vp, l, i, i, i, i, f, i]
+        L.gio_prefill_tc64_i8.argtypes = [vp, l, vp, vp, vp, vp, l, vp, l, i, i, i, i, f, i]
         L.gio_prefill_tc256_i8.argtypes = [vp, l, vp, vp, vp, vp, l, vp, l, i, i, i, i, f, i]
         L.gio_kv4_fwht.argtypes = [vp, l]
         L.gio_kv4_quant.argtypes = [vp, l, vp, vp]
@@ -276,31 +278,31 @@ def prefill_tc256_q4(q, kc, vc, ks, vs, pos0, n_heads, n_kv, scale=None, threads
 
 def prefill_tc_semantics(q, kc, vc, pos0, n_heads, n_kv, scale=None, threads=8, hd=128):
     """attn_prefill_tc<128> (src/cuda.rs:2408-2617): f16-rounded Q*scale*log2(e) and P; hd=256 follows
-    attention_prefill_tc256 (src/cuda.rs:2623), the same arithmetic."""
+    attention_prefill_tc256 (src/cuda.rs:2623) and hd=64 attention_prefill_tc64 (src/cuda.rs:2620), the same
+    arithmetic."""
     q = _rows(q, np.float32)
     n = q.shape[0]
     kc, vc = _rows(kc, np.uint16), _rows(vc, np.uint16)
     if scale is None:
         scale = 1.0 / np.sqrt(hd)
     out = np.zeros((n, n_heads * hd), dtype=np.float32)
-    fn = lib().gio_prefill_tc256 if hd == 256 else lib().gio_prefill_tc
-    assert hd in (128, 256)
+    fn = {64: lib().gio_prefill_tc64, 128: lib().gio_prefill_tc, 256: lib().gio_prefill_tc256}[hd]
     fn(_p(q), q.shape[1], _p(kc), _p(vc), kc.shape[1], _p(out), out.shape[1], pos0, n, n_heads, n_kv, scale, threads)
     return out
 
 
 def prefill_tc_semantics_i8(q, kc, vc, ks, vs, pos0, n_heads, n_kv, scale=None, threads=8, hd=128):
     """attn_prefill_tc<128> over the KV8 cache (src/cuda.rs:2408-2617 with KV8); hd=256 follows
-    attention_prefill_tc256 (src/cuda.rs:2623). kc/vc int8 [pos, n_kv*hd], ks/vs f32 [pos, n_kv]."""
+    attention_prefill_tc256 (src/cuda.rs:2623) and hd=64 attention_prefill_tc64 (src/cuda.rs:2620). kc/vc int8
+    [pos, n_kv*hd], ks/vs f32 [pos, n_kv]."""
     q = _rows(q, np.float32)
     n = q.shape[0]
     kc, vc = _rows(kc, np.int8), _rows(vc, np.int8)
     ks, vs = _rows(ks, np.float32), _rows(vs, np.float32)
-    assert hd in (128, 256)
     if scale is None:
         scale = 1.0 / np.sqrt(hd)
     out = np.zeros((n, n_heads * hd), dtype=np.float32)
-    fn = lib().gio_prefill_tc256_i8 if hd == 256 else lib().gio_prefill_tc_i8
+    fn = {64: lib().gio_prefill_tc64_i8, 128: lib().gio_prefill_tc_i8, 256: lib().gio_prefill_tc256_i8}[hd]
     fn(_p(q), q.shape[1], _p(kc), _p(vc), _p(ks), _p(vs), kc.shape[1], _p(out), out.shape[1], pos0, n, n_heads, n_kv,
        scale, threads)
     return out

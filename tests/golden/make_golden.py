@@ -1,6 +1,6 @@
 """Writes the small golden fixtures of the attention path: seeded inputs and float64 expected outputs.
 
-    python tests/golden/make_golden.py
+    python tests/golden/make_golden.py [NAME ...]   (no names: every case)
 
 The expected outputs come from the textbook causal softmax attention in float64
 (tests/attn_common.reference_f64, over the dequantised cache for int8 and the 4-bit cache), not from the oracle
@@ -35,11 +35,20 @@ CASES = {
     "decode_h256_q4_ctx200": (113, 1, 199, 16, 2, np.float32, 256, "q4"),
     "verify_h256_q4_3tok_ctx90": (114, 3, 87, 16, 2, np.float32, 256, "q4"),
     "prefill_h256_q4_40tok": (115, 40, 0, 4, 1, np.float32, 256, "q4"),
+    # head size 64 at SmolLM2-135M's 9 query / 3 kv heads (the reference's attention_prefill_tc64 and its split
+    # decode at head size 64)
+    "decode_h64_smollm2_ctx300": (116, 1, 299, 9, 3, np.float32, 64, False),
+    "verify_h64_smollm2_5tok_ctx130": (117, 5, 125, 9, 3, np.float32, 64, False),
+    "prefill_h64_smollm2_48tok": (118, 48, 0, 9, 3, np.float16, 64, False),
+    "decode_h64_i8_smollm2_ctx300": (119, 1, 299, 9, 3, np.float32, 64, True),
+    "prefill_h64_i8_smollm2_40tok": (120, 40, 0, 9, 3, np.float32, 64, True),
 }
 
 
 def main():
-    for name, (seed, n_tok, pos0, n_heads, n_kv, qd, hd, i8) in CASES.items():
+    names = sys.argv[1:] or list(CASES)
+    for name in names:
+        seed, n_tok, pos0, n_heads, n_kv, qd, hd, i8 = CASES[name]
         extra = {}
         if i8 == "q4":  # random nibbles with f16 scales near 1/4, dequantised values of standard deviation ~1
             q, k, v, ks, vs = make_inputs_q4(seed, n_tok, pos0 + n_tok, n_heads, n_kv)

@@ -47,9 +47,11 @@ def test_code_object_built():
 def test_unsupported_head_size_is_rejected_with_message():
     lib = gi_attn.load_library()
     c, n = ctypes.c_int(), ctypes.c_int()
-    rc = lib.gi_attn_decode_plan(100, 1, 32, 8, 64, ctypes.byref(c), ctypes.byref(n))
+    rc = lib.gi_attn_decode_plan(100, 1, 32, 8, 96, ctypes.byref(c), ctypes.byref(n))
     assert rc == -1
-    assert "head size 64" in lib.gi_last_error().decode()
+    assert "head size 96" in lib.gi_last_error().decode()
+    for hd in (64, 128, 256):
+        assert lib.gi_attn_decode_plan(100, 1, 32, 8, hd, ctypes.byref(c), ctypes.byref(n)) == 0
     rc = lib.gi_attn_decode_plan(100, 1, 30, 8, 128, ctypes.byref(c), ctypes.byref(n))
     assert rc == -1 and "multiple of n_kv" in lib.gi_last_error().decode()
 
@@ -117,7 +119,8 @@ def test_relayout_rejects_bad_arguments_before_any_launch():
 @pytest.mark.parametrize("ctx,n_tok,n_heads,n_kv,hd", [(4096, 1, 32, 8, 128), (65536, 1, 32, 4, 128),
                                                        (32776, 8, 32, 4, 128), (100, 15, 8, 1, 128),
                                                        (1, 1, 32, 4, 128), (65536, 1, 16, 2, 256),
-                                                       (32776, 8, 16, 2, 256), (5000, 15, 16, 2, 256)])
+                                                       (32776, 8, 16, 2, 256), (5000, 15, 16, 2, 256),
+                                                       (4096, 1, 9, 3, 64), (32776, 15, 9, 3, 64)])
 def test_decode_plan_covers_the_span(ctx, n_tok, n_heads, n_kv, hd):
     part = (hd + 4) * 4  # bytes of one slice partial
 

@@ -249,25 +249,26 @@ def _q_between_f16(hd, n_heads, x):
     return q, qs
 
 
-def test_prefill_tc_semantics_roundings_by_hand():
+@pytest.mark.parametrize("hd", [64, 128])
+def test_prefill_tc_semantics_roundings_by_hand(hd):
     # One query at position 1 over two keys: key 0 all ones, key 1 zero; value 0 all ones, value 1 zero. Each
-    # element of Q*scale*log2e is 2^-7 (1 + 1.25 * 2^-10), which f16 rounds down to 2^-7 (1 + 2^-10), so the
-    # score of key 0 is 128 * that = 1 + 2^-10 exactly (unrounded: 1 + 1.25 * 2^-10). Then P0 = 1, P1 =
-    # f16(exp2(-(1 + 2^-10))), l = P0 + P1 (the rounded P), out = P0 / l in every dim.
-    x = 2.0 ** -7 * (1 + 1.25 * 2.0 ** -10)
-    q, qs = _q_between_f16(128, 1, x)
-    k = np.zeros((2, 128), np.float16)
+    # element of Q*scale*log2e is 2^-7 (1 + 1.25 * 2^-10) (head size 64: 2^-6 (...)), which f16 rounds down to
+    # 2^-7 (1 + 2^-10), so the score of key 0 is 128 * that = 1 + 2^-10 exactly (unrounded: 1 + 1.25 * 2^-10).
+    # Then P0 = 1, P1 = f16(exp2(-(1 + 2^-10))), l = P0 + P1 (the rounded P), out = P0 / l in every dim.
+    x = (128.0 / hd) * 2.0 ** -7 * (1 + 1.25 * 2.0 ** -10)
+    q, qs = _q_between_f16(hd, 1, x)
+    k = np.zeros((2, hd), np.float16)
     k[0] = 1
-    v = np.zeros((2, 128), np.float16)
+    v = np.zeros((2, hd), np.float16)
     v[0] = 1
-    got = O.prefill_tc_semantics(q, k.view(np.uint16), v.view(np.uint16), 1, 1, 1)
-    s0 = np.float32(128) * _f16(q[0, 0] * qs)
+    got = O.prefill_tc_semantics(q, k.view(np.uint16), v.view(np.uint16), 1, 1, 1, hd=hd)
+    s0 = np.float32(hd) * _f16(q[0, 0] * qs)
     assert s0 == np.float32(1 + 2.0 ** -10)
     p1 = _f16(np.exp2(-s0))
     want = np.float32(1) / (np.float32(1) + p1)
     np.testing.assert_allclose(got, want, rtol=2e-7, atol=0)
     # each plausible slip moves the result far beyond that tolerance
-    s0_unrounded = np.float32(128) * (q[0, 0] * qs)
+    s0_unrounded = np.float32(hd) * (q[0, 0] * qs)
     slips = {"Q not rounded": 1 / (1 + _f16(np.exp2(-s0_unrounded))),
              "P not rounded": 1 / (1 + np.exp2(-s0)),
              "natural-log softmax": 1 / (1 + _f16(np.exp(-s0)))}
@@ -308,14 +309,14 @@ def test_decode_tc256_i8_roundings_by_hand():
         assert abs(float(alt) - float(want)) > 1e-5 * float(want), what
 
 
-@pytest.mark.parametrize("hd", [128, 256])
+@pytest.mark.parametrize("hd", [64, 128, 256])
 def test_prefill_tc_i8_roundings_by_hand(hd):
     # attn_prefill_tc over the int8 cache (src/cuda.rs:2466-2498, 2548-2605), one query at position 1 over two
     # keys: key 0 all ones (scale 1), key 1 zero; Q*scale*log2e rounds to f16 so that score 0 = 1 + 2^-10
     # exactly. Values: row 0 all 1 with scale 1/3, row 1 all 2 with scale 1/5 (non-unit, so every rounding step
     # shows). The reference biases each value scale by 2^10 as it loads it, rounds p * (vscale * 2^10) to f16
     # for P V, sums the f16-rounded p into l, and scales the output by (2^-10 / l).
-    x = (2.0 ** -7 if hd == 128 else 2.0 ** -8) * (1 + 1.25 * 2.0 ** -10)
+    x = (128.0 / hd) * 2.0 ** -7 * (1 + 1.25 * 2.0 ** -10)
     q, qs = _q_between_f16(hd, 1, x)
     k = np.zeros((2, hd), np.int8)
     k[0] = 1
@@ -451,8 +452,14 @@ def test_oracle_against_golden(name):
     elif "ks" in z.files and hd == 256:  # attention_decode_tc256 rounds Q and P*vscale to f16: the parity bar
         got = O.decode_tc256_i8(q, z["k"], z["v"], z["ks"], z["vs"], pos0, n_heads, n_kv)
         assert_close(got, z["out"], what=name)
-    elif "ks" in z.files:  # the int8 split path keeps f32 precision
+    elif "ks" in z.files and hd == 128:  # the int8 split path keeps f32 precision
         got = O.decode_gpu_semantics_i8(q, z["k"], z["v"], z["ks"], z["vs"], pos0, n_heads, n_kv)
+        assert_close(got, z["out"], max_abs=2e-5, rel_l2=2e-6, what=name)
+    elif "ks" in z.files:  # head size 64: Model::attention over the dequantised cache (f32 precision)
+        def deq(c, sc):
+            return (c.reshape(c.shape[0], n_kv, hd).astype(np.float32) * sc[:, :, None]).reshape(c.shape[0], -1)
+
+        got = O.attention(q, deq(z["k"], z["ks"]), deq(z["v"], z["vs"]), pos0, n_heads, n_kv, hd=hd)
         assert_close(got, z["out"], max_abs=2e-5, rel_l2=2e-6, what=name)
     else:
         got = O.attention(q, z["k"], z["v"], pos0, n_heads, n_kv, hd=hd)
@@ -641,6 +648,38 @@ def test_prefill_tc_semantics_hd256_within_parity_bar(n, pos0, n_heads, n_kv):
     got2 = O.prefill_tc_semantics(q, k, v2.reshape(v.shape), pos0, n_heads, n_kv, hd=256).reshape(n, n_heads, 256)
     np.testing.assert_array_equal(got2[:, :, :128], got.reshape(n, n_heads, 256)[:, :, :128])
     assert not got2[:, :, 128:].any()
+
+
+@pytest.mark.parametrize("n,pos0,n_heads,n_kv,i8", [(48, 0, 9, 3, False), (70, 33, 4, 1, False), (48, 0, 9, 3, True),
+                                                    (70, 33, 4, 1, True)])
+def test_prefill_tc_semantics_hd64_within_parity_bar(n, pos0, n_heads, n_kv, i8):
+    # attention_prefill_tc64's arithmetic (head size 64, f16 and int8 caches): within the bar of the exact attention,
+    # its f16 roundings visible; and the head-64 restatement is the head-128 one on rows zero-padded to 128 dims
+    # (padding adds nothing to a dot product or to P V), with the scale passed explicitly
+    if i8:
+        q, k, v, ks, vs = make_inputs_i8(91 + n, n, pos0 + n, n_heads, n_kv, hd=64)
+        got = O.prefill_tc_semantics_i8(q, k, v, ks, vs, pos0, n_heads, n_kv, hd=64)
+        want = reference_f64_i8(q, k, v, ks, vs, pos0, n_heads, n_kv, hd=64)
+    else:
+        q, k, v = make_inputs(91 + n, n, pos0 + n, n_heads, n_kv, hd=64)
+        got = O.prefill_tc_semantics(q, k, v, pos0, n_heads, n_kv, hd=64)
+        want = reference_f64(q, k, v, pos0, n_heads, n_kv, hd=64)
+    ma, _ = assert_close(got, want, what="prefill_tc hd64 semantics vs f64")
+    assert ma > 1e-6
+
+    def pad(x, rows, heads):
+        y = np.zeros((rows, heads, 128), dtype=x.dtype)
+        y[:, :, :64] = x.reshape(rows, heads, 64)
+        return y.reshape(rows, heads * 128)
+
+    qp = pad(q, n, n_heads)
+    if i8:
+        padded = O.prefill_tc_semantics_i8(qp, pad(k, k.shape[0], n_kv), pad(v, v.shape[0], n_kv), ks, vs, pos0,
+                                           n_heads, n_kv, scale=1 / 8.0, hd=128)
+    else:
+        padded = O.prefill_tc_semantics(qp, pad(k, k.shape[0], n_kv), pad(v, v.shape[0], n_kv), pos0, n_heads, n_kv,
+                                        scale=1 / 8.0, hd=128)
+    np.testing.assert_array_equal(padded.reshape(n, n_heads, 128)[:, :, :64].reshape(n, -1), got)
 
 
 # ---------------------------------------------------------------- the 4-bit cache (KV4)
