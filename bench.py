@@ -3,7 +3,7 @@
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload decode64k|decode4k|verify|prefill8k|chunked|qkrope|
                     decode64k_i8|verify_i8|prefill8k_i8|decode64k_h256|verify_h256|prefill8k_h256|
                     decode64k_h256_i8|verify_h256_i8|prefill8k_h256_i8|decode64k_h256_q4|verify_h256_q4|
-                    prefill8k_h256_q4]
+                    prefill8k_h256_q4|decode64k_h64|decode64k_h64_i8|prefill8k_h64|prefill8k_h64_i8]
                     [--no-cpu-baseline] [--no-secondary] [--reference-layout] [--verbose]
                     [--detail-out FILE] [--full-line]
 
@@ -22,6 +22,8 @@ A step is one pass of the hot path over one batch of synthetic seeded input alre
              head size 256 over the int8 cache (the reference's attention_decode_tc256 / prefill_tc256 shapes)
   decode64k_h256_q4, verify_h256_q4, prefill8k_h256_q4
              head size 256 over the 4-bit cache (the reference's --kv q4: 128 bytes a row plus 8 f16 scales)
+  decode64k_h64, decode64k_h64_i8, prefill8k_h64, prefill8k_h64_i8
+             head size 64 (Llama-3.2-1B-style 32 query / 8 kv heads) over the f16 and int8 caches
   decode64k_i8, verify_i8, prefill8k_i8
              configs 2, 4 and 3 over the int8 cache (the reference's KV8 format: int8 rows, an f32 scale per
              position and kv head); bytes are the int8 rows plus their scales
@@ -31,7 +33,7 @@ model's layer loop does, so no step finds its K/V in the last-level cache.
 Prints ONE JSON line (rank 0), kept under ~2 KB so that a record holding only the end of the output holds
 all of it. With the default workload the line also carries configs 1, 3, 4 and 5 under "secondary" (decode4k,
 verify, prefill8k and chunked: value, time, roofline; chunked also the total time and every 16th chunk's
-TFLOP/s) and the roofline fraction of every int8, head-256 and 4-bit workload; and the CPU baseline: the
+TFLOP/s) and the roofline fraction of every int8, head-64, head-256 and 4-bit workload; and the CPU baseline: the
 oracle's restatement of the reference's CPU attention (src/model.rs:1320-1409) over the same inputs with the
 cache widened to f32 (as the reference's CPU session holds it), timed on this host at its CPU share (up to 16
 threads) and at half of it (the reference's default logical/2), for configs 2 and 1 and a bounded sample of
@@ -136,12 +138,14 @@ def decode_kernel_name(n_tok, n_heads, n_kv, hd, i8):
         return "gi_decode_pm_2_q4" if i8 == "q4" else "gi_decode_pm_ws2_1_i8_h256"
     if pairs <= p:
         name = "gi_decode_partial_1"
+    elif hd == 64:
+        name = "gi_decode_pm_2" if pairs > 2 * p else "gi_decode_pm_1"
     elif hd == 256:
         name = "gi_decode_pm_ws2_1"
     else:
         name = ("gi_decode_pm_ws2_2" if pairs > 4 * p and not i8 else
                 "gi_decode_pm_2" if pairs > 2 * p else "gi_decode_pm_1")
-    return name + ("_i8" if i8 else "") + ("_h256" if hd == 256 else "")
+    return name + ("_i8" if i8 else "") + ("_h256" if hd == 256 else "_h64" if hd == 64 else "")
 
 
 def profile_traffic(name):
@@ -507,6 +511,10 @@ DECODE_WORKLOADS = {
                                                       "reference's --kv q4), 1 token, ctx 65536, 16q/2kv"),
     "verify_h256_q4": (32776, 16, 2, 8, 256, "q4", "verify with 256-wide heads over the 4-bit cache, 8 tokens at a "
                                                    "32768-key prefix, 16q/2kv"),
+    "decode64k_h64": (65536, 32, 8, 1, 64, False, "decode with 64-wide heads (Llama-3.2-1B-style 32q/8kv), 1 token, "
+                                                  "ctx 65536, f16 cache"),
+    "decode64k_h64_i8": (65536, 32, 8, 1, 64, True, "decode with 64-wide heads over the int8 cache, 1 token, ctx "
+                                                    "65536, 32q/8kv"),
 }
 
 
@@ -554,25 +562,29 @@ def run_decode(torch, gi_attn, dev, w, steps, warmup, n_tok_override=None, refer
     return line, r
 
 
-PREFILL_WORKLOADS = ("prefill8k", "prefill8k_i8", "prefill8k_h256", "prefill8k_h256_i8", "prefill8k_h256_q4")
+PREFILL_WORKLOADS = ("prefill8k", "prefill8k_i8", "prefill8k_h256", "prefill8k_h256_i8", "prefill8k_h256_q4",
+                     "prefill8k_h64", "prefill8k_h64_i8")
 
 
 def run_prefill(torch, gi_attn, dev, w, steps, warmup):
     i8 = "q4" if w.endswith("_q4") else w.endswith("_i8")
-    hd = 256 if "_h256" in w else HD
+    hd = 256 if "_h256" in w else 64 if "_h64" in w else HD
     nh, nkv = (16, 2) if hd == 256 else (32, 8)
     cache = " over the 4-bit cache" if i8 == "q4" else " over the int8 cache" if i8 else ""
     log(f"[bench] causal prefill 8192 tokens, {nh}q/{nkv}kv, hd {hd}{cache}")
     r = prefill_workload(torch, gi_attn, dev, 8192, nh, nkv, steps, warmup, 99, i8=i8, hd=hd)
     tf = r["flops"] / r["seconds"] / 1e12
     kernel = ("gi_prefill_fwd_h256r" + ("_q4" if i8 == "q4" else "_i8" if i8 else "") if hd == 256
+              else "gi_prefill_fwd_h64" + ("_i8" if i8 else "") if hd == 64
               else "gi_prefill_fwd_i8" if i8 else "gi_prefill_fwd")
     line = {
         "value": round(tf, 1), "unit": "TFLOP/s", "ms_per_step": r["seconds"] * 1e3,
         "dtype": ("4-bit K/V widened to f16 MFMA, f32 acc" if i8 == "q4" else
                   "int8 K/V widened to f16 MFMA, f32 acc" if i8 else "f16 MFMA, f32 acc"),
         "config": {"workload": (f"causal prefill, 8192 tokens, {nh}q/{nkv}kv, hd 256 (Qwen3.5-style heads){cache}"
-                                if hd == 256 else "config 3: causal prefill, 8192 tokens, 32q/8kv, hd 128" +
+                                if hd == 256 else
+                                f"causal prefill, 8192 tokens, 32q/8kv, hd 64 (Llama-3.2-1B-style heads){cache}"
+                                if hd == 64 else "config 3: causal prefill, 8192 tokens, 32q/8kv, hd 128" +
                                 (", int8 cache" if i8 else "")), "flops_per_step": r["flops"]},
         "roofline": prefill_roofline(gi_attn, r, steps, torch, f"pmc_prefill_{w}", kernel),
     }
@@ -759,11 +771,12 @@ def main():
         sec["chunked"] = secondary_entry(run_chunked(torch, gi_attn, dev))
         # the cache formats and head sizes beyond the configs: int8, head size 256 over f16, int8 and 4 bits
         for w2 in ("decode64k_i8", "verify_i8", "decode64k_h256", "verify_h256", "decode64k_h256_i8",
-                   "verify_h256_i8", "decode64k_h256_q4", "verify_h256_q4"):
+                   "verify_h256_i8", "decode64k_h256_q4", "verify_h256_q4", "decode64k_h64", "decode64k_h64_i8"):
             line, r2 = run_decode(torch, gi_attn, dev, w2, steps2, warm2)
             sec[w2] = secondary_entry(line)
             del r2
-        for w2 in ("prefill8k_i8", "prefill8k_h256", "prefill8k_h256_i8", "prefill8k_h256_q4"):
+        for w2 in ("prefill8k_i8", "prefill8k_h256", "prefill8k_h256_i8", "prefill8k_h256_q4", "prefill8k_h64",
+                   "prefill8k_h64_i8"):
             line, r2 = run_prefill(torch, gi_attn, dev, w2, 20, 5)
             sec[w2] = secondary_entry(line)
             del r2

@@ -47,7 +47,7 @@ void gi_ok(int rc, const char* what) {
 }
 
 void usage() {
-    printf("usage: gi_layer_harness [--prompt N] [--steps S] [--heads H] [--kv K] [--hd 128|256] [--int8 | --q4]\n"
+    printf("usage: gi_layer_harness [--prompt N] [--steps S] [--heads H] [--kv K] [--hd 64|128|256] [--int8 | --q4]\n"
            "                        [--no-graph] [--seed X] [--dump FILE]\n"
            "Plays one layer's attention through the C ABI (cache write + prefill for the prompt, then one\n"
            "decode step per token, replayed from a HIP graph), checks every output row against the exact\n"
@@ -81,9 +81,9 @@ Opts parse(int argc, char** argv) {
         }
         else die("unknown argument " + a);
     }
-    if (o.prompt < 1 || o.steps < 0 || o.heads < 1 || o.kv < 1 || o.heads % o.kv || (o.hd != 128 && o.hd != 256) ||
-        (o.q4 && (o.hd != 256 || o.i8)))
-        die("bad shape (heads a multiple of kv; hd 128 or 256; --q4 takes hd 256 and not --int8)");
+    if (o.prompt < 1 || o.steps < 0 || o.heads < 1 || o.kv < 1 || o.heads % o.kv ||
+        (o.hd != 64 && o.hd != 128 && o.hd != 256) || (o.q4 && (o.hd != 256 || o.i8)))
+        die("bad shape (heads a multiple of kv; hd 64, 128 or 256; --q4 takes hd 256 and not --int8)");
     return o;
 }
 

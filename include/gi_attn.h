@@ -27,10 +27,12 @@
  *    set) clamp *posp into [0, ctx_cap - n_tok] and return the attention at the clamped position; the
  *    cache writes store no row at a position outside [0, ctx_cap). A caller that can overrun checks its position on the host before
  *    replaying (the reference trusts *posp the same way, src/cuda.rs:8686-8712).
- *  - hd is 128 or 256 (the reference's wide heads: attention_partial_gqa's hd 256 branch src/cuda.rs:1762-1781,
- *    attention_prefill_tc256 src/cuda.rs:2622-2623, attention_decode_tc256 src/cuda.rs:2625-2802) with the f16
- *    and the int8 caches, and 256 with the 4-bit cache (the *_q4 entry points); n_heads must be a multiple of
- *    n_kv.
+ *  - hd is 64, 128 or 256 with the f16 and the int8 caches, and 256 with the 4-bit cache (the *_q4 entry
+ *    points); n_heads must be a multiple of n_kv. Head size 64 is attention_partial_gqa at a head size that is a
+ *    multiple of 32 (src/cuda.rs:8419-8422) and attention_prefill_tc64 (src/cuda.rs:2620, dispatched at
+ *    src/cuda.rs:8452-8456); 256 the reference's wide heads (attention_partial_gqa's hd 256 branch
+ *    src/cuda.rs:1762-1781, attention_prefill_tc256 src/cuda.rs:2622-2623, attention_decode_tc256
+ *    src/cuda.rs:2625-2802).
  */
 #ifndef GI_ATTN_H
 #define GI_ATTN_H
@@ -126,8 +128,9 @@ int gi_attn_decode_q4(void* stream, const float* q, long long q_stride, const ui
 
 /* Causal prefill attention for n tokens at positions pos0..pos0+n-1 whose K/V rows are already in the
  * cache (keys 0..pos0+n-1 are read; pos0 > 0 is a chunk of a longer prompt). q: rows of q_dtype
- * (GI_F32 or GI_F16); out: rows of out_dtype. Replaces: attention_prefill_tc128 (src/cuda.rs:2408-2621),
- * launched by GpuModel::attention for batches of >= 16 tokens (src/cuda.rs:8459-8466). */
+ * (GI_F32 or GI_F16); out: rows of out_dtype. Replaces: attention_prefill_tc128 (src/cuda.rs:2408-2621), and
+ * attention_prefill_tc64 / attention_prefill_tc256 at hd 64 / 256 (src/cuda.rs:2620-2623), launched by
+ * GpuModel::attention for batches of >= 16 tokens (src/cuda.rs:8452-8466). */
 int gi_attn_prefill(void* stream, const void* q, int q_dtype, long long q_stride, const uint16_t* kc,
                     const uint16_t* vc, long long kv_stride, long long kv_head_stride, void* out, int out_dtype,
                     long long out_stride, int pos0, int n, int n_heads, int n_kv, int hd, float scale);
@@ -135,7 +138,7 @@ int gi_attn_prefill(void* stream, const void* q, int q_dtype, long long q_stride
 /* gi_attn_prefill over an int8 KV cache (layouts and scales as gi_attn_decode_i8). The keys enter the
  * scores as exact integers times their scale; P V takes f16(p * vs) and the row sum the f16-rounded p.
  * Dequantised values must stay within |v| < 4000 (the f16 range of p * vs with p <= 256); the output is
- * O / 2^10 / l. hd 128 or 256. Replaces: attention_prefill_tc128 and attention_prefill_tc256 compiled with KV8
+ * O / 2^10 / l. hd 64, 128 or 256. Replaces: attention_prefill_tc64/128/256 compiled with KV8
  * (src/cuda.rs:2408-2623, int8 staging src/cuda.rs:2466-2498). */
 int gi_attn_prefill_i8(void* stream, const void* q, int q_dtype, long long q_stride, const int8_t* kc, const int8_t* vc,
                        const float* ks, const float* vs, long long kv_stride, long long kv_head_stride,

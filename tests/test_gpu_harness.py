@@ -29,6 +29,10 @@ CASES = [
      "q4"),
     (["--heads", "16", "--kv", "2", "--hd", "256", "--prompt", "100", "--steps", "10"], 100, 10, 16, 2, 256, False),
     (["--no-graph", "--prompt", "40", "--steps", "6", "--heads", "32", "--kv", "4"], 40, 6, 32, 4, 128, False),
+    # head size 64 at SmolLM2-135M's 9 query / 3 kv heads, f16 and int8
+    (["--heads", "9", "--kv", "3", "--hd", "64", "--prompt", "200", "--steps", "12"], 200, 12, 9, 3, 64, False),
+    (["--int8", "--heads", "9", "--kv", "3", "--hd", "64", "--prompt", "200", "--steps", "12"], 200, 12, 9, 3, 64,
+     True),
 ]
 
 
@@ -75,8 +79,15 @@ def test_layer_harness(case, tmp_path):
         vc, vs = O.kv_quant_i8(vr.reshape(total, K, hd))
         kc, vc = kc.reshape(total, K * hd), vc.reshape(total, K * hd)
         want_pre = O.prefill_tc_semantics_i8(q[pre], kc, vc, ks, vs, 0, H, K, hd=hd)
-        want_dec = (O.decode_tc256_i8(q[dec], kc, vc, ks, vs, prompt, H, K) if hd == 256
-                    else O.decode_gpu_semantics_i8(q[dec], kc, vc, ks, vs, prompt, H, K))
+        if hd == 256:
+            want_dec = O.decode_tc256_i8(q[dec], kc, vc, ks, vs, prompt, H, K)
+        elif hd == 128:
+            want_dec = O.decode_gpu_semantics_i8(q[dec], kc, vc, ks, vs, prompt, H, K)
+        else:  # Model::attention over the dequantised cache
+            def deq(c, sc):
+                return (c.reshape(total, K, hd).astype(np.float32) * sc[:, :, None]).reshape(total, -1)
+
+            want_dec = O.attention(q[dec], deq(kc, ks), deq(vc, vs), prompt, H, K, hd=hd)
         f64 = reference_f64_i8(q, kc, vc, ks, vs, 0, H, K, hd=hd)
     else:
         kc = kr.astype(np.float16).view(np.uint16)
