@@ -3,7 +3,7 @@
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload decode64k|decode4k|verify|prefill8k|chunked|qkrope|
                     decode64k_i8|verify_i8|prefill8k_i8|decode64k_h256|verify_h256|prefill8k_h256|
                     decode64k_h256_i8|verify_h256_i8|prefill8k_h256_i8|decode64k_h256_q4|verify_h256_q4|
-                    prefill8k_h256_q4|decode64k_h64|decode64k_h64_i8|prefill8k_h64|prefill8k_h64_i8]
+                    prefill8k_h256_q4|decode64k_h64|decode64k_h64_i8|prefill8k_h64|prefill8k_h64_i8|decode16k_h80|prefill8k_h96]
                     [--no-cpu-baseline] [--no-secondary] [--reference-layout] [--verbose]
                     [--detail-out FILE] [--full-line]
 
@@ -24,6 +24,8 @@ A step is one pass of the hot path over one batch of synthetic seeded input alre
              head size 256 over the 4-bit cache (the reference's --kv q4: 128 bytes a row plus 8 f16 scales)
   decode64k_h64, decode64k_h64_i8, prefill8k_h64, prefill8k_h64_i8
              head size 64 (Llama-3.2-1B-style 32 query / 8 kv heads) over the f16 and int8 caches
+  decode16k_h80, prefill8k_h96
+             the f32 kernels' head sizes (Phi-2-style 80, Phi-3-style 96; 32 query / 32 kv heads)
   decode64k_i8, verify_i8, prefill8k_i8
              configs 2, 4 and 3 over the int8 cache (the reference's KV8 format: int8 rows, an f32 scale per
              position and kv head); bytes are the int8 rows plus their scales
@@ -132,6 +134,8 @@ def decode_kernel_name(n_tok, n_heads, n_kv, hd, i8):
     256 over the f16 cache; over its int8 and 4-bit caches one pair per column throughout, 16 pairs per workgroup
     or, above 16 pairs, two pair sets (int8) or two column blocks per wave (4-bit))."""
     pairs, p = n_tok * (n_heads // n_kv), 8
+    if hd not in (64, 128, 256):  # the f32 kernels' head sizes
+        return "gi_decode_f32" + ("_i8" if i8 else "")
     if hd == 256 and i8:  # the reference's tc256 roundings, one pair per column: 16 or 32 pairs per workgroup
         if pairs <= 2 * p:
             return "gi_decode_pm_1" + ("_q4" if i8 == "q4" else "_i8_h256")
@@ -515,6 +519,8 @@ DECODE_WORKLOADS = {
                                                   "ctx 65536, f16 cache"),
     "decode64k_h64_i8": (65536, 32, 8, 1, 64, True, "decode with 64-wide heads over the int8 cache, 1 token, ctx "
                                                     "65536, 32q/8kv"),
+    "decode16k_h80": (16384, 32, 32, 1, 80, False, "decode with 80-wide heads (Phi-2-style 32q/32kv, the f32 kernels), "
+                                                   "1 token, ctx 16384, f16 cache"),
 }
 
 
@@ -563,19 +569,20 @@ def run_decode(torch, gi_attn, dev, w, steps, warmup, n_tok_override=None, refer
 
 
 PREFILL_WORKLOADS = ("prefill8k", "prefill8k_i8", "prefill8k_h256", "prefill8k_h256_i8", "prefill8k_h256_q4",
-                     "prefill8k_h64", "prefill8k_h64_i8")
+                     "prefill8k_h64", "prefill8k_h64_i8", "prefill8k_h96")
 
 
 def run_prefill(torch, gi_attn, dev, w, steps, warmup):
     i8 = "q4" if w.endswith("_q4") else w.endswith("_i8")
-    hd = 256 if "_h256" in w else 64 if "_h64" in w else HD
-    nh, nkv = (16, 2) if hd == 256 else (32, 8)
+    hd = 256 if "_h256" in w else 64 if "_h64" in w else 96 if "_h96" in w else HD
+    nh, nkv = (16, 2) if hd == 256 else (32, 32) if hd == 96 else (32, 8)
     cache = " over the 4-bit cache" if i8 == "q4" else " over the int8 cache" if i8 else ""
     log(f"[bench] causal prefill 8192 tokens, {nh}q/{nkv}kv, hd {hd}{cache}")
     r = prefill_workload(torch, gi_attn, dev, 8192, nh, nkv, steps, warmup, 99, i8=i8, hd=hd)
     tf = r["flops"] / r["seconds"] / 1e12
     kernel = ("gi_prefill_fwd_h256r" + ("_q4" if i8 == "q4" else "_i8" if i8 else "") if hd == 256
               else "gi_prefill_fwd_h64" + ("_i8" if i8 else "") if hd == 64
+              else "gi_prefill_f32" if hd == 96
               else "gi_prefill_fwd_i8" if i8 else "gi_prefill_fwd")
     line = {
         "value": round(tf, 1), "unit": "TFLOP/s", "ms_per_step": r["seconds"] * 1e3,
@@ -584,7 +591,9 @@ def run_prefill(torch, gi_attn, dev, w, steps, warmup):
         "config": {"workload": (f"causal prefill, 8192 tokens, {nh}q/{nkv}kv, hd 256 (Qwen3.5-style heads){cache}"
                                 if hd == 256 else
                                 f"causal prefill, 8192 tokens, 32q/8kv, hd 64 (Llama-3.2-1B-style heads){cache}"
-                                if hd == 64 else "config 3: causal prefill, 8192 tokens, 32q/8kv, hd 128" +
+                                if hd == 64 else
+                                "causal prefill, 8192 tokens, 32q/32kv, hd 96 (Phi-3-style heads, the f32 kernels)"
+                                if hd == 96 else "config 3: causal prefill, 8192 tokens, 32q/8kv, hd 128" +
                                 (", int8 cache" if i8 else "")), "flops_per_step": r["flops"]},
         "roofline": prefill_roofline(gi_attn, r, steps, torch, f"pmc_prefill_{w}", kernel),
     }

@@ -120,7 +120,7 @@ struct GiPrefillArgs {
     float qscale;
     int q_f16;
     int out_f16;
-    int pad_;
+    int hd;
     const float* ks;
     const float* vs;
     long long sc_stride;
@@ -128,6 +128,11 @@ struct GiPrefillArgs {
 };
 
 constexpr float kLog2e = 1.4426950408889634f;
+constexpr int kF32Rows = 32; // query rows per gi_prefill_f32 workgroup; must match the kernels' PF32_ROWS
+
+// Head sizes of the f32 kernels (gi_attn_f32.hip): the multiples of 16 up to 112 that the MFMA kernels do not
+// take, the reference's f32 fallback cases (attention_partial / attention_prefill, src/cuda.rs:1866-2041).
+bool f32_hd(int hd) { return hd % 16 == 0 && hd >= 16 && hd <= 112 && hd != 64; }
 constexpr int kMaxDevices = 64;
 constexpr int kRopeHeads = 16; // heads per gi_qk_norm_rope workgroup; must match the kernels' ROPE_HEADS
 constexpr int kCombineSplit = 8; // combine workgroups per (head, token); must match the kernels' CMB_DSPLIT
@@ -171,6 +176,7 @@ struct Module {
     hipFunction_t dec_pm256[2] = {};  // head size 256, one pair per column, two pair sets of two waves: [f16, int8]
     hipFunction_t prefill[2] = {};   // [int8 cache], head size 128
     hipFunction_t prefill64[2] = {}; // [int8 cache], head size 64 (the same launch shape and block size)
+    hipFunction_t dec_f32[2] = {}, prefill_f32[2] = {}; // [int8 cache]: the f32 kernels
     hipFunction_t prefill256r = nullptr; // head size 256 (f16 cache), 16 rows per wave: one workgroup per query tile
     hipFunction_t prefill256r_fmt[2] = {}; // the same over the int8 and the 4-bit cache
     hipFunction_t combine = nullptr, rope = nullptr, relayout = nullptr, hadamard = nullptr;
@@ -234,6 +240,10 @@ int load_module(const char* path, Module** out) {
             {&m.prefill[1], "gi_prefill_fwd_i8"},
             {&m.prefill64[0], "gi_prefill_fwd_h64"},
             {&m.prefill64[1], "gi_prefill_fwd_h64_i8"},
+            {&m.dec_f32[0], "gi_decode_f32"},
+            {&m.dec_f32[1], "gi_decode_f32_i8"},
+            {&m.prefill_f32[0], "gi_prefill_f32"},
+            {&m.prefill_f32[1], "gi_prefill_f32_i8"},
             {&m.prefill256r, "gi_prefill_fwd_h256r"},
             {&m.prefill256r_fmt[0], "gi_prefill_fwd_h256r_i8"},
             {&m.prefill256r_fmt[1], "gi_prefill_fwd_h256r_q4"},
@@ -333,6 +343,7 @@ struct DecVariant {
 DecVariant dec_variant(int n_tok, int G, int hd = 128, int fmt = 0) {
     const int pairs = n_tok * G;
     const bool i8 = fmt == 1;
+    if (f32_hd(hd)) return DecVariant{1, false, false, 1}; // one workgroup per (slice, head, token)
     if (hd == 256 && fmt) {
         // Above 16 pairs, split kernel at 32768 keys, 64 pairs, 16/2 (same box): 4-bit two column blocks per wave
         // 29.0 us, two pair sets of one block over two waves each 29.5 (the hi/lo-split kernel before: 31.3); int8
@@ -383,6 +394,13 @@ DecVariant dec_variant(int n_tok, int G, int hd = 128, int fmt = 0) {
     return v;
 }
 
+// Most slices per (kv head, pair group): the grid stays near decode_target_wgs() workgroups. The f32 kernels take
+// one workgroup per (slice, head) and hold few registers, so they aim at four workgroups per CU.
+int slices_per_slot(int n_heads, int n_kv, int groups, int hd) {
+    if (f32_hd(hd)) return std::max(1, 4 * decode_target_wgs() / std::max(1, n_heads));
+    return std::max(1, decode_target_wgs() / std::max(1, n_kv * groups));
+}
+
 // Slices of a span: at most per_slot per (kv head, pair group), so the grid stays near decode_target_wgs(). A
 // slice holds whole wave tiles (unit / 4 keys: the waves of a workgroup take a slice's tiles in turn) and at least
 // `unit` keys (one tile per wave), and is as short as the cap allows: within one tile of the span's even share
@@ -392,7 +410,7 @@ void plan(int max_span, int n_tok, int n_heads, int n_kv, int* chunk, int* nspli
           int hd = 128, int fmt = 0) {
     int G = n_heads / n_kv;
     int groups = dec_variant(n_tok, G, hd, fmt).groups;
-    int per_slot = std::max(1, decode_target_wgs() / std::max(1, n_kv * groups));
+    int per_slot = slices_per_slot(n_heads, n_kv, groups, hd);
     const int tile = unit / kDecWaves;
     const int least = (max_span + per_slot - 1) / per_slot; // the shortest slice the cap allows
     *chunk = std::max(unit, (least + tile - 1) / tile * tile);
@@ -425,10 +443,12 @@ int check_scales(const float* ks, const float* vs, long long sc_stride, long lon
 int slice_unit(bool i8, int hd) { return hd == 256 ? kDecWaves * kDecTile / 2 : i8 ? 2 * kSliceUnit : kSliceUnit; }
 
 // Head sizes 64 (attn_prefill_tc<64>, src/cuda.rs:2620; attention_partial_gqa at any multiple of 32), 128 and 256
-// (the 4-bit cache: 256 only, checked by its entry points).
+// on the MFMA kernels (the 4-bit cache: 256 only, checked by its entry points), and the f32 kernels' multiples of
+// 16 up to 112.
 int check_shape(int n_heads, int n_kv, int hd, bool = true) {
-    if (hd != 64 && hd != 128 && hd != 256)
-        return fail("head size %d unsupported (the gfx950 kernels take 64, 128 or 256)", hd);
+    if (hd != 64 && hd != 128 && hd != 256 && !f32_hd(hd))
+        return fail("head size %d unsupported (the gfx950 kernels take 64, 128, 256 and the multiples of 16 up to "
+                    "112)", hd);
     if (n_kv <= 0 || n_heads <= 0 || n_heads % n_kv != 0)
         return fail("n_heads %d must be a positive multiple of n_kv %d", n_heads, n_kv);
     return 0;
@@ -500,6 +520,13 @@ int decode_impl(void* stream, const float* q, long long q_stride, const void* kc
         a.sc_head_stride = sc_head_stride;
     }
     hipStream_t st = (hipStream_t)stream;
+    if (f32_hd(hd)) {
+        if (int e = launch(kDecodePartial, m->dec_f32[i8], dim3(a.nsplit, n_heads, n_tok), dim3(256), st, &a, sizeof a))
+            return e;
+        if (a.nsplit == 1) return 0;
+        return launch(kDecodeCombine, m->combine, dim3(n_heads, n_tok, kCombineSplit * hd / 128), dim3(64), st, &a,
+                      sizeof a);
+    }
     hipFunction_t f = hd == 64    ? m->dec64[i8][var.pm ? var.ncb : 0]
                       : hd == 256 ? (var.ws2 ? m->dec_pm256[fmt] : fmt ? m->dec_ref[fmt - 1 + var.ncb - 1]
                                    : var.pm ? m->dec_pm256[0] : m->dec256)
@@ -517,7 +544,8 @@ int rope_impl(void* stream, float* qkv, const float* qn, const float* kn, void* 
               int pos0, const int* posp, int ctx_cap, int n, int n_heads, int n_kv, int hd, int rope_dim, float base,
               const float* ff, int neox, float eps) {
     if (fmt == 2 && hd != 256) return fail("the 4-bit cache takes head size 256 only (got %d)", hd);
-    if (hd != 64 && hd != 128 && hd != 256) return fail("head size %d unsupported by the KV store (64, 128, 256)", hd);
+    if (hd != 64 && hd != 128 && hd != 256 && !f32_hd(hd))
+        return fail("head size %d unsupported by the KV store (64, 128, 256, the multiples of 16 up to 112)", hd);
     if (n_kv <= 0 || n_heads <= 0 || n_heads % n_kv != 0)
         return fail("n_heads %d must be a positive multiple of n_kv %d", n_heads, n_kv);
     if (n <= 0) return fail("n %d must be positive", n);
@@ -630,6 +658,10 @@ int prefill_impl(void* stream, const void* q, int q_dtype, long long q_stride, c
     a.qscale = scale * kLog2e;
     a.q_f16 = q_dtype == GI_F16;
     a.out_f16 = out_dtype == GI_F16;
+    a.hd = hd;
+    if (f32_hd(hd)) // one workgroup per (head, 32 query rows)
+        return launch(kPrefill, m->prefill_f32[i8], dim3((n + kF32Rows - 1) / kF32Rows * n_heads, 1, 1), dim3(256),
+                      (hipStream_t)stream, &a, sizeof a);
     if (hd == 256) // one workgroup per (head, 128 query rows), 16 rows per wave
         return launch(kPrefill, fmt ? m->prefill256r_fmt[fmt - 1] : m->prefill256r, dim3((n + kPrefill256rRows - 1) / kPrefill256rRows * n_heads, 1, 1),
                       dim3(m->prefill256r_threads), (hipStream_t)stream, &a, sizeof a);
@@ -673,7 +705,7 @@ size_t gi_attn_decode_workspace_bytes(int ctx_cap, int n_tok, int n_heads, int n
     for (int t = 1; t <= n_tok; t++)
         for (int fmt = 0; fmt < (hd == 256 ? 3 : 2); fmt++) {
             int groups = dec_variant(t, G, hd, fmt).groups;
-            int per_slot = std::max(1, decode_target_wgs() / std::max(1, n_kv * groups));
+            int per_slot = slices_per_slot(n_heads, n_kv, groups, hd);
             int most = std::max(1, std::min(per_slot, (ctx_cap + unit - 1) / unit));
             best = std::max(best, (size_t)t * n_heads * most * (hd + 4) * sizeof(float));
         }

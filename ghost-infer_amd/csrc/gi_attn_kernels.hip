@@ -1283,7 +1283,7 @@ struct GiPrefillArgs {
     float qscale;          // scale * log2(e), applied to the f32 scores
     int q_f16;
     int out_f16;
-    int pad_;
+    int hd;                // head size (the f32 kernels of gi_attn_f32.hip read it; the MFMA kernels are built per size)
     // int8 cache only (gi_prefill_fwd_i8): kc / vc hold int8 rows in the same element layout; the f32 scale
     // of position t, kv head h is at ks / vs [t*sc_stride + h*sc_head_stride]
     const float* ks;
@@ -2209,7 +2209,7 @@ struct GiRopeArgs {
     int n;                 // tokens
     int n_heads;
     int n_kv;
-    int hd;                // 64, 128 or 256
+    int hd;                // 64, 128, 256, or a multiple of 16 up to 112 (the lane-masked form)
     int rope_dim;          // rotated dims (even, <= hd); the rest pass unchanged
     float base;
     float eps;
@@ -2268,9 +2268,10 @@ __device__ __forceinline__ void gi_store_row(const GiRopeArgs& a, uint16_t* cach
                                              const float __attribute__((ext_vector_type(PER))) x, int lane) {
     if (pos < 0 || pos >= a.ctx_cap) return; // (a device position past the capacity writes nothing)
     const long long off = (long long)pos * a.kv_stride + (long long)kh * a.kv_head_stride;
+    const bool act = PER * lane < a.hd; // (lanes past a lane-masked head's dims hold zeros and store nothing)
     if (a.fmt == 0) {
         typedef _Float16 hv __attribute__((ext_vector_type(PER)));
-        *reinterpret_cast<hv*>(cache + off + PER * lane) = __builtin_convertvector(x, hv);
+        if (act) *reinterpret_cast<hv*>(cache + off + PER * lane) = __builtin_convertvector(x, hv);
         return;
     }
     float amax = 0.f;
@@ -2298,16 +2299,20 @@ __device__ __forceinline__ void gi_store_row(const GiRopeArgs& a, uint16_t* cach
     bv q;
 #pragma unroll
     for (int j = 0; j < PER; j++) q[j] = (int8_t)__float2int_rn(x[j] * inv);
-    *reinterpret_cast<bv*>(reinterpret_cast<int8_t*>(cache) + off + PER * lane) = q;
+    if (act) *reinterpret_cast<bv*>(reinterpret_cast<int8_t*>(cache) + off + PER * lane) = q;
     if (lane == 0) scale[(long long)pos * a.sc_stride + (long long)kh * a.sc_head_stride] = dd;
 }
 
-// PER = hd / 64 values per lane, dims PER*lane .. PER*lane + PER - 1 (one 4, 8 or 16-byte access per row)
-template <int PER>
+// PER = hd / 64 values per lane, dims PER*lane .. PER*lane + PER - 1 (one 4, 8 or 16-byte access per row).
+// MASKED (PER = 2): any even head size up to 128 (the f32 kernels' head sizes): lanes past hd / 2 hold zeros and
+// neither load nor store.
+template <int PER, bool MASKED = false>
 __device__ __forceinline__ void gi_qk_norm_rope_t(const GiRopeArgs& a, float (*cs_sh)[2], float (*row_sh)[256]) {
     typedef float fv __attribute__((ext_vector_type(PER)));
-    constexpr int HD = 64 * PER;
+    static_assert(!MASKED || PER == 2, "the lane-masked form: two values per lane");
+    const int HD = MASKED ? a.hd : 64 * PER;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const bool act = !MASKED || PER * lane < HD; // the lane holds dims of the head
     const int items = a.n_heads + 2 * a.n_kv;
     const int b = blockIdx.y, h0 = blockIdx.x * ROPE_HEADS;
     const int pos = (a.posp ? *a.posp : a.pos0) + b;
@@ -2329,7 +2334,8 @@ __device__ __forceinline__ void gi_qk_norm_rope_t(const GiRopeArgs& a, float (*c
 #pragma unroll
     for (int k = 0; k < HPW; k++) {
         const int h = h0 + wave + 4 * k;
-        if (h < items) v[k] = *reinterpret_cast<const fv*>(row + (long long)h * HD + PER * lane); // q, k, v heads in turn
+        v[k] = fv{};
+        if (h < items && act) v[k] = *reinterpret_cast<const fv*>(row + (long long)h * HD + PER * lane); // q, k, v heads in turn
     }
 #pragma unroll
     for (int k = 0; k < HPW; k++) {
@@ -2350,11 +2356,11 @@ __device__ __forceinline__ void gi_qk_norm_rope_t(const GiRopeArgs& a, float (*c
             for (int j = 0; j < PER; j++) ss = fmaf(x[j], x[j], ss);
             for (int m = 32; m > 0; m >>= 1) ss += __shfl_xor(ss, m, 64);
             const float scale = __frsqrt_rn(ss / (float)HD + a.eps);
-            const fv wv = *reinterpret_cast<const fv*>(w + PER * lane);
+            const fv wv = act ? *reinterpret_cast<const fv*>(w + PER * lane) : fv{};
 #pragma unroll
             for (int j = 0; j < PER; j++) x[j] = x[j] * scale * wv[j];
         }
-        *reinterpret_cast<fv*>(sh + PER * lane) = x;
+        if (act) *reinterpret_cast<fv*>(sh + PER * lane) = x;
         __builtin_amdgcn_wave_barrier();
         for (int i = lane; i < half; i += 64) {
             const int ia = a.neox ? i : 2 * i, ib = a.neox ? i + half : 2 * i + 1;
@@ -2363,11 +2369,11 @@ __device__ __forceinline__ void gi_qk_norm_rope_t(const GiRopeArgs& a, float (*c
             sh[ib] = p * s + q * c;
         }
         __builtin_amdgcn_wave_barrier();
-        x = *reinterpret_cast<const fv*>(sh + PER * lane);
+        if (act) x = *reinterpret_cast<const fv*>(sh + PER * lane);
         // the 4-bit cache (src/cuda.rs:472-479): q and k heads rotated alike, so their dot products are kept
         if constexpr (PER == 4)
             if (a.fmt == 2) gi_fwht256(x, lane);
-        *reinterpret_cast<fv*>(row + (long long)h * HD + PER * lane) = x;
+        if (act) *reinterpret_cast<fv*>(row + (long long)h * HD + PER * lane) = x;
         if (h >= a.n_heads) gi_store_row<PER>(a, a.kc, a.ks, pos, h - a.n_heads, x, lane);
         __builtin_amdgcn_wave_barrier(); // the row buffer is reused by the wave's next head
     }
@@ -2377,7 +2383,8 @@ extern "C" __global__ void __launch_bounds__(256) gi_qk_norm_rope(GiRopeArgs a) 
     __shared__ float row_sh[4][256]; // a head row per wave
     if (a.hd == 64) gi_qk_norm_rope_t<1>(a, cs_sh, row_sh);
     else if (a.hd == 128) gi_qk_norm_rope_t<2>(a, cs_sh, row_sh);
-    else gi_qk_norm_rope_t<4>(a, cs_sh, row_sh);
+    else if (a.hd == 256) gi_qk_norm_rope_t<4>(a, cs_sh, row_sh);
+    else gi_qk_norm_rope_t<2, true>(a, cs_sh, row_sh);
 }
 
 // ------------------------------------------------------------------------------- output rotation (4-bit cache)
@@ -2435,3 +2442,6 @@ extern "C" __global__ void __launch_bounds__(256) gi_kv_relayout(GiRelayoutArgs 
         else *reinterpret_cast<uint32_t*>(dp) = *reinterpret_cast<const uint32_t*>(sp);
     }
 }
+
+// ------------------------------------------------------------------------------------------------ f32 fallback
+#include "gi_attn_f32.hip"

@@ -47,10 +47,10 @@ def test_code_object_built():
 def test_unsupported_head_size_is_rejected_with_message():
     lib = gi_attn.load_library()
     c, n = ctypes.c_int(), ctypes.c_int()
-    rc = lib.gi_attn_decode_plan(100, 1, 32, 8, 96, ctypes.byref(c), ctypes.byref(n))
+    rc = lib.gi_attn_decode_plan(100, 1, 32, 8, 72, ctypes.byref(c), ctypes.byref(n))
     assert rc == -1
-    assert "head size 96" in lib.gi_last_error().decode()
-    for hd in (64, 128, 256):
+    assert "head size 72" in lib.gi_last_error().decode()
+    for hd in (64, 128, 256, 16, 32, 48, 80, 96, 112):
         assert lib.gi_attn_decode_plan(100, 1, 32, 8, hd, ctypes.byref(c), ctypes.byref(n)) == 0
     rc = lib.gi_attn_decode_plan(100, 1, 30, 8, 128, ctypes.byref(c), ctypes.byref(n))
     assert rc == -1 and "multiple of n_kv" in lib.gi_last_error().decode()
@@ -59,11 +59,11 @@ def test_unsupported_head_size_is_rejected_with_message():
 def test_decode_rejects_bad_arguments_before_any_launch():
     _fake_pointers_only_without_a_gpu()
     lib = gi_attn.load_library()
-    # null tensors, hd 96, misaligned pointers: all refused on the host
+    # null tensors, hd 72, misaligned pointers: all refused on the host
     rc = lib.gi_attn_decode(None, None, 4096, None, None, 512, 128, None, 4096, None, 0, 0, None, 0, 1, 32, 4, 128,
                             0.088)
     assert rc == -1 and "null" in lib.gi_last_error().decode()
-    rc = lib.gi_attn_decode(None, 16, 4096, 16, 16, 512, 128, 16, 4096, None, 0, 0, None, 0, 1, 32, 4, 96, 0.1)
+    rc = lib.gi_attn_decode(None, 16, 4096, 16, 16, 512, 128, 16, 4096, None, 0, 0, None, 0, 1, 32, 4, 72, 0.1)
     assert rc == -1 and "head size" in lib.gi_last_error().decode()
     rc = lib.gi_attn_decode(None, 8, 4096, 16, 16, 512, 128, 16, 4096, None, 0, 0, None, 0, 1, 32, 4, 128, 0.1)
     assert rc == -1 and "aligned" in lib.gi_last_error().decode()

@@ -188,6 +188,8 @@ ROPE_I8_SHAPES = [
     (7, 100, 16, 4, 64, False, False, "reference"),
     (300, 0, 32, 4, 128, True, True, "head_major"),
     (3, 2000, 8, 2, 256, True, True, "reference"),
+    (5, 300, 12, 4, 96, True, True, "reference"),   # a head size of the f32 kernels (the lane-masked store)
+    (33, 40, 32, 32, 80, False, True, "head_major"),
 ]
 # seeded random shapes: head sizes 64/128/256, 1-300 rows at positions up to 5000, 1-8 kv heads, group sizes 1-8
 _rng = np.random.default_rng(51)

@@ -365,6 +365,11 @@ def _rope_cases(count, seed):
 
 
 ROPE_SHAPES += _rope_cases(12, 41)
+# head sizes of the f32 kernels (the lane-masked cache write): Phi-2-style 80, Phi-3-style 96, 32 and 112
+ROPE_SHAPES += [(5, 300, 32, 32, 80, 32, True, True, False, "reference"),
+                (9, 1000, 32, 8, 96, 96, True, True, True, "head_major"),
+                (3, 17, 8, 2, 32, 32, False, False, False, "reference"),
+                (40, 0, 12, 4, 112, 56, True, True, False, "head_major")]
 
 
 @pytest.mark.parametrize("n,pos0,n_heads,n_kv,hd,rope_dim,neox,norm,use_ff,layout", ROPE_SHAPES)
