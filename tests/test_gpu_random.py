@@ -35,7 +35,20 @@ def cases(fmt, count=12, seed=0):
     return out
 
 
-CASES = cases("f16", seed=11) + cases("i8", seed=12) + cases("q4", seed=13)
+def cases_hd(fmt, hds, count, seed):
+    """Cases at head sizes beyond 128 and 256: 64 (the MFMA kernels) and the f32 kernels' multiples of 16."""
+    rng = np.random.default_rng(seed)
+    out = []
+    for i in range(count):
+        n_kv = int(rng.choice([1, 2, 4, 8]))
+        out.append((fmt, 100 + i, int(rng.integers(1, 16)), int(rng.integers(0, 6000)), n_kv * int(rng.integers(1, 9)),
+                    n_kv, int(rng.choice(hds))))
+    return out
+
+
+CASES = (cases("f16", seed=11) + cases("i8", seed=12) + cases("q4", seed=13) + cases_hd("f16", [64], 6, 14)
+         + cases_hd("i8", [64], 6, 15) + cases_hd("f16", [16, 32, 48, 80, 96, 112], 6, 16)
+         + cases_hd("i8", [32, 80, 96, 112], 4, 17))
 
 
 @pytest.mark.parametrize("fmt,i,n_tok,pos0,n_heads,n_kv,hd", CASES, ids=lambda v: str(v))

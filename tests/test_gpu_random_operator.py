@@ -32,7 +32,7 @@ def cases(fmt, count, seed):
         G = int(rng.integers(1, 9))
         n = int(rng.choice([int(rng.integers(1, 16)), int(rng.integers(16, 61))]))
         pos0 = int(rng.integers(0, 3001))
-        hd = 256 if fmt == "q4" else int(rng.choice([128, 256]))
+        hd = 256 if fmt == "q4" else int(rng.choice([64, 96, 128, 256]))
         exact = bool(rng.integers(0, 2))
         out.append((fmt, i, n, pos0, n_kv * G, n_kv, hd, exact))
     return out

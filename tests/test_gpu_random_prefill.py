@@ -37,7 +37,8 @@ def cases(fmt, hd, count, seed):
 
 
 CASES = (cases("f16", 128, 6, 21) + cases("f16", 256, 6, 22) + cases("i8", 128, 6, 23) + cases("i8", 256, 6, 24)
-         + cases("q4", 256, 6, 25))
+         + cases("q4", 256, 6, 25) + cases("f16", 64, 4, 26) + cases("i8", 64, 4, 27) + cases("f16", 96, 3, 28)
+         + cases("i8", 80, 3, 29))
 DT = {"f32": torch.float32, "f16": torch.float16}
 
 
