@@ -39,8 +39,8 @@ TFLOP/s) and the roofline fraction of every int8, head-64, head-256 and 4-bit wo
 oracle's restatement of the reference's CPU attention (src/model.rs:1320-1409) over the same inputs with the
 cache widened to f32 (as the reference's CPU session holds it), timed on this host at its CPU share (up to 16
 threads) and at half of it (the reference's default logical/2), for configs 2 and 1 and a bounded sample of
-config 3. The full record (every field of every workload, every chunk, the box's measured peaks) goes to
---detail-out (default gpurun_out/bench_detail.json); --full-line prints it instead. Progress messages go to
+config 3. The full record (every field of every workload, every chunk, the box's measured peaks) goes to the
+file --detail-out names; --full-line prints it instead. Progress messages go to
 stderr with --verbose.
 """
 import argparse
@@ -704,8 +704,8 @@ def main():
     ap.add_argument("--reference-layout", action="store_true",
                     help="decode workloads: also time the reference's cache layout")
     ap.add_argument("--verbose", action="store_true", help="progress messages on stderr")
-    ap.add_argument("--detail-out", default=os.path.join(ROOT, "gpurun_out", "bench_detail.json"),
-                    help="file for the full record (every field of every workload); '' for none")
+    ap.add_argument("--detail-out", default="",
+                    help="file for the full record (every field of every workload); none by default")
     ap.add_argument("--full-line", action="store_true", help="print the full record instead of the compact line")
     args = ap.parse_args()
     global VERBOSE
