@@ -55,6 +55,7 @@ sys.path.insert(0, os.path.join(ROOT, "ghost-infer_amd"))
 
 HBM_PEAK_GBS = 8000.0      # MI355X HBM3E, published
 F16_DENSE_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA, published
+FP32_DENSE_PEAK_TFLOPS = 157.3  # MI355X dense fp32 MFMA, published (the f32 kernels' prefill)
 METRIC = "decode-attn HBM GB/s @64K ctx; prefill-attn TFLOPS @8K; % of roofline"
 HD = 128
 
@@ -135,7 +136,7 @@ def decode_kernel_name(n_tok, n_heads, n_kv, hd, i8):
     or, above 16 pairs, two pair sets (int8) or two column blocks per wave (4-bit))."""
     pairs, p = n_tok * (n_heads // n_kv), 8
     if hd not in (64, 128, 256):  # the f32 kernels' head sizes
-        return "gi_decode_f32" + ("_i8" if i8 else "")
+        return "gi_decode_f32" + ("_i8" if i8 else "") + f"_h{hd}"
     if hd == 256 and i8:  # the reference's tc256 roundings, one pair per column: 16 or 32 pairs per workgroup
         if pairs <= 2 * p:
             return "gi_decode_pm_1" + ("_q4" if i8 == "q4" else "_i8_h256")
@@ -482,14 +483,17 @@ def cpu_baseline_prefill(q, k, v, n_heads, n_kv, threads, rows=64, budget_s=8.0)
     return flops / t / 1e12, runs, flops, t
 
 
-def prefill_roofline(gi_attn, r, steps, torch, profile="pmc_prefill_prefill8k", kernel="gi_prefill_fwd"):
-    """Roofline object of the prefill kernel: algorithmic flops of one launch / its mean duration."""
+def prefill_roofline(gi_attn, r, steps, torch, profile="pmc_prefill_prefill8k", kernel="gi_prefill_fwd",
+                     peak=None):
+    """Roofline object of the prefill kernel: algorithmic flops of one launch / its mean duration, against the
+    dense f16 MFMA peak (the f32 kernels: the dense f32 MFMA peak)."""
+    peak = peak or F16_DENSE_PEAK_TFLOPS
     # ~0.1 s of launches before the timed ones (at most 100)
     warm = min(100, max(0, math.ceil(0.1 / r["seconds"])))
     ms, n = kernel_times(gi_attn, r["step"], steps, torch, ("prefill",), warm)["prefill"]
     tf = r["flops"] / (ms / 1e3) / 1e12
-    return {"bound": "mfma", "achieved": round(tf, 1), "peak": F16_DENSE_PEAK_TFLOPS, "unit": "TFLOP/s",
-            "frac": round(tf / F16_DENSE_PEAK_TFLOPS, 4), "traffic": profile_traffic(profile),
+    return {"bound": "mfma", "achieved": round(tf, 1), "peak": peak, "unit": "TFLOP/s",
+            "frac": round(tf / peak, 4), "traffic": profile_traffic(profile),
             "kernel": kernel, "algorithmic_flops_per_launch": r["flops"],
             "kernel_ms_per_launch": round(ms, 5), "launches_timed": n}
 
@@ -582,11 +586,12 @@ def run_prefill(torch, gi_attn, dev, w, steps, warmup):
     tf = r["flops"] / r["seconds"] / 1e12
     kernel = ("gi_prefill_fwd_h256r" + ("_q4" if i8 == "q4" else "_i8" if i8 else "") if hd == 256
               else "gi_prefill_fwd_h64" + ("_i8" if i8 else "") if hd == 64
-              else "gi_prefill_f32" if hd == 96
+              else f"gi_prefill_f32_h{hd}" if hd not in (64, 128)
               else "gi_prefill_fwd_i8" if i8 else "gi_prefill_fwd")
     line = {
         "value": round(tf, 1), "unit": "TFLOP/s", "ms_per_step": r["seconds"] * 1e3,
         "dtype": ("4-bit K/V widened to f16 MFMA, f32 acc" if i8 == "q4" else
+                  "f32 MFMA (f16 cache widened), f32 acc" if hd not in (64, 128, 256) else
                   "int8 K/V widened to f16 MFMA, f32 acc" if i8 else "f16 MFMA, f32 acc"),
         "config": {"workload": (f"causal prefill, 8192 tokens, {nh}q/{nkv}kv, hd 256 (Qwen3.5-style heads){cache}"
                                 if hd == 256 else
@@ -595,7 +600,8 @@ def run_prefill(torch, gi_attn, dev, w, steps, warmup):
                                 "causal prefill, 8192 tokens, 32q/32kv, hd 96 (Phi-3-style heads, the f32 kernels)"
                                 if hd == 96 else "config 3: causal prefill, 8192 tokens, 32q/8kv, hd 128" +
                                 (", int8 cache" if i8 else "")), "flops_per_step": r["flops"]},
-        "roofline": prefill_roofline(gi_attn, r, steps, torch, f"pmc_prefill_{w}", kernel),
+        "roofline": prefill_roofline(gi_attn, r, steps, torch, f"pmc_prefill_{w}", kernel,
+                                     FP32_DENSE_PEAK_TFLOPS if hd not in (64, 128, 256) else None),
     }
     return line, r
 

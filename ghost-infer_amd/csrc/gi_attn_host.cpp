@@ -128,11 +128,14 @@ struct GiPrefillArgs {
 };
 
 constexpr float kLog2e = 1.4426950408889634f;
-constexpr int kF32Rows = 32; // query rows per gi_prefill_f32 workgroup; must match the kernels' PF32_ROWS
+constexpr int kF32Rows = 128;   // query rows per gi_prefill_f32_* workgroup; must match the kernels' PF32_ROWS
+constexpr int kF32Threads = 512; // its block size (8 waves of 16 rows)
 
 // Head sizes of the f32 kernels (gi_attn_f32.hip): the multiples of 16 up to 112 that the MFMA kernels do not
 // take, the reference's f32 fallback cases (attention_partial / attention_prefill, src/cuda.rs:1866-2041).
 bool f32_hd(int hd) { return hd % 16 == 0 && hd >= 16 && hd <= 112 && hd != 64; }
+constexpr int kF32Sizes[6] = {16, 32, 48, 80, 96, 112}; // the f32 kernels' builds, in this order
+int f32_index(int hd) { return hd < 64 ? hd / 16 - 1 : hd / 16 - 2; }
 constexpr int kMaxDevices = 64;
 constexpr int kRopeHeads = 16; // heads per gi_qk_norm_rope workgroup; must match the kernels' ROPE_HEADS
 constexpr int kCombineSplit = 8; // combine workgroups per (head, token); must match the kernels' CMB_DSPLIT
@@ -176,7 +179,7 @@ struct Module {
     hipFunction_t dec_pm256[2] = {};  // head size 256, one pair per column, two pair sets of two waves: [f16, int8]
     hipFunction_t prefill[2] = {};   // [int8 cache], head size 128
     hipFunction_t prefill64[2] = {}; // [int8 cache], head size 64 (the same launch shape and block size)
-    hipFunction_t dec_f32[2] = {}, prefill_f32[2] = {}; // [int8 cache]: the f32 kernels
+    hipFunction_t dec_f32[2][6] = {}, prefill_f32[2][6] = {}; // the f32 kernels: [int8 cache][kF32Sizes index]
     hipFunction_t prefill256r = nullptr; // head size 256 (f16 cache), 16 rows per wave: one workgroup per query tile
     hipFunction_t prefill256r_fmt[2] = {}; // the same over the int8 and the 4-bit cache
     hipFunction_t combine = nullptr, rope = nullptr, relayout = nullptr, hadamard = nullptr;
@@ -240,10 +243,6 @@ int load_module(const char* path, Module** out) {
             {&m.prefill[1], "gi_prefill_fwd_i8"},
             {&m.prefill64[0], "gi_prefill_fwd_h64"},
             {&m.prefill64[1], "gi_prefill_fwd_h64_i8"},
-            {&m.dec_f32[0], "gi_decode_f32"},
-            {&m.dec_f32[1], "gi_decode_f32_i8"},
-            {&m.prefill_f32[0], "gi_prefill_f32"},
-            {&m.prefill_f32[1], "gi_prefill_f32_i8"},
             {&m.prefill256r, "gi_prefill_fwd_h256r"},
             {&m.prefill256r_fmt[0], "gi_prefill_fwd_h256r_i8"},
             {&m.prefill256r_fmt[1], "gi_prefill_fwd_h256r_q4"},
@@ -254,6 +253,19 @@ int load_module(const char* path, Module** out) {
                 (void)hipModuleUnload(m.mod);
                 m.mod = nullptr;
                 return e;
+            }
+        for (int i8 = 0; i8 < 2; i8++)
+            for (int i = 0; i < 6; i++) {
+                char dn[64], pn[64];
+                snprintf(dn, sizeof dn, "gi_decode_f32%s_h%d", i8 ? "_i8" : "", kF32Sizes[i]);
+                snprintf(pn, sizeof pn, "gi_prefill_f32%s_h%d", i8 ? "_i8" : "", kF32Sizes[i]);
+                int e = check(hipModuleGetFunction(&m.dec_f32[i8][i], m.mod, dn), dn);
+                if (!e) e = check(hipModuleGetFunction(&m.prefill_f32[i8][i], m.mod, pn), pn);
+                if (e) {
+                    (void)hipModuleUnload(m.mod);
+                    m.mod = nullptr;
+                    return e;
+                }
             }
         if (int e = check(hipFuncGetAttribute(&m.prefill_threads[0], HIP_FUNC_ATTRIBUTE_MAX_THREADS_PER_BLOCK, m.prefill[0]),
                           "hipFuncGetAttribute(gi_prefill_fwd)") ||
@@ -521,7 +533,7 @@ int decode_impl(void* stream, const float* q, long long q_stride, const void* kc
     }
     hipStream_t st = (hipStream_t)stream;
     if (f32_hd(hd)) {
-        if (int e = launch(kDecodePartial, m->dec_f32[i8], dim3(a.nsplit, n_heads, n_tok), dim3(256), st, &a, sizeof a))
+        if (int e = launch(kDecodePartial, m->dec_f32[i8][f32_index(hd)], dim3(a.nsplit, n_heads, n_tok), dim3(256), st, &a, sizeof a))
             return e;
         if (a.nsplit == 1) return 0;
         return launch(kDecodeCombine, m->combine, dim3(n_heads, n_tok, kCombineSplit * hd / 128), dim3(64), st, &a,
@@ -659,9 +671,9 @@ int prefill_impl(void* stream, const void* q, int q_dtype, long long q_stride, c
     a.q_f16 = q_dtype == GI_F16;
     a.out_f16 = out_dtype == GI_F16;
     a.hd = hd;
-    if (f32_hd(hd)) // one workgroup per (head, 32 query rows)
-        return launch(kPrefill, m->prefill_f32[i8], dim3((n + kF32Rows - 1) / kF32Rows * n_heads, 1, 1), dim3(256),
-                      (hipStream_t)stream, &a, sizeof a);
+    if (f32_hd(hd)) // one workgroup per (head, 128 query rows)
+        return launch(kPrefill, m->prefill_f32[i8][f32_index(hd)], dim3((n + kF32Rows - 1) / kF32Rows * n_heads, 1, 1),
+                      dim3(kF32Threads), (hipStream_t)stream, &a, sizeof a);
     if (hd == 256) // one workgroup per (head, 128 query rows), 16 rows per wave
         return launch(kPrefill, fmt ? m->prefill256r_fmt[fmt - 1] : m->prefill256r, dim3((n + kPrefill256rRows - 1) / kPrefill256rRows * n_heads, 1, 1),
                       dim3(m->prefill256r_threads), (hipStream_t)stream, &a, sizeof a);
