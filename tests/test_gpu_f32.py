@@ -41,6 +41,8 @@ DECODE_SHAPES = [
     (15, 513, 8, 1, 48),
     (1, 20000, 16, 4, 32),
     (2, 77, 4, 2, 16),
+    (15, 0, 6, 2, 112),     # every token's span inside the first tile
+    (4, 65535, 8, 8, 80),   # many slices, a span ending one key short of a tile
 ]
 
 
@@ -97,6 +99,13 @@ PREFILL_SHAPES = [
     (64, 500, 8, 1, 48, np.float16, torch.float32, "reference"),
     (33, 0, 4, 2, 16, np.float32, torch.float32, "head_major"),
     (600, 0, 16, 4, 32, np.float32, torch.float32, "reference"),
+    # one row, a few rows and the 128-row workgroup's edges, after a prefix (a chunk of a longer prompt)
+    (1, 0, 8, 8, 80, np.float32, torch.float32, "reference"),
+    (1, 700, 8, 2, 96, np.float16, torch.float32, "head_major"),
+    (5, 61, 6, 3, 48, np.float32, torch.float32, "reference"),
+    (127, 1, 4, 4, 112, np.float32, torch.float32, "reference"),
+    (129, 200, 4, 1, 80, np.float32, torch.float32, "head_major"),
+    (300, 4000, 2, 2, 16, np.float16, torch.float16, "reference"),
 ]
 
 
