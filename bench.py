@@ -3,7 +3,8 @@
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload decode64k|decode4k|verify|prefill8k|chunked|qkrope|
                     decode64k_i8|verify_i8|prefill8k_i8|decode64k_h256|verify_h256|prefill8k_h256|
                     decode64k_h256_i8|verify_h256_i8|prefill8k_h256_i8|decode64k_h256_q4|verify_h256_q4|
-                    prefill8k_h256_q4|decode64k_h64|decode64k_h64_i8|prefill8k_h64|prefill8k_h64_i8|decode16k_h80|prefill8k_h96]
+                    prefill8k_h256_q4|decode64k_h64|decode64k_h64_i8|prefill8k_h64|prefill8k_h64_i8|decode16k_h80|prefill8k_h96|
+                    decode16k_h80_i8|prefill8k_h96_i8]
                     [--no-cpu-baseline] [--no-secondary] [--reference-layout] [--verbose]
                     [--detail-out FILE] [--full-line]
 
@@ -24,8 +25,9 @@ A step is one pass of the hot path over one batch of synthetic seeded input alre
              head size 256 over the 4-bit cache (the reference's --kv q4: 128 bytes a row plus 8 f16 scales)
   decode64k_h64, decode64k_h64_i8, prefill8k_h64, prefill8k_h64_i8
              head size 64 (Llama-3.2-1B-style 32 query / 8 kv heads) over the f16 and int8 caches
-  decode16k_h80, prefill8k_h96
-             the f32 kernels' head sizes (Phi-2-style 80, Phi-3-style 96; 32 query / 32 kv heads)
+  decode16k_h80, prefill8k_h96, decode16k_h80_i8, prefill8k_h96_i8
+             the f32 kernels' head sizes (Phi-2-style 80, Phi-3-style 96; 32 query / 32 kv heads), over the f16
+             and int8 caches
   decode64k_i8, verify_i8, prefill8k_i8
              configs 2, 4 and 3 over the int8 cache (the reference's KV8 format: int8 rows, an f32 scale per
              position and kv head); bytes are the int8 rows plus their scales
@@ -525,6 +527,8 @@ DECODE_WORKLOADS = {
                                                     "65536, 32q/8kv"),
     "decode16k_h80": (16384, 32, 32, 1, 80, False, "decode with 80-wide heads (Phi-2-style 32q/32kv, the f32 kernels), "
                                                    "1 token, ctx 16384, f16 cache"),
+    "decode16k_h80_i8": (16384, 32, 32, 1, 80, True, "decode with 80-wide heads over the int8 cache (the f32 kernels), "
+                                                     "1 token, ctx 16384, 32q/32kv"),
 }
 
 
@@ -573,7 +577,7 @@ def run_decode(torch, gi_attn, dev, w, steps, warmup, n_tok_override=None, refer
 
 
 PREFILL_WORKLOADS = ("prefill8k", "prefill8k_i8", "prefill8k_h256", "prefill8k_h256_i8", "prefill8k_h256_q4",
-                     "prefill8k_h64", "prefill8k_h64_i8", "prefill8k_h96")
+                     "prefill8k_h64", "prefill8k_h64_i8", "prefill8k_h96", "prefill8k_h96_i8")
 
 
 def run_prefill(torch, gi_attn, dev, w, steps, warmup):
@@ -586,18 +590,18 @@ def run_prefill(torch, gi_attn, dev, w, steps, warmup):
     tf = r["flops"] / r["seconds"] / 1e12
     kernel = ("gi_prefill_fwd_h256r" + ("_q4" if i8 == "q4" else "_i8" if i8 else "") if hd == 256
               else "gi_prefill_fwd_h64" + ("_i8" if i8 else "") if hd == 64
-              else f"gi_prefill_f32_h{hd}" if hd not in (64, 128)
+              else "gi_prefill_f32" + ("_i8" if i8 else "") + f"_h{hd}" if hd not in (64, 128)
               else "gi_prefill_fwd_i8" if i8 else "gi_prefill_fwd")
     line = {
         "value": round(tf, 1), "unit": "TFLOP/s", "ms_per_step": r["seconds"] * 1e3,
         "dtype": ("4-bit K/V widened to f16 MFMA, f32 acc" if i8 == "q4" else
-                  "f32 MFMA (f16 cache widened), f32 acc" if hd not in (64, 128, 256) else
+                  "f32 MFMA (" + ("int8" if i8 else "f16") + " cache widened), f32 acc" if hd not in (64, 128, 256) else
                   "int8 K/V widened to f16 MFMA, f32 acc" if i8 else "f16 MFMA, f32 acc"),
         "config": {"workload": (f"causal prefill, 8192 tokens, {nh}q/{nkv}kv, hd 256 (Qwen3.5-style heads){cache}"
                                 if hd == 256 else
                                 f"causal prefill, 8192 tokens, 32q/8kv, hd 64 (Llama-3.2-1B-style heads){cache}"
                                 if hd == 64 else
-                                "causal prefill, 8192 tokens, 32q/32kv, hd 96 (Phi-3-style heads, the f32 kernels)"
+                                "causal prefill, 8192 tokens, 32q/32kv, hd 96 (Phi-3-style heads, the f32 kernels)" + cache
                                 if hd == 96 else "config 3: causal prefill, 8192 tokens, 32q/8kv, hd 128" +
                                 (", int8 cache" if i8 else "")), "flops_per_step": r["flops"]},
         "roofline": prefill_roofline(gi_attn, r, steps, torch, f"pmc_prefill_{w}", kernel,
