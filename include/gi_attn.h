@@ -25,13 +25,13 @@
  *  - Device positions (posp, graph replay): no entry point reports a device position that overruns the
  *    cache, since the host never sees it. The decode kernels (which gi_attention* use whenever posp is
  *    set) clamp *posp into [0, ctx_cap - n_tok] and return the attention at the clamped position; the
- *    cache writes store no row at a position outside [0, ctx_cap). A caller that can overrun checks its position on the host before
- *    replaying (the reference trusts *posp the same way, src/cuda.rs:8686-8712).
+ *    cache writes store no row at a position outside [0, ctx_cap). A caller that can overrun checks its
+ *    position on the host before replaying (the reference trusts *posp the same way, src/cuda.rs:8686-8712).
  *  - hd is 64, 128 or 256 with the f16 and the int8 caches, and 256 with the 4-bit cache (the *_q4 entry
  *    points); also 16, 32, 48, 80, 96 or 112 with the f16 and the int8 caches, on f32 kernels (the reference's
  *    f32 fallback, attention_partial and attention_prefill, src/cuda.rs:1866-2041); n_heads must be a multiple
- *    of n_kv. Head size 64 is attention_partial_gqa at a head size that is a
- *    multiple of 32 (src/cuda.rs:8419-8422) and attention_prefill_tc64 (src/cuda.rs:2620, dispatched at
+ *    of n_kv. Head size 64 is attention_partial_gqa at a head size that is a multiple of 32
+ *    (src/cuda.rs:8419-8422) and attention_prefill_tc64 (src/cuda.rs:2620, dispatched at
  *    src/cuda.rs:8452-8456); 256 the reference's wide heads (attention_partial_gqa's hd 256 branch
  *    src/cuda.rs:1762-1781, attention_prefill_tc256 src/cuda.rs:2622-2623, attention_decode_tc256
  *    src/cuda.rs:2625-2802).
