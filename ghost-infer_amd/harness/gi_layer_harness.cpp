@@ -47,7 +47,7 @@ void gi_ok(int rc, const char* what) {
 }
 
 void usage() {
-    printf("usage: gi_layer_harness [--prompt N] [--steps S] [--heads H] [--kv K] [--hd 64|128|256] [--int8 | --q4]\n"
+    printf("usage: gi_layer_harness [--prompt N] [--steps S] [--heads H] [--kv K] [--hd 64|128|256|16..112] [--int8 | --q4]\n"
            "                        [--no-graph] [--seed X] [--dump FILE]\n"
            "Plays one layer's attention through the C ABI (cache write + prefill for the prompt, then one\n"
            "decode step per token, replayed from a HIP graph), checks every output row against the exact\n"
@@ -81,9 +81,11 @@ Opts parse(int argc, char** argv) {
         }
         else die("unknown argument " + a);
     }
+    const bool f32_hd = o.hd % 16 == 0 && o.hd >= 16 && o.hd <= 112 && o.hd != 64; // the f32 kernels' sizes
     if (o.prompt < 1 || o.steps < 0 || o.heads < 1 || o.kv < 1 || o.heads % o.kv ||
-        (o.hd != 64 && o.hd != 128 && o.hd != 256) || (o.q4 && (o.hd != 256 || o.i8)))
-        die("bad shape (heads a multiple of kv; hd 64, 128 or 256; --q4 takes hd 256 and not --int8)");
+        (o.hd != 64 && o.hd != 128 && o.hd != 256 && !f32_hd) || (o.q4 && (o.hd != 256 || o.i8)))
+        die("bad shape (heads a multiple of kv; hd 64, 128, 256 or a multiple of 16 up to 112; --q4 takes hd 256 "
+            "and not --int8)");
     return o;
 }
 
@@ -265,7 +267,9 @@ int main(int argc, char** argv) {
     // attention_decode_tc256 does, against each launch's own running maxima, so a decode step and a verify block
     // of the reference pass agree to about f16's step)
     const double tol_split = hd == 256 && (o.i8 || o.q4) ? 1e-3 : 2e-5;
-    const double tol_prompt = o.prompt >= 16 ? 2e-3 : tol_split, tol_decode = tol_split;
+    // (the f32 kernels' head sizes compute prompts in f32 too: no f16 P)
+    const bool f32_path = hd != 64 && hd != 128 && hd != 256;
+    const double tol_prompt = o.prompt >= 16 && !f32_path ? 2e-3 : tol_split, tol_decode = tol_split;
     const bool ok = finite && err_prompt <= tol_prompt && err_decode <= tol_decode;
     printf("{\"prompt\": %d, \"steps\": %d, \"heads\": %d, \"kv\": %d, \"hd\": %d, \"cache\": \"%s\", \"graph\": %s, "
            "\"prompt_ms\": %.4f, \"decode_step_us\": %.2f, \"max_abs_prompt\": %.3g, \"max_abs_decode\": %.3g, "

@@ -33,6 +33,10 @@ CASES = [
     (["--heads", "9", "--kv", "3", "--hd", "64", "--prompt", "200", "--steps", "12"], 200, 12, 9, 3, 64, False),
     (["--int8", "--heads", "9", "--kv", "3", "--hd", "64", "--prompt", "200", "--steps", "12"], 200, 12, 9, 3, 64,
      True),
+    # the f32 kernels' head sizes: Phi-2-style 80 (32 / 32 heads), and 96 grouped over the int8 cache
+    (["--heads", "32", "--kv", "32", "--hd", "80", "--prompt", "150", "--steps", "8"], 150, 8, 32, 32, 80, False),
+    (["--int8", "--heads", "12", "--kv", "4", "--hd", "96", "--prompt", "130", "--steps", "8"], 130, 8, 12, 4, 96,
+     True),
 ]
 
 
@@ -59,6 +63,7 @@ def test_layer_harness(case, tmp_path):
     kr = qkv[:, orow:orow + K * hd]
     vr = qkv[:, orow + K * hd:]
     pre, dec = slice(0, prompt), slice(prompt, total)
+    f32_path = hd not in (64, 128, 256)  # the f32 kernels: prompts in f32 as well
     if i8 == "q4":
         # the cache the kernels hold: the rotated k rows and the v rows rotated here, each quantised by kv_store's
         # KV4; the oracle attends with the rotated queries and its output is rotated back
@@ -78,27 +83,30 @@ def test_layer_harness(case, tmp_path):
         kc, ks = O.kv_quant_i8(kr.reshape(total, K, hd))
         vc, vs = O.kv_quant_i8(vr.reshape(total, K, hd))
         kc, vc = kc.reshape(total, K * hd), vc.reshape(total, K * hd)
-        want_pre = O.prefill_tc_semantics_i8(q[pre], kc, vc, ks, vs, 0, H, K, hd=hd)
+
+        def deq(c, sc):
+            return (c.reshape(total, K, hd).astype(np.float32) * sc[:, :, None]).reshape(total, -1)
+
+        want_pre = (O.prefill_tc_semantics_i8(q[pre], kc, vc, ks, vs, 0, H, K, hd=hd) if not f32_path
+                    else O.attention(q[pre], deq(kc, ks), deq(vc, vs), 0, H, K, hd=hd))
         if hd == 256:
             want_dec = O.decode_tc256_i8(q[dec], kc, vc, ks, vs, prompt, H, K)
         elif hd == 128:
             want_dec = O.decode_gpu_semantics_i8(q[dec], kc, vc, ks, vs, prompt, H, K)
         else:  # Model::attention over the dequantised cache
-            def deq(c, sc):
-                return (c.reshape(total, K, hd).astype(np.float32) * sc[:, :, None]).reshape(total, -1)
-
             want_dec = O.attention(q[dec], deq(kc, ks), deq(vc, vs), prompt, H, K, hd=hd)
         f64 = reference_f64_i8(q, kc, vc, ks, vs, 0, H, K, hd=hd)
     else:
         kc = kr.astype(np.float16).view(np.uint16)
         vc = vr.astype(np.float16).view(np.uint16)
-        want_pre = (O.prefill_tc_semantics(q[pre], kc, vc, 0, H, K, hd=hd) if prompt >= 16
+        want_pre = (O.prefill_tc_semantics(q[pre], kc, vc, 0, H, K, hd=hd) if prompt >= 16 and not f32_path
                     else O.attention(q[pre], kc, vc, 0, H, K, hd=hd))
         want_dec = O.attention(q[dec], kc, vc, prompt, H, K, hd=hd)
         f64 = reference_f64(q, kc, vc, 0, H, K, hd=hd)
     # prompt rows: the prefill path (f16 P) against the reference's prefill semantics and float64, the bar
+    ptol = split_f64_tol("i8" if i8 else "f16", hd) if f32_path else ()
     assert_close(got[pre], want_pre, what="harness prompt rows vs oracle")
-    assert_close(got[pre], f64[pre], what="harness prompt rows vs f64")
+    assert_close(got[pre], f64[pre], *ptol, what="harness prompt rows vs f64")
     # decoded rows: the split path (f32 precision; head size 256 over the int8 and 4-bit caches the reference's
     # tc256 roundings), against the oracle and float64
     fmt = "q4" if i8 == "q4" else "i8" if i8 else "f16"
