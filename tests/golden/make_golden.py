@@ -42,6 +42,11 @@ CASES = {
     "prefill_h64_smollm2_48tok": (118, 48, 0, 9, 3, np.float16, 64, False),
     "decode_h64_i8_smollm2_ctx300": (119, 1, 299, 9, 3, np.float32, 64, True),
     "prefill_h64_i8_smollm2_40tok": (120, 40, 0, 9, 3, np.float32, 64, True),
+    # the f32 kernels' head sizes: Phi-2-style 80 and Phi-3-style 96 (the reference's f32 fallback kernels)
+    "decode_h80_ctx300": (121, 1, 299, 4, 4, np.float32, 80, False),
+    "verify_h96_i8_4tok_ctx100": (122, 4, 96, 12, 4, np.float32, 96, True),
+    "prefill_h96_48tok": (123, 48, 0, 8, 8, np.float16, 96, False),
+    "prefill_h80_i8_40tok": (124, 40, 0, 8, 2, np.float32, 80, True),
 }
 
 
