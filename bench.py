@@ -264,12 +264,15 @@ def prefill_workload(torch, gi_attn, dev, n, n_heads, n_kv, steps, warmup, seed,
     q = torch.randn((n, n_heads * hd), generator=gen, device=dev, dtype=torch.float32).half()
     k, v, ks, vs = seeded_cache(gen, n, n_kv, dev, torch, i8=i8, hd=hd)
     out = torch.empty((n, n_heads * hd), device=dev, dtype=torch.float16)
+    # the int8 and 4-bit caches: the keys widened into a workspace first (one launch of gi_kv_widen per step, inside
+    # the timed step), then staged as the f16 cache's tiles are
+    ws = gi_attn.prefill_workspace(n, n_kv, hd, 2 if i8 == "q4" else 1, dev) if i8 else None
 
     def step(i):
         if i8 == "q4":
-            gi_attn.prefill_q4(q, k, v, ks, vs, 0, n_heads, n_kv, out=out)
+            gi_attn.prefill_q4(q, k, v, ks, vs, 0, n_heads, n_kv, out=out, workspace=ws)
         else:
-            gi_attn.prefill(q, k, v, 0, n_heads, n_kv, hd=hd, out=out, k_scale=ks, v_scale=vs)
+            gi_attn.prefill(q, k, v, 0, n_heads, n_kv, hd=hd, out=out, k_scale=ks, v_scale=vs, workspace=ws)
 
     t = time_steps(step, steps, warmup, torch)
     return {"seconds": t, "flops": prefill_flops(n, 0, n_heads, hd), "step": step, "q": q, "k": k, "v": v}
@@ -492,12 +495,16 @@ def prefill_roofline(gi_attn, r, steps, torch, profile="pmc_prefill_prefill8k", 
     peak = peak or F16_DENSE_PEAK_TFLOPS
     # ~0.1 s of launches before the timed ones (at most 100)
     warm = min(100, max(0, math.ceil(0.1 / r["seconds"])))
-    ms, n = kernel_times(gi_attn, r["step"], steps, torch, ("prefill",), warm)["prefill"]
+    kt = kernel_times(gi_attn, r["step"], steps, torch, ("prefill", "kv_widen"), warm)
+    ms, n = kt["prefill"]
     tf = r["flops"] / (ms / 1e3) / 1e12
-    return {"bound": "mfma", "achieved": round(tf, 1), "peak": peak, "unit": "TFLOP/s",
+    line = {"bound": "mfma", "achieved": round(tf, 1), "peak": peak, "unit": "TFLOP/s",
             "frac": round(tf / peak, 4), "traffic": profile_traffic(profile),
             "kernel": kernel, "algorithmic_flops_per_launch": r["flops"],
             "kernel_ms_per_launch": round(ms, 5), "launches_timed": n}
+    if kt["kv_widen"][1]:  # the int8 / 4-bit cache's widening launch, part of every step
+        line["widen_ms_per_launch"] = round(kt["kv_widen"][0], 5)
+    return line
 
 
 # ---------------------------------------------------------------- one line per workload
@@ -588,10 +595,11 @@ def run_prefill(torch, gi_attn, dev, w, steps, warmup):
     log(f"[bench] causal prefill 8192 tokens, {nh}q/{nkv}kv, hd {hd}{cache}")
     r = prefill_workload(torch, gi_attn, dev, 8192, nh, nkv, steps, warmup, 99, i8=i8, hd=hd)
     tf = r["flops"] / r["seconds"] / 1e12
-    kernel = ("gi_prefill_fwd_h256r" + ("_q4" if i8 == "q4" else "_i8" if i8 else "") if hd == 256
-              else "gi_prefill_fwd_h64" + ("_i8" if i8 else "") if hd == 64
+    # (the int8 cache: the kernels staging the pre-widened keys, *_i8s; the 4-bit cache widened runs the f16 kernel)
+    kernel = ("gi_prefill_fwd_h256r" + ("_i8s" if i8 is True else "") if hd == 256
+              else "gi_prefill_fwd_h64" + ("_i8s" if i8 else "") if hd == 64
               else "gi_prefill_f32" + ("_i8" if i8 else "") + f"_h{hd}" if hd not in (64, 128)
-              else "gi_prefill_fwd_i8" if i8 else "gi_prefill_fwd")
+              else "gi_prefill_fwd_i8s" if i8 else "gi_prefill_fwd")
     line = {
         "value": round(tf, 1), "unit": "TFLOP/s", "ms_per_step": r["seconds"] * 1e3,
         "dtype": ("4-bit K/V widened to f16 MFMA, f32 acc" if i8 == "q4" else

@@ -103,6 +103,29 @@ struct GiRelayoutArgs {
     int pad_;
 };
 
+// Must match the kernels' GiWidenArgs.
+struct GiWidenArgs {
+    const void* kc;
+    const void* vc;
+    const void* ks;
+    const void* vs;
+    void* kw;
+    void* vw;
+    float* ksw;
+    float* vsw;
+    long long kv_stride;
+    long long kv_head_stride;
+    long long sc_stride;
+    long long sc_head_stride;
+    int n_rows;
+    int n_kv;
+    int hd;
+    int fmt;
+    float vbias;
+    int pad_;
+};
+constexpr float kPrefillI8VBias = 8.f; // the head-64/128 int8 prefill's value-scale bias (the kernels' PF_I8_VBIAS)
+
 // Must match the kernels' GiPrefillArgs.
 struct GiPrefillArgs {
     const void* q;
@@ -182,6 +205,9 @@ struct Module {
     hipFunction_t dec_f32[2][6] = {}, prefill_f32[2][6] = {}; // the f32 kernels: [int8 cache][kF32Sizes index]
     hipFunction_t prefill256r = nullptr; // head size 256 (f16 cache), 16 rows per wave: one workgroup per query tile
     hipFunction_t prefill256r_fmt[2] = {}; // the same over the int8 and the 4-bit cache
+    // pre-widened staging: gi_kv_widen, then the int8 kernels that stage the widened tiles by LDS-DMA (head sizes
+    // 128, 64, 256; the widened 4-bit cache runs prefill256r)
+    hipFunction_t widen = nullptr, prefill_i8s[3] = {};
     hipFunction_t combine = nullptr, rope = nullptr, relayout = nullptr, hadamard = nullptr;
     int prefill_threads[2] = {}; // each prefill kernel's block size (its launch bound: waves x 64)
     int prefill256r_threads = 0;
@@ -246,6 +272,10 @@ int load_module(const char* path, Module** out) {
             {&m.prefill256r, "gi_prefill_fwd_h256r"},
             {&m.prefill256r_fmt[0], "gi_prefill_fwd_h256r_i8"},
             {&m.prefill256r_fmt[1], "gi_prefill_fwd_h256r_q4"},
+            {&m.widen, "gi_kv_widen"},
+            {&m.prefill_i8s[0], "gi_prefill_fwd_i8s"},
+            {&m.prefill_i8s[1], "gi_prefill_fwd_h64_i8s"},
+            {&m.prefill_i8s[2], "gi_prefill_fwd_h256r_i8s"},
             {&m.rope, "gi_qk_norm_rope"},
         };
         for (auto& f : fns)
@@ -292,9 +322,10 @@ int load_module(const char* path, Module** out) {
 }
 
 // ---- per-kernel timing (gi_kernel_timing): event pairs around each launch, per kernel kind
-enum Kind { kDecodePartial = 0, kDecodeCombine = 1, kPrefill = 2, kRope = 3, kRelayout = 4, kHadamard = 5, kKinds = 6 };
+enum Kind { kDecodePartial = 0, kDecodeCombine = 1, kPrefill = 2, kRope = 3, kRelayout = 4, kHadamard = 5, kWiden = 6,
+            kKinds = 7 };
 const char* const kKindNames[kKinds] = {"decode_partial", "decode_combine", "prefill", "qk_norm_rope", "kv_relayout",
-                                        "hadamard_rows"};
+                                        "hadamard_rows", "kv_widen"};
 struct Timing {
     std::mutex mu;
     bool on = false;
@@ -613,12 +644,22 @@ int rope_impl(void* stream, float* qkv, const float* qn, const float* kn, void* 
     return launch(kRope, m->rope, dim3(groups, n, 1), dim3(256), (hipStream_t)stream, &a, sizeof a);
 }
 
+size_t align256(size_t x) { return (x + 255) / 256 * 256; }
+// Workspace of the pre-widened prefill over kv_len keys: f16 K and V rows [n_kv][kv_len][hd], and for the int8
+// cache f32 K and V scales [n_kv][kv_len], each region 256-byte aligned.
+size_t prefill_ws_bytes(int kv_len, int n_kv, int hd, int fmt) {
+    const size_t rows = align256((size_t)n_kv * kv_len * hd * 2), scales = fmt == 1 ? align256((size_t)n_kv * kv_len * 4) : 0;
+    return 2 * rows + 2 * scales;
+}
+
 // gi_attn_prefill, gi_attn_prefill_i8 and gi_attn_prefill_q4: the same launch with the f16, int8 or 4-bit kernel
-// (fmt 0, 1, 2).
+// (fmt 0, 1, 2). With a workspace (int8 and 4-bit caches, head sizes 64, 128, 256) the keys 0..pos0+n-1 are first
+// widened into it (gi_kv_widen) and the prefill stages the widened tiles by LDS-DMA, as it stages the f16 cache.
 int prefill_impl(void* stream, const void* q, int q_dtype, long long q_stride, const void* kc, const void* vc,
                  const float* ks, const float* vs, long long sc_stride, long long sc_head_stride, int fmt,
                  long long kv_stride, long long kv_head_stride, void* out, int out_dtype, long long out_stride, int pos0,
-                 int n, int n_heads, int n_kv, int hd, float scale) {
+                 int n, int n_heads, int n_kv, int hd, float scale, void* workspace = nullptr,
+                 size_t workspace_bytes = 0) {
     const bool i8 = fmt == 1;
     if (int e = check_shape(n_heads, n_kv, hd, true)) return e;
     if (fmt == 2 && hd != 256) return fail("the 4-bit cache takes head size 256 only (got %d)", hd);
@@ -671,6 +712,51 @@ int prefill_impl(void* stream, const void* q, int q_dtype, long long q_stride, c
     a.q_f16 = q_dtype == GI_F16;
     a.out_f16 = out_dtype == GI_F16;
     a.hd = hd;
+    if (fmt && workspace && !f32_hd(hd)) {
+        const int len = pos0 + n;
+        const size_t need = prefill_ws_bytes(len, n_kv, hd, fmt);
+        if (workspace_bytes < need)
+            return fail("the prefill workspace holds %zu bytes; %zu needed (gi_attn_prefill_workspace_bytes)",
+                        workspace_bytes, need);
+        if ((uintptr_t)workspace & 255) return fail("the prefill workspace must be 256-byte aligned");
+        unsigned char* w = (unsigned char*)workspace;
+        const size_t rows = align256((size_t)n_kv * len * hd * 2), scales = fmt == 1 ? align256((size_t)n_kv * len * 4) : 0;
+        GiWidenArgs wa{};
+        wa.kc = kc;
+        wa.vc = vc;
+        wa.ks = ks;
+        wa.vs = vs;
+        wa.kw = w;
+        wa.vw = w + rows;
+        wa.ksw = fmt == 1 ? (float*)(w + 2 * rows) : nullptr;
+        wa.vsw = fmt == 1 ? (float*)(w + 2 * rows + scales) : nullptr;
+        wa.kv_stride = kv_stride;
+        wa.kv_head_stride = kv_head_stride;
+        wa.sc_stride = sc_stride;
+        wa.sc_head_stride = sc_head_stride;
+        wa.n_rows = len;
+        wa.n_kv = n_kv;
+        wa.hd = hd;
+        wa.fmt = fmt;
+        wa.vbias = hd == 256 ? 1.f : kPrefillI8VBias;
+        const long long units = (long long)n_kv * len * (hd / 8);
+        const unsigned blocks = (unsigned)std::min<long long>((units + 255) / 256, 8192);
+        if (int e = launch(kWiden, m->widen, dim3(blocks), dim3(256), (hipStream_t)stream, &wa, sizeof wa)) return e;
+        a.kc = (const uint16_t*)wa.kw;
+        a.vc = (const uint16_t*)wa.vw;
+        a.kv_stride = hd;
+        a.kv_head_stride = (long long)len * hd;
+        a.ks = wa.ksw;
+        a.vs = wa.vsw;
+        a.sc_stride = 1;
+        a.sc_head_stride = len;
+        if (hd == 256)
+            return launch(kPrefill, fmt == 2 ? m->prefill256r : m->prefill_i8s[2],
+                          dim3((n + kPrefill256rRows - 1) / kPrefill256rRows * n_heads, 1, 1), dim3(m->prefill256r_threads),
+                          (hipStream_t)stream, &a, sizeof a);
+        return launch(kPrefill, m->prefill_i8s[hd == 64 ? 1 : 0], dim3((n + kPrefillRows - 1) / kPrefillRows * n_heads, 1, 1),
+                      dim3(m->prefill_threads[1]), (hipStream_t)stream, &a, sizeof a);
+    }
     if (f32_hd(hd)) // one workgroup per (head, 128 query rows)
         return launch(kPrefill, m->prefill_f32[i8][f32_index(hd)], dim3((n + kF32Rows - 1) / kF32Rows * n_heads, 1, 1),
                       dim3(kF32Threads), (hipStream_t)stream, &a, sizeof a);
@@ -798,6 +884,37 @@ int gi_attn_prefill_q4(void* stream, const void* q, int q_dtype, long long q_str
                         256, scale);
 }
 
+size_t gi_attn_prefill_workspace_bytes(int kv_len, int n_kv, int hd, int fmt) {
+    if (kv_len <= 0 || n_kv <= 0 || (fmt != 1 && fmt != 2) || (hd != 64 && hd != 128 && hd != 256) ||
+        (fmt == 2 && hd != 256))
+        return 0;
+    return prefill_ws_bytes(kv_len, n_kv, hd, fmt);
+}
+
+int gi_attn_prefill_i8_ws(void* stream, const void* q, int q_dtype, long long q_stride, const int8_t* kc,
+                          const int8_t* vc, const float* ks, const float* vs, long long kv_stride,
+                          long long kv_head_stride, long long sc_stride, long long sc_head_stride, void* out,
+                          int out_dtype, long long out_stride, int pos0, int n, int n_heads, int n_kv, int hd,
+                          float scale, void* workspace, size_t workspace_bytes) {
+    if (!workspace) return fail("null workspace");
+    if (sc_stride == 0 && sc_head_stride == 0) sc_stride = n_kv, sc_head_stride = 1;
+    return prefill_impl(stream, q, q_dtype, q_stride, kc, vc, ks, vs, sc_stride, sc_head_stride, 1, kv_stride,
+                        kv_head_stride, out, out_dtype, out_stride, pos0, n, n_heads, n_kv, hd, scale, workspace,
+                        workspace_bytes);
+}
+
+int gi_attn_prefill_q4_ws(void* stream, const void* q, int q_dtype, long long q_stride, const uint8_t* kc,
+                          const uint8_t* vc, const uint16_t* ks, const uint16_t* vs, long long kv_stride,
+                          long long kv_head_stride, long long sc_stride, long long sc_head_stride, void* out,
+                          int out_dtype, long long out_stride, int pos0, int n, int n_heads, int n_kv, float scale,
+                          void* workspace, size_t workspace_bytes) {
+    if (!workspace) return fail("null workspace");
+    if (sc_stride == 0 && sc_head_stride == 0) sc_stride = 8LL * n_kv, sc_head_stride = 8;
+    return prefill_impl(stream, q, q_dtype, q_stride, kc, vc, (const float*)ks, (const float*)vs, sc_stride,
+                        sc_head_stride, 2, kv_stride, kv_head_stride, out, out_dtype, out_stride, pos0, n, n_heads, n_kv,
+                        256, scale, workspace, workspace_bytes);
+}
+
 int gi_attention(void* stream, const float* qkv, const uint16_t* kc, const uint16_t* vc, float* out,
                  void* workspace, size_t workspace_bytes, int pos0, const int* posp, int ctx_cap, int n, int n_heads,
                  int n_kv, int hd, int exact) {
@@ -850,8 +967,10 @@ int attention_impl(void* stream, const float* qkv, const void* kc, const void* v
     const long long scs = fmt == 2 ? (long long)n_kv * (hd / 32) : n_kv, sch = fmt == 2 ? hd / 32 : 1;
     if (n >= kTiledMinBatch && !exact) {
         if (posp) return fail("a device position (posp) is only taken by the split path");
+        // the int8 and 4-bit caches: pre-widened staging when the workspace holds it
+        const bool staged = fmt && workspace && workspace_bytes >= prefill_ws_bytes(pos0 + n, n_kv, hd, fmt);
         return prefill_impl(stream, qkv, GI_F32, row, kc, vc, ks, vs, scs, sch, fmt, kvs, kvh, out, GI_F32, q_dim, pos0,
-                            n, n_heads, n_kv, hd, scale);
+                            n, n_heads, n_kv, hd, scale, staged ? workspace : nullptr, workspace_bytes);
     }
     for (int b0 = 0; b0 < n; b0 += kSplitMaxBatch) {
         int m = std::min(n - b0, kSplitMaxBatch);
@@ -879,8 +998,9 @@ int gi_kernel_timing_read(const char* kernel, double* total_ms, int* launches) {
     int kind = -1;
     for (int k = 0; k < kKinds; k++)
         if (std::strcmp(kernel, kKindNames[k]) == 0) kind = k;
-    if (kind < 0) return fail("unknown kernel \"%s\" (decode_partial, decode_combine, prefill, qk_norm_rope, kv_relayout or hadamard_rows)",
-                             kernel);
+    if (kind < 0)
+        return fail("unknown kernel \"%s\" (decode_partial, decode_combine, prefill, qk_norm_rope, kv_relayout, "
+                    "hadamard_rows or kv_widen)", kernel);
     std::vector<std::pair<hipEvent_t, hipEvent_t>> ev;
     {
         std::lock_guard<std::mutex> lock(g_timing.mu);

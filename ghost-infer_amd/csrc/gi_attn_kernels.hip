@@ -1377,13 +1377,19 @@ typedef short gi_s4 __attribute__((__vector_size__(8))); // 4 f16 as ds_read_b64
 // HD = 64 (attn_prefill_tc<64>, src/cuda.rs:2620): the same kernel with half the QK k-steps and O^T blocks. The
 // LDS image keeps the head-128 layout: each 128-byte row sits in a 256-byte slot, its 8 units at the swizzled
 // positions the operand reads compute (the staging loads of the other 8 positions are switched off by lane).
-template <bool I8, int HD = 128>
+template <bool I8, int HD = 128, bool STG = false>
 __device__ __forceinline__ void gi_prefill_t(const GiPrefillArgs& a) {
     static_assert(HD == 64 || HD == 128, "head sizes 64, 128 (256: gi_prefill256r)");
+    static_assert(!STG || I8, "pre-widened staging: the int8 cache");
+    // STG: the int8 cache already widened to exact f16 integers in a workspace (gi_kv_widen, rows [n_kv][len][hd],
+    // scales [n_kv][len], the value scales times PF_I8_VBIAS), staged by LDS-DMA as the f16 cache is; else int8
+    // tiles are widened through registers (RSTG)
+    constexpr bool RSTG = I8 && !STG;
     constexpr int WAVES = PF_WAVES;
     constexpr int BQ = 32 * WAVES;  // query rows per workgroup
     constexpr int SW = WAVES / 2;   // waves staging each of K and V
     constexpr int LPW = 16 / SW;    // 1 KB loads per staging wave and tile
+    constexpr int LPT = LPW + (STG ? 1 : 0); // loads per staging wave and tile (STG: plus a quarter of the scales)
     constexpr int BK = PF_BK;       // keys per tile
     constexpr int NBLK = BK / 32;   // S^T blocks of 32 keys
     constexpr int KS = HD / 16;     // QK k-steps
@@ -1430,6 +1436,13 @@ __device__ __forceinline__ void gi_prefill_t(const GiPrefillArgs& a) {
 #pragma unroll
         for (int i = 0; i < LPW; i++)
             if (HD == 128 || sval[i]) gi_stage16(src, bytes, (GI_LDS void*)(dst + 1024 * i), soff[i]);
+        if constexpr (STG) {
+            // this wave's quarter of the tile's 64 scales (16 floats: lanes 0-3, 16 bytes each)
+            const float* sp = (stage_v ? a.vs : a.ks) + kvh * a.sc_head_stride + t0;
+            if (lane < 4)
+                gi_stage16(sp, (long long)(kv_len - t0) * 4, (GI_LDS void*)&scl[t & (PF_NBUF - 1)][stage_v ? 1 : 0][16 * (wave % SW)],
+                           64 * (wave % SW) + 16 * lane);
+        }
     };
     // int8 staging: thread -> tile row sr, 16-byte chunk sch (dims 16sch..16sch+15) of K and of V; threads
     // 0-63 also take the K scale of key tid, 64-127 the V scale of key tid-64 (times PF_I8_VBIAS)
@@ -1582,7 +1595,7 @@ __device__ __forceinline__ void gi_prefill_t(const GiPrefillArgs& a) {
 
     // Prologue: tiles 0-2 start loading; tile 0 is waited for and published, and its QK issued. (int8:
     // tiles 0 and 1 are loaded and written, tile 2's loads stay in flight into registers.)
-    if constexpr (I8) {
+    if constexpr (RSTG) {
         load8(0);
         write8(0);
         if (ntiles > 1) {
@@ -1595,8 +1608,8 @@ __device__ __forceinline__ void gi_prefill_t(const GiPrefillArgs& a) {
         stage(0);
         if (ntiles > 1) stage(1);
         if (ntiles > 2) stage(2);
-        if (ntiles > 2) __builtin_amdgcn_s_waitcnt(GI_VMCNT(2 * LPW)); // tile 0 is in
-        else if (ntiles > 1) __builtin_amdgcn_s_waitcnt(GI_VMCNT(LPW));
+        if (ntiles > 2) __builtin_amdgcn_s_waitcnt(GI_VMCNT(2 * LPT)); // tile 0 is in
+        else if (ntiles > 1) __builtin_amdgcn_s_waitcnt(GI_VMCNT(LPT));
         else __builtin_amdgcn_s_waitcnt(GI_VMCNT(0));
     }
     asm volatile("s_barrier" ::: "memory");
@@ -1689,14 +1702,14 @@ __device__ __forceinline__ void gi_prefill_t(const GiPrefillArgs& a) {
     // has passed tile it-2) right after the barrier, and tile it+3's loads go out; a wave's LDS writes are
     // complete before the next barrier publishes them.
     auto iteration = [&](int it, f16x* s, f16x* sn) {
-        if constexpr (I8) {
+        if constexpr (RSTG) {
             __builtin_amdgcn_s_waitcnt(0xC07F); // lgkmcnt(0)
         } else {
-            if (it + 2 < ntiles) __builtin_amdgcn_s_waitcnt(GI_VMCNT(LPW)); // tile it+2's loads may stay in flight
+            if (it + 2 < ntiles) __builtin_amdgcn_s_waitcnt(GI_VMCNT(LPT)); // tile it+2's loads may stay in flight
             else __builtin_amdgcn_s_waitcnt(GI_VMCNT(0));
         }
         asm volatile("s_barrier" ::: "memory");
-        if constexpr (I8) {
+        if constexpr (RSTG) {
             if (it + 2 < ntiles) {
                 write8(it + 2);
                 if (it + 3 < ntiles) load8(it + 3);
@@ -1788,13 +1801,17 @@ __device__ __forceinline__ int pf256r_swz_v(int r) { return ((r & 3) << 2) | (((
 // ahead of the barrier that publishes it. int8 also stages each tile's key and value scales: a score is the dot
 // product with the integer key times the key's scale, P V takes f16(p * vscale * 2^10), the row sum the f16 p,
 // and the output is divided by 2^10.
-template <int NKBUF, int NVBUF, int FMT = 0>
+template <int NKBUF, int NVBUF, int FMT = 0, bool STG = false>
 __device__ __forceinline__ void gi_prefill256r(const GiPrefillArgs& a) {
     static_assert(NKBUF >= 2 && NVBUF >= 2 && NKBUF + NVBUF <= 5, "K and V rings within 160 KB");
-    constexpr bool REG = FMT != 0; // staging through registers
+    static_assert(!STG || FMT == 1, "pre-widened staging: the int8 cache (the 4-bit one widens to the f16 kernel's input)");
+    // STG: the int8 cache already widened to exact f16 integers in a workspace (gi_kv_widen: rows [n_kv][len][256],
+    // raw scales [n_kv][len]), staged by LDS-DMA as the f16 cache is
+    constexpr bool REG = FMT != 0 && !STG; // staging through registers
     constexpr int HD = 256, WAVES = PF256R_WAVES, BQ = PF256R_BQ, BK = 64;
     constexpr int SW = WAVES / 2;            // waves staging each of K and V
     constexpr int LPW = (BK / 2) / SW;       // 1 KB loads per staging wave and tile (K or V: BK * 512 bytes)
+    constexpr int LPT = LPW + (STG ? 1 : 0); // loads per staging wave and tile (STG: plus a quarter of the scales)
     constexpr int KS = HD / 32;              // QK k-steps
     constexpr int NKB = BK / 16;             // S^T blocks of 16 keys
     constexpr int NDB = HD / 16;             // O^T blocks of 16 dims
@@ -1809,8 +1826,8 @@ __device__ __forceinline__ void gi_prefill256r(const GiPrefillArgs& a) {
     // wait until at most n (0..2) of this wave's tile loads are outstanding
     auto wait_tiles = [&](int n) {
         if constexpr (REG) return; // (register staging: the compiler waits for the loads it issued)
-        if (n >= 2) __builtin_amdgcn_s_waitcnt(GI_VMCNT(2 * LPW));
-        else if (n == 1) __builtin_amdgcn_s_waitcnt(GI_VMCNT(LPW));
+        if (n >= 2) __builtin_amdgcn_s_waitcnt(GI_VMCNT(2 * LPT));
+        else if (n == 1) __builtin_amdgcn_s_waitcnt(GI_VMCNT(LPT));
         else __builtin_amdgcn_s_waitcnt(GI_VMCNT(0));
     };
     static_assert(NKBUF <= 4 && NVBUF <= 4, "wait_tiles covers two tiles in flight past the one waited for");
@@ -1854,6 +1871,14 @@ __device__ __forceinline__ void gi_prefill256r(const GiPrefillArgs& a) {
         unsigned char* dst = (stage_v ? vbuf(t) : kbuf(t)) + 1024 * LPW * (wave % SW);
 #pragma unroll
         for (int i = 0; i < LPW; i++) gi_stage16(src, bytes, (GI_LDS void*)(dst + 1024 * i), soff[i]);
+        if constexpr (STG) {
+            // this wave's quarter of the tile's 64 scales (16 floats: lanes 0-3, 16 bytes each)
+            static_assert(SW * 16 == BK, "a quarter of the scales per staging wave");
+            const float* sp = (stage_v ? a.vs : a.ks) + kvh * a.sc_head_stride + t0;
+            if (lane < 4)
+                gi_stage16(sp, (long long)(kv_len - t0) * 4, (GI_LDS void*)((stage_v ? vscl(t) : kscl(t)) + 16 * (wave % SW)),
+                           64 * (wave % SW) + 16 * lane);
+        }
     };
     // ---- register staging (FMT 1, 2): staging lane l takes a quarter (l/16) of key 16(wave % SW) + l%16's row,
     // values 64 quarter .. +63, i.e. image row key + 64(quarter/2), units 8(quarter%2) .. +7 (swizzled as above):
@@ -2175,6 +2200,9 @@ extern "C" __global__ void __launch_bounds__(64 * PF_WAVES, 1) gi_prefill_fwd(Gi
 extern "C" __global__ void __launch_bounds__(64 * PF_WAVES, 1) gi_prefill_fwd_i8(GiPrefillArgs a) { gi_prefill_t<true>(a); }
 extern "C" __global__ void __launch_bounds__(64 * PF_WAVES, 1) gi_prefill_fwd_h64(GiPrefillArgs a) { gi_prefill_t<false, 64>(a); }
 extern "C" __global__ void __launch_bounds__(64 * PF_WAVES, 1) gi_prefill_fwd_h64_i8(GiPrefillArgs a) { gi_prefill_t<true, 64>(a); }
+// the int8 cache pre-widened by gi_kv_widen, staged as the f16 cache is
+extern "C" __global__ void __launch_bounds__(64 * PF_WAVES, 1) gi_prefill_fwd_i8s(GiPrefillArgs a) { gi_prefill_t<true, 128, true>(a); }
+extern "C" __global__ void __launch_bounds__(64 * PF_WAVES, 1) gi_prefill_fwd_h64_i8s(GiPrefillArgs a) { gi_prefill_t<true, 64, true>(a); }
 #ifndef PF256R_KBUF
 #define PF256R_KBUF 2 // K tile buffers of gi_prefill_fwd_h256r
 #endif
@@ -2189,6 +2217,10 @@ extern "C" __global__ void __launch_bounds__(64 * PF256R_WAVES, 1) gi_prefill_fw
 }
 extern "C" __global__ void __launch_bounds__(64 * PF256R_WAVES, 1) gi_prefill_fwd_h256r_q4(GiPrefillArgs a) {
     gi_prefill256r<PF256R_KBUF, PF256R_VBUF, 2>(a);
+}
+// the int8 cache pre-widened by gi_kv_widen (the 4-bit cache pre-widened runs gi_prefill_fwd_h256r itself)
+extern "C" __global__ void __launch_bounds__(64 * PF256R_WAVES, 1) gi_prefill_fwd_h256r_i8s(GiPrefillArgs a) {
+    gi_prefill256r<PF256R_KBUF, PF256R_VBUF, 1, true>(a);
 }
 
 // ------------------------------------------------------------------------------------------------ KV store
@@ -2440,6 +2472,71 @@ extern "C" __global__ void __launch_bounds__(256) gi_kv_relayout(GiRelayoutArgs 
         unsigned char* dp = a.dst + t * a.dst_stride + h * a.dst_head_stride + (long long)u * a.unit;
         if (a.unit == 16) *reinterpret_cast<u4*>(dp) = *reinterpret_cast<const u4*>(sp);
         else *reinterpret_cast<uint32_t*>(dp) = *reinterpret_cast<const uint32_t*>(sp);
+    }
+}
+
+// ------------------------------------------------------------------------------------- pre-widened prefill staging
+
+// Arguments of gi_kv_widen (must match gi_attn_host.cpp).
+struct GiWidenArgs {
+    const unsigned char* kc;   // int8 rows (fmt 1) or 4-bit rows of hd / 2 bytes (fmt 2)
+    const unsigned char* vc;
+    const void* ks;            // fmt 1: f32 scale per (position, kv head); fmt 2: hd / 32 f16 scales a row
+    const void* vs;
+    uint16_t* kw;              // f16 rows [n_kv][n_rows][hd]
+    uint16_t* vw;
+    float* ksw;                // fmt 1: f32 scales [n_kv][n_rows] (values times vbias)
+    float* vsw;
+    long long kv_stride;       // bytes between positions
+    long long kv_head_stride;  // bytes between kv heads
+    long long sc_stride;       // scale elements between positions
+    long long sc_head_stride;  // scale elements between kv heads
+    int n_rows;
+    int n_kv;
+    int hd;
+    int fmt;
+    float vbias;
+    int pad_;
+};
+// The compressed cache widened once per prefill launch into a workspace that the prefill kernels stage by LDS-DMA,
+// as they stage the f16 cache (the widening inside the prefill costs its LDS writes from registers). int8: the
+// exact f16 integers and the row scales (the prefill applies them as over the int8 cache); 4-bit: f16((n - 8) *
+// scale), the values attention_prefill_tc256 with KV4 feeds its tensor cores (src/cuda.rs:2495-2514). Thread -> one
+// 16-byte unit (8 values) of a K and a V row, consecutive threads along a head's rows.
+extern "C" __global__ void __launch_bounds__(256) gi_kv_widen(GiWidenArgs a) {
+    const int upr = a.hd / 8; // units per row
+    const long long n_units = (long long)a.n_kv * a.n_rows * upr;
+    for (long long i = blockIdx.x * 256ll + threadIdx.x; i < n_units; i += (long long)gridDim.x * 256) {
+        const int u = (int)(i % upr);
+        const long long r = i / upr;
+        const int t = (int)(r % a.n_rows), h = (int)(r / a.n_rows);
+        const long long src = t * a.kv_stride + h * a.kv_head_stride;
+        const long long se = t * a.sc_stride + h * a.sc_head_stride;
+        u4 kw, vw;
+        if (a.fmt == 1) {
+            const u2 k8 = *reinterpret_cast<const u2*>(a.kc + src + 8 * u);
+            const u2 v8 = *reinterpret_cast<const u2*>(a.vc + src + 8 * u);
+            const uint32_t k0 = gi_i8_in(k8.x), k1 = gi_i8_in(k8.y), v0 = gi_i8_in(v8.x), v1 = gi_i8_in(v8.y);
+            kw = u4{i8_f16x2(k0, GI_I8_LO), i8_f16x2(k0, GI_I8_HI), i8_f16x2(k1, GI_I8_LO), i8_f16x2(k1, GI_I8_HI)};
+            vw = u4{i8_f16x2(v0, GI_I8_LO), i8_f16x2(v0, GI_I8_HI), i8_f16x2(v1, GI_I8_LO), i8_f16x2(v1, GI_I8_HI)};
+            if (u == 0) {
+                a.ksw[r] = reinterpret_cast<const float*>(a.ks)[se];
+                a.vsw[r] = reinterpret_cast<const float*>(a.vs)[se] * a.vbias;
+            }
+        } else {
+            // values 8u .. 8u + 7: bytes 4u .. 4u + 3 (value 2i in byte i's low nibble), scale group u / 4
+            const uint32_t k4 = *reinterpret_cast<const uint32_t*>(a.kc + src + 4 * u);
+            const uint32_t v4 = *reinterpret_cast<const uint32_t*>(a.vc + src + 4 * u);
+            const uint16_t kb = reinterpret_cast<const uint16_t*>(a.ks)[se + u / 4];
+            const uint16_t vb = reinterpret_cast<const uint16_t*>(a.vs)[se + u / 4];
+            const h2x ksc = __builtin_bit_cast(h2x, (uint32_t)kb * 0x10001u), vsc = __builtin_bit_cast(h2x, (uint32_t)vb * 0x10001u);
+            kw = u4{q4_f16x2(k4 >> 4, k4, 0, ksc), q4_f16x2(k4 >> 4, k4, 1, ksc), q4_f16x2(k4 >> 4, k4, 2, ksc),
+                    q4_f16x2(k4 >> 4, k4, 3, ksc)};
+            vw = u4{q4_f16x2(v4 >> 4, v4, 0, vsc), q4_f16x2(v4 >> 4, v4, 1, vsc), q4_f16x2(v4 >> 4, v4, 2, vsc),
+                    q4_f16x2(v4 >> 4, v4, 3, vsc)};
+        }
+        *reinterpret_cast<u4*>(a.kw + r * a.hd + 8 * u) = kw;
+        *reinterpret_cast<u4*>(a.vw + r * a.hd + 8 * u) = vw;
     }
 }
 

@@ -40,6 +40,9 @@ SYMBOLS = (
     "gi_attention",
     "gi_attention_i8",
     "gi_attn_prefill_q4",
+    "gi_attn_prefill_workspace_bytes",
+    "gi_attn_prefill_i8_ws",
+    "gi_attn_prefill_q4_ws",
     "gi_attention_q4",
     "gi_hadamard_rows",
     "gi_qk_norm_rope",
@@ -98,6 +101,14 @@ def load_library(path=LIB_PATH):
     lib.gi_attn_prefill_q4.restype = i
     lib.gi_attention_q4.argtypes = [vp, vp, vp, vp, vp, vp, vp, vp, sz, i, vp, i, i, i, i, i]
     lib.gi_attention_q4.restype = i
+    lib.gi_attn_prefill_workspace_bytes.argtypes = [i, i, i, i]
+    lib.gi_attn_prefill_workspace_bytes.restype = sz
+    lib.gi_attn_prefill_i8_ws.argtypes = [vp, vp, i, ll, vp, vp, vp, vp, ll, ll, ll, ll, vp, i, ll, i, i, i, i, i, f,
+                                          vp, sz]
+    lib.gi_attn_prefill_i8_ws.restype = i
+    lib.gi_attn_prefill_q4_ws.argtypes = [vp, vp, i, ll, vp, vp, vp, vp, ll, ll, ll, ll, vp, i, ll, i, i, i, i, f, vp,
+                                          sz]
+    lib.gi_attn_prefill_q4_ws.restype = i
     lib.gi_hadamard_rows.argtypes = [vp, vp, ll, i, i]
     lib.gi_hadamard_rows.restype = i
     lib.gi_qk_norm_rope.argtypes = [vp, vp, vp, vp, vp, vp, ll, ll, i, vp, i, i, i, i, i, i, f, vp, i, f]
@@ -304,10 +315,19 @@ def decode_q4(q, k_cache, v_cache, k_scale, v_scale, pos0, n_heads, n_kv, scale=
     return out
 
 
+def prefill_workspace(kv_len, n_kv, hd, fmt, device):
+    """A workspace for the pre-widened prefill over kv_len keys (fmt 1 int8, 2 the 4-bit cache), or None where that
+    path does not apply (gi_attn_prefill_workspace_bytes is 0)."""
+    nbytes = load_library().gi_attn_prefill_workspace_bytes(kv_len, n_kv, hd, fmt)
+    return torch.empty(nbytes, dtype=torch.uint8, device=device) if nbytes else None
+
+
 def prefill_q4(q, k_cache, v_cache, k_scale, v_scale, pos0, n_heads, n_kv, scale=None, out=None, out_dtype=None,
-               kv_layout="reference"):
+               kv_layout="reference", staged=True, workspace=None):
     """Causal prefill over the 4-bit cache (head size 256; attention_prefill_tc256 with KV4, src/cuda.rs:2495-2514):
-    q the rotated queries, f32 or f16 [n, >= n_heads*256]; returns rotated rows of out_dtype (default q's)."""
+    q the rotated queries, f32 or f16 [n, >= n_heads*256]; returns rotated rows of out_dtype (default q's).
+    staged: widen the keys into a workspace first (allocated here unless given) and stage the widened tiles as the
+    f16 cache's are (the same outputs); else the kernel widens each tile as it stages it."""
     if q.dtype not in (torch.float32, torch.float16):
         raise GiAttnError("q must be float32 or float16")
     _need(q, "q", q.dtype)
@@ -325,10 +345,19 @@ def prefill_q4(q, k_cache, v_cache, k_scale, v_scale, pos0, n_heads, n_kv, scale
     _need(out, "out", out.dtype)
     qd = GI_F16 if q.dtype == torch.float16 else GI_F32
     od = GI_F16 if out.dtype == torch.float16 else GI_F32
-    _check(load_library().gi_attn_prefill_q4(_stream(), _ptr(q), qd, q.stride(0), _ptr(k_cache), _ptr(v_cache),
-                                             _ptr(k_scale), _ptr(v_scale), kv_stride, kv_head_stride, sc_stride,
-                                             sc_head_stride, _ptr(out), od, out.stride(0), pos0, n, n_heads, n_kv,
-                                             scale))
+    lib = load_library()
+    if staged and workspace is None:
+        workspace = prefill_workspace(pos0 + n, n_kv, 256, 2, q.device)
+    if staged:
+        _need(workspace, "workspace", torch.uint8)
+        _check(lib.gi_attn_prefill_q4_ws(_stream(), _ptr(q), qd, q.stride(0), _ptr(k_cache), _ptr(v_cache),
+                                         _ptr(k_scale), _ptr(v_scale), kv_stride, kv_head_stride, sc_stride,
+                                         sc_head_stride, _ptr(out), od, out.stride(0), pos0, n, n_heads, n_kv, scale,
+                                         _ptr(workspace), workspace.numel()))
+        return out
+    _check(lib.gi_attn_prefill_q4(_stream(), _ptr(q), qd, q.stride(0), _ptr(k_cache), _ptr(v_cache),
+                                  _ptr(k_scale), _ptr(v_scale), kv_stride, kv_head_stride, sc_stride,
+                                  sc_head_stride, _ptr(out), od, out.stride(0), pos0, n, n_heads, n_kv, scale))
     return out
 
 
@@ -356,6 +385,11 @@ def attention_q4(qkv, k_cache, v_cache, k_scale, v_scale, pos0, n_heads, n_kv, e
             cap = ctx_cap if posp is not None else pos0 + n
             workspace = new_workspace(cap, min(n, SPLIT_MAX_BATCH), n_heads, n_kv, 256, qkv.device)
         ws_ptr, ws_bytes = _ptr(workspace), workspace.numel() * workspace.element_size()
+    else:
+        # a prefill batch: the pre-widened staging, whose workspace the library checks
+        if workspace is None:
+            workspace = prefill_workspace(pos0 + n, n_kv, 256, 2, qkv.device)
+        ws_ptr, ws_bytes = _ptr(workspace), workspace.numel() * workspace.element_size()
     _check(load_library().gi_attention_q4(_stream(), _ptr(qkv), _ptr(k_cache), _ptr(v_cache), _ptr(k_scale),
                                           _ptr(v_scale), _ptr(out), ws_ptr, ws_bytes, pos0, _ptr(posp), ctx_cap, n,
                                           n_heads, n_kv, 1 if exact else 0))
@@ -373,11 +407,13 @@ def hadamard_rows(x):
 
 
 def prefill(q, k_cache, v_cache, pos0, n_heads, n_kv, hd=128, scale=None, out=None, out_dtype=None,
-            kv_layout="reference", k_scale=None, v_scale=None):
+            kv_layout="reference", k_scale=None, v_scale=None, staged=True, workspace=None):
     """Causal prefill of n = q.shape[0] tokens at positions pos0..pos0+n-1 (their K/V already cached).
 
     q: f32 or f16 [n, >= n_heads*hd]; caches f16, or int8 with f32 k_scale / v_scale; returns
-    [n, n_heads*hd] of out_dtype (default: q's dtype).
+    [n, n_heads*hd] of out_dtype (default: q's dtype). int8 at head sizes 64, 128, 256 with staged: the keys are
+    widened into a workspace first (allocated here unless given) and the widened tiles staged as the f16 cache's
+    are (the same outputs); else the kernel widens each tile as it stages it.
     """
     if q.dtype not in (torch.float32, torch.float16):
         raise GiAttnError("q must be float32 or float16")
@@ -400,7 +436,15 @@ def prefill(q, k_cache, v_cache, pos0, n_heads, n_kv, hd=128, scale=None, out=No
     lib = load_library()
     qd = GI_F16 if q.dtype == torch.float16 else GI_F32
     od = GI_F16 if out.dtype == torch.float16 else GI_F32
-    if i8:
+    if i8 and staged and hd in (64, 128, 256):
+        if workspace is None:
+            workspace = prefill_workspace(pos0 + n, n_kv, hd, 1, q.device)
+        _need(workspace, "workspace", torch.uint8)
+        _check(lib.gi_attn_prefill_i8_ws(_stream(), _ptr(q), qd, q.stride(0), _ptr(k_cache), _ptr(v_cache),
+                                         _ptr(k_scale), _ptr(v_scale), kv_stride, kv_head_stride, sc[0], sc[1],
+                                         _ptr(out), od, out.stride(0), pos0, n, n_heads, n_kv, hd, scale,
+                                         _ptr(workspace), workspace.numel()))
+    elif i8:
         _check(lib.gi_attn_prefill_i8(_stream(), _ptr(q), qd, q.stride(0), _ptr(k_cache), _ptr(v_cache), _ptr(k_scale),
                                       _ptr(v_scale), kv_stride, kv_head_stride, sc[0], sc[1], _ptr(out), od,
                                       out.stride(0), pos0, n, n_heads, n_kv, hd, scale))
@@ -441,6 +485,12 @@ def attention(qkv, k_cache, v_cache, pos0, n_heads, n_kv, hd=128, exact=False, o
             cap = ctx_cap if posp is not None else pos0 + n
             workspace = new_workspace(cap, min(n, SPLIT_MAX_BATCH), n_heads, n_kv, hd, qkv.device)
         ws_ptr, ws_bytes = _ptr(workspace), workspace.numel() * workspace.element_size()
+    elif i8:
+        # a prefill batch over the int8 cache: the pre-widened staging, whose workspace the library checks
+        if workspace is None:
+            workspace = prefill_workspace(pos0 + n, n_kv, hd, 1, qkv.device)
+        if workspace is not None:
+            ws_ptr, ws_bytes = _ptr(workspace), workspace.numel() * workspace.element_size()
     lib = load_library()
     if i8:
         _check(lib.gi_attention_i8(_stream(), _ptr(qkv), _ptr(k_cache), _ptr(v_cache), _ptr(k_scale), _ptr(v_scale),
@@ -558,7 +608,7 @@ def kernel_timing(on):
 
 def kernel_timing_read(kernel):
     """(total milliseconds, launches) of kernel kind "decode_partial", "decode_combine", "prefill",
-    "qk_norm_rope" or "kv_relayout" since the previous read of that kind."""
+    "qk_norm_rope", "kv_relayout", "hadamard_rows" or "kv_widen" since the previous read of that kind."""
     ms, n = ctypes.c_double(), ctypes.c_int()
     _check(load_library().gi_kernel_timing_read(kernel.encode(), ctypes.byref(ms), ctypes.byref(n)))
     return ms.value, n.value

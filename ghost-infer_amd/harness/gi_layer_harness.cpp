@@ -129,8 +129,11 @@ int main(int argc, char** argv) {
     float* vs = o.i8 || o.q4 ? (float*)dev_alloc<char>(sc_bytes) : nullptr;
     const long long kv_stride = o.q4 ? hd / 2 : hd, kv_head_stride = (long long)cap * kv_stride;
     const long long sc_stride = o.q4 ? hd / 32 : 1, sc_head_stride = (long long)cap * sc_stride;
-    const size_t ws_bytes = gi_attn_decode_workspace_bytes(cap, 15, H, K, hd);
-    if (ws_bytes == 0) die("gi_attn_decode_workspace_bytes rejected the shape");
+    // one workspace for the decode partials and, over the int8 and 4-bit caches, the prompt's widened keys
+    const size_t part_bytes = gi_attn_decode_workspace_bytes(cap, 15, H, K, hd);
+    if (part_bytes == 0) die("gi_attn_decode_workspace_bytes rejected the shape");
+    const size_t widen_bytes = o.i8 || o.q4 ? gi_attn_prefill_workspace_bytes(cap, K, hd, o.q4 ? 2 : 1) : 0;
+    const size_t ws_bytes = part_bytes > widen_bytes ? part_bytes : widen_bytes;
     void* ws = dev_alloc<char>(ws_bytes);
     // the engine's fixed per-step buffers: the current token's qkv row and output row, and its position
     float* cur_row = dev_alloc<float>(row);
@@ -157,9 +160,14 @@ int main(int argc, char** argv) {
         const float scale = 1.f / sqrtf((float)hd);
         if (n >= 16 && !exact) {
             if (o.q4)
-                return gi_attn_prefill_q4(st, rows, GI_F32, row, (const uint8_t*)kc, (const uint8_t*)vc,
-                                          (const uint16_t*)ks, (const uint16_t*)vs, kv_stride, kv_head_stride,
-                                          sc_stride, sc_head_stride, o_rows, GI_F32, orow, pos0, n, H, K, scale);
+                return gi_attn_prefill_q4_ws(st, rows, GI_F32, row, (const uint8_t*)kc, (const uint8_t*)vc,
+                                             (const uint16_t*)ks, (const uint16_t*)vs, kv_stride, kv_head_stride,
+                                             sc_stride, sc_head_stride, o_rows, GI_F32, orow, pos0, n, H, K, scale, ws,
+                                             ws_bytes);
+            if (o.i8 && widen_bytes) // (the f32 kernels' head sizes take no widened keys)
+                return gi_attn_prefill_i8_ws(st, rows, GI_F32, row, (const int8_t*)kc, (const int8_t*)vc, ks, vs,
+                                             kv_stride, kv_head_stride, sc_stride, sc_head_stride, o_rows, GI_F32,
+                                             orow, pos0, n, H, K, hd, scale, ws, ws_bytes);
             if (o.i8)
                 return gi_attn_prefill_i8(st, rows, GI_F32, row, (const int8_t*)kc, (const int8_t*)vc, ks, vs,
                                           kv_stride, kv_head_stride, sc_stride, sc_head_stride, o_rows, GI_F32, orow,

@@ -156,6 +156,29 @@ int gi_attn_prefill_q4(void* stream, const void* q, int q_dtype, long long q_str
                        long long kv_head_stride, long long sc_stride, long long sc_head_stride, void* out, int out_dtype,
                        long long out_stride, int pos0, int n, int n_heads, int n_kv, float scale);
 
+/* Bytes of the workspace gi_attn_prefill_i8_ws / gi_attn_prefill_q4_ws take for kv_len = pos0 + n keys (fmt 1: the
+ * int8 cache, hd 64, 128 or 256; fmt 2: the 4-bit cache, hd 256); 0 for any other shape. No counterpart in the
+ * reference, whose prefill widens each tile inside the kernel: f16 K and V rows [n_kv][kv_len][hd] (and for int8
+ * f32 scales [n_kv][kv_len]), 256-byte aligned regions. */
+size_t gi_attn_prefill_workspace_bytes(int kv_len, int n_kv, int hd, int fmt);
+
+/* gi_attn_prefill_i8 / gi_attn_prefill_q4 with a caller-owned workspace (256-byte aligned, at least
+ * gi_attn_prefill_workspace_bytes(pos0 + n, ...) bytes): the keys 0..pos0+n-1 are first widened into it to the f16
+ * values the tiles take (int8: the exact integers, the scales kept apart; 4-bit: f16((n - 8) * scale)), and the
+ * prefill then stages the widened tiles as it stages the f16 cache. The same arithmetic and outputs, bit for bit, as
+ * the entry points without a workspace (replaces what they replace). gi_attention_i8 / gi_attention_q4 take this
+ * path for prefill batches whenever their workspace holds it. */
+int gi_attn_prefill_i8_ws(void* stream, const void* q, int q_dtype, long long q_stride, const int8_t* kc,
+                          const int8_t* vc, const float* ks, const float* vs, long long kv_stride,
+                          long long kv_head_stride, long long sc_stride, long long sc_head_stride, void* out,
+                          int out_dtype, long long out_stride, int pos0, int n, int n_heads, int n_kv, int hd,
+                          float scale, void* workspace, size_t workspace_bytes);
+int gi_attn_prefill_q4_ws(void* stream, const void* q, int q_dtype, long long q_stride, const uint8_t* kc,
+                          const uint8_t* vc, const uint16_t* ks, const uint16_t* vs, long long kv_stride,
+                          long long kv_head_stride, long long sc_stride, long long sc_head_stride, void* out,
+                          int out_dtype, long long out_stride, int pos0, int n, int n_heads, int n_kv, float scale,
+                          void* workspace, size_t workspace_bytes);
+
 /* The attention operator of one layer, as GpuModel::attention (src/cuda.rs:8448-8541) dispatches it:
  * qkv rows are [q (n_heads*hd) | k | v] f32 (stride n_heads*hd + 2*n_kv*hd, src/cuda.rs:1713), out rows
  * n_heads*hd f32. Batches of >= 16 tokens that are not `exact` (verify) go to prefill; the rest to the
