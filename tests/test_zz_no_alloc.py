@@ -59,6 +59,24 @@ def test_noalloc_decode_matches_the_workspace_entry_point(gpu):
         assert torch.equal(out.view(torch.int32), want.view(torch.int32)), f"noalloc posp {pos} differs"
 
 
+@pytest.mark.parametrize("hd,n_heads,n_kv", [(64, 9, 3), (256, 16, 2), (80, 32, 32), (96, 12, 4)])
+def test_noalloc_other_head_sizes(gpu, hd, n_heads, n_kv):
+    # head sizes 64 and 256 on MFMA, 80 and 96 on the f32 kernels: two calls in a row, the second smaller
+    gen = torch.Generator(device=gpu)
+    gen.manual_seed(hd)
+    for ctx, n_tok in ((5000, 3), (700, 1)):
+        say("noalloc hd", hd, ctx, n_tok)
+        k = torch.randn((n_kv, ctx, hd), generator=gen, device=gpu).half()
+        v = torch.randn((n_kv, ctx, hd), generator=gen, device=gpu).half()
+        q = torch.randn((n_tok, n_heads * hd), generator=gen, device=gpu)
+        pos0 = ctx - n_tok
+        want = gi_attn.decode(q, k, v, pos0, n_heads, n_kv, hd=hd, kv_layout="head_major")
+        out = torch.full_like(want, float("nan"))
+        assert noalloc(q, k, v, pos0, n_heads, n_kv, out, hd=hd) == 0, gi_attn.load_library().gi_last_error().decode()
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int32), want.view(torch.int32)), f"noalloc hd {hd} differs"
+
+
 def test_noalloc_config4_verify_fits(gpu):
     # config 4's verify block (8 tokens at a 32768-key prefix, 32 / 4 heads) fits the array
     gen = torch.Generator(device=gpu)
