@@ -4,7 +4,7 @@
                     decode64k_i8|verify_i8|prefill8k_i8|decode64k_h256|verify_h256|prefill8k_h256|
                     decode64k_h256_i8|verify_h256_i8|prefill8k_h256_i8|decode64k_h256_q4|verify_h256_q4|
                     prefill8k_h256_q4|decode64k_h64|decode64k_h64_i8|prefill8k_h64|prefill8k_h64_i8|decode16k_h80|prefill8k_h96|
-                    decode16k_h80_i8|prefill8k_h96_i8]
+                    decode16k_h80_i8|prefill8k_h96_i8|prefill8k_f32]
                     [--no-cpu-baseline] [--no-secondary] [--reference-layout] [--verbose]
                     [--detail-out FILE] [--full-line]
 
@@ -28,6 +28,8 @@ A step is one pass of the hot path over one batch of synthetic seeded input alre
   decode16k_h80, prefill8k_h96, decode16k_h80_i8, prefill8k_h96_i8
              the f32 kernels' head sizes (Phi-2-style 80, Phi-3-style 96; 32 query / 32 kv heads), over the f16
              and int8 caches
+  prefill8k_f32
+             config 3's prompt in f32 (the reference's attention_prefill, GHOST_INFER_NO_TC_ATT)
   decode64k_i8, verify_i8, prefill8k_i8
              configs 2, 4 and 3 over the int8 cache (the reference's KV8 format: int8 rows, an f32 scale per
              position and kv head); bytes are the int8 rows plus their scales
@@ -258,7 +260,7 @@ def prefill_flops(n, pos0, n_heads, hd=HD):
     return 4 * n_heads * hd * keys
 
 
-def prefill_workload(torch, gi_attn, dev, n, n_heads, n_kv, steps, warmup, seed, i8=False, hd=HD):
+def prefill_workload(torch, gi_attn, dev, n, n_heads, n_kv, steps, warmup, seed, i8=False, hd=HD, f32=False):
     gen = torch.Generator(device=dev)
     gen.manual_seed(seed)
     q = torch.randn((n, n_heads * hd), generator=gen, device=dev, dtype=torch.float32).half()
@@ -272,7 +274,7 @@ def prefill_workload(torch, gi_attn, dev, n, n_heads, n_kv, steps, warmup, seed,
         if i8 == "q4":
             gi_attn.prefill_q4(q, k, v, ks, vs, 0, n_heads, n_kv, out=out, workspace=ws)
         else:
-            gi_attn.prefill(q, k, v, 0, n_heads, n_kv, hd=hd, out=out, k_scale=ks, v_scale=vs, workspace=ws)
+            gi_attn.prefill(q, k, v, 0, n_heads, n_kv, hd=hd, out=out, k_scale=ks, v_scale=vs, workspace=ws, f32=f32)
 
     t = time_steps(step, steps, warmup, torch)
     return {"seconds": t, "flops": prefill_flops(n, 0, n_heads, hd), "step": step, "q": q, "k": k, "v": v}
@@ -584,7 +586,7 @@ def run_decode(torch, gi_attn, dev, w, steps, warmup, n_tok_override=None, refer
 
 
 PREFILL_WORKLOADS = ("prefill8k", "prefill8k_i8", "prefill8k_h256", "prefill8k_h256_i8", "prefill8k_h256_q4",
-                     "prefill8k_h64", "prefill8k_h64_i8", "prefill8k_h96", "prefill8k_h96_i8")
+                     "prefill8k_h64", "prefill8k_h64_i8", "prefill8k_h96", "prefill8k_h96_i8", "prefill8k_f32")
 
 
 def run_prefill(torch, gi_attn, dev, w, steps, warmup):
@@ -593,27 +595,31 @@ def run_prefill(torch, gi_attn, dev, w, steps, warmup):
     nh, nkv = (16, 2) if hd == 256 else (32, 32) if hd == 96 else (32, 8)
     cache = " over the 4-bit cache" if i8 == "q4" else " over the int8 cache" if i8 else ""
     log(f"[bench] causal prefill 8192 tokens, {nh}q/{nkv}kv, hd {hd}{cache}")
-    r = prefill_workload(torch, gi_attn, dev, 8192, nh, nkv, steps, warmup, 99, i8=i8, hd=hd)
+    f32 = w == "prefill8k_f32"  # config 3's prompt in f32 (the reference's GHOST_INFER_NO_TC_ATT)
+    r = prefill_workload(torch, gi_attn, dev, 8192, nh, nkv, steps, warmup, 99, i8=i8, hd=hd, f32=f32)
     tf = r["flops"] / r["seconds"] / 1e12
     # (the int8 cache: the kernels staging the pre-widened keys, *_i8s; the 4-bit cache widened runs the f16 kernel)
     kernel = ("gi_prefill_fwd_h256r" + ("_i8s" if i8 is True else "") if hd == 256
               else "gi_prefill_fwd_h64" + ("_i8s" if i8 else "") if hd == 64
               else "gi_prefill_f32" + ("_i8" if i8 else "") + f"_h{hd}" if hd not in (64, 128)
+              else "gi_prefill_f32_h128" if f32
               else "gi_prefill_fwd_i8s" if i8 else "gi_prefill_fwd")
     line = {
         "value": round(tf, 1), "unit": "TFLOP/s", "ms_per_step": r["seconds"] * 1e3,
         "dtype": ("4-bit K/V widened to f16 MFMA, f32 acc" if i8 == "q4" else
-                  "f32 MFMA (" + ("int8" if i8 else "f16") + " cache widened), f32 acc" if hd not in (64, 128, 256) else
+                  "f32 MFMA (" + ("int8" if i8 else "f16") + " cache widened), f32 acc" if hd not in (64, 128, 256) or f32
+                  else
                   "int8 K/V widened to f16 MFMA, f32 acc" if i8 else "f16 MFMA, f32 acc"),
         "config": {"workload": (f"causal prefill, 8192 tokens, {nh}q/{nkv}kv, hd 256 (Qwen3.5-style heads){cache}"
                                 if hd == 256 else
                                 f"causal prefill, 8192 tokens, 32q/8kv, hd 64 (Llama-3.2-1B-style heads){cache}"
                                 if hd == 64 else
                                 "causal prefill, 8192 tokens, 32q/32kv, hd 96 (Phi-3-style heads, the f32 kernels)" + cache
-                                if hd == 96 else "config 3: causal prefill, 8192 tokens, 32q/8kv, hd 128" +
+                                if hd == 96 else "config 3's prompt in f32 (no f16 Q or P: GHOST_INFER_NO_TC_ATT)"
+                                if f32 else "config 3: causal prefill, 8192 tokens, 32q/8kv, hd 128" +
                                 (", int8 cache" if i8 else "")), "flops_per_step": r["flops"]},
         "roofline": prefill_roofline(gi_attn, r, steps, torch, f"pmc_prefill_{w}", kernel,
-                                     FP32_DENSE_PEAK_TFLOPS if hd not in (64, 128, 256) else None),
+                                     FP32_DENSE_PEAK_TFLOPS if hd not in (64, 128, 256) or f32 else None),
     }
     return line, r
 

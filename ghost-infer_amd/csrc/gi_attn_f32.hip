@@ -330,6 +330,17 @@ __device__ __forceinline__ void gi_prefill_f32_t(const GiPrefillArgs& a) {
     extern "C" __global__ void __launch_bounds__(64 * PF32_WAVES) gi_prefill_f32_i8_h##HD(GiPrefillArgs a) {            \
         gi_prefill_f32_t<true, HD>(a);                                                                                  \
     }
+// head sizes 64 and 128: the prompt kernel only, for f32-precision prompts (the reference's attention_prefill with the
+// tensor-core prefill off, GHOST_INFER_NO_TC_ATT; its decode at these sizes is the MFMA split path, f32-precise)
+#define GI_F32_PREFILL_KERNELS(HD)                                                                                      \
+    extern "C" __global__ void __launch_bounds__(64 * PF32_WAVES) gi_prefill_f32_h##HD(GiPrefillArgs a) {               \
+        gi_prefill_f32_t<false, HD>(a);                                                                                 \
+    }                                                                                                                   \
+    extern "C" __global__ void __launch_bounds__(64 * PF32_WAVES) gi_prefill_f32_i8_h##HD(GiPrefillArgs a) {            \
+        gi_prefill_f32_t<true, HD>(a);                                                                                  \
+    }
+GI_F32_PREFILL_KERNELS(64)
+GI_F32_PREFILL_KERNELS(128)
 GI_F32_KERNELS(16)
 GI_F32_KERNELS(32)
 GI_F32_KERNELS(48)

@@ -203,6 +203,7 @@ struct Module {
     hipFunction_t prefill[2] = {};   // [int8 cache], head size 128
     hipFunction_t prefill64[2] = {}; // [int8 cache], head size 64 (the same launch shape and block size)
     hipFunction_t dec_f32[2][6] = {}, prefill_f32[2][6] = {}; // the f32 kernels: [int8 cache][kF32Sizes index]
+    hipFunction_t prefill_f32p[2][2] = {}; // f32 prompts at head sizes 64 and 128: [int8 cache][64, 128]
     hipFunction_t prefill256r = nullptr; // head size 256 (f16 cache), 16 rows per wave: one workgroup per query tile
     hipFunction_t prefill256r_fmt[2] = {}; // the same over the int8 and the 4-bit cache
     // pre-widened staging: gi_kv_widen, then the int8 kernels that stage the widened tiles by LDS-DMA (head sizes
@@ -291,6 +292,10 @@ int load_module(const char* path, Module** out) {
                 snprintf(pn, sizeof pn, "gi_prefill_f32%s_h%d", i8 ? "_i8" : "", kF32Sizes[i]);
                 int e = check(hipModuleGetFunction(&m.dec_f32[i8][i], m.mod, dn), dn);
                 if (!e) e = check(hipModuleGetFunction(&m.prefill_f32[i8][i], m.mod, pn), pn);
+                if (!e && i < 2) {
+                    snprintf(pn, sizeof pn, "gi_prefill_f32%s_h%d", i8 ? "_i8" : "", 64 << i);
+                    e = check(hipModuleGetFunction(&m.prefill_f32p[i8][i], m.mod, pn), pn);
+                }
                 if (e) {
                     (void)hipModuleUnload(m.mod);
                     m.mod = nullptr;
@@ -659,10 +664,12 @@ int prefill_impl(void* stream, const void* q, int q_dtype, long long q_stride, c
                  const float* ks, const float* vs, long long sc_stride, long long sc_head_stride, int fmt,
                  long long kv_stride, long long kv_head_stride, void* out, int out_dtype, long long out_stride, int pos0,
                  int n, int n_heads, int n_kv, int hd, float scale, void* workspace = nullptr,
-                 size_t workspace_bytes = 0) {
+                 size_t workspace_bytes = 0, bool f32_prompt = false) {
     const bool i8 = fmt == 1;
     if (int e = check_shape(n_heads, n_kv, hd, true)) return e;
     if (fmt == 2 && hd != 256) return fail("the 4-bit cache takes head size 256 only (got %d)", hd);
+    if (f32_prompt && (fmt == 2 || hd > 128))
+        return fail("f32 prompts take the f16 and int8 caches at head sizes up to 128 (the reference's attention_prefill)");
     if (n <= 0 || pos0 < 0) return fail("n %d must be positive and pos0 %d >= 0", n, pos0);
     if (!q || !kc || !vc || !out) return fail("null tensor pointer");
     if ((q_dtype != GI_F32 && q_dtype != GI_F16) || (out_dtype != GI_F32 && out_dtype != GI_F16))
@@ -712,6 +719,9 @@ int prefill_impl(void* stream, const void* q, int q_dtype, long long q_stride, c
     a.q_f16 = q_dtype == GI_F16;
     a.out_f16 = out_dtype == GI_F16;
     a.hd = hd;
+    if (f32_prompt && !f32_hd(hd)) // head sizes 64 and 128 in f32: one workgroup per (head, 128 query rows)
+        return launch(kPrefill, m->prefill_f32p[i8][hd == 128], dim3((n + kF32Rows - 1) / kF32Rows * n_heads, 1, 1),
+                      dim3(kF32Threads), (hipStream_t)stream, &a, sizeof a);
     if (fmt && workspace && !f32_hd(hd)) {
         const int len = pos0 + n;
         const size_t need = prefill_ws_bytes(len, n_kv, hd, fmt);
@@ -884,6 +894,16 @@ int gi_attn_prefill_q4(void* stream, const void* q, int q_dtype, long long q_str
                         256, scale);
 }
 
+int gi_attn_prefill_f32(void* stream, const void* q, int q_dtype, long long q_stride, const void* kc, const void* vc,
+                        const float* ks, const float* vs, int kv_int8, long long kv_stride, long long kv_head_stride,
+                        long long sc_stride, long long sc_head_stride, void* out, int out_dtype, long long out_stride,
+                        int pos0, int n, int n_heads, int n_kv, int hd, float scale) {
+    if (kv_int8 && sc_stride == 0 && sc_head_stride == 0) sc_stride = n_kv, sc_head_stride = 1;
+    return prefill_impl(stream, q, q_dtype, q_stride, kc, vc, kv_int8 ? ks : nullptr, kv_int8 ? vs : nullptr,
+                        kv_int8 ? sc_stride : 0, kv_int8 ? sc_head_stride : 0, kv_int8 ? 1 : 0, kv_stride,
+                        kv_head_stride, out, out_dtype, out_stride, pos0, n, n_heads, n_kv, hd, scale, nullptr, 0, true);
+}
+
 size_t gi_attn_prefill_workspace_bytes(int kv_len, int n_kv, int hd, int fmt) {
     if (kv_len <= 0 || n_kv <= 0 || (fmt != 1 && fmt != 2) || (hd != 64 && hd != 128 && hd != 256) ||
         (fmt == 2 && hd != 256))
@@ -965,6 +985,14 @@ int attention_impl(void* stream, const float* qkv, const void* kc, const void* v
     // [position][n_kv] (the 4-bit cache: [position][n_kv][hd / 32] f16)
     const long long kvs = fmt == 2 ? kv_dim / 2 : kv_dim, kvh = fmt == 2 ? hd / 2 : hd;
     const long long scs = fmt == 2 ? (long long)n_kv * (hd / 32) : n_kv, sch = fmt == 2 ? hd / 32 : 1;
+    // exact 2: prompts in f32 (the reference with its tensor-core prefill off, GHOST_INFER_NO_TC_ATT, launches
+    // attention_prefill for head sizes up to 128, src/cuda.rs:8452-8476); the 4-bit cache and head size 256 have no
+    // such kernel there and take the split path
+    if (n >= kTiledMinBatch && exact == 2 && fmt != 2 && hd <= 128) {
+        if (posp) return fail("a device position (posp) is only taken by the split path");
+        return prefill_impl(stream, qkv, GI_F32, row, kc, vc, ks, vs, scs, sch, fmt, kvs, kvh, out, GI_F32, q_dim, pos0,
+                            n, n_heads, n_kv, hd, scale, nullptr, 0, true);
+    }
     if (n >= kTiledMinBatch && !exact) {
         if (posp) return fail("a device position (posp) is only taken by the split path");
         // the int8 and 4-bit caches: pre-widened staging when the workspace holds it

@@ -41,6 +41,7 @@ SYMBOLS = (
     "gi_attention_i8",
     "gi_attn_prefill_q4",
     "gi_attn_prefill_workspace_bytes",
+    "gi_attn_prefill_f32",
     "gi_attn_prefill_i8_ws",
     "gi_attn_prefill_q4_ws",
     "gi_attention_q4",
@@ -101,6 +102,8 @@ def load_library(path=LIB_PATH):
     lib.gi_attn_prefill_q4.restype = i
     lib.gi_attention_q4.argtypes = [vp, vp, vp, vp, vp, vp, vp, vp, sz, i, vp, i, i, i, i, i]
     lib.gi_attention_q4.restype = i
+    lib.gi_attn_prefill_f32.argtypes = [vp, vp, i, ll, vp, vp, vp, vp, i, ll, ll, ll, ll, vp, i, ll, i, i, i, i, i, f]
+    lib.gi_attn_prefill_f32.restype = i
     lib.gi_attn_prefill_workspace_bytes.argtypes = [i, i, i, i]
     lib.gi_attn_prefill_workspace_bytes.restype = sz
     lib.gi_attn_prefill_i8_ws.argtypes = [vp, vp, i, ll, vp, vp, vp, vp, ll, ll, ll, ll, vp, i, ll, i, i, i, i, i, f,
@@ -407,13 +410,14 @@ def hadamard_rows(x):
 
 
 def prefill(q, k_cache, v_cache, pos0, n_heads, n_kv, hd=128, scale=None, out=None, out_dtype=None,
-            kv_layout="reference", k_scale=None, v_scale=None, staged=True, workspace=None):
+            kv_layout="reference", k_scale=None, v_scale=None, staged=True, workspace=None, f32=False):
     """Causal prefill of n = q.shape[0] tokens at positions pos0..pos0+n-1 (their K/V already cached).
 
     q: f32 or f16 [n, >= n_heads*hd]; caches f16, or int8 with f32 k_scale / v_scale; returns
     [n, n_heads*hd] of out_dtype (default: q's dtype). int8 at head sizes 64, 128, 256 with staged: the keys are
     widened into a workspace first (allocated here unless given) and the widened tiles staged as the f16 cache's
-    are (the same outputs); else the kernel widens each tile as it stages it.
+    are (the same outputs); else the kernel widens each tile as it stages it. f32: the prompt in f32 (no f16
+    rounding of Q or P), the reference's attention_prefill with its tensor-core prefill off (head sizes up to 128).
     """
     if q.dtype not in (torch.float32, torch.float16):
         raise GiAttnError("q must be float32 or float16")
@@ -436,7 +440,12 @@ def prefill(q, k_cache, v_cache, pos0, n_heads, n_kv, hd=128, scale=None, out=No
     lib = load_library()
     qd = GI_F16 if q.dtype == torch.float16 else GI_F32
     od = GI_F16 if out.dtype == torch.float16 else GI_F32
-    if i8 and staged and hd in (64, 128, 256):
+    if f32:
+        _check(lib.gi_attn_prefill_f32(_stream(), _ptr(q), qd, q.stride(0), _ptr(k_cache), _ptr(v_cache),
+                                       _ptr(k_scale) if i8 else None, _ptr(v_scale) if i8 else None, 1 if i8 else 0,
+                                       kv_stride, kv_head_stride, sc[0] if i8 else 0, sc[1] if i8 else 0, _ptr(out), od,
+                                       out.stride(0), pos0, n, n_heads, n_kv, hd, scale))
+    elif i8 and staged and hd in (64, 128, 256):
         if workspace is None:
             workspace = prefill_workspace(pos0 + n, n_kv, hd, 1, q.device)
         _need(workspace, "workspace", torch.uint8)
@@ -455,13 +464,14 @@ def prefill(q, k_cache, v_cache, pos0, n_heads, n_kv, hd=128, scale=None, out=No
 
 
 def attention(qkv, k_cache, v_cache, pos0, n_heads, n_kv, hd=128, exact=False, out=None, workspace=None,
-              posp=None, ctx_cap=0, k_scale=None, v_scale=None):
+              posp=None, ctx_cap=0, k_scale=None, v_scale=None, f32_prompts=False):
     """GpuModel::attention (src/cuda.rs:8448-8541) for one layer.
 
     qkv: f32 [n, n_heads*hd + 2*n_kv*hd] rows [q | k | v] (only q is read: the cache already holds this
     batch's K/V rows, as qk_norm_rope wrote them); returns f32 [n, n_heads*hd]. n >= 16 and not exact ->
     causal prefill kernel; otherwise the split decode path, 15 tokens per launch. The caches are the
     reference's [capacity, n_kv, hd]: f16, or int8 with f32 scales [capacity, n_kv] (its (kc, vc, ks, vs)).
+    f32_prompts: batches of >= 16 tokens in f32 (the reference's GHOST_INFER_NO_TC_ATT; head sizes up to 128).
     """
     _need(qkv, "qkv", torch.float32)
     n = qkv.shape[0]
@@ -480,12 +490,14 @@ def attention(qkv, k_cache, v_cache, pos0, n_heads, n_kv, hd=128, exact=False, o
     if posp is not None:
         _need(posp, "posp", torch.int32)
     ws_ptr, ws_bytes = None, 0
-    if n < TILED_MIN_BATCH or exact:
+    code = 1 if exact else 2 if f32_prompts else 0
+    split = n < TILED_MIN_BATCH or exact or (f32_prompts and hd > 128)
+    if split:
         if workspace is None:
             cap = ctx_cap if posp is not None else pos0 + n
             workspace = new_workspace(cap, min(n, SPLIT_MAX_BATCH), n_heads, n_kv, hd, qkv.device)
         ws_ptr, ws_bytes = _ptr(workspace), workspace.numel() * workspace.element_size()
-    elif i8:
+    elif i8 and not f32_prompts:
         # a prefill batch over the int8 cache: the pre-widened staging, whose workspace the library checks
         if workspace is None:
             workspace = prefill_workspace(pos0 + n, n_kv, hd, 1, qkv.device)
@@ -494,11 +506,10 @@ def attention(qkv, k_cache, v_cache, pos0, n_heads, n_kv, hd=128, exact=False, o
     lib = load_library()
     if i8:
         _check(lib.gi_attention_i8(_stream(), _ptr(qkv), _ptr(k_cache), _ptr(v_cache), _ptr(k_scale), _ptr(v_scale),
-                                   _ptr(out), ws_ptr, ws_bytes, pos0, _ptr(posp), ctx_cap, n, n_heads, n_kv, hd,
-                                   1 if exact else 0))
+                                   _ptr(out), ws_ptr, ws_bytes, pos0, _ptr(posp), ctx_cap, n, n_heads, n_kv, hd, code))
     else:
         _check(lib.gi_attention(_stream(), _ptr(qkv), _ptr(k_cache), _ptr(v_cache), _ptr(out), ws_ptr, ws_bytes, pos0,
-                                _ptr(posp), ctx_cap, n, n_heads, n_kv, hd, 1 if exact else 0))
+                                _ptr(posp), ctx_cap, n, n_heads, n_kv, hd, code))
     return out
 
 

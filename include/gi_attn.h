@@ -156,6 +156,16 @@ int gi_attn_prefill_q4(void* stream, const void* q, int q_dtype, long long q_str
                        long long kv_head_stride, long long sc_stride, long long sc_head_stride, void* out, int out_dtype,
                        long long out_stride, int pos0, int n, int n_heads, int n_kv, float scale);
 
+/* Causal prefill in f32 (no f16 rounding of Q or P; f32 MFMA operands and accumulation) over the f16 cache or, with
+ * kv_int8, the int8 cache (ks / vs and the scale strides as gi_attn_prefill_i8), head sizes 16 to 128 in steps of 16.
+ * Replaces: attention_prefill (src/cuda.rs:1934-2041), which GpuModel::attention launches for prompts when the
+ * tensor-core prefill is off (GHOST_INFER_NO_TC_ATT, src/cuda.rs:5648-5654) or the head size has none
+ * (src/cuda.rs:8452-8476). gi_attention / gi_attention_i8 take this path for prompts with exact = 2. */
+int gi_attn_prefill_f32(void* stream, const void* q, int q_dtype, long long q_stride, const void* kc, const void* vc,
+                        const float* ks, const float* vs, int kv_int8, long long kv_stride, long long kv_head_stride,
+                        long long sc_stride, long long sc_head_stride, void* out, int out_dtype, long long out_stride,
+                        int pos0, int n, int n_heads, int n_kv, int hd, float scale);
+
 /* Bytes of the workspace gi_attn_prefill_i8_ws / gi_attn_prefill_q4_ws take for kv_len = pos0 + n keys (fmt 1: the
  * int8 cache, hd 64, 128 or 256; fmt 2: the 4-bit cache, hd 256); 0 for any other shape. No counterpart in the
  * reference, whose prefill widens each tile inside the kernel: f16 K and V rows [n_kv][kv_len][hd] (and for int8
@@ -182,7 +192,9 @@ int gi_attn_prefill_q4_ws(void* stream, const void* q, int q_dtype, long long q_
 /* The attention operator of one layer, as GpuModel::attention (src/cuda.rs:8448-8541) dispatches it:
  * qkv rows are [q (n_heads*hd) | k | v] f32 (stride n_heads*hd + 2*n_kv*hd, src/cuda.rs:1713), out rows
  * n_heads*hd f32. Batches of >= 16 tokens that are not `exact` (verify) go to prefill; the rest to the
- * split decode path in launches of at most 15 tokens (SPLIT_MAX_BATCH, src/cuda.rs:119). fixed_split
+ * split decode path in launches of at most 15 tokens (SPLIT_MAX_BATCH, src/cuda.rs:119). exact = 2: batches of
+ * >= 16 tokens take the f32 prefill (gi_attn_prefill_f32) at head sizes up to 128 over the f16 and int8 caches,
+ * as the reference does with GHOST_INFER_NO_TC_ATT; elsewhere the split path. fixed_split
  * with posp: the grid is sized for ctx_cap (the session capacity), as max_splits does. scale is
  * 1/sqrt(hd) as in the reference. */
 int gi_attention(void* stream, const float* qkv, const uint16_t* kc, const uint16_t* vc, float* out,

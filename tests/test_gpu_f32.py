@@ -162,3 +162,67 @@ def test_attention_operator_f32_head_size(gpu, n, pos0, exact, i8):
         want = reference_f64(q, k, v, pos0, n_heads, n_kv, hd=hd)
     torch.cuda.synchronize()
     assert_close(out.cpu().numpy(), want, *SPLIT_F64_TOL, what="operator f32 head size vs f64")
+
+
+F32_PROMPT_SHAPES = [
+    # (n, pos0, n_heads, n_kv, hd, layout, int8): the reference's attention_prefill with its tensor-core prefill off
+    (16, 0, 8, 2, 128, "reference", False),
+    (300, 0, 32, 8, 128, "head_major", False),
+    (129, 700, 16, 4, 128, "reference", True),
+    (200, 0, 9, 3, 64, "head_major", False),
+    (64, 3000, 8, 8, 64, "reference", True),
+]
+
+
+@pytest.mark.parametrize("n,pos0,n_heads,n_kv,hd,layout,i8", F32_PROMPT_SHAPES)
+def test_prefill_f32_prompts_at_mfma_head_sizes(gpu, n, pos0, n_heads, n_kv, hd, layout, i8):
+    say("prefill f32 prompts", n, pos0, n_heads, n_kv, hd, layout, i8)
+    if i8:
+        q, k, v, ks, vs = make_inputs_i8(5500 + n + pos0, n, pos0 + n, n_heads, n_kv, hd=hd)
+        kd = [np.ascontiguousarray(x) for x in (k, v, ks, vs)]
+        if layout == "head_major":
+            kd = [np.ascontiguousarray(x.reshape(x.shape[0], n_kv, hd).transpose(1, 0, 2)) for x in kd[:2]] + \
+                 [np.ascontiguousarray(x.T) for x in kd[2:]]
+        t = [torch.from_numpy(x).to(gpu) for x in kd]
+        out = gi_attn.prefill(torch.from_numpy(q).to(gpu), t[0], t[1], pos0, n_heads, n_kv, hd=hd,
+                              out_dtype=torch.float32, kv_layout=layout, k_scale=t[2], v_scale=t[3], f32=True)
+        want = reference_f64_i8(q, k, v, ks, vs, pos0, n_heads, n_kv, hd=hd)
+    else:
+        q, k, v = make_inputs(5600 + n + pos0, n, pos0 + n, n_heads, n_kv, hd=hd)
+        kt, vt = f16_dev(k, gpu), f16_dev(v, gpu)
+        if layout == "head_major":
+            kt = kt.view(-1, n_kv, hd).transpose(0, 1).contiguous()
+            vt = vt.view(-1, n_kv, hd).transpose(0, 1).contiguous()
+        out = gi_attn.prefill(torch.from_numpy(q).to(gpu), kt, vt, pos0, n_heads, n_kv, hd=hd, out_dtype=torch.float32,
+                              kv_layout=layout, f32=True)
+        want = reference_f64(q, k, v, pos0, n_heads, n_kv, hd=hd)
+    torch.cuda.synchronize()
+    assert_close(out.cpu().numpy(), want, *SPLIT_F64_TOL, what="f32 prompts vs f64")
+
+
+@pytest.mark.parametrize("hd,i8", [(128, False), (128, True), (64, False), (256, False)])
+def test_operator_f32_prompts_matches_the_split_path(gpu, hd, i8):
+    # exact = 2 (GHOST_INFER_NO_TC_ATT): prompts in f32; head size 256 has no such kernel and takes the split path
+    n, pos0 = 40, 90
+    n_heads, n_kv = (16, 2) if hd == 256 else (8, 2)
+    say("operator f32 prompts", hd, i8)
+    row = (n_heads + 2 * n_kv) * hd
+    qkv = np.random.default_rng(777 + hd).standard_normal((n, row), dtype=np.float32)
+    qkv_t = torch.from_numpy(qkv).to(gpu)
+    q = np.ascontiguousarray(qkv[:, :n_heads * hd])
+    if i8:
+        _, k, v, ks, vs = make_inputs_i8(778 + hd, 1, pos0 + n, n_heads, n_kv, hd=hd)
+        t = [torch.from_numpy(x).to(gpu) for x in (k, v, ks, vs)]
+        kw = dict(hd=hd, k_scale=t[2], v_scale=t[3])
+        kc, vc = t[0].view(-1, n_kv, hd), t[1].view(-1, n_kv, hd)
+        want = reference_f64_i8(q, k, v, ks, vs, pos0, n_heads, n_kv, hd=hd)
+    else:
+        _, k, v = make_inputs(778 + hd, 1, pos0 + n, n_heads, n_kv, hd=hd)
+        kw = dict(hd=hd)
+        kc, vc = f16_dev(k, gpu), f16_dev(v, gpu)
+        want = reference_f64(q, k, v, pos0, n_heads, n_kv, hd=hd)
+    a = gi_attn.attention(qkv_t, kc, vc, pos0, n_heads, n_kv, f32_prompts=True, **kw)
+    b = gi_attn.attention(qkv_t, kc, vc, pos0, n_heads, n_kv, exact=True, **kw)
+    torch.cuda.synchronize()
+    assert_close(a.cpu().numpy(), want, *SPLIT_F64_TOL, what="f32 prompts vs f64")
+    assert_close(a.cpu().numpy(), b.cpu().numpy(), *SPLIT_F64_TOL, what="f32 prompts vs the split path")
