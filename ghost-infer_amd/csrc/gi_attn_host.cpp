@@ -200,6 +200,7 @@ struct Module {
     hipFunction_t dec_ref[3] = {};    // head size 256, one pair per column, the reference's tc256 roundings: int8
                                       // one column block, 4-bit one and two column blocks
     hipFunction_t dec_pm256[2] = {};  // head size 256, one pair per column, two pair sets of two waves: [f16, int8]
+    hipFunction_t dec_i8_256f[2] = {}; // head size 256 over the int8 cache in f32 precision: [up to 8 pairs, above]
     hipFunction_t prefill[2] = {};   // [int8 cache], head size 128
     hipFunction_t prefill64[2] = {}; // [int8 cache], head size 64 (the same launch shape and block size)
     hipFunction_t dec_f32[2][6] = {}, prefill_f32[2][6] = {}; // the f32 kernels: [int8 cache][kF32Sizes index]
@@ -263,6 +264,8 @@ int load_module(const char* path, Module** out) {
             {&m.dec_ws2[1], "gi_decode_pm_ws2_2_i8"},
             {&m.dec_pm256[0], "gi_decode_pm_ws2_1_h256"},
             {&m.dec_pm256[1], "gi_decode_pm_ws2_1_i8_h256"},
+            {&m.dec_i8_256f[0], "gi_decode_partial_1_i8_h256f"},
+            {&m.dec_i8_256f[1], "gi_decode_pm_ws2_1_i8_h256f"},
             {&m.combine, "gi_decode_combine"},
             {&m.relayout, "gi_kv_relayout"},
             {&m.hadamard, "gi_hadamard_rows"},
@@ -507,7 +510,8 @@ int check_shape(int n_heads, int n_kv, int hd, bool = true) {
 int decode_impl(void* stream, const float* q, long long q_stride, const void* kc, const void* vc, const float* ks,
                 const float* vs, long long sc_stride, long long sc_head_stride, int fmt, long long kv_stride,
                 long long kv_head_stride, float* out, long long out_stride, void* workspace, size_t workspace_bytes,
-                int pos0, const int* posp, int ctx_cap, int n_tok, int n_heads, int n_kv, int hd, float scale) {
+                int pos0, const int* posp, int ctx_cap, int n_tok, int n_heads, int n_kv, int hd, float scale,
+                bool f32_256 = false) {
     if (int e = check_shape(n_heads, n_kv, hd, true)) return e;
     if (fmt == 2 && hd != 256) return fail("the 4-bit cache takes head size 256 only (got %d)", hd);
     const bool i8 = fmt == 1;
@@ -537,9 +541,12 @@ int decode_impl(void* stream, const float* q, long long q_stride, const void* kc
     if (posp && ctx_cap < n_tok) return fail("ctx_cap %d must cover the %d tokens", ctx_cap, n_tok);
     Module* m;
     if (int e = load_module(nullptr, &m)) return e;
-    const DecVariant var = dec_variant(n_tok, n_heads / n_kv, hd, fmt);
+    // f32_256: head size 256 over the int8 cache in f32 precision, with the f16 cache's pair layouts and slice plan
+    const bool f32_i8 = f32_256 && fmt == 1 && hd == 256;
+    const int vfmt = f32_i8 ? 0 : fmt;
+    const DecVariant var = dec_variant(n_tok, n_heads / n_kv, hd, vfmt);
     GiDecodeArgs a{};
-    plan(max_span, n_tok, n_heads, n_kv, &a.chunk, &a.nsplit, slice_unit(i8, hd), hd, fmt);
+    plan(max_span, n_tok, n_heads, n_kv, &a.chunk, &a.nsplit, slice_unit(i8, hd), hd, vfmt);
     size_t need = a.nsplit == 1 ? 0 : (size_t)n_tok * n_heads * a.nsplit * (hd + 4) * sizeof(float);
     if (need && (!workspace || workspace_bytes < need))
         return fail("workspace of %zu bytes too small: %zu needed", workspace_bytes, need);
@@ -575,7 +582,8 @@ int decode_impl(void* stream, const float* q, long long q_stride, const void* kc
         return launch(kDecodeCombine, m->combine, dim3(n_heads, n_tok, kCombineSplit * hd / 128), dim3(64), st, &a,
                       sizeof a);
     }
-    hipFunction_t f = hd == 64    ? m->dec64[i8][var.pm ? var.ncb : 0]
+    hipFunction_t f = f32_i8      ? m->dec_i8_256f[var.ws2 ? 1 : 0]
+                      : hd == 64  ? m->dec64[i8][var.pm ? var.ncb : 0]
                       : hd == 256 ? (var.ws2 ? m->dec_pm256[fmt] : fmt ? m->dec_ref[fmt - 1 + var.ncb - 1]
                                    : var.pm ? m->dec_pm256[0] : m->dec256)
                       : var.ws2   ? m->dec_ws2[i8]
@@ -1005,7 +1013,8 @@ int attention_impl(void* stream, const float* qkv, const void* kc, const void* v
         // with a device position every launch reads *posp, so only single launches take it
         if (posp && n > kSplitMaxBatch) return fail("posp takes at most %d tokens", kSplitMaxBatch);
         if (int e = decode_impl(stream, qkv + b0 * row, row, kc, vc, ks, vs, scs, sch, fmt, kvs, kvh, out + b0 * q_dim,
-                                q_dim, workspace, workspace_bytes, pos0 + b0, posp, ctx_cap, m, n_heads, n_kv, hd, scale))
+                                q_dim, workspace, workspace_bytes, pos0 + b0, posp, ctx_cap, m, n_heads, n_kv, hd, scale,
+                                exact == 2))
             return e;
     }
     return 0;

@@ -245,13 +245,18 @@ __device__ __forceinline__ uint32_t q4_f16x2(uint32_t hi, uint32_t lo, int j, h2
 // tensor cores, and the rest is the f16 cache's path (unit key and value scales). Lane (c, grp) takes values
 // 64grp .. 64grp + 63 of key row c (k-step kk: 64grp + 8kk .. + 7, the query loaded to match), so each lane's two
 // 16-byte loads are whole scale groups.
-template <int NCB, int WS, bool I8, int HD = 128, bool PM = false, bool Q4 = false>
+// F32 = true (head size 256 over the int8 cache): f32 precision through the f16 high/remainder split, as at the
+// other head sizes, instead of the tc256 roundings: the reference's attention_partial_gqa hd-256 branch
+// (src/cuda.rs:1762-1781), which serves this cache when its tensor-core decode is off (GHOST_INFER_NO_TC_ATT or
+// GHOST_INFER_NO_TC_DECODE, src/cuda.rs:5655).
+template <int NCB, int WS, bool I8, int HD = 128, bool PM = false, bool Q4 = false, bool F32 = false>
 __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
     static_assert(HD == 64 || HD == 128 || HD == 256, "head sizes: 64, 128, 256");
     static_assert(!Q4 || (HD == 256 && !I8), "the 4-bit cache: head size 256");
+    static_assert(!F32 || (I8 && HD == 256), "the f32-precise form: head size 256 over the int8 cache");
     // the reference's tc256 arithmetic (one f16 Q, one f16 P; see DEC_REF_VB): head size 256 over the int8 and
     // 4-bit caches, which these kernels serve with one pair per column
-    constexpr bool REF = (I8 || Q4) && HD == 256;
+    constexpr bool REF = (I8 || Q4) && HD == 256 && !F32;
     static_assert(!REF || PM, "head size 256 over the int8 and 4-bit caches: one pair per column");
     // the bias on P that the merge divides out
     constexpr float PBIAS = REF && I8 ? DEC_REF_VB : I8 && PM ? DEC_I8_VB : 1.f;
@@ -1209,6 +1214,14 @@ GI_DEC_PM256_KERNEL(gi_decode_pm_1_i8_h256, 1, DEC_WAVES, true)
 GI_DEC_PM256_KERNEL(gi_decode_pm_ws2_1_i8_h256, 1, 2, true)
 GI_DEC_Q4_KERNEL(gi_decode_pm_1_q4, 1, DEC_WAVES)
 GI_DEC_Q4_KERNEL(gi_decode_pm_2_q4, 2, DEC_WAVES)
+// head size 256 over the int8 cache in f32 precision (the f16 cache's layouts: up to 8 pairs the high/remainder
+// columns, above two pair sets of 16 per workgroup)
+extern "C" __global__ void __launch_bounds__(256, DEC_MINWG) gi_decode_partial_1_i8_h256f(GiDecodeArgs a) {
+    gi_decode_partial_t<1, DEC_WAVES, true, 256, false, false, true>(a);
+}
+extern "C" __global__ void __launch_bounds__(256, DEC_MINWG) gi_decode_pm_ws2_1_i8_h256f(GiDecodeArgs a) {
+    gi_decode_partial_t<1, 2, true, 256, true, false, true>(a);
+}
 
 
 // Merge the slices of each (token, head): M = max m_s, w_s = 2^(m_s - M), out = sum w_s O_s / sum w_s l_s

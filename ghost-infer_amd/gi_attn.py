@@ -464,14 +464,16 @@ def prefill(q, k_cache, v_cache, pos0, n_heads, n_kv, hd=128, scale=None, out=No
 
 
 def attention(qkv, k_cache, v_cache, pos0, n_heads, n_kv, hd=128, exact=False, out=None, workspace=None,
-              posp=None, ctx_cap=0, k_scale=None, v_scale=None, f32_prompts=False):
+              posp=None, ctx_cap=0, k_scale=None, v_scale=None, no_tc=False):
     """GpuModel::attention (src/cuda.rs:8448-8541) for one layer.
 
     qkv: f32 [n, n_heads*hd + 2*n_kv*hd] rows [q | k | v] (only q is read: the cache already holds this
     batch's K/V rows, as qk_norm_rope wrote them); returns f32 [n, n_heads*hd]. n >= 16 and not exact ->
     causal prefill kernel; otherwise the split decode path, 15 tokens per launch. The caches are the
     reference's [capacity, n_kv, hd]: f16, or int8 with f32 scales [capacity, n_kv] (its (kc, vc, ks, vs)).
-    f32_prompts: batches of >= 16 tokens in f32 (the reference's GHOST_INFER_NO_TC_ATT; head sizes up to 128).
+    no_tc: the reference's GHOST_INFER_NO_TC_ATT: batches of >= 16 tokens in f32 (head sizes up to 128; above, the
+    split path), and at head size 256 over the int8 cache the split path in f32 precision instead of the tc256
+    roundings.
     """
     _need(qkv, "qkv", torch.float32)
     n = qkv.shape[0]
@@ -490,14 +492,14 @@ def attention(qkv, k_cache, v_cache, pos0, n_heads, n_kv, hd=128, exact=False, o
     if posp is not None:
         _need(posp, "posp", torch.int32)
     ws_ptr, ws_bytes = None, 0
-    code = 1 if exact else 2 if f32_prompts else 0
-    split = n < TILED_MIN_BATCH or exact or (f32_prompts and hd > 128)
+    code = 2 if no_tc else 1 if exact else 0
+    split = n < TILED_MIN_BATCH or exact or (no_tc and hd > 128)
     if split:
         if workspace is None:
             cap = ctx_cap if posp is not None else pos0 + n
             workspace = new_workspace(cap, min(n, SPLIT_MAX_BATCH), n_heads, n_kv, hd, qkv.device)
         ws_ptr, ws_bytes = _ptr(workspace), workspace.numel() * workspace.element_size()
-    elif i8 and not f32_prompts:
+    elif i8 and not no_tc:
         # a prefill batch over the int8 cache: the pre-widened staging, whose workspace the library checks
         if workspace is None:
             workspace = prefill_workspace(pos0 + n, n_kv, hd, 1, qkv.device)

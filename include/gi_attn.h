@@ -194,7 +194,9 @@ int gi_attn_prefill_q4_ws(void* stream, const void* q, int q_dtype, long long q_
  * n_heads*hd f32. Batches of >= 16 tokens that are not `exact` (verify) go to prefill; the rest to the
  * split decode path in launches of at most 15 tokens (SPLIT_MAX_BATCH, src/cuda.rs:119). exact = 2: batches of
  * >= 16 tokens take the f32 prefill (gi_attn_prefill_f32) at head sizes up to 128 over the f16 and int8 caches,
- * as the reference does with GHOST_INFER_NO_TC_ATT; elsewhere the split path. fixed_split
+ * and the split path at head size 256 over the int8 cache computes in f32 precision instead of
+ * attention_decode_tc256's roundings, as the reference does with GHOST_INFER_NO_TC_ATT (src/cuda.rs:5648-5655);
+ * everything else as exact = 1. fixed_split
  * with posp: the grid is sized for ctx_cap (the session capacity), as max_splits does. scale is
  * 1/sqrt(hd) as in the reference. */
 int gi_attention(void* stream, const float* qkv, const uint16_t* kc, const uint16_t* vc, float* out,

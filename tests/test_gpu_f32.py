@@ -200,12 +200,14 @@ def test_prefill_f32_prompts_at_mfma_head_sizes(gpu, n, pos0, n_heads, n_kv, hd,
     assert_close(out.cpu().numpy(), want, *SPLIT_F64_TOL, what="f32 prompts vs f64")
 
 
-@pytest.mark.parametrize("hd,i8", [(128, False), (128, True), (64, False), (256, False)])
-def test_operator_f32_prompts_matches_the_split_path(gpu, hd, i8):
-    # exact = 2 (GHOST_INFER_NO_TC_ATT): prompts in f32; head size 256 has no such kernel and takes the split path
-    n, pos0 = 40, 90
+@pytest.mark.parametrize("hd,i8,n", [(128, False, 40), (128, True, 40), (64, False, 40), (256, False, 40),
+                                    (256, True, 40), (256, True, 5), (256, True, 12)])
+def test_operator_f32_prompts_matches_the_split_path(gpu, hd, i8, n):
+    # exact = 2 (GHOST_INFER_NO_TC_ATT): prompts in f32; head size 256 has no such kernel and takes the split path,
+    # over the int8 cache in f32 precision (attention_partial_gqa's hd-256 branch) instead of the tc256 roundings
+    pos0 = 90
     n_heads, n_kv = (16, 2) if hd == 256 else (8, 2)
-    say("operator f32 prompts", hd, i8)
+    say("operator f32 prompts", hd, i8, n)
     row = (n_heads + 2 * n_kv) * hd
     qkv = np.random.default_rng(777 + hd).standard_normal((n, row), dtype=np.float32)
     qkv_t = torch.from_numpy(qkv).to(gpu)
@@ -221,8 +223,10 @@ def test_operator_f32_prompts_matches_the_split_path(gpu, hd, i8):
         kw = dict(hd=hd)
         kc, vc = f16_dev(k, gpu), f16_dev(v, gpu)
         want = reference_f64(q, k, v, pos0, n_heads, n_kv, hd=hd)
-    a = gi_attn.attention(qkv_t, kc, vc, pos0, n_heads, n_kv, f32_prompts=True, **kw)
+    a = gi_attn.attention(qkv_t, kc, vc, pos0, n_heads, n_kv, no_tc=True, **kw)
     b = gi_attn.attention(qkv_t, kc, vc, pos0, n_heads, n_kv, exact=True, **kw)
     torch.cuda.synchronize()
     assert_close(a.cpu().numpy(), want, *SPLIT_F64_TOL, what="f32 prompts vs f64")
-    assert_close(a.cpu().numpy(), b.cpu().numpy(), *SPLIT_F64_TOL, what="f32 prompts vs the split path")
+    # (exact = 1 at head size 256 over the int8 cache keeps the tc256 roundings: the parity bar between the two)
+    ab_tol = (2e-3, 1e-3) if hd == 256 and i8 else SPLIT_F64_TOL
+    assert_close(a.cpu().numpy(), b.cpu().numpy(), *ab_tol, what="f32 prompts vs the split path")
