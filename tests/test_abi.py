@@ -193,3 +193,20 @@ def test_q4_entry_points_reject_bad_arguments_before_any_launch():
     assert rc == -1 and "scale" in lib.gi_last_error().decode()
     rc = lib.gi_hadamard_rows(None, 16, 256, 4, 300)
     assert rc == -1 and "multiple of 256" in lib.gi_last_error().decode()
+
+
+def test_prefill_workspace_bytes():
+    # f16 K and V rows [n_kv][kv_len][hd] (and for int8 f32 scales [n_kv][kv_len]), each region 256-byte aligned;
+    # 0 where no widened staging applies (the f16 cache, the f32 kernels' head sizes, the 4-bit cache below 256)
+    lib = gi_attn.load_library()
+
+    def a256(x):
+        return (x + 255) // 256 * 256
+
+    for kv_len, n_kv, hd in ((8192, 8, 128), (1, 1, 64), (1000, 3, 64), (777, 2, 256)):
+        want_i8 = 2 * a256(n_kv * kv_len * hd * 2) + 2 * a256(n_kv * kv_len * 4)
+        assert lib.gi_attn_prefill_workspace_bytes(kv_len, n_kv, hd, 1) == want_i8
+    assert lib.gi_attn_prefill_workspace_bytes(777, 2, 256, 2) == 2 * a256(2 * 777 * 256 * 2)
+    for args in ((100, 2, 128, 0), (100, 2, 96, 1), (100, 2, 128, 2), (0, 2, 128, 1), (100, 0, 128, 1),
+                 (100, 2, 72, 1)):
+        assert lib.gi_attn_prefill_workspace_bytes(*args) == 0, args
