@@ -210,3 +210,16 @@ def test_prefill_workspace_bytes():
     for args in ((100, 2, 128, 0), (100, 2, 96, 1), (100, 2, 128, 2), (0, 2, 128, 1), (100, 0, 128, 1),
                  (100, 2, 72, 1)):
         assert lib.gi_attn_prefill_workspace_bytes(*args) == 0, args
+
+
+def test_f32_prompts_and_widened_prefill_reject_bad_arguments_before_any_launch():
+    _fake_pointers_only_without_a_gpu()
+    lib = gi_attn.load_library()
+    # gi_attn_prefill_f32: head sizes up to 128 (the reference's attention_prefill)
+    rc = lib.gi_attn_prefill_f32(None, 16, 0, 8192, 16, 16, None, None, 0, 512, 256, 0, 0, 16, 0, 4096, 0, 16, 16, 2,
+                                 256, 0.0625)
+    assert rc == -1 and "up to 128" in lib.gi_last_error().decode()
+    # the widened int8 prefill: a workspace is required
+    rc = lib.gi_attn_prefill_i8_ws(None, 16, 0, 4096, 16, 16, 16, 16, 1024, 128, 0, 0, 16, 0, 4096, 0, 16, 32, 8, 128,
+                                   0.088, None, 0)
+    assert rc == -1 and "workspace" in lib.gi_last_error().decode()
