@@ -120,3 +120,30 @@ def test_prefill_workspace_is_checked(gpu):
     ref2 = gi_attn.prefill(q2, k, v, pos0, n_heads, n_kv, hd=hd, k_scale=ks, v_scale=vs, staged=False)
     torch.cuda.synchronize()
     assert torch.equal(second, ref2) and torch.isfinite(first).all()
+
+
+def test_widened_prefill_graph_replay(gpu):
+    # the widening launch and the prefill captured together, replayed with new queries and eager work between the
+    # replays; every replay against the eager result
+    n, pos0, n_heads, n_kv, hd = 96, 200, 8, 2, 128
+    q, (k, v, ks, vs) = _i8_tensors(6500, n, pos0, n_heads, n_kv, hd, "reference", gpu)
+    ws = gi_attn.prefill_workspace(pos0 + n, n_kv, hd, 1, gpu)
+    out = torch.empty((n, n_heads * hd), dtype=torch.float32, device=gpu)
+    kw = dict(hd=hd, k_scale=ks, v_scale=vs, workspace=ws, out=out)
+    gi_attn.prefill(q, k, v, pos0, n_heads, n_kv, **kw)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        gi_attn.prefill(q, k, v, pos0, n_heads, n_kv, **kw)
+    gen = torch.Generator(device=gpu)
+    gen.manual_seed(6501)
+    for r in range(3):
+        say("widened prefill replay", r)
+        q.copy_(torch.randn(q.shape, generator=gen, device=gpu))
+        want = gi_attn.prefill(q, k, v, pos0, n_heads, n_kv, hd=hd, k_scale=ks, v_scale=vs, staged=False,
+                               out_dtype=torch.float32)
+        torch.cuda.synchronize()
+        out.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, want), f"replay {r}"
