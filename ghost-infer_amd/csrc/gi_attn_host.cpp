@@ -993,15 +993,17 @@ int attention_impl(void* stream, const float* qkv, const void* kc, const void* v
     // [position][n_kv] (the 4-bit cache: [position][n_kv][hd / 32] f16)
     const long long kvs = fmt == 2 ? kv_dim / 2 : kv_dim, kvh = fmt == 2 ? hd / 2 : hd;
     const long long scs = fmt == 2 ? (long long)n_kv * (hd / 32) : n_kv, sch = fmt == 2 ? hd / 32 : 1;
-    // exact 2: prompts in f32 (the reference with its tensor-core prefill off, GHOST_INFER_NO_TC_ATT, launches
-    // attention_prefill for head sizes up to 128, src/cuda.rs:8452-8476); the 4-bit cache and head size 256 have no
-    // such kernel there and take the split path
-    if (n >= kTiledMinBatch && exact == 2 && fmt != 2 && hd <= 128) {
+    // exact bit 0: a verify batch, every token on the split path (s.exact, src/cuda.rs:8457-8458). Bit 1: the
+    // reference with its tensor-core kernels off (GHOST_INFER_NO_TC_ATT): prompts in f32 (attention_prefill, head sizes
+    // up to 128, src/cuda.rs:8452-8476; the 4-bit cache and head size 256 have no such kernel there and take the split
+    // path), and the head-256 int8 decode in f32 precision (no attention_decode_tc256, src/cuda.rs:5655)
+    const bool verify = exact & 1, no_tc = exact & 2;
+    if (n >= kTiledMinBatch && !verify && no_tc && fmt != 2 && hd <= 128) {
         if (posp) return fail("a device position (posp) is only taken by the split path");
         return prefill_impl(stream, qkv, GI_F32, row, kc, vc, ks, vs, scs, sch, fmt, kvs, kvh, out, GI_F32, q_dim, pos0,
                             n, n_heads, n_kv, hd, scale, nullptr, 0, true);
     }
-    if (n >= kTiledMinBatch && !exact) {
+    if (n >= kTiledMinBatch && !verify && !no_tc) {
         if (posp) return fail("a device position (posp) is only taken by the split path");
         // the int8 and 4-bit caches: pre-widened staging when the workspace holds it
         const bool staged = fmt && workspace && workspace_bytes >= prefill_ws_bytes(pos0 + n, n_kv, hd, fmt);
@@ -1014,7 +1016,7 @@ int attention_impl(void* stream, const float* qkv, const void* kc, const void* v
         if (posp && n > kSplitMaxBatch) return fail("posp takes at most %d tokens", kSplitMaxBatch);
         if (int e = decode_impl(stream, qkv + b0 * row, row, kc, vc, ks, vs, scs, sch, fmt, kvs, kvh, out + b0 * q_dim,
                                 q_dim, workspace, workspace_bytes, pos0 + b0, posp, ctx_cap, m, n_heads, n_kv, hd, scale,
-                                exact == 2))
+                                no_tc))
             return e;
     }
     return 0;

@@ -492,7 +492,7 @@ def attention(qkv, k_cache, v_cache, pos0, n_heads, n_kv, hd=128, exact=False, o
     if posp is not None:
         _need(posp, "posp", torch.int32)
     ws_ptr, ws_bytes = None, 0
-    code = 2 if no_tc else 1 if exact else 0
+    code = (1 if exact else 0) | (2 if no_tc else 0)  # the library's exact bits: verify, no tensor-core kernels
     split = n < TILED_MIN_BATCH or exact or (no_tc and hd > 128)
     if split:
         if workspace is None:

@@ -160,7 +160,7 @@ int gi_attn_prefill_q4(void* stream, const void* q, int q_dtype, long long q_str
  * kv_int8, the int8 cache (ks / vs and the scale strides as gi_attn_prefill_i8), head sizes 16 to 128 in steps of 16.
  * Replaces: attention_prefill (src/cuda.rs:1934-2041), which GpuModel::attention launches for prompts when the
  * tensor-core prefill is off (GHOST_INFER_NO_TC_ATT, src/cuda.rs:5648-5654) or the head size has none
- * (src/cuda.rs:8452-8476). gi_attention / gi_attention_i8 take this path for prompts with exact = 2. */
+ * (src/cuda.rs:8452-8476). gi_attention / gi_attention_i8 take this path for prompts with bit 1 of exact set. */
 int gi_attn_prefill_f32(void* stream, const void* q, int q_dtype, long long q_stride, const void* kc, const void* vc,
                         const float* ks, const float* vs, int kv_int8, long long kv_stride, long long kv_head_stride,
                         long long sc_stride, long long sc_head_stride, void* out, int out_dtype, long long out_stride,
@@ -191,12 +191,12 @@ int gi_attn_prefill_q4_ws(void* stream, const void* q, int q_dtype, long long q_
 
 /* The attention operator of one layer, as GpuModel::attention (src/cuda.rs:8448-8541) dispatches it:
  * qkv rows are [q (n_heads*hd) | k | v] f32 (stride n_heads*hd + 2*n_kv*hd, src/cuda.rs:1713), out rows
- * n_heads*hd f32. Batches of >= 16 tokens that are not `exact` (verify) go to prefill; the rest to the
- * split decode path in launches of at most 15 tokens (SPLIT_MAX_BATCH, src/cuda.rs:119). exact = 2: batches of
- * >= 16 tokens take the f32 prefill (gi_attn_prefill_f32) at head sizes up to 128 over the f16 and int8 caches,
- * and the split path at head size 256 over the int8 cache computes in f32 precision instead of
- * attention_decode_tc256's roundings, as the reference does with GHOST_INFER_NO_TC_ATT (src/cuda.rs:5648-5655);
- * everything else as exact = 1. fixed_split
+ * n_heads*hd f32. Batches of >= 16 tokens go to prefill; the rest, and every batch with bit 0 of `exact` set (a
+ * verify batch, the reference's s.exact), to the split decode path in launches of at most 15 tokens
+ * (SPLIT_MAX_BATCH, src/cuda.rs:119). Bit 1 of `exact` is the reference's GHOST_INFER_NO_TC_ATT
+ * (src/cuda.rs:5648-5655): prefill batches take the f32 prefill (gi_attn_prefill_f32) at head sizes up to 128 over
+ * the f16 and int8 caches and the split path elsewhere, and at head size 256 over the int8 cache the split path
+ * computes in f32 precision instead of attention_decode_tc256's roundings. fixed_split
  * with posp: the grid is sized for ctx_cap (the session capacity), as max_splits does. scale is
  * 1/sqrt(hd) as in the reference. */
 int gi_attention(void* stream, const float* qkv, const uint16_t* kc, const uint16_t* vc, float* out,

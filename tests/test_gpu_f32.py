@@ -203,7 +203,7 @@ def test_prefill_f32_prompts_at_mfma_head_sizes(gpu, n, pos0, n_heads, n_kv, hd,
 @pytest.mark.parametrize("hd,i8,n", [(128, False, 40), (128, True, 40), (64, False, 40), (256, False, 40),
                                     (256, True, 40), (256, True, 5), (256, True, 12)])
 def test_operator_f32_prompts_matches_the_split_path(gpu, hd, i8, n):
-    # exact = 2 (GHOST_INFER_NO_TC_ATT): prompts in f32; head size 256 has no such kernel and takes the split path,
+    # bit 1 of exact (GHOST_INFER_NO_TC_ATT): prompts in f32; head size 256 has no such kernel and takes the split path,
     # over the int8 cache in f32 precision (attention_partial_gqa's hd-256 branch) instead of the tc256 roundings
     pos0 = 90
     n_heads, n_kv = (16, 2) if hd == 256 else (8, 2)
@@ -230,3 +230,34 @@ def test_operator_f32_prompts_matches_the_split_path(gpu, hd, i8, n):
     # (exact = 1 at head size 256 over the int8 cache keeps the tc256 roundings: the parity bar between the two)
     ab_tol = (2e-3, 1e-3) if hd == 256 and i8 else SPLIT_F64_TOL
     assert_close(a.cpu().numpy(), b.cpu().numpy(), *ab_tol, what="f32 prompts vs the split path")
+
+
+@pytest.mark.parametrize("hd,i8", [(128, False), (256, True)])
+def test_operator_verify_with_no_tc(gpu, hd, i8):
+    # bits 0 and 1 of exact: a verify batch under GHOST_INFER_NO_TC_ATT stays on the split path (every token a
+    # decode step, as s.exact does), in f32 precision at head size 256 over the int8 cache as well
+    n, pos0 = 40, 90
+    n_heads, n_kv = (16, 2) if hd == 256 else (8, 2)
+    say("operator verify no_tc", hd, i8)
+    row = (n_heads + 2 * n_kv) * hd
+    qkv = np.random.default_rng(888 + hd).standard_normal((n, row), dtype=np.float32)
+    qkv_t = torch.from_numpy(qkv).to(gpu)
+    q = np.ascontiguousarray(qkv[:, :n_heads * hd])
+    if i8:
+        _, k, v, ks, vs = make_inputs_i8(889 + hd, 1, pos0 + n, n_heads, n_kv, hd=hd)
+        t = [torch.from_numpy(x).to(gpu) for x in (k, v, ks, vs)]
+        kw = dict(hd=hd, k_scale=t[2], v_scale=t[3])
+        kc, vc = t[0].view(-1, n_kv, hd), t[1].view(-1, n_kv, hd)
+        want = reference_f64_i8(q, k, v, ks, vs, pos0, n_heads, n_kv, hd=hd)
+    else:
+        _, k, v = make_inputs(889 + hd, 1, pos0 + n, n_heads, n_kv, hd=hd)
+        kw = dict(hd=hd)
+        kc, vc = f16_dev(k, gpu), f16_dev(v, gpu)
+        want = reference_f64(q, k, v, pos0, n_heads, n_kv, hd=hd)
+    a = gi_attn.attention(qkv_t, kc, vc, pos0, n_heads, n_kv, exact=True, no_tc=True, **kw)
+    torch.cuda.synchronize()
+    assert_close(a.cpu().numpy(), want, *SPLIT_F64_TOL, what="verify under no_tc vs f64")
+    if not i8:  # the split path itself: the same kernels as exact alone, bit for bit
+        b = gi_attn.attention(qkv_t, kc, vc, pos0, n_heads, n_kv, exact=True, **kw)
+        torch.cuda.synchronize()
+        assert torch.equal(a, b)
