@@ -4,8 +4,9 @@ every cache format: 1-60 tokens of reference-layout qkv rows at a prefix of up t
 operator takes the split path in launches of at most 15 tokens (the split path's bar, 2e-5; at head size 256 over
 the int8 and 4-bit caches, whose split path rounds Q and P to f16 as the reference does, the north star's); from 16
 tokens it
-takes the prefill kernel (the prefill bar, 2e-3 max-abs and 1e-3 relative L2). Seeded, so that a failure names
-its case and reproduces."""
+takes the prefill kernel (the prefill bar, 2e-3 max-abs and 1e-3 relative L2). With bit 1 of `exact` (the
+reference's GHOST_INFER_NO_TC_ATT) every batch computes in f32 precision (the 2e-5 bar). Seeded, so that a failure
+names its case and reproduces."""
 import sys
 
 import numpy as np
@@ -75,3 +76,33 @@ def test_random_operator(gpu, fmt, i, n, pos0, n_heads, n_kv, hd, exact):
     split = n < 16 or exact
     tol = split_f64_tol(fmt, hd) if split else (2e-3, 1e-3)
     assert_close(got, want, max_abs=tol[0], rel_l2=tol[1], what=f"{fmt} case {i} ({'split' if split else 'prefill'})")
+
+
+NO_TC_CASES = [c + (True,) for c in cases("f16", 6, 34) + cases("i8", 6, 35)]
+
+
+@pytest.mark.parametrize("fmt,i,n,pos0,n_heads,n_kv,hd,exact,no_tc", NO_TC_CASES, ids=lambda v: str(v))
+def test_random_operator_no_tc(gpu, fmt, i, n, pos0, n_heads, n_kv, hd, exact, no_tc):
+    # bit 1 of exact (GHOST_INFER_NO_TC_ATT): every batch in f32 precision (prompts up to head size 128 on the f32
+    # prefill, the rest on the split path, head size 256 over int8 without the tc256 roundings): the 2e-5 bar
+    say("random operator no_tc", fmt, i, n, pos0, n_heads, n_kv, hd, exact)
+    seed = 9500 + 71 * i + {"f16": 0, "i8": 1}[fmt]
+    ctx = pos0 + n
+    row = n_heads * hd + 2 * n_kv * hd
+    qkv = np.random.default_rng(seed + 10).standard_normal((n, row), dtype=np.float32)
+    qt = torch.from_numpy(qkv).to(gpu)
+    q = np.ascontiguousarray(qkv[:, :n_heads * hd])
+    if fmt == "f16":
+        _, k, v = make_inputs(seed, 1, ctx, n_heads, n_kv, hd=hd)
+        kt, vt = (torch.from_numpy(x.view(np.int16)).to(gpu).view(torch.float16).view(ctx, n_kv, hd) for x in (k, v))
+        out = gi_attn.attention(qt, kt, vt, pos0, n_heads, n_kv, hd=hd, exact=exact, no_tc=no_tc)
+        want = reference_f64(q, k, v, pos0, n_heads, n_kv, hd=hd)
+    else:
+        _, k, v, ks, vs = make_inputs_i8(seed, 1, ctx, n_heads, n_kv, hd=hd)
+        kt, vt = (torch.from_numpy(x).to(gpu).view(ctx, n_kv, hd) for x in (k, v))
+        kst, vst = (torch.from_numpy(x).to(gpu) for x in (ks, vs))
+        out = gi_attn.attention(qt, kt, vt, pos0, n_heads, n_kv, hd=hd, exact=exact, k_scale=kst, v_scale=vst,
+                                no_tc=no_tc)
+        want = reference_f64_i8(q, k, v, ks, vs, pos0, n_heads, n_kv, hd=hd)
+    torch.cuda.synchronize()
+    assert_close(out.cpu().numpy(), want, *split_f64_tol("f16", hd), what=f"{fmt} case {i} no_tc")
