@@ -202,7 +202,13 @@ int main(int argc, char** argv) {
     hip_ok(hipEventCreate(&e0), "hipEventCreate");
     hip_ok(hipEventCreate(&e1), "hipEventCreate");
 
+    // progress on stderr, flushed, so that a run that stalls shows how far it got
+    auto stage = [](const char* what) {
+        fprintf(stderr, "[harness] %s\n", what);
+        fflush(stderr);
+    };
     // 1. the prompt
+    stage("prompt");
     hip_ok(hipEventRecord(e0, st), "hipEventRecord");
     gi_ok(write_cache(qkv, 0, nullptr, o.prompt), "cache write (prompt)");
     gi_ok(attention(qkv, out, 0, nullptr, o.prompt, 0), "attention (prompt)");
@@ -212,6 +218,7 @@ int main(int argc, char** argv) {
     hip_ok(hipEventElapsedTime(&prompt_ms, e0, e1), "hipEventElapsedTime");
 
     // 2. decode steps
+    stage("decode steps");
     hipGraphExec_t exec = nullptr;
     if (o.graph && o.steps > 0) {
         hipGraph_t graph;
@@ -248,6 +255,7 @@ int main(int argc, char** argv) {
     }
 
     // 3. the reference pass over the whole (already rotated) sequence, exact split path
+    stage("reference pass");
     gi_ok(attention(qkv, ref, 0, nullptr, total, 1), "attention (reference pass)");
     hip_ok(hipStreamSynchronize(st), "hipStreamSynchronize");
     std::vector<float> got((size_t)total * orow), want((size_t)total * orow);
@@ -285,6 +293,8 @@ int main(int argc, char** argv) {
            o.prompt, o.steps, H, K, hd, o.q4 ? "q4" : o.i8 ? "int8" : "f16", exec ? "true" : "false", prompt_ms,
            o.steps ? 1e3 * step_ms / o.steps : 0.0, err_prompt, err_decode, tol_prompt, tol_decode,
            ok ? "true" : "false");
+    fflush(stdout);
+    stage("done");
     if (exec) (void)hipGraphExecDestroy(exec);
     return ok ? 0 : 1;
 }

@@ -55,7 +55,12 @@ def test_layer_harness(case, tmp_path):
     assert os.path.exists(HARNESS), "gi_layer_harness is not built (run __graft_entry__.build())"
     dump = str(tmp_path / "rows.bin")
     print("harness", " ".join(args), flush=True)
-    r = subprocess.run([HARNESS, *args, "--dump", dump], capture_output=True, text=True, timeout=120)
+    # (a run that does not finish is stopped well inside pytest's own limit, so that its output, the harness's
+    # progress lines on stderr included, is reported)
+    try:
+        r = subprocess.run([HARNESS, *args, "--dump", dump], capture_output=True, text=True, timeout=60)
+    except subprocess.TimeoutExpired as e:
+        pytest.fail(f"harness did not finish in 60 s; stdout {e.stdout!r}, stderr {e.stderr!r}")
     sys.stdout.write(r.stdout)
     sys.stderr.write(r.stderr)
     assert r.returncode == 0, f"harness exit {r.returncode}: {r.stderr.strip() or r.stdout.strip()}"
