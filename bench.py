@@ -350,7 +350,7 @@ def peak_probes(torch, dev, reps=5):
     if hip.hipModuleLoad(ctypes.byref(mod), path.encode()):
         raise RuntimeError("hipModuleLoad of the probe code object failed")
     fns = {}
-    for name in ("gi_probe_mfma", "gi_probe_read", "gi_probe_lds"):
+    for name in ("gi_probe_mfma", "gi_probe_mfma_rand", "gi_probe_read", "gi_probe_lds"):
         f = ctypes.c_void_p()
         if hip.hipModuleGetFunction(ctypes.byref(f), mod, name.encode()):
             raise RuntimeError(f"probe kernel {name} not found")
@@ -391,6 +391,9 @@ def peak_probes(torch, dev, reps=5):
     t = timed(lambda: launch(fns["gi_probe_mfma"], wgs, MfmaArgs(iters, 0, sink.data_ptr())))
     mfma_tflops = wgs * 4 * iters * 32 * 32768 / t / 1e12
     res = {"mfma_f16_dense_TFLOPs": round(mfma_tflops, 1)}
+    # the same over operands that change every instruction, as N(0,1) data does
+    t = timed(lambda: launch(fns["gi_probe_mfma_rand"], wgs, MfmaArgs(iters, 0, sink.data_ptr())))
+    res["mfma_f16_dense_random_operands_TFLOPs"] = round(wgs * 4 * iters * 32 * 32768 / t / 1e12, 1)
     flag = torch.zeros(1, dtype=torch.int32, device=dev)
     for label, nbytes, rd_wgs in (("hbm_read_GBs_1GiB", 1 << 30, 1024), ("hbm_read_GBs_134MB", 134217728, 256)):
         bufs = [torch.empty(nbytes, dtype=torch.uint8, device=dev) for _ in range(3)]  # rotate past the 256 MB cache
@@ -672,7 +675,7 @@ def compact_roofline(rf, extra=()):
 def compact_line(result):
     """The printed line: the headline fields, its roofline and CPU baseline, and for each other benchmark config
     (1, 3, 4 and 5) its value, time and roofline; every other workload's roofline fraction. The full record
-    (every field, every workload) goes to the detail file. Kept under ~2 KB so that a record holding only the
+    (every field, every workload) goes to the detail file. Kept near 2 KB so that a record holding only the
     end of the output still holds all of it."""
     out = {k: result[k] for k in ("metric", "value", "unit", "n_gpus", "steps", "warmup", "ms_per_step",
                                   "higher_is_better", "scaling", "vs_baseline", "dtype", "data") if k in result}
@@ -701,6 +704,12 @@ def compact_line(result):
                     pc = c["per_chunk_tflops"]
                     # every 16th chunk (chunk index 16i) and the last; all of them are in the detail file
                     cs[w]["per_chunk_tflops_every16"] = [round(t) for t in pc[::16]] + [round(pc[-1])]
+        pk = sec.get("peaks_measured")
+        if isinstance(pk, dict):
+            # this box's measured ceilings: MFMA over constant and over changing operands, the 134 MB read
+            cs["peaks"] = {short: pk[k] for short, k in (("mfma_TF", "mfma_f16_dense_TFLOPs"),
+                                                         ("mfma_rand_TF", "mfma_f16_dense_random_operands_TFLOPs"),
+                                                         ("read134_GBs", "hbm_read_GBs_134MB")) if k in pk}
         # "workload=frac ..." in one string: the shortest form that keeps every name
         cs["frac_other"] = " ".join(f"{w}={sec[w]['roofline']['frac']:.3f}" for w in sec
                                     if w not in cs and isinstance(sec[w], dict) and "roofline" in sec[w])

@@ -2,6 +2,8 @@
 // kernel's roofline fraction can be read against the measured peaks as well as the published ones.
 //  - gi_probe_mfma: v_mfma_f32_32x32x16_f16 only (the prefill's instruction), four independent accumulator
 //    chains per wave, two waves per SIMD: the dense f16 MFMA rate at the clock the chip holds under it.
+//  - gi_probe_mfma_rand: the same over pseudo-random operands that change every instruction (the power the
+//    prefill's N(0,1) data draws, and so the clock the chip holds under it).
 //  - gi_probe_read: a pure HBM read stream: each workgroup reads one contiguous chunk with 16 16-byte
 //    loads in flight per lane, streaming (nt) cache policy (the decode's access pattern and policy).
 //  - gi_probe_lds: LDS operand reads only, 16 in flight per lane, either ds_read_b128 (the prefill's K
@@ -36,6 +38,51 @@ extern "C" __global__ void __launch_bounds__(256) gi_probe_mfma(int iters, float
 #pragma unroll
         for (int e = 0; e < 16; e++) r += acc[k][e];
     out[blockIdx.x * blockDim.x + threadIdx.x] = r;
+}
+
+// The same instruction and schedule over operands that look like the prefill's: every lane holds 8 A and 8 B
+// fragments of pseudo-random f16 values in [-2, 2) (a hash of lane and index), and consecutive MFMAs of a chain
+// take different fragments, so the matrix core's inputs change every instruction as they do over N(0,1) K, Q,
+// V and P. The dense rate then reflects the clock the chip holds under data that toggles (gi_probe_mfma's
+// constant operands draw less power). flops per launch as gi_probe_mfma.
+__device__ __forceinline__ h8 gi_probe_frag(uint32_t seed) {
+    h8 r;
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+        uint32_t x = (seed * 8u + (uint32_t)e) * 2654435761u;
+        x ^= x >> 15;
+        x *= 2246822519u;
+        x ^= x >> 13;
+        r[e] = (_Float16)((float)(x >> 8) * (4.f / 16777216.f) - 2.f);
+    }
+    return r;
+}
+extern "C" __global__ void __launch_bounds__(256) gi_probe_mfma_rand(int iters, float* out) {
+    const uint32_t g = blockIdx.x * blockDim.x + threadIdx.x;
+    h8 a[8], b[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        a[i] = gi_probe_frag(g * 16u + (uint32_t)i);
+        b[i] = gi_probe_frag(g * 16u + 8u + (uint32_t)i);
+    }
+    f16x acc[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++)
+#pragma unroll
+        for (int e = 0; e < 16; e++) acc[k][e] = 0.f;
+    for (int it = 0; it < iters; it++) {
+#pragma unroll
+        for (int s = 0; s < 8; s++)
+#pragma unroll
+            for (int k = 0; k < 4; k++)
+                acc[k] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[(s + 2 * k) & 7], b[(s + 3 * k + 1) & 7], acc[k], 0, 0, 0);
+    }
+    float r = 0.f;
+#pragma unroll
+    for (int k = 0; k < 4; k++)
+#pragma unroll
+        for (int e = 0; e < 16; e++) r += acc[k][e];
+    out[g] = r;
 }
 
 // Workgroup w reads 16-byte units [w * n16, (w + 1) * n16) of p; out gets a fold of the data (never equal to
