@@ -97,6 +97,10 @@ __device__ __attribute__((used, aligned(256))) unsigned char gi_scratch[GI_SCRAT
 #define DEC_CPOL 2
 #endif
 #define DEC_PAIRS 8 // (token, head) pairs per column block of 16 columns
+#ifndef DEC_I8_MFMA // int8 cache, up to 8 pairs (hi/lo columns): QK on int8 MFMA against the query's int8 limbs
+#define DEC_I8_MFMA 1
+#endif
+typedef int i4v __attribute__((ext_vector_type(4)));
 #define DEC_RESCALE_LOG2 8.0f
 // int8 cache: the probability's f16 remainder column is scaled by 2^12 (undone when the columns merge).
 // Times a value scale of ~0.03 the remainder would otherwise fall into f16's subnormal range.
@@ -325,6 +329,16 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
     // int8: this lane dims 16grp + 8(kk%2) + 64(kk/2) .. +7 (the bytes its two 16-byte key loads bring)
     h8 qf[NCB][KK];
     h8 qfl[NCB][REF ? 1 : KK]; // PM: the remainders (REF: none; else unused)
+    // I8M: the int8 cache with up to 8 pairs at head sizes 64 and 128 (two columns a pair): the keys stay int8 and
+    // QK runs on v_mfma_i32_16x16x64_i8 against the query as an integer. Per pair, Q * scale * log2(e) is scaled
+    // by 2^(22 - e) (every element then below 2^22 in magnitude, e the exponent of the pair's largest) and rounded
+    // to an integer qi = 65536 L0 + 256 L1 + L2 with balanced int8 limbs (L1, L2 in [-128, 127], |L0| <= 65). The
+    // pair's even column holds L0 (qb1) and L2 (qb2), its odd column L1 (qb1) and zeros (qb2), so the two columns'
+    // exact int32 dot products, scaled by qcm / qc2 and added, give the score; the query is represented to 2^-23 of
+    // its largest element (the f16 high/remainder split of the other kernels: 2^-22 of each element).
+    constexpr bool I8M = DEC_I8_MFMA && I8 && !PM && HD != 256;
+    i4v qb1[HD / 64], qb2[HD / 64];
+    float qcm = 0.f, qc2 = 0.f;
     {
         __amdgpu_buffer_rsrc_t rq = gi_rsrc(a.q, (long long)a.n_tok * a.q_stride * 4);
 #pragma unroll
@@ -562,6 +576,23 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
     };
     // the int8 cache's QK over one 64-key tile: the keys widened to exact f16, sacc from zero
     auto qk_i8 = [&](auto& B, f4 (&sacc)[NCB][4]) {
+        if constexpr (I8M) {
+            // the key bytes as they were loaded (dims 64h + 16grp .. + 15 of the block's key), against the limbs of the
+            // same dims; an exact int32 dot product per column and limb set
+#pragma unroll
+            for (int b = 0; b < 4; b++) {
+                i4v a1 = i4v{0, 0, 0, 0}, a2 = a1;
+#pragma unroll
+                for (int h = 0; h < HD / 64; h++) {
+                    const i4v kb = __builtin_bit_cast(i4v, B.k[b][h]);
+                    a1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(kb, qb1[h], a1, 0, 0, 0);
+                    a2 = __builtin_amdgcn_mfma_i32_16x16x64_i8(kb, qb2[h], a2, 0, 0, 0);
+                }
+#pragma unroll
+                for (int j = 0; j < 4; j++) sacc[0][b][j] = fmaf((float)a1[j], qcm, (float)a2[j] * qc2);
+            }
+            return;
+        }
 #pragma unroll
         for (int b = 0; b < 4; b++) {
             u4 kf[KK]; // k-step kk: dims 16grp + 8(kk%2) + 64(kk/2) of this block's key, as f16 pairs
@@ -1009,6 +1040,48 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
         load_v(B[i], t_first + i * STRIDE);
         __builtin_amdgcn_sched_barrier(0);
     }
+    if constexpr (I8M) {
+        float qv[KK][8];
+        float mx = 0.f;
+#pragma unroll
+        for (int kk = 0; kk < KK; kk++)
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const uint32_t bits = qraw[0][kk][e >> 2][e & 3];
+                qv[kk][e] = valid[0] ? __uint_as_float(bits) * a.qscale : 0.f;
+                mx = fmaxf(mx, fabsf(qv[kk][e]));
+            }
+        // the pair's row spans the lanes c, c + 16, c + 32, c + 48
+        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        const int ex = mx > 0.f ? __builtin_amdgcn_frexp_expf(mx) : 0; // mx < 2^ex
+        const float up = __builtin_ldexpf(1.f, 22 - ex);
+        qc2 = __builtin_ldexpf(1.f, ex - 22);
+        qcm = __builtin_ldexpf(1.f, ex - ((c & 1) ? 14 : 6));
+#pragma unroll
+        for (int h = 0; h < HD / 64; h++) {
+            uint32_t w1[4], w2[4];
+#pragma unroll
+            for (int w = 0; w < 4; w++) {
+                w1[w] = 0u;
+                w2[w] = 0u;
+            }
+#pragma unroll
+            for (int j = 0; j < 16; j++) {
+                // element j of the lane's 16 dims of this half: k-step 2h + j / 8, element j % 8
+                const int qi = __float2int_rn(qv[2 * h + (j >> 3)][j & 7] * up);
+                const int l2 = ((qi + 128) & 255) - 128;
+                const int q1 = (qi - l2) >> 8;
+                const int l1 = ((q1 + 128) & 255) - 128;
+                const int l0 = (q1 - l1) >> 8;
+                const uint32_t b1 = (uint32_t)((c & 1) ? l1 : l0) & 255u, b2 = (c & 1) ? 0u : (uint32_t)l2 & 255u;
+                w1[j >> 2] |= b1 << (8 * (j & 3));
+                w2[j >> 2] |= b2 << (8 * (j & 3));
+            }
+            qb1[h] = i4v{(int)w1[0], (int)w1[1], (int)w1[2], (int)w1[3]};
+            qb2[h] = i4v{(int)w2[0], (int)w2[1], (int)w2[2], (int)w2[3]};
+        }
+    } else
     // Q * scale * log2(e) in f32, split into an f16 high part (even columns) and its f16 remainder (odd)
 #pragma unroll
     for (int cb = 0; cb < NCB; cb++)
