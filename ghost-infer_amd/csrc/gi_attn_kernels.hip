@@ -337,6 +337,7 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
     // exact int32 dot products, scaled by qcm / qc2 and added, give the score; the query is represented to 2^-23 of
     // its largest element (the f16 high/remainder split of the other kernels: 2^-22 of each element).
     constexpr bool I8M = DEC_I8_MFMA && I8 && !PM && HD != 256;
+    static_assert(!I8M || NCB == 1, "the int8-MFMA QK: one column block");
     i4v qb1[HD / 64], qb2[HD / 64];
     float qcm = 0.f, qc2 = 0.f;
     {
