@@ -226,8 +226,9 @@ __device__ __forceinline__ uint32_t q4_f16x2(uint32_t hi, uint32_t lo, int j, h2
 // I8 = true: an int8 cache (kv_store's KV8 format, src/cuda.rs:333-339: a row of int8 values and one f32
 // scale per (position, kv head)). Scores are attention_partial_gqa's (src/cuda.rs:1750-1760): the dot
 // product with the integer key, times the key's scale; the value scale rides on the probability
-// (src/cuda.rs:1812-1822) and the exp-sum is of the unscaled probabilities. Bytes are widened to exact f16
-// in registers and both products stay on the f16 MFMA. Tiles are 64 keys (the same register bytes as 32
+// (src/cuda.rs:1812-1822) and the exp-sum is of the unscaled probabilities. Value bytes are widened to exact f16
+// in registers for the f16 P V MFMA; key bytes too where the query takes two f16 columns a pair (one pair per
+// column), and otherwise QK runs on int8 MFMA against the query's integer limbs (I8M below). Tiles are 64 keys (the same register bytes as 32
 // f16 keys); lane (c, grp) holds the S^T rows of keys 16grp + 4b + j (block b, row 4grp + j, so A-row c of
 // block b loads key 16(c/4) + c%4 + 4b) and feeds PV with V rows 16grp..16grp+15 (k-step ks: 8ks..8ks+7),
 // dims 8c..8c+7. Each key's scale is loaded by lane key%64 and broadcast across its 16-lane row.
@@ -575,7 +576,7 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
         __builtin_amdgcn_sched_barrier(0);
         if (reload) load_v(B, t + NB * STRIDE);
     };
-    // the int8 cache's QK over one 64-key tile: the keys widened to exact f16, sacc from zero
+    // the int8 cache's QK over one 64-key tile (sacc from zero): on int8 MFMA (I8M), else the keys widened to exact f16
     auto qk_i8 = [&](auto& B, f4 (&sacc)[NCB][4]) {
         if constexpr (I8M) {
             // the key bytes as they were loaded (dims 64h + 16grp .. + 15 of the block's key), against the limbs of the
