@@ -97,6 +97,9 @@ __device__ __attribute__((used, aligned(256))) unsigned char gi_scratch[GI_SCRAT
 #define DEC_CPOL 2
 #endif
 #define DEC_PAIRS 8 // (token, head) pairs per column block of 16 columns
+#ifndef DEC_V256_DENSE // f16 cache, head size 256: each V load instruction reads whole 256-byte runs of a row
+#define DEC_V256_DENSE 1
+#endif
 #ifndef DEC_I8_MFMA // int8 cache, up to 8 pairs (hi/lo columns): QK on int8 MFMA against the query's int8 limbs
 #define DEC_I8_MFMA 1
 #endif
@@ -392,7 +395,11 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
     const int scoff = lane * (int)scs * 4;
     // head size 256: K row c, dims 8grp + 32kk; V keys 4grp + i, dims 16c..16c+15
     const int koff256 = (c * (int)kvs + 8 * grp) * 2;
-    const int voff256 = (4 * grp * (int)kvs + 16 * c) * 2;
+    // f16 V (DEC_V256_DENSE): the lane's two 16-byte loads of key 4grp + i are dims 8c .. 8c + 7 and 128 + 8c .. + 7, so
+    // the 16 lanes of a key read two whole 256-byte runs of its row per instruction (dims 16c .. 16c + 15 put 16 bytes
+    // every 32 bytes); O^T block dd then holds dims 128(dd / 8) + 8m + dd % 8 in row m
+    constexpr bool V256D = DEC_V256_DENSE && HD == 256 && !I8 && !Q4;
+    const int voff256 = (4 * grp * (int)kvs + (V256D ? 8 : 16) * c) * 2;
     // head size 256, int8 (byte offsets): K row c, bytes 16grp (+64i); V rows 4grp + i, bytes 16c; the scales of
     // tile key 4(lane/16) + lane%4
     const int koff256_8 = c * (int)kvs + 16 * grp;
@@ -466,7 +473,7 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 B.v[i][0] = gi_load16p<CPOL>(r, voff256 + i * vstep);
-                B.v[i][1] = gi_load16p<CPOL>(r, voff256 + i * vstep + 16);
+                B.v[i][1] = gi_load16p<CPOL>(r, voff256 + i * vstep + (V256D ? 256 : 16));
             }
         } else if constexpr (I8) {
             __amdgpu_buffer_rsrc_t r = gi_rsrc(vslice8 + (long long)t * kvs, (long long)(nkeys - t) * kvs);
@@ -1173,10 +1180,11 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
         float l = rows_sum(l_run[cb]);
 #pragma unroll
         for (int j = 0; j < 4; j++) {
-            float* row = &sm_o[wave][16 * cb + c][(HD / 4) * grp + (ND)*j];
+            // (V256D: row m = 4grp + j of block dd is dim 128(dd / 8) + 8m + dd % 8)
+            float* row = &sm_o[wave][16 * cb + c][V256D ? 8 * (4 * grp + j) : (HD / 4) * grp + (ND)*j];
 #pragma unroll
             for (int q4 = 0; q4 < ND / 4; q4++)
-                *reinterpret_cast<float4*>(row + 4 * q4) =
+                *reinterpret_cast<float4*>(row + (V256D ? 128 * (q4 >> 1) + 4 * (q4 & 1) : 4 * q4)) =
                     make_float4(o[cb][4 * q4][j], o[cb][4 * q4 + 1][j], o[cb][4 * q4 + 2][j], o[cb][4 * q4 + 3][j]);
         }
         if (lane < 16 && (PM || (c & 1) == 0)) {
