@@ -131,13 +131,14 @@ def kernel_times(gi_attn, fn, steps, torch, kinds, warm_steps=0):
     return res
 
 
-def decode_kernel_name(n_tok, n_heads, n_kv, hd, i8):
+def decode_kernel_name(n_tok, n_heads, n_kv, hd, i8, chunk=None):
     """Name of the split-K kernel a decode call of this shape launches: the host library's variant rule
     (up to 8 (token, head) pairs per kv head: one column block with two columns per pair; above, one pair
     per MFMA column, with two column blocks per wave above 16 pairs at head size 128 (f16 above 32 pairs:
     two pair sets per workgroup, each over two waves), and two pair sets of one column block at head size
     256 over the f16 cache; over its int8 and 4-bit caches one pair per column throughout, 16 pairs per workgroup
-    or, above 16 pairs, two pair sets (int8) or two column blocks per wave (4-bit))."""
+    or, above 16 pairs, two pair sets (int8) or two column blocks per wave (4-bit)). The f16 head-128 kernel with up
+    to 8 pairs has a short-span form (`..._1s`) for slices (`chunk` keys) of at most two tiles per wave."""
     pairs, p = n_tok * (n_heads // n_kv), 8
     if hd not in (64, 128, 256):  # the f32 kernels' head sizes
         return "gi_decode_f32" + ("_i8" if i8 else "") + f"_h{hd}"
@@ -147,6 +148,8 @@ def decode_kernel_name(n_tok, n_heads, n_kv, hd, i8):
         return "gi_decode_pm_2_q4" if i8 == "q4" else "gi_decode_pm_ws2_1_i8_h256"
     if pairs <= p:
         name = "gi_decode_partial_1"
+        if hd == 128 and not i8 and chunk is not None and chunk <= 256:
+            return name + "s"
     elif hd == 64:
         name = "gi_decode_pm_2" if pairs > 2 * p else "gi_decode_pm_1"
     elif hd == 256:
@@ -572,7 +575,7 @@ def run_decode(torch, gi_attn, dev, w, steps, warmup, n_tok_override=None, refer
                    "slices": nsplit, "keys_per_slice": chunk, "kv_layout": f"head_major [n_kv][ctx][{hd}]"},
         "roofline": {"bound": "hbm", "achieved": round(kern_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(kern_gbs / HBM_PEAK_GBS, 4), "traffic": profile_traffic(f"pmc_decode_partial_{w}"),
-                     "kernel": decode_kernel_name(n_tok, n_heads, n_kv, hd, i8) + " (split-K pass)",
+                     "kernel": decode_kernel_name(n_tok, n_heads, n_kv, hd, i8, chunk) + " (split-K pass)",
                      "algorithmic_bytes_per_launch": part_bytes,
                      "kernel_ms_per_launch": round(part_ms, 5), "launches_timed": part_n,
                      "combine_ms_per_launch": round(comb_ms, 5) if comb_ms else None,

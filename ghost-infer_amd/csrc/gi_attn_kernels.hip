@@ -257,7 +257,8 @@ __device__ __forceinline__ uint32_t q4_f16x2(uint32_t hi, uint32_t lo, int j, h2
 // other head sizes, instead of the tc256 roundings: the reference's attention_partial_gqa hd-256 branch
 // (src/cuda.rs:1762-1781), which serves this cache when its tensor-core decode is off (GHOST_INFER_NO_TC_ATT or
 // GHOST_INFER_NO_TC_DECODE, src/cuda.rs:5655).
-template <int NCB, int WS, bool I8, int HD = 128, bool PM = false, bool Q4 = false, bool F32 = false>
+// NBO: tiles in flight per wave when nonzero (the short-span kernel: one, since each wave then has a tile or two)
+template <int NCB, int WS, bool I8, int HD = 128, bool PM = false, bool Q4 = false, bool F32 = false, int NBO = 0>
 __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
     static_assert(HD == 64 || HD == 128 || HD == 256, "head sizes: 64, 128, 256");
     static_assert(!Q4 || (HD == 256 && !I8), "the 4-bit cache: head size 256");
@@ -269,7 +270,7 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
     // the bias on P that the merge divides out
     constexpr float PBIAS = REF && I8 ? DEC_REF_VB : I8 && PM ? DEC_I8_VB : 1.f;
     // tiles in flight per wave: an int8 tile at head size 256 holds half the bytes of the others (4-bit: a quarter)
-    constexpr int NB = (I8 || Q4) && HD == 256 ? 2 * DEC_NB : DEC_NB;
+    constexpr int NB = NBO ? NBO : (I8 || Q4) && HD == 256 ? 2 * DEC_NB : DEC_NB;
     constexpr int CPAIRS = PM ? 2 * DEC_PAIRS : DEC_PAIRS; // pairs per column block
     constexpr int TILE = HD == 256 ? DEC_TILE / 2 : I8 ? 2 * DEC_TILE : DEC_TILE; // keys per wave tile
     constexpr int KK = HD / 32;                 // QK k-steps
@@ -1269,6 +1270,12 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
 #define GI_DEC_PM_KERNEL(name, NCB, WS, I8) \
     extern "C" __global__ void __launch_bounds__(256, DEC_MINWG) name(GiDecodeArgs a) { gi_decode_partial_t<NCB, WS, I8, 128, true>(a); }
 GI_DEC_KERNEL(gi_decode_partial_1, 1, DEC_WAVES, false, 128)
+// Short spans (at most two tiles per wave, as at config 1's 4096 keys): one register buffer, and the register budget of
+// two workgroups per CU, 161 registers against 264. Config 1, graph-replayed step, two alternating runs on one box: 8.95 /
+// 8.95 µs against 9.47 / 9.46 with the default kernel; at config 2 the same build measured level with it.
+extern "C" __global__ void __launch_bounds__(256, 2) gi_decode_partial_1s(GiDecodeArgs a) {
+    gi_decode_partial_t<1, DEC_WAVES, false, 128, false, false, false, 1>(a);
+}
 // head size 64 (the reference's attention_partial_gqa at any head size a multiple of 32, src/cuda.rs:1684-1865)
 #define GI_DEC_PM64_KERNEL(name, NCB, I8) \
     extern "C" __global__ void __launch_bounds__(256, DEC_MINWG) name(GiDecodeArgs a) { gi_decode_partial_t<NCB, DEC_WAVES, I8, 64, true>(a); }
