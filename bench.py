@@ -148,8 +148,8 @@ def decode_kernel_name(n_tok, n_heads, n_kv, hd, i8, chunk=None):
         return "gi_decode_pm_2_q4" if i8 == "q4" else "gi_decode_pm_ws2_1_i8_h256"
     if pairs <= p:
         name = "gi_decode_partial_1"
-        if hd == 128 and not i8 and chunk is not None and chunk <= 256:
-            return name + "s"
+        if hd in (64, 128) and i8 != "q4" and chunk is not None and chunk <= (512 if i8 else 256):
+            return name + "s" + ("_i8" if i8 else "_h64" if hd == 64 else "")
     elif hd == 64:
         name = "gi_decode_pm_2" if pairs > 2 * p else "gi_decode_pm_1"
     elif hd == 256:
@@ -521,6 +521,8 @@ DECODE_WORKLOADS = {
     # name: (ctx, n_heads, n_kv, n_tok, hd, int8, description)
     "decode64k": (65536, 32, 4, 1, 128, False, "config 2: decode, 1 token, ctx 65536, 32q/4kv, hd 128"),
     "decode4k": (4096, 32, 8, 1, 128, False, "config 1: decode, 1 token, ctx 4096, 32q/8kv, hd 128"),
+    "decode4k_i8": (4096, 32, 8, 1, 128, True, "config 1 over the int8 cache: decode, 1 token, ctx 4096, 32q/8kv"),
+    "decode4k_h64": (4096, 32, 8, 1, 64, False, "config 1's shape with 64-wide heads: decode, 1 token, ctx 4096, 32q/8kv"),
     "verify": (32776, 32, 4, 8, 128, False, "config 4: verify, 8 tokens at a 32768-key prefix, 32q/4kv, hd 128"),
     "decode64k_i8": (65536, 32, 4, 1, 128, True, "config 2 over the int8 cache: decode, 1 token, ctx 65536, 32q/4kv"),
     "verify_i8": (32776, 32, 4, 8, 128, True, "config 4 over the int8 cache: verify, 8 tokens at 32768, 32q/4kv"),
@@ -559,6 +561,10 @@ def run_decode(torch, gi_attn, dev, w, steps, warmup, n_tok_override=None, refer
     chunk, nsplit = gi_attn.decode_plan(ctx, n_tok, n_heads, n_kv, hd)
     if i8:  # the plan query is the f16 cache's; the int8 and 4-bit kernels' pair groups (and tiles) differ
         chunk = nsplit = None
+        if i8 is True and hd == 128 and n_tok * n_heads // n_kv <= 8:
+            # the int8 head-128 decode's plan with one pair group: slices of whole 64-key tiles, at least 256 keys
+            least = -(-ctx // max(1, 256 // n_kv))
+            chunk = max(256, -(-least // 64) * 64)
     kt = kernel_times(gi_attn, r["step"], steps, torch, ("decode_partial", "decode_combine"))
     part_ms, part_n = kt["decode_partial"]
     comb_ms, _ = kt["decode_combine"]

@@ -193,7 +193,7 @@ struct Module {
     bool loaded = false;
     hipModule_t mod = nullptr;
     hipFunction_t dec[2] = {};        // up to 8 pairs, head size 128: [int8 cache]
-    hipFunction_t dec_short = nullptr; // the same over the f16 cache for spans of at most two tiles per wave
+    hipFunction_t dec_short[3] = {}; // one-buffer forms for slices of at most two tiles per wave: f16, int8, f16 hd 64
     hipFunction_t dec256 = nullptr;   // up to 8 pairs, head size 256, the f16 cache
     hipFunction_t dec64[2][3] = {};   // head size 64: [int8 cache][up to 8 pairs, one column block, two]
     hipFunction_t dec_pm[2][2] = {};  // [int8 cache][column blocks - 1]: one pair per column
@@ -246,7 +246,9 @@ int load_module(const char* path, Module** out) {
         if (int e = check(hipModuleLoad(&m.mod, p.c_str()), ("hipModuleLoad(" + p + ")").c_str())) return e;
         struct { hipFunction_t* f; const char* name; } fns[] = {
             {&m.dec[0], "gi_decode_partial_1"},
-            {&m.dec_short, "gi_decode_partial_1s"},
+            {&m.dec_short[0], "gi_decode_partial_1s"},
+            {&m.dec_short[1], "gi_decode_partial_1s_i8"},
+            {&m.dec_short[2], "gi_decode_partial_1s_h64"},
             {&m.dec[1], "gi_decode_partial_1_i8"},
             {&m.dec256, "gi_decode_partial_1_h256"},
             {&m.dec64[0][0], "gi_decode_partial_1_h64"},
@@ -592,7 +594,9 @@ int decode_impl(void* stream, const float* q, long long q_stride, const void* kc
                       : var.pm    ? m->dec_pm[i8][var.ncb - 1]
                                   : m->dec[i8];
     // slices of at most two tiles per wave (kDecWaves waves of kDecTile keys each): the one-buffer kernel
-    if (f == m->dec[0] && a.chunk <= 2 * kDecWaves * kDecTile) f = m->dec_short;
+    if (f == m->dec[0] && a.chunk <= 2 * kDecWaves * kDecTile) f = m->dec_short[0];
+    else if (f == m->dec[1] && a.chunk <= 4 * kDecWaves * kDecTile) f = m->dec_short[1]; // (int8 tiles: 64 keys)
+    else if (f == m->dec64[0][0] && a.chunk <= 2 * kDecWaves * kDecTile) f = m->dec_short[2];
     if (int e = launch(kDecodePartial, f, dim3(a.nsplit, n_kv, var.groups), dim3(256), st, &a, sizeof a)) return e;
     if (a.nsplit == 1) return 0;
     return launch(kDecodeCombine, m->combine, dim3(n_heads, n_tok, kCombineSplit * hd / 128), dim3(64), st, &a, sizeof a);

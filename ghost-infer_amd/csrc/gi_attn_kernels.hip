@@ -1276,6 +1276,13 @@ GI_DEC_KERNEL(gi_decode_partial_1, 1, DEC_WAVES, false, 128)
 extern "C" __global__ void __launch_bounds__(256, 2) gi_decode_partial_1s(GiDecodeArgs a) {
     gi_decode_partial_t<1, DEC_WAVES, false, 128, false, false, false, 1>(a);
 }
+// the same over the int8 cache (tiles of 64 keys) and at head size 64
+extern "C" __global__ void __launch_bounds__(256, 2) gi_decode_partial_1s_i8(GiDecodeArgs a) {
+    gi_decode_partial_t<1, DEC_WAVES, true, 128, false, false, false, 1>(a);
+}
+extern "C" __global__ void __launch_bounds__(256, 2) gi_decode_partial_1s_h64(GiDecodeArgs a) {
+    gi_decode_partial_t<1, DEC_WAVES, false, 64, false, false, false, 1>(a);
+}
 // head size 64 (the reference's attention_partial_gqa at any head size a multiple of 32, src/cuda.rs:1684-1865)
 #define GI_DEC_PM64_KERNEL(name, NCB, I8) \
     extern "C" __global__ void __launch_bounds__(256, DEC_MINWG) name(GiDecodeArgs a) { gi_decode_partial_t<NCB, DEC_WAVES, I8, 64, true>(a); }
