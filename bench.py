@@ -144,12 +144,13 @@ def decode_kernel_name(n_tok, n_heads, n_kv, hd, i8, chunk=None):
         return "gi_decode_f32" + ("_i8" if i8 else "") + f"_h{hd}"
     if hd == 256 and i8:  # the reference's tc256 roundings, one pair per column: 16 or 32 pairs per workgroup
         if pairs <= 2 * p:
-            return "gi_decode_pm_1" + ("_q4" if i8 == "q4" else "_i8_h256")
+            short = "s" if chunk is not None and chunk <= 128 else ""
+            return "gi_decode_pm_1" + short + ("_q4" if i8 == "q4" else "_i8_h256")
         return "gi_decode_pm_2_q4" if i8 == "q4" else "gi_decode_pm_ws2_1_i8_h256"
     if pairs <= p:
         name = "gi_decode_partial_1"
-        if hd in (64, 128) and i8 != "q4" and chunk is not None and chunk <= (512 if i8 else 256):
-            return name + "s" + ("_i8" if i8 else "_h64" if hd == 64 else "")
+        if chunk is not None and chunk <= (128 if hd == 256 else 512 if i8 else 256):
+            return name + "s" + ("_i8" if i8 else "_h64" if hd == 64 else "_h256" if hd == 256 else "")
     elif hd == 64:
         name = "gi_decode_pm_2" if pairs > 2 * p else "gi_decode_pm_1"
     elif hd == 256:
@@ -523,6 +524,8 @@ DECODE_WORKLOADS = {
     "decode4k": (4096, 32, 8, 1, 128, False, "config 1: decode, 1 token, ctx 4096, 32q/8kv, hd 128"),
     "decode4k_i8": (4096, 32, 8, 1, 128, True, "config 1 over the int8 cache: decode, 1 token, ctx 4096, 32q/8kv"),
     "decode4k_h64": (4096, 32, 8, 1, 64, False, "config 1's shape with 64-wide heads: decode, 1 token, ctx 4096, 32q/8kv"),
+    "decode4k_h256": (4096, 16, 2, 1, 256, False, "decode with 256-wide heads (16q/2kv), 1 token, ctx 4096, f16 cache"),
+    "decode4k_h256_i8": (4096, 16, 2, 1, 256, True, "decode with 256-wide heads (16q/2kv), 1 token, ctx 4096, int8 cache"),
     "verify": (32776, 32, 4, 8, 128, False, "config 4: verify, 8 tokens at a 32768-key prefix, 32q/4kv, hd 128"),
     "decode64k_i8": (65536, 32, 4, 1, 128, True, "config 2 over the int8 cache: decode, 1 token, ctx 65536, 32q/4kv"),
     "verify_i8": (32776, 32, 4, 8, 128, True, "config 4 over the int8 cache: verify, 8 tokens at 32768, 32q/4kv"),
@@ -561,10 +564,12 @@ def run_decode(torch, gi_attn, dev, w, steps, warmup, n_tok_override=None, refer
     chunk, nsplit = gi_attn.decode_plan(ctx, n_tok, n_heads, n_kv, hd)
     if i8:  # the plan query is the f16 cache's; the int8 and 4-bit kernels' pair groups (and tiles) differ
         chunk = nsplit = None
-        if i8 is True and hd == 128 and n_tok * n_heads // n_kv <= 8:
-            # the int8 head-128 decode's plan with one pair group: slices of whole 64-key tiles, at least 256 keys
+        if (hd == 128 and i8 is True and n_tok * n_heads // n_kv <= 8) or (hd == 256 and n_tok * n_heads // n_kv <= 16):
+            # the plan of these kernels' single pair group: slices of whole wave tiles (64 int8 keys at head size 128,
+            # 16 keys at 256), at least one tile per wave
+            tile = 64 if hd == 128 else 16
             least = -(-ctx // max(1, 256 // n_kv))
-            chunk = max(256, -(-least // 64) * 64)
+            chunk = max(4 * tile, -(-least // tile) * tile)
     kt = kernel_times(gi_attn, r["step"], steps, torch, ("decode_partial", "decode_combine"))
     part_ms, part_n = kt["decode_partial"]
     comb_ms, _ = kt["decode_combine"]

@@ -193,7 +193,8 @@ struct Module {
     bool loaded = false;
     hipModule_t mod = nullptr;
     hipFunction_t dec[2] = {};        // up to 8 pairs, head size 128: [int8 cache]
-    hipFunction_t dec_short[3] = {}; // one-buffer forms for slices of at most two tiles per wave: f16, int8, f16 hd 64
+    // one-buffer forms for slices of at most two tiles per wave: f16, int8, f16 hd 64, f16 hd 256, int8 hd 256, 4-bit
+    hipFunction_t dec_short[6] = {};
     hipFunction_t dec256 = nullptr;   // up to 8 pairs, head size 256, the f16 cache
     hipFunction_t dec64[2][3] = {};   // head size 64: [int8 cache][up to 8 pairs, one column block, two]
     hipFunction_t dec_pm[2][2] = {};  // [int8 cache][column blocks - 1]: one pair per column
@@ -249,6 +250,9 @@ int load_module(const char* path, Module** out) {
             {&m.dec_short[0], "gi_decode_partial_1s"},
             {&m.dec_short[1], "gi_decode_partial_1s_i8"},
             {&m.dec_short[2], "gi_decode_partial_1s_h64"},
+            {&m.dec_short[3], "gi_decode_partial_1s_h256"},
+            {&m.dec_short[4], "gi_decode_pm_1s_i8_h256"},
+            {&m.dec_short[5], "gi_decode_pm_1s_q4"},
             {&m.dec[1], "gi_decode_partial_1_i8"},
             {&m.dec256, "gi_decode_partial_1_h256"},
             {&m.dec64[0][0], "gi_decode_partial_1_h64"},
@@ -597,6 +601,11 @@ int decode_impl(void* stream, const float* q, long long q_stride, const void* kc
     if (f == m->dec[0] && a.chunk <= 2 * kDecWaves * kDecTile) f = m->dec_short[0];
     else if (f == m->dec[1] && a.chunk <= 4 * kDecWaves * kDecTile) f = m->dec_short[1]; // (int8 tiles: 64 keys)
     else if (f == m->dec64[0][0] && a.chunk <= 2 * kDecWaves * kDecTile) f = m->dec_short[2];
+    else if (a.chunk <= kDecWaves * kDecTile) { // head size 256 (16-key tiles)
+        if (f == m->dec256) f = m->dec_short[3];
+        else if (f == m->dec_ref[0]) f = m->dec_short[4];
+        else if (f == m->dec_ref[1]) f = m->dec_short[5];
+    }
     if (int e = launch(kDecodePartial, f, dim3(a.nsplit, n_kv, var.groups), dim3(256), st, &a, sizeof a)) return e;
     if (a.nsplit == 1) return 0;
     return launch(kDecodeCombine, m->combine, dim3(n_heads, n_tok, kCombineSplit * hd / 128), dim3(64), st, &a, sizeof a);

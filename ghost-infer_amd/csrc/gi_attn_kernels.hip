@@ -1127,7 +1127,7 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
     // Steady state: every buffer gets a further tile (those past the slice read zeros and are never
     // processed). The last round of tiles runs without reloads, so no load is left in flight at the end.
     int t = t_first;
-    if constexpr (DEC_PIPE && PM) {
+    if constexpr (DEC_PIPE && PM && NB % 2 == 0) { // (its two score sets alternate with the buffers: NB even)
         // State at the top of each step: tile t in B[0] with its scores (row max taken, O rescaled), its K buffer
         // already refilled with tile t + NB STRIDE; tiles t + i STRIDE in B[i]. A step finishes tiles t ..
         // t + (NB-1) STRIDE and scores tile t + NB STRIDE, so it runs while that tile needs no mask.
@@ -1282,6 +1282,17 @@ extern "C" __global__ void __launch_bounds__(256, 2) gi_decode_partial_1s_i8(GiD
 }
 extern "C" __global__ void __launch_bounds__(256, 2) gi_decode_partial_1s_h64(GiDecodeArgs a) {
     gi_decode_partial_t<1, DEC_WAVES, false, 64, false, false, false, 1>(a);
+}
+// head size 256 (16-key tiles): the f16 cache, and the int8 and 4-bit caches' tc256 kernels (which otherwise keep four
+// tiles in flight)
+extern "C" __global__ void __launch_bounds__(256, 2) gi_decode_partial_1s_h256(GiDecodeArgs a) {
+    gi_decode_partial_t<1, DEC_WAVES, false, 256, false, false, false, 1>(a);
+}
+extern "C" __global__ void __launch_bounds__(256, 2) gi_decode_pm_1s_i8_h256(GiDecodeArgs a) {
+    gi_decode_partial_t<1, DEC_WAVES, true, 256, true, false, false, 1>(a);
+}
+extern "C" __global__ void __launch_bounds__(256, 2) gi_decode_pm_1s_q4(GiDecodeArgs a) {
+    gi_decode_partial_t<1, DEC_WAVES, false, 256, true, true, false, 1>(a);
 }
 // head size 64 (the reference's attention_partial_gqa at any head size a multiple of 32, src/cuda.rs:1684-1865)
 #define GI_DEC_PM64_KERNEL(name, NCB, I8) \
