@@ -119,6 +119,17 @@ typedef int i4v __attribute__((ext_vector_type(4)));
 #define GI_RSRC_FLAGS 0x00020000
 
 __device__ __forceinline__ float wave_xor(float v, int m) { return __shfl_xor(v, m, 64); }
+// Scales an MFMA accumulator (held in AGPRs) by alpha in the rare rescale branch of an online softmax. The empty
+// asm statements pin the accumulator to AGPRs on both sides of the multiply, so the AGPR -> VGPR copies it needs are
+// made inside the branch; without them the compiler hoists those copies into every tile iteration (up to 135
+// accvgpr reads per tile in the head-256 4-bit verify, all dead unless the branch is taken).
+// PIN = false: kernels whose accumulators the compiler keeps in VGPRs (the prefill's two waves per SIMD and the
+// short-span decode), where the pin would move them into AGPRs and spill.
+template <bool PIN, typename T> __device__ __forceinline__ void gi_acc_scale(T& acc, float alpha) {
+    if constexpr (PIN) asm volatile("" : "+a"(acc));
+    acc *= alpha;
+    if constexpr (PIN) asm volatile("" : "+a"(acc));
+}
 // v of lane l ^ 1 (DPP quad permutation, no LDS round trip)
 __device__ __forceinline__ float lane_xor1(float v) {
     return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, false));
@@ -548,7 +559,7 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
                 m_run[cb] = m_new;
                 l_run[cb] *= alpha;
 #pragma unroll
-                for (int dd = 0; dd < ND; dd++) o[cb][dd] *= alpha;
+                for (int dd = 0; dd < ND; dd++) gi_acc_scale<NBO == 0 && HD != 128>(o[cb][dd], alpha);
             }
             const float m_use = m_run[cb] == GI_NEG_INF ? 0.f : m_run[cb]; // no key seen yet: p = 0
             float psum = 0.f;
@@ -703,7 +714,7 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
                 m_run[cb] = m_new;
                 l_run[cb] *= alpha;
 #pragma unroll
-                for (int dd = 0; dd < ND; dd++) o[cb][dd] *= alpha;
+                for (int dd = 0; dd < ND; dd++) gi_acc_scale<NBO == 0 && HD != 128>(o[cb][dd], alpha);
             }
             const float m_use = m_run[cb] == GI_NEG_INF ? 0.f : m_run[cb];
             float psum = 0.f;
@@ -846,7 +857,7 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
                 m_run[cb] = m_new;
                 l_run[cb] *= alpha;
 #pragma unroll
-                for (int dd = 0; dd < ND; dd++) o[cb][dd] *= alpha;
+                for (int dd = 0; dd < ND; dd++) gi_acc_scale<NBO == 0 && HD != 128>(o[cb][dd], alpha);
             }
             const float m_use = m_run[cb] == GI_NEG_INF ? 0.f : m_run[cb];
             float psum = 0.f;
@@ -964,7 +975,7 @@ __device__ __forceinline__ void gi_decode_partial_t(GiDecodeArgs a) {
                 m_run[cb] = m_new;
                 l_run[cb] *= alpha;
 #pragma unroll
-                for (int dd = 0; dd < ND; dd++) o[cb][dd] *= alpha;
+                for (int dd = 0; dd < ND; dd++) gi_acc_scale<NBO == 0 && HD != 128>(o[cb][dd], alpha);
 #pragma unroll
                 for (int b = 0; b < PB; b++) S.v[cb][b] -= delta;
             }
@@ -1766,7 +1777,7 @@ __device__ __forceinline__ void gi_prefill_t(const GiPrefillArgs& a) {
             for (int e = 0; e < 16; e++) negm[e] = -m_run;
             l_run *= alpha;
 #pragma unroll
-            for (int db = 0; db < NDB; db++) o[db] *= alpha;
+            for (int db = 0; db < NDB; db++) gi_acc_scale<false>(o[db], alpha);
 #pragma unroll
             for (int bb = 0; bb < NBLK; bb++) s[bb] -= delta;
         }
@@ -2181,7 +2192,7 @@ __device__ __forceinline__ void gi_prefill256r(const GiPrefillArgs& a) {
             negm = f4{-m_run, -m_run, -m_run, -m_run};
             l_run *= alpha;
 #pragma unroll
-            for (int db = 0; db < NDB; db++) o[db] *= alpha;
+            for (int db = 0; db < NDB; db++) gi_acc_scale<false>(o[db], alpha);
 #pragma unroll
             for (int kb = 0; kb < NKB; kb++) s[kb] -= delta;
         }
