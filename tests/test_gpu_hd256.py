@@ -55,6 +55,8 @@ DECODE_SHAPES_256 = [
     (6, 130, 16, 2),  # 48 pairs
     (1, 3000, 32, 2), # G = 16: one token's 16 pairs, one pair per column
     (2, 2000, 32, 1), # G = 32, two tokens: 64 pairs on one kv head
+    (8, 249, 16, 2),  # token 0's span ends before the last slice: its partial there is empty (m = -inf) and the merge skips it
+    (2, 63, 16, 2),   # the same with 4 pairs: token 0 sees all of slice 0 and none of slice 1
 ]
 
 

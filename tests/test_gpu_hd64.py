@@ -59,6 +59,7 @@ DECODE_SHAPES_64 = [
     (3, 60, 16, 1),     # G = 16: 48 pairs on one kv head
     (1, 1000, 32, 2),   # G = 16, one token
     (16, 1000, 4, 4),   # G = 1
+    (8, 249, 16, 4),  # token 0's span ends before the last slice: its partial there is empty (m = -inf) and the merge skips it
 ]
 
 

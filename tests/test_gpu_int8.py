@@ -97,6 +97,8 @@ DECODE_SHAPES_I8 = [
     (16, 1000, 32, 4),  # 128 pairs: two pair sets of 32 per workgroup, two workgroups per (slice, kv head)
     (32, 513, 32, 4),   # 256 pairs: the same layout, four workgroups
     (8, 2500, 64, 4),   # 128 pairs at G = 16, a span of several slices
+    (8, 249, 32, 4),  # token 0's span ends before the last slice: its partial there is empty (m = -inf) and the merge skips it
+    (2, 255, 8, 2),    # the same with 8 pairs: token 0 sees all of slice 0 and none of slice 1
 ]
 
 

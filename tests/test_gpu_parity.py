@@ -63,6 +63,9 @@ DECODE_SHAPES = [
     (1, 5000, 64, 4),  # G = 16: one token's 16 pairs in one column block
     (1, 3000, 32, 1),  # G = 32: two column blocks
     (2, 2000, 64, 2),  # G = 32, two tokens: 64 pairs, two pair sets
+    (8, 249, 32, 4),  # token 0's span ends before the last slice: its partial there is empty (m = -inf) and the merge skips it
+    (2, 127, 8, 2),    # the same with 8 pairs (hi/lo columns): token 0 sees all of slice 0 and none of slice 1
+    (16, 1020, 32, 4),  # the same at 128 pairs (two pair sets, two workgroups): tokens 0-3 see none of slice 8
 ]
 
 

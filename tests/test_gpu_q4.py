@@ -50,6 +50,8 @@ DECODE_SHAPES_Q4 = [
     (8, 2000, 16, 2),
     (15, 513, 16, 2),
     (1, 40000, 16, 2),
+    (8, 249, 16, 2),  # token 0's span ends before the last slice: its partial there is empty (m = -inf) and the merge skips it
+    (2, 63, 16, 2),    # the same with 4 pairs: token 0 sees all of slice 0 and none of slice 1
 ]
 
 
